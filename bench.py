@@ -1,0 +1,173 @@
+"""Benchmark of the compressed-KV decode step on one MI355X.
+
+Workload (Llama-3-8B shape at 128K context, bf16, batch 1): 32 layers, each
+with 8 KV rows whose lengths are the per-head budgets of a seeded synthetic
+head classification at compression ratio 0.5 (keep heads hold all 131072
+tokens).  K/V, queries and new tokens are seeded random data resident in HBM.
+
+One step = for every layer: append the new token of every row, then decode
+attention of the 32 query heads (GQA 4) over the ragged rows.  Prints one
+JSON line (metric/value/unit ... roofline, cpu_baseline).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "decode attn µs/layer + HBM GB/s (% of peak) at 128K ctx, Llama-3-8B shape"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--ctx", type=int, default=131072)
+    p.add_argument("--layers", type=int, default=32)
+    p.add_argument("--ratio", type=float, default=0.5)
+    p.add_argument("--tiles-per-wave", type=int, default=None)
+    p.add_argument("--seed", type=int, default=1002)
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--unfused-append", action="store_true", help="append in its own launch before attention")
+    return p.parse_args()
+
+
+def cpu_baseline(ctx, budgets, seconds):
+    """Time the C oracle's decode attention on one layer at the same shape."""
+    from oracle import c_oracle
+    c_oracle.build()
+    threads = min(os.cpu_count() or 1, 16)
+    c_oracle.set_threads(threads)
+    rng = np.random.default_rng(7)
+    lens = np.asarray(budgets, dtype=np.int64)
+    total = int(lens.sum())
+    # bf16 bit patterns of N(0,1) values, natural [tokens, 128] layout.
+    def bf16_bits(n):
+        x = rng.standard_normal(n, dtype=np.float32)
+        u = x.view(np.uint32)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    k = bf16_bits(total * 128)
+    v = bf16_bits(total * 128)
+    q = bf16_bits(len(lens) * 4 * 128).reshape(len(lens), 4, 128)
+    off = np.zeros(len(lens), dtype=np.int64)
+    off[1:] = np.cumsum(lens)[:-1]
+    scale = 1.0 / math.sqrt(128)
+    c_oracle.decode_attention(q, k, v, off, lens, scale, 2)  # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        c_oracle.decode_attention(q, k, v, off, lens, scale, 2)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 50:
+            break
+    per = el / n
+    nbytes = total * 128 * 2 * 2
+    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"C oracle decode attention, one layer ({total} K/V rows, bf16, G=4), {n} passes in "
+                      f"{el:.1f}s; {per * 1e6:.0f} us/layer"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the path is sharded by KV head "
+              "across GPUs by design but no multi-GPU run is part of this build.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from heterocache_amd import ops, workloads
+    from heterocache_amd.store import KVStore
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(args.seed)
+    L, Hkv, G, D = args.ctx, 8, 4, 128
+    data = workloads.synthetic_head_json(args.layers, Hkv, args.seed)
+    max_gen = args.warmup + args.steps + 8
+    stores, budgets = [], []
+    for layer in range(args.layers):
+        lens, base = workloads.row_budgets(data, layer, L, args.ratio, args.layers, Hkv)
+        st = KVStore(lens + max_gen, torch.bfloat16, dev)
+        st.k.normal_()
+        st.v.normal_()
+        st.set_lengths(lens)
+        stores.append(st)
+        budgets.append(lens)
+    tpw = args.tiles_per_wave or ops.DEFAULT_TILES_PER_WAVE
+    q = torch.randn((args.layers, Hkv, G, D), device=dev).to(torch.bfloat16)
+    kn = torch.randn((args.layers, Hkv, D), device=dev).to(torch.bfloat16)
+    vn = torch.randn((args.layers, Hkv, D), device=dev).to(torch.bfloat16)
+    outs = [torch.empty((Hkv, G, D), dtype=torch.bfloat16, device=dev) for _ in range(args.layers)]
+    scale = 1.0 / math.sqrt(D)
+
+    def step():
+        # One layer = the fused append + split-K attention launch and its merge.
+        for layer, st in enumerate(stores):
+            if args.unfused_append:
+                st.append(kn[layer], vn[layer])
+                st.attend(q[layer], scale, out=outs[layer], tiles_per_wave=tpw)
+            else:
+                st.attend(q[layer], scale, out=outs[layer], k_new=kn[layer], v_new=vn[layer], tiles_per_wave=tpw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # One event pair per step on the launch stream (per-layer event records
+    # would themselves add gaps between the kernels they bracket).
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    attn_bytes = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        ev[s][0].record()
+        step()
+        ev[s][1].record()
+        attn_bytes += sum(st.kv_bytes() for st in stores)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    step_ms = [e0.elapsed_time(e1) for (e0, e1) in ev]
+    us_layer = float(np.mean(step_ms)) * 1e3 / args.layers
+    # Algorithmic bytes per layer: every retained K and V row once (the new
+    # token included), plus queries and outputs.
+    q_out_bytes = 2 * Hkv * G * D * 2
+    per_launch = attn_bytes / (args.steps * args.layers) + q_out_bytes
+    gbs = per_launch / (us_layer * 1e-6) / 1e9
+    ms_step = float(np.mean(step_ms))
+    rec = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded random K/V/q, synthetic head classification)",
+        "config": {"workload": f"decode step, Llama-3-8B shape, {L} ctx, ratio {args.ratio}, batch 1, "
+                               f"{args.layers} layers, 8 KV rows x GQA 4, head_dim 128",
+                   "ctx": L, "layers": args.layers, "kv_heads": Hkv, "q_heads": Hkv * G, "head_dim": D,
+                   "ratio": args.ratio, "batch": 1, "tiles_per_wave": tpw},
+        "us_per_layer": round(us_layer, 3),
+        "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "hc::decode_partial_kernel + decode_merge_kernel (one layer of the step)",
+                     "bytes_per_launch": int(per_launch)},
+    }
+    if not args.no_cpu_baseline:
+        rec["cpu_baseline"] = cpu_baseline(L, budgets[0], args.cpu_seconds)
+    print(json.dumps(rec))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,127 @@
+// Device-side building blocks shared by every libhc kernel (gfx950 / CDNA4).
+//
+// Ragged per-head KV store ("tiled head-major"):
+//   Every (batch, kv-head) row owns a contiguous run of 32-token tiles inside
+//   one per-layer K buffer and one per-layer V buffer.  A tile holds
+//   32 tokens x 128 channels and is laid out so that one 16-byte load per lane
+//   lands directly in the operand register of a 16x16x32 MFMA:
+//
+//   K tile element (t, d):  h=t/16 m=t%16 s=d/32 g=(d%32)/8 i=d%8
+//                           offset = (((h*4 + s)*4 + g)*16 + m)*8 + i
+//   V tile element (t, d):  mt=d/16 n=d%16 r=t%16 g=r/4 i=4*(t/16)+r%4
+//                           offset = ((mt*4 + g)*16 + n)*8 + i
+//
+//   For K, MFMA step (h, s) reads lane l = g*16+m at ((h*4+s)*64 + l)*8: one
+//   1 KB fully coalesced wave load.  For V, MFMA step mt reads lane
+//   l = g*16+n at (mt*64 + l)*8, again 1 KB contiguous.  The V token order
+//   inside a lane matches the order in which the Q.K^T MFMA leaves scores in
+//   its accumulator, so P never moves between lanes.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+#define HC_HEAD_DIM 128
+#define HC_TILE 32
+#define HC_TILE_ELEMS (HC_TILE * HC_HEAD_DIM)
+
+namespace hc {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 f16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+
+enum DType { F32 = 0, F16 = 1, BF16 = 2 };
+
+__host__ __device__ __forceinline__ int64_t k_tile_offset(int t, int d) {
+  int h = t >> 4, m = t & 15, s = d >> 5, g = (d >> 3) & 3, i = d & 7;
+  return ((((h * 4 + s) * 4 + g) * 16 + m) * 8) + i;
+}
+
+__host__ __device__ __forceinline__ int64_t v_tile_offset(int t, int d) {
+  int mt = d >> 4, n = d & 15, r = t & 15, g = r >> 2, i = ((t >> 4) << 2) | (r & 3);
+  return (((mt * 4 + g) * 16 + n) * 8) + i;
+}
+
+// Element traits: storage type, 8-element lane vector and conversions.
+template <typename T> struct Elem;
+
+template <> struct Elem<__bf16> {
+  typedef bf16x8 vec8;
+  static __device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
+  static __device__ __forceinline__ __bf16 from_f32(float x) { return (__bf16)x; }
+};
+template <> struct Elem<_Float16> {
+  typedef f16x8 vec8;
+  static __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+  static __device__ __forceinline__ _Float16 from_f32(float x) { return (_Float16)x; }
+};
+template <> struct Elem<float> {
+  struct vec8 { f32x4 lo, hi; };
+  static __device__ __forceinline__ float to_f32(float x) { return x; }
+  static __device__ __forceinline__ float from_f32(float x) { return x; }
+};
+
+// Load 8 consecutive elements (16 B for 16-bit types, 32 B for fp32).
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::vec8 load8(const T* p) {
+  return *reinterpret_cast<const typename Elem<T>::vec8*>(p);
+}
+template <>
+__device__ __forceinline__ Elem<float>::vec8 load8<float>(const float* p) {
+  Elem<float>::vec8 r;
+  r.lo = *reinterpret_cast<const f32x4*>(p);
+  r.hi = *reinterpret_cast<const f32x4*>(p + 4);
+  return r;
+}
+
+// acc += A(16x32) * B(32x16) where each lane supplies 8 k-values of its row
+// (A) / column (B): lane l owns row/col l%16 and k-slots 8*(l/16)+[0..8).
+// For fp32 the same 32-wide contraction is issued as 8 x (16x16x4) MFMAs in
+// which step e covers k-slots {8g+e : g=0..3}; the result is identical up to
+// summation order.
+__device__ __forceinline__ f32x4 mma_16x16x32(bf16x8 a, bf16x8 b, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma_16x16x32(f16x8 a, f16x8 b, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma_16x16x32(Elem<float>::vec8 a, Elem<float>::vec8 b, f32x4 acc) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.lo[e], b.lo[e], acc, 0, 0, 0);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a.hi[e], b.hi[e], acc, 0, 0, 0);
+  return acc;
+}
+
+// Pack 8 fp32 values into the lane vector of T (round-to-nearest-even).
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::vec8 pack8(const float (&v)[8]) {
+  typename Elem<T>::vec8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = Elem<T>::from_f32(v[e]);
+  return r;
+}
+template <>
+__device__ __forceinline__ Elem<float>::vec8 pack8<float>(const float (&v)[8]) {
+  Elem<float>::vec8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) { r.lo[e] = v[e]; r.hi[e] = v[e + 4]; }
+  return r;
+}
+
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::vec8 zero8() {
+  float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  return pack8<T>(z);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask, 64));
+}
+
+}  // namespace hc

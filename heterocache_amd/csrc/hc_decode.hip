@@ -1,0 +1,485 @@
+// Split-K GQA flash-decode over the ragged per-head tiled KV store.
+//
+// Replaces the paged `flash_attn_with_kvcache(q, k_pool, v_pool,
+// cache_seqlens, block_table, causal=False)` call of the reference decode
+// step (heterocache/llama_model.py:382-389, heterocache/qwen_model.py:194-201)
+// and, optionally, the decode-token append that precedes it
+// (heterocache/cache_utils.py:970-1005).
+//
+// Two back-to-back launches per layer and step, no cross-workgroup
+// synchronisation inside a kernel (an agent-scope fence costs an L2
+// write-back per workgroup on a multi-XCD part):
+//  * decode_partial_kernel: every row (batch, kv-head) is cut into chunks of
+//    NWAVES*tiles_per_wave 32-token tiles, one workgroup per chunk, rows
+//    visited in row_order (longest first).  Each wave streams its run of
+//    tiles with one-tile prefetch, computes S = K.Q^T on the matrix cores
+//    (the G query heads of the group share every K load), an online base-2
+//    softmax and O^T += V^T.P^T on the matrix cores; the waves' states are
+//    combined through LDS into one (m, l, O) partial per workgroup.
+//  * decode_merge_kernel: one workgroup per (row, query, 32-channel slice)
+//    folds the row's partials.
+//  * with k_new/v_new the new token is attended at slot len (patched into the
+//    operand registers) and written into the store by the wave owning that
+//    slot; the merge advances row_len by one.
+#include "hc_common.h"
+#include "hc_internal.h"
+
+namespace hc {
+
+struct ChunkLoc {
+  int row;      // store row
+  int chunk;    // chunk index inside the row
+  int len;      // tokens attended (stored length, +1 with a fused append)
+  int nparts;   // chunks of the row
+  int64_t p0;   // global part index of the row's first chunk
+  int64_t total;  // chunks of all rows
+  bool found;
+};
+
+// Map a workgroup index onto (row, chunk) from the device-resident lengths.
+__device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len, const int* __restrict__ row_order,
+                                                 int rows, int extra, int chunk_tiles, int64_t b) {
+  ChunkLoc c;
+  c.found = false;
+  c.row = 0;
+  c.chunk = 0;
+  c.len = 0;
+  c.nparts = 0;
+  c.p0 = 0;
+  int64_t acc = 0;
+  for (int k = 0; k < rows; ++k) {
+    const int r = row_order ? row_order[k] : k;
+    const int l = row_len[r] + extra;
+    const int64_t nt = (l + HC_TILE - 1) / HC_TILE;
+    // An empty row still gets one workgroup, which writes its zero output.
+    const int64_t nc = nt > 0 ? (nt + chunk_tiles - 1) / chunk_tiles : 1;
+    if (!c.found && b < acc + nc) {
+      c.found = true;
+      c.row = r;
+      c.chunk = (int)(b - acc);
+      c.len = l;
+      c.nparts = (int)nc;
+      c.p0 = acc;
+    }
+    acc += nc;
+  }
+  c.total = acc;
+  return c;
+}
+
+// Overwrite token `tn` of the tile held in (kr, vr) with the new token.
+// Every register index is a compile-time constant (value selects only), so
+// the operand arrays stay in registers.
+template <typename T>
+__device__ __forceinline__ void patch_new_token(typename Elem<T>::vec8 (&kr)[8], typename Elem<T>::vec8 (&vr)[8],
+                                                const T* __restrict__ kn, const T* __restrict__ vn, int tn, int lane) {
+  typedef typename Elem<T>::vec8 vec8;
+  const int m = lane & 15, g = lane >> 4;
+  if (m == (tn & 15)) {
+    const bool lo = tn < 16;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const vec8 x = load8<T>(kn + 32 * s + 8 * g);
+      const vec8 a = kr[s], b = kr[4 + s];
+      kr[s] = lo ? x : a;
+      kr[4 + s] = lo ? b : x;
+    }
+  }
+  if (g == ((tn & 15) >> 2)) {
+    const int i = 4 * (tn >> 4) + (tn & 3);
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+      const T x = vn[16 * mt + m];
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vr[mt].lo[e] = (e == i) ? x : vr[mt].lo[e];
+          vr[mt].hi[e] = (e + 4 == i) ? x : vr[mt].hi[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vr[mt][e] = (e == i) ? x : vr[mt][e];
+      }
+    }
+  }
+}
+
+template <typename T, int NWAVES>
+__global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_partial_kernel(
+    const T* __restrict__ q, T* __restrict__ kstore, T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off,
+    const int* __restrict__ row_len, const int* __restrict__ row_order, int rows, int G, float scale_log2,
+    int tiles_per_wave, const T* __restrict__ k_new, const T* __restrict__ v_new, float* __restrict__ part_o,
+    float* __restrict__ part_ml, int* __restrict__ row_info) {
+  typedef typename Elem<T>::vec8 vec8;
+  constexpr int NT = NWAVES * 64;
+  const int chunk_tiles = NWAVES * tiles_per_wave;
+  const bool fused_append = (k_new != nullptr);
+  const ChunkLoc loc = locate_chunk(row_len, row_order, rows, fused_append ? 1 : 0, chunk_tiles, blockIdx.x);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int n = lane & 15;  // query slot owned by this lane
+  const int g = lane >> 4;  // k-group of this lane
+
+  __shared__ float s_m[NWAVES][16];
+  __shared__ float s_l[NWAVES][16];
+  __shared__ float s_o[NWAVES][16][HC_HEAD_DIM + 4];
+
+  if (!loc.found) return;
+  if (loc.total > (int64_t)gridDim.x) {
+    // The launch grid is smaller than the device lengths need: flag the row
+    // so the merge writes NaN instead of a silently partial result.
+    if (threadIdx.x == 0 && loc.chunk == 0) {
+      row_info[2 * loc.row] = 0;
+      row_info[2 * loc.row + 1] = -1;
+    }
+    return;
+  }
+  {
+    const int row = loc.row, len = loc.len;
+    const int new_pos = fused_append ? len - 1 : -1;
+    const T* kn = fused_append ? k_new + (int64_t)row * HC_HEAD_DIM : nullptr;
+    const T* vn = fused_append ? v_new + (int64_t)row * HC_HEAD_DIM : nullptr;
+
+    // Query operand: lane owns Q[n][32s + 8g + e] (zero for padded slots).
+    vec8 qreg[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (n < G)
+        qreg[s] = load8<T>(q + ((int64_t)row * G + n) * HC_HEAD_DIM + 32 * s + 8 * g);
+      else
+        qreg[s] = zero8<T>();
+    }
+
+    const int ntiles = (len + HC_TILE - 1) / HC_TILE;
+    const int t_begin = loc.chunk * chunk_tiles + wave * tiles_per_wave;
+    const int t_end = min(t_begin + tiles_per_wave, ntiles);
+
+    float m_run = -INFINITY, l_run = 0.f;
+    f32x4 o[8];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if (t_begin < t_end) {
+      const int64_t row_base = row_tile_off[row] * (int64_t)HC_TILE_ELEMS;
+      const T* kb = kstore + row_base + lane * 8;
+      const T* vb = vstore + row_base + lane * 8;
+      vec8 kr[8], vr[8];
+#pragma unroll
+      for (int x = 0; x < 8; ++x) {
+        kr[x] = load8<T>(kb + (int64_t)t_begin * HC_TILE_ELEMS + x * 512);
+        vr[x] = load8<T>(vb + (int64_t)t_begin * HC_TILE_ELEMS + x * 512);
+      }
+      for (int t = t_begin; t < t_end; ++t) {
+        vec8 kn_[8], vn_[8];
+        const bool more = (t + 1 < t_end);
+        if (more) {
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            kn_[x] = load8<T>(kb + (int64_t)(t + 1) * HC_TILE_ELEMS + x * 512);
+            vn_[x] = load8<T>(vb + (int64_t)(t + 1) * HC_TILE_ELEMS + x * 512);
+          }
+        }
+        const int tok0 = t * HC_TILE;
+        if (fused_append && new_pos >= tok0 && new_pos < tok0 + HC_TILE)
+          patch_new_token<T>(kr, vr, kn, vn, new_pos - tok0, lane);
+        // S^T(token, query) for the two 16-token halves of the tile.
+        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          s0 = mma_16x16x32(kr[s], qreg[s], s0);
+          s1 = mma_16x16x32(kr[4 + s], qreg[s], s1);
+        }
+        // Element e of this lane holds token 16*(e/4) + 4g + e%4 of the tile.
+        float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+        if (tok0 + HC_TILE > len) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int tok = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
+            if (tok >= len) sv[e] = -INFINITY;
+          }
+#pragma unroll
+          for (int mt = 0; mt < 8; ++mt) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int tok = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
+              if (tok >= len) {
+                if constexpr (sizeof(T) == 4) {
+                  if (e < 4) vr[mt].lo[e] = 0.f; else vr[mt].hi[e - 4] = 0.f;
+                } else {
+                  vr[mt][e] = Elem<T>::from_f32(0.f);
+                }
+              }
+            }
+          }
+        }
+        float mx = sv[0];
+#pragma unroll
+        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+        mx = wave_max_xor(mx, 16);
+        mx = wave_max_xor(mx, 32);
+        const float m_new = fmaxf(m_run, mx * scale_log2);
+        const float alpha = fast_exp2(m_run - m_new);
+        float p[8];
+        float psum = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          p[e] = fast_exp2(fmaf(sv[e], scale_log2, -m_new));
+          psum += p[e];
+        }
+        l_run = fmaf(l_run, alpha, psum);
+        m_run = m_new;
+        vec8 pb = pack8<T>(p);
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+          o[mt] = o[mt] * alpha;
+          o[mt] = mma_16x16x32(vr[mt], pb, o[mt]);
+        }
+        if (more) {
+#pragma unroll
+          for (int x = 0; x < 8; ++x) {
+            kr[x] = kn_[x];
+            vr[x] = vn_[x];
+          }
+        }
+      }
+      // The wave that attended the new token also stores it (no other
+      // workgroup of this launch reads that slot).
+      if (fused_append && new_pos >= t_begin * HC_TILE && new_pos < t_end * HC_TILE) {
+        const int64_t tb = row_base + (int64_t)(new_pos / HC_TILE) * HC_TILE_ELEMS;
+        const int tn = new_pos % HC_TILE;
+        for (int d = lane; d < HC_HEAD_DIM; d += 64) {
+          kstore[tb + k_tile_offset(tn, d)] = kn[d];
+          vstore[tb + v_tile_offset(tn, d)] = vn[d];
+        }
+      }
+    }
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+
+    // Wave states -> LDS.  Lane holds O^T[d = 16mt + 4g + j][q = n].
+    if (n < G) {
+      if (g == 0) {
+        s_m[wave][n] = m_run;
+        s_l[wave][n] = l_run;
+      }
+#pragma unroll
+      for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s_o[wave][n][16 * mt + 4 * g + j] = o[mt][j];
+    }
+    __syncthreads();
+
+    const int64_t part = loc.p0 + loc.chunk;
+    for (int idx = threadIdx.x; idx < G * HC_HEAD_DIM; idx += NT) {
+      const int qq = idx / HC_HEAD_DIM, d = idx % HC_HEAD_DIM;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NWAVES; ++w) M = fmaxf(M, s_m[w][qq]);
+      float acc = 0.f, lsum = 0.f;
+#pragma unroll
+      for (int w = 0; w < NWAVES; ++w) {
+        const float f = (s_m[w][qq] == -INFINITY) ? 0.f : fast_exp2(s_m[w][qq] - M);
+        acc = fmaf(s_o[w][qq][d], f, acc);
+        lsum = fmaf(s_l[w][qq], f, lsum);
+      }
+      part_o[(part * G + qq) * HC_HEAD_DIM + d] = acc;
+      if (d == 0) {
+        part_ml[(part * G + qq) * 2 + 0] = M;
+        part_ml[(part * G + qq) * 2 + 1] = lsum;
+      }
+    }
+    if (threadIdx.x == 0 && loc.chunk == 0) {
+      row_info[2 * row] = (int)loc.p0;
+      row_info[2 * row + 1] = loc.nparts;
+    }
+  }
+}
+
+// Fold the partials of one row for one query slot and kMergeSlice channels;
+// the (row, 0, 0) workgroup also advances row_len after a fused append.
+// kMergeGroups part-groups run in parallel so each thread issues only a few
+// independent loads (the merge is latency-bound, not bandwidth-bound).
+constexpr int kMergeSlice = 16;
+constexpr int kMergeGroups = 16;
+constexpr int kMergeThreads = kMergeSlice * kMergeGroups;
+constexpr int kMergeLdsParts = 2048;
+
+__device__ __forceinline__ float block_reduce(float v, float* s_red, bool is_max) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float o = __shfl_xor(v, off, 64);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  if ((tid & 63) == 0) s_red[tid >> 6] = v;
+  __syncthreads();
+  float r = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kMergeThreads / 64; ++w) r = is_max ? fmaxf(r, s_red[w]) : r + s_red[w];
+  __syncthreads();
+  return r;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml, const int* __restrict__ row_info, int G,
+    int* __restrict__ row_len, int advance, T* __restrict__ out) {
+  constexpr int kBatch = 8;  // parts per thread whose loads are in flight together
+  const int row = blockIdx.x, qq = blockIdx.y, d0 = blockIdx.z * kMergeSlice;
+  const int tid = threadIdx.x;
+  const int p0 = row_info[2 * row], np = row_info[2 * row + 1];
+  __shared__ float s_red[kMergeThreads];
+  __shared__ float s_f[kMergeLdsParts];
+  T* o = out + ((int64_t)row * G + qq) * HC_HEAD_DIM + d0;
+  if (advance && qq == 0 && blockIdx.z == 0 && tid == 0) row_len[row] += 1;
+  if (np < 0) {
+    if (tid < kMergeSlice) o[tid] = Elem<T>::from_f32(NAN);
+    return;
+  }
+  const float* ml = part_ml + ((int64_t)p0 * G + qq) * 2;
+  const int dl = tid % kMergeSlice, grp = tid / kMergeSlice;
+  const float* po = part_o + ((int64_t)p0 * G + qq) * HC_HEAD_DIM + d0 + dl;
+  const int64_t pstride = (int64_t)G * HC_HEAD_DIM;
+  // Issue the first batch of partial-output loads before anything depends on
+  // the row maximum, so they overlap the (m, l) loads and reductions.
+  float ov[kBatch];
+#pragma unroll
+  for (int k = 0; k < kBatch; ++k) {
+    const int p = grp + k * kMergeGroups;
+    ov[k] = p < np ? po[p * pstride] : 0.f;
+  }
+  float mv = -INFINITY, lv = 0.f;
+  if (tid < np) {
+    mv = ml[(int64_t)tid * G * 2];
+    lv = ml[(int64_t)tid * G * 2 + 1];
+  }
+  float mx = mv;
+  for (int p = tid + kMergeThreads; p < np; p += kMergeThreads) mx = fmaxf(mx, ml[(int64_t)p * G * 2]);
+  const float M = block_reduce(mx, s_red, true);
+  if (M == -INFINITY) {  // empty row
+    if (tid < kMergeSlice) o[tid] = Elem<T>::from_f32(0.f);
+    return;
+  }
+  float ls = 0.f;
+  if (tid < np) {
+    const float f = fast_exp2(mv - M);
+    ls = lv * f;
+    if (tid < kMergeLdsParts) s_f[tid] = f;
+  }
+  for (int p = tid + kMergeThreads; p < np; p += kMergeThreads) {
+    const float f = fast_exp2(ml[(int64_t)p * G * 2] - M);
+    ls = fmaf(ml[(int64_t)p * G * 2 + 1], f, ls);
+    if (p < kMergeLdsParts) s_f[p] = f;
+  }
+  const float L = block_reduce(ls, s_red, false);  // its barriers also publish s_f
+  auto factor = [&](int p) { return p < kMergeLdsParts ? s_f[p] : fast_exp2(ml[(int64_t)p * G * 2] - M); };
+  float acc = 0.f;
+#pragma unroll
+  for (int k = 0; k < kBatch; ++k) {
+    const int p = grp + k * kMergeGroups;
+    if (p < np) acc = fmaf(ov[k], factor(p), acc);
+  }
+  for (int p = grp + kBatch * kMergeGroups; p < np; p += kMergeGroups) acc = fmaf(po[p * pstride], factor(p), acc);
+  s_red[tid] = acc;
+  __syncthreads();
+  if (grp == 0) {
+    float a = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMergeGroups; ++k) a += s_red[k * kMergeSlice + dl];
+    o[dl] = Elem<T>::from_f32(a / L);
+  }
+}
+
+constexpr int kDecodeWaves = 4;
+
+int64_t decode_num_parts(const int* host_row_len, int rows, int tiles_per_wave) {
+  const int chunk_tiles = kDecodeWaves * tiles_per_wave;
+  int64_t total = 0;
+  for (int r = 0; r < rows; ++r) {
+    int64_t nt = (host_row_len[r] + HC_TILE - 1) / HC_TILE;
+    total += nt > 0 ? (nt + chunk_tiles - 1) / chunk_tiles : 1;
+  }
+  return total;
+}
+
+// Workspace: [row_info: (first part, part count) per row, padded to 256 B]
+//            [part_ml: parts*G*2 f32][part_o: parts*G*128 f32]
+// Every field is written before it is read within one call, so the buffer
+// needs no initialisation and may be reused freely by calls on one stream.
+static size_t workspace_head(int rows) { return ((size_t)rows * 2 * sizeof(int) + 255) / 256 * 256; }
+
+size_t decode_workspace_bytes_rows(int rows, int group, int64_t num_parts) {
+  if (num_parts <= 0 || group <= 0) return workspace_head(rows);
+  return workspace_head(rows) + (size_t)num_parts * (size_t)group * (HC_HEAD_DIM + 2) * sizeof(float);
+}
+
+template <typename T>
+static int launch_decode(const void* q, void* kstore, void* vstore, const int64_t* row_tile_off, int* row_len,
+                         const int* row_order, int rows, int G, float scale, const void* k_new, const void* v_new,
+                         void* out, void* workspace, size_t workspace_bytes, int64_t grid_parts, int tiles_per_wave,
+                         hipStream_t stream) {
+  if (grid_parts < rows)
+    return set_error(HC_ERR_INVALID, "hc_decode_attn: num_parts=%lld below the row count %d", (long long)grid_parts,
+                     rows);
+  if (grid_parts > 0x7fffffffLL) return set_error(HC_ERR_INVALID, "hc_decode_attn: too many parts");
+  const size_t need = decode_workspace_bytes_rows(rows, G, grid_parts);
+  if (!workspace || workspace_bytes < need)
+    return set_error(HC_ERR_INVALID, "hc_decode_attn: workspace too small (%zu < %zu bytes)", workspace_bytes, need);
+  int* row_info = reinterpret_cast<int*>(workspace);
+  float* part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + workspace_head(rows));
+  float* part_o = part_ml + (size_t)grid_parts * G * 2;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves>), dim3((unsigned)grid_parts), dim3(kDecodeWaves * 64),
+                     0, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off, row_len, row_order, rows, G,
+                     scale_log2, tiles_per_wave, (const T*)k_new, (const T*)v_new, part_o, part_ml, row_info);
+  int rc = check_launch("hc_decode_attn(partial)");
+  if (rc) return rc;
+  hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(rows, G, HC_HEAD_DIM / kMergeSlice),
+                     dim3(kMergeSlice * kMergeGroups), 0, stream, part_o, part_ml, row_info, G, row_len,
+                     k_new ? 1 : 0, (T*)out);
+  return check_launch("hc_decode_attn(merge)");
+}
+
+}  // namespace hc
+
+using namespace hc;
+
+extern "C" size_t hc_decode_workspace_size(int rows, int group, int64_t num_parts) {
+  return decode_workspace_bytes_rows(rows, group, num_parts);
+}
+
+extern "C" int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, int tiles_per_wave) {
+  if (!host_row_len || rows < 0 || tiles_per_wave <= 0) return -1;
+  return decode_num_parts(host_row_len, rows, tiles_per_wave);
+}
+
+extern "C" int hc_decode_attn(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
+                              int32_t* row_len, const int32_t* row_order, int rows, int group, float scale,
+                              const void* k_new, const void* v_new, void* out, void* workspace,
+                              size_t workspace_bytes, int64_t num_parts, int tiles_per_wave, void* stream) {
+  clear_error();
+  if (rows < 0 || group < 1 || group > 16)
+    return set_error(HC_ERR_INVALID, "hc_decode_attn: rows=%d group=%d (group must be 1..16)", rows, group);
+  if (tiles_per_wave < 1 || tiles_per_wave > 4096)
+    return set_error(HC_ERR_INVALID, "hc_decode_attn: tiles_per_wave=%d out of range", tiles_per_wave);
+  if (rows == 0) return HC_OK;
+  if (!q || !kstore || !vstore || !row_tile_off || !row_len || !out)
+    return set_error(HC_ERR_INVALID, "hc_decode_attn: null pointer argument");
+  if ((k_new == nullptr) != (v_new == nullptr))
+    return set_error(HC_ERR_INVALID, "hc_decode_attn: k_new and v_new must be given together");
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case HC_DTYPE_BF16:
+      return launch_decode<__bf16>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
+                                   v_new, out, workspace, workspace_bytes, num_parts, tiles_per_wave, s);
+    case HC_DTYPE_F16:
+      return launch_decode<_Float16>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
+                                     v_new, out, workspace, workspace_bytes, num_parts, tiles_per_wave, s);
+    case HC_DTYPE_F32:
+      return launch_decode<float>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
+                                  v_new, out, workspace, workspace_bytes, num_parts, tiles_per_wave, s);
+    default:
+      return set_error(HC_ERR_INVALID, "hc_decode_attn: unknown dtype %d", dtype);
+  }
+}

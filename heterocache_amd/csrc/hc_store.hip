@@ -1,0 +1,255 @@
+// Writers and readers of the tiled ragged per-head KV store.
+//
+//   hc_gather_store  rows of a natural-layout [.., tokens, 128] source (device
+//                    memory or a device-mapped host-pinned buffer) gathered by
+//                    an index list into store slots [0, count) of a row.
+//                    Serves the prefill keep-head copy
+//                    (heterocache/cache_utils.py:914-937), the compressed-head
+//                    gather + index_copy_ (heterocache/cache_utils.py:854-877)
+//                    and the retrieval upload from the host tier
+//                    (heterocache/cache_utils.py:1097-1123).
+//   hc_append        one decode token per row at slot len[row], then len+1
+//                    (heterocache/cache_utils.py:970-1005).
+//   hc_store_read    unpack store slots [0, count) of rows back to natural
+//                    layout (diagnostics and tests).
+#include "hc_common.h"
+#include "hc_internal.h"
+
+namespace hc {
+
+// One workgroup moves one 32-token tile of one job through LDS: natural-layout
+// 16-byte reads in, tile-permuted 16-byte writes out.
+template <typename T>
+__global__ __launch_bounds__(256) void gather_store_kernel(
+    const T* __restrict__ src_k, const T* __restrict__ src_v, const int64_t* __restrict__ src_off,
+    int64_t src_tok_stride, int src_len, const int32_t* __restrict__ idx, const int64_t* __restrict__ idx_off,
+    const int32_t* __restrict__ count, const int32_t* __restrict__ dst_row, T* __restrict__ kstore,
+    T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off, const int32_t* __restrict__ trigger) {
+  if (trigger && *trigger == 0) return;
+  const int job = blockIdx.y;
+  const int tile = blockIdx.x;
+  const int n = count[job];
+  const int tok0 = tile * HC_TILE;
+  if (tok0 >= n) return;
+  const int valid = min(HC_TILE, n - tok0);
+
+  __shared__ T sk[HC_TILE][HC_HEAD_DIM + 8];
+  __shared__ T sv[HC_TILE][HC_HEAD_DIM + 8];
+
+  const T* bk = src_k + src_off[job];
+  const T* bv = src_v + src_off[job];
+  const int32_t* ix = idx ? idx + idx_off[job] : nullptr;
+  // 32 tokens x 16 chunks of 8 elements.
+  for (int c = threadIdx.x; c < HC_TILE * 16; c += 256) {
+    const int t = c >> 4, ch = c & 15;
+    if (t < valid) {
+      // Positions are clamped into the source like the reference's
+      // clamp(max=L-1) before its gather (heterocache/cache_utils.py:852).
+      const int64_t stok = ix ? (int64_t)min(max(ix[tok0 + t], 0), src_len - 1) : (int64_t)(tok0 + t);
+      const int64_t off = stok * src_tok_stride + ch * 8;
+      typename Elem<T>::vec8 a = load8<T>(bk + off);
+      typename Elem<T>::vec8 b = load8<T>(bv + off);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (sizeof(T) == 4) {
+          sk[t][ch * 8 + e] = e < 4 ? a.lo[e] : a.hi[e - 4];
+          sv[t][ch * 8 + e] = e < 4 ? b.lo[e] : b.hi[e - 4];
+        } else {
+          sk[t][ch * 8 + e] = a[e];
+          sv[t][ch * 8 + e] = b[e];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const int64_t tile_base = (row_tile_off[dst_row[job]] + tile) * (int64_t)HC_TILE_ELEMS;
+  T* kt = kstore + tile_base;
+  T* vt = vstore + tile_base;
+  for (int c = threadIdx.x; c < HC_TILE_ELEMS / 8; c += 256) {
+    // K chunk c = ((h*4+s)*4+g)*16+m : token 16h+m, channels 32s+8g+[0,8).
+    {
+      const int m = c & 15, g = (c >> 4) & 3, s = (c >> 6) & 3, h = c >> 8;
+      const int t = 16 * h + m;
+      if (t < valid) {
+        float v8[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v8[e] = Elem<T>::to_f32(sk[t][32 * s + 8 * g + e]);
+        *reinterpret_cast<typename Elem<T>::vec8*>(kt + c * 8) = pack8<T>(v8);
+      }
+    }
+    // V chunk c = (mt*4+g)*16+nn : channel 16mt+nn, tokens 16*(i/4)+4g+i%4.
+    {
+      const int nn = c & 15, g = (c >> 4) & 3, mt = c >> 6;
+      const int d = 16 * mt + nn;
+      if (valid == HC_TILE) {
+        float v8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v8[i] = Elem<T>::to_f32(sv[16 * (i >> 2) + 4 * g + (i & 3)][d]);
+        *reinterpret_cast<typename Elem<T>::vec8*>(vt + c * 8) = pack8<T>(v8);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int t = 16 * (i >> 2) + 4 * g + (i & 3);
+          if (t < valid) vt[c * 8 + i] = sv[t][d];
+        }
+      }
+    }
+  }
+}
+
+// One wave per row: store the row's new token at slot len, then len += 1.
+template <typename T>
+__global__ __launch_bounds__(64) void append_kernel(const T* __restrict__ k_new, const T* __restrict__ v_new,
+                                                    int64_t src_row_stride, T* __restrict__ kstore,
+                                                    T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off,
+                                                    int32_t* __restrict__ row_len, const int32_t* __restrict__ row_cap,
+                                                    int32_t* __restrict__ status) {
+  const int row = blockIdx.x;
+  const int len = row_len[row];
+  if (len >= row_cap[row]) {
+    if (threadIdx.x == 0 && status) atomicOr(status, 1);
+    return;
+  }
+  const int tile = len / HC_TILE, t = len % HC_TILE;
+  const int64_t base = (row_tile_off[row] + tile) * (int64_t)HC_TILE_ELEMS;
+  const T* ks = k_new + (int64_t)row * src_row_stride;
+  const T* vs = v_new + (int64_t)row * src_row_stride;
+  for (int d = threadIdx.x; d < HC_HEAD_DIM; d += 64) {
+    kstore[base + k_tile_offset(t, d)] = ks[d];
+    vstore[base + v_tile_offset(t, d)] = vs[d];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) row_len[row] = len + 1;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void store_read_kernel(const T* __restrict__ kstore, const T* __restrict__ vstore,
+                                                         const int64_t* __restrict__ row_tile_off,
+                                                         const int32_t* __restrict__ rows_sel, int count,
+                                                         T* __restrict__ dst_k, T* __restrict__ dst_v) {
+  const int j = blockIdx.y;
+  const int row = rows_sel[j];
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)count * HC_HEAD_DIM) return;
+  const int tok = (int)(e / HC_HEAD_DIM), d = (int)(e % HC_HEAD_DIM);
+  const int64_t base = (row_tile_off[row] + tok / HC_TILE) * (int64_t)HC_TILE_ELEMS;
+  dst_k[(int64_t)j * count * HC_HEAD_DIM + e] = kstore[base + k_tile_offset(tok % HC_TILE, d)];
+  dst_v[(int64_t)j * count * HC_HEAD_DIM + e] = vstore[base + v_tile_offset(tok % HC_TILE, d)];
+}
+
+template <typename T>
+static int launch_gather_store(const void* src_k, const void* src_v, const int64_t* src_off, int64_t src_tok_stride,
+                               int src_len, const int32_t* idx, const int64_t* idx_off, const int32_t* count,
+                               const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off,
+                               int njobs, int max_count, const int32_t* trigger, hipStream_t s) {
+  dim3 grid((max_count + HC_TILE - 1) / HC_TILE, njobs);
+  hipLaunchKernelGGL((gather_store_kernel<T>), grid, dim3(256), 0, s, (const T*)src_k, (const T*)src_v, src_off,
+                     src_tok_stride, src_len, idx, idx_off, count, dst_row, (T*)kstore, (T*)vstore, row_tile_off, trigger);
+  return check_launch("hc_gather_store");
+}
+
+// Translate a pointer into host-pinned memory to its device-mapped address.
+static int map_host_ptr(const void* host, const void** dev) {
+  void* d = nullptr;
+  hipError_t e = hipHostGetDevicePointer(&d, const_cast<void*>(host), 0);
+  if (e != hipSuccess)
+    return set_error(HC_ERR_INVALID, "source is not device-mapped pinned host memory: %s", hipGetErrorString(e));
+  *dev = d;
+  return HC_OK;
+}
+
+}  // namespace hc
+
+using namespace hc;
+
+extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, int src_is_host,
+                               const int64_t* src_off, int64_t src_tok_stride, int src_len, const int32_t* idx,
+                               const int64_t* idx_off, const int32_t* count, const int32_t* dst_row, void* kstore,
+                               void* vstore, const int64_t* row_tile_off, int njobs, int max_count,
+                               const int32_t* trigger, void* stream) {
+  clear_error();
+  if (njobs < 0 || max_count < 0 || njobs > 65535)
+    return set_error(HC_ERR_INVALID, "hc_gather_store: njobs=%d max_count=%d", njobs, max_count);
+  if (njobs == 0 || max_count == 0) return HC_OK;
+  if (src_len <= 0) return set_error(HC_ERR_INVALID, "hc_gather_store: src_len=%d", src_len);
+  if (!idx && max_count > src_len)
+    return set_error(HC_ERR_INVALID, "hc_gather_store: identity copy of %d tokens from a %d-token source", max_count,
+                     src_len);
+  if (!src_k || !src_v || !src_off || !count || !dst_row || !kstore || !vstore || !row_tile_off ||
+      (idx && !idx_off))
+    return set_error(HC_ERR_INVALID, "hc_gather_store: null pointer argument");
+  if (src_tok_stride < HC_HEAD_DIM || (src_tok_stride % 8) != 0)
+    return set_error(HC_ERR_INVALID, "hc_gather_store: token stride %lld must be >=128 and a multiple of 8",
+                     (long long)src_tok_stride);
+  const void* sk = src_k;
+  const void* sv = src_v;
+  if (src_is_host) {
+    int rc = map_host_ptr(src_k, &sk);
+    if (rc) return rc;
+    rc = map_host_ptr(src_v, &sv);
+    if (rc) return rc;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case HC_DTYPE_BF16:
+      return launch_gather_store<__bf16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
+                                         vstore, row_tile_off, njobs, max_count, trigger, s);
+    case HC_DTYPE_F16:
+      return launch_gather_store<_Float16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
+                                           vstore, row_tile_off, njobs, max_count, trigger, s);
+    case HC_DTYPE_F32:
+      return launch_gather_store<float>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
+                                        vstore, row_tile_off, njobs, max_count, trigger, s);
+    default:
+      return set_error(HC_ERR_INVALID, "hc_gather_store: unknown dtype %d", dtype);
+  }
+}
+
+extern "C" int hc_append(int dtype, const void* k_new, const void* v_new, int64_t src_row_stride, void* kstore,
+                         void* vstore, const int64_t* row_tile_off, int32_t* row_len, const int32_t* row_cap,
+                         int rows, int32_t* status, void* stream) {
+  clear_error();
+  if (rows < 0) return set_error(HC_ERR_INVALID, "hc_append: rows=%d", rows);
+  if (rows == 0) return HC_OK;
+  if (!k_new || !v_new || !kstore || !vstore || !row_tile_off || !row_len || !row_cap)
+    return set_error(HC_ERR_INVALID, "hc_append: null pointer argument");
+  if (src_row_stride < HC_HEAD_DIM)
+    return set_error(HC_ERR_INVALID, "hc_append: row stride %lld < 128", (long long)src_row_stride);
+  hipStream_t s = (hipStream_t)stream;
+#define HC_APPEND(T)                                                                                            \
+  hipLaunchKernelGGL((append_kernel<T>), dim3(rows), dim3(64), 0, s, (const T*)k_new, (const T*)v_new,          \
+                     src_row_stride, (T*)kstore, (T*)vstore, row_tile_off, row_len, row_cap, status);           \
+  return check_launch("hc_append");
+  switch (dtype) {
+    case HC_DTYPE_BF16: { HC_APPEND(__bf16) }
+    case HC_DTYPE_F16: { HC_APPEND(_Float16) }
+    case HC_DTYPE_F32: { HC_APPEND(float) }
+    default:
+      return set_error(HC_ERR_INVALID, "hc_append: unknown dtype %d", dtype);
+  }
+#undef HC_APPEND
+}
+
+extern "C" int hc_store_read(int dtype, const void* kstore, const void* vstore, const int64_t* row_tile_off,
+                             const int32_t* rows_sel, int nrows, int count, void* dst_k, void* dst_v, void* stream) {
+  clear_error();
+  if (nrows < 0 || count < 0 || nrows > 65535) return set_error(HC_ERR_INVALID, "hc_store_read: bad sizes");
+  if (nrows == 0 || count == 0) return HC_OK;
+  if (!kstore || !vstore || !row_tile_off || !rows_sel || !dst_k || !dst_v)
+    return set_error(HC_ERR_INVALID, "hc_store_read: null pointer argument");
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid((unsigned)(((int64_t)count * HC_HEAD_DIM + 255) / 256), nrows);
+#define HC_READ(T)                                                                                         \
+  hipLaunchKernelGGL((store_read_kernel<T>), grid, dim3(256), 0, s, (const T*)kstore, (const T*)vstore,    \
+                     row_tile_off, rows_sel, count, (T*)dst_k, (T*)dst_v);                                 \
+  return check_launch("hc_store_read");
+  switch (dtype) {
+    case HC_DTYPE_BF16: { HC_READ(__bf16) }
+    case HC_DTYPE_F16: { HC_READ(_Float16) }
+    case HC_DTYPE_F32: { HC_READ(float) }
+    default:
+      return set_error(HC_ERR_INVALID, "hc_store_read: unknown dtype %d", dtype);
+  }
+#undef HC_READ
+}

@@ -1,0 +1,169 @@
+"""Thin torch-tensor wrappers over the libhc C ABI.
+
+Torch provides device memory and streams; every computation happens in the
+HIP kernels of libhc.so.  Shapes, dtypes and devices are checked here, on the
+host, before any kernel is launched.
+"""
+import ctypes
+
+import numpy as np
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+TILE = 32
+
+_DTYPES = {torch.float32: _lib.HC_DTYPE_F32, torch.float16: _lib.HC_DTYPE_F16, torch.bfloat16: _lib.HC_DTYPE_BF16}
+
+DEFAULT_TILES_PER_WAVE = 4
+
+
+def dtype_code(dt):
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dt}; expected float32, float16 or bfloat16") from None
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("libhc ops need tensors on a ROCm device")
+
+
+class Workspace:
+    """Grow-only, zero-initialised per-device scratch buffer.
+
+    The decode kernel keeps self-resetting counters at the head of its
+    workspace, so the buffer is zero-filled when (re)allocated and then reused
+    by launches on one stream.  Work on another stream needs its own instance.
+    """
+
+    def __init__(self):
+        self._buf = {}
+
+    def get(self, device, nbytes):
+        dev = torch.device(device)
+        key = dev.index if dev.index is not None else torch.cuda.current_device()
+        buf = self._buf.get(key)
+        if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                torch.cuda.current_stream(dev).synchronize()
+            buf = torch.zeros(max(nbytes, 1 << 22), dtype=torch.uint8, device=dev)
+            self._buf[key] = buf
+        return buf
+
+
+WORKSPACE = Workspace()
+
+
+def decode_num_parts(host_row_len, tiles_per_wave=DEFAULT_TILES_PER_WAVE):
+    lens = np.ascontiguousarray(host_row_len, dtype=np.int32)
+    n = _lib.load().hc_decode_num_parts(lens.ctypes.data_as(ctypes.c_void_p), len(lens), tiles_per_wave)
+    if n < 0:
+        raise ValueError("bad arguments to hc_decode_num_parts")
+    return n
+
+
+def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, out=None, row_order=None,
+                k_new=None, v_new=None, tiles_per_wave=DEFAULT_TILES_PER_WAVE, stream=None, workspace=None):
+    """out[r, g] = softmax(scale * q[r, g] . K_r^T) V_r over row_len[r] tokens.
+
+    q: [rows, G, 128]; host_row_len: host copy of the lengths (sizes the grid).
+    With k_new/v_new [rows, 128] the new token is appended and attended in the
+    same launch; row_len advances by one (the caller advances its mirror).
+    """
+    lib = _lib.load()
+    _require_cuda(q, kstore, vstore, row_tile_off, row_len, row_order, k_new, v_new)
+    if q.dim() != 3 or q.shape[-1] != HEAD_DIM:
+        raise ValueError(f"q must be [rows, G, {HEAD_DIM}], got {tuple(q.shape)}")
+    rows, G, _ = q.shape
+    if row_len.numel() != rows or row_tile_off.numel() != rows or len(host_row_len) != rows:
+        raise ValueError("row metadata does not match q's row count")
+    if row_len.dtype != torch.int32 or row_tile_off.dtype != torch.int64:
+        raise TypeError("row_len must be int32 and row_tile_off int64")
+    if kstore.dtype != q.dtype or vstore.dtype != q.dtype:
+        raise TypeError("q and the store must share a dtype")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new go together")
+    if k_new is not None:
+        if k_new.shape != (rows, HEAD_DIM) or v_new.shape != (rows, HEAD_DIM):
+            raise ValueError(f"k_new/v_new must be [{rows}, {HEAD_DIM}]")
+        if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+            raise TypeError("k_new/v_new must share q's dtype")
+        k_new = k_new.contiguous()
+        v_new = v_new.contiguous()
+        host_row_len = np.asarray(host_row_len) + 1
+    if row_order is not None and (row_order.dtype != torch.int32 or row_order.numel() != rows):
+        raise ValueError("row_order must be an int32 permutation of the rows")
+    q = q.contiguous()
+    if out is None:
+        out = torch.empty_like(q)
+    nparts = decode_num_parts(host_row_len, tiles_per_wave)
+    nbytes = lib.hc_decode_workspace_size(rows, G, nparts)
+    ws = workspace if workspace is not None else WORKSPACE.get(q.device, nbytes)
+    _lib.check(lib.hc_decode_attn(dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
+                                  _ptr(row_len), _ptr(row_order), rows, G, float(scale), _ptr(k_new), _ptr(v_new),
+                                  _ptr(out), _ptr(ws), ws.numel(), nparts, tiles_per_wave, _stream(stream)))
+    return out
+
+
+def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore, vstore, row_tile_off,
+                 max_count, src_is_host=False, trigger=None, stream=None):
+    """store[dst_row[j]][i] = src[src_off[j] + idx[idx_off[j] + i] * stride], i < count[j]."""
+    lib = _lib.load()
+    _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger)
+    if src_is_host:
+        if src_k.is_cuda or not src_k.is_pinned() or not src_v.is_pinned():
+            raise ValueError("host sources must be pinned CPU tensors")
+    else:
+        _require_cuda(src_k, src_v)
+    if src_k.dtype != kstore.dtype or src_v.dtype != vstore.dtype:
+        raise TypeError("source and store dtypes differ")
+    for name, t, dt in (("src_off", src_off, torch.int64), ("count", count, torch.int32),
+                        ("dst_row", dst_row, torch.int32), ("idx", idx, torch.int32),
+                        ("idx_off", idx_off, torch.int64), ("trigger", trigger, torch.int32)):
+        if t is not None and t.dtype != dt:
+            raise TypeError(f"{name} must be {dt}")
+    njobs = count.numel()
+    _lib.check(lib.hc_gather_store(dtype_code(kstore.dtype), _ptr(src_k), _ptr(src_v), int(bool(src_is_host)),
+                                   _ptr(src_off), int(src_tok_stride), int(src_len), _ptr(idx), _ptr(idx_off), _ptr(count),
+                                   _ptr(dst_row), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off), njobs,
+                                   int(max_count), _ptr(trigger), _stream(stream)))
+
+
+def append(k_new, v_new, kstore, vstore, row_tile_off, row_len, row_cap, status=None, stream=None):
+    """Write k_new/v_new [rows, 128] at slot row_len[r] of every row, then row_len += 1."""
+    lib = _lib.load()
+    _require_cuda(k_new, v_new, kstore, vstore, row_tile_off, row_len, row_cap, status)
+    rows = row_len.numel()
+    if k_new.shape != (rows, HEAD_DIM) or v_new.shape != (rows, HEAD_DIM):
+        raise ValueError(f"new k/v must be [{rows}, {HEAD_DIM}]")
+    k_new = k_new.contiguous()
+    v_new = v_new.contiguous()
+    _lib.check(lib.hc_append(dtype_code(kstore.dtype), _ptr(k_new), _ptr(v_new), HEAD_DIM, _ptr(kstore),
+                             _ptr(vstore), _ptr(row_tile_off), _ptr(row_len), _ptr(row_cap), rows, _ptr(status),
+                             _stream(stream)))
+
+
+def store_read(kstore, vstore, row_tile_off, rows_sel, count, stream=None):
+    """Natural-layout copy [len(rows_sel), count, 128] of store slots [0, count)."""
+    lib = _lib.load()
+    _require_cuda(kstore, vstore, row_tile_off)
+    rows_sel = torch.as_tensor(rows_sel, dtype=torch.int32, device=kstore.device)
+    n = rows_sel.numel()
+    dk = torch.empty((n, count, HEAD_DIM), dtype=kstore.dtype, device=kstore.device)
+    dv = torch.empty_like(dk)
+    _lib.check(lib.hc_store_read(dtype_code(kstore.dtype), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
+                                 _ptr(rows_sel), n, int(count), _ptr(dk), _ptr(dv), _stream(stream)))
+    return dk, dv

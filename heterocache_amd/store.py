@@ -1,0 +1,159 @@
+"""Ragged per-head KV store of one layer (tiled head-major layout).
+
+Replaces the reference's paged pool (`key_pools` / `value_pools` /
+`block_tables` / `heads_len`, heterocache/cache_utils.py:693-766): instead of
+256-token pages reached through a block table, every row (b, kv-head) owns
+one contiguous run of 32-token tiles sized for its whole lifetime
+(prefill budget + max_gen_len).  The reference sizes pages the same way
+(cache_utils.py:719-722), so nothing is lost by dropping the indirection.
+"""
+import numpy as np
+import torch
+
+from . import ops
+
+TILE = ops.TILE
+HEAD_DIM = ops.HEAD_DIM
+
+
+class KVStore:
+    """Device buffers + row metadata of one layer's compressed cache.
+
+    row_caps: capacity in tokens of every row (rounded up to whole tiles).
+    Host mirror `host_len` tracks row_len exactly: lengths only change through
+    this object's methods, so the grid of every kernel is sized without a
+    device->host sync.
+    """
+
+    def __init__(self, row_caps, dtype, device):
+        caps = np.asarray(row_caps, dtype=np.int64)
+        if (caps < 0).any():
+            raise ValueError("negative row capacity")
+        tiles = (caps + TILE - 1) // TILE
+        off = np.zeros(len(caps), dtype=np.int64)
+        if len(caps) > 1:
+            off[1:] = np.cumsum(tiles)[:-1]
+        self.rows = len(caps)
+        self.dtype = dtype
+        self.device = torch.device(device)
+        self.host_cap = tiles * TILE
+        self.host_tile_off = off
+        self.total_tiles = int(tiles.sum())
+        n = max(self.total_tiles, 1) * TILE * HEAD_DIM
+        self.k = torch.zeros(n, dtype=dtype, device=self.device)
+        self.v = torch.zeros(n, dtype=dtype, device=self.device)
+        self.row_tile_off = torch.as_tensor(off, dtype=torch.int64).to(self.device)
+        self.row_cap = torch.as_tensor(self.host_cap, dtype=torch.int32).to(self.device)
+        self.row_len = torch.zeros(self.rows, dtype=torch.int32, device=self.device)
+        self.host_len = np.zeros(self.rows, dtype=np.int64)
+        self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.row_order = torch.arange(self.rows, dtype=torch.int32, device=self.device)
+
+    # -- bookkeeping -------------------------------------------------------
+    def bytes_per_token(self):
+        return 2 * HEAD_DIM * self.k.element_size()
+
+    def kv_bytes(self):
+        """Algorithmic K+V bytes one decode attention pass streams."""
+        return int(self.host_len.sum()) * self.bytes_per_token()
+
+    def set_lengths(self, lens, rows=None):
+        rows = np.arange(self.rows) if rows is None else np.asarray(rows, dtype=np.int64)
+        lens = np.asarray(lens, dtype=np.int64)
+        if (lens > self.host_cap[rows]).any() or (lens < 0).any():
+            raise RuntimeError("row length outside its capacity")
+        self.host_len[rows] = lens
+        idx = torch.as_tensor(rows, dtype=torch.int64).to(self.device)
+        self.row_len.index_copy_(0, idx, torch.as_tensor(lens, dtype=torch.int32).to(self.device))
+        # Longest rows are scheduled first; appends keep this order.
+        order = np.argsort(-self.host_len, kind="stable").astype(np.int32)
+        self.row_order = torch.as_tensor(order).to(self.device)
+
+    # -- writers -----------------------------------------------------------
+    def write_rows(self, src_k, src_v, src_bh, rows, counts, idx=None, src_is_host=False, stream=None,
+                   trigger=None, set_len=True):
+        """store[rows[j]][i] = src[b_j, h_j, idx[j][i]] (or token i), i < counts[j].
+
+        src_k / src_v: [B, H, L, 128] with unit channel stride (any other
+        strides), on the device or host-pinned.  src_bh: [jobs, 2] (b, h) of
+        each job's source head.  idx: [jobs, M] int32 device tensor of source
+        positions (None copies positions 0..count-1).
+        """
+        rows = np.asarray(rows, dtype=np.int64)
+        counts = np.asarray(counts, dtype=np.int64)
+        src_bh = np.asarray(src_bh, dtype=np.int64).reshape(-1, 2)
+        if len(rows) == 0:
+            return
+        if len(src_bh) != len(rows) or len(counts) != len(rows):
+            raise ValueError("one (b, h) source and one count per destination row")
+        if (counts > self.host_cap[rows]).any():
+            raise RuntimeError("write exceeds a row's capacity")
+        if src_k.shape != src_v.shape or src_k.stride() != src_v.stride():
+            raise ValueError("K and V sources must have one shape and stride")
+        if src_k.dim() != 4 or src_k.shape[-1] != HEAD_DIM or src_k.stride(-1) != 1:
+            raise ValueError("sources must be [B, H, L, 128] with unit channel stride")
+        if src_k.dtype != self.dtype:
+            raise TypeError("source dtype differs from the store's")
+        B, H, L, _ = src_k.shape
+        if (src_bh[:, 0] >= B).any() or (src_bh[:, 1] >= H).any() or (src_bh < 0).any():
+            raise ValueError("source head out of range")
+        if idx is None and (counts > L).any():
+            raise ValueError("count exceeds the source length")
+        tok_stride = src_k.stride(2)
+        src_off = src_bh[:, 0] * src_k.stride(0) + src_bh[:, 1] * src_k.stride(1)
+        esz = src_k.element_size()
+        if (src_k.data_ptr() % 16) or (src_v.data_ptr() % 16) or (tok_stride * esz) % 16 or \
+                ((src_off * esz) % 16).any():
+            raise ValueError("sources must be 16-byte aligned per token")
+        dev = self.device
+        idx_off = None
+        if idx is not None:
+            if idx.dtype != torch.int32 or idx.dim() != 2 or idx.shape[0] != len(rows):
+                raise ValueError("idx must be int32 [jobs, M]")
+            if (counts > idx.shape[1]).any():
+                raise ValueError("count exceeds the index list")
+            idx = idx.contiguous()
+            idx_off = torch.arange(len(rows), dtype=torch.int64, device=dev) * idx.shape[1]
+        ops.gather_store(src_k, src_v, torch.as_tensor(src_off).to(dev), tok_stride, L, idx, idx_off,
+                         torch.as_tensor(counts, dtype=torch.int32).to(dev),
+                         torch.as_tensor(rows, dtype=torch.int32).to(dev), self.k, self.v, self.row_tile_off,
+                         int(counts.max()), src_is_host=src_is_host, trigger=trigger, stream=stream)
+        if set_len:
+            self.set_lengths(counts, rows)
+
+    def append(self, k_new, v_new, stream=None):
+        """Write one token per row at slot len and advance every length by one.
+
+        k_new / v_new: [rows, 128].  Raises like the reference's "OOM" when a
+        row is full (heterocache/cache_utils.py:988-990).
+        """
+        if (self.host_len + 1 > self.host_cap).any():
+            full = np.nonzero(self.host_len + 1 > self.host_cap)[0].tolist()
+            raise RuntimeError(f"KV store OOM: rows {full} are at capacity")
+        ops.append(k_new, v_new, self.k, self.v, self.row_tile_off, self.row_len, self.row_cap, self.status,
+                   stream=stream)
+        self.host_len += 1
+
+    # -- readers -----------------------------------------------------------
+    def read_rows(self, rows, count):
+        if count > int(self.host_cap[np.asarray(rows, dtype=np.int64)].min()):
+            raise ValueError("read past a row's capacity")
+        return ops.store_read(self.k, self.v, self.row_tile_off, rows, count)
+
+    def attend(self, q, scale, out=None, k_new=None, v_new=None, tiles_per_wave=ops.DEFAULT_TILES_PER_WAVE,
+               stream=None):
+        """Decode attention of q [rows, G, 128] over every row's tokens.
+
+        With k_new / v_new [rows, 128] the decode append happens in the same
+        launch: the new token is attended, stored at slot len and every
+        length advances by one.
+        """
+        if k_new is not None and (self.host_len + 1 > self.host_cap).any():
+            full = np.nonzero(self.host_len + 1 > self.host_cap)[0].tolist()
+            raise RuntimeError(f"KV store OOM: rows {full} are at capacity")
+        out = ops.decode_attn(q, self.k, self.v, self.row_tile_off, self.row_len, self.host_len, scale, out=out,
+                              row_order=self.row_order, k_new=k_new, v_new=v_new, tiles_per_wave=tiles_per_wave,
+                              stream=stream)
+        if k_new is not None:
+            self.host_len += 1
+        return out

@@ -1,0 +1,378 @@
+"""Numpy restatement of HeteroCache's compressed-KV attention path (oracle).
+
+TEST INFRASTRUCTURE ONLY -- imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, never by the product.
+
+Conventions: arrays are numpy; a "row" is one (batch, kv-head) pair, row =
+b * Hkv + h; tensors follow the reference's [B, heads, seq, d] layout.
+
+Tie-break (stated, the reference's torch.topk order on its GPU is
+implementation defined): among equal scores the LOWER token index ranks
+first.  Every selection here is "sort by (-score, index), take the first k".
+
+Pinning of each function (beyond its own formula) -- tests/test_oracle.py:
+  get_compress_len / prefill_caps / capacity_f64  hand vectors from the
+      reference's numbers (49629 @128K, 2048 @config-0, f32-vs-f64 edge).
+  softmax / pooling / group max   torch.nn.functional (softmax, avg_pool1d,
+      max_pool1d) on random inputs, and closed forms (uniform scores).
+  topk_select                     brute force over all subsets on tiny
+      inputs; torch.topk on distinct scores.
+  window_scores                   reduces to last_query_scores at W=1 and to
+      snapkv_update_kv at G=1 (the two reference functions it generalises).
+  decode_attention                float64 closed form vs torch SDPA; a
+      one-token row returns V exactly; uniform keys give the mean of V.
+  drift_check                     overlap of identical sets is 1, of disjoint
+      sets is 0; statistics.median.
+  retrieval_indices               ascending-prefix rule on a hand example.
+  reorder_plan                    the committed Llama-3.1-8B head JSON, layer
+      23 (leader order quirk) worked out by hand.
+"""
+import math
+import statistics
+
+import numpy as np
+
+HEAD_DIM = 128
+
+
+# --------------------------------------------------------------------------
+# a1, a2: budgets
+# --------------------------------------------------------------------------
+def get_compress_len(compression_ratio, full_heads, ori_len, num_kv_heads):
+    """heterocache/cache_utils.py:15-16 (float64, truncation toward zero)."""
+    return int((compression_ratio * num_kv_heads - full_heads) * ori_len / (num_kv_heads - full_heads))
+
+
+def prefill_caps(base, ratios, seq_len):
+    """Per-head prefill budget, float32 product then truncation, clamped to L.
+
+    heterocache/cache_utils.py:793-799: caps = (base * ratios_f32).int();
+    keep_lens = clamp(caps, max=L).
+    """
+    r = np.asarray(ratios, dtype=np.float32)
+    caps = (np.float32(base) * r).astype(np.float32)
+    caps = np.trunc(caps).astype(np.int64)
+    return np.minimum(caps, seq_len)
+
+
+def capacity_f64(base, ratio, seq_len):
+    """Float64 budget used for pool sizing and retrieval lengths.
+
+    heterocache/cache_utils.py:714-718 and :1084-1087: min(int(base*ratio), L).
+    """
+    return max(min(int(base * ratio), seq_len), 0)
+
+
+# --------------------------------------------------------------------------
+# dtype emulation
+# --------------------------------------------------------------------------
+def round_bf16(x):
+    """Round float32 values to bfloat16 (round-to-nearest-even), as float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    u = x.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).reshape(x.shape)
+
+
+def round_to(x, io_dtype):
+    """Round to the model dtype ('bfloat16' / 'float16'); None keeps float32."""
+    x = np.asarray(x, dtype=np.float32)
+    if io_dtype is None or io_dtype == "float32":
+        return x
+    if io_dtype == "bfloat16":
+        return round_bf16(x)
+    if io_dtype == "float16":
+        return x.astype(np.float16).astype(np.float32)
+    raise ValueError(io_dtype)
+
+
+# --------------------------------------------------------------------------
+# scoring primitives
+# --------------------------------------------------------------------------
+def softmax_f32(logits, axis=-1):
+    """nn.functional.softmax(x, dtype=float32): evaluated in float64, rounded."""
+    z = np.asarray(logits, dtype=np.float64)
+    m = np.max(z, axis=axis, keepdims=True)
+    e = np.exp(z - m)
+    return (e / np.sum(e, axis=axis, keepdims=True)).astype(np.float32)
+
+
+def pool1d(x, kind, kernel):
+    """F.avg_pool1d / F.max_pool1d with padding=kernel//2, stride 1 (last axis).
+
+    avg: zero padding, divisor = kernel (count_include_pad=True).
+    max: -inf padding.  Only odd kernels keep the length (reference uses 5, 7).
+    """
+    if kernel % 2 != 1:
+        raise ValueError("pooling kernel must be odd")
+    x = np.asarray(x, dtype=np.float64)
+    p = kernel // 2
+    L = x.shape[-1]
+    pad_val = 0.0 if kind == "avgpool" else -np.inf
+    xp = np.full(x.shape[:-1] + (L + 2 * p,), pad_val, dtype=np.float64)
+    xp[..., p:p + L] = x
+    win = np.stack([xp[..., j:j + L] for j in range(kernel)], axis=0)
+    if kind == "avgpool":
+        return (win.sum(axis=0) / kernel).astype(np.float32)
+    if kind == "maxpool":
+        return win.max(axis=0).astype(np.float32)
+    raise ValueError(f"Pooling method not supported: {kind}")
+
+
+def last_query_scores(q_last, k, pooling, kernel, io_dtype=None, scale=None):
+    """Pooled last-query attention, max over the query group.
+
+    heterocache/cache_utils.py:807-829 (prefill_select) and :1158-1187
+    (init_coefficient):  w = softmax_f32(q.K^T/sqrt(d)).to(dtype);
+    pool_k(w); max over the G query heads of each kv head.
+    q_last: [n_kv, G, d]; k: [n_kv, L, d] -> scores [n_kv, L] (float32).
+    """
+    q_last = np.asarray(q_last, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    d = q_last.shape[-1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    logits = np.einsum("hgd,hld->hgl", q_last, k)
+    if io_dtype not in (None, "float32"):
+        logits = round_to(round_to(logits, io_dtype) * np.float32(scale), io_dtype)
+    else:
+        logits = (logits * scale).astype(np.float32)
+    w = round_to(softmax_f32(logits), io_dtype)
+    w = round_to(pool1d(w, pooling, kernel), io_dtype)
+    return w.max(axis=1)
+
+
+def window_scores(q_win, k, pooling, kernel, window_keep, io_dtype=None, scale=None):
+    """Observation-window score, generalising the reference's two scorers.
+
+    S_h[t] = max_g pool_k( sum_w softmax_t(q_{g,w}.k_t/sqrt(d) + causal) )
+    q_win: [n_kv, G, W, d], the last W query positions; k: [n_kv, L, d].
+    The window's own W keys are causally masked (query w sees key L-W+j only
+    for j <= w), kv_cluster.py:169-175.  With window_keep the scored span is
+    [0, L-W) (kv_cluster.py:178) -- at G=1 this is SnapKVCluster.update_kv's
+    score (heterocache/kv_cluster.py:155-185).  Without it the span is [0, L)
+    and at W=1 this is last_query_scores (heterocache/cache_utils.py:807-829).
+    The window sum of a cast softmax is rounded once (ATen reductions
+    accumulate in float32).  Returns [n_kv, span] float32.
+    """
+    q_win = np.asarray(q_win, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    n_kv, G, W, d = q_win.shape
+    L = k.shape[1]
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    logits = np.einsum("hgwd,hld->hgwl", q_win, k)
+    if io_dtype not in (None, "float32"):
+        logits = round_to(round_to(logits, io_dtype) * np.float32(scale), io_dtype).astype(np.float64)
+    else:
+        logits = (logits * scale).astype(np.float32).astype(np.float64)
+    # causal mask inside the window: query w may see window key j <= w.
+    for w in range(W):
+        logits[:, :, w, L - W + w + 1:] = -np.inf
+    p = round_to(softmax_f32(logits), io_dtype)
+    span = L - W if window_keep else L
+    s = round_to(p[..., :span].astype(np.float64).sum(axis=2), io_dtype)
+    s = round_to(pool1d(s, pooling, kernel), io_dtype)
+    return s.max(axis=1)
+
+
+def snapkv_update_kv(key_states, query_states, value_states, window_size, compression_ratio, pooling, kernel,
+                     num_key_value_groups, io_dtype=None):
+    """SnapKVCluster.update_kv, heterocache/kv_cluster.py:155-199.
+
+    key/query/value: [B, H, L, d] (keys already repeated per query head).
+    Returns compressed (key, value) [B, H, cap, d].
+    """
+    B, H, L, d = query_states.shape
+    cap = max(int(compression_ratio * L / num_key_value_groups), 2)
+    if cap > L:
+        return key_states, value_states
+    W = window_size
+    ks, vs = [], []
+    for b in range(B):
+        kb, vb = [], []
+        for h in range(H):
+            s = window_scores(query_states[b, h][None, None, -W:], key_states[b, h][None], pooling, kernel,
+                              window_keep=True, io_dtype=io_dtype)[0]
+            top = topk_indices(s, cap - W)  # reference order: descending score
+            kb.append(np.concatenate([key_states[b, h, :L - W][top], key_states[b, h, L - W:]], axis=0))
+            vb.append(np.concatenate([value_states[b, h, :L - W][top], value_states[b, h, L - W:]], axis=0))
+        ks.append(np.stack(kb))
+        vs.append(np.stack(vb))
+    return np.stack(ks), np.stack(vs)
+
+
+# --------------------------------------------------------------------------
+# selection
+# --------------------------------------------------------------------------
+def topk_indices(scores, k):
+    """Indices of the k largest scores, descending, ties -> lower index first.
+
+    Stands in for torch.topk(k, sorted=True) (heterocache/cache_utils.py:832,
+    :1061, :1092, :1189) under the stated tie-break.
+    """
+    s = np.asarray(scores)
+    order = np.argsort(-s.astype(np.float64), kind="stable")
+    return order[:k].astype(np.int64)
+
+
+def topk_select(scores, cap):
+    """Kept token set of one head, ascending positions.
+
+    heterocache/cache_utils.py:831-851: topk(max cap) -> mask rank >= cap_h
+    -> ascending sort.  The first cap_h entries of the sorted top-max_k list
+    are the head's own top-cap_h, so the result is sort(topk(cap_h)).
+    """
+    return np.sort(topk_indices(scores, cap))
+
+
+def select_with_window(scores, cap, seq_len, window):
+    """Budget cap with the last `window` tokens force-kept (SnapKV style).
+
+    heterocache/kv_cluster.py:187-197: topk(cap - W) over [0, L-W) plus the
+    window.  Returned ascending (the store keeps temporal order,
+    heterocache/cache_utils.py:782-786).
+    """
+    if cap >= seq_len:
+        return np.arange(seq_len, dtype=np.int64)
+    body = topk_select(scores[:seq_len - window], max(cap - window, 0))
+    return np.concatenate([body, np.arange(seq_len - window, seq_len, dtype=np.int64)])
+
+
+# --------------------------------------------------------------------------
+# a10: decode attention
+# --------------------------------------------------------------------------
+def decode_attention(q, ks, vs, scale=None):
+    """softmax(scale * q K^T) V per row, float64 closed form.
+
+    Stands in for flash_attn_with_kvcache(..., causal=False)
+    (heterocache/llama_model.py:382-389).  q: [rows, G, d]; ks/vs: lists of
+    [len_r, d] arrays.  Returns [rows, G, d] float64 (zeros for empty rows).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    rows, G, d = q.shape
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    out = np.zeros((rows, G, d), dtype=np.float64)
+    for r in range(rows):
+        k = np.asarray(ks[r], dtype=np.float64)
+        v = np.asarray(vs[r], dtype=np.float64)
+        if k.shape[0] == 0:
+            continue
+        z = scale * (q[r] @ k.T)
+        z -= z.max(axis=-1, keepdims=True)
+        p = np.exp(z)
+        p /= p.sum(axis=-1, keepdims=True)
+        out[r] = p @ v
+    return out
+
+
+# --------------------------------------------------------------------------
+# a12, a13: pivot drift and retrieval
+# --------------------------------------------------------------------------
+def pivot_step_scores(q_steps, k_prefill, pooling, kernel, io_dtype=None, scale=None):
+    """Scores of the buffered decode queries against a pivot's prefill keys.
+
+    heterocache/cache_utils.py:1030-1057: logits of every (query head g,
+    step s) -> softmax_f32 -> cast -> pool -> max over g.
+    q_steps: [G, S, d]; k_prefill: [L, d] -> [S, L] float32.
+    """
+    q = np.asarray(q_steps, dtype=np.float64)
+    G, S, d = q.shape
+    out = last_query_scores(q.transpose(1, 0, 2).reshape(S, G, d),
+                            np.broadcast_to(np.asarray(k_prefill), (S,) + np.asarray(k_prefill).shape),
+                            pooling, kernel, io_dtype=io_dtype, scale=scale)
+    return out
+
+
+def drift_check(step_scores, ref_set, base_len, threshold):
+    """Top-K overlap of each buffered step with the reference set, median.
+
+    heterocache/cache_utils.py:1059-1080.  step_scores: [B, S, L];
+    ref_set: [B, K] indices.  overlap_s = mean_b |topK_s ∩ ref_b| / K;
+    coefficient = statistics.median(overlap); trigger = coefficient < thr.
+    Returns (overlaps [S], median, trigger, cur_last [B, K] (topK of last step)).
+    """
+    B, S, L = step_scores.shape
+    overl = np.zeros((B, S), dtype=np.float64)
+    cur_last = []
+    for b in range(B):
+        ref = set(np.asarray(ref_set[b]).tolist())
+        for s in range(S):
+            cur = topk_indices(step_scores[b, s], base_len)
+            overl[b, s] = np.float32(len(ref.intersection(cur.tolist()))) / np.float32(base_len)
+            if s == S - 1:
+                cur_last.append(cur)
+    overlaps = overl.astype(np.float32).mean(axis=0, dtype=np.float32)
+    med = statistics.median([float(x) for x in overlaps])
+    return overlaps, med, med < threshold, np.stack(cur_last)
+
+
+def retrieval_lengths(base_len, member_ratios, seq_len, topk=None, use_f32=True):
+    """Tokens retrieved into each satellite, heterocache/cache_utils.py:1084-1087.
+
+    The reference uses float64 min(int(base*ratio), L); with use_f32 the
+    float32 prefill cap is used instead so the write never passes the
+    prefill region.  topk (the north-star retrieval size) caps every length.
+    """
+    if use_f32:
+        lens = prefill_caps(base_len, member_ratios, seq_len).tolist()
+    else:
+        lens = [capacity_f64(base_len, r, seq_len) for r in member_ratios]
+    if topk is not None:
+        lens = [min(n, topk) for n in lens]
+    return [int(n) for n in lens]
+
+
+def retrieval_indices(last_step_scores, lengths):
+    """Ascending top-max(len) list; member m takes its first len_m entries.
+
+    heterocache/cache_utils.py:1090-1105 (per batch row; the reference's
+    squeeze() makes the B=1 case the defined one).
+    """
+    mk = max(lengths) if lengths else 0
+    idx = np.sort(topk_indices(last_step_scores, mk))
+    return [idx[:n] for n in lengths]
+
+
+# --------------------------------------------------------------------------
+# a14: head order and derived lists
+# --------------------------------------------------------------------------
+SORT_PRIORITY = {1: 0, 4: 1, 2: 2, 3: 3}
+
+
+def reorder_plan(classification, relations):
+    """Head permutation and derived lists of one layer.
+
+    heterocache/utils.py:101-116 (stable sort anchor, satellite, volatile,
+    pivot) and :300-343 (derived lists, relations remapped in the original
+    dict order, members sorted).
+    Returns dict(perm, compress, select, update, keep, relations).
+    """
+    perm = [i for i, _ in sorted(enumerate(classification), key=lambda x: SORT_PRIORITY.get(x[1], 99))]
+    cls = [classification[i] for i in perm]
+    o2n = {old: new for new, old in enumerate(perm)}
+    rel = {}
+    for leader, members in relations.items():
+        if int(leader) in o2n:
+            rel[str(o2n[int(leader)])] = sorted(o2n[m] for m in members if m in o2n)
+    return {
+        "perm": perm,
+        "compress": cls.count(1) + cls.count(4),
+        "select": [i for i, x in enumerate(cls) if x == 3],
+        "update": [i for i, x in enumerate(cls) if x == 4],
+        "keep": [i for i, x in enumerate(cls) if x in (2, 3)],
+        "relations": rel,
+    }
+
+
+def allocation_ratios(stabilities):
+    """Inverse-stability allocation, tools/get_cluster.py:276-307.
+
+    stabilities: list of per-layer lists, -1 for full-KV heads.  Targets get
+    ratio = (1/(s+1e-6)) / sum(1/(s'+1e-6)) * n_targets (mean exactly 1).
+    """
+    targets = [s for row in stabilities for s in row if s > -0.5]
+    n = len(targets)
+    tot = sum(1.0 / (s + 1e-6) for s in targets)
+    out = []
+    for row in stabilities:
+        out.append([((1.0 / (s + 1e-6)) / tot * n) if s > -0.5 else -1.0 for s in row])
+    return out

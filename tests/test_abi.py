@@ -1,0 +1,65 @@
+"""The C-ABI library loads and exports every symbol include/hc.h declares.
+
+CPU only: nothing here launches a kernel.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from heterocache_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "hc.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"\b(hc_[a-z0-9_]+)\s*\(", text)
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    for required in ("hc_decode_attn", "hc_gather_store", "hc_append", "hc_last_error"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhc.so not built")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, f"symbols declared in hc.h but not exported: {missing}"
+
+
+def test_python_mirror_matches_header():
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_constants_and_error_reporting_without_gpu():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhc.so not built")
+    lib = _lib.load()
+    assert lib.hc_version() == 1
+    assert lib.hc_tile_tokens() == 32
+    assert lib.hc_head_dim() == 128
+    # Argument validation happens before any HIP call, so it runs on the CPU.
+    rc = lib.hc_decode_attn(2, None, None, None, None, None, None, 4, 0, 1.0, None, None, None, None, 0, 1, 4, None)
+    assert rc == _lib.HC_ERR_INVALID
+    assert b"group" in lib.hc_last_error()
+    rc = lib.hc_gather_store(2, None, None, 0, None, 128, 16, None, None, None, None, None, None, None, 1, 4, None, None)
+    assert rc == _lib.HC_ERR_INVALID
+    assert b"null pointer" in lib.hc_last_error()
+    assert lib.hc_decode_num_parts(None, 1, 4) == -1
+
+
+def test_num_parts_matches_chunking():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhc.so not built")
+    from heterocache_amd import ops
+    # 4 waves x tiles_per_wave tiles of 32 tokens per part; an empty row still
+    # takes one part (it writes the row's zero output).
+    assert ops.decode_num_parts([0, 1, 512, 513], tiles_per_wave=4) == 1 + 1 + 1 + 2
+    assert ops.decode_num_parts([131072], tiles_per_wave=8) == 131072 // 1024

@@ -1,0 +1,160 @@
+"""Decode attention (hc_decode_attn) vs the float64 closed form of the oracle.
+
+Parity bar: max-abs <= 2e-2 (bf16), 1e-2 (fp16), 1e-4 (fp32).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from heterocache_amd.store import KVStore
+from oracle import hc_oracle as O
+from tests.gpu_util import ATTN_TOL, TORCH_DT, as_np, fill_store
+
+pytestmark = pytest.mark.gpu
+
+
+def run_case(dev, dt, lens, G, seed, tiles_per_wave=4, extra_cap=0, scale=None, outliers=False):
+    rng = np.random.default_rng(seed)
+    tdt = TORCH_DT[dt]
+    ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32) for L in lens]
+    vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32) for L in lens]
+    if outliers:  # a few large channels and one dominant token per row
+        for k in ks:
+            k[:, :4] *= 8
+            if k.shape[0] > 3:
+                k[3] *= 3
+    q = torch.as_tensor(rng.standard_normal((len(lens), G, 128)), dtype=torch.float32)
+    store = KVStore([L + extra_cap for L in lens], tdt, dev)
+    fill_store(store, [k.to(dev) for k in ks], [v.to(dev) for v in vs], dev)
+    qd = q.to(tdt).to(dev)
+    scale = 1.0 / math.sqrt(128) if scale is None else scale
+    out = store.attend(qd, scale, tiles_per_wave=tiles_per_wave)
+    torch.cuda.synchronize()
+    # The oracle sees exactly the values the device holds.
+    ref = O.decode_attention(as_np(qd), [as_np(k.to(tdt)) for k in ks], [as_np(v.to(tdt)) for v in vs], scale)
+    err = np.abs(as_np(out) - ref).max() if out.numel() else 0.0
+    return err, out
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_ragged_rows_gqa4(dev, dt):
+    lens = [1, 31, 32, 33, 100, 1000, 4097, 255]
+    err, _ = run_case(dev, dt, lens, 4, seed=11)
+    assert err <= ATTN_TOL[dt], err
+
+
+@pytest.mark.parametrize("G", [1, 2, 7, 8, 16])
+def test_group_sizes(dev, G):
+    err, _ = run_case(dev, "bf16", [77, 513, 2048, 3], G, seed=100 + G)
+    assert err <= ATTN_TOL["bf16"], err
+
+
+@pytest.mark.parametrize("tpw", [1, 2, 8, 16])
+def test_chunking_is_invisible(dev, tpw):
+    err, _ = run_case(dev, "f32", [5000, 17, 1024], 4, seed=7, tiles_per_wave=tpw)
+    assert err <= ATTN_TOL["f32"], err
+
+
+def test_empty_row_gives_zeros(dev):
+    err, out = run_case(dev, "bf16", [0, 50, 0, 7], 4, seed=3)
+    assert err <= ATTN_TOL["bf16"]
+    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[2]) == 0
+
+
+def test_outliers_and_sinks(dev):
+    err, _ = run_case(dev, "bf16", [4096, 1500], 4, seed=5, outliers=True)
+    assert err <= ATTN_TOL["bf16"], err
+    err, _ = run_case(dev, "f32", [4096, 1500], 4, seed=5, outliers=True)
+    assert err <= ATTN_TOL["f32"], err
+
+
+def test_stale_tail_does_not_leak(dev):
+    """Slots past len hold other data (here: NaN); the kernel must mask them."""
+    lens = [45, 70]
+    rng = np.random.default_rng(9)
+    store = KVStore([128, 128], torch.bfloat16, dev)
+    store.k.fill_(float("nan"))
+    store.v.fill_(float("nan"))
+    ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    fill_store(store, ks, vs, dev)
+    q = torch.as_tensor(rng.standard_normal((2, 4, 128)), dtype=torch.float32).to(torch.bfloat16).to(dev)
+    out = store.attend(q, 1 / math.sqrt(128))
+    ref = O.decode_attention(as_np(q), [as_np(k.bfloat16()) for k in ks], [as_np(v.bfloat16()) for v in vs])
+    assert np.isfinite(as_np(out)).all()
+    assert np.abs(as_np(out) - ref).max() <= ATTN_TOL["bf16"]
+
+
+def test_matches_torch_sdpa_fp32(dev):
+    """Independent check against torch's own attention in float32."""
+    rng = np.random.default_rng(21)
+    L, G = 3000, 4
+    k = torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev)
+    v = torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev)
+    q = torch.as_tensor(rng.standard_normal((1, G, 128)), dtype=torch.float32).to(dev)
+    store = KVStore([L], torch.float32, dev)
+    fill_store(store, [k], [v], dev)
+    out = store.attend(q, 1 / math.sqrt(128))
+    ref = torch.softmax((q[0] @ k.T) / math.sqrt(128), dim=-1) @ v
+    assert (out[0] - ref).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_fused_append_matches_oracle_over_steps(dev, dt):
+    """attend(k_new=...) == append then attend, step after step (counters reset)."""
+    lens = [0, 1, 31, 32, 63, 100, 1023, 1024, 2500, 4096]
+    steps, G = 6, 4
+    tdt = TORCH_DT[dt]
+    rng = np.random.default_rng(77)
+    ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(tdt).to(dev) for L in lens]
+    vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(tdt).to(dev) for L in lens]
+    a = KVStore([L + steps for L in lens], tdt, dev)
+    b = KVStore([L + steps for L in lens], tdt, dev)
+    fill_store(a, ks, vs, dev)
+    fill_store(b, ks, vs, dev)
+    hist_k = [as_np(k) for k in ks]
+    hist_v = [as_np(v) for v in vs]
+    scale = 1 / math.sqrt(128)
+    for s in range(steps):
+        kn = torch.as_tensor(rng.standard_normal((len(lens), 128)), dtype=torch.float32).to(tdt).to(dev)
+        vn = torch.as_tensor(rng.standard_normal((len(lens), 128)), dtype=torch.float32).to(tdt).to(dev)
+        q = torch.as_tensor(rng.standard_normal((len(lens), G, 128)), dtype=torch.float32).to(tdt).to(dev)
+        a.append(kn, vn)
+        oa = a.attend(q, scale)
+        ob = b.attend(q, scale, k_new=kn, v_new=vn)
+        torch.cuda.synchronize()
+        for r in range(len(lens)):
+            hist_k[r] = np.concatenate([hist_k[r], as_np(kn[r:r + 1])])
+            hist_v[r] = np.concatenate([hist_v[r], as_np(vn[r:r + 1])])
+        ref = O.decode_attention(as_np(q), hist_k, hist_v, scale)
+        assert np.abs(as_np(ob) - ref).max() <= ATTN_TOL[dt]
+        assert torch.equal(oa, ob), f"step {s}: fused append differs from append+attend"
+    assert b.row_len.tolist() == [L + steps for L in lens]
+    assert b.host_len.tolist() == [L + steps for L in lens]
+    for r in range(len(lens)):
+        ka, va = a.read_rows([r], lens[r] + steps)
+        kb, vb = b.read_rows([r], lens[r] + steps)
+        assert torch.equal(ka, kb) and torch.equal(va, vb)
+
+
+def test_merge_without_lds_factors(dev):
+    """A row with more (part, query) pairs than the LDS factor table holds."""
+    err, _ = run_case(dev, "bf16", [70000, 300], 16, seed=31, tiles_per_wave=1)
+    assert err <= ATTN_TOL["bf16"], err
+
+
+def test_row_order_does_not_change_results(dev):
+    lens = [300, 5000, 64, 2049]
+    rng = np.random.default_rng(4)
+    ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    st = KVStore(lens, torch.float32, dev)
+    fill_store(st, ks, vs, dev)
+    q = torch.as_tensor(rng.standard_normal((4, 4, 128)), dtype=torch.float32).to(dev)
+    o1 = st.attend(q, 0.1).clone()
+    st.row_order = torch.tensor([2, 0, 3, 1], dtype=torch.int32, device=dev)
+    o2 = st.attend(q, 0.1)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)

@@ -1,0 +1,128 @@
+"""Tiled KV store writers/readers: bit-exact against plain indexing.
+
+Covers the prefill keep-head copy, the indexed (compressed-head / retrieval)
+gather from device and from host-pinned memory, partial-tile writes that
+must preserve existing slots, decode append and the capacity error.
+"""
+import numpy as np
+import pytest
+import torch
+
+from heterocache_amd.store import KVStore
+
+pytestmark = pytest.mark.gpu
+
+
+def rand(shape, dtype, dev, seed):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return torch.randn(shape, generator=g).to(dtype).to(dev)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_identity_copy_roundtrip(dev, dtype):
+    B, H, L = 2, 3, 200
+    k = rand((B, H, L, 128), dtype, dev, 1)
+    v = rand((B, H, L, 128), dtype, dev, 2)
+    store = KVStore([L + 50] * (B * H), dtype, dev)
+    jobs = [(b, h) for b in range(B) for h in range(H)]
+    store.write_rows(k, v, jobs, list(range(B * H)), [L] * (B * H))
+    rk, rv = store.read_rows(list(range(B * H)), L)
+    assert torch.equal(rk, k.reshape(B * H, L, 128))
+    assert torch.equal(rv, v.reshape(B * H, L, 128))
+    assert store.row_len.tolist() == [L] * (B * H)
+
+
+def test_strided_projection_source(dev):
+    """K as produced by proj(x).view(B, L, H, d).transpose(1, 2) (non-contiguous)."""
+    B, H, L = 1, 8, 77
+    x = rand((B, L, H * 128), torch.bfloat16, dev, 3)
+    k = x.view(B, L, H, 128).transpose(1, 2)
+    store = KVStore([L] * H, torch.bfloat16, dev)
+    store.write_rows(k, k, [(0, h) for h in range(H)], list(range(H)), [L] * H)
+    rk, _ = store.read_rows(list(range(H)), L)
+    assert torch.equal(rk, k[0])
+
+
+@pytest.mark.parametrize("host", [False, True])
+def test_indexed_gather(dev, host):
+    B, H, L = 1, 4, 1000
+    k = rand((B, H, L, 128), torch.bfloat16, dev, 4)
+    v = rand((B, H, L, 128), torch.bfloat16, dev, 5)
+    if host:
+        kh = torch.empty(k.shape, dtype=k.dtype, pin_memory=True)
+        vh = torch.empty(v.shape, dtype=v.dtype, pin_memory=True)
+        kh.copy_(k.cpu())
+        vh.copy_(v.cpu())
+        src_k, src_v = kh, vh
+    else:
+        src_k, src_v = k, v
+    rng = np.random.default_rng(0)
+    counts = [300, 1, 33, 0]
+    M = max(counts)
+    idx = np.zeros((H, M), dtype=np.int32)
+    for h in range(H):
+        idx[h, :counts[h]] = np.sort(rng.choice(L, counts[h], replace=False))
+    store = KVStore([512] * H, torch.bfloat16, dev)
+    store.write_rows(src_k, src_v, [(0, h) for h in range(H)], list(range(H)), counts,
+                     idx=torch.as_tensor(idx).to(dev), src_is_host=host)
+    torch.cuda.synchronize()
+    for h in range(H):
+        n = counts[h]
+        if n == 0:
+            continue
+        rk, rv = store.read_rows([h], n)
+        sel = torch.as_tensor(idx[h, :n], dtype=torch.long, device=dev)
+        assert torch.equal(rk[0], k[0, h].index_select(0, sel))
+        assert torch.equal(rv[0], v[0, h].index_select(0, sel))
+
+
+def test_partial_tile_write_preserves_tail(dev):
+    L = 100
+    k = rand((1, 1, L, 128), torch.bfloat16, dev, 6)
+    v = rand((1, 1, L, 128), torch.bfloat16, dev, 7)
+    k2 = rand((1, 1, L, 128), torch.bfloat16, dev, 8)
+    v2 = rand((1, 1, L, 128), torch.bfloat16, dev, 9)
+    store = KVStore([L], torch.bfloat16, dev)
+    store.write_rows(k, v, [(0, 0)], [0], [L])
+    idx = torch.arange(40, dtype=torch.int32, device=dev).view(1, 40) * 2
+    store.write_rows(k2, v2, [(0, 0)], [0], [40], idx=idx, set_len=False)
+    rk, rv = store.read_rows([0], L)
+    sel = idx[0].long()
+    assert torch.equal(rk[0, :40], k2[0, 0].index_select(0, sel))
+    assert torch.equal(rv[0, :40], v2[0, 0].index_select(0, sel))
+    assert torch.equal(rk[0, 40:], k[0, 0, 40:])
+    assert torch.equal(rv[0, 40:], v[0, 0, 40:])
+    assert store.host_len.tolist() == [L]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_append_sequence(dev, dtype):
+    rows, L0, steps = 5, [0, 31, 32, 63, 100], 40
+    store = KVStore([L + steps for L in L0], dtype, dev)
+    base_k = rand((1, rows, max(L0), 128), dtype, dev, 10)
+    base_v = rand((1, rows, max(L0), 128), dtype, dev, 11)
+    store.write_rows(base_k, base_v, [(0, r) for r in range(rows)], list(range(rows)), L0)
+    new_k = rand((steps, rows, 128), dtype, dev, 12)
+    new_v = rand((steps, rows, 128), dtype, dev, 13)
+    for s in range(steps):
+        store.append(new_k[s], new_v[s])
+    torch.cuda.synchronize()
+    assert store.row_len.tolist() == [L + steps for L in L0]
+    assert store.host_len.tolist() == [L + steps for L in L0]
+    for r in range(rows):
+        n = L0[r] + steps
+        rk, rv = store.read_rows([r], n)
+        exp_k = torch.cat([base_k[0, r, :L0[r]], new_k[:, r]])
+        exp_v = torch.cat([base_v[0, r, :L0[r]], new_v[:, r]])
+        assert torch.equal(rk[0], exp_k)
+        assert torch.equal(rv[0], exp_v)
+    assert store.status.item() == 0
+
+
+def test_append_capacity_error(dev):
+    store = KVStore([32, 64], torch.bfloat16, dev)
+    store.set_lengths([32, 10])
+    kn = torch.zeros((2, 128), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(RuntimeError, match="OOM"):
+        store.append(kn, kn)
+    assert store.host_len.tolist() == [32, 10]
