@@ -1,0 +1,310 @@
+"""Pinning of the CPU oracle (oracle/hc_oracle.py) -- CPU only.
+
+Each test checks an oracle function against something other than its own
+formula: hand vectors from the reference's numbers, torch's library routines
+(softmax, avg/max pooling, SDPA, topk), closed forms, brute force on tiny
+inputs, and the reference's committed head-classification JSON.
+"""
+import itertools
+import json
+import math
+import os
+import statistics
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import c_oracle
+from oracle import hc_oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# -- a1 / a2 ------------------------------------------------------------------
+@pytest.mark.parametrize("args,expect", [
+    ((0.5, 50, 131072, 256), 49629),   # Llama JSON (F = 50), 128K
+    ((0.5, 50, 32768, 256), 12407),
+    ((0.5, 50, 229376, 256), 86851),
+    ((0.5, 0, 4096, 8), 2048),         # single layer, no full heads
+    ((0.25, 0, 100, 8), 25),
+])
+def test_get_compress_len_vectors(args, expect):
+    assert O.get_compress_len(*args) == expect
+
+
+def test_prefill_caps_match_torch_float32_product():
+    rng = np.random.default_rng(0)
+    ratios = rng.uniform(0.2, 3.0, 500).astype(np.float32)
+    for base in (49629, 2048, 86851, 7):
+        t = (base * torch.tensor(ratios, dtype=torch.float32)).int().numpy()
+        assert (O.prefill_caps(base, ratios, 10 ** 9) == t).all()
+    assert (O.prefill_caps(2048, [0.5, 1.5, 5.0], 4096) == [1024, 3072, 4096]).all()
+
+
+def test_f32_and_f64_budgets_can_differ_by_one():
+    """The reference sizes capacity/retrieval in float64 but caps in float32."""
+    base, r = 2048, 0.7944335746509517
+    assert O.prefill_caps(base, [r], 10 ** 9)[0] == 1627
+    assert O.capacity_f64(base, r, 10 ** 9) == 1626
+    assert O.retrieval_lengths(base, [r], 10 ** 9, use_f32=False) == [1626]
+    assert O.retrieval_lengths(base, [r], 10 ** 9, use_f32=True) == [1627]
+    assert O.retrieval_lengths(base, [r], 10 ** 9, topk=1024) == [1024]
+
+
+# -- dtype rounding ------------------------------------------------------------
+def test_round_bf16_matches_torch():
+    x = np.random.default_rng(1).standard_normal(10000).astype(np.float32) * 100
+    ref = torch.tensor(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(O.round_bf16(x), ref)
+    assert np.array_equal(O.round_to(x, "float16"), torch.tensor(x).half().float().numpy())
+
+
+# -- scoring primitives -----------------------------------------------------------
+def test_softmax_matches_torch():
+    x = np.random.default_rng(2).standard_normal((5, 300)).astype(np.float32) * 4
+    ref = torch.softmax(torch.tensor(x), dim=-1).numpy()
+    assert np.abs(O.softmax_f32(x) - ref).max() < 1e-7
+
+
+@pytest.mark.parametrize("kind", ["avgpool", "maxpool"])
+@pytest.mark.parametrize("k", [1, 3, 5, 7])
+def test_pooling_matches_torch(kind, k):
+    x = np.random.default_rng(3).random((4, 257)).astype(np.float32)
+    t = torch.tensor(x).unsqueeze(1)
+    fn = F.avg_pool1d if kind == "avgpool" else F.max_pool1d
+    ref = fn(t, kernel_size=k, padding=k // 2, stride=1).squeeze(1).numpy()
+    assert np.abs(O.pool1d(x, kind, k) - ref).max() < 4e-7  # a few float32 ulps of summation order
+
+
+def test_pooling_rejects_even_kernel():
+    with pytest.raises(ValueError):
+        O.pool1d(np.zeros((1, 8)), "avgpool", 4)
+
+
+def test_avgpool_closed_form_at_edges():
+    """Uniform input u: interior -> u, position 0 -> u*(p+1)/k (zero padding)."""
+    L, k, u = 50, 5, 0.02
+    y = O.pool1d(np.full((1, L), u, np.float32), "avgpool", k)[0]
+    assert abs(y[10] - u) < 1e-8 and abs(y[0] - u * 3 / 5) < 1e-8 and abs(y[1] - u * 4 / 5) < 1e-8
+
+
+def _torch_last_query_scores(q, k, pooling, kernel):
+    """The reference op sequence (heterocache/cache_utils.py:807-829) in torch fp32."""
+    qt, kt = torch.tensor(q), torch.tensor(k)
+    n, G, d = qt.shape
+    w = torch.matmul(qt.view(1, n, G, 1, d), kt.view(1, n, 1, -1, d).transpose(-1, -2)) / math.sqrt(d)
+    w = torch.softmax(w.view(1, n * G, 1, -1), dim=-1, dtype=torch.float32).squeeze(2)
+    fn = F.avg_pool1d if pooling == "avgpool" else F.max_pool1d
+    w = fn(w, kernel_size=kernel, padding=kernel // 2, stride=1)
+    return w.view(1, n, G, -1).max(dim=-2).values[0].numpy()
+
+
+@pytest.mark.parametrize("pooling,kernel", [("avgpool", 5), ("maxpool", 7)])
+def test_last_query_scores_match_reference_sequence(pooling, kernel):
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal((3, 4, 128)).astype(np.float32)
+    k = rng.standard_normal((3, 600, 128)).astype(np.float32)
+    got = O.last_query_scores(q, k, pooling, kernel)
+    ref = _torch_last_query_scores(q, k, pooling, kernel)
+    assert np.abs(got - ref).max() < 1e-6
+
+
+def test_uniform_keys_give_uniform_scores():
+    L = 64
+    k = np.ones((1, L, 128), np.float32)
+    q = np.random.default_rng(5).standard_normal((1, 4, 128)).astype(np.float32)
+    s = O.last_query_scores(q, k, "maxpool", 3)
+    assert np.allclose(s, 1.0 / L, rtol=1e-6)
+
+
+def test_window_scores_reduce_to_last_query_at_w1():
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((2, 4, 1, 128)).astype(np.float32)
+    k = rng.standard_normal((2, 300, 128)).astype(np.float32)
+    a = O.window_scores(q, k, "avgpool", 5, window_keep=False)
+    b = O.last_query_scores(q[:, :, 0], k, "avgpool", 5)
+    assert np.array_equal(a, b)
+
+
+def _torch_snapkv_scores(q, k, W, pooling, kernel):
+    """SnapKVCluster.update_kv score (heterocache/kv_cluster.py:165-185) in torch fp32."""
+    qt, kt = torch.tensor(q)[None], torch.tensor(k)[None]
+    d = qt.shape[-1]
+    aw = torch.matmul(qt[..., -W:, :], kt.transpose(2, 3)) / math.sqrt(d)
+    mask = torch.full((W, W), torch.finfo(aw.dtype).min)
+    cond = torch.arange(W)
+    mask.masked_fill_(cond < (cond + 1).view(W, 1), 0)
+    aw[:, :, -W:, -W:] += mask[None, None]
+    aw = torch.softmax(aw, dim=-1, dtype=torch.float32)
+    s = aw[:, :, -W:, :-W].sum(dim=-2)
+    fn = F.avg_pool1d if pooling == "avgpool" else F.max_pool1d
+    return fn(s, kernel_size=kernel, padding=kernel // 2, stride=1)[0].numpy()
+
+
+def test_window_scores_reduce_to_snapkv_at_g1():
+    rng = np.random.default_rng(7)
+    H, L, W = 3, 400, 32
+    q = rng.standard_normal((H, L, 128)).astype(np.float32)
+    k = rng.standard_normal((H, L, 128)).astype(np.float32)
+    got = O.window_scores(q[:, None, -W:], k, "maxpool", 7, window_keep=True)
+    ref = _torch_snapkv_scores(q, k, W, "maxpool", 7)
+    assert got.shape == (H, L - W)
+    assert np.abs(got - ref).max() < 2e-6
+
+
+def test_snapkv_update_kv_keeps_window_and_budget():
+    rng = np.random.default_rng(8)
+    B, H, L, W = 1, 2, 256, 16
+    q = rng.standard_normal((B, H, L, 128)).astype(np.float32)
+    k = rng.standard_normal((B, H, L, 128)).astype(np.float32)
+    v = rng.standard_normal((B, H, L, 128)).astype(np.float32)
+    ck, cv = O.snapkv_update_kv(k, q, v, W, 0.5, "avgpool", 5, 1)
+    cap = int(0.5 * L)
+    assert ck.shape == (B, H, cap, 128)
+    assert np.array_equal(ck[0, 0, -W:], k[0, 0, -W:])
+
+
+# -- selection ------------------------------------------------------------------
+def _is_topk_set(s, sel):
+    """Every selected index ranks before every unselected one under (-s, idx)."""
+    sel = set(sel.tolist())
+    rest = [j for j in range(len(s)) if j not in sel]
+    return all((s[i] > s[j]) or (s[i] == s[j] and i < j) for i in sel for j in rest)
+
+
+def test_topk_select_brute_force_with_ties():
+    rng = np.random.default_rng(9)
+    for trial in range(200):
+        L = int(rng.integers(1, 9))
+        s = rng.integers(0, 3, L).astype(np.float32)   # many ties
+        k = int(rng.integers(0, L + 1))
+        sel = O.topk_select(s, k)
+        assert len(sel) == k and list(sel) == sorted(sel)
+        assert _is_topk_set(s, sel)
+        # unique among all subsets of size k
+        winners = [c for c in itertools.combinations(range(L), k) if _is_topk_set(s, np.array(c, dtype=np.int64))]
+        assert winners == [tuple(sel.tolist())]
+
+
+def test_topk_matches_torch_on_distinct_scores():
+    s = np.random.default_rng(10).permutation(5000).astype(np.float32)
+    ref = torch.topk(torch.tensor(s), 700).indices.numpy()
+    assert np.array_equal(O.topk_indices(s, 700), ref)
+
+
+def test_select_with_window():
+    s = np.arange(20, dtype=np.float32)[::-1].copy()  # earliest tokens score highest
+    sel = O.select_with_window(s, 8, 20, 4)
+    assert sel.tolist() == [0, 1, 2, 3, 16, 17, 18, 19]
+    assert O.select_with_window(s, 30, 20, 4).tolist() == list(range(20))
+
+
+def test_c_oracle_topk_matches_numpy():
+    rng = np.random.default_rng(11)
+    s = rng.integers(0, 50, 3000).astype(np.float32)
+    for k in (0, 1, 100, 2999, 3000):
+        assert np.array_equal(c_oracle.topk_select(s, k), O.topk_select(s, k))
+
+
+# -- a10: attention -----------------------------------------------------------------
+def test_decode_attention_matches_sdpa_float64():
+    rng = np.random.default_rng(12)
+    lens = [1, 7, 300]
+    q = rng.standard_normal((3, 4, 128))
+    ks = [rng.standard_normal((L, 128)) for L in lens]
+    vs = [rng.standard_normal((L, 128)) for L in lens]
+    got = O.decode_attention(q, ks, vs)
+    for r in range(3):
+        ref = F.scaled_dot_product_attention(torch.tensor(q[r])[None], torch.tensor(ks[r])[None],
+                                             torch.tensor(vs[r])[None])[0].numpy()
+        assert np.abs(got[r] - ref).max() < 1e-12
+
+
+def test_decode_attention_closed_forms():
+    rng = np.random.default_rng(13)
+    v = rng.standard_normal((1, 128))
+    q = rng.standard_normal((1, 2, 128))
+    assert np.array_equal(O.decode_attention(q, [rng.standard_normal((1, 128))], [v])[0, 0], v[0])
+    k = np.ones((50, 128))
+    v = rng.standard_normal((50, 128))
+    assert np.allclose(O.decode_attention(q, [k], [v])[0, 1], v.mean(axis=0))
+    assert not O.decode_attention(q, [np.zeros((0, 128))], [np.zeros((0, 128))]).any()
+
+
+def test_c_oracle_decode_matches_numpy():
+    rng = np.random.default_rng(14)
+    lens = [3, 5000, 129]
+    q = rng.standard_normal((3, 4, 128)).astype(np.float32)
+    ks = [rng.standard_normal((L, 128)).astype(np.float32) for L in lens]
+    vs = [rng.standard_normal((L, 128)).astype(np.float32) for L in lens]
+    off = np.cumsum([0] + lens[:-1])
+    got = c_oracle.decode_attention(q, np.concatenate(ks), np.concatenate(vs), off, lens, 1 / math.sqrt(128), 0,
+                                    chunk=777)
+    assert np.abs(got - O.decode_attention(q, ks, vs)).max() < 1e-5
+
+
+# -- a12 / a13: drift and retrieval -----------------------------------------------
+def test_drift_overlap_extremes_and_median():
+    L, K = 100, 10
+    s = np.zeros((1, 5, L), np.float32)
+    for st in range(5):
+        s[0, st, st * 10:(st + 1) * 10] = 1.0 + st  # step st's top-10 = [10st, 10st+10)
+    ref = np.arange(10)[None]
+    ov, med, trig, last = O.drift_check(s, ref, K, 0.5)
+    assert ov.tolist() == [1.0, 0, 0, 0, 0]
+    assert med == statistics.median([1.0, 0, 0, 0, 0]) == 0.0 and trig
+    assert sorted(last[0].tolist()) == list(range(40, 50))
+    ov, med, trig, _ = O.drift_check(np.repeat(s[:, :1], 5, axis=1), ref, K, 0.5)
+    assert med == 1.0 and not trig
+
+
+def test_drift_mean_over_batch():
+    s = np.zeros((2, 1, 20), np.float32)
+    s[0, 0, :4] = 1
+    s[1, 0, 10:14] = 1
+    ov, med, _, _ = O.drift_check(s, np.array([[0, 1, 2, 3], [0, 1, 2, 3]]), 4, 0.5)
+    assert ov.tolist() == [0.5] and med == 0.5
+
+
+def test_retrieval_takes_ascending_prefix_of_the_longest_list():
+    s = np.array([9, 1, 8, 2, 7, 3, 6, 4], np.float32)  # top-4 by score: 0, 2, 4, 6
+    out = O.retrieval_indices(s, [4, 2])
+    assert out[0].tolist() == [0, 2, 4, 6]
+    assert out[1].tolist() == [0, 2]  # prefix of the ascending list, not the member's own top-2
+
+
+def test_pivot_step_scores_shape_and_group_max():
+    rng = np.random.default_rng(15)
+    q = rng.standard_normal((4, 5, 128)).astype(np.float32)
+    k = rng.standard_normal((80, 128)).astype(np.float32)
+    s = O.pivot_step_scores(q, k, "avgpool", 5)
+    assert s.shape == (5, 80)
+    one = O.last_query_scores(q[:, 2][None], k[None], "avgpool", 5)[0]
+    assert np.array_equal(s[2], one)
+
+
+# -- a14: head order -----------------------------------------------------------------
+def test_reorder_plan_on_reference_json_layer23():
+    data = json.load(open(os.path.join(GOLDEN, "head_analysis_llama-3.1-8b-instruct.json")))
+    assert data["meta"]["counts"] == {"anchor": 10, "volatile": 17, "pivot": 33, "satellite": 196}
+    cls, rel = data["classification_matrix"][23], data["leader_member_relations"][23]
+    assert cls == [4, 4, 4, 4, 3, 4, 3, 4] and rel == {"6": [0, 1, 2, 3, 5], "4": [7]}
+    plan = O.reorder_plan(cls, rel)
+    # satellites 0,1,2,3,5,7 keep their order, then pivots 4, 6.
+    assert plan["perm"] == [0, 1, 2, 3, 5, 7, 4, 6]
+    assert plan["compress"] == 6 and plan["select"] == [6, 7] and plan["keep"] == [6, 7]
+    assert plan["update"] == [0, 1, 2, 3, 4, 5]
+    # relations keep the JSON's leader order: old 6 -> new 7 first, old 4 -> new 6.
+    assert list(plan["relations"].items()) == [("7", [0, 1, 2, 3, 4]), ("6", [5])]
+
+
+def test_allocation_ratios_average_one():
+    rng = np.random.default_rng(16)
+    st = [[float(x) if x > 0.2 else -1.0 for x in rng.random(8)] for _ in range(6)]
+    al = O.allocation_ratios(st)
+    vals = [a for row in al for a in row if a > -0.5]
+    assert abs(np.mean(vals) - 1.0) < 1e-9
+    s0 = [s for row in st for s in row if s > -0.5]
+    assert vals[int(np.argmin(s0))] == max(vals)  # least stable head gets the most
