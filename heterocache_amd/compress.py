@@ -1,0 +1,112 @@
+"""Prefill compression and pivot scoring on libhc kernels.
+
+Host-side composition of hc_score / hc_select_topk / hc_gather_store into the
+reference's operations:
+
+  last_query_scores   pooled last-query attention per KV head
+                      (heterocache/cache_utils.py:807-829, :1158-1187)
+  window_scores       SnapKV observation-window scores
+                      (heterocache/kv_cluster.py:165-185), generalised to a
+                      GQA group (max over the group)
+  pivot_step_scores   buffered decode queries vs a pivot's prefill keys read
+                      in place from the store (heterocache/cache_utils.py:1030-1057)
+  select_kept         per-head budget top-k in ascending order
+                      (heterocache/cache_utils.py:831-851)
+"""
+import math
+
+import torch
+
+from . import _lib, ops
+
+ROUND_FLAGS = {None: 0, torch.float32: 0, torch.bfloat16: _lib.HC_SCORE_ROUND_BF16,
+               torch.float16: _lib.HC_SCORE_ROUND_F16}
+
+
+def _check_qk(q, k):
+    if q.dim() != 4 or k.dim() != 4 or q.shape[-1] != 128 or k.shape[-1] != 128:
+        raise ValueError("q and k must be [B, heads, seq, 128]")
+    if q.stride(-1) != 1 or k.stride(-1) != 1:
+        raise ValueError("q and k need a unit channel stride")
+    if q.shape[0] != k.shape[0]:
+        raise ValueError("q and k batch sizes differ")
+
+
+def _dev_i64(vals, device):
+    return torch.tensor(list(vals), dtype=torch.int64).to(device)
+
+
+def window_scores(q, k, kv_heads, group, window, pooling="avgpool", kernel=5, window_keep=False, causal=True,
+                  round_dtype=None, scale=None, stream=None):
+    """Scores [B * len(kv_heads), span] of the last `window` query positions.
+
+    q: [B, Hq, Lq, 128]; k: [B, Hkv, L, 128] (post-RoPE, any strides with unit
+    channel stride).  Query heads h*group .. h*group+group-1 score kv head h.
+    window_keep=True scores only [0, L - window) (SnapKV); otherwise [0, L).
+    round_dtype reproduces the reference's casts to that dtype.
+    """
+    _check_qk(q, k)
+    B, Hq, Lq, _ = q.shape
+    L = k.shape[2]
+    if window > Lq:
+        raise ValueError("window longer than the query sequence")
+    scale = 1.0 / math.sqrt(128) if scale is None else scale
+    kv_heads = list(kv_heads)
+    q_off, k_off = [], []
+    for b in range(B):
+        for h in kv_heads:
+            q_off.append(b * q.stride(0) + h * group * q.stride(1) + (Lq - window) * q.stride(2))
+            k_off.append(b * k.stride(0) + h * k.stride(1))
+    flags = ROUND_FLAGS[round_dtype] | _lib.HC_SCORE_SUM_WINDOW
+    if causal:
+        flags |= _lib.HC_SCORE_CAUSAL_WINDOW
+    span = L - window if window_keep else L
+    out = ops.score(q, _dev_i64(q_off, q.device), q.stride(1), q.stride(2), k, _dev_i64(k_off, q.device), k.stride(2),
+                    L, group, window, span, pooling, kernel, scale, flags=flags, stream=stream)
+    return out.view(len(q_off), span)
+
+
+def last_query_scores(q, k, kv_heads, group, pooling="avgpool", kernel=5, round_dtype=None, scale=None, stream=None):
+    """Pooled last-query attention per KV head, max over its query group."""
+    return window_scores(q, k, kv_heads, group, 1, pooling, kernel, window_keep=False, causal=False,
+                         round_dtype=round_dtype, scale=scale, stream=stream)
+
+
+def pivot_step_scores(q_steps, store, rows, heads, group, seq_len, pooling="avgpool", kernel=5, round_dtype=None,
+                      scale=None, stream=None):
+    """Scores [len(rows), S, seq_len] of S buffered decode queries per pivot.
+
+    q_steps: [B, Hq, S, 128]; rows[j] is the store row of pivot j (batch
+    b_j = rows[j] // Hkv) whose query heads are heads[j]*group + g.  Keys are
+    the pivot's store slots [0, seq_len), read in place.
+    """
+    B, Hq, S, D = q_steps.shape
+    if D != 128 or q_steps.stride(-1) != 1:
+        raise ValueError("q_steps must be [B, Hq, S, 128] with unit channel stride")
+    scale = 1.0 / math.sqrt(128) if scale is None else scale
+    hkv = store.rows // B
+    q_off = [(r // hkv) * q_steps.stride(0) + h * group * q_steps.stride(1) for r, h in zip(rows, heads)]
+    flags = ROUND_FLAGS[round_dtype]
+    k_row = torch.tensor(list(rows), dtype=torch.int32).to(q_steps.device)
+    out = ops.score(q_steps, _dev_i64(q_off, q_steps.device), q_steps.stride(1), q_steps.stride(2), store.k, None, 0,
+                    seq_len, group, S, seq_len, pooling, kernel, scale, flags=flags,
+                    row_tile_off=store.row_tile_off, k_row=k_row, stream=stream)
+    return out.view(len(rows), S, seq_len)
+
+
+def select_kept(scores, caps, window=0, max_cap=None, stream=None):
+    """Ascending kept positions [jobs, max_cap (+window)] and counts [jobs].
+
+    scores: [jobs, span] float32 (span excludes a force-kept window).
+    caps: per-job budgets (python ints or an int32 device tensor).
+    """
+    jobs, span = scores.shape
+    if not torch.is_tensor(caps):
+        caps_list = [int(c) for c in caps]
+        caps = torch.tensor(caps_list, dtype=torch.int32).to(scores.device)
+        if max_cap is None:
+            max_cap = max(caps_list) if caps_list else 0
+    width = max(1, min(max_cap if max_cap is not None else span + window, span + window))
+    idx = torch.empty((jobs, width), dtype=torch.int32, device=scores.device)
+    idx, counts = ops.select_topk(scores, caps, span, window=window, idx=idx, stream=stream)
+    return idx, counts

@@ -1,0 +1,422 @@
+// Observation-window attention scores, pooled and maxed over the GQA group.
+//
+//   S_j[w'][t] = max_g round(pool_k(round(sum_w round(softmax_t(q_{g,w}.k_t * scale + mask)))))
+//
+// One implementation serves every scorer of the path:
+//  * prefill budget scoring, last query (W = 1): HeteroCache.prefill_select
+//    and init_coefficient (heterocache/cache_utils.py:807-829, :1158-1187);
+//  * SnapKV window scoring (W = 32, causal window, sum over the window, span
+//    L - W): SnapKVCluster.update_kv (heterocache/kv_cluster.py:165-185);
+//  * pivot drift scoring of the buffered decode queries against a pivot's
+//    prefill keys read in place from the tiled store (W = decode_step rows,
+//    no sum): HeteroCache.decode_select (heterocache/cache_utils.py:1030-1057).
+// `round` reproduces the reference's casts to the model dtype when asked
+// (HC_SCORE_ROUND_BF16 / _F16); by default everything stays float32.
+//
+// Phases (all launched by hc_score):
+//  1. score_stats_kernel: per (job, 256-token chunk) the logits of all
+//     G*W query rows against 16-token key sub-tiles on the MFMA (K is the A
+//     operand, loaded straight from HBM; queries are B operands staged in
+//     LDS), reduced to a running (max, sum exp) per row.
+//  2. score_stats_merge_kernel: fold the chunks' (max, sum) per row.
+//  3. score_probs_kernel: recompute the logits, normalise, sum over the
+//     window rows of each query head (xor-shuffle tree: fixed order), write
+//     A[job][w'][g][t].
+//  4. score_pool_kernel: pooling over t and max over g -> S[job][w'][t].
+#include "hc_common.h"
+#include "hc_internal.h"
+
+namespace hc {
+
+constexpr int kScoreWaves = 4;
+constexpr int kScoreChunk = 256;  // tokens per workgroup
+constexpr int kQPitch = HC_HEAD_DIM + 8;
+
+struct ScoreArgs {
+  const void* q;
+  const int64_t* q_off;
+  int64_t q_head_stride, q_row_stride;
+  const void* k;
+  const int64_t* k_off;
+  int64_t k_tok_stride;
+  const int64_t* row_tile_off;
+  const int32_t* k_row;
+  int L, G, W, R, NT, flags, span;
+  float scale;
+};
+
+__device__ __forceinline__ float round_mode(float x, int flags) {
+  if (flags & HC_SCORE_ROUND_BF16) return (float)(__bf16)x;
+  if (flags & HC_SCORE_ROUND_F16) return (float)(_Float16)x;
+  return x;
+}
+
+// Stage the query rows (row r = g*W + w) of a job in LDS, zero-padded to NT*16.
+template <typename T>
+__device__ __forceinline__ void stage_queries(const ScoreArgs& a, int job, T* s_q) {
+  const T* q = reinterpret_cast<const T*>(a.q) + a.q_off[job];
+  const int rows = a.NT * 16;
+  for (int c = threadIdx.x; c < rows * 16; c += kScoreWaves * 64) {
+    const int r = c >> 4, ch = c & 15;
+    typename Elem<T>::vec8 v = zero8<T>();
+    if (r < a.R) {
+      const int g = r / a.W, w = r % a.W;
+      v = load8<T>(q + g * a.q_head_stride + w * a.q_row_stride + ch * 8);
+    }
+    *reinterpret_cast<typename Elem<T>::vec8*>(s_q + r * kQPitch + ch * 8) = v;
+  }
+}
+
+// K operand of one 16-token sub-tile: lane holds token t0 + (lane & 15),
+// channels 32s + 8*(lane >> 4) + [0, 8).
+template <typename T, bool STORE>
+__device__ __forceinline__ void load_k_subtile(const ScoreArgs& a, int job, int t0, int lane,
+                                               typename Elem<T>::vec8 (&kr)[4]) {
+  if constexpr (STORE) {
+    const T* base = reinterpret_cast<const T*>(a.k) + (a.row_tile_off[a.k_row[job]] + t0 / HC_TILE) * (int64_t)HC_TILE_ELEMS;
+    const int h = (t0 / 16) & 1;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) kr[s] = load8<T>(base + (h * 4 + s) * 512 + lane * 8);
+  } else {
+    const int t = t0 + (lane & 15);
+    if (t < a.L) {
+      const T* p = reinterpret_cast<const T*>(a.k) + a.k_off[job] + (int64_t)t * a.k_tok_stride + 8 * (lane >> 4);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kr[s] = load8<T>(p + 32 * s);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kr[s] = zero8<T>();
+    }
+  }
+}
+
+// Logits (base 2) of rows 16nt + (lane & 15) for tokens t0 + 4*(lane>>4) + j.
+template <typename T>
+__device__ __forceinline__ void subtile_logits(const ScoreArgs& a, const typename Elem<T>::vec8 (&kr)[4],
+                                               const T* s_q, int nt, int t0, int lane, float (&x)[4]) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const T* qrow = s_q + (16 * nt + (lane & 15)) * kQPitch + 8 * (lane >> 4);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mma_16x16x32(kr[s], load8<T>(qrow + 32 * s), acc);
+  const int r = 16 * nt + (lane & 15);
+  const int w = r % a.W;
+  const int causal_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W + w : a.L - 1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int t = t0 + 4 * (lane >> 4) + j;
+    float v;
+    if (a.flags & (HC_SCORE_ROUND_BF16 | HC_SCORE_ROUND_F16))
+      v = round_mode(round_mode(acc[j], a.flags) * a.scale, a.flags);
+    else
+      v = acc[j] * a.scale;
+    v *= 1.4426950408889634f;
+    x[j] = (t < a.L && t <= causal_limit) ? v : -INFINITY;
+  }
+}
+
+__device__ __forceinline__ void merge_ml(float& m, float& l, float m2, float l2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  l = l * fast_exp2(m - mn) + l2 * fast_exp2(m2 - mn);
+  m = mn;
+}
+
+template <typename T, bool STORE>
+__global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs a, float* __restrict__ part) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* s_q = reinterpret_cast<T*>(smem);
+  float* s_st = reinterpret_cast<float*>(smem + (size_t)a.NT * 16 * kQPitch * sizeof(T));  // [waves][rows][2]
+  const int job = blockIdx.y, chunk = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = a.NT * 16;
+  stage_queries<T>(a, job, s_q);
+  for (int i = threadIdx.x; i < kScoreWaves * rows; i += kScoreWaves * 64) {
+    s_st[2 * i] = -INFINITY;
+    s_st[2 * i + 1] = 0.f;
+  }
+  __syncthreads();
+  float* my = s_st + (size_t)wave * rows * 2;
+  for (int st = wave; st < kScoreChunk / 16; st += kScoreWaves) {
+    const int t0 = chunk * kScoreChunk + st * 16;
+    if (t0 >= a.L) break;
+    typename Elem<T>::vec8 kr[4];
+    load_k_subtile<T, STORE>(a, job, t0, lane, kr);
+    for (int nt = 0; nt < a.NT; ++nt) {
+      float x[4];
+      subtile_logits<T>(a, kr, s_q, nt, t0, lane, x);
+      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      float sm = 0.f;
+      if (mx != -INFINITY) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sm += fast_exp2(x[j] - mx);
+      }
+      sm += __shfl_xor(sm, 16, 64);
+      sm += __shfl_xor(sm, 32, 64);
+      if (lane < 16) {
+        const int r = 16 * nt + lane;
+        float m = my[2 * r], l = my[2 * r + 1];
+        merge_ml(m, l, mx, sm);
+        my[2 * r] = m;
+        my[2 * r + 1] = l;
+      }
+    }
+  }
+  __syncthreads();
+  const int nchunks = gridDim.x;
+  for (int r = threadIdx.x; r < a.R; r += kScoreWaves * 64) {
+    float m = -INFINITY, l = 0.f;
+#pragma unroll
+    for (int w = 0; w < kScoreWaves; ++w) merge_ml(m, l, s_st[(w * rows + r) * 2], s_st[(w * rows + r) * 2 + 1]);
+    float* o = part + (((int64_t)job * nchunks + chunk) * a.R + r) * 2;
+    o[0] = m;
+    o[1] = l;
+  }
+}
+
+// One wave per (job, row): lanes stride over the chunks, then a xor tree.
+__global__ __launch_bounds__(256) void score_stats_merge_kernel(const float* __restrict__ part, int nchunks, int R,
+                                                                int njobs, float* __restrict__ stats) {
+  const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (i >= njobs * R) return;
+  const int job = i / R, r = i % R;
+  float m = -INFINITY, l = 0.f;
+  for (int c = lane; c < nchunks; c += 64) {
+    const float* p = part + (((int64_t)job * nchunks + c) * R + r) * 2;
+    merge_ml(m, l, p[0], p[1]);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, 64), l2 = __shfl_xor(l, off, 64);
+    merge_ml(m, l, m2, l2);
+  }
+  if (lane == 0) {
+    stats[2 * i] = m;
+    stats[2 * i + 1] = l;
+  }
+}
+
+template <typename T, bool STORE>
+__global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs a, const float* __restrict__ stats,
+                                                                      float* __restrict__ A) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* s_q = reinterpret_cast<T*>(smem);
+  float* s_ml = reinterpret_cast<float*>(smem + (size_t)a.NT * 16 * kQPitch * sizeof(T));  // [rows][2]
+  const int job = blockIdx.y, chunk = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rows = a.NT * 16;
+  const bool sum_w = (a.flags & HC_SCORE_SUM_WINDOW) != 0;
+  stage_queries<T>(a, job, s_q);
+  for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
+    s_ml[2 * r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] : -INFINITY;
+    s_ml[2 * r + 1] = r < a.R ? stats[((int64_t)job * a.R + r) * 2 + 1] : 1.f;
+  }
+  __syncthreads();
+  const int wout = sum_w ? 1 : a.W;
+  for (int st = wave; st < kScoreChunk / 16; st += kScoreWaves) {
+    const int t0 = chunk * kScoreChunk + st * 16;
+    if (t0 >= a.span) break;
+    typename Elem<T>::vec8 kr[4];
+    load_k_subtile<T, STORE>(a, job, t0, lane, kr);
+    float gsum[4] = {0.f, 0.f, 0.f, 0.f};  // running window sum (W >= 16)
+    for (int nt = 0; nt < a.NT; ++nt) {
+      float x[4];
+      subtile_logits<T>(a, kr, s_q, nt, t0, lane, x);
+      const int r = 16 * nt + (lane & 15);
+      const float M = s_ml[2 * r], Z = s_ml[2 * r + 1];
+      float p[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        p[j] = (x[j] == -INFINITY || r >= a.R) ? 0.f : round_mode(fast_exp2(x[j] - M) / Z, a.flags);
+      if (!sum_w) {
+        // Row r = g*W + w -> A[job][w][g][t].
+        if (r < a.R) {
+          const int g = r / a.W, w = r % a.W;
+          float* o = A + (((int64_t)job * wout + w) * a.G + g) * a.span;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 4 * (lane >> 4) + j;
+            if (t < a.span) o[t] = p[j];
+          }
+        }
+        continue;
+      }
+      if (a.W >= 16) {
+        // The 16 rows of this N-tile all belong to one query head.
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float v = p[j];
+          v += __shfl_xor(v, 1, 64);
+          v += __shfl_xor(v, 2, 64);
+          v += __shfl_xor(v, 4, 64);
+          v += __shfl_xor(v, 8, 64);
+          gsum[j] += v;
+        }
+        if (((16 * (nt + 1)) % a.W) == 0) {
+          const int g = (16 * nt) / a.W;
+          if ((lane & 15) == 0 && g < a.G) {
+            float* o = A + ((int64_t)job * a.G + g) * a.span;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int t = t0 + 4 * (lane >> 4) + j;
+              if (t < a.span) o[t] = round_mode(gsum[j], a.flags);
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) gsum[j] = 0.f;
+        }
+      } else {
+        // W in {1, 2, 4, 8}: a query head's rows are W adjacent lanes.
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float v = p[j];
+          for (int off = 1; off < a.W; off <<= 1) v += __shfl_xor(v, off, 64);
+          p[j] = v;
+        }
+        if ((lane & (a.W - 1)) == 0 && r < a.R) {
+          const int g = r / a.W;
+          float* o = A + ((int64_t)job * a.G + g) * a.span;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int t = t0 + 4 * (lane >> 4) + j;
+            if (t < a.span) o[t] = round_mode(p[j], a.flags);
+          }
+        }
+      }
+    }
+  }
+}
+
+__global__ void score_pool_kernel(const float* __restrict__ A, int G, int span, int pooling, int kernel, int flags,
+                                  float* __restrict__ S) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int jw = blockIdx.y;  // job * wout + w'
+  if (t >= span) return;
+  const int p = kernel / 2;
+  float best = -INFINITY;
+  for (int g = 0; g < G; ++g) {
+    const float* a = A + ((int64_t)jw * G + g) * span;
+    float acc = pooling == 0 ? 0.f : -INFINITY;
+    for (int d = -p; d <= p; ++d) {
+      const int u = t + d;
+      if (u < 0 || u >= span) continue;  // zero / -inf padding
+      acc = pooling == 0 ? acc + a[u] : fmaxf(acc, a[u]);
+    }
+    if (pooling == 0) acc = acc / (float)kernel;
+    best = fmaxf(best, round_mode(acc, flags));
+  }
+  S[(int64_t)jw * span + t] = best;
+}
+
+static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+size_t score_workspace_bytes(int njobs, int L, int G, int W, int flags) {
+  const int R = G * W;
+  const int nchunks = (L + kScoreChunk - 1) / kScoreChunk;
+  const int wout = (flags & HC_SCORE_SUM_WINDOW) ? 1 : W;
+  return align256((size_t)njobs * nchunks * R * 2 * sizeof(float)) +
+         align256((size_t)njobs * R * 2 * sizeof(float)) + align256((size_t)njobs * wout * G * L * sizeof(float));
+}
+
+template <typename T, bool STORE>
+static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* scores, void* ws, hipStream_t s) {
+  const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
+  const int wout = (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : a.W;
+  float* part = reinterpret_cast<float*>(ws);
+  float* stats = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) +
+                                          align256((size_t)njobs * nchunks * a.R * 2 * sizeof(float)));
+  float* A = reinterpret_cast<float*>(reinterpret_cast<char*>(stats) + align256((size_t)njobs * a.R * 2 * sizeof(float)));
+  const size_t qbytes = (size_t)a.NT * 16 * kQPitch * sizeof(T);
+  const size_t lds1 = qbytes + (size_t)kScoreWaves * a.NT * 16 * 2 * sizeof(float);
+  const size_t lds3 = qbytes + (size_t)a.NT * 16 * 2 * sizeof(float);
+  hipLaunchKernelGGL((score_stats_kernel<T, STORE>), dim3(nchunks, njobs), dim3(kScoreWaves * 64), lds1, s, a, part);
+  int rc = check_launch("hc_score(stats)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nchunks, a.R,
+                     njobs, stats);
+  if ((rc = check_launch("hc_score(merge)"))) return rc;
+  const int nchunks_span = (a.span + kScoreChunk - 1) / kScoreChunk;
+  if (nchunks_span > 0) {
+    hipLaunchKernelGGL((score_probs_kernel<T, STORE>), dim3(nchunks_span, njobs), dim3(kScoreWaves * 64), lds3, s, a,
+                       stats, A);
+    if ((rc = check_launch("hc_score(probs)"))) return rc;
+    hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + 255) / 256, njobs * wout), dim3(256), 0, s, A, a.G, a.span,
+                       pooling, kernel, a.flags, scores);
+    if ((rc = check_launch("hc_score(pool)"))) return rc;
+  }
+  return HC_OK;
+}
+
+}  // namespace hc
+
+using namespace hc;
+
+extern "C" size_t hc_score_workspace_size(int njobs, int seq_len, int group, int window, int flags) {
+  if (njobs <= 0 || seq_len <= 0 || group <= 0 || window <= 0) return 0;
+  return score_workspace_bytes(njobs, seq_len, group, window, flags);
+}
+
+extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride, int64_t q_row_stride,
+                        const void* k, const int64_t* k_off, int64_t k_tok_stride, const int64_t* row_tile_off,
+                        const int32_t* k_row, int njobs, int seq_len, int group, int window, int flags, int span,
+                        int pooling, int kernel, float scale, float* scores, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (njobs < 0 || njobs > 65535 || seq_len < 0 || group < 1 || window < 1)
+    return set_error(HC_ERR_INVALID, "hc_score: njobs=%d seq_len=%d group=%d window=%d", njobs, seq_len, group,
+                     window);
+  if (njobs == 0 || seq_len == 0) return HC_OK;
+  const bool sum_w = (flags & HC_SCORE_SUM_WINDOW) != 0;
+  if (sum_w && window >= 16 ? (window % 16) != 0 : (sum_w && (window & (window - 1)) != 0))
+    return set_error(HC_ERR_INVALID, "hc_score: a summed window must be 1, 2, 4, 8 or a multiple of 16 (got %d)",
+                     window);
+  if (span < 0 || span > seq_len) return set_error(HC_ERR_INVALID, "hc_score: span %d outside [0, %d]", span, seq_len);
+  if (pooling != 0 && pooling != 1) return set_error(HC_ERR_INVALID, "hc_score: pooling must be 0 (avg) or 1 (max)");
+  if (kernel < 1 || (kernel % 2) == 0 || kernel > 63)
+    return set_error(HC_ERR_INVALID, "hc_score: pooling kernel must be odd and <= 63 (got %d)", kernel);
+  const int R = group * window;
+  int NT = (R + 15) / 16;
+  if (NT > 16) return set_error(HC_ERR_INVALID, "hc_score: group*window = %d exceeds 256 rows", R);
+  if (dtype == HC_DTYPE_F32 && NT > 8)
+    return set_error(HC_ERR_INVALID, "hc_score: float32 supports group*window <= 128 (got %d)", R);
+  if (!q || !q_off || !k || !scores || !workspace)
+    return set_error(HC_ERR_INVALID, "hc_score: null pointer argument");
+  const bool store = row_tile_off != nullptr;
+  if (store ? !k_row : !k_off) return set_error(HC_ERR_INVALID, "hc_score: missing key addressing");
+  if (!store && (k_tok_stride < HC_HEAD_DIM || (k_tok_stride % 8) != 0))
+    return set_error(HC_ERR_INVALID, "hc_score: key token stride %lld", (long long)k_tok_stride);
+  if (workspace_bytes < score_workspace_bytes(njobs, seq_len, group, window, flags))
+    return set_error(HC_ERR_INVALID, "hc_score: workspace too small");
+  ScoreArgs a;
+  a.q = q;
+  a.q_off = q_off;
+  a.q_head_stride = q_head_stride;
+  a.q_row_stride = q_row_stride;
+  a.k = k;
+  a.k_off = k_off;
+  a.k_tok_stride = k_tok_stride;
+  a.row_tile_off = row_tile_off;
+  a.k_row = k_row;
+  a.L = seq_len;
+  a.G = group;
+  a.W = window;
+  a.R = R;
+  a.NT = NT;
+  a.flags = flags;
+  a.span = span;
+  a.scale = scale;
+  hipStream_t s = (hipStream_t)stream;
+#define HC_SCORE_DISPATCH(T)                                                                          \
+  return store ? launch_score<T, true>(a, njobs, pooling, kernel, scores, workspace, s)               \
+               : launch_score<T, false>(a, njobs, pooling, kernel, scores, workspace, s);
+  switch (dtype) {
+    case HC_DTYPE_BF16: { HC_SCORE_DISPATCH(__bf16) }
+    case HC_DTYPE_F16: { HC_SCORE_DISPATCH(_Float16) }
+    case HC_DTYPE_F32: { HC_SCORE_DISPATCH(float) }
+    default:
+      return set_error(HC_ERR_INVALID, "hc_score: unknown dtype %d", dtype);
+  }
+#undef HC_SCORE_DISPATCH
+}

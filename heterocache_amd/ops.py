@@ -167,3 +167,53 @@ def store_read(kstore, vstore, row_tile_off, rows_sel, count, stream=None):
     _lib.check(lib.hc_store_read(dtype_code(kstore.dtype), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
                                  _ptr(rows_sel), n, int(count), _ptr(dk), _ptr(dv), _stream(stream)))
     return dk, dv
+
+
+def score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, seq_len, group, window, span, pooling,
+          kernel, scale, flags=0, row_tile_off=None, k_row=None, out=None, stream=None):
+    """Pooled window scores [jobs, W', span] (see hc_score in include/hc.h).
+
+    q / k are the base tensors; q_off / k_off are int64 device tensors of
+    per-job element offsets (k_off unused when reading a tiled store through
+    row_tile_off / k_row).
+    """
+    lib = _lib.load()
+    _require_cuda(q, k, q_off, k_off, row_tile_off, k_row)
+    if q.dtype != k.dtype:
+        raise TypeError("q and k must share a dtype")
+    njobs = q_off.numel()
+    wout = 1 if flags & _lib.HC_SCORE_SUM_WINDOW else window
+    if out is None:
+        out = torch.empty((njobs, wout, span), dtype=torch.float32, device=q.device)
+    elif out.dtype != torch.float32 or out.numel() < njobs * wout * span or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float32 tensor of [jobs, W', span]")
+    if q_off.dtype != torch.int64 or (k_off is not None and k_off.dtype != torch.int64):
+        raise TypeError("offsets must be int64")
+    if k_row is not None and k_row.dtype != torch.int32:
+        raise TypeError("k_row must be int32")
+    nbytes = lib.hc_score_workspace_size(njobs, seq_len, group, window, flags)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    pool = {"avgpool": 0, "maxpool": 1}[pooling] if isinstance(pooling, str) else int(pooling)
+    _lib.check(lib.hc_score(dtype_code(q.dtype), _ptr(q), _ptr(q_off), int(q_head_stride), int(q_row_stride), _ptr(k),
+                            _ptr(k_off), int(k_tok_stride), _ptr(row_tile_off), _ptr(k_row), njobs, int(seq_len),
+                            int(group), int(window), int(flags), int(span), pool, int(kernel), float(scale),
+                            _ptr(out), _ptr(ws), ws.numel(), _stream(stream)))
+    return out
+
+
+def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None):
+    """Ascending kept positions per job: scores [jobs, >= span] float32, caps int32 [jobs]."""
+    lib = _lib.load()
+    _require_cuda(scores, caps, idx, counts)
+    if scores.dtype != torch.float32 or scores.dim() != 2 or scores.stride(1) != 1:
+        raise ValueError("scores must be float32 [jobs, n] with unit stride")
+    if caps.dtype != torch.int32:
+        raise TypeError("caps must be int32")
+    njobs = scores.shape[0]
+    if idx is None:
+        idx = torch.empty((njobs, span + window), dtype=torch.int32, device=scores.device)
+    if counts is None:
+        counts = torch.empty(njobs, dtype=torch.int32, device=scores.device)
+    _lib.check(lib.hc_select_topk(_ptr(scores), scores.stride(0), njobs, int(span), _ptr(caps), int(window), _ptr(idx),
+                                  idx.stride(0), _ptr(counts), _stream(stream)))
+    return idx, counts

@@ -106,6 +106,45 @@ int hc_append(int dtype, const void* k_new, const void* v_new, int64_t src_row_s
 int hc_store_read(int dtype, const void* kstore, const void* vstore, const int64_t* row_tile_off,
                   const int32_t* rows_sel, int nrows, int count, void* dst_k, void* dst_v, void* stream);
 
+/* hc_score flags */
+#define HC_SCORE_CAUSAL_WINDOW 1 /* window row w sees keys t <= L - W + w (kv_cluster.py:169-175) */
+#define HC_SCORE_SUM_WINDOW 2    /* sum probabilities over the W rows of a query head (kv_cluster.py:178) */
+#define HC_SCORE_ROUND_BF16 4    /* reproduce the reference's casts to bfloat16 */
+#define HC_SCORE_ROUND_F16 8     /* reproduce the reference's casts to float16 */
+
+/*
+ * Pooled observation-window scores, maxed over the GQA group:
+ *   S[j][w'][t] = max_g pool_k( sum_w softmax_t(scale * q_{j,g,w} . k_{j,t} + mask) ),  t < span
+ * (no sum, w' = w, without HC_SCORE_SUM_WINDOW).  Query row (g, w) of job j is
+ * q + q_off[j] + g*q_head_stride + w*q_row_stride (128 contiguous elements).
+ * Keys: natural layout, token t of job j at k + k_off[j] + t*k_tok_stride; or,
+ * when row_tile_off != NULL, slots [0, seq_len) of store row k_row[j] of the
+ * tiled store k (read in place).  pooling: 0 = avg_pool1d (zero padding,
+ * divisor kernel), 1 = max_pool1d (-inf padding); odd kernel, padding kernel/2.
+ * scores: [njobs][W' ][span] float32.  Replaces the scoring op sequences of
+ * HeteroCache.prefill_select (heterocache/cache_utils.py:807-829),
+ * init_coefficient (:1158-1187), decode_select (:1030-1057) and
+ * SnapKVCluster.update_kv (heterocache/kv_cluster.py:165-185).
+ */
+int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride, int64_t q_row_stride,
+             const void* k, const int64_t* k_off, int64_t k_tok_stride, const int64_t* row_tile_off,
+             const int32_t* k_row, int njobs, int seq_len, int group, int window, int flags, int span, int pooling,
+             int kernel, float scale, float* scores, void* workspace, size_t workspace_bytes, void* stream);
+size_t hc_score_workspace_size(int njobs, int seq_len, int group, int window, int flags);
+
+/*
+ * Per-job top-k kept set in ascending position order.  Job j keeps the
+ * cap[j] positions of scores[j*score_stride + t], t < span, ranked by (score
+ * descending, position ascending); with window > 0 it keeps cap[j] - window of
+ * them and appends positions span .. span+window-1.  Writes idx[j*idx_stride
+ * + i] (at most idx_stride entries per job) and counts[j] (optional).
+ * Replaces topk -> mask -> sort of heterocache/cache_utils.py:831-851, the
+ * SnapKV topk + window concat of heterocache/kv_cluster.py:187-197 and the
+ * drift / retrieval topk of heterocache/cache_utils.py:1060-1061, 1090-1093.
+ */
+int hc_select_topk(const float* scores, int64_t score_stride, int njobs, int span, const int32_t* caps, int window,
+                   int32_t* idx, int64_t idx_stride, int32_t* counts, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

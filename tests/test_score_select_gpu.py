@@ -1,0 +1,165 @@
+"""hc_score and hc_select_topk against the oracle.
+
+Scores: float32 chain within rtol 2e-4 of the float64-evaluated oracle on the
+same (dtype-rounded) inputs; bf16 cast chain within one bf16 ulp with >= 97%
+exact.  Selection: bit-exact against the oracle's (-score, index) ranking on
+the SAME score array (ties included).  End to end (GPU scores -> GPU
+selection vs oracle scores -> oracle selection): identical except for
+positions whose oracle score lies within 1e-5 (relative) of the budget
+threshold.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from heterocache_amd import compress
+from heterocache_amd.store import KVStore
+from oracle import hc_oracle as O
+from tests.gpu_util import as_np
+
+pytestmark = pytest.mark.gpu
+
+
+def qk(dev, B, Hq, Hkv, Lq, L, dtype, seed, strided=True, sinks=False):
+    g = torch.Generator().manual_seed(seed)
+    if strided:  # the projection layout: [B, L, H, d].transpose(1, 2)
+        q = torch.randn((B, Lq, Hq, 128), generator=g).to(dtype).to(dev).transpose(1, 2)
+        k = torch.randn((B, L, Hkv, 128), generator=g).to(dtype).to(dev).transpose(1, 2)
+    else:
+        q = torch.randn((B, Hq, Lq, 128), generator=g).to(dtype).to(dev)
+        k = torch.randn((B, Hkv, L, 128), generator=g).to(dtype).to(dev)
+    if sinks:
+        k = k.clone()
+        k[:, :, :4] = 2 * q[:, ::Hq // Hkv, -1:].mean(dim=2, keepdim=True)[:, :Hkv].to(dtype)
+    return q, k
+
+
+def rel_err(a, b):
+    return np.abs(a - b).max() / max(np.abs(b).max(), 1e-30)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32, torch.float16])
+@pytest.mark.parametrize("pooling,kernel", [("avgpool", 5), ("maxpool", 7)])
+def test_last_query_scores(dev, dtype, pooling, kernel):
+    B, Hq, Hkv, L = 1, 32, 8, 3000
+    q, k = qk(dev, B, Hq, Hkv, L, L, dtype, 1, sinks=True)
+    heads = [0, 1, 2, 5, 7]
+    s = compress.last_query_scores(q, k, heads, 4, pooling, kernel)
+    qn, kn = as_np(q), as_np(k)
+    ref = O.last_query_scores(np.stack([qn[0, h * 4:(h + 1) * 4, -1] for h in heads]), kn[0, heads], pooling, kernel)
+    assert s.shape == (len(heads), L)
+    assert rel_err(as_np(s), ref) < 2e-4
+
+
+def test_last_query_scores_batch_and_gqa7(dev):
+    B, Hq, Hkv, L = 2, 28, 4, 1500
+    q, k = qk(dev, B, Hq, Hkv, L, L, torch.bfloat16, 2)
+    s = compress.last_query_scores(q, k, range(Hkv), 7, "avgpool", 5)
+    qn, kn = as_np(q), as_np(k)
+    for b in range(B):
+        ref = O.last_query_scores(np.stack([qn[b, h * 7:(h + 1) * 7, -1] for h in range(Hkv)]), kn[b], "avgpool", 5)
+        assert rel_err(as_np(s[b * Hkv:(b + 1) * Hkv]), ref) < 2e-4
+
+
+@pytest.mark.parametrize("G,W", [(4, 32), (1, 32), (4, 16), (2, 8), (4, 4)])
+def test_snapkv_window_scores(dev, G, W):
+    B, Hkv, L = 1, 3, 2000
+    q, k = qk(dev, B, Hkv * G, Hkv, L, L, torch.float32, 3)
+    s = compress.window_scores(q, k, range(Hkv), G, W, "maxpool", 7, window_keep=True)
+    qn, kn = as_np(q), as_np(k)
+    qw = np.stack([qn[0, h * G:(h + 1) * G, -W:] for h in range(Hkv)])
+    ref = O.window_scores(qw, kn[0], "maxpool", 7, window_keep=True)
+    assert s.shape == (Hkv, L - W)
+    assert rel_err(as_np(s), ref) < 2e-4
+
+
+def test_bf16_cast_chain(dev):
+    B, Hq, Hkv, L = 1, 32, 8, 4096
+    q, k = qk(dev, B, Hq, Hkv, L, L, torch.bfloat16, 4)
+    s = as_np(compress.last_query_scores(q, k, range(Hkv), 4, "avgpool", 5, round_dtype=torch.bfloat16))
+    qn, kn = as_np(q), as_np(k)
+    ref = O.last_query_scores(np.stack([qn[0, h * 4:(h + 1) * 4, -1] for h in range(Hkv)]), kn[0], "avgpool", 5,
+                              io_dtype="bfloat16")
+    assert np.array_equal(s, O.round_bf16(s)), "scores must be bf16 values"
+    rel = np.abs(s - ref) / np.maximum(np.abs(ref), 1e-30)
+    assert rel.max() <= 2.0 ** -7 + 1e-9
+    assert (s == ref).mean() >= 0.97
+
+
+def test_pivot_step_scores_read_store_in_place(dev):
+    B, Hq, Hkv, L, S, G = 1, 32, 8, 2500, 5, 4
+    q, k = qk(dev, B, Hq, Hkv, 1, L, torch.bfloat16, 5, strided=False)
+    steps = torch.randn((B, Hq, S, 128), generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).to(dev)
+    store = KVStore([L + 64] * Hkv, torch.bfloat16, dev)
+    store.write_rows(k, k, [(0, h) for h in range(Hkv)], list(range(Hkv)), [L] * Hkv)
+    pivots = [6, 7]
+    s = compress.pivot_step_scores(steps, store, pivots, pivots, G, L, "avgpool", 5)
+    sn, kn = as_np(steps), as_np(k)
+    for j, h in enumerate(pivots):
+        ref = O.pivot_step_scores(sn[0, h * G:(h + 1) * G], kn[0, h], "avgpool", 5)
+        assert rel_err(as_np(s[j]), ref) < 2e-4
+
+
+# -- selection --------------------------------------------------------------------
+def check_select(scores_np, caps, window, idx, counts):
+    span = scores_np.shape[1]
+    for j, cap in enumerate(caps):
+        if window:
+            body = O.topk_select(scores_np[j], min(max(cap - window, 0), span))
+            ref = np.concatenate([body, np.arange(span, span + window)])
+        else:
+            ref = O.topk_select(scores_np[j], min(cap, span))
+        assert counts[j] == len(ref), (j, counts[j], len(ref))
+        assert np.array_equal(idx[j, :len(ref)], ref), f"job {j}: kept set differs"
+
+
+@pytest.mark.parametrize("quant", [None, 1e-3, 0.25])
+def test_select_bit_exact_with_ties(dev, quant):
+    rng = np.random.default_rng(7)
+    span = 10007
+    s = rng.random((6, span)).astype(np.float32)
+    if quant:  # heavy ties
+        s = (np.round(s / quant) * quant).astype(np.float32)
+    s[0, 100:200] = 0.0
+    caps = [0, 1, 37, 5000, span, span + 5]
+    st = torch.tensor(s).to(dev)
+    idx, counts = compress.select_kept(st, caps)
+    check_select(s, caps, 0, as_np(idx).astype(np.int64), as_np(counts).astype(np.int64))
+
+
+def test_select_window_mode(dev):
+    rng = np.random.default_rng(8)
+    span, W = 4000, 32
+    s = rng.random((3, span)).astype(np.float32)
+    caps = [W, 1000, span + W]
+    idx, counts = compress.select_kept(torch.tensor(s).to(dev), caps, window=W)
+    check_select(s, caps, W, as_np(idx).astype(np.int64), as_np(counts).astype(np.int64))
+
+
+def test_select_all_equal_scores(dev):
+    s = np.full((2, 3000), 0.125, np.float32)
+    idx, counts = compress.select_kept(torch.tensor(s).to(dev), [1500, 7])
+    assert as_np(idx)[0, :1500].tolist() == list(range(1500))
+    assert as_np(idx)[1, :7].tolist() == list(range(7))
+
+
+def test_end_to_end_indices_outside_tie_band(dev):
+    """GPU scores + GPU selection vs oracle scores + oracle selection."""
+    B, Hq, Hkv, L = 1, 32, 8, 4096
+    q, k = qk(dev, B, Hq, Hkv, L, L, torch.float32, 9, sinks=True)
+    caps = [1024, 3072, 1024, 3072, 1024, 1024, 3072, 3072]
+    s = compress.last_query_scores(q, k, range(Hkv), 4, "maxpool", 7)
+    idx, counts = compress.select_kept(s, caps)
+    qn, kn = as_np(q), as_np(k)
+    ref_s = O.last_query_scores(np.stack([qn[0, h * 4:(h + 1) * 4, -1] for h in range(Hkv)]), kn[0], "maxpool", 7)
+    idx, counts = idx.cpu().numpy(), counts.cpu().numpy()
+    for h in range(Hkv):
+        got = set(idx[h, :counts[h]].tolist())
+        ref = O.topk_select(ref_s[h], caps[h])
+        tau = np.sort(ref_s[h])[::-1][caps[h] - 1]
+        diff = got.symmetric_difference(ref.tolist())
+        band = [t for t in diff if abs(ref_s[h][t] - tau) > 1e-5 * abs(tau)]
+        assert not band, f"head {h}: {len(band)} positions differ outside the tie band"
+        assert len(diff) <= 0.01 * caps[h]
