@@ -47,6 +47,12 @@ SIGNATURES = {
     "hc_score_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "hc_select_topk": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int, c_void_p, c_int64, c_void_p,
                                c_void_p]),
+    "hc_set_bits": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,
+                            c_void_p]),
+    "hc_overlap_count": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,
+                                 c_void_p]),
+    "hc_drift_decide": (c_int, [c_void_p, c_int, c_int, c_int, c_int, ctypes.c_double, c_void_p, c_void_p, c_void_p,
+                                c_void_p]),
     "hc_store_read": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,
                               c_void_p]),
 }

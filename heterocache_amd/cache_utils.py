@@ -1,0 +1,437 @@
+"""HeteroCache: the reference's KV-cache manager on libhc kernels.
+
+Drop-in for heterocache/cache_utils.py:610-1196 (same class and method names,
+argument meaning and errors).  Storage is the tiled ragged store
+(`heterocache_amd.store.KVStore`, one per layer) instead of the paged pool;
+every tensor operation on the path is a libhc kernel:
+
+  update (prefill)     keep-head copy -> hc_gather_store; full-KV tier backup
+                       of satellite heads -> async D2H copy on a side stream
+  update (decode)      the new token is held and appended by the fused decode
+                       attention launch (or hc_append if something else
+                       observes the lengths first)
+  init_coefficient     hc_score + hc_select_topk + hc_set_bits (pivot sets)
+  prefill_select       hc_score + hc_select_topk + hc_gather_store
+  decode_attention     hc_decode_attn (replaces flash_attn_with_kvcache)
+  decode_select        hc_score on the store + hc_select_topk +
+                       hc_overlap_count + hc_drift_decide; the retrieval
+                       gather from the host tier runs on the side stream and
+                       is gated by the device trigger flag -- no host sync.
+
+Behavioural choices (defaults; `reference_quirks=True` restores the
+reference's behaviour where it differs):
+  * retrieval lengths use the float32 prefill cap (the reference's float64
+    lengths can exceed the prefill region by one row and overwrite the first
+    generated token, heterocache/cache_utils.py:1084-1087);
+  * the pivot reference set is the pivot's own (the reference indexes its
+    sets by relation order but builds them in ascending pivot order,
+    heterocache/cache_utils.py:1063 vs :1156-1190);
+  * batch > 1 is supported per row (the reference's pool sizing and
+    retrieval squeeze() assume batch 1, heterocache/cache_utils.py:704-722,
+    :1093).
+"""
+from typing import Dict, Optional
+
+import numpy as np
+import torch
+from transformers.cache_utils import DynamicCache
+
+from . import compress, ops
+from .store import KVStore
+
+
+def get_compress_len(compression_ratio, full_heads, ori_len, num_kv_heads):
+    """Base budget, heterocache/cache_utils.py:15-16 (float64, truncated)."""
+    return int((compression_ratio * num_kv_heads - full_heads) * ori_len / (num_kv_heads - full_heads))
+
+
+class HeteroCacheConfig:
+    """heterocache/cache_utils.py:41-68, plus the options of this build.
+
+    retrieval_topk: cap on the tokens retrieved into a satellite (None =
+    the reference's full budget).  window_size: observation window of the
+    prefill scorer (1 = the reference's last query).  round_scores: reproduce
+    the reference's casts of scores to the model dtype.  reference_quirks:
+    float64 retrieval lengths and relation-order pivot sets, as the reference.
+    """
+
+    def __init__(self, data: Optional[Dict], compression_ratio: Optional[float] = 0.5,
+                 stable_threshold: Optional[float] = 0.5, real_offload: Optional[bool] = True,
+                 max_gen_len: Optional[int] = 128, decode_step: Optional[int] = 4, pooling: Optional[str] = "avgpool",
+                 kernel_size: Optional[int] = 5, num_attn_heads: Optional[int] = 32, num_kv_heads: Optional[int] = 8,
+                 num_layers: Optional[int] = 32, retrieval_topk: Optional[int] = None, window_size: int = 1,
+                 round_scores: bool = False, reference_quirks: bool = False, tiles_per_wave: Optional[int] = None):
+        self.data = data
+        self.stable_threshold = stable_threshold
+        self.compression_ratio = compression_ratio
+        self.real_offload = real_offload
+        self.max_gen_len = max_gen_len
+        self.decode_step = decode_step
+        self.pooling = pooling
+        self.kernel_size = kernel_size
+        self.quant_method = None
+        self.num_attn_heads = num_attn_heads
+        self.num_kv_heads = num_kv_heads
+        self.num_layers = num_layers
+        self.retrieval_topk = retrieval_topk
+        self.window_size = window_size
+        self.round_scores = round_scores
+        self.reference_quirks = reference_quirks
+        self.tiles_per_wave = tiles_per_wave
+
+
+def _f32_caps(base, ratios, seq_len):
+    """(base * ratio_f32).int() clamped to [0, L] (heterocache/cache_utils.py:793-799)."""
+    r = np.asarray(ratios, dtype=np.float32)
+    caps = np.trunc(np.float32(base) * r).astype(np.int64)
+    return np.clip(caps, 0, seq_len)
+
+
+class _LayerDrift:
+    """Device state of one layer's pivot monitoring."""
+
+    def __init__(self):
+        self.leaders = []      # relation order: pivot kv-head per leader
+        self.members = []      # satellite kv-heads per leader
+        self.ref_bits = None   # [n_lead * B, words] int32 bitmask sets
+        self.trigger = None    # [n_lead] int32
+        self.qbuf = None       # [B, Hq, S, 128] buffered decode queries
+        self.count = 0
+
+
+class HeteroCache(DynamicCache):
+    """Compressed per-head KV cache (heterocache/cache_utils.py:610)."""
+
+    def __init__(self, cache_config):
+        super().__init__()
+        cfg = cache_config
+        self.config = cfg
+        self.num_attn_heads = cfg.num_attn_heads
+        self.num_kv_heads = cfg.num_kv_heads
+        self.num_layers = cfg.num_layers
+        self.gqa = self.num_kv_heads != self.num_attn_heads
+        self.num_key_value_groups = self.num_attn_heads // self.num_kv_heads
+        self.total_kv_heads = self.num_kv_heads * self.num_layers
+        self.compression_ratio = cfg.compression_ratio
+        self.data = cfg.data
+        self.full_heads = self.data["meta"]["counts"]["volatile"] + self.data["meta"]["counts"]["pivot"]
+        self.decode_step = cfg.decode_step
+        self.stable_threshold = cfg.stable_threshold
+        self.device = "cpu" if cfg.real_offload else "cuda"
+        self.pooling = cfg.pooling
+        self.kernel_size = cfg.kernel_size
+        self.quirks = bool(getattr(cfg, "reference_quirks", False))
+        self.retrieval_topk = getattr(cfg, "retrieval_topk", None)
+        self.window_size = int(getattr(cfg, "window_size", 1) or 1)
+        self.round_scores = bool(getattr(cfg, "round_scores", False))
+        self.tiles_per_wave = getattr(cfg, "tiles_per_wave", None) or ops.DEFAULT_TILES_PER_WAVE
+
+        self.stores = [None] * self.num_layers
+        self.prefill_topk_set = [None] * self.num_layers
+        self.key_cache_cpu = [None] * self.num_layers
+        self.value_cache_cpu = [None] * self.num_layers
+        self._tier_heads = [None] * self.num_layers   # kv-head -> head index inside the tier tensor
+        self._tier_ready = [None] * self.num_layers   # event: tier copy done (side stream)
+        self._retrieval_done = [None] * self.num_layers
+        self._pending = [None] * self.num_layers      # decode token awaiting its append
+        self._drift = [None] * self.num_layers
+        self.layer_head_capacities = [None] * self.num_layers
+        self.bsz = None
+        self.head_dim = None
+        self.prefill_len = None
+        self._seen_tokens = 0
+        self._side = None
+
+    # -- reference API ------------------------------------------------------
+    def __bool__(self):
+        return True
+
+    def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
+        return self._seen_tokens if self._seen_tokens is not None else 0
+
+    @property
+    def heads_len(self):
+        """Per-layer int32 [B*Hkv] lengths (heterocache/cache_utils.py:658)."""
+        for i in range(self.num_layers):
+            self._flush_append(i)
+        return [s.row_len if s is not None else None for s in self.stores]
+
+    def _side_stream(self, device):
+        if self._side is None:
+            self._side = torch.cuda.Stream(device=device)
+        return self._side
+
+    def _init_layer_storage(self, layer_idx, device, dtype):
+        """Row capacities for the whole lifetime (heterocache/cache_utils.py:693-766)."""
+        L, gen = self.prefill_len, self.config.max_gen_len
+        keep = set(self.data["need_to_keep_counts"][layer_idx])
+        alloc = self.data["allocation_matrix"][layer_idx]
+        caps = []
+        for h in range(self.num_kv_heads):
+            if h in keep:
+                cap = L
+            else:
+                c64 = max(min(int(self.base_compress_len * alloc[h]), L), 0)
+                c32 = int(_f32_caps(self.base_compress_len, [alloc[h]], L)[0])
+                cap = max(c64, c32)
+            caps.append(cap)
+        self.layer_head_capacities[layer_idx] = caps
+        row_caps = [caps[r % self.num_kv_heads] + gen for r in range(self.bsz * self.num_kv_heads)]
+        self.stores[layer_idx] = KVStore(row_caps, dtype, device)
+
+    def update(self, key_states, value_states, layer_idx, cache_kwargs=None):
+        """heterocache/cache_utils.py:884-1005."""
+        if layer_idx == 0:
+            self._seen_tokens += key_states.shape[-2]
+        if self.bsz is None:
+            self.bsz = key_states.shape[0]
+            self.head_dim = key_states.shape[-1]
+            if self.head_dim != 128:
+                raise ValueError(f"head_dim {self.head_dim} is not supported (128 only)")
+        if not hasattr(self, "base_compress_len"):
+            self.prefill_len = key_states.shape[-2]
+            self.base_compress_len = get_compress_len(self.compression_ratio, self.full_heads, self.prefill_len,
+                                                      self.total_kv_heads)
+        if self.stores[layer_idx] is None:
+            self._init_layer_storage(layer_idx, key_states.device, key_states.dtype)
+        store = self.stores[layer_idx]
+        seq_len = key_states.shape[-2]
+        if seq_len > 1:
+            self.prefill_len = seq_len
+            keep = self.data["need_to_keep_counts"][layer_idx]
+            if keep:
+                bh = [(b, h) for b in range(self.bsz) for h in keep]
+                store.write_rows(key_states, value_states, bh, [b * self.num_kv_heads + h for b, h in bh],
+                                 [seq_len] * len(bh))
+            self._backup_full_tier(key_states, value_states, layer_idx)
+            return key_states, value_states
+        self._flush_append(layer_idx)
+        self._pending[layer_idx] = (key_states, value_states)
+        return key_states, value_states
+
+    def _backup_full_tier(self, key_states, value_states, layer_idx):
+        """Full-KV tier of the satellite heads (heterocache/cache_utils.py:939-967)."""
+        sats = list(self.data["need_to_update_counts"][layer_idx])
+        if not sats:
+            return
+        if self.device != "cpu":
+            # GPU direct mode keeps the prefill K/V itself, as the reference.
+            self.key_cache_cpu[layer_idx] = key_states.detach()
+            self.value_cache_cpu[layer_idx] = value_states.detach()
+            self._tier_heads[layer_idx] = {h: h for h in sats}
+            return
+        main = torch.cuda.current_stream(key_states.device)
+        side = self._side_stream(key_states.device)
+        shape = (self.bsz, len(sats), key_states.shape[-2], self.head_dim)
+        kc = torch.empty(shape, dtype=key_states.dtype, pin_memory=True)
+        vc = torch.empty(shape, dtype=value_states.dtype, pin_memory=True)
+        idx = torch.tensor(sats, dtype=torch.long, device=key_states.device)
+        ksrc = key_states.index_select(1, idx)
+        vsrc = value_states.index_select(1, idx)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            kc.copy_(ksrc, non_blocking=True)
+            vc.copy_(vsrc, non_blocking=True)
+            ev = torch.cuda.Event()
+            ev.record(side)
+        ksrc.record_stream(side)
+        vsrc.record_stream(side)
+        self.key_cache_cpu[layer_idx] = kc
+        self.value_cache_cpu[layer_idx] = vc
+        self._tier_heads[layer_idx] = {h: i for i, h in enumerate(sats)}
+        self._tier_ready[layer_idx] = ev
+
+    def _flush_append(self, layer_idx):
+        p = self._pending[layer_idx]
+        if p is None:
+            return
+        self._pending[layer_idx] = None
+        k, v = p
+        self.stores[layer_idx].append(k.reshape(-1, self.head_dim), v.reshape(-1, self.head_dim))
+
+    def _round_dtype(self, dtype):
+        return dtype if self.round_scores else None
+
+    def init_coefficient(self, query_states, key_states, layer_idx):
+        """Pivot reference sets: top-base of the pooled last-query scores
+        (heterocache/cache_utils.py:1149-1190), kept as device bitmasks."""
+        pivots = list(self.data["need_to_select_counts"][layer_idx])
+        rel = self.data["leader_member_relations"][layer_idx]
+        st = _LayerDrift()
+        self._drift[layer_idx] = st
+        if not pivots:
+            return
+        L = key_states.shape[-2]
+        G = self.num_key_value_groups
+        scores = compress.last_query_scores(query_states, key_states, pivots, G, self.pooling, self.kernel_size,
+                                            round_dtype=self._round_dtype(query_states.dtype))
+        K = min(self.base_compress_len, L)
+        idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
+        # Sets are stored in relation order, one row per (leader, batch).
+        leaders = [int(h) for h, m in rel.items()]
+        members = [list(m) for h, m in rel.items()]
+        st.leaders, st.members = leaders, members
+        if self.quirks:
+            # The i-th relation is compared with the i-th ascending pivot's set.
+            src = [min(i, len(pivots) - 1) for i in range(len(leaders))]
+        else:
+            src = [pivots.index(h) for h in leaders]
+        # Score rows are (b, pivot position); reorder them to (leader, b).
+        order = torch.tensor([self._score_row(b, s, len(pivots)) for s in src for b in range(self.bsz)],
+                             dtype=torch.long, device=idx.device)
+        words = (L + 31) // 32
+        st.ref_bits = torch.zeros((len(leaders) * self.bsz, max(words, 1)), dtype=torch.int32, device=idx.device)
+        if len(leaders):
+            ops.set_bits(idx.index_select(0, order).contiguous(), None, st.ref_bits, L, fixed_count=K)
+        st.trigger = torch.zeros(max(len(leaders), 1), dtype=torch.int32, device=idx.device)
+        self.prefill_topk_set[layer_idx] = st.ref_bits
+
+    @staticmethod
+    def _score_row(b, pivot_pos, npiv):
+        return b * npiv + pivot_pos
+
+    def prefill_select(self, query_states, key_states, value_states, layer_idx):
+        """Compressed heads keep their top cap_h tokens in temporal order
+        (heterocache/cache_utils.py:782-882)."""
+        n_c = self.data["need_to_compress_counts"][layer_idx]
+        if n_c == 0:
+            return
+        store = self.stores[layer_idx]
+        L = key_states.shape[-2]
+        caps = _f32_caps(self.base_compress_len, self.data["allocation_matrix"][layer_idx][:n_c], L)
+        rows = [b * self.num_kv_heads + h for b in range(self.bsz) for h in range(n_c)]
+        caps_rows = [int(caps[h]) for b in range(self.bsz) for h in range(n_c)]
+        if max(caps_rows) == 0:
+            store.set_lengths([0] * len(rows), rows)
+            return
+        G = self.num_key_value_groups
+        W = self.window_size
+        if W > 1:
+            scores = compress.window_scores(query_states, key_states, range(n_c), G, W, self.pooling,
+                                            self.kernel_size, window_keep=True,
+                                            round_dtype=self._round_dtype(query_states.dtype))
+        else:
+            scores = compress.last_query_scores(query_states, key_states, range(n_c), G, self.pooling,
+                                                self.kernel_size, round_dtype=self._round_dtype(query_states.dtype))
+        idx, _ = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0)
+        store.write_rows(key_states, value_states, [(b, h) for b in range(self.bsz) for h in range(n_c)], rows,
+                         caps_rows, idx=idx)
+
+    def decode_attention(self, query_states, layer_idx, out=None):
+        """Decode attention of q [B, Hq, 1, 128] over the layer's rows, with the
+        pending token appended in the same launch.  Returns [B, 1, Hq*128]."""
+        B, Hq, ql, D = query_states.shape
+        if ql != 1:
+            raise ValueError("decode_attention takes one query position")
+        store = self.stores[layer_idx]
+        ev = self._retrieval_done[layer_idx]
+        if ev is not None:
+            torch.cuda.current_stream(query_states.device).wait_event(ev)
+            self._retrieval_done[layer_idx] = None
+        q = query_states.reshape(B * self.num_kv_heads, self.num_key_value_groups, D)
+        p = self._pending[layer_idx]
+        self._pending[layer_idx] = None
+        kn = vn = None
+        if p is not None:
+            kn = p[0].reshape(-1, D)
+            vn = p[1].reshape(-1, D)
+        o = store.attend(q, 1.0 / (D ** 0.5), out=out, k_new=kn, v_new=vn, tiles_per_wave=self.tiles_per_wave)
+        return o.view(B, 1, Hq * D)
+
+    def decode_select(self, query_states, layer_idx):
+        """Buffered pivot drift check and satellite retrieval
+        (heterocache/cache_utils.py:1007-1147), without host syncs."""
+        st = self._drift[layer_idx]
+        if st is None:
+            st = self._drift[layer_idx] = _LayerDrift()
+        S = self.decode_step
+        if st.qbuf is None:
+            st.qbuf = torch.empty((self.bsz, self.num_attn_heads, S, self.head_dim), dtype=query_states.dtype,
+                                  device=query_states.device)
+        st.qbuf[:, :, st.count].copy_(query_states[:, :, -1])
+        st.count += 1
+        if st.count < S:
+            return
+        st.count = 0
+        if not st.leaders:
+            return
+        work = [(i, h, m) for i, (h, m) in enumerate(zip(st.leaders, st.members)) if m]
+        if not work:
+            return
+        store = self.stores[layer_idx]
+        L, G, B, Hkv = self.prefill_len, self.num_key_value_groups, self.bsz, self.num_kv_heads
+        K = min(self.base_compress_len, L)
+        nl = len(st.leaders)
+        # Scores of every leader (relation order) x batch row: [nl*B, S, L].
+        rows = [b * Hkv + h for h in st.leaders for b in range(B)]
+        heads = [h for h in st.leaders for b in range(B)]
+        scores = compress.pivot_step_scores(st.qbuf, store, rows, heads, G, L, self.pooling, self.kernel_size,
+                                            round_dtype=self._round_dtype(query_states.dtype))
+        cur, _ = compress.select_kept(scores.view(nl * B * S, L), [K] * (nl * B * S), max_cap=max(K, 1))
+        ref_of = torch.arange(nl * B, dtype=torch.int32, device=cur.device).repeat_interleave(S)
+        counts = ops.overlap_count(cur, K, st.ref_bits, L, ref_of=ref_of)
+        ops.drift_decide(counts, nl, B, S, K, self.stable_threshold, st.trigger)
+        # On trigger: the reference set becomes the last step's top-K set.
+        last = cur.view(nl * B, S, -1)[:, S - 1]
+        trig_of = torch.arange(nl, dtype=torch.int32, device=cur.device).repeat_interleave(B)
+        ops.set_bits(last, None, st.ref_bits, L, fixed_count=K, trigger=st.trigger, trig_of=trig_of)
+        self._retrieve(layer_idx, st, scores[:, S - 1], work)
+
+    def _retrieval_lengths(self, layer_idx, members):
+        alloc = self.data["allocation_matrix"][layer_idx]
+        L = self.prefill_len
+        if self.quirks:
+            lens = [max(min(int(self.base_compress_len * alloc[m]), L), 0) for m in members]
+        else:
+            lens = [int(x) for x in _f32_caps(self.base_compress_len, [alloc[m] for m in members], L)]
+        if self.retrieval_topk is not None:
+            lens = [min(n, int(self.retrieval_topk)) for n in lens]
+        return lens
+
+    def _retrieve(self, layer_idx, st, last_scores, work):
+        """Gather each satellite's tokens from the full-KV tier into slots
+        [0, len) of its row (heterocache/cache_utils.py:1084-1123): the
+        satellite takes the ascending prefix of its leader's top-max(len)
+        list of the last buffered step.  Gated by the device trigger flag and
+        run on the side stream."""
+        B, Hkv = self.bsz, self.num_kv_heads
+        store = self.stores[layer_idx]
+        plans = []
+        for i, lead, members in work:
+            lens = self._retrieval_lengths(layer_idx, members)
+            if max(lens) > 0:
+                plans.append((i, members, lens))
+        if not plans:
+            return
+        nl = len(st.leaders)
+        mk = max(max(lens) for _, _, lens in plans)
+        caps = [0] * (nl * B)
+        for i, _, lens in plans:
+            for b in range(B):
+                caps[i * B + b] = max(lens)
+        ret_idx, _ = compress.select_kept(last_scores.contiguous(), caps, max_cap=mk)
+        dev = ret_idx.device
+        main = torch.cuda.current_stream(dev)
+        kc, vc = self.key_cache_cpu[layer_idx], self.value_cache_cpu[layer_idx]
+        tier_heads = self._tier_heads[layer_idx]
+        host = self.device == "cpu"
+        side = self._side_stream(dev) if host else main
+        if host:
+            side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for i, members, lens in plans:
+                jobs = [(b, m, n) for b in range(B) for m, n in zip(members, lens) if n > 0]
+                if not jobs:
+                    continue
+                idx_rows = [i * B + b for b, m, n in jobs]
+                store.write_rows(kc, vc, [(b, tier_heads[m]) for b, m, n in jobs],
+                                 [b * Hkv + m for b, m, n in jobs], [n for b, m, n in jobs], idx=ret_idx,
+                                 idx_rows=idx_rows, src_is_host=host, trigger=st.trigger[i:i + 1],
+                                 set_len=False, stream=side)
+            if host:
+                ev = torch.cuda.Event()
+                ev.record(side)
+                self._retrieval_done[layer_idx] = ev
+        if host:
+            ret_idx.record_stream(side)
+            st.trigger.record_stream(side)

@@ -1,0 +1,132 @@
+// Pivot-head drift monitoring, entirely on the device (no host sync).
+//
+// The reference (heterocache/cache_utils.py:1059-1082) keeps, per pivot, the
+// prefill top-K position set; every decode_step calls it takes the top-K set
+// of each buffered step, measures |cur ∩ ref| / K, averages over the batch,
+// takes the median over the steps and, when it falls below stable_threshold,
+// replaces the reference set by the last step's set and retrieves tokens for
+// the pivot's satellites.  Here:
+//   hc_set_bits        position lists -> per-set bitmasks (optionally only for
+//                      sets whose trigger flag is raised);
+//   hc_overlap_count   |list ∩ bitmask| per list (bit tests + block reduce);
+//   hc_drift_decide    per pivot: batch mean, median over steps, threshold,
+//                      trigger flag written to device memory.
+// The trigger flag gates the set update and the retrieval gather
+// (hc_gather_store's trigger argument), so the decode loop never waits on the
+// host.
+#include "hc_common.h"
+#include "hc_internal.h"
+
+namespace hc {
+
+__global__ __launch_bounds__(256) void set_bits_kernel(const int32_t* __restrict__ idx, int64_t idx_stride,
+                                                       const int32_t* __restrict__ counts, int fixed_count,
+                                                       uint32_t* __restrict__ bits, int64_t words, int nbits,
+                                                       const int32_t* __restrict__ trigger,
+                                                       const int32_t* __restrict__ trig_of) {
+  const int j = blockIdx.x;
+  if (trigger && trigger[trig_of ? trig_of[j] : j] == 0) return;
+  uint32_t* b = bits + (int64_t)j * words;
+  for (int64_t w = threadIdx.x; w < words; w += blockDim.x) b[w] = 0u;
+  __syncthreads();
+  const int n = counts ? counts[j] : fixed_count;
+  const int32_t* ix = idx + (int64_t)j * idx_stride;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
+    const int t = ix[i];
+    if (t >= 0 && t < nbits) atomicOr(&b[t >> 5], 1u << (t & 31));
+  }
+}
+
+__global__ __launch_bounds__(256) void overlap_count_kernel(const int32_t* __restrict__ idx, int64_t idx_stride,
+                                                            int count, const uint32_t* __restrict__ bits,
+                                                            int64_t words, int nbits,
+                                                            const int32_t* __restrict__ ref_of,
+                                                            int32_t* __restrict__ out) {
+  const int j = blockIdx.x;
+  const uint32_t* b = bits + (int64_t)(ref_of ? ref_of[j] : j) * words;
+  const int32_t* ix = idx + (int64_t)j * idx_stride;
+  int c = 0;
+  for (int i = threadIdx.x; i < count; i += blockDim.x) {
+    const int t = ix[i];
+    if (t >= 0 && t < nbits) c += (b[t >> 5] >> (t & 31)) & 1u;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off, 64);
+  __shared__ int s[4];
+  if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = c;
+  __syncthreads();
+  if (threadIdx.x == 0) out[j] = s[0] + s[1] + s[2] + s[3];
+}
+
+// counts: [npiv][batch][steps]; one thread per pivot.
+__global__ void drift_decide_kernel(const int32_t* __restrict__ counts, int npiv, int batch, int steps, int K,
+                                    double threshold, float* __restrict__ overlap, double* __restrict__ median,
+                                    int32_t* __restrict__ trigger) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= npiv) return;
+  float v[64];
+  for (int s = 0; s < steps; ++s) {
+    // (count / K) per batch row in float32, then the float32 batch mean.
+    float acc = 0.f;
+    for (int b = 0; b < batch; ++b) acc += (float)counts[((int64_t)p * batch + b) * steps + s] / (float)K;
+    v[s] = acc / (float)batch;
+    if (overlap) overlap[(int64_t)p * steps + s] = v[s];
+  }
+  // Insertion sort of the (<= 64) step values, then the median as
+  // statistics.median defines it (mean of the middle pair for even counts).
+  for (int i = 1; i < steps; ++i) {
+    const float x = v[i];
+    int j = i - 1;
+    while (j >= 0 && v[j] > x) {
+      v[j + 1] = v[j];
+      --j;
+    }
+    v[j + 1] = x;
+  }
+  const double med = (steps & 1) ? (double)v[steps / 2] : ((double)v[steps / 2 - 1] + (double)v[steps / 2]) / 2.0;
+  if (median) median[p] = med;
+  trigger[p] = med < threshold ? 1 : 0;
+}
+
+}  // namespace hc
+
+using namespace hc;
+
+extern "C" int hc_set_bits(const int32_t* idx, int64_t idx_stride, const int32_t* counts, int fixed_count, int nsets,
+                           uint32_t* bits, int64_t words, int nbits, const int32_t* trigger, const int32_t* trig_of,
+                           void* stream) {
+  clear_error();
+  if (nsets < 0 || nsets > 65535 || words < (nbits + 31) / 32 || nbits < 0)
+    return set_error(HC_ERR_INVALID, "hc_set_bits: nsets=%d words=%lld nbits=%d", nsets, (long long)words, nbits);
+  if (nsets == 0) return HC_OK;
+  if (!idx || !bits) return set_error(HC_ERR_INVALID, "hc_set_bits: null pointer argument");
+  if (!counts && fixed_count > idx_stride) return set_error(HC_ERR_INVALID, "hc_set_bits: count exceeds the stride");
+  hipLaunchKernelGGL(set_bits_kernel, dim3(nsets), dim3(256), 0, (hipStream_t)stream, idx, idx_stride, counts,
+                     fixed_count, bits, words, nbits, trigger, trig_of);
+  return check_launch("hc_set_bits");
+}
+
+extern "C" int hc_overlap_count(const int32_t* idx, int64_t idx_stride, int count, int nlists, const uint32_t* bits,
+                                int64_t words, int nbits, const int32_t* ref_of, int32_t* out, void* stream) {
+  clear_error();
+  if (nlists < 0 || nlists > 65535 || count < 0 || count > idx_stride || words < (nbits + 31) / 32)
+    return set_error(HC_ERR_INVALID, "hc_overlap_count: nlists=%d count=%d stride=%lld", nlists, count,
+                     (long long)idx_stride);
+  if (nlists == 0) return HC_OK;
+  if (!idx || !bits || !out) return set_error(HC_ERR_INVALID, "hc_overlap_count: null pointer argument");
+  hipLaunchKernelGGL(overlap_count_kernel, dim3(nlists), dim3(256), 0, (hipStream_t)stream, idx, idx_stride, count,
+                     bits, words, nbits, ref_of, out);
+  return check_launch("hc_overlap_count");
+}
+
+extern "C" int hc_drift_decide(const int32_t* counts, int npiv, int batch, int steps, int K, double threshold,
+                               float* overlap, double* median, int32_t* trigger, void* stream) {
+  clear_error();
+  if (npiv < 0 || batch < 1 || steps < 1 || steps > 64 || K < 1)
+    return set_error(HC_ERR_INVALID, "hc_drift_decide: npiv=%d batch=%d steps=%d K=%d", npiv, batch, steps, K);
+  if (npiv == 0) return HC_OK;
+  if (!counts || !trigger) return set_error(HC_ERR_INVALID, "hc_drift_decide: null pointer argument");
+  hipLaunchKernelGGL(drift_decide_kernel, dim3((npiv + 63) / 64), dim3(64), 0, (hipStream_t)stream, counts, npiv,
+                     batch, steps, K, threshold, overlap, median, trigger);
+  return check_launch("hc_drift_decide");
+}

@@ -1,0 +1,101 @@
+"""Llama attention with HeteroCache on libhc kernels.
+
+Drop-in for heterocache/llama_model.py:279-405 (`LlamaAttention`): same
+constructor, same forward contract, same call order on the cache:
+  prefill: update -> init_coefficient -> prefill_select -> full causal
+           attention over the uncompressed K/V -> o_proj
+  decode:  update -> decode attention (hc_decode_attn, replacing
+           flash_attn_with_kvcache) -> decode_select -> o_proj
+The forward accepts the transformers 4.57 keyword set (attention_mask,
+position_ids, output_attentions, use_cache, cache_position,
+position_embeddings, past_key_values) and the 5.x one (extra **kwargs).
+"""
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+
+
+def prefill_attention(query_states, key_states, value_states, attention_mask, scaling):
+    """Full causal attention over the uncompressed prefill K/V (outside the
+    compressed path: the reference calls flash-attn here, this build calls
+    PyTorch's SDPA).  Returns [B, L, Hq*d]."""
+    B, Hq, L, D = query_states.shape
+    q = query_states.contiguous()
+    k = key_states.contiguous()
+    v = value_states.contiguous()
+    mask = attention_mask
+    if mask is not None and mask.dim() == 4:
+        mask = mask[..., :L, :k.shape[2]]
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=scaling, enable_gqa=Hq != k.shape[1])
+    else:
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scaling, enable_gqa=Hq != k.shape[1])
+    return out.transpose(1, 2).reshape(B, L, Hq * D)
+
+
+class LlamaAttention(nn.Module):
+    """Multi-headed attention whose KV cache is a HeteroCache."""
+
+    def __init__(self, config, layer_idx: Optional[int] = None):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.attention_dropout = config.attention_dropout
+        self.hidden_size = config.hidden_size
+        self.num_heads = config.num_attention_heads
+        self.head_dim = getattr(config, "head_dim", None) or self.hidden_size // self.num_heads
+        self.num_key_value_heads = config.num_key_value_heads
+        self.num_key_value_groups = self.num_heads // self.num_key_value_heads
+        self.max_position_embeddings = getattr(config, "max_position_embeddings", None)
+        self.rope_theta = getattr(config, "rope_theta", None)
+        self.is_causal = True
+        self.scaling = self.head_dim ** -0.5
+        bias = getattr(config, "attention_bias", False)
+        self.q_proj = nn.Linear(self.hidden_size, self.num_heads * self.head_dim, bias=bias)
+        self.k_proj = nn.Linear(self.hidden_size, self.num_key_value_heads * self.head_dim, bias=bias)
+        self.v_proj = nn.Linear(self.hidden_size, self.num_key_value_heads * self.head_dim, bias=bias)
+        self.o_proj = nn.Linear(self.num_heads * self.head_dim, self.hidden_size, bias=bias)
+
+    # Qwen2 runs decode_select before the decode attention.
+    select_before_attention = False
+
+    def _project(self, hidden_states, position_embeddings):
+        input_shape = hidden_states.shape[:-1]
+        hidden_shape = (*input_shape, -1, self.head_dim)
+        q = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        k = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        cos, sin = position_embeddings
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        return q, k, v
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
+                position_ids: Optional[torch.LongTensor] = None, output_attentions: bool = False,
+                use_cache: bool = False, cache_position: Optional[torch.LongTensor] = None,
+                position_embeddings: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, past_key_values=None,
+                **kwargs) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+        if position_embeddings is None:
+            raise ValueError("position_embeddings (cos, sin) are required")
+        bsz, q_len, _ = hidden_states.size()
+        query_states, key_states, value_states = self._project(hidden_states, position_embeddings)
+        cache = past_key_values
+        if cache is None:
+            out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling)
+            return self.o_proj(out), None
+        cos, sin = position_embeddings
+        cache_kwargs = {"sin": sin, "cos": cos, "cache_position": cache_position, "attention_mask": attention_mask,
+                        "num_key_value_groups": self.num_key_value_groups, "query_states": query_states}
+        key_states, value_states = cache.update(key_states, value_states, self.layer_idx, cache_kwargs)
+        if query_states.shape[-2] != 1:
+            cache.init_coefficient(query_states, key_states, self.layer_idx)
+            cache.prefill_select(query_states, key_states, value_states, self.layer_idx)
+            out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling)
+        else:
+            if self.select_before_attention:
+                cache.decode_select(query_states, self.layer_idx)
+            out = cache.decode_attention(query_states, self.layer_idx)
+            if not self.select_before_attention:
+                cache.decode_select(query_states, self.layer_idx)
+        return self.o_proj(out), None

@@ -217,3 +217,32 @@ def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None
     _lib.check(lib.hc_select_topk(_ptr(scores), scores.stride(0), njobs, int(span), _ptr(caps), int(window), _ptr(idx),
                                   idx.stride(0), _ptr(counts), _stream(stream)))
     return idx, counts
+
+
+def set_bits(idx, counts, bits, nbits, fixed_count=0, trigger=None, trig_of=None, stream=None):
+    """bits[j] = set of the first counts[j] (or fixed_count) positions of idx[j] (cleared first)."""
+    lib = _lib.load()
+    _require_cuda(idx, counts, bits, trigger, trig_of)
+    if idx.dtype != torch.int32 or bits.dtype != torch.int32 or idx.dim() != 2 or bits.dim() != 2:
+        raise TypeError("idx and bits must be 2-D int32 tensors")
+    _lib.check(lib.hc_set_bits(_ptr(idx), idx.stride(0), _ptr(counts), int(fixed_count), idx.shape[0], _ptr(bits),
+                               bits.stride(0), int(nbits), _ptr(trigger), _ptr(trig_of), _stream(stream)))
+
+
+def overlap_count(idx, count, bits, nbits, ref_of=None, out=None, stream=None):
+    """|first `count` positions of idx[j]  ∩  bits[ref_of[j]]| per list j."""
+    lib = _lib.load()
+    _require_cuda(idx, bits, ref_of, out)
+    if out is None:
+        out = torch.empty(idx.shape[0], dtype=torch.int32, device=idx.device)
+    _lib.check(lib.hc_overlap_count(_ptr(idx), idx.stride(0), int(count), idx.shape[0], _ptr(bits), bits.stride(0),
+                                    int(nbits), _ptr(ref_of), _ptr(out), _stream(stream)))
+    return out
+
+
+def drift_decide(counts, npiv, batch, steps, K, threshold, trigger, overlap=None, median=None, stream=None):
+    """Per pivot: batch-mean overlap per step, median over steps, trigger = median < threshold."""
+    lib = _lib.load()
+    _require_cuda(counts, trigger, overlap, median)
+    _lib.check(lib.hc_drift_decide(_ptr(counts), int(npiv), int(batch), int(steps), int(K), float(threshold),
+                                   _ptr(overlap), _ptr(median), _ptr(trigger), _stream(stream)))

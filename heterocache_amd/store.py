@@ -70,14 +70,16 @@ class KVStore:
         self.row_order = torch.as_tensor(order).to(self.device)
 
     # -- writers -----------------------------------------------------------
-    def write_rows(self, src_k, src_v, src_bh, rows, counts, idx=None, src_is_host=False, stream=None,
-                   trigger=None, set_len=True):
-        """store[rows[j]][i] = src[b_j, h_j, idx[j][i]] (or token i), i < counts[j].
+    def write_rows(self, src_k, src_v, src_bh, rows, counts, idx=None, idx_rows=None, src_is_host=False,
+                   stream=None, trigger=None, set_len=True):
+        """store[rows[j]][i] = src[b_j, h_j, idx[r_j][i]] (or token i), i < counts[j].
 
         src_k / src_v: [B, H, L, 128] with unit channel stride (any other
         strides), on the device or host-pinned.  src_bh: [jobs, 2] (b, h) of
-        each job's source head.  idx: [jobs, M] int32 device tensor of source
-        positions (None copies positions 0..count-1).
+        each job's source head.  idx: [n, M] int32 device tensor of source
+        positions (None copies positions 0..count-1); job j reads row
+        r_j = idx_rows[j] (default j).  trigger: int32 device flag gating the
+        copy.
         """
         rows = np.asarray(rows, dtype=np.int64)
         counts = np.asarray(counts, dtype=np.int64)
@@ -108,12 +110,14 @@ class KVStore:
         dev = self.device
         idx_off = None
         if idx is not None:
-            if idx.dtype != torch.int32 or idx.dim() != 2 or idx.shape[0] != len(rows):
-                raise ValueError("idx must be int32 [jobs, M]")
+            if idx.dtype != torch.int32 or idx.dim() != 2 or idx.stride(1) != 1:
+                raise ValueError("idx must be int32 [n, M] with unit stride")
+            r = np.arange(len(rows), dtype=np.int64) if idx_rows is None else np.asarray(idx_rows, dtype=np.int64)
+            if len(r) != len(rows) or (r < 0).any() or (r >= idx.shape[0]).any():
+                raise ValueError("idx_rows must name one index row per job")
             if (counts > idx.shape[1]).any():
                 raise ValueError("count exceeds the index list")
-            idx = idx.contiguous()
-            idx_off = torch.arange(len(rows), dtype=torch.int64, device=dev) * idx.shape[1]
+            idx_off = torch.as_tensor(r * idx.stride(0)).to(dev)
         ops.gather_store(src_k, src_v, torch.as_tensor(src_off).to(dev), tok_stride, L, idx, idx_off,
                          torch.as_tensor(counts, dtype=torch.int32).to(dev),
                          torch.as_tensor(rows, dtype=torch.int32).to(dev), self.k, self.v, self.row_tile_off,

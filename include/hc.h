@@ -145,6 +145,33 @@ size_t hc_score_workspace_size(int njobs, int seq_len, int group, int window, in
 int hc_select_topk(const float* scores, int64_t score_stride, int njobs, int span, const int32_t* caps, int window,
                    int32_t* idx, int64_t idx_stride, int32_t* counts, void* stream);
 
+/*
+ * Position lists -> bitmasks: set j (words uint32 words at bits + j*words) is
+ * cleared and then holds the first counts[j] (or fixed_count) positions of
+ * idx + j*idx_stride.  With trigger != NULL set j is left untouched unless
+ * trigger[trig_of ? trig_of[j] : j] != 0.  Holds the pivot reference sets of
+ * heterocache/cache_utils.py:1189-1190 (prefill) and :1082 (update on drift).
+ */
+int hc_set_bits(const int32_t* idx, int64_t idx_stride, const int32_t* counts, int fixed_count, int nsets,
+                uint32_t* bits, int64_t words, int nbits, const int32_t* trigger, const int32_t* trig_of,
+                void* stream);
+
+/*
+ * out[j] = |{ idx[j*idx_stride + i] : i < count } ∩ set(ref_of ? ref_of[j] : j)|.
+ * The searchsorted overlap of heterocache/cache_utils.py:1063-1073.
+ */
+int hc_overlap_count(const int32_t* idx, int64_t idx_stride, int count, int nlists, const uint32_t* bits,
+                     int64_t words, int nbits, const int32_t* ref_of, int32_t* out, void* stream);
+
+/*
+ * counts: [npiv][batch][steps] overlap counts of top-K sets.  Per pivot:
+ * overlap[s] = mean_b(count/K) (float32), median over steps as
+ * statistics.median defines it, trigger = median < threshold
+ * (heterocache/cache_utils.py:1073-1080).  overlap and median are optional.
+ */
+int hc_drift_decide(const int32_t* counts, int npiv, int batch, int steps, int K, double threshold, float* overlap,
+                    double* median, int32_t* trigger, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

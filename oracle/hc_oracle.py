@@ -376,3 +376,123 @@ def allocation_ratios(stabilities):
     for row in stabilities:
         out.append([((1.0 / (s + 1e-6)) / tot * n) if s > -0.5 else -1.0 for s in row])
     return out
+
+
+# --------------------------------------------------------------------------
+# End-to-end cache flow (one layer at a time), numpy
+# --------------------------------------------------------------------------
+class CacheOracle:
+    """HeteroCache's per-layer flow on numpy arrays.
+
+    Follows heterocache/cache_utils.py:884-1005 (update), :1149-1190
+    (init_coefficient), :782-882 (prefill_select), :1007-1147
+    (decode_select) and heterocache/llama_model.py:368-401 /
+    heterocache/qwen_model.py:176-211 (decode order).  `data` is the
+    augmented head record (derived lists in reordered head indices).  Defaults
+    match the device build: float32 retrieval lengths and each pivot compared
+    with its own reference set (quirks=True: the reference's float64 lengths
+    and relation-order set indexing).
+    """
+
+    def __init__(self, data, batch, q_heads, kv_heads, num_layers, ratio, threshold, decode_step, pooling, kernel,
+                 retrieval_topk=None, quirks=False, select_before_attention=False):
+        self.data = data
+        self.B, self.Hq, self.Hkv, self.NL = batch, q_heads, kv_heads, num_layers
+        self.G = q_heads // kv_heads
+        self.ratio, self.threshold, self.S = ratio, threshold, decode_step
+        self.pooling, self.kernel = pooling, kernel
+        self.topk, self.quirks, self.select_first = retrieval_topk, quirks, select_before_attention
+        self.full_heads = data["meta"]["counts"]["volatile"] + data["meta"]["counts"]["pivot"]
+        self.rows = {}      # layer -> list over b*Hkv+h of [len, 128] K and V arrays
+        self.tier = {}      # layer -> (K, V) [B, Hkv, L, 128]
+        self.ref = {}       # layer -> {leader: [set per b]}
+        self.qbuf = {}
+        self.base = None
+        self.L = None
+        self.triggers = []  # (layer, leader, triggered) per check
+
+    def prefill(self, layer, q, k, v):
+        B, Hkv, L, _ = k.shape
+        if self.base is None:
+            self.L = L
+            self.base = get_compress_len(self.ratio, self.full_heads, L, Hkv * self.NL)
+        keep = set(self.data["need_to_keep_counts"][layer])
+        n_c = self.data["need_to_compress_counts"][layer]
+        caps = prefill_caps(self.base, self.data["allocation_matrix"][layer][:n_c], L)
+        rows = []
+        for b in range(B):
+            for h in range(Hkv):
+                if h in keep:
+                    rows.append([k[b, h].copy(), v[b, h].copy()])
+                elif h < n_c:
+                    s = last_query_scores(q[b, h * self.G:(h + 1) * self.G, -1][None], k[b, h][None], self.pooling,
+                                          self.kernel)[0]
+                    sel = topk_select(s, int(caps[h]))
+                    rows.append([k[b, h][sel], v[b, h][sel]])
+                else:
+                    rows.append([np.zeros((0, k.shape[-1]), k.dtype), np.zeros((0, k.shape[-1]), k.dtype)])
+        self.rows[layer] = rows
+        self.tier[layer] = (k.copy(), v.copy())
+        pivots = list(self.data["need_to_select_counts"][layer])
+        rel = self.data["leader_member_relations"][layer]
+        K = min(self.base, L)
+        sets = {}
+        for p in pivots:
+            sets[p] = [set(topk_indices(last_query_scores(q[b, p * self.G:(p + 1) * self.G, -1][None], k[b, p][None],
+                                                          self.pooling, self.kernel)[0], K).tolist())
+                       for b in range(B)]
+        ref = {}
+        for i, leader in enumerate(int(x) for x in rel):
+            src = pivots[min(i, len(pivots) - 1)] if self.quirks else leader
+            ref[leader] = sets[src]
+        self.ref[layer] = ref
+        self.qbuf[layer] = []
+
+    def decode(self, layer, q, k_new, v_new):
+        """One decode step of one layer; returns attention output [B, Hq, 128] (float64)."""
+        B, Hkv = self.B, self.Hkv
+        for b in range(B):
+            for h in range(Hkv):
+                r = self.rows[layer][b * Hkv + h]
+                r[0] = np.concatenate([r[0], k_new[b, h]])
+                r[1] = np.concatenate([r[1], v_new[b, h]])
+        if self.select_first:
+            self._select(layer, q)
+        qa = q[:, :, 0].reshape(B * Hkv, self.G, -1)
+        out = decode_attention(qa, [r[0] for r in self.rows[layer]], [r[1] for r in self.rows[layer]])
+        if not self.select_first:
+            self._select(layer, q)
+        return out.reshape(B, self.Hq, -1)
+
+    def _select(self, layer, q):
+        self.qbuf[layer].append(q[:, :, 0])
+        if len(self.qbuf[layer]) < self.S:
+            return
+        qs = np.stack(self.qbuf[layer], axis=2)  # [B, Hq, S, d]
+        self.qbuf[layer] = []
+        rel = self.data["leader_member_relations"][layer]
+        K = min(self.base, self.L)
+        alloc = self.data["allocation_matrix"][layer]
+        kt, vt = self.tier[layer]
+        for leader_s, members in rel.items():
+            leader = int(leader_s)
+            if not members:
+                continue
+            sc = np.stack([pivot_step_scores(qs[b, leader * self.G:(leader + 1) * self.G],
+                                             self.rows[layer][b * self.Hkv + leader][0][:self.L], self.pooling,
+                                             self.kernel) for b in range(self.B)])
+            _, med, trig, cur_last = drift_check(sc, [sorted(s) for s in self.ref[layer][leader]], K, self.threshold)
+            self.triggers.append((layer, leader, bool(trig)))
+            if not trig:
+                continue
+            self.ref[layer][leader] = [set(c.tolist()) for c in cur_last]
+            lens = retrieval_lengths(self.base, [alloc[m] for m in members], self.L, topk=self.topk,
+                                     use_f32=not self.quirks)
+            for b in range(self.B):
+                idxs = retrieval_indices(sc[b, -1], lens)
+                for m, ix in zip(members, idxs):
+                    if len(ix) == 0:
+                        continue
+                    r = self.rows[layer][b * self.Hkv + m]
+                    r[0][:len(ix)] = kt[b, m][ix]
+                    r[1][:len(ix)] = vt[b, m][ix]

@@ -1,0 +1,115 @@
+"""HeteroCache end to end (prefill, decode, drift, retrieval) vs CacheOracle.
+
+Two layers, GQA 4, one batch row.  Decode steps 0-4 repeat the last prefill
+query (pivot overlap 1.0: no retrieval); steps 5-9 use fresh random queries
+(overlap ~ K/L ~ 0.33 < 0.5: retrieval).  Every step's attention output is
+compared with the oracle (1e-4 float32, 2e-2 bf16); trigger decisions and the
+final store rows (copies: bit-exact) are compared too.  Llama order, Qwen
+order (select before attention), retrieval top-k and the reference-quirk
+mode are covered.
+"""
+import numpy as np
+import pytest
+import torch
+
+from heterocache_amd import workloads
+from heterocache_amd.cache_utils import HeteroCache, HeteroCacheConfig
+from heterocache_amd.utils import augment_head_data, head_permutation
+from oracle import hc_oracle as O
+from tests.gpu_util import as_np
+
+pytestmark = pytest.mark.gpu
+
+CLASSES = [[1, 4, 4, 1, 2, 3, 4, 1],   # layer 0: one volatile, one pivot
+           [4, 4, 3, 1, 1, 4, 3, 4]]   # layer 1: two pivots, relations not in ascending order
+RELATIONS = [{"5": [1, 2, 6]}, {"6": [0, 1], "2": [5, 7]}]
+
+
+def head_data(seed=0):
+    rng = np.random.default_rng(seed)
+    stab = [[float(rng.uniform(0.3, 0.9)) if t in (1, 4) else -1.0 for t in row] for row in CLASSES]
+    counts = {"anchor": 0, "volatile": 0, "pivot": 0, "satellite": 0}
+    names = {1: "anchor", 2: "volatile", 3: "pivot", 4: "satellite"}
+    for row in CLASSES:
+        for t in row:
+            counts[names[t]] += 1
+    raw = {"meta": {"type_map": dict(workloads.TYPE_MAP), "counts": counts},
+           "classification_matrix": [list(r) for r in CLASSES],
+           "allocation_matrix": workloads.inverse_stability_allocation(stab),
+           "leader_member_relations": [dict(r) for r in RELATIONS]}
+    perms = [head_permutation(r) for r in CLASSES]
+    return augment_head_data(raw, perms)
+
+
+def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10):
+    torch.manual_seed(0)
+    B, Hq, Hkv, NL, D = 1, 32, 8, 2, 128
+    data = head_data()
+    cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
+                            max_gen_len=steps + 4, decode_step=5, pooling="avgpool", kernel_size=5,
+                            num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=topk,
+                            reference_quirks=quirks)
+    cache = HeteroCache(cfg)
+    orc = O.CacheOracle(data, B, Hq, Hkv, NL, 0.5, 0.5, 5, "avgpool", 5, retrieval_topk=topk, quirks=quirks,
+                        select_before_attention=select_first)
+    g = torch.Generator().manual_seed(1)
+    last_q = []
+    for layer in range(NL):
+        q = torch.randn((B, Hq, L, D), generator=g).to(dtype).to(dev)
+        k = torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev)
+        v = torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev)
+        k, v = cache.update(k, v, layer)
+        cache.init_coefficient(q, k, layer)
+        cache.prefill_select(q, k, v, layer)
+        orc.prefill(layer, as_np(q), as_np(k), as_np(v))
+        last_q.append(q[:, :, -1:].clone())
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    triggers = []
+    for step in range(steps):
+        for layer in range(NL):
+            q = last_q[layer] if step < 5 else torch.randn((B, Hq, 1, D), generator=g).to(dtype).to(dev)
+            kn = torch.randn((B, Hkv, 1, D), generator=g).to(dtype).to(dev)
+            vn = torch.randn((B, Hkv, 1, D), generator=g).to(dtype).to(dev)
+            cache.update(kn, vn, layer)
+            if select_first:
+                cache.decode_select(q, layer)
+            out = cache.decode_attention(q, layer)
+            if not select_first:
+                cache.decode_select(q, layer)
+            ref = orc.decode(layer, as_np(q), as_np(kn), as_np(vn))
+            err = np.abs(as_np(out).reshape(B, Hq, D) - ref).max()
+            assert err <= tol, f"step {step} layer {layer}: max-abs {err}"
+            if (step + 1) % 5 == 0:
+                st = cache._drift[layer]
+                for i, leader in enumerate(st.leaders):
+                    triggers.append((layer, leader, bool(st.trigger[i].item())))
+    torch.cuda.synchronize()
+    assert triggers == orc.triggers
+    for layer in range(NL):
+        store = cache.stores[layer]
+        for r in range(B * Hkv):
+            n = int(store.host_len[r])
+            ks, vs = store.read_rows([r], n)
+            ok, ov = orc.rows[layer][r]
+            assert n == len(ok), (layer, r)
+            assert np.array_equal(as_np(ks[0]), ok) and np.array_equal(as_np(vs[0]), ov), (layer, r)
+    return triggers
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_llama_order(dev, dtype):
+    trig = run(dev, dtype)
+    # First check: overlap 1.0 everywhere; second: every leader retrieves.
+    assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
+
+
+def test_qwen_order_select_before_attention(dev):
+    run(dev, torch.float32, select_first=True)
+
+
+def test_retrieval_topk(dev):
+    run(dev, torch.float32, topk=64)
+
+
+def test_reference_quirks(dev):
+    run(dev, torch.float32, quirks=True)
