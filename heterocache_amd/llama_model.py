@@ -17,21 +17,30 @@ import torch.nn as nn
 import torch.nn.functional as F
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
+from .cache_utils import HeteroCache
+
 
 def prefill_attention(query_states, key_states, value_states, attention_mask, scaling):
-    """Full causal attention over the uncompressed prefill K/V (outside the
-    compressed path: the reference calls flash-attn here, this build calls
-    PyTorch's SDPA).  Returns [B, L, Hq*d]."""
+    """Causal attention of the L query positions over the uncompressed K/V
+    (outside the compressed path: the reference calls flash-attn here, this
+    build calls PyTorch's SDPA).  Queries are the last L positions of the
+    keys.  Returns [B, L, Hq*d]."""
     B, Hq, L, D = query_states.shape
+    Lk = key_states.shape[2]
     q = query_states.contiguous()
     k = key_states.contiguous()
     v = value_states.contiguous()
+    gqa = Hq != k.shape[1]
     mask = attention_mask
     if mask is not None and mask.dim() == 4:
-        mask = mask[..., :L, :k.shape[2]]
-        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=scaling, enable_gqa=Hq != k.shape[1])
-    else:
-        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scaling, enable_gqa=Hq != k.shape[1])
+        mask = mask[..., :L, :Lk]
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=scaling, enable_gqa=gqa)
+    elif L == Lk:
+        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scaling, enable_gqa=gqa)
+    else:  # queries at positions Lk-L .. Lk-1
+        pos_q = torch.arange(Lk - L, Lk, device=q.device)[:, None]
+        allowed = torch.arange(Lk, device=q.device)[None, :] <= pos_q
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=allowed, scale=scaling, enable_gqa=gqa)
     return out.transpose(1, 2).reshape(B, L, Hq * D)
 
 
@@ -81,7 +90,11 @@ class LlamaAttention(nn.Module):
         bsz, q_len, _ = hidden_states.size()
         query_states, key_states, value_states = self._project(hidden_states, position_embeddings)
         cache = past_key_values
-        if cache is None:
+        if cache is None or not isinstance(cache, HeteroCache):
+            # No HeteroCache: plain causal attention (through whatever cache
+            # the caller supplied), so the patched class stays usable.
+            if cache is not None:
+                key_states, value_states = cache.update(key_states, value_states, self.layer_idx)
             out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling)
             return self.o_proj(out), None
         cos, sin = position_embeddings

@@ -117,15 +117,31 @@ def build_cache_config(model, data, compression_ratio=0.5, stable_threshold=0.5,
                              num_kv_heads=cfg.num_key_value_heads, num_layers=cfg.num_hidden_layers, **extra)
 
 
-def install_attention_patch():
-    """Swap this build's attention classes into transformers; call before the
-    model is constructed (the decoder layer instantiates the module global)."""
-    import transformers.models.llama.modeling_llama as ml
-    import transformers.models.qwen2.modeling_qwen2 as mq
-    from .llama_model import LlamaAttention
-    from .qwen_model import Qwen2Attention
-    ml.LlamaAttention = LlamaAttention
-    mq.Qwen2Attention = Qwen2Attention
+class install_attention_patch:
+    """Swap this build's attention classes into transformers; do it before
+    the model is constructed (the decoder layer instantiates the module
+    global).  Usable as a plain call or as a context manager that restores
+    the original classes on exit."""
+
+    def __init__(self):
+        import transformers.models.llama.modeling_llama as ml
+        import transformers.models.qwen2.modeling_qwen2 as mq
+        from .llama_model import LlamaAttention
+        from .qwen_model import Qwen2Attention
+        self._saved = [(ml, "LlamaAttention", ml.LlamaAttention), (mq, "Qwen2Attention", mq.Qwen2Attention)]
+        ml.LlamaAttention = LlamaAttention
+        mq.Qwen2Attention = Qwen2Attention
+
+    def restore(self):
+        for mod, name, cls in self._saved:
+            setattr(mod, name, cls)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.restore()
+        return False
 
 
 def attach_cache(model, cache_config):
