@@ -35,6 +35,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--unfused-append", action="store_true", help="append in its own launch before attention")
+    p.add_argument("--full-steps", type=int, default=20, help="decode steps of the HeteroCache phase")
+    p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
     return p.parse_args()
 
 
@@ -71,6 +73,109 @@ def cpu_baseline(ctx, budgets, seconds):
     return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"C oracle decode attention, one layer ({total} K/V rows, bf16, G=4), {n} passes in "
                       f"{el:.1f}s; {per * 1e6:.0f} us/layer"}
+
+
+def full_step_phase(args, torch, dev):
+    """Decode steps through HeteroCache at the same shape, with the pivot
+    drift check every 5 steps and top-1024 retrieval from the host-pinned
+    full-KV tier (satellite heads) on the side stream.
+
+    Runs twice on fresh caches: with a threshold no overlap can reach (drift
+    checked, never triggered) and with one every overlap is below (every
+    check retrieves), so the difference per step is the retrieval time the
+    decode step does not hide.  Also times the prefill compression of each
+    layer (scores, top-k, gathers and the tier copy).
+    """
+    from heterocache_amd import utils, workloads
+    from heterocache_amd.cache_utils import HeteroCache, HeteroCacheConfig
+    L, Hkv, G, D, NL = args.ctx, 8, 4, 128, args.layers
+    raw = workloads.synthetic_head_json(NL, Hkv, args.seed)
+    data = utils.augment_head_data(raw, [utils.head_permutation(r) for r in raw["classification_matrix"]])
+    steps = args.full_steps
+    res = {}
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    for label, thr in (("no_trigger", -1.0), ("always_trigger", 2.0)):
+        cfg = HeteroCacheConfig(data, compression_ratio=args.ratio, stable_threshold=thr, real_offload=True,
+                                max_gen_len=steps + 8, decode_step=5, pooling="avgpool", kernel_size=5,
+                                num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024)
+        cache = HeteroCache(cfg)
+        pre_ms = 0.0
+        for layer in range(NL):
+            k = torch.randn((1, Hkv, L, D), device=dev, generator=g, dtype=torch.bfloat16)
+            v = torch.randn((1, Hkv, L, D), device=dev, generator=g, dtype=torch.bfloat16)
+            q = torch.randn((1, Hkv * G, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            cache.update(k, v, layer)
+            cache.init_coefficient(q, k, layer)
+            cache.prefill_select(q, k, v, layer)
+            e1.record()
+            torch.cuda.synchronize()
+            pre_ms += e0.elapsed_time(e1)
+            del k, v
+        qs = torch.randn((steps + 5, NL, 1, Hkv * G, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
+        kn = torch.randn((steps + 5, NL, 1, Hkv, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
+
+        def decode_step(t):
+            for layer in range(NL):
+                cache.update(kn[t, layer], kn[t, layer], layer)
+                cache.decode_attention(qs[t, layer], layer)
+                cache.decode_select(qs[t, layer], layer)
+
+        for t in range(5):  # warm-up: one full check builds the per-layer metadata
+            decode_step(t)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for t in range(5, 5 + steps):
+            decode_step(t)
+        e1.record()
+        torch.cuda.synchronize()
+        res[label] = {"ms_per_step": e0.elapsed_time(e1) / steps,
+                      "wall_ms_per_step": (time.perf_counter() - t0) * 1e3 / steps,
+                      "prefill_compress_ms_per_layer": pre_ms / NL}
+        trig = [int(cache._drift[l].trigger.sum().item()) for l in range(NL) if cache._drift[l] is not None
+                and cache._drift[l].trigger is not None]
+        res[label]["leaders_triggered_last_check"] = int(sum(trig))
+        del cache, qs, kn
+        torch.cuda.empty_cache()
+    # Retrieval bytes per check: every satellite gathers min(cap, 1024) K and V rows.
+    sats = sum(len(r) for r in data["need_to_update_counts"])
+    per_check = sats * 1024 * D * 2 * 2
+    exposed = (res["always_trigger"]["ms_per_step"] - res["no_trigger"]["ms_per_step"]) * 5
+    return {"steps": steps, "decode_step": 5, "retrieval_topk": 1024, "satellites": sats,
+            "retrieval_bytes_per_check": per_check,
+            "ms_per_step_no_retrieval": round(res["no_trigger"]["ms_per_step"], 4),
+            "ms_per_step_retrieval_every_check": round(res["always_trigger"]["ms_per_step"], 4),
+            "retrieval_exposed_ms_per_check": round(exposed, 4),
+            "prefill_compress_ms_per_layer": round(res["no_trigger"]["prefill_compress_ms_per_layer"], 3),
+            "leaders_triggered_last_check": res["always_trigger"]["leaders_triggered_last_check"]}
+
+
+def window_scoring_phase(args, torch, dev):
+    """SnapKV-style window scoring (W = 32, GQA 4, 8 KV heads) of one layer at
+    the bench context: MFMA rate of the two logit passes."""
+    from heterocache_amd import compress
+    L, Hkv, G, W, D = args.ctx, 8, 4, 32, 128
+    q = torch.randn((1, Hkv * G, W, D), device=dev, dtype=torch.bfloat16)
+    k = torch.randn((1, Hkv, L, D), device=dev, dtype=torch.bfloat16)
+    compress.window_scores(q, k, range(Hkv), G, W, "maxpool", 7, window_keep=True)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = 5
+    e0.record()
+    for _ in range(n):
+        compress.window_scores(q, k, range(Hkv), G, W, "maxpool", 7, window_keep=True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    flops = 2 * 2 * Hkv * G * W * L * D  # two logit passes (statistics, probabilities)
+    kbytes = 2 * Hkv * L * D * 2          # K read once per pass
+    return {"ms_per_layer": round(ms, 4), "tflops": round(flops / ms / 1e9, 2),
+            "mfma_util_vs_bf16_dense_peak": round(flops / ms / 1e9 / 2500.0, 4),
+            "k_read_gbs": round(kbytes / ms / 1e6, 1), "window": W, "ctx": L}
 
 
 def main():
@@ -164,6 +269,11 @@ def main():
                      "kernel": "hc::decode_partial_kernel + decode_merge_kernel (one layer of the step)",
                      "bytes_per_launch": int(per_launch)},
     }
+    del stores, q, kn, vn, outs
+    torch.cuda.empty_cache()
+    if not args.no_full_step:
+        rec["full_decode_step"] = full_step_phase(args, torch, dev)
+        rec["window_scoring"] = window_scoring_phase(args, torch, dev)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(L, budgets[0], args.cpu_seconds)
     print(json.dumps(rec))

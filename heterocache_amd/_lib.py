@@ -38,7 +38,7 @@ SIGNATURES = {
     "hc_decode_num_parts": (c_int64, [c_void_p, c_int, c_int]),
     "hc_decode_workspace_size": (c_size_t, [c_int, c_int, c_int64]),
     "hc_gather_store": (c_int, [c_int, c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p,
-                                c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]),
+                                c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
     "hc_append": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                           c_int, c_void_p, c_void_p]),
     "hc_score": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
@@ -46,7 +46,9 @@ SIGNATURES = {
                          c_void_p, c_size_t, c_void_p]),
     "hc_score_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "hc_select_topk": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int, c_void_p, c_int64, c_void_p,
-                               c_void_p]),
+                               c_void_p, c_size_t, c_void_p, c_size_t, c_void_p]),
+    "hc_select_hist_size": (c_size_t, [c_int]),
+    "hc_select_scratch_size": (c_size_t, [c_int, c_int]),
     "hc_set_bits": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,
                             c_void_p]),
     "hc_overlap_count": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,

@@ -97,6 +97,7 @@ class _LayerDrift:
         self.trigger = None    # [n_lead] int32
         self.qbuf = None       # [B, Hq, S, 128] buffered decode queries
         self.count = 0
+        self.meta = None       # device metadata and buffers, built on the first check
 
 
 class HeteroCache(DynamicCache):
@@ -340,7 +341,8 @@ class HeteroCache(DynamicCache):
 
     def decode_select(self, query_states, layer_idx):
         """Buffered pivot drift check and satellite retrieval
-        (heterocache/cache_utils.py:1007-1147), without host syncs."""
+        (heterocache/cache_utils.py:1007-1147), without host syncs: after the
+        first check of a layer every launch reuses device metadata built once."""
         st = self._drift[layer_idx]
         if st is None:
             st = self._drift[layer_idx] = _LayerDrift()
@@ -353,29 +355,74 @@ class HeteroCache(DynamicCache):
         if st.count < S:
             return
         st.count = 0
-        if not st.leaders:
+        if not st.leaders or not any(st.members):
             return
-        work = [(i, h, m) for i, (h, m) in enumerate(zip(st.leaders, st.members)) if m]
-        if not work:
-            return
+        if st.meta is None:
+            st.meta = self._drift_metadata(layer_idx, st)
+        m = st.meta
         store = self.stores[layer_idx]
-        L, G, B, Hkv = self.prefill_len, self.num_key_value_groups, self.bsz, self.num_kv_heads
+        L, G, B = self.prefill_len, self.num_key_value_groups, self.bsz
+        K, nl = m["K"], len(st.leaders)
+        # Scores of every (leader in relation order, batch row): [nl*B, S, L].
+        scores = compress.pivot_step_scores(st.qbuf, store, None, None, G, L, self.pooling, self.kernel_size,
+                                            round_dtype=self._round_dtype(query_states.dtype),
+                                            metadata=m["score_meta"])
+        ops.select_topk(scores.view(nl * B * S, L), m["caps_K"], L, idx=m["cur"], counts=m["cur_counts"])
+        ops.overlap_count(m["cur"], K, st.ref_bits, L, ref_of=m["ref_of"], out=m["overlap"])
+        ops.drift_decide(m["overlap"], nl, B, S, K, self.stable_threshold, st.trigger)
+        # On trigger the reference set becomes the last step's top-K set.
+        last = m["cur"].view(nl * B, S, -1)[:, S - 1]
+        ops.set_bits(last, None, st.ref_bits, L, fixed_count=K, trigger=st.trigger, trig_of=m["trig_of"])
+        if m["plans"]:
+            self._retrieve(layer_idx, st, scores[:, S - 1])
+
+    def _drift_metadata(self, layer_idx, st):
+        """Device tensors and buffers of one layer's drift check and retrieval."""
+        store = self.stores[layer_idx]
+        dev = st.qbuf.device
+        L, G, B, Hkv, S = self.prefill_len, self.num_key_value_groups, self.bsz, self.num_kv_heads, self.decode_step
         K = min(self.base_compress_len, L)
         nl = len(st.leaders)
-        # Scores of every leader (relation order) x batch row: [nl*B, S, L].
         rows = [b * Hkv + h for h in st.leaders for b in range(B)]
         heads = [h for h in st.leaders for b in range(B)]
-        scores = compress.pivot_step_scores(st.qbuf, store, rows, heads, G, L, self.pooling, self.kernel_size,
-                                            round_dtype=self._round_dtype(query_states.dtype))
-        cur, _ = compress.select_kept(scores.view(nl * B * S, L), [K] * (nl * B * S), max_cap=max(K, 1))
-        ref_of = torch.arange(nl * B, dtype=torch.int32, device=cur.device).repeat_interleave(S)
-        counts = ops.overlap_count(cur, K, st.ref_bits, L, ref_of=ref_of)
-        ops.drift_decide(counts, nl, B, S, K, self.stable_threshold, st.trigger)
-        # On trigger: the reference set becomes the last step's top-K set.
-        last = cur.view(nl * B, S, -1)[:, S - 1]
-        trig_of = torch.arange(nl, dtype=torch.int32, device=cur.device).repeat_interleave(B)
-        ops.set_bits(last, None, st.ref_bits, L, fixed_count=K, trigger=st.trigger, trig_of=trig_of)
-        self._retrieve(layer_idx, st, scores[:, S - 1], work)
+        m = {"K": K}
+        m["score_meta"] = compress.pivot_step_metadata(st.qbuf, store, rows, heads, G)
+        m["caps_K"] = torch.full((nl * B * S,), K, dtype=torch.int32, device=dev)
+        m["cur"] = torch.empty((nl * B * S, max(K, 1)), dtype=torch.int32, device=dev)
+        m["cur_counts"] = torch.empty(nl * B * S, dtype=torch.int32, device=dev)
+        m["overlap"] = torch.empty(nl * B * S, dtype=torch.int32, device=dev)
+        m["ref_of"] = torch.arange(nl * B, dtype=torch.int32, device=dev).repeat_interleave(S)
+        m["trig_of"] = torch.arange(nl, dtype=torch.int32, device=dev).repeat_interleave(B)
+        # Retrieval: per leader, one gather job per (batch row, satellite).
+        plans = []
+        caps = [0] * (nl * B)
+        for i, members in enumerate(st.members):
+            if not members:
+                continue
+            lens = self._retrieval_lengths(layer_idx, members)
+            if max(lens) == 0:
+                continue
+            for b in range(B):
+                caps[i * B + b] = max(lens)
+            plans.append((i, members, lens))
+        m["plans"] = []
+        if plans:
+            mk = max(caps)
+            m["ret_caps"] = torch.tensor(caps, dtype=torch.int32).to(dev)
+            m["ret_idx"] = torch.empty((nl * B, mk), dtype=torch.int32, device=dev)
+            m["ret_counts"] = torch.empty(nl * B, dtype=torch.int32, device=dev)
+            kc = self.key_cache_cpu[layer_idx]
+            tier_heads = self._tier_heads[layer_idx]
+            # One gather for every (leader, batch row, satellite) of the layer;
+            # each job is gated by its leader's trigger flag.
+            jobs = [(i, b, mm, n) for i, members, lens in plans for b in range(B) for mm, n in zip(members, lens)
+                    if n > 0]
+            plan = store.plan_rows(kc, [(b, tier_heads[mm]) for i, b, mm, n in jobs],
+                                   [b * Hkv + mm for i, b, mm, n in jobs], [n for i, b, mm, n in jobs],
+                                   idx=m["ret_idx"], idx_rows=[i * B + b for i, b, mm, n in jobs],
+                                   trig_of=[i for i, b, mm, n in jobs])
+            m["plans"].append(plan)
+        return m
 
     def _retrieval_lengths(self, layer_idx, members):
         alloc = self.data["allocation_matrix"][layer_idx]
@@ -388,50 +435,28 @@ class HeteroCache(DynamicCache):
             lens = [min(n, int(self.retrieval_topk)) for n in lens]
         return lens
 
-    def _retrieve(self, layer_idx, st, last_scores, work):
+    def _retrieve(self, layer_idx, st, last_scores):
         """Gather each satellite's tokens from the full-KV tier into slots
         [0, len) of its row (heterocache/cache_utils.py:1084-1123): the
         satellite takes the ascending prefix of its leader's top-max(len)
-        list of the last buffered step.  Gated by the device trigger flag and
-        run on the side stream."""
-        B, Hkv = self.bsz, self.num_kv_heads
-        store = self.stores[layer_idx]
-        plans = []
-        for i, lead, members in work:
-            lens = self._retrieval_lengths(layer_idx, members)
-            if max(lens) > 0:
-                plans.append((i, members, lens))
-        if not plans:
-            return
-        nl = len(st.leaders)
-        mk = max(max(lens) for _, _, lens in plans)
-        caps = [0] * (nl * B)
-        for i, _, lens in plans:
-            for b in range(B):
-                caps[i * B + b] = max(lens)
-        ret_idx, _ = compress.select_kept(last_scores.contiguous(), caps, max_cap=mk)
-        dev = ret_idx.device
+        list of the last buffered step.  Gated by the device trigger flag;
+        from the host tier it runs on the side stream, overlapping whatever
+        the main stream does until this layer's next attention."""
+        m = st.meta
+        ops.select_topk(last_scores, m["ret_caps"], last_scores.shape[1], idx=m["ret_idx"], counts=m["ret_counts"])
+        dev = last_scores.device
         main = torch.cuda.current_stream(dev)
         kc, vc = self.key_cache_cpu[layer_idx], self.value_cache_cpu[layer_idx]
-        tier_heads = self._tier_heads[layer_idx]
         host = self.device == "cpu"
+        store = self.stores[layer_idx]
         side = self._side_stream(dev) if host else main
         if host:
             side.wait_stream(main)
         with torch.cuda.stream(side):
-            for i, members, lens in plans:
-                jobs = [(b, m, n) for b in range(B) for m, n in zip(members, lens) if n > 0]
-                if not jobs:
-                    continue
-                idx_rows = [i * B + b for b, m, n in jobs]
-                store.write_rows(kc, vc, [(b, tier_heads[m]) for b, m, n in jobs],
-                                 [b * Hkv + m for b, m, n in jobs], [n for b, m, n in jobs], idx=ret_idx,
-                                 idx_rows=idx_rows, src_is_host=host, trigger=st.trigger[i:i + 1],
-                                 set_len=False, stream=side)
+            for plan in m["plans"]:
+                store.launch_rows(plan, kc, vc, idx=m["ret_idx"], src_is_host=host, stream=side, trigger=st.trigger,
+                                  set_len=False)
             if host:
                 ev = torch.cuda.Event()
                 ev.record(side)
                 self._retrieval_done[layer_idx] = ev
-        if host:
-            ret_idx.record_stream(side)
-            st.trigger.record_stream(side)

@@ -72,8 +72,16 @@ def last_query_scores(q, k, kv_heads, group, pooling="avgpool", kernel=5, round_
                          round_dtype=round_dtype, scale=scale, stream=stream)
 
 
+def pivot_step_metadata(q_steps, store, rows, heads, group):
+    """Device offset tensors of pivot_step_scores for a fixed pivot set."""
+    B = q_steps.shape[0]
+    hkv = store.rows // B
+    q_off = [(r // hkv) * q_steps.stride(0) + h * group * q_steps.stride(1) for r, h in zip(rows, heads)]
+    return _dev_i64(q_off, q_steps.device), torch.tensor(list(rows), dtype=torch.int32).to(q_steps.device)
+
+
 def pivot_step_scores(q_steps, store, rows, heads, group, seq_len, pooling="avgpool", kernel=5, round_dtype=None,
-                      scale=None, stream=None):
+                      scale=None, stream=None, metadata=None):
     """Scores [len(rows), S, seq_len] of S buffered decode queries per pivot.
 
     q_steps: [B, Hq, S, 128]; rows[j] is the store row of pivot j (batch
@@ -84,14 +92,12 @@ def pivot_step_scores(q_steps, store, rows, heads, group, seq_len, pooling="avgp
     if D != 128 or q_steps.stride(-1) != 1:
         raise ValueError("q_steps must be [B, Hq, S, 128] with unit channel stride")
     scale = 1.0 / math.sqrt(128) if scale is None else scale
-    hkv = store.rows // B
-    q_off = [(r // hkv) * q_steps.stride(0) + h * group * q_steps.stride(1) for r, h in zip(rows, heads)]
+    q_off, k_row = metadata if metadata is not None else pivot_step_metadata(q_steps, store, rows, heads, group)
     flags = ROUND_FLAGS[round_dtype]
-    k_row = torch.tensor(list(rows), dtype=torch.int32).to(q_steps.device)
-    out = ops.score(q_steps, _dev_i64(q_off, q_steps.device), q_steps.stride(1), q_steps.stride(2), store.k, None, 0,
+    out = ops.score(q_steps, q_off, q_steps.stride(1), q_steps.stride(2), store.k, None, 0,
                     seq_len, group, S, seq_len, pooling, kernel, scale, flags=flags,
                     row_tile_off=store.row_tile_off, k_row=k_row, stream=stream)
-    return out.view(len(rows), S, seq_len)
+    return out.view(q_off.numel(), S, seq_len)
 
 
 def select_kept(scores, caps, window=0, max_cap=None, stream=None):

@@ -19,43 +19,78 @@
 
 namespace hc {
 
-__global__ __launch_bounds__(256) void set_bits_kernel(const int32_t* __restrict__ idx, int64_t idx_stride,
-                                                       const int32_t* __restrict__ counts, int fixed_count,
-                                                       uint32_t* __restrict__ bits, int64_t words, int nbits,
-                                                       const int32_t* __restrict__ trigger,
-                                                       const int32_t* __restrict__ trig_of) {
+// Sets of up to kBitsLds words are built in LDS (atomics stay on chip), then
+// written with coalesced stores; longer sets use global atomics.
+constexpr int kBitsLds = 8192;  // words (262144 positions, 32 KB)
+
+__global__ __launch_bounds__(1024) void set_bits_kernel(const int32_t* __restrict__ idx, int64_t idx_stride,
+                                                        const int32_t* __restrict__ counts, int fixed_count,
+                                                        uint32_t* __restrict__ bits, int64_t words, int nbits,
+                                                        const int32_t* __restrict__ trigger,
+                                                        const int32_t* __restrict__ trig_of) {
   const int j = blockIdx.x;
   if (trigger && trigger[trig_of ? trig_of[j] : j] == 0) return;
+  __shared__ uint32_t s_bits[kBitsLds];
   uint32_t* b = bits + (int64_t)j * words;
-  for (int64_t w = threadIdx.x; w < words; w += blockDim.x) b[w] = 0u;
-  __syncthreads();
   const int n = counts ? counts[j] : fixed_count;
   const int32_t* ix = idx + (int64_t)j * idx_stride;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) {
-    const int t = ix[i];
-    if (t >= 0 && t < nbits) atomicOr(&b[t >> 5], 1u << (t & 31));
+  if (words <= kBitsLds) {
+    for (int w = threadIdx.x; w < words; w += blockDim.x) s_bits[w] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int t = ix[i];
+      if (t >= 0 && t < nbits) atomicOr(&s_bits[t >> 5], 1u << (t & 31));
+    }
+    __syncthreads();
+    for (int w = threadIdx.x; w < words; w += blockDim.x) b[w] = s_bits[w];
+  } else {
+    for (int64_t w = threadIdx.x; w < words; w += blockDim.x) b[w] = 0u;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+      const int t = ix[i];
+      if (t >= 0 && t < nbits) atomicOr(&b[t >> 5], 1u << (t & 31));
+    }
   }
 }
 
-__global__ __launch_bounds__(256) void overlap_count_kernel(const int32_t* __restrict__ idx, int64_t idx_stride,
-                                                            int count, const uint32_t* __restrict__ bits,
-                                                            int64_t words, int nbits,
-                                                            const int32_t* __restrict__ ref_of,
-                                                            int32_t* __restrict__ out) {
+__global__ __launch_bounds__(1024) void overlap_count_kernel(const int32_t* __restrict__ idx, int64_t idx_stride,
+                                                             int count, const uint32_t* __restrict__ bits,
+                                                             int64_t words, int nbits,
+                                                             const int32_t* __restrict__ ref_of,
+                                                             int32_t* __restrict__ out) {
   const int j = blockIdx.x;
   const uint32_t* b = bits + (int64_t)(ref_of ? ref_of[j] : j) * words;
   const int32_t* ix = idx + (int64_t)j * idx_stride;
+  __shared__ uint32_t s_bits[kBitsLds];
+  const bool lds = words <= kBitsLds;
+  if (lds) {
+    for (int w = threadIdx.x; w < words; w += blockDim.x) s_bits[w] = b[w];
+    __syncthreads();
+  }
+  const uint32_t* bb = lds ? s_bits : b;
   int c = 0;
-  for (int i = threadIdx.x; i < count; i += blockDim.x) {
+  int i = threadIdx.x;
+  for (; i + 3 * 1024 < count; i += 4 * 1024) {
+    const int t0 = ix[i], t1 = ix[i + 1024], t2 = ix[i + 2048], t3 = ix[i + 3072];
+    c += (t0 >= 0 && t0 < nbits) ? (bb[t0 >> 5] >> (t0 & 31)) & 1u : 0;
+    c += (t1 >= 0 && t1 < nbits) ? (bb[t1 >> 5] >> (t1 & 31)) & 1u : 0;
+    c += (t2 >= 0 && t2 < nbits) ? (bb[t2 >> 5] >> (t2 & 31)) & 1u : 0;
+    c += (t3 >= 0 && t3 < nbits) ? (bb[t3 >> 5] >> (t3 & 31)) & 1u : 0;
+  }
+  for (; i < count; i += 1024) {
     const int t = ix[i];
-    if (t >= 0 && t < nbits) c += (b[t >> 5] >> (t & 31)) & 1u;
+    if (t >= 0 && t < nbits) c += (bb[t >> 5] >> (t & 31)) & 1u;
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) c += __shfl_xor(c, off, 64);
-  __shared__ int s[4];
+  __shared__ int s[16];
   if ((threadIdx.x & 63) == 0) s[threadIdx.x >> 6] = c;
   __syncthreads();
-  if (threadIdx.x == 0) out[j] = s[0] + s[1] + s[2] + s[3];
+  if (threadIdx.x == 0) {
+    int tot = 0;
+    for (int w = 0; w < 16; ++w) tot += s[w];
+    out[j] = tot;
+  }
 }
 
 // counts: [npiv][batch][steps]; one thread per pivot.
@@ -101,7 +136,7 @@ extern "C" int hc_set_bits(const int32_t* idx, int64_t idx_stride, const int32_t
   if (nsets == 0) return HC_OK;
   if (!idx || !bits) return set_error(HC_ERR_INVALID, "hc_set_bits: null pointer argument");
   if (!counts && fixed_count > idx_stride) return set_error(HC_ERR_INVALID, "hc_set_bits: count exceeds the stride");
-  hipLaunchKernelGGL(set_bits_kernel, dim3(nsets), dim3(256), 0, (hipStream_t)stream, idx, idx_stride, counts,
+  hipLaunchKernelGGL(set_bits_kernel, dim3(nsets), dim3(1024), 0, (hipStream_t)stream, idx, idx_stride, counts,
                      fixed_count, bits, words, nbits, trigger, trig_of);
   return check_launch("hc_set_bits");
 }
@@ -114,7 +149,7 @@ extern "C" int hc_overlap_count(const int32_t* idx, int64_t idx_stride, int coun
                      (long long)idx_stride);
   if (nlists == 0) return HC_OK;
   if (!idx || !bits || !out) return set_error(HC_ERR_INVALID, "hc_overlap_count: null pointer argument");
-  hipLaunchKernelGGL(overlap_count_kernel, dim3(nlists), dim3(256), 0, (hipStream_t)stream, idx, idx_stride, count,
+  hipLaunchKernelGGL(overlap_count_kernel, dim3(nlists), dim3(1024), 0, (hipStream_t)stream, idx, idx_stride, count,
                      bits, words, nbits, ref_of, out);
   return check_launch("hc_overlap_count");
 }

@@ -29,7 +29,8 @@
 namespace hc {
 
 constexpr int kScoreWaves = 4;
-constexpr int kScoreChunk = 256;  // tokens per workgroup
+constexpr int kSubTiles = 4;                      // 16-token sub-tiles per wave
+constexpr int kScoreChunk = kScoreWaves * 16 * kSubTiles;  // 256 tokens per workgroup
 constexpr int kQPitch = HC_HEAD_DIM + 8;
 
 struct ScoreArgs {
@@ -73,6 +74,11 @@ template <typename T, bool STORE>
 __device__ __forceinline__ void load_k_subtile(const ScoreArgs& a, int job, int t0, int lane,
                                                typename Elem<T>::vec8 (&kr)[4]) {
   if constexpr (STORE) {
+    if (t0 >= a.L) {  // the sub-tile may lie past the row's capacity
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kr[s] = zero8<T>();
+      return;
+    }
     const T* base = reinterpret_cast<const T*>(a.k) + (a.row_tile_off[a.k_row[job]] + t0 / HC_TILE) * (int64_t)HC_TILE_ELEMS;
     const int h = (t0 / 16) & 1;
 #pragma unroll
@@ -136,11 +142,17 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
   }
   __syncthreads();
   float* my = s_st + (size_t)wave * rows * 2;
-  for (int st = wave; st < kScoreChunk / 16; st += kScoreWaves) {
-    const int t0 = chunk * kScoreChunk + st * 16;
+  // Each wave owns kSubTiles consecutive 16-token sub-tiles; all their key
+  // loads are issued before any is used.
+  const int tw = chunk * kScoreChunk + wave * 16 * kSubTiles;
+  typename Elem<T>::vec8 krs[kSubTiles][4];
+#pragma unroll
+  for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, krs[u]);
+#pragma unroll
+  for (int u = 0; u < kSubTiles; ++u) {
+    const int t0 = tw + 16 * u;
     if (t0 >= a.L) break;
-    typename Elem<T>::vec8 kr[4];
-    load_k_subtile<T, STORE>(a, job, t0, lane, kr);
+    const typename Elem<T>::vec8(&kr)[4] = krs[u];
     for (int nt = 0; nt < a.NT; ++nt) {
       float x[4];
       subtile_logits<T>(a, kr, s_q, nt, t0, lane, x);
@@ -215,11 +227,15 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   }
   __syncthreads();
   const int wout = sum_w ? 1 : a.W;
-  for (int st = wave; st < kScoreChunk / 16; st += kScoreWaves) {
-    const int t0 = chunk * kScoreChunk + st * 16;
+  const int tw = chunk * kScoreChunk + wave * 16 * kSubTiles;
+  typename Elem<T>::vec8 krs[kSubTiles][4];
+#pragma unroll
+  for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, krs[u]);
+#pragma unroll
+  for (int u = 0; u < kSubTiles; ++u) {
+    const int t0 = tw + 16 * u;
     if (t0 >= a.span) break;
-    typename Elem<T>::vec8 kr[4];
-    load_k_subtile<T, STORE>(a, job, t0, lane, kr);
+    const typename Elem<T>::vec8(&kr)[4] = krs[u];
     float gsum[4] = {0.f, 0.f, 0.f, 0.f};  // running window sum (W >= 16)
     for (int nt = 0; nt < a.NT; ++nt) {
       float x[4];
@@ -289,25 +305,38 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   }
 }
 
-__global__ void score_pool_kernel(const float* __restrict__ A, int G, int span, int pooling, int kernel, int flags,
-                                  float* __restrict__ S) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+// 256 consecutive positions of one (job, w') per workgroup; each query
+// head's strip and its pooling halo are staged in LDS once.
+constexpr int kPoolThreads = 256;
+constexpr int kPoolMaxHalf = 31;
+
+__global__ __launch_bounds__(kPoolThreads) void score_pool_kernel(const float* __restrict__ A, int G, int span,
+                                                                  int pooling, int kernel, int flags,
+                                                                  float* __restrict__ S) {
+  __shared__ float s_a[kPoolThreads + 2 * kPoolMaxHalf];
+  const int t0 = blockIdx.x * kPoolThreads;
+  const int t = t0 + threadIdx.x;
   const int jw = blockIdx.y;  // job * wout + w'
-  if (t >= span) return;
   const int p = kernel / 2;
+  const float pad = pooling == 0 ? 0.f : -INFINITY;
   float best = -INFINITY;
   for (int g = 0; g < G; ++g) {
     const float* a = A + ((int64_t)jw * G + g) * span;
-    float acc = pooling == 0 ? 0.f : -INFINITY;
-    for (int d = -p; d <= p; ++d) {
-      const int u = t + d;
-      if (u < 0 || u >= span) continue;  // zero / -inf padding
-      acc = pooling == 0 ? acc + a[u] : fmaxf(acc, a[u]);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kPoolThreads + 2 * p; i += kPoolThreads) {
+      const int u = t0 - p + i;
+      s_a[i] = (u >= 0 && u < span) ? a[u] : pad;
+    }
+    __syncthreads();
+    float acc = pad;
+    for (int d = 0; d <= 2 * p; ++d) {
+      const float x = s_a[threadIdx.x + d];
+      acc = pooling == 0 ? acc + x : fmaxf(acc, x);
     }
     if (pooling == 0) acc = acc / (float)kernel;
     best = fmaxf(best, round_mode(acc, flags));
   }
-  S[(int64_t)jw * span + t] = best;
+  if (t < span) S[(int64_t)jw * span + t] = best;
 }
 
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
@@ -342,8 +371,8 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
     hipLaunchKernelGGL((score_probs_kernel<T, STORE>), dim3(nchunks_span, njobs), dim3(kScoreWaves * 64), lds3, s, a,
                        stats, A);
     if ((rc = check_launch("hc_score(probs)"))) return rc;
-    hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + 255) / 256, njobs * wout), dim3(256), 0, s, A, a.G, a.span,
-                       pooling, kernel, a.flags, scores);
+    hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + kPoolThreads - 1) / kPoolThreads, njobs * wout),
+                       dim3(kPoolThreads), 0, s, A, a.G, a.span, pooling, kernel, a.flags, scores);
     if ((rc = check_launch("hc_score(pool)"))) return rc;
   }
   return HC_OK;

@@ -11,20 +11,32 @@
 // (heterocache/cache_utils.py:1060-1061, :1090-1093) under the stated tie
 // rule: equal scores keep the lower position first.
 //
-// One 1024-thread workgroup per job:
-//  1. radix select, four 8-bit MSB-first passes over order-preserving uint32
-//     keys with an LDS histogram, finds the exact key tau of the last kept
-//     element and how many elements equal to tau are kept;
-//  2. one ordered pass emits every position with key > tau plus the first
-//     `need_eq` positions with key == tau, using block-wide exclusive scans,
-//     so the output is ascending by construction.
+// Multi-workgroup radix select: every job is cut into 4096-position chunks,
+// one 256-thread workgroup per (chunk, job), six launches per call:
+//  1-4. select_hist_kernel(pass p): histogram of the 8-bit digit p (MSB
+//       first) of the order-preserving uint32 keys that match the digits
+//       already fixed, per wave in LDS, summed into a global per-job
+//       histogram.  Each workgroup recovers the fixed digits by replaying
+//       the picks on the earlier global histograms (one wave-wide scan each).
+//  5.   select_count_kernel: replays all four picks -> the exact key tau of
+//       the last kept element and how many elements equal to tau are kept;
+//       counts per chunk the keys above tau and equal to tau.
+//  6.   select_write_kernel: chunk bases from the per-chunk counts, then an
+//       ordered compaction (ballot ranks inside each 64-position row, LDS
+//       scan across rows), so the output is ascending by construction.  It
+//       also clears the global histograms for the next call and writes the
+//       force-kept window tail.
 #include "hc_common.h"
 #include "hc_internal.h"
 
 namespace hc {
 
-constexpr int kSelThreads = 1024;
-constexpr int kSelItems = 4;  // consecutive positions per thread per compaction step
+constexpr int kSelThreads = 256;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kSelChunk = 4096;                      // positions per workgroup
+constexpr int kSelRows = kSelChunk / kSelThreads;    // 16 rows of 256 positions
+constexpr int kSelBins = 256;
+constexpr int kSelMaxChunks = 4096;
 
 __device__ __forceinline__ uint32_t order_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -32,151 +44,330 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Exclusive scan of one int per thread across the workgroup; returns the
-// exclusive prefix and writes the total to *total.
-__device__ __forceinline__ int block_exclusive_scan(int v, int* s_wave, int* total) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
-  if (lane == 63) s_wave[wave] = x;
-  __syncthreads();
-  if (wave == 0) {
-    int w = lane < kSelThreads / 64 ? s_wave[lane] : 0;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int y = __shfl_up(w, off, 64);
-      if (lane >= off) w += y;
-    }
-    if (lane < kSelThreads / 64) s_wave[lane] = w;  // inclusive prefix of wave totals
-  }
-  __syncthreads();
-  const int before = wave > 0 ? s_wave[wave - 1] : 0;
-  *total = s_wave[kSelThreads / 64 - 1];
-  __syncthreads();
-  return before + x - v;
+struct SelJob {
+  int body;  // positions selected from [0, span)
+  int tail;  // window positions appended
+};
+
+// Budget clamped to what the index row can hold; a window (SnapKV) is always
+// kept whole (its reference asserts cap > window).
+__device__ __forceinline__ SelJob sel_job(const int32_t* caps, int job, int span, int window, int64_t idx_stride) {
+  const int cap = max(0, (int)min((int64_t)caps[job], idx_stride));
+  SelJob j;
+  j.tail = window;
+  const int body = min(window > 0 ? max(cap - window, 0) : cap, span);
+  j.body = min(body, (int)max((int64_t)0, idx_stride - window));
+  return j;
 }
 
-__global__ __launch_bounds__(kSelThreads) void select_topk_kernel(const float* __restrict__ scores,
+struct SelState {
+  uint32_t prefix, mask;
+  int k_rem, ties;
+};
+
+// Replay the digit picks of passes [0, npass) from the global histograms.
+// Reached by every thread of the workgroup; wave 0 does the scans.
+__device__ __forceinline__ SelState sel_replay(const unsigned* __restrict__ ghist, int body, int npass,
+                                               int* s_pick) {
+  SelState st;
+  st.prefix = 0;
+  st.mask = 0;
+  st.k_rem = body;
+  st.ties = 0;
+  const int lane = threadIdx.x & 63;
+  for (int p = 0; p < npass; ++p) {
+    if (threadIdx.x < 64) {
+      // Lane l owns bins 255-4l .. 252-4l (descending digit order).
+      int c[4], sum = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = (int)ghist[p * kSelBins + kSelBins - 1 - 4 * lane - i];
+        sum += c[i];
+      }
+      int incl = sum;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      int above = incl - sum;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (above < st.k_rem && above + c[i] >= st.k_rem) {
+          s_pick[0] = kSelBins - 1 - 4 * lane - i;
+          s_pick[1] = above;
+          s_pick[2] = c[i];
+        }
+        above += c[i];
+      }
+    }
+    __syncthreads();
+    const int shift = 24 - 8 * p;
+    st.prefix |= (uint32_t)s_pick[0] << shift;
+    st.mask |= 0xFFu << shift;
+    st.k_rem -= s_pick[1];
+    st.ties = s_pick[2];
+    __syncthreads();
+  }
+  return st;
+}
+
+__global__ __launch_bounds__(kSelThreads) void select_hist_kernel(const float* __restrict__ scores,
+                                                                  int64_t score_stride, int span,
+                                                                  const int32_t* __restrict__ caps, int window,
+                                                                  int64_t idx_stride, unsigned* __restrict__ ghist,
+                                                                  int pass) {
+  const int job = blockIdx.y, chunk = blockIdx.x;
+  const SelJob jb = sel_job(caps, job, span, window, idx_stride);
+  if (jb.body <= 0 || jb.body >= span) return;
+  __shared__ unsigned s_hist[kSelWaves][kSelBins];
+  __shared__ int s_pick[3];
+  unsigned* gh = ghist + (int64_t)job * 4 * kSelBins;
+  const SelState st = sel_replay(gh, jb.body, pass, s_pick);
+  for (int i = threadIdx.x; i < kSelWaves * kSelBins; i += kSelThreads) (&s_hist[0][0])[i] = 0;
+  __syncthreads();
+  const float* s = scores + (int64_t)job * score_stride;
+  const int t0 = chunk * kSelChunk;
+  const int shift = 24 - 8 * pass;
+  unsigned* wh = s_hist[threadIdx.x >> 6];
+  float v[kSelRows];
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + threadIdx.x;
+    v[r] = t < span ? s[t] : 0.f;
+  }
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + threadIdx.x;
+    const uint32_t u = order_key(v[r]);
+    const bool valid = t < span && (u & st.mask) == st.prefix;
+    const uint32_t d = (u >> shift) & 0xFFu;
+    // A wave whose valid lanes share one digit issues a single atomic.
+    const uint64_t act = __ballot(valid);
+    if (act == 0) continue;
+    const int leader = __ffsll((long long)act) - 1;
+    const uint32_t dl = __shfl(d, leader, 64);
+    if (__ballot(valid && d == dl) == act) {
+      if ((int)(threadIdx.x & 63) == leader) atomicAdd(&wh[dl], (unsigned)__popcll(act));
+    } else if (valid) {
+      atomicAdd(&wh[d], 1u);
+    }
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < kSelBins; b += kSelThreads) {
+    unsigned c = 0;
+#pragma unroll
+    for (int w = 0; w < kSelWaves; ++w) c += s_hist[w][b];
+    if (c) atomicAdd(&gh[pass * kSelBins + b], c);
+  }
+}
+
+// state[job] = {tau, need_eq, all_ties}; cnt[job][chunk] = {#key > tau, #key == tau}.
+__global__ __launch_bounds__(kSelThreads) void select_count_kernel(const float* __restrict__ scores,
+                                                                   int64_t score_stride, int span,
+                                                                   const int32_t* __restrict__ caps, int window,
+                                                                   int64_t idx_stride,
+                                                                   const unsigned* __restrict__ ghist,
+                                                                   int* __restrict__ state, int* __restrict__ cnt,
+                                                                   int32_t* __restrict__ counts, int nchunks) {
+  const int job = blockIdx.y, chunk = blockIdx.x;
+  const SelJob jb = sel_job(caps, job, span, window, idx_stride);
+  if (chunk == 0 && threadIdx.x == 0 && counts) counts[job] = jb.body + jb.tail;
+  if (jb.body <= 0 || jb.body >= span) return;
+  __shared__ int s_pick[3];
+  __shared__ int s_red[2][kSelWaves];
+  const SelState st = sel_replay(ghist + (int64_t)job * 4 * kSelBins, jb.body, 4, s_pick);
+  const uint32_t tau = st.prefix;
+  if (chunk == 0 && threadIdx.x == 0) {
+    int* sp = state + job * 4;
+    sp[0] = (int)tau;
+    sp[1] = st.k_rem;
+    sp[2] = st.ties == st.k_rem ? 1 : 0;
+  }
+  const float* s = scores + (int64_t)job * score_stride;
+  const int t0 = chunk * kSelChunk;
+  int n_gt = 0, n_eq = 0;
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + threadIdx.x;
+    if (t < span) {
+      const uint32_t u = order_key(s[t]);
+      n_gt += u > tau;
+      n_eq += u == tau;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    n_gt += __shfl_xor(n_gt, off, 64);
+    n_eq += __shfl_xor(n_eq, off, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    s_red[0][threadIdx.x >> 6] = n_gt;
+    s_red[1][threadIdx.x >> 6] = n_eq;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int a = 0, b = 0;
+    for (int w = 0; w < kSelWaves; ++w) {
+      a += s_red[0][w];
+      b += s_red[1][w];
+    }
+    cnt[((int64_t)job * nchunks + chunk) * 2 + 0] = a;
+    cnt[((int64_t)job * nchunks + chunk) * 2 + 1] = b;
+  }
+}
+
+__global__ __launch_bounds__(kSelThreads) void select_write_kernel(const float* __restrict__ scores,
                                                                    int64_t score_stride, int span,
                                                                    const int32_t* __restrict__ caps, int window,
                                                                    int32_t* __restrict__ idx, int64_t idx_stride,
-                                                                   int32_t* __restrict__ counts) {
-  const int job = blockIdx.x;
-  const float* s = scores + (int64_t)job * score_stride;
+                                                                   unsigned* __restrict__ ghist,
+                                                                   const int* __restrict__ state,
+                                                                   const int* __restrict__ cnt, int nchunks) {
+  const int job = blockIdx.y, chunk = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const SelJob jb = sel_job(caps, job, span, window, idx_stride);
   int32_t* out = idx + (int64_t)job * idx_stride;
-  const int tid = threadIdx.x;
-  __shared__ unsigned s_hist[256];
-  __shared__ int s_wave[kSelThreads / 64];
-  __shared__ unsigned s_digit, s_above;
-
-  // Budget clamped to what the index row can hold; a window (SnapKV) is
-  // always kept whole (its reference asserts cap > window).
-  const int cap = max(0, (int)min((int64_t)caps[job], idx_stride));
-  const int tail = window;
-  int body = min(window > 0 ? max(cap - window, 0) : cap, span);
-  body = min(body, (int)max((int64_t)0, idx_stride - tail));
-
-  if (body >= span) {
-    for (int t = tid; t < span; t += kSelThreads) out[t] = t;
-  } else if (body > 0) {
-    // 1. radix select of the body-th largest key.
-    uint32_t prefix = 0, mask = 0;
-    int k_rem = body;
-    for (int pass = 0; pass < 4; ++pass) {
-      const int shift = 24 - 8 * pass;
-      for (int i = tid; i < 256; i += kSelThreads) s_hist[i] = 0;
-      __syncthreads();
-      for (int t = tid; t < span; t += kSelThreads) {
-        const uint32_t u = order_key(s[t]);
-        if ((u & mask) == prefix) atomicAdd(&s_hist[(u >> shift) & 255u], 1u);
-      }
-      __syncthreads();
-      if (tid == 0) {
-        unsigned above = 0;
-        int d = 255;
-        for (; d > 0; --d) {
-          if (above + s_hist[d] >= (unsigned)k_rem) break;
-          above += s_hist[d];
-        }
-        s_digit = (unsigned)d;
-        s_above = above;
-      }
-      __syncthreads();
-      prefix |= s_digit << shift;
-      mask |= 255u << shift;
-      k_rem -= (int)s_above;
-      __syncthreads();
-    }
-    const uint32_t tau = prefix;
-    const int need_eq = k_rem;  // >= 1 elements equal to tau are kept
-    // 2. ordered compaction.
-    int sel_base = 0, eq_base = 0;
-    for (int t0 = 0; t0 < span; t0 += kSelThreads * kSelItems) {
-      const int tb = t0 + tid * kSelItems;
-      uint32_t keys[kSelItems];
-      int n_eq = 0;
-#pragma unroll
-      for (int i = 0; i < kSelItems; ++i) {
-        const int t = tb + i;
-        keys[i] = t < span ? order_key(s[t]) : 0u;
-        if (t < span) n_eq += keys[i] == tau;
-      }
-      int tot_eq;
-      const int eq_before = eq_base + block_exclusive_scan(n_eq, s_wave, &tot_eq);
-      // Positions this thread keeps, given the running count of ties.
-      int n_sel = 0;
-      {
-        int e = eq_before;
-#pragma unroll
-        for (int i = 0; i < kSelItems; ++i) {
-          const int t = tb + i;
-          if (t >= span) continue;
-          if (keys[i] > tau) ++n_sel;
-          else if (keys[i] == tau) { n_sel += (e < need_eq); ++e; }
-        }
-      }
-      int tot_sel;
-      int pos = sel_base + block_exclusive_scan(n_sel, s_wave, &tot_sel);
-      {
-        int e = eq_before;
-#pragma unroll
-        for (int i = 0; i < kSelItems; ++i) {
-          const int t = tb + i;
-          if (t >= span) continue;
-          bool take = false;
-          if (keys[i] > tau) take = true;
-          else if (keys[i] == tau) { take = (e < need_eq); ++e; }
-          if (take) out[pos++] = t;
-        }
-      }
-      sel_base += tot_sel;
-      eq_base += tot_eq;
-    }
+  const int t0 = chunk * kSelChunk;
+  if (chunk == 0) {
+    for (int i = tid; i < jb.tail; i += kSelThreads) out[jb.body + i] = span + i;
+    for (int i = tid; i < 4 * kSelBins; i += kSelThreads) ghist[(int64_t)job * 4 * kSelBins + i] = 0u;
   }
-  // Force-kept window tail.
-  for (int i = tid; i < tail; i += kSelThreads) out[body + i] = span + i;
-  if (tid == 0 && counts) counts[job] = body + tail;
+  if (jb.body <= 0) return;
+  if (jb.body >= span) {
+    for (int i = tid; i < kSelChunk; i += kSelThreads)
+      if (t0 + i < span) out[t0 + i] = t0 + i;
+    return;
+  }
+  __shared__ int s_base[2];
+  __shared__ int s_cnt[2][kSelRows][kSelWaves];
+  __shared__ int s_off[2][kSelRows][kSelWaves];
+  const uint32_t tau = (uint32_t)state[job * 4];
+  const int need_eq = state[job * 4 + 1];
+  const bool all_ties = state[job * 4 + 2] != 0;
+  if (tid == 0) {
+    // Kept elements and ties in the chunks before this one.
+    int sel = 0, eq = 0;
+    for (int c = 0; c < chunk; ++c) {
+      const int g = cnt[((int64_t)job * nchunks + c) * 2], e = cnt[((int64_t)job * nchunks + c) * 2 + 1];
+      sel += g + (all_ties ? e : max(0, min(e, need_eq - eq)));
+      eq += e;
+    }
+    s_base[0] = sel;
+    s_base[1] = eq;
+  }
+  const float* s = scores + (int64_t)job * score_stride;
+  uint32_t keys[kSelRows];
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + tid;
+    keys[r] = t < span ? order_key(s[t]) : 0u;
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  // Ties: ranks of equal keys in position order (row-major over (row, wave)).
+  uint64_t eqm[kSelRows];
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + tid;
+    eqm[r] = __ballot(t < span && keys[r] == tau);
+    if (lane == 0) s_cnt[1][r][wave] = __popcll(eqm[r]);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int e = s_base[1];
+    for (int r = 0; r < kSelRows; ++r)
+      for (int w = 0; w < kSelWaves; ++w) {
+        s_off[1][r][w] = e;
+        e += s_cnt[1][r][w];
+      }
+  }
+  __syncthreads();
+  uint64_t selm[kSelRows];
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + tid;
+    bool take = t < span && keys[r] > tau;
+    if (t < span && keys[r] == tau) {
+      const int rank = s_off[1][r][wave] + __popcll(eqm[r] & below);
+      take = all_ties || rank < need_eq;
+    }
+    selm[r] = __ballot(take);
+    if (lane == 0) s_cnt[0][r][wave] = __popcll(selm[r]);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int p = s_base[0];
+    for (int r = 0; r < kSelRows; ++r)
+      for (int w = 0; w < kSelWaves; ++w) {
+        s_off[0][r][w] = p;
+        p += s_cnt[0][r][w];
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    if ((selm[r] >> lane) & 1ull) out[s_off[0][r][wave] + __popcll(selm[r] & below)] = t0 + r * kSelThreads + tid;
+  }
+}
+
+// The histograms live in a buffer that must be zero before the first call and
+// that every completed call leaves zeroed; state and chunk counts live in a
+// per-call scratch buffer that needs no initialisation.
+size_t select_hist_bytes(int njobs) { return (size_t)njobs * 4 * kSelBins * sizeof(unsigned); }
+
+size_t select_scratch_bytes(int njobs, int span) {
+  const int nchunks = (span + kSelChunk - 1) / kSelChunk;
+  return (size_t)njobs * (4 * sizeof(int) + (size_t)nchunks * 2 * sizeof(int));
 }
 
 }  // namespace hc
 
 using namespace hc;
 
+extern "C" size_t hc_select_hist_size(int njobs) {
+  if (njobs <= 0) return 0;
+  return select_hist_bytes(njobs);
+}
+
+extern "C" size_t hc_select_scratch_size(int njobs, int span) {
+  if (njobs <= 0 || span < 0) return 0;
+  return select_scratch_bytes(njobs, span);
+}
+
 extern "C" int hc_select_topk(const float* scores, int64_t score_stride, int njobs, int span, const int32_t* caps,
-                              int window, int32_t* idx, int64_t idx_stride, int32_t* counts, void* stream) {
+                              int window, int32_t* idx, int64_t idx_stride, int32_t* counts, void* hist,
+                              size_t hist_bytes, void* scratch, size_t scratch_bytes, void* stream) {
   clear_error();
   if (njobs < 0 || njobs > 65535 || span < 0 || window < 0)
     return set_error(HC_ERR_INVALID, "hc_select_topk: njobs=%d span=%d window=%d", njobs, span, window);
   if (njobs == 0) return HC_OK;
-  if (!scores || !caps || !idx) return set_error(HC_ERR_INVALID, "hc_select_topk: null pointer argument");
+  if (!scores || !caps || !idx || !hist || !scratch)
+    return set_error(HC_ERR_INVALID, "hc_select_topk: null pointer argument");
   if (score_stride < span || idx_stride < window || idx_stride < 1)
     return set_error(HC_ERR_INVALID, "hc_select_topk: strides too small (scores %lld, idx %lld)",
                      (long long)score_stride, (long long)idx_stride);
-  hipLaunchKernelGGL(select_topk_kernel, dim3(njobs), dim3(kSelThreads), 0, (hipStream_t)stream, scores,
-                     score_stride, span, caps, window, idx, idx_stride, counts);
-  return check_launch("hc_select_topk");
+  const int nchunks = (span + kSelChunk - 1) / kSelChunk;
+  if (nchunks > kSelMaxChunks) return set_error(HC_ERR_INVALID, "hc_select_topk: span %d too long", span);
+  if (hist_bytes < select_hist_bytes(njobs) || scratch_bytes < select_scratch_bytes(njobs, span))
+    return set_error(HC_ERR_INVALID, "hc_select_topk: histogram or scratch buffer too small");
+  unsigned* ghist = reinterpret_cast<unsigned*>(hist);
+  int* state = reinterpret_cast<int*>(scratch);
+  int* cnt = state + (size_t)njobs * 4;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(nchunks > 0 ? nchunks : 1, njobs);
+  if (nchunks > 0) {
+    for (int pass = 0; pass < 4; ++pass) {
+      hipLaunchKernelGGL(select_hist_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, window,
+                         idx_stride, ghist, pass);
+      int rc = check_launch("hc_select_topk(hist)");
+      if (rc) return rc;
+    }
+  }
+  hipLaunchKernelGGL(select_count_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, window,
+                     idx_stride, ghist, state, cnt, counts, nchunks);
+  int rc = check_launch("hc_select_topk(count)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(select_write_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, window,
+                     idx, idx_stride, ghist, state, cnt, nchunks);
+  return check_launch("hc_select_topk(write)");
 }

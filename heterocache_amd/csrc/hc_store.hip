@@ -24,9 +24,10 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
     const T* __restrict__ src_k, const T* __restrict__ src_v, const int64_t* __restrict__ src_off,
     int64_t src_tok_stride, int src_len, const int32_t* __restrict__ idx, const int64_t* __restrict__ idx_off,
     const int32_t* __restrict__ count, const int32_t* __restrict__ dst_row, T* __restrict__ kstore,
-    T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off, const int32_t* __restrict__ trigger) {
-  if (trigger && *trigger == 0) return;
+    T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off, const int32_t* __restrict__ trigger,
+    const int32_t* __restrict__ trig_of) {
   const int job = blockIdx.y;
+  if (trigger && trigger[trig_of ? trig_of[job] : 0] == 0) return;
   const int tile = blockIdx.x;
   const int n = count[job];
   const int tok0 = tile * HC_TILE;
@@ -142,10 +143,12 @@ template <typename T>
 static int launch_gather_store(const void* src_k, const void* src_v, const int64_t* src_off, int64_t src_tok_stride,
                                int src_len, const int32_t* idx, const int64_t* idx_off, const int32_t* count,
                                const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off,
-                               int njobs, int max_count, const int32_t* trigger, hipStream_t s) {
+                               int njobs, int max_count, const int32_t* trigger, const int32_t* trig_of,
+                               hipStream_t s) {
   dim3 grid((max_count + HC_TILE - 1) / HC_TILE, njobs);
   hipLaunchKernelGGL((gather_store_kernel<T>), grid, dim3(256), 0, s, (const T*)src_k, (const T*)src_v, src_off,
-                     src_tok_stride, src_len, idx, idx_off, count, dst_row, (T*)kstore, (T*)vstore, row_tile_off, trigger);
+                     src_tok_stride, src_len, idx, idx_off, count, dst_row, (T*)kstore, (T*)vstore, row_tile_off, trigger,
+                     trig_of);
   return check_launch("hc_gather_store");
 }
 
@@ -167,7 +170,7 @@ extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, 
                                const int64_t* src_off, int64_t src_tok_stride, int src_len, const int32_t* idx,
                                const int64_t* idx_off, const int32_t* count, const int32_t* dst_row, void* kstore,
                                void* vstore, const int64_t* row_tile_off, int njobs, int max_count,
-                               const int32_t* trigger, void* stream) {
+                               const int32_t* trigger, const int32_t* trig_of, void* stream) {
   clear_error();
   if (njobs < 0 || max_count < 0 || njobs > 65535)
     return set_error(HC_ERR_INVALID, "hc_gather_store: njobs=%d max_count=%d", njobs, max_count);
@@ -194,13 +197,13 @@ extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, 
   switch (dtype) {
     case HC_DTYPE_BF16:
       return launch_gather_store<__bf16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                         vstore, row_tile_off, njobs, max_count, trigger, s);
+                                         vstore, row_tile_off, njobs, max_count, trigger, trig_of, s);
     case HC_DTYPE_F16:
       return launch_gather_store<_Float16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                           vstore, row_tile_off, njobs, max_count, trigger, s);
+                                           vstore, row_tile_off, njobs, max_count, trigger, trig_of, s);
     case HC_DTYPE_F32:
       return launch_gather_store<float>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                        vstore, row_tile_off, njobs, max_count, trigger, s);
+                                        vstore, row_tile_off, njobs, max_count, trigger, trig_of, s);
     default:
       return set_error(HC_ERR_INVALID, "hc_gather_store: unknown dtype %d", dtype);
   }

@@ -65,6 +65,8 @@ class Workspace:
 
 
 WORKSPACE = Workspace()
+# hc_select_topk keeps self-clearing histograms in this buffer.
+SELECT_HIST = Workspace()
 
 
 def decode_num_parts(host_row_len, tiles_per_wave=DEFAULT_TILES_PER_WAVE):
@@ -119,10 +121,10 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
 
 
 def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore, vstore, row_tile_off,
-                 max_count, src_is_host=False, trigger=None, stream=None):
+                 max_count, src_is_host=False, trigger=None, trig_of=None, stream=None):
     """store[dst_row[j]][i] = src[src_off[j] + idx[idx_off[j] + i] * stride], i < count[j]."""
     lib = _lib.load()
-    _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger)
+    _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger, trig_of)
     if src_is_host:
         if src_k.is_cuda or not src_k.is_pinned() or not src_v.is_pinned():
             raise ValueError("host sources must be pinned CPU tensors")
@@ -132,14 +134,15 @@ def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, c
         raise TypeError("source and store dtypes differ")
     for name, t, dt in (("src_off", src_off, torch.int64), ("count", count, torch.int32),
                         ("dst_row", dst_row, torch.int32), ("idx", idx, torch.int32),
-                        ("idx_off", idx_off, torch.int64), ("trigger", trigger, torch.int32)):
+                        ("idx_off", idx_off, torch.int64), ("trigger", trigger, torch.int32),
+                        ("trig_of", trig_of, torch.int32)):
         if t is not None and t.dtype != dt:
             raise TypeError(f"{name} must be {dt}")
     njobs = count.numel()
     _lib.check(lib.hc_gather_store(dtype_code(kstore.dtype), _ptr(src_k), _ptr(src_v), int(bool(src_is_host)),
                                    _ptr(src_off), int(src_tok_stride), int(src_len), _ptr(idx), _ptr(idx_off), _ptr(count),
                                    _ptr(dst_row), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off), njobs,
-                                   int(max_count), _ptr(trigger), _stream(stream)))
+                                   int(max_count), _ptr(trigger), _ptr(trig_of), _stream(stream)))
 
 
 def append(k_new, v_new, kstore, vstore, row_tile_off, row_len, row_cap, status=None, stream=None):
@@ -214,8 +217,12 @@ def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None
         idx = torch.empty((njobs, span + window), dtype=torch.int32, device=scores.device)
     if counts is None:
         counts = torch.empty(njobs, dtype=torch.int32, device=scores.device)
+    hist = SELECT_HIST.get(scores.device, lib.hc_select_hist_size(njobs))
+    scratch = torch.empty(max(lib.hc_select_scratch_size(njobs, int(span)), 16), dtype=torch.uint8,
+                          device=scores.device)
     _lib.check(lib.hc_select_topk(_ptr(scores), scores.stride(0), njobs, int(span), _ptr(caps), int(window), _ptr(idx),
-                                  idx.stride(0), _ptr(counts), _stream(stream)))
+                                  idx.stride(0), _ptr(counts), _ptr(hist), hist.numel(), _ptr(scratch),
+                                  scratch.numel(), _stream(stream)))
     return idx, counts
 
 

@@ -70,28 +70,24 @@ class KVStore:
         self.row_order = torch.as_tensor(order).to(self.device)
 
     # -- writers -----------------------------------------------------------
-    def write_rows(self, src_k, src_v, src_bh, rows, counts, idx=None, idx_rows=None, src_is_host=False,
-                   stream=None, trigger=None, set_len=True):
-        """store[rows[j]][i] = src[b_j, h_j, idx[r_j][i]] (or token i), i < counts[j].
+    def plan_rows(self, src_k, src_bh, rows, counts, idx=None, idx_rows=None, trig_of=None):
+        """Validate a gather and build its device metadata (see write_rows).
 
-        src_k / src_v: [B, H, L, 128] with unit channel stride (any other
-        strides), on the device or host-pinned.  src_bh: [jobs, 2] (b, h) of
-        each job's source head.  idx: [n, M] int32 device tensor of source
-        positions (None copies positions 0..count-1); job j reads row
-        r_j = idx_rows[j] (default j).  trigger: int32 device flag gating the
-        copy.
+        The returned plan can be launched many times with launch_rows (the
+        sources, index tensor and counts must keep their shapes); building
+        it copies small host lists to the device, launching it does not.
         """
         rows = np.asarray(rows, dtype=np.int64)
         counts = np.asarray(counts, dtype=np.int64)
         src_bh = np.asarray(src_bh, dtype=np.int64).reshape(-1, 2)
         if len(rows) == 0:
-            return
+            return None
         if len(src_bh) != len(rows) or len(counts) != len(rows):
             raise ValueError("one (b, h) source and one count per destination row")
-        if (counts > self.host_cap[rows]).any():
+        if (rows < 0).any() or (rows >= self.rows).any():
+            raise ValueError("destination row out of range")
+        if (counts > self.host_cap[rows]).any() or (counts < 0).any():
             raise RuntimeError("write exceeds a row's capacity")
-        if src_k.shape != src_v.shape or src_k.stride() != src_v.stride():
-            raise ValueError("K and V sources must have one shape and stride")
         if src_k.dim() != 4 or src_k.shape[-1] != HEAD_DIM or src_k.stride(-1) != 1:
             raise ValueError("sources must be [B, H, L, 128] with unit channel stride")
         if src_k.dtype != self.dtype:
@@ -104,8 +100,7 @@ class KVStore:
         tok_stride = src_k.stride(2)
         src_off = src_bh[:, 0] * src_k.stride(0) + src_bh[:, 1] * src_k.stride(1)
         esz = src_k.element_size()
-        if (src_k.data_ptr() % 16) or (src_v.data_ptr() % 16) or (tok_stride * esz) % 16 or \
-                ((src_off * esz) % 16).any():
+        if (src_k.data_ptr() % 16) or (tok_stride * esz) % 16 or ((src_off * esz) % 16).any():
             raise ValueError("sources must be 16-byte aligned per token")
         dev = self.device
         idx_off = None
@@ -118,12 +113,49 @@ class KVStore:
             if (counts > idx.shape[1]).any():
                 raise ValueError("count exceeds the index list")
             idx_off = torch.as_tensor(r * idx.stride(0)).to(dev)
-        ops.gather_store(src_k, src_v, torch.as_tensor(src_off).to(dev), tok_stride, L, idx, idx_off,
-                         torch.as_tensor(counts, dtype=torch.int32).to(dev),
-                         torch.as_tensor(rows, dtype=torch.int32).to(dev), self.k, self.v, self.row_tile_off,
-                         int(counts.max()), src_is_host=src_is_host, trigger=trigger, stream=stream)
+        if trig_of is not None:
+            trig_of = torch.as_tensor(np.asarray(trig_of, dtype=np.int32)).to(dev)
+        return {"src_off": torch.as_tensor(src_off).to(dev), "tok_stride": tok_stride, "src_len": L,
+                "trig_of": trig_of,
+                "shape": tuple(src_k.shape), "stride": tuple(src_k.stride()), "idx_off": idx_off,
+                "counts": torch.as_tensor(counts, dtype=torch.int32).to(dev), "host_counts": counts,
+                "rows": torch.as_tensor(rows, dtype=torch.int32).to(dev), "host_rows": rows,
+                "max_count": int(counts.max())}
+
+    def launch_rows(self, plan, src_k, src_v, idx=None, src_is_host=False, stream=None, trigger=None,
+                    set_len=True):
+        """Run a gather planned by plan_rows (no host-to-device copies)."""
+        if plan is None:
+            return
+        if tuple(src_k.shape) != plan["shape"] or tuple(src_k.stride()) != plan["stride"] or \
+                src_v.shape != src_k.shape or src_v.stride() != src_k.stride():
+            raise ValueError("sources do not match the plan")
+        if src_v.data_ptr() % 16:
+            raise ValueError("sources must be 16-byte aligned per token")
+        if (idx is None) != (plan["idx_off"] is None):
+            raise ValueError("index tensor does not match the plan")
+        ops.gather_store(src_k, src_v, plan["src_off"], plan["tok_stride"], plan["src_len"], idx, plan["idx_off"],
+                         plan["counts"], plan["rows"], self.k, self.v, self.row_tile_off, plan["max_count"],
+                         src_is_host=src_is_host, trigger=trigger, trig_of=plan["trig_of"], stream=stream)
         if set_len:
-            self.set_lengths(counts, rows)
+            self.set_lengths(plan["host_counts"], plan["host_rows"])
+
+    def write_rows(self, src_k, src_v, src_bh, rows, counts, idx=None, idx_rows=None, src_is_host=False,
+                   stream=None, trigger=None, set_len=True):
+        """store[rows[j]][i] = src[b_j, h_j, idx[r_j][i]] (or token i), i < counts[j].
+
+        src_k / src_v: [B, H, L, 128] with unit channel stride (any other
+        strides), on the device or host-pinned.  src_bh: [jobs, 2] (b, h) of
+        each job's source head.  idx: [n, M] int32 device tensor of source
+        positions (None copies positions 0..count-1); job j reads row
+        r_j = idx_rows[j] (default j).  trigger: int32 device flag gating the
+        copy.
+        """
+        if src_k.shape != src_v.shape or src_k.stride() != src_v.stride():
+            raise ValueError("K and V sources must have one shape and stride")
+        plan = self.plan_rows(src_k, src_bh, rows, counts, idx=idx, idx_rows=idx_rows)
+        self.launch_rows(plan, src_k, src_v, idx=idx, src_is_host=src_is_host, stream=stream, trigger=trigger,
+                         set_len=set_len)
 
     def append(self, k_new, v_new, stream=None):
         """Write one token per row at slot len and advance every length by one.

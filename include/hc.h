@@ -77,7 +77,8 @@ size_t hc_decode_workspace_size(int rows, int group, int64_t num_parts);
  * (idx == NULL copies source tokens 0..count-1; indices are clamped into
  * [0, src_len) like the reference's clamp before its gather).  With src_is_host != 0 the
  * sources are host-pinned, device-mapped buffers read over the host link.
- * When trigger != NULL the call does nothing unless *trigger != 0 (device).
+ * When trigger != NULL job j is skipped unless trigger[trig_of ? trig_of[j] : 0]
+ * != 0 (device flags; one launch can serve several gated groups of jobs).
  * Replaces the keep-head index_copy_ (heterocache/cache_utils.py:914-937),
  * the compressed-head gather + index_copy_ (heterocache/cache_utils.py:854-877)
  * and the retrieval index_select + copy_ (heterocache/cache_utils.py:1097-1123).
@@ -85,7 +86,7 @@ size_t hc_decode_workspace_size(int rows, int group, int64_t num_parts);
 int hc_gather_store(int dtype, const void* src_k, const void* src_v, int src_is_host, const int64_t* src_off,
                     int64_t src_tok_stride, int src_len, const int32_t* idx, const int64_t* idx_off, const int32_t* count,
                     const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off, int njobs,
-                    int max_count, const int32_t* trigger, void* stream);
+                    int max_count, const int32_t* trigger, const int32_t* trig_of, void* stream);
 
 /*
  * Append one token per row at slot row_len[r], then row_len[r] += 1.
@@ -143,7 +144,13 @@ size_t hc_score_workspace_size(int njobs, int seq_len, int group, int window, in
  * drift / retrieval topk of heterocache/cache_utils.py:1060-1061, 1090-1093.
  */
 int hc_select_topk(const float* scores, int64_t score_stride, int njobs, int span, const int32_t* caps, int window,
-                   int32_t* idx, int64_t idx_stride, int32_t* counts, void* stream);
+                   int32_t* idx, int64_t idx_stride, int32_t* counts, void* hist, size_t hist_bytes, void* scratch,
+                   size_t scratch_bytes, void* stream);
+/* hist: hc_select_hist_size(njobs) bytes, zero-filled before its first use;
+ * every completed call leaves it zeroed again (calls on one stream may share
+ * it).  scratch: hc_select_scratch_size(njobs, span) bytes, no initialisation. */
+size_t hc_select_hist_size(int njobs);
+size_t hc_select_scratch_size(int njobs, int span);
 
 /*
  * Position lists -> bitmasks: set j (words uint32 words at bits + j*words) is

@@ -49,7 +49,8 @@ def test_constants_and_error_reporting_without_gpu():
     rc = lib.hc_decode_attn(2, None, None, None, None, None, None, 4, 0, 1.0, None, None, None, None, 0, 1, 4, None)
     assert rc == _lib.HC_ERR_INVALID
     assert b"group" in lib.hc_last_error()
-    rc = lib.hc_gather_store(2, None, None, 0, None, 128, 16, None, None, None, None, None, None, None, 1, 4, None, None)
+    rc = lib.hc_gather_store(2, None, None, 0, None, 128, 16, None, None, None, None, None, None, None, 1, 4, None, None,
+                             None)
     assert rc == _lib.HC_ERR_INVALID
     assert b"null pointer" in lib.hc_last_error()
     assert lib.hc_decode_num_parts(None, 1, 4) == -1
