@@ -77,6 +77,20 @@ __device__ __forceinline__ Elem<float>::vec8 load8<float>(const float* p) {
   return r;
 }
 
+// Streaming variant of load8 for data read once per launch (KV tiles): the
+// nontemporal hint keeps the stream from displacing reusable lines in L2.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::vec8 load8_stream(const T* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const typename Elem<T>::vec8*>(p));
+}
+template <>
+__device__ __forceinline__ Elem<float>::vec8 load8_stream<float>(const float* p) {
+  Elem<float>::vec8 r;
+  r.lo = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  r.hi = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p + 4));
+  return r;
+}
+
 // acc += A(16x32) * B(32x16) where each lane supplies 8 k-values of its row
 // (A) / column (B): lane l owns row/col l%16 and k-slots 8*(l/16)+[0..8).
 // For fp32 the same 32-wide contraction is issued as 8 x (16x16x4) MFMAs in
@@ -116,6 +130,17 @@ template <typename T>
 __device__ __forceinline__ typename Elem<T>::vec8 zero8() {
   float z[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   return pack8<T>(z);
+}
+
+// Element e of a lane vector as fp32 (e must be a compile-time constant
+// after unrolling, so the vector stays in registers).
+template <typename T>
+__device__ __forceinline__ float vec8_at(const typename Elem<T>::vec8& v, int e) {
+  return Elem<T>::to_f32(v[e]);
+}
+template <>
+__device__ __forceinline__ float vec8_at<float>(const Elem<float>::vec8& v, int e) {
+  return e < 4 ? v.lo[e] : v.hi[e - 4];
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -12,33 +12,57 @@
 //  * decode_partial_kernel: every row (batch, kv-head) is cut into chunks of
 //    NWAVES*tiles_per_wave 32-token tiles, one workgroup per chunk, rows
 //    visited in row_order (longest first).  Each wave streams its run of
-//    tiles with one-tile prefetch, computes S = K.Q^T on the matrix cores
+//    tiles with nontemporal loads, computes S = K.Q^T on the matrix cores
 //    (the G query heads of the group share every K load), an online base-2
 //    softmax and O^T += V^T.P^T on the matrix cores; the waves' states are
 //    combined through LDS into one (m, l, O) partial per workgroup.
 //  * decode_merge_kernel: one workgroup per (row, query, 32-channel slice)
 //    folds the row's partials.
-//  * with k_new/v_new the new token is attended at slot len (patched into the
-//    operand registers) and written into the store by the wave owning that
-//    slot; the merge advances row_len by one.
+//  * with k_new/v_new the new token is attended at slot len by the wave
+//    owning that slot (folded into its softmax state after its stored
+//    tiles) and written into the store by that wave; the merge advances
+//    row_len by one.
 #include "hc_common.h"
 #include "hc_internal.h"
 
 namespace hc {
 
 struct ChunkLoc {
-  int row;      // store row
-  int chunk;    // chunk index inside the row
-  int len;      // tokens attended (stored length, +1 with a fused append)
-  int nparts;   // chunks of the row
-  int64_t p0;   // global part index of the row's first chunk
-  int64_t total;  // chunks of all rows
+  int row;        // store row
+  int chunk;      // chunk index inside the row
+  int len;        // tokens attended (stored length, +1 with a fused append)
+  int nparts;     // chunks of the row
+  int p0;         // global part index of the row's first chunk
+  int total;      // chunks of all rows
+  int64_t tiles;  // first tile of the row in the store (row_tile_off[row])
   bool found;
 };
 
-// Map a workgroup index onto (row, chunk) from the device-resident lengths.
+__device__ __forceinline__ int chunks_of(int len, int chunk_tiles) {
+  const int nt = (len + HC_TILE - 1) / HC_TILE;
+  // An empty row still gets one workgroup, which writes its zero output.
+  return nt > 0 ? (nt + chunk_tiles - 1) / chunk_tiles : 1;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  return v;
+}
+
+// Map workgroup index b onto (row, chunk) from the device-resident lengths.
+// Each wave scans the rows 64 at a time, one row per lane: the per-row loads
+// of a block are issued together (for up to 64 rows, row_order, row_len and
+// row_tile_off are all read in one round trip and the order is applied by a
+// lane permute), so locating costs one or two memory latencies, not one per
+// row.
 __device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len, const int* __restrict__ row_order,
-                                                 int rows, int extra, int chunk_tiles, int64_t b) {
+                                                 const int64_t* __restrict__ row_tile_off, int rows, int extra,
+                                                 int chunk_tiles, int b) {
+  const int lane = threadIdx.x & 63;
   ChunkLoc c;
   c.found = false;
   c.row = 0;
@@ -46,63 +70,163 @@ __device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len
   c.len = 0;
   c.nparts = 0;
   c.p0 = 0;
-  int64_t acc = 0;
-  for (int k = 0; k < rows; ++k) {
-    const int r = row_order ? row_order[k] : k;
-    const int l = row_len[r] + extra;
-    const int64_t nt = (l + HC_TILE - 1) / HC_TILE;
-    // An empty row still gets one workgroup, which writes its zero output.
-    const int64_t nc = nt > 0 ? (nt + chunk_tiles - 1) / chunk_tiles : 1;
-    if (!c.found && b < acc + nc) {
+  c.tiles = 0;
+  int acc = 0;
+  if (rows <= 64) {
+    const bool live = lane < rows;
+    const int own_len = live ? row_len[lane] : 0;
+    const int64_t own_off = live ? row_tile_off[lane] : 0;
+    const int r = live ? (row_order ? row_order[lane] : lane) : 0;
+    const int l = __shfl(own_len, r, 64) + extra;
+    const int nc = live ? chunks_of(l, chunk_tiles) : 0;
+    const int incl = wave_inclusive_scan(nc, lane);
+    const int excl = incl - nc;
+    const uint64_t hit = __ballot(live && b >= excl && b < incl);
+    acc = __shfl(incl, 63, 64);
+    if (hit) {
+      const int src = __builtin_ctzll(hit);
       c.found = true;
-      c.row = r;
-      c.chunk = (int)(b - acc);
-      c.len = l;
-      c.nparts = (int)nc;
-      c.p0 = acc;
+      c.row = __shfl(r, src, 64);
+      c.len = __shfl(l, src, 64);
+      c.nparts = __shfl(nc, src, 64);
+      c.p0 = __shfl(excl, src, 64);
+      c.chunk = b - c.p0;
+      c.tiles = __shfl(own_off, c.row, 64);
     }
-    acc += nc;
+  } else {
+    for (int base = 0; base < rows; base += 64) {
+      const int k = base + lane;
+      const bool live = k < rows;
+      const int r = live ? (row_order ? row_order[k] : k) : 0;
+      const int l = live ? row_len[r] + extra : 0;
+      const int nc = live ? chunks_of(l, chunk_tiles) : 0;
+      const int incl = acc + wave_inclusive_scan(nc, lane);
+      const int excl = incl - nc;
+      const uint64_t hit = __ballot(live && b >= excl && b < incl);
+      if (hit && !c.found) {
+        const int src = __builtin_ctzll(hit);
+        c.found = true;
+        c.row = __shfl(r, src, 64);
+        c.len = __shfl(l, src, 64);
+        c.nparts = __shfl(nc, src, 64);
+        c.p0 = __shfl(excl, src, 64);
+        c.chunk = b - c.p0;
+      }
+      acc = __shfl(incl, 63, 64);
+    }
+    if (c.found) c.tiles = row_tile_off[c.row];
   }
   c.total = acc;
   return c;
 }
 
-// Overwrite token `tn` of the tile held in (kr, vr) with the new token.
-// Every register index is a compile-time constant (value selects only), so
-// the operand arrays stay in registers.
+// Request the K and V parts of tile t (16 wave-loads of 1 KB, contiguous).
 template <typename T>
-__device__ __forceinline__ void patch_new_token(typename Elem<T>::vec8 (&kr)[8], typename Elem<T>::vec8 (&vr)[8],
-                                                const T* __restrict__ kn, const T* __restrict__ vn, int tn, int lane) {
-  typedef typename Elem<T>::vec8 vec8;
-  const int m = lane & 15, g = lane >> 4;
-  if (m == (tn & 15)) {
-    const bool lo = tn < 16;
+__device__ __forceinline__ void load_tile(typename Elem<T>::vec8 (&kr)[8], typename Elem<T>::vec8 (&vr)[8],
+                                          const T* __restrict__ kb, const T* __restrict__ vb, int t) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const vec8 x = load8<T>(kn + 32 * s + 8 * g);
-      const vec8 a = kr[s], b = kr[4 + s];
-      kr[s] = lo ? x : a;
-      kr[4 + s] = lo ? b : x;
-    }
+  for (int x = 0; x < 8; ++x) {
+    kr[x] = load8_stream<T>(kb + (int64_t)t * HC_TILE_ELEMS + x * 512);
+    vr[x] = load8_stream<T>(vb + (int64_t)t * HC_TILE_ELEMS + x * 512);
   }
-  if (g == ((tn & 15) >> 2)) {
-    const int i = 4 * (tn >> 4) + (tn & 3);
+}
+
+// Attend the resident tile t: S^T = K.Q^T on the matrix cores, mask of the
+// tokens at or beyond len, online base-2 softmax, O^T += V^T.P^T.  Lane
+// state: m_run is the running maximum of query n = lane%16 (scaled, base 2),
+// l_run this lane's share of the running sum, o[mt][j] = O^T[16mt+4g+j][n].
+template <typename T>
+__device__ __forceinline__ void attend_tile(typename Elem<T>::vec8 (&kr)[8], typename Elem<T>::vec8 (&vr)[8],
+                                            const typename Elem<T>::vec8 (&qreg)[4], int t, int len, int lane,
+                                            float scale_log2, float& m_run, float& l_run, f32x4 (&o)[8]) {
+  typedef typename Elem<T>::vec8 vec8;
+  const int g = lane >> 4;
+  const int tok0 = t * HC_TILE;
+  // S^T(token, query) for the two 16-token halves of the tile.
+  f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    s0 = mma_16x16x32(kr[s], qreg[s], s0);
+    s1 = mma_16x16x32(kr[4 + s], qreg[s], s1);
+  }
+  // Element e of this lane holds token 16*(e/4) + 4g + e%4 of the tile.
+  float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+  if (tok0 + HC_TILE > len) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
+      if (tok >= len) sv[e] = -INFINITY;
+    }
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) {
-      const T x = vn[16 * mt + m];
-      if constexpr (sizeof(T) == 4) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vr[mt].lo[e] = (e == i) ? x : vr[mt].lo[e];
-          vr[mt].hi[e] = (e + 4 == i) ? x : vr[mt].hi[e];
+      for (int e = 0; e < 8; ++e) {
+        const int tok = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
+        if (tok >= len) {
+          if constexpr (sizeof(T) == 4) {
+            if (e < 4) vr[mt].lo[e] = 0.f; else vr[mt].hi[e - 4] = 0.f;
+          } else {
+            vr[mt][e] = Elem<T>::from_f32(0.f);
+          }
         }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) vr[mt][e] = (e == i) ? x : vr[mt][e];
       }
     }
   }
+  float mx = sv[0];
+#pragma unroll
+  for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
+  mx = wave_max_xor(mx, 16);
+  mx = wave_max_xor(mx, 32);
+  const float m_new = fmaxf(m_run, mx * scale_log2);
+  const float alpha = fast_exp2(m_run - m_new);
+  float p[8];
+  float psum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    p[e] = fast_exp2(fmaf(sv[e], scale_log2, -m_new));
+    psum += p[e];
+  }
+  l_run = fmaf(l_run, alpha, psum);
+  m_run = m_new;
+  vec8 pb = pack8<T>(p);
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt) {
+    o[mt] = o[mt] * alpha;
+    o[mt] = mma_16x16x32(vr[mt], pb, o[mt]);
+  }
 }
+
+// Fold the appended token (k_new, v_new of this row) into the lane state of
+// attend_tile.  The score is a VALU dot product of the operand registers
+// (exact bf16/f16 products, fp32 sums), reduced over the four k-groups; P is
+// rounded to T as on the matrix-core path.
+template <typename T>
+__device__ __forceinline__ void attend_new_token(const typename Elem<T>::vec8 (&qreg)[4], const T* __restrict__ kn,
+                                                 const T* __restrict__ vn, int lane, float scale_log2, float& m_run,
+                                                 float& l_run, f32x4 (&o)[8]) {
+  const int g = lane >> 4;
+  float dot = 0.f;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const typename Elem<T>::vec8 k8 = load8<T>(kn + 32 * s + 8 * g);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dot = fmaf(vec8_at<T>(qreg[s], e), vec8_at<T>(k8, e), dot);
+  }
+  dot += __shfl_xor(dot, 16, 64);
+  dot += __shfl_xor(dot, 32, 64);
+  const float sc = dot * scale_log2;
+  const float m_new = fmaxf(m_run, sc);
+  const float alpha = fast_exp2(m_run - m_new);
+  const float p = Elem<T>::to_f32(Elem<T>::from_f32(fast_exp2(sc - m_new)));
+  l_run = fmaf(l_run, alpha, g == 0 ? p : 0.f);
+  m_run = m_new;
+#pragma unroll
+  for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[mt][j] = fmaf(p, Elem<T>::to_f32(vn[16 * mt + 4 * g + j]), o[mt][j] * alpha);
+}
+
+constexpr int kOPitch = HC_HEAD_DIM + 4;
 
 template <typename T, int NWAVES>
 __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_partial_kernel(
@@ -114,7 +238,8 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
   constexpr int NT = NWAVES * 64;
   const int chunk_tiles = NWAVES * tiles_per_wave;
   const bool fused_append = (k_new != nullptr);
-  const ChunkLoc loc = locate_chunk(row_len, row_order, rows, fused_append ? 1 : 0, chunk_tiles, blockIdx.x);
+  const ChunkLoc loc =
+      locate_chunk(row_len, row_order, row_tile_off, rows, fused_append ? 1 : 0, chunk_tiles, (int)blockIdx.x);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -123,10 +248,12 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
 
   __shared__ float s_m[NWAVES][16];
   __shared__ float s_l[NWAVES][16];
-  __shared__ float s_o[NWAVES][16][HC_HEAD_DIM + 4];
+  // Per-wave O^T of the G queries, [wave][query][channel], pitch kOPitch;
+  // sized by the launch for G queries.
+  extern __shared__ float s_o[];
 
   if (!loc.found) return;
-  if (loc.total > (int64_t)gridDim.x) {
+  if (loc.total > (int)gridDim.x) {
     // The launch grid is smaller than the device lengths need: flag the row
     // so the merge writes NaN instead of a silently partial result.
     if (threadIdx.x == 0 && loc.chunk == 0) {
@@ -154,104 +281,55 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
     const int ntiles = (len + HC_TILE - 1) / HC_TILE;
     const int t_begin = loc.chunk * chunk_tiles + wave * tiles_per_wave;
     const int t_end = min(t_begin + tiles_per_wave, ntiles);
+    // Stored tokens only: the appended token is folded in separately.
+    const int len_st = fused_append ? len - 1 : len;
+    const int t_end_st = min(t_end, (len_st + HC_TILE - 1) / HC_TILE);
 
     float m_run = -INFINITY, l_run = 0.f;
     f32x4 o[8];
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    if (t_begin < t_end) {
-      const int64_t row_base = row_tile_off[row] * (int64_t)HC_TILE_ELEMS;
+    const int64_t row_base = loc.tiles * (int64_t)HC_TILE_ELEMS;
+    if (t_begin < t_end_st) {
       const T* kb = kstore + row_base + lane * 8;
       const T* vb = vstore + row_base + lane * 8;
-      vec8 kr[8], vr[8];
-#pragma unroll
-      for (int x = 0; x < 8; ++x) {
-        kr[x] = load8<T>(kb + (int64_t)t_begin * HC_TILE_ELEMS + x * 512);
-        vr[x] = load8<T>(vb + (int64_t)t_begin * HC_TILE_ELEMS + x * 512);
+      // Two tile buffers: the next tile's 16 wave-loads are in flight while
+      // the current one is consumed.  The buffers alternate by name (no
+      // register copies) and the loads inside the paired loop are
+      // unconditional, so every wait leaves the younger tile outstanding.
+      // Scheduling barriers keep each request between the two consumers
+      // (hoisting both requests would hold three tiles and spill).
+      vec8 kA[8], vA[8], kB[8], vB[8];
+      load_tile<T>(kA, vA, kb, vb, t_begin);
+      int t = t_begin;
+      for (; t + 2 < t_end_st; t += 2) {
+        load_tile<T>(kB, vB, kb, vb, t + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        attend_tile<T>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o);
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile<T>(kA, vA, kb, vb, t + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        attend_tile<T>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o);
+        __builtin_amdgcn_sched_barrier(0);
       }
-      for (int t = t_begin; t < t_end; ++t) {
-        vec8 kn_[8], vn_[8];
-        const bool more = (t + 1 < t_end);
-        if (more) {
-#pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            kn_[x] = load8<T>(kb + (int64_t)(t + 1) * HC_TILE_ELEMS + x * 512);
-            vn_[x] = load8<T>(vb + (int64_t)(t + 1) * HC_TILE_ELEMS + x * 512);
-          }
-        }
-        const int tok0 = t * HC_TILE;
-        if (fused_append && new_pos >= tok0 && new_pos < tok0 + HC_TILE)
-          patch_new_token<T>(kr, vr, kn, vn, new_pos - tok0, lane);
-        // S^T(token, query) for the two 16-token halves of the tile.
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          s0 = mma_16x16x32(kr[s], qreg[s], s0);
-          s1 = mma_16x16x32(kr[4 + s], qreg[s], s1);
-        }
-        // Element e of this lane holds token 16*(e/4) + 4g + e%4 of the tile.
-        float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-        if (tok0 + HC_TILE > len) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int tok = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
-            if (tok >= len) sv[e] = -INFINITY;
-          }
-#pragma unroll
-          for (int mt = 0; mt < 8; ++mt) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int tok = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
-              if (tok >= len) {
-                if constexpr (sizeof(T) == 4) {
-                  if (e < 4) vr[mt].lo[e] = 0.f; else vr[mt].hi[e - 4] = 0.f;
-                } else {
-                  vr[mt][e] = Elem<T>::from_f32(0.f);
-                }
-              }
-            }
-          }
-        }
-        float mx = sv[0];
-#pragma unroll
-        for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
-        mx = wave_max_xor(mx, 16);
-        mx = wave_max_xor(mx, 32);
-        const float m_new = fmaxf(m_run, mx * scale_log2);
-        const float alpha = fast_exp2(m_run - m_new);
-        float p[8];
-        float psum = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          p[e] = fast_exp2(fmaf(sv[e], scale_log2, -m_new));
-          psum += p[e];
-        }
-        l_run = fmaf(l_run, alpha, psum);
-        m_run = m_new;
-        vec8 pb = pack8<T>(p);
-#pragma unroll
-        for (int mt = 0; mt < 8; ++mt) {
-          o[mt] = o[mt] * alpha;
-          o[mt] = mma_16x16x32(vr[mt], pb, o[mt]);
-        }
-        if (more) {
-#pragma unroll
-          for (int x = 0; x < 8; ++x) {
-            kr[x] = kn_[x];
-            vr[x] = vn_[x];
-          }
-        }
+      if (t + 1 < t_end_st) {
+        load_tile<T>(kB, vB, kb, vb, t + 1);
+        attend_tile<T>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o);
+        attend_tile<T>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o);
+      } else {
+        attend_tile<T>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o);
       }
-      // The wave that attended the new token also stores it (no other
-      // workgroup of this launch reads that slot).
-      if (fused_append && new_pos >= t_begin * HC_TILE && new_pos < t_end * HC_TILE) {
-        const int64_t tb = row_base + (int64_t)(new_pos / HC_TILE) * HC_TILE_ELEMS;
-        const int tn = new_pos % HC_TILE;
-        for (int d = lane; d < HC_HEAD_DIM; d += 64) {
-          kstore[tb + k_tile_offset(tn, d)] = kn[d];
-          vstore[tb + v_tile_offset(tn, d)] = vn[d];
-        }
+    }
+    // The wave whose tile range holds the new slot attends the new token and
+    // stores it (no other workgroup of this launch reads that slot).
+    if (fused_append && new_pos >= t_begin * HC_TILE && new_pos < t_end * HC_TILE) {
+      attend_new_token<T>(qreg, kn, vn, lane, scale_log2, m_run, l_run, o);
+      const int64_t tb = row_base + (int64_t)(new_pos / HC_TILE) * HC_TILE_ELEMS;
+      const int tn = new_pos % HC_TILE;
+      for (int d = lane; d < HC_HEAD_DIM; d += 64) {
+        kstore[tb + k_tile_offset(tn, d)] = kn[d];
+        vstore[tb + v_tile_offset(tn, d)] = vn[d];
       }
     }
     l_run += __shfl_xor(l_run, 16, 64);
@@ -266,7 +344,7 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s_o[wave][n][16 * mt + 4 * g + j] = o[mt][j];
+        for (int j = 0; j < 4; ++j) s_o[(wave * G + n) * kOPitch + 16 * mt + 4 * g + j] = o[mt][j];
     }
     __syncthreads();
 
@@ -280,7 +358,7 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
 #pragma unroll
       for (int w = 0; w < NWAVES; ++w) {
         const float f = (s_m[w][qq] == -INFINITY) ? 0.f : fast_exp2(s_m[w][qq] - M);
-        acc = fmaf(s_o[w][qq][d], f, acc);
+        acc = fmaf(s_o[(w * G + qq) * kOPitch + d], f, acc);
         lsum = fmaf(s_l[w][qq], f, lsum);
       }
       part_o[(part * G + qq) * HC_HEAD_DIM + d] = acc;
@@ -430,8 +508,9 @@ static int launch_decode(const void* q, void* kstore, void* vstore, const int64_
   float* part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + workspace_head(rows));
   float* part_o = part_ml + (size_t)grid_parts * G * 2;
   const float scale_log2 = scale * 1.4426950408889634f;
+  const size_t lds_o = (size_t)kDecodeWaves * G * kOPitch * sizeof(float);
   hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves>), dim3((unsigned)grid_parts), dim3(kDecodeWaves * 64),
-                     0, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off, row_len, row_order, rows, G,
+                     lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off, row_len, row_order, rows, G,
                      scale_log2, tiles_per_wave, (const T*)k_new, (const T*)v_new, part_o, part_ml, row_info);
   int rc = check_launch("hc_decode_attn(partial)");
   if (rc) return rc;

@@ -103,7 +103,10 @@ def test_matches_torch_sdpa_fp32(dev):
 
 @pytest.mark.parametrize("dt", ["bf16", "f32"])
 def test_fused_append_matches_oracle_over_steps(dev, dt):
-    """attend(k_new=...) == append then attend, step after step (counters reset)."""
+    """attend(k_new=...) matches the oracle and append-then-attend step after
+    step (the fused path folds the new token in after the stored tiles, so
+    the two agree to the attention tolerance, not bitwise); the stores end
+    up bit-identical."""
     lens = [0, 1, 31, 32, 63, 100, 1023, 1024, 2500, 4096]
     steps, G = 6, 4
     tdt = TORCH_DT[dt]
@@ -130,7 +133,8 @@ def test_fused_append_matches_oracle_over_steps(dev, dt):
             hist_v[r] = np.concatenate([hist_v[r], as_np(vn[r:r + 1])])
         ref = O.decode_attention(as_np(q), hist_k, hist_v, scale)
         assert np.abs(as_np(ob) - ref).max() <= ATTN_TOL[dt]
-        assert torch.equal(oa, ob), f"step {s}: fused append differs from append+attend"
+        assert np.abs(as_np(oa) - ref).max() <= ATTN_TOL[dt]
+        assert (oa.float() - ob.float()).abs().max().item() <= ATTN_TOL[dt], f"step {s}: fused vs append+attend"
     assert b.row_len.tolist() == [L + steps for L in lens]
     assert b.host_len.tolist() == [L + steps for L in lens]
     for r in range(len(lens)):
