@@ -30,7 +30,7 @@ def parse():
     p.add_argument("--ctx", type=int, default=131072)
     p.add_argument("--layers", type=int, default=32)
     p.add_argument("--ratio", type=float, default=0.5)
-    p.add_argument("--tiles-per-wave", type=int, default=None)
+    p.add_argument("--chunk-tiles", type=int, default=None, help="tiles per workgroup (default: one-round auto)")
     p.add_argument("--seed", type=int, default=1002)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -202,7 +202,7 @@ def main():
         st.set_lengths(lens)
         stores.append(st)
         budgets.append(lens)
-    tpw = args.tiles_per_wave or ops.DEFAULT_TILES_PER_WAVE
+    chunk = args.chunk_tiles
     q = torch.randn((args.layers, Hkv, G, D), device=dev).to(torch.bfloat16)
     kn = torch.randn((args.layers, Hkv, D), device=dev).to(torch.bfloat16)
     vn = torch.randn((args.layers, Hkv, D), device=dev).to(torch.bfloat16)
@@ -214,9 +214,9 @@ def main():
         for layer, st in enumerate(stores):
             if args.unfused_append:
                 st.append(kn[layer], vn[layer])
-                st.attend(q[layer], scale, out=outs[layer], tiles_per_wave=tpw)
+                st.attend(q[layer], scale, out=outs[layer], chunk_tiles=chunk)
             else:
-                st.attend(q[layer], scale, out=outs[layer], k_new=kn[layer], v_new=vn[layer], tiles_per_wave=tpw)
+                st.attend(q[layer], scale, out=outs[layer], k_new=kn[layer], v_new=vn[layer], chunk_tiles=chunk)
 
     for _ in range(args.warmup):
         step()
@@ -261,7 +261,7 @@ def main():
         "config": {"workload": f"decode step, Llama-3-8B shape, {L} ctx, ratio {args.ratio}, batch 1, "
                                f"{args.layers} layers, 8 KV rows x GQA 4, head_dim 128",
                    "ctx": L, "layers": args.layers, "kv_heads": Hkv, "q_heads": Hkv * G, "head_dim": D,
-                   "ratio": args.ratio, "batch": 1, "tiles_per_wave": tpw},
+                   "ratio": args.ratio, "batch": 1, "chunk_tiles": chunk or "auto"},
         "us_per_layer": round(us_layer, 3),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -60,7 +60,7 @@ class HeteroCacheConfig:
                  max_gen_len: Optional[int] = 128, decode_step: Optional[int] = 4, pooling: Optional[str] = "avgpool",
                  kernel_size: Optional[int] = 5, num_attn_heads: Optional[int] = 32, num_kv_heads: Optional[int] = 8,
                  num_layers: Optional[int] = 32, retrieval_topk: Optional[int] = None, window_size: int = 1,
-                 round_scores: bool = False, reference_quirks: bool = False, tiles_per_wave: Optional[int] = None):
+                 round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None):
         self.data = data
         self.stable_threshold = stable_threshold
         self.compression_ratio = compression_ratio
@@ -77,7 +77,7 @@ class HeteroCacheConfig:
         self.window_size = window_size
         self.round_scores = round_scores
         self.reference_quirks = reference_quirks
-        self.tiles_per_wave = tiles_per_wave
+        self.chunk_tiles = chunk_tiles
 
 
 def _f32_caps(base, ratios, seq_len):
@@ -125,7 +125,7 @@ class HeteroCache(DynamicCache):
         self.retrieval_topk = getattr(cfg, "retrieval_topk", None)
         self.window_size = int(getattr(cfg, "window_size", 1) or 1)
         self.round_scores = bool(getattr(cfg, "round_scores", False))
-        self.tiles_per_wave = getattr(cfg, "tiles_per_wave", None) or ops.DEFAULT_TILES_PER_WAVE
+        self.chunk_tiles = getattr(cfg, "chunk_tiles", None)
 
         self.stores = [None] * self.num_layers
         self.prefill_topk_set = [None] * self.num_layers
@@ -336,7 +336,7 @@ class HeteroCache(DynamicCache):
         if p is not None:
             kn = p[0].reshape(-1, D)
             vn = p[1].reshape(-1, D)
-        o = store.attend(q, 1.0 / (D ** 0.5), out=out, k_new=kn, v_new=vn, tiles_per_wave=self.tiles_per_wave)
+        o = store.attend(q, 1.0 / (D ** 0.5), out=out, k_new=kn, v_new=vn, chunk_tiles=self.chunk_tiles)
         return o.view(B, 1, Hq * D)
 
     def decode_select(self, query_states, layer_idx):

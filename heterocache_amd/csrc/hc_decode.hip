@@ -10,7 +10,8 @@
 // synchronisation inside a kernel (an agent-scope fence costs an L2
 // write-back per workgroup on a multi-XCD part):
 //  * decode_partial_kernel: every row (batch, kv-head) is cut into chunks of
-//    NWAVES*tiles_per_wave 32-token tiles, one workgroup per chunk, rows
+//    chunk_tiles 32-token tiles, one workgroup per chunk (its NWAVES waves
+//    split the chunk evenly), rows
 //    visited in row_order (longest first).  Each wave streams its run of
 //    tiles with nontemporal loads, computes S = K.Q^T on the matrix cores
 //    (the G query heads of the group share every K load), an online base-2
@@ -22,6 +23,8 @@
 //    owning that slot (folded into its softmax state after its stored
 //    tiles) and written into the store by that wave; the merge advances
 //    row_len by one.
+#include <mutex>
+
 #include "hc_common.h"
 #include "hc_internal.h"
 
@@ -232,11 +235,10 @@ template <typename T, int NWAVES>
 __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_partial_kernel(
     const T* __restrict__ q, T* __restrict__ kstore, T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off,
     const int* __restrict__ row_len, const int* __restrict__ row_order, int rows, int G, float scale_log2,
-    int tiles_per_wave, const T* __restrict__ k_new, const T* __restrict__ v_new, float* __restrict__ part_o,
+    int chunk_tiles, const T* __restrict__ k_new, const T* __restrict__ v_new, float* __restrict__ part_o,
     float* __restrict__ part_ml, int* __restrict__ row_info) {
   typedef typename Elem<T>::vec8 vec8;
   constexpr int NT = NWAVES * 64;
-  const int chunk_tiles = NWAVES * tiles_per_wave;
   const bool fused_append = (k_new != nullptr);
   const ChunkLoc loc =
       locate_chunk(row_len, row_order, row_tile_off, rows, fused_append ? 1 : 0, chunk_tiles, (int)blockIdx.x);
@@ -279,8 +281,9 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
     }
 
     const int ntiles = (len + HC_TILE - 1) / HC_TILE;
-    const int t_begin = loc.chunk * chunk_tiles + wave * tiles_per_wave;
-    const int t_end = min(t_begin + tiles_per_wave, ntiles);
+    const int t0 = loc.chunk * chunk_tiles;
+    const int t_begin = t0 + (wave * chunk_tiles) / NWAVES;
+    const int t_end = min(t0 + ((wave + 1) * chunk_tiles) / NWAVES, ntiles);
     // Stored tokens only: the appended token is folded in separately.
     const int len_st = fused_append ? len - 1 : len;
     const int t_end_st = min(t_end, (len_st + HC_TILE - 1) / HC_TILE);
@@ -471,8 +474,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
 
 constexpr int kDecodeWaves = 4;
 
-int64_t decode_num_parts(const int* host_row_len, int rows, int tiles_per_wave) {
-  const int chunk_tiles = kDecodeWaves * tiles_per_wave;
+int64_t decode_num_parts(const int* host_row_len, int rows, int chunk_tiles) {
   int64_t total = 0;
   for (int r = 0; r < rows; ++r) {
     int64_t nt = (host_row_len[r] + HC_TILE - 1) / HC_TILE;
@@ -495,7 +497,7 @@ size_t decode_workspace_bytes_rows(int rows, int group, int64_t num_parts) {
 template <typename T>
 static int launch_decode(const void* q, void* kstore, void* vstore, const int64_t* row_tile_off, int* row_len,
                          const int* row_order, int rows, int G, float scale, const void* k_new, const void* v_new,
-                         void* out, void* workspace, size_t workspace_bytes, int64_t grid_parts, int tiles_per_wave,
+                         void* out, void* workspace, size_t workspace_bytes, int64_t grid_parts, int chunk_tiles,
                          hipStream_t stream) {
   if (grid_parts < rows)
     return set_error(HC_ERR_INVALID, "hc_decode_attn: num_parts=%lld below the row count %d", (long long)grid_parts,
@@ -511,13 +513,57 @@ static int launch_decode(const void* q, void* kstore, void* vstore, const int64_
   const size_t lds_o = (size_t)kDecodeWaves * G * kOPitch * sizeof(float);
   hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves>), dim3((unsigned)grid_parts), dim3(kDecodeWaves * 64),
                      lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off, row_len, row_order, rows, G,
-                     scale_log2, tiles_per_wave, (const T*)k_new, (const T*)v_new, part_o, part_ml, row_info);
+                     scale_log2, chunk_tiles, (const T*)k_new, (const T*)v_new, part_o, part_ml, row_info);
   int rc = check_launch("hc_decode_attn(partial)");
   if (rc) return rc;
   hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(rows, G, HC_HEAD_DIM / kMergeSlice),
                      dim3(kMergeSlice * kMergeGroups), 0, stream, part_o, part_ml, row_info, G, row_len,
                      k_new ? 1 : 0, (T*)out);
   return check_launch("hc_decode_attn(merge)");
+}
+
+// Workgroups of decode_partial_kernel<T> resident on the current device at
+// once (occupancy per CU x CU count), cached per (device, dtype, group).
+static int decode_slots(int dtype, int G) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -1;
+  static std::mutex mu;
+  static int cache[64][3][17];  // zero = not yet queried
+  std::lock_guard<std::mutex> lock(mu);
+  int& slot = cache[dev][dtype][G];
+  if (slot > 0) return slot;
+  const size_t lds = (size_t)kDecodeWaves * G * kOPitch * sizeof(float);
+  const void* fn = nullptr;
+  switch (dtype) {
+    case HC_DTYPE_BF16: fn = reinterpret_cast<const void*>(decode_partial_kernel<__bf16, kDecodeWaves>); break;
+    case HC_DTYPE_F16: fn = reinterpret_cast<const void*>(decode_partial_kernel<_Float16, kDecodeWaves>); break;
+    default: fn = reinterpret_cast<const void*>(decode_partial_kernel<float, kDecodeWaves>); break;
+  }
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDecodeWaves * 64, lds) != hipSuccess) return -1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return -1;
+  slot = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  return slot;
+}
+
+// Smallest chunk (>= one tile per wave) whose grid fits in one resident
+// round: a second, partly filled round of workgroups leaves HBM idle at the
+// end of the launch, while smaller chunks keep more loads in flight.
+static int decode_auto_chunk(const int* host_row_len, int rows, int slots) {
+  int max_nt = 0;
+  for (int r = 0; r < rows; ++r) max_nt = max(max_nt, (host_row_len[r] + HC_TILE - 1) / HC_TILE);
+  if (max_nt <= kDecodeWaves) return kDecodeWaves;
+  // One part per row already exceeds the resident slots: one chunk per row.
+  if (decode_num_parts(host_row_len, rows, max_nt) > slots) return max_nt;
+  int lo = kDecodeWaves, hi = max_nt;  // parts(chunk) does not increase with chunk
+  while (lo < hi) {
+    const int mid = lo + (hi - lo) / 2;
+    if (decode_num_parts(host_row_len, rows, mid) <= slots)
+      hi = mid;
+    else
+      lo = mid + 1;
+  }
+  return lo;
 }
 
 }  // namespace hc
@@ -528,20 +574,33 @@ extern "C" size_t hc_decode_workspace_size(int rows, int group, int64_t num_part
   return decode_workspace_bytes_rows(rows, group, num_parts);
 }
 
-extern "C" int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, int tiles_per_wave) {
-  if (!host_row_len || rows < 0 || tiles_per_wave <= 0) return -1;
-  return decode_num_parts(host_row_len, rows, tiles_per_wave);
+extern "C" int hc_decode_chunk_tiles(int dtype, const int32_t* host_row_len, int rows, int group) {
+  clear_error();
+  if (dtype != HC_DTYPE_BF16 && dtype != HC_DTYPE_F16 && dtype != HC_DTYPE_F32)
+    return set_error(HC_ERR_INVALID, "hc_decode_chunk_tiles: unknown dtype %d", dtype);
+  if (rows < 0 || group < 1 || group > 16 || (rows > 0 && !host_row_len))
+    return set_error(HC_ERR_INVALID, "hc_decode_chunk_tiles: rows=%d group=%d", rows, group);
+  for (int r = 0; r < rows; ++r)
+    if (host_row_len[r] < 0) return set_error(HC_ERR_INVALID, "hc_decode_chunk_tiles: negative length at row %d", r);
+  const int slots = decode_slots(dtype, group);
+  if (slots <= 0) return set_error(HC_ERR_HIP, "hc_decode_chunk_tiles: occupancy query failed");
+  return decode_auto_chunk(host_row_len, rows, slots);
+}
+
+extern "C" int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, int chunk_tiles) {
+  if (!host_row_len || rows < 0 || chunk_tiles <= 0) return -1;
+  return decode_num_parts(host_row_len, rows, chunk_tiles);
 }
 
 extern "C" int hc_decode_attn(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
                               int32_t* row_len, const int32_t* row_order, int rows, int group, float scale,
                               const void* k_new, const void* v_new, void* out, void* workspace,
-                              size_t workspace_bytes, int64_t num_parts, int tiles_per_wave, void* stream) {
+                              size_t workspace_bytes, int64_t num_parts, int chunk_tiles, void* stream) {
   clear_error();
   if (rows < 0 || group < 1 || group > 16)
     return set_error(HC_ERR_INVALID, "hc_decode_attn: rows=%d group=%d (group must be 1..16)", rows, group);
-  if (tiles_per_wave < 1 || tiles_per_wave > 4096)
-    return set_error(HC_ERR_INVALID, "hc_decode_attn: tiles_per_wave=%d out of range", tiles_per_wave);
+  if (chunk_tiles < 1 || chunk_tiles > (1 << 22))
+    return set_error(HC_ERR_INVALID, "hc_decode_attn: chunk_tiles=%d out of range", chunk_tiles);
   if (rows == 0) return HC_OK;
   if (!q || !kstore || !vstore || !row_tile_off || !row_len || !out)
     return set_error(HC_ERR_INVALID, "hc_decode_attn: null pointer argument");
@@ -551,13 +610,13 @@ extern "C" int hc_decode_attn(int dtype, const void* q, void* kstore, void* vsto
   switch (dtype) {
     case HC_DTYPE_BF16:
       return launch_decode<__bf16>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
-                                   v_new, out, workspace, workspace_bytes, num_parts, tiles_per_wave, s);
+                                   v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, s);
     case HC_DTYPE_F16:
       return launch_decode<_Float16>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
-                                     v_new, out, workspace, workspace_bytes, num_parts, tiles_per_wave, s);
+                                     v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, s);
     case HC_DTYPE_F32:
       return launch_decode<float>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
-                                  v_new, out, workspace, workspace_bytes, num_parts, tiles_per_wave, s);
+                                  v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, s);
     default:
       return set_error(HC_ERR_INVALID, "hc_decode_attn: unknown dtype %d", dtype);
   }

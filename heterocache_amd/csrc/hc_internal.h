@@ -21,6 +21,6 @@ inline int check_launch(const char* what) {
 }
 
 size_t decode_workspace_bytes_rows(int rows, int group, int64_t num_parts);
-int64_t decode_num_parts(const int* host_row_len, int rows, int tiles_per_wave);
+int64_t decode_num_parts(const int* host_row_len, int rows, int chunk_tiles);
 
 }  // namespace hc

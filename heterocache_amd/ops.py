@@ -16,8 +16,6 @@ TILE = 32
 
 _DTYPES = {torch.float32: _lib.HC_DTYPE_F32, torch.float16: _lib.HC_DTYPE_F16, torch.bfloat16: _lib.HC_DTYPE_BF16}
 
-DEFAULT_TILES_PER_WAVE = 4
-
 
 def dtype_code(dt):
     try:
@@ -69,21 +67,35 @@ WORKSPACE = Workspace()
 SELECT_HIST = Workspace()
 
 
-def decode_num_parts(host_row_len, tiles_per_wave=DEFAULT_TILES_PER_WAVE):
+def decode_num_parts(host_row_len, chunk_tiles):
+    """Workgroups of one decode launch: chunks of chunk_tiles 32-token tiles
+    per row (an empty row still takes one)."""
     lens = np.ascontiguousarray(host_row_len, dtype=np.int32)
-    n = _lib.load().hc_decode_num_parts(lens.ctypes.data_as(ctypes.c_void_p), len(lens), tiles_per_wave)
+    n = _lib.load().hc_decode_num_parts(lens.ctypes.data_as(ctypes.c_void_p), len(lens), int(chunk_tiles))
     if n < 0:
         raise ValueError("bad arguments to hc_decode_num_parts")
     return n
 
 
+def decode_chunk_tiles(host_row_len, group, dtype):
+    """The chunk size whose grid fills the current device in one resident
+    round for these lengths (hc_decode_chunk_tiles)."""
+    lens = np.ascontiguousarray(host_row_len, dtype=np.int32)
+    n = _lib.load().hc_decode_chunk_tiles(dtype_code(dtype), lens.ctypes.data_as(ctypes.c_void_p), len(lens),
+                                          int(group))
+    _lib.check(min(n, 0))
+    return n
+
+
 def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, out=None, row_order=None,
-                k_new=None, v_new=None, tiles_per_wave=DEFAULT_TILES_PER_WAVE, stream=None, workspace=None):
+                k_new=None, v_new=None, chunk_tiles=None, stream=None, workspace=None):
     """out[r, g] = softmax(scale * q[r, g] . K_r^T) V_r over row_len[r] tokens.
 
     q: [rows, G, 128]; host_row_len: host copy of the lengths (sizes the grid).
     With k_new/v_new [rows, 128] the new token is appended and attended in the
     same launch; row_len advances by one (the caller advances its mirror).
+    chunk_tiles: tiles per workgroup; None picks the one-round chunk for
+    these lengths.
     """
     lib = _lib.load()
     _require_cuda(q, kstore, vstore, row_tile_off, row_len, row_order, k_new, v_new)
@@ -111,12 +123,14 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
     q = q.contiguous()
     if out is None:
         out = torch.empty_like(q)
-    nparts = decode_num_parts(host_row_len, tiles_per_wave)
+    if chunk_tiles is None:
+        chunk_tiles = decode_chunk_tiles(host_row_len, G, q.dtype)
+    nparts = decode_num_parts(host_row_len, chunk_tiles)
     nbytes = lib.hc_decode_workspace_size(rows, G, nparts)
     ws = workspace if workspace is not None else WORKSPACE.get(q.device, nbytes)
     _lib.check(lib.hc_decode_attn(dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
                                   _ptr(row_len), _ptr(row_order), rows, G, float(scale), _ptr(k_new), _ptr(v_new),
-                                  _ptr(out), _ptr(ws), ws.numel(), nparts, tiles_per_wave, _stream(stream)))
+                                  _ptr(out), _ptr(ws), ws.numel(), nparts, int(chunk_tiles), _stream(stream)))
     return out
 
 

@@ -176,7 +176,7 @@ class KVStore:
             raise ValueError("read past a row's capacity")
         return ops.store_read(self.k, self.v, self.row_tile_off, rows, count)
 
-    def attend(self, q, scale, out=None, k_new=None, v_new=None, tiles_per_wave=ops.DEFAULT_TILES_PER_WAVE,
+    def attend(self, q, scale, out=None, k_new=None, v_new=None, chunk_tiles=None,
                stream=None):
         """Decode attention of q [rows, G, 128] over every row's tokens.
 
@@ -188,7 +188,7 @@ class KVStore:
             full = np.nonzero(self.host_len + 1 > self.host_cap)[0].tolist()
             raise RuntimeError(f"KV store OOM: rows {full} are at capacity")
         out = ops.decode_attn(q, self.k, self.v, self.row_tile_off, self.row_len, self.host_len, scale, out=out,
-                              row_order=self.row_order, k_new=k_new, v_new=v_new, tiles_per_wave=tiles_per_wave,
+                              row_order=self.row_order, k_new=k_new, v_new=v_new, chunk_tiles=chunk_tiles,
                               stream=stream)
         if k_new is not None:
             self.host_len += 1

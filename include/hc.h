@@ -57,18 +57,30 @@ int hc_head_dim(void);
  * is attended at slot row_len[r], stored there, and every row_len advances by
  * one when the launch completes (the append of heterocache/cache_utils.py:
  * 970-1005 and the attention in one launch).
- * num_parts: hc_decode_num_parts() of the lengths the launch attends
- * (row_len, +1 with k_new).  workspace: at least
- * hc_decode_workspace_size(rows, group, num_parts) bytes, zero-filled before
- * its first use; each completed launch leaves its counters at zero again, so
- * one workspace serves any sequence of launches on one stream (launches that
- * overlap in time need separate workspaces).
+ * chunk_tiles: 32-token tiles per workgroup (each row is cut into chunks of
+ * this many tiles; the 4 waves of a workgroup split a chunk evenly);
+ * hc_decode_chunk_tiles() picks the value that fills the device in one
+ * resident round for the given lengths.
+ * num_parts: hc_decode_num_parts(lengths, rows, chunk_tiles) of the lengths
+ * the launch attends (row_len, +1 with k_new); the grid it sizes must cover
+ * the device lengths (rows whose chunks fall outside it return NaN).
+ * workspace: at least hc_decode_workspace_size(rows, group, num_parts) bytes;
+ * every field is written before it is read within one call, so it needs no
+ * initialisation, and one workspace serves any sequence of launches on one
+ * stream (launches that overlap in time need separate workspaces).
  */
 int hc_decode_attn(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off, int32_t* row_len,
                    const int32_t* row_order, int rows, int group, float scale, const void* k_new, const void* v_new,
-                   void* out, void* workspace, size_t workspace_bytes, int64_t num_parts, int tiles_per_wave,
+                   void* out, void* workspace, size_t workspace_bytes, int64_t num_parts, int chunk_tiles,
                    void* stream);
-int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, int tiles_per_wave);
+/* Workgroups (chunks) of one hc_decode_attn launch over these lengths. */
+int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, int chunk_tiles);
+/* chunk_tiles for hc_decode_attn: the smallest chunk (at least 4 tiles)
+ * whose grid fits the current device's resident workgroup slots for this
+ * dtype and group (one chunk per row when even that does not fit); negative
+ * hc_status on error.  No counterpart in the reference (flash-attn chooses
+ * its split internally). */
+int hc_decode_chunk_tiles(int dtype, const int32_t* host_row_len, int rows, int group);
 size_t hc_decode_workspace_size(int rows, int group, int64_t num_parts);
 
 /*

@@ -60,7 +60,8 @@ def test_num_parts_matches_chunking():
     if not os.path.exists(_lib.LIB_PATH):
         pytest.skip("libhc.so not built")
     from heterocache_amd import ops
-    # 4 waves x tiles_per_wave tiles of 32 tokens per part; an empty row still
-    # takes one part (it writes the row's zero output).
-    assert ops.decode_num_parts([0, 1, 512, 513], tiles_per_wave=4) == 1 + 1 + 1 + 2
-    assert ops.decode_num_parts([131072], tiles_per_wave=8) == 131072 // 1024
+    # chunk_tiles tiles of 32 tokens per part; an empty row still takes one
+    # part (it writes the row's zero output).
+    assert ops.decode_num_parts([0, 1, 512, 513], chunk_tiles=16) == 1 + 1 + 1 + 2
+    assert ops.decode_num_parts([131072], chunk_tiles=32) == 131072 // 1024
+    assert ops.decode_num_parts([100, 4097], chunk_tiles=5) == 1 + 26

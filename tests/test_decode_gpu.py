@@ -2,6 +2,7 @@
 
 Parity bar: max-abs <= 2e-2 (bf16), 1e-2 (fp16), 1e-4 (fp32).
 """
+import ctypes
 import math
 
 import numpy as np
@@ -15,7 +16,7 @@ from tests.gpu_util import ATTN_TOL, TORCH_DT, as_np, fill_store
 pytestmark = pytest.mark.gpu
 
 
-def run_case(dev, dt, lens, G, seed, tiles_per_wave=4, extra_cap=0, scale=None, outliers=False):
+def run_case(dev, dt, lens, G, seed, chunk_tiles=16, extra_cap=0, scale=None, outliers=False):
     rng = np.random.default_rng(seed)
     tdt = TORCH_DT[dt]
     ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32) for L in lens]
@@ -30,7 +31,7 @@ def run_case(dev, dt, lens, G, seed, tiles_per_wave=4, extra_cap=0, scale=None, 
     fill_store(store, [k.to(dev) for k in ks], [v.to(dev) for v in vs], dev)
     qd = q.to(tdt).to(dev)
     scale = 1.0 / math.sqrt(128) if scale is None else scale
-    out = store.attend(qd, scale, tiles_per_wave=tiles_per_wave)
+    out = store.attend(qd, scale, chunk_tiles=chunk_tiles)
     torch.cuda.synchronize()
     # The oracle sees exactly the values the device holds.
     ref = O.decode_attention(as_np(qd), [as_np(k.to(tdt)) for k in ks], [as_np(v.to(tdt)) for v in vs], scale)
@@ -51,9 +52,11 @@ def test_group_sizes(dev, G):
     assert err <= ATTN_TOL["bf16"], err
 
 
-@pytest.mark.parametrize("tpw", [1, 2, 8, 16])
-def test_chunking_is_invisible(dev, tpw):
-    err, _ = run_case(dev, "f32", [5000, 17, 1024], 4, seed=7, tiles_per_wave=tpw)
+@pytest.mark.parametrize("chunk", [1, 3, 4, 5, 8, 30, 64, None])
+def test_chunking_is_invisible(dev, chunk):
+    """Any chunk size (including ones that leave waves idle or split unevenly)
+    and the automatic choice give the same attention."""
+    err, _ = run_case(dev, "f32", [5000, 17, 1024], 4, seed=7, chunk_tiles=chunk)
     assert err <= ATTN_TOL["f32"], err
 
 
@@ -145,7 +148,7 @@ def test_fused_append_matches_oracle_over_steps(dev, dt):
 
 def test_merge_without_lds_factors(dev):
     """A row with more (part, query) pairs than the LDS factor table holds."""
-    err, _ = run_case(dev, "bf16", [70000, 300], 16, seed=31, tiles_per_wave=1)
+    err, _ = run_case(dev, "bf16", [70000, 300], 16, seed=31, chunk_tiles=4)
     assert err <= ATTN_TOL["bf16"], err
 
 
@@ -162,3 +165,19 @@ def test_row_order_does_not_change_results(dev):
     o2 = st.attend(q, 0.1)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2)
+
+
+def test_auto_chunk_fits_one_round(dev):
+    """hc_decode_chunk_tiles: at least one tile per wave, minimal (one tile
+    less would need more workgroups), one chunk per row when rows alone
+    exceed the device's slots, and an error for a bad dtype."""
+    from heterocache_amd import _lib, ops
+    for lens in ([131072] * 4 + [65536] * 4, [5000, 17, 1024], [0, 3], [200_000] * 3 + [10] * 5):
+        c = ops.decode_chunk_tiles(lens, 4, torch.bfloat16)
+        assert c >= 4
+        if c > 4:
+            assert ops.decode_num_parts(lens, c - 1) > ops.decode_num_parts(lens, c)
+    many = [4096] * 20000
+    assert ops.decode_chunk_tiles(many, 4, torch.bfloat16) == 128
+    lens = np.asarray([10], dtype=np.int32)
+    assert _lib.load().hc_decode_chunk_tiles(9, lens.ctypes.data_as(ctypes.c_void_p), 1, 4) == _lib.HC_ERR_INVALID
