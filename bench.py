@@ -37,7 +37,40 @@ def parse():
     p.add_argument("--unfused-append", action="store_true", help="append in its own launch before attention")
     p.add_argument("--full-steps", type=int, default=20, help="decode steps of the HeteroCache phase")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="after the decode phase, run a 256 MiB fp32 streaming copy (negate) three times as the "
+                        "reference kernel for HBM counter calibration")
     return p.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "decode_attn_llama8b_128k_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per decode launch (partial + merge) from the committed
+    FETCH_SIZE / WRITE_SIZE counter summary, or None when absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def copy_calibration(torch, dev):
+    """A plain streaming copy of known size (reads and writes 256 MiB) for
+    scaling the FETCH_SIZE / WRITE_SIZE counters to HBM bytes."""
+    n = 1 << 26
+    a = torch.ones(n, dtype=torch.float32, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        torch.neg(a, out=b)
+    torch.cuda.synchronize()
+    del a, b
+    return {"kernel": "torch.neg fp32 elementwise", "bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}
 
 
 def cpu_baseline(ctx, budgets, seconds):
@@ -265,12 +298,14 @@ def main():
         "us_per_layer": round(us_layer, 3),
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "kernel": "hc::decode_partial_kernel + decode_merge_kernel (one layer of the step)",
                      "bytes_per_launch": int(per_launch)},
     }
     del stores, q, kn, vn, outs
     torch.cuda.empty_cache()
+    if args.calibrate_copy:
+        rec["copy_calibration"] = copy_calibration(torch, dev)
     if not args.no_full_step:
         rec["full_decode_step"] = full_step_phase(args, torch, dev)
         rec["window_scoring"] = window_scoring_phase(args, torch, dev)
