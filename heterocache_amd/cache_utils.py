@@ -30,6 +30,7 @@ reference's behaviour where it differs):
     retrieval squeeze() assume batch 1, heterocache/cache_utils.py:704-722,
     :1093).
 """
+import math
 from typing import Dict, Optional
 
 import numpy as np
@@ -53,6 +54,11 @@ class HeteroCacheConfig:
     prefill scorer (1 = the reference's last query).  round_scores: reproduce
     the reference's casts of scores to the model dtype.  reference_quirks:
     float64 retrieval lengths and relation-order pivot sets, as the reference.
+    chunk_tiles: decode-attention chunk (None = one resident round).
+    batched_drift_check: when the model selects after attention (Llama
+    order), run the drift checks of all layers of a check step as one launch
+    sequence after the last layer (their results are first used by the next
+    step, so the outputs are unchanged).
     """
 
     def __init__(self, data: Optional[Dict], compression_ratio: Optional[float] = 0.5,
@@ -60,7 +66,8 @@ class HeteroCacheConfig:
                  max_gen_len: Optional[int] = 128, decode_step: Optional[int] = 4, pooling: Optional[str] = "avgpool",
                  kernel_size: Optional[int] = 5, num_attn_heads: Optional[int] = 32, num_kv_heads: Optional[int] = 8,
                  num_layers: Optional[int] = 32, retrieval_topk: Optional[int] = None, window_size: int = 1,
-                 round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None):
+                 round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None,
+                 batched_drift_check: bool = True):
         self.data = data
         self.stable_threshold = stable_threshold
         self.compression_ratio = compression_ratio
@@ -78,6 +85,7 @@ class HeteroCacheConfig:
         self.round_scores = round_scores
         self.reference_quirks = reference_quirks
         self.chunk_tiles = chunk_tiles
+        self.batched_drift_check = batched_drift_check
 
 
 def _f32_caps(base, ratios, seq_len):
@@ -95,7 +103,8 @@ class _LayerDrift:
         self.members = []      # satellite kv-heads per leader
         self.ref_bits = None   # [n_lead * B, words] int32 bitmask sets
         self.trigger = None    # [n_lead] int32
-        self.qbuf = None       # [B, Hq, S, 128] buffered decode queries
+        self.qbuf = None       # [B, Hq, S, 128] buffered decode queries (view of the model-wide buffer)
+        self.qlist = []        # the step queries [B, Hq, 1, 128] since the last check (references)
         self.count = 0
         self.meta = None       # device metadata and buffers, built on the first check
 
@@ -126,6 +135,7 @@ class HeteroCache(DynamicCache):
         self.window_size = int(getattr(cfg, "window_size", 1) or 1)
         self.round_scores = bool(getattr(cfg, "round_scores", False))
         self.chunk_tiles = getattr(cfg, "chunk_tiles", None)
+        self.batched_check = bool(getattr(cfg, "batched_drift_check", True))
 
         self.stores = [None] * self.num_layers
         self.prefill_topk_set = [None] * self.num_layers
@@ -142,6 +152,16 @@ class HeteroCache(DynamicCache):
         self.prefill_len = None
         self._seen_tokens = 0
         self._side = None
+        # Model-wide buffers: one K/V arena for every layer's rows, and the
+        # drift state of every layer (per-layer objects hold views of them).
+        self._arena = None
+        self._tile_table = None      # int64 arena tile offsets of all rows, layer-major
+        self._qbuf_all = None        # [NL, B, Hq, S, 128] buffered decode queries
+        self._ref_bits_all = None    # [leaders * B, words] pivot reference sets
+        self._trigger_all = None     # [leaders] int32 drift flags
+        self._lead_base = None       # first global leader index of each layer
+        self._due = []               # layers whose check waits for the batched launch
+        self._batch_meta = {}
 
     # -- reference API ------------------------------------------------------
     def __bool__(self):
@@ -162,7 +182,7 @@ class HeteroCache(DynamicCache):
             self._side = torch.cuda.Stream(device=device)
         return self._side
 
-    def _init_layer_storage(self, layer_idx, device, dtype):
+    def _layer_row_caps(self, layer_idx):
         """Row capacities for the whole lifetime (heterocache/cache_utils.py:693-766)."""
         L, gen = self.prefill_len, self.config.max_gen_len
         keep = set(self.data["need_to_keep_counts"][layer_idx])
@@ -177,8 +197,22 @@ class HeteroCache(DynamicCache):
                 cap = max(c64, c32)
             caps.append(cap)
         self.layer_head_capacities[layer_idx] = caps
-        row_caps = [caps[r % self.num_kv_heads] + gen for r in range(self.bsz * self.num_kv_heads)]
-        self.stores[layer_idx] = KVStore(row_caps, dtype, device)
+        return [caps[r % self.num_kv_heads] + gen for r in range(self.bsz * self.num_kv_heads)]
+
+    def _init_storage(self, device, dtype):
+        """Every layer's store in one K and one V arena, sized at the first
+        prefill (all capacities follow from the prefill length)."""
+        row_caps = [self._layer_row_caps(layer) for layer in range(self.num_layers)]
+        tiles = [KVStore.tiles_for(c) for c in row_caps]
+        n = max(sum(tiles), 1) * ops.TILE * ops.HEAD_DIM
+        k = torch.zeros(n, dtype=dtype, device=device)
+        v = torch.zeros(n, dtype=dtype, device=device)
+        self._arena = (k, v)
+        base = 0
+        for layer in range(self.num_layers):
+            self.stores[layer] = KVStore(row_caps[layer], dtype, device, arena=(k, v, base))
+            base += tiles[layer]
+        self._tile_table = torch.cat([st.row_tile_off for st in self.stores])
 
     def update(self, key_states, value_states, layer_idx, cache_kwargs=None):
         """heterocache/cache_utils.py:884-1005."""
@@ -194,7 +228,7 @@ class HeteroCache(DynamicCache):
             self.base_compress_len = get_compress_len(self.compression_ratio, self.full_heads, self.prefill_len,
                                                       self.total_kv_heads)
         if self.stores[layer_idx] is None:
-            self._init_layer_storage(layer_idx, key_states.device, key_states.dtype)
+            self._init_storage(key_states.device, key_states.dtype)
         store = self.stores[layer_idx]
         seq_len = key_states.shape[-2]
         if seq_len > 1:
@@ -280,12 +314,30 @@ class HeteroCache(DynamicCache):
         # Score rows are (b, pivot position); reorder them to (leader, b).
         order = torch.tensor([self._score_row(b, s, len(pivots)) for s in src for b in range(self.bsz)],
                              dtype=torch.long, device=idx.device)
-        words = (L + 31) // 32
-        st.ref_bits = torch.zeros((len(leaders) * self.bsz, max(words, 1)), dtype=torch.int32, device=idx.device)
+        if self._ref_bits_all is None:
+            self._init_drift_buffers(idx.device, L)
+        lb, B = self._lead_base[layer_idx], self.bsz
+        if len(leaders) != self._lead_base[layer_idx + 1] - lb:
+            raise ValueError(f"layer {layer_idx}: leader count differs from leader_member_relations")
+        st.ref_bits = self._ref_bits_all[lb * B:(lb + len(leaders)) * B]
         if len(leaders):
             ops.set_bits(idx.index_select(0, order).contiguous(), None, st.ref_bits, L, fixed_count=K)
-        st.trigger = torch.zeros(max(len(leaders), 1), dtype=torch.int32, device=idx.device)
+            st.trigger = self._trigger_all[lb:lb + len(leaders)]
+        else:
+            st.trigger = torch.zeros(1, dtype=torch.int32, device=idx.device)
         self.prefill_topk_set[layer_idx] = st.ref_bits
+
+    def _init_drift_buffers(self, device, seq_len):
+        """Model-wide reference sets and trigger flags, one row per (leader,
+        batch) in layer order, then relation order, then batch."""
+        nlead = [len(self.data["leader_member_relations"][layer]) for layer in range(self.num_layers)]
+        self._lead_base = [0]
+        for n in nlead:
+            self._lead_base.append(self._lead_base[-1] + n)
+        total = self._lead_base[-1]
+        words = max((seq_len + 31) // 32, 1)
+        self._ref_bits_all = torch.zeros((total * self.bsz, words), dtype=torch.int32, device=device)
+        self._trigger_all = torch.zeros(max(total, 1), dtype=torch.int32, device=device)
 
     @staticmethod
     def _score_row(b, pivot_pos, npiv):
@@ -324,6 +376,8 @@ class HeteroCache(DynamicCache):
         B, Hq, ql, D = query_states.shape
         if ql != 1:
             raise ValueError("decode_attention takes one query position")
+        if layer_idx in self._due:
+            self._flush_checks()
         store = self.stores[layer_idx]
         ev = self._retrieval_done[layer_idx]
         if ev is not None:
@@ -342,21 +396,65 @@ class HeteroCache(DynamicCache):
     def decode_select(self, query_states, layer_idx):
         """Buffered pivot drift check and satellite retrieval
         (heterocache/cache_utils.py:1007-1147), without host syncs: after the
-        first check of a layer every launch reuses device metadata built once."""
+        first check every launch reuses device metadata built once.
+
+        Llama order (attention already ran this step): the check is deferred
+        and the checks of all layers run as one launch sequence after the
+        last layer (their results are first read by the next step's
+        attention).  Qwen order (select before attention): each layer checks
+        at once, as its attention in this step reads the result."""
         st = self._drift[layer_idx]
         if st is None:
             st = self._drift[layer_idx] = _LayerDrift()
         S = self.decode_step
         if st.qbuf is None:
-            st.qbuf = torch.empty((self.bsz, self.num_attn_heads, S, self.head_dim), dtype=query_states.dtype,
-                                  device=query_states.device)
-        st.qbuf[:, :, st.count].copy_(query_states[:, :, -1])
+            if self._qbuf_all is None:
+                self._qbuf_all = torch.empty((self.num_layers, self.bsz, self.num_attn_heads, S, self.head_dim),
+                                             dtype=query_states.dtype, device=query_states.device)
+            st.qbuf = self._qbuf_all[layer_idx]
+        # The step queries are fresh tensors the model does not touch again;
+        # keeping references until the check avoids a copy per layer and step.
+        if st.leaders:
+            st.qlist.append(query_states)
         st.count += 1
-        if st.count < S:
-            return
-        st.count = 0
+        if st.count >= S:
+            st.count = 0
+            if st.leaders:
+                if self.batched_check and self._pending[layer_idx] is None:
+                    self._due.append(layer_idx)
+                else:
+                    self._gather_queries([layer_idx])
+                    self._check_layer(layer_idx)
+        if self._due and layer_idx == self.num_layers - 1:
+            self._flush_checks()
+
+    def _gather_queries(self, layers):
+        """Buffered step queries of these layers -> qbuf [B, Hq, S, 128] each
+        (one stack launch per layer)."""
+        for layer in layers:
+            st = self._drift[layer]
+            qs, st.qlist = st.qlist, []
+            torch.stack([q[:, :, -1] for q in qs], dim=2, out=st.qbuf)
+
+    def _flush_checks(self):
+        """Run the deferred checks: one batched launch sequence when they
+        cover every layer that has leaders (the lockstep case), otherwise
+        layer by layer."""
+        layers, self._due = sorted(self._due), []
+        self._gather_queries(layers)
+        lead_layers = [l for l in range(self.num_layers) if self._drift[l] is not None and self._drift[l].leaders]
+        if layers == lead_layers and self._ref_bits_all is not None:
+            self._check_batched(layers)
+        else:
+            for layer in layers:
+                self._check_layer(layer)
+
+    def _check_layer(self, layer_idx):
+        """One layer's drift check and gated retrieval."""
+        st = self._drift[layer_idx]
         if not st.leaders or not any(st.members):
             return
+        S = self.decode_step
         if st.meta is None:
             st.meta = self._drift_metadata(layer_idx, st)
         m = st.meta
@@ -365,7 +463,7 @@ class HeteroCache(DynamicCache):
         K, nl = m["K"], len(st.leaders)
         # Scores of every (leader in relation order, batch row): [nl*B, S, L].
         scores = compress.pivot_step_scores(st.qbuf, store, None, None, G, L, self.pooling, self.kernel_size,
-                                            round_dtype=self._round_dtype(query_states.dtype),
+                                            round_dtype=self._round_dtype(st.qbuf.dtype),
                                             metadata=m["score_meta"])
         ops.select_topk(scores.view(nl * B * S, L), m["caps_K"], L, idx=m["cur"], counts=m["cur_counts"])
         ops.overlap_count(m["cur"], K, st.ref_bits, L, ref_of=m["ref_of"], out=m["overlap"])
@@ -375,6 +473,103 @@ class HeteroCache(DynamicCache):
         ops.set_bits(last, None, st.ref_bits, L, fixed_count=K, trigger=st.trigger, trig_of=m["trig_of"])
         if m["plans"]:
             self._retrieve(layer_idx, st, scores[:, S - 1])
+
+    def _check_batched(self, layers):
+        """Drift checks of all leader layers in one launch sequence: scores
+        of every (layer, leader, batch) row read in place from the shared
+        arena, one selection, overlap, decision and set update for all, one
+        retrieval selection; then the gated gathers layer by layer on the
+        side stream (each layer's event guards its next attention)."""
+        key = tuple(layers)
+        bm = self._batch_meta.get(key)
+        if bm is None:
+            bm = self._batch_meta[key] = self._batched_metadata(layers)
+        S, L, G, B = self.decode_step, self.prefill_len, self.num_key_value_groups, self.bsz
+        K, J = bm["K"], bm["J"]
+        qa = self._qbuf_all
+        flags = compress.ROUND_FLAGS[self._round_dtype(qa.dtype)]
+        scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,
+                           self.pooling, self.kernel_size, 1.0 / math.sqrt(self.head_dim), flags=flags,
+                           row_tile_off=self._tile_table, k_row=bm["k_row"]).view(J, S, L)
+        ops.select_topk(scores.view(J * S, L), bm["caps_K"], L, idx=bm["cur"], counts=bm["cur_counts"])
+        ops.overlap_count(bm["cur"], K, self._ref_bits_all, L, ref_of=bm["ref_of"], out=bm["overlap"])
+        ops.drift_decide(bm["overlap"], J // B, B, S, K, self.stable_threshold, self._trigger_all)
+        last = bm["cur"].view(J, S, -1)[:, S - 1]
+        ops.set_bits(last, None, self._ref_bits_all, L, fixed_count=K, trigger=self._trigger_all,
+                     trig_of=bm["trig_of"])
+        if not bm["plans"]:
+            return
+        ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
+        dev = qa.device
+        main = torch.cuda.current_stream(dev)
+        host = self.device == "cpu"
+        side = self._side_stream(dev) if host else main
+        if host:
+            side.wait_stream(main)
+        with torch.cuda.stream(side):
+            for layer, plan in bm["plans"]:
+                kc, vc = self.key_cache_cpu[layer], self.value_cache_cpu[layer]
+                self.stores[layer].launch_rows(plan, kc, vc, idx=bm["ret_idx"], src_is_host=host, stream=side,
+                                               trigger=self._trigger_all, set_len=False)
+                if host:
+                    ev = torch.cuda.Event()
+                    ev.record(side)
+                    self._retrieval_done[layer] = ev
+
+    def _batched_metadata(self, layers):
+        """Device metadata of _check_batched; rows j follow the global
+        (layer, leader, batch) order of the reference sets and triggers."""
+        dev = self._qbuf_all.device
+        qa = self._qbuf_all
+        B, Hkv, G, S, L = self.bsz, self.num_kv_heads, self.num_key_value_groups, self.decode_step, self.prefill_len
+        K = min(self.base_compress_len, L)
+        q_off, k_row, trig_of, ret_caps, jobs = [], [], [], [], {}
+        j = 0
+        for layer in layers:
+            st = self._drift[layer]
+            lb = self._lead_base[layer]
+            for i, h in enumerate(st.leaders):
+                members = st.members[i]
+                lens = self._retrieval_lengths(layer, members) if members else []
+                mx = max(lens) if lens else 0
+                for b in range(B):
+                    if j != (lb + i) * B + b:
+                        raise RuntimeError("batched drift rows out of the global leader order")
+                    q_off.append(layer * qa.stride(0) + b * qa.stride(1) + h * G * qa.stride(2))
+                    k_row.append(layer * B * Hkv + b * Hkv + h)
+                    trig_of.append(lb + i)
+                    ret_caps.append(mx)
+                    for mm, n in zip(members, lens):
+                        if n > 0:
+                            jobs.setdefault(layer, []).append((j, lb + i, b, mm, n))
+                    j += 1
+        J = j
+        m = {"K": K, "J": J}
+        m["q_off"] = torch.as_tensor(np.asarray(q_off, dtype=np.int64)).to(dev)
+        m["k_row"] = torch.as_tensor(np.asarray(k_row, dtype=np.int32)).to(dev)
+        m["caps_K"] = torch.full((J * S,), K, dtype=torch.int32, device=dev)
+        m["cur"] = torch.empty((J * S, max(K, 1)), dtype=torch.int32, device=dev)
+        m["cur_counts"] = torch.empty(J * S, dtype=torch.int32, device=dev)
+        m["overlap"] = torch.empty(J * S, dtype=torch.int32, device=dev)
+        m["ref_of"] = torch.arange(J, dtype=torch.int32, device=dev).repeat_interleave(S)
+        m["trig_of"] = torch.as_tensor(np.asarray(trig_of, dtype=np.int32)).to(dev)
+        m["plans"] = []
+        if jobs:
+            mk = max(ret_caps)
+            m["ret_caps"] = torch.as_tensor(np.asarray(ret_caps, dtype=np.int32)).to(dev)
+            m["ret_idx"] = torch.empty((J, max(mk, 1)), dtype=torch.int32, device=dev)
+            m["ret_counts"] = torch.empty(J, dtype=torch.int32, device=dev)
+            for layer in layers:
+                lj = jobs.get(layer)
+                if not lj:
+                    continue
+                tier_heads = self._tier_heads[layer]
+                plan = self.stores[layer].plan_rows(
+                    self.key_cache_cpu[layer], [(b, tier_heads[mm]) for _, _, b, mm, _ in lj],
+                    [b * Hkv + mm for _, _, b, mm, _ in lj], [n for _, _, _, _, n in lj], idx=m["ret_idx"],
+                    idx_rows=[jj for jj, _, _, _, _ in lj], trig_of=[t for _, t, _, _, _ in lj])
+                m["plans"].append((layer, plan))
+        return m
 
     def _drift_metadata(self, layer_idx, st):
         """Device tensors and buffers of one layer's drift check and retrieval."""

@@ -25,12 +25,16 @@ def dtype_code(dt):
 
 
 def _ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    # ctypes passes a Python int (or None) for a c_void_p argument as is.
+    return t.data_ptr() if t is not None else None
 
 
-def _stream(stream=None):
-    s = stream if stream is not None else torch.cuda.current_stream()
-    return ctypes.c_void_p(s.cuda_stream)
+def _stream(stream, like):
+    """Raw HIP stream: the given one, else the current stream of the device
+    of tensor `like` (read without constructing a torch Stream object)."""
+    if stream is not None:
+        return stream.cuda_stream
+    return torch._C._cuda_getCurrentRawStream(like.device.index)
 
 
 def _require_cuda(*ts):
@@ -67,11 +71,18 @@ WORKSPACE = Workspace()
 SELECT_HIST = Workspace()
 
 
+def _lens_i32(host_row_len):
+    lens = np.asarray(host_row_len)
+    if lens.dtype != np.int32 or not lens.flags.c_contiguous:
+        lens = np.ascontiguousarray(lens, dtype=np.int32)
+    return lens
+
+
 def decode_num_parts(host_row_len, chunk_tiles):
     """Workgroups of one decode launch: chunks of chunk_tiles 32-token tiles
     per row (an empty row still takes one)."""
-    lens = np.ascontiguousarray(host_row_len, dtype=np.int32)
-    n = _lib.load().hc_decode_num_parts(lens.ctypes.data_as(ctypes.c_void_p), len(lens), int(chunk_tiles))
+    lens = _lens_i32(host_row_len)
+    n = _lib.load().hc_decode_num_parts(lens.ctypes.data, len(lens), int(chunk_tiles))
     if n < 0:
         raise ValueError("bad arguments to hc_decode_num_parts")
     return n
@@ -80,9 +91,8 @@ def decode_num_parts(host_row_len, chunk_tiles):
 def decode_chunk_tiles(host_row_len, group, dtype):
     """The chunk size whose grid fills the current device in one resident
     round for these lengths (hc_decode_chunk_tiles)."""
-    lens = np.ascontiguousarray(host_row_len, dtype=np.int32)
-    n = _lib.load().hc_decode_chunk_tiles(dtype_code(dtype), lens.ctypes.data_as(ctypes.c_void_p), len(lens),
-                                          int(group))
+    lens = _lens_i32(host_row_len)
+    n = _lib.load().hc_decode_chunk_tiles(dtype_code(dtype), lens.ctypes.data, len(lens), int(group))
     _lib.check(min(n, 0))
     return n
 
@@ -117,12 +127,14 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
             raise TypeError("k_new/v_new must share q's dtype")
         k_new = k_new.contiguous()
         v_new = v_new.contiguous()
-        host_row_len = np.asarray(host_row_len) + 1
+        host_row_len = _lens_i32(host_row_len) + np.int32(1)
     if row_order is not None and (row_order.dtype != torch.int32 or row_order.numel() != rows):
         raise ValueError("row_order must be an int32 permutation of the rows")
     q = q.contiguous()
     if out is None:
         out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or not out.is_contiguous() or out.device != q.device:
+        raise ValueError("out must be a contiguous tensor of q's shape, dtype and device")
     if chunk_tiles is None:
         chunk_tiles = decode_chunk_tiles(host_row_len, G, q.dtype)
     nparts = decode_num_parts(host_row_len, chunk_tiles)
@@ -130,7 +142,7 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
     ws = workspace if workspace is not None else WORKSPACE.get(q.device, nbytes)
     _lib.check(lib.hc_decode_attn(dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
                                   _ptr(row_len), _ptr(row_order), rows, G, float(scale), _ptr(k_new), _ptr(v_new),
-                                  _ptr(out), _ptr(ws), ws.numel(), nparts, int(chunk_tiles), _stream(stream)))
+                                  _ptr(out), _ptr(ws), ws.numel(), nparts, int(chunk_tiles), _stream(stream, q)))
     return out
 
 
@@ -156,7 +168,7 @@ def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, c
     _lib.check(lib.hc_gather_store(dtype_code(kstore.dtype), _ptr(src_k), _ptr(src_v), int(bool(src_is_host)),
                                    _ptr(src_off), int(src_tok_stride), int(src_len), _ptr(idx), _ptr(idx_off), _ptr(count),
                                    _ptr(dst_row), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off), njobs,
-                                   int(max_count), _ptr(trigger), _ptr(trig_of), _stream(stream)))
+                                   int(max_count), _ptr(trigger), _ptr(trig_of), _stream(stream, kstore)))
 
 
 def append(k_new, v_new, kstore, vstore, row_tile_off, row_len, row_cap, status=None, stream=None):
@@ -170,7 +182,7 @@ def append(k_new, v_new, kstore, vstore, row_tile_off, row_len, row_cap, status=
     v_new = v_new.contiguous()
     _lib.check(lib.hc_append(dtype_code(kstore.dtype), _ptr(k_new), _ptr(v_new), HEAD_DIM, _ptr(kstore),
                              _ptr(vstore), _ptr(row_tile_off), _ptr(row_len), _ptr(row_cap), rows, _ptr(status),
-                             _stream(stream)))
+                             _stream(stream, kstore)))
 
 
 def store_read(kstore, vstore, row_tile_off, rows_sel, count, stream=None):
@@ -182,7 +194,7 @@ def store_read(kstore, vstore, row_tile_off, rows_sel, count, stream=None):
     dk = torch.empty((n, count, HEAD_DIM), dtype=kstore.dtype, device=kstore.device)
     dv = torch.empty_like(dk)
     _lib.check(lib.hc_store_read(dtype_code(kstore.dtype), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
-                                 _ptr(rows_sel), n, int(count), _ptr(dk), _ptr(dv), _stream(stream)))
+                                 _ptr(rows_sel), n, int(count), _ptr(dk), _ptr(dv), _stream(stream, kstore)))
     return dk, dv
 
 
@@ -214,7 +226,7 @@ def score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, seq_len
     _lib.check(lib.hc_score(dtype_code(q.dtype), _ptr(q), _ptr(q_off), int(q_head_stride), int(q_row_stride), _ptr(k),
                             _ptr(k_off), int(k_tok_stride), _ptr(row_tile_off), _ptr(k_row), njobs, int(seq_len),
                             int(group), int(window), int(flags), int(span), pool, int(kernel), float(scale),
-                            _ptr(out), _ptr(ws), ws.numel(), _stream(stream)))
+                            _ptr(out), _ptr(ws), ws.numel(), _stream(stream, q)))
     return out
 
 
@@ -236,7 +248,7 @@ def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None
                           device=scores.device)
     _lib.check(lib.hc_select_topk(_ptr(scores), scores.stride(0), njobs, int(span), _ptr(caps), int(window), _ptr(idx),
                                   idx.stride(0), _ptr(counts), _ptr(hist), hist.numel(), _ptr(scratch),
-                                  scratch.numel(), _stream(stream)))
+                                  scratch.numel(), _stream(stream, scores)))
     return idx, counts
 
 
@@ -247,7 +259,7 @@ def set_bits(idx, counts, bits, nbits, fixed_count=0, trigger=None, trig_of=None
     if idx.dtype != torch.int32 or bits.dtype != torch.int32 or idx.dim() != 2 or bits.dim() != 2:
         raise TypeError("idx and bits must be 2-D int32 tensors")
     _lib.check(lib.hc_set_bits(_ptr(idx), idx.stride(0), _ptr(counts), int(fixed_count), idx.shape[0], _ptr(bits),
-                               bits.stride(0), int(nbits), _ptr(trigger), _ptr(trig_of), _stream(stream)))
+                               bits.stride(0), int(nbits), _ptr(trigger), _ptr(trig_of), _stream(stream, bits)))
 
 
 def overlap_count(idx, count, bits, nbits, ref_of=None, out=None, stream=None):
@@ -257,7 +269,7 @@ def overlap_count(idx, count, bits, nbits, ref_of=None, out=None, stream=None):
     if out is None:
         out = torch.empty(idx.shape[0], dtype=torch.int32, device=idx.device)
     _lib.check(lib.hc_overlap_count(_ptr(idx), idx.stride(0), int(count), idx.shape[0], _ptr(bits), bits.stride(0),
-                                    int(nbits), _ptr(ref_of), _ptr(out), _stream(stream)))
+                                    int(nbits), _ptr(ref_of), _ptr(out), _stream(stream, bits)))
     return out
 
 
@@ -266,4 +278,4 @@ def drift_decide(counts, npiv, batch, steps, K, threshold, trigger, overlap=None
     lib = _lib.load()
     _require_cuda(counts, trigger, overlap, median)
     _lib.check(lib.hc_drift_decide(_ptr(counts), int(npiv), int(batch), int(steps), int(K), float(threshold),
-                                   _ptr(overlap), _ptr(median), _ptr(trigger), _stream(stream)))
+                                   _ptr(overlap), _ptr(median), _ptr(trigger), _stream(stream, counts)))

@@ -23,9 +23,15 @@ class KVStore:
     Host mirror `host_len` tracks row_len exactly: lengths only change through
     this object's methods, so the grid of every kernel is sized without a
     device->host sync.
+
+    arena: optional (k, v, tile_base) -- flat K and V buffers shared by
+    several stores (for example every layer of a model); this store's rows
+    then occupy tiles [tile_base, tile_base + total_tiles) of them and its
+    row_tile_off holds arena-wide tile indices, so one launch can address
+    rows of several stores through the shared base pointers.
     """
 
-    def __init__(self, row_caps, dtype, device):
+    def __init__(self, row_caps, dtype, device, arena=None):
         caps = np.asarray(row_caps, dtype=np.int64)
         if (caps < 0).any():
             raise ValueError("negative row capacity")
@@ -37,17 +43,37 @@ class KVStore:
         self.dtype = dtype
         self.device = torch.device(device)
         self.host_cap = tiles * TILE
-        self.host_tile_off = off
         self.total_tiles = int(tiles.sum())
-        n = max(self.total_tiles, 1) * TILE * HEAD_DIM
-        self.k = torch.zeros(n, dtype=dtype, device=self.device)
-        self.v = torch.zeros(n, dtype=dtype, device=self.device)
+        if arena is None:
+            n = max(self.total_tiles, 1) * TILE * HEAD_DIM
+            self.k = torch.zeros(n, dtype=dtype, device=self.device)
+            self.v = torch.zeros(n, dtype=dtype, device=self.device)
+            self.tile_base = 0
+        else:
+            k, v, tile_base = arena
+            if k.dtype != dtype or v.dtype != dtype or k.shape != v.shape or k.dim() != 1:
+                raise ValueError("arena buffers must be flat and of the store's dtype")
+            if k.device != self.device or v.device != self.device:
+                raise ValueError("arena buffers must live on the store's device")
+            if tile_base < 0 or (tile_base + self.total_tiles) * TILE * HEAD_DIM > k.numel():
+                raise ValueError("store rows exceed the arena")
+            self.k, self.v = k, v
+            self.tile_base = int(tile_base)
+            off = off + self.tile_base
+        self.host_tile_off = off
         self.row_tile_off = torch.as_tensor(off, dtype=torch.int64).to(self.device)
         self.row_cap = torch.as_tensor(self.host_cap, dtype=torch.int32).to(self.device)
         self.row_len = torch.zeros(self.rows, dtype=torch.int32, device=self.device)
-        self.host_len = np.zeros(self.rows, dtype=np.int64)
+        self.host_len = np.zeros(self.rows, dtype=np.int32)
+        self._headroom = int(self.host_cap.min()) if self.rows else 0  # min over rows of cap - len
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.row_order = torch.arange(self.rows, dtype=torch.int32, device=self.device)
+
+    @staticmethod
+    def tiles_for(row_caps):
+        """Tiles a store with these row capacities occupies in an arena."""
+        caps = np.asarray(row_caps, dtype=np.int64)
+        return int(((caps + TILE - 1) // TILE).sum())
 
     # -- bookkeeping -------------------------------------------------------
     def bytes_per_token(self):
@@ -66,7 +92,8 @@ class KVStore:
         idx = torch.as_tensor(rows, dtype=torch.int64).to(self.device)
         self.row_len.index_copy_(0, idx, torch.as_tensor(lens, dtype=torch.int32).to(self.device))
         # Longest rows are scheduled first; appends keep this order.
-        order = np.argsort(-self.host_len, kind="stable").astype(np.int32)
+        order = np.argsort(-self.host_len.astype(np.int64), kind="stable").astype(np.int32)
+        self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
         self.row_order = torch.as_tensor(order).to(self.device)
 
     # -- writers -----------------------------------------------------------
@@ -163,12 +190,11 @@ class KVStore:
         k_new / v_new: [rows, 128].  Raises like the reference's "OOM" when a
         row is full (heterocache/cache_utils.py:988-990).
         """
-        if (self.host_len + 1 > self.host_cap).any():
-            full = np.nonzero(self.host_len + 1 > self.host_cap)[0].tolist()
-            raise RuntimeError(f"KV store OOM: rows {full} are at capacity")
+        self._check_room()
         ops.append(k_new, v_new, self.k, self.v, self.row_tile_off, self.row_len, self.row_cap, self.status,
                    stream=stream)
         self.host_len += 1
+        self._headroom -= 1
 
     # -- readers -----------------------------------------------------------
     def read_rows(self, rows, count):
@@ -184,12 +210,19 @@ class KVStore:
         launch: the new token is attended, stored at slot len and every
         length advances by one.
         """
-        if k_new is not None and (self.host_len + 1 > self.host_cap).any():
-            full = np.nonzero(self.host_len + 1 > self.host_cap)[0].tolist()
-            raise RuntimeError(f"KV store OOM: rows {full} are at capacity")
+        if k_new is not None:
+            self._check_room()
         out = ops.decode_attn(q, self.k, self.v, self.row_tile_off, self.row_len, self.host_len, scale, out=out,
                               row_order=self.row_order, k_new=k_new, v_new=v_new, chunk_tiles=chunk_tiles,
                               stream=stream)
         if k_new is not None:
             self.host_len += 1
+            self._headroom -= 1
         return out
+
+    def _check_room(self):
+        """Raise like the reference's "OOM" when a row cannot take one more
+        token (heterocache/cache_utils.py:988-990)."""
+        if self._headroom < 1:
+            full = np.nonzero(self.host_len.astype(np.int64) + 1 > self.host_cap)[0].tolist()
+            raise RuntimeError(f"KV store OOM: rows {full} are at capacity")
