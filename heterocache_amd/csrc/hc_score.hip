@@ -96,27 +96,36 @@ __device__ __forceinline__ void load_k_subtile(const ScoreArgs& a, int job, int 
   }
 }
 
-// Logits (base 2) of rows 16nt + (lane & 15) for tokens t0 + 4*(lane>>4) + j.
+// Last key position row r may see: L - W + w under the causal window mask,
+// else L - 1; -1 for padding rows (r >= R).  Computed once per row tile, so
+// the inner loops hold no integer division.
+__device__ __forceinline__ int row_limit(const ScoreArgs& a, int r) {
+  if (r >= a.R) return -1;
+  return (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W + r % a.W : a.L - 1;
+}
+
+__device__ __forceinline__ float scaled_logit(const ScoreArgs& a, float acc) {
+  float v;
+  if (a.flags & (HC_SCORE_ROUND_BF16 | HC_SCORE_ROUND_F16))
+    v = round_mode(round_mode(acc, a.flags) * a.scale, a.flags);
+  else
+    v = acc * a.scale;
+  return v * 1.4426950408889634f;
+}
+
+// Logits (base 2) of row 16nt + (lane & 15) (visible up to `limit`) for
+// tokens t0 + 4*(lane>>4) + j; keys are the A operand.
 template <typename T>
 __device__ __forceinline__ void subtile_logits(const ScoreArgs& a, const typename Elem<T>::vec8 (&kr)[4],
-                                               const T* s_q, int nt, int t0, int lane, float (&x)[4]) {
+                                               const T* s_q, int nt, int t0, int lane, int limit, float (&x)[4]) {
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const T* qrow = s_q + (16 * nt + (lane & 15)) * kQPitch + 8 * (lane >> 4);
 #pragma unroll
   for (int s = 0; s < 4; ++s) acc = mma_16x16x32(kr[s], load8<T>(qrow + 32 * s), acc);
-  const int r = 16 * nt + (lane & 15);
-  const int w = r % a.W;
-  const int causal_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W + w : a.L - 1;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int t = t0 + 4 * (lane >> 4) + j;
-    float v;
-    if (a.flags & (HC_SCORE_ROUND_BF16 | HC_SCORE_ROUND_F16))
-      v = round_mode(round_mode(acc[j], a.flags) * a.scale, a.flags);
-    else
-      v = acc[j] * a.scale;
-    v *= 1.4426950408889634f;
-    x[j] = (t < a.L && t <= causal_limit) ? v : -INFINITY;
+    x[j] = t <= limit ? scaled_logit(a, acc[j]) : -INFINITY;
   }
 }
 
@@ -136,54 +145,65 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rows = a.NT * 16;
   stage_queries<T>(a, job, s_q);
-  for (int i = threadIdx.x; i < kScoreWaves * rows; i += kScoreWaves * 64) {
-    s_st[2 * i] = -INFINITY;
-    s_st[2 * i + 1] = 0.f;
-  }
-  __syncthreads();
-  float* my = s_st + (size_t)wave * rows * 2;
   // Each wave owns kSubTiles consecutive 16-token sub-tiles; all their key
   // loads are issued before any is used.
   const int tw = chunk * kScoreChunk + wave * 16 * kSubTiles;
   typename Elem<T>::vec8 krs[kSubTiles][4];
 #pragma unroll
   for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, krs[u]);
+  __syncthreads();
+  // Lane state: running (max, sum) of row 16nt + lane%16 over this lane's
+  // tokens; the four lanes of a row are combined once, after the loop.
+  float m[16], l[16];
 #pragma unroll
-  for (int u = 0; u < kSubTiles; ++u) {
-    const int t0 = tw + 16 * u;
-    if (t0 >= a.L) break;
-    const typename Elem<T>::vec8(&kr)[4] = krs[u];
-    for (int nt = 0; nt < a.NT; ++nt) {
-      float x[4];
-      subtile_logits<T>(a, kr, s_q, nt, t0, lane, x);
-      float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      float sm = 0.f;
-      if (mx != -INFINITY) {
+  for (int nt = 0; nt < 16; ++nt) {
+    m[nt] = -INFINITY;
+    l[nt] = 0.f;
+  }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sm += fast_exp2(x[j] - mx);
+  for (int nt = 0; nt < 16; ++nt) {
+    if (nt < a.NT) {
+      const int limit = row_limit(a, 16 * nt + (lane & 15));
+#pragma unroll
+      for (int u = 0; u < kSubTiles; ++u) {
+        float x[4];
+        subtile_logits<T>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
+        const float mn = fmaxf(fmaxf(m[nt], fmaxf(x[0], x[1])), fmaxf(x[2], x[3]));
+        if (mn != -INFINITY) {
+          float sm = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) sm += fast_exp2(x[j] - mn);
+          l[nt] = fmaf(l[nt], fast_exp2(m[nt] - mn), sm);
+          m[nt] = mn;
+        }
       }
-      sm += __shfl_xor(sm, 16, 64);
-      sm += __shfl_xor(sm, 32, 64);
+    }
+  }
+  float* my = s_st + (size_t)wave * rows * 2;
+#pragma unroll
+  for (int nt = 0; nt < 16; ++nt) {
+    if (nt < a.NT) {
+      float mm = m[nt], ll = l[nt];
+#pragma unroll
+      for (int off = 16; off <= 32; off <<= 1) {
+        const float m2 = __shfl_xor(mm, off, 64), l2 = __shfl_xor(ll, off, 64);
+        merge_ml(mm, ll, m2, l2);
+      }
       if (lane < 16) {
-        const int r = 16 * nt + lane;
-        float m = my[2 * r], l = my[2 * r + 1];
-        merge_ml(m, l, mx, sm);
-        my[2 * r] = m;
-        my[2 * r + 1] = l;
+        my[2 * (16 * nt + lane)] = mm;
+        my[2 * (16 * nt + lane) + 1] = ll;
       }
     }
   }
   __syncthreads();
   const int nchunks = gridDim.x;
   for (int r = threadIdx.x; r < a.R; r += kScoreWaves * 64) {
-    float m = -INFINITY, l = 0.f;
+    float mm = -INFINITY, ll = 0.f;
 #pragma unroll
-    for (int w = 0; w < kScoreWaves; ++w) merge_ml(m, l, s_st[(w * rows + r) * 2], s_st[(w * rows + r) * 2 + 1]);
+    for (int w = 0; w < kScoreWaves; ++w) merge_ml(mm, ll, s_st[(w * rows + r) * 2], s_st[(w * rows + r) * 2 + 1]);
     float* o = part + (((int64_t)job * nchunks + chunk) * a.R + r) * 2;
-    o[0] = m;
-    o[1] = l;
+    o[0] = mm;
+    o[1] = ll;
   }
 }
 
@@ -210,95 +230,104 @@ __global__ __launch_bounds__(256) void score_stats_merge_kernel(const float* __r
   }
 }
 
+// Logits (base 2) with the queries as the A operand: lane holds rows
+// 16nt + 4*(lane>>4) + j (visible up to limit[j]) of token t0 + lane%16, so
+// sums over a query head's window rows are in-lane adds plus at most two
+// cross-lane steps.
+template <typename T>
+__device__ __forceinline__ void subtile_logits_rows(const ScoreArgs& a, const typename Elem<T>::vec8 (&kr)[4],
+                                                    const T* s_q, int nt, int t0, int lane, const int (&limit)[4],
+                                                    float (&x)[4]) {
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const T* qrow = s_q + (16 * nt + (lane & 15)) * kQPitch + 8 * (lane >> 4);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) acc = mma_16x16x32(load8<T>(qrow + 32 * s), kr[s], acc);
+  const int t = t0 + (lane & 15);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[j] = t <= limit[j] ? scaled_logit(a, acc[j]) : -INFINITY;
+}
+
 template <typename T, bool STORE>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs a, const float* __restrict__ stats,
                                                                       float* __restrict__ A) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_q = reinterpret_cast<T*>(smem);
-  float* s_ml = reinterpret_cast<float*>(smem + (size_t)a.NT * 16 * kQPitch * sizeof(T));  // [rows][2]
+  const int rows = a.NT * 16;
+  float* s_m = reinterpret_cast<float*>(smem + (size_t)rows * kQPitch * sizeof(T));  // [rows] row max
+  float* s_iz = s_m + rows;                                                           // [rows] 1 / row sum
   const int job = blockIdx.y, chunk = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int rows = a.NT * 16;
+  const int rg = lane >> 4;
   const bool sum_w = (a.flags & HC_SCORE_SUM_WINDOW) != 0;
   stage_queries<T>(a, job, s_q);
   for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
-    s_ml[2 * r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] : -INFINITY;
-    s_ml[2 * r + 1] = r < a.R ? stats[((int64_t)job * a.R + r) * 2 + 1] : 1.f;
+    s_m[r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] : -INFINITY;
+    s_iz[r] = r < a.R ? 1.f / stats[((int64_t)job * a.R + r) * 2 + 1] : 0.f;
   }
-  __syncthreads();
   const int wout = sum_w ? 1 : a.W;
   const int tw = chunk * kScoreChunk + wave * 16 * kSubTiles;
   typename Elem<T>::vec8 krs[kSubTiles][4];
 #pragma unroll
   for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, krs[u]);
+  __syncthreads();
+  float gsum[kSubTiles];  // running window sum per sub-tile (W >= 16)
 #pragma unroll
-  for (int u = 0; u < kSubTiles; ++u) {
-    const int t0 = tw + 16 * u;
-    if (t0 >= a.span) break;
-    const typename Elem<T>::vec8(&kr)[4] = krs[u];
-    float gsum[4] = {0.f, 0.f, 0.f, 0.f};  // running window sum (W >= 16)
-    for (int nt = 0; nt < a.NT; ++nt) {
-      float x[4];
-      subtile_logits<T>(a, kr, s_q, nt, t0, lane, x);
-      const int r = 16 * nt + (lane & 15);
-      const float M = s_ml[2 * r], Z = s_ml[2 * r + 1];
-      float p[4];
+  for (int u = 0; u < kSubTiles; ++u) gsum[u] = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        p[j] = (x[j] == -INFINITY || r >= a.R) ? 0.f : round_mode(fast_exp2(x[j] - M) / Z, a.flags);
-      if (!sum_w) {
-        // Row r = g*W + w -> A[job][w][g][t].
-        if (r < a.R) {
-          const int g = r / a.W, w = r % a.W;
-          float* o = A + (((int64_t)job * wout + w) * a.G + g) * a.span;
+  for (int nt = 0; nt < 16; ++nt) {
+    if (nt < a.NT) {
+      const int r0 = 16 * nt + 4 * rg;
+      float M[4], IZ[4];
+      int limit[4];
+      int64_t orow[4];  // output row of each j without the window sum: A[job][w][g]
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int t = t0 + 4 * (lane >> 4) + j;
-            if (t < a.span) o[t] = p[j];
-          }
-        }
-        continue;
+      for (int j = 0; j < 4; ++j) {
+        M[j] = s_m[r0 + j];
+        IZ[j] = s_iz[r0 + j];
+        limit[j] = row_limit(a, r0 + j);
+        if (!sum_w) orow[j] = (((int64_t)job * wout + (r0 + j) % a.W) * a.G + (r0 + j) / a.W) * a.span;
       }
-      if (a.W >= 16) {
-        // The 16 rows of this N-tile all belong to one query head.
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v = p[j];
-          v += __shfl_xor(v, 1, 64);
-          v += __shfl_xor(v, 2, 64);
-          v += __shfl_xor(v, 4, 64);
-          v += __shfl_xor(v, 8, 64);
-          gsum[j] += v;
-        }
-        if (((16 * (nt + 1)) % a.W) == 0) {
-          const int g = (16 * nt) / a.W;
-          if ((lane & 15) == 0 && g < a.G) {
-            float* o = A + ((int64_t)job * a.G + g) * a.span;
+      for (int u = 0; u < kSubTiles; ++u) {
+        const int t = tw + 16 * u + (lane & 15);
+        float x[4], p[4];
+        subtile_logits_rows<T>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int t = t0 + 4 * (lane >> 4) + j;
-              if (t < a.span) o[t] = round_mode(gsum[j], a.flags);
-            }
+        for (int j = 0; j < 4; ++j) p[j] = x[j] == -INFINITY ? 0.f : round_mode(fast_exp2(x[j] - M[j]) * IZ[j], a.flags);
+        if (!sum_w) {
+          // Row r = g*W + w -> A[job][w][g][t].
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (r0 + j < a.R && t < a.span) A[orow[j] + t] = p[j];
+        } else if (a.W >= 16) {
+          // The 16 rows of this tile all belong to one query head.
+          float v = (p[0] + p[1]) + (p[2] + p[3]);
+          v += __shfl_xor(v, 16, 64);
+          v += __shfl_xor(v, 32, 64);
+          gsum[u] += v;
+          if (((16 * (nt + 1)) % a.W) == 0) {
+            const int g = (16 * nt) / a.W;
+            if (rg == 0 && g < a.G && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_mode(gsum[u], a.flags);
+            gsum[u] = 0.f;
           }
+        } else if (a.W == 8) {
+          float v = (p[0] + p[1]) + (p[2] + p[3]);
+          v += __shfl_xor(v, 16, 64);
+          const int g = r0 / 8;
+          if ((rg & 1) == 0 && r0 < a.R && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_mode(v, a.flags);
+        } else if (a.W == 4) {
+          // A head's rows are the four j of this lane.
+          const float v = (p[0] + p[1]) + (p[2] + p[3]);
+          if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 4) * a.span + t] = round_mode(v, a.flags);
+        } else if (a.W == 2) {
+          const float v0 = p[0] + p[1], v1 = p[2] + p[3];
+          if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2) * a.span + t] = round_mode(v0, a.flags);
+          if (r0 + 2 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2 + 1) * a.span + t] = round_mode(v1, a.flags);
+        } else {
+          // W == 1: every row is its own query head.
 #pragma unroll
-          for (int j = 0; j < 4; ++j) gsum[j] = 0.f;
-        }
-      } else {
-        // W in {1, 2, 4, 8}: a query head's rows are W adjacent lanes.
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v = p[j];
-          for (int off = 1; off < a.W; off <<= 1) v += __shfl_xor(v, off, 64);
-          p[j] = v;
-        }
-        if ((lane & (a.W - 1)) == 0 && r < a.R) {
-          const int g = r / a.W;
-          float* o = A + ((int64_t)job * a.G + g) * a.span;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int t = t0 + 4 * (lane >> 4) + j;
-            if (t < a.span) o[t] = round_mode(p[j], a.flags);
-          }
+          for (int j = 0; j < 4; ++j)
+            if (r0 + j < a.R && t < a.span) A[((int64_t)job * a.G + r0 + j) * a.span + t] = round_mode(p[j], a.flags);
         }
       }
     }
