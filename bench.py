@@ -116,8 +116,9 @@ def full_step_phase(args, torch, dev):
     Runs twice on fresh caches: with a threshold no overlap can reach (drift
     checked, never triggered) and with one every overlap is below (every
     check retrieves), so the difference per step is the retrieval time the
-    decode step does not hide.  Also times the prefill compression of each
-    layer (scores, top-k, gathers and the tier copy).
+    decode step does not hide.  Also times the prefill of all layers: with
+    the full-KV tier in HBM (compression kernels alone) and in host-pinned
+    memory (bounded by the tier copy over the host link).
     """
     from heterocache_amd import utils, workloads
     from heterocache_amd.cache_utils import HeteroCache, HeteroCacheConfig
@@ -127,26 +128,46 @@ def full_step_phase(args, torch, dev):
     steps = args.full_steps
     res = {}
     g = torch.Generator(device=dev).manual_seed(args.seed)
-    for label, thr in (("no_trigger", -1.0), ("always_trigger", 2.0)):
-        cfg = HeteroCacheConfig(data, compression_ratio=args.ratio, stable_threshold=thr, real_offload=True,
+
+    def make_cache(thr, host_tier):
+        cfg = HeteroCacheConfig(data, compression_ratio=args.ratio, stable_threshold=thr, real_offload=host_tier,
                                 max_gen_len=steps + 8, decode_step=5, pooling="avgpool", kernel_size=5,
                                 num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024)
-        cache = HeteroCache(cfg)
-        pre_ms = 0.0
+        return HeteroCache(cfg)
+
+    def prefill(cache):
+        """All layers' prefill on resident inputs: main-stream ms per layer
+        (events) and total ms until every stream is idle (tier copies
+        included)."""
+        ks = [torch.randn((1, Hkv, L, D), device=dev, generator=g, dtype=torch.bfloat16) for _ in range(NL)]
+        vs = [torch.randn((1, Hkv, L, D), device=dev, generator=g, dtype=torch.bfloat16) for _ in range(NL)]
+        q = torch.randn((1, Hkv * G, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
         for layer in range(NL):
-            k = torch.randn((1, Hkv, L, D), device=dev, generator=g, dtype=torch.bfloat16)
-            v = torch.randn((1, Hkv, L, D), device=dev, generator=g, dtype=torch.bfloat16)
-            q = torch.randn((1, Hkv * G, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            cache.update(k, v, layer)
-            cache.init_coefficient(q, k, layer)
-            cache.prefill_select(q, k, v, layer)
-            e1.record()
-            torch.cuda.synchronize()
-            pre_ms += e0.elapsed_time(e1)
-            del k, v
+            cache.update(ks[layer], vs[layer], layer)
+            cache.init_coefficient(q, ks[layer], layer)
+            cache.prefill_select(q, ks[layer], vs[layer], layer)
+        e1.record()
+        torch.cuda.synchronize()
+        total = (time.perf_counter() - t0) * 1e3
+        del ks, vs
+        return e0.elapsed_time(e1) / NL, total
+
+    # Compression alone: the full-KV tier stays in HBM (no host-link copy).
+    # The first prefill pays one-time costs (arena and workspace allocation,
+    # library load) and is reported separately.
+    cache = make_cache(-1.0, False)
+    _, first_total = prefill(cache)
+    del cache
+    cache = make_cache(-1.0, False)
+    hbm_layer_ms, hbm_total = prefill(cache)
+    del cache
+    for label, thr in (("no_trigger", -1.0), ("always_trigger", 2.0)):
+        cache = make_cache(thr, True)
+        pre_ms, pre_total = prefill(cache)
         qs = torch.randn((steps + 5, NL, 1, Hkv * G, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
         kn = torch.randn((steps + 5, NL, 1, Hkv, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
 
@@ -168,7 +189,7 @@ def full_step_phase(args, torch, dev):
         torch.cuda.synchronize()
         res[label] = {"ms_per_step": e0.elapsed_time(e1) / steps,
                       "wall_ms_per_step": (time.perf_counter() - t0) * 1e3 / steps,
-                      "prefill_compress_ms_per_layer": pre_ms / NL}
+                      "prefill_main_ms_per_layer": pre_ms, "prefill_total_ms": pre_total}
         trig = [int(cache._drift[l].trigger.sum().item()) for l in range(NL) if cache._drift[l] is not None
                 and cache._drift[l].trigger is not None]
         res[label]["leaders_triggered_last_check"] = int(sum(trig))
@@ -176,6 +197,7 @@ def full_step_phase(args, torch, dev):
         torch.cuda.empty_cache()
     # Retrieval bytes per check: every satellite gathers min(cap, 1024) K and V rows.
     sats = sum(len(r) for r in data["need_to_update_counts"])
+    tier_bytes = sats * L * D * 2 * 2  # satellites' full K and V, written once over the host link
     per_check = sats * 1024 * D * 2 * 2
     exposed = (res["always_trigger"]["ms_per_step"] - res["no_trigger"]["ms_per_step"]) * 5
     return {"steps": steps, "decode_step": 5, "retrieval_topk": 1024, "satellites": sats,
@@ -183,13 +205,70 @@ def full_step_phase(args, torch, dev):
             "ms_per_step_no_retrieval": round(res["no_trigger"]["ms_per_step"], 4),
             "ms_per_step_retrieval_every_check": round(res["always_trigger"]["ms_per_step"], 4),
             "retrieval_exposed_ms_per_check": round(exposed, 4),
-            "prefill_compress_ms_per_layer": round(res["no_trigger"]["prefill_compress_ms_per_layer"], 3),
-            "leaders_triggered_last_check": res["always_trigger"]["leaders_triggered_last_check"]}
+            "leaders_triggered_last_check": res["always_trigger"]["leaders_triggered_last_check"],
+            "prefill": {"compress_ms_per_layer_hbm_tier": round(hbm_layer_ms, 3),
+                        "total_ms_hbm_tier": round(hbm_total, 1),
+                        "first_prefill_total_ms_hbm_tier": round(first_total, 1),
+                        "total_ms_host_tier": round(res["always_trigger"]["prefill_total_ms"], 1),
+                        "host_tier_bytes": tier_bytes,
+                        "host_tier_link_gbs": round(tier_bytes / res["always_trigger"]["prefill_total_ms"] / 1e6, 1)}}
+
+
+def gather_phase(args, torch, dev):
+    """hc_gather_store throughput at the bench shape.
+
+    device: each of 8 heads keeps an ascending random half of its L
+    positions (the prefill compressed-head gather) from device K/V
+    [1, 8, L, 128]; algorithmic bytes = every kept K and V row read once and
+    written once.  host: retrieval-style, 64 satellite rows x top-1024 from a
+    host-pinned tier [1, 64, 16384, 128]; bytes = rows read over the link.
+    """
+    import numpy as np
+    from heterocache_amd.store import KVStore
+    L, H, D = args.ctx, 8, 128
+    g = torch.Generator(device=dev).manual_seed(args.seed + 7)
+    k = torch.randn((1, H, L, D), device=dev, generator=g, dtype=torch.bfloat16)
+    v = torch.randn((1, H, L, D), device=dev, generator=g, dtype=torch.bfloat16)
+    n = L // 2
+    idx = torch.sort(torch.randperm(L, device=dev, generator=g)[:n])[0].to(torch.int32)
+    idx = idx.repeat(H, 1).contiguous()
+    st = KVStore([n] * H, torch.bfloat16, dev)
+
+    def timed(fn, reps=5):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    plan = st.plan_rows(k, [(0, h) for h in range(H)], list(range(H)), [n] * H, idx=idx)
+    ms = timed(lambda: st.launch_rows(plan, k, v, idx=idx, set_len=False))
+    dbytes = H * n * D * 2 * 2 * 2  # K and V rows, read + write
+    out = {"device_src": {"ms": round(ms, 4), "tokens": H * n, "gbs": round(dbytes / ms / 1e6, 1),
+                          "pct_of_hbm_peak": round(100 * dbytes / ms / 1e6 / HBM_PEAK_GBS, 2)}}
+    del k, v, st, idx
+    R, LT, M = 64, 16384, 1024
+    kc = torch.randn((1, R, LT, D), dtype=torch.bfloat16).pin_memory()
+    vc = torch.randn((1, R, LT, D), dtype=torch.bfloat16).pin_memory()
+    rng = np.random.default_rng(args.seed)
+    hidx = torch.as_tensor(np.stack([np.sort(rng.choice(LT, M, replace=False)) for _ in range(R)]).astype(np.int32))
+    hidx = hidx.to(dev)
+    st = KVStore([M] * R, torch.bfloat16, dev)
+    plan = st.plan_rows(kc, [(0, r) for r in range(R)], list(range(R)), [M] * R, idx=hidx)
+    ms = timed(lambda: st.launch_rows(plan, kc, vc, idx=hidx, src_is_host=True, set_len=False))
+    hbytes = R * M * D * 2 * 2
+    out["host_src"] = {"ms": round(ms, 4), "tokens": R * M, "link_gbs": round(hbytes / ms / 1e6, 1)}
+    return out
 
 
 def window_scoring_phase(args, torch, dev):
     """SnapKV-style window scoring (W = 32, GQA 4, 8 KV heads) of one layer at
-    the bench context: MFMA rate of the two logit passes."""
+    the bench context.  The MFMA figure counts the algorithmic product once;
+    the kernels form the logits twice (statistics pass, probability pass)."""
     from heterocache_amd import compress
     L, Hkv, G, W, D = args.ctx, 8, 4, 32, 128
     q = torch.randn((1, Hkv * G, W, D), device=dev, dtype=torch.bfloat16)
@@ -204,10 +283,11 @@ def window_scoring_phase(args, torch, dev):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / n
-    flops = 2 * 2 * Hkv * G * W * L * D  # two logit passes (statistics, probabilities)
-    kbytes = 2 * Hkv * L * D * 2          # K read once per pass
-    return {"ms_per_layer": round(ms, 4), "tflops": round(flops / ms / 1e9, 2),
+    flops = 2 * Hkv * G * W * L * D  # algorithmic: one logit product (the kernels compute it twice)
+    kbytes = 2 * Hkv * L * D * 2     # K read once per pass, two passes
+    return {"ms_per_layer": round(ms, 4), "tflops_algorithmic": round(flops / ms / 1e9, 2),
             "mfma_util_vs_bf16_dense_peak": round(flops / ms / 1e9 / 2500.0, 4),
+            "tflops_executed": round(2 * flops / ms / 1e9, 2),
             "k_read_gbs": round(kbytes / ms / 1e6, 1), "window": W, "ctx": L}
 
 
@@ -309,6 +389,7 @@ def main():
     if not args.no_full_step:
         rec["full_decode_step"] = full_step_phase(args, torch, dev)
         rec["window_scoring"] = window_scoring_phase(args, torch, dev)
+        rec["gather"] = gather_phase(args, torch, dev)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(L, budgets[0], args.cpu_seconds)
     print(json.dumps(rec))

@@ -112,6 +112,9 @@ class _LayerDrift:
 class HeteroCache(DynamicCache):
     """Compressed per-head KV cache (heterocache/cache_utils.py:610)."""
 
+    # Workgroups of the prefill copy into the host-pinned tier.
+    TIER_COPY_WORKGROUPS = 32
+
     def __init__(self, cache_config):
         super().__init__()
         cfg = cache_config
@@ -255,22 +258,26 @@ class HeteroCache(DynamicCache):
             self.value_cache_cpu[layer_idx] = value_states.detach()
             self._tier_heads[layer_idx] = {h: h for h in sats}
             return
-        main = torch.cuda.current_stream(key_states.device)
-        side = self._side_stream(key_states.device)
-        shape = (self.bsz, len(sats), key_states.shape[-2], self.head_dim)
+        dev = key_states.device
+        main = torch.cuda.current_stream(dev)
+        side = self._side_stream(dev)
+        L = key_states.shape[-2]
+        shape = (self.bsz, len(sats), L, self.head_dim)
         kc = torch.empty(shape, dtype=key_states.dtype, pin_memory=True)
         vc = torch.empty(shape, dtype=value_states.dtype, pin_memory=True)
-        idx = torch.tensor(sats, dtype=torch.long, device=key_states.device)
-        ksrc = key_states.index_select(1, idx)
-        vsrc = value_states.index_select(1, idx)
+        src = [(b, h) for b in range(self.bsz) for h in sats]
+        dst = [(b, i) for b in range(self.bsz) for i in range(len(sats))]
         side.wait_stream(main)
+        # A few workgroups write the satellites' rows straight from the
+        # prefill tensors into the pinned tier at link speed, beside the
+        # compression kernels on the main stream.
+        ops.copy_rows(key_states, value_states, src, kc, vc, dst, [L] * len(src), dst_is_host=True,
+                      max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
         with torch.cuda.stream(side):
-            kc.copy_(ksrc, non_blocking=True)
-            vc.copy_(vsrc, non_blocking=True)
             ev = torch.cuda.Event()
             ev.record(side)
-        ksrc.record_stream(side)
-        vsrc.record_stream(side)
+        key_states.record_stream(side)
+        value_states.record_stream(side)
         self.key_cache_cpu[layer_idx] = kc
         self.value_cache_cpu[layer_idx] = vc
         self._tier_heads[layer_idx] = {h: i for i, h in enumerate(sats)}

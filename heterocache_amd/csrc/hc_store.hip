@@ -12,6 +12,13 @@
 //                    (heterocache/cache_utils.py:970-1005).
 //   hc_store_read    unpack store slots [0, count) of rows back to natural
 //                    layout (diagnostics and tests).
+//   hc_copy_rows     natural-layout token rows of selected heads copied to a
+//                    natural-layout destination, typically the host-pinned
+//                    full-KV tier (heterocache/cache_utils.py:939-967), by a
+//                    capped number of workgroups so the copy runs at link
+//                    speed beside compute instead of occupying the device.
+#include <algorithm>
+
 #include "hc_common.h"
 #include "hc_internal.h"
 
@@ -152,6 +159,51 @@ static int launch_gather_store(const void* src_k, const void* src_v, const int64
   return check_launch("hc_gather_store");
 }
 
+// Work item = (job, 32-token chunk); workgroups stride over the items, so a
+// small grid streams any amount.  Rows are moved as 16-byte vectors.
+constexpr int kCopyChunk = 32;
+
+__global__ __launch_bounds__(256) void copy_rows_kernel(const uint8_t* __restrict__ src_k,
+                                                       const uint8_t* __restrict__ src_v,
+                                                       const int64_t* __restrict__ src_off, int64_t src_stride_b,
+                                                       uint8_t* __restrict__ dst_k, uint8_t* __restrict__ dst_v,
+                                                       const int64_t* __restrict__ dst_off, int64_t dst_stride_b,
+                                                       const int32_t* __restrict__ count, int njobs,
+                                                       int chunks_per_job, int vecs_per_row, int esz) {
+  const int64_t items = (int64_t)njobs * chunks_per_job;
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+    const int job = (int)(item / chunks_per_job), chunk = (int)(item % chunks_per_job);
+    const int t0 = chunk * kCopyChunk;
+    const int valid = min(kCopyChunk, count[job] - t0);
+    if (valid <= 0) continue;
+    const int64_t so = (src_off[job] * esz) + (int64_t)t0 * src_stride_b;
+    const int64_t dofs = (dst_off[job] * esz) + (int64_t)t0 * dst_stride_b;
+    const int n = valid * vecs_per_row;
+    for (int c0 = threadIdx.x; c0 < n; c0 += 2 * 256) {
+      // Two vectors of K and two of V in flight per thread.
+      u32x4 a[2], b[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int c = c0 + u * 256;
+        if (c < n) {
+          const int64_t off = (int64_t)(c / vecs_per_row) * src_stride_b + (c % vecs_per_row) * 16;
+          a[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src_k + so + off));
+          b[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src_v + so + off));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int c = c0 + u * 256;
+        if (c < n) {
+          const int64_t off = (int64_t)(c / vecs_per_row) * dst_stride_b + (c % vecs_per_row) * 16;
+          *reinterpret_cast<u32x4*>(dst_k + dofs + off) = a[u];
+          *reinterpret_cast<u32x4*>(dst_v + dofs + off) = b[u];
+        }
+      }
+    }
+  }
+}
+
 // Translate a pointer into host-pinned memory to its device-mapped address.
 static int map_host_ptr(const void* host, const void** dev) {
   void* d = nullptr;
@@ -255,4 +307,42 @@ extern "C" int hc_store_read(int dtype, const void* kstore, const void* vstore, 
       return set_error(HC_ERR_INVALID, "hc_store_read: unknown dtype %d", dtype);
   }
 #undef HC_READ
+}
+
+extern "C" int hc_copy_rows(int dtype, const void* src_k, const void* src_v, const int64_t* src_off,
+                            int64_t src_tok_stride, void* dst_k, void* dst_v, int dst_is_host, const int64_t* dst_off,
+                            int64_t dst_tok_stride, const int32_t* count, int njobs, int max_count,
+                            int max_workgroups, void* stream) {
+  clear_error();
+  const int esz = dtype == HC_DTYPE_F32 ? 4 : (dtype == HC_DTYPE_BF16 || dtype == HC_DTYPE_F16) ? 2 : 0;
+  if (esz == 0) return set_error(HC_ERR_INVALID, "hc_copy_rows: unknown dtype %d", dtype);
+  if (njobs < 0 || max_count < 0 || max_workgroups < 1)
+    return set_error(HC_ERR_INVALID, "hc_copy_rows: njobs=%d max_count=%d max_workgroups=%d", njobs, max_count,
+                     max_workgroups);
+  if (njobs == 0 || max_count == 0) return HC_OK;
+  if (!src_k || !src_v || !src_off || !dst_k || !dst_v || !dst_off || !count)
+    return set_error(HC_ERR_INVALID, "hc_copy_rows: null pointer argument");
+  if (src_tok_stride < HC_HEAD_DIM || dst_tok_stride < HC_HEAD_DIM || (src_tok_stride * esz) % 16 ||
+      (dst_tok_stride * esz) % 16)
+    return set_error(HC_ERR_INVALID, "hc_copy_rows: token strides must be >= 128 elements and 16-byte multiples");
+  if (((uintptr_t)src_k | (uintptr_t)src_v | (uintptr_t)dst_k | (uintptr_t)dst_v) % 16)
+    return set_error(HC_ERR_INVALID, "hc_copy_rows: buffers must be 16-byte aligned");
+  void* dk = dst_k;
+  void* dv = dst_v;
+  if (dst_is_host) {
+    const void* m = nullptr;
+    int rc = map_host_ptr(dst_k, &m);
+    if (rc) return rc;
+    dk = const_cast<void*>(m);
+    rc = map_host_ptr(dst_v, &m);
+    if (rc) return rc;
+    dv = const_cast<void*>(m);
+  }
+  const int chunks = (max_count + kCopyChunk - 1) / kCopyChunk;
+  const int64_t items = (int64_t)njobs * chunks;
+  const unsigned grid = (unsigned)std::min<int64_t>(items, max_workgroups);
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src_k,
+                     (const uint8_t*)src_v, src_off, src_tok_stride * esz, (uint8_t*)dk, (uint8_t*)dv, dst_off,
+                     dst_tok_stride * esz, count, njobs, chunks, HC_HEAD_DIM * esz / 16, esz);
+  return check_launch("hc_copy_rows");
 }

@@ -171,6 +171,57 @@ def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, c
                                    int(max_count), _ptr(trigger), _ptr(trig_of), _stream(stream, kstore)))
 
 
+def copy_rows(src_k, src_v, src_bh, dst_k, dst_v, dst_bh, counts, dst_is_host=False, max_workgroups=32,
+              stream=None):
+    """dst[b', h', t] = src[b, h, t] for t < counts[j], (b, h) = src_bh[j], (b', h') = dst_bh[j].
+
+    src / dst: [B, H, L, 128] tensors with unit channel stride; dst may be a
+    pinned CPU tensor (dst_is_host).  At most max_workgroups workgroups run
+    the copy.  With `stream`, that stream first waits for the current one
+    (which builds the small offset tensors).
+    """
+    lib = _lib.load()
+    _require_cuda(src_k, src_v)
+    if dst_is_host:
+        if dst_k.is_cuda or not dst_k.is_pinned() or not dst_v.is_pinned():
+            raise ValueError("host destinations must be pinned CPU tensors")
+    else:
+        _require_cuda(dst_k, dst_v)
+    for t in (src_k, src_v, dst_k, dst_v):
+        if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+            raise ValueError("sources and destinations must be [B, H, L, 128] with unit channel stride")
+    if src_k.stride() != src_v.stride() or dst_k.stride() != dst_v.stride():
+        raise ValueError("K and V must share strides")
+    if not (src_k.dtype == src_v.dtype == dst_k.dtype == dst_v.dtype):
+        raise TypeError("sources and destinations must share a dtype")
+    src_bh = np.asarray(src_bh, dtype=np.int64).reshape(-1, 2)
+    dst_bh = np.asarray(dst_bh, dtype=np.int64).reshape(-1, 2)
+    counts = np.asarray(counts, dtype=np.int64)
+    if not (len(src_bh) == len(dst_bh) == len(counts)):
+        raise ValueError("one source head, destination head and count per job")
+    if len(counts) == 0:
+        return
+    for bh, t in ((src_bh, src_k), (dst_bh, dst_k)):
+        if (bh < 0).any() or (bh[:, 0] >= t.shape[0]).any() or (bh[:, 1] >= t.shape[1]).any():
+            raise ValueError("head index out of range")
+    if (counts < 0).any() or (counts > src_k.shape[2]).any() or (counts > dst_k.shape[2]).any():
+        raise ValueError("count exceeds a source or destination length")
+    dev = src_k.device
+    src_off = torch.as_tensor(src_bh[:, 0] * src_k.stride(0) + src_bh[:, 1] * src_k.stride(1)).to(dev)
+    dst_off = torch.as_tensor(dst_bh[:, 0] * dst_k.stride(0) + dst_bh[:, 1] * dst_k.stride(1)).to(dev)
+    cnt = torch.as_tensor(counts.astype(np.int32)).to(dev)
+    if stream is not None:
+        # The launch stream waits for the offsets (and whatever produced the
+        # sources) on the current stream.
+        stream.wait_stream(torch.cuda.current_stream(dev))
+        for t in (src_off, dst_off, cnt):
+            t.record_stream(stream)
+    _lib.check(lib.hc_copy_rows(dtype_code(src_k.dtype), _ptr(src_k), _ptr(src_v), _ptr(src_off), src_k.stride(2),
+                                _ptr(dst_k), _ptr(dst_v), int(bool(dst_is_host)), _ptr(dst_off), dst_k.stride(2),
+                                _ptr(cnt), len(counts), int(counts.max()), int(max_workgroups),
+                                _stream(stream, src_k)))
+
+
 def append(k_new, v_new, kstore, vstore, row_tile_off, row_len, row_cap, status=None, stream=None):
     """Write k_new/v_new [rows, 128] at slot row_len[r] of every row, then row_len += 1."""
     lib = _lib.load()

@@ -119,6 +119,21 @@ int hc_append(int dtype, const void* k_new, const void* v_new, int64_t src_row_s
 int hc_store_read(int dtype, const void* kstore, const void* vstore, const int64_t* row_tile_off,
                   const int32_t* rows_sel, int nrows, int count, void* dst_k, void* dst_v, void* stream);
 
+/*
+ * Copy token rows [0, count[j]) (128 channels each) of K and V between two
+ * natural layouts:
+ *   dst[dst_off[j] + t*dst_tok_stride + c] = src[src_off[j] + t*src_tok_stride + c]
+ * (offsets and strides in elements; rows 16-byte aligned).  With
+ * dst_is_host != 0 the destination is host-pinned memory written through its
+ * device mapping.  At most max_workgroups workgroups stride over the work, so
+ * a copy to the host link can run beside compute without occupying the
+ * device.  Replaces the D2H copy of the satellite heads' full K/V into the
+ * pinned tier (heterocache/cache_utils.py:939-967).
+ */
+int hc_copy_rows(int dtype, const void* src_k, const void* src_v, const int64_t* src_off, int64_t src_tok_stride,
+                 void* dst_k, void* dst_v, int dst_is_host, const int64_t* dst_off, int64_t dst_tok_stride,
+                 const int32_t* count, int njobs, int max_count, int max_workgroups, void* stream);
+
 /* hc_score flags */
 #define HC_SCORE_CAUSAL_WINDOW 1 /* window row w sees keys t <= L - W + w (kv_cluster.py:169-175) */
 #define HC_SCORE_SUM_WINDOW 2    /* sum probabilities over the W rows of a query head (kv_cluster.py:178) */

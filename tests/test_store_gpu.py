@@ -126,3 +126,36 @@ def test_append_capacity_error(dev):
     with pytest.raises(RuntimeError, match="OOM"):
         store.append(kn, kn)
     assert store.host_len.tolist() == [32, 10]
+
+
+@pytest.mark.parametrize("to_host", [False, True])
+def test_copy_rows_strided_source_small_grid(dev, to_host):
+    """hc_copy_rows: selected heads of a transposed-view source into another
+    layout (device or host-pinned), bit-exact, with a grid smaller than the
+    work and counts below the length."""
+    from heterocache_amd import ops
+    B, H, L = 2, 5, 700
+    g = torch.Generator().manual_seed(21)
+    k = torch.randn((B, L, H, 128), generator=g).to(torch.bfloat16).to(dev).transpose(1, 2)
+    v = torch.randn((B, L, H, 128), generator=g).to(torch.bfloat16).to(dev).transpose(1, 2)
+    shape = (B, 3, L, 128)
+    if to_host:
+        dk = torch.zeros(shape, dtype=torch.bfloat16).pin_memory()
+        dv = torch.zeros(shape, dtype=torch.bfloat16).pin_memory()
+    else:
+        dk = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+        dv = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+    src = [(0, 4), (1, 1), (0, 0), (1, 3)]
+    dst = [(1, 2), (0, 0), (0, 1), (1, 0)]
+    counts = [L, 33, 1, 650]
+    side = torch.cuda.Stream()
+    ops.copy_rows(k, v, src, dk, dv, dst, counts, dst_is_host=to_host, max_workgroups=3, stream=side)
+    torch.cuda.synchronize()
+    dk, dv = dk.cpu(), dv.cpu()
+    kc, vc = k.cpu(), v.cpu()
+    for (b, h), (b2, h2), n in zip(src, dst, counts):
+        assert torch.equal(dk[b2, h2, :n], kc[b, h, :n]) and torch.equal(dv[b2, h2, :n], vc[b, h, :n])
+        assert not dk[b2, h2, n:].any()
+    ek = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match="count exceeds"):
+        ops.copy_rows(k, v, [(0, 0)], ek, ek.clone(), [(0, 0)], [L + 1])
