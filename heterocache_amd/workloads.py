@@ -97,3 +97,38 @@ def row_budgets(data, layer, seq_len, compression_ratio, num_layers, num_kv_head
         else:
             out.append(int(min(np.trunc(np.float32(base) * alloc[h]), seq_len)))
     return np.tile(np.asarray(out, dtype=np.int64), batch), base
+
+
+def config0_inputs(seed=1000, seq_len=4096, q_heads=32, kv_heads=8, window=32, outlier_channels=4,
+                   outlier_scale=8.0, sinks=4, compression_ratio=0.5, weights=(0.5, 1.5)):
+    """One Llama-3-8B-shape layer for the CPU-runnable reference case.
+
+    float32 q [1, Hq, L, 128] (the last `window` rows are the observation
+    window), K/V [1, Hkv, L, 128] ~ N(0, 1) with `outlier_channels` seeded
+    channels per head scaled by `outlier_scale`; positions [0, sinks) hold
+    attention-sink keys equal to twice the mean window query of the head's
+    group.  A seeded half of the KV heads gets allocation weight weights[0],
+    the rest weights[1]; budgets are the float32 caps of
+    get_compress_len(ratio, 0, L, Hkv) times the weight.  One decode step of
+    fresh q / k / v follows.
+    """
+    rng = np.random.default_rng(seed)
+    d, G = 128, q_heads // kv_heads
+    q = rng.standard_normal((1, q_heads, seq_len, d)).astype(np.float32)
+    k = rng.standard_normal((1, kv_heads, seq_len, d)).astype(np.float32)
+    v = rng.standard_normal((1, kv_heads, seq_len, d)).astype(np.float32)
+    for h in range(kv_heads):
+        ch = rng.choice(d, outlier_channels, replace=False)
+        k[0, h][:, ch] *= outlier_scale
+        v[0, h][:, ch] *= outlier_scale
+        k[0, h, :sinks] = 2.0 * q[0, h * G:(h + 1) * G, seq_len - window:].mean(axis=(0, 1))
+    perm = rng.permutation(kv_heads)
+    alloc = np.empty(kv_heads)
+    alloc[perm[:kv_heads // 2]] = weights[0]
+    alloc[perm[kv_heads // 2:]] = weights[1]
+    base = get_compress_len(compression_ratio, 0, seq_len, kv_heads)
+    caps = np.minimum(np.trunc(np.float32(base) * alloc.astype(np.float32)).astype(np.int64), seq_len)
+    return {"q": q, "k": k, "v": v, "caps": caps, "alloc": alloc, "base": base, "window": window,
+            "q_dec": rng.standard_normal((1, q_heads, 1, d)).astype(np.float32),
+            "k_dec": rng.standard_normal((1, kv_heads, 1, d)).astype(np.float32),
+            "v_dec": rng.standard_normal((1, kv_heads, 1, d)).astype(np.float32)}

@@ -308,3 +308,24 @@ def test_allocation_ratios_average_one():
     assert abs(np.mean(vals) - 1.0) < 1e-9
     s0 = [s for row in st for s in row if s > -0.5]
     assert vals[int(np.argmin(s0))] == max(vals)  # least stable head gets the most
+
+
+def test_config0_inputs_and_oracle_pipeline():
+    """The config-0 generator (budgets 1024/3072 from base 2048, sink keys
+    at 0-3) and the oracle's SnapKV pipeline on it: every head keeps its
+    observation window and exactly its cap, in ascending order."""
+    from heterocache_amd import workloads
+    c = workloads.config0_inputs()
+    L, W = 4096, c["window"]
+    assert c["base"] == 2048
+    assert sorted(c["caps"].tolist()) == [1024] * 4 + [3072] * 4
+    for h in range(8):
+        assert np.allclose(c["k"][0, h, :4], 2 * c["q"][0, 4 * h:4 * h + 4, L - W:].mean(axis=(0, 1)))
+    G = 4
+    qw = np.stack([c["q"][0, h * G:(h + 1) * G, L - W:] for h in range(8)])
+    s = O.window_scores(qw, c["k"][0], "maxpool", 7, window_keep=True)
+    for h in range(8):
+        kept = O.select_with_window(s[h], int(c["caps"][h]), L, W)
+        assert len(kept) == c["caps"][h]
+        assert kept[-W:].tolist() == list(range(L - W, L))
+        assert np.all(np.diff(kept) > 0)
