@@ -137,7 +137,8 @@ __device__ __forceinline__ void merge_ml(float& m, float& l, float m2, float l2)
 }
 
 template <typename T, bool STORE>
-__global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs a, float* __restrict__ part) {
+__global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs a, float* __restrict__ part,
+                                                                      float* __restrict__ logits) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_q = reinterpret_cast<T*>(smem);
   float* s_st = reinterpret_cast<float*>(smem + (size_t)a.NT * 16 * kQPitch * sizeof(T));  // [waves][rows][2]
@@ -168,6 +169,20 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
       for (int u = 0; u < kSubTiles; ++u) {
         float x[4];
         subtile_logits<T>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
+        if (logits) {
+          // Row r, tokens t..t+3 (16 bytes) of the job's [R][span] logits.
+          const int r = 16 * nt + (lane & 15), t = tw + 16 * u + 4 * (lane >> 4);
+          if (r < a.R && t < a.span) {
+            float* o = logits + ((int64_t)job * a.R + r) * a.span + t;
+            if (t + 4 <= a.span && (a.span & 3) == 0) {
+              *reinterpret_cast<f32x4*>(o) = f32x4{x[0], x[1], x[2], x[3]};
+            } else {
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                if (t + j < a.span) o[j] = x[j];
+            }
+          }
+        }
         const float mn = fmaxf(fmaxf(m[nt], fmaxf(x[0], x[1])), fmaxf(x[2], x[3]));
         if (mn != -INFINITY) {
           float sm = 0.f;
@@ -368,14 +383,77 @@ __global__ __launch_bounds__(kPoolThreads) void score_pool_kernel(const float* _
   if (t < span) S[(int64_t)jw * span + t] = best;
 }
 
+// Small query sets (R < 32 rows): the statistics pass stored the logits,
+// so probabilities, the window sum, pooling and the group max are formed in
+// one pass over them instead of a second pass over K.  One workgroup per
+// (job, w', kFinTile positions); each query head's strip plus its pooling
+// halo is built in LDS.
+constexpr int kFinTile = 1024;
+
+__global__ __launch_bounds__(256) void score_finish_kernel(const float* __restrict__ logits,
+                                                           const float* __restrict__ stats, int R, int G, int W,
+                                                           int span, int sum_w, int pooling, int kernel, int flags,
+                                                           float* __restrict__ S) {
+  __shared__ float s_a[kFinTile + 2 * kPoolMaxHalf];
+  const int wout = sum_w ? 1 : W;
+  const int job = blockIdx.y / wout, wo = blockIdx.y % wout;
+  const int t0 = blockIdx.x * kFinTile;
+  const int p = kernel / 2;
+  const float pad = pooling == 0 ? 0.f : -INFINITY;
+  float best[kFinTile / 256];
+#pragma unroll
+  for (int i = 0; i < kFinTile / 256; ++i) best[i] = -INFINITY;
+  for (int g = 0; g < G; ++g) {
+    const int w_lo = sum_w ? 0 : wo, w_hi = sum_w ? W : wo + 1;
+    __syncthreads();
+    for (int i = threadIdx.x; i < kFinTile + 2 * p; i += 256) {
+      const int t = t0 - p + i;
+      float acc = pad;
+      if (t >= 0 && t < span) {
+        acc = 0.f;
+        for (int w = w_lo; w < w_hi; ++w) {
+          const int r = g * W + w;
+          const float M = stats[((int64_t)job * R + r) * 2], Z = stats[((int64_t)job * R + r) * 2 + 1];
+          const float x = logits[((int64_t)job * R + r) * span + t];
+          acc += x == -INFINITY ? 0.f : round_mode(fast_exp2(x - M) * (1.f / Z), flags);
+        }
+        acc = round_mode(acc, flags);
+      }
+      s_a[i] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kFinTile / 256; ++i) {
+      const int c = threadIdx.x + 256 * i;
+      float v = pad;
+      for (int d = 0; d <= 2 * p; ++d) {
+        const float x = s_a[c + d];
+        v = pooling == 0 ? v + x : fmaxf(v, x);
+      }
+      if (pooling == 0) v = v / (float)kernel;
+      best[i] = fmaxf(best[i], round_mode(v, flags));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kFinTile / 256; ++i) {
+    const int t = t0 + threadIdx.x + 256 * i;
+    if (t < span) S[((int64_t)job * wout + wo) * span + t] = best[i];
+  }
+}
+
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Query sets below this many rows take the logit-store path.
+constexpr int kLogitRows = 32;
 
 size_t score_workspace_bytes(int njobs, int L, int G, int W, int flags) {
   const int R = G * W;
   const int nchunks = (L + kScoreChunk - 1) / kScoreChunk;
   const int wout = (flags & HC_SCORE_SUM_WINDOW) ? 1 : W;
+  const size_t tail = R < kLogitRows ? (size_t)njobs * R * L * sizeof(float)          // logits
+                                     : (size_t)njobs * wout * G * L * sizeof(float);  // probabilities
   return align256((size_t)njobs * nchunks * R * 2 * sizeof(float)) +
-         align256((size_t)njobs * R * 2 * sizeof(float)) + align256((size_t)njobs * wout * G * L * sizeof(float));
+         align256((size_t)njobs * R * 2 * sizeof(float)) + align256(tail);
 }
 
 template <typename T, bool STORE>
@@ -389,12 +467,23 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   const size_t qbytes = (size_t)a.NT * 16 * kQPitch * sizeof(T);
   const size_t lds1 = qbytes + (size_t)kScoreWaves * a.NT * 16 * 2 * sizeof(float);
   const size_t lds3 = qbytes + (size_t)a.NT * 16 * 2 * sizeof(float);
-  hipLaunchKernelGGL((score_stats_kernel<T, STORE>), dim3(nchunks, njobs), dim3(kScoreWaves * 64), lds1, s, a, part);
+  const bool via_logits = a.R < kLogitRows;
+  hipLaunchKernelGGL((score_stats_kernel<T, STORE>), dim3(nchunks, njobs), dim3(kScoreWaves * 64), lds1, s, a, part,
+                     via_logits ? A : nullptr);
   int rc = check_launch("hc_score(stats)");
   if (rc) return rc;
   hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nchunks, a.R,
                      njobs, stats);
   if ((rc = check_launch("hc_score(merge)"))) return rc;
+  if (via_logits) {
+    if (a.span > 0) {
+      hipLaunchKernelGGL(score_finish_kernel, dim3((a.span + kFinTile - 1) / kFinTile, njobs * wout), dim3(256), 0,
+                         s, A, stats, a.R, a.G, a.W, a.span, (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : 0, pooling, kernel,
+                         a.flags, scores);
+      if ((rc = check_launch("hc_score(finish)"))) return rc;
+    }
+    return HC_OK;
+  }
   const int nchunks_span = (a.span + kScoreChunk - 1) / kScoreChunk;
   if (nchunks_span > 0) {
     hipLaunchKernelGGL((score_probs_kernel<T, STORE>), dim3(nchunks_span, njobs), dim3(kScoreWaves * 64), lds3, s, a,
@@ -435,6 +524,9 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
   if (kernel < 1 || (kernel % 2) == 0 || kernel > 63)
     return set_error(HC_ERR_INVALID, "hc_score: pooling kernel must be odd and <= 63 (got %d)", kernel);
   const int R = group * window;
+  if ((int64_t)njobs * ((flags & HC_SCORE_SUM_WINDOW) ? 1 : window) > 65535)
+    return set_error(HC_ERR_INVALID, "hc_score: njobs x window rows %lld exceed 65535",
+                     (long long)njobs * window);
   int NT = (R + 15) / 16;
   if (NT > 16) return set_error(HC_ERR_INVALID, "hc_score: group*window = %d exceeds 256 rows", R);
   if (dtype == HC_DTYPE_F32 && NT > 8)
