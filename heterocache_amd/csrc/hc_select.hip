@@ -37,6 +37,8 @@ constexpr int kSelChunk = 4096;                      // positions per workgroup
 constexpr int kSelRows = kSelChunk / kSelThreads;    // 16 rows of 256 positions
 constexpr int kSelBins = 256;
 constexpr int kSelMaxChunks = 4096;
+constexpr int kSelMatch = 6;  // digits aggregated per wave before per-lane atomics
+constexpr int kSelSub = 1;    // LDS sub-histograms per wave (power of two)
 
 __device__ __forceinline__ uint32_t order_key(float f) {
   uint32_t u = __float_as_uint(f);
@@ -120,16 +122,17 @@ __global__ __launch_bounds__(kSelThreads) void select_hist_kernel(const float* _
   const int job = blockIdx.y, chunk = blockIdx.x;
   const SelJob jb = sel_job(caps, job, span, window, idx_stride);
   if (jb.body <= 0 || jb.body >= span) return;
-  __shared__ unsigned s_hist[kSelWaves][kSelBins];
+  // kSelSub histograms per wave (lane % kSelSub) spread same-bin atomics.
+  __shared__ unsigned s_hist[kSelWaves * kSelSub][kSelBins];
   __shared__ int s_pick[3];
   unsigned* gh = ghist + (int64_t)job * 4 * kSelBins;
   const SelState st = sel_replay(gh, jb.body, pass, s_pick);
-  for (int i = threadIdx.x; i < kSelWaves * kSelBins; i += kSelThreads) (&s_hist[0][0])[i] = 0;
+  for (int i = threadIdx.x; i < kSelWaves * kSelSub * kSelBins; i += kSelThreads) (&s_hist[0][0])[i] = 0;
   __syncthreads();
   const float* s = scores + (int64_t)job * score_stride;
   const int t0 = chunk * kSelChunk;
   const int shift = 24 - 8 * pass;
-  unsigned* wh = s_hist[threadIdx.x >> 6];
+  unsigned* wh = s_hist[(threadIdx.x >> 6) * kSelSub + (threadIdx.x & (kSelSub - 1))];
   float v[kSelRows];
 #pragma unroll
   for (int r = 0; r < kSelRows; ++r) {
@@ -142,22 +145,27 @@ __global__ __launch_bounds__(kSelThreads) void select_hist_kernel(const float* _
     const uint32_t u = order_key(v[r]);
     const bool valid = t < span && (u & st.mask) == st.prefix;
     const uint32_t d = (u >> shift) & 0xFFu;
-    // A wave whose valid lanes share one digit issues a single atomic.
-    const uint64_t act = __ballot(valid);
-    if (act == 0) continue;
-    const int leader = __ffsll((long long)act) - 1;
-    const uint32_t dl = __shfl(d, leader, 64);
-    if (__ballot(valid && d == dl) == act) {
-      if ((int)(threadIdx.x & 63) == leader) atomicAdd(&wh[dl], (unsigned)__popcll(act));
-    } else if (valid) {
-      atomicAdd(&wh[d], 1u);
+    // Lanes sharing a digit are counted by one atomic of their first lane:
+    // up to kSelMatch distinct digits per wave this way (score digits
+    // cluster in few bins, where per-lane LDS atomics would serialise),
+    // the remaining lanes one atomic each.
+    uint64_t rem = __ballot(valid);
+#pragma unroll
+    for (int it = 0; it < kSelMatch; ++it) {
+      if (rem == 0) break;
+      const int leader = __ffsll((long long)rem) - 1;
+      const uint32_t dl = (uint32_t)__builtin_amdgcn_readlane((int)d, leader);
+      const uint64_t m = __ballot(valid && d == dl) & rem;
+      if ((int)(threadIdx.x & 63) == leader) atomicAdd(&wh[dl], (unsigned)__popcll(m));
+      rem &= ~m;
     }
+    if ((rem >> (threadIdx.x & 63)) & 1ull) atomicAdd(&wh[d], 1u);
   }
   __syncthreads();
   for (int b = threadIdx.x; b < kSelBins; b += kSelThreads) {
     unsigned c = 0;
 #pragma unroll
-    for (int w = 0; w < kSelWaves; ++w) c += s_hist[w][b];
+    for (int w = 0; w < kSelWaves * kSelSub; ++w) c += s_hist[w][b];
     if (c) atomicAdd(&gh[pass * kSelBins + b], c);
   }
 }
