@@ -56,9 +56,11 @@ class HeteroCacheConfig:
     float64 retrieval lengths and relation-order pivot sets, as the reference.
     chunk_tiles: decode-attention chunk (None = one resident round).
     batched_drift_check: when the model selects after attention (Llama
-    order), run the drift checks of all layers of a check step as one launch
-    sequence after the last layer (their results are first used by the next
-    step, so the outputs are unchanged).
+    order), run the drift checks of a group of layers as one launch sequence
+    after the group's last layer (their results are first used by the next
+    step, so the outputs are unchanged).  drift_check_groups: number of
+    contiguous layer groups checked separately (1 = all layers after the
+    last one; more groups start the early groups' retrieval sooner).
     """
 
     def __init__(self, data: Optional[Dict], compression_ratio: Optional[float] = 0.5,
@@ -67,7 +69,7 @@ class HeteroCacheConfig:
                  kernel_size: Optional[int] = 5, num_attn_heads: Optional[int] = 32, num_kv_heads: Optional[int] = 8,
                  num_layers: Optional[int] = 32, retrieval_topk: Optional[int] = None, window_size: int = 1,
                  round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None,
-                 batched_drift_check: bool = True):
+                 batched_drift_check: bool = True, drift_check_groups: int = 1):
         self.data = data
         self.stable_threshold = stable_threshold
         self.compression_ratio = compression_ratio
@@ -86,6 +88,7 @@ class HeteroCacheConfig:
         self.reference_quirks = reference_quirks
         self.chunk_tiles = chunk_tiles
         self.batched_drift_check = batched_drift_check
+        self.drift_check_groups = drift_check_groups
 
 
 def _f32_caps(base, ratios, seq_len):
@@ -139,6 +142,9 @@ class HeteroCache(DynamicCache):
         self.round_scores = bool(getattr(cfg, "round_scores", False))
         self.chunk_tiles = getattr(cfg, "chunk_tiles", None)
         self.batched_check = bool(getattr(cfg, "batched_drift_check", True))
+        ngroups = max(1, min(int(getattr(cfg, "drift_check_groups", 1) or 1), self.num_layers))
+        # Last layer of each check group (contiguous layer ranges).
+        self._group_end = {((g + 1) * self.num_layers) // ngroups - 1 for g in range(ngroups)}
 
         self.stores = [None] * self.num_layers
         self.prefill_topk_set = [None] * self.num_layers
@@ -432,7 +438,7 @@ class HeteroCache(DynamicCache):
                 else:
                     self._gather_queries([layer_idx])
                     self._check_layer(layer_idx)
-        if self._due and layer_idx == self.num_layers - 1:
+        if self._due and layer_idx in self._group_end:
             self._flush_checks()
 
     def _gather_queries(self, layers):
@@ -444,12 +450,13 @@ class HeteroCache(DynamicCache):
             torch.stack([q[:, :, -1] for q in qs], dim=2, out=st.qbuf)
 
     def _flush_checks(self):
-        """Run the deferred checks: one batched launch sequence when they
-        cover every layer that has leaders (the lockstep case), otherwise
-        layer by layer."""
+        """Run the deferred checks: one batched launch sequence when they are
+        exactly the leader layers of a contiguous layer range (the lockstep
+        case), otherwise layer by layer."""
         layers, self._due = sorted(self._due), []
         self._gather_queries(layers)
-        lead_layers = [l for l in range(self.num_layers) if self._drift[l] is not None and self._drift[l].leaders]
+        lead_layers = [l for l in range(layers[0], layers[-1] + 1)
+                       if self._drift[l] is not None and self._drift[l].leaders]
         if layers == lead_layers and self._ref_bits_all is not None:
             self._check_batched(layers)
         else:
@@ -482,7 +489,7 @@ class HeteroCache(DynamicCache):
             self._retrieve(layer_idx, st, scores[:, S - 1])
 
     def _check_batched(self, layers):
-        """Drift checks of all leader layers in one launch sequence: scores
+        """Drift checks of a group of leader layers in one launch sequence: scores
         of every (layer, leader, batch) row read in place from the shared
         arena, one selection, overlap, decision and set update for all, one
         retrieval selection; then the gated gathers layer by layer on the
@@ -494,16 +501,19 @@ class HeteroCache(DynamicCache):
         S, L, G, B = self.decode_step, self.prefill_len, self.num_key_value_groups, self.bsz
         K, J = bm["K"], bm["J"]
         qa = self._qbuf_all
+        # The group's leaders are contiguous in the model-wide buffers.
+        gl0, nlead = bm["lead0"], J // B
+        trig = self._trigger_all[gl0:gl0 + nlead]
+        bits = self._ref_bits_all[gl0 * B:(gl0 + nlead) * B]
         flags = compress.ROUND_FLAGS[self._round_dtype(qa.dtype)]
         scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,
                            self.pooling, self.kernel_size, 1.0 / math.sqrt(self.head_dim), flags=flags,
                            row_tile_off=self._tile_table, k_row=bm["k_row"]).view(J, S, L)
         ops.select_topk(scores.view(J * S, L), bm["caps_K"], L, idx=bm["cur"], counts=bm["cur_counts"])
-        ops.overlap_count(bm["cur"], K, self._ref_bits_all, L, ref_of=bm["ref_of"], out=bm["overlap"])
-        ops.drift_decide(bm["overlap"], J // B, B, S, K, self.stable_threshold, self._trigger_all)
+        ops.overlap_count(bm["cur"], K, bits, L, ref_of=bm["ref_of"], out=bm["overlap"])
+        ops.drift_decide(bm["overlap"], nlead, B, S, K, self.stable_threshold, trig)
         last = bm["cur"].view(J, S, -1)[:, S - 1]
-        ops.set_bits(last, None, self._ref_bits_all, L, fixed_count=K, trigger=self._trigger_all,
-                     trig_of=bm["trig_of"])
+        ops.set_bits(last, None, bits, L, fixed_count=K, trigger=trig, trig_of=bm["trig_of"])
         if not bm["plans"]:
             return
         ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
@@ -517,24 +527,26 @@ class HeteroCache(DynamicCache):
             for layer, plan in bm["plans"]:
                 kc, vc = self.key_cache_cpu[layer], self.value_cache_cpu[layer]
                 self.stores[layer].launch_rows(plan, kc, vc, idx=bm["ret_idx"], src_is_host=host, stream=side,
-                                               trigger=self._trigger_all, set_len=False)
+                                               trigger=trig, set_len=False)
                 if host:
                     ev = torch.cuda.Event()
                     ev.record(side)
                     self._retrieval_done[layer] = ev
 
     def _batched_metadata(self, layers):
-        """Device metadata of _check_batched; rows j follow the global
-        (layer, leader, batch) order of the reference sets and triggers."""
+        """Device metadata of _check_batched; rows j follow the
+        (layer, leader, batch) order of the reference sets and triggers,
+        counted from the group's first leader."""
         dev = self._qbuf_all.device
         qa = self._qbuf_all
         B, Hkv, G, S, L = self.bsz, self.num_kv_heads, self.num_key_value_groups, self.decode_step, self.prefill_len
         K = min(self.base_compress_len, L)
         q_off, k_row, trig_of, ret_caps, jobs = [], [], [], [], {}
+        gl0 = self._lead_base[layers[0]]
         j = 0
         for layer in layers:
             st = self._drift[layer]
-            lb = self._lead_base[layer]
+            lb = self._lead_base[layer] - gl0  # group-local leader index
             for i, h in enumerate(st.leaders):
                 members = st.members[i]
                 lens = self._retrieval_lengths(layer, members) if members else []
@@ -551,7 +563,7 @@ class HeteroCache(DynamicCache):
                             jobs.setdefault(layer, []).append((j, lb + i, b, mm, n))
                     j += 1
         J = j
-        m = {"K": K, "J": J}
+        m = {"K": K, "J": J, "lead0": gl0}
         m["q_off"] = torch.as_tensor(np.asarray(q_off, dtype=np.int64)).to(dev)
         m["k_row"] = torch.as_tensor(np.asarray(k_row, dtype=np.int32)).to(dev)
         m["caps_K"] = torch.full((J * S,), K, dtype=torch.int32, device=dev)

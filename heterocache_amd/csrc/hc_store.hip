@@ -24,25 +24,29 @@
 
 namespace hc {
 
-// One workgroup moves one 32-token tile of one job through LDS: natural-layout
-// 16-byte reads in, tile-permuted 16-byte writes out.
+// A workgroup moves one 32-token tile of one job at a time through LDS:
+// natural-layout 16-byte reads in, tile-permuted 16-byte writes out.  Work
+// items (job, tile) are strided over the grid, so a host-sourced gather can
+// run on a few workgroups: its reads wait on the host link, and a full grid
+// would hold CU slots the decode kernel (sized to fill the device) needs.
 template <typename T>
 __global__ __launch_bounds__(256) void gather_store_kernel(
     const T* __restrict__ src_k, const T* __restrict__ src_v, const int64_t* __restrict__ src_off,
     int64_t src_tok_stride, int src_len, const int32_t* __restrict__ idx, const int64_t* __restrict__ idx_off,
     const int32_t* __restrict__ count, const int32_t* __restrict__ dst_row, T* __restrict__ kstore,
     T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off, const int32_t* __restrict__ trigger,
-    const int32_t* __restrict__ trig_of) {
-  const int job = blockIdx.y;
-  if (trigger && trigger[trig_of ? trig_of[job] : 0] == 0) return;
-  const int tile = blockIdx.x;
-  const int n = count[job];
-  const int tok0 = tile * HC_TILE;
-  if (tok0 >= n) return;
-  const int valid = min(HC_TILE, n - tok0);
-
+    const int32_t* __restrict__ trig_of, int njobs, int tiles_per_job) {
   __shared__ T sk[HC_TILE][HC_HEAD_DIM + 8];
   __shared__ T sv[HC_TILE][HC_HEAD_DIM + 8];
+  const int64_t items = (int64_t)njobs * tiles_per_job;
+  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+  const int job = (int)(item / tiles_per_job);
+  const int tile = (int)(item % tiles_per_job);
+  if (trigger && trigger[trig_of ? trig_of[job] : 0] == 0) continue;
+  const int n = count[job];
+  const int tok0 = tile * HC_TILE;
+  if (tok0 >= n) continue;
+  const int valid = min(HC_TILE, n - tok0);
 
   const T* bk = src_k + src_off[job];
   const T* bv = src_v + src_off[job];
@@ -104,6 +108,8 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
       }
     }
   }
+  __syncthreads();  // the next item refills the LDS tiles
+  }
 }
 
 // One wave per row: store the row's new token at slot len, then len += 1.
@@ -146,16 +152,21 @@ __global__ __launch_bounds__(256) void store_read_kernel(const T* __restrict__ k
   dst_v[(int64_t)j * count * HC_HEAD_DIM + e] = vstore[base + v_tile_offset(tok % HC_TILE, d)];
 }
 
+// Workgroups of a gather whose source is host memory read over the link.
+constexpr int kHostGatherWorkgroups = 64;
+
 template <typename T>
 static int launch_gather_store(const void* src_k, const void* src_v, const int64_t* src_off, int64_t src_tok_stride,
                                int src_len, const int32_t* idx, const int64_t* idx_off, const int32_t* count,
                                const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off,
                                int njobs, int max_count, const int32_t* trigger, const int32_t* trig_of,
-                               hipStream_t s) {
-  dim3 grid((max_count + HC_TILE - 1) / HC_TILE, njobs);
-  hipLaunchKernelGGL((gather_store_kernel<T>), grid, dim3(256), 0, s, (const T*)src_k, (const T*)src_v, src_off,
+                               bool host_src, hipStream_t s) {
+  const int tiles = (max_count + HC_TILE - 1) / HC_TILE;
+  const int64_t items = (int64_t)tiles * njobs;
+  const unsigned grid = (unsigned)(host_src ? std::min<int64_t>(items, kHostGatherWorkgroups) : items);
+  hipLaunchKernelGGL((gather_store_kernel<T>), dim3(grid), dim3(256), 0, s, (const T*)src_k, (const T*)src_v, src_off,
                      src_tok_stride, src_len, idx, idx_off, count, dst_row, (T*)kstore, (T*)vstore, row_tile_off, trigger,
-                     trig_of);
+                     trig_of, njobs, tiles);
   return check_launch("hc_gather_store");
 }
 
@@ -249,13 +260,13 @@ extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, 
   switch (dtype) {
     case HC_DTYPE_BF16:
       return launch_gather_store<__bf16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                         vstore, row_tile_off, njobs, max_count, trigger, trig_of, s);
+                                         vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, s);
     case HC_DTYPE_F16:
       return launch_gather_store<_Float16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                           vstore, row_tile_off, njobs, max_count, trigger, trig_of, s);
+                                           vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, s);
     case HC_DTYPE_F32:
       return launch_gather_store<float>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                        vstore, row_tile_off, njobs, max_count, trigger, trig_of, s);
+                                        vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, s);
     default:
       return set_error(HC_ERR_INVALID, "hc_gather_store: unknown dtype %d", dtype);
   }

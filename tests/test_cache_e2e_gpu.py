@@ -41,14 +41,14 @@ def head_data(seed=0):
     return augment_head_data(raw, perms)
 
 
-def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True):
+def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True, groups=1):
     torch.manual_seed(0)
     B, Hq, Hkv, NL, D = 1, 32, 8, 2, 128
     data = head_data()
     cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
                             max_gen_len=steps + 4, decode_step=5, pooling="avgpool", kernel_size=5,
                             num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=topk,
-                            reference_quirks=quirks, batched_drift_check=batched)
+                            reference_quirks=quirks, batched_drift_check=batched, drift_check_groups=groups)
     cache = HeteroCache(cfg)
     orc = O.CacheOracle(data, B, Hq, Hkv, NL, 0.5, 0.5, 5, "avgpool", 5, retrieval_topk=topk, quirks=quirks,
                         select_before_attention=select_first)
@@ -102,6 +102,13 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
 def test_llama_order(dev, dtype):
     trig = run(dev, dtype)
     # First check: overlap 1.0 everywhere; second: every leader retrieves.
+    assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
+
+
+def test_llama_order_two_check_groups(dev):
+    """Each layer's check as its own batched group (the second group's
+    leaders start past the first global leader)."""
+    trig = run(dev, torch.float32, groups=2)
     assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
 
 
