@@ -389,55 +389,119 @@ __global__ __launch_bounds__(kPoolThreads) void score_pool_kernel(const float* _
 // (job, w', kFinTile positions); each query head's strip plus its pooling
 // halo is built in LDS.
 constexpr int kFinTile = 1024;
+constexpr int kLogitRowsMax = 32;  // rows of the logit-store path (R < 32)
 
+// Rounding of the reference's casts, fixed per kernel instance.
+template <int RMODE>
+__device__ __forceinline__ float round_fixed(float x) {
+  if constexpr (RMODE == 1) return (float)(__bf16)x;
+  if constexpr (RMODE == 2) return (float)(_Float16)x;
+  return x;
+}
+
+// Probability of one logit (0 for a masked position), as the probability
+// pass forms it.
+template <int RMODE>
+__device__ __forceinline__ float fin_prob(float x, float m, float iz) {
+  return x == -INFINITY ? 0.f : round_fixed<RMODE>(fast_exp2(x - m) * iz);
+}
+
+constexpr int kFinHalo = 32;  // >= kPoolMaxHalf, keeps the strip 16-byte aligned
+constexpr int kFinHeads = 4;  // query heads whose loads are in flight together
+
+template <int RMODE, int POOL>
 __global__ __launch_bounds__(256) void score_finish_kernel(const float* __restrict__ logits,
                                                            const float* __restrict__ stats, int R, int G, int W,
-                                                           int span, int sum_w, int pooling, int kernel, int flags,
+                                                           int span, int sum_w, int kernel,
                                                            float* __restrict__ S) {
-  __shared__ float s_a[kFinTile + 2 * kPoolMaxHalf];
+  // s_a[kFinHalo + i] holds position t0 + i of the current head's strip,
+  // i in [-p, kFinTile + p).  Thread x loads positions t0 + 4x .. +3 (one
+  // 16-byte load per row) and pools positions t0 + x + 256k, so LDS reads
+  // of neighbouring lanes are consecutive words.
+  __shared__ __align__(16) float s_a[kFinTile + 2 * kFinHalo];
+  __shared__ float s_m[kLogitRowsMax], s_iz[kLogitRowsMax];  // row max, 1 / row sum
   const int wout = sum_w ? 1 : W;
   const int job = blockIdx.y / wout, wo = blockIdx.y % wout;
   const int t0 = blockIdx.x * kFinTile;
   const int p = kernel / 2;
-  const float pad = pooling == 0 ? 0.f : -INFINITY;
-  float best[kFinTile / 256];
+  constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
+  for (int r = threadIdx.x; r < R; r += 256) {
+    s_m[r] = stats[((int64_t)job * R + r) * 2];
+    s_iz[r] = 1.f / stats[((int64_t)job * R + r) * 2 + 1];
+  }
+  const int w_lo = sum_w ? 0 : wo, w_hi = sum_w ? W : wo + 1;
+  const int tb = t0 + 4 * threadIdx.x;
+  const bool vec_ok = (span & 3) == 0 && tb + 4 <= span;
+  // Halo: threads [0, p) load t0 - p + x (left), threads [p, 2p) load
+  // t0 + kFinTile + (x - p) (right).
+  const bool halo = threadIdx.x < 2 * p;
+  const int th = threadIdx.x < p ? t0 - p + threadIdx.x : t0 + kFinTile + (threadIdx.x - p);
+  const int sh = threadIdx.x < p ? kFinHalo - p + threadIdx.x : kFinHalo + kFinTile + (threadIdx.x - p);
+  const float inv_k = 1.f / (float)kernel;
+  float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  __syncthreads();
+  // Heads are taken kFinHeads at a time: all their rows' loads are issued
+  // before any strip is pooled.
+  for (int g0 = 0; g0 < G; g0 += kFinHeads) {
+    f32x4 a4[kFinHeads];
+    float ah[kFinHeads];
 #pragma unroll
-  for (int i = 0; i < kFinTile / 256; ++i) best[i] = -INFINITY;
-  for (int g = 0; g < G; ++g) {
-    const int w_lo = sum_w ? 0 : wo, w_hi = sum_w ? W : wo + 1;
-    __syncthreads();
-    for (int i = threadIdx.x; i < kFinTile + 2 * p; i += 256) {
-      const int t = t0 - p + i;
-      float acc = pad;
-      if (t >= 0 && t < span) {
-        acc = 0.f;
+    for (int gg = 0; gg < kFinHeads; ++gg) {
+      const int g = g0 + gg;
+      a4[gg] = f32x4{pad, pad, pad, pad};
+      ah[gg] = pad;
+      if (g >= G) continue;
+      if (tb < span) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
         for (int w = w_lo; w < w_hi; ++w) {
           const int r = g * W + w;
-          const float M = stats[((int64_t)job * R + r) * 2], Z = stats[((int64_t)job * R + r) * 2 + 1];
-          const float x = logits[((int64_t)job * R + r) * span + t];
-          acc += x == -INFINITY ? 0.f : round_mode(fast_exp2(x - M) * (1.f / Z), flags);
-        }
-        acc = round_mode(acc, flags);
-      }
-      s_a[i] = acc;
-    }
-    __syncthreads();
+          const float* row = logits + ((int64_t)job * R + r) * span;
+          const float m = s_m[r], iz = s_iz[r];
+          if (vec_ok) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(row + tb);
 #pragma unroll
-    for (int i = 0; i < kFinTile / 256; ++i) {
-      const int c = threadIdx.x + 256 * i;
-      float v = pad;
-      for (int d = 0; d <= 2 * p; ++d) {
-        const float x = s_a[c + d];
-        v = pooling == 0 ? v + x : fmaxf(v, x);
+            for (int e = 0; e < 4; ++e) acc[e] += fin_prob<RMODE>(x[e], m, iz);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (tb + e < span) acc[e] += fin_prob<RMODE>(row[tb + e], m, iz);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a4[gg][e] = tb + e < span ? round_fixed<RMODE>(acc[e]) : pad;
       }
-      if (pooling == 0) v = v / (float)kernel;
-      best[i] = fmaxf(best[i], round_mode(v, flags));
+      if (halo && th >= 0 && th < span) {
+        float acc = 0.f;
+        for (int w = w_lo; w < w_hi; ++w) {
+          const int r = g * W + w;
+          acc += fin_prob<RMODE>(logits[((int64_t)job * R + r) * span + th], s_m[r], s_iz[r]);
+        }
+        ah[gg] = round_fixed<RMODE>(acc);
+      }
+    }
+#pragma unroll
+    for (int gg = 0; gg < kFinHeads; ++gg) {
+      if (g0 + gg >= G) break;
+      __syncthreads();  // the previous strip has been pooled
+      *reinterpret_cast<f32x4*>(&s_a[kFinHalo + 4 * threadIdx.x]) = a4[gg];
+      if (halo) s_a[sh] = ah[gg];
+      __syncthreads();
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int c = threadIdx.x + 256 * k;  // output position t0 + c
+        const float* win = s_a + kFinHalo + c - p;
+        float v = pad;
+        for (int d = 0; d <= 2 * p; ++d) v = POOL == 0 ? v + win[d] : fmaxf(v, win[d]);
+        if constexpr (POOL == 0) v *= inv_k;
+        best[k] = fmaxf(best[k], round_fixed<RMODE>(v));
+      }
     }
   }
+  float* o = S + ((int64_t)job * wout + wo) * span;
 #pragma unroll
-  for (int i = 0; i < kFinTile / 256; ++i) {
-    const int t = t0 + threadIdx.x + 256 * i;
-    if (t < span) S[((int64_t)job * wout + wo) * span + t] = best[i];
+  for (int k = 0; k < 4; ++k) {
+    const int t = t0 + threadIdx.x + 256 * k;
+    if (t < span) o[t] = best[k];
   }
 }
 
@@ -477,9 +541,16 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   if ((rc = check_launch("hc_score(merge)"))) return rc;
   if (via_logits) {
     if (a.span > 0) {
-      hipLaunchKernelGGL(score_finish_kernel, dim3((a.span + kFinTile - 1) / kFinTile, njobs * wout), dim3(256), 0,
-                         s, A, stats, a.R, a.G, a.W, a.span, (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : 0, pooling, kernel,
-                         a.flags, scores);
+      const dim3 fgrid((a.span + kFinTile - 1) / kFinTile, njobs * wout);
+      const int sum_w = (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : 0;
+      const int rmode = (a.flags & HC_SCORE_ROUND_BF16) ? 1 : (a.flags & HC_SCORE_ROUND_F16) ? 2 : 0;
+#define HC_FINISH(RM, PL)                                                                                  \
+  hipLaunchKernelGGL((score_finish_kernel<RM, PL>), fgrid, dim3(256), 0, s, A, stats, a.R, a.G, a.W, a.span, \
+                     sum_w, kernel, scores)
+      if (rmode == 0) { if (pooling == 0) HC_FINISH(0, 0); else HC_FINISH(0, 1); }
+      else if (rmode == 1) { if (pooling == 0) HC_FINISH(1, 0); else HC_FINISH(1, 1); }
+      else { if (pooling == 0) HC_FINISH(2, 0); else HC_FINISH(2, 1); }
+#undef HC_FINISH
       if ((rc = check_launch("hc_score(finish)"))) return rc;
     }
     return HC_OK;
