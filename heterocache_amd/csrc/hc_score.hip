@@ -23,6 +23,9 @@
 //     window rows of each query head (xor-shuffle tree: fixed order), write
 //     A[job][w'][g][t].
 //  4. score_pool_kernel: pooling over t and max over g -> S[job][w'][t].
+#include <cfloat>
+#include <type_traits>
+
 #include "hc_common.h"
 #include "hc_internal.h"
 
@@ -44,7 +47,17 @@ struct ScoreArgs {
   const int32_t* k_row;
   int L, G, W, R, NT, flags, span;
   float scale;
+  float scale2;  // scale * log2(e): base-2 logits without the reference's casts
 };
+
+// Rounding of the reference's casts, fixed per kernel instance: 0 none,
+// 1 bfloat16, 2 float16.
+template <int RM>
+__device__ __forceinline__ float round_fixed(float x) {
+  if constexpr (RM == 1) return (float)(__bf16)x;
+  if constexpr (RM == 2) return (float)(_Float16)x;
+  return x;
+}
 
 __device__ __forceinline__ float round_mode(float x, int flags) {
   if (flags & HC_SCORE_ROUND_BF16) return (float)(__bf16)x;
@@ -104,18 +117,15 @@ __device__ __forceinline__ int row_limit(const ScoreArgs& a, int r) {
   return (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W + r % a.W : a.L - 1;
 }
 
+template <int RM>
 __device__ __forceinline__ float scaled_logit(const ScoreArgs& a, float acc) {
-  float v;
-  if (a.flags & (HC_SCORE_ROUND_BF16 | HC_SCORE_ROUND_F16))
-    v = round_mode(round_mode(acc, a.flags) * a.scale, a.flags);
-  else
-    v = acc * a.scale;
-  return v * 1.4426950408889634f;
+  if constexpr (RM == 0) return acc * a.scale2;
+  return round_fixed<RM>(round_fixed<RM>(acc) * a.scale) * 1.4426950408889634f;
 }
 
 // Logits (base 2) of row 16nt + (lane & 15) (visible up to `limit`) for
 // tokens t0 + 4*(lane>>4) + j; keys are the A operand.
-template <typename T>
+template <typename T, int RM, bool MASK>
 __device__ __forceinline__ void subtile_logits(const ScoreArgs& a, const typename Elem<T>::vec8 (&kr)[4],
                                                const T* s_q, int nt, int t0, int lane, int limit, float (&x)[4]) {
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -125,7 +135,7 @@ __device__ __forceinline__ void subtile_logits(const ScoreArgs& a, const typenam
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int t = t0 + 4 * (lane >> 4) + j;
-    x[j] = t <= limit ? scaled_logit(a, acc[j]) : -INFINITY;
+    x[j] = (!MASK || t <= limit) ? scaled_logit<RM>(a, acc[j]) : -INFINITY;
   }
 }
 
@@ -136,7 +146,7 @@ __device__ __forceinline__ void merge_ml(float& m, float& l, float m2, float l2)
   m = mn;
 }
 
-template <typename T, bool STORE>
+template <typename T, bool STORE, int RM, bool LOGITS>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs a, float* __restrict__ part,
                                                                       float* __restrict__ logits) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -155,45 +165,57 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
   __syncthreads();
   // Lane state: running (max, sum) of row 16nt + lane%16 over this lane's
   // tokens; the four lanes of a row are combined once, after the loop.
+  // -FLT_MAX (not -inf) as the empty maximum keeps the update branch-free:
+  // exp2(-inf - m) = 0 and exp2(m - m) = 1 for a still-empty row.
   float m[16], l[16];
 #pragma unroll
   for (int nt = 0; nt < 16; ++nt) {
-    m[nt] = -INFINITY;
+    m[nt] = -FLT_MAX;
     l[nt] = 0.f;
   }
+  const bool vec_logits = (a.span & 3) == 0;
+  // Masks matter only where this workgroup's tokens reach past the lowest
+  // row limit (the causal window or the end of the keys); elsewhere every
+  // logit is visible and the per-value test is skipped.
+  const int min_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W : a.L - 1;
+  const bool need_mask = chunk * kScoreChunk + kScoreChunk - 1 > min_limit;
+  auto body = [&](auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
-  for (int nt = 0; nt < 16; ++nt) {
-    if (nt < a.NT) {
-      const int limit = row_limit(a, 16 * nt + (lane & 15));
+    for (int nt = 0; nt < 16; ++nt) {
+      if (nt < a.NT) {
+        const int limit = row_limit(a, 16 * nt + (lane & 15));
 #pragma unroll
-      for (int u = 0; u < kSubTiles; ++u) {
-        float x[4];
-        subtile_logits<T>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
-        if (logits) {
-          // Row r, tokens t..t+3 (16 bytes) of the job's [R][span] logits.
-          const int r = 16 * nt + (lane & 15), t = tw + 16 * u + 4 * (lane >> 4);
-          if (r < a.R && t < a.span) {
+        for (int u = 0; u < kSubTiles; ++u) {
+          float x[4];
+          subtile_logits<T, RM, MASK>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
+          if constexpr (LOGITS) {
+            // Row r, tokens t..t+3 (16 bytes) of the job's [R][span] logits.
+            const int r = 16 * nt + (lane & 15), t = tw + 16 * u + 4 * (lane >> 4);
             float* o = logits + ((int64_t)job * a.R + r) * a.span + t;
-            if (t + 4 <= a.span && (a.span & 3) == 0) {
-              *reinterpret_cast<f32x4*>(o) = f32x4{x[0], x[1], x[2], x[3]};
-            } else {
+            if (r < a.R) {
+              if (vec_logits && t + 4 <= a.span) {
+                *reinterpret_cast<f32x4*>(o) = f32x4{x[0], x[1], x[2], x[3]};
+              } else {
 #pragma unroll
-              for (int j = 0; j < 4; ++j)
-                if (t + j < a.span) o[j] = x[j];
+                for (int j = 0; j < 4; ++j)
+                  if (t + j < a.span) o[j] = x[j];
+              }
             }
           }
-        }
-        const float mn = fmaxf(fmaxf(m[nt], fmaxf(x[0], x[1])), fmaxf(x[2], x[3]));
-        if (mn != -INFINITY) {
-          float sm = 0.f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) sm += fast_exp2(x[j] - mn);
+          const float mn = fmaxf(fmaxf(m[nt], fmaxf(x[0], x[1])), fmaxf(x[2], x[3]));
+          const float sm =
+              (fast_exp2(x[0] - mn) + fast_exp2(x[1] - mn)) + (fast_exp2(x[2] - mn) + fast_exp2(x[3] - mn));
           l[nt] = fmaf(l[nt], fast_exp2(m[nt] - mn), sm);
           m[nt] = mn;
         }
       }
     }
-  }
+  };
+  if (need_mask)
+    body(std::true_type{});
+  else
+    body(std::false_type{});
   float* my = s_st + (size_t)wave * rows * 2;
 #pragma unroll
   for (int nt = 0; nt < 16; ++nt) {
@@ -249,7 +271,7 @@ __global__ __launch_bounds__(256) void score_stats_merge_kernel(const float* __r
 // 16nt + 4*(lane>>4) + j (visible up to limit[j]) of token t0 + lane%16, so
 // sums over a query head's window rows are in-lane adds plus at most two
 // cross-lane steps.
-template <typename T>
+template <typename T, int RM, bool MASK>
 __device__ __forceinline__ void subtile_logits_rows(const ScoreArgs& a, const typename Elem<T>::vec8 (&kr)[4],
                                                     const T* s_q, int nt, int t0, int lane, const int (&limit)[4],
                                                     float (&x)[4]) {
@@ -259,10 +281,10 @@ __device__ __forceinline__ void subtile_logits_rows(const ScoreArgs& a, const ty
   for (int s = 0; s < 4; ++s) acc = mma_16x16x32(load8<T>(qrow + 32 * s), kr[s], acc);
   const int t = t0 + (lane & 15);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) x[j] = t <= limit[j] ? scaled_logit(a, acc[j]) : -INFINITY;
+  for (int j = 0; j < 4; ++j) x[j] = (!MASK || t <= limit[j]) ? scaled_logit<RM>(a, acc[j]) : -INFINITY;
 }
 
-template <typename T, bool STORE>
+template <typename T, bool STORE, int RM>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs a, const float* __restrict__ stats,
                                                                       float* __restrict__ A) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -276,7 +298,8 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   const bool sum_w = (a.flags & HC_SCORE_SUM_WINDOW) != 0;
   stage_queries<T>(a, job, s_q);
   for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
-    s_m[r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] : -INFINITY;
+    // Padding rows get probability 0 even where logits are not masked.
+    s_m[r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] : 0.f;
     s_iz[r] = r < a.R ? 1.f / stats[((int64_t)job * a.R + r) * 2 + 1] : 0.f;
   }
   const int wout = sum_w ? 1 : a.W;
@@ -288,65 +311,74 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   float gsum[kSubTiles];  // running window sum per sub-tile (W >= 16)
 #pragma unroll
   for (int u = 0; u < kSubTiles; ++u) gsum[u] = 0.f;
-#pragma unroll
-  for (int nt = 0; nt < 16; ++nt) {
-    if (nt < a.NT) {
-      const int r0 = 16 * nt + 4 * rg;
-      float M[4], IZ[4];
-      int limit[4];
-      int64_t orow[4];  // output row of each j without the window sum: A[job][w][g]
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        M[j] = s_m[r0 + j];
-        IZ[j] = s_iz[r0 + j];
-        limit[j] = row_limit(a, r0 + j);
-        if (!sum_w) orow[j] = (((int64_t)job * wout + (r0 + j) % a.W) * a.G + (r0 + j) / a.W) * a.span;
-      }
-#pragma unroll
-      for (int u = 0; u < kSubTiles; ++u) {
-        const int t = tw + 16 * u + (lane & 15);
-        float x[4], p[4];
-        subtile_logits_rows<T>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p[j] = x[j] == -INFINITY ? 0.f : round_mode(fast_exp2(x[j] - M[j]) * IZ[j], a.flags);
-        if (!sum_w) {
-          // Row r = g*W + w -> A[job][w][g][t].
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (r0 + j < a.R && t < a.span) A[orow[j] + t] = p[j];
-        } else if (a.W >= 16) {
-          // The 16 rows of this tile all belong to one query head.
-          float v = (p[0] + p[1]) + (p[2] + p[3]);
-          v += __shfl_xor(v, 16, 64);
-          v += __shfl_xor(v, 32, 64);
-          gsum[u] += v;
-          if (((16 * (nt + 1)) % a.W) == 0) {
-            const int g = (16 * nt) / a.W;
-            if (rg == 0 && g < a.G && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_mode(gsum[u], a.flags);
-            gsum[u] = 0.f;
+  const int min_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W : a.L - 1;
+  const bool need_mask = chunk * kScoreChunk + kScoreChunk - 1 > min_limit;
+  auto body = [&](auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+  #pragma unroll
+    for (int nt = 0; nt < 16; ++nt) {
+      if (nt < a.NT) {
+        const int r0 = 16 * nt + 4 * rg;
+        float M[4], IZ[4];
+        int limit[4];
+        int64_t orow[4];  // output row of each j without the window sum: A[job][w][g]
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          M[j] = s_m[r0 + j];
+          IZ[j] = s_iz[r0 + j];
+          limit[j] = row_limit(a, r0 + j);
+          if (!sum_w) orow[j] = (((int64_t)job * wout + (r0 + j) % a.W) * a.G + (r0 + j) / a.W) * a.span;
+        }
+  #pragma unroll
+        for (int u = 0; u < kSubTiles; ++u) {
+          const int t = tw + 16 * u + (lane & 15);
+          float x[4], p[4];
+          subtile_logits_rows<T, RM, MASK>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) p[j] = x[j] == -INFINITY ? 0.f : round_fixed<RM>(fast_exp2(x[j] - M[j]) * IZ[j]);
+          if (!sum_w) {
+            // Row r = g*W + w -> A[job][w][g][t].
+  #pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (r0 + j < a.R && t < a.span) A[orow[j] + t] = p[j];
+          } else if (a.W >= 16) {
+            // The 16 rows of this tile all belong to one query head.
+            float v = (p[0] + p[1]) + (p[2] + p[3]);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            gsum[u] += v;
+            if (((16 * (nt + 1)) % a.W) == 0) {
+              const int g = (16 * nt) / a.W;
+              if (rg == 0 && g < a.G && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_fixed<RM>(gsum[u]);
+              gsum[u] = 0.f;
+            }
+          } else if (a.W == 8) {
+            float v = (p[0] + p[1]) + (p[2] + p[3]);
+            v += __shfl_xor(v, 16, 64);
+            const int g = r0 / 8;
+            if ((rg & 1) == 0 && r0 < a.R && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_fixed<RM>(v);
+          } else if (a.W == 4) {
+            // A head's rows are the four j of this lane.
+            const float v = (p[0] + p[1]) + (p[2] + p[3]);
+            if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 4) * a.span + t] = round_fixed<RM>(v);
+          } else if (a.W == 2) {
+            const float v0 = p[0] + p[1], v1 = p[2] + p[3];
+            if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2) * a.span + t] = round_fixed<RM>(v0);
+            if (r0 + 2 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2 + 1) * a.span + t] = round_fixed<RM>(v1);
+          } else {
+            // W == 1: every row is its own query head.
+  #pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (r0 + j < a.R && t < a.span) A[((int64_t)job * a.G + r0 + j) * a.span + t] = round_fixed<RM>(p[j]);
           }
-        } else if (a.W == 8) {
-          float v = (p[0] + p[1]) + (p[2] + p[3]);
-          v += __shfl_xor(v, 16, 64);
-          const int g = r0 / 8;
-          if ((rg & 1) == 0 && r0 < a.R && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_mode(v, a.flags);
-        } else if (a.W == 4) {
-          // A head's rows are the four j of this lane.
-          const float v = (p[0] + p[1]) + (p[2] + p[3]);
-          if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 4) * a.span + t] = round_mode(v, a.flags);
-        } else if (a.W == 2) {
-          const float v0 = p[0] + p[1], v1 = p[2] + p[3];
-          if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2) * a.span + t] = round_mode(v0, a.flags);
-          if (r0 + 2 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2 + 1) * a.span + t] = round_mode(v1, a.flags);
-        } else {
-          // W == 1: every row is its own query head.
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (r0 + j < a.R && t < a.span) A[((int64_t)job * a.G + r0 + j) * a.span + t] = round_mode(p[j], a.flags);
         }
       }
     }
-  }
+  };
+  if (need_mask)
+    body(std::true_type{});
+  else
+    body(std::false_type{});
 }
 
 // 256 consecutive positions of one (job, w') per workgroup; each query
@@ -390,14 +422,6 @@ __global__ __launch_bounds__(kPoolThreads) void score_pool_kernel(const float* _
 // halo is built in LDS.
 constexpr int kFinTile = 1024;
 constexpr int kLogitRowsMax = 32;  // rows of the logit-store path (R < 32)
-
-// Rounding of the reference's casts, fixed per kernel instance.
-template <int RMODE>
-__device__ __forceinline__ float round_fixed(float x) {
-  if constexpr (RMODE == 1) return (float)(__bf16)x;
-  if constexpr (RMODE == 2) return (float)(_Float16)x;
-  return x;
-}
 
 // Probability of one logit (0 for a masked position), as the probability
 // pass forms it.
@@ -532,8 +556,16 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   const size_t lds1 = qbytes + (size_t)kScoreWaves * a.NT * 16 * 2 * sizeof(float);
   const size_t lds3 = qbytes + (size_t)a.NT * 16 * 2 * sizeof(float);
   const bool via_logits = a.R < kLogitRows;
-  hipLaunchKernelGGL((score_stats_kernel<T, STORE>), dim3(nchunks, njobs), dim3(kScoreWaves * 64), lds1, s, a, part,
-                     via_logits ? A : nullptr);
+  const int rm = (a.flags & HC_SCORE_ROUND_BF16) ? 1 : (a.flags & HC_SCORE_ROUND_F16) ? 2 : 0;
+#define HC_STATS(RM, LG)                                                                                   \
+  hipLaunchKernelGGL((score_stats_kernel<T, STORE, RM, LG>), dim3(nchunks, njobs), dim3(kScoreWaves * 64), lds1, s, \
+                     a, part, LG ? A : nullptr)
+  if (via_logits) {
+    if (rm == 0) HC_STATS(0, true); else if (rm == 1) HC_STATS(1, true); else HC_STATS(2, true);
+  } else {
+    if (rm == 0) HC_STATS(0, false); else if (rm == 1) HC_STATS(1, false); else HC_STATS(2, false);
+  }
+#undef HC_STATS
   int rc = check_launch("hc_score(stats)");
   if (rc) return rc;
   hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nchunks, a.R,
@@ -543,7 +575,7 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
     if (a.span > 0) {
       const dim3 fgrid((a.span + kFinTile - 1) / kFinTile, njobs * wout);
       const int sum_w = (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : 0;
-      const int rmode = (a.flags & HC_SCORE_ROUND_BF16) ? 1 : (a.flags & HC_SCORE_ROUND_F16) ? 2 : 0;
+      const int rmode = rm;
 #define HC_FINISH(RM, PL)                                                                                  \
   hipLaunchKernelGGL((score_finish_kernel<RM, PL>), fgrid, dim3(256), 0, s, A, stats, a.R, a.G, a.W, a.span, \
                      sum_w, kernel, scores)
@@ -557,8 +589,11 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   }
   const int nchunks_span = (a.span + kScoreChunk - 1) / kScoreChunk;
   if (nchunks_span > 0) {
-    hipLaunchKernelGGL((score_probs_kernel<T, STORE>), dim3(nchunks_span, njobs), dim3(kScoreWaves * 64), lds3, s, a,
-                       stats, A);
+#define HC_PROBS(RM)                                                                                        \
+  hipLaunchKernelGGL((score_probs_kernel<T, STORE, RM>), dim3(nchunks_span, njobs), dim3(kScoreWaves * 64), lds3, s, \
+                     a, stats, A)
+    if (rm == 0) HC_PROBS(0); else if (rm == 1) HC_PROBS(1); else HC_PROBS(2);
+#undef HC_PROBS
     if ((rc = check_launch("hc_score(probs)"))) return rc;
     hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + kPoolThreads - 1) / kPoolThreads, njobs * wout),
                        dim3(kPoolThreads), 0, s, A, a.G, a.span, pooling, kernel, a.flags, scores);
@@ -628,6 +663,7 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
   a.flags = flags;
   a.span = span;
   a.scale = scale;
+  a.scale2 = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
 #define HC_SCORE_DISPATCH(T)                                                                          \
   return store ? launch_score<T, true>(a, njobs, pooling, kernel, scores, workspace, s)               \
