@@ -1,0 +1,366 @@
+// Causal prefill attention (flash-attention forward) on gfx950 MFMA.
+//
+//   out[b, i, hq, :] = sum_t softmax_t(scale * q[b, hq, i] . k[b, hq/G, t]) v[b, hq/G, t]
+//   over keys t <= Lk - Lq + i
+//
+// The queries are the last Lq positions of the Lk keys (bottom-right causal
+// alignment, as flash-attn's causal=True), so one kernel serves a whole
+// prompt (Lq == Lk) and each chunk of a chunked prefill (Lq < Lk).  Replaces
+// the flash-attn prefill call of LlamaAttention / Qwen2Attention
+// (heterocache/llama_model.py:353-361, through transformers'
+// flash_attention_forward; heterocache/qwen_model.py follows the same path).
+//
+// Structure:
+//  * a workgroup holds 4 waves x 32 queries of one query head; the blockIdx
+//    order puts every workgroup of a KV row on the same XCD (rows are
+//    interleaved modulo the grid's round-robin over XCDs) and dispatches the
+//    query blocks with the most keys first;
+//  * keys advance 64 per iteration (two 32-token tiles).  K and V arrive in
+//    natural layout with arbitrary batch/head/token strides and are staged
+//    through double-buffered LDS in the KV store's tile layout, so every MFMA
+//    operand is one 16-byte LDS read:
+//      - K chunks of 8 channels land contiguously (the tile layout keeps them
+//        together);
+//      - V is transposed in registers, 4 tokens x 8 channels per thread, and
+//        written as 4-element groups whose position inside each 16-channel
+//        block is rotated by the block index, which keeps the writes and the
+//        operand reads free of bank conflicts;
+//  * S^T = K Q^T per 16-key x 16-query block (K as the A operand), online
+//    base-2 softmax per query column, O^T += V^T P^T with P taken straight
+//    from the S accumulators (the tile layout's V token order is the order in
+//    which the accumulator holds the scores), fp32 accumulation.
+#include <cfloat>
+#include <cmath>
+#include <mutex>
+
+#include "hc_common.h"
+#include "hc_internal.h"
+
+namespace hc {
+namespace {
+
+constexpr int kPfWaves = 4;
+constexpr int kPfWaveQ = 32;                    // queries per wave: two 16-column MFMA blocks
+constexpr int kPfBlockQ = kPfWaves * kPfWaveQ;  // queries per workgroup
+constexpr int kPfTiles = 2;                     // 32-token tiles per iteration
+constexpr int kPfKeys = kPfTiles * HC_TILE;     // keys per iteration
+constexpr int kPfThreads = kPfWaves * 64;
+
+struct PfArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int64_t q_sb, q_sh, q_st;  // element strides: batch, head, token (channels contiguous)
+  int64_t k_sb, k_sh, k_st;
+  int64_t v_sb, v_sh, v_st;
+  int64_t o_sb, o_sh, o_st;
+  int Hq, Hkv, Lq, Lk, nqb, rows;  // rows = batch * Hkv
+  float scale_log2;
+};
+
+// LDS elements of one buffer set (K tiles then V tiles).
+constexpr int kPfSetElems = 2 * kPfTiles * HC_TILE_ELEMS;
+
+template <typename T>
+constexpr size_t pf_lds_bytes() {
+  return (size_t)2 * kPfSetElems * sizeof(T);
+}
+
+// Four elements of T as one vector store (8 bytes for 16-bit types).
+template <typename T>
+struct Quad {
+  typedef T type __attribute__((ext_vector_type(4)));
+};
+
+// Write channel e of the thread's 4 staged V tokens as one 4-element group.
+template <typename T>
+__device__ __forceinline__ void store_v_quad(T* dst, const typename Elem<T>::vec8 (&vr)[4], int e) {
+  if constexpr (sizeof(T) == 2) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x4* w = reinterpret_cast<const u32x4*>(&vr[0]);
+    const int j = e >> 1;
+    const uint32_t a0 = w[0][j], a1 = w[1][j], a2 = w[2][j], a3 = w[3][j];
+    u32x2 r;
+    if (e & 1) {
+      r.x = (a0 >> 16) | (a1 & 0xffff0000u);
+      r.y = (a2 >> 16) | (a3 & 0xffff0000u);
+    } else {
+      r.x = (a0 & 0xffffu) | (a1 << 16);
+      r.y = (a2 & 0xffffu) | (a3 << 16);
+    }
+    *reinterpret_cast<u32x2*>(dst) = r;
+  } else {
+    typename Quad<T>::type r;
+    r.x = vec8_at<T>(vr[0], e);
+    r.y = vec8_at<T>(vr[1], e);
+    r.z = vec8_at<T>(vr[2], e);
+    r.w = vec8_at<T>(vr[3], e);
+    *reinterpret_cast<typename Quad<T>::type*>(dst) = r;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_attn_kernel(const PfArgs a) {
+  typedef typename Elem<T>::vec8 vec8;
+  extern __shared__ __attribute__((aligned(16))) unsigned char pf_lds[];
+  T* lds = reinterpret_cast<T*>(pf_lds);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g4 = lane >> 4, n16 = lane & 15;
+  const int G = a.Hq / a.Hkv;
+  // Workgroup -> (KV row, query head of its group, query block).
+  const int x = blockIdx.x;
+  const int row = x % a.rows;
+  const int rest = x / a.rows;
+  const int gi = rest % G;
+  const int qb = a.nqb - 1 - rest / G;
+  const int b = row / a.Hkv, kvh = row % a.Hkv, hq = kvh * G + gi;
+
+  const T* qbase = reinterpret_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
+  const T* kbase = reinterpret_cast<const T*>(a.k) + b * a.k_sb + kvh * a.k_sh;
+  const T* vbase = reinterpret_cast<const T*>(a.v) + b * a.v_sb + kvh * a.v_sh;
+  T* obase = reinterpret_cast<T*>(a.out) + b * a.o_sb + hq * a.o_sh;
+
+  const int shift = a.Lk - a.Lq;  // position of query i is shift + i
+  const int q_last = min(qb * kPfBlockQ + kPfBlockQ - 1, a.Lq - 1);
+  const int nit = (shift + q_last + 1 + kPfKeys - 1) / kPfKeys;
+  const int qw0 = qb * kPfBlockQ + wave * kPfWaveQ;
+  const bool active = qw0 < a.Lq;
+  const int pos_lo = shift + qw0;                           // first query position of this wave
+  const int pos_hi = shift + min(qw0 + kPfWaveQ - 1, a.Lq - 1);
+
+  // Q^T operands: column = query 16j + n16, k-slots = channels 32s + 8*g4 + [0, 8).
+  vec8 qop[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int qi = qw0 + 16 * j + n16;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      qop[j][s] = qi < a.Lq ? load8(qbase + (int64_t)qi * a.q_st + 32 * s + 8 * g4) : zero8<T>();
+  }
+
+  f32x4 o[8][2];
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) o[db][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+
+  // Staging roles.  K: four chunks (token, 8 channels) per thread, chunk
+  // u = r*256 + tid is tile u/512, tile chunk u%512 = ((h*4+s)*4+g)*16+m.
+  // V: 4 tokens {16*half + 4*vg + [0,4)} of tile vc, channels 8*vd + [0, 8).
+  const int vc = tid >> 7, vg = (tid >> 5) & 3, vhalf = (tid >> 4) & 1, vd = tid & 15;
+  vec8 kreg[4], vreg[4];
+
+  auto stage_load = [&](int it) {
+    const int t0 = it * kPfKeys;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int u = r * kPfThreads + tid;
+      const int c = u >> 9, v = u & 511;
+      const int h = v >> 8, s = (v >> 6) & 3, g = (v >> 4) & 3, mm = v & 15;
+      const int t = t0 + c * HC_TILE + h * 16 + mm;
+      kreg[r] = t < a.Lk ? load8(kbase + (int64_t)t * a.k_st + 32 * s + 8 * g) : zero8<T>();
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + vc * HC_TILE + vhalf * 16 + vg * 4 + r;
+      vreg[r] = t < a.Lk ? load8(vbase + (int64_t)t * a.v_st + 8 * vd) : zero8<T>();
+    }
+  };
+  auto stage_store = [&](int buf) {
+    T* sk = lds + buf * kPfSetElems;
+    T* sv = sk + kPfTiles * HC_TILE_ELEMS;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int u = r * kPfThreads + tid;
+      *reinterpret_cast<vec8*>(sk + (u >> 9) * HC_TILE_ELEMS + (u & 511) * 8) = kreg[r];
+    }
+    T* dv = sv + vc * HC_TILE_ELEMS + vhalf * 4;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = 8 * vd + e, mt = d >> 4, n = d & 15;
+      store_v_quad<T>(dv + mt * 512 + (vg * 16 + ((n + mt) & 15)) * 8, vreg, e);
+    }
+  };
+
+  stage_load(0);
+  stage_store(0);
+  __syncthreads();
+
+  for (int it = 0; it < nit; ++it) {
+    const int cur = it & 1;
+    const int t0 = it * kPfKeys;
+    if (it + 1 < nit) stage_load(it + 1);
+    if (active && t0 <= pos_hi) {
+      const T* sk = lds + cur * kPfSetElems;
+      const T* sv = sk + kPfTiles * HC_TILE_ELEMS;
+      // S^T blocks: rows = keys 16*tb + 4*g4 + r, column = query 16j + n16.
+      f32x4 sacc[4][2];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) sacc[tb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const T* kt = sk + (tb >> 1) * HC_TILE_ELEMS + (tb & 1) * 4 * 64 * 8;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const vec8 ka = load8(kt + (s * 64 + lane) * 8);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) sacc[tb][j] = mma_16x16x32(ka, qop[j][s], sacc[tb][j]);
+        }
+      }
+      const bool need_mask = t0 + kPfKeys - 1 > pos_lo;
+      vec8 pb[2][2];  // [tile][query block]: B operand of the P.V step
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int pj = pos_lo + 16 * j + n16;
+        float xs[4][4];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float sv2 = sacc[tb][j][r] * a.scale_log2;
+            if (need_mask && t0 + 16 * tb + 4 * g4 + r > pj) sv2 = -INFINITY;
+            xs[tb][r] = sv2;
+            mx = fmaxf(mx, sv2);
+          }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mnew = fmaxf(m[j], mx);
+        const float msafe = mnew == -INFINITY ? 0.f : mnew;
+        const float alpha = fast_exp2(m[j] - msafe);
+        m[j] = mnew;
+        float ps = 0.f;
+        float p[4][4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            p[tb][r] = fast_exp2(xs[tb][r] - msafe);
+            ps += p[tb][r];
+          }
+        l[j] = fmaf(l[j], alpha, ps);
+#pragma unroll
+        for (int db = 0; db < 8; ++db)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[db][j][r] *= alpha;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float pv[8] = {p[2 * c][0],     p[2 * c][1],     p[2 * c][2],     p[2 * c][3],
+                               p[2 * c + 1][0], p[2 * c + 1][1], p[2 * c + 1][2], p[2 * c + 1][3]};
+          pb[c][j] = pack8<T>(pv);
+        }
+      }
+      // O^T blocks: rows = channels 16*db + 4*g4 + r, column = query.
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const T* vt = sv + c * HC_TILE_ELEMS;
+#pragma unroll
+        for (int db = 0; db < 8; ++db) {
+          const vec8 va = load8(vt + db * 512 + (g4 * 16 + ((n16 + db) & 15)) * 8);
+#pragma unroll
+          for (int j = 0; j < 2; ++j) o[db][j] = mma_16x16x32(va, pb[c][j], o[db][j]);
+        }
+      }
+    }
+    if (it + 1 < nit) stage_store(cur ^ 1);
+    __syncthreads();
+  }
+
+  if (!active) return;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    float lt = l[j];
+    lt += __shfl_xor(lt, 16, 64);
+    lt += __shfl_xor(lt, 32, 64);
+    const float inv = 1.f / lt;
+    const int qi = qw0 + 16 * j + n16;
+    if (qi >= a.Lq) continue;
+    T* orow = obase + (int64_t)qi * a.o_st + 4 * g4;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      typename Quad<T>::type r;
+      r.x = Elem<T>::from_f32(o[db][j][0] * inv);
+      r.y = Elem<T>::from_f32(o[db][j][1] * inv);
+      r.z = Elem<T>::from_f32(o[db][j][2] * inv);
+      r.w = Elem<T>::from_f32(o[db][j][3] * inv);
+      *reinterpret_cast<typename Quad<T>::type*>(orow + 16 * db) = r;
+    }
+  }
+}
+
+template <typename T>
+int launch_prefill(const PfArgs& a, hipStream_t stream) {
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_kernel<T>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<T>());
+  });
+  if (attr != hipSuccess) return set_error(HC_ERR_HIP, "hc_prefill_attn: %s", hipGetErrorString(attr));
+  const int64_t grid = (int64_t)a.rows * (a.Hq / a.Hkv) * a.nqb;
+  hipLaunchKernelGGL((prefill_attn_kernel<T>), dim3((unsigned)grid), dim3(kPfThreads), pf_lds_bytes<T>(), stream,
+                     a);
+  return check_launch("hc_prefill_attn");
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+}  // namespace hc
+
+using namespace hc;
+
+extern "C" int hc_prefill_attn(int dtype, const void* q, const int64_t* q_strides, const void* k,
+                               const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out,
+                               const int64_t* out_strides, int batch, int q_heads, int kv_heads, int q_len,
+                               int kv_len, float scale, void* stream) {
+  clear_error();
+  const int esz = dtype == HC_DTYPE_F32 ? 4 : (dtype == HC_DTYPE_BF16 || dtype == HC_DTYPE_F16) ? 2 : 0;
+  if (esz == 0) return set_error(HC_ERR_INVALID, "hc_prefill_attn: unknown dtype %d", dtype);
+  if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || q_len < 0 || kv_len < 0)
+    return set_error(HC_ERR_INVALID, "hc_prefill_attn: batch=%d q_heads=%d kv_heads=%d q_len=%d kv_len=%d", batch,
+                     q_heads, kv_heads, q_len, kv_len);
+  if (q_len > kv_len)
+    return set_error(HC_ERR_INVALID, "hc_prefill_attn: q_len %d exceeds kv_len %d (queries are the last keys)", q_len,
+                     kv_len);
+  if (batch == 0 || q_len == 0) return HC_OK;
+  if (!q || !k || !v || !out || !q_strides || !k_strides || !v_strides || !out_strides)
+    return set_error(HC_ERR_INVALID, "hc_prefill_attn: null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+    return set_error(HC_ERR_INVALID, "hc_prefill_attn: buffers must be 16-byte aligned");
+  const int64_t* st[4] = {q_strides, k_strides, v_strides, out_strides};
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 3; ++j)
+      if (st[i][j] < 0 || (st[i][j] * esz) % 16)
+        return set_error(HC_ERR_INVALID, "hc_prefill_attn: strides must be non-negative 16-byte multiples");
+  if (!std::isfinite(scale)) return set_error(HC_ERR_INVALID, "hc_prefill_attn: scale must be finite");
+  PfArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.out = out;
+  a.q_sb = q_strides[0], a.q_sh = q_strides[1], a.q_st = q_strides[2];
+  a.k_sb = k_strides[0], a.k_sh = k_strides[1], a.k_st = k_strides[2];
+  a.v_sb = v_strides[0], a.v_sh = v_strides[1], a.v_st = v_strides[2];
+  a.o_sb = out_strides[0], a.o_sh = out_strides[1], a.o_st = out_strides[2];
+  a.Hq = q_heads;
+  a.Hkv = kv_heads;
+  a.Lq = q_len;
+  a.Lk = kv_len;
+  a.nqb = (q_len + kPfBlockQ - 1) / kPfBlockQ;
+  a.rows = batch * kv_heads;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  const int64_t grid = (int64_t)a.rows * (q_heads / kv_heads) * a.nqb;
+  if (grid > 0x7fffffffLL) return set_error(HC_ERR_INVALID, "hc_prefill_attn: grid too large");
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case HC_DTYPE_BF16: return launch_prefill<__bf16>(a, s);
+    case HC_DTYPE_F16: return launch_prefill<_Float16>(a, s);
+    default: return launch_prefill<float>(a, s);
+  }
+}

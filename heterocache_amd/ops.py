@@ -222,6 +222,46 @@ def copy_rows(src_k, src_v, src_bh, dst_k, dst_v, dst_bh, counts, dst_is_host=Fa
                                 _stream(stream, src_k)))
 
 
+def prefill_attn(q, k, v, scale, out=None, stream=None):
+    """Causal attention of the last Lq positions over Lk keys (hc_prefill_attn).
+
+    q: [B, Hq, Lq, 128]; k, v: [B, Hkv, Lk, 128] (any batch/head/token
+    strides, unit channel stride; Lq <= Lk, query i sits at position
+    Lk - Lq + i).  Returns out [B, Lq, Hq, 128] (or writes the given `out`,
+    which may be any view of that shape with unit channel stride).
+    """
+    lib = _lib.load()
+    _require_cuda(q, k, v, out)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k and v must be [B, H, L, 128]")
+    B, Hq, Lq, D = q.shape
+    if D != HEAD_DIM or k.shape[-1] != HEAD_DIM or v.shape != k.shape or k.shape[0] != B:
+        raise ValueError(f"q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}: head_dim must be 128 "
+                         "and k, v must share [B, Hkv, Lk]")
+    Hkv, Lk = k.shape[1], k.shape[2]
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads are not a multiple of {Hkv} KV heads")
+    if Lq > Lk:
+        raise ValueError(f"{Lq} queries exceed {Lk} keys")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise TypeError("q, k and v must share a dtype")
+    if out is None:
+        out = torch.empty((B, Lq, Hq, HEAD_DIM), dtype=q.dtype, device=q.device)
+    elif out.shape != (B, Lq, Hq, HEAD_DIM) or out.dtype != q.dtype:
+        raise ValueError(f"out must be [{B}, {Lq}, {Hq}, {HEAD_DIM}] of {q.dtype}")
+    for name, t in (("q", q), ("k", k), ("v", v), ("out", out)):
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name} needs a unit channel stride")
+    strides = np.array([[q.stride(0), q.stride(1), q.stride(2)],
+                        [k.stride(0), k.stride(1), k.stride(2)],
+                        [v.stride(0), v.stride(1), v.stride(2)],
+                        [out.stride(0), out.stride(2), out.stride(1)]], dtype=np.int64)
+    base = strides.ctypes.data
+    _lib.check(lib.hc_prefill_attn(dtype_code(q.dtype), _ptr(q), base, _ptr(k), base + 24, _ptr(v), base + 48,
+                                   _ptr(out), base + 72, B, Hq, Hkv, Lq, Lk, float(scale), _stream(stream, q)))
+    return out
+
+
 def append(k_new, v_new, kstore, vstore, row_tile_off, row_len, row_cap, status=None, stream=None):
     """Write k_new/v_new [rows, 128] at slot row_len[r] of every row, then row_len += 1."""
     lib = _lib.load()

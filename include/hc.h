@@ -134,6 +134,25 @@ int hc_copy_rows(int dtype, const void* src_k, const void* src_v, const int64_t*
                  void* dst_k, void* dst_v, int dst_is_host, const int64_t* dst_off, int64_t dst_tok_stride,
                  const int32_t* count, int njobs, int max_count, int max_workgroups, void* stream);
 
+/*
+ * Causal prefill attention (flash-attention forward), head_dim 128:
+ *   out[b, i, hq, :] = sum_t softmax_t(scale * q[b, hq, i] . k[b, hq/G, t]) v[b, hq/G, t],
+ *   t <= kv_len - q_len + i,  G = q_heads / kv_heads.
+ * The queries are the last q_len of the kv_len positions (bottom-right causal
+ * alignment), so the same call serves a whole prompt (q_len == kv_len) and a
+ * chunk of a chunked prefill over the keys staged so far.  Each of q, k, v and
+ * out is addressed as base + b*strides[0] + h*strides[1] + t*strides[2] + c
+ * (element strides, 16-byte multiples; channels contiguous), so the
+ * projections' [B, T, H, 128] layout is read without a copy.  Arithmetic: MFMA
+ * on the input type, fp32 accumulation and softmax, probabilities rounded to
+ * the input type for the P.V product.  Replaces the flash-attn prefill call
+ * of LlamaAttention / Qwen2Attention (heterocache/llama_model.py:353-361,
+ * through transformers' flash_attention_forward).
+ */
+int hc_prefill_attn(int dtype, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                    const void* v, const int64_t* v_strides, void* out, const int64_t* out_strides, int batch,
+                    int q_heads, int kv_heads, int q_len, int kv_len, float scale, void* stream);
+
 /* hc_score flags */
 #define HC_SCORE_CAUSAL_WINDOW 1 /* window row w sees keys t <= L - W + w (kv_cluster.py:169-175) */
 #define HC_SCORE_SUM_WINDOW 2    /* sum probabilities over the W rows of a query head (kv_cluster.py:178) */

@@ -264,6 +264,36 @@ def decode_attention(q, ks, vs, scale=None):
     return out
 
 
+def prefill_attention(q, k, v, scale=None):
+    """Causal prefill attention, float64 closed form.
+
+    Stands in for the flash-attn prefill call of LlamaAttention
+    (heterocache/llama_model.py:353-361, transformers' flash_attention_forward
+    with causal=True).  q: [B, Hq, Lq, d]; k, v: [B, Hkv, Lk, d] with
+    Lq <= Lk; query i sits at position Lk - Lq + i and sees keys t <= that
+    position (flash-attn's bottom-right alignment).  Query head h reads KV
+    head h // (Hq // Hkv).  Returns [B, Lq, Hq, d] float64.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    B, Hq, Lq, d = q.shape
+    Hkv, Lk = k.shape[1], k.shape[2]
+    G = Hq // Hkv
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    visible = np.arange(Lk)[None, :] <= (Lk - Lq + np.arange(Lq))[:, None]
+    out = np.zeros((B, Lq, Hq, d), dtype=np.float64)
+    for b in range(B):
+        for h in range(Hq):
+            z = scale * (q[b, h] @ k[b, h // G].T)
+            z = np.where(visible, z, -np.inf)
+            z -= z.max(axis=-1, keepdims=True)
+            p = np.exp(z)
+            p /= p.sum(axis=-1, keepdims=True)
+            out[b, :, h] = p @ v[b, h // G]
+    return out
+
+
 # --------------------------------------------------------------------------
 # a12, a13: pivot drift and retrieval
 # --------------------------------------------------------------------------

@@ -233,6 +233,40 @@ def test_decode_attention_closed_forms():
     assert not O.decode_attention(q, [np.zeros((0, 128))], [np.zeros((0, 128))]).any()
 
 
+def test_prefill_attention_matches_sdpa_float64():
+    """Square prompt: torch's causal SDPA; a chunk (Lq < Lk): SDPA with the
+    lower-triangular mask shifted by Lk - Lq (torch.tril's diagonal offset),
+    each with the KV heads repeated over the query group."""
+    rng = np.random.default_rng(15)
+    for B, Hq, Hkv, Lq, Lk in ((1, 4, 2, 37, 37), (2, 6, 3, 20, 75), (1, 2, 2, 1, 9)):
+        q = rng.standard_normal((B, Hq, Lq, 128))
+        k = rng.standard_normal((B, Hkv, Lk, 128))
+        v = rng.standard_normal((B, Hkv, Lk, 128))
+        got = O.prefill_attention(q, k, v)
+        G = Hq // Hkv
+        kt = torch.tensor(k).repeat_interleave(G, dim=1)
+        vt = torch.tensor(v).repeat_interleave(G, dim=1)
+        if Lq == Lk:
+            ref = F.scaled_dot_product_attention(torch.tensor(q), kt, vt, is_causal=True)
+        else:
+            mask = torch.ones(Lq, Lk, dtype=torch.bool).tril(diagonal=Lk - Lq)
+            ref = F.scaled_dot_product_attention(torch.tensor(q), kt, vt, attn_mask=mask)
+        assert np.abs(got - ref.transpose(1, 2).numpy()).max() < 1e-12
+
+
+def test_prefill_attention_closed_forms():
+    rng = np.random.default_rng(16)
+    q = rng.standard_normal((1, 2, 5, 128))
+    k = rng.standard_normal((1, 1, 5, 128))
+    v = rng.standard_normal((1, 1, 5, 128))
+    out = O.prefill_attention(q, k, v)
+    assert np.allclose(out[0, 0, :], v[0, 0, 0])            # the first query sees key 0 only
+    last = O.decode_attention(q[0, :, -1][None], [k[0, 0]], [v[0, 0]])
+    assert np.allclose(out[0, -1], last[0])                  # the last query sees every key
+    ones = O.prefill_attention(q, np.ones((1, 1, 5, 128)), v)
+    assert np.allclose(ones[0, 2, 1], v[0, 0, :3].mean(axis=0))  # equal logits: mean of the visible values
+
+
 def test_c_oracle_decode_matches_numpy():
     rng = np.random.default_rng(14)
     lens = [3, 5000, 129]

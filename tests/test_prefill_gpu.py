@@ -1,0 +1,120 @@
+"""Prefill attention (hc_prefill_attn) vs the float64 closed form of the oracle.
+
+Parity bar: max-abs <= 2e-2 (bf16), 1e-2 (fp16), 1e-4 (fp32), the decode
+bar: both kernels round the softmax probabilities to the input type for the
+P.V product and accumulate in fp32.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from heterocache_amd import ops
+from oracle import hc_oracle as O
+from tests.gpu_util import ATTN_TOL, TORCH_DT, as_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(dev, dt, B, Hq, Hkv, Lq, Lk, seed, layout="bhld", pad=0):
+    """Seeded q [B, Hq, Lq, 128], k/v [B, Hkv, Lk, 128] on the device.
+
+    layout "blhd" builds them as transposed views of [B, L, H, 128] tensors,
+    the projections' layout.  `pad` extra NaN tokens follow each K/V row in
+    memory, so a read past Lk would poison the output.
+    """
+    g = torch.Generator().manual_seed(seed)
+    tdt = TORCH_DT[dt]
+    q = torch.randn(B, Hq, Lq, 128, generator=g)
+    k = torch.randn(B, Hkv, Lk, 128, generator=g)
+    v = torch.randn(B, Hkv, Lk, 128, generator=g)
+    k[..., :4] *= 6  # outlier channels, as post-RoPE keys carry
+    if layout == "blhd":
+        qd = q.transpose(1, 2).contiguous().to(tdt).to(dev).transpose(1, 2)
+        kfull = torch.full((B, Lk + pad, Hkv, 128), float("nan"), dtype=tdt, device=dev)
+        vfull = torch.full_like(kfull, float("nan"))
+        kfull[:, :Lk] = k.transpose(1, 2).to(tdt).to(dev)
+        vfull[:, :Lk] = v.transpose(1, 2).to(tdt).to(dev)
+        kd, vd = kfull[:, :Lk].transpose(1, 2), vfull[:, :Lk].transpose(1, 2)
+    else:
+        qd = q.to(tdt).to(dev)
+        kfull = torch.full((B, Hkv, Lk + pad, 128), float("nan"), dtype=tdt, device=dev)
+        vfull = torch.full_like(kfull, float("nan"))
+        kfull[:, :, :Lk] = k.to(tdt).to(dev)
+        vfull[:, :, :Lk] = v.to(tdt).to(dev)
+        kd, vd = kfull[:, :, :Lk], vfull[:, :, :Lk]
+    return qd, kd, vd
+
+
+CASES = [
+    # B, Hq, Hkv, Lq, Lk
+    (1, 8, 2, 300, 300),     # whole prompt, GQA 4, ragged last block
+    (2, 4, 4, 64, 200),      # chunk over staged keys, no GQA, batch 2
+    (1, 7, 1, 1, 129),       # one query (GQA 7), keys past a tile edge
+    (1, 4, 1, 130, 1000),    # chunk spanning two query blocks
+    (1, 2, 1, 1, 1),         # single key
+    (1, 4, 2, 33, 33),       # just past one 32-token tile
+    (1, 28, 4, 256, 256),    # Qwen2.5-7B head geometry
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("case", CASES)
+def test_prefill_matches_oracle(dev, dt, case):
+    B, Hq, Hkv, Lq, Lk = case
+    seed = 2000 + sum(case)
+    print(f"prefill_attn dt={dt} B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} seed={seed}", flush=True)
+    q, k, v = _inputs(dev, dt, B, Hq, Hkv, Lq, Lk, seed, pad=40)
+    scale = 1.0 / math.sqrt(128)
+    out = ops.prefill_attn(q, k, v, scale)
+    torch.cuda.synchronize()
+    ref = O.prefill_attention(as_np(q), as_np(k), as_np(v), scale)
+    got = as_np(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref).max()
+    assert err <= ATTN_TOL[dt], f"max-abs {err}"
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_prefill_projection_layout_and_out_view(dev, dt):
+    """Inputs as transposed [B, L, H, 128] views; output written into a view
+    of a wider buffer; other elements untouched."""
+    B, Hq, Hkv, Lq, Lk = 2, 8, 2, 150, 150
+    print(f"prefill_attn layout dt={dt}", flush=True)
+    q, k, v = _inputs(dev, dt, B, Hq, Hkv, Lq, Lk, 77, layout="blhd", pad=8)
+    buf = torch.full((B, Lq, Hq, 256), 7.0, dtype=q.dtype, device=dev)
+    out = buf[..., 64:192]
+    ops.prefill_attn(q, k, v, 0.1, out=out)
+    torch.cuda.synchronize()
+    ref = O.prefill_attention(as_np(q), as_np(k), as_np(v), 0.1)
+    assert np.abs(as_np(out) - ref).max() <= ATTN_TOL[dt]
+    assert (buf[..., :64] == 7).all() and (buf[..., 192:] == 7).all()
+
+
+def test_prefill_chunks_equal_whole_prompt(dev):
+    """Chunked prefill: attention of each chunk over the keys staged so far
+    matches the rows of the whole-prompt call (same kernel, same keys)."""
+    B, Hq, Hkv, L, C = 1, 8, 2, 700, 256
+    print("prefill_attn chunks", flush=True)
+    q, k, v = _inputs(dev, "bf16", B, Hq, Hkv, L, L, 99)
+    whole = ops.prefill_attn(q, k, v, 1 / math.sqrt(128))
+    parts = []
+    for s in range(0, L, C):
+        e = min(L, s + C)
+        parts.append(ops.prefill_attn(q[:, :, s:e], k[:, :, :e], v[:, :, :e], 1 / math.sqrt(128)))
+    torch.cuda.synchronize()
+    chunked = torch.cat(parts, dim=1)
+    ref = O.prefill_attention(as_np(q), as_np(k), as_np(v))
+    assert np.abs(as_np(chunked) - ref).max() <= ATTN_TOL["bf16"]
+    assert np.abs(as_np(chunked) - as_np(whole)).max() <= ATTN_TOL["bf16"]
+
+
+def test_prefill_rejects_bad_shapes(dev):
+    q = torch.zeros(1, 4, 10, 128, dtype=torch.bfloat16, device=dev)
+    k = torch.zeros(1, 2, 5, 128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        ops.prefill_attn(q, k, k, 0.1)          # more queries than keys
+    k3 = torch.zeros(1, 3, 20, 128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        ops.prefill_attn(q, k3, k3, 0.1)        # 4 query heads over 3 KV heads
