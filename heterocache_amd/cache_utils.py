@@ -159,6 +159,13 @@ class HeteroCache(DynamicCache):
         self.bsz = None
         self.head_dim = None
         self.prefill_len = None
+        # Chunked prefill: declared prompt length, per-layer staged K/V
+        # [B, Hkv, prompt, 128], tokens staged, and the last window_size
+        # query rows seen (the rows the selection scores use).
+        self._prompt_len = None
+        self._stage = [None] * self.num_layers
+        self._staged = [0] * self.num_layers
+        self._q_tail = [None] * self.num_layers
         self._seen_tokens = 0
         self._side = None
         # Model-wide buffers: one K/V arena for every layer's rows, and the
@@ -185,6 +192,62 @@ class HeteroCache(DynamicCache):
         for i in range(self.num_layers):
             self._flush_append(i)
         return [s.row_len if s is not None else None for s in self.stores]
+
+    def begin_prefill(self, prompt_len):
+        """Declare the prompt length ahead of a chunked prefill.
+
+        The reference has no chunked prefill (one update per layer holds the
+        whole prompt).  After this call, prefill chunks of any length (one
+        token included) are staged per layer until `prompt_len` tokens have
+        arrived; each chunk's attention runs over the keys staged so far, and
+        the selection (init_coefficient, prefill_select), the keep-head store
+        writes and the full-KV tier copy run once, on the complete prompt,
+        exactly as a single-shot prefill of the same K/V would."""
+        if self.bsz is not None:
+            raise RuntimeError("begin_prefill must precede the first update")
+        if int(prompt_len) < 1:
+            raise ValueError(f"prompt length {prompt_len} must be positive")
+        self._prompt_len = int(prompt_len)
+
+    def prefill_pending(self, layer_idx):
+        """True while a declared chunked prefill still expects tokens for this layer."""
+        return self._prompt_len is not None and self._staged[layer_idx] < self._prompt_len
+
+    def _stage_chunk(self, key_states, value_states, layer_idx, cache_kwargs):
+        B, H, c, D = key_states.shape
+        start = self._staged[layer_idx]
+        end = start + c
+        if end > self._prompt_len:
+            raise ValueError(f"layer {layer_idx}: chunk ends at token {end}, past the declared prompt "
+                             f"length {self._prompt_len}")
+        if self._stage[layer_idx] is None:
+            shape = (B, H, self._prompt_len, D)
+            self._stage[layer_idx] = (torch.empty(shape, dtype=key_states.dtype, device=key_states.device),
+                                      torch.empty(shape, dtype=value_states.dtype, device=value_states.device))
+        kb, vb = self._stage[layer_idx]
+        kb[:, :, start:end].copy_(key_states)
+        vb[:, :, start:end].copy_(value_states)
+        q = cache_kwargs.get("query_states") if cache_kwargs else None
+        if q is not None:
+            tail = q if self._q_tail[layer_idx] is None else torch.cat([self._q_tail[layer_idx], q], dim=2)
+            self._q_tail[layer_idx] = tail[:, :, -self.window_size:]
+        self._staged[layer_idx] = end
+        k, v = kb[:, :, :end], vb[:, :, :end]
+        if end == self._prompt_len:
+            self._prefill_update(k, v, layer_idx)
+            self._stage[layer_idx] = None  # the returned views keep the buffers alive
+        return k, v
+
+    def _prefill_queries(self, query_states, layer_idx):
+        """Queries the selection scores read: the call's own rows, or after a
+        chunked prefill the last window_size rows of the whole prompt."""
+        tail = self._q_tail[layer_idx]
+        if tail is None:
+            return query_states
+        if tail.shape[2] < self.window_size:
+            raise ValueError(f"layer {layer_idx}: {tail.shape[2]} query rows staged, the observation window "
+                             f"needs {self.window_size}")
+        return tail
 
     def _side_stream(self, device):
         if self._side is None:
@@ -233,25 +296,31 @@ class HeteroCache(DynamicCache):
             if self.head_dim != 128:
                 raise ValueError(f"head_dim {self.head_dim} is not supported (128 only)")
         if not hasattr(self, "base_compress_len"):
-            self.prefill_len = key_states.shape[-2]
+            self.prefill_len = self._prompt_len if self._prompt_len is not None else key_states.shape[-2]
             self.base_compress_len = get_compress_len(self.compression_ratio, self.full_heads, self.prefill_len,
                                                       self.total_kv_heads)
         if self.stores[layer_idx] is None:
             self._init_storage(key_states.device, key_states.dtype)
-        store = self.stores[layer_idx]
-        seq_len = key_states.shape[-2]
-        if seq_len > 1:
-            self.prefill_len = seq_len
-            keep = self.data["need_to_keep_counts"][layer_idx]
-            if keep:
-                bh = [(b, h) for b in range(self.bsz) for h in keep]
-                store.write_rows(key_states, value_states, bh, [b * self.num_kv_heads + h for b, h in bh],
-                                 [seq_len] * len(bh))
-            self._backup_full_tier(key_states, value_states, layer_idx)
+        if self.prefill_pending(layer_idx):
+            return self._stage_chunk(key_states, value_states, layer_idx, cache_kwargs)
+        if key_states.shape[-2] > 1:
+            self._prefill_update(key_states, value_states, layer_idx)
             return key_states, value_states
         self._flush_append(layer_idx)
         self._pending[layer_idx] = (key_states, value_states)
         return key_states, value_states
+
+    def _prefill_update(self, key_states, value_states, layer_idx):
+        """Prefill branch of update (heterocache/cache_utils.py:906-968): keep
+        heads store the whole prompt; the satellites' K/V go to the tier."""
+        seq_len = key_states.shape[-2]
+        self.prefill_len = seq_len
+        keep = self.data["need_to_keep_counts"][layer_idx]
+        if keep:
+            bh = [(b, h) for b in range(self.bsz) for h in keep]
+            self.stores[layer_idx].write_rows(key_states, value_states, bh,
+                                              [b * self.num_kv_heads + h for b, h in bh], [seq_len] * len(bh))
+        self._backup_full_tier(key_states, value_states, layer_idx)
 
     def _backup_full_tier(self, key_states, value_states, layer_idx):
         """Full-KV tier of the satellite heads (heterocache/cache_utils.py:939-967)."""
@@ -303,6 +372,9 @@ class HeteroCache(DynamicCache):
     def init_coefficient(self, query_states, key_states, layer_idx):
         """Pivot reference sets: top-base of the pooled last-query scores
         (heterocache/cache_utils.py:1149-1190), kept as device bitmasks."""
+        if self.prefill_pending(layer_idx):
+            return
+        query_states = self._prefill_queries(query_states, layer_idx)
         pivots = list(self.data["need_to_select_counts"][layer_idx])
         rel = self.data["leader_member_relations"][layer_idx]
         st = _LayerDrift()
@@ -359,6 +431,9 @@ class HeteroCache(DynamicCache):
     def prefill_select(self, query_states, key_states, value_states, layer_idx):
         """Compressed heads keep their top cap_h tokens in temporal order
         (heterocache/cache_utils.py:782-882)."""
+        if self.prefill_pending(layer_idx):
+            return
+        query_states = self._prefill_queries(query_states, layer_idx)
         n_c = self.data["need_to_compress_counts"][layer_idx]
         if n_c == 0:
             return

@@ -3,13 +3,16 @@
 Drop-in for heterocache/llama_model.py:279-405 (`LlamaAttention`): same
 constructor, same forward contract, same call order on the cache:
   prefill: update -> init_coefficient -> prefill_select -> full causal
-           attention over the uncompressed K/V -> o_proj
+           attention over the uncompressed K/V (hc_prefill_attn) -> o_proj;
+           in a chunked prefill every chunk runs this branch, and the two
+           selection calls act once the declared prompt is complete
   decode:  update -> decode attention (hc_decode_attn, replacing
            flash_attn_with_kvcache) -> decode_select -> o_proj
 The forward accepts the transformers 4.57 keyword set (attention_mask,
 position_ids, output_attentions, use_cache, cache_position,
 position_embeddings, past_key_values) and the 5.x one (extra **kwargs).
 """
+import weakref
 from typing import Optional, Tuple
 
 import torch
@@ -17,21 +20,49 @@ import torch.nn as nn
 import torch.nn.functional as F
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
+from . import ops
 from .cache_utils import HeteroCache
 
 
+# The last 4-D mask checked by _plain_causal (weakly held) and its verdict.
+_MASK_CHECK = {"ref": None, "shape": None, "plain": False}
+
+
+def _plain_causal(mask, Lq, Lk):
+    """True when a 4-D attention mask encodes bottom-right causality and
+    nothing else (no padding): allowed[i, t] == (t <= Lk - Lq + i) for every
+    batch row.  Every layer of one forward receives the same mask object, so
+    the device comparison (and its host sync) runs once per forward."""
+    ref = _MASK_CHECK["ref"]
+    if ref is not None and ref() is mask and _MASK_CHECK["shape"] == (Lq, Lk):
+        return _MASK_CHECK["plain"]
+    m = mask[..., :Lq, :Lk]
+    allowed = m if m.dtype == torch.bool else (m == 0)
+    want = torch.ones(Lq, Lk, dtype=torch.bool, device=m.device).tril(diagonal=Lk - Lq)
+    plain = m.shape[-2:] == (Lq, Lk) and bool((allowed == want).all().item())
+    _MASK_CHECK.update(ref=weakref.ref(mask), shape=(Lq, Lk), plain=plain)
+    return plain
+
+
 def prefill_attention(query_states, key_states, value_states, attention_mask, scaling):
-    """Causal attention of the L query positions over the uncompressed K/V
-    (outside the compressed path: the reference calls flash-attn here, this
-    build calls PyTorch's SDPA).  Queries are the last L positions of the
-    keys.  Returns [B, L, Hq*d]."""
+    """Causal attention of the L query positions over the Lk uncompressed
+    keys; the queries are the last L positions (a whole prompt, or one chunk
+    of a chunked prefill over the keys staged so far).  Returns [B, L, Hq*d].
+
+    On a ROCm device without a padding mask this is hc_prefill_attn (the
+    reference calls flash-attn here, heterocache/llama_model.py:353-361).  A
+    mask that carries padding goes through PyTorch's SDPA with that mask."""
     B, Hq, L, D = query_states.shape
     Lk = key_states.shape[2]
+    mask = attention_mask
+    if mask is not None and mask.dim() == 4 and _plain_causal(mask, L, Lk):
+        mask = None
+    if query_states.is_cuda and mask is None and D == ops.HEAD_DIM:
+        return ops.prefill_attn(query_states, key_states, value_states, scaling).view(B, L, Hq * D)
     q = query_states.contiguous()
     k = key_states.contiguous()
     v = value_states.contiguous()
     gqa = Hq != k.shape[1]
-    mask = attention_mask
     if mask is not None and mask.dim() == 4:
         mask = mask[..., :L, :Lk]
         out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=scaling, enable_gqa=gqa)
@@ -100,8 +131,11 @@ class LlamaAttention(nn.Module):
         cos, sin = position_embeddings
         cache_kwargs = {"sin": sin, "cos": cos, "cache_position": cache_position, "attention_mask": attention_mask,
                         "num_key_value_groups": self.num_key_value_groups, "query_states": query_states}
+        # A chunked prefill stays in the prefill branch until the declared
+        # prompt is complete, even for a one-token last chunk.
+        prefill = query_states.shape[-2] != 1 or cache.prefill_pending(self.layer_idx)
         key_states, value_states = cache.update(key_states, value_states, self.layer_idx, cache_kwargs)
-        if query_states.shape[-2] != 1:
+        if prefill:
             cache.init_coefficient(query_states, key_states, self.layer_idx)
             cache.prefill_select(query_states, key_states, value_states, self.layer_idx)
             out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling)

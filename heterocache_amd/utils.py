@@ -145,8 +145,22 @@ class install_attention_patch:
 
 
 def attach_cache(model, cache_config):
-    """Make generate() construct a HeteroCache(cache_config)."""
+    """Make generate() construct a HeteroCache(cache_config).
+
+    With generation_config.prefill_chunk_size set (transformers' chunked
+    prefill), the cache is told the prompt length, taken from the attention
+    mask or else from max_length - max_new_tokens."""
     def _prepare_cache_for_generation(self, generation_config, model_kwargs, *args, **kwargs):
-        model_kwargs["past_key_values"] = HeteroCache(cache_config)
+        cache = HeteroCache(cache_config)
+        if getattr(generation_config, "prefill_chunk_size", None):
+            mask = model_kwargs.get("attention_mask")
+            if mask is not None:
+                prompt = mask.shape[-1]
+            elif generation_config.max_new_tokens is not None and generation_config.max_length is not None:
+                prompt = generation_config.max_length - generation_config.max_new_tokens
+            else:
+                raise ValueError("chunked prefill needs the prompt length: pass attention_mask or max_new_tokens")
+            cache.begin_prefill(prompt)
+        model_kwargs["past_key_values"] = cache
     model._prepare_cache_for_generation = _prepare_cache_for_generation.__get__(model, model.__class__)
     return model

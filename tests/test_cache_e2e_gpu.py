@@ -41,7 +41,8 @@ def head_data(seed=0):
     return augment_head_data(raw, perms)
 
 
-def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True, groups=1):
+def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True, groups=1,
+        chunks=None):
     torch.manual_seed(0)
     B, Hq, Hkv, NL, D = 1, 32, 8, 2, 128
     data = head_data()
@@ -50,6 +51,8 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
                             num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=topk,
                             reference_quirks=quirks, batched_drift_check=batched, drift_check_groups=groups)
     cache = HeteroCache(cfg)
+    if chunks is not None:
+        cache.begin_prefill(L)
     orc = O.CacheOracle(data, B, Hq, Hkv, NL, 0.5, 0.5, 5, "avgpool", 5, retrieval_topk=topk, quirks=quirks,
                         select_before_attention=select_first)
     g = torch.Generator().manual_seed(1)
@@ -58,9 +61,20 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
         q = torch.randn((B, Hq, L, D), generator=g).to(dtype).to(dev)
         k = torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev)
         v = torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev)
-        k, v = cache.update(k, v, layer)
-        cache.init_coefficient(q, k, layer)
-        cache.prefill_select(q, k, v, layer)
+        if chunks is None:
+            kc, vc = cache.update(k, v, layer)
+            cache.init_coefficient(q, kc, layer)
+            cache.prefill_select(q, kc, vc, layer)
+        else:  # chunked prefill: the oracle still sees the whole prompt
+            bounds = np.cumsum([0] + list(chunks))
+            assert bounds[-1] == L
+            for s, e in zip(bounds[:-1], bounds[1:]):
+                qc = q[:, :, s:e]
+                kc, vc = cache.update(k[:, :, s:e], v[:, :, s:e], layer, {"query_states": qc})
+                assert kc.shape[2] == e
+                cache.init_coefficient(qc, kc, layer)
+                cache.prefill_select(qc, kc, vc, layer)
+                assert cache.prefill_pending(layer) == (e < L)
         orc.prefill(layer, as_np(q), as_np(k), as_np(v))
         last_q.append(q[:, :, -1:].clone())
     tol = 1e-4 if dtype == torch.float32 else 2e-2
@@ -129,3 +143,11 @@ def test_retrieval_topk(dev):
 
 def test_reference_quirks(dev):
     run(dev, torch.float32, quirks=True)
+
+
+@pytest.mark.parametrize("chunks", [[700, 700, 648], [1024, 1023, 1]])
+def test_chunked_prefill_equals_single_shot(dev, chunks):
+    """A prefill staged in chunks (the last one a single token in the second
+    case) selects, stores and decodes exactly as the single-shot oracle."""
+    trig = run(dev, torch.float32, chunks=chunks)
+    assert [t for _, _, t in trig] == [False] * 3 + [True] * 3

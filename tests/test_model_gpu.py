@@ -111,3 +111,19 @@ def test_qwen2_gqa7_batch2_generation_runs(dev):
     with torch.no_grad():
         out = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=11, do_sample=False)
     assert out.shape == (2, 611)
+
+
+def test_chunked_prefill_generation_matches_single_shot(dev):
+    """generate(prefill_chunk_size=256) on a compressed Llama: the chunks'
+    attention runs over the keys staged so far, selection runs once on the
+    whole prompt, and the greedy tokens equal the single-shot run's."""
+    cfg = llama_cfg(layers=3, q_heads=8, kv_heads=4)
+    classes = [[4, 3, 4, 1], [1, 1, 2, 4], [3, 4, 4, 1]]
+    relations = [{"1": [0, 2]}, {}, {"0": [1, 2]}]
+    model, cc = build(LlamaForCausalLM, cfg, head_json(classes, relations), torch.bfloat16, dev,
+                      compression_ratio=0.5, max_gen_len=24, decode_step=5, retrieval_topk=64)
+    ids = torch.randint(0, 512, (1, 1000), generator=torch.Generator().manual_seed(6)).to(dev)
+    with torch.no_grad():
+        whole = model.generate(ids, max_new_tokens=16, do_sample=False)
+        chunked = model.generate(ids, max_new_tokens=16, do_sample=False, prefill_chunk_size=256)
+    assert torch.equal(whole, chunked)
