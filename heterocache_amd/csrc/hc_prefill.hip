@@ -28,7 +28,14 @@
 //  * S^T = K Q^T per 16-key x 16-query block (K as the A operand), online
 //    base-2 softmax per query column, O^T += V^T P^T with P taken straight
 //    from the S accumulators (the tile layout's V token order is the order in
-//    which the accumulator holds the scores), fp32 accumulation.
+//    which the accumulator holds the scores), fp32 accumulation;
+//  * the softmax is VALU work beside the MFMAs (CDNA4 issues a wave64 VALU
+//    op over 4 cycles, v_exp at a quarter of that rate), so it is kept lean:
+//    the tile maximum is taken on raw scores and the scale folded into the
+//    exp2 argument's fma, masking runs only on tiles that cross the
+//    diagonal, and O is rescaled only when the running maximum grows by more
+//    than 2^8.
+#include <algorithm>
 #include <cfloat>
 #include <cmath>
 #include <mutex>
@@ -45,6 +52,7 @@ constexpr int kPfBlockQ = kPfWaves * kPfWaveQ;  // queries per workgroup
 constexpr int kPfTiles = 2;                     // 32-token tiles per iteration
 constexpr int kPfKeys = kPfTiles * HC_TILE;     // keys per iteration
 constexpr int kPfThreads = kPfWaves * 64;
+constexpr float kPfLazy = 8.f;                  // lazy-rescale threshold, log2 units
 
 struct PfArgs {
   const void* q;
@@ -106,7 +114,10 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
   extern __shared__ __attribute__((aligned(16))) unsigned char pf_lds[];
   T* lds = reinterpret_cast<T*>(pf_lds);
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // The wave index is read through readfirstlane so that every quantity
+  // derived from it (query range, masking, skipping) is known to be uniform
+  // and branches on it stay scalar.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, n16 = lane & 15;
   const int G = a.Hq / a.Hkv;
   // Workgroup -> (KV row, query head of its group, query block).
@@ -150,28 +161,48 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
   // Staging roles.  K: four chunks (token, 8 channels) per thread, chunk
   // u = r*256 + tid is tile u/512, tile chunk u%512 = ((h*4+s)*4+g)*16+m.
   // V: 4 tokens {16*half + 4*vg + [0,4)} of tile vc, channels 8*vd + [0, 8).
+  // Each load is a uniform per-iteration base plus a fixed 32-bit byte
+  // offset (the host bounds 64 token strides below 2^31 bytes).  In the last
+  // window, lanes past Lk read the window's first token instead (a select,
+  // not a branch, so no load waits at a join) and store zeros.
   const int vc = tid >> 7, vg = (tid >> 5) & 3, vhalf = (tid >> 4) & 1, vd = tid & 15;
+  int ktok[4], vtok[4];
+  uint32_t koff[4], voff[4], kch, vch;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int u = r * kPfThreads + tid;
+    const int c = u >> 9, v = u & 511;
+    const int h = v >> 8, s = (v >> 6) & 3, g = (v >> 4) & 3, mm = v & 15;
+    ktok[r] = c * HC_TILE + h * 16 + mm;
+    vtok[r] = vc * HC_TILE + vhalf * 16 + vg * 4 + r;
+    koff[r] = (uint32_t)((ktok[r] * a.k_st + 32 * s + 8 * g) * (int64_t)sizeof(T));
+    voff[r] = (uint32_t)((vtok[r] * a.v_st + 8 * vd) * (int64_t)sizeof(T));
+  }
+  kch = (uint32_t)((32 * ((tid >> 6) & 3) + 8 * ((tid >> 4) & 3)) * sizeof(T));  // channel part, same for all r
+  vch = (uint32_t)(8 * vd * sizeof(T));
   vec8 kreg[4], vreg[4];
 
   auto stage_load = [&](int it) {
     const int t0 = it * kPfKeys;
+    const char* kit = reinterpret_cast<const char*>(kbase) + (int64_t)t0 * a.k_st * (int64_t)sizeof(T);
+    const char* vit = reinterpret_cast<const char*>(vbase) + (int64_t)t0 * a.v_st * (int64_t)sizeof(T);
+    const int lim = a.Lk - t0;  // tokens of this window that exist
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int u = r * kPfThreads + tid;
-      const int c = u >> 9, v = u & 511;
-      const int h = v >> 8, s = (v >> 6) & 3, g = (v >> 4) & 3, mm = v & 15;
-      const int t = t0 + c * HC_TILE + h * 16 + mm;
-      kreg[r] = t < a.Lk ? load8(kbase + (int64_t)t * a.k_st + 32 * s + 8 * g) : zero8<T>();
-    }
+    for (int r = 0; r < 4; ++r) kreg[r] = load8(reinterpret_cast<const T*>(kit + (ktok[r] < lim ? koff[r] : kch)));
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = t0 + vc * HC_TILE + vhalf * 16 + vg * 4 + r;
-      vreg[r] = t < a.Lk ? load8(vbase + (int64_t)t * a.v_st + 8 * vd) : zero8<T>();
-    }
+    for (int r = 0; r < 4; ++r) vreg[r] = load8(reinterpret_cast<const T*>(vit + (vtok[r] < lim ? voff[r] : vch)));
   };
-  auto stage_store = [&](int buf) {
+  auto stage_store = [&](int buf, int it) {
     T* sk = lds + buf * kPfSetElems;
     T* sv = sk + kPfTiles * HC_TILE_ELEMS;
+    const int lim = a.Lk - it * kPfKeys;
+    if (lim < kPfKeys) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (ktok[r] >= lim) kreg[r] = zero8<T>();
+        if (vtok[r] >= lim) vreg[r] = zero8<T>();
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int u = r * kPfThreads + tid;
@@ -186,7 +217,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
   };
 
   stage_load(0);
-  stage_store(0);
+  stage_store(0, 0);
   __syncthreads();
 
   for (int it = 0; it < nit; ++it) {
@@ -213,41 +244,54 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
         }
       }
       const bool need_mask = t0 + kPfKeys - 1 > pos_lo;
+      if (need_mask) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int pj = pos_lo + 16 * j + n16;
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (t0 + 16 * tb + 4 * g4 + r > pj) sacc[tb][j][r] = -INFINITY;
+        }
+      }
       vec8 pb[2][2];  // [tile][query block]: B operand of the P.V step
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const int pj = pos_lo + 16 * j + n16;
-        float xs[4][4];
+        // Raw tile maximum (scale > 0), shared by the 4 lanes of a query.
         float mx = -INFINITY;
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float sv2 = sacc[tb][j][r] * a.scale_log2;
-            if (need_mask && t0 + 16 * tb + 4 * g4 + r > pj) sv2 = -INFINITY;
-            xs[tb][r] = sv2;
-            mx = fmaxf(mx, sv2);
-          }
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sacc[tb][j][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mnew = fmaxf(m[j], mx);
-        const float msafe = mnew == -INFINITY ? 0.f : mnew;
-        const float alpha = fast_exp2(m[j] - msafe);
-        m[j] = mnew;
-        float ps = 0.f;
+        const float mt = mx * a.scale_log2;
+        // Lazy rescaling: the reference maximum m only moves when a tile
+        // maximum exceeds it by more than kPfLazy (log2 units), so the O
+        // rescale runs on a few tiles per row; probabilities stay below
+        // 2^kPfLazy, well inside every input type's range.
+        if (__any(mt > m[j] + kPfLazy)) {
+          const float mnew = fmaxf(m[j], mt);
+          const float alpha = m[j] == -INFINITY ? 0.f : fast_exp2(m[j] - mnew);
+          m[j] = mnew;
+          l[j] *= alpha;
+#pragma unroll
+          for (int db = 0; db < 8; ++db)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[db][j][r] *= alpha;
+        }
+        const float nm = -m[j];
         float p[4][4];
+        float ps = 0.f;
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            p[tb][r] = fast_exp2(xs[tb][r] - msafe);
+            p[tb][r] = fast_exp2(fmaf(sacc[tb][j][r], a.scale_log2, nm));
             ps += p[tb][r];
           }
-        l[j] = fmaf(l[j], alpha, ps);
-#pragma unroll
-        for (int db = 0; db < 8; ++db)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) o[db][j][r] *= alpha;
+        l[j] += ps;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const float pv[8] = {p[2 * c][0],     p[2 * c][1],     p[2 * c][2],     p[2 * c][3],
@@ -267,7 +311,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
         }
       }
     }
-    if (it + 1 < nit) stage_store(cur ^ 1);
+    if (it + 1 < nit) stage_store(cur ^ 1, it + 1);
     __syncthreads();
   }
 
@@ -338,7 +382,11 @@ extern "C" int hc_prefill_attn(int dtype, const void* q, const int64_t* q_stride
     for (int j = 0; j < 3; ++j)
       if (st[i][j] < 0 || (st[i][j] * esz) % 16)
         return set_error(HC_ERR_INVALID, "hc_prefill_attn: strides must be non-negative 16-byte multiples");
-  if (!std::isfinite(scale)) return set_error(HC_ERR_INVALID, "hc_prefill_attn: scale must be finite");
+  const int64_t max_tok_stride = std::max(k_strides[2], v_strides[2]);
+  if ((int64_t)kPfKeys * max_tok_stride * esz >= (int64_t)1 << 31)
+    return set_error(HC_ERR_INVALID, "hc_prefill_attn: K/V token strides too large");
+  if (!std::isfinite(scale) || !(scale > 0.f))
+    return set_error(HC_ERR_INVALID, "hc_prefill_attn: scale must be finite and positive");
   PfArgs a;
   a.q = q;
   a.k = k;

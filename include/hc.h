@@ -143,7 +143,7 @@ int hc_copy_rows(int dtype, const void* src_k, const void* src_v, const int64_t*
  * chunk of a chunked prefill over the keys staged so far.  Each of q, k, v and
  * out is addressed as base + b*strides[0] + h*strides[1] + t*strides[2] + c
  * (element strides, 16-byte multiples; channels contiguous), so the
- * projections' [B, T, H, 128] layout is read without a copy.  Arithmetic: MFMA
+ * projections' [B, T, H, 128] layout is read without a copy; scale > 0.  Arithmetic: MFMA
  * on the input type, fp32 accumulation and softmax, probabilities rounded to
  * the input type for the P.V product.  Replaces the flash-attn prefill call
  * of LlamaAttention / Qwen2Attention (heterocache/llama_model.py:353-361,
