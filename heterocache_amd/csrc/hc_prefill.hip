@@ -225,6 +225,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
     const int t0 = it * kPfKeys;
     if (it + 1 < nit) stage_load(it + 1);
     if (active && t0 <= pos_hi) {
+      __builtin_amdgcn_s_setprio(0);
       const T* sk = lds + cur * kPfSetElems;
       const T* sv = sk + kPfTiles * HC_TILE_ELEMS;
       // S^T blocks: rows = keys 16*tb + 4*g4 + r, column = query 16j + n16.
@@ -243,6 +244,9 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
           for (int j = 0; j < 2; ++j) sacc[tb][j] = mma_16x16x32(ka, qop[j][s], sacc[tb][j]);
         }
       }
+      // The softmax runs at raised wave priority: the SIMD's other wave,
+      // in its MFMA phase, then fills the matrix pipe meanwhile.
+      __builtin_amdgcn_s_setprio(1);
       const bool need_mask = t0 + kPfKeys - 1 > pos_lo;
       if (need_mask) {
 #pragma unroll
@@ -299,6 +303,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
           pb[c][j] = pack8<T>(pv);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       // O^T blocks: rows = channels 16*db + 4*g4 + r, column = query.
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -311,6 +316,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if (it + 1 < nit) stage_store(cur ^ 1, it + 1);
     __syncthreads();
   }
