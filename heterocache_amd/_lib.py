@@ -43,7 +43,9 @@ SIGNATURES = {
     "hc_copy_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int, c_void_p,
                              c_int64, c_void_p, c_int, c_int, c_int, c_void_p]),
     "hc_prefill_attn": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-                                c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p]),
+                                c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t,
+                                c_void_p]),
+    "hc_prefill_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "hc_append": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                           c_int, c_void_p, c_void_p]),
     "hc_score": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p,

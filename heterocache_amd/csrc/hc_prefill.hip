@@ -15,16 +15,12 @@
 //    order puts every workgroup of a KV row on the same XCD (rows are
 //    interleaved modulo the grid's round-robin over XCDs) and dispatches the
 //    query blocks with the most keys first;
-//  * keys advance 64 per iteration (two 32-token tiles).  K and V arrive in
-//    natural layout with arbitrary batch/head/token strides and are staged
-//    through double-buffered LDS in the KV store's tile layout, so every MFMA
-//    operand is one 16-byte LDS read:
-//      - K chunks of 8 channels land contiguously (the tile layout keeps them
-//        together);
-//      - V is transposed in registers, 4 tokens x 8 channels per thread, and
-//        written as 4-element groups whose position inside each 16-channel
-//        block is rotated by the block index, which keeps the writes and the
-//        operand reads free of bank conflicts;
+//  * keys advance 64 per iteration (two 32-token tiles), staged through
+//    double-buffered LDS in the KV store's tile layout so every MFMA operand
+//    is one 16-byte LDS read.  K is read in natural layout (arbitrary
+//    batch/head/token strides): its 8-channel chunks stay whole in the tile
+//    layout.  V is first re-laid out into tiles by v_tiles_kernel (once per
+//    tile, into the caller's workspace), so its staging is a plain copy;
 //  * S^T = K Q^T per 16-key x 16-query block (K as the A operand), online
 //    base-2 softmax per query column, O^T += V^T P^T with P taken straight
 //    from the S accumulators (the tile layout's V token order is the order in
@@ -57,13 +53,15 @@ constexpr float kPfLazy = 8.f;                  // lazy-rescale threshold, log2 
 struct PfArgs {
   const void* q;
   const void* k;
-  const void* v;
+  const void* v;   // natural layout (read by v_tiles_kernel)
+  const void* vt;  // V in tile layout: [rows][vt_tiles][HC_TILE_ELEMS]
   void* out;
   int64_t q_sb, q_sh, q_st;  // element strides: batch, head, token (channels contiguous)
   int64_t k_sb, k_sh, k_st;
   int64_t v_sb, v_sh, v_st;
   int64_t o_sb, o_sh, o_st;
   int Hq, Hkv, Lq, Lk, nqb, rows;  // rows = batch * Hkv
+  int vt_tiles;                    // tiles per row of vt
   float scale_log2;
 };
 
@@ -81,30 +79,42 @@ struct Quad {
   typedef T type __attribute__((ext_vector_type(4)));
 };
 
-// Write channel e of the thread's 4 staged V tokens as one 4-element group.
+// V rows in natural layout -> the KV store's V tile layout, one 32-token tile
+// per workgroup, zeros past kv_len.  The attention kernel then stages V with
+// plain 16-byte copies, and the transposition is paid once per tile rather
+// than once per (query head, query block) that reads it.
 template <typename T>
-__device__ __forceinline__ void store_v_quad(T* dst, const typename Elem<T>::vec8 (&vr)[4], int e) {
-  if constexpr (sizeof(T) == 2) {
-    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    const u32x4* w = reinterpret_cast<const u32x4*>(&vr[0]);
-    const int j = e >> 1;
-    const uint32_t a0 = w[0][j], a1 = w[1][j], a2 = w[2][j], a3 = w[3][j];
-    u32x2 r;
-    if (e & 1) {
-      r.x = (a0 >> 16) | (a1 & 0xffff0000u);
-      r.y = (a2 >> 16) | (a3 & 0xffff0000u);
-    } else {
-      r.x = (a0 & 0xffffu) | (a1 << 16);
-      r.y = (a2 & 0xffffu) | (a3 << 16);
+__global__ __launch_bounds__(256) void v_tiles_kernel(const PfArgs a) {
+  typedef typename Elem<T>::vec8 vec8;
+  __shared__ T s[HC_TILE][HC_HEAD_DIM + 8];
+  const int tile = blockIdx.x, row = blockIdx.y;
+  const int b = row / a.Hkv, h = row % a.Hkv;
+  const T* src = reinterpret_cast<const T*>(a.v) + b * a.v_sb + h * a.v_sh;
+  const int t0 = tile * HC_TILE;
+  for (int c = threadIdx.x; c < HC_TILE * 16; c += 256) {
+    const int t = c >> 4, d0 = (c & 15) * 8;
+    const vec8 x = t0 + t < a.Lk ? load8(src + (int64_t)(t0 + t) * a.v_st + d0) : zero8<T>();
+    *reinterpret_cast<vec8*>(&s[t][d0]) = x;
+  }
+  __syncthreads();
+  T* dst = reinterpret_cast<T*>(const_cast<void*>(a.vt)) + ((int64_t)row * a.vt_tiles + tile) * HC_TILE_ELEMS;
+  for (int c = threadIdx.x; c < HC_TILE * 16; c += 256) {
+    // Output chunk c = (mt*4 + g)*16 + n: channel 16mt+n, tokens
+    // {4g + [0,4), 16 + 4g + [0,4)} (the order the scores take in the MFMA
+    // accumulator).
+    const int n = c & 15, g = (c >> 4) & 3, mt = c >> 6;
+    const int d = mt * 16 + n;
+    typename Elem<T>::vec8 o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const T x = s[16 * (i >> 2) + 4 * g + (i & 3)][d];
+      if constexpr (sizeof(T) == 4) {
+        if (i < 4) o.lo[i] = x; else o.hi[i - 4] = x;
+      } else {
+        o[i] = x;
+      }
     }
-    *reinterpret_cast<u32x2*>(dst) = r;
-  } else {
-    typename Quad<T>::type r;
-    r.x = vec8_at<T>(vr[0], e);
-    r.y = vec8_at<T>(vr[1], e);
-    r.z = vec8_at<T>(vr[2], e);
-    r.w = vec8_at<T>(vr[3], e);
-    *reinterpret_cast<typename Quad<T>::type*>(dst) = r;
+    *reinterpret_cast<vec8*>(dst + c * 8) = o;
   }
 }
 
@@ -130,7 +140,6 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
 
   const T* qbase = reinterpret_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
   const T* kbase = reinterpret_cast<const T*>(a.k) + b * a.k_sb + kvh * a.k_sh;
-  const T* vbase = reinterpret_cast<const T*>(a.v) + b * a.v_sb + kvh * a.v_sh;
   T* obase = reinterpret_cast<T*>(a.out) + b * a.o_sb + hq * a.o_sh;
 
   const int shift = a.Lk - a.Lq;  // position of query i is shift + i
@@ -158,39 +167,40 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
     for (int j = 0; j < 2; ++j) o[db][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
 
-  // Staging roles.  K: four chunks (token, 8 channels) per thread, chunk
-  // u = r*256 + tid is tile u/512, tile chunk u%512 = ((h*4+s)*4+g)*16+m.
-  // V: 4 tokens {16*half + 4*vg + [0,4)} of tile vc, channels 8*vd + [0, 8).
-  // Each load is a uniform per-iteration base plus a fixed 32-bit byte
-  // offset (the host bounds 64 token strides below 2^31 bytes).  In the last
-  // window, lanes past Lk read the window's first token instead (a select,
-  // not a branch, so no load waits at a join) and store zeros.
-  const int vc = tid >> 7, vg = (tid >> 5) & 3, vhalf = (tid >> 4) & 1, vd = tid & 15;
-  int ktok[4], vtok[4];
-  uint32_t koff[4], voff[4], kch, vch;
+  // Staging roles: four 16-byte chunks of K and four of V per thread; chunk
+  // u = r*256 + tid is tile u/512, tile chunk u%512, written to LDS at
+  // u*16 bytes (contiguous per wave).
+  //  * K arrives in natural layout.  Tile chunk ((h*4+s)*4+g)*16+m holds
+  //    token 16h+m, channels 32s+8g+[0,8): one strided 16-byte read.  Each
+  //    load is a uniform per-iteration base plus a fixed 32-bit byte offset
+  //    (the host bounds 64 token strides below 2^31 bytes); in the last
+  //    window, lanes past Lk read the window's first token instead (a select,
+  //    not a branch, so no load waits at a join) and store zeros.
+  //  * V arrives already in tile layout (v_tiles_kernel, zeros past Lk), so
+  //    its chunks are plain contiguous reads.
+  int ktok[4];
+  uint32_t koff[4], kch;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int u = r * kPfThreads + tid;
     const int c = u >> 9, v = u & 511;
     const int h = v >> 8, s = (v >> 6) & 3, g = (v >> 4) & 3, mm = v & 15;
     ktok[r] = c * HC_TILE + h * 16 + mm;
-    vtok[r] = vc * HC_TILE + vhalf * 16 + vg * 4 + r;
     koff[r] = (uint32_t)((ktok[r] * a.k_st + 32 * s + 8 * g) * (int64_t)sizeof(T));
-    voff[r] = (uint32_t)((vtok[r] * a.v_st + 8 * vd) * (int64_t)sizeof(T));
   }
   kch = (uint32_t)((32 * ((tid >> 6) & 3) + 8 * ((tid >> 4) & 3)) * sizeof(T));  // channel part, same for all r
-  vch = (uint32_t)(8 * vd * sizeof(T));
+  const T* vtiles = reinterpret_cast<const T*>(a.vt) + (int64_t)row * a.vt_tiles * HC_TILE_ELEMS + tid * 8;
   vec8 kreg[4], vreg[4];
 
   auto stage_load = [&](int it) {
     const int t0 = it * kPfKeys;
     const char* kit = reinterpret_cast<const char*>(kbase) + (int64_t)t0 * a.k_st * (int64_t)sizeof(T);
-    const char* vit = reinterpret_cast<const char*>(vbase) + (int64_t)t0 * a.v_st * (int64_t)sizeof(T);
     const int lim = a.Lk - t0;  // tokens of this window that exist
 #pragma unroll
     for (int r = 0; r < 4; ++r) kreg[r] = load8(reinterpret_cast<const T*>(kit + (ktok[r] < lim ? koff[r] : kch)));
+    const T* vit = vtiles + (int64_t)it * kPfTiles * HC_TILE_ELEMS;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) vreg[r] = load8(reinterpret_cast<const T*>(vit + (vtok[r] < lim ? voff[r] : vch)));
+    for (int r = 0; r < 4; ++r) vreg[r] = load8(vit + r * kPfThreads * 8);
   };
   auto stage_store = [&](int buf, int it) {
     T* sk = lds + buf * kPfSetElems;
@@ -198,21 +208,14 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
     const int lim = a.Lk - it * kPfKeys;
     if (lim < kPfKeys) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < 4; ++r)
         if (ktok[r] >= lim) kreg[r] = zero8<T>();
-        if (vtok[r] >= lim) vreg[r] = zero8<T>();
-      }
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int u = r * kPfThreads + tid;
-      *reinterpret_cast<vec8*>(sk + (u >> 9) * HC_TILE_ELEMS + (u & 511) * 8) = kreg[r];
-    }
-    T* dv = sv + vc * HC_TILE_ELEMS + vhalf * 4;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = 8 * vd + e, mt = d >> 4, n = d & 15;
-      store_v_quad<T>(dv + mt * 512 + (vg * 16 + ((n + mt) & 15)) * 8, vreg, e);
+      *reinterpret_cast<vec8*>(sk + u * 8) = kreg[r];
+      *reinterpret_cast<vec8*>(sv + u * 8) = vreg[r];
     }
   };
 
@@ -310,7 +313,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
         const T* vt = sv + c * HC_TILE_ELEMS;
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
-          const vec8 va = load8(vt + db * 512 + (g4 * 16 + ((n16 + db) & 15)) * 8);
+          const vec8 va = load8(vt + (db * 64 + lane) * 8);
 #pragma unroll
           for (int j = 0; j < 2; ++j) o[db][j] = mma_16x16x32(va, pb[c][j], o[db][j]);
         }
@@ -345,6 +348,9 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
 
 template <typename T>
 int launch_prefill(const PfArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL((v_tiles_kernel<T>), dim3((unsigned)a.vt_tiles, (unsigned)a.rows), dim3(256), 0, stream, a);
+  int rc = check_launch("hc_prefill_attn(v tiles)");
+  if (rc) return rc;
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
@@ -360,15 +366,27 @@ int launch_prefill(const PfArgs& a, hipStream_t stream) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Tiles per row of the V tile buffer: kv_len rounded up to whole iterations.
+int64_t v_tiles_per_row(int kv_len) {
+  const int64_t it = ((int64_t)kv_len + kPfKeys - 1) / kPfKeys;
+  return it * kPfTiles;
+}
+
 }  // namespace
 }  // namespace hc
 
 using namespace hc;
 
+extern "C" size_t hc_prefill_workspace_size(int dtype, int batch, int kv_heads, int kv_len) {
+  const int esz = dtype == HC_DTYPE_F32 ? 4 : 2;
+  if (batch <= 0 || kv_heads <= 0 || kv_len <= 0) return 0;
+  return (size_t)batch * kv_heads * v_tiles_per_row(kv_len) * HC_TILE_ELEMS * esz;
+}
+
 extern "C" int hc_prefill_attn(int dtype, const void* q, const int64_t* q_strides, const void* k,
                                const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out,
                                const int64_t* out_strides, int batch, int q_heads, int kv_heads, int q_len,
-                               int kv_len, float scale, void* stream) {
+                               int kv_len, float scale, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   const int esz = dtype == HC_DTYPE_F32 ? 4 : (dtype == HC_DTYPE_BF16 || dtype == HC_DTYPE_F16) ? 2 : 0;
   if (esz == 0) return set_error(HC_ERR_INVALID, "hc_prefill_attn: unknown dtype %d", dtype);
@@ -393,10 +411,15 @@ extern "C" int hc_prefill_attn(int dtype, const void* q, const int64_t* q_stride
     return set_error(HC_ERR_INVALID, "hc_prefill_attn: K/V token strides too large");
   if (!std::isfinite(scale) || !(scale > 0.f))
     return set_error(HC_ERR_INVALID, "hc_prefill_attn: scale must be finite and positive");
+  const size_t need = hc_prefill_workspace_size(dtype, batch, kv_heads, kv_len);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return set_error(HC_ERR_INVALID, "hc_prefill_attn: workspace too small or unaligned (%zu < %zu bytes)",
+                     workspace_bytes, need);
   PfArgs a;
   a.q = q;
   a.k = k;
   a.v = v;
+  a.vt = workspace;
   a.out = out;
   a.q_sb = q_strides[0], a.q_sh = q_strides[1], a.q_st = q_strides[2];
   a.k_sb = k_strides[0], a.k_sh = k_strides[1], a.k_st = k_strides[2];
@@ -407,6 +430,7 @@ extern "C" int hc_prefill_attn(int dtype, const void* q, const int64_t* q_stride
   a.Lq = q_len;
   a.Lk = kv_len;
   a.nqb = (q_len + kPfBlockQ - 1) / kPfBlockQ;
+  a.vt_tiles = (int)v_tiles_per_row(kv_len);
   a.rows = batch * kv_heads;
   a.scale_log2 = scale * 1.4426950408889634f;
   const int64_t grid = (int64_t)a.rows * (q_heads / kv_heads) * a.nqb;

@@ -257,8 +257,13 @@ def prefill_attn(q, k, v, scale, out=None, stream=None):
                         [v.stride(0), v.stride(1), v.stride(2)],
                         [out.stride(0), out.stride(2), out.stride(1)]], dtype=np.int64)
     base = strides.ctypes.data
-    _lib.check(lib.hc_prefill_attn(dtype_code(q.dtype), _ptr(q), base, _ptr(k), base + 24, _ptr(v), base + 48,
-                                   _ptr(out), base + 72, B, Hq, Hkv, Lq, Lk, float(scale), _stream(stream, q)))
+    code = dtype_code(q.dtype)
+    nbytes = lib.hc_prefill_workspace_size(code, B, Hkv, Lk)
+    # Per-call scratch from the caching allocator (stream-ordered reuse).
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
+    _lib.check(lib.hc_prefill_attn(code, _ptr(q), base, _ptr(k), base + 24, _ptr(v), base + 48, _ptr(out),
+                                   base + 72, B, Hq, Hkv, Lq, Lk, float(scale), _ptr(ws), ws.numel(),
+                                   _stream(stream, q)))
     return out
 
 

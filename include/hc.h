@@ -151,7 +151,12 @@ int hc_copy_rows(int dtype, const void* src_k, const void* src_v, const int64_t*
  */
 int hc_prefill_attn(int dtype, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                     const void* v, const int64_t* v_strides, void* out, const int64_t* out_strides, int batch,
-                    int q_heads, int kv_heads, int q_len, int kv_len, float scale, void* stream);
+                    int q_heads, int kv_heads, int q_len, int kv_len, float scale, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* Device workspace bytes hc_prefill_attn needs (V re-laid out in 32-token
+ * tiles, written and read within the call: no initialisation). */
+size_t hc_prefill_workspace_size(int dtype, int batch, int kv_heads, int kv_len);
 
 /* hc_score flags */
 #define HC_SCORE_CAUSAL_WINDOW 1 /* window row w sees keys t <= L - W + w (kv_cluster.py:169-175) */
