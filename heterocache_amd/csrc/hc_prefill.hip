@@ -20,7 +20,8 @@
 //    is one 16-byte LDS read.  K is read in natural layout (arbitrary
 //    batch/head/token strides): its 8-channel chunks stay whole in the tile
 //    layout.  V is first re-laid out into tiles by v_tiles_kernel (once per
-//    tile, into the caller's workspace), so its staging is a plain copy;
+//    tile, into the caller's workspace).  Both are then plain 16-byte copies,
+//    issued as LDS-DMA loads (global_load_lds) that hold no registers;
 //  * S^T = K Q^T per 16-key x 16-query block (K as the A operand), online
 //    base-2 softmax per query column, O^T += V^T P^T with P taken straight
 //    from the S accumulators (the tile layout's V token order is the order in
@@ -118,6 +119,14 @@ __global__ __launch_bounds__(256) void v_tiles_kernel(const PfArgs a) {
   }
 }
 
+// 16 bytes per lane straight from global memory into LDS: lane i's bytes
+// land at lds + 16*i (lds is wave-uniform).
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, lds, 16, 0, 0);
+}
+// s_waitcnt vmcnt(0): every LDS-DMA load of this wave has landed.
+__device__ __forceinline__ void wait_lds_dma() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+
 template <typename T>
 __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_attn_kernel(const PfArgs a) {
   typedef typename Elem<T>::vec8 vec8;
@@ -178,55 +187,53 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
   //    not a branch, so no load waits at a join) and store zeros.
   //  * V arrives already in tile layout (v_tiles_kernel, zeros past Lk), so
   //    its chunks are plain contiguous reads.
-  int ktok[4];
-  uint32_t koff[4], kch;
+  // Staging goes straight from global memory into LDS (global_load_lds:
+  // each lane's 16 bytes land at the wave's LDS base + lane*16), so it
+  // takes no registers and no LDS store instructions.  The copy runs in
+  // 16-byte units, kUnits per 8-element chunk (1 for 16-bit types, 2 for
+  // fp32); unit w = r*256 + tid lands at LDS byte 16*w of the K (or V) set,
+  // which is chunk w / kUnits of the tile layout.  Keys past Lk read the
+  // window's first token: they are masked, as they follow every query.
+  constexpr int kUnits = (int)sizeof(T) / 2;
+  constexpr int kUnitsPerThread = 4 * kUnits;
+  uint32_t koff[kUnitsPerThread], kch[kUnitsPerThread];
+  int ktok[kUnitsPerThread];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int u = r * kPfThreads + tid;
+  for (int r = 0; r < kUnitsPerThread; ++r) {
+    const int w = r * kPfThreads + tid;
+    const int u = w / kUnits, half = w % kUnits;
     const int c = u >> 9, v = u & 511;
     const int h = v >> 8, s = (v >> 6) & 3, g = (v >> 4) & 3, mm = v & 15;
     ktok[r] = c * HC_TILE + h * 16 + mm;
-    koff[r] = (uint32_t)((ktok[r] * a.k_st + 32 * s + 8 * g) * (int64_t)sizeof(T));
+    kch[r] = (uint32_t)((32 * s + 8 * g) * (int64_t)sizeof(T) + 16 * half);
+    koff[r] = (uint32_t)(ktok[r] * a.k_st * (int64_t)sizeof(T)) + kch[r];
   }
-  kch = (uint32_t)((32 * ((tid >> 6) & 3) + 8 * ((tid >> 4) & 3)) * sizeof(T));  // channel part, same for all r
-  const T* vtiles = reinterpret_cast<const T*>(a.vt) + (int64_t)row * a.vt_tiles * HC_TILE_ELEMS + tid * 8;
-  vec8 kreg[4], vreg[4];
+  const char* vtiles = reinterpret_cast<const char*>(a.vt) +
+                       ((int64_t)row * a.vt_tiles * HC_TILE_ELEMS) * (int64_t)sizeof(T) + 16 * tid;
 
-  auto stage_load = [&](int it) {
+  auto stage = [&](int buf, int it) {
+    char* sk = reinterpret_cast<char*>(lds + buf * kPfSetElems);
+    char* sv = reinterpret_cast<char*>(lds + buf * kPfSetElems + kPfTiles * HC_TILE_ELEMS);
     const int t0 = it * kPfKeys;
     const char* kit = reinterpret_cast<const char*>(kbase) + (int64_t)t0 * a.k_st * (int64_t)sizeof(T);
-    const int lim = a.Lk - t0;  // tokens of this window that exist
+    const int lim = a.Lk - t0;
+    const char* vit = vtiles + (int64_t)it * kPfTiles * HC_TILE_ELEMS * (int64_t)sizeof(T);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) kreg[r] = load8(reinterpret_cast<const T*>(kit + (ktok[r] < lim ? koff[r] : kch)));
-    const T* vit = vtiles + (int64_t)it * kPfTiles * HC_TILE_ELEMS;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) vreg[r] = load8(vit + r * kPfThreads * 8);
-  };
-  auto stage_store = [&](int buf, int it) {
-    T* sk = lds + buf * kPfSetElems;
-    T* sv = sk + kPfTiles * HC_TILE_ELEMS;
-    const int lim = a.Lk - it * kPfKeys;
-    if (lim < kPfKeys) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (ktok[r] >= lim) kreg[r] = zero8<T>();
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int u = r * kPfThreads + tid;
-      *reinterpret_cast<vec8*>(sk + u * 8) = kreg[r];
-      *reinterpret_cast<vec8*>(sv + u * 8) = vreg[r];
+    for (int r = 0; r < kUnitsPerThread; ++r) {
+      const int wb = r * kPfThreads + wave * 64;  // first unit of this wave
+      lds_dma16(kit + (ktok[r] < lim ? koff[r] : kch[r]), sk + 16 * wb);
+      lds_dma16(vit + 16 * r * kPfThreads, sv + 16 * wb);
     }
   };
 
-  stage_load(0);
-  stage_store(0, 0);
+  stage(0, 0);
+  wait_lds_dma();
   __syncthreads();
 
   for (int it = 0; it < nit; ++it) {
     const int cur = it & 1;
     const int t0 = it * kPfKeys;
-    if (it + 1 < nit) stage_load(it + 1);
+    if (it + 1 < nit) stage(cur ^ 1, it + 1);
     if (active && t0 <= pos_hi) {
       __builtin_amdgcn_s_setprio(0);
       const T* sk = lds + cur * kPfSetElems;
@@ -320,7 +327,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
       }
     }
     __builtin_amdgcn_s_setprio(0);
-    if (it + 1 < nit) stage_store(cur ^ 1, it + 1);
+    wait_lds_dma();
     __syncthreads();
   }
 
