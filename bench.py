@@ -291,6 +291,76 @@ def window_scoring_phase(args, torch, dev):
             "k_read_gbs": round(kbytes / ms / 1e6, 1), "window": W, "ctx": L}
 
 
+def decode_configs_phase(args, torch, dev):
+    """Decode attention (fused append + split-K + merge per layer, all layers
+    of a step) on the other decode workloads: a Qwen2.5-7B-shaped batch of
+    four sequences at 16/32/48/64K with ratio 0.25 (4 KV heads, GQA 7, 28
+    layers), and Llama-3-8B at 224K with ratio 0.5.  Same timing as the
+    headline: one event pair per step, algorithmic bytes = retained K/V rows
+    plus queries and outputs."""
+    from heterocache_amd import workloads
+    from heterocache_amd.store import KVStore
+    D = 128
+    def qwen_budgets(layer, L):
+        # 14 of the 112 KV heads keep the full context (one per even layer);
+        # the rest share the budget with allocation weights 0.5 / 1.0 / 1.5.
+        # (A seeded synthetic head JSON has more full heads than ratio 0.25
+        # leaves room for: its base length would go negative.)
+        base = workloads.get_compress_len(0.25, 14, L, 4 * 28)
+        cap = lambda w: int(np.trunc(np.float32(base) * np.float32(w)))
+        return [L, cap(0.5), cap(1.0), cap(1.5)] if layer % 2 == 0 else [cap(0.5), cap(1.0), cap(1.0), cap(1.5)]
+
+    cases = [("qwen2.5-7b_b4_ragged_16-64k_r0.25", [16384, 32768, 49152, 65536], 0.25, 28, 4, 7),
+             ("llama3-8b_224k_r0.5", [229376], 0.5, 32, 8, 4)]
+    out = {}
+    for name, contexts, ratio, NL, Hkv, G in cases:
+        data = workloads.synthetic_head_json(NL, Hkv, args.seed)
+        steps, warm = 10, 3
+        stores = []
+        for layer in range(NL):
+            if G == 7:
+                lens = np.asarray([n for L in contexts for n in qwen_budgets(layer, L)], dtype=np.int64)
+            else:
+                lens = np.concatenate([workloads.row_budgets(data, layer, L, ratio, NL, Hkv)[0] for L in contexts])
+            st = KVStore(lens + steps + warm + 2, torch.bfloat16, dev)
+            st.k.normal_()
+            st.v.normal_()
+            st.set_lengths(lens)
+            stores.append(st)
+        rows = len(contexts) * Hkv
+        q = torch.randn((NL, rows, G, D), device=dev).to(torch.bfloat16)
+        kn = torch.randn((NL, rows, D), device=dev).to(torch.bfloat16)
+        vn = torch.randn((NL, rows, D), device=dev).to(torch.bfloat16)
+        o = [torch.empty((rows, G, D), dtype=torch.bfloat16, device=dev) for _ in range(NL)]
+        scale = 1.0 / math.sqrt(D)
+
+        def step():
+            for layer, st in enumerate(stores):
+                st.attend(q[layer], scale, out=o[layer], k_new=kn[layer], v_new=vn[layer])
+
+        for _ in range(warm):
+            step()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        nbytes = 0
+        for i in range(steps):
+            ev[i][0].record()
+            step()
+            ev[i][1].record()
+            nbytes += sum(st.kv_bytes() for st in stores)
+        torch.cuda.synchronize()
+        ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+        per_launch = nbytes / (steps * NL) + 2 * rows * G * D * 2
+        us = ms * 1e3 / NL
+        gbs = per_launch / (us * 1e-6) / 1e9
+        out[name] = {"contexts": contexts, "layers": NL, "kv_rows": rows, "group": G, "ratio": ratio,
+                     "us_per_layer": round(us, 3), "bytes_per_layer": int(per_launch), "gbs": round(gbs, 1),
+                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        del stores, q, kn, vn, o
+        torch.cuda.empty_cache()
+    return out
+
+
 def prefill_attention_phase(args, torch, dev):
     """Causal prefill attention of one Llama-3-8B layer (32 query heads over 8
     KV heads, projection layout [B, T, H, 128]): a 32K prompt in one call, and
@@ -445,6 +515,7 @@ def main():
         rec["window_scoring"] = window_scoring_phase(args, torch, dev)
         rec["gather"] = gather_phase(args, torch, dev)
         rec["prefill_attention"] = prefill_attention_phase(args, torch, dev)
+        rec["decode_other_configs"] = decode_configs_phase(args, torch, dev)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(L, budgets[0], args.cpu_seconds)
     print(json.dumps(rec))
