@@ -361,6 +361,38 @@ def decode_configs_phase(args, torch, dev):
     return out
 
 
+def baseline_compressors_phase(args, torch, dev):
+    """The reference's baseline compressors on one Llama-3-8B layer at an 8K
+    prompt, keys and values repeated per query head as their callers pass
+    them (32 heads), bf16, ratio 0.5: time per update_kv call."""
+    from heterocache_amd import kv_cluster
+    H, L, D, G = 32, 8192, 128, 4
+    q = torch.randn((1, H, L, D), device=dev, dtype=torch.bfloat16)
+    k = torch.randn((1, H, L, D), device=dev, dtype=torch.bfloat16)
+    v = torch.randn((1, H, L, D), device=dev, dtype=torch.bfloat16)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = {}
+    makers = {"snapkv": lambda: kv_cluster.SnapKVCluster(window_size=32, compression_ratio=0.5),
+              "pyramidkv_layer0": lambda: kv_cluster.PyramidKVCluster(window_size=32, compression_ratio=0.5,
+                                                                      layer_idx=0),
+              "h2o": lambda: kv_cluster.H2OKVCluster(compression_ratio=0.5),
+              "streamingllm": lambda: kv_cluster.StreamingLLMKVCluster(compression_ratio=0.5)}
+    for name, make in makers.items():
+        make().update_kv(k, q, v, None, G)
+        torch.cuda.synchronize()
+        reps = 3
+        e0.record()
+        for _ in range(reps):
+            ko, _ = make().update_kv(k, q, v, None, G)
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = {"ms": round(e0.elapsed_time(e1) / reps, 3), "kept": int(ko.shape[2])}
+    out["config"] = {"heads": H, "prompt": L, "ratio": 0.5, "group": G, "dtype": "bf16"}
+    del q, k, v
+    torch.cuda.empty_cache()
+    return out
+
+
 def prefill_attention_phase(args, torch, dev):
     """Causal prefill attention of one Llama-3-8B layer (32 query heads over 8
     KV heads, projection layout [B, T, H, 128]): a 32K prompt in one call, and
@@ -516,6 +548,7 @@ def main():
         rec["gather"] = gather_phase(args, torch, dev)
         rec["prefill_attention"] = prefill_attention_phase(args, torch, dev)
         rec["decode_other_configs"] = decode_configs_phase(args, torch, dev)
+        rec["baseline_compressors"] = baseline_compressors_phase(args, torch, dev)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(L, budgets[0], args.cpu_seconds)
     print(json.dumps(rec))

@@ -18,6 +18,7 @@ HC_SCORE_CAUSAL_WINDOW = 1
 HC_SCORE_SUM_WINDOW = 2
 HC_SCORE_ROUND_BF16 = 4
 HC_SCORE_ROUND_F16 = 8
+HC_SCORE_ACCUMULATE = 16
 
 HC_DTYPE_F32 = 0
 HC_DTYPE_F16 = 1
@@ -46,6 +47,8 @@ SIGNATURES = {
                                 c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t,
                                 c_void_p]),
     "hc_prefill_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "hc_gather_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p,
+                               c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p]),
     "hc_append": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                           c_int, c_void_p, c_void_p]),
     "hc_score": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p,

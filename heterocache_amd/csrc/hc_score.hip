@@ -412,7 +412,10 @@ __global__ __launch_bounds__(kPoolThreads) void score_pool_kernel(const float* _
     if (pooling == 0) acc = acc / (float)kernel;
     best = fmaxf(best, round_mode(acc, flags));
   }
-  if (t < span) S[(int64_t)jw * span + t] = best;
+  if (t < span) {
+    float* o = S + (int64_t)jw * span + t;
+    *o = (flags & HC_SCORE_ACCUMULATE) ? *o + best : best;
+  }
 }
 
 // Small query sets (R < 32 rows): the statistics pass stored the logits,
@@ -436,7 +439,7 @@ constexpr int kFinHeads = 4;  // query heads whose loads are in flight together
 template <int RMODE, int POOL>
 __global__ __launch_bounds__(256) void score_finish_kernel(const float* __restrict__ logits,
                                                            const float* __restrict__ stats, int R, int G, int W,
-                                                           int span, int sum_w, int kernel,
+                                                           int span, int sum_w, int kernel, int accumulate,
                                                            float* __restrict__ S) {
   // s_a[kFinHalo + i] holds position t0 + i of the current head's strip,
   // i in [-p, kFinTile + p).  Thread x loads positions t0 + 4x .. +3 (one
@@ -525,7 +528,7 @@ __global__ __launch_bounds__(256) void score_finish_kernel(const float* __restri
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int t = t0 + threadIdx.x + 256 * k;
-    if (t < span) o[t] = best[k];
+    if (t < span) o[t] = accumulate ? o[t] + best[k] : best[k];
   }
 }
 
@@ -578,7 +581,7 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
       const int rmode = rm;
 #define HC_FINISH(RM, PL)                                                                                  \
   hipLaunchKernelGGL((score_finish_kernel<RM, PL>), fgrid, dim3(256), 0, s, A, stats, a.R, a.G, a.W, a.span, \
-                     sum_w, kernel, scores)
+                     sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores)
       if (rmode == 0) { if (pooling == 0) HC_FINISH(0, 0); else HC_FINISH(0, 1); }
       else if (rmode == 1) { if (pooling == 0) HC_FINISH(1, 0); else HC_FINISH(1, 1); }
       else { if (pooling == 0) HC_FINISH(2, 0); else HC_FINISH(2, 1); }

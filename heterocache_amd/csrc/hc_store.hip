@@ -12,6 +12,9 @@
 //                    (heterocache/cache_utils.py:970-1005).
 //   hc_store_read    unpack store slots [0, count) of rows back to natural
 //                    layout (diagnostics and tests).
+//   hc_gather_rows   natural-layout token rows picked by index lists, into a
+//                    natural-layout destination (the baseline compressors'
+//                    kept-token gathers, heterocache/kv_cluster.py).
 //   hc_copy_rows     natural-layout token rows of selected heads copied to a
 //                    natural-layout destination, typically the host-pinned
 //                    full-KV tier (heterocache/cache_utils.py:939-967), by a
@@ -180,14 +183,19 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(const uint8_t* __restric
                                                        uint8_t* __restrict__ dst_k, uint8_t* __restrict__ dst_v,
                                                        const int64_t* __restrict__ dst_off, int64_t dst_stride_b,
                                                        const int32_t* __restrict__ count, int njobs,
-                                                       int chunks_per_job, int vecs_per_row, int esz) {
+                                                       int chunks_per_job, int vecs_per_row, int esz,
+                                                       const int32_t* __restrict__ idx, int64_t idx_stride,
+                                                       int src_len) {
   const int64_t items = (int64_t)njobs * chunks_per_job;
   for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
     const int job = (int)(item / chunks_per_job), chunk = (int)(item % chunks_per_job);
     const int t0 = chunk * kCopyChunk;
     const int valid = min(kCopyChunk, count[job] - t0);
     if (valid <= 0) continue;
-    const int64_t so = (src_off[job] * esz) + (int64_t)t0 * src_stride_b;
+    // Source token of destination token t: t itself, or idx[job][t] clamped
+    // into [0, src_len) when an index list is given.
+    const int32_t* ix = idx ? idx + (int64_t)job * idx_stride + t0 : nullptr;
+    const int64_t so = (src_off[job] * esz) + (ix ? 0 : (int64_t)t0 * src_stride_b);
     const int64_t dofs = (dst_off[job] * esz) + (int64_t)t0 * dst_stride_b;
     const int n = valid * vecs_per_row;
     for (int c0 = threadIdx.x; c0 < n; c0 += 2 * 256) {
@@ -197,7 +205,9 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(const uint8_t* __restric
       for (int u = 0; u < 2; ++u) {
         const int c = c0 + u * 256;
         if (c < n) {
-          const int64_t off = (int64_t)(c / vecs_per_row) * src_stride_b + (c % vecs_per_row) * 16;
+          const int r = c / vecs_per_row;
+          const int64_t tok = ix ? (int64_t)min(max(ix[r], 0), src_len - 1) : r;
+          const int64_t off = tok * src_stride_b + (c % vecs_per_row) * 16;
           a[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src_k + so + off));
           b[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src_v + so + off));
         }
@@ -354,6 +364,35 @@ extern "C" int hc_copy_rows(int dtype, const void* src_k, const void* src_v, con
   const unsigned grid = (unsigned)std::min<int64_t>(items, max_workgroups);
   hipLaunchKernelGGL(copy_rows_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src_k,
                      (const uint8_t*)src_v, src_off, src_tok_stride * esz, (uint8_t*)dk, (uint8_t*)dv, dst_off,
-                     dst_tok_stride * esz, count, njobs, chunks, HC_HEAD_DIM * esz / 16, esz);
+                     dst_tok_stride * esz, count, njobs, chunks, HC_HEAD_DIM * esz / 16, esz, nullptr, 0, 0);
   return check_launch("hc_copy_rows");
+}
+
+extern "C" int hc_gather_rows(int dtype, const void* src_k, const void* src_v, const int64_t* src_off,
+                              int64_t src_tok_stride, int src_len, const int32_t* idx, int64_t idx_stride,
+                              void* dst_k, void* dst_v, const int64_t* dst_off, int64_t dst_tok_stride,
+                              const int32_t* count, int njobs, int max_count, void* stream) {
+  clear_error();
+  const int esz = dtype == HC_DTYPE_F32 ? 4 : (dtype == HC_DTYPE_BF16 || dtype == HC_DTYPE_F16) ? 2 : 0;
+  if (esz == 0) return set_error(HC_ERR_INVALID, "hc_gather_rows: unknown dtype %d", dtype);
+  if (njobs < 0 || max_count < 0 || src_len < 0 || idx_stride < 0)
+    return set_error(HC_ERR_INVALID, "hc_gather_rows: njobs=%d max_count=%d src_len=%d", njobs, max_count, src_len);
+  if (njobs == 0 || max_count == 0) return HC_OK;
+  if (src_len == 0) return set_error(HC_ERR_INVALID, "hc_gather_rows: empty source");
+  if (!src_k || !src_v || !src_off || !idx || !dst_k || !dst_v || !dst_off || !count)
+    return set_error(HC_ERR_INVALID, "hc_gather_rows: null pointer argument");
+  if (idx_stride < max_count) return set_error(HC_ERR_INVALID, "hc_gather_rows: idx_stride below max_count");
+  if (src_tok_stride < HC_HEAD_DIM || dst_tok_stride < HC_HEAD_DIM || (src_tok_stride * esz) % 16 ||
+      (dst_tok_stride * esz) % 16)
+    return set_error(HC_ERR_INVALID, "hc_gather_rows: token strides must be >= 128 elements and 16-byte multiples");
+  if (((uintptr_t)src_k | (uintptr_t)src_v | (uintptr_t)dst_k | (uintptr_t)dst_v) % 16)
+    return set_error(HC_ERR_INVALID, "hc_gather_rows: buffers must be 16-byte aligned");
+  const int chunks = (max_count + kCopyChunk - 1) / kCopyChunk;
+  const int64_t items = (int64_t)njobs * chunks;
+  const unsigned grid = (unsigned)std::min<int64_t>(items, 65535);
+  hipLaunchKernelGGL(copy_rows_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, (const uint8_t*)src_k,
+                     (const uint8_t*)src_v, src_off, src_tok_stride * esz, (uint8_t*)dst_k, (uint8_t*)dst_v, dst_off,
+                     dst_tok_stride * esz, count, njobs, chunks, HC_HEAD_DIM * esz / 16, esz, idx, idx_stride,
+                     src_len);
+  return check_launch("hc_gather_rows");
 }

@@ -267,6 +267,45 @@ def prefill_attn(q, k, v, scale, out=None, stream=None):
     return out
 
 
+def gather_rows(src_k, src_v, idx, counts, dst_k=None, dst_v=None, stream=None):
+    """dst[b, h, t] = src[b, h, idx[b*H + h, t]] for t < counts[b*H + h].
+
+    src: [B, H, L, 128] (unit channel stride, any other strides); idx: int32
+    [B*H, width] device tensor of source positions (clamped into [0, L));
+    counts: int32 [B*H] device tensor or a python int for every job.  The
+    destinations default to new [B, H, width, 128] tensors.
+    """
+    lib = _lib.load()
+    _require_cuda(src_k, src_v, idx)
+    if src_k.dim() != 4 or src_k.shape[-1] != HEAD_DIM or src_k.stride(-1) != 1 or src_v.shape != src_k.shape:
+        raise ValueError("sources must be [B, H, L, 128] with unit channel stride")
+    if src_k.stride() != src_v.stride():
+        raise ValueError("K and V sources must share strides")
+    B, H, L, D = src_k.shape
+    if idx.dtype != torch.int32 or idx.dim() != 2 or idx.shape[0] != B * H or idx.stride(1) != 1:
+        raise ValueError(f"idx must be int32 [{B * H}, width] with unit inner stride")
+    width = idx.shape[1]
+    if dst_k is None:
+        dst_k = torch.empty((B, H, width, D), dtype=src_k.dtype, device=src_k.device)
+        dst_v = torch.empty_like(dst_k)
+    if dst_k.shape != (B, H, width, D) or dst_v.shape != dst_k.shape or dst_k.stride() != dst_v.stride() \
+            or dst_k.stride(-1) != 1:
+        raise ValueError(f"destinations must be [{B}, {H}, {width}, 128] sharing strides")
+    if not torch.is_tensor(counts):
+        counts = torch.full((B * H,), int(counts), dtype=torch.int32, device=src_k.device)
+    if counts.dtype != torch.int32 or counts.numel() != B * H:
+        raise ValueError("counts must be int32 [B*H]")
+    if width == 0 or B * H == 0:
+        return dst_k, dst_v
+    bh = np.arange(B * H, dtype=np.int64)
+    src_off = torch.as_tensor((bh // H) * src_k.stride(0) + (bh % H) * src_k.stride(1)).to(src_k.device)
+    dst_off = torch.as_tensor((bh // H) * dst_k.stride(0) + (bh % H) * dst_k.stride(1)).to(src_k.device)
+    _lib.check(lib.hc_gather_rows(dtype_code(src_k.dtype), _ptr(src_k), _ptr(src_v), _ptr(src_off), src_k.stride(2), L,
+                                  _ptr(idx), idx.stride(0), _ptr(dst_k), _ptr(dst_v), _ptr(dst_off), dst_k.stride(2),
+                                  _ptr(counts), B * H, width, _stream(stream, src_k)))
+    return dst_k, dst_v
+
+
 def append(k_new, v_new, kstore, vstore, row_tile_off, row_len, row_cap, status=None, stream=None):
     """Write k_new/v_new [rows, 128] at slot row_len[r] of every row, then row_len += 1."""
     lib = _lib.load()

@@ -158,11 +158,26 @@ int hc_prefill_attn(int dtype, const void* q, const int64_t* q_strides, const vo
  * tiles, written and read within the call: no initialisation). */
 size_t hc_prefill_workspace_size(int dtype, int batch, int kv_heads, int kv_len);
 
+/*
+ * Gather token rows by index between natural layouts:
+ *   dst[dst_off[j] + t*dst_tok_stride + c] = src[src_off[j] + i*src_tok_stride + c],
+ *   i = clamp(idx[j*idx_stride + t], 0, src_len - 1),  t < count[j]
+ * (offsets and strides in elements; rows 16-byte aligned).  Replaces the
+ * kept-token `gather` + `cat` of the baseline compressors (PyramidKV, SnapKV,
+ * H2O, StreamingLLM: heterocache/kv_cluster.py:101-106 and :130-135,
+ * :192-197, :448-449, :517-522).
+ */
+int hc_gather_rows(int dtype, const void* src_k, const void* src_v, const int64_t* src_off, int64_t src_tok_stride,
+                   int src_len, const int32_t* idx, int64_t idx_stride, void* dst_k, void* dst_v,
+                   const int64_t* dst_off, int64_t dst_tok_stride, const int32_t* count, int njobs, int max_count,
+                   void* stream);
+
 /* hc_score flags */
 #define HC_SCORE_CAUSAL_WINDOW 1 /* window row w sees keys t <= L - W + w (kv_cluster.py:169-175) */
 #define HC_SCORE_SUM_WINDOW 2    /* sum probabilities over the W rows of a query head (kv_cluster.py:178) */
 #define HC_SCORE_ROUND_BF16 4    /* reproduce the reference's casts to bfloat16 */
 #define HC_SCORE_ROUND_F16 8     /* reproduce the reference's casts to float16 */
+#define HC_SCORE_ACCUMULATE 16   /* add the call's scores into `scores` instead of overwriting them */
 
 /*
  * Pooled observation-window scores, maxed over the GQA group:

@@ -200,6 +200,90 @@ def snapkv_update_kv(key_states, query_states, value_states, window_size, compre
     return np.stack(ks), np.stack(vs)
 
 
+def pyramidkv_layer_capacity(max_capacity_prompt, q_len, window, beta, num_hidden_layers, layer_idx):
+    """Kept tokens before the window of PyramidKVCluster.update_kv, or None
+    when the prompt stays uncompressed (heterocache/kv_cluster.py:61-79,
+    :84, :97, :126).  Python floor division as the reference."""
+    cap, W = max_capacity_prompt, window
+    min_num = (cap - W) // beta
+    max_num = (cap - W) * 2 - min_num
+    if max_num >= q_len - W:
+        max_num = q_len - W
+        min_num = (cap - W) * 2 - max_num
+    steps = (max_num - min_num) // (num_hidden_layers - 1)
+    if q_len < cap:
+        return None
+    if q_len < (cap - W) * 2:
+        return cap - W
+    return max_num - layer_idx * steps
+
+
+def pyramidkv_update_kv(key_states, query_states, value_states, window_size, compression_ratio, pooling, kernel,
+                        num_key_value_groups, num_hidden_layers, layer_idx, beta=20, io_dtype=None):
+    """PyramidKVCluster.update_kv, heterocache/kv_cluster.py:55-136: the
+    SnapKV score with a per-layer capacity.  Returns compressed (key, value)
+    [B, H, keep + W, d] in the reference's order (top-k by descending score,
+    then the window)."""
+    B, H, L, d = query_states.shape
+    cap = int(compression_ratio * L / num_key_value_groups)
+    keep = pyramidkv_layer_capacity(cap, L, window_size, beta, num_hidden_layers, layer_idx)
+    if keep is None:
+        return key_states, value_states
+    W = window_size
+    ks, vs = [], []
+    for b in range(B):
+        kb, vb = [], []
+        for h in range(H):
+            sc = window_scores(query_states[b, h][None, None, -W:], key_states[b, h][None], pooling, kernel,
+                               window_keep=True, io_dtype=io_dtype)[0]
+            top = topk_indices(sc, keep)
+            kb.append(np.concatenate([key_states[b, h, :L - W][top], key_states[b, h, L - W:]], axis=0))
+            vb.append(np.concatenate([value_states[b, h, :L - W][top], value_states[b, h, L - W:]], axis=0))
+        ks.append(np.stack(kb))
+        vs.append(np.stack(vb))
+    return np.stack(ks), np.stack(vs)
+
+
+def h2o_scores(query_states, key_states, scale=None):
+    """Heavy-hitter score of H2OKVCluster.update_kv (heterocache/kv_cluster.py:
+    406-440): softmax over all keys of every query position (no mask), summed
+    over the query positions.  [B, H, L] float64."""
+    q = np.asarray(query_states, dtype=np.float64)
+    k = np.asarray(key_states, dtype=np.float64)
+    scale = 1.0 / math.sqrt(q.shape[-1]) if scale is None else scale
+    z = scale * np.einsum("bhid,bhtd->bhit", q, k)
+    z -= z.max(axis=-1, keepdims=True)
+    p = np.exp(z)
+    p /= p.sum(axis=-1, keepdims=True)
+    return p.sum(axis=2)
+
+
+def h2o_update_kv(key_states, query_states, value_states, compression_ratio, num_key_value_groups):
+    """H2OKVCluster.update_kv (heterocache/kv_cluster.py:397-450): the top
+    capacity keys by heavy-hitter score, no window.  Returns (key, value, kept
+    index lists [B, H, cap] in descending score order)."""
+    B, H, L, d = query_states.shape
+    cap = max(int(compression_ratio * L / num_key_value_groups), 2)
+    if cap > L:
+        return key_states, value_states, None
+    sc = h2o_scores(query_states, key_states)
+    top = np.stack([np.stack([topk_indices(sc[b, h], cap) for h in range(H)]) for b in range(B)])
+    k = np.take_along_axis(np.asarray(key_states), top[..., None], axis=2)
+    v = np.take_along_axis(np.asarray(value_states), top[..., None], axis=2)
+    return k, v, top
+
+
+def streamingllm_update_kv(key_states, value_states, compression_ratio, sink=4):
+    """StreamingLLMKVCluster.update_kv (heterocache/kv_cluster.py:500-523):
+    the first `sink` tokens and the last max(int(r L), 5) - 4 tokens."""
+    L = key_states.shape[2]
+    recent = max(int(compression_ratio * L), 5) - 4
+    if recent > L:
+        return key_states, value_states
+    keep = np.concatenate([np.arange(sink), np.arange(L - recent, L)])
+    return key_states[:, :, keep], value_states[:, :, keep]
+
+
 # --------------------------------------------------------------------------
 # selection
 # --------------------------------------------------------------------------

@@ -363,3 +363,47 @@ def test_config0_inputs_and_oracle_pipeline():
         assert len(kept) == c["caps"][h]
         assert kept[-W:].tolist() == list(range(L - W, L))
         assert np.all(np.diff(kept) > 0)
+
+
+# -- baseline compressors (heterocache/kv_cluster.py) ------------------------------
+def test_pyramidkv_capacity_hand_values():
+    # cap 1024, window 32, beta 20, 32 layers, 4096 tokens: min 992//20 = 49,
+    # max 1984 - 49 = 1935, steps (1935 - 49)//31 = 60.
+    assert O.pyramidkv_layer_capacity(1024, 4096, 32, 20, 32, 0) == 1935
+    assert O.pyramidkv_layer_capacity(1024, 4096, 32, 20, 32, 31) == 1935 - 31 * 60
+    assert O.pyramidkv_layer_capacity(1024, 1000, 32, 20, 32, 3) is None        # shorter than the capacity
+    assert O.pyramidkv_layer_capacity(1024, 1500, 32, 20, 32, 3) == 1024 - 32    # below 2 (cap - W)
+    assert O.pyramidkv_layer_capacity(1024, 1984, 32, 20, 32, 0) == 1935      # at 2 (cap - W): the pyramid
+    # The pyramid keeps about the same total as a flat cap - W per layer.
+    per_layer = [O.pyramidkv_layer_capacity(1024, 4096, 32, 20, 32, l) for l in range(32)]
+    assert abs(np.mean(per_layer) - (1024 - 32)) < 0.02 * (1024 - 32)
+    assert all(a > b for a, b in zip(per_layer, per_layer[1:]))
+
+
+def test_pyramidkv_flat_branch_is_snapkv():
+    rng = np.random.default_rng(17)
+    q = rng.standard_normal((1, 2, 300, 128))
+    k = rng.standard_normal((1, 2, 300, 128))
+    v = rng.standard_normal((1, 2, 300, 128))
+    # cap = int(0.9*300/1) = 270 <= 300 < 2*(270-16): keeps cap - W, as SnapKV.
+    kp, vp = O.pyramidkv_update_kv(k, q, v, 16, 0.9, "avgpool", 5, 1, 32, 7)
+    ks, vs = O.snapkv_update_kv(k, q, v, 16, 0.9, "avgpool", 5, 1)
+    assert kp.shape[2] == 270
+    assert np.array_equal(kp, ks) and np.array_equal(vp, vs)
+
+
+def test_h2o_scores_match_torch_softmax_and_sum_to_query_count():
+    rng = np.random.default_rng(18)
+    q = rng.standard_normal((1, 2, 70, 128))
+    k = rng.standard_normal((1, 2, 70, 128))
+    s = O.h2o_scores(q, k)
+    p = torch.softmax(torch.tensor(q) @ torch.tensor(k).transpose(-1, -2) / math.sqrt(128), dim=-1).sum(dim=2)
+    assert np.abs(s - p.numpy()).max() < 1e-12
+    assert np.allclose(s.sum(axis=-1), 70)  # every query's row sums to 1
+
+
+def test_streamingllm_keeps_sinks_and_recent():
+    k = np.arange(1000)[None, None, :, None] * np.ones((1, 1, 1, 2))
+    ko, _ = O.streamingllm_update_kv(k, k, 0.3)
+    kept = ko[0, 0, :, 0].astype(int).tolist()
+    assert kept == [0, 1, 2, 3] + list(range(1000 - 296, 1000))   # max(int(300), 5) - 4 = 296
