@@ -11,7 +11,8 @@
 // flash_attention_forward; heterocache/qwen_model.py follows the same path).
 //
 // Structure:
-//  * a workgroup holds 4 waves x 32 queries of one query head; the blockIdx
+//  * a workgroup holds 4 waves x 32 queries of one query head, three
+//    workgroups per CU (168 VGPRs, 48 KB LDS); the blockIdx
 //    order puts every workgroup of a KV row on the same XCD (rows are
 //    interleaved modulo the grid's round-robin over XCDs) and dispatches the
 //    query blocks with the most keys first;
@@ -66,12 +67,10 @@ struct PfArgs {
   float scale_log2;
 };
 
-// LDS elements of one buffer set (K tiles then V tiles).
-constexpr int kPfSetElems = 2 * kPfTiles * HC_TILE_ELEMS;
-
+// LDS: two K buffers and one V buffer of kPfTiles tiles each.
 template <typename T>
 constexpr size_t pf_lds_bytes() {
-  return (size_t)2 * kPfSetElems * sizeof(T);
+  return (size_t)3 * kPfTiles * HC_TILE_ELEMS * sizeof(T);
 }
 
 // Four elements of T as one vector store (8 bytes for 16-bit types).
@@ -126,9 +125,16 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
 }
 // s_waitcnt vmcnt(0): every LDS-DMA load of this wave has landed.
 __device__ __forceinline__ void wait_lds_dma() { __builtin_amdgcn_s_waitcnt(0x0f70); }
+// s_waitcnt vmcnt(N): all but this wave's N most recent vector loads have
+// landed (loads complete in order).
+template <int N>
+__device__ __forceinline__ void wait_lds_dma_but() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | N);
+}
 
 template <typename T>
-__global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_attn_kernel(const PfArgs a) {
+__global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_attn_kernel(const PfArgs a) {
   typedef typename Elem<T>::vec8 vec8;
   extern __shared__ __attribute__((aligned(16))) unsigned char pf_lds[];
   T* lds = reinterpret_cast<T*>(pf_lds);
@@ -196,10 +202,12 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
   // window's first token: they are masked, as they follow every query.
   constexpr int kUnits = (int)sizeof(T) / 2;
   constexpr int kUnitsPerThread = 4 * kUnits;
-  uint32_t koff[kUnitsPerThread], kch[kUnitsPerThread];
-  int ktok[kUnitsPerThread];
+  // 16-bit types: unit r is token 16r + tid%16 with fixed channels, so one
+  // offset and a uniform step describe all four; fp32 keeps a table.
+  uint32_t koff[kUnits == 1 ? 1 : kUnitsPerThread], kch[kUnits == 1 ? 1 : kUnitsPerThread];
+  int ktok[kUnits == 1 ? 1 : kUnitsPerThread];
 #pragma unroll
-  for (int r = 0; r < kUnitsPerThread; ++r) {
+  for (int r = 0; r < (kUnits == 1 ? 1 : kUnitsPerThread); ++r) {
     const int w = r * kPfThreads + tid;
     const int u = w / kUnits, half = w % kUnits;
     const int c = u >> 9, v = u & 511;
@@ -208,36 +216,54 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
     kch[r] = (uint32_t)((32 * s + 8 * g) * (int64_t)sizeof(T) + 16 * half);
     koff[r] = (uint32_t)(ktok[r] * a.k_st * (int64_t)sizeof(T)) + kch[r];
   }
+  const uint32_t kstep = (uint32_t)(16 * a.k_st * (int64_t)sizeof(T));
   const char* vtiles = reinterpret_cast<const char*>(a.vt) +
                        ((int64_t)row * a.vt_tiles * HC_TILE_ELEMS) * (int64_t)sizeof(T) + 16 * tid;
+  T* const vbuf = lds + 2 * kPfTiles * HC_TILE_ELEMS;
 
-  auto stage = [&](int buf, int it) {
-    char* sk = reinterpret_cast<char*>(lds + buf * kPfSetElems);
-    char* sv = reinterpret_cast<char*>(lds + buf * kPfSetElems + kPfTiles * HC_TILE_ELEMS);
+  auto stage_k = [&](int buf, int it) {
+    char* sk = reinterpret_cast<char*>(lds + buf * kPfTiles * HC_TILE_ELEMS);
     const int t0 = it * kPfKeys;
     const char* kit = reinterpret_cast<const char*>(kbase) + (int64_t)t0 * a.k_st * (int64_t)sizeof(T);
     const int lim = a.Lk - t0;
-    const char* vit = vtiles + (int64_t)it * kPfTiles * HC_TILE_ELEMS * (int64_t)sizeof(T);
 #pragma unroll
     for (int r = 0; r < kUnitsPerThread; ++r) {
       const int wb = r * kPfThreads + wave * 64;  // first unit of this wave
-      lds_dma16(kit + (ktok[r] < lim ? koff[r] : kch[r]), sk + 16 * wb);
-      lds_dma16(vit + 16 * r * kPfThreads, sv + 16 * wb);
+      if constexpr (kUnits == 1) {
+        const int tok = 16 * r + (tid & 15);
+        lds_dma16(kit + (tok < lim ? koff[0] + r * kstep : kch[0]), sk + 16 * wb);
+      } else {
+        lds_dma16(kit + (ktok[r] < lim ? koff[r] : kch[r]), sk + 16 * wb);
+      }
     }
   };
+  auto stage_v = [&](int it) {
+    char* sv = reinterpret_cast<char*>(vbuf);
+    const char* vit = vtiles + (int64_t)it * kPfTiles * HC_TILE_ELEMS * (int64_t)sizeof(T);
+#pragma unroll
+    for (int r = 0; r < kUnitsPerThread; ++r)
+      lds_dma16(vit + 16 * r * kPfThreads, sv + 16 * (r * kPfThreads + wave * 64));
+  };
 
-  stage(0, 0);
+  // K is double-buffered (K(it+1) loads during iteration it); V has one
+  // buffer, loaded between two barriers around the P.V step: V(it+1)
+  // arrives while the next iteration forms its scores and probabilities.
+  // 48 KB of LDS per workgroup leaves room for three workgroups per CU.
+  stage_k(0, 0);
+  stage_v(0);
   wait_lds_dma();
   __syncthreads();
 
   for (int it = 0; it < nit; ++it) {
     const int cur = it & 1;
     const int t0 = it * kPfKeys;
-    if (it + 1 < nit) stage(cur ^ 1, it + 1);
-    if (active && t0 <= pos_hi) {
+    const bool more = it + 1 < nit;
+    if (more) stage_k(cur ^ 1, it + 1);
+    const bool work = active && t0 <= pos_hi;
+    vec8 pb[2][2];  // [tile][query block]: B operand of the P.V step
+    if (work) {
       __builtin_amdgcn_s_setprio(0);
-      const T* sk = lds + cur * kPfSetElems;
-      const T* sv = sk + kPfTiles * HC_TILE_ELEMS;
+      const T* sk = lds + cur * kPfTiles * HC_TILE_ELEMS;
       // S^T blocks: rows = keys 16*tb + 4*g4 + r, column = query 16j + n16.
       f32x4 sacc[4][2];
 #pragma unroll
@@ -269,7 +295,6 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
               if (t0 + 16 * tb + 4 * g4 + r > pj) sacc[tb][j][r] = -INFINITY;
         }
       }
-      vec8 pb[2][2];  // [tile][query block]: B operand of the P.V step
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         // Raw tile maximum (scale > 0), shared by the 4 lanes of a query.
@@ -314,10 +339,19 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
         }
       }
       __builtin_amdgcn_s_setprio(0);
+    }
+    // V(it) (issued before K(it+1)) has landed in every wave's part of the
+    // buffer once each wave's older loads are done.
+    if (more)
+      wait_lds_dma_but<kUnitsPerThread>();
+    else
+      wait_lds_dma();
+    __syncthreads();
+    if (work) {
       // O^T blocks: rows = channels 16*db + 4*g4 + r, column = query.
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const T* vt = sv + c * HC_TILE_ELEMS;
+        const T* vt = vbuf + c * HC_TILE_ELEMS;
 #pragma unroll
         for (int db = 0; db < 8; ++db) {
           const vec8 va = load8(vt + (db * 64 + lane) * 8);
@@ -326,9 +360,9 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 2) void prefill_at
         }
       }
     }
-    __builtin_amdgcn_s_setprio(0);
-    wait_lds_dma();
-    __syncthreads();
+    wait_lds_dma();  // K(it+1) has landed
+    __syncthreads();  // ... and V(it) is no longer read
+    if (more) stage_v(it + 1);
   }
 
   if (!active) return;
