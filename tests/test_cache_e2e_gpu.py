@@ -151,3 +151,56 @@ def test_chunked_prefill_equals_single_shot(dev, chunks):
     case) selects, stores and decodes exactly as the single-shot oracle."""
     trig = run(dev, torch.float32, chunks=chunks)
     assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
+
+
+def test_chunked_prefill_with_observation_window_equals_single_shot(dev):
+    """window_size = 8 with a last chunk shorter than the window: the kept
+    query rows span two chunks; stores, reference sets and one decode step
+    equal the single-shot cache's bit for bit."""
+    torch.manual_seed(0)
+    B, Hq, Hkv, NL, D, L = 1, 32, 8, 2, 128, 1500
+    data = head_data()
+
+    def make():
+        cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
+                                max_gen_len=4, decode_step=5, pooling="maxpool", kernel_size=7,
+                                num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, window_size=8)
+        return HeteroCache(cfg)
+
+    g = torch.Generator().manual_seed(9)
+    qs = [torch.randn((B, Hq, L, D), generator=g).to(dev) for _ in range(NL)]
+    ks = [torch.randn((B, Hkv, L, D), generator=g).to(dev) for _ in range(NL)]
+    vs = [torch.randn((B, Hkv, L, D), generator=g).to(dev) for _ in range(NL)]
+    whole, chunked = make(), make()
+    chunked.begin_prefill(L)
+    for layer in range(NL):
+        kc, vc = whole.update(ks[layer], vs[layer], layer)
+        whole.init_coefficient(qs[layer], kc, layer)
+        whole.prefill_select(qs[layer], kc, vc, layer)
+        for s, e in ((0, 745), (745, 1497), (1497, 1500)):
+            qc = qs[layer][:, :, s:e]
+            kc, vc = chunked.update(ks[layer][:, :, s:e], vs[layer][:, :, s:e], layer, {"query_states": qc})
+            chunked.init_coefficient(qc, kc, layer)
+            chunked.prefill_select(qc, kc, vc, layer)
+    q1 = torch.randn((B, Hq, 1, D), generator=g).to(dev)
+    k1 = torch.randn((B, Hkv, 1, D), generator=g).to(dev)
+    v1 = torch.randn((B, Hkv, 1, D), generator=g).to(dev)
+    outs = []
+    for cache in (whole, chunked):
+        o = []
+        for layer in range(NL):
+            cache.update(k1, v1, layer)
+            o.append(cache.decode_attention(q1, layer))
+        outs.append(torch.stack(o))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    for layer in range(NL):
+        a, b = whole.stores[layer], chunked.stores[layer]
+        assert a.host_len.tolist() == b.host_len.tolist()
+        for r in range(B * Hkv):
+            n = int(a.host_len[r])
+            ka, va = a.read_rows([r], n)
+            kb, vb = b.read_rows([r], n)
+            assert torch.equal(ka, kb) and torch.equal(va, vb), (layer, r)
+        if whole._drift[layer].ref_bits is not None:
+            assert torch.equal(whole._drift[layer].ref_bits, chunked._drift[layer].ref_bits)
