@@ -35,6 +35,7 @@ constexpr int kScoreWaves = 4;
 constexpr int kSubTiles = 4;                      // 16-token sub-tiles per wave
 constexpr int kScoreChunk = kScoreWaves * 16 * kSubTiles;  // 256 tokens per workgroup
 constexpr int kQPitch = HC_HEAD_DIM + 8;
+constexpr float kScoreLazy = 8.f;  // lazy-maximum threshold, log2 units
 
 struct ScoreArgs {
   const void* q;
@@ -203,11 +204,17 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
               }
             }
           }
-          const float mn = fmaxf(fmaxf(m[nt], fmaxf(x[0], x[1])), fmaxf(x[2], x[3]));
-          const float sm =
-              (fast_exp2(x[0] - mn) + fast_exp2(x[1] - mn)) + (fast_exp2(x[2] - mn) + fast_exp2(x[3] - mn));
-          l[nt] = fmaf(l[nt], fast_exp2(m[nt] - mn), sm);
-          m[nt] = mn;
+          // Lazy running maximum: m moves only when a value exceeds it by
+          // more than 2^kScoreLazy, so the rescale (and its exp2) is rare
+          // and each value costs a subtract, an exp2 and an add.
+          const float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+          if (__any(mx > m[nt] + kScoreLazy)) {
+            if (mx > m[nt] + kScoreLazy) {
+              l[nt] *= fast_exp2(m[nt] - mx);
+              m[nt] = mx;
+            }
+          }
+          l[nt] += (fast_exp2(x[0] - m[nt]) + fast_exp2(x[1] - m[nt])) + (fast_exp2(x[2] - m[nt]) + fast_exp2(x[3] - m[nt]));
         }
       }
     }
@@ -299,8 +306,14 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   stage_queries<T>(a, job, s_q);
   for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
     // Padding rows get probability 0 even where logits are not masked.
-    s_m[r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] : 0.f;
-    s_iz[r] = r < a.R ? 1.f / stats[((int64_t)job * a.R + r) * 2 + 1] : 0.f;
+    if constexpr (RM == 0) {
+      // Without casts p = exp2(x - (m + log2 l)): one subtract, no divide.
+      s_m[r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] + __log2f(stats[((int64_t)job * a.R + r) * 2 + 1])
+                       : INFINITY;
+    } else {
+      s_m[r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] : 0.f;
+      s_iz[r] = r < a.R ? 1.f / stats[((int64_t)job * a.R + r) * 2 + 1] : 0.f;
+    }
   }
   const int wout = sum_w ? 1 : a.W;
   const int tw = chunk * kScoreChunk + wave * 16 * kSubTiles;
@@ -335,21 +348,28 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
           float x[4], p[4];
           subtile_logits_rows<T, RM, MASK>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
   #pragma unroll
-          for (int j = 0; j < 4; ++j) p[j] = x[j] == -INFINITY ? 0.f : round_fixed<RM>(fast_exp2(x[j] - M[j]) * IZ[j]);
+          for (int j = 0; j < 4; ++j) {
+            if constexpr (RM == 0)
+              p[j] = fast_exp2(x[j] - M[j]);  // M holds m + log2 l; masked logits give 0
+            else
+              p[j] = x[j] == -INFINITY ? 0.f : round_fixed<RM>(fast_exp2(x[j] - M[j]) * IZ[j]);
+          }
           if (!sum_w) {
             // Row r = g*W + w -> A[job][w][g][t].
   #pragma unroll
             for (int j = 0; j < 4; ++j)
               if (r0 + j < a.R && t < a.span) A[orow[j] + t] = p[j];
           } else if (a.W >= 16) {
-            // The 16 rows of this tile all belong to one query head.
-            float v = (p[0] + p[1]) + (p[2] + p[3]);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            gsum[u] += v;
+            // The 16 rows of this tile all belong to one query head; each
+            // lane sums its 4 rows over the head's tiles, and the 4 lane
+            // groups are combined once per head.
+            gsum[u] += (p[0] + p[1]) + (p[2] + p[3]);
             if (((16 * (nt + 1)) % a.W) == 0) {
+              float v = gsum[u];
+              v += __shfl_xor(v, 16, 64);
+              v += __shfl_xor(v, 32, 64);
               const int g = (16 * nt) / a.W;
-              if (rg == 0 && g < a.G && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_fixed<RM>(gsum[u]);
+              if (rg == 0 && g < a.G && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_fixed<RM>(v);
               gsum[u] = 0.f;
             }
           } else if (a.W == 8) {
