@@ -37,6 +37,8 @@ def parse():
     p.add_argument("--unfused-append", action="store_true", help="append in its own launch before attention")
     p.add_argument("--full-steps", type=int, default=20, help="decode steps of the HeteroCache phase")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
+    p.add_argument("--prefill-only", action="store_true",
+                   help="run only the prefill-attention phase and print its figures (for counter profiling)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="after the decode phase, run a 256 MiB fp32 streaming copy (negate) three times as the "
                         "reference kernel for HBM counter calibration")
@@ -458,6 +460,9 @@ def main():
     from heterocache_amd.store import KVStore
 
     dev = torch.device("cuda:0")
+    if args.prefill_only:
+        print(json.dumps({"prefill_attention": prefill_attention_phase(args, torch, dev)}))
+        return
     torch.manual_seed(args.seed)
     L, Hkv, G, D = args.ctx, 8, 4, 128
     data = workloads.synthetic_head_json(args.layers, Hkv, args.seed)
