@@ -46,9 +46,10 @@ def _require_cuda(*ts):
 class Workspace:
     """Grow-only, zero-initialised per-device scratch buffer.
 
-    The decode kernel keeps self-resetting counters at the head of its
-    workspace, so the buffer is zero-filled when (re)allocated and then reused
-    by launches on one stream.  Work on another stream needs its own instance.
+    hc_select_topk's histograms must start at zero (each call leaves them
+    zeroed again), so the buffer is zero-filled when (re)allocated; the
+    decode workspace needs no initialisation.  Launches on one stream reuse
+    it; work on another stream needs its own instance.
     """
 
     def __init__(self):
