@@ -395,6 +395,22 @@ def baseline_compressors_phase(args, torch, dev):
     return out
 
 
+def head_analysis_phase(args, torch, dev):
+    """The head-classification JSON producer on Llama-3-8B-shaped synthetic
+    attention maps: 32 layers, a prefill step and five decode steps, the
+    last query row of 32 query heads over 5000 positions, top-1024."""
+    from heterocache_amd import head_analysis
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    maps = {l: {s: torch.rand((1, 32, 1, 5000), device=dev, generator=g) for s in range(6)} for l in range(32)}
+    head_analysis.analyze(maps, 32, 32, 8, topk=1024, max_length=5000, decode_step=5)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out = head_analysis.analyze(maps, 32, 32, 8, topk=1024, max_length=5000, decode_step=5)
+    torch.cuda.synchronize()
+    return {"seconds": round(time.perf_counter() - t0, 3), "layers": 32, "steps": 6, "positions": 5000,
+            "topk": 1024, "counts": out["meta"]["counts"]}
+
+
 def prefill_attention_phase(args, torch, dev):
     """Causal prefill attention of one Llama-3-8B layer (32 query heads over 8
     KV heads, projection layout [B, T, H, 128]): a 32K prompt in one call, and
@@ -554,6 +570,7 @@ def main():
         rec["prefill_attention"] = prefill_attention_phase(args, torch, dev)
         rec["decode_other_configs"] = decode_configs_phase(args, torch, dev)
         rec["baseline_compressors"] = baseline_compressors_phase(args, torch, dev)
+        rec["head_analysis"] = head_analysis_phase(args, torch, dev)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(L, budgets[0], args.cpu_seconds)
     print(json.dumps(rec))

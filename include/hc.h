@@ -172,6 +172,18 @@ int hc_gather_rows(int dtype, const void* src_k, const void* src_v, const int64_
                    const int64_t* dst_off, int64_t dst_tok_stride, const int32_t* count, int njobs, int max_count,
                    void* stream);
 
+/*
+ * Head-analysis pooling (offline head classification):
+ *   out[b*heads_out + h][t] = avg_pool_k(mean_{g<group} attn[b*batch_stride + (h*group + g)*head_stride + t])
+ * for t < span; zero padding kernel/2, divisor kernel (odd kernel).  With
+ * 16-bit input the group mean is rounded to the input type.  Replaces the
+ * GQA mean + last-row sum + avg_pool1d of get_head_topk_exact
+ * (tools/get_cluster.py:13-56); the top-k that follows is hc_select_topk and
+ * the overlap ratios hc_set_bits + hc_overlap_count.
+ */
+int hc_head_pool(int dtype, const void* attn, int64_t batch_stride, int64_t head_stride, int batch, int heads_out,
+                 int group, int span, int kernel, float* out, void* stream);
+
 /* hc_score flags */
 #define HC_SCORE_CAUSAL_WINDOW 1 /* window row w sees keys t <= L - W + w (kv_cluster.py:169-175) */
 #define HC_SCORE_SUM_WINDOW 2    /* sum probabilities over the W rows of a query head (kv_cluster.py:178) */

@@ -284,6 +284,142 @@ def streamingllm_update_kv(key_states, value_states, compression_ratio, sink=4):
     return key_states[:, :, keep], value_states[:, :, keep]
 
 
+def head_topk_sets(attn, num_q_heads, num_kv_heads, max_length, topk, io_dtype=None):
+    """get_head_topk_exact, tools/get_cluster.py:13-56: the last query row of
+    each (KV) head -- its query group averaged when the map holds the query
+    heads of a GQA model -- limited to max_length, avg-pooled (k = min(5, n),
+    zero padding k//2, divisor k) and its top-k position set.  attn:
+    [B, heads, rows, seq] (or [B, heads, seq]).  Returns sets[h][b] (python
+    sets) and the head count."""
+    a = np.asarray(attn, dtype=np.float32)
+    if a.ndim == 3:
+        a = a[:, :, None]
+    B, Hs, R, S = a.shape
+    if num_q_heads != num_kv_heads and Hs == num_q_heads:
+        G = num_q_heads // num_kv_heads
+        a = a.reshape(B, num_kv_heads, G, R, S).mean(axis=2, dtype=np.float32)
+        if io_dtype is not None:
+            a = round_to(a, io_dtype)
+    H = a.shape[1]
+    sets = [[set() for _ in range(B)] for _ in range(H)]
+    n = min(max_length, S)
+    for h in range(H):
+        vec = a[:, h, -1, :n]
+        if vec.shape[-1] == 0:
+            continue
+        k = min(5, vec.shape[-1])
+        pooled = pool1d(vec.astype(np.float32), "avgpool", k).astype(np.float32)
+        kk = min(topk, vec.shape[-1])
+        if kk == 0:
+            continue
+        for b in range(B):
+            sets[h][b] = set(topk_indices(pooled[b], kk).tolist())
+    return sets, H
+
+
+def overlap_ratio(set_a, set_b, topk):
+    """calculate_overlap_ratio, tools/get_cluster.py:58-66."""
+    if not set_a or not set_b:
+        return 0.0
+    return len(set_a & set_b) / (len(set_a) if set_a else topk)
+
+
+def star_clusters_greedy(adjacency, heads):
+    """find_star_clusters_greedy, tools/get_cluster.py:70-110."""
+    unassigned = set(heads)
+    clusters, assigned = {}, set()
+    while unassigned:
+        cands = [(len(adjacency.get(n, set()) & unassigned), n, adjacency.get(n, set()) & unassigned)
+                 for n in unassigned]
+        cands.sort(key=lambda x: (-x[0], x[1]))
+        degree, leader, members = cands[0]
+        if degree == 0:
+            break
+        clusters[leader] = sorted(members)
+        unassigned.remove(leader)
+        assigned.add(leader)
+        for m in members:
+            unassigned.remove(m)
+            assigned.add(m)
+    return clusters, assigned
+
+
+def head_analysis(maps, num_layers, num_q_heads, num_kv_heads, topk, max_length, stable_threshold, sim_threshold,
+                  decode_step):
+    """analyze_combined_heads, tools/get_cluster.py:113-330, on maps[layer][step]
+    -> [B, heads, rows, seq] arrays.  Returns the JSON dict (relations keyed by
+    int head; json.dumps turns them into the reference's string keys)."""
+    type_map = {"anchor": 1, "volatile": 2, "pivot": 3, "satellite": 4}
+    total = num_q_heads
+    cls = [[0] * total for _ in range(num_layers)]
+    alloc = [[-1.0] * total for _ in range(num_layers)]
+    rel = [{} for _ in range(num_layers)]
+    counts = {k: 0 for k in type_map}
+    steps = sorted({s for per in maps.values() for s in per})
+    prefill, decode = steps[0], steps[1:]
+    spatial = decode_step if decode_step in steps else steps[-1]
+    for layer in range(num_layers):
+        if layer not in maps or prefill not in maps[layer]:
+            continue
+        base, H = head_topk_sets(maps[layer][prefill], num_q_heads, num_kv_heads, max_length, topk)
+        B = len(base[0])
+        if H != total and layer == 0:
+            cls = [[0] * H for _ in range(num_layers)]
+            alloc = [[-1.0] * H for _ in range(num_layers)]
+        history = {h: [] for h in range(H)}
+        for step in decode:
+            if step not in maps[layer]:
+                continue
+            cur, _ = head_topk_sets(maps[layer][step], num_q_heads, num_kv_heads, max_length, topk)
+            for h in range(H):
+                ovs = [overlap_ratio(base[h][b], cur[h][b], topk) for b in range(B)]
+                history[h].append(sum(ovs) / len(ovs))
+        med, dyn = {}, {}
+        for h in range(H):
+            if not history[h]:
+                dyn[h], med[h] = "volatile", 0.0
+            else:
+                med[h] = float(np.median(history[h]))
+                dyn[h] = "volatile" if med[h] < stable_threshold else "anchor"
+        adj = {}
+        if spatial in maps[layer]:
+            sp, _ = head_topk_sets(maps[layer][spatial], num_q_heads, num_kv_heads, max_length, topk)
+            for i in range(H):
+                for j in range(H):
+                    if i == j:
+                        continue
+                    sim = sum(overlap_ratio(sp[i][b], sp[j][b], topk) for b in range(B)) / B
+                    if sim >= sim_threshold:
+                        adj.setdefault(i, set()).add(j)
+        clusters, assigned = star_clusters_greedy(adj, list(range(H)))
+        rel[layer] = clusters
+        for h in range(H):
+            alloc[layer][h] = med[h]
+            if h in clusters:
+                cls[layer][h] = type_map["pivot"]
+                counts["pivot"] += 1
+                alloc[layer][h] = -1.0
+            elif h in assigned:
+                cls[layer][h] = type_map["satellite"]
+                counts["satellite"] += 1
+            elif dyn[h] == "anchor":
+                cls[layer][h] = type_map["anchor"]
+                counts["anchor"] += 1
+            else:
+                cls[layer][h] = type_map["volatile"]
+                counts["volatile"] += 1
+                alloc[layer][h] = -1.0
+    targets = [v for row in alloc for v in row if v > -0.5]
+    inv_total = sum(1.0 / (v + 1e-6) for v in targets)
+    if targets and inv_total > 1e-9:
+        for r in range(len(alloc)):
+            for c in range(len(alloc[r])):
+                if alloc[r][c] > -0.5:
+                    alloc[r][c] = (1.0 / (alloc[r][c] + 1e-6)) / inv_total * len(targets)
+    return {"meta": {"type_map": type_map, "counts": counts}, "classification_matrix": cls,
+            "allocation_matrix": alloc, "leader_member_relations": rel}
+
+
 # --------------------------------------------------------------------------
 # selection
 # --------------------------------------------------------------------------

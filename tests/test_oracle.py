@@ -407,3 +407,49 @@ def test_streamingllm_keeps_sinks_and_recent():
     ko, _ = O.streamingllm_update_kv(k, k, 0.3)
     kept = ko[0, 0, :, 0].astype(int).tolist()
     assert kept == [0, 1, 2, 3] + list(range(1000 - 296, 1000))   # max(int(300), 5) - 4 = 296
+
+
+# -- head analysis (tools/get_cluster.py) -------------------------------------------
+def test_head_topk_sets_pooling_matches_torch():
+    rng = np.random.default_rng(19)
+    attn = rng.random((2, 8, 3, 40)).astype(np.float32)   # 8 query heads over 2 KV heads
+    sets, H = O.head_topk_sets(attn, 8, 2, 37, 6)
+    assert H == 2
+    a = torch.tensor(attn).view(2, 2, 4, 3, 40).mean(dim=2)[:, :, -1, :37]
+    pooled = F.avg_pool1d(a, kernel_size=5, padding=2, stride=1)
+    for h in range(2):
+        for b in range(2):
+            assert sets[h][b] == set(torch.topk(pooled[b, h], 6).indices.tolist())
+
+
+def test_star_clusters_hand_example():
+    # 0 has three neighbours, 4 two (one of them, 1, taken by 0's star); 5 alone.
+    adj = {0: {1, 2, 3}, 1: {0}, 4: {1, 5}, 2: {0}, 3: {0}, 5: {4}}
+    clusters, assigned = O.star_clusters_greedy(adj, list(range(6)))
+    assert clusters == {0: [1, 2, 3], 4: [5]}
+    assert assigned == {0, 1, 2, 3, 4, 5}
+    assert O.star_clusters_greedy({}, [0, 1]) == ({}, set())
+
+
+def test_head_analysis_allocation_and_types():
+    """Two layers, 4 heads: identical stable heads 0-1 (a star), a stable
+    unique head 2 (anchor), a drifting head 3 (volatile); allocation ratios of
+    the anchor and satellite heads average one."""
+    rng = np.random.default_rng(20)
+    S = 200
+    base = rng.random((1, 4, 1, S)).astype(np.float32)
+    base[:, 1] = base[:, 0]
+    maps = {}
+    for layer in range(2):
+        per = {0: base.copy()}
+        for step in range(1, 4):
+            m = base.copy()
+            m[:, 3] = rng.random((1, 1, S))
+            per[step] = m
+        maps[layer] = per
+    out = O.head_analysis(maps, 2, 4, 4, 20, 5000, 0.5, 0.5, 3)
+    assert out["classification_matrix"][0] == [3, 4, 1, 2]
+    assert out["leader_member_relations"][0] == {0: [1]}
+    vals = [v for row in out["allocation_matrix"] for v in row if v > -0.5]
+    assert len(vals) == 4 and abs(np.mean(vals) - 1.0) < 1e-12
+    assert out["meta"]["counts"] == {"anchor": 2, "volatile": 2, "pivot": 2, "satellite": 2}
