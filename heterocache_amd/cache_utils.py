@@ -31,7 +31,7 @@ reference's behaviour where it differs):
     :1093).
 """
 import math
-from typing import Dict, Optional
+from typing import Dict, List, Optional
 
 import numpy as np
 import torch
@@ -749,3 +749,167 @@ class HeteroCache(DynamicCache):
                 ev = torch.cuda.Event()
                 ev.record(side)
                 self._retrieval_done[layer_idx] = ev
+
+
+# ---------------------------------------------------------------------------
+# Baseline compressor caches (heterocache/cache_utils.py:18-41, 81-420)
+# ---------------------------------------------------------------------------
+class CompressionCacheConfig:
+    """heterocache/cache_utils.py:18-40."""
+
+    def __init__(self, window_size: Optional[int] = 32, compression_ratio: Optional[float] = 0.5,
+                 pooling: Optional[str] = "avgpool", kernel_size: Optional[int] = 5,
+                 num_attn_heads: Optional[int] = 32, num_kv_heads: Optional[int] = 8, num_layers: Optional[int] = 32):
+        self.window_size = window_size
+        self.compression_ratio = compression_ratio
+        self.pooling = pooling
+        self.kernel_size = kernel_size
+        self.num_attn_heads = num_attn_heads
+        self.num_kv_heads = num_kv_heads
+        self.num_layers = num_layers
+        self.n_init = 128
+
+
+def _repeat_kv(x, n_rep):
+    """K/V repeated per query head (the reference's repeat_kv): an expanded
+    view materialised by one copy."""
+    if n_rep == 1:
+        return x
+    B, H, L, D = x.shape
+    return x[:, :, None].expand(B, H, n_rep, L, D).reshape(B, H * n_rep, L, D)
+
+
+class BaseKVCache(DynamicCache):
+    """heterocache/cache_utils.py:81-222: each layer's prompt K/V (repeated per
+    query head) goes through the layer's compressor once; decode tokens are
+    appended; update returns the layer's whole cache, which the model's own
+    attention reads (hc_prefill_attn through the patched attention class)."""
+
+    def __init__(self):
+        super().__init__()
+        self._seen_tokens = 0
+        self.key_cache: List[torch.Tensor] = []
+        self.value_cache: List[torch.Tensor] = []
+        self.kv_clusters = {}
+        self.kv_cluster_granularity = "layer"
+        self.temp_key_cache = []
+        self.temp_value_cache = []
+
+    def __bool__(self):
+        return True
+
+    def get_kv_cluster_class_config(self, layer_idx: int, head_idx: int = None):
+        raise NotImplementedError("Make sure to implement `get_kv_cluster_class_config` in a subclass.")
+
+    def get_kv_cluster_class(self, layer_idx: int, head_idx=None):
+        name, cls, config = self.get_kv_cluster_class_config(layer_idx, head_idx)
+        if name not in self.kv_clusters:
+            self.kv_clusters[name] = cls(**config)
+        return self.kv_clusters[name]
+
+    def compressed_kv(self, key_states, query_states, value_states, attention_mask, num_key_value_groups, layer_idx):
+        if self.kv_cluster_granularity != "layer":
+            raise AssertionError(f"kv_cluster_granularity {self.kv_cluster_granularity} not supported")
+        cluster = self.get_kv_cluster_class(layer_idx)
+        k, v = cluster.update_kv(key_states, query_states, value_states, attention_mask, num_key_value_groups)
+        self.key_cache.append(k)
+        self.value_cache.append(v)
+
+    def update(self, key_states, value_states, layer_idx, cache_kwargs=None):
+        cache_kwargs = cache_kwargs or {}
+        update_global = cache_kwargs.get("update_global_past_kv", True)
+        query_states = cache_kwargs["query_states"]
+        groups = cache_kwargs["num_key_value_groups"]
+        if key_states.size(1) != query_states.size(1):
+            key_states = _repeat_kv(key_states, groups)
+            value_states = _repeat_kv(value_states, groups)
+        if layer_idx == 0:
+            self._seen_tokens += key_states.shape[-2]
+        initializing = len(self.key_cache) == layer_idx
+        if initializing:
+            self.compressed_kv(key_states, query_states, value_states, cache_kwargs.get("attention_mask"), groups,
+                               layer_idx)
+        elif update_global:
+            self.key_cache[layer_idx] = torch.cat([self.key_cache[layer_idx], key_states], dim=-2)
+            self.value_cache[layer_idx] = torch.cat([self.value_cache[layer_idx], value_states], dim=-2)
+        elif len(self.temp_key_cache) == layer_idx:
+            self.temp_key_cache.append(key_states)
+            self.temp_value_cache.append(value_states)
+        else:
+            self.temp_key_cache[layer_idx] = torch.cat([self.temp_key_cache[layer_idx], key_states], dim=-2)
+            self.temp_value_cache[layer_idx] = torch.cat([self.temp_value_cache[layer_idx], value_states], dim=-2)
+        if initializing:
+            return key_states, value_states
+        if self.temp_key_cache:
+            return (torch.cat([self.key_cache[layer_idx], self.temp_key_cache[layer_idx]], dim=-2),
+                    torch.cat([self.value_cache[layer_idx], self.temp_value_cache[layer_idx]], dim=-2))
+        return self.key_cache[layer_idx], self.value_cache[layer_idx]
+
+    def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
+        if len(self.key_cache) <= (layer_idx or 0):
+            return 0
+        return self._seen_tokens
+
+    def clear_temp_kv_cache(self):
+        if self.temp_key_cache:
+            self._seen_tokens -= self.temp_key_cache[-1].shape[-2]
+        self.temp_key_cache = []
+        self.temp_value_cache = []
+
+
+class SnapKVCache(BaseKVCache):
+    """heterocache/cache_utils.py:256-273."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.window_size = config.window_size
+        self.compression_ratio = config.compression_ratio
+        self.kernel_size = config.kernel_size
+        self.pooling = config.pooling
+
+    def get_kv_cluster_class_config(self, layer_idx: int, head_idx: int = None):
+        from .kv_cluster import SnapKVCluster
+        cfg = {"window_size": self.window_size, "compression_ratio": self.compression_ratio,
+               "kernel_size": self.kernel_size, "pooling": self.pooling}
+        return ",".join(["snapkv"] + [str(v) for v in cfg.values()]), SnapKVCluster, cfg
+
+
+class PyramidKVCache(SnapKVCache):
+    """heterocache/cache_utils.py:375-392."""
+
+    def __init__(self, config):
+        super().__init__(config)
+        self.num_layers = config.num_layers
+
+    def get_kv_cluster_class_config(self, layer_idx: int, head_idx: int = None):
+        from .kv_cluster import PyramidKVCluster
+        cfg = {"num_hidden_layers": self.num_layers, "window_size": self.window_size,
+               "compression_ratio": self.compression_ratio, "kernel_size": self.kernel_size,
+               "pooling": self.pooling, "layer_idx": layer_idx}
+        return ",".join(["pyramidv"] + [str(v) for v in cfg.values()]), PyramidKVCluster, cfg
+
+
+class H2OKVCache(BaseKVCache):
+    """heterocache/cache_utils.py:237-254."""
+
+    def __init__(self, config):
+        super().__init__()
+        self.window_size = config.window_size
+        self.compression_ratio = config.compression_ratio
+        self.kernel_size = config.kernel_size
+        self.pooling = config.pooling
+
+    def get_kv_cluster_class_config(self, layer_idx: int, head_idx: int = None):
+        from .kv_cluster import H2OKVCluster
+        cfg = {"window_size": self.window_size, "compression_ratio": self.compression_ratio,
+               "kernel_size": self.kernel_size, "pooling": self.pooling}
+        return ",".join(["h2o"] + [str(v) for v in cfg.values()]), H2OKVCluster, cfg
+
+
+class StreamingLLMKVCache(SnapKVCache):
+    """heterocache/cache_utils.py:395-419."""
+
+    def get_kv_cluster_class_config(self, layer_idx: int, head_idx: int = None):
+        from .kv_cluster import StreamingLLMKVCluster
+        cfg = {"window_size": self.window_size, "compression_ratio": self.compression_ratio}
+        return ",".join(["streamingllm"] + [str(v) for v in cfg.values()]), StreamingLLMKVCluster, cfg

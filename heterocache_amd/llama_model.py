@@ -121,16 +121,17 @@ class LlamaAttention(nn.Module):
         bsz, q_len, _ = hidden_states.size()
         query_states, key_states, value_states = self._project(hidden_states, position_embeddings)
         cache = past_key_values
-        if cache is None or not isinstance(cache, HeteroCache):
-            # No HeteroCache: plain causal attention (through whatever cache
-            # the caller supplied), so the patched class stays usable.
-            if cache is not None:
-                key_states, value_states = cache.update(key_states, value_states, self.layer_idx)
-            out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling)
-            return self.o_proj(out), None
         cos, sin = position_embeddings
         cache_kwargs = {"sin": sin, "cos": cos, "cache_position": cache_position, "attention_mask": attention_mask,
                         "num_key_value_groups": self.num_key_value_groups, "query_states": query_states}
+        if cache is None or not isinstance(cache, HeteroCache):
+            # No HeteroCache: causal attention over whatever the cache returns
+            # (a plain DynamicCache, or a baseline compressor's cache, which
+            # returns its compressed rows; heterocache/llama_model.py:45-94).
+            if cache is not None:
+                key_states, value_states = cache.update(key_states, value_states, self.layer_idx, cache_kwargs)
+            out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling)
+            return self.o_proj(out), None
         # A chunked prefill stays in the prefill branch until the declared
         # prompt is complete, even for a one-token last chunk.
         prefill = query_states.shape[-2] != 1 or cache.prefill_pending(self.layer_idx)

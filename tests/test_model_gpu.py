@@ -127,3 +127,36 @@ def test_chunked_prefill_generation_matches_single_shot(dev):
         whole = model.generate(ids, max_new_tokens=16, do_sample=False)
         chunked = model.generate(ids, max_new_tokens=16, do_sample=False, prefill_chunk_size=256)
     assert torch.equal(whole, chunked)
+
+
+@pytest.mark.parametrize("name", ["snapkv", "pyramidkv", "h2o", "streamingllm"])
+def test_baseline_caches_generate(dev, name):
+    """The baseline compressor caches through generate() on a random Llama:
+    with a ratio that keeps every token the greedy tokens equal the stock
+    model's; with ratio 0.3 each layer holds its compressor's kept rows plus
+    the generated tokens."""
+    from heterocache_amd import cache_utils as C
+    classes = {"snapkv": C.SnapKVCache, "pyramidkv": C.PyramidKVCache, "h2o": C.H2OKVCache,
+               "streamingllm": C.StreamingLLMKVCache}
+    cfg = llama_cfg(layers=2, q_heads=8, kv_heads=2)
+    with utils.install_attention_patch():
+        torch.manual_seed(0)
+        model = LlamaForCausalLM(cfg).to(torch.float32).to(dev).eval()
+    torch.manual_seed(0)
+    ref_model = LlamaForCausalLM(cfg).to(torch.float32).to(dev).eval()
+    ids = torch.randint(0, 512, (1, 400), generator=torch.Generator().manual_seed(7)).to(dev)
+    with torch.no_grad():
+        ref = ref_model.generate(ids, max_new_tokens=8, do_sample=False)
+        keep_all = C.CompressionCacheConfig(window_size=16, compression_ratio=50.0, num_attn_heads=8, num_kv_heads=2,
+                                            num_layers=2)
+        out = model.generate(ids, max_new_tokens=8, do_sample=False, past_key_values=classes[name](keep_all))
+    assert torch.equal(out, ref)
+    cache = classes[name](C.CompressionCacheConfig(window_size=16, compression_ratio=0.3, num_attn_heads=8,
+                                                   num_kv_heads=2, num_layers=2))
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=8, do_sample=False, past_key_values=cache)
+    assert out.shape == (1, 408)
+    for layer in range(2):
+        n = cache.key_cache[layer].shape[2]
+        assert cache.key_cache[layer].shape[1] == 8           # repeated per query head
+        assert n < 400 and n > 7                              # compressed, then 7 appended tokens
