@@ -57,6 +57,10 @@ SIGNATURES = {
                          c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p,
                          c_void_p, c_size_t, c_void_p]),
     "hc_score_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "hc_cake_score": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int, c_int,
+                              c_int, c_int, c_int, c_int, c_float, c_float, c_void_p, c_void_p, c_void_p, c_size_t,
+                              c_void_p]),
+    "hc_cake_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "hc_select_topk": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int, c_void_p, c_int64, c_void_p,
                                c_void_p, c_size_t, c_void_p, c_size_t, c_void_p]),
     "hc_select_hist_size": (c_size_t, [c_int]),

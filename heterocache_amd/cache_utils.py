@@ -785,6 +785,9 @@ class BaseKVCache(DynamicCache):
     appended; update returns the layer's whole cache, which the model's own
     attention reads (hc_prefill_attn through the patched attention class)."""
 
+    # Compressors of this family take K/V repeated per query head.
+    repeat_kv_heads = True
+
     def __init__(self):
         super().__init__()
         self._seen_tokens = 0
@@ -820,7 +823,7 @@ class BaseKVCache(DynamicCache):
         update_global = cache_kwargs.get("update_global_past_kv", True)
         query_states = cache_kwargs["query_states"]
         groups = cache_kwargs["num_key_value_groups"]
-        if key_states.size(1) != query_states.size(1):
+        if self.repeat_kv_heads and key_states.size(1) != query_states.size(1):
             key_states = _repeat_kv(key_states, groups)
             value_states = _repeat_kv(value_states, groups)
         if layer_idx == 0:
@@ -913,3 +916,36 @@ class StreamingLLMKVCache(SnapKVCache):
         from .kv_cluster import StreamingLLMKVCluster
         cfg = {"window_size": self.window_size, "compression_ratio": self.compression_ratio}
         return ",".join(["streamingllm"] + [str(v) for v in cfg.values()]), StreamingLLMKVCluster, cfg
+
+
+class CAKECache(BaseKVCache):
+    """heterocache/cache_utils.py:277-373: the prompt K/V of each layer (one
+    row per KV head, not repeated) enter the cache whole, then CAKECluster
+    scores the layer and evicts every layer seen so far to its budget."""
+
+    repeat_kv_heads = False
+
+    def __init__(self, config):
+        super().__init__()
+        self.window_size = config.window_size
+        self.compression_ratio = config.compression_ratio
+        self.kernel_size = config.kernel_size
+        self.pooling = config.pooling
+        self.pref_scores = []
+        self.evict_scores = []
+        self.layer_budget = []
+        self.num_layers = config.num_layers
+
+    def compressed_kv(self, key_states, query_states, value_states, attention_mask, num_key_value_groups, layer_idx):
+        if self.kv_cluster_granularity != "layer":
+            raise AssertionError(f"kv_cluster_granularity {self.kv_cluster_granularity} not supported")
+        cluster = self.get_kv_cluster_class(layer_idx)
+        self.key_cache.append(key_states)
+        self.value_cache.append(value_states)
+        cluster.update_kv(self, key_states, query_states, value_states, attention_mask, num_key_value_groups)
+
+    def get_kv_cluster_class_config(self, layer_idx: int, head_idx: int = None):
+        from .kv_cluster import CAKECluster
+        cfg = {"window_size": self.window_size, "compression_ratio": self.compression_ratio,
+               "kernel_size": self.kernel_size, "pooling": self.pooling}
+        return ",".join(["cake"] + [str(v) for v in cfg.values()]), CAKECluster, cfg

@@ -8,6 +8,8 @@ reference's operations:
   window_scores       SnapKV observation-window scores
                       (heterocache/kv_cluster.py:165-185), generalised to a
                       GQA group (max over the group)
+  cake_scores         CAKE mean + gamma * variance scores with the layer's
+                      entropy and variance sums (heterocache/kv_cluster.py:284-315)
   pivot_step_scores   buffered decode queries vs a pivot's prefill keys read
                       in place from the store (heterocache/cache_utils.py:1030-1057)
   select_kept         per-head budget top-k in ascending order
@@ -64,6 +66,32 @@ def window_scores(q, k, kv_heads, group, window, pooling="avgpool", kernel=5, wi
     out = ops.score(q, _dev_i64(q_off, q.device), q.stride(1), q.stride(2), k, _dev_i64(k_off, q.device), k.stride(2),
                     L, group, window, span, pooling, kernel, scale, flags=flags, stream=stream)
     return out.view(len(q_off), span)
+
+
+def cake_scores(q, k, window, gamma=200.0, round_dtype=None, scale=None, stream=None):
+    """CAKE heavy-hitter scores [B * Hkv, L - window] and the device triple
+    (entropy, variance sum, preference) of one layer
+    (heterocache/kv_cluster.py:284-315).
+
+    q: [B, Hq, Lq, 128] (the last `window` positions are the observation
+    window); k: [B, Hkv, L, 128], not repeated: query heads h*G .. h*G+G-1
+    score kv head h.
+    """
+    _check_qk(q, k)
+    B, Hq, Lq, _ = q.shape
+    Hkv, L = k.shape[1], k.shape[2]
+    if Hq % Hkv:
+        raise ValueError(f"{Hq} query heads do not group over {Hkv} kv heads")
+    if window > Lq:
+        raise ValueError("window longer than the query sequence")
+    group = Hq // Hkv
+    scale = 1.0 / math.sqrt(128) if scale is None else scale
+    q_off = [b * q.stride(0) + h * group * q.stride(1) + (Lq - window) * q.stride(2)
+             for b in range(B) for h in range(Hkv)]
+    k_off = [b * k.stride(0) + h * k.stride(1) for b in range(B) for h in range(Hkv)]
+    return ops.cake_score(q, _dev_i64(q_off, q.device), q.stride(1), q.stride(2), k, _dev_i64(k_off, q.device),
+                          k.stride(2), B, Hkv, L, group, window, scale, gamma, flags=ROUND_FLAGS[round_dtype],
+                          stream=stream)
 
 
 def last_query_scores(q, k, kv_heads, group, pooling="avgpool", kernel=5, round_dtype=None, scale=None, stream=None):

@@ -24,6 +24,7 @@
 //     A[job][w'][g][t].
 //  4. score_pool_kernel: pooling over t and max over g -> S[job][w'][t].
 #include <cfloat>
+#include <cmath>
 #include <type_traits>
 
 #include "hc_common.h"
@@ -291,9 +292,13 @@ __device__ __forceinline__ void subtile_logits_rows(const ScoreArgs& a, const ty
   for (int j = 0; j < 4; ++j) x[j] = (!MASK || t <= limit[j]) ? scaled_logit<RM>(a, acc[j]) : -INFINITY;
 }
 
-template <typename T, bool STORE, int RM>
+// MOM (CAKE scoring, W a multiple of 16): besides the window sum A, write
+// the window sum of squares A2 unrounded and one partial of
+// sum p*log(p + 1e-10) over t < span per (job, chunk) into ent.
+template <typename T, bool STORE, int RM, bool MOM>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs a, const float* __restrict__ stats,
-                                                                      float* __restrict__ A) {
+                                                                      float* __restrict__ A, float* __restrict__ A2,
+                                                                      float* __restrict__ ent) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_q = reinterpret_cast<T*>(smem);
   const int rows = a.NT * 16;
@@ -321,9 +326,10 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
 #pragma unroll
   for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, krs[u]);
   __syncthreads();
-  float gsum[kSubTiles];  // running window sum per sub-tile (W >= 16)
+  float gsum[kSubTiles], gsq[kSubTiles];  // running window sum (and sum of squares) per sub-tile (W >= 16)
 #pragma unroll
-  for (int u = 0; u < kSubTiles; ++u) gsum[u] = 0.f;
+  for (int u = 0; u < kSubTiles; ++u) gsum[u] = gsq[u] = 0.f;
+  float ent_acc = 0.f;
   const int min_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W : a.L - 1;
   const bool need_mask = chunk * kScoreChunk + kScoreChunk - 1 > min_limit;
   auto body = [&](auto mask_tag) {
@@ -354,6 +360,13 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
             else
               p[j] = x[j] == -INFINITY ? 0.f : round_fixed<RM>(fast_exp2(x[j] - M[j]) * IZ[j]);
           }
+          if constexpr (MOM) {
+            // Padding rows have p = 0 and add 0 * log(1e-10) = 0.
+            if (t < a.span) {
+  #pragma unroll
+              for (int j = 0; j < 4; ++j) ent_acc += p[j] * __logf(p[j] + 1e-10f);
+            }
+          }
           if (!sum_w) {
             // Row r = g*W + w -> A[job][w][g][t].
   #pragma unroll
@@ -364,12 +377,25 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
             // lane sums its 4 rows over the head's tiles, and the 4 lane
             // groups are combined once per head.
             gsum[u] += (p[0] + p[1]) + (p[2] + p[3]);
+            if constexpr (MOM) gsq[u] += (p[0] * p[0] + p[1] * p[1]) + (p[2] * p[2] + p[3] * p[3]);
             if (((16 * (nt + 1)) % a.W) == 0) {
               float v = gsum[u];
               v += __shfl_xor(v, 16, 64);
               v += __shfl_xor(v, 32, 64);
               const int g = (16 * nt) / a.W;
-              if (rg == 0 && g < a.G && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_fixed<RM>(v);
+              const int64_t o = ((int64_t)job * a.G + g) * a.span + t;
+              if constexpr (MOM) {
+                float v2 = gsq[u];
+                v2 += __shfl_xor(v2, 16, 64);
+                v2 += __shfl_xor(v2, 32, 64);
+                if (rg == 0 && g < a.G && t < a.span) {
+                  A[o] = v;
+                  A2[o] = v2;
+                }
+                gsq[u] = 0.f;
+              } else {
+                if (rg == 0 && g < a.G && t < a.span) A[o] = round_fixed<RM>(v);
+              }
               gsum[u] = 0.f;
             }
           } else if (a.W == 8) {
@@ -399,6 +425,14 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
     body(std::true_type{});
   else
     body(std::false_type{});
+  if constexpr (MOM) {
+    __shared__ float s_ent[kScoreWaves];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ent_acc += __shfl_xor(ent_acc, off, 64);
+    if (lane == 0) s_ent[wave] = ent_acc;
+    __syncthreads();
+    if (threadIdx.x == 0) ent[(int64_t)job * gridDim.x + chunk] = (s_ent[0] + s_ent[1]) + (s_ent[2] + s_ent[3]);
+  }
 }
 
 // 256 consecutive positions of one (job, w') per workgroup; each query
@@ -613,8 +647,8 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   const int nchunks_span = (a.span + kScoreChunk - 1) / kScoreChunk;
   if (nchunks_span > 0) {
 #define HC_PROBS(RM)                                                                                        \
-  hipLaunchKernelGGL((score_probs_kernel<T, STORE, RM>), dim3(nchunks_span, njobs), dim3(kScoreWaves * 64), lds3, s, \
-                     a, stats, A)
+  hipLaunchKernelGGL((score_probs_kernel<T, STORE, RM, false>), dim3(nchunks_span, njobs), dim3(kScoreWaves * 64), \
+                     lds3, s, a, stats, A, nullptr, nullptr)
     if (rm == 0) HC_PROBS(0); else if (rm == 1) HC_PROBS(1); else HC_PROBS(2);
 #undef HC_PROBS
     if ((rc = check_launch("hc_score(probs)"))) return rc;
@@ -623,6 +657,162 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
     if ((rc = check_launch("hc_score(pool)"))) return rc;
   }
   return HC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// CAKE layer scoring (heterocache/kv_cluster.py:284-315).  From the window
+// sum s1 and sum of squares s2 of the cast probabilities of one query head:
+//   mean = s1 / W, var = unbiased variance over the W rows,
+//   hh   = max_g avg_pool5(round(round(mean) + round(gamma * round(var)))),
+//   entropy = -sum p log(p + 1e-10) and the variance sum over t < span,
+// with the reference's casts (round) when its model dtype is 16-bit.
+// ---------------------------------------------------------------------------
+constexpr int kCakeThreads = 256;
+constexpr int kCakeHalf = 2;  // avg_pool1d(kernel_size=5, padding=2), kv_cluster.py:309
+
+template <int RM>
+__device__ __forceinline__ float cake_var(float s1, float s2, int W) {
+  return round_fixed<RM>(fmaxf(s2 - s1 * (s1 * (1.f / (float)W)), 0.f) / (float)(W - 1));
+}
+
+template <int RM>
+__device__ __forceinline__ float cake_score(float s1, float s2, int W, float gamma) {
+  const float mean = round_fixed<RM>(s1 * (1.f / (float)W));
+  return round_fixed<RM>(mean + round_fixed<RM>(gamma * cake_var<RM>(s1, s2, W)));
+}
+
+// hh[job][t]: one workgroup per (job, 256 positions); each query head's
+// scores plus the pooling halo are formed in LDS (zero outside [0, span)).
+template <int RM>
+__global__ __launch_bounds__(kCakeThreads) void cake_pool_kernel(const float* __restrict__ A1,
+                                                                 const float* __restrict__ A2, int G, int W, int span,
+                                                                 float gamma, float* __restrict__ S) {
+  __shared__ float s_a[kCakeThreads + 2 * kCakeHalf];
+  const int t0 = blockIdx.x * kCakeThreads, t = t0 + threadIdx.x;
+  const int job = blockIdx.y;
+  float best = -INFINITY;
+  for (int g = 0; g < G; ++g) {
+    const int64_t base = ((int64_t)job * G + g) * span;
+    __syncthreads();
+    for (int i = threadIdx.x; i < kCakeThreads + 2 * kCakeHalf; i += kCakeThreads) {
+      const int u = t0 - kCakeHalf + i;
+      s_a[i] = (u >= 0 && u < span) ? cake_score<RM>(A1[base + u], A2[base + u], W, gamma) : 0.f;
+    }
+    __syncthreads();
+    float acc = 0.f;
+#pragma unroll
+    for (int d = 0; d <= 2 * kCakeHalf; ++d) acc += s_a[threadIdx.x + d];
+    best = fmaxf(best, round_fixed<RM>(acc / (float)(2 * kCakeHalf + 1)));
+  }
+  if (t < span) S[(int64_t)job * span + t] = best;
+}
+
+// Variance sum in the reference's order: var[B][H][span].sum(0) (cast),
+// .sum(0) over heads (cast), then over positions; one partial per 256
+// positions.  Query head h of batch b is plane b*heads + h of A1 / A2.
+template <int RM>
+__global__ __launch_bounds__(kCakeThreads) void cake_varsum_kernel(const float* __restrict__ A1,
+                                                                   const float* __restrict__ A2, int batch, int heads,
+                                                                   int W, int span, float* __restrict__ part) {
+  __shared__ float s_p[kCakeThreads / 64];
+  const int t = blockIdx.x * kCakeThreads + threadIdx.x;
+  float y = 0.f;
+  if (t < span) {
+    for (int h = 0; h < heads; ++h) {
+      float x = 0.f;
+      for (int b = 0; b < batch; ++b) {
+        const int64_t o = ((int64_t)b * heads + h) * span + t;
+        x += cake_var<RM>(A1[o], A2[o], W);
+      }
+      y += round_fixed<RM>(x);
+    }
+    y = round_fixed<RM>(y);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) y += __shfl_xor(y, off, 64);
+  if ((threadIdx.x & 63) == 0) s_p[threadIdx.x >> 6] = y;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = (s_p[0] + s_p[1]) + (s_p[2] + s_p[3]);
+}
+
+// out = {entropy, variance sum, preference}; preference = entropy * variance
+// sum, or 0 when either is NaN (kv_cluster.py:297-303, tau1 = tau2 = 1).
+template <int RM>
+__global__ __launch_bounds__(kCakeThreads) void cake_final_kernel(const float* __restrict__ ent, int n_ent,
+                                                                  const float* __restrict__ part, int n_part,
+                                                                  float* __restrict__ out) {
+  __shared__ float s_e[kCakeThreads / 64], s_v[kCakeThreads / 64];
+  float e = 0.f, v = 0.f;
+  for (int i = threadIdx.x; i < n_ent; i += kCakeThreads) e += ent[i];
+  for (int i = threadIdx.x; i < n_part; i += kCakeThreads) v += part[i];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    e += __shfl_xor(e, off, 64);
+    v += __shfl_xor(v, off, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    s_e[threadIdx.x >> 6] = e;
+    s_v[threadIdx.x >> 6] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float disp = -((s_e[0] + s_e[1]) + (s_e[2] + s_e[3]));
+    const float var = round_fixed<RM>((s_v[0] + s_v[1]) + (s_v[2] + s_v[3]));
+    out[0] = disp;
+    out[1] = var;
+    out[2] = (isnan(disp) || isnan(var)) ? 0.f : disp * var;
+  }
+}
+
+size_t cake_workspace_bytes(int njobs, int L, int G, int W) {
+  const int R = G * W;
+  const size_t nchunks = (L + kScoreChunk - 1) / kScoreChunk;
+  const size_t span = L - W, nspan = (span + kScoreChunk - 1) / kScoreChunk;
+  return align256(njobs * nchunks * R * 2 * sizeof(float)) + align256((size_t)njobs * R * 2 * sizeof(float)) +
+         2 * align256((size_t)njobs * G * span * sizeof(float)) + align256(njobs * nspan * sizeof(float)) +
+         align256(nspan * sizeof(float));
+}
+
+template <typename T, int RM>
+static int launch_cake(ScoreArgs a, int njobs, int batch, int heads, float gamma, float* scores, float* out, void* ws,
+                       hipStream_t s) {
+  const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
+  const int nspan = (a.span + kScoreChunk - 1) / kScoreChunk;
+  char* w = reinterpret_cast<char*>(ws);
+  float* part = reinterpret_cast<float*>(w);
+  w += align256((size_t)njobs * nchunks * a.R * 2 * sizeof(float));
+  float* stats = reinterpret_cast<float*>(w);
+  w += align256((size_t)njobs * a.R * 2 * sizeof(float));
+  float* A1 = reinterpret_cast<float*>(w);
+  w += align256((size_t)njobs * a.G * a.span * sizeof(float));
+  float* A2 = reinterpret_cast<float*>(w);
+  w += align256((size_t)njobs * a.G * a.span * sizeof(float));
+  float* ent = reinterpret_cast<float*>(w);
+  w += align256((size_t)njobs * nspan * sizeof(float));
+  float* vpart = reinterpret_cast<float*>(w);
+  const size_t qbytes = (size_t)a.NT * 16 * kQPitch * sizeof(T);
+  const size_t lds1 = qbytes + (size_t)kScoreWaves * a.NT * 16 * 2 * sizeof(float);
+  const size_t lds3 = qbytes + (size_t)a.NT * 16 * 2 * sizeof(float);
+  int rc;
+  hipLaunchKernelGGL((score_stats_kernel<T, false, RM, false>), dim3(nchunks, njobs), dim3(kScoreWaves * 64), lds1, s,
+                     a, part, nullptr);
+  if ((rc = check_launch("hc_cake_score(stats)"))) return rc;
+  hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nchunks, a.R,
+                     njobs, stats);
+  if ((rc = check_launch("hc_cake_score(merge)"))) return rc;
+  hipLaunchKernelGGL((score_probs_kernel<T, false, RM, true>), dim3(nspan, njobs), dim3(kScoreWaves * 64), lds3, s, a,
+                     stats, A1, A2, ent);
+  if ((rc = check_launch("hc_cake_score(probs)"))) return rc;
+  hipLaunchKernelGGL((cake_pool_kernel<RM>), dim3((a.span + kCakeThreads - 1) / kCakeThreads, njobs),
+                     dim3(kCakeThreads), 0, s, A1, A2, a.G, a.W, a.span, gamma, scores);
+  if ((rc = check_launch("hc_cake_score(pool)"))) return rc;
+  const int nvar = (a.span + kCakeThreads - 1) / kCakeThreads;
+  hipLaunchKernelGGL((cake_varsum_kernel<RM>), dim3(nvar), dim3(kCakeThreads), 0, s, A1, A2, batch, heads, a.W,
+                     a.span, vpart);
+  if ((rc = check_launch("hc_cake_score(varsum)"))) return rc;
+  hipLaunchKernelGGL((cake_final_kernel<RM>), dim3(1), dim3(kCakeThreads), 0, s, ent, njobs * nspan, vpart, nvar,
+                     out);
+  return check_launch("hc_cake_score(final)");
 }
 
 }  // namespace hc
@@ -699,4 +889,74 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
       return set_error(HC_ERR_INVALID, "hc_score: unknown dtype %d", dtype);
   }
 #undef HC_SCORE_DISPATCH
+}
+
+extern "C" size_t hc_cake_workspace_size(int batch, int kv_heads, int seq_len, int group, int window) {
+  if (batch <= 0 || kv_heads <= 0 || group <= 0 || window <= 0 || seq_len <= window) return 0;
+  return cake_workspace_bytes(batch * kv_heads, seq_len, group, window);
+}
+
+extern "C" int hc_cake_score(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride,
+                             int64_t q_row_stride, const void* k, const int64_t* k_off, int64_t k_tok_stride,
+                             int batch, int kv_heads, int seq_len, int group, int window, int flags, float scale,
+                             float gamma, float* scores, float* stats_out, void* workspace, size_t workspace_bytes,
+                             void* stream) {
+  clear_error();
+  if (batch < 1 || kv_heads < 1 || group < 1 || (int64_t)batch * kv_heads > 65535)
+    return set_error(HC_ERR_INVALID, "hc_cake_score: batch=%d kv_heads=%d group=%d", batch, kv_heads, group);
+  if (window < 16 || (window % 16) != 0)
+    return set_error(HC_ERR_INVALID, "hc_cake_score: the window must be a positive multiple of 16 (got %d)", window);
+  if (seq_len <= window)
+    return set_error(HC_ERR_INVALID, "hc_cake_score: seq_len %d must exceed the window %d", seq_len, window);
+  if ((flags & ~(HC_SCORE_ROUND_BF16 | HC_SCORE_ROUND_F16)) != 0 ||
+      (flags & (HC_SCORE_ROUND_BF16 | HC_SCORE_ROUND_F16)) == (HC_SCORE_ROUND_BF16 | HC_SCORE_ROUND_F16))
+    return set_error(HC_ERR_INVALID, "hc_cake_score: flags 0x%x (only one rounding flag is accepted)", flags);
+  if (!(scale > 0.f) || !std::isfinite(gamma))
+    return set_error(HC_ERR_INVALID, "hc_cake_score: scale %g, gamma %g", (double)scale, (double)gamma);
+  const int R = group * window;
+  const int NT = (R + 15) / 16;
+  if (NT > 16) return set_error(HC_ERR_INVALID, "hc_cake_score: group*window = %d exceeds 256 rows", R);
+  if (dtype == HC_DTYPE_F32 && NT > 8)
+    return set_error(HC_ERR_INVALID, "hc_cake_score: float32 supports group*window <= 128 (got %d)", R);
+  if (!q || !q_off || !k || !k_off || !scores || !stats_out || !workspace)
+    return set_error(HC_ERR_INVALID, "hc_cake_score: null pointer argument");
+  if (k_tok_stride < HC_HEAD_DIM || (k_tok_stride % 8) != 0)
+    return set_error(HC_ERR_INVALID, "hc_cake_score: key token stride %lld", (long long)k_tok_stride);
+  const int njobs = batch * kv_heads;
+  if (workspace_bytes < cake_workspace_bytes(njobs, seq_len, group, window))
+    return set_error(HC_ERR_INVALID, "hc_cake_score: workspace too small");
+  ScoreArgs a;
+  a.q = q;
+  a.q_off = q_off;
+  a.q_head_stride = q_head_stride;
+  a.q_row_stride = q_row_stride;
+  a.k = k;
+  a.k_off = k_off;
+  a.k_tok_stride = k_tok_stride;
+  a.row_tile_off = nullptr;
+  a.k_row = nullptr;
+  a.L = seq_len;
+  a.G = group;
+  a.W = window;
+  a.R = R;
+  a.NT = NT;
+  a.flags = flags | HC_SCORE_CAUSAL_WINDOW | HC_SCORE_SUM_WINDOW;
+  a.span = seq_len - window;
+  a.scale = scale;
+  a.scale2 = scale * 1.4426950408889634f;
+  hipStream_t s = (hipStream_t)stream;
+  const int rm = (flags & HC_SCORE_ROUND_BF16) ? 1 : (flags & HC_SCORE_ROUND_F16) ? 2 : 0;
+  const int heads = kv_heads * group;
+#define HC_CAKE_DISPATCH(T)                                                                          \
+  return rm == 0   ? launch_cake<T, 0>(a, njobs, batch, heads, gamma, scores, stats_out, workspace, s) \
+         : rm == 1 ? launch_cake<T, 1>(a, njobs, batch, heads, gamma, scores, stats_out, workspace, s) \
+                   : launch_cake<T, 2>(a, njobs, batch, heads, gamma, scores, stats_out, workspace, s);
+  switch (dtype) {
+    case HC_DTYPE_BF16: { HC_CAKE_DISPATCH(__bf16) }
+    case HC_DTYPE_F16: { HC_CAKE_DISPATCH(_Float16) }
+    case HC_DTYPE_F32: { HC_CAKE_DISPATCH(float) }
+    default:
+      return set_error(HC_ERR_INVALID, "hc_cake_score: unknown dtype %d", dtype);
+  }
+#undef HC_CAKE_DISPATCH
 }

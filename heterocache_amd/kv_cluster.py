@@ -14,10 +14,11 @@ ascending position order, the order a causal cache holds them in.  Attention
 over the result is the same, as it does not depend on key order; the kept
 position sets are identical (tests compare sets and rows).
 
-CAKECluster (heterocache/kv_cluster.py:201-379) is not provided: its
-cross-layer budget re-allocation evicts from every earlier layer's cache at
-each layer and needs entropy and variance reductions of the window
-probabilities, a different scorer.
+CAKECluster keeps the reference's calling convention, which differs from
+the others: update_kv takes the cache first, scores the layer with
+hc_cake_score (keys not repeated: a kv head's query group is scored
+against it directly) and evicts every layer scored so far to its share of
+the total budget, in place in the cache.
 """
 import math
 
@@ -228,3 +229,123 @@ class StreamingLLMKVCluster:
         keep = np.concatenate([np.arange(self.sink_token), np.arange(q_len - recent, q_len)]).astype(np.int32)
         idx = torch.as_tensor(np.tile(keep, (B * H, 1))).to(key_states.device)
         return ops.gather_rows(key_states, value_states, idx, len(keep))
+
+
+class CAKECluster:
+    """heterocache/kv_cluster.py:201-379: layer budgets in proportion to a
+    preference score (entropy times variance of the window's attention), and
+    per-layer eviction by mean + gamma * variance of the window attention.
+
+    Each layer's prompt is scored once (hc_cake_score: heavy-hitter scores,
+    entropy, variance sum); after layer l the total budget
+    (capacity - window) * num_layers is split over layers 0..l and every one
+    of them is evicted to its share (hc_select_topk over its current scores,
+    hc_gather_rows of its cached rows).  Kept rows stay in position order.
+    """
+
+    def __init__(self, window_size=64, compression_ratio=0.5, kernel_size=5, pooling="avgpool", round_scores=True):
+        self.window_size = window_size
+        self.compression_ratio = compression_ratio
+        self.kernel_size = kernel_size
+        self.pooling = pooling
+        self.round_scores = round_scores
+        self.tau1 = 1
+        self.tau2 = 1
+        self.gamma = 200.0
+
+    def reset(self, window_size=64, max_capacity_prompt=256 + 64, kernel_size=5, pooling="avgpool"):
+        self.window_size = window_size
+        self.max_capacity_prompt = max_capacity_prompt
+        assert self.max_capacity_prompt - self.window_size > 0
+        self.kernel_size = kernel_size
+        self.pooling = pooling
+
+    def adjust_budgets(self, budget_list, total_budget, seq_len, layer_nums):
+        """Integer layer budgets (heterocache/kv_cluster.py:225-271): truncate,
+        clip at seq_len and spread the clipped excess evenly over the layers
+        below seq_len (remainder one each to the first of them); then spread
+        the difference to total_budget the same way, adding over the layers
+        below seq_len or taking from the layers above 1."""
+        budgets = [int(x) for x in budget_list]
+
+        def spread(amount, members, sign):
+            per, rem = divmod(amount, len(members))
+            for n, i in enumerate(members):
+                budgets[i] += sign * (per + (1 if n < rem else 0))
+
+        excess = sum(max(x - seq_len, 0) for x in budgets)
+        budgets = [min(x, seq_len) for x in budgets]
+        below = [i for i, x in enumerate(budgets) if x < seq_len]
+        if excess > 0 and below:
+            spread(excess, below, 1)
+        diff = total_budget - sum(budgets)
+        if diff > 0:
+            members = [i for i, x in enumerate(budgets) if x < seq_len]
+        else:
+            members = [i for i, x in enumerate(budgets) if x > 1]
+        if diff != 0 and members:
+            spread(abs(diff), members, 1 if diff > 0 else -1)
+        return budgets
+
+    def preference(self, entropy, variance):
+        """entropy**(1/tau1) * variance**(1/tau2) in float32, 0 when either
+        is NaN (heterocache/kv_cluster.py:305-313)."""
+        entropy, variance = np.float32(entropy), np.float32(variance)
+        if np.isnan(entropy) or np.isnan(variance):
+            return np.float32(0.0)
+        return np.float32(entropy ** np.float32(1 / self.tau1) * variance ** np.float32(1 / self.tau2))
+
+    def update_kv(self, past_key_values, key_states, query_states, value_states, attention_mask, num_key_value_groups):
+        assert key_states.shape[-2] == query_states.shape[-2]
+        B, H, q_len, D = query_states.shape
+        if not hasattr(self, "max_capacity_prompt"):
+            self.max_capacity_prompt = max(int(self.compression_ratio * q_len), 2)
+            self.total_size = (self.max_capacity_prompt - self.window_size) * past_key_values.num_layers
+        if self.max_capacity_prompt > q_len:
+            return key_states, value_states
+        W = self.window_size
+        if self.max_capacity_prompt < W or q_len <= W:
+            raise ValueError(f"capacity {self.max_capacity_prompt} / prompt {q_len} leave no room beside the "
+                             f"window {W}")
+        hh, stats = compress.cake_scores(query_states, key_states, W, gamma=self.gamma,
+                                         round_dtype=_round_dtype(query_states.dtype, self.round_scores))
+        entropy, variance, _ = stats.cpu().numpy()
+        past_key_values.pref_scores.append(self.preference(entropy, variance))
+        past_key_values.evict_scores.append(hh.view(B, key_states.shape[1], q_len - W))
+        past_key_values.layer_budget.append(self.max_capacity_prompt - W)
+        prefs = past_key_values.pref_scores
+        total_pref = sum(prefs)
+        if total_pref == 0:
+            # Every preference is 0 (NaN statistics): the reference divides
+            # 0 by 0; split the total evenly instead.
+            shares = [np.float32(self.total_size / len(prefs))] * len(prefs)
+        else:
+            shares = [p / total_pref * self.total_size for p in prefs]
+        budgets = self.adjust_budgets(shares, self.total_size, q_len - W, past_key_values.num_layers)
+        for layer_idx, budget in enumerate(budgets):
+            budget = min(budget, q_len - W)
+            self.evcit_layer_kvcache(past_key_values, layer_idx, budget)
+            past_key_values.layer_budget[layer_idx] = budget
+
+    def evcit_layer_kvcache(self, past_key_values, layer_idx, budget):
+        """Keep the top `budget` rows of the layer by its current scores
+        plus the window (heterocache/kv_cluster.py:351-379; the name is the
+        reference's)."""
+        scores = past_key_values.evict_scores[layer_idx]
+        B, Hkv, n = scores.shape
+        budget = min(budget, n)
+        if budget < 0:
+            raise ValueError(f"negative budget {budget} for layer {layer_idx}")
+        if budget == n:
+            return past_key_values
+        W = self.window_size
+        flat = scores.reshape(B * Hkv, n)
+        idx, counts = compress.select_kept(flat, [budget + W] * (B * Hkv), window=W, max_cap=budget + W)
+        k, v = ops.gather_rows(past_key_values.key_cache[layer_idx], past_key_values.value_cache[layer_idx], idx,
+                               counts)
+        past_key_values.key_cache[layer_idx] = k
+        past_key_values.value_cache[layer_idx] = v
+        past_key_values.evict_scores[layer_idx] = torch.gather(flat, 1, idx[:, :budget].long()).view(B, Hkv, budget)
+        return past_key_values
+
+    evict_layer_kvcache = evcit_layer_kvcache

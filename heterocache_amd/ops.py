@@ -366,6 +366,35 @@ def score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, seq_len
     return out
 
 
+def cake_score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, batch, kv_heads, seq_len, group,
+               window, scale, gamma, flags=0, out=None, stats=None, stream=None):
+    """CAKE scores [batch * kv_heads, seq_len - window] and the float32 device
+    triple (entropy, variance sum, preference) (see hc_cake_score in
+    include/hc.h).  q_off / k_off: int64 device tensors of per-job offsets."""
+    lib = _lib.load()
+    _require_cuda(q, k, q_off, k_off)
+    if q.dtype != k.dtype:
+        raise TypeError("q and k must share a dtype")
+    if q_off.dtype != torch.int64 or k_off.dtype != torch.int64:
+        raise TypeError("offsets must be int64")
+    njobs, span = batch * kv_heads, seq_len - window
+    if q_off.numel() != njobs or k_off.numel() != njobs:
+        raise ValueError(f"expected {njobs} job offsets")
+    if out is None:
+        out = torch.empty((njobs, max(span, 0)), dtype=torch.float32, device=q.device)
+    elif out.dtype != torch.float32 or out.numel() < njobs * span or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float32 tensor of [jobs, span]")
+    if stats is None:
+        stats = torch.empty(3, dtype=torch.float32, device=q.device)
+    nbytes = lib.hc_cake_workspace_size(batch, kv_heads, seq_len, group, window)
+    ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
+    _lib.check(lib.hc_cake_score(dtype_code(q.dtype), _ptr(q), _ptr(q_off), int(q_head_stride), int(q_row_stride),
+                                 _ptr(k), _ptr(k_off), int(k_tok_stride), int(batch), int(kv_heads), int(seq_len),
+                                 int(group), int(window), int(flags), float(scale), float(gamma), _ptr(out),
+                                 _ptr(stats), _ptr(ws), ws.numel(), _stream(stream, q)))
+    return out, stats
+
+
 def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None):
     """Ascending kept positions per job: scores [jobs, >= span] float32, caps int32 [jobs]."""
     lib = _lib.load()

@@ -212,6 +212,31 @@ int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stri
 size_t hc_score_workspace_size(int njobs, int seq_len, int group, int window, int flags);
 
 /*
+ * CAKE layer scoring, CAKECluster.update_kv (heterocache/kv_cluster.py:284-315).
+ * Job j = b*kv_heads + h holds query heads h*group .. h*group+group-1; query
+ * row (g, w) is q + q_off[j] + g*q_head_stride + w*q_row_stride, w < window
+ * (the last `window` positions), and key t is k + k_off[j] + t*k_tok_stride.
+ * p = softmax over the seq_len keys of scale * q.k with the window causally
+ * masked (row w sees t <= seq_len - window + w), cast to the model dtype
+ * under HC_SCORE_ROUND_BF16 / _F16 (the only flags accepted).  Over the
+ * positions t < span = seq_len - window:
+ *   scores[j][t] = max_g avg_pool1d_5(mean_w p + gamma * var_w p)
+ *     (unbiased variance over the window rows; casts where the reference
+ *     casts: mean, var, gamma*var, their sum, the pooled value);
+ *   stats_out[0] = -sum p log(p + 1e-10) over every row and t < span;
+ *   stats_out[1] = sum of var_w p over batch, then heads, then t (cast after
+ *     each stage, as var.sum(0).sum(0).sum(0));
+ *   stats_out[2] = stats_out[0] * stats_out[1], or 0 when either is NaN.
+ * window: a positive multiple of 16 below seq_len; group*window <= 256
+ * (<= 128 for float32).  stats_out: 3 floats in device memory.
+ */
+int hc_cake_score(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride, int64_t q_row_stride,
+                  const void* k, const int64_t* k_off, int64_t k_tok_stride, int batch, int kv_heads, int seq_len,
+                  int group, int window, int flags, float scale, float gamma, float* scores, float* stats_out,
+                  void* workspace, size_t workspace_bytes, void* stream);
+size_t hc_cake_workspace_size(int batch, int kv_heads, int seq_len, int group, int window);
+
+/*
  * Per-job top-k kept set in ascending position order.  Job j keeps the
  * cap[j] positions of scores[j*score_stride + t], t < span, ranked by (score
  * descending, position ascending); with window > 0 it keeps cap[j] - window of

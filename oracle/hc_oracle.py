@@ -26,6 +26,14 @@ Pinning of each function (beyond its own formula) -- tests/test_oracle.py:
   retrieval_indices               ascending-prefix rule on a hand example.
   reorder_plan                    the committed Llama-3.1-8B head JSON, layer
       23 (leader order quirk) worked out by hand.
+  cake_layer_scores               at gamma 0 and G = 1, W * hh equals
+      window_scores (SnapKV avgpool-5); uniform keys against closed forms
+      (statistics.variance, the entropy of 1/n rows, zero-padded pooling
+      edges); the group max of two one-head calls.
+  cake_adjust_budgets             hand vectors (clip + spread, truncation,
+      negative difference) and sum == total on random budgets.
+  cake_prefill                    final kept set of every layer = top-(min of
+      its budgets over the prompt) of its own scores; budgets sum to the total.
 """
 import math
 import statistics
@@ -282,6 +290,120 @@ def streamingllm_update_kv(key_states, value_states, compression_ratio, sink=4):
         return key_states, value_states
     keep = np.concatenate([np.arange(sink), np.arange(L - recent, L)])
     return key_states[:, :, keep], value_states[:, :, keep]
+
+
+def cake_layer_scores(query_states, key_states, window, gamma=200.0, io_dtype=None, scale=None):
+    """Scoring of CAKECluster.update_kv for one layer (heterocache/kv_cluster.py:284-315).
+
+    query_states [B, Hq, L, d]; key_states [B, Hkv, L, d], repeated over the
+    query group for the logits (:290-292).  p = softmax_f32 of the last W
+    query rows against all L keys, the window causally masked, cast to
+    io_dtype (:293-303).  Over the positions t < L - W:
+      entropy = -sum p log(p + 1e-10)                       (:220-224, :305)
+      var     = unbiased variance over the W rows (cast); var_sum =
+                var.sum(0) .sum(0) .sum(0), cast after each stage  (:307)
+      pref    = entropy * var_sum, 0.0 when either is NaN   (:308-313)
+      hh      = max over a kv head's query heads of
+                avg_pool5(cast(cast(mean) + cast(gamma * var)))  (:317-324)
+    Returns (hh [B, Hkv, L - W] float32, entropy, var_sum, pref).
+    """
+    q = np.asarray(query_states, dtype=np.float64)
+    k = np.asarray(key_states, dtype=np.float64)
+    B, Hq, L, d = q.shape
+    Hkv = k.shape[1]
+    G, W = Hq // Hkv, window
+    span = L - W
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    logits = np.einsum("bhwd,bhld->bhwl", q[:, :, L - W:], np.repeat(k, G, axis=1))
+    if io_dtype not in (None, "float32"):
+        logits = round_to(round_to(logits, io_dtype) * np.float32(scale), io_dtype).astype(np.float64)
+    else:
+        logits = (logits * scale).astype(np.float32).astype(np.float64)
+    for w in range(W):
+        logits[:, :, w, L - W + w + 1:] = -np.inf
+    p = round_to(softmax_f32(logits), io_dtype)[..., :span]          # float32 values
+    p64 = p.astype(np.float64)
+    entropy = -float(np.sum(p64 * np.log((p + np.float32(1e-10)).astype(np.float64))))
+    mean = round_to(p64.mean(axis=2), io_dtype).astype(np.float64)   # [B, Hq, span]
+    var = round_to(p64.var(axis=2, ddof=1), io_dtype).astype(np.float64)
+    score = round_to(mean + round_to(gamma * var, io_dtype), io_dtype)
+    pooled = round_to(pool1d(score, "avgpool", 5), io_dtype)
+    hh = pooled.reshape(B, Hkv, G, span).max(axis=2)
+    vs = round_to(var.sum(axis=0), io_dtype).astype(np.float64)      # over the batch
+    vs = round_to(vs.sum(axis=0), io_dtype).astype(np.float64)       # over the heads
+    var_sum = float(round_to(vs.sum(), io_dtype).reshape(-1)[0])
+    entropy = float(np.float32(entropy))
+    pref = 0.0 if (math.isnan(entropy) or math.isnan(var_sum)) else float(np.float32(entropy) * np.float32(var_sum))
+    return hh, entropy, var_sum, pref
+
+
+def cake_adjust_budgets(budget_list, total_budget, seq_len):
+    """CAKECluster.adjust_budgets (heterocache/kv_cluster.py:225-271).
+
+    Budgets truncate toward zero and are clipped at seq_len; the clipped
+    excess is spread evenly over the layers still below seq_len (the
+    remainder one each to the first of them).  The difference to
+    total_budget is then spread the same way: added over the layers below
+    seq_len, or taken from the layers above 1.
+    """
+    b = np.array(budget_list, dtype=np.int64)
+    excess = int(np.maximum(b - seq_len, 0).sum())
+    b = np.minimum(b, seq_len)
+    if excess > 0:
+        open_ = np.flatnonzero(b < seq_len)
+        if open_.size:
+            b[open_] += excess // open_.size
+            b[open_[:excess % open_.size]] += 1
+    diff = int(total_budget - b.sum())
+    if diff != 0:
+        open_ = np.flatnonzero(b < seq_len) if diff > 0 else np.flatnonzero(b > 1)
+        if open_.size:
+            step, rem = divmod(abs(diff), open_.size)
+            sign = 1 if diff > 0 else -1
+            b[open_] += sign * step
+            b[open_[:rem]] += sign
+    return [int(x) for x in b]
+
+
+def cake_prefill(layers, compression_ratio, window, num_layers, gamma=200.0, io_dtype=None):
+    """CAKECache + CAKECluster over one prompt, layer by layer
+    (heterocache/kv_cluster.py:273-379, heterocache/cache_utils.py:277-373).
+
+    layers: [(query_states [B, Hq, L, d], key_states [B, Hkv, L, d]), ...] in
+    layer order.  After scoring layer l the total budget
+    (cap - W) * num_layers is split over layers 0..l in proportion to their
+    preference scores (float32, as the reference's numpy values), adjusted,
+    and every layer 0..l is evicted again to its budget: top-k of its
+    current scores (descending, ties to the lower position), window kept.
+    Returns None when the prompt stays whole (cap > L), else
+    (kept, budgets, prefs): kept[l] [B, Hkv, budget_l] int64 positions in
+    the reference's order (window positions L-W.. follow), budgets[l] the
+    final layer_budget entries, prefs the float32 preference scores.
+    """
+    L = layers[0][0].shape[2]
+    W = window
+    cap = max(int(compression_ratio * L), 2)
+    if cap > L:
+        return None
+    total = (cap - W) * num_layers
+    prefs, scores, kept, budgets = [], [], [], []
+    for q, k in layers:
+        hh, _, _, pref = cake_layer_scores(q, k, W, gamma, io_dtype)
+        B, Hkv, span = hh.shape
+        prefs.append(np.float32(pref))
+        scores.append(hh)
+        kept.append(np.broadcast_to(np.arange(span), (B, Hkv, span)).copy())
+        budgets.append(cap - W)
+        tot = sum(prefs)
+        split = cake_adjust_budgets([p / tot * total for p in prefs], total, L - W)
+        for i, bud in enumerate(split):
+            bud = min(bud, L - W)
+            n = min(bud, scores[i].shape[-1])
+            top = np.stack([np.stack([topk_indices(scores[i][b, h], n) for h in range(Hkv)]) for b in range(B)])
+            scores[i] = np.take_along_axis(scores[i], top, axis=-1)
+            kept[i] = np.take_along_axis(kept[i], top, axis=-1)
+            budgets[i] = bud
+    return kept, budgets, prefs
 
 
 def head_topk_sets(attn, num_q_heads, num_kv_heads, max_length, topk, io_dtype=None):

@@ -1,8 +1,8 @@
-"""Baseline compressors (SnapKV, PyramidKV, H2O, StreamingLLM) on the libhc
-kernels vs the oracle's restatements of heterocache/kv_cluster.py.
+"""Baseline compressors (SnapKV, PyramidKV, H2O, StreamingLLM, CAKE) on the
+libhc kernels vs the oracle's restatements of heterocache/kv_cluster.py.
 
 Keys and values arrive repeated per query head, as the reference's callers
-pass them.  Channel 127 of V holds each token's position, so the kept
+pass them (CAKE: one row per KV head, as its cache holds them).  Channel 127 of V holds each token's position, so the kept
 positions are read back from the gathered rows.  Kept sets must equal the
 oracle's except inside the tie band around the budget threshold (float32
 noise, or one bf16 ulp with the reference's casts); gathered rows are exact
@@ -140,3 +140,67 @@ def test_short_prompts_stay_uncompressed(dev):
                kv_cluster.StreamingLLMKVCluster(compression_ratio=2.0)):
         ko, vo = cl.update_kv(k, q, v, None, 1)
         assert ko is k and vo is v
+
+
+@pytest.mark.parametrize("dtype,Hq,Hkv", [(torch.float32, 4, 2), (torch.bfloat16, 4, 2), (torch.bfloat16, 7, 1)])
+def test_cake_scores(dev, dtype, Hq, Hkv):
+    """hc_cake_score vs the oracle: heavy-hitter scores, entropy, variance sum
+    and preference of one layer (keys not repeated; bf16 with the
+    reference's casts: agreement to about one bf16 ulp)."""
+    from heterocache_amd import compress
+    g = torch.Generator().manual_seed(21)
+    B, L, W = 2, 700, 32
+    q = torch.randn(B, Hq, L, 128, generator=g).to(dtype)
+    k = torch.randn(B, Hkv, L, 128, generator=g)
+    k[..., :4] *= 4
+    k = k.to(dtype)
+    io = None if dtype == torch.float32 else "bfloat16"
+    hh, stats = compress.cake_scores(q.to(dev), k.to(dev), W, round_dtype=None if io is None else dtype)
+    ref_hh, ent, var_sum, pref = O.cake_layer_scores(q.float().numpy(), k.float().numpy(), W, io_dtype=io)
+    got = as_np(hh).reshape(B, Hkv, L - W)
+    st = as_np(stats).astype(np.float64)
+    if io is None:
+        np.testing.assert_allclose(got, ref_hh, rtol=1e-4, atol=1e-8)
+        tol = 1e-4
+    else:
+        np.testing.assert_allclose(got, ref_hh, rtol=1.6e-2, atol=1e-6)
+        tol = 1e-2
+    assert st[0] == pytest.approx(ent, rel=tol)
+    assert st[1] == pytest.approx(var_sum, rel=tol)
+    assert st[2] == pytest.approx(pref, rel=2 * tol)
+
+
+def test_cake_cache_prefill_matches_oracle(dev):
+    """Three layers through CAKECache.update: layer budgets equal the
+    oracle's, every layer keeps the oracle's positions (tie band aside) plus
+    the window, in position order, as exact row copies; the prefill
+    attention sees the whole prompt."""
+    from heterocache_amd.cache_utils import CAKECache, CompressionCacheConfig
+    B, Hq, Hkv, L, W, NL, ratio = 1, 4, 2, 600, 32, 3, 0.3
+    cache = CAKECache(CompressionCacheConfig(window_size=W, compression_ratio=ratio, num_attn_heads=Hq,
+                                             num_kv_heads=Hkv, num_layers=NL))
+    layers = []
+    for layer in range(NL):
+        g = torch.Generator().manual_seed(30 + layer)
+        q = torch.randn(B, Hq, L, 128, generator=g)
+        k = torch.randn(B, Hkv, L, 128, generator=g)
+        k[..., :4] *= 4
+        v = torch.randn(B, Hkv, L, 128, generator=g)
+        v[..., 127] = torch.arange(L, dtype=torch.float32)
+        layers.append((q.numpy(), k.numpy()))
+        ko, vo = cache.update(k.to(dev), v.to(dev), layer,
+                              {"query_states": q.to(dev), "num_key_value_groups": Hq // Hkv, "attention_mask": None})
+        assert ko.shape == (B, Hkv, L, 128)
+    kept, budgets, prefs = O.cake_prefill(layers, ratio, W, NL)
+    assert cache.layer_budget == budgets
+    np.testing.assert_allclose(np.array(cache.pref_scores, np.float64), np.array(prefs, np.float64), rtol=1e-3)
+    for layer in range(NL):
+        hh, _, _, _ = O.cake_layer_scores(*layers[layer], W)
+        pos = as_np(cache.value_cache[layer][..., 127]).astype(np.int64)
+        n = kept[layer].shape[-1]
+        assert pos.shape == (B, Hkv, n + W)
+        for h in range(Hkv):
+            got = pos[0, h]
+            np.testing.assert_array_equal(got[n:], np.arange(L - W, L))
+            _check_kept(got[:n], kept[layer][0, h], hh[0, h], n, lambda tau: 1e-4 * abs(tau) + 1e-9)
+            np.testing.assert_array_equal(as_np(cache.key_cache[layer][0, h]), layers[layer][1][0, h][got])

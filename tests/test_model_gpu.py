@@ -160,3 +160,34 @@ def test_baseline_caches_generate(dev, name):
         n = cache.key_cache[layer].shape[2]
         assert cache.key_cache[layer].shape[1] == 8           # repeated per query head
         assert n < 400 and n > 7                              # compressed, then 7 appended tokens
+
+
+def test_cake_cache_generate(dev):
+    """CAKECache through generate(): a ratio that keeps every token gives the
+    stock model's greedy tokens; at ratio 0.3 the layer budgets add up to
+    (int(0.3 L) - W) * layers and each layer holds its kept rows, the
+    window and the generated tokens, one row per KV head."""
+    from heterocache_amd import cache_utils as C
+    cfg = llama_cfg(layers=2, q_heads=8, kv_heads=2)
+    with utils.install_attention_patch():
+        torch.manual_seed(0)
+        model = LlamaForCausalLM(cfg).to(torch.float32).to(dev).eval()
+    torch.manual_seed(0)
+    ref_model = LlamaForCausalLM(cfg).to(torch.float32).to(dev).eval()
+    ids = torch.randint(0, 512, (1, 400), generator=torch.Generator().manual_seed(8)).to(dev)
+
+    def config(ratio):
+        return C.CompressionCacheConfig(window_size=32, compression_ratio=ratio, num_attn_heads=8, num_kv_heads=2,
+                                        num_layers=2)
+    with torch.no_grad():
+        ref = ref_model.generate(ids, max_new_tokens=8, do_sample=False)
+        out = model.generate(ids, max_new_tokens=8, do_sample=False, past_key_values=C.CAKECache(config(50.0)))
+    assert torch.equal(out, ref)
+    cache = C.CAKECache(config(0.3))
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=8, do_sample=False, past_key_values=cache)
+    assert out.shape == (1, 408)
+    assert sum(cache.layer_budget) == (int(0.3 * 400) - 32) * 2
+    for layer in range(2):
+        assert cache.key_cache[layer].shape[1] == 2
+        assert 32 + 7 < cache.key_cache[layer].shape[2] <= cache.layer_budget[layer] + 32 + 7

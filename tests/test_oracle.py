@@ -453,3 +453,101 @@ def test_head_analysis_allocation_and_types():
     vals = [v for row in out["allocation_matrix"] for v in row if v > -0.5]
     assert len(vals) == 4 and abs(np.mean(vals) - 1.0) < 1e-12
     assert out["meta"]["counts"] == {"anchor": 2, "volatile": 2, "pivot": 2, "satellite": 2}
+
+
+# -- CAKE ---------------------------------------------------------------------
+def _cake_inputs(seed, B, Hq, Hkv, L):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, Hq, L, 128)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, L, 128)).astype(np.float32)
+    k[..., :4] *= 4
+    return q, k
+
+
+def test_cake_scores_at_gamma_zero_are_snapkv_window_scores():
+    """Without the variance term, W * hh is SnapKV's pooled window sum."""
+    q, k = _cake_inputs(0, 1, 2, 2, 90)
+    W = 16
+    hh, _, _, _ = O.cake_layer_scores(q, k, W, gamma=0.0)
+    snap = O.window_scores(q[0][:, None, -W:], k[0], "avgpool", 5, window_keep=True)
+    np.testing.assert_allclose(hh[0] * W, snap, rtol=1e-5, atol=1e-8)
+
+
+def test_cake_scores_uniform_keys_closed_form():
+    """Identical keys: window row w spreads 1/n_w over its n_w = L-W+w+1
+    visible keys, so every position t < L-W sees the same W values."""
+    B, Hq, Hkv, L, W, gamma = 2, 4, 2, 100, 16, 200.0
+    q, _ = _cake_inputs(1, B, Hq, Hkv, L)
+    k = np.zeros((B, Hkv, L, 128), dtype=np.float32)
+    hh, ent, var_sum, pref = O.cake_layer_scores(q, k, W, gamma=gamma)
+    vals = [1.0 / (L - W + w + 1) for w in range(W)]
+    var = statistics.variance(vals)          # sample (n - 1) variance
+    score = statistics.fmean(vals) + gamma * var
+    span = L - W
+    expect = np.full(span, score)
+    expect[[0, -1]] *= 3 / 5                 # zero padding of avg_pool1d(5, padding 2)
+    expect[[1, -2]] *= 4 / 5
+    for b in range(B):
+        for h in range(Hkv):
+            np.testing.assert_allclose(hh[b, h], expect, rtol=2e-6)
+    ent_expect = -B * Hq * span * sum(v * math.log(v + 1e-10) for v in vals)
+    assert ent == pytest.approx(ent_expect, rel=1e-5)
+    assert var_sum == pytest.approx(B * Hq * span * var, rel=1e-5)
+    assert pref == pytest.approx(ent_expect * B * Hq * span * var, rel=1e-4)
+
+
+def test_cake_scores_group_max_of_single_heads():
+    q, k = _cake_inputs(2, 1, 2, 1, 70)
+    hh2, _, _, _ = O.cake_layer_scores(q, k, 16)
+    a, _, _, _ = O.cake_layer_scores(q[:, :1], k, 16)
+    b, _, _, _ = O.cake_layer_scores(q[:, 1:], k, 16)
+    np.testing.assert_array_equal(hh2, np.maximum(a, b))
+
+
+@pytest.mark.parametrize("budgets,total,seq_len,expect", [
+    ([10, 50, 40], 100, 45, [13, 45, 42]),      # excess 5 -> 2 each, remainder to the first
+    ([3.9, 3.9, 3.9], 12, 10, [4, 4, 4]),       # truncation, then +1 each
+    ([5.5, 2.2, 4.3], 10, 100, [4, 2, 4]),      # sum 11: one taken from the first layer above 1
+    ([0.5, 0.5], 10, 3, [5, 5]),                # the difference is not clipped again
+])
+def test_cake_adjust_budgets_hand_values(budgets, total, seq_len, expect):
+    assert O.cake_adjust_budgets(budgets, total, seq_len) == expect
+
+
+def test_cake_adjust_budgets_keeps_the_total():
+    rng = np.random.default_rng(3)
+    for _ in range(50):
+        n = int(rng.integers(1, 12))
+        total = int(rng.integers(n, 5000))
+        prefs = rng.random(n).astype(np.float32) + np.float32(1e-3)
+        tot = sum(prefs)
+        out = O.cake_adjust_budgets([p / tot * total for p in prefs], total, 10 ** 6)
+        assert sum(out) == total and min(out) >= 0
+
+
+def test_cake_prefill_nested_eviction():
+    """Each layer ends with the top (final count) positions of its own
+    scores; the final budgets add up to the total."""
+    layers = [_cake_inputs(10 + i, 1, 2, 1, 80) for i in range(3)]
+    W, ratio = 16, 0.5
+    kept, budgets, prefs = O.cake_prefill(layers, ratio, W, 3)
+    total = (int(ratio * 80) - W) * 3
+    assert sum(budgets) == total
+    for (q, k), kl in zip(layers, kept):
+        hh, _, _, _ = O.cake_layer_scores(q, k, W)
+        n = kl.shape[-1]
+        assert set(kl[0, 0].tolist()) == set(O.topk_indices(hh[0, 0], n).tolist())
+    assert O.cake_prefill(layers, 1.5, W, 3) is None
+
+
+def test_cake_cluster_budget_logic_matches_oracle():
+    """The product's integer budget rule (host code) against the oracle's."""
+    from heterocache_amd.kv_cluster import CAKECluster
+    c = CAKECluster()
+    rng = np.random.default_rng(4)
+    for _ in range(200):
+        n = int(rng.integers(1, 40))
+        total = int(rng.integers(0, 20000))
+        seq_len = int(rng.integers(1, 3000))
+        shares = list((rng.random(n) * 2 * total / n).astype(np.float32))
+        assert c.adjust_budgets(shares, total, seq_len, n) == O.cake_adjust_budgets(shares, total, seq_len)
