@@ -379,28 +379,16 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
 
 // Fold the partials of one row for one query slot and kMergeSlice channels;
 // the (row, 0, 0) workgroup also advances row_len after a fused append.
-// kMergeGroups part-groups run in parallel so each thread issues only a few
-// independent loads (the merge is latency-bound, not bandwidth-bound).
+// Thread (group, channel) takes parts group, group + kMergeGroups, ...: its
+// kBatch O and (m, l) loads are issued unconditionally (addresses clamped
+// into the row, values masked after), so they are in flight together, and
+// are folded in registers; the groups' (m, l, o) are combined once through
+// LDS.  The merge is latency-bound, not bandwidth-bound: loads under a
+// per-part branch, or a separate block reduction for the row maximum and
+// sum, each add a dependent round.
 constexpr int kMergeSlice = 16;
 constexpr int kMergeGroups = 16;
 constexpr int kMergeThreads = kMergeSlice * kMergeGroups;
-constexpr int kMergeLdsParts = 2048;
-
-__device__ __forceinline__ float block_reduce(float v, float* s_red, bool is_max) {
-  const int tid = threadIdx.x;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float o = __shfl_xor(v, off, 64);
-    v = is_max ? fmaxf(v, o) : v + o;
-  }
-  if ((tid & 63) == 0) s_red[tid >> 6] = v;
-  __syncthreads();
-  float r = s_red[0];
-#pragma unroll
-  for (int w = 1; w < kMergeThreads / 64; ++w) r = is_max ? fmaxf(r, s_red[w]) : r + s_red[w];
-  __syncthreads();
-  return r;
-}
 
 template <typename T>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
@@ -410,64 +398,72 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   const int row = blockIdx.x, qq = blockIdx.y, d0 = blockIdx.z * kMergeSlice;
   const int tid = threadIdx.x;
   const int p0 = row_info[2 * row], np = row_info[2 * row + 1];
-  __shared__ float s_red[kMergeThreads];
-  __shared__ float s_f[kMergeLdsParts];
+  __shared__ float s_m[kMergeGroups], s_l[kMergeGroups];
+  __shared__ float s_o[kMergeGroups][kMergeSlice];
   T* o = out + ((int64_t)row * G + qq) * HC_HEAD_DIM + d0;
   if (advance && qq == 0 && blockIdx.z == 0 && tid == 0) row_len[row] += 1;
   if (np < 0) {
     if (tid < kMergeSlice) o[tid] = Elem<T>::from_f32(NAN);
     return;
   }
-  const float* ml = part_ml + ((int64_t)p0 * G + qq) * 2;
+  // np >= 1 here: an empty row still has its one (empty) part.
   const int dl = tid % kMergeSlice, grp = tid / kMergeSlice;
+  const float* ml = part_ml + ((int64_t)p0 * G + qq) * 2;
   const float* po = part_o + ((int64_t)p0 * G + qq) * HC_HEAD_DIM + d0 + dl;
   const int64_t pstride = (int64_t)G * HC_HEAD_DIM;
-  // Issue the first batch of partial-output loads before anything depends on
-  // the row maximum, so they overlap the (m, l) loads and reductions.
   float ov[kBatch];
+  float2 mv[kBatch];
 #pragma unroll
   for (int k = 0; k < kBatch; ++k) {
-    const int p = grp + k * kMergeGroups;
-    ov[k] = p < np ? po[p * pstride] : 0.f;
+    const int pc = min(grp + k * kMergeGroups, np - 1);
+    ov[k] = po[pc * pstride];
+    mv[k] = *reinterpret_cast<const float2*>(ml + (int64_t)pc * G * 2);
   }
-  float mv = -INFINITY, lv = 0.f;
-  if (tid < np) {
-    mv = ml[(int64_t)tid * G * 2];
-    lv = ml[(int64_t)tid * G * 2 + 1];
-  }
-  float mx = mv;
-  for (int p = tid + kMergeThreads; p < np; p += kMergeThreads) mx = fmaxf(mx, ml[(int64_t)p * G * 2]);
-  const float M = block_reduce(mx, s_red, true);
-  if (M == -INFINITY) {  // empty row
-    if (tid < kMergeSlice) o[tid] = Elem<T>::from_f32(0.f);
-    return;
-  }
-  float ls = 0.f;
-  if (tid < np) {
-    const float f = fast_exp2(mv - M);
-    ls = lv * f;
-    if (tid < kMergeLdsParts) s_f[tid] = f;
-  }
-  for (int p = tid + kMergeThreads; p < np; p += kMergeThreads) {
-    const float f = fast_exp2(ml[(int64_t)p * G * 2] - M);
-    ls = fmaf(ml[(int64_t)p * G * 2 + 1], f, ls);
-    if (p < kMergeLdsParts) s_f[p] = f;
-  }
-  const float L = block_reduce(ls, s_red, false);  // its barriers also publish s_f
-  auto factor = [&](int p) { return p < kMergeLdsParts ? s_f[p] : fast_exp2(ml[(int64_t)p * G * 2] - M); };
-  float acc = 0.f;
+  float m = -INFINITY;
 #pragma unroll
-  for (int k = 0; k < kBatch; ++k) {
-    const int p = grp + k * kMergeGroups;
-    if (p < np) acc = fmaf(ov[k], factor(p), acc);
+  for (int k = 0; k < kBatch; ++k)
+    if (grp + k * kMergeGroups < np) m = fmaxf(m, mv[k].x);
+  float l = 0.f, acc = 0.f;
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const float e = grp + k * kMergeGroups < np ? fast_exp2(mv[k].x - m) : 0.f;
+      l = fmaf(mv[k].y, e, l);
+      acc = fmaf(ov[k], e, acc);
+    }
   }
-  for (int p = grp + kBatch * kMergeGroups; p < np; p += kMergeGroups) acc = fmaf(po[p * pstride], factor(p), acc);
-  s_red[tid] = acc;
+  // Rows of more than kBatch * kMergeGroups parts: online fold of the rest.
+  for (int p = grp + kBatch * kMergeGroups; p < np; p += kMergeGroups) {
+    const float2 x = *reinterpret_cast<const float2*>(ml + (int64_t)p * G * 2);
+    const float y = po[p * pstride];
+    const float mn = fmaxf(m, x.x);
+    if (mn == -INFINITY) continue;
+    const float f = fast_exp2(m - mn), e = fast_exp2(x.x - mn);
+    l = fmaf(l, f, x.y * e);
+    acc = fmaf(acc, f, y * e);
+    m = mn;
+  }
+  if (dl == 0) {
+    s_m[grp] = m;
+    s_l[grp] = l;
+  }
+  s_o[grp][dl] = acc;
   __syncthreads();
   if (grp == 0) {
-    float a = 0.f;
+    float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < kMergeGroups; ++k) a += s_red[k * kMergeSlice + dl];
+    for (int g = 0; g < kMergeGroups; ++g) M = fmaxf(M, s_m[g]);
+    if (M == -INFINITY) {  // empty row
+      o[dl] = Elem<T>::from_f32(0.f);
+      return;
+    }
+    float L = 0.f, a = 0.f;
+#pragma unroll
+    for (int g = 0; g < kMergeGroups; ++g) {
+      const float e = fast_exp2(s_m[g] - M);
+      L = fmaf(s_l[g], e, L);
+      a = fmaf(s_o[g][dl], e, a);
+    }
     o[dl] = Elem<T>::from_f32(a / L);
   }
 }
