@@ -24,6 +24,13 @@ Per layer:
 Inputs are tensors (``maps[layer][step] -> [B, heads, rows, seq]``) or a
 directory of the reference's ``attn_weights_{layer}_{step}.pt`` files, read
 with torch.load(weights_only=True).
+
+The maps themselves come from a calibration generate() (tools/get_weights.py:
+30-212): collect_maps runs greedy generation through the patched attention
+with an AttentionRecorder attached, which keeps each layer's last query row
+of attention probabilities at the prefill and at every decode step (the only
+row the classification reads), computed by hc_score, instead of saving whole
+[B, heads, q_len, kv_len] maps.
 """
 import glob
 import os
@@ -32,7 +39,7 @@ import pathlib
 import numpy as np
 import torch
 
-from . import _lib, ops
+from . import _lib, compress, ops
 
 TYPE_MAP = {"anchor": 1, "volatile": 2, "pivot": 3, "satellite": 4}
 POOL_KERNEL = 5
@@ -195,3 +202,61 @@ def load_maps(tensor_save_dir, device="cuda"):
             continue
         maps.setdefault(layer, {})[step] = torch.load(f, map_location="cpu", weights_only=True).to(device)
     return maps
+
+
+class AttentionRecorder:
+    """Attention observer of the patched attention: per layer and forward,
+    the last query row's probabilities softmax(scale * q_last . K^T) over all
+    kv_len keys, [B, Hq, 1, kv_len] in the model dtype (the reference casts
+    its float32 softmax to the model dtype, tools/get_weights.py:53-55),
+    stored as maps[layer][kv_len].  With save_dir each map is also written
+    as the reference's attn_weights_{layer}_{kv_len}.pt.
+
+    hc_score computes it: one job per (batch, query head) against its KV
+    head's keys, window 1, pooling kernel 1 (the identity), with the
+    reference's casts of the logits and probabilities in 16-bit models."""
+
+    def __init__(self, save_dir=None):
+        self.maps = {}
+        self.save_dir = save_dir
+        if save_dir:
+            os.makedirs(save_dir, exist_ok=True)
+
+    def __call__(self, layer_idx, query_states, key_states, attention_mask, scaling):
+        q, k = query_states, key_states
+        B, Hq, Lq, _ = q.shape
+        Hkv, L = k.shape[1], k.shape[2]
+        if attention_mask is not None and attention_mask.dim() == 4:
+            last = attention_mask[..., -1, :L]
+            hidden = ~last if last.dtype == torch.bool else last != 0
+            if bool(hidden.any()):
+                raise NotImplementedError("attention recording takes unpadded batches (the last row sees every key)")
+        G = Hq // Hkv
+        q_off = [b * q.stride(0) + h * q.stride(1) + (Lq - 1) * q.stride(2) for b in range(B) for h in range(Hq)]
+        k_off = [b * k.stride(0) + (h // G) * k.stride(1) for b in range(B) for h in range(Hq)]
+        dev = q.device
+        probs = ops.score(q, torch.tensor(q_off, dtype=torch.int64).to(dev), q.stride(1), q.stride(2), k,
+                          torch.tensor(k_off, dtype=torch.int64).to(dev), k.stride(2), L, 1, 1, L, "avgpool", 1,
+                          float(scaling), flags=compress.ROUND_FLAGS.get(q.dtype, 0))
+        m = probs.view(B, Hq, 1, L).to(q.dtype)
+        self.maps.setdefault(layer_idx, {})[L] = m
+        if self.save_dir:
+            torch.save(m.cpu(), os.path.join(self.save_dir, f"attn_weights_{layer_idx}_{L}.pt"))
+
+
+def collect_maps(model, input_ids, max_new_tokens, attention_mask=None, save_dir=None):
+    """Calibration run (tools/get_weights.py:140-212): greedy generate() of
+    max_new_tokens on a model built under utils.install_attention_patch(),
+    with a plain cache, recording the attention maps.  Returns (maps, the
+    generated ids); maps[layer] has one entry per forward, keyed by kv_len
+    (the prompt length, then one more per decode step)."""
+    from . import llama_model
+    rec = AttentionRecorder(save_dir)
+    llama_model.ATTENTION_OBSERVERS.append(rec)
+    try:
+        with torch.no_grad():
+            out = model.generate(input_ids, attention_mask=attention_mask, max_new_tokens=max_new_tokens,
+                                 do_sample=False)
+    finally:
+        llama_model.ATTENTION_OBSERVERS.remove(rec)
+    return rec.maps, out

@@ -23,6 +23,13 @@ from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 from . import ops
 from .cache_utils import HeteroCache
 
+# Callables observer(layer_idx, query_states, key_states, attention_mask,
+# scaling) run by the patched attention after a cache update that is not a
+# HeteroCache's (keys are the layer's whole cache, one row per KV head): the
+# attention recording of tools/get_weights.py:30-138 hooks in here
+# (head_analysis.AttentionRecorder).
+ATTENTION_OBSERVERS = []
+
 
 # The last 4-D mask checked by _plain_causal (weakly held) and its verdict.
 _MASK_CHECK = {"ref": None, "shape": None, "plain": False}
@@ -130,6 +137,8 @@ class LlamaAttention(nn.Module):
             # returns its compressed rows; heterocache/llama_model.py:45-94).
             if cache is not None:
                 key_states, value_states = cache.update(key_states, value_states, self.layer_idx, cache_kwargs)
+            for observer in ATTENTION_OBSERVERS:
+                observer(self.layer_idx, query_states, key_states, attention_mask, self.scaling)
             out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling)
             return self.o_proj(out), None
         # A chunked prefill stays in the prefill branch until the declared

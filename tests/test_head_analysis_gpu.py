@@ -65,3 +65,41 @@ def test_head_topk_sets_match_oracle(dev, dtype):
     for b in range(2):
         for h in range(H):
             assert set(got[b * H + h, :k].tolist()) == sets[h][b]
+
+
+def test_calibration_maps_match_eager_attention_and_feed_the_producer(dev, tmp_path):
+    """collect_maps on a random-init Llama: the recorded last-row attention
+    of the prefill and of every decode step equals the stock model's eager
+    attention rows (float32); the files it writes load back with load_maps;
+    the JSON built from the recorded maps equals the oracle's."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from heterocache_amd import utils
+    def config(impl):
+        return LlamaConfig(vocab_size=512, hidden_size=8 * 128, intermediate_size=1024, num_hidden_layers=2,
+                           num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=4096,
+                           attn_implementation=impl)
+    cfg = config("sdpa")
+    with utils.install_attention_patch():
+        torch.manual_seed(0)
+        model = LlamaForCausalLM(cfg).to(torch.float32).to(dev).eval()
+    ids = torch.randint(0, 512, (1, 300), generator=torch.Generator().manual_seed(9)).to(dev)
+    maps, out = head_analysis.collect_maps(model, ids, 4, save_dir=str(tmp_path))
+    assert sorted(maps) == [0, 1] and sorted(maps[0]) == [300, 301, 302, 303]
+    torch.manual_seed(0)
+    ref_model = LlamaForCausalLM(config("eager")).to(torch.float32).to(dev).eval()
+    with torch.no_grad():
+        att = ref_model(out[:, :303], output_attentions=True).attentions
+    for layer in range(2):
+        for n in range(300, 304):
+            got = as_np(maps[layer][n])[0, :, 0]
+            want = as_np(att[layer])[0, :, n - 1, :n]
+            np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-6)
+    back = head_analysis.load_maps(str(tmp_path), device=dev)
+    assert sorted(back) == [0, 1] and all(torch.equal(back[l][n], maps[l][n]) for l in back for n in back[l])
+    kw = dict(topk=32, max_length=300, stable_threshold=0.5, sim_threshold=0.3, decode_step=303)
+    got = head_analysis.analyze(maps, 2, 8, 2, **kw)
+    ref = O.head_analysis({l: {n: as_np(m) for n, m in per.items()} for l, per in maps.items()}, 2, 8, 2, **kw)
+    assert got["classification_matrix"] == ref["classification_matrix"]
+    assert got["leader_member_relations"] == ref["leader_member_relations"]
+    np.testing.assert_allclose(np.asarray(got["allocation_matrix"]), np.asarray(ref["allocation_matrix"]),
+                               rtol=1e-12, atol=1e-12)
