@@ -28,13 +28,21 @@ FLAGS = [
 ]
 
 
+# Per-source additions.  The scorer keeps MFMA accumulators in VGPRs: its
+# softmax reads every accumulator, and with the compiler's AGPR choice each
+# read is an extra v_accvgpr_read.
+EXTRA_FLAGS = {
+    "hc_score.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src):
     obj = os.path.join(OBJ, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
+    cmd = [HIPCC] + FLAGS + EXTRA_FLAGS.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:

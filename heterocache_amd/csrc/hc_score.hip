@@ -24,8 +24,11 @@
 //     A[job][w'][g][t].
 //  4. score_pool_kernel: pooling over t and max over g -> S[job][w'][t].
 #include <cfloat>
+#include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "hc_common.h"
 #include "hc_internal.h"
@@ -36,7 +39,6 @@ constexpr int kScoreWaves = 4;
 constexpr int kSubTiles = 4;                      // 16-token sub-tiles per wave
 constexpr int kScoreChunk = kScoreWaves * 16 * kSubTiles;  // 256 tokens per workgroup
 constexpr int kQPitch = HC_HEAD_DIM + 8;
-constexpr float kScoreLazy = 8.f;  // lazy-maximum threshold, log2 units
 
 struct ScoreArgs {
   const void* q;
@@ -48,6 +50,7 @@ struct ScoreArgs {
   const int64_t* row_tile_off;
   const int32_t* k_row;
   int L, G, W, R, NT, flags, span;
+  int cpw;  // 256-token chunks per workgroup of the statistics and probability passes
   float scale;
   float scale2;  // scale * log2(e): base-2 logits without the reference's casts
 };
@@ -126,8 +129,9 @@ __device__ __forceinline__ float scaled_logit(const ScoreArgs& a, float acc) {
 }
 
 // Logits (base 2) of row 16nt + (lane & 15) (visible up to `limit`) for
-// tokens t0 + 4*(lane>>4) + j; keys are the A operand.
-template <typename T, int RM, bool MASK>
+// tokens t0 + 4*(lane>>4) + j; keys are the A operand.  RAW (no casts):
+// the unscaled dot products, the caller folds scale2 into its exp2 argument.
+template <typename T, int RM, bool MASK, bool RAW = false>
 __device__ __forceinline__ void subtile_logits(const ScoreArgs& a, const typename Elem<T>::vec8 (&kr)[4],
                                                const T* s_q, int nt, int t0, int lane, int limit, float (&x)[4]) {
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -137,7 +141,7 @@ __device__ __forceinline__ void subtile_logits(const ScoreArgs& a, const typenam
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int t = t0 + 4 * (lane >> 4) + j;
-    x[j] = (!MASK || t <= limit) ? scaled_logit<RM>(a, acc[j]) : -INFINITY;
+    x[j] = (!MASK || t <= limit) ? (RAW ? acc[j] : scaled_logit<RM>(a, acc[j])) : -INFINITY;
   }
 }
 
@@ -148,105 +152,132 @@ __device__ __forceinline__ void merge_ml(float& m, float& l, float m2, float l2)
   m = mn;
 }
 
+// Key registers of one wave's kSubTiles sub-tiles.
+template <typename T>
+struct KRegs {
+  typename Elem<T>::vec8 v[kSubTiles][4];
+};
+
+template <typename T, bool STORE>
+__device__ __forceinline__ void load_k_chunk(const ScoreArgs& a, int job, int tw, int lane, KRegs<T>& k) {
+#pragma unroll
+  for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, k.v[u]);
+}
+
+// Statistics of one 256-token chunk: the (max, sum) of every row over this
+// wave's 64 tokens (lane l holds row 16nt + l%16, tokens 4*(l/16) + j of
+// each sub-tile), merged into the wave's LDS entry of the row.  One 16-row
+// tile at a time, in a rolled loop: unrolled over the 16 tiles and the mask
+// variants the kernel outgrows the instruction cache.
+template <typename T, int RM, bool LOGITS, bool MASK>
+__device__ __forceinline__ void stats_chunk(const ScoreArgs& a, const KRegs<T>& k, const T* s_q, float* my, int job,
+                                            int tw, int lane, float* __restrict__ logits) {
+  const bool vec_logits = (a.span & 3) == 0;
+  for (int nt = 0; nt < a.NT; ++nt) {
+    const int limit = row_limit(a, 16 * nt + (lane & 15));
+    // All sub-tiles' logits first (independent MFMA chains, no branch
+    // between them); then the row's maximum over its four lanes, and one sum
+    // of exp2 against it (no rescaling).  Without casts the maximum is taken
+    // on the unscaled products and the scale folds into each exp2's fma.
+    constexpr bool RAW = RM == 0 && !LOGITS;
+    float x[kSubTiles][4];
+#pragma unroll
+    for (int u = 0; u < kSubTiles; ++u) {
+      subtile_logits<T, RM, MASK, RAW>(a, k.v[u], s_q, nt, tw + 16 * u, lane, limit, x[u]);
+      if constexpr (LOGITS) {
+        // Row r, tokens t..t+3 (16 bytes) of the job's [R][span] logits.
+        const int r = 16 * nt + (lane & 15), t = tw + 16 * u + 4 * (lane >> 4);
+        float* o = logits + ((int64_t)job * a.R + r) * a.span + t;
+        if (r < a.R) {
+          if (vec_logits && t + 4 <= a.span) {
+            *reinterpret_cast<f32x4*>(o) = f32x4{x[u][0], x[u][1], x[u][2], x[u][3]};
+          } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (t + j < a.span) o[j] = x[u][j];
+          }
+        }
+      }
+    }
+    // -FLT_MAX (not -inf) as the empty maximum: exp2(-inf - m) = 0 for a
+    // row with no visible value, never NaN.
+    float m = -FLT_MAX;
+#pragma unroll
+    for (int u = 0; u < kSubTiles; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u][0], x[u][1]), fmaxf(x[u][2], x[u][3])));
+    m = fmaxf(m, __shfl_xor(m, 16, 64));
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    float l = 0.f;
+    if constexpr (RAW) {
+      m = fmaxf(m * a.scale2, -FLT_MAX);  // base-2 scaled maximum, finite
+#pragma unroll
+      for (int u = 0; u < kSubTiles; ++u)
+        l += (fast_exp2(fmaf(x[u][0], a.scale2, -m)) + fast_exp2(fmaf(x[u][1], a.scale2, -m))) +
+             (fast_exp2(fmaf(x[u][2], a.scale2, -m)) + fast_exp2(fmaf(x[u][3], a.scale2, -m)));
+    } else {
+#pragma unroll
+      for (int u = 0; u < kSubTiles; ++u)
+        l += (fast_exp2(x[u][0] - m) + fast_exp2(x[u][1] - m)) + (fast_exp2(x[u][2] - m) + fast_exp2(x[u][3] - m));
+    }
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    if (lane < 16) {  // each row entry belongs to one lane of this wave
+      float* e = my + 2 * (16 * nt + lane);
+      float em = e[0], el = e[1];
+      merge_ml(em, el, m, l);
+      e[0] = em;
+      e[1] = el;
+    }
+  }
+}
+
+// Each workgroup takes a.cpw consecutive 256-token chunks of one job; its
+// queries are staged in LDS once.  One (max, sum) partial per workgroup and
+// row.  (A second register set for the next chunk's keys halves occupancy
+// and was slower: the passes are bound by latency within a chunk.)
 template <typename T, bool STORE, int RM, bool LOGITS>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs a, float* __restrict__ part,
                                                                       float* __restrict__ logits) {
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_q = reinterpret_cast<T*>(smem);
   float* s_st = reinterpret_cast<float*>(smem + (size_t)a.NT * 16 * kQPitch * sizeof(T));  // [waves][rows][2]
-  const int job = blockIdx.y, chunk = blockIdx.x;
+  const int job = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rows = a.NT * 16;
+  const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
+  const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
+  // Each wave owns kSubTiles consecutive 16-token sub-tiles of a chunk.
+  const int woff = wave * 16 * kSubTiles;
+  KRegs<T> ka;
+  load_k_chunk<T, STORE>(a, job, c0 * kScoreChunk + woff, lane, ka);
   stage_queries<T>(a, job, s_q);
-  // Each wave owns kSubTiles consecutive 16-token sub-tiles; all their key
-  // loads are issued before any is used.
-  const int tw = chunk * kScoreChunk + wave * 16 * kSubTiles;
-  typename Elem<T>::vec8 krs[kSubTiles][4];
-#pragma unroll
-  for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, krs[u]);
-  __syncthreads();
-  // Lane state: running (max, sum) of row 16nt + lane%16 over this lane's
-  // tokens; the four lanes of a row are combined once, after the loop.
-  // -FLT_MAX (not -inf) as the empty maximum keeps the update branch-free:
-  // exp2(-inf - m) = 0 and exp2(m - m) = 1 for a still-empty row.
-  float m[16], l[16];
-#pragma unroll
-  for (int nt = 0; nt < 16; ++nt) {
-    m[nt] = -FLT_MAX;
-    l[nt] = 0.f;
-  }
-  const bool vec_logits = (a.span & 3) == 0;
-  // Masks matter only where this workgroup's tokens reach past the lowest
-  // row limit (the causal window or the end of the keys); elsewhere every
-  // logit is visible and the per-value test is skipped.
-  const int min_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W : a.L - 1;
-  const bool need_mask = chunk * kScoreChunk + kScoreChunk - 1 > min_limit;
-  auto body = [&](auto mask_tag) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-#pragma unroll
-    for (int nt = 0; nt < 16; ++nt) {
-      if (nt < a.NT) {
-        const int limit = row_limit(a, 16 * nt + (lane & 15));
-#pragma unroll
-        for (int u = 0; u < kSubTiles; ++u) {
-          float x[4];
-          subtile_logits<T, RM, MASK>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
-          if constexpr (LOGITS) {
-            // Row r, tokens t..t+3 (16 bytes) of the job's [R][span] logits.
-            const int r = 16 * nt + (lane & 15), t = tw + 16 * u + 4 * (lane >> 4);
-            float* o = logits + ((int64_t)job * a.R + r) * a.span + t;
-            if (r < a.R) {
-              if (vec_logits && t + 4 <= a.span) {
-                *reinterpret_cast<f32x4*>(o) = f32x4{x[0], x[1], x[2], x[3]};
-              } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                  if (t + j < a.span) o[j] = x[j];
-              }
-            }
-          }
-          // Lazy running maximum: m moves only when a value exceeds it by
-          // more than 2^kScoreLazy, so the rescale (and its exp2) is rare
-          // and each value costs a subtract, an exp2 and an add.
-          const float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-          if (__any(mx > m[nt] + kScoreLazy)) {
-            if (mx > m[nt] + kScoreLazy) {
-              l[nt] *= fast_exp2(m[nt] - mx);
-              m[nt] = mx;
-            }
-          }
-          l[nt] += (fast_exp2(x[0] - m[nt]) + fast_exp2(x[1] - m[nt])) + (fast_exp2(x[2] - m[nt]) + fast_exp2(x[3] - m[nt]));
-        }
-      }
-    }
-  };
-  if (need_mask)
-    body(std::true_type{});
-  else
-    body(std::false_type{});
   float* my = s_st + (size_t)wave * rows * 2;
-#pragma unroll
-  for (int nt = 0; nt < 16; ++nt) {
-    if (nt < a.NT) {
-      float mm = m[nt], ll = l[nt];
-#pragma unroll
-      for (int off = 16; off <= 32; off <<= 1) {
-        const float m2 = __shfl_xor(mm, off, 64), l2 = __shfl_xor(ll, off, 64);
-        merge_ml(mm, ll, m2, l2);
-      }
-      if (lane < 16) {
-        my[2 * (16 * nt + lane)] = mm;
-        my[2 * (16 * nt + lane) + 1] = ll;
-      }
-    }
+  for (int r = lane; r < rows; r += 64) {
+    my[2 * r] = -INFINITY;
+    my[2 * r + 1] = 0.f;
   }
   __syncthreads();
-  const int nchunks = gridDim.x;
+  // Masks matter only where a chunk reaches past the lowest row limit (the
+  // causal window or the end of the keys); elsewhere every logit is visible
+  // and the per-value test is skipped.
+  const int min_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W : a.L - 1;
+  auto chunk_stats = [&](const KRegs<T>& k, int c) {
+    const int tw = c * kScoreChunk + woff;
+    if (c * kScoreChunk + kScoreChunk - 1 > min_limit)
+      stats_chunk<T, RM, LOGITS, true>(a, k, s_q, my, job, tw, lane, logits);
+    else
+      stats_chunk<T, RM, LOGITS, false>(a, k, s_q, my, job, tw, lane, logits);
+  };
+  for (int c = c0; c < c1; ++c) {
+    if (c > c0) load_k_chunk<T, STORE>(a, job, c * kScoreChunk + woff, lane, ka);
+    chunk_stats(ka, c);
+  }
+  __syncthreads();
+  const int nparts = gridDim.x;
   for (int r = threadIdx.x; r < a.R; r += kScoreWaves * 64) {
     float mm = -INFINITY, ll = 0.f;
 #pragma unroll
     for (int w = 0; w < kScoreWaves; ++w) merge_ml(mm, ll, s_st[(w * rows + r) * 2], s_st[(w * rows + r) * 2 + 1]);
-    float* o = part + (((int64_t)job * nchunks + chunk) * a.R + r) * 2;
+    float* o = part + (((int64_t)job * nparts + blockIdx.x) * a.R + r) * 2;
     o[0] = mm;
     o[1] = ll;
   }
@@ -278,8 +309,8 @@ __global__ __launch_bounds__(256) void score_stats_merge_kernel(const float* __r
 // Logits (base 2) with the queries as the A operand: lane holds rows
 // 16nt + 4*(lane>>4) + j (visible up to limit[j]) of token t0 + lane%16, so
 // sums over a query head's window rows are in-lane adds plus at most two
-// cross-lane steps.
-template <typename T, int RM, bool MASK>
+// cross-lane steps.  RAW as for subtile_logits.
+template <typename T, int RM, bool MASK, bool RAW = false>
 __device__ __forceinline__ void subtile_logits_rows(const ScoreArgs& a, const typename Elem<T>::vec8 (&kr)[4],
                                                     const T* s_q, int nt, int t0, int lane, const int (&limit)[4],
                                                     float (&x)[4]) {
@@ -289,13 +320,21 @@ __device__ __forceinline__ void subtile_logits_rows(const ScoreArgs& a, const ty
   for (int s = 0; s < 4; ++s) acc = mma_16x16x32(load8<T>(qrow + 32 * s), kr[s], acc);
   const int t = t0 + (lane & 15);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) x[j] = (!MASK || t <= limit[j]) ? scaled_logit<RM>(a, acc[j]) : -INFINITY;
+  for (int j = 0; j < 4; ++j)
+    x[j] = (!MASK || t <= limit[j]) ? (RAW ? acc[j] : scaled_logit<RM>(a, acc[j])) : -INFINITY;
 }
 
-// MOM (CAKE scoring, W a multiple of 16): besides the window sum A, write
-// the window sum of squares A2 unrounded and one partial of
-// sum p*log(p + 1e-10) over t < span per (job, chunk) into ent.
-template <typename T, bool STORE, int RM, bool MOM>
+// Window modes of the probability pass, fixed per kernel instance so each
+// instance holds one output path (with all of them, and the 16 row tiles
+// unrolled, the kernel outgrew the instruction cache).
+enum WinMode { kWinNone = 0, kWin16 = 1, kWin8 = 2, kWin4 = 3, kWin2 = 4, kWin1 = 5 };
+
+// Probabilities of every (row, token) of the workgroup's chunk, summed over
+// the window rows of each query head per WM (kWinNone: no sum).
+// MOM (CAKE scoring, kWin16): besides the window sum A, write the window sum
+// of squares A2 unrounded and one partial of sum p*log(p + 1e-10) over
+// t < span per (job, chunk) into ent.
+template <typename T, bool STORE, int RM, int WM, bool MOM>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs a, const float* __restrict__ stats,
                                                                       float* __restrict__ A, float* __restrict__ A2,
                                                                       float* __restrict__ ent) {
@@ -304,10 +343,14 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   const int rows = a.NT * 16;
   float* s_m = reinterpret_cast<float*>(smem + (size_t)rows * kQPitch * sizeof(T));  // [rows] row max
   float* s_iz = s_m + rows;                                                           // [rows] 1 / row sum
-  const int job = blockIdx.y, chunk = blockIdx.x;
+  const int job = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rg = lane >> 4;
-  const bool sum_w = (a.flags & HC_SCORE_SUM_WINDOW) != 0;
+  const int nchunks = (a.span + kScoreChunk - 1) / kScoreChunk;
+  const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
+  const int woff = wave * 16 * kSubTiles;
+  KRegs<T> ka;
+  load_k_chunk<T, STORE>(a, job, c0 * kScoreChunk + woff, lane, ka);
   stage_queries<T>(a, job, s_q);
   for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
     // Padding rows get probability 0 even where logits are not masked.
@@ -320,23 +363,17 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
       s_iz[r] = r < a.R ? 1.f / stats[((int64_t)job * a.R + r) * 2 + 1] : 0.f;
     }
   }
-  const int wout = sum_w ? 1 : a.W;
-  const int tw = chunk * kScoreChunk + wave * 16 * kSubTiles;
-  typename Elem<T>::vec8 krs[kSubTiles][4];
-#pragma unroll
-  for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, krs[u]);
+  const int wout = WM == kWinNone ? a.W : 1;
   __syncthreads();
-  float gsum[kSubTiles], gsq[kSubTiles];  // running window sum (and sum of squares) per sub-tile (W >= 16)
+  float gsum[kSubTiles], gsq[kSubTiles];  // running window sum (and sum of squares) per sub-tile (kWin16)
 #pragma unroll
   for (int u = 0; u < kSubTiles; ++u) gsum[u] = gsq[u] = 0.f;
   float ent_acc = 0.f;
   const int min_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W : a.L - 1;
-  const bool need_mask = chunk * kScoreChunk + kScoreChunk - 1 > min_limit;
-  auto body = [&](auto mask_tag) {
+  auto body = [&](auto mask_tag, const KRegs<T>& k, int tw) {
     constexpr bool MASK = decltype(mask_tag)::value;
-  #pragma unroll
-    for (int nt = 0; nt < 16; ++nt) {
-      if (nt < a.NT) {
+    for (int nt = 0; nt < a.NT; ++nt) {
+      {
         const int r0 = 16 * nt + 4 * rg;
         float M[4], IZ[4];
         int limit[4];
@@ -346,43 +383,72 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
           M[j] = s_m[r0 + j];
           IZ[j] = s_iz[r0 + j];
           limit[j] = row_limit(a, r0 + j);
-          if (!sum_w) orow[j] = (((int64_t)job * wout + (r0 + j) % a.W) * a.G + (r0 + j) / a.W) * a.span;
+          if constexpr (WM == kWinNone) orow[j] = (((int64_t)job * wout + (r0 + j) % a.W) * a.G + (r0 + j) / a.W) * a.span;
         }
+        // All sub-tiles' logits first (independent MFMA chains, no branch
+        // between them), then the probabilities and their sums.
+        float x[kSubTiles][4];
+  #pragma unroll
+        for (int u = 0; u < kSubTiles; ++u)
+          subtile_logits_rows<T, RM, MASK, RM == 0>(a, k.v[u], s_q, nt, tw + 16 * u, lane, limit, x[u]);
   #pragma unroll
         for (int u = 0; u < kSubTiles; ++u) {
           const int t = tw + 16 * u + (lane & 15);
-          float x[4], p[4];
-          subtile_logits_rows<T, RM, MASK>(a, krs[u], s_q, nt, tw + 16 * u, lane, limit, x);
+          float p[4];
   #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            if constexpr (RM == 0)
-              p[j] = fast_exp2(x[j] - M[j]);  // M holds m + log2 l; masked logits give 0
+            if constexpr (RM == 0)  // x: unscaled products; M holds m + log2 l; masked logits give 0
+              p[j] = fast_exp2(fmaf(x[u][j], a.scale2, -M[j]));
             else
-              p[j] = x[j] == -INFINITY ? 0.f : round_fixed<RM>(fast_exp2(x[j] - M[j]) * IZ[j]);
+              p[j] = x[u][j] == -INFINITY ? 0.f : round_fixed<RM>(fast_exp2(x[u][j] - M[j]) * IZ[j]);
           }
           if constexpr (MOM) {
             // Padding rows have p = 0 and add 0 * log(1e-10) = 0.
-            if (t < a.span) {
+            float e = 0.f;
   #pragma unroll
-              for (int j = 0; j < 4; ++j) ent_acc += p[j] * __logf(p[j] + 1e-10f);
-            }
+            for (int j = 0; j < 4; ++j) e += p[j] * __logf(p[j] + 1e-10f);
+            ent_acc += t < a.span ? e : 0.f;
           }
-          if (!sum_w) {
+          if constexpr (WM == kWinNone) {
             // Row r = g*W + w -> A[job][w][g][t].
   #pragma unroll
             for (int j = 0; j < 4; ++j)
               if (r0 + j < a.R && t < a.span) A[orow[j] + t] = p[j];
-          } else if (a.W >= 16) {
+          } else if constexpr (WM == kWin16) {
             // The 16 rows of this tile all belong to one query head; each
             // lane sums its 4 rows over the head's tiles, and the 4 lane
-            // groups are combined once per head.
+            // groups are combined once per head (below).
             gsum[u] += (p[0] + p[1]) + (p[2] + p[3]);
             if constexpr (MOM) gsq[u] += (p[0] * p[0] + p[1] * p[1]) + (p[2] * p[2] + p[3] * p[3]);
-            if (((16 * (nt + 1)) % a.W) == 0) {
+          } else if constexpr (WM == kWin8) {
+            float v = (p[0] + p[1]) + (p[2] + p[3]);
+            v += __shfl_xor(v, 16, 64);
+            const int g = r0 / 8;
+            if ((rg & 1) == 0 && r0 < a.R && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_fixed<RM>(v);
+          } else if constexpr (WM == kWin4) {
+            // A head's rows are the four j of this lane.
+            const float v = (p[0] + p[1]) + (p[2] + p[3]);
+            if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 4) * a.span + t] = round_fixed<RM>(v);
+          } else if constexpr (WM == kWin2) {
+            const float v0 = p[0] + p[1], v1 = p[2] + p[3];
+            if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2) * a.span + t] = round_fixed<RM>(v0);
+            if (r0 + 2 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2 + 1) * a.span + t] = round_fixed<RM>(v1);
+          } else {
+            // W == 1: every row is its own query head.
+  #pragma unroll
+            for (int j = 0; j < 4; ++j)
+              if (r0 + j < a.R && t < a.span) A[((int64_t)job * a.G + r0 + j) * a.span + t] = round_fixed<RM>(p[j]);
+          }
+        }
+        if constexpr (WM == kWin16) {
+          if (((16 * (nt + 1)) % a.W) == 0) {  // the last tile of a query head
+            const int g = (16 * nt) / a.W;
+  #pragma unroll
+            for (int u = 0; u < kSubTiles; ++u) {
+              const int t = tw + 16 * u + (lane & 15);
               float v = gsum[u];
               v += __shfl_xor(v, 16, 64);
               v += __shfl_xor(v, 32, 64);
-              const int g = (16 * nt) / a.W;
               const int64_t o = ((int64_t)job * a.G + g) * a.span + t;
               if constexpr (MOM) {
                 float v2 = gsq[u];
@@ -398,40 +464,30 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
               }
               gsum[u] = 0.f;
             }
-          } else if (a.W == 8) {
-            float v = (p[0] + p[1]) + (p[2] + p[3]);
-            v += __shfl_xor(v, 16, 64);
-            const int g = r0 / 8;
-            if ((rg & 1) == 0 && r0 < a.R && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_fixed<RM>(v);
-          } else if (a.W == 4) {
-            // A head's rows are the four j of this lane.
-            const float v = (p[0] + p[1]) + (p[2] + p[3]);
-            if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 4) * a.span + t] = round_fixed<RM>(v);
-          } else if (a.W == 2) {
-            const float v0 = p[0] + p[1], v1 = p[2] + p[3];
-            if (r0 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2) * a.span + t] = round_fixed<RM>(v0);
-            if (r0 + 2 < a.R && t < a.span) A[((int64_t)job * a.G + r0 / 2 + 1) * a.span + t] = round_fixed<RM>(v1);
-          } else {
-            // W == 1: every row is its own query head.
-  #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              if (r0 + j < a.R && t < a.span) A[((int64_t)job * a.G + r0 + j) * a.span + t] = round_fixed<RM>(p[j]);
           }
         }
       }
     }
   };
-  if (need_mask)
-    body(std::true_type{});
-  else
-    body(std::false_type{});
+  // The workgroup's chunks in order (queries and row statistics staged once).
+  auto chunk_probs = [&](const KRegs<T>& k, int c) {
+    const int tw = c * kScoreChunk + woff;
+    if (c * kScoreChunk + kScoreChunk - 1 > min_limit)
+      body(std::true_type{}, k, tw);
+    else
+      body(std::false_type{}, k, tw);
+  };
+  for (int c = c0; c < c1; ++c) {
+    if (c > c0) load_k_chunk<T, STORE>(a, job, c * kScoreChunk + woff, lane, ka);
+    chunk_probs(ka, c);
+  }
   if constexpr (MOM) {
     __shared__ float s_ent[kScoreWaves];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) ent_acc += __shfl_xor(ent_acc, off, 64);
     if (lane == 0) s_ent[wave] = ent_acc;
     __syncthreads();
-    if (threadIdx.x == 0) ent[(int64_t)job * gridDim.x + chunk] = (s_ent[0] + s_ent[1]) + (s_ent[2] + s_ent[3]);
+    if (threadIdx.x == 0) ent[(int64_t)job * gridDim.x + blockIdx.x] = (s_ent[0] + s_ent[1]) + (s_ent[2] + s_ent[3]);
   }
 }
 
@@ -601,6 +657,41 @@ size_t score_workspace_bytes(int njobs, int L, int G, int W, int flags) {
          align256((size_t)njobs * R * 2 * sizeof(float)) + align256(tail);
 }
 
+// Workgroups of one score kernel instance (kScoreWaves * 64 threads, `lds`
+// bytes of dynamic LDS) resident on the current device at once, cached per
+// (device, instance, lds); 0 when the query fails.
+static int resident_wgs(const void* fn, size_t lds) {
+  struct Entry {
+    int dev;
+    const void* fn;
+    size_t lds;
+    int slots;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (const Entry& e : cache)
+    if (e.dev == dev && e.fn == fn && e.lds == lds) return e.slots;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kScoreWaves * 64, lds) != hipSuccess) return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  const int slots = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  cache.push_back({dev, fn, lds, slots});
+  return slots;
+}
+
+// Chunks per workgroup so that one resident round of workgroups covers the
+// njobs * nchunks chunks (each workgroup then streams its chunks with the
+// next one's keys in flight); sets a.cpw, returns the grid's x extent.
+static int plan_chunks(const void* fn, size_t lds, int njobs, int nchunks, ScoreArgs& a) {
+  const int slots = resident_wgs(fn, lds);
+  const int64_t total = (int64_t)njobs * nchunks;
+  a.cpw = slots > 0 ? (int)std::max<int64_t>(1, (total + slots - 1) / slots) : 1;
+  return (nchunks + a.cpw - 1) / a.cpw;
+}
+
 template <typename T, bool STORE>
 static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* scores, void* ws, hipStream_t s) {
   const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
@@ -614,9 +705,14 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   const size_t lds3 = qbytes + (size_t)a.NT * 16 * 2 * sizeof(float);
   const bool via_logits = a.R < kLogitRows;
   const int rm = (a.flags & HC_SCORE_ROUND_BF16) ? 1 : (a.flags & HC_SCORE_ROUND_F16) ? 2 : 0;
-#define HC_STATS(RM, LG)                                                                                   \
-  hipLaunchKernelGGL((score_stats_kernel<T, STORE, RM, LG>), dim3(nchunks, njobs), dim3(kScoreWaves * 64), lds1, s, \
-                     a, part, LG ? A : nullptr)
+  int nparts = 0;  // statistics partials per job: the stats grid's x extent
+#define HC_STATS(RM, LG)                                                                                    \
+  do {                                                                                                      \
+    auto fn = score_stats_kernel<T, STORE, RM, LG>;                                                         \
+    ScoreArgs as = a;                                                                                       \
+    nparts = plan_chunks(reinterpret_cast<const void*>(fn), lds1, njobs, nchunks, as);                      \
+    hipLaunchKernelGGL(fn, dim3(nparts, njobs), dim3(kScoreWaves * 64), lds1, s, as, part, LG ? A : nullptr); \
+  } while (0)
   if (via_logits) {
     if (rm == 0) HC_STATS(0, true); else if (rm == 1) HC_STATS(1, true); else HC_STATS(2, true);
   } else {
@@ -625,7 +721,7 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
 #undef HC_STATS
   int rc = check_launch("hc_score(stats)");
   if (rc) return rc;
-  hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nchunks, a.R,
+  hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nparts, a.R,
                      njobs, stats);
   if ((rc = check_launch("hc_score(merge)"))) return rc;
   if (via_logits) {
@@ -646,10 +742,30 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   }
   const int nchunks_span = (a.span + kScoreChunk - 1) / kScoreChunk;
   if (nchunks_span > 0) {
-#define HC_PROBS(RM)                                                                                        \
-  hipLaunchKernelGGL((score_probs_kernel<T, STORE, RM, false>), dim3(nchunks_span, njobs), dim3(kScoreWaves * 64), \
-                     lds3, s, a, stats, A, nullptr, nullptr)
-    if (rm == 0) HC_PROBS(0); else if (rm == 1) HC_PROBS(1); else HC_PROBS(2);
+    const int wm = !(a.flags & HC_SCORE_SUM_WINDOW) ? kWinNone
+                   : a.W >= 16                       ? kWin16
+                   : a.W == 8                        ? kWin8
+                   : a.W == 4                        ? kWin4
+                   : a.W == 2                        ? kWin2
+                                                     : kWin1;
+#define HC_PROBS(RM, WM)                                                                                    \
+  do {                                                                                                      \
+    auto fn = score_probs_kernel<T, STORE, RM, WM, false>;                                                  \
+    ScoreArgs as = a;                                                                                       \
+    const int gx = plan_chunks(reinterpret_cast<const void*>(fn), lds3, njobs, nchunks_span, as);           \
+    hipLaunchKernelGGL(fn, dim3(gx, njobs), dim3(kScoreWaves * 64), lds3, s, as, stats, A, nullptr, nullptr); \
+  } while (0)
+#define HC_PROBS_RM(RM)                                     \
+  switch (wm) {                                             \
+    case kWinNone: HC_PROBS(RM, kWinNone); break;           \
+    case kWin16: HC_PROBS(RM, kWin16); break;               \
+    case kWin8: HC_PROBS(RM, kWin8); break;                 \
+    case kWin4: HC_PROBS(RM, kWin4); break;                 \
+    case kWin2: HC_PROBS(RM, kWin2); break;                 \
+    default: HC_PROBS(RM, kWin1); break;                    \
+  }
+    if (rm == 0) { HC_PROBS_RM(0) } else if (rm == 1) { HC_PROBS_RM(1) } else { HC_PROBS_RM(2) }
+#undef HC_PROBS_RM
 #undef HC_PROBS
     if ((rc = check_launch("hc_score(probs)"))) return rc;
     hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + kPoolThreads - 1) / kPoolThreads, njobs * wout),
@@ -794,14 +910,18 @@ static int launch_cake(ScoreArgs a, int njobs, int batch, int heads, float gamma
   const size_t lds1 = qbytes + (size_t)kScoreWaves * a.NT * 16 * 2 * sizeof(float);
   const size_t lds3 = qbytes + (size_t)a.NT * 16 * 2 * sizeof(float);
   int rc;
-  hipLaunchKernelGGL((score_stats_kernel<T, false, RM, false>), dim3(nchunks, njobs), dim3(kScoreWaves * 64), lds1, s,
-                     a, part, nullptr);
+  auto fstats = score_stats_kernel<T, false, RM, false>;
+  ScoreArgs as = a;
+  const int nparts = plan_chunks(reinterpret_cast<const void*>(fstats), lds1, njobs, nchunks, as);
+  hipLaunchKernelGGL(fstats, dim3(nparts, njobs), dim3(kScoreWaves * 64), lds1, s, as, part, nullptr);
   if ((rc = check_launch("hc_cake_score(stats)"))) return rc;
-  hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nchunks, a.R,
+  hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nparts, a.R,
                      njobs, stats);
   if ((rc = check_launch("hc_cake_score(merge)"))) return rc;
-  hipLaunchKernelGGL((score_probs_kernel<T, false, RM, true>), dim3(nspan, njobs), dim3(kScoreWaves * 64), lds3, s, a,
-                     stats, A1, A2, ent);
+  auto fprobs = score_probs_kernel<T, false, RM, kWin16, true>;
+  ScoreArgs ap = a;
+  const int nprob = plan_chunks(reinterpret_cast<const void*>(fprobs), lds3, njobs, nspan, ap);
+  hipLaunchKernelGGL(fprobs, dim3(nprob, njobs), dim3(kScoreWaves * 64), lds3, s, ap, stats, A1, A2, ent);
   if ((rc = check_launch("hc_cake_score(probs)"))) return rc;
   hipLaunchKernelGGL((cake_pool_kernel<RM>), dim3((a.span + kCakeThreads - 1) / kCakeThreads, njobs),
                      dim3(kCakeThreads), 0, s, A1, A2, a.G, a.W, a.span, gamma, scores);
@@ -810,7 +930,7 @@ static int launch_cake(ScoreArgs a, int njobs, int batch, int heads, float gamma
   hipLaunchKernelGGL((cake_varsum_kernel<RM>), dim3(nvar), dim3(kCakeThreads), 0, s, A1, A2, batch, heads, a.W,
                      a.span, vpart);
   if ((rc = check_launch("hc_cake_score(varsum)"))) return rc;
-  hipLaunchKernelGGL((cake_final_kernel<RM>), dim3(1), dim3(kCakeThreads), 0, s, ent, njobs * nspan, vpart, nvar,
+  hipLaunchKernelGGL((cake_final_kernel<RM>), dim3(1), dim3(kCakeThreads), 0, s, ent, njobs * nprob, vpart, nvar,
                      out);
   return check_launch("hc_cake_score(final)");
 }
@@ -877,6 +997,7 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
   a.span = span;
   a.scale = scale;
   a.scale2 = scale * 1.4426950408889634f;
+  a.cpw = 1;
   hipStream_t s = (hipStream_t)stream;
 #define HC_SCORE_DISPATCH(T)                                                                          \
   return store ? launch_score<T, true>(a, njobs, pooling, kernel, scores, workspace, s)               \
@@ -944,6 +1065,7 @@ extern "C" int hc_cake_score(int dtype, const void* q, const int64_t* q_off, int
   a.span = seq_len - window;
   a.scale = scale;
   a.scale2 = scale * 1.4426950408889634f;
+  a.cpw = 1;
   hipStream_t s = (hipStream_t)stream;
   const int rm = (flags & HC_SCORE_ROUND_BF16) ? 1 : (flags & HC_SCORE_ROUND_F16) ? 2 : 0;
   const int heads = kv_heads * group;
