@@ -38,6 +38,24 @@ def _dev_i64(vals, device):
     return torch.tensor(list(vals), dtype=torch.int64).to(device)
 
 
+# Per-job element offsets depend only on shapes and strides, not on the data:
+# they are built and copied to the device once per layout.
+_OFFSETS = {}
+_OFFSETS_MAX = 256
+
+
+def _job_offsets(key, device, build):
+    """(q_off, k_off) int64 device tensors for a layout key, built by build()."""
+    key = (str(device),) + key
+    hit = _OFFSETS.get(key)
+    if hit is None:
+        if len(_OFFSETS) >= _OFFSETS_MAX:
+            _OFFSETS.clear()
+        q_off, k_off = build()
+        hit = _OFFSETS[key] = (_dev_i64(q_off, device), _dev_i64(k_off, device))
+    return hit
+
+
 def window_scores(q, k, kv_heads, group, window, pooling="avgpool", kernel=5, window_keep=False, causal=True,
                   round_dtype=None, scale=None, stream=None):
     """Scores [B * len(kv_heads), span] of the last `window` query positions.
@@ -53,19 +71,22 @@ def window_scores(q, k, kv_heads, group, window, pooling="avgpool", kernel=5, wi
     if window > Lq:
         raise ValueError("window longer than the query sequence")
     scale = 1.0 / math.sqrt(128) if scale is None else scale
-    kv_heads = list(kv_heads)
-    q_off, k_off = [], []
-    for b in range(B):
-        for h in kv_heads:
-            q_off.append(b * q.stride(0) + h * group * q.stride(1) + (Lq - window) * q.stride(2))
-            k_off.append(b * k.stride(0) + h * k.stride(1))
+    kv_heads = tuple(kv_heads)
+
+    def build():
+        q_off = [b * q.stride(0) + h * group * q.stride(1) + (Lq - window) * q.stride(2)
+                 for b in range(B) for h in kv_heads]
+        k_off = [b * k.stride(0) + h * k.stride(1) for b in range(B) for h in kv_heads]
+        return q_off, k_off
+    q_off, k_off = _job_offsets(("window", B, kv_heads, group, window, Lq, q.stride()[:3], k.stride()[:2]),
+                                q.device, build)
     flags = ROUND_FLAGS[round_dtype] | _lib.HC_SCORE_SUM_WINDOW
     if causal:
         flags |= _lib.HC_SCORE_CAUSAL_WINDOW
     span = L - window if window_keep else L
-    out = ops.score(q, _dev_i64(q_off, q.device), q.stride(1), q.stride(2), k, _dev_i64(k_off, q.device), k.stride(2),
-                    L, group, window, span, pooling, kernel, scale, flags=flags, stream=stream)
-    return out.view(len(q_off), span)
+    out = ops.score(q, q_off, q.stride(1), q.stride(2), k, k_off, k.stride(2), L, group, window, span, pooling, kernel,
+                    scale, flags=flags, stream=stream)
+    return out.view(q_off.numel(), span)
 
 
 def cake_scores(q, k, window, gamma=200.0, round_dtype=None, scale=None, stream=None):
@@ -86,12 +107,14 @@ def cake_scores(q, k, window, gamma=200.0, round_dtype=None, scale=None, stream=
         raise ValueError("window longer than the query sequence")
     group = Hq // Hkv
     scale = 1.0 / math.sqrt(128) if scale is None else scale
-    q_off = [b * q.stride(0) + h * group * q.stride(1) + (Lq - window) * q.stride(2)
-             for b in range(B) for h in range(Hkv)]
-    k_off = [b * k.stride(0) + h * k.stride(1) for b in range(B) for h in range(Hkv)]
-    return ops.cake_score(q, _dev_i64(q_off, q.device), q.stride(1), q.stride(2), k, _dev_i64(k_off, q.device),
-                          k.stride(2), B, Hkv, L, group, window, scale, gamma, flags=ROUND_FLAGS[round_dtype],
-                          stream=stream)
+    def build():
+        q_off = [b * q.stride(0) + h * group * q.stride(1) + (Lq - window) * q.stride(2)
+                 for b in range(B) for h in range(Hkv)]
+        k_off = [b * k.stride(0) + h * k.stride(1) for b in range(B) for h in range(Hkv)]
+        return q_off, k_off
+    q_off, k_off = _job_offsets(("cake", B, Hkv, group, window, Lq, q.stride()[:3], k.stride()[:2]), q.device, build)
+    return ops.cake_score(q, q_off, q.stride(1), q.stride(2), k, k_off, k.stride(2), B, Hkv, L, group, window, scale,
+                          gamma, flags=ROUND_FLAGS[round_dtype], stream=stream)
 
 
 def last_query_scores(q, k, kv_heads, group, pooling="avgpool", kernel=5, round_dtype=None, scale=None, stream=None):

@@ -491,40 +491,105 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   }
 }
 
-// 256 consecutive positions of one (job, w') per workgroup; each query
-// head's strip and its pooling halo are staged in LDS once.
+// kPoolTile consecutive positions of one (job, w') per workgroup, four
+// consecutive ones per thread (one 16-byte load per query head); each head's
+// strip and its pooling halo are staged in LDS in turn.  Kernels up to
+// 2 * kPoolRegHalf + 1 pool from three 16-byte LDS reads held in registers;
+// wider ones walk the window in LDS.
 constexpr int kPoolThreads = 256;
+constexpr int kPoolTile = 4 * kPoolThreads;
 constexpr int kPoolMaxHalf = 31;
+constexpr int kPoolHalo = 32;     // >= kPoolMaxHalf, keeps the strip 16-byte aligned
+constexpr int kPoolRegHalf = 4;   // register path: kernel <= 9
+constexpr int kPoolHeads = 4;     // heads whose loads are in flight together
 
 __global__ __launch_bounds__(kPoolThreads) void score_pool_kernel(const float* __restrict__ A, int G, int span,
                                                                   int pooling, int kernel, int flags,
                                                                   float* __restrict__ S) {
-  __shared__ float s_a[kPoolThreads + 2 * kPoolMaxHalf];
-  const int t0 = blockIdx.x * kPoolThreads;
-  const int t = t0 + threadIdx.x;
+  __shared__ __align__(16) float s_a[kPoolTile + 2 * kPoolHalo];
+  const int t0 = blockIdx.x * kPoolTile;
   const int jw = blockIdx.y;  // job * wout + w'
   const int p = kernel / 2;
   const float pad = pooling == 0 ? 0.f : -INFINITY;
-  float best = -INFINITY;
-  for (int g = 0; g < G; ++g) {
-    const float* a = A + ((int64_t)jw * G + g) * span;
-    __syncthreads();
-    for (int i = threadIdx.x; i < kPoolThreads + 2 * p; i += kPoolThreads) {
-      const int u = t0 - p + i;
-      s_a[i] = (u >= 0 && u < span) ? a[u] : pad;
+  const int tb = t0 + 4 * threadIdx.x;
+  const bool vec_ok = (span & 3) == 0 && tb + 4 <= span;
+  // Halo of hw positions each side (at least kPoolRegHalf, so the register
+  // path reads only loaded values): threads [0, hw) load t0 - hw + x,
+  // threads [hw, 2hw) load t0 + kPoolTile + (x - hw).
+  const int hw = max(p, kPoolRegHalf);
+  const bool halo = threadIdx.x < 2 * hw;
+  const int th = threadIdx.x < hw ? t0 - hw + threadIdx.x : t0 + kPoolTile + (threadIdx.x - hw);
+  const int sh = threadIdx.x < hw ? kPoolHalo - hw + threadIdx.x : kPoolHalo + kPoolTile + (threadIdx.x - hw);
+  float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  for (int g0 = 0; g0 < G; g0 += kPoolHeads) {
+    f32x4 v[kPoolHeads];
+    float hv[kPoolHeads];
+#pragma unroll
+    for (int gg = 0; gg < kPoolHeads; ++gg) {
+      const int g = min(g0 + gg, G - 1);  // past G: a repeated (unused) head
+      const float* a = A + ((int64_t)jw * G + g) * span;
+      if (vec_ok) {
+        v[gg] = *reinterpret_cast<const f32x4*>(a + tb);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[gg][e] = tb + e < span ? a[tb + e] : pad;
+      }
+      hv[gg] = halo && th >= 0 && th < span ? a[th] : pad;
     }
-    __syncthreads();
-    float acc = pad;
-    for (int d = 0; d <= 2 * p; ++d) {
-      const float x = s_a[threadIdx.x + d];
-      acc = pooling == 0 ? acc + x : fmaxf(acc, x);
+#pragma unroll
+    for (int gg = 0; gg < kPoolHeads; ++gg) {
+      if (g0 + gg >= G) break;
+      __syncthreads();  // the previous strip has been pooled
+      *reinterpret_cast<f32x4*>(&s_a[kPoolHalo + 4 * threadIdx.x]) = v[gg];
+      if (halo) s_a[sh] = hv[gg];
+      __syncthreads();
+      float r[4];
+      if (p <= kPoolRegHalf) {
+        // w[i] = position 4*tid - 4 + i of the strip.
+        float w[12];
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(&s_a[kPoolHalo + 4 * threadIdx.x - 4 + 4 * c]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[4 * c + e] = x[e];
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float acc = pad;
+#pragma unroll
+          for (int d = -kPoolRegHalf; d <= kPoolRegHalf; ++d) {
+            const float x = w[4 + e + d];
+            const float y = pooling == 0 ? acc + x : fmaxf(acc, x);
+            acc = (d >= -p && d <= p) ? y : acc;
+          }
+          r[e] = acc;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float* win = s_a + kPoolHalo + 4 * threadIdx.x + e - p;
+          float acc = pad;
+          for (int d = 0; d <= 2 * p; ++d) acc = pooling == 0 ? acc + win[d] : fmaxf(acc, win[d]);
+          r[e] = acc;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float acc = pooling == 0 ? r[e] / (float)kernel : r[e];
+        best[e] = fmaxf(best[e], round_mode(acc, flags));
+      }
     }
-    if (pooling == 0) acc = acc / (float)kernel;
-    best = fmaxf(best, round_mode(acc, flags));
   }
-  if (t < span) {
-    float* o = S + (int64_t)jw * span + t;
-    *o = (flags & HC_SCORE_ACCUMULATE) ? *o + best : best;
+  float* o = S + (int64_t)jw * span + tb;
+  const bool acc_out = (flags & HC_SCORE_ACCUMULATE) != 0;
+  if (vec_ok) {
+    f32x4 b = {best[0], best[1], best[2], best[3]};
+    if (acc_out) b += *reinterpret_cast<const f32x4*>(o);
+    *reinterpret_cast<f32x4*>(o) = b;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (tb + e < span) o[e] = acc_out ? o[e] + best[e] : best[e];
   }
 }
 
@@ -768,7 +833,7 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
 #undef HC_PROBS_RM
 #undef HC_PROBS
     if ((rc = check_launch("hc_score(probs)"))) return rc;
-    hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + kPoolThreads - 1) / kPoolThreads, njobs * wout),
+    hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + kPoolTile - 1) / kPoolTile, njobs * wout),
                        dim3(kPoolThreads), 0, s, A, a.G, a.span, pooling, kernel, a.flags, scores);
     if ((rc = check_launch("hc_score(pool)"))) return rc;
   }
