@@ -35,6 +35,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--unfused-append", action="store_true", help="append in its own launch before attention")
+    p.add_argument("--no-graph", action="store_true",
+                   help="report the eager decode step (one host call per layer) instead of the HIP graph replay")
     p.add_argument("--full-steps", type=int, default=20, help="decode steps of the HeteroCache phase")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
     p.add_argument("--prefill-only", action="store_true",
@@ -293,6 +295,56 @@ def window_scoring_phase(args, torch, dev):
             "k_read_gbs": round(kbytes / ms / 1e6, 1), "window": W, "ctx": L}
 
 
+def time_decode_steps(torch, stores, q, kn, vn, outs, scale, steps, chunk=None, graph=False):
+    """Time `steps` decode steps; a step is, for every layer's store, the
+    fused append of one token per row plus the split-K attention and its
+    merge.  Eager: one host call per layer.  graph: the step captured once
+    in a HIP graph and replayed, with each layer's chunk size fixed and its
+    grid sized for the lengths the last replay reaches (surplus workgroups
+    exit), so no host work sits between the layers' kernels.  Returns (ms
+    per step, algorithmic K+V bytes attended over the timed steps)."""
+    from heterocache_amd import _lib, ops
+    len0 = [st.host_len.astype(np.int64).copy() for st in stores]
+    if graph:
+        lib = _lib.load()
+        G = q.shape[2]
+        cts, parts = [], []
+        for st in stores:
+            ct = chunk or ops.decode_chunk_tiles(st.host_len + 1, G, q.dtype)
+            cts.append(ct)
+            parts.append(ops.decode_num_parts(st.host_len + 1 + steps, ct))
+        rows = stores[0].rows
+        ws = torch.empty(max(lib.hc_decode_workspace_size(rows, G, n) for n in parts), dtype=torch.uint8,
+                         device=q.device)
+        g = torch.cuda.CUDAGraph()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g):
+            for layer, st in enumerate(stores):
+                st.attend(q[layer], scale, out=outs[layer], k_new=kn[layer], v_new=vn[layer], chunk_tiles=cts[layer],
+                          num_parts=parts[layer], workspace=ws)
+        run = g.replay
+    else:
+        def run():
+            for layer, st in enumerate(stores):
+                st.attend(q[layer], scale, out=outs[layer], k_new=kn[layer], v_new=vn[layer], chunk_tiles=chunk)
+    # One event pair per step on the launch stream (per-layer event records
+    # would themselves add gaps between the kernels they bracket).
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        ev[i][0].record()
+        run()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    if graph:
+        # Replays advance the device lengths only; bring the host mirrors along.
+        for st, l0 in zip(stores, len0):
+            st.sync_host_lengths(l0 + steps)
+    # Step i attends every row's stored tokens plus the one it appends.
+    nbytes = sum(int((l0 + i + 1).sum()) * st.bytes_per_token() for st, l0 in zip(stores, len0) for i in range(steps))
+    return [a.elapsed_time(b) for a, b in ev], nbytes
+
+
 def decode_configs_phase(args, torch, dev):
     """Decode attention (fused append + split-K + merge per layer, all layers
     of a step) on the other decode workloads: a Qwen2.5-7B-shaped batch of
@@ -324,7 +376,7 @@ def decode_configs_phase(args, torch, dev):
                 lens = np.asarray([n for L in contexts for n in qwen_budgets(layer, L)], dtype=np.int64)
             else:
                 lens = np.concatenate([workloads.row_budgets(data, layer, L, ratio, NL, Hkv)[0] for L in contexts])
-            st = KVStore(lens + steps + warm + 2, torch.bfloat16, dev)
+            st = KVStore(lens + 2 * steps + warm + 2, torch.bfloat16, dev)
             st.k.normal_()
             st.v.normal_()
             st.set_lengths(lens)
@@ -336,28 +388,18 @@ def decode_configs_phase(args, torch, dev):
         o = [torch.empty((rows, G, D), dtype=torch.bfloat16, device=dev) for _ in range(NL)]
         scale = 1.0 / math.sqrt(D)
 
-        def step():
-            for layer, st in enumerate(stores):
-                st.attend(q[layer], scale, out=o[layer], k_new=kn[layer], v_new=vn[layer])
-
-        for _ in range(warm):
-            step()
-        torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-        nbytes = 0
-        for i in range(steps):
-            ev[i][0].record()
-            step()
-            ev[i][1].record()
-            nbytes += sum(st.kv_bytes() for st in stores)
-        torch.cuda.synchronize()
-        ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
-        per_launch = nbytes / (steps * NL) + 2 * rows * G * D * 2
-        us = ms * 1e3 / NL
-        gbs = per_launch / (us * 1e-6) / 1e9
-        out[name] = {"contexts": contexts, "layers": NL, "kv_rows": rows, "group": G, "ratio": ratio,
-                     "us_per_layer": round(us, 3), "bytes_per_layer": int(per_launch), "gbs": round(gbs, 1),
-                     "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        time_decode_steps(torch, stores, q, kn, vn, o, scale, warm)
+        res = {"contexts": contexts, "layers": NL, "kv_rows": rows, "group": G, "ratio": ratio}
+        for mode in ("graph", "eager"):
+            ms_steps, nbytes = time_decode_steps(torch, stores, q, kn, vn, o, scale, steps, graph=mode == "graph")
+            per_launch = nbytes / (steps * NL) + 2 * rows * G * D * 2
+            us = float(np.mean(ms_steps)) * 1e3 / NL
+            gbs = per_launch / (us * 1e-6) / 1e9
+            sfx = "" if mode == "graph" else "_eager"
+            res.update({"us_per_layer" + sfx: round(us, 3), "gbs" + sfx: round(gbs, 1),
+                        "frac_of_hbm_peak" + sfx: round(gbs / HBM_PEAK_GBS, 4)})
+            res["bytes_per_layer"] = int(per_launch)
+        out[name] = res
         del stores, q, kn, vn, o
         torch.cuda.empty_cache()
     return out
@@ -511,7 +553,7 @@ def main():
     torch.manual_seed(args.seed)
     L, Hkv, G, D = args.ctx, 8, 4, 128
     data = workloads.synthetic_head_json(args.layers, Hkv, args.seed)
-    max_gen = args.warmup + args.steps + 8
+    max_gen = args.warmup + 2 * args.steps + 8
     stores, budgets = [], []
     for layer in range(args.layers):
         lens, base = workloads.row_budgets(data, layer, L, args.ratio, args.layers, Hkv)
@@ -528,34 +570,44 @@ def main():
     outs = [torch.empty((Hkv, G, D), dtype=torch.bfloat16, device=dev) for _ in range(args.layers)]
     scale = 1.0 / math.sqrt(D)
 
-    def step():
-        # One layer = the fused append + split-K attention launch and its merge.
-        for layer, st in enumerate(stores):
-            if args.unfused_append:
+    if args.unfused_append:
+        def step():
+            # One layer = the append, then the split-K attention and its merge.
+            for layer, st in enumerate(stores):
                 st.append(kn[layer], vn[layer])
                 st.attend(q[layer], scale, out=outs[layer], chunk_tiles=chunk)
-            else:
-                st.attend(q[layer], scale, out=outs[layer], k_new=kn[layer], v_new=vn[layer], chunk_tiles=chunk)
-
-    for _ in range(args.warmup):
-        step()
+        for _ in range(args.warmup):
+            step()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+        attn_bytes = 0
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for s in range(args.steps):
+            ev[s][0].record()
+            step()
+            ev[s][1].record()
+            attn_bytes += sum(st.kv_bytes() for st in stores)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        step_ms = [e0.elapsed_time(e1) for (e0, e1) in ev]
+        eager_ms = None
+    else:
+        time_decode_steps(torch, stores, q, kn, vn, outs, scale, args.warmup, chunk=chunk)
+        # Eager (one host call per layer) first, then the same step as a HIP
+        # graph replay, which is the figure reported: the kernels are the
+        # same, the replay only removes host launch work between them.
+        eager_steps, _ = time_decode_steps(torch, stores, q, kn, vn, outs, scale, args.steps, chunk=chunk)
+        eager_ms = float(np.mean(eager_steps))
+        if args.no_graph:
+            step_ms, attn_bytes = eager_steps, _
+            wall = None
+        else:
+            t0 = time.perf_counter()
+            step_ms, attn_bytes = time_decode_steps(torch, stores, q, kn, vn, outs, scale, args.steps, chunk=chunk,
+                                                    graph=True)
+            wall = time.perf_counter() - t0
     torch.cuda.synchronize()
 
-    # One event pair per step on the launch stream (per-layer event records
-    # would themselves add gaps between the kernels they bracket).
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    attn_bytes = 0
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for s in range(args.steps):
-        ev[s][0].record()
-        step()
-        ev[s][1].record()
-        attn_bytes += sum(st.kv_bytes() for st in stores)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-
-    step_ms = [e0.elapsed_time(e1) for (e0, e1) in ev]
     us_layer = float(np.mean(step_ms)) * 1e3 / args.layers
     # Algorithmic bytes per layer: every retained K and V row once (the new
     # token included), plus queries and outputs.
@@ -571,7 +623,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
-        "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "wall_ms_per_step": round(wall * 1e3 / args.steps, 4) if wall is not None else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -580,8 +632,11 @@ def main():
         "config": {"workload": f"decode step, Llama-3-8B shape, {L} ctx, ratio {args.ratio}, batch 1, "
                                f"{args.layers} layers, 8 KV rows x GQA 4, head_dim 128",
                    "ctx": L, "layers": args.layers, "kv_heads": Hkv, "q_heads": Hkv * G, "head_dim": D,
-                   "ratio": args.ratio, "batch": 1, "chunk_tiles": chunk or "auto"},
+                   "ratio": args.ratio, "batch": 1, "chunk_tiles": chunk or "auto",
+                   "launch": "one HIP graph replay per step" if not (args.no_graph or args.unfused_append)
+                   else "one host call per layer"},
         "us_per_layer": round(us_layer, 3),
+        "us_per_layer_eager": round(eager_ms * 1e3 / args.layers, 3) if eager_ms is not None else None,
         "pct_of_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),

@@ -99,14 +99,17 @@ def decode_chunk_tiles(host_row_len, group, dtype):
 
 
 def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, out=None, row_order=None,
-                k_new=None, v_new=None, chunk_tiles=None, stream=None, workspace=None):
+                k_new=None, v_new=None, chunk_tiles=None, stream=None, workspace=None, num_parts=None):
     """out[r, g] = softmax(scale * q[r, g] . K_r^T) V_r over row_len[r] tokens.
 
     q: [rows, G, 128]; host_row_len: host copy of the lengths (sizes the grid).
     With k_new/v_new [rows, 128] the new token is appended and attended in the
     same launch; row_len advances by one (the caller advances its mirror).
     chunk_tiles: tiles per workgroup; None picks the one-round chunk for
-    these lengths.
+    these lengths.  num_parts: grid size, at least what these lengths need;
+    a larger grid (surplus workgroups exit at once) lets a captured HIP graph
+    replay while the device lengths grow.  workspace: a uint8 device tensor
+    of at least hc_decode_workspace_size bytes (default: a shared buffer).
     """
     lib = _lib.load()
     _require_cuda(q, kstore, vstore, row_tile_off, row_len, row_order, k_new, v_new)
@@ -139,6 +142,10 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
     if chunk_tiles is None:
         chunk_tiles = decode_chunk_tiles(host_row_len, G, q.dtype)
     nparts = decode_num_parts(host_row_len, chunk_tiles)
+    if num_parts is not None:
+        if int(num_parts) < nparts:
+            raise ValueError(f"num_parts {num_parts} is below the {nparts} parts these lengths need")
+        nparts = int(num_parts)
     nbytes = lib.hc_decode_workspace_size(rows, G, nparts)
     ws = workspace if workspace is not None else WORKSPACE.get(q.device, nbytes)
     _lib.check(lib.hc_decode_attn(dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),

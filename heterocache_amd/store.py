@@ -96,6 +96,16 @@ class KVStore:
         self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
         self.row_order = torch.as_tensor(order).to(self.device)
 
+    def sync_host_lengths(self, lens):
+        """Set the host mirror to lengths the device already holds (after HIP
+        graph replays of attend/append advanced row_len on the device); the
+        device lengths and the row order are left as they are."""
+        lens = np.asarray(lens, dtype=np.int64)
+        if lens.shape != (self.rows,) or (lens > self.host_cap).any() or (lens < 0).any():
+            raise RuntimeError("row lengths outside their capacity")
+        self.host_len[:] = lens
+        self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
+
     # -- writers -----------------------------------------------------------
     def plan_rows(self, src_k, src_bh, rows, counts, idx=None, idx_rows=None, trig_of=None):
         """Validate a gather and build its device metadata (see write_rows).
@@ -203,18 +213,22 @@ class KVStore:
         return ops.store_read(self.k, self.v, self.row_tile_off, rows, count)
 
     def attend(self, q, scale, out=None, k_new=None, v_new=None, chunk_tiles=None,
-               stream=None):
+               stream=None, num_parts=None, workspace=None):
         """Decode attention of q [rows, G, 128] over every row's tokens.
 
         With k_new / v_new [rows, 128] the decode append happens in the same
         launch: the new token is attended, stored at slot len and every
-        length advances by one.
+        length advances by one.  num_parts / workspace: see ops.decode_attn
+        (a fixed chunk_tiles, a num_parts covering the longest lengths to
+        come and an explicit workspace make the call capturable in a HIP
+        graph; a replay advances the device lengths, not this object's host
+        mirror).
         """
         if k_new is not None:
             self._check_room()
         out = ops.decode_attn(q, self.k, self.v, self.row_tile_off, self.row_len, self.host_len, scale, out=out,
                               row_order=self.row_order, k_new=k_new, v_new=v_new, chunk_tiles=chunk_tiles,
-                              stream=stream)
+                              stream=stream, workspace=workspace, num_parts=num_parts)
         if k_new is not None:
             self.host_len += 1
             self._headroom -= 1

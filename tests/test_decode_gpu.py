@@ -181,3 +181,59 @@ def test_auto_chunk_fits_one_round(dev):
     assert ops.decode_chunk_tiles(many, 4, torch.bfloat16) == 128
     lens = np.asarray([10], dtype=np.int32)
     assert _lib.load().hc_decode_chunk_tiles(9, lens.ctypes.data_as(ctypes.c_void_p), 1, 4) == _lib.HC_ERR_INVALID
+
+
+def test_graph_replays_match_eager_steps(dev):
+    """The decode step (fused append + attention over two stores) captured
+    in a HIP graph with fixed chunk sizes and grids sized for the lengths
+    the last replay reaches: each of several replays, with new inputs
+    written eagerly in between, equals the same step run eagerly with the
+    same chunk sizes (bitwise), and the stores end up identical."""
+    from heterocache_amd import _lib, ops
+    steps, G = 5, 4
+    lens = [[0, 31, 700, 5000, 33], [1, 1024, 12000, 64, 2047]]
+    tdt = torch.bfloat16
+    rng = np.random.default_rng(91)
+    graph_stores, eager_stores = [], []
+    for ls in lens:
+        ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(tdt).to(dev) for L in ls]
+        vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(tdt).to(dev) for L in ls]
+        for group in (graph_stores, eager_stores):
+            st = KVStore([L + steps for L in ls], tdt, dev)
+            fill_store(st, ks, vs, dev)
+            group.append(st)
+    rows = len(lens[0])
+    q = torch.zeros((2, rows, G, 128), dtype=tdt, device=dev)
+    kn = torch.zeros((2, rows, 128), dtype=tdt, device=dev)
+    vn = torch.zeros_like(kn)
+    out_g = torch.empty((2, rows, G, 128), dtype=tdt, device=dev)
+    out_e = torch.empty_like(out_g)
+    scale = 1 / math.sqrt(128)
+    cts = [ops.decode_chunk_tiles(st.host_len + 1, G, tdt) for st in graph_stores]
+    parts = [ops.decode_num_parts(st.host_len + steps, ct) for st, ct in zip(graph_stores, cts)]
+    ws = torch.empty(max(_lib.load().hc_decode_workspace_size(rows, G, n) for n in parts), dtype=torch.uint8,
+                     device=dev)
+    len0 = [st.host_len.astype(np.int64).copy() for st in graph_stores]
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        for i, st in enumerate(graph_stores):
+            st.attend(q[i], scale, out=out_g[i], k_new=kn[i], v_new=vn[i], chunk_tiles=cts[i], num_parts=parts[i],
+                      workspace=ws)
+    for s in range(steps):
+        q.copy_(torch.as_tensor(rng.standard_normal(tuple(q.shape)), dtype=torch.float32).to(tdt))
+        kn.copy_(torch.as_tensor(rng.standard_normal(tuple(kn.shape)), dtype=torch.float32).to(tdt))
+        vn.copy_(torch.as_tensor(rng.standard_normal(tuple(vn.shape)), dtype=torch.float32).to(tdt))
+        graph.replay()
+        for i, st in enumerate(eager_stores):
+            st.attend(q[i], scale, out=out_e[i], k_new=kn[i], v_new=vn[i], chunk_tiles=cts[i])
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), f"replay {s}"
+        assert not torch.isnan(out_g.float()).any()
+    for st, l0, ref in zip(graph_stores, len0, eager_stores):
+        st.sync_host_lengths(l0 + steps)
+        assert st.row_len.tolist() == ref.row_len.tolist() == (l0 + steps).tolist()
+        for r in range(rows):
+            ka, va = st.read_rows([r], int(l0[r]) + steps)
+            kb, vb = ref.read_rows([r], int(l0[r]) + steps)
+            assert torch.equal(ka, kb) and torch.equal(va, vb)
