@@ -748,10 +748,14 @@ static int resident_wgs(const void* fn, size_t lds) {
 }
 
 // Chunks per workgroup so that one resident round of workgroups covers the
-// njobs * nchunks chunks (each workgroup then streams its chunks with the
-// next one's keys in flight); sets a.cpw, returns the grid's x extent.
-static int plan_chunks(const void* fn, size_t lds, int njobs, int nchunks, ScoreArgs& a) {
-  const int slots = resident_wgs(fn, lds);
+// njobs * nchunks chunks (queries staged once per workgroup); sets a.cpw,
+// returns the grid's x extent.  The statistics pass that also stores every
+// logit takes one chunk per workgroup (multi = false), measured faster
+// there: vmcnt counts stores as well as loads, so a workgroup's wait for its
+// next chunk's keys also waits for its previous chunk's 4R-byte-per-token
+// stores, while a finished workgroup leaves them draining behind the next.
+static int plan_chunks(const void* fn, size_t lds, int njobs, int nchunks, ScoreArgs& a, bool multi = true) {
+  const int slots = multi ? resident_wgs(fn, lds) : 0;
   const int64_t total = (int64_t)njobs * nchunks;
   a.cpw = slots > 0 ? (int)std::max<int64_t>(1, (total + slots - 1) / slots) : 1;
   return (nchunks + a.cpw - 1) / a.cpw;
@@ -775,7 +779,7 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   do {                                                                                                      \
     auto fn = score_stats_kernel<T, STORE, RM, LG>;                                                         \
     ScoreArgs as = a;                                                                                       \
-    nparts = plan_chunks(reinterpret_cast<const void*>(fn), lds1, njobs, nchunks, as);                      \
+    nparts = plan_chunks(reinterpret_cast<const void*>(fn), lds1, njobs, nchunks, as, !LG);                 \
     hipLaunchKernelGGL(fn, dim3(nparts, njobs), dim3(kScoreWaves * 64), lds1, s, as, part, LG ? A : nullptr); \
   } while (0)
   if (via_logits) {
