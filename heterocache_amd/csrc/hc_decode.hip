@@ -390,10 +390,13 @@ constexpr int kMergeSlice = 16;
 constexpr int kMergeGroups = 16;
 constexpr int kMergeThreads = kMergeSlice * kMergeGroups;
 
+// A row whose part range lies outside this launch's grid_parts partials
+// (flagged np = -1 by an undersized grid, or left stale because no
+// workgroup of this launch reached the row) is written as NaN.
 template <typename T>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml, const int* __restrict__ row_info, int G,
-    int* __restrict__ row_len, int advance, T* __restrict__ out) {
+    int64_t grid_parts, int* __restrict__ row_len, int advance, T* __restrict__ out) {
   constexpr int kBatch = 8;  // parts per thread whose loads are in flight together
   const int row = blockIdx.x, qq = blockIdx.y, d0 = blockIdx.z * kMergeSlice;
   const int tid = threadIdx.x;
@@ -402,7 +405,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   __shared__ float s_o[kMergeGroups][kMergeSlice];
   T* o = out + ((int64_t)row * G + qq) * HC_HEAD_DIM + d0;
   if (advance && qq == 0 && blockIdx.z == 0 && tid == 0) row_len[row] += 1;
-  if (np < 0) {
+  if (np < 1 || p0 < 0 || (int64_t)p0 + np > grid_parts) {
     if (tid < kMergeSlice) o[tid] = Elem<T>::from_f32(NAN);
     return;
   }
@@ -513,7 +516,7 @@ static int launch_decode(const void* q, void* kstore, void* vstore, const int64_
   int rc = check_launch("hc_decode_attn(partial)");
   if (rc) return rc;
   hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(rows, G, HC_HEAD_DIM / kMergeSlice),
-                     dim3(kMergeSlice * kMergeGroups), 0, stream, part_o, part_ml, row_info, G, row_len,
+                     dim3(kMergeSlice * kMergeGroups), 0, stream, part_o, part_ml, row_info, G, grid_parts, row_len,
                      k_new ? 1 : 0, (T*)out);
   return check_launch("hc_decode_attn(merge)");
 }

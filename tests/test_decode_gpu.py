@@ -237,3 +237,33 @@ def test_graph_replays_match_eager_steps(dev):
             ka, va = st.read_rows([r], int(l0[r]) + steps)
             kb, vb = ref.read_rows([r], int(l0[r]) + steps)
             assert torch.equal(ka, kb) and torch.equal(va, vb)
+
+
+def test_undersized_grid_gives_nan_rows(dev):
+    """hc_decode_attn called (through the C ABI, which the Python wrapper
+    would refuse) with fewer workgroups than the lengths need: no partial is
+    written, every row comes out NaN rather than a silently partial result,
+    and the lengths are untouched (no append)."""
+    from heterocache_amd import _lib, ops
+    lens, G = [5000, 3000, 40], 4
+    rng = np.random.default_rng(5)
+    ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    store = KVStore(lens, torch.bfloat16, dev)
+    fill_store(store, ks, vs, dev)
+    q = torch.randn((len(lens), G, 128), device=dev).to(torch.bfloat16)
+    out = torch.zeros_like(q)
+    chunk = 4
+    need = ops.decode_num_parts(store.host_len, chunk)
+    small = 10
+    assert need > small
+    lib = _lib.load()
+    ws = torch.zeros(lib.hc_decode_workspace_size(len(lens), G, small), dtype=torch.uint8, device=dev)
+    rc = lib.hc_decode_attn(ops.dtype_code(q.dtype), q.data_ptr(), store.k.data_ptr(), store.v.data_ptr(),
+                            store.row_tile_off.data_ptr(), store.row_len.data_ptr(), store.row_order.data_ptr(),
+                            len(lens), G, 1 / math.sqrt(128), None, None, out.data_ptr(), ws.data_ptr(), ws.numel(),
+                            small, chunk, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0
+    assert torch.isnan(out.float()).all()
+    assert store.row_len.tolist() == lens
