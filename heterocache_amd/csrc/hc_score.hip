@@ -14,15 +14,19 @@
 // (HC_SCORE_ROUND_BF16 / _F16); by default everything stays float32.
 //
 // Phases (all launched by hc_score):
-//  1. score_stats_kernel: per (job, 256-token chunk) the logits of all
-//     G*W query rows against 16-token key sub-tiles on the MFMA (K is the A
-//     operand, loaded straight from HBM; queries are B operands staged in
-//     LDS), reduced to a running (max, sum exp) per row.
-//  2. score_stats_merge_kernel: fold the chunks' (max, sum) per row.
-//  3. score_probs_kernel: recompute the logits, normalise, sum over the
-//     window rows of each query head (xor-shuffle tree: fixed order), write
-//     A[job][w'][g][t].
-//  4. score_pool_kernel: pooling over t and max over g -> S[job][w'][t].
+//  1. score_stats_kernel: per (job, run of 256-token chunks) the logits of
+//     all G*W query rows against 16-token key sub-tiles on the MFMA (K is
+//     the A operand, loaded straight from HBM; queries are B operands staged
+//     in LDS once per workgroup), reduced to a (max, sum exp) per row; with
+//     fewer than 32 rows the logits are stored too.
+//  2. score_stats_merge_kernel: fold the workgroups' (max, sum) per row.
+//  3a. (>= 32 rows) score_probs_kernel: recompute the logits, normalise, sum
+//     over the window rows of each query head (xor-shuffle tree: fixed
+//     order), write A[job][w'][g][t]; score_pool_kernel: pooling over t and
+//     max over g -> S[job][w'][t].
+//  3b. (< 32 rows) score_finish_kernel: the same from the stored logits.
+// CAKE scoring (hc_cake_score) runs phases 1-2, the probability pass with
+// window moments, and its own pooling and reductions.
 #include <cfloat>
 #include <algorithm>
 #include <cmath>
