@@ -173,6 +173,7 @@ class HeteroCache(DynamicCache):
         self._arena = None
         self._tile_table = None      # int64 arena tile offsets of all rows, layer-major
         self._qbuf_all = None        # [NL, B, Hq, S, 128] buffered decode queries
+        self._qbuf_index = {}        # layers of a batched query gather -> device index
         self._ref_bits_all = None    # [leaders * B, words] pivot reference sets
         self._trigger_all = None     # [leaders] int32 drift flags
         self._lead_base = None       # first global leader index of each layer
@@ -517,12 +518,29 @@ class HeteroCache(DynamicCache):
             self._flush_checks()
 
     def _gather_queries(self, layers):
-        """Buffered step queries of these layers -> qbuf [B, Hq, S, 128] each
-        (one stack launch per layer)."""
+        """Buffered step queries of these layers -> qbuf [B, Hq, S, 128] each.
+        With one-token queries all layers take one concatenation and one
+        indexed copy into the model-wide buffer instead of one stack per
+        layer (host launch time between those was idle GPU time)."""
+        S = self.decode_step
+        lists = []
         for layer in layers:
             st = self._drift[layer]
-            qs, st.qlist = st.qlist, []
-            torch.stack([q[:, :, -1] for q in qs], dim=2, out=st.qbuf)
+            lists.append(st.qlist)
+            st.qlist = []
+        one_token = all(len(qs) == S and qs[0].shape[2] == 1 for qs in lists)
+        if self._qbuf_all is not None and one_token and len(layers) > 1:
+            flat = torch.cat([q for qs in lists for q in qs], dim=2)        # [B, Hq, n*S, 128]
+            B, H, _, D = flat.shape
+            src = flat.view(B, H, len(layers), S, D).permute(2, 0, 1, 3, 4)  # [n, B, Hq, S, 128]
+            key = tuple(layers)
+            idx = self._qbuf_index.get(key)
+            if idx is None:
+                idx = self._qbuf_index[key] = torch.tensor(layers, dtype=torch.int64).to(flat.device)
+            self._qbuf_all.index_copy_(0, idx, src)
+            return
+        for layer, qs in zip(layers, lists):
+            torch.stack([q[:, :, -1] for q in qs], dim=2, out=self._drift[layer].qbuf)
 
     def _flush_checks(self):
         """Run the deferred checks: one batched launch sequence when they are
