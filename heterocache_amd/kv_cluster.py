@@ -340,7 +340,9 @@ class CAKECluster:
             return past_key_values
         W = self.window_size
         flat = scores.reshape(B * Hkv, n)
-        idx, counts = compress.select_kept(flat, [budget + W] * (B * Hkv), window=W, max_cap=budget + W)
+        # Budgets filled on the device: a host list would cost a blocking copy per eviction.
+        caps = torch.full((B * Hkv,), budget + W, dtype=torch.int32, device=flat.device)
+        idx, counts = compress.select_kept(flat, caps, window=W, max_cap=budget + W)
         k, v = ops.gather_rows(past_key_values.key_cache[layer_idx], past_key_values.value_cache[layer_idx], idx,
                                counts)
         past_key_values.key_cache[layer_idx] = k

@@ -275,6 +275,24 @@ def prefill_attn(q, k, v, scale, out=None, stream=None):
     return out
 
 
+# Per-(batch, head) element offsets of gather_rows depend only on shapes and
+# strides: built and copied to the device once per layout.
+_ROW_OFFSETS = {}
+
+
+def _row_offsets(B, H, src_strides, dst_strides, device):
+    key = (str(device), B, H, tuple(src_strides[:2]), tuple(dst_strides[:2]))
+    hit = _ROW_OFFSETS.get(key)
+    if hit is None:
+        if len(_ROW_OFFSETS) >= 256:
+            _ROW_OFFSETS.clear()
+        bh = np.arange(B * H, dtype=np.int64)
+        hit = _ROW_OFFSETS[key] = (
+            torch.as_tensor((bh // H) * src_strides[0] + (bh % H) * src_strides[1]).to(device),
+            torch.as_tensor((bh // H) * dst_strides[0] + (bh % H) * dst_strides[1]).to(device))
+    return hit
+
+
 def gather_rows(src_k, src_v, idx, counts, dst_k=None, dst_v=None, stream=None):
     """dst[b, h, t] = src[b, h, idx[b*H + h, t]] for t < counts[b*H + h].
 
@@ -305,9 +323,7 @@ def gather_rows(src_k, src_v, idx, counts, dst_k=None, dst_v=None, stream=None):
         raise ValueError("counts must be int32 [B*H]")
     if width == 0 or B * H == 0:
         return dst_k, dst_v
-    bh = np.arange(B * H, dtype=np.int64)
-    src_off = torch.as_tensor((bh // H) * src_k.stride(0) + (bh % H) * src_k.stride(1)).to(src_k.device)
-    dst_off = torch.as_tensor((bh // H) * dst_k.stride(0) + (bh % H) * dst_k.stride(1)).to(src_k.device)
+    src_off, dst_off = _row_offsets(B, H, src_k.stride(), dst_k.stride(), src_k.device)
     _lib.check(lib.hc_gather_rows(dtype_code(src_k.dtype), _ptr(src_k), _ptr(src_v), _ptr(src_off), src_k.stride(2), L,
                                   _ptr(idx), idx.stride(0), _ptr(dst_k), _ptr(dst_v), _ptr(dst_off), dst_k.stride(2),
                                   _ptr(counts), B * H, width, _stream(stream, src_k)))
