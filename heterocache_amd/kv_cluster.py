@@ -174,10 +174,11 @@ class H2OKVCluster:
         for w in ([tail // 16 * 16] if tail >= 16 else []) + [b for b in (8, 4, 2, 1) if tail % 16 & b]:
             blocks.append((s, w))
             s += w
-        for s, w in blocks:
-            q_off = torch.as_tensor([o + s * query_states.stride(2) for o in base],
-                                    dtype=torch.int64).to(query_states.device)
-            ops.score(query_states, q_off, query_states.stride(1), query_states.stride(2), key_states, k_off,
+        # Every block's query offsets in one host-to-device copy.
+        q_offs = torch.as_tensor(np.asarray([[o + s * query_states.stride(2) for o in base] for s, _ in blocks],
+                                            dtype=np.int64)).to(query_states.device)
+        for i, (s, w) in enumerate(blocks):
+            ops.score(query_states, q_offs[i], query_states.stride(1), query_states.stride(2), key_states, k_off,
                       key_states.stride(2), L, 1, w, L, "avgpool", 1, 1.0 / math.sqrt(D),
                       flags=flags | (_lib.HC_SCORE_ACCUMULATE if s else 0), out=scores)
         return scores.view(B * H, L)
