@@ -398,8 +398,8 @@ class HeteroCache(DynamicCache):
         else:
             src = [pivots.index(h) for h in leaders]
         # Score rows are (b, pivot position); reorder them to (leader, b).
-        order = torch.tensor([self._score_row(b, s, len(pivots)) for s in src for b in range(self.bsz)],
-                             dtype=torch.long, device=idx.device)
+        order = ops.to_device([self._score_row(b, s, len(pivots)) for s in src for b in range(self.bsz)], idx.device,
+                              torch.long)
         if self._ref_bits_all is None:
             self._init_drift_buffers(idx.device, L)
         lb, B = self._lead_base[layer_idx], self.bsz

@@ -35,7 +35,7 @@ def _check_qk(q, k):
 
 
 def _dev_i64(vals, device):
-    return torch.tensor(list(vals), dtype=torch.int64).to(device)
+    return ops.to_device(list(vals), device, torch.int64)
 
 
 # Per-job element offsets depend only on shapes and strides, not on the data:
@@ -128,7 +128,7 @@ def pivot_step_metadata(q_steps, store, rows, heads, group):
     B = q_steps.shape[0]
     hkv = store.rows // B
     q_off = [(r // hkv) * q_steps.stride(0) + h * group * q_steps.stride(1) for r, h in zip(rows, heads)]
-    return _dev_i64(q_off, q_steps.device), torch.tensor(list(rows), dtype=torch.int32).to(q_steps.device)
+    return _dev_i64(q_off, q_steps.device), ops.to_device(list(rows), q_steps.device, torch.int32)
 
 
 def pivot_step_scores(q_steps, store, rows, heads, group, seq_len, pooling="avgpool", kernel=5, round_dtype=None,
@@ -160,7 +160,7 @@ def select_kept(scores, caps, window=0, max_cap=None, stream=None):
     jobs, span = scores.shape
     if not torch.is_tensor(caps):
         caps_list = [int(c) for c in caps]
-        caps = torch.tensor(caps_list, dtype=torch.int32).to(scores.device)
+        caps = ops.to_device(caps_list, scores.device, torch.int32)
         if max_cap is None:
             max_cap = max(caps_list) if caps_list else 0
     width = max(1, min(max_cap if max_cap is not None else span + window, span + window))

@@ -24,6 +24,18 @@ def dtype_code(dt):
         raise TypeError(f"unsupported dtype {dt}; expected float32, float16 or bfloat16") from None
 
 
+def to_device(values, device, dtype=None):
+    """Small host metadata (a list or numpy array) as a device tensor without
+    a host sync: staged in pinned memory (torch's caching host allocator)
+    and copied asynchronously on the current stream.  A plain .to(device)
+    of pageable memory synchronises the stream, draining the GPU at every
+    metadata copy."""
+    t = torch.as_tensor(np.asarray(values), dtype=dtype)
+    if t.device.type != "cpu":
+        return t.to(device)
+    return t.pin_memory().to(device, non_blocking=True)
+
+
 def _ptr(t):
     # ctypes passes a Python int (or None) for a c_void_p argument as is.
     return t.data_ptr() if t is not None else None
@@ -287,9 +299,8 @@ def _row_offsets(B, H, src_strides, dst_strides, device):
         if len(_ROW_OFFSETS) >= 256:
             _ROW_OFFSETS.clear()
         bh = np.arange(B * H, dtype=np.int64)
-        hit = _ROW_OFFSETS[key] = (
-            torch.as_tensor((bh // H) * src_strides[0] + (bh % H) * src_strides[1]).to(device),
-            torch.as_tensor((bh // H) * dst_strides[0] + (bh % H) * dst_strides[1]).to(device))
+        hit = _ROW_OFFSETS[key] = (to_device((bh // H) * src_strides[0] + (bh % H) * src_strides[1], device),
+                                   to_device((bh // H) * dst_strides[0] + (bh % H) * dst_strides[1], device))
     return hit
 
 

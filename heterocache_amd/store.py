@@ -89,12 +89,12 @@ class KVStore:
         if (lens > self.host_cap[rows]).any() or (lens < 0).any():
             raise RuntimeError("row length outside its capacity")
         self.host_len[rows] = lens
-        idx = torch.as_tensor(rows, dtype=torch.int64).to(self.device)
-        self.row_len.index_copy_(0, idx, torch.as_tensor(lens, dtype=torch.int32).to(self.device))
+        idx = ops.to_device(rows, self.device, torch.int64)
+        self.row_len.index_copy_(0, idx, ops.to_device(lens, self.device, torch.int32))
         # Longest rows are scheduled first; appends keep this order.
         order = np.argsort(-self.host_len.astype(np.int64), kind="stable").astype(np.int32)
         self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
-        self.row_order = torch.as_tensor(order).to(self.device)
+        self.row_order = ops.to_device(order, self.device)
 
     def sync_host_lengths(self, lens):
         """Set the host mirror to lengths the device already holds (after HIP
@@ -149,14 +149,14 @@ class KVStore:
                 raise ValueError("idx_rows must name one index row per job")
             if (counts > idx.shape[1]).any():
                 raise ValueError("count exceeds the index list")
-            idx_off = torch.as_tensor(r * idx.stride(0)).to(dev)
+            idx_off = ops.to_device(r * idx.stride(0), dev)
         if trig_of is not None:
-            trig_of = torch.as_tensor(np.asarray(trig_of, dtype=np.int32)).to(dev)
-        return {"src_off": torch.as_tensor(src_off).to(dev), "tok_stride": tok_stride, "src_len": L,
+            trig_of = ops.to_device(np.asarray(trig_of, dtype=np.int32), dev)
+        return {"src_off": ops.to_device(src_off, dev), "tok_stride": tok_stride, "src_len": L,
                 "trig_of": trig_of,
                 "shape": tuple(src_k.shape), "stride": tuple(src_k.stride()), "idx_off": idx_off,
-                "counts": torch.as_tensor(counts, dtype=torch.int32).to(dev), "host_counts": counts,
-                "rows": torch.as_tensor(rows, dtype=torch.int32).to(dev), "host_rows": rows,
+                "counts": ops.to_device(counts, dev, torch.int32), "host_counts": counts,
+                "rows": ops.to_device(rows, dev, torch.int32), "host_rows": rows,
                 "max_count": int(counts.max())}
 
     def launch_rows(self, plan, src_k, src_v, idx=None, src_is_host=False, stream=None, trigger=None,
