@@ -83,7 +83,7 @@ def _intersections(lists, k, sets, nbits, ref_of):
     words = max((nbits + 31) // 32, 1)
     bits = torch.zeros((sets.shape[0], words), dtype=torch.int32, device=dev)
     ops.set_bits(sets, None, bits, nbits, fixed_count=k)
-    ref = torch.as_tensor(np.asarray(ref_of, dtype=np.int32)).to(dev)
+    ref = ops.to_device(np.asarray(ref_of, dtype=np.int32), dev)
     return ops.overlap_count(lists, k, bits, nbits, ref_of=ref).cpu().numpy()
 
 
@@ -235,8 +235,8 @@ class AttentionRecorder:
         q_off = [b * q.stride(0) + h * q.stride(1) + (Lq - 1) * q.stride(2) for b in range(B) for h in range(Hq)]
         k_off = [b * k.stride(0) + (h // G) * k.stride(1) for b in range(B) for h in range(Hq)]
         dev = q.device
-        probs = ops.score(q, torch.tensor(q_off, dtype=torch.int64).to(dev), q.stride(1), q.stride(2), k,
-                          torch.tensor(k_off, dtype=torch.int64).to(dev), k.stride(2), L, 1, 1, L, "avgpool", 1,
+        probs = ops.score(q, ops.to_device(q_off, dev, torch.int64), q.stride(1), q.stride(2), k,
+                          ops.to_device(k_off, dev, torch.int64), k.stride(2), L, 1, 1, L, "avgpool", 1,
                           float(scaling), flags=compress.ROUND_FLAGS.get(q.dtype, 0))
         m = probs.view(B, Hq, 1, L).to(q.dtype)
         self.maps.setdefault(layer_idx, {})[L] = m

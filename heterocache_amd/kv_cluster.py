@@ -159,8 +159,8 @@ class H2OKVCluster:
         """[B*H, L] float32: sum over every query position of its softmax row."""
         B, H, L, D = query_states.shape
         scores = torch.empty((B * H, 1, L), dtype=torch.float32, device=query_states.device)
-        k_off = torch.as_tensor([b * key_states.stride(0) + h * key_states.stride(1)
-                                 for b in range(B) for h in range(H)], dtype=torch.int64).to(query_states.device)
+        k_off = ops.to_device([b * key_states.stride(0) + h * key_states.stride(1) for b in range(B) for h in range(H)],
+                              query_states.device, torch.int64)
         base = [b * query_states.stride(0) + h * query_states.stride(1) for b in range(B) for h in range(H)]
         flags = _lib.HC_SCORE_SUM_WINDOW
         chunk = self.QUERY_CHUNK.get(query_states.dtype, 256)
@@ -175,8 +175,8 @@ class H2OKVCluster:
             blocks.append((s, w))
             s += w
         # Every block's query offsets in one host-to-device copy.
-        q_offs = torch.as_tensor(np.asarray([[o + s * query_states.stride(2) for o in base] for s, _ in blocks],
-                                            dtype=np.int64)).to(query_states.device)
+        q_offs = ops.to_device(np.asarray([[o + s * query_states.stride(2) for o in base] for s, _ in blocks],
+                                          dtype=np.int64), query_states.device)
         for i, (s, w) in enumerate(blocks):
             ops.score(query_states, q_offs[i], query_states.stride(1), query_states.stride(2), key_states, k_off,
                       key_states.stride(2), L, 1, w, L, "avgpool", 1, 1.0 / math.sqrt(D),
@@ -228,7 +228,7 @@ class StreamingLLMKVCluster:
             return key_states, value_states
         recent = self.max_capacity_prompt
         keep = np.concatenate([np.arange(self.sink_token), np.arange(q_len - recent, q_len)]).astype(np.int32)
-        idx = torch.as_tensor(np.tile(keep, (B * H, 1))).to(key_states.device)
+        idx = ops.to_device(np.tile(keep, (B * H, 1)), key_states.device)
         return ops.gather_rows(key_states, value_states, idx, len(keep))
 
 
