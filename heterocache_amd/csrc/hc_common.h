@@ -150,4 +150,34 @@ __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask, 64));
 }
 
+// Combine a value over the four lanes l, l^16, l^32, l^48 of a wave (one
+// lane per 16-lane row), as the MFMA layouts need for a per-column max or
+// sum.  gfx950's row swaps (v_permlane16_swap / v_permlane32_swap) move the
+// data between VGPRs without an LDS round trip.  With both operands equal,
+// each swap hands every lane its own value and its partner's (l^16, then
+// l^32) as the two results, in a lane-dependent order; max and + are
+// commutative, so the result equals that of the xor-shuffle form bit for bit.
+__device__ __forceinline__ float rows4_max(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float w = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned uw = __float_as_uint(w);
+  const auto b = __builtin_amdgcn_permlane32_swap(uw, uw, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+// Sum over the two lanes l and l^16 (row swap only).
+__device__ __forceinline__ float rows2_sum(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
+}
+__device__ __forceinline__ float rows4_sum(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float w = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const unsigned uw = __float_as_uint(w);
+  const auto b = __builtin_amdgcn_permlane32_swap(uw, uw, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 }  // namespace hc

@@ -215,8 +215,7 @@ __device__ __forceinline__ void attend_new_token(const typename Elem<T>::vec8 (&
 #pragma unroll
     for (int e = 0; e < 8; ++e) dot = fmaf(vec8_at<T>(qreg[s], e), vec8_at<T>(k8, e), dot);
   }
-  dot += __shfl_xor(dot, 16, 64);
-  dot += __shfl_xor(dot, 32, 64);
+  dot = rows4_sum(dot);
   const float sc = dot * scale_log2;
   const float m_new = fmaxf(m_run, sc);
   const float alpha = fast_exp2(m_run - m_new);
@@ -335,8 +334,7 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
         vstore[tb + v_tile_offset(tn, d)] = vn[d];
       }
     }
-    l_run += __shfl_xor(l_run, 16, 64);
-    l_run += __shfl_xor(l_run, 32, 64);
+    l_run = rows4_sum(l_run);
 
     // Wave states -> LDS.  Lane holds O^T[d = 16mt + 4g + j][q = n].
     if (n < G) {

@@ -303,8 +303,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
         for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
           for (int r = 0; r < 4; ++r) mx = fmaxf(mx, sacc[tb][j][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        mx = rows4_max(mx);
         const float mt = mx * a.scale_log2;
         // Lazy rescaling: the reference maximum m only moves when a tile
         // maximum exceeds it by more than kPfLazy (log2 units), so the O
@@ -368,9 +367,7 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
   if (!active) return;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
-    float lt = l[j];
-    lt += __shfl_xor(lt, 16, 64);
-    lt += __shfl_xor(lt, 32, 64);
+    const float lt = rows4_sum(l[j]);
     const float inv = 1.f / lt;
     const int qi = qw0 + 16 * j + n16;
     if (qi >= a.Lq) continue;

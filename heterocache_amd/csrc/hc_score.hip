@@ -208,8 +208,7 @@ __device__ __forceinline__ void stats_chunk(const ScoreArgs& a, const KRegs<T>& 
     float m = -FLT_MAX;
 #pragma unroll
     for (int u = 0; u < kSubTiles; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u][0], x[u][1]), fmaxf(x[u][2], x[u][3])));
-    m = fmaxf(m, __shfl_xor(m, 16, 64));
-    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    m = rows4_max(m);
     float l = 0.f;
     if constexpr (RAW) {
       m = fmaxf(m * a.scale2, -FLT_MAX);  // base-2 scaled maximum, finite
@@ -222,8 +221,7 @@ __device__ __forceinline__ void stats_chunk(const ScoreArgs& a, const KRegs<T>& 
       for (int u = 0; u < kSubTiles; ++u)
         l += (fast_exp2(x[u][0] - m) + fast_exp2(x[u][1] - m)) + (fast_exp2(x[u][2] - m) + fast_exp2(x[u][3] - m));
     }
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    l = rows4_sum(l);
     if (lane < 16) {  // each row entry belongs to one lane of this wave
       float* e = my + 2 * (16 * nt + lane);
       float em = e[0], el = e[1];
@@ -426,7 +424,7 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
             if constexpr (MOM) gsq[u] += (p[0] * p[0] + p[1] * p[1]) + (p[2] * p[2] + p[3] * p[3]);
           } else if constexpr (WM == kWin8) {
             float v = (p[0] + p[1]) + (p[2] + p[3]);
-            v += __shfl_xor(v, 16, 64);
+            v = rows2_sum(v);
             const int g = r0 / 8;
             if ((rg & 1) == 0 && r0 < a.R && t < a.span) A[((int64_t)job * a.G + g) * a.span + t] = round_fixed<RM>(v);
           } else if constexpr (WM == kWin4) {
@@ -451,13 +449,11 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
             for (int u = 0; u < kSubTiles; ++u) {
               const int t = tw + 16 * u + (lane & 15);
               float v = gsum[u];
-              v += __shfl_xor(v, 16, 64);
-              v += __shfl_xor(v, 32, 64);
+              v = rows4_sum(v);
               const int64_t o = ((int64_t)job * a.G + g) * a.span + t;
               if constexpr (MOM) {
                 float v2 = gsq[u];
-                v2 += __shfl_xor(v2, 16, 64);
-                v2 += __shfl_xor(v2, 32, 64);
+                v2 = rows4_sum(v2);
                 if (rg == 0 && g < a.G && t < a.span) {
                   A[o] = v;
                   A2[o] = v2;
