@@ -340,7 +340,10 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
       __builtin_amdgcn_s_setprio(0);
     }
     // V(it) (issued before K(it+1)) has landed in every wave's part of the
-    // buffer once each wave's older loads are done.
+    // buffer once each wave's older loads are done.  The release fence of
+    // __syncthreads() then drains K(it+1) too; a barrier that waits on LDS
+    // reads only, keeping K(it+1) in flight over the P.V step, measured no
+    // faster, since the loads have landed by then.
     if (more)
       wait_lds_dma_but<kUnitsPerThread>();
     else
