@@ -146,10 +146,6 @@ __device__ __forceinline__ float vec8_at<float>(const Elem<float>::vec8& v, int 
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float wave_max_xor(float v, int mask) {
-  return fmaxf(v, __shfl_xor(v, mask, 64));
-}
-
 // Combine a value over the four lanes l, l^16, l^32, l^48 of a wave (one
 // lane per 16-lane row), as the MFMA layouts need for a per-column max or
 // sum.  gfx950's row swaps (v_permlane16_swap / v_permlane32_swap) move the

@@ -178,8 +178,7 @@ __device__ __forceinline__ void attend_tile(typename Elem<T>::vec8 (&kr)[8], typ
   float mx = sv[0];
 #pragma unroll
   for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sv[e]);
-  mx = wave_max_xor(mx, 16);
-  mx = wave_max_xor(mx, 32);
+  mx = rows4_max(mx);
   const float m_new = fmaxf(m_run, mx * scale_log2);
   const float alpha = fast_exp2(m_run - m_new);
   float p[8];
