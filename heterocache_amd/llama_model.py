@@ -31,7 +31,7 @@ from .cache_utils import HeteroCache
 ATTENTION_OBSERVERS = []
 
 
-# The last 4-D mask checked by _plain_causal (weakly held) and its verdict.
+# The last 4-D mask checked by _plain_causal (weakly held) and the result.
 _MASK_CHECK = {"ref": None, "shape": None, "plain": False}
 
 

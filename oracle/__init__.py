@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing here is part of the product: only the
 tests, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` import it, and only as the checker or the CPU baseline.
+``bench.py`` import it, and only as the reference results a test compares
+against or as the CPU baseline.
 
 ``hc_oracle.py`` is a numpy restatement of the reference's algorithm (each
 function cites the reference file:line it follows); ``hc_oracle.c`` restates
