@@ -34,8 +34,10 @@ SIGNATURES = {
     "hc_version": (c_int, []),
     "hc_tile_tokens": (c_int, []),
     "hc_head_dim": (c_int, []),
-    "hc_decode_attn": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
-                               c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_int64, c_int, c_void_p]),
+    "hc_read_status": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "hc_decode_attn": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                               c_int, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_int64, c_int,
+                               c_void_p, c_void_p]),
     "hc_decode_num_parts": (c_int64, [c_void_p, c_int, c_int]),
     "hc_decode_chunk_tiles": (c_int, [c_int, c_void_p, c_int, c_int]),
     "hc_decode_workspace_size": (c_size_t, [c_int, c_int, c_int64]),
@@ -106,8 +108,5 @@ def load():
 def check(rc):
     if rc != HC_OK:
         msg = load().hc_last_error()
-        msg = msg.decode() if msg else ""
-        if rc == HC_ERR_CAPACITY:
-            raise HCError(rc, msg)
-        raise HCError(rc, msg)
+        raise HCError(rc, msg.decode() if msg else "")
     return rc

@@ -283,7 +283,7 @@ class HeteroCache(DynamicCache):
         self._arena = (k, v)
         base = 0
         for layer in range(self.num_layers):
-            self.stores[layer] = KVStore(row_caps[layer], dtype, device, arena=(k, v, base))
+            self.stores[layer] = KVStore(row_caps[layer], dtype, device, arena=(k, v, base), layer_idx=layer)
             base += tiles[layer]
         self._tile_table = torch.cat([st.row_tile_off for st in self.stores])
 

@@ -39,6 +39,7 @@ struct ChunkLoc {
   int total;      // chunks of all rows
   int64_t tiles;  // first tile of the row in the store (row_tile_off[row])
   bool found;
+  bool full;      // a fused append was asked for but the row is at capacity
 };
 
 __device__ __forceinline__ int chunks_of(int len, int chunk_tiles) {
@@ -58,16 +59,20 @@ __device__ __forceinline__ int wave_inclusive_scan(int v, int lane) {
 
 // Map workgroup index b onto (row, chunk) from the device-resident lengths.
 // Each wave scans the rows 64 at a time, one row per lane: the per-row loads
-// of a block are issued together (for up to 64 rows, row_order, row_len and
-// row_tile_off are all read in one round trip and the order is applied by a
-// lane permute), so locating costs one or two memory latencies, not one per
-// row.
-__device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len, const int* __restrict__ row_order,
+// of a block are issued together (for up to 64 rows, row_order, row_len,
+// row_cap and row_tile_off are all read in one round trip and the order is
+// applied by a lane permute), so locating costs one or two memory latencies,
+// not one per row.  With a fused append (extra = 1) a row attends one more
+// token unless it is at capacity (row_cap), in which case it is marked full
+// and attends nothing new.
+__device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len, const int* __restrict__ row_cap,
+                                                 const int* __restrict__ row_order,
                                                  const int64_t* __restrict__ row_tile_off, int rows, int extra,
                                                  int chunk_tiles, int b) {
   const int lane = threadIdx.x & 63;
   ChunkLoc c;
   c.found = false;
+  c.full = false;
   c.row = 0;
   c.chunk = 0;
   c.len = 0;
@@ -78,9 +83,12 @@ __device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len
   if (rows <= 64) {
     const bool live = lane < rows;
     const int own_len = live ? row_len[lane] : 0;
+    const int own_cap = (live && extra) ? row_cap[lane] : 0;
     const int64_t own_off = live ? row_tile_off[lane] : 0;
     const int r = live ? (row_order ? row_order[lane] : lane) : 0;
-    const int l = __shfl(own_len, r, 64) + extra;
+    const int own_ext = (extra && own_len < own_cap) ? 1 : 0;
+    const int l = __shfl(own_len + own_ext, r, 64);
+    const int fl = __shfl(extra - own_ext, r, 64);
     const int nc = live ? chunks_of(l, chunk_tiles) : 0;
     const int incl = wave_inclusive_scan(nc, lane);
     const int excl = incl - nc;
@@ -91,6 +99,7 @@ __device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len
       c.found = true;
       c.row = __shfl(r, src, 64);
       c.len = __shfl(l, src, 64);
+      c.full = __shfl(fl, src, 64) != 0;
       c.nparts = __shfl(nc, src, 64);
       c.p0 = __shfl(excl, src, 64);
       c.chunk = b - c.p0;
@@ -101,7 +110,10 @@ __device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len
       const int k = base + lane;
       const bool live = k < rows;
       const int r = live ? (row_order ? row_order[k] : k) : 0;
-      const int l = live ? row_len[r] + extra : 0;
+      const int len0 = live ? row_len[r] : 0;
+      const int ext = (live && extra && len0 < row_cap[r]) ? 1 : 0;
+      const int l = len0 + ext;
+      const int fl = live ? extra - ext : 0;
       const int nc = live ? chunks_of(l, chunk_tiles) : 0;
       const int incl = acc + wave_inclusive_scan(nc, lane);
       const int excl = incl - nc;
@@ -111,6 +123,7 @@ __device__ __forceinline__ ChunkLoc locate_chunk(const int* __restrict__ row_len
         c.found = true;
         c.row = __shfl(r, src, 64);
         c.len = __shfl(l, src, 64);
+        c.full = __shfl(fl, src, 64) != 0;
         c.nparts = __shfl(nc, src, 64);
         c.p0 = __shfl(excl, src, 64);
         c.chunk = b - c.p0;
@@ -232,14 +245,14 @@ constexpr int kOPitch = HC_HEAD_DIM + 4;
 template <typename T, int NWAVES>
 __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_partial_kernel(
     const T* __restrict__ q, T* __restrict__ kstore, T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off,
-    const int* __restrict__ row_len, const int* __restrict__ row_order, int rows, int G, float scale_log2,
-    int chunk_tiles, const T* __restrict__ k_new, const T* __restrict__ v_new, float* __restrict__ part_o,
-    float* __restrict__ part_ml, int* __restrict__ row_info) {
+    const int* __restrict__ row_len, const int* __restrict__ row_cap, const int* __restrict__ row_order, int rows,
+    int G, float scale_log2, int chunk_tiles, const T* __restrict__ k_new, const T* __restrict__ v_new,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ row_info, int* __restrict__ status) {
   typedef typename Elem<T>::vec8 vec8;
   constexpr int NT = NWAVES * 64;
   const bool fused_append = (k_new != nullptr);
-  const ChunkLoc loc =
-      locate_chunk(row_len, row_order, row_tile_off, rows, fused_append ? 1 : 0, chunk_tiles, (int)blockIdx.x);
+  const ChunkLoc loc = locate_chunk(row_len, row_cap, row_order, row_tile_off, rows, fused_append ? 1 : 0,
+                                    chunk_tiles, (int)blockIdx.x);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -252,13 +265,26 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
   // sized by the launch for G queries.
   extern __shared__ float s_o[];
 
-  if (!loc.found) return;
   if (loc.total > (int)gridDim.x) {
-    // The launch grid is smaller than the device lengths need: flag the row
-    // so the merge writes NaN instead of a silently partial result.
+    // The launch grid is smaller than the device lengths need (every
+    // workgroup sees the same lengths, so all of them take this branch):
+    // flag every row -- workgroup b the rows b, b + grid, ... -- so the
+    // merge writes NaN and advances no length, whatever a previous launch
+    // left in the workspace.  Nothing is attended or stored.
+    for (int64_t r = blockIdx.x + (int64_t)threadIdx.x * gridDim.x; r < rows; r += (int64_t)NT * gridDim.x) {
+      row_info[2 * r] = 0;
+      row_info[2 * r + 1] = -1;
+    }
+    return;
+  }
+  if (!loc.found) return;
+  if (loc.full) {
+    // Fused append into a row at capacity: the row is left unchanged, its
+    // output is NaN (flag) and bit 0 of *status reports it.
     if (threadIdx.x == 0 && loc.chunk == 0) {
       row_info[2 * loc.row] = 0;
       row_info[2 * loc.row + 1] = -1;
+      if (status) atomicOr(status, 1);
     }
     return;
   }
@@ -388,8 +414,9 @@ constexpr int kMergeGroups = 16;
 constexpr int kMergeThreads = kMergeSlice * kMergeGroups;
 
 // A row whose part range lies outside this launch's grid_parts partials
-// (flagged np = -1 by an undersized grid, or left stale because no
-// workgroup of this launch reached the row) is written as NaN.
+// (flagged np = -1 by an undersized grid or a full row) is written as NaN
+// and its length is not advanced: only rows whose new token was stored and
+// attended advance.
 template <typename T>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml, const int* __restrict__ row_info, int G,
@@ -401,8 +428,9 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   __shared__ float s_m[kMergeGroups], s_l[kMergeGroups];
   __shared__ float s_o[kMergeGroups][kMergeSlice];
   T* o = out + ((int64_t)row * G + qq) * HC_HEAD_DIM + d0;
-  if (advance && qq == 0 && blockIdx.z == 0 && tid == 0) row_len[row] += 1;
-  if (np < 1 || p0 < 0 || (int64_t)p0 + np > grid_parts) {
+  const bool valid = np >= 1 && p0 >= 0 && (int64_t)p0 + np <= grid_parts;
+  if (advance && valid && qq == 0 && blockIdx.z == 0 && tid == 0) row_len[row] += 1;
+  if (!valid) {
     if (tid < kMergeSlice) o[tid] = Elem<T>::from_f32(NAN);
     return;
   }
@@ -492,9 +520,9 @@ size_t decode_workspace_bytes_rows(int rows, int group, int64_t num_parts) {
 
 template <typename T>
 static int launch_decode(const void* q, void* kstore, void* vstore, const int64_t* row_tile_off, int* row_len,
-                         const int* row_order, int rows, int G, float scale, const void* k_new, const void* v_new,
-                         void* out, void* workspace, size_t workspace_bytes, int64_t grid_parts, int chunk_tiles,
-                         hipStream_t stream) {
+                         const int* row_cap, const int* row_order, int rows, int G, float scale, const void* k_new,
+                         const void* v_new, void* out, void* workspace, size_t workspace_bytes, int64_t grid_parts,
+                         int chunk_tiles, int* status, hipStream_t stream) {
   if (grid_parts < rows)
     return set_error(HC_ERR_INVALID, "hc_decode_attn: num_parts=%lld below the row count %d", (long long)grid_parts,
                      rows);
@@ -508,8 +536,9 @@ static int launch_decode(const void* q, void* kstore, void* vstore, const int64_
   const float scale_log2 = scale * 1.4426950408889634f;
   const size_t lds_o = (size_t)kDecodeWaves * G * kOPitch * sizeof(float);
   hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves>), dim3((unsigned)grid_parts), dim3(kDecodeWaves * 64),
-                     lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off, row_len, row_order, rows, G,
-                     scale_log2, chunk_tiles, (const T*)k_new, (const T*)v_new, part_o, part_ml, row_info);
+                     lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off, row_len, row_cap, row_order,
+                     rows, G, scale_log2, chunk_tiles, (const T*)k_new, (const T*)v_new, part_o, part_ml, row_info,
+                     status);
   int rc = check_launch("hc_decode_attn(partial)");
   if (rc) return rc;
   hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(rows, G, HC_HEAD_DIM / kMergeSlice),
@@ -588,11 +617,11 @@ extern "C" int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, in
   return decode_num_parts(host_row_len, rows, chunk_tiles);
 }
 
-extern "C" int hc_decode_attn(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
-                              int32_t* row_len, const int32_t* row_order, int rows, int group, float scale,
-                              const void* k_new, const void* v_new, void* out, void* workspace,
-                              size_t workspace_bytes, int64_t num_parts, int chunk_tiles, void* stream) {
-  clear_error();
+// Argument checks and dtype dispatch shared by the decode entry points.
+static int decode_entry(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
+                        int32_t* row_len, const int32_t* row_cap, const int32_t* row_order, int rows, int group,
+                        float scale, const void* k_new, const void* v_new, void* out, void* workspace,
+                        size_t workspace_bytes, int64_t num_parts, int chunk_tiles, int32_t* status, void* stream) {
   if (rows < 0 || group < 1 || group > 16)
     return set_error(HC_ERR_INVALID, "hc_decode_attn: rows=%d group=%d (group must be 1..16)", rows, group);
   if (chunk_tiles < 1 || chunk_tiles > (1 << 22))
@@ -602,18 +631,29 @@ extern "C" int hc_decode_attn(int dtype, const void* q, void* kstore, void* vsto
     return set_error(HC_ERR_INVALID, "hc_decode_attn: null pointer argument");
   if ((k_new == nullptr) != (v_new == nullptr))
     return set_error(HC_ERR_INVALID, "hc_decode_attn: k_new and v_new must be given together");
+  if (k_new && !row_cap) return set_error(HC_ERR_INVALID, "hc_decode_attn: a fused append needs row_cap");
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case HC_DTYPE_BF16:
-      return launch_decode<__bf16>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
-                                   v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, s);
+      return launch_decode<__bf16>(q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale,
+                                   k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, s);
     case HC_DTYPE_F16:
-      return launch_decode<_Float16>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
-                                     v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, s);
+      return launch_decode<_Float16>(q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale,
+                                     k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, s);
     case HC_DTYPE_F32:
-      return launch_decode<float>(q, kstore, vstore, row_tile_off, row_len, row_order, rows, group, scale, k_new,
-                                  v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, s);
+      return launch_decode<float>(q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale,
+                                  k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, s);
     default:
       return set_error(HC_ERR_INVALID, "hc_decode_attn: unknown dtype %d", dtype);
   }
+}
+
+extern "C" int hc_decode_attn(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
+                              int32_t* row_len, const int32_t* row_cap, const int32_t* row_order, int rows, int group,
+                              float scale, const void* k_new, const void* v_new, void* out, void* workspace,
+                              size_t workspace_bytes, int64_t num_parts, int chunk_tiles, int32_t* status,
+                              void* stream) {
+  clear_error();
+  return decode_entry(dtype, q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale, k_new,
+                      v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, stream);
 }

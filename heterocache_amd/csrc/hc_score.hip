@@ -498,8 +498,9 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
 // wider ones walk the window in LDS.
 constexpr int kPoolThreads = 256;
 constexpr int kPoolTile = 4 * kPoolThreads;
-constexpr int kPoolMaxHalf = 31;
-constexpr int kPoolHalo = 32;     // >= kPoolMaxHalf, keeps the strip 16-byte aligned
+constexpr int kPoolMaxKernel = 63;  // widest pooling kernel: half-width 31
+constexpr int kPoolHalo = 32;       // >= kPoolMaxKernel / 2, keeps the strip 16-byte aligned
+static_assert(kPoolHalo >= kPoolMaxKernel / 2, "pooling halo narrower than the widest kernel");
 constexpr int kPoolRegHalf = 4;   // register path: kernel <= 9
 constexpr int kPoolHeads = 4;     // heads whose loads are in flight together
 
@@ -1029,8 +1030,8 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
                      window);
   if (span < 0 || span > seq_len) return set_error(HC_ERR_INVALID, "hc_score: span %d outside [0, %d]", span, seq_len);
   if (pooling != 0 && pooling != 1) return set_error(HC_ERR_INVALID, "hc_score: pooling must be 0 (avg) or 1 (max)");
-  if (kernel < 1 || (kernel % 2) == 0 || kernel > 63)
-    return set_error(HC_ERR_INVALID, "hc_score: pooling kernel must be odd and <= 63 (got %d)", kernel);
+  if (kernel < 1 || (kernel % 2) == 0 || kernel > kPoolMaxKernel)
+    return set_error(HC_ERR_INVALID, "hc_score: pooling kernel must be odd and <= %d (got %d)", kPoolMaxKernel, kernel);
   const int R = group * window;
   if ((int64_t)njobs * ((flags & HC_SCORE_SUM_WINDOW) ? 1 : window) > 65535)
     return set_error(HC_ERR_INVALID, "hc_score: njobs x window rows %lld exceed 65535",

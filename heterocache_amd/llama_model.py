@@ -130,7 +130,8 @@ class LlamaAttention(nn.Module):
         cache = past_key_values
         cos, sin = position_embeddings
         cache_kwargs = {"sin": sin, "cos": cos, "cache_position": cache_position, "attention_mask": attention_mask,
-                        "num_key_value_groups": self.num_key_value_groups, "query_states": query_states}
+                        "num_key_value_groups": self.num_key_value_groups, "query_states": query_states,
+                        "update_global_past_kv": getattr(self, "update_global_past_kv", True)}
         if cache is None or not isinstance(cache, HeteroCache):
             # No HeteroCache: causal attention over whatever the cache returns
             # (a plain DynamicCache, or a baseline compressor's cache, which

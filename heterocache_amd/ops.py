@@ -111,12 +111,16 @@ def decode_chunk_tiles(host_row_len, group, dtype):
 
 
 def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, out=None, row_order=None,
-                k_new=None, v_new=None, chunk_tiles=None, stream=None, workspace=None, num_parts=None):
+                k_new=None, v_new=None, chunk_tiles=None, stream=None, workspace=None, num_parts=None,
+                row_cap=None, status=None):
     """out[r, g] = softmax(scale * q[r, g] . K_r^T) V_r over row_len[r] tokens.
 
     q: [rows, G, 128]; host_row_len: host copy of the lengths (sizes the grid).
     With k_new/v_new [rows, 128] the new token is appended and attended in the
     same launch; row_len advances by one (the caller advances its mirror).
+    row_cap (int32 [rows], required with k_new): a row at capacity is left
+    unchanged, its output is NaN and bit 0 of status (int32 device word,
+    optional) is set -- read it with read_status.
     chunk_tiles: tiles per workgroup; None picks the one-round chunk for
     these lengths.  num_parts: grid size, at least what these lengths need;
     a larger grid (surplus workgroups exit at once) lets a captured HIP graph
@@ -136,7 +140,12 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
         raise TypeError("q and the store must share a dtype")
     if (k_new is None) != (v_new is None):
         raise ValueError("k_new and v_new go together")
+    _require_cuda(row_cap, status)
     if k_new is not None:
+        if row_cap is None or row_cap.dtype != torch.int32 or row_cap.numel() != rows:
+            raise ValueError("a fused append needs row_cap, int32 [rows]")
+        if status is not None and (status.dtype != torch.int32 or status.numel() < 1):
+            raise ValueError("status must be an int32 device word")
         if k_new.shape != (rows, HEAD_DIM) or v_new.shape != (rows, HEAD_DIM):
             raise ValueError(f"k_new/v_new must be [{rows}, {HEAD_DIM}]")
         if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
@@ -161,9 +170,23 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
     nbytes = lib.hc_decode_workspace_size(rows, G, nparts)
     ws = workspace if workspace is not None else WORKSPACE.get(q.device, nbytes)
     _lib.check(lib.hc_decode_attn(dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
-                                  _ptr(row_len), _ptr(row_order), rows, G, float(scale), _ptr(k_new), _ptr(v_new),
-                                  _ptr(out), _ptr(ws), ws.numel(), nparts, int(chunk_tiles), _stream(stream, q)))
+                                  _ptr(row_len), _ptr(row_cap), _ptr(row_order), rows, G, float(scale), _ptr(k_new),
+                                  _ptr(v_new), _ptr(out), _ptr(ws), ws.numel(), nparts, int(chunk_tiles),
+                                  _ptr(status) if k_new is not None else None, _stream(stream, q)))
     return out
+
+
+def read_status(status, clear=True, stream=None):
+    """Wait for the stream and read the device status word of hc_append /
+    hc_decode_attn (zeroing it when clear).  Returns the word; raises
+    HCError(HC_ERR_CAPACITY) when a row was at capacity."""
+    _require_cuda(status)
+    if status.dtype != torch.int32 or status.numel() < 1:
+        raise ValueError("status must be an int32 device word")
+    val = ctypes.c_int32(0)
+    _lib.check(_lib.load().hc_read_status(_ptr(status), int(bool(clear)), ctypes.addressof(val),
+                                          _stream(stream, status)))
+    return val.value
 
 
 def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore, vstore, row_tile_off,

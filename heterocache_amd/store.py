@@ -10,7 +10,7 @@ one contiguous run of 32-token tiles sized for its whole lifetime
 import numpy as np
 import torch
 
-from . import ops
+from . import _lib, ops
 
 TILE = ops.TILE
 HEAD_DIM = ops.HEAD_DIM
@@ -31,7 +31,7 @@ class KVStore:
     rows of several stores through the shared base pointers.
     """
 
-    def __init__(self, row_caps, dtype, device, arena=None):
+    def __init__(self, row_caps, dtype, device, arena=None, layer_idx=None):
         caps = np.asarray(row_caps, dtype=np.int64)
         if (caps < 0).any():
             raise ValueError("negative row capacity")
@@ -40,6 +40,7 @@ class KVStore:
         if len(caps) > 1:
             off[1:] = np.cumsum(tiles)[:-1]
         self.rows = len(caps)
+        self.layer_idx = layer_idx
         self.dtype = dtype
         self.device = torch.device(device)
         self.host_cap = tiles * TILE
@@ -228,15 +229,31 @@ class KVStore:
             self._check_room()
         out = ops.decode_attn(q, self.k, self.v, self.row_tile_off, self.row_len, self.host_len, scale, out=out,
                               row_order=self.row_order, k_new=k_new, v_new=v_new, chunk_tiles=chunk_tiles,
-                              stream=stream, workspace=workspace, num_parts=num_parts)
+                              stream=stream, workspace=workspace, num_parts=num_parts, row_cap=self.row_cap,
+                              status=self.status)
         if k_new is not None:
             self.host_len += 1
             self._headroom -= 1
         return out
 
+    def _oom(self):
+        name = "?" if self.layer_idx is None else self.layer_idx
+        return RuntimeError(f"Layer {name} OOM.")
+
     def _check_room(self):
-        """Raise like the reference's "OOM" when a row cannot take one more
-        token (heterocache/cache_utils.py:988-990)."""
+        """Raise the reference's "Layer i OOM." when a row cannot take one
+        more token (heterocache/cache_utils.py:988-990)."""
         if self._headroom < 1:
-            full = np.nonzero(self.host_len.astype(np.int64) + 1 > self.host_cap)[0].tolist()
-            raise RuntimeError(f"KV store OOM: rows {full} are at capacity")
+            raise self._oom()
+
+    def check_status(self, stream=None):
+        """After launches no host check preceded (HIP graph replays of
+        attend/append): wait for the stream, clear the device status word and
+        raise "Layer i OOM." if a row was at capacity.  Such a row was left
+        unchanged and its output is NaN."""
+        try:
+            ops.read_status(self.status, clear=True, stream=stream)
+        except _lib.HCError as e:
+            if e.code == _lib.HC_ERR_CAPACITY:
+                raise self._oom() from e
+            raise

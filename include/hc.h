@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define HC_ABI_VERSION 1
+#define HC_ABI_VERSION 2
 
 enum hc_status {
   HC_OK = 0,
@@ -38,6 +38,17 @@ enum hc_dtype { HC_DTYPE_F32 = 0, HC_DTYPE_F16 = 1, HC_DTYPE_BF16 = 2 };
 
 /* Thread-local description of the last error (empty string after success). */
 const char* hc_last_error(void);
+
+/*
+ * Read the device status word that hc_append and hc_decode_attn raise when a
+ * row is at capacity: waits for `stream`, stores the word in *value (optional),
+ * zeroes it when `clear` is set, and returns HC_ERR_CAPACITY when bit 0 is
+ * set (HC_OK otherwise).  The one call that synchronises the host; it exists
+ * so that launches replayed from a HIP graph, which no host check precedes,
+ * still surface the reference's pool exhaustion ("Layer i OOM.",
+ * heterocache/cache_utils.py:988-990) as a typed error.
+ */
+int hc_read_status(int32_t* status, int clear, int32_t* value, void* stream);
 int hc_version(void);
 int hc_tile_tokens(void);
 int hc_head_dim(void);
@@ -54,25 +65,32 @@ int hc_head_dim(void);
  * row_order (optional): permutation of the rows giving the order in which
  * their chunks are scheduled (longest first is fastest).
  * k_new/v_new (optional, [rows, 128]): fused decode append -- the new token
- * is attended at slot row_len[r], stored there, and every row_len advances by
+ * is attended at slot row_len[r], stored there, and row_len[r] advances by
  * one when the launch completes (the append of heterocache/cache_utils.py:
- * 970-1005 and the attention in one launch).
+ * 970-1005 and the attention in one launch).  row_cap is required with a
+ * fused append: a row with row_len[r] >= row_cap[r] is left unchanged (no
+ * store, no advance), its output is NaN and bit 0 of *status is set (status
+ * optional) -- the device-side form of the reference's "Layer i OOM."
+ * (heterocache/cache_utils.py:988-990); hc_read_status turns it into
+ * HC_ERR_CAPACITY.
  * chunk_tiles: 32-token tiles per workgroup (each row is cut into chunks of
  * this many tiles; the 4 waves of a workgroup split a chunk evenly);
  * hc_decode_chunk_tiles() picks the value that fills the device in one
  * resident round for the given lengths.
  * num_parts: hc_decode_num_parts(lengths, rows, chunk_tiles) of the lengths
- * the launch attends (row_len, +1 with k_new); the grid it sizes must cover
- * the device lengths (rows whose chunks fall outside it return NaN).
+ * the launch attends (row_len, +1 with k_new); a larger value (surplus
+ * workgroups exit) lets a captured graph replay while the lengths grow.  If
+ * the grid it sizes is smaller than the device lengths need, every row's
+ * output is NaN and nothing is stored or advanced.
  * workspace: at least hc_decode_workspace_size(rows, group, num_parts) bytes;
  * every field is written before it is read within one call, so it needs no
  * initialisation, and one workspace serves any sequence of launches on one
  * stream (launches that overlap in time need separate workspaces).
  */
 int hc_decode_attn(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off, int32_t* row_len,
-                   const int32_t* row_order, int rows, int group, float scale, const void* k_new, const void* v_new,
-                   void* out, void* workspace, size_t workspace_bytes, int64_t num_parts, int chunk_tiles,
-                   void* stream);
+                   const int32_t* row_cap, const int32_t* row_order, int rows, int group, float scale,
+                   const void* k_new, const void* v_new, void* out, void* workspace, size_t workspace_bytes,
+                   int64_t num_parts, int chunk_tiles, int32_t* status, void* stream);
 /* Workgroups (chunks) of one hc_decode_attn launch over these lengths. */
 int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, int chunk_tiles);
 /* chunk_tiles for hc_decode_attn: the smallest chunk (at least 4 tiles)

@@ -42,13 +42,21 @@ def test_constants_and_error_reporting_without_gpu():
     if not os.path.exists(_lib.LIB_PATH):
         pytest.skip("libhc.so not built")
     lib = _lib.load()
-    assert lib.hc_version() == 1
+    assert lib.hc_version() == 2
     assert lib.hc_tile_tokens() == 32
     assert lib.hc_head_dim() == 128
     # Argument validation happens before any HIP call, so it runs on the CPU.
-    rc = lib.hc_decode_attn(2, None, None, None, None, None, None, 4, 0, 1.0, None, None, None, None, 0, 1, 4, None)
+    rc = lib.hc_decode_attn(2, None, None, None, None, None, None, None, 4, 0, 1.0, None, None, None, None, 0, 1, 4,
+                            None, None)
     assert rc == _lib.HC_ERR_INVALID
     assert b"group" in lib.hc_last_error()
+    # A fused append without row capacities is refused.
+    fake = 16  # never dereferenced: validation fails first
+    rc = lib.hc_decode_attn(2, fake, fake, fake, fake, fake, None, None, 4, 4, 1.0, fake, fake, fake, fake, 1 << 20, 4,
+                            4, None, None)
+    assert rc == _lib.HC_ERR_INVALID
+    assert b"row_cap" in lib.hc_last_error()
+    assert lib.hc_read_status(None, 1, None, None) == _lib.HC_ERR_INVALID
     rc = lib.hc_gather_store(2, None, None, 0, None, 128, 16, None, None, None, None, None, None, None, 1, 4, None, None,
                              None)
     assert rc == _lib.HC_ERR_INVALID

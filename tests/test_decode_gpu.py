@@ -240,31 +240,141 @@ def test_graph_replays_match_eager_steps(dev):
             assert torch.equal(ka, kb) and torch.equal(va, vb)
 
 
+def _abi_decode(lib, ops, store, q, out, ws, parts, chunk, kn=None, vn=None, status=None):
+    """hc_decode_attn through the C ABI (no host-side capacity or grid check)."""
+    return lib.hc_decode_attn(ops.dtype_code(q.dtype), q.data_ptr(), store.k.data_ptr(), store.v.data_ptr(),
+                              store.row_tile_off.data_ptr(), store.row_len.data_ptr(), store.row_cap.data_ptr(),
+                              store.row_order.data_ptr(), q.shape[0], q.shape[1], 1 / math.sqrt(128),
+                              kn.data_ptr() if kn is not None else None, vn.data_ptr() if vn is not None else None,
+                              out.data_ptr(), ws.data_ptr(), ws.numel(), parts, chunk,
+                              status.data_ptr() if status is not None else None,
+                              torch.cuda.current_stream().cuda_stream)
+
+
+def _store_snapshot(store):
+    return [tuple(t.clone() for t in store.read_rows([r], int(store.host_cap[r]))) for r in range(store.rows)]
+
+
 def test_undersized_grid_gives_nan_rows(dev):
     """hc_decode_attn called (through the C ABI, which the Python wrapper
-    would refuse) with fewer workgroups than the lengths need: no partial is
-    written, every row comes out NaN rather than a silently partial result,
-    and the lengths are untouched (no append)."""
+    would refuse) with fewer workgroups than the lengths need, into a
+    workspace a valid launch over the same rows has just filled: every row
+    comes out NaN (no stale partial of the earlier launch is merged), the
+    fused append stores nothing and no length advances."""
     from heterocache_amd import _lib, ops
     lens, G = [5000, 3000, 40], 4
     rng = np.random.default_rng(5)
     ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
     vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
-    store = KVStore(lens, torch.bfloat16, dev)
+    store = KVStore([L + 8 for L in lens], torch.bfloat16, dev)
     fill_store(store, ks, vs, dev)
     q = torch.randn((len(lens), G, 128), device=dev).to(torch.bfloat16)
-    out = torch.zeros_like(q)
+    kn = torch.randn((len(lens), 128), device=dev).to(torch.bfloat16)
+    vn = torch.randn((len(lens), 128), device=dev).to(torch.bfloat16)
     chunk = 4
-    need = ops.decode_num_parts(store.host_len, chunk)
+    need = ops.decode_num_parts(store.host_len + 1, chunk)
     small = 10
     assert need > small
     lib = _lib.load()
-    ws = torch.zeros(lib.hc_decode_workspace_size(len(lens), G, small), dtype=torch.uint8, device=dev)
-    rc = lib.hc_decode_attn(ops.dtype_code(q.dtype), q.data_ptr(), store.k.data_ptr(), store.v.data_ptr(),
-                            store.row_tile_off.data_ptr(), store.row_len.data_ptr(), store.row_order.data_ptr(),
-                            len(lens), G, 1 / math.sqrt(128), None, None, out.data_ptr(), ws.data_ptr(), ws.numel(),
-                            small, chunk, torch.cuda.current_stream().cuda_stream)
+    ws = torch.zeros(lib.hc_decode_workspace_size(len(lens), G, need), dtype=torch.uint8, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    # A valid launch (no append) leaves finite partials and row info in ws.
+    out = torch.zeros_like(q)
+    assert _abi_decode(lib, ops, store, q, out, ws, need, chunk) == 0
     torch.cuda.synchronize()
-    assert rc == 0
+    assert torch.isfinite(out.float()).all()
+    before = _store_snapshot(store)
+    out = torch.zeros_like(q)
+    assert _abi_decode(lib, ops, store, q, out, ws, small, chunk, kn, vn, status) == 0
+    torch.cuda.synchronize()
     assert torch.isnan(out.float()).all()
     assert store.row_len.tolist() == lens
+    assert status.item() == 0
+    after = _store_snapshot(store)
+    for (ka, va), (kb, vb) in zip(before, after):
+        assert torch.equal(ka, kb) and torch.equal(va, vb)
+
+
+def test_fused_append_at_capacity_sets_status(dev):
+    """A row at capacity (not the last row of the buffer) under a fused
+    append, launched without the host check (as a graph replay would): the
+    row is unchanged and comes out NaN, the status word is set, the other
+    rows append and attend normally and their neighbours' tiles are
+    untouched; KVStore.check_status raises the reference's "Layer i OOM."
+    and clears the word."""
+    from heterocache_amd import _lib, ops
+    caps, G = [64, 96, 40], 4
+    lens = [64, 50, 39]          # row 0 is full; row 1 follows it in the buffer
+    rng = np.random.default_rng(11)
+    ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    store = KVStore(caps, torch.float32, dev, layer_idx=7)
+    fill_store(store, ks, vs, dev)
+    q = torch.randn((3, G, 128), device=dev)
+    kn = torch.randn((3, 128), device=dev)
+    vn = torch.randn((3, 128), device=dev)
+    before = _store_snapshot(store)
+    out = ops.decode_attn(q, store.k, store.v, store.row_tile_off, store.row_len, store.host_len + 0, 1 / math.sqrt(128),
+                          row_order=store.row_order, k_new=kn, v_new=vn, row_cap=store.row_cap, status=store.status)
+    torch.cuda.synchronize()
+    assert store.row_len.tolist() == [64, 51, 40]
+    assert store.status.item() == 1
+    o = as_np(out)
+    assert np.isnan(o[0]).all()
+    kk = [np.concatenate([as_np(ks[r]), as_np(kn[r:r + 1])]) for r in (1, 2)]
+    vv = [np.concatenate([as_np(vs[r]), as_np(vn[r:r + 1])]) for r in (1, 2)]
+    ref = O.decode_attention(as_np(q[1:]), kk, vv)
+    assert np.abs(o[1:] - ref).max() <= 1e-4
+    after = _store_snapshot(store)
+    assert torch.equal(before[0][0], after[0][0]) and torch.equal(before[0][1], after[0][1])
+    for r in (1, 2):
+        n = lens[r]
+        assert torch.equal(before[r][0][0, :n], after[r][0][0, :n])
+        assert torch.equal(after[r][0][0, n], kn[r]) and torch.equal(after[r][1][0, n], vn[r])
+        assert torch.equal(before[r][0][0, n + 1:], after[r][0][0, n + 1:])
+    with pytest.raises(RuntimeError, match="Layer 7 OOM."):
+        store.check_status()
+    assert store.status.item() == 0
+    store.check_status()  # cleared
+
+
+def test_graph_replay_past_capacity_raises_oom(dev):
+    """A captured decode step replayed past a row's capacity: replays up to
+    the capacity match eager steps, the replay past it leaves that row (the
+    first of three) unchanged and NaN, and check_status raises."""
+    from heterocache_amd import _lib, ops
+    caps, lens, G = [64, 96, 96], [62, 60, 33], 4   # capacities are whole 32-token tiles
+    rng = np.random.default_rng(12)
+    ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(dev) for L in lens]
+    gst, est = (KVStore(caps, torch.bfloat16, dev, layer_idx=3) for _ in range(2))
+    for st in (gst, est):
+        fill_store(st, ks, vs, dev)
+    q = torch.randn((3, G, 128), device=dev).to(torch.bfloat16)
+    kn = torch.randn((3, 128), device=dev).to(torch.bfloat16)
+    vn = torch.randn((3, 128), device=dev).to(torch.bfloat16)
+    ct = 4
+    parts = ops.decode_num_parts(np.asarray(caps) + 1, ct)
+    lib = _lib.load()
+    ws = torch.empty(lib.hc_decode_workspace_size(3, G, parts), dtype=torch.uint8, device=dev)
+    out_g = torch.empty_like(q)
+    out_e = torch.empty_like(q)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        gst.attend(q, 1 / math.sqrt(128), out=out_g, k_new=kn, v_new=vn, chunk_tiles=ct, num_parts=parts, workspace=ws)
+    for s in range(2):       # row 0 goes 62 -> 63 -> 64 (its capacity)
+        graph.replay()
+        est.attend(q, 1 / math.sqrt(128), out=out_e, k_new=kn, v_new=vn, chunk_tiles=ct)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), s
+    gst.check_status()
+    snap = _store_snapshot(gst)
+    graph.replay()           # row 0 is full now
+    torch.cuda.synchronize()
+    assert gst.row_len.tolist() == [64, 63, 36]
+    assert torch.isnan(out_g[0].float()).all() and torch.isfinite(out_g[1:].float()).all()
+    after = _store_snapshot(gst)
+    assert torch.equal(snap[0][0], after[0][0]) and torch.equal(snap[0][1], after[0][1])
+    with pytest.raises(RuntimeError, match="Layer 3 OOM."):
+        gst.check_status()

@@ -191,3 +191,40 @@ def test_cake_cache_generate(dev):
     for layer in range(2):
         assert cache.key_cache[layer].shape[1] == 2
         assert 32 + 7 < cache.key_cache[layer].shape[2] <= cache.layer_budget[layer] + 32 + 7
+
+
+def test_temp_kv_cache_through_patched_attention(dev):
+    """update_global_past_kv = False on the attention modules reaches the
+    baseline cache (the reference passes it in cache_kwargs): a decode
+    forward then keeps its token in the temporary cache, gives the same
+    logits as a global append, and clear_temp_kv_cache drops it."""
+    from heterocache_amd import cache_utils as C
+    cfg = llama_cfg(layers=2, q_heads=8, kv_heads=2)
+    with utils.install_attention_patch():
+        torch.manual_seed(0)
+        model = LlamaForCausalLM(cfg).to(torch.float32).to(dev).eval()
+    ids = torch.randint(0, 512, (1, 300), generator=torch.Generator().manual_seed(8)).to(dev)
+    mk = lambda: C.SnapKVCache(C.CompressionCacheConfig(window_size=16, compression_ratio=0.3, num_attn_heads=8,
+                                                         num_kv_heads=2, num_layers=2))
+    glob, temp = mk(), mk()
+    nxt = torch.tensor([[5]], device=dev)
+    pos = torch.tensor([[300]], device=dev)
+    with torch.no_grad():
+        model(ids, past_key_values=glob, use_cache=True)
+        model(ids, past_key_values=temp, use_cache=True)
+        kept = [temp.key_cache[l].shape[2] for l in range(2)]
+        ref = model(nxt, past_key_values=glob, use_cache=True, position_ids=pos).logits
+        attn = [layer.self_attn for layer in model.model.layers]
+        for a in attn:
+            a.update_global_past_kv = False
+        try:
+            got = model(nxt, past_key_values=temp, use_cache=True, position_ids=pos).logits
+        finally:
+            for a in attn:
+                del a.update_global_past_kv
+    assert [temp.key_cache[l].shape[2] for l in range(2)] == kept
+    assert [tuple(t.shape[1:3]) for t in temp.temp_key_cache] == [(8, 1), (8, 1)]  # one token per query head
+    assert torch.allclose(got, ref, atol=1e-5, rtol=0)
+    seen = temp._seen_tokens
+    temp.clear_temp_kv_cache()
+    assert temp.temp_key_cache == [] and temp._seen_tokens == seen - 1

@@ -551,3 +551,96 @@ def test_cake_cluster_budget_logic_matches_oracle():
         seq_len = int(rng.integers(1, 3000))
         shares = list((rng.random(n) * 2 * total / n).astype(np.float32))
         assert c.adjust_budgets(shares, total, seq_len, n) == O.cake_adjust_budgets(shares, total, seq_len)
+
+
+# -- CacheOracle, worked by hand -------------------------------------------------
+def _hand_case_data():
+    """One layer, 3 KV heads after the reorder: satellites 0 and 1 (allocation
+    0.5 and 1.5) and pivot 2 leading both."""
+    return {"meta": {"counts": {"anchor": 0, "volatile": 0, "pivot": 1, "satellite": 2}},
+            "need_to_keep_counts": [[2]], "need_to_compress_counts": [2], "need_to_select_counts": [[2]],
+            "need_to_update_counts": [[0, 1]], "leader_member_relations": [{"2": [0, 1]}],
+            "allocation_matrix": [[0.5, 1.5, -1.0]]}
+
+
+def _hand_case_run(select_first):
+    """L = 16, d = 128, G = 1, decode_step 2, kernel-1 average pooling (the
+    scores are the softmax itself).  Every key holds its position t in
+    channel 0, so a query +e0 ranks positions t descending and -e0
+    ascending; channel 1 of K and channel 0 of V hold a label (100 h + t
+    for prompt tokens, 1000 + 100 h + j for the decode token of step j).
+    The satellites' decode queries are zero, so their attention output is
+    the mean of their rows' V labels."""
+    L, d, H = 16, 128, 3
+    k = np.zeros((1, H, L, d))
+    v = np.zeros((1, H, L, d))
+    for h in range(H):
+        for t in range(L):
+            k[0, h, t, 0] = t
+            k[0, h, t, 1] = 100 * h + t
+            v[0, h, t, 0] = 100 * h + t
+    q = np.zeros((1, H, L, d))
+    q[0, :, -1, 0] = 1.0
+    orc = O.CacheOracle(_hand_case_data(), 1, H, H, 1, 0.5, 0.5, 2, "avgpool", 1,
+                        select_before_attention=select_first)
+    orc.prefill(0, q, k, v)
+    signs = [+1, +1, +1, -1, -1, -1]   # the pivot's query direction per decode step
+    outs, refs = [], []
+    for j, sgn in enumerate(signs):
+        qd = np.zeros((1, H, 1, d))
+        qd[0, 2, 0, 0] = sgn
+        kn = np.zeros((1, H, 1, d))
+        vn = np.zeros((1, H, 1, d))
+        for h in range(H):
+            kn[0, h, 0, 1] = 1000 + 100 * h + j
+            vn[0, h, 0, 0] = 1000 + 100 * h + j
+        outs.append(orc.decode(0, qd, kn, vn))
+        refs.append([sorted(s) for s in orc.ref[0][2]])
+    return orc, outs, refs
+
+
+@pytest.mark.parametrize("select_first", [False, True])
+def test_cache_oracle_hand_worked_drift_and_retrieval(select_first):
+    orc, outs, refs = _hand_case_run(select_first)
+    # base = int((0.5*3 - 1) * 16 / (3 - 1)) = 4; satellite caps 2 and 6.
+    assert orc.base == 4
+    assert [len(r[0]) for r in orc.rows[0]] == [2 + 6, 6 + 6, 16 + 6]
+    # Checks after steps 1, 3, 5.  Reference set: top-4 of +e0 = {12..15}.
+    # Step overlaps: (1, 1) -> median 1; (1, 0) -> median 0.5, not < 0.5;
+    # (0, 0) -> median 0 -> trigger.
+    assert orc.triggers == [(0, 2, False), (0, 2, False), (0, 2, True)]
+    assert refs[:5] == [[[12, 13, 14, 15]]] * 5
+    # On trigger the set becomes the last step's top-4 of -e0 = {0..3}.
+    assert refs[5] == [[0, 1, 2, 3]]
+    # Retrieval: ascending top-6 of the last step = positions 0..5; satellite
+    # 0 (length 2) takes the prefix [0, 1], satellite 1 all six.  Slots past
+    # the retrieved prefix keep the prompt tokens kept at prefill (satellite
+    # 1's slot 6+ are the decode tokens, satellite 0 kept {14, 15}).
+    k0, v0 = orc.rows[0][0]
+    k1, v1 = orc.rows[0][1]
+    assert k0[:2, 1].tolist() == [0, 1] and v0[:2, 0].tolist() == [0, 1]
+    assert k0[2:, 1].tolist() == [1000 + j for j in range(6)]
+    assert k1[:6, 1].tolist() == [100 + t for t in range(6)] and v1[:6, 0].tolist() == [100 + t for t in range(6)]
+    assert v1[6:, 0].tolist() == [1100 + j for j in range(6)]
+    # The pivot keeps its whole prompt; retrieval never writes it.
+    assert orc.rows[0][2][1][:16, 0].tolist() == [200 + t for t in range(16)]
+    # Step 5's attention for satellite 1 (zero query: the mean of its V
+    # labels over 12 tokens).  Qwen order retrieves before attending, Llama
+    # order after, so only the Qwen output already sees positions 0..5.
+    got = outs[5][0, 1, 0]
+    expect = (sum(range(100, 106)) + sum(range(1100, 1106))) / 12 if select_first else \
+        (sum(range(110, 116)) + sum(range(1100, 1106))) / 12
+    assert abs(got - expect) < 1e-9
+    # Before any retrieval satellite 0 attends its prompt picks {14, 15}.
+    assert abs(outs[0][0, 0, 0] - (14 + 15 + 1000) / 3) < 1e-9
+
+
+def test_drift_check_even_median_is_not_below_threshold():
+    """The middle check of the hand case: overlaps 1 and 0 give the median
+    0.5 (mean of the middle pair), which does not trigger at threshold 0.5."""
+    scores = np.zeros((1, 2, 16), dtype=np.float32)
+    scores[0, 0] = np.arange(16)
+    scores[0, 1] = -np.arange(16)
+    ov, med, trig, cur = O.drift_check(scores, [[12, 13, 14, 15]], 4, 0.5)
+    assert ov.tolist() == [1.0, 0.0] and med == 0.5 and not trig
+    assert sorted(cur[0].tolist()) == [0, 1, 2, 3]
