@@ -38,6 +38,9 @@ SIGNATURES = {
     "hc_decode_attn": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                c_int, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_int64, c_int,
                                c_void_p, c_void_p]),
+    "hc_decode_attn_noalloc": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_int, c_int, c_float, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p,
+                                       c_void_p]),
     "hc_decode_num_parts": (c_int64, [c_void_p, c_int, c_int]),
     "hc_decode_chunk_tiles": (c_int, [c_int, c_void_p, c_int, c_int]),
     "hc_decode_workspace_size": (c_size_t, [c_int, c_int, c_int64]),

@@ -498,6 +498,14 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
 
 constexpr int kDecodeWaves = 4;
 
+// Device-resident workspace of hc_decode_attn_noalloc, for callers that
+// cannot allocate.  Each device holds its own copy for the life of the
+// process; host code never passes the symbol itself to a kernel (in host
+// code it only names the symbol), it uses the address hipGetSymbolAddress
+// returns for the current device.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
 int64_t decode_num_parts(const int* host_row_len, int rows, int chunk_tiles) {
   int64_t total = 0;
   for (int r = 0; r < rows; ++r) {
@@ -656,4 +664,47 @@ extern "C" int hc_decode_attn(int dtype, const void* q, void* kstore, void* vsto
   clear_error();
   return decode_entry(dtype, q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale, k_new,
                       v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, stream);
+}
+
+// Address of this device's scratch array, resolved once per device on the
+// first call made with that device current.
+static int noalloc_scratch(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return set_error(HC_ERR_HIP, "hc_decode_attn_noalloc: no current device");
+  static std::mutex mu;
+  static void* addr[64] = {nullptr};
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(HC_ERR_HIP, "hc_decode_attn_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return HC_OK;
+}
+
+extern "C" int hc_decode_attn_noalloc(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
+                                      int32_t* row_len, const int32_t* row_cap, const int32_t* row_order, int rows,
+                                      int group, float scale, const void* k_new, const void* v_new, void* out,
+                                      int64_t num_parts, int chunk_tiles, int32_t* status, void* stream) {
+  clear_error();
+  if (rows > 0 && group >= 1 && group <= 16 && num_parts > 0) {
+    const size_t need = decode_workspace_bytes_rows(rows, group, num_parts);
+    if (need > kNoAllocScratchBytes)
+      return set_error(HC_ERR_INVALID,
+                       "hc_decode_attn_noalloc: %d rows x group %d x %lld parts need %zu bytes of workspace, above the "
+                       "%zu-byte device scratch (use hc_decode_attn with a caller workspace)",
+                       rows, group, (long long)num_parts, need, kNoAllocScratchBytes);
+  }
+  if (rows <= 0 || group < 1 || group > 16 || chunk_tiles < 1)
+    return decode_entry(dtype, q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale,
+                        k_new, v_new, out, nullptr, 0, num_parts, chunk_tiles, status, stream);
+  void* ws = nullptr;
+  const int rc = noalloc_scratch(&ws);
+  if (rc) return rc;
+  return decode_entry(dtype, q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale, k_new,
+                      v_new, out, ws, kNoAllocScratchBytes, num_parts, chunk_tiles, status, stream);
 }

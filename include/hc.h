@@ -91,6 +91,25 @@ int hc_decode_attn(int dtype, const void* q, void* kstore, void* vstore, const i
                    const int32_t* row_cap, const int32_t* row_order, int rows, int group, float scale,
                    const void* k_new, const void* v_new, void* out, void* workspace, size_t workspace_bytes,
                    int64_t num_parts, int chunk_tiles, int32_t* status, void* stream);
+/*
+ * hc_decode_attn without a caller workspace, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc); it has no counterpart in the reference.  Arguments and
+ * results are those of hc_decode_attn; the split-K partials live in a 16 MiB
+ * device array of the library (one per device, held until the process ends,
+ * its address resolved on the first call made on that device -- make that
+ * first call outside graph capture).  Launches whose
+ * hc_decode_workspace_size(rows, group, num_parts) exceeds 16 MiB are
+ * rejected with HC_ERR_INVALID.  Every call on a device shares that device's
+ * array: calls that overlap in time on one device (two streams, or two
+ * threads) race and must be serialised by the caller.  The array needs no
+ * clearing between calls.  The call allocates and frees nothing.
+ */
+int hc_decode_attn_noalloc(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
+                           int32_t* row_len, const int32_t* row_cap, const int32_t* row_order, int rows, int group,
+                           float scale, const void* k_new, const void* v_new, void* out, int64_t num_parts,
+                           int chunk_tiles, int32_t* status, void* stream);
+
 /* Workgroups (chunks) of one hc_decode_attn launch over these lengths. */
 int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, int chunk_tiles);
 /* chunk_tiles for hc_decode_attn: the smallest chunk (at least 4 tiles)
