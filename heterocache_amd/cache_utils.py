@@ -179,6 +179,14 @@ class HeteroCache(DynamicCache):
         self._lead_base = None       # first global leader index of each layer
         self._due = []               # layers whose check waits for the batched launch
         self._batch_meta = {}
+        # Optional callable observer(event, **tensors), told about every score
+        # array the cache ranks and the sets and flags it derives from them
+        # (device tensors, valid on the current stream): "prefill_select"
+        # (layer, rows, scores [rows, L], idx, counts), "pivot_sets" (layer,
+        # pivots, scores [B * npiv, L] rows (b, pivot), K), "drift_check"
+        # (row_ids [(layer, leader head, b)], scores [J, S, L], cur, trigger,
+        # trig_of, ret_idx, ret_counts).  None (the default) costs nothing.
+        self.observer = None
 
     # -- reference API ------------------------------------------------------
     def __bool__(self):
@@ -388,6 +396,8 @@ class HeteroCache(DynamicCache):
                                             round_dtype=self._round_dtype(query_states.dtype))
         K = min(self.base_compress_len, L)
         idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
+        if self.observer is not None:
+            self.observer("pivot_sets", layer=layer_idx, pivots=pivots, scores=scores, idx=idx, K=K)
         # Sets are stored in relation order, one row per (leader, batch).
         leaders = [int(h) for h, m in rel.items()]
         members = [list(m) for h, m in rel.items()]
@@ -455,7 +465,9 @@ class HeteroCache(DynamicCache):
         else:
             scores = compress.last_query_scores(query_states, key_states, range(n_c), G, self.pooling,
                                                 self.kernel_size, round_dtype=self._round_dtype(query_states.dtype))
-        idx, _ = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0)
+        idx, counts = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0)
+        if self.observer is not None:
+            self.observer("prefill_select", layer=layer_idx, rows=rows, scores=scores, idx=idx, counts=counts)
         store.write_rows(key_states, value_states, [(b, h) for b in range(self.bsz) for h in range(n_c)], rows,
                          caps_rows, idx=idx)
 
@@ -580,6 +592,10 @@ class HeteroCache(DynamicCache):
         ops.set_bits(last, None, st.ref_bits, L, fixed_count=K, trigger=st.trigger, trig_of=m["trig_of"])
         if m["plans"]:
             self._retrieve(layer_idx, st, scores[:, S - 1])
+        if self.observer is not None:
+            self.observer("drift_check", row_ids=[(layer_idx, h, b) for h in st.leaders for b in range(B)],
+                          scores=scores.view(nl * B, S, L), cur=m["cur"], trigger=st.trigger, trig_of=m["trig_of"],
+                          ret_idx=m.get("ret_idx"), ret_counts=m.get("ret_counts"))
 
     def _check_batched(self, layers):
         """Drift checks of a group of leader layers in one launch sequence: scores
@@ -607,9 +623,13 @@ class HeteroCache(DynamicCache):
         ops.drift_decide(bm["overlap"], nlead, B, S, K, self.stable_threshold, trig)
         last = bm["cur"].view(J, S, -1)[:, S - 1]
         ops.set_bits(last, None, bits, L, fixed_count=K, trigger=trig, trig_of=bm["trig_of"])
+        if bm["plans"]:
+            ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
+        if self.observer is not None:
+            self.observer("drift_check", row_ids=bm["row_ids"], scores=scores, cur=bm["cur"], trigger=trig,
+                          trig_of=bm["trig_of"], ret_idx=bm.get("ret_idx"), ret_counts=bm.get("ret_counts"))
         if not bm["plans"]:
             return
-        ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
         dev = qa.device
         main = torch.cuda.current_stream(dev)
         host = self.device == "cpu"
@@ -634,7 +654,7 @@ class HeteroCache(DynamicCache):
         qa = self._qbuf_all
         B, Hkv, G, S, L = self.bsz, self.num_kv_heads, self.num_key_value_groups, self.decode_step, self.prefill_len
         K = min(self.base_compress_len, L)
-        q_off, k_row, trig_of, ret_caps, jobs = [], [], [], [], {}
+        q_off, k_row, trig_of, ret_caps, jobs, row_ids = [], [], [], [], {}, []
         gl0 = self._lead_base[layers[0]]
         j = 0
         for layer in layers:
@@ -647,6 +667,7 @@ class HeteroCache(DynamicCache):
                 for b in range(B):
                     if j != (lb + i) * B + b:
                         raise RuntimeError("batched drift rows out of the global leader order")
+                    row_ids.append((layer, h, b))
                     q_off.append(layer * qa.stride(0) + b * qa.stride(1) + h * G * qa.stride(2))
                     k_row.append(layer * B * Hkv + b * Hkv + h)
                     trig_of.append(lb + i)
@@ -656,7 +677,7 @@ class HeteroCache(DynamicCache):
                             jobs.setdefault(layer, []).append((j, lb + i, b, mm, n))
                     j += 1
         J = j
-        m = {"K": K, "J": J, "lead0": gl0}
+        m = {"K": K, "J": J, "lead0": gl0, "row_ids": row_ids}
         m["q_off"] = torch.as_tensor(np.asarray(q_off, dtype=np.int64)).to(dev)
         m["k_row"] = torch.as_tensor(np.asarray(k_row, dtype=np.int32)).to(dev)
         m["caps_K"] = torch.full((J * S,), K, dtype=torch.int32, device=dev)

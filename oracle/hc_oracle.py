@@ -764,24 +764,54 @@ class CacheOracle:
     match the device build: float32 retrieval lengths and each pivot compared
     with its own reference set (quirks=True: the reference's float64 lengths
     and relation-order set indexing).
+
+    Rows live in buffers sized for `max_gen` decode tokens, so long contexts
+    append without copying; rows[layer][r] is [K view, V view] of the row's
+    current tokens.
+
+    score_hook(kind, layer, head, scores) -> scores, when given, sees every
+    score array the flow ranks before it is ranked and returns the array the
+    selection then uses: kind "prefill" (head h, [L] for one batch row --
+    called once per (b, h) in batch-major order), "pivot" (pivot head, [L]
+    per batch row), "drift" (leader head, [B, S, L]).  A test can record the
+    oracle's own scores there and substitute a device's, so that the flow's
+    integer logic (top-k and its tie rule, overlaps, medians, triggers,
+    ascending prefixes, slot writes) is checked exactly on the device's
+    scores while the scores themselves are compared within a tolerance.
     """
 
     def __init__(self, data, batch, q_heads, kv_heads, num_layers, ratio, threshold, decode_step, pooling, kernel,
-                 retrieval_topk=None, quirks=False, select_before_attention=False):
+                 retrieval_topk=None, quirks=False, select_before_attention=False, max_gen=64, score_hook=None):
         self.data = data
         self.B, self.Hq, self.Hkv, self.NL = batch, q_heads, kv_heads, num_layers
         self.G = q_heads // kv_heads
         self.ratio, self.threshold, self.S = ratio, threshold, decode_step
         self.pooling, self.kernel = pooling, kernel
         self.topk, self.quirks, self.select_first = retrieval_topk, quirks, select_before_attention
+        self.max_gen = max_gen
+        self.score_hook = score_hook
         self.full_heads = data["meta"]["counts"]["volatile"] + data["meta"]["counts"]["pivot"]
-        self.rows = {}      # layer -> list over b*Hkv+h of [len, 128] K and V arrays
+        self.rows = {}      # layer -> list over b*Hkv+h of [K, V] views [len, 128]
+        self._buf = {}      # layer -> list over rows of (K, V) buffers [len + max_gen, 128]
         self.tier = {}      # layer -> (K, V) [B, Hkv, L, 128]
         self.ref = {}       # layer -> {leader: [set per b]}
         self.qbuf = {}
         self.base = None
         self.L = None
         self.triggers = []  # (layer, leader, triggered) per check
+        self.medians = []   # (layer, leader, median) per check
+
+    def _scores(self, kind, layer, head, scores):
+        return scores if self.score_hook is None else self.score_hook(kind, layer, head, scores)
+
+    def _set_row(self, layer, r, k_rows, v_rows):
+        n, d = k_rows.shape
+        kb = np.zeros((n + self.max_gen, d), dtype=k_rows.dtype)
+        vb = np.zeros((n + self.max_gen, d), dtype=v_rows.dtype)
+        kb[:n] = k_rows
+        vb[:n] = v_rows
+        self._buf[layer][r] = (kb, vb)
+        self.rows[layer][r] = [kb[:n], vb[:n]]
 
     def prefill(self, layer, q, k, v):
         B, Hkv, L, _ = k.shape
@@ -791,28 +821,33 @@ class CacheOracle:
         keep = set(self.data["need_to_keep_counts"][layer])
         n_c = self.data["need_to_compress_counts"][layer]
         caps = prefill_caps(self.base, self.data["allocation_matrix"][layer][:n_c], L)
-        rows = []
+        self.rows[layer] = [None] * (B * Hkv)
+        self._buf[layer] = [None] * (B * Hkv)
+        empty = np.zeros((0, k.shape[-1]), k.dtype)
         for b in range(B):
             for h in range(Hkv):
+                r = b * Hkv + h
                 if h in keep:
-                    rows.append([k[b, h].copy(), v[b, h].copy()])
+                    self._set_row(layer, r, k[b, h], v[b, h])
                 elif h < n_c:
                     s = last_query_scores(q[b, h * self.G:(h + 1) * self.G, -1][None], k[b, h][None], self.pooling,
                                           self.kernel)[0]
+                    s = self._scores("prefill", layer, h, s)
                     sel = topk_select(s, int(caps[h]))
-                    rows.append([k[b, h][sel], v[b, h][sel]])
+                    self._set_row(layer, r, k[b, h][sel], v[b, h][sel])
                 else:
-                    rows.append([np.zeros((0, k.shape[-1]), k.dtype), np.zeros((0, k.shape[-1]), k.dtype)])
-        self.rows[layer] = rows
-        self.tier[layer] = (k.copy(), v.copy())
+                    self._set_row(layer, r, empty, empty)
+        self.tier[layer] = (k, v)
         pivots = list(self.data["need_to_select_counts"][layer])
         rel = self.data["leader_member_relations"][layer]
         K = min(self.base, L)
         sets = {}
         for p in pivots:
-            sets[p] = [set(topk_indices(last_query_scores(q[b, p * self.G:(p + 1) * self.G, -1][None], k[b, p][None],
-                                                          self.pooling, self.kernel)[0], K).tolist())
-                       for b in range(B)]
+            sets[p] = []
+            for b in range(B):
+                s = last_query_scores(q[b, p * self.G:(p + 1) * self.G, -1][None], k[b, p][None], self.pooling,
+                                      self.kernel)[0]
+                sets[p].append(set(topk_indices(self._scores("pivot", layer, p, s), K).tolist()))
         ref = {}
         for i, leader in enumerate(int(x) for x in rel):
             src = pivots[min(i, len(pivots) - 1)] if self.quirks else leader
@@ -820,21 +855,31 @@ class CacheOracle:
         self.ref[layer] = ref
         self.qbuf[layer] = []
 
-    def decode(self, layer, q, k_new, v_new):
-        """One decode step of one layer; returns attention output [B, Hq, 128] (float64)."""
+    def decode(self, layer, q, k_new, v_new, attend=True):
+        """One decode step of one layer; returns attention output [B, Hq, 128]
+        (float64), or None with attend=False (the step's append and selection
+        still happen)."""
         B, Hkv = self.B, self.Hkv
         for b in range(B):
             for h in range(Hkv):
-                r = self.rows[layer][b * Hkv + h]
-                r[0] = np.concatenate([r[0], k_new[b, h]])
-                r[1] = np.concatenate([r[1], v_new[b, h]])
+                r = b * Hkv + h
+                kb, vb = self._buf[layer][r]
+                n = len(self.rows[layer][r][0])
+                if n >= len(kb):
+                    raise RuntimeError(f"Layer {layer} OOM.")
+                kb[n] = k_new[b, h, 0]
+                vb[n] = v_new[b, h, 0]
+                self.rows[layer][r] = [kb[:n + 1], vb[:n + 1]]
         if self.select_first:
             self._select(layer, q)
-        qa = q[:, :, 0].reshape(B * Hkv, self.G, -1)
-        out = decode_attention(qa, [r[0] for r in self.rows[layer]], [r[1] for r in self.rows[layer]])
+        out = None
+        if attend:
+            qa = q[:, :, 0].reshape(B * Hkv, self.G, -1)
+            out = decode_attention(qa, [r[0] for r in self.rows[layer]], [r[1] for r in self.rows[layer]])
+            out = out.reshape(B, self.Hq, -1)
         if not self.select_first:
             self._select(layer, q)
-        return out.reshape(B, self.Hq, -1)
+        return out
 
     def _select(self, layer, q):
         self.qbuf[layer].append(q[:, :, 0])
@@ -853,8 +898,10 @@ class CacheOracle:
             sc = np.stack([pivot_step_scores(qs[b, leader * self.G:(leader + 1) * self.G],
                                              self.rows[layer][b * self.Hkv + leader][0][:self.L], self.pooling,
                                              self.kernel) for b in range(self.B)])
+            sc = self._scores("drift", layer, leader, sc)
             _, med, trig, cur_last = drift_check(sc, [sorted(s) for s in self.ref[layer][leader]], K, self.threshold)
             self.triggers.append((layer, leader, bool(trig)))
+            self.medians.append((layer, leader, med))
             if not trig:
                 continue
             self.ref[layer][leader] = [set(c.tolist()) for c in cur_last]
