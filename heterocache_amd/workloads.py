@@ -266,17 +266,17 @@ class BlockDriftWorkload:
         return (slots * self.block).tolist()
 
     def prefill(self, layer):
-        """Prefill K/V [1, Hkv, L, d] (generated once per layer)."""
+        """Prefill K/V [1, Hkv, L, d] in the workload dtype."""
         torch, dev = self.torch, self.device
         g = torch.Generator(device=dev)
         g.manual_seed(self.seed * 1_000_003 + layer * 7919)
-        k = torch.randn((1, self.Hkv, self.L, self.d), generator=g, device=dev)
-        v = torch.randn((1, self.Hkv, self.L, self.d), generator=g, device=dev)
+        k = torch.randn((1, self.Hkv, self.L, self.d), generator=g, device=dev).to(self.dtype)
+        v = torch.randn((1, self.Hkv, self.L, self.d), generator=g, device=dev).to(self.dtype)
         return k, v
 
     def queries(self, layer, k):
         """The last prefill query [1, Hq, 1, d], decode queries [steps, 1, Hq,
-        1, d] and new K/V [steps, 1, Hkv, 1, d] for prefill keys k (float)."""
+        1, d] and new K/V [steps, 1, Hkv, 1, d] for this layer's prefill keys."""
         torch, dev, d = self.torch, self.device, self.d
         Hq = self.Hkv * self.G
         g = torch.Generator(device=dev)

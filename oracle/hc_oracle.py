@@ -138,12 +138,18 @@ def last_query_scores(q_last, k, pooling, kernel, io_dtype=None, scale=None):
     q_last = np.asarray(q_last, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
     d = q_last.shape[-1]
+    return _pooled_group_max(np.einsum("hgd,hld->hgl", q_last, k), d, pooling, kernel, io_dtype, scale)
+
+
+def _pooled_group_max(dots, d, pooling, kernel, io_dtype, scale):
+    """The steps of last_query_scores after the dot products q.k
+    (dots [n, G, L] float64): scale and casts, softmax_f32, pooling, max
+    over the group."""
     scale = 1.0 / math.sqrt(d) if scale is None else scale
-    logits = np.einsum("hgd,hld->hgl", q_last, k)
     if io_dtype not in (None, "float32"):
-        logits = round_to(round_to(logits, io_dtype) * np.float32(scale), io_dtype)
+        logits = round_to(round_to(dots, io_dtype) * np.float32(scale), io_dtype)
     else:
-        logits = (logits * scale).astype(np.float32)
+        logits = (dots * scale).astype(np.float32)
     w = round_to(softmax_f32(logits), io_dtype)
     w = round_to(pool1d(w, pooling, kernel), io_dtype)
     return w.max(axis=1)
@@ -648,10 +654,11 @@ def pivot_step_scores(q_steps, k_prefill, pooling, kernel, io_dtype=None, scale=
     """
     q = np.asarray(q_steps, dtype=np.float64)
     G, S, d = q.shape
-    out = last_query_scores(q.transpose(1, 0, 2).reshape(S, G, d),
-                            np.broadcast_to(np.asarray(k_prefill), (S,) + np.asarray(k_prefill).shape),
-                            pooling, kernel, io_dtype=io_dtype, scale=scale)
-    return out
+    k = np.asarray(k_prefill, dtype=np.float64)
+    # Every (step, head) row against the same keys: one product, then the
+    # per-step steps of last_query_scores.
+    dots = (q.transpose(1, 0, 2).reshape(S * G, d) @ k.T).reshape(S, G, -1)
+    return _pooled_group_max(dots, d, pooling, kernel, io_dtype, scale)
 
 
 def drift_check(step_scores, ref_set, base_len, threshold):

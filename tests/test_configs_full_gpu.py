@@ -203,3 +203,309 @@ def test_config2_needles_128k_llama_json(dev):
                 rows_k = orc.rows[layer][m][0][:n]
                 for p in needles[layer]:
                     assert (rows_k == tier_k[m, p]).all(axis=1).any(), (layer, m, p)
+
+
+def test_config4_chunked_224k_then_drift_block(dev):
+    """Config 4: Llama-3-8B shape at 229376 tokens, all 32 layers with the
+    reference's head JSON.  An 8K-chunked prefill (chunks fed layer by
+    layer, in model order) leaves every store, length and reference set
+    identical to a single-shot prefill of the same K/V.  Then 205 decode
+    steps on the chunked cache (full-KV tier in host-pinned memory,
+    top-1024 retrieval) with attention drifting to a new block of 8 keys
+    at step 200: no leader triggers in the 40 checks inside the first block,
+    every leader triggers at the check after the boundary.  Layer 23 is
+    checked against the oracle stage by stage (attention at sampled
+    steps)."""
+    L, Hkv, G, D, NL, S, steps, chunk = 229376, 8, 4, 128, 32, 5, 205, 8192
+    checked = [23]
+    data = llama_json()
+    rec = Recorder(checked)
+
+    def make(host_tier):
+        cfg = HeteroCacheConfig(data, compression_ratio=0.5, stable_threshold=0.5, real_offload=host_tier,
+                                max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
+                                num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024)
+        return HeteroCache(cfg)
+
+    whole, chunked = make(False), make(True)
+    chunked.begin_prefill(L)
+    chunked.observer = rec
+    wl = workloads.BlockDriftWorkload(L, kv_heads=Hkv, group=G, steps=steps, period=200, seed=1004, device=dev)
+    kv, step_inputs = {}, {}
+    for layer in range(NL):
+        k, v = wl.prefill(layer)
+        x = wl.queries(layer, k)
+        kv[layer] = (k, v)
+        step_inputs[layer] = (x["q_last"], x["q_steps"], x["k_new"], x["v_new"])
+        kc, vc = whole.update(k, v, layer)
+        whole.init_coefficient(x["q_last"], kc, layer)
+        whole.prefill_select(x["q_last"], kc, vc, layer)
+    filler = torch.zeros((1, Hkv * G, 1, D), dtype=torch.bfloat16, device=dev)
+    for s in range(0, L, chunk):
+        e = min(s + chunk, L)
+        for layer in range(NL):
+            k, v = kv[layer]
+            q = step_inputs[layer][0] if e == L else filler
+            kc, vc = chunked.update(k[:, :, s:e], v[:, :, s:e], layer, {"query_states": q})
+            assert kc.shape[2] == e
+            chunked.init_coefficient(q, kc, layer)
+            chunked.prefill_select(q, kc, vc, layer)
+            assert chunked.prefill_pending(layer) == (e < L)
+    torch.cuda.synchronize()
+    assert whole.base_compress_len == chunked.base_compress_len == 86851
+    assert torch.equal(whole._arena[0], chunked._arena[0]) and torch.equal(whole._arena[1], chunked._arena[1])
+    assert torch.equal(whole._ref_bits_all, chunked._ref_bits_all)
+    for a, b in zip(whole.stores, chunked.stores):
+        assert a.host_len.tolist() == b.host_len.tolist() and torch.equal(a.row_len, b.row_len)
+    del whole
+    hook = DeviceScores(rec, 0.5)
+    orc = O.CacheOracle(data, 1, Hkv * G, Hkv, NL, 0.5, 0.5, S, "avgpool", 5, retrieval_topk=1024,
+                        max_gen=steps + 4, score_hook=hook)
+    hook.orc = orc
+    for layer in checked:
+        orc.prefill(layer, as_np(step_inputs[layer][0]), as_np(kv[layer][0]), as_np(kv[layer][1]))
+    kv.clear()
+    attend_at = {0, 1, 100, 199, 200, 201, 204}
+    for t in range(steps):
+        outs = {}
+        for layer in range(NL):
+            _, qs, kn, vn = step_inputs[layer]
+            chunked.update(kn[t], vn[t], layer)
+            o = chunked.decode_attention(qs[t], layer)
+            chunked.decode_select(qs[t], layer)
+            if layer in checked:
+                outs[layer] = o
+        for layer in checked:
+            _, qs, kn, vn = step_inputs[layer]
+            ref = orc.decode(layer, as_np(qs[t]), as_np(kn[t]), as_np(vn[t]), attend=t in attend_at)
+            if ref is not None:
+                err = np.abs(as_np(outs[layer]).reshape(1, Hkv * G, D) - ref).max()
+                assert err <= ATTN_TOL, f"step {t} layer {layer}: max-abs {err}"
+    torch.cuda.synchronize()
+    assert len(rec.checks) == steps // S == 41
+    for c, flags in enumerate(rec.checks):
+        assert len(flags) == 33
+        assert all(f == (c == 40) for f in flags.values()), (c, [k for k, f in flags.items() if f != (c == 40)])
+    dev_trig = [(l, h, rec.checks[c][(l, h)]) for c in range(len(rec.checks)) for l in checked
+                for h in chunked._drift[l].leaders]
+    assert sorted(dev_trig) == sorted(orc.triggers)
+    for layer, leader, own_med, own_trig, dev_med in hook.own:
+        assert abs(own_med - 0.5) >= 0.05 and abs(dev_med - own_med) < 5e-3
+    assert [t for *_, t, _ in hook.own] == [t for _, _, t in orc.triggers]
+    assert max(e for *_, e in hook.err) <= SCORE_RTOL
+    check_stores(chunked, orc, checked, 1, Hkv)
+    check_ref_sets(chunked, orc, checked, L)
+
+
+@pytest.mark.parametrize("ctx", [16384, 32768, 49152, 65536])
+def test_config3_qwen_sequence_full_context(dev, ctx):
+    """Config 3, one sequence of the ragged batch per run (the reference's
+    cache is defined for batch 1, so each sequence is checked against a
+    batch-1 oracle run): Qwen2.5-7B shape (28 layers, 4 KV heads, GQA 7),
+    ratio 0.25, synthetic head JSON with at most 14 full heads, top-512
+    retrieval, drift check every 5 steps at threshold 0.5, Qwen order
+    (select before attention, so a retrieval is attended in its own step).
+    10 decode steps: every leader keeps its set at the first check and
+    triggers at the second.  The first layer with a satellite is checked
+    against the oracle stage by stage."""
+    Hkv, G, D, NL, S, steps = 4, 7, 128, 28, 5, 10
+    raw = workloads.synthetic_head_json(NL, Hkv, 1003, max_full=14)
+    data = utils.augment_head_data(raw, [utils.head_permutation(r) for r in raw["classification_matrix"]])
+    checked = [next(l for l in range(NL) if any(data["leader_member_relations"][l].values()))]
+    rec = Recorder(checked)
+    cfg = HeteroCacheConfig(data, compression_ratio=0.25, stable_threshold=0.5, real_offload=True,
+                            max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
+                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=512)
+    cache = HeteroCache(cfg)
+    cache.observer = rec
+    wl = workloads.NeedleWorkload(ctx, kv_heads=Hkv, group=G, steps=steps, decode_step=S, seed=1003 + ctx, device=dev)
+    hook = DeviceScores(rec, 0.5)
+    orc = O.CacheOracle(data, 1, Hkv * G, Hkv, NL, 0.25, 0.5, S, "avgpool", 5, retrieval_topk=512,
+                        select_before_attention=True, max_gen=steps + 4, score_hook=hook)
+    hook.orc = orc
+    step_inputs = {}
+    for layer in range(NL):
+        x = wl.layer(layer)
+        k, v = cache.update(x["k"], x["v"], layer)
+        cache.init_coefficient(x["q_last"], k, layer)
+        cache.prefill_select(x["q_last"], k, v, layer)
+        if layer in checked:
+            orc.prefill(layer, as_np(x["q_last"]), as_np(x["k"]), as_np(x["v"]))
+        step_inputs[layer] = (x["q_steps"], x["k_new"], x["v_new"])
+        del x, k, v
+    F = data["meta"]["counts"]["volatile"] + data["meta"]["counts"]["pivot"]
+    assert cache.base_compress_len == orc.base == workloads.get_compress_len(0.25, F, ctx, Hkv * NL) > 0
+    for t in range(steps):
+        outs = {}
+        for layer in range(NL):
+            q, kn, vn = (a[t] for a in step_inputs[layer])
+            cache.update(kn, vn, layer)
+            cache.decode_select(q, layer)
+            o = cache.decode_attention(q, layer)
+            if layer in checked:
+                outs[layer] = o
+        for layer in checked:
+            q, kn, vn = (as_np(a[t]) for a in step_inputs[layer])
+            ref = orc.decode(layer, q, kn, vn)
+            err = np.abs(as_np(outs[layer]).reshape(1, Hkv * G, D) - ref).max()
+            assert err <= ATTN_TOL, f"step {t} layer {layer}: max-abs {err}"
+    torch.cuda.synchronize()
+    nlead = sum(len(r) for r in data["leader_member_relations"])
+    # Qwen order checks layer by layer: group each leader's flags over the checks.
+    flags = {}
+    for f in rec.checks:
+        for key, val in f.items():
+            flags.setdefault(key, []).append(val)
+    assert len(flags) == nlead and all(v == [False, True] for v in flags.values()), flags
+    dev_trig = [(l, h, flags[(l, h)][c]) for c in range(2) for l in checked for h in cache._drift[l].leaders]
+    assert sorted(dev_trig) == sorted(orc.triggers)
+    for layer, leader, own_med, own_trig, dev_med in hook.own:
+        assert abs(own_med - 0.5) >= 0.05 and abs(dev_med - own_med) < 5e-3
+    assert [t for *_, t, _ in hook.own] == [t for _, _, t in orc.triggers]
+    assert max(e for *_, e in hook.err) <= SCORE_RTOL
+    check_stores(cache, orc, checked, 1, Hkv)
+    check_ref_sets(cache, orc, checked, ctx)
+
+
+def _sdpa_repeated_kv(module, query, key, value, attention_mask, dropout=0.0, scaling=None, is_causal=None,
+                      **kwargs):
+    """transformers attention function for the float32 stock reference:
+    K/V repeated to the query heads, then PyTorch SDPA with the causal flag
+    (transformers' own SDPA path passes grouped K/V, which only SDPA's math
+    kernel takes; at 32K in float32 its score matrix does not fit)."""
+    import torch.nn.functional as F
+    if attention_mask is not None:
+        raise ValueError("the float32 reference runs without an attention mask")
+    rep = query.shape[1] // key.shape[1]
+    key = key.repeat_interleave(rep, dim=1)
+    value = value.repeat_interleave(rep, dim=1)
+    out = F.scaled_dot_product_attention(query, key, value, is_causal=query.shape[2] > 1, scale=scaling)
+    return out.transpose(1, 2).contiguous(), None
+
+
+def _llama8b_config(max_pos, attn="sdpa"):
+    from transformers import LlamaConfig
+    return LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                       num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=max_pos,
+                       rope_theta=500000.0, attn_implementation=attn)
+
+
+def test_config1_llama8b_32k_generate(dev):
+    """Config 1: the 32-layer Llama-3-8B shape (random init, vocab 128256) on
+    a 32768-token prompt of seeded random ids, 256 greedy tokens.
+
+    * Keep-all budgets (one anchor keeping the whole prompt, every other head
+      full) in float32: the patched model's generate() under HeteroCache
+      returns the stock transformers model's tokens (SDPA attention,
+      DynamicCache), and its per-step logits agree within 1e-3 relative.
+      (In bf16 a random-init 32-layer model turns rounding into logit
+      differences of several percent -- transformers' own eager and SDPA
+      paths differ by about 9 % -- so greedy tokens cannot pin equivalence
+      there.)
+    * Compressed, bf16, as the configuration specifies: ratio 0.5 with the
+      seeded synthetic clusters of 1-4 heads, drift checks every 5 steps;
+      layer 17's decode attention at steps 0, 127 and 254 equals the float64
+      closed form over its store rows and the appended token (<= 2e-2), and
+      every row's length advances by one per generated token."""
+    from transformers import LlamaForCausalLM
+    L, new, D = 32768, 256, 128
+    cfg = _llama8b_config(L + new + 8)
+    ids = torch.randint(0, 128256, (1, L), generator=torch.Generator().manual_seed(1001)).to(dev)
+    def greedy(model, cache):
+        """Greedy decoding by plain forwards, without an attention mask."""
+        toks, logits = [], []
+        with torch.no_grad():
+            o = model(ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+            for _ in range(new):
+                lg = o.logits[:, -1].float()
+                logits.append(lg)
+                toks.append(lg.argmax(-1))
+                o = model(toks[-1].view(1, 1), past_key_values=o.past_key_values, use_cache=True)
+        return torch.stack(toks, 1), torch.cat(logits)
+
+    from transformers import AttentionInterface
+    AttentionInterface.register("sdpa_repeated_kv", _sdpa_repeated_kv)
+    torch.manual_seed(0)
+    with torch.device(dev):
+        stock = LlamaForCausalLM(_llama8b_config(L + new + 8, "sdpa_repeated_kv")).eval()
+    ref_toks, ref_logits = greedy(stock, None)
+    weights = stock.state_dict()
+    del stock
+    torch.cuda.empty_cache()
+    keep_all = {"meta": {"type_map": dict(workloads.TYPE_MAP),
+                         "counts": {"anchor": 1, "volatile": 255, "pivot": 0, "satellite": 0}},
+                "classification_matrix": [[1] + [2] * 7] + [[2] * 8 for _ in range(31)],
+                "allocation_matrix": [[1.0] + [-1.0] * 7] + [[-1.0] * 8 for _ in range(31)],
+                "leader_member_relations": [{} for _ in range(32)]}
+    with utils.install_attention_patch():
+        with torch.device(dev):
+            model = LlamaForCausalLM(cfg).eval()
+    model.load_state_dict(weights)
+    perms = utils.reorder_model_weights_by_classification(model, keep_all)
+    cc = utils.build_cache_config(model, utils.augment_head_data(keep_all, perms), compression_ratio=1.0,
+                                  max_gen_len=new + 8)
+    toks, logits = greedy(model, HeteroCache(cc))
+    assert torch.equal(toks, ref_toks)
+    rel = ((logits - ref_logits).norm(dim=-1) / ref_logits.norm(dim=-1)).max().item()
+    assert rel <= 1e-3, rel
+    del model, toks, logits, ref_toks, ref_logits
+    torch.cuda.empty_cache()
+
+    # Compressed bf16 run of the configuration.
+    raw = workloads.synthetic_head_json(32, 8, 1001)
+    with utils.install_attention_patch():
+        with torch.device(dev):
+            model = LlamaForCausalLM(cfg).to(torch.bfloat16).eval()
+    model.load_state_dict({k: v.to(torch.bfloat16) for k, v in weights.items()})
+    del weights
+    perms = utils.reorder_model_weights_by_classification(model, raw)
+    data = utils.augment_head_data(raw, perms)
+    cc = utils.build_cache_config(model, data, compression_ratio=0.5, max_gen_len=new + 8, decode_step=5)
+    utils.attach_cache(model, cc)
+    sampled, at, errs, caches = 17, {0, 127, new - 2}, [], []   # decode forwards are steps 0 .. new - 2
+    orig_attn, orig_init = HeteroCache.decode_attention, HeteroCache.__init__
+    calls = {"n": 0}
+
+    def spy_init(self, c):
+        orig_init(self, c)
+        caches.append(self)
+
+    def spy_attn(self, query_states, layer_idx, out=None):
+        if layer_idx != sampled:
+            return orig_attn(self, query_states, layer_idx, out)
+        step = calls["n"]
+        calls["n"] += 1
+        if step not in at:
+            return orig_attn(self, query_states, layer_idx, out)
+        torch.cuda.synchronize()   # retrieval gathers on the side stream included
+        store = self.stores[layer_idx]
+        kn, vn = self._pending[layer_idx]
+        rows = range(store.rows)
+        ks = [np.concatenate([as_np(store.read_rows([r], int(store.host_len[r]))[0][0]), as_np(kn[0, r])])
+              for r in rows]
+        vs = [np.concatenate([as_np(store.read_rows([r], int(store.host_len[r]))[1][0]), as_np(vn[0, r])])
+              for r in rows]
+        o = orig_attn(self, query_states, layer_idx, out)
+        qq = as_np(query_states).reshape(store.rows, -1, D)
+        errs.append(float(np.abs(as_np(o).reshape(store.rows, -1, D) - O.decode_attention(qq, ks, vs)).max()))
+        return o
+
+    HeteroCache.decode_attention, HeteroCache.__init__ = spy_attn, spy_init
+    try:
+        with torch.no_grad():
+            seq = model.generate(ids, max_new_tokens=new, do_sample=False)
+    finally:
+        HeteroCache.decode_attention, HeteroCache.__init__ = orig_attn, orig_init
+    torch.cuda.synchronize()
+    assert seq.shape == (1, L + new)
+    assert len(errs) == 3 and max(errs) <= ATTN_TOL, errs
+    cache = caches[-1]
+    assert sum(len(r) for r in data["leader_member_relations"]) > 0
+    # 255 decode forwards after the prefill (the last token is not fed back):
+    # keep heads hold the prompt, compressed heads their float32 budget.
+    for layer in range(32):
+        n_c = data["need_to_compress_counts"][layer]
+        caps = O.prefill_caps(cache.base_compress_len, data["allocation_matrix"][layer][:n_c], L)
+        keep = set(data["need_to_keep_counts"][layer])
+        expect = [(L if h in keep else int(caps[h])) + new - 1 for h in range(8)]
+        assert cache.stores[layer].row_len.tolist() == expect, layer

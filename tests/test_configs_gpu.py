@@ -65,13 +65,12 @@ def test_config0_snapkv_layer_then_decode(dev):
 
 def test_config3_qwen_gqa7_ragged_batch_decode(dev):
     """Config 3 geometry (Qwen2.5-7B: 4 KV heads, GQA 7, ratio 0.25) with
-    four sequences of ragged contexts, one row per (sequence, KV head):
-    each sequence's budgets follow its own context (the reference handles
-    batch rows one sequence at a time); contexts are the configuration's
-    16/32/48/64K scaled down by 4.  One decode step with the fused append,
-    bf16, against the float64 oracle."""
+    four sequences of ragged contexts 16/32/48/64K in one launch, one row
+    per (sequence, KV head): each sequence's budgets follow its own context
+    (the reference handles batch rows one sequence at a time).  One decode
+    step with the fused append, bf16, against the float64 oracle."""
     NL, Hkv, G = 28, 4, 7
-    contexts = [4096, 8192, 12288, 16384]
+    contexts = [16384, 32768, 49152, 65536]
     # One full-KV head per layer pair (14 of 112 heads) and compressed heads
     # with allocation weights 0.5 / 1.0 / 1.5 (mean 1).
     lens = []
