@@ -37,7 +37,11 @@ def parse():
     p.add_argument("--unfused-append", action="store_true", help="append in its own launch before attention")
     p.add_argument("--no-graph", action="store_true",
                    help="report the eager decode step (one host call per layer) instead of the HIP graph replay")
-    p.add_argument("--full-steps", type=int, default=20, help="decode steps of the HeteroCache phase")
+    p.add_argument("--full-steps", type=int, default=1000,
+                   help="decode steps of the natural-trigger run of the HeteroCache phase")
+    p.add_argument("--drift-groups", type=int, default=None,
+                   help="drift_check_groups of the HeteroCache phase (default: the config's default)")
+    p.add_argument("--full-step-only", action="store_true", help="run only the HeteroCache full-step phase")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
     p.add_argument("--prefill-only", action="store_true",
                    help="run only the prefill-attention phase and print its figures (for counter profiling)")
@@ -112,110 +116,152 @@ def cpu_baseline(ctx, budgets, seconds):
                       f"{el:.1f}s; {per * 1e6:.0f} us/layer"}
 
 
+def llama_head_json():
+    """The reference's head classification of Llama-3.1-8B-Instruct (33
+    pivots, 196 satellites, 17 volatile heads), after the head reorder."""
+    from heterocache_amd import utils
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
+                        "head_analysis_llama-3.1-8b-instruct.json")
+    with open(path) as f:
+        raw = json.load(f)
+    return utils.augment_head_data(raw, [utils.head_permutation(r) for r in raw["classification_matrix"]])
+
+
 def full_step_phase(args, torch, dev):
-    """Decode steps through HeteroCache at the same shape, with the pivot
-    drift check every 5 steps and top-1024 retrieval from the host-pinned
-    full-KV tier (satellite heads) on the side stream.
+    """The whole HeteroCache decode step on the 128K Llama-3-8B workload with
+    the reference's head JSON: per layer the fused append + attention, then
+    the pivot drift check every 5 steps (threshold 0.5) and top-1024
+    retrieval from the host-pinned full-KV tier into the satellites on the
+    side stream.  Step queries come from the needle workload (16 keys at
+    +6 sigma, query directions that move every other check), so checks
+    trigger naturally: every leader at every second check.
 
-    Runs twice on fresh caches: with a threshold no overlap can reach (drift
-    checked, never triggered) and with one every overlap is below (every
-    check retrieves), so the difference per step is the retrieval time the
-    decode step does not hide.  Also times the prefill of all layers: with
-    the full-KV tier in HBM (compression kernels alone) and in host-pinned
-    memory (bounded by the tier copy over the host link).
-    """
-    from heterocache_amd import utils, workloads
+    Three runs on fresh caches: natural triggers; a threshold no overlap
+    reaches (checks run, never trigger); one every overlap is below (every
+    check retrieves).  The difference between the last two, times 5, is the
+    retrieval time per check that the step does not hide.  The roofline
+    counts, per step, the attended K/V bytes, the pivots' keys read by the
+    check (amortised over its 5 steps) and the retrieved rows written into
+    HBM (amortised, triggered checks only), over the step time."""
+    from heterocache_amd import workloads
     from heterocache_amd.cache_utils import HeteroCache, HeteroCacheConfig
-    L, Hkv, G, D, NL = args.ctx, 8, 4, 128, args.layers
-    raw = workloads.synthetic_head_json(NL, Hkv, args.seed)
-    data = utils.augment_head_data(raw, [utils.head_permutation(r) for r in raw["classification_matrix"]])
-    steps = args.full_steps
+    L, Hkv, G, D, NL, S = args.ctx, 8, 4, 128, args.layers, 5
+    data = llama_head_json()
+    if NL != len(data["classification_matrix"]):
+        raise ValueError("the full step runs the reference JSON's 32 layers")
+    groups = args.drift_groups
+    # (label, threshold, steps, tier placement): the default placement keeps
+    # the 12.8 GB tier in HBM; the host-pinned tier is measured beside it.
+    runs = (("natural", 0.5, args.full_steps, "auto"), ("never", -1.0, 100, "auto"), ("always", 2.0, 100, "auto"),
+            ("host_never", -1.0, 100, "host"), ("host_always", 2.0, 100, "host"))
+    nsteps = max(n for _, _, n, _ in runs) + S
+    wl = workloads.NeedleWorkload(L, kv_heads=Hkv, group=G, steps=nsteps, decode_step=S, seed=args.seed, device=dev)
+    npiv = sum(len(p) for p in data["need_to_select_counts"])
+    sats = sum(len(r) for r in data["need_to_update_counts"])
+    check_k_bytes = npiv * L * D * 2
     res = {}
-    g = torch.Generator(device=dev).manual_seed(args.seed)
 
-    def make_cache(thr, host_tier):
-        cfg = HeteroCacheConfig(data, compression_ratio=args.ratio, stable_threshold=thr, real_offload=host_tier,
-                                max_gen_len=steps + 8, decode_step=5, pooling="avgpool", kernel_size=5,
-                                num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024)
+    def make_cache(thr, tier, max_gen):
+        kw = {} if groups is None else {"drift_check_groups": groups}
+        cfg = HeteroCacheConfig(data, compression_ratio=args.ratio, stable_threshold=thr, real_offload=True,
+                                max_gen_len=max_gen, decode_step=S, pooling="avgpool", kernel_size=5,
+                                num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
+                                tier_placement=tier, **kw)
         return HeteroCache(cfg)
 
-    def prefill(cache):
-        """All layers' prefill on resident inputs: main-stream ms per layer
-        (events) and total ms until every stream is idle (tier copies
-        included)."""
-        ks = [torch.randn((1, Hkv, L, D), device=dev, generator=g, dtype=torch.bfloat16) for _ in range(NL)]
-        vs = [torch.randn((1, Hkv, L, D), device=dev, generator=g, dtype=torch.bfloat16) for _ in range(NL)]
-        q = torch.randn((1, Hkv * G, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        t0 = time.perf_counter()
-        e0.record()
+    def prefill(cache, keep_inputs):
+        """All layers' prefill: main-stream ms per layer (events) and total
+        ms until every stream is idle (tier copies included)."""
+        inputs = []
+        ms, total = 0.0, 0.0
         for layer in range(NL):
-            cache.update(ks[layer], vs[layer], layer)
-            cache.init_coefficient(q, ks[layer], layer)
-            cache.prefill_select(q, ks[layer], vs[layer], layer)
-        e1.record()
-        torch.cuda.synchronize()
-        total = (time.perf_counter() - t0) * 1e3
-        del ks, vs
-        return e0.elapsed_time(e1) / NL, total
+            x = wl.layer(layer)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record()
+            k, v = cache.update(x["k"], x["v"], layer)
+            cache.init_coefficient(x["q_last"], k, layer)
+            cache.prefill_select(x["q_last"], k, v, layer)
+            e1.record()
+            torch.cuda.synchronize()
+            total += (time.perf_counter() - t0) * 1e3
+            ms += e0.elapsed_time(e1)
+            inputs.append((x["q_steps"], x["k_new"], x["v_new"]))
+            del x, k, v
+        return ms / NL, total, inputs
 
-    # Compression alone: the full-KV tier stays in HBM (no host-link copy).
-    # The first prefill pays one-time costs (arena and workspace allocation,
-    # library load) and is reported separately.
-    cache = make_cache(-1.0, False)
-    _, first_total = prefill(cache)
-    del cache
-    cache = make_cache(-1.0, False)
-    hbm_layer_ms, hbm_total = prefill(cache)
-    del cache
-    for label, thr in (("no_trigger", -1.0), ("always_trigger", 2.0)):
-        cache = make_cache(thr, True)
-        pre_ms, pre_total = prefill(cache)
-        qs = torch.randn((steps + 5, NL, 1, Hkv * G, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
-        kn = torch.randn((steps + 5, NL, 1, Hkv, 1, D), device=dev, generator=g, dtype=torch.bfloat16)
+    for label, thr, steps, tier in runs:
+        cache = make_cache(thr, tier, steps + S + 8)
+        pre_ms, pre_total, inputs = prefill(cache, True)
+        tier_mode = cache.tier_mode
 
         def decode_step(t):
             for layer in range(NL):
-                cache.update(kn[t, layer], kn[t, layer], layer)
-                cache.decode_attention(qs[t, layer], layer)
-                cache.decode_select(qs[t, layer], layer)
+                qs, kn, vn = inputs[layer]
+                cache.update(kn[t], vn[t], layer)
+                cache.decode_attention(qs[t], layer)
+                cache.decode_select(qs[t], layer)
 
-        for t in range(5):  # warm-up: one full check builds the per-layer metadata
+        for t in range(S):  # warm-up: one full check builds the per-layer metadata
             decode_step(t)
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        len0 = sum(int(st.host_len.astype(np.int64).sum()) for st in cache.stores)
+        rows = sum(st.rows for st in cache.stores)
+        trig = cache._trigger_all
+        triggered = torch.zeros_like(trig)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         t0 = time.perf_counter()
-        e0.record()
-        for t in range(5, 5 + steps):
-            decode_step(t)
-        e1.record()
+        for i in range(steps):
+            ev[i][0].record()
+            decode_step(S + i)
+            ev[i][1].record()
+            if (S + i + 1) % S == 0:
+                triggered += trig      # device-side count of triggered leaders
         torch.cuda.synchronize()
-        res[label] = {"ms_per_step": e0.elapsed_time(e1) / steps,
-                      "wall_ms_per_step": (time.perf_counter() - t0) * 1e3 / steps,
-                      "prefill_main_ms_per_layer": pre_ms, "prefill_total_ms": pre_total}
-        trig = [int(cache._drift[l].trigger.sum().item()) for l in range(NL) if cache._drift[l] is not None
-                and cache._drift[l].trigger is not None]
-        res[label]["leaders_triggered_last_check"] = int(sum(trig))
-        del cache, qs, kn
+        wall = (time.perf_counter() - t0) * 1e3 / steps
+        step_ms = [a.elapsed_time(b) for a, b in ev]
+        checks = steps // S
+        trig_total = int(triggered.sum().item())
+        # Retrieved rows written per check: each triggered leader's members.
+        per_leader_rows = {}
+        for layer in range(NL):
+            for h, members in data["leader_member_relations"][layer].items():
+                per_leader_rows[(layer, int(h))] = len(members) * 1024
+        ret_bytes = trig_total * (sum(per_leader_rows.values()) / max(len(per_leader_rows), 1)) * D * 2 * 2
+        attn_bytes = sum((len0 + rows * (i + 1)) * D * 2 * 2 for i in range(steps)) + steps * NL * 2 * Hkv * G * D * 2
+        nbytes = attn_bytes + checks * check_k_bytes + ret_bytes
+        ms = float(np.mean(step_ms))
+        res[label] = {"tier": tier_mode, "steps": steps, "checks": checks, "ms_per_step": round(ms, 4),
+                      "wall_ms_per_step": round(wall, 4),
+                      "leader_triggers": trig_total, "leaders": int(trig.numel()),
+                      "bytes_per_step": int(nbytes / steps),
+                      "tbs": round(nbytes / steps / (ms * 1e-3) / 1e12, 3),
+                      "frac_of_hbm_peak": round(nbytes / steps / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                      "prefill_main_ms_per_layer": round(pre_ms, 3), "prefill_total_ms": round(pre_total, 1)}
+        del cache, inputs
         torch.cuda.empty_cache()
-    # Retrieval bytes per check: every satellite gathers min(cap, 1024) K and V rows.
-    sats = sum(len(r) for r in data["need_to_update_counts"])
-    tier_bytes = sats * L * D * 2 * 2  # satellites' full K and V, written once over the host link
+    tier_bytes = sats * L * D * 2 * 2  # satellites' full K and V
     per_check = sats * 1024 * D * 2 * 2
-    exposed = (res["always_trigger"]["ms_per_step"] - res["no_trigger"]["ms_per_step"]) * 5
-    return {"steps": steps, "decode_step": 5, "retrieval_topk": 1024, "satellites": sats,
-            "retrieval_bytes_per_check": per_check,
-            "ms_per_step_no_retrieval": round(res["no_trigger"]["ms_per_step"], 4),
-            "ms_per_step_retrieval_every_check": round(res["always_trigger"]["ms_per_step"], 4),
-            "retrieval_exposed_ms_per_check": round(exposed, 4),
-            "leaders_triggered_last_check": res["always_trigger"]["leaders_triggered_last_check"],
-            "prefill": {"compress_ms_per_layer_hbm_tier": round(hbm_layer_ms, 3),
-                        "total_ms_hbm_tier": round(hbm_total, 1),
-                        "first_prefill_total_ms_hbm_tier": round(first_total, 1),
-                        "total_ms_host_tier": round(res["always_trigger"]["prefill_total_ms"], 1),
-                        "host_tier_bytes": tier_bytes,
-                        "host_tier_link_gbs": round(tier_bytes / res["always_trigger"]["prefill_total_ms"] / 1e6, 1)}}
+    a = res["always"]
+    return {"workload": "reference Llama-3.1-8B head JSON (33 pivots, 196 satellites), 131072 ctx, ratio 0.5, "
+                        "needle queries with natural drift, top-1024 retrieval from the full-KV tier",
+            "decode_step": S, "retrieval_topk": 1024, "pivots": npiv, "satellites": sats,
+            "drift_check_groups": groups or HeteroCacheConfig(None).drift_check_groups,
+            "check_key_bytes": check_k_bytes, "tier_bytes": tier_bytes, "tier": a["tier"],
+            "retrieval_bytes_per_check": per_check, "runs": res,
+            "ms_per_step_no_retrieval": res["never"]["ms_per_step"],
+            "ms_per_step_retrieval_every_check": a["ms_per_step"],
+            "retrieval_exposed_ms_per_check": round((a["ms_per_step"] - res["never"]["ms_per_step"]) * S, 4),
+            "host_tier_retrieval_exposed_ms_per_check":
+                round((res["host_always"]["ms_per_step"] - res["host_never"]["ms_per_step"]) * S, 4),
+            "roofline": {"bound": "hbm", "achieved": round(a["tbs"] * 1000, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": a["frac_of_hbm_peak"], "run": f"retrieval every check, {a['tier']} tier",
+                         "bytes": "attended K/V + q/out, pivot keys per check / 5, retrieved rows written / 5"},
+            "prefill": {"compress_ms_per_layer": a["prefill_main_ms_per_layer"],
+                        "total_ms_device_tier": a["prefill_total_ms"],
+                        "total_ms_host_tier": res["host_always"]["prefill_total_ms"],
+                        "host_tier_link_gbs": round(tier_bytes / res["host_always"]["prefill_total_ms"] / 1e6, 1)}}
 
 
 def gather_phase(args, torch, dev):
@@ -549,6 +595,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.prefill_only:
         print(json.dumps({"prefill_attention": prefill_attention_phase(args, torch, dev)}))
+        return
+    if args.full_step_only:
+        print(json.dumps({"full_decode_step": full_step_phase(args, torch, dev)}))
         return
     torch.manual_seed(args.seed)
     L, Hkv, G, D = args.ctx, 8, 4, 128

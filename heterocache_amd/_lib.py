@@ -45,7 +45,8 @@ SIGNATURES = {
     "hc_decode_chunk_tiles": (c_int, [c_int, c_void_p, c_int, c_int]),
     "hc_decode_workspace_size": (c_size_t, [c_int, c_int, c_int64]),
     "hc_gather_store": (c_int, [c_int, c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p,
-                                c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+                                c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int,
+                                c_void_p]),
     "hc_copy_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int, c_void_p,
                              c_int64, c_void_p, c_int, c_int, c_int, c_void_p]),
     "hc_prefill_attn": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -61,6 +61,13 @@ class HeteroCacheConfig:
     step, so the outputs are unchanged).  drift_check_groups: number of
     contiguous layer groups checked separately (1 = all layers after the
     last one; more groups start the early groups' retrieval sooner).
+    tier_placement: where the satellites' full-KV tier lives when
+    real_offload is set -- "host" (pinned host memory, retrieval read over
+    the host link), "device" (an HBM arena, retrieval a device gather) or
+    "auto" (device when the whole model's tier fits in tier_device_budget
+    bytes, default a quarter of the device's memory; host otherwise).
+    Without real_offload the tier is the prefill K/V itself, as in the
+    reference's GPU mode.
     """
 
     def __init__(self, data: Optional[Dict], compression_ratio: Optional[float] = 0.5,
@@ -69,7 +76,8 @@ class HeteroCacheConfig:
                  kernel_size: Optional[int] = 5, num_attn_heads: Optional[int] = 32, num_kv_heads: Optional[int] = 8,
                  num_layers: Optional[int] = 32, retrieval_topk: Optional[int] = None, window_size: int = 1,
                  round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None,
-                 batched_drift_check: bool = True, drift_check_groups: int = 1):
+                 batched_drift_check: bool = True, drift_check_groups: int = 1, tier_placement: str = "auto",
+                 tier_device_budget: Optional[int] = None):
         self.data = data
         self.stable_threshold = stable_threshold
         self.compression_ratio = compression_ratio
@@ -89,6 +97,10 @@ class HeteroCacheConfig:
         self.chunk_tiles = chunk_tiles
         self.batched_drift_check = batched_drift_check
         self.drift_check_groups = drift_check_groups
+        if tier_placement not in ("auto", "host", "device"):
+            raise ValueError(f"tier_placement must be 'auto', 'host' or 'device', not {tier_placement!r}")
+        self.tier_placement = tier_placement
+        self.tier_device_budget = tier_device_budget
 
 
 def _f32_caps(base, ratios, seq_len):
@@ -117,6 +129,10 @@ class HeteroCache(DynamicCache):
 
     # Workgroups of the prefill copy into the host-pinned tier.
     TIER_COPY_WORKGROUPS = 32
+    # Workgroups of a retrieval gather from the host-pinned tier.  Reads over
+    # the host link slow concurrent HBM streaming in proportion to the reads
+    # in flight; 32 workgroups keep the link near its peak.
+    RETRIEVAL_WORKGROUPS = 32
 
     def __init__(self, cache_config):
         super().__init__()
@@ -151,7 +167,9 @@ class HeteroCache(DynamicCache):
         self.key_cache_cpu = [None] * self.num_layers
         self.value_cache_cpu = [None] * self.num_layers
         self._tier_heads = [None] * self.num_layers   # kv-head -> head index inside the tier tensor
-        self._tier_ready = [None] * self.num_layers   # event: tier copy done (side stream)
+        self._tier_base = [0] * self.num_layers      # first tier-arena row of each layer's satellites
+        self._tier = None            # (K, V) [rows, L, 128] arena of every layer's satellites, or None
+        self.tier_mode = None        # "host", "device" or "prefill" (the prefill K/V kept as is)
         self._retrieval_done = [None] * self.num_layers
         self._pending = [None] * self.num_layers      # decode token awaiting its append
         self._drift = [None] * self.num_layers
@@ -294,6 +312,38 @@ class HeteroCache(DynamicCache):
             self.stores[layer] = KVStore(row_caps[layer], dtype, device, arena=(k, v, base), layer_idx=layer)
             base += tiles[layer]
         self._tile_table = torch.cat([st.row_tile_off for st in self.stores])
+        self._init_tier(device, dtype)
+
+    def _init_tier(self, device, dtype):
+        """Place the satellites' full-KV tier: one arena of [rows, L, 128] K
+        and V for every layer, rows (layer, b, satellite) in that order, in
+        HBM or in pinned host memory (see HeteroCacheConfig.tier_placement)."""
+        if not self.config.real_offload:
+            self.tier_mode = "prefill"
+            return
+        nsat = [len(self.data["need_to_update_counts"][layer]) for layer in range(self.num_layers)]
+        rows, base = 0, []
+        for n in nsat:
+            base.append(rows)
+            rows += self.bsz * n
+        self._tier_base = base
+        L = self.prefill_len
+        nbytes = 2 * rows * L * self.head_dim * torch.empty((), dtype=dtype).element_size()
+        mode = getattr(self.config, "tier_placement", "auto")
+        if mode == "auto":
+            budget = getattr(self.config, "tier_device_budget", None)
+            if budget is None:
+                budget = torch.cuda.get_device_properties(device).total_memory // 4
+            mode = "device" if nbytes <= budget else "host"
+        self.tier_mode = mode
+        if rows == 0:
+            return
+        shape = (rows, L, self.head_dim)
+        if mode == "device":
+            self._tier = (torch.empty(shape, dtype=dtype, device=device), torch.empty(shape, dtype=dtype, device=device))
+        else:
+            self._tier = (torch.empty(shape, dtype=dtype, pin_memory=True),
+                          torch.empty(shape, dtype=dtype, pin_memory=True))
 
     def update(self, key_states, value_states, layer_idx, cache_kwargs=None):
         """heterocache/cache_utils.py:884-1005."""
@@ -336,36 +386,50 @@ class HeteroCache(DynamicCache):
         sats = list(self.data["need_to_update_counts"][layer_idx])
         if not sats:
             return
-        if self.device != "cpu":
+        if self.tier_mode == "prefill":
             # GPU direct mode keeps the prefill K/V itself, as the reference.
             self.key_cache_cpu[layer_idx] = key_states.detach()
             self.value_cache_cpu[layer_idx] = value_states.detach()
             self._tier_heads[layer_idx] = {h: h for h in sats}
             return
-        dev = key_states.device
-        main = torch.cuda.current_stream(dev)
-        side = self._side_stream(dev)
         L = key_states.shape[-2]
-        shape = (self.bsz, len(sats), L, self.head_dim)
-        kc = torch.empty(shape, dtype=key_states.dtype, pin_memory=True)
-        vc = torch.empty(shape, dtype=value_states.dtype, pin_memory=True)
+        n = len(sats)
+        r0 = self._tier_base[layer_idx]
+        tk, tv = self._tier_arena4()
         src = [(b, h) for b in range(self.bsz) for h in sats]
-        dst = [(b, i) for b in range(self.bsz) for i in range(len(sats))]
-        side.wait_stream(main)
-        # A few workgroups write the satellites' rows straight from the
-        # prefill tensors into the pinned tier at link speed, beside the
-        # compression kernels on the main stream.
-        ops.copy_rows(key_states, value_states, src, kc, vc, dst, [L] * len(src), dst_is_host=True,
-                      max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
-        with torch.cuda.stream(side):
-            ev = torch.cuda.Event()
-            ev.record(side)
-        key_states.record_stream(side)
-        value_states.record_stream(side)
-        self.key_cache_cpu[layer_idx] = kc
-        self.value_cache_cpu[layer_idx] = vc
+        dst = [(0, r0 + b * n + i) for b in range(self.bsz) for i in range(n)]
+        if self.tier_mode == "device":
+            ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), max_workgroups=1024)
+        else:
+            dev = key_states.device
+            side = self._side_stream(dev)
+            side.wait_stream(torch.cuda.current_stream(dev))
+            # A few workgroups write the satellites' rows straight from the
+            # prefill tensors into the pinned tier at link speed, beside the
+            # compression kernels on the main stream.
+            ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), dst_is_host=True,
+                          max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
+            key_states.record_stream(side)
+            value_states.record_stream(side)
+        # The layer's rows of the arena, in the reference's [B, heads, L, 128] shape.
+        self.key_cache_cpu[layer_idx] = self._tier[0][r0:r0 + self.bsz * n].view(self.bsz, n, L, self.head_dim)
+        self.value_cache_cpu[layer_idx] = self._tier[1][r0:r0 + self.bsz * n].view(self.bsz, n, L, self.head_dim)
         self._tier_heads[layer_idx] = {h: i for i, h in enumerate(sats)}
-        self._tier_ready[layer_idx] = ev
+
+    def _tier_arena4(self):
+        """The tier arena as [1, rows, L, 128] K and V (gathers address its
+        rows from the allocation's base)."""
+        tk, tv = self._tier
+        return tk.unsqueeze(0), tv.unsqueeze(0)
+
+    def _tier_source(self, layer, b, m):
+        """(K, V, (b', h')) addressing satellite m of batch row b of a layer
+        in the tier: a row of the arena, or the prefill K/V in GPU mode."""
+        if self.tier_mode == "prefill":
+            return self.key_cache_cpu[layer], self.value_cache_cpu[layer], (b, m)
+        tk, tv = self._tier_arena4()
+        n = len(self._tier_heads[layer])
+        return tk, tv, (0, self._tier_base[layer] + b * n + self._tier_heads[layer][m])
 
     def _flush_append(self, layer_idx):
         p = self._pending[layer_idx]
@@ -623,28 +687,38 @@ class HeteroCache(DynamicCache):
         ops.drift_decide(bm["overlap"], nlead, B, S, K, self.stable_threshold, trig)
         last = bm["cur"].view(J, S, -1)[:, S - 1]
         ops.set_bits(last, None, bits, L, fixed_count=K, trigger=trig, trig_of=bm["trig_of"])
-        if bm["plans"]:
+        if bm["retrieve"]:
             ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
         if self.observer is not None:
             self.observer("drift_check", row_ids=bm["row_ids"], scores=scores, cur=bm["cur"], trigger=trig,
                           trig_of=bm["trig_of"], ret_idx=bm.get("ret_idx"), ret_counts=bm.get("ret_counts"))
-        if not bm["plans"]:
+        if not bm["retrieve"]:
             return
         dev = qa.device
         main = torch.cuda.current_stream(dev)
-        host = self.device == "cpu"
+        host = self.tier_mode == "host"
         side = self._side_stream(dev) if host else main
         if host:
             side.wait_stream(main)
+        gp = bm["group_plan"]
         with torch.cuda.stream(side):
+            if gp is not None:
+                # Every layer of the group in one launch from the tier arena.
+                tk, tv = self._tier
+                ops.gather_store(tk, tv, gp["src_off"], self.head_dim, L, bm["ret_idx"], gp["idx_off"], gp["counts"],
+                                 gp["dst_row"], self._arena[0], self._arena[1], self._tile_table, gp["max_count"],
+                                 src_is_host=host, trigger=trig, trig_of=gp["trig_of"], stream=side,
+                                 max_workgroups=self.RETRIEVAL_WORKGROUPS if host else 0)
+                if host:
+                    ev = torch.cuda.Event()
+                    ev.record(side)
+                    for layer in gp["layers"]:
+                        self._retrieval_done[layer] = ev
+                return
             for layer, plan in bm["plans"]:
                 kc, vc = self.key_cache_cpu[layer], self.value_cache_cpu[layer]
                 self.stores[layer].launch_rows(plan, kc, vc, idx=bm["ret_idx"], src_is_host=host, stream=side,
                                                trigger=trig, set_len=False)
-                if host:
-                    ev = torch.cuda.Event()
-                    ev.record(side)
-                    self._retrieval_done[layer] = ev
 
     def _batched_metadata(self, layers):
         """Device metadata of _check_batched; rows j follow the
@@ -692,17 +766,49 @@ class HeteroCache(DynamicCache):
             m["ret_caps"] = torch.as_tensor(np.asarray(ret_caps, dtype=np.int32)).to(dev)
             m["ret_idx"] = torch.empty((J, max(mk, 1)), dtype=torch.int32, device=dev)
             m["ret_counts"] = torch.empty(J, dtype=torch.int32, device=dev)
-            for layer in layers:
-                lj = jobs.get(layer)
-                if not lj:
-                    continue
-                tier_heads = self._tier_heads[layer]
-                plan = self.stores[layer].plan_rows(
-                    self.key_cache_cpu[layer], [(b, tier_heads[mm]) for _, _, b, mm, _ in lj],
-                    [b * Hkv + mm for _, _, b, mm, _ in lj], [n for _, _, _, _, n in lj], idx=m["ret_idx"],
-                    idx_rows=[jj for jj, _, _, _, _ in lj], trig_of=[t for _, t, _, _, _ in lj])
-                m["plans"].append((layer, plan))
+            if self.tier_mode in ("host", "device"):
+                m["group_plan"] = self._group_retrieval_plan(jobs, m["ret_idx"])
+            else:
+                for layer in layers:
+                    lj = jobs.get(layer)
+                    if not lj:
+                        continue
+                    tier_heads = self._tier_heads[layer]
+                    plan = self.stores[layer].plan_rows(
+                        self.key_cache_cpu[layer], [(b, tier_heads[mm]) for _, _, b, mm, _ in lj],
+                        [b * Hkv + mm for _, _, b, mm, _ in lj], [n for _, _, _, _, n in lj], idx=m["ret_idx"],
+                        idx_rows=[jj for jj, _, _, _, _ in lj], trig_of=[t for _, t, _, _, _ in lj])
+                    m["plans"].append((layer, plan))
+        m.setdefault("group_plan", None)
+        m["retrieve"] = bool(jobs)
         return m
+
+    def _group_retrieval_plan(self, jobs, ret_idx):
+        """One gather for every (layer, leader, batch row, satellite) retrieval
+        job of a check group: sources are rows of the tier arena, destinations
+        rows of the model-wide KV arena (global row = layer * B * Hkv + b *
+        Hkv + satellite), each job gated by its leader's trigger flag."""
+        B, Hkv, L, D = self.bsz, self.num_kv_heads, self.prefill_len, self.head_dim
+        dev = ret_idx.device
+        src_off, idx_off, counts, dst, trig_of, layers = [], [], [], [], [], []
+        for layer, lj in sorted(jobs.items()):
+            n_sat = len(self._tier_heads[layer])
+            caps = self.stores[layer].host_cap
+            for jj, t, b, mm, n in lj:
+                if n > caps[b * Hkv + mm]:
+                    raise RuntimeError(f"Layer {layer} OOM.")
+                src_off.append((self._tier_base[layer] + b * n_sat + self._tier_heads[layer][mm]) * L * D)
+                idx_off.append(jj * ret_idx.stride(0))
+                counts.append(n)
+                dst.append(layer * B * Hkv + b * Hkv + mm)
+                trig_of.append(t)
+            layers.append(layer)
+        return {"src_off": ops.to_device(np.asarray(src_off, dtype=np.int64), dev),
+                "idx_off": ops.to_device(np.asarray(idx_off, dtype=np.int64), dev),
+                "counts": ops.to_device(np.asarray(counts, dtype=np.int32), dev),
+                "dst_row": ops.to_device(np.asarray(dst, dtype=np.int32), dev),
+                "trig_of": ops.to_device(np.asarray(trig_of, dtype=np.int32), dev),
+                "max_count": int(max(counts)), "layers": layers}
 
     def _drift_metadata(self, layer_idx, st):
         """Device tensors and buffers of one layer's drift check and retrieval."""
@@ -739,13 +845,13 @@ class HeteroCache(DynamicCache):
             m["ret_caps"] = torch.tensor(caps, dtype=torch.int32).to(dev)
             m["ret_idx"] = torch.empty((nl * B, mk), dtype=torch.int32, device=dev)
             m["ret_counts"] = torch.empty(nl * B, dtype=torch.int32, device=dev)
-            kc = self.key_cache_cpu[layer_idx]
-            tier_heads = self._tier_heads[layer_idx]
             # One gather for every (leader, batch row, satellite) of the layer;
             # each job is gated by its leader's trigger flag.
             jobs = [(i, b, mm, n) for i, members, lens in plans for b in range(B) for mm, n in zip(members, lens)
                     if n > 0]
-            plan = store.plan_rows(kc, [(b, tier_heads[mm]) for i, b, mm, n in jobs],
+            srcs = [self._tier_source(layer_idx, b, mm) for i, b, mm, n in jobs]
+            m["tier"] = srcs[0][:2]
+            plan = store.plan_rows(m["tier"][0], [bh for _, _, bh in srcs],
                                    [b * Hkv + mm for i, b, mm, n in jobs], [n for i, b, mm, n in jobs],
                                    idx=m["ret_idx"], idx_rows=[i * B + b for i, b, mm, n in jobs],
                                    trig_of=[i for i, b, mm, n in jobs])
@@ -774,8 +880,8 @@ class HeteroCache(DynamicCache):
         ops.select_topk(last_scores, m["ret_caps"], last_scores.shape[1], idx=m["ret_idx"], counts=m["ret_counts"])
         dev = last_scores.device
         main = torch.cuda.current_stream(dev)
-        kc, vc = self.key_cache_cpu[layer_idx], self.value_cache_cpu[layer_idx]
-        host = self.device == "cpu"
+        kc, vc = m["tier"]
+        host = self.tier_mode == "host"
         store = self.stores[layer_idx]
         side = self._side_stream(dev) if host else main
         if host:

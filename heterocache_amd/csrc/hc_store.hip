@@ -156,17 +156,18 @@ __global__ __launch_bounds__(256) void store_read_kernel(const T* __restrict__ k
 }
 
 // Workgroups of a gather whose source is host memory read over the link.
-constexpr int kHostGatherWorkgroups = 64;
+constexpr int kHostGatherWorkgroups = 64;  // default cap of a host-sourced gather's grid
 
 template <typename T>
 static int launch_gather_store(const void* src_k, const void* src_v, const int64_t* src_off, int64_t src_tok_stride,
                                int src_len, const int32_t* idx, const int64_t* idx_off, const int32_t* count,
                                const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off,
                                int njobs, int max_count, const int32_t* trigger, const int32_t* trig_of,
-                               bool host_src, hipStream_t s) {
+                               bool host_src, int max_workgroups, hipStream_t s) {
   const int tiles = (max_count + HC_TILE - 1) / HC_TILE;
   const int64_t items = (int64_t)tiles * njobs;
-  const unsigned grid = (unsigned)(host_src ? std::min<int64_t>(items, kHostGatherWorkgroups) : items);
+  const int64_t cap = max_workgroups > 0 ? max_workgroups : (host_src ? kHostGatherWorkgroups : items);
+  const unsigned grid = (unsigned)std::min<int64_t>(items, cap);
   hipLaunchKernelGGL((gather_store_kernel<T>), dim3(grid), dim3(256), 0, s, (const T*)src_k, (const T*)src_v, src_off,
                      src_tok_stride, src_len, idx, idx_off, count, dst_row, (T*)kstore, (T*)vstore, row_tile_off, trigger,
                      trig_of, njobs, tiles);
@@ -243,9 +244,9 @@ extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, 
                                const int64_t* src_off, int64_t src_tok_stride, int src_len, const int32_t* idx,
                                const int64_t* idx_off, const int32_t* count, const int32_t* dst_row, void* kstore,
                                void* vstore, const int64_t* row_tile_off, int njobs, int max_count,
-                               const int32_t* trigger, const int32_t* trig_of, void* stream) {
+                               const int32_t* trigger, const int32_t* trig_of, int max_workgroups, void* stream) {
   clear_error();
-  if (njobs < 0 || max_count < 0 || njobs > 65535)
+  if (njobs < 0 || max_count < 0 || njobs > 65535 || max_workgroups < 0)
     return set_error(HC_ERR_INVALID, "hc_gather_store: njobs=%d max_count=%d", njobs, max_count);
   if (njobs == 0 || max_count == 0) return HC_OK;
   if (src_len <= 0) return set_error(HC_ERR_INVALID, "hc_gather_store: src_len=%d", src_len);
@@ -270,13 +271,13 @@ extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, 
   switch (dtype) {
     case HC_DTYPE_BF16:
       return launch_gather_store<__bf16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                         vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, s);
+                                         vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s);
     case HC_DTYPE_F16:
       return launch_gather_store<_Float16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                           vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, s);
+                                           vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s);
     case HC_DTYPE_F32:
       return launch_gather_store<float>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                        vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, s);
+                                        vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s);
     default:
       return set_error(HC_ERR_INVALID, "hc_gather_store: unknown dtype %d", dtype);
   }

@@ -190,8 +190,10 @@ def read_status(status, clear=True, stream=None):
 
 
 def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore, vstore, row_tile_off,
-                 max_count, src_is_host=False, trigger=None, trig_of=None, stream=None):
-    """store[dst_row[j]][i] = src[src_off[j] + idx[idx_off[j] + i] * stride], i < count[j]."""
+                 max_count, src_is_host=False, trigger=None, trig_of=None, stream=None, max_workgroups=0):
+    """store[dst_row[j]][i] = src[src_off[j] + idx[idx_off[j] + i] * stride], i < count[j].
+
+    max_workgroups: grid cap (0: the library default for the source kind)."""
     lib = _lib.load()
     _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger, trig_of)
     if src_is_host:
@@ -211,7 +213,8 @@ def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, c
     _lib.check(lib.hc_gather_store(dtype_code(kstore.dtype), _ptr(src_k), _ptr(src_v), int(bool(src_is_host)),
                                    _ptr(src_off), int(src_tok_stride), int(src_len), _ptr(idx), _ptr(idx_off), _ptr(count),
                                    _ptr(dst_row), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off), njobs,
-                                   int(max_count), _ptr(trigger), _ptr(trig_of), _stream(stream, kstore)))
+                                   int(max_count), _ptr(trigger), _ptr(trig_of), int(max_workgroups),
+                                   _stream(stream, kstore)))
 
 
 def copy_rows(src_k, src_v, src_bh, dst_k, dst_v, dst_bh, counts, dst_is_host=False, max_workgroups=32,

@@ -161,7 +161,7 @@ class KVStore:
                 "max_count": int(counts.max())}
 
     def launch_rows(self, plan, src_k, src_v, idx=None, src_is_host=False, stream=None, trigger=None,
-                    set_len=True):
+                    set_len=True, max_workgroups=0):
         """Run a gather planned by plan_rows (no host-to-device copies)."""
         if plan is None:
             return
@@ -174,7 +174,8 @@ class KVStore:
             raise ValueError("index tensor does not match the plan")
         ops.gather_store(src_k, src_v, plan["src_off"], plan["tok_stride"], plan["src_len"], idx, plan["idx_off"],
                          plan["counts"], plan["rows"], self.k, self.v, self.row_tile_off, plan["max_count"],
-                         src_is_host=src_is_host, trigger=trigger, trig_of=plan["trig_of"], stream=stream)
+                         src_is_host=src_is_host, trigger=trigger, trig_of=plan["trig_of"], stream=stream,
+                         max_workgroups=max_workgroups)
         if set_len:
             self.set_lengths(plan["host_counts"], plan["host_rows"])
 

@@ -128,6 +128,11 @@ size_t hc_decode_workspace_size(int rows, int group, int64_t num_parts);
  * sources are host-pinned, device-mapped buffers read over the host link.
  * When trigger != NULL job j is skipped unless trigger[trig_of ? trig_of[j] : 0]
  * != 0 (device flags; one launch can serve several gated groups of jobs).
+ * max_workgroups caps the grid, whose workgroups stride over the (job,
+ * 32-token tile) items (0: one workgroup per item from device memory, 64
+ * from host memory -- a host-sourced gather waits on the link, and beside a
+ * decode launch that fills the device its workgroups take slots the decode
+ * kernel needs).
  * Replaces the keep-head index_copy_ (heterocache/cache_utils.py:914-937),
  * the compressed-head gather + index_copy_ (heterocache/cache_utils.py:854-877)
  * and the retrieval index_select + copy_ (heterocache/cache_utils.py:1097-1123).
@@ -135,7 +140,7 @@ size_t hc_decode_workspace_size(int rows, int group, int64_t num_parts);
 int hc_gather_store(int dtype, const void* src_k, const void* src_v, int src_is_host, const int64_t* src_off,
                     int64_t src_tok_stride, int src_len, const int32_t* idx, const int64_t* idx_off, const int32_t* count,
                     const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off, int njobs,
-                    int max_count, const int32_t* trigger, const int32_t* trig_of, void* stream);
+                    int max_count, const int32_t* trigger, const int32_t* trig_of, int max_workgroups, void* stream);
 
 /*
  * Append one token per row at slot row_len[r], then row_len[r] += 1.

@@ -42,14 +42,17 @@ def head_data(seed=0):
 
 
 def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True, groups=1,
-        chunks=None):
+        chunks=None, tier="host"):
+    """tier: "host" / "device" placement of the full-KV tier, or "prefill"
+    (real_offload=False: the prefill K/V kept as the tier)."""
     torch.manual_seed(0)
     B, Hq, Hkv, NL, D = 1, 32, 8, 2, 128
     data = head_data()
-    cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
+    cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=tier != "prefill",
                             max_gen_len=steps + 4, decode_step=5, pooling="avgpool", kernel_size=5,
                             num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=topk,
-                            reference_quirks=quirks, batched_drift_check=batched, drift_check_groups=groups)
+                            reference_quirks=quirks, batched_drift_check=batched, drift_check_groups=groups,
+                            tier_placement="host" if tier == "prefill" else tier)
     cache = HeteroCache(cfg)
     if chunks is not None:
         cache.begin_prefill(L)
@@ -100,6 +103,7 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
                 for i, leader in enumerate(st.leaders):
                     triggers.append((layer, leader, bool(st.trigger[i].item())))
     torch.cuda.synchronize()
+    assert cache.tier_mode == tier
     assert triggers == orc.triggers
     for layer in range(NL):
         store = cache.stores[layer]
@@ -135,6 +139,17 @@ def test_llama_order_layer_by_layer_checks(dev):
 
 def test_qwen_order_select_before_attention(dev):
     run(dev, torch.float32, select_first=True)
+
+
+@pytest.mark.parametrize("tier", ["device", "prefill"])
+@pytest.mark.parametrize("select_first", [False, True])
+def test_tier_placements(dev, tier, select_first):
+    """The full-KV tier in an HBM arena, or (real_offload=False) the prefill
+    K/V kept as is: same outputs, triggers and stores as the oracle, in both
+    step orders (the batched check retrieves every layer of its group in
+    one gather from the arena)."""
+    trig = run(dev, torch.float32, select_first=select_first, topk=64, tier=tier)
+    assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
 
 
 def test_retrieval_topk(dev):

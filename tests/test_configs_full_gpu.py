@@ -140,7 +140,8 @@ def test_config2_needles_128k_llama_json(dev):
     rec = Recorder(checked)
     cfg = HeteroCacheConfig(data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
                             max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
-                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024)
+                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
+                            tier_placement="host")
     cache = HeteroCache(cfg)
     cache.observer = rec
     wl = workloads.NeedleWorkload(L, kv_heads=Hkv, group=G, steps=steps, decode_step=S, seed=1002, device=dev)
@@ -224,7 +225,8 @@ def test_config4_chunked_224k_then_drift_block(dev):
     def make(host_tier):
         cfg = HeteroCacheConfig(data, compression_ratio=0.5, stable_threshold=0.5, real_offload=host_tier,
                                 max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
-                                num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024)
+                                num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
+                                tier_placement="host")
         return HeteroCache(cfg)
 
     whole, chunked = make(False), make(True)
