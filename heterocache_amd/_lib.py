@@ -75,6 +75,9 @@ SIGNATURES = {
                             c_void_p]),
     "hc_overlap_count": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,
                                  c_void_p]),
+    "hc_drift_select": (c_int, [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int64,
+                                c_void_p, c_int, ctypes.c_double, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p,
+                                c_size_t, c_void_p]),
     "hc_drift_decide": (c_int, [c_void_p, c_int, c_int, c_int, c_int, ctypes.c_double, c_void_p, c_void_p, c_void_p,
                                 c_void_p]),
     "hc_store_read": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,

@@ -202,8 +202,9 @@ class HeteroCache(DynamicCache):
         # (device tensors, valid on the current stream): "prefill_select"
         # (layer, rows, scores [rows, L], idx, counts), "pivot_sets" (layer,
         # pivots, scores [B * npiv, L] rows (b, pivot), K), "drift_check"
-        # (row_ids [(layer, leader head, b)], scores [J, S, L], cur, trigger,
-        # trig_of, ret_idx, ret_counts).  None (the default) costs nothing.
+        # (row_ids [(layer, leader head, b)], scores [J, S, L], overlap [J * S],
+        # trigger, trig_of, ret_idx, ret_counts).  None (the default) costs
+        # nothing.
         self.observer = None
 
     # -- reference API ------------------------------------------------------
@@ -648,18 +649,16 @@ class HeteroCache(DynamicCache):
         scores = compress.pivot_step_scores(st.qbuf, store, None, None, G, L, self.pooling, self.kernel_size,
                                             round_dtype=self._round_dtype(st.qbuf.dtype),
                                             metadata=m["score_meta"])
-        ops.select_topk(scores.view(nl * B * S, L), m["caps_K"], L, idx=m["cur"], counts=m["cur_counts"])
-        ops.overlap_count(m["cur"], K, st.ref_bits, L, ref_of=m["ref_of"], out=m["overlap"])
-        ops.drift_decide(m["overlap"], nl, B, S, K, self.stable_threshold, st.trigger)
-        # On trigger the reference set becomes the last step's top-K set.
-        last = m["cur"].view(nl * B, S, -1)[:, S - 1]
-        ops.set_bits(last, None, st.ref_bits, L, fixed_count=K, trigger=st.trigger, trig_of=m["trig_of"])
+        # Overlaps, decision and, on trigger, the last step's top-K as the new
+        # reference set -- all from the step thresholds.
+        ops.drift_select(scores.view(nl * B * S, L), m["caps_K"], K, st.ref_bits, L, m["trig_of"], nl, B, S,
+                         self.stable_threshold, st.trigger, overlap=m["overlap"])
         if m["plans"]:
             self._retrieve(layer_idx, st, scores[:, S - 1])
         if self.observer is not None:
             self.observer("drift_check", row_ids=[(layer_idx, h, b) for h in st.leaders for b in range(B)],
-                          scores=scores.view(nl * B, S, L), cur=m["cur"], trigger=st.trigger, trig_of=m["trig_of"],
-                          ret_idx=m.get("ret_idx"), ret_counts=m.get("ret_counts"))
+                          scores=scores.view(nl * B, S, L), overlap=m["overlap"], trigger=st.trigger,
+                          trig_of=m["trig_of"], ret_idx=m.get("ret_idx"), ret_counts=m.get("ret_counts"))
 
     def _check_batched(self, layers):
         """Drift checks of a group of leader layers in one launch sequence: scores
@@ -682,15 +681,12 @@ class HeteroCache(DynamicCache):
         scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,
                            self.pooling, self.kernel_size, 1.0 / math.sqrt(self.head_dim), flags=flags,
                            row_tile_off=self._tile_table, k_row=bm["k_row"]).view(J, S, L)
-        ops.select_topk(scores.view(J * S, L), bm["caps_K"], L, idx=bm["cur"], counts=bm["cur_counts"])
-        ops.overlap_count(bm["cur"], K, bits, L, ref_of=bm["ref_of"], out=bm["overlap"])
-        ops.drift_decide(bm["overlap"], nlead, B, S, K, self.stable_threshold, trig)
-        last = bm["cur"].view(J, S, -1)[:, S - 1]
-        ops.set_bits(last, None, bits, L, fixed_count=K, trigger=trig, trig_of=bm["trig_of"])
+        ops.drift_select(scores.view(J * S, L), bm["caps_K"], K, bits, L, bm["trig_of"], nlead, B, S,
+                         self.stable_threshold, trig, overlap=bm["overlap"])
         if bm["retrieve"]:
             ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
         if self.observer is not None:
-            self.observer("drift_check", row_ids=bm["row_ids"], scores=scores, cur=bm["cur"], trigger=trig,
+            self.observer("drift_check", row_ids=bm["row_ids"], scores=scores, overlap=bm["overlap"], trigger=trig,
                           trig_of=bm["trig_of"], ret_idx=bm.get("ret_idx"), ret_counts=bm.get("ret_counts"))
         if not bm["retrieve"]:
             return
@@ -755,10 +751,7 @@ class HeteroCache(DynamicCache):
         m["q_off"] = torch.as_tensor(np.asarray(q_off, dtype=np.int64)).to(dev)
         m["k_row"] = torch.as_tensor(np.asarray(k_row, dtype=np.int32)).to(dev)
         m["caps_K"] = torch.full((J * S,), K, dtype=torch.int32, device=dev)
-        m["cur"] = torch.empty((J * S, max(K, 1)), dtype=torch.int32, device=dev)
-        m["cur_counts"] = torch.empty(J * S, dtype=torch.int32, device=dev)
         m["overlap"] = torch.empty(J * S, dtype=torch.int32, device=dev)
-        m["ref_of"] = torch.arange(J, dtype=torch.int32, device=dev).repeat_interleave(S)
         m["trig_of"] = torch.as_tensor(np.asarray(trig_of, dtype=np.int32)).to(dev)
         m["plans"] = []
         if jobs:
@@ -822,10 +815,7 @@ class HeteroCache(DynamicCache):
         m = {"K": K}
         m["score_meta"] = compress.pivot_step_metadata(st.qbuf, store, rows, heads, G)
         m["caps_K"] = torch.full((nl * B * S,), K, dtype=torch.int32, device=dev)
-        m["cur"] = torch.empty((nl * B * S, max(K, 1)), dtype=torch.int32, device=dev)
-        m["cur_counts"] = torch.empty(nl * B * S, dtype=torch.int32, device=dev)
         m["overlap"] = torch.empty(nl * B * S, dtype=torch.int32, device=dev)
-        m["ref_of"] = torch.arange(nl * B, dtype=torch.int32, device=dev).repeat_interleave(S)
         m["trig_of"] = torch.arange(nl, dtype=torch.int32, device=dev).repeat_interleave(B)
         # Retrieval: per leader, one gather job per (batch row, satellite).
         plans = []

@@ -177,10 +177,12 @@ __global__ __launch_bounds__(kSelThreads) void select_count_kernel(const float* 
                                                                    int64_t idx_stride,
                                                                    const unsigned* __restrict__ ghist,
                                                                    int* __restrict__ state, int* __restrict__ cnt,
-                                                                   int32_t* __restrict__ counts, int nchunks) {
+                                                                   int32_t* __restrict__ counts, int nchunks,
+                                                                   int32_t* __restrict__ zero_out) {
   const int job = blockIdx.y, chunk = blockIdx.x;
   const SelJob jb = sel_job(caps, job, span, window, idx_stride);
   if (chunk == 0 && threadIdx.x == 0 && counts) counts[job] = jb.body + jb.tail;
+  if (chunk == 0 && threadIdx.x == 0 && zero_out) zero_out[job] = 0;
   if (jb.body <= 0 || jb.body >= span) return;
   __shared__ int s_pick[3];
   __shared__ int s_red[2][kSelWaves];
@@ -318,6 +320,149 @@ __global__ __launch_bounds__(kSelThreads) void select_write_kernel(const float* 
   }
 }
 
+// Ties of tau in the chunks before `chunk` (from the count kernel's
+// per-chunk counts).
+__device__ __forceinline__ int ties_before(const int* __restrict__ cnt, int job, int chunk, int nchunks) {
+  int eq = 0;
+  for (int c = 0; c < chunk; ++c) eq += cnt[((int64_t)job * nchunks + c) * 2 + 1];
+  return eq;
+}
+
+// Keep masks of one chunk: selm[r] is, per wave, the ballot over positions
+// t0 + r*256 + 64*wave + lane of "kept" -- the key is above tau, or equals it
+// and ranks below need_eq among the ties in position order (eq_before ties
+// in earlier chunks).  Reached by the whole workgroup.
+__device__ __forceinline__ void chunk_keep_masks(const float* __restrict__ s, int span, int t0, uint32_t tau,
+                                                 int need_eq, bool all_ties, int eq_before,
+                                                 uint64_t (&selm)[kSelRows], int (*s_cnt)[kSelWaves],
+                                                 int (*s_off)[kSelWaves]) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint32_t keys[kSelRows];
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + tid;
+    keys[r] = t < span ? order_key(s[t]) : 0u;
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  uint64_t eqm[kSelRows];
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + tid;
+    eqm[r] = __ballot(t < span && keys[r] == tau);
+    if (lane == 0) s_cnt[r][wave] = __popcll(eqm[r]);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int e = eq_before;
+    for (int r = 0; r < kSelRows; ++r)
+      for (int w = 0; w < kSelWaves; ++w) {
+        s_off[r][w] = e;
+        e += s_cnt[r][w];
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + tid;
+    bool take = t < span && keys[r] > tau;
+    if (t < span && keys[r] == tau) {
+      const int rank = s_off[r][wave] + __popcll(eqm[r] & below);
+      take = all_ties || rank < need_eq;
+    }
+    selm[r] = __ballot(take);
+  }
+  __syncthreads();
+}
+
+// 64 bits of a bitmask set starting at a multiple-of-64 position.
+__device__ __forceinline__ uint64_t bits64(const uint32_t* __restrict__ b, int64_t words, int pos) {
+  const int64_t w = pos >> 5;
+  const uint64_t lo = w < words ? b[w] : 0u, hi = w + 1 < words ? b[w + 1] : 0u;
+  return lo | (hi << 32);
+}
+
+// out[job] += |kept(job) ∩ set(job / steps)| over this chunk (out zeroed by
+// the count kernel).  Chunk 0 clears the job's histograms for the next call.
+__global__ __launch_bounds__(kSelThreads) void select_overlap_kernel(
+    const float* __restrict__ scores, int64_t score_stride, int span, const int32_t* __restrict__ caps,
+    unsigned* __restrict__ ghist, const int* __restrict__ state, const int* __restrict__ cnt, int nchunks,
+    const uint32_t* __restrict__ bits, int64_t words, int steps, int32_t* __restrict__ out) {
+  const int job = blockIdx.y, chunk = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const SelJob jb = sel_job(caps, job, span, 0, span);
+  if (chunk == 0)
+    for (int i = tid; i < 4 * kSelBins; i += kSelThreads) ghist[(int64_t)job * 4 * kSelBins + i] = 0u;
+  if (jb.body <= 0) return;
+  __shared__ int s_eq;
+  __shared__ int s_cnt[kSelRows][kSelWaves];
+  __shared__ int s_off[kSelRows][kSelWaves];
+  __shared__ int s_sum[kSelWaves];
+  const uint32_t* ref = bits + (int64_t)(job / steps) * words;
+  const int t0 = chunk * kSelChunk;
+  uint64_t selm[kSelRows];
+  if (jb.body >= span) {
+#pragma unroll
+    for (int r = 0; r < kSelRows; ++r) selm[r] = __ballot(t0 + r * kSelThreads + tid < span);
+  } else {
+    if (tid == 0) s_eq = ties_before(cnt, job, chunk, nchunks);
+    __syncthreads();
+    chunk_keep_masks(scores + (int64_t)job * score_stride, span, t0, (uint32_t)state[job * 4], state[job * 4 + 1],
+                     state[job * 4 + 2] != 0, s_eq, selm, s_cnt, s_off);
+  }
+  int c = 0;
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < kSelRows; ++r) c += __popcll(selm[r] & bits64(ref, words, t0 + r * kSelThreads + 64 * wave));
+    s_sum[wave] = c;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int tot = 0;
+    for (int w = 0; w < kSelWaves; ++w) tot += s_sum[w];
+    if (tot) atomicAdd(out + job, tot);
+  }
+}
+
+// Set j := kept(job j*steps + steps-1) as a bitmask, for sets whose leader
+// triggered (trigger[trig_of[j]] != 0); other sets are left as they are.
+// Each workgroup writes the words of its chunk (and chunk 0 any words past
+// the last chunk), so no set needs clearing first.
+__global__ __launch_bounds__(kSelThreads) void select_bits_kernel(
+    const float* __restrict__ scores, int64_t score_stride, int span, const int32_t* __restrict__ caps,
+    const int* __restrict__ state, const int* __restrict__ cnt, int nchunks, uint32_t* __restrict__ bits,
+    int64_t words, int steps, const int32_t* __restrict__ trigger, const int32_t* __restrict__ trig_of) {
+  const int set = blockIdx.y, chunk = blockIdx.x;
+  if (trigger[trig_of ? trig_of[set] : set] == 0) return;
+  const int job = set * steps + steps - 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const SelJob jb = sel_job(caps, job, span, 0, span);
+  uint32_t* out = bits + (int64_t)set * words;
+  const int t0 = chunk * kSelChunk;
+  if (chunk == 0)
+    for (int64_t w = (int64_t)nchunks * (kSelChunk / 32) + tid; w < words; w += kSelThreads) out[w] = 0u;
+  __shared__ int s_eq;
+  __shared__ int s_cnt[kSelRows][kSelWaves];
+  __shared__ int s_off[kSelRows][kSelWaves];
+  uint64_t selm[kSelRows];
+  if (jb.body <= 0 || jb.body >= span) {
+#pragma unroll
+    for (int r = 0; r < kSelRows; ++r) selm[r] = __ballot(jb.body > 0 && t0 + r * kSelThreads + tid < span);
+  } else {
+    if (tid == 0) s_eq = ties_before(cnt, job, chunk, nchunks);
+    __syncthreads();
+    chunk_keep_masks(scores + (int64_t)job * score_stride, span, t0, (uint32_t)state[job * 4], state[job * 4 + 1],
+                     state[job * 4 + 2] != 0, s_eq, selm, s_cnt, s_off);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < kSelRows; ++r) {
+      const int64_t w = (t0 + r * kSelThreads + 64 * wave) >> 5;
+      if (w < words) out[w] = (uint32_t)selm[r];
+      if (w + 1 < words) out[w + 1] = (uint32_t)(selm[r] >> 32);
+    }
+  }
+}
+
 // The histograms live in a buffer that must be zero before the first call and
 // that every completed call leaves zeroed; state and chunk counts live in a
 // per-call scratch buffer that needs no initialisation.
@@ -372,10 +517,55 @@ extern "C" int hc_select_topk(const float* scores, int64_t score_stride, int njo
     }
   }
   hipLaunchKernelGGL(select_count_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, window,
-                     idx_stride, ghist, state, cnt, counts, nchunks);
+                     idx_stride, ghist, state, cnt, counts, nchunks, (int32_t*)nullptr);
   int rc = check_launch("hc_select_topk(count)");
   if (rc) return rc;
   hipLaunchKernelGGL(select_write_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, window,
                      idx, idx_stride, ghist, state, cnt, nchunks);
   return check_launch("hc_select_topk(write)");
+}
+
+extern "C" int hc_drift_select(const float* scores, int64_t score_stride, int nsets, int steps, int batch, int span,
+                               const int32_t* caps, int K, uint32_t* bits, int64_t words, const int32_t* trig_of,
+                               int nlead, double threshold, int32_t* overlap, int32_t* trigger, void* hist,
+                               size_t hist_bytes, void* scratch, size_t scratch_bytes, void* stream) {
+  clear_error();
+  const int64_t njobs64 = (int64_t)nsets * steps;
+  if (nsets < 0 || steps < 1 || steps > 64 || batch < 1 || span < 1 || K < 1 || njobs64 > 65535 ||
+      (int64_t)nlead * batch != nsets || words < (span + 31) / 32)
+    return set_error(HC_ERR_INVALID, "hc_drift_select: nsets=%d steps=%d batch=%d span=%d K=%d nlead=%d words=%lld",
+                     nsets, steps, batch, span, K, nlead, (long long)words);
+  if (nsets == 0) return HC_OK;
+  if (!scores || !caps || !bits || !overlap || !trigger || !hist || !scratch)
+    return set_error(HC_ERR_INVALID, "hc_drift_select: null pointer argument");
+  const int njobs = (int)njobs64;
+  if (score_stride < span) return set_error(HC_ERR_INVALID, "hc_drift_select: score stride below the span");
+  const int nchunks = (span + kSelChunk - 1) / kSelChunk;
+  if (nchunks > kSelMaxChunks) return set_error(HC_ERR_INVALID, "hc_drift_select: span %d too long", span);
+  if (hist_bytes < select_hist_bytes(njobs) || scratch_bytes < select_scratch_bytes(njobs, span))
+    return set_error(HC_ERR_INVALID, "hc_drift_select: histogram or scratch buffer too small");
+  unsigned* ghist = reinterpret_cast<unsigned*>(hist);
+  int* state = reinterpret_cast<int*>(scratch);
+  int* cnt = state + (size_t)njobs * 4;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid(nchunks, njobs);
+  for (int pass = 0; pass < 4; ++pass) {
+    hipLaunchKernelGGL(select_hist_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, 0,
+                       (int64_t)span, ghist, pass);
+    int rc = check_launch("hc_drift_select(hist)");
+    if (rc) return rc;
+  }
+  hipLaunchKernelGGL(select_count_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, 0,
+                     (int64_t)span, ghist, state, cnt, (int32_t*)nullptr, nchunks, overlap);
+  int rc = check_launch("hc_drift_select(count)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(select_overlap_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, ghist,
+                     state, cnt, nchunks, bits, words, steps, overlap);
+  rc = check_launch("hc_drift_select(overlap)");
+  if (rc) return rc;
+  rc = hc_drift_decide(overlap, nlead, batch, steps, K, threshold, nullptr, nullptr, trigger, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(select_bits_kernel, dim3(nchunks, nsets), dim3(kSelThreads), 0, s, scores, score_stride, span,
+                     caps, state, cnt, nchunks, bits, words, steps, trigger, trig_of);
+  return check_launch("hc_drift_select(bits)");
 }

@@ -477,6 +477,38 @@ def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None
     return idx, counts
 
 
+def drift_select(scores, caps, K, bits, nbits, trig_of, nlead, batch, steps, threshold, trigger, overlap=None,
+                 stream=None):
+    """Drift decision of sets j = leader * batch + b from their step scores
+    (scores [sets * steps, >= nbits] float32, row j * steps + s): per step the
+    overlap of its top-K with bits[j] (out: overlap [sets * steps] int32),
+    trigger[leader] = median over steps of the batch-mean overlap / K <
+    threshold, and bits[j] := top-K of the last step where trigger[trig_of[j]]."""
+    lib = _lib.load()
+    _require_cuda(scores, caps, bits, trig_of, trigger, overlap)
+    if scores.dtype != torch.float32 or scores.dim() != 2 or scores.stride(1) != 1:
+        raise ValueError("scores must be float32 [jobs, n] with unit stride")
+    for name, t in (("caps", caps), ("bits", bits), ("trig_of", trig_of), ("trigger", trigger)):
+        if t.dtype != torch.int32:
+            raise TypeError(f"{name} must be int32")
+    njobs = scores.shape[0]
+    if njobs % steps or caps.numel() < njobs:
+        raise ValueError("scores rows must be sets x steps, with one cap per row")
+    nsets = njobs // steps
+    if bits.dim() != 2 or bits.shape[0] < nsets or trig_of.numel() < nsets:
+        raise ValueError("one bitmask set and one leader index per set")
+    if overlap is None:
+        overlap = torch.empty(njobs, dtype=torch.int32, device=scores.device)
+    hist = SELECT_HIST.get(scores.device, lib.hc_select_hist_size(njobs))
+    scratch = torch.empty(max(lib.hc_select_scratch_size(njobs, int(nbits)), 16), dtype=torch.uint8,
+                          device=scores.device)
+    _lib.check(lib.hc_drift_select(_ptr(scores), scores.stride(0), nsets, int(steps), int(batch), int(nbits),
+                                   _ptr(caps), int(K), _ptr(bits), bits.stride(0), _ptr(trig_of), int(nlead),
+                                   float(threshold), _ptr(overlap), _ptr(trigger), _ptr(hist), hist.numel(),
+                                   _ptr(scratch), scratch.numel(), _stream(stream, scores)))
+    return overlap
+
+
 def set_bits(idx, counts, bits, nbits, fixed_count=0, trigger=None, trig_of=None, stream=None):
     """bits[j] = set of the first counts[j] (or fixed_count) positions of idx[j] (cleared first)."""
     lib = _lib.load()

@@ -316,6 +316,28 @@ int hc_overlap_count(const int32_t* idx, int64_t idx_stride, int count, int nlis
                      int64_t words, int nbits, const int32_t* ref_of, int32_t* out, void* stream);
 
 /*
+ * The whole drift decision of a group of pivot rows from their step scores,
+ * without index lists.  Row j of nsets (j = leader * batch + b) holds `steps`
+ * score rows scores[(j*steps + s)*score_stride + t], t < span; caps[j*steps +
+ * s] (= K) is the size of each step's top set, ranked by (score descending,
+ * position ascending).  Computes overlap[j*steps + s] = |top_K(j, s) ∩ set j|
+ * against the bitmask sets (set j: `words` uint32 words at bits + j*words)
+ * straight from each step's threshold, then trigger[leader] as
+ * hc_drift_decide does (batch mean of count / K, median over the steps, <
+ * threshold), and finally, for every set whose leader triggered
+ * (trigger[trig_of[j]]), rewrites set j as top_K of its last step.  Replaces
+ * the topk + sort + searchsorted + median + set update of
+ * heterocache/cache_utils.py:1059-1082 (hc_select_topk + hc_overlap_count +
+ * hc_drift_decide + hc_set_bits in one pass structure that never writes the
+ * K-long index lists).  hist / scratch: as hc_select_topk for nsets*steps
+ * jobs.
+ */
+int hc_drift_select(const float* scores, int64_t score_stride, int nsets, int steps, int batch, int span,
+                    const int32_t* caps, int K, uint32_t* bits, int64_t words, const int32_t* trig_of, int nlead,
+                    double threshold, int32_t* overlap, int32_t* trigger, void* hist, size_t hist_bytes,
+                    void* scratch, size_t scratch_bytes, void* stream);
+
+/*
  * counts: [npiv][batch][steps] overlap counts of top-K sets.  Per pivot:
  * overlap[s] = mean_b(count/K) (float32), median over steps as
  * statistics.median defines it, trigger = median < threshold
