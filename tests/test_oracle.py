@@ -644,3 +644,37 @@ def test_drift_check_even_median_is_not_below_threshold():
     ov, med, trig, cur = O.drift_check(scores, [[12, 13, 14, 15]], 4, 0.5)
     assert ov.tolist() == [1.0, 0.0] and med == 0.5 and not trig
     assert sorted(cur[0].tolist()) == [0, 1, 2, 3]
+
+
+# -- PyTorch-CPU restatement (the CPU baseline) ---------------------------------
+def test_torch_cpu_restatement_matches_the_oracle():
+    """The CPU baseline's torch op sequence on the config-0 layer: its window
+    scores equal the numpy oracle's (float32 vs float64 evaluation), its kept
+    sets equal the oracle's selection except among positions tied at the
+    threshold (max pooling makes neighbours share a value, and torch.topk
+    orders ties its own way), and its decode output equals the float64
+    closed form over the rows it kept."""
+    from heterocache_amd import workloads
+    from oracle import torch_cpu
+    c = workloads.config0_inputs()
+    t = torch_cpu.config0_tensors(c)
+    L, W, G = 4096, c["window"], 4
+    s, kept = torch_cpu.score_select(t["q_win"], t["k"], t["caps"], W, 7)
+    qw = np.stack([c["q"][0, h * G:(h + 1) * G, L - W:] for h in range(8)])
+    ref = O.window_scores(qw, c["k"][0], "maxpool", 7, window_keep=True)
+    assert np.max(np.abs(s.numpy() - ref) / np.maximum(np.abs(ref), 1e-30)) < 1e-4
+    for h in range(8):
+        mine = set(kept[h].tolist())
+        theirs = set(O.select_with_window(ref[h], t["caps"][h], L, W).tolist())
+        assert len(mine) == len(theirs) == t["caps"][h]
+        sh = s[h].numpy()
+        tau = np.sort(sh)[::-1][t["caps"][h] - W - 1]
+        assert all(sh[p] == tau for p in mine ^ theirs), h
+    ks, vs = torch_cpu.gather(t["k"], t["v"], kept)
+    out = torch_cpu.decode(t["q_dec"], ks, vs, t["k_dec"], t["v_dec"])
+    rows_k = [np.concatenate([c["k"][0, h][kept[h].numpy()], c["k_dec"][0, h]]) for h in range(8)]
+    rows_v = [np.concatenate([c["v"][0, h][kept[h].numpy()], c["v_dec"][0, h]]) for h in range(8)]
+    ref_out = O.decode_attention(c["q_dec"][0].reshape(8, G, 128), rows_k, rows_v)
+    assert np.abs(out.numpy() - ref_out).max() < 1e-4
+    med = torch_cpu.time_stages(t, threads=1, runs=2, warmup=1)
+    assert set(med) >= {"score_pool_topk", "gather", "decode", "decode_gbs"}
