@@ -11,9 +11,14 @@ Counterpart of heterocache/utils.py:
   install_attention_patch                  (:195-197) swaps the attention
       classes into transformers before a model is built;
   attach_cache                             (:372-383) makes generate() build a
-      HeteroCache.
+      HeteroCache;
+  load_model_and_tokenizer                 (:178-384) all of the above from a
+      model directory, a method name and the head-analysis JSON found by its
+      naming convention.
 """
 import copy
+import json
+import os
 
 import numpy as np
 import torch
@@ -164,3 +169,82 @@ def attach_cache(model, cache_config):
         model_kwargs["past_key_values"] = cache
     model._prepare_cache_for_generation = _prepare_cache_for_generation.__get__(model, model.__class__)
     return model
+
+
+def head_analysis_path(load_dir, model_path, topk, stable_threshold, sim_threshold, decode_step):
+    """The head-analysis JSON of a model, named as the reference names it
+    (heterocache/utils.py:218-222)."""
+    name = str(model_path).lower().rstrip("/").split("/")[-1]
+    return os.path.join(load_dir, f"Head_Analysis_{name}_topk{topk}_th{stable_threshold}_sim{sim_threshold}"
+                                  f"_step{decode_step}.json")
+
+
+def attach_cache_factory(model, factory):
+    """Make generate() construct its cache with factory()."""
+    def _prepare_cache_for_generation(self, generation_config, model_kwargs, *args, **kwargs):
+        model_kwargs["past_key_values"] = factory()
+    model._prepare_cache_for_generation = _prepare_cache_for_generation.__get__(model, model.__class__)
+    return model
+
+
+def load_model_and_tokenizer(args):
+    """Model and tokenizer with a KV-cache method attached
+    (heterocache/utils.py:178-384).
+
+    args (a namespace, as the reference's command line gives it): method
+    (fullkv, snapkv, pyramidkv, streamingllm, h2o, cake, heterocache),
+    model_path, compression_ratio, and for heterocache load_dir, topk,
+    stable_threshold, sim_threshold, decode_step (the JSON's name),
+    real_offload, max_gen_len, steps (the drift-check period).  Optional:
+    attn_implementation (default "sdpa"), torch_dtype (default float16, as
+    the reference), device_map (default "auto").  The attention classes are
+    patched before the model is built (every method runs this build's
+    kernels); heterocache reorders the heads by the JSON, augments it and
+    checks the ratio as the reference does.  4-bit quantization (the
+    reference's bitsandbytes path) is not provided.
+    """
+    from transformers import AutoModelForCausalLM, AutoTokenizer, DynamicCache
+    from . import cache_utils as C
+    method = args.method.lower()
+    classes = {"fullkv": None, "snapkv": C.SnapKVCache, "pyramidkv": C.PyramidKVCache,
+               "streamingllm": C.StreamingLLMKVCache, "h2o": C.H2OKVCache, "cake": C.CAKECache,
+               "heterocache": HeteroCache}
+    if method not in classes:
+        raise ValueError(f"unknown method {args.method!r}; expected one of {sorted(classes)}")
+    if getattr(args, "quant", False):
+        raise NotImplementedError("4-bit quantization (bitsandbytes) is not provided by this build")
+    data = None
+    if method == "heterocache":
+        path = head_analysis_path(args.load_dir, args.model_path, args.topk, args.stable_threshold,
+                                  args.sim_threshold, args.decode_step)
+        with open(path, "r", encoding="utf-8") as f:
+            data = json.load(f)
+    dtype = getattr(args, "torch_dtype", torch.float16)
+    with install_attention_patch():
+        model = AutoModelForCausalLM.from_pretrained(
+            args.model_path, torch_dtype=dtype, low_cpu_mem_usage=True,
+            device_map=getattr(args, "device_map", "auto"),
+            attn_implementation=getattr(args, "attn_implementation", "sdpa"))
+    tokenizer = AutoTokenizer.from_pretrained(args.model_path, use_fast=True, padding_side="left")
+    cfg = model.config
+    common = {"pooling": "avgpool", "kernel_size": 5, "num_attn_heads": cfg.num_attention_heads,
+              "num_kv_heads": cfg.num_key_value_heads, "num_layers": cfg.num_hidden_layers,
+              "compression_ratio": args.compression_ratio}
+    if method == "heterocache":
+        perms = reorder_model_weights_by_classification(model, data)
+        data = augment_head_data(data, perms)
+        cache_config = build_cache_config(model, data, stable_threshold=args.stable_threshold,
+                                          real_offload=args.real_offload, max_gen_len=args.max_gen_len,
+                                          decode_step=args.steps, **{k: v for k, v in common.items()
+                                                                     if k not in ("num_attn_heads", "num_kv_heads",
+                                                                                  "num_layers")})
+        attach_cache(model, cache_config)
+    elif method == "fullkv":
+        cache_config = {}
+        attach_cache_factory(model, DynamicCache)
+    else:
+        cache_config = C.CompressionCacheConfig(window_size=32 if method == "cake" else 1, **common)
+        cls = classes[method]
+        attach_cache_factory(model, lambda: cls(cache_config))
+    model.config.cache_config = cache_config
+    return model, tokenizer

@@ -228,3 +228,27 @@ def test_temp_kv_cache_through_patched_attention(dev):
     seen = temp._seen_tokens
     temp.clear_temp_kv_cache()
     assert temp.temp_key_cache == [] and temp._seen_tokens == seen - 1
+
+
+def test_load_model_and_tokenizer_generate(dev, tmp_path):
+    """Models loaded by utils.load_model_and_tokenizer from a saved
+    directory and a head JSON found by the reference's naming convention:
+    HeteroCache generation in float16 (the reference's load dtype) runs
+    through prefill selection, drift checks and retrieval; the full-KV
+    method in float32 gives the stock model's greedy tokens."""
+    from tests.test_utils_cpu import _args, _saved_model_dir
+    model_dir, load_dir, _ = _saved_model_dir(tmp_path, [[3, 4], [1, 2]], [{"0": [1]}, {}])
+    model, tok = utils.load_model_and_tokenizer(_args(model_dir, load_dir, torch_dtype=torch.float16,
+                                                      device_map="cuda:0", max_gen_len=32))
+    text = " ".join(f"w{(7 * i) % 512}" for i in range(600))
+    ids = tok(text, return_tensors="pt")["input_ids"].to(dev)
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=12, do_sample=False)
+    assert out.shape == (1, 612)
+    full, _ = utils.load_model_and_tokenizer(_args(model_dir, load_dir, method="fullkv", torch_dtype=torch.float32,
+                                                   device_map="cuda:0"))
+    stock = LlamaForCausalLM.from_pretrained(model_dir, torch_dtype=torch.float32).to(dev).eval()
+    with torch.no_grad():
+        a = full.generate(ids[:, :300], max_new_tokens=10, do_sample=False)
+        b = stock.generate(ids[:, :300], max_new_tokens=10, do_sample=False)
+    assert torch.equal(a, b)
