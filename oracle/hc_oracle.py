@@ -788,7 +788,8 @@ class CacheOracle:
     """
 
     def __init__(self, data, batch, q_heads, kv_heads, num_layers, ratio, threshold, decode_step, pooling, kernel,
-                 retrieval_topk=None, quirks=False, select_before_attention=False, max_gen=64, score_hook=None):
+                 retrieval_topk=None, quirks=False, select_before_attention=False, max_gen=64, score_hook=None,
+                 io_dtype=None):
         self.data = data
         self.B, self.Hq, self.Hkv, self.NL = batch, q_heads, kv_heads, num_layers
         self.G = q_heads // kv_heads
@@ -797,6 +798,7 @@ class CacheOracle:
         self.topk, self.quirks, self.select_first = retrieval_topk, quirks, select_before_attention
         self.max_gen = max_gen
         self.score_hook = score_hook
+        self.io_dtype = io_dtype    # the reference's casts of scores to the model dtype ("bfloat16", ...)
         self.full_heads = data["meta"]["counts"]["volatile"] + data["meta"]["counts"]["pivot"]
         self.rows = {}      # layer -> list over b*Hkv+h of [K, V] views [len, 128]
         self._buf = {}      # layer -> list over rows of (K, V) buffers [len + max_gen, 128]
@@ -838,7 +840,7 @@ class CacheOracle:
                     self._set_row(layer, r, k[b, h], v[b, h])
                 elif h < n_c:
                     s = last_query_scores(q[b, h * self.G:(h + 1) * self.G, -1][None], k[b, h][None], self.pooling,
-                                          self.kernel)[0]
+                                          self.kernel, io_dtype=self.io_dtype)[0]
                     s = self._scores("prefill", layer, h, s)
                     sel = topk_select(s, int(caps[h]))
                     self._set_row(layer, r, k[b, h][sel], v[b, h][sel])
@@ -853,7 +855,7 @@ class CacheOracle:
             sets[p] = []
             for b in range(B):
                 s = last_query_scores(q[b, p * self.G:(p + 1) * self.G, -1][None], k[b, p][None], self.pooling,
-                                      self.kernel)[0]
+                                      self.kernel, io_dtype=self.io_dtype)[0]
                 sets[p].append(set(topk_indices(self._scores("pivot", layer, p, s), K).tolist()))
         ref = {}
         for i, leader in enumerate(int(x) for x in rel):
@@ -904,7 +906,7 @@ class CacheOracle:
                 continue
             sc = np.stack([pivot_step_scores(qs[b, leader * self.G:(leader + 1) * self.G],
                                              self.rows[layer][b * self.Hkv + leader][0][:self.L], self.pooling,
-                                             self.kernel) for b in range(self.B)])
+                                             self.kernel, io_dtype=self.io_dtype) for b in range(self.B)])
             sc = self._scores("drift", layer, leader, sc)
             _, med, trig, cur_last = drift_check(sc, [sorted(s) for s in self.ref[layer][leader]], K, self.threshold)
             self.triggers.append((layer, leader, bool(trig)))

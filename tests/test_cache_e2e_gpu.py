@@ -219,3 +219,60 @@ def test_chunked_prefill_with_observation_window_equals_single_shot(dev):
             assert torch.equal(ka, kb) and torch.equal(va, vb), (layer, r)
         if whole._drift[layer].ref_bits is not None:
             assert torch.equal(whole._drift[layer].ref_bits, chunked._drift[layer].ref_bits)
+
+
+def test_reference_cast_chain_bf16(dev):
+    """round_scores=True (the reference's casts of logits, probabilities and
+    pooled scores to bfloat16) on a bfloat16 model: the device scores equal
+    the oracle's cast chain to within one bfloat16 step; the oracle's
+    integer flow run on the device scores reproduces the
+    triggers and the stores bit for bit, and the attention outputs match
+    the float64 closed form.  The cast scores tie massively, so this also
+    exercises the lowest-position tie rule of every selection."""
+    from tests.test_configs_full_gpu import DeviceScores, Recorder
+    B, Hq, Hkv, NL, D, L, steps = 1, 32, 8, 2, 128, 2048, 10
+    data = head_data()
+    cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
+                            max_gen_len=steps + 4, decode_step=5, pooling="avgpool", kernel_size=5,
+                            num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, round_scores=True)
+    cache = HeteroCache(cfg)
+    rec = Recorder(range(NL))
+    cache.observer = rec
+    hook = DeviceScores(rec, 0.5)
+    orc = O.CacheOracle(data, B, Hq, Hkv, NL, 0.5, 0.5, 5, "avgpool", 5, score_hook=hook, io_dtype="bfloat16")
+    hook.orc = orc
+    g = torch.Generator().manual_seed(3)
+    last_q = []
+    for layer in range(NL):
+        q = torch.randn((B, Hq, 1, D), generator=g).to(torch.bfloat16).to(dev)
+        k = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(dev)
+        v = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(dev)
+        kc, vc = cache.update(k, v, layer)
+        cache.init_coefficient(q, kc, layer)
+        cache.prefill_select(q, kc, vc, layer)
+        orc.prefill(layer, as_np(q), as_np(k), as_np(v))
+        last_q.append(q)
+    for step in range(steps):
+        outs = []
+        for layer in range(NL):
+            q = last_q[layer] if step < 5 else torch.randn((B, Hq, 1, D), generator=g).to(torch.bfloat16).to(dev)
+            kn = torch.randn((B, Hkv, 1, D), generator=g).to(torch.bfloat16).to(dev)
+            vn = torch.randn((B, Hkv, 1, D), generator=g).to(torch.bfloat16).to(dev)
+            cache.update(kn, vn, layer)
+            outs.append((cache.decode_attention(q, layer), q, kn, vn))
+            cache.decode_select(q, layer)
+        # The device checks this step's layers after the last one; the oracle follows.
+        for layer, (out, q, kn, vn) in enumerate(outs):
+            ref = orc.decode(layer, as_np(q), as_np(kn), as_np(vn))
+            assert np.abs(as_np(out).reshape(B, Hq, D) - ref).max() <= 2e-2
+    torch.cuda.synchronize()
+    flags = [(l, h, c[(l, h)]) for c in rec.checks for l in range(NL) for h in cache._drift[l].leaders]
+    assert flags == orc.triggers and [f for *_, f in flags] == [False] * 3 + [True] * 3
+    assert max(e for *_, e in hook.err) <= 2.0 ** -7 * 1.01
+    for layer in range(NL):
+        store = cache.stores[layer]
+        for r in range(B * Hkv):
+            n = int(store.host_len[r])
+            ks, vs = store.read_rows([r], n)
+            ok, ov = orc.rows[layer][r]
+            assert n == len(ok) and np.array_equal(as_np(ks[0]), ok) and np.array_equal(as_np(vs[0]), ov)
