@@ -61,7 +61,7 @@ SIGNATURES = {
                           c_int, c_void_p, c_void_p]),
     "hc_score": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
                          c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p,
-                         c_void_p, c_size_t, c_void_p]),
+                         c_void_p, c_size_t, c_void_p, c_void_p]),
     "hc_score_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "hc_cake_score": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int, c_int,
                               c_int, c_int, c_int, c_int, c_float, c_float, c_void_p, c_void_p, c_void_p, c_size_t,
@@ -76,8 +76,9 @@ SIGNATURES = {
     "hc_overlap_count": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,
                                  c_void_p]),
     "hc_drift_select": (c_int, [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int64,
-                                c_void_p, c_int, ctypes.c_double, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p,
-                                c_size_t, c_void_p]),
+                                c_void_p, c_int, ctypes.c_double, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                c_void_p]),
+    "hc_drift_scratch_size": (c_size_t, [c_int, c_int]),
     "hc_drift_decide": (c_int, [c_void_p, c_int, c_int, c_int, c_int, ctypes.c_double, c_void_p, c_void_p, c_void_p,
                                 c_void_p]),
     "hc_store_read": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p,

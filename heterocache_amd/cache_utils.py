@@ -648,11 +648,11 @@ class HeteroCache(DynamicCache):
         # Scores of every (leader in relation order, batch row): [nl*B, S, L].
         scores = compress.pivot_step_scores(st.qbuf, store, None, None, G, L, self.pooling, self.kernel_size,
                                             round_dtype=self._round_dtype(st.qbuf.dtype),
-                                            metadata=m["score_meta"])
+                                            metadata=m["score_meta"], hist=m["hist"])
         # Overlaps, decision and, on trigger, the last step's top-K as the new
         # reference set -- all from the step thresholds.
         ops.drift_select(scores.view(nl * B * S, L), m["caps_K"], K, st.ref_bits, L, m["trig_of"], nl, B, S,
-                         self.stable_threshold, st.trigger, overlap=m["overlap"])
+                         self.stable_threshold, st.trigger, m["hist"], overlap=m["overlap"])
         if m["plans"]:
             self._retrieve(layer_idx, st, scores[:, S - 1])
         if self.observer is not None:
@@ -680,9 +680,9 @@ class HeteroCache(DynamicCache):
         flags = compress.ROUND_FLAGS[self._round_dtype(qa.dtype)]
         scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,
                            self.pooling, self.kernel_size, 1.0 / math.sqrt(self.head_dim), flags=flags,
-                           row_tile_off=self._tile_table, k_row=bm["k_row"]).view(J, S, L)
+                           row_tile_off=self._tile_table, k_row=bm["k_row"], hist=bm["hist"]).view(J, S, L)
         ops.drift_select(scores.view(J * S, L), bm["caps_K"], K, bits, L, bm["trig_of"], nlead, B, S,
-                         self.stable_threshold, trig, overlap=bm["overlap"])
+                         self.stable_threshold, trig, bm["hist"], overlap=bm["overlap"])
         if bm["retrieve"]:
             ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
         if self.observer is not None:
@@ -752,6 +752,7 @@ class HeteroCache(DynamicCache):
         m["k_row"] = torch.as_tensor(np.asarray(k_row, dtype=np.int32)).to(dev)
         m["caps_K"] = torch.full((J * S,), K, dtype=torch.int32, device=dev)
         m["overlap"] = torch.empty(J * S, dtype=torch.int32, device=dev)
+        m["hist"] = self._drift_hist(J * S, dev)
         m["trig_of"] = torch.as_tensor(np.asarray(trig_of, dtype=np.int32)).to(dev)
         m["plans"] = []
         if jobs:
@@ -816,6 +817,7 @@ class HeteroCache(DynamicCache):
         m["score_meta"] = compress.pivot_step_metadata(st.qbuf, store, rows, heads, G)
         m["caps_K"] = torch.full((nl * B * S,), K, dtype=torch.int32, device=dev)
         m["overlap"] = torch.empty(nl * B * S, dtype=torch.int32, device=dev)
+        m["hist"] = self._drift_hist(nl * B * S, dev)
         m["trig_of"] = torch.arange(nl, dtype=torch.int32, device=dev).repeat_interleave(B)
         # Retrieval: per leader, one gather job per (batch row, satellite).
         plans = []
@@ -847,6 +849,15 @@ class HeteroCache(DynamicCache):
                                    trig_of=[i for i, b, mm, n in jobs])
             m["plans"].append(plan)
         return m
+
+    def _drift_hist(self, rows, dev):
+        """First-digit key histograms the scorer builds for the drift
+        selection, one per step row; None when the group's S buffered queries
+        are too many rows for the scorer to build them (the selection then
+        builds its own)."""
+        if self.num_key_value_groups * self.decode_step > ops.HIST_MAX_ROWS:
+            return None
+        return torch.empty((rows, ops.HIST_BINS), dtype=torch.int32, device=dev)
 
     def _retrieval_lengths(self, layer_idx, members):
         alloc = self.data["allocation_matrix"][layer_idx]

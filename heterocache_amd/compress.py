@@ -132,8 +132,9 @@ def pivot_step_metadata(q_steps, store, rows, heads, group):
 
 
 def pivot_step_scores(q_steps, store, rows, heads, group, seq_len, pooling="avgpool", kernel=5, round_dtype=None,
-                      scale=None, stream=None, metadata=None):
-    """Scores [len(rows), S, seq_len] of S buffered decode queries per pivot.
+                      scale=None, stream=None, metadata=None, hist=None):
+    """Scores [len(rows), S, seq_len] of S buffered decode queries per pivot
+    (and, into `hist`, their first-digit key histograms; see ops.score).
 
     q_steps: [B, Hq, S, 128]; rows[j] is the store row of pivot j (batch
     b_j = rows[j] // Hkv) whose query heads are heads[j]*group + g.  Keys are
@@ -147,7 +148,7 @@ def pivot_step_scores(q_steps, store, rows, heads, group, seq_len, pooling="avgp
     flags = ROUND_FLAGS[round_dtype]
     out = ops.score(q_steps, q_off, q_steps.stride(1), q_steps.stride(2), store.k, None, 0,
                     seq_len, group, S, seq_len, pooling, kernel, scale, flags=flags,
-                    row_tile_off=store.row_tile_off, k_row=k_row, stream=stream)
+                    row_tile_off=store.row_tile_off, k_row=k_row, hist=hist, stream=stream)
     return out.view(q_off.numel(), S, seq_len)
 
 

@@ -175,4 +175,18 @@ __device__ __forceinline__ float rows4_sum(float v) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Order-preserving uint32 key of a float score (larger float, larger key;
+// -0 ranks equal to +0), used by every selection over scores.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Width of the first digit of the drift check's selection: the histogram
+// the scorer builds over its scores' top kKeyDigitBits key bits.
+constexpr int kKeyDigitBits = 12;
+constexpr int kKeyDigitBins = 1 << kKeyDigitBits;
+constexpr int kKeyDigitShift = 32 - kKeyDigitBits;
+
 }  // namespace hc

@@ -287,7 +287,10 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
 
 // One wave per (job, row): lanes stride over the chunks, then a xor tree.
 __global__ __launch_bounds__(256) void score_stats_merge_kernel(const float* __restrict__ part, int nchunks, int R,
-                                                                int njobs, float* __restrict__ stats) {
+                                                                int njobs, float* __restrict__ stats,
+                                                                uint32_t* __restrict__ hist, int64_t hist_words) {
+  // Zero the optional score histogram the finish pass accumulates into.
+  for (int64_t w = (int64_t)blockIdx.x * 256 + threadIdx.x; w < hist_words; w += (int64_t)gridDim.x * 256) hist[w] = 0u;
   const int i = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (i >= njobs * R) return;
@@ -612,101 +615,127 @@ __device__ __forceinline__ float fin_prob(float x, float m, float iz) {
 constexpr int kFinHalo = 32;  // >= kPoolMaxHalf, keeps the strip 16-byte aligned
 constexpr int kFinHeads = 4;  // query heads whose loads are in flight together
 
-template <int RMODE, int POOL>
+// With HIST, every output row also gets a kKeyDigitBins histogram of the
+// top kKeyDigitBits bits of its scores' order keys (hist[row][digit], zeroed
+// by the statistics merge): the first digit of the drift check's selection,
+// built while the scores are in registers.  Workgroups then take several
+// tiles of their row (gridDim.x < tiles) so that each flushes its LDS
+// histogram to the row's once.
+template <int RMODE, int POOL, bool HIST>
 __global__ __launch_bounds__(256) void score_finish_kernel(const float* __restrict__ logits,
                                                            const float* __restrict__ stats, int R, int G, int W,
                                                            int span, int sum_w, int kernel, int accumulate,
-                                                           float* __restrict__ S) {
+                                                           float* __restrict__ S, uint32_t* __restrict__ hist) {
   // s_a[kFinHalo + i] holds position t0 + i of the current head's strip,
   // i in [-p, kFinTile + p).  Thread x loads positions t0 + 4x .. +3 (one
   // 16-byte load per row) and pools positions t0 + x + 256k, so LDS reads
   // of neighbouring lanes are consecutive words.
   __shared__ __align__(16) float s_a[kFinTile + 2 * kFinHalo];
   __shared__ float s_m[kLogitRowsMax], s_iz[kLogitRowsMax];  // row max, 1 / row sum
+  __shared__ uint32_t s_hist[HIST ? kKeyDigitBins : 1];
   const int wout = sum_w ? 1 : W;
   const int job = blockIdx.y / wout, wo = blockIdx.y % wout;
-  const int t0 = blockIdx.x * kFinTile;
+  const int ntiles = (span + kFinTile - 1) / kFinTile;
   const int p = kernel / 2;
   constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
   for (int r = threadIdx.x; r < R; r += 256) {
     s_m[r] = stats[((int64_t)job * R + r) * 2];
     s_iz[r] = 1.f / stats[((int64_t)job * R + r) * 2 + 1];
   }
+  if constexpr (HIST)
+    for (int b = threadIdx.x; b < kKeyDigitBins; b += 256) s_hist[b] = 0u;
   const int w_lo = sum_w ? 0 : wo, w_hi = sum_w ? W : wo + 1;
-  const int tb = t0 + 4 * threadIdx.x;
-  const bool vec_ok = (span & 3) == 0 && tb + 4 <= span;
-  // Halo: threads [0, p) load t0 - p + x (left), threads [p, 2p) load
-  // t0 + kFinTile + (x - p) (right).
   const bool halo = threadIdx.x < 2 * p;
-  const int th = threadIdx.x < p ? t0 - p + threadIdx.x : t0 + kFinTile + (threadIdx.x - p);
-  const int sh = threadIdx.x < p ? kFinHalo - p + threadIdx.x : kFinHalo + kFinTile + (threadIdx.x - p);
   const float inv_k = 1.f / (float)kernel;
-  float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  float* o = S + ((int64_t)job * wout + wo) * span;
   __syncthreads();
-  // Heads are taken kFinHeads at a time: all their rows' loads are issued
-  // before any strip is pooled.
-  for (int g0 = 0; g0 < G; g0 += kFinHeads) {
-    f32x4 a4[kFinHeads];
-    float ah[kFinHeads];
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int t0 = tile * kFinTile;
+    const int tb = t0 + 4 * threadIdx.x;
+    const bool vec_ok = (span & 3) == 0 && tb + 4 <= span;
+    // Halo: threads [0, p) load t0 - p + x (left), threads [p, 2p) load
+    // t0 + kFinTile + (x - p) (right).
+    const int th = threadIdx.x < p ? t0 - p + threadIdx.x : t0 + kFinTile + (threadIdx.x - p);
+    const int sh = threadIdx.x < p ? kFinHalo - p + threadIdx.x : kFinHalo + kFinTile + (threadIdx.x - p);
+    float best[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    // Heads are taken kFinHeads at a time: all their rows' loads are issued
+    // before any strip is pooled.
+    for (int g0 = 0; g0 < G; g0 += kFinHeads) {
+      f32x4 a4[kFinHeads];
+      float ah[kFinHeads];
 #pragma unroll
-    for (int gg = 0; gg < kFinHeads; ++gg) {
-      const int g = g0 + gg;
-      a4[gg] = f32x4{pad, pad, pad, pad};
-      ah[gg] = pad;
-      if (g >= G) continue;
-      if (tb < span) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        for (int w = w_lo; w < w_hi; ++w) {
-          const int r = g * W + w;
-          const float* row = logits + ((int64_t)job * R + r) * span;
-          const float m = s_m[r], iz = s_iz[r];
-          if (vec_ok) {
-            const f32x4 x = *reinterpret_cast<const f32x4*>(row + tb);
+      for (int gg = 0; gg < kFinHeads; ++gg) {
+        const int g = g0 + gg;
+        a4[gg] = f32x4{pad, pad, pad, pad};
+        ah[gg] = pad;
+        if (g >= G) continue;
+        if (tb < span) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          for (int w = w_lo; w < w_hi; ++w) {
+            const int r = g * W + w;
+            const float* row = logits + ((int64_t)job * R + r) * span;
+            const float m = s_m[r], iz = s_iz[r];
+            if (vec_ok) {
+              const f32x4 x = *reinterpret_cast<const f32x4*>(row + tb);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] += fin_prob<RMODE>(x[e], m, iz);
-          } else {
+              for (int e = 0; e < 4; ++e) acc[e] += fin_prob<RMODE>(x[e], m, iz);
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (tb + e < span) acc[e] += fin_prob<RMODE>(row[tb + e], m, iz);
+              for (int e = 0; e < 4; ++e)
+                if (tb + e < span) acc[e] += fin_prob<RMODE>(row[tb + e], m, iz);
+            }
           }
-        }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a4[gg][e] = tb + e < span ? round_fixed<RMODE>(acc[e]) : pad;
-      }
-      if (halo && th >= 0 && th < span) {
-        float acc = 0.f;
-        for (int w = w_lo; w < w_hi; ++w) {
-          const int r = g * W + w;
-          acc += fin_prob<RMODE>(logits[((int64_t)job * R + r) * span + th], s_m[r], s_iz[r]);
+          for (int e = 0; e < 4; ++e) a4[gg][e] = tb + e < span ? round_fixed<RMODE>(acc[e]) : pad;
         }
-        ah[gg] = round_fixed<RMODE>(acc);
+        if (halo && th >= 0 && th < span) {
+          float acc = 0.f;
+          for (int w = w_lo; w < w_hi; ++w) {
+            const int r = g * W + w;
+            acc += fin_prob<RMODE>(logits[((int64_t)job * R + r) * span + th], s_m[r], s_iz[r]);
+          }
+          ah[gg] = round_fixed<RMODE>(acc);
+        }
+      }
+#pragma unroll
+      for (int gg = 0; gg < kFinHeads; ++gg) {
+        if (g0 + gg >= G) break;
+        __syncthreads();  // the previous strip has been pooled
+        *reinterpret_cast<f32x4*>(&s_a[kFinHalo + 4 * threadIdx.x]) = a4[gg];
+        if (halo) s_a[sh] = ah[gg];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int c = threadIdx.x + 256 * k;  // output position t0 + c
+          const float* win = s_a + kFinHalo + c - p;
+          float v = pad;
+          for (int d = 0; d <= 2 * p; ++d) v = POOL == 0 ? v + win[d] : fmaxf(v, win[d]);
+          if constexpr (POOL == 0) v *= inv_k;
+          best[k] = fmaxf(best[k], round_fixed<RMODE>(v));
+        }
       }
     }
 #pragma unroll
-    for (int gg = 0; gg < kFinHeads; ++gg) {
-      if (g0 + gg >= G) break;
-      __syncthreads();  // the previous strip has been pooled
-      *reinterpret_cast<f32x4*>(&s_a[kFinHalo + 4 * threadIdx.x]) = a4[gg];
-      if (halo) s_a[sh] = ah[gg];
-      __syncthreads();
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int c = threadIdx.x + 256 * k;  // output position t0 + c
-        const float* win = s_a + kFinHalo + c - p;
-        float v = pad;
-        for (int d = 0; d <= 2 * p; ++d) v = POOL == 0 ? v + win[d] : fmaxf(v, win[d]);
-        if constexpr (POOL == 0) v *= inv_k;
-        best[k] = fmaxf(best[k], round_fixed<RMODE>(v));
+    for (int k = 0; k < 4; ++k) {
+      const int t = t0 + threadIdx.x + 256 * k;
+      if (t < span) {
+        o[t] = accumulate ? o[t] + best[k] : best[k];
+        if constexpr (HIST) atomicAdd(&s_hist[order_key(best[k]) >> kKeyDigitShift], 1u);
       }
     }
   }
-  float* o = S + ((int64_t)job * wout + wo) * span;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int t = t0 + threadIdx.x + 256 * k;
-    if (t < span) o[t] = accumulate ? o[t] + best[k] : best[k];
+  if constexpr (HIST) {
+    __syncthreads();
+    uint32_t* h = hist + ((int64_t)job * wout + wo) * kKeyDigitBins;
+    for (int b = threadIdx.x; b < kKeyDigitBins; b += 256)
+      if (s_hist[b]) atomicAdd(&h[b], s_hist[b]);
   }
 }
+
+// Tiles per workgroup of the histogram-building finish: each workgroup
+// flushes its histogram once, so a row's histogram takes tiles / this many
+// flushes (global atomics on the same few lines serialise).
+constexpr int kFinHistTiles = 4;
 
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
@@ -763,7 +792,8 @@ static int plan_chunks(const void* fn, size_t lds, int njobs, int nchunks, Score
 }
 
 template <typename T, bool STORE>
-static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* scores, void* ws, hipStream_t s) {
+static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* scores, void* ws, uint32_t* hist,
+                        hipStream_t s) {
   const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
   const int wout = (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : a.W;
   float* part = reinterpret_cast<float*>(ws);
@@ -792,20 +822,31 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   int rc = check_launch("hc_score(stats)");
   if (rc) return rc;
   hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nparts, a.R,
-                     njobs, stats);
+                     njobs, stats, hist, hist ? (int64_t)njobs * wout * kKeyDigitBins : (int64_t)0);
   if ((rc = check_launch("hc_score(merge)"))) return rc;
   if (via_logits) {
     if (a.span > 0) {
-      const dim3 fgrid((a.span + kFinTile - 1) / kFinTile, njobs * wout);
+      const int ntiles = (a.span + kFinTile - 1) / kFinTile;
+      const int rows = njobs * wout;
+      const int per_row = hist ? (ntiles + kFinHistTiles - 1) / kFinHistTiles : ntiles;
+      const dim3 fgrid(per_row, rows);
       const int sum_w = (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : 0;
       const int rmode = rm;
-#define HC_FINISH(RM, PL)                                                                                  \
-  hipLaunchKernelGGL((score_finish_kernel<RM, PL>), fgrid, dim3(256), 0, s, A, stats, a.R, a.G, a.W, a.span, \
-                     sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores)
+#define HC_FINISH2(RM, PL, HI)                                                                             \
+  hipLaunchKernelGGL((score_finish_kernel<RM, PL, HI>), fgrid, dim3(256), 0, s, A, stats, a.R, a.G, a.W,       \
+                     a.span, sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores, hist)
+#define HC_FINISH(RM, PL)          \
+  do {                             \
+    if (hist)                      \
+      HC_FINISH2(RM, PL, true);    \
+    else                           \
+      HC_FINISH2(RM, PL, false);   \
+  } while (0)
       if (rmode == 0) { if (pooling == 0) HC_FINISH(0, 0); else HC_FINISH(0, 1); }
       else if (rmode == 1) { if (pooling == 0) HC_FINISH(1, 0); else HC_FINISH(1, 1); }
       else { if (pooling == 0) HC_FINISH(2, 0); else HC_FINISH(2, 1); }
 #undef HC_FINISH
+#undef HC_FINISH2
       if ((rc = check_launch("hc_score(finish)"))) return rc;
     }
     return HC_OK;
@@ -986,7 +1027,7 @@ static int launch_cake(ScoreArgs a, int njobs, int batch, int heads, float gamma
   hipLaunchKernelGGL(fstats, dim3(nparts, njobs), dim3(kScoreWaves * 64), lds1, s, as, part, nullptr);
   if ((rc = check_launch("hc_cake_score(stats)"))) return rc;
   hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nparts, a.R,
-                     njobs, stats);
+                     njobs, stats, (uint32_t*)nullptr, (int64_t)0);
   if ((rc = check_launch("hc_cake_score(merge)"))) return rc;
   auto fprobs = score_probs_kernel<T, false, RM, kWin16, true>;
   ScoreArgs ap = a;
@@ -1018,7 +1059,7 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
                         const void* k, const int64_t* k_off, int64_t k_tok_stride, const int64_t* row_tile_off,
                         const int32_t* k_row, int njobs, int seq_len, int group, int window, int flags, int span,
                         int pooling, int kernel, float scale, float* scores, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+                        size_t workspace_bytes, uint32_t* hist, void* stream) {
   clear_error();
   if (njobs < 0 || njobs > 65535 || seq_len < 0 || group < 1 || window < 1)
     return set_error(HC_ERR_INVALID, "hc_score: njobs=%d seq_len=%d group=%d window=%d", njobs, seq_len, group,
@@ -1048,6 +1089,9 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
     return set_error(HC_ERR_INVALID, "hc_score: key token stride %lld", (long long)k_tok_stride);
   if (workspace_bytes < score_workspace_bytes(njobs, seq_len, group, window, flags))
     return set_error(HC_ERR_INVALID, "hc_score: workspace too small");
+  if (hist && (R >= kLogitRows || (flags & HC_SCORE_ACCUMULATE)))
+    return set_error(HC_ERR_INVALID, "hc_score: a score histogram needs fewer than %d query rows and no accumulation",
+                     kLogitRows);
   ScoreArgs a;
   a.q = q;
   a.q_off = q_off;
@@ -1070,8 +1114,8 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
   a.cpw = 1;
   hipStream_t s = (hipStream_t)stream;
 #define HC_SCORE_DISPATCH(T)                                                                          \
-  return store ? launch_score<T, true>(a, njobs, pooling, kernel, scores, workspace, s)               \
-               : launch_score<T, false>(a, njobs, pooling, kernel, scores, workspace, s);
+  return store ? launch_score<T, true>(a, njobs, pooling, kernel, scores, workspace, hist, s)         \
+               : launch_score<T, false>(a, njobs, pooling, kernel, scores, workspace, hist, s);
   switch (dtype) {
     case HC_DTYPE_BF16: { HC_SCORE_DISPATCH(__bf16) }
     case HC_DTYPE_F16: { HC_SCORE_DISPATCH(_Float16) }

@@ -40,12 +40,6 @@ constexpr int kSelMaxChunks = 4096;
 constexpr int kSelMatch = 6;  // digits aggregated per wave before per-lane atomics
 constexpr int kSelSub = 1;    // LDS sub-histograms per wave (power of two)
 
-__device__ __forceinline__ uint32_t order_key(float f) {
-  uint32_t u = __float_as_uint(f);
-  if (u == 0x80000000u) u = 0u;  // -0 ranks equal to +0
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
 struct SelJob {
   int body;  // positions selected from [0, span)
   int tail;  // window positions appended
@@ -320,60 +314,6 @@ __global__ __launch_bounds__(kSelThreads) void select_write_kernel(const float* 
   }
 }
 
-// Ties of tau in the chunks before `chunk` (from the count kernel's
-// per-chunk counts).
-__device__ __forceinline__ int ties_before(const int* __restrict__ cnt, int job, int chunk, int nchunks) {
-  int eq = 0;
-  for (int c = 0; c < chunk; ++c) eq += cnt[((int64_t)job * nchunks + c) * 2 + 1];
-  return eq;
-}
-
-// Keep masks of one chunk: selm[r] is, per wave, the ballot over positions
-// t0 + r*256 + 64*wave + lane of "kept" -- the key is above tau, or equals it
-// and ranks below need_eq among the ties in position order (eq_before ties
-// in earlier chunks).  Reached by the whole workgroup.
-__device__ __forceinline__ void chunk_keep_masks(const float* __restrict__ s, int span, int t0, uint32_t tau,
-                                                 int need_eq, bool all_ties, int eq_before,
-                                                 uint64_t (&selm)[kSelRows], int (*s_cnt)[kSelWaves],
-                                                 int (*s_off)[kSelWaves]) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  uint32_t keys[kSelRows];
-#pragma unroll
-  for (int r = 0; r < kSelRows; ++r) {
-    const int t = t0 + r * kSelThreads + tid;
-    keys[r] = t < span ? order_key(s[t]) : 0u;
-  }
-  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  uint64_t eqm[kSelRows];
-#pragma unroll
-  for (int r = 0; r < kSelRows; ++r) {
-    const int t = t0 + r * kSelThreads + tid;
-    eqm[r] = __ballot(t < span && keys[r] == tau);
-    if (lane == 0) s_cnt[r][wave] = __popcll(eqm[r]);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int e = eq_before;
-    for (int r = 0; r < kSelRows; ++r)
-      for (int w = 0; w < kSelWaves; ++w) {
-        s_off[r][w] = e;
-        e += s_cnt[r][w];
-      }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < kSelRows; ++r) {
-    const int t = t0 + r * kSelThreads + tid;
-    bool take = t < span && keys[r] > tau;
-    if (t < span && keys[r] == tau) {
-      const int rank = s_off[r][wave] + __popcll(eqm[r] & below);
-      take = all_ties || rank < need_eq;
-    }
-    selm[r] = __ballot(take);
-  }
-  __syncthreads();
-}
-
 // 64 bits of a bitmask set starting at a multiple-of-64 position.
 __device__ __forceinline__ uint64_t bits64(const uint32_t* __restrict__ b, int64_t words, int pos) {
   const int64_t w = pos >> 5;
@@ -381,84 +321,379 @@ __device__ __forceinline__ uint64_t bits64(const uint32_t* __restrict__ b, int64
   return lo | (hi << 32);
 }
 
-// out[job] += |kept(job) ∩ set(job / steps)| over this chunk (out zeroed by
-// the count kernel).  Chunk 0 clears the job's histograms for the next call.
-__global__ __launch_bounds__(kSelThreads) void select_overlap_kernel(
-    const float* __restrict__ scores, int64_t score_stride, int span, const int32_t* __restrict__ caps,
-    unsigned* __restrict__ ghist, const int* __restrict__ state, const int* __restrict__ cnt, int nchunks,
-    const uint32_t* __restrict__ bits, int64_t words, int steps, int32_t* __restrict__ out) {
-  const int job = blockIdx.y, chunk = blockIdx.x;
+// ---------------------------------------------------------------------------
+// Drift selection (hc_drift_select).  The scorer left per step row a
+// histogram of the top kKeyDigitBits bits of its scores' keys, so:
+//  pick     the bin b* holding the K-th largest key and how many of the bin
+//           are still to keep (k);
+//  compact  one pass over the scores, chunk by chunk: keys above b* are kept
+//           (the chunk's reference-set hits are counted), keys in b* are the
+//           chunk's candidates (key, position), written to the chunk's own
+//           segment -- no global atomics;
+//  resolve  per row, a radix over the candidates' remaining key bits gives
+//           the exact threshold tau and how many of its ties to keep, and a
+//           radix over the ties' positions the cut pcut (the lowest
+//           positions win); kept candidates add their hits;
+//  decide   median of the batch-mean overlaps < threshold;
+//  bits     triggered sets := keys > tau, or == tau at positions <= pcut.
+// ---------------------------------------------------------------------------
+enum DriftMode { kDriftNone = 0, kDriftAll = 1, kDriftPartial = 2 };
+
+static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+static int drift_chunks(int span) { return (span + kSelChunk - 1) / kSelChunk; }
+// state [njobs][4], thresholds [njobs][4], per-chunk (candidates, hits) [njobs][nchunks][2]
+static size_t drift_head_bytes(int njobs, int span) {
+  return align256((size_t)njobs * 8 * sizeof(int) + (size_t)njobs * drift_chunks(span) * 2 * sizeof(int));
+}
+static size_t drift_cand_bytes(int njobs, int span) {
+  return (size_t)njobs * drift_chunks(span) * kSelChunk * sizeof(uint2);
+}
+static size_t drift_hist_bytes(int njobs) { return (size_t)njobs * kKeyDigitBins * sizeof(uint32_t); }
+
+// [head][candidate segments][histograms, used when the caller brings none]
+size_t drift_scratch_bytes(int njobs, int span) {
+  return drift_head_bytes(njobs, span) + drift_cand_bytes(njobs, span) + drift_hist_bytes(njobs);
+}
+
+// First-digit key histogram of one score row per workgroup, for callers whose
+// scorer did not build it.
+__global__ __launch_bounds__(1024) void drift_hist_kernel(const float* __restrict__ scores, int64_t score_stride,
+                                                          int span, uint32_t* __restrict__ hist) {
+  __shared__ uint32_t h[kKeyDigitBins];
+  for (int b = threadIdx.x; b < kKeyDigitBins; b += 1024) h[b] = 0u;
+  __syncthreads();
+  const float* s = scores + (int64_t)blockIdx.x * score_stride;
+  for (int t = threadIdx.x; t < span; t += 1024) atomicAdd(&h[order_key(s[t]) >> kKeyDigitShift], 1u);
+  __syncthreads();
+  uint32_t* o = hist + (int64_t)blockIdx.x * kKeyDigitBins;
+  for (int b = threadIdx.x; b < kKeyDigitBins; b += 1024) o[b] = h[b];
+}
+
+// Inclusive prefix sum of one value per thread across a workgroup of NT.
+template <int NT>
+__device__ __forceinline__ int block_inclusive_scan(int v, int* s_tmp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int u = __shfl_up(v, d, 64);
+    if (lane >= d) v += u;
+  }
+  if (lane == 63) s_tmp[wave] = v;
+  __syncthreads();
+  int add = 0;
+  for (int w = 0; w < wave; ++w) add += s_tmp[w];
+  __syncthreads();
+  return v + add;
+}
+
+// The bin of an NBINS histogram where the count, accumulated in scan order
+// (descending bins when desc), reaches k (1 <= k <= total): s_out = {bin,
+// k - count before the bin}.  Reached by the whole workgroup.
+template <int NT, int NBINS>
+__device__ __forceinline__ void block_find_bin(const uint32_t* h, int k, bool desc, int* s_tmp, int* s_out) {
+  constexpr int BPT = NBINS / NT;
+  static_assert(BPT * NT == NBINS, "bins must split evenly over the threads");
+  if (threadIdx.x == 0) {  // stays {0, 0} if the histogram holds fewer than k
+    s_out[0] = 0;
+    s_out[1] = 0;
+  }
+  int c[BPT], sum = 0;
+#pragma unroll
+  for (int i = 0; i < BPT; ++i) {
+    const int pos = threadIdx.x * BPT + i;
+    c[i] = (int)h[desc ? NBINS - 1 - pos : pos];
+    sum += c[i];
+  }
+  const int incl = block_inclusive_scan<NT>(sum, s_tmp);
+  int before = incl - sum;
+  if (before < k && incl >= k) {
+#pragma unroll
+    for (int i = 0; i < BPT; ++i) {
+      if (before < k && before + c[i] >= k) {
+        const int pos = threadIdx.x * BPT + i;
+        s_out[0] = desc ? NBINS - 1 - pos : pos;
+        s_out[1] = k - before;
+      }
+      before += c[i];
+    }
+  }
+  __syncthreads();
+}
+
+// state[job] = {b*, k, mode}.
+__global__ __launch_bounds__(256) void drift_pick_kernel(const uint32_t* __restrict__ hist,
+                                                         const int32_t* __restrict__ caps, int span,
+                                                         int* __restrict__ state) {
+  const int job = blockIdx.x;
+  __shared__ int s_tmp[4], s_out[2];
+  const int K = max(0, min((int)caps[job], span));
+  int* st = state + job * 4;
+  if (K == 0 || K >= span) {
+    if (threadIdx.x == 0) {
+      st[0] = 0;
+      st[1] = 0;
+      st[2] = K == 0 ? kDriftNone : kDriftAll;
+    }
+    return;
+  }
+  block_find_bin<256, kKeyDigitBins>(hist + (int64_t)job * kKeyDigitBins, K, true, s_tmp, s_out);
+  if (threadIdx.x == 0) {
+    st[0] = s_out[0];
+    st[1] = s_out[1];
+    st[2] = kDriftPartial;
+  }
+}
+
+// One chunk of one step row: its hits of the keys above b* against the row's
+// reference set, and its keys in b* as candidates (key, position) in the
+// chunk's segment; chunk_info[job][chunk] = {candidates, hits}.
+__global__ __launch_bounds__(kSelThreads) void drift_compact_kernel(
+    const float* __restrict__ scores, int64_t score_stride, int span, const int* __restrict__ state,
+    const uint32_t* __restrict__ bits, int64_t words, int steps, int* __restrict__ chunk_info,
+    uint2* __restrict__ cand, int64_t cand_stride) {
+  const int job = blockIdx.y, chunk = blockIdx.x, nchunks = gridDim.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const SelJob jb = sel_job(caps, job, span, 0, span);
-  if (chunk == 0)
-    for (int i = tid; i < 4 * kSelBins; i += kSelThreads) ghist[(int64_t)job * 4 * kSelBins + i] = 0u;
-  if (jb.body <= 0) return;
-  __shared__ int s_eq;
-  __shared__ int s_cnt[kSelRows][kSelWaves];
-  __shared__ int s_off[kSelRows][kSelWaves];
-  __shared__ int s_sum[kSelWaves];
+  const int* st = state + job * 4;
+  const int mode = st[2];
+  if (mode == kDriftNone) return;
+  const uint32_t bstar = (uint32_t)st[0];
+  const float* s = scores + (int64_t)job * score_stride;
   const uint32_t* ref = bits + (int64_t)(job / steps) * words;
   const int t0 = chunk * kSelChunk;
-  uint64_t selm[kSelRows];
-  if (jb.body >= span) {
-#pragma unroll
-    for (int r = 0; r < kSelRows; ++r) selm[r] = __ballot(t0 + r * kSelThreads + tid < span);
-  } else {
-    if (tid == 0) s_eq = ties_before(cnt, job, chunk, nchunks);
-    __syncthreads();
-    chunk_keep_masks(scores + (int64_t)job * score_stride, span, t0, (uint32_t)state[job * 4], state[job * 4 + 1],
-                     state[job * 4 + 2] != 0, s_eq, selm, s_cnt, s_off);
+  uint2* seg = cand + (int64_t)job * cand_stride + t0;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  constexpr int kWords = kSelChunk / 32;
+  __shared__ uint32_t s_ref[kWords];
+  __shared__ int s_cnt;
+  __shared__ int s_sum[kSelWaves];
+  if (tid == 0) s_cnt = 0;
+  for (int w = tid; w < kWords; w += kSelThreads) {
+    const int64_t gw = (int64_t)(t0 >> 5) + w;
+    s_ref[w] = gw < words ? ref[gw] : 0u;
   }
-  int c = 0;
-  if (lane == 0) {
+  float v[kSelRows];
 #pragma unroll
-    for (int r = 0; r < kSelRows; ++r) c += __popcll(selm[r] & bits64(ref, words, t0 + r * kSelThreads + 64 * wave));
-    s_sum[wave] = c;
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + tid;
+    v[r] = t < span ? s[t] : 0.f;
   }
+  __syncthreads();
+  // Per row: the wave's hits above b* and its candidate ballot; then one
+  // LDS reservation per wave for all rows' candidates.
+  int hits = 0, ncand = 0;
+  uint64_t mc[kSelRows];
+  uint32_t keys[kSelRows];
+#pragma unroll
+  for (int r = 0; r < kSelRows; ++r) {
+    const int wb = r * kSelThreads + 64 * wave;  // chunk-local position of the wave's lane 0
+    const bool valid = t0 + wb + lane < span;
+    keys[r] = order_key(v[r]);
+    const uint32_t d = keys[r] >> kKeyDigitShift;
+    const uint64_t mh = __ballot(valid && (mode == kDriftAll || d > bstar));
+    const uint64_t rb = (uint64_t)s_ref[wb >> 5] | ((uint64_t)s_ref[(wb >> 5) + 1] << 32);
+    hits += __popcll(mh & rb);
+    mc[r] = __ballot(valid && mode == kDriftPartial && d == bstar);
+    ncand += __popcll(mc[r]);
+  }
+  if (ncand) {
+    int base = 0;
+    if (lane == 0) base = atomicAdd(&s_cnt, ncand);
+    base = __shfl(base, 0, 64);
+#pragma unroll
+    for (int r = 0; r < kSelRows; ++r) {
+      if ((mc[r] >> lane) & 1ull)
+        seg[base + __popcll(mc[r] & below)] = make_uint2(keys[r], (uint32_t)(t0 + r * kSelThreads + 64 * wave + lane));
+      base += __popcll(mc[r]);
+    }
+  }
+  if (lane == 0) s_sum[wave] = hits;
   __syncthreads();
   if (tid == 0) {
     int tot = 0;
     for (int w = 0; w < kSelWaves; ++w) tot += s_sum[w];
-    if (tot) atomicAdd(out + job, tot);
+    int* ci = chunk_info + ((int64_t)job * nchunks + chunk) * 2;
+    ci[0] = s_cnt;
+    ci[1] = tot;
   }
 }
 
-// Set j := kept(job j*steps + steps-1) as a bitmask, for sets whose leader
+constexpr int kResolveThreads = 1024;
+constexpr int kResolveRegs = 16;  // candidates per thread kept in registers
+
+// Candidate i of a row whose chunk segments start at s_pref (exclusive
+// prefix of the chunk counts, s_pref[nchunks] = total).
+__device__ __forceinline__ uint2 cand_at(const uint2* __restrict__ c, const int* s_pref, int nchunks, int i) {
+  int lo = 0, hi = nchunks - 1;  // last chunk whose prefix is <= i
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= i) lo = mid; else hi = mid - 1;
+  }
+  return c[(int64_t)lo * kSelChunk + (i - s_pref[lo])];
+}
+
+// thr[job] = {tau, pcut, mode}: kept = key > tau, or key == tau at a
+// position <= pcut; overlap[job] = the chunks' hits + the kept candidates'.
+__global__ __launch_bounds__(kResolveThreads) void drift_resolve_kernel(
+    const int* __restrict__ state, const int* __restrict__ chunk_info, int nchunks, const uint2* __restrict__ cand,
+    int64_t cand_stride, const uint32_t* __restrict__ bits, int64_t words, int steps, int32_t* __restrict__ overlap,
+    int* __restrict__ thr) {
+  const int job = blockIdx.x, tid = threadIdx.x;
+  const int* st = state + job * 4;
+  int* th = thr + job * 4;
+  const int mode = st[2];
+  __shared__ uint32_t h[2048];
+  __shared__ int s_pref[kSelMaxChunks + 1];
+  __shared__ int s_tmp[kResolveThreads / 64], s_out[2];
+  if (mode == kDriftNone) {
+    if (tid == 0) {
+      th[0] = 0;
+      th[1] = -1;
+      th[2] = kDriftNone;
+      overlap[job] = 0;
+    }
+    return;
+  }
+  // Chunk prefix of the candidate counts and the sum of the chunks' hits.
+  const int* ci = chunk_info + (int64_t)job * nchunks * 2;
+  int n = 0, hits = 0;
+  for (int base = 0; base < nchunks; base += kResolveThreads) {
+    const int ch = base + tid;
+    const int cnt = ch < nchunks ? ci[2 * ch] : 0;
+    if (ch < nchunks) hits += ci[2 * ch + 1];
+    const int incl = block_inclusive_scan<kResolveThreads>(cnt, s_tmp);
+    if (ch < nchunks) s_pref[ch] = n + incl - cnt;
+    if (tid == kResolveThreads - 1) s_out[0] = incl;  // the block's total
+    __syncthreads();
+    n += s_out[0];
+    __syncthreads();
+  }
+  if (tid == 0) s_pref[nchunks] = n;
+  const uint2* c = cand + (int64_t)job * cand_stride;
+  const uint32_t* ref = bits + (int64_t)(job / steps) * words;
+  uint32_t tau = 0;
+  int pcut = mode == kDriftAll ? INT_MAX : -1;
+  __syncthreads();
+  if (mode == kDriftPartial) {
+    const uint32_t bstar = (uint32_t)st[0];
+    int k = st[1];
+    // The first kResolveRegs * kResolveThreads candidates stay in registers
+    // for all the passes below; any beyond are re-read each pass.
+    uint2 rc[kResolveRegs];
+#pragma unroll
+    for (int u = 0; u < kResolveRegs; ++u) {
+      const int i = tid + u * kResolveThreads;
+      rc[u] = i < n ? cand_at(c, s_pref, nchunks, i) : make_uint2(0u, 0u);
+    }
+    auto visit = [&](auto&& f) {
+#pragma unroll
+      for (int u = 0; u < kResolveRegs; ++u)
+        if (tid + u * kResolveThreads < n) f(rc[u]);
+      for (int i = tid + kResolveRegs * kResolveThreads; i < n; i += kResolveThreads) f(cand_at(c, s_pref, nchunks, i));
+    };
+    // Key bits [19:10], then [9:0] within the chosen bin.
+    for (int b = tid; b < 1024; b += kResolveThreads) h[b] = 0u;
+    __syncthreads();
+    visit([&](uint2 x) { atomicAdd(&h[(x.x >> 10) & 1023u], 1u); });
+    __syncthreads();
+    block_find_bin<kResolveThreads, 1024>(h, k, true, s_tmp, s_out);
+    const uint32_t ba = (uint32_t)s_out[0];
+    k = s_out[1];
+    for (int b = tid; b < 1024; b += kResolveThreads) h[b] = 0u;
+    __syncthreads();
+    visit([&](uint2 x) {
+      if (((x.x >> 10) & 1023u) == ba) atomicAdd(&h[x.x & 1023u], 1u);
+    });
+    __syncthreads();
+    block_find_bin<kResolveThreads, 1024>(h, k, true, s_tmp, s_out);
+    const uint32_t bb = (uint32_t)s_out[0];
+    k = s_out[1];
+    tau = (bstar << kKeyDigitShift) | (ba << 10) | bb;
+    const int n_eq = (int)h[bb];
+    __syncthreads();
+    pcut = INT_MAX;
+    if (k < n_eq) {
+      // The k lowest positions among the keys equal to tau: position bits
+      // [30:20], [19:10], [9:0], ascending.
+      uint32_t pref = 0;  // position bits found so far
+      for (int lv = 0; lv < 3; ++lv) {
+        const int shift = lv == 0 ? 20 : (lv == 1 ? 10 : 0);
+        const int nb = lv == 0 ? 2048 : 1024;
+        for (int b = tid; b < nb; b += kResolveThreads) h[b] = 0u;
+        __syncthreads();
+        visit([&](uint2 x) {
+          if (x.x == tau && (lv == 0 || (x.y >> (shift + 10)) == pref))
+            atomicAdd(&h[(x.y >> shift) & (uint32_t)(nb - 1)], 1u);
+        });
+        __syncthreads();
+        if (lv == 0)
+          block_find_bin<kResolveThreads, 2048>(h, k, false, s_tmp, s_out);
+        else
+          block_find_bin<kResolveThreads, 1024>(h, k, false, s_tmp, s_out);
+        pref = lv == 0 ? (uint32_t)s_out[0] : (pref << 10) | (uint32_t)s_out[0];
+        k = s_out[1];
+        __syncthreads();
+      }
+      pcut = (int)pref;
+    }
+    visit([&](uint2 x) {
+      const int pos = (int)x.y;
+      if ((x.x > tau || (x.x == tau && pos <= pcut)) && ((ref[pos >> 5] >> (pos & 31)) & 1u)) ++hits;
+    });
+  }
+  if (tid == 0) {
+    th[0] = (int)tau;
+    th[1] = pcut;
+    th[2] = mode;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) hits += __shfl_xor(hits, off, 64);
+  if ((tid & 63) == 0) s_tmp[tid >> 6] = hits;
+  __syncthreads();
+  if (tid == 0) {
+    int tot = 0;
+    for (int w = 0; w < kResolveThreads / 64; ++w) tot += s_tmp[w];
+    overlap[job] = tot;
+  }
+}
+
+// Set j := the kept positions of its last step row, for sets whose leader
 // triggered (trigger[trig_of[j]] != 0); other sets are left as they are.
-// Each workgroup writes the words of its chunk (and chunk 0 any words past
-// the last chunk), so no set needs clearing first.
-__global__ __launch_bounds__(kSelThreads) void select_bits_kernel(
-    const float* __restrict__ scores, int64_t score_stride, int span, const int32_t* __restrict__ caps,
-    const int* __restrict__ state, const int* __restrict__ cnt, int nchunks, uint32_t* __restrict__ bits,
-    int64_t words, int steps, const int32_t* __restrict__ trigger, const int32_t* __restrict__ trig_of) {
+// Each workgroup writes its chunk's words (chunk 0 also any words past the
+// last chunk), so no set needs clearing first.
+__global__ __launch_bounds__(kSelThreads) void drift_bits_kernel(
+    const float* __restrict__ scores, int64_t score_stride, int span, const int* __restrict__ thr,
+    uint32_t* __restrict__ bits, int64_t words, int steps, const int32_t* __restrict__ trigger,
+    const int32_t* __restrict__ trig_of, int nchunks) {
   const int set = blockIdx.y, chunk = blockIdx.x;
   if (trigger[trig_of ? trig_of[set] : set] == 0) return;
   const int job = set * steps + steps - 1;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const SelJob jb = sel_job(caps, job, span, 0, span);
+  const int* th = thr + job * 4;
+  const uint32_t tau = (uint32_t)th[0];
+  const int pcut = th[1], mode = th[2];
+  const float* s = scores + (int64_t)job * score_stride;
   uint32_t* out = bits + (int64_t)set * words;
   const int t0 = chunk * kSelChunk;
   if (chunk == 0)
     for (int64_t w = (int64_t)nchunks * (kSelChunk / 32) + tid; w < words; w += kSelThreads) out[w] = 0u;
-  __shared__ int s_eq;
-  __shared__ int s_cnt[kSelRows][kSelWaves];
-  __shared__ int s_off[kSelRows][kSelWaves];
-  uint64_t selm[kSelRows];
-  if (jb.body <= 0 || jb.body >= span) {
+  float v[kSelRows];
 #pragma unroll
-    for (int r = 0; r < kSelRows; ++r) selm[r] = __ballot(jb.body > 0 && t0 + r * kSelThreads + tid < span);
-  } else {
-    if (tid == 0) s_eq = ties_before(cnt, job, chunk, nchunks);
-    __syncthreads();
-    chunk_keep_masks(scores + (int64_t)job * score_stride, span, t0, (uint32_t)state[job * 4], state[job * 4 + 1],
-                     state[job * 4 + 2] != 0, s_eq, selm, s_cnt, s_off);
+  for (int r = 0; r < kSelRows; ++r) {
+    const int t = t0 + r * kSelThreads + tid;
+    v[r] = t < span ? s[t] : 0.f;
   }
-  if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < kSelRows; ++r) {
-      const int64_t w = (t0 + r * kSelThreads + 64 * wave) >> 5;
-      if (w < words) out[w] = (uint32_t)selm[r];
-      if (w + 1 < words) out[w + 1] = (uint32_t)(selm[r] >> 32);
+  for (int r = 0; r < kSelRows; ++r) {
+    const int tb = t0 + r * kSelThreads + 64 * wave;
+    const int t = tb + lane;
+    const uint32_t key = order_key(v[r]);
+    const bool keep = t < span && (mode == kDriftAll ||
+                                   (mode == kDriftPartial && (key > tau || (key == tau && t <= pcut))));
+    const uint64_t m = __ballot(keep);
+    if (lane == 0) {
+      const int64_t w = tb >> 5;
+      if (w < words) out[w] = (uint32_t)m;
+      if (w + 1 < words) out[w + 1] = (uint32_t)(m >> 32);
     }
   }
 }
@@ -525,10 +760,15 @@ extern "C" int hc_select_topk(const float* scores, int64_t score_stride, int njo
   return check_launch("hc_select_topk(write)");
 }
 
+extern "C" size_t hc_drift_scratch_size(int njobs, int span) {
+  if (njobs <= 0 || span <= 0) return 0;
+  return drift_scratch_bytes(njobs, span);
+}
+
 extern "C" int hc_drift_select(const float* scores, int64_t score_stride, int nsets, int steps, int batch, int span,
                                const int32_t* caps, int K, uint32_t* bits, int64_t words, const int32_t* trig_of,
-                               int nlead, double threshold, int32_t* overlap, int32_t* trigger, void* hist,
-                               size_t hist_bytes, void* scratch, size_t scratch_bytes, void* stream) {
+                               int nlead, double threshold, int32_t* overlap, int32_t* trigger, const uint32_t* hist,
+                               void* scratch, size_t scratch_bytes, void* stream) {
   clear_error();
   const int64_t njobs64 = (int64_t)nsets * steps;
   if (nsets < 0 || steps < 1 || steps > 64 || batch < 1 || span < 1 || K < 1 || njobs64 > 65535 ||
@@ -536,36 +776,40 @@ extern "C" int hc_drift_select(const float* scores, int64_t score_stride, int ns
     return set_error(HC_ERR_INVALID, "hc_drift_select: nsets=%d steps=%d batch=%d span=%d K=%d nlead=%d words=%lld",
                      nsets, steps, batch, span, K, nlead, (long long)words);
   if (nsets == 0) return HC_OK;
-  if (!scores || !caps || !bits || !overlap || !trigger || !hist || !scratch)
+  if (!scores || !caps || !bits || !overlap || !trigger || !scratch)
     return set_error(HC_ERR_INVALID, "hc_drift_select: null pointer argument");
   const int njobs = (int)njobs64;
   if (score_stride < span) return set_error(HC_ERR_INVALID, "hc_drift_select: score stride below the span");
-  const int nchunks = (span + kSelChunk - 1) / kSelChunk;
+  const int nchunks = drift_chunks(span);
   if (nchunks > kSelMaxChunks) return set_error(HC_ERR_INVALID, "hc_drift_select: span %d too long", span);
-  if (hist_bytes < select_hist_bytes(njobs) || scratch_bytes < select_scratch_bytes(njobs, span))
-    return set_error(HC_ERR_INVALID, "hc_drift_select: histogram or scratch buffer too small");
-  unsigned* ghist = reinterpret_cast<unsigned*>(hist);
+  if (scratch_bytes < drift_scratch_bytes(njobs, span))
+    return set_error(HC_ERR_INVALID, "hc_drift_select: scratch buffer too small (%zu < %zu bytes)", scratch_bytes,
+                     drift_scratch_bytes(njobs, span));
   int* state = reinterpret_cast<int*>(scratch);
-  int* cnt = state + (size_t)njobs * 4;
+  int* thr = state + (size_t)njobs * 4;
+  int* chunk_info = thr + (size_t)njobs * 4;
+  char* base = reinterpret_cast<char*>(scratch);
+  uint2* cand = reinterpret_cast<uint2*>(base + drift_head_bytes(njobs, span));
+  const int64_t cand_stride = (int64_t)nchunks * kSelChunk;
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(nchunks, njobs);
-  for (int pass = 0; pass < 4; ++pass) {
-    hipLaunchKernelGGL(select_hist_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, 0,
-                       (int64_t)span, ghist, pass);
-    int rc = check_launch("hc_drift_select(hist)");
-    if (rc) return rc;
+  int rc;
+  if (!hist) {
+    uint32_t* own = reinterpret_cast<uint32_t*>(base + drift_head_bytes(njobs, span) + drift_cand_bytes(njobs, span));
+    hipLaunchKernelGGL(drift_hist_kernel, dim3(njobs), dim3(1024), 0, s, scores, score_stride, span, own);
+    if ((rc = check_launch("hc_drift_select(hist)"))) return rc;
+    hist = own;
   }
-  hipLaunchKernelGGL(select_count_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, 0,
-                     (int64_t)span, ghist, state, cnt, (int32_t*)nullptr, nchunks, overlap);
-  int rc = check_launch("hc_drift_select(count)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(select_overlap_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, ghist,
-                     state, cnt, nchunks, bits, words, steps, overlap);
-  rc = check_launch("hc_drift_select(overlap)");
-  if (rc) return rc;
+  hipLaunchKernelGGL(drift_pick_kernel, dim3(njobs), dim3(256), 0, s, hist, caps, span, state);
+  if ((rc = check_launch("hc_drift_select(pick)"))) return rc;
+  hipLaunchKernelGGL(drift_compact_kernel, dim3(nchunks, njobs), dim3(kSelThreads), 0, s, scores, score_stride, span,
+                     state, bits, words, steps, chunk_info, cand, cand_stride);
+  if ((rc = check_launch("hc_drift_select(compact)"))) return rc;
+  hipLaunchKernelGGL(drift_resolve_kernel, dim3(njobs), dim3(kResolveThreads), 0, s, state, chunk_info, nchunks, cand,
+                     cand_stride, bits, words, steps, overlap, thr);
+  if ((rc = check_launch("hc_drift_select(resolve)"))) return rc;
   rc = hc_drift_decide(overlap, nlead, batch, steps, K, threshold, nullptr, nullptr, trigger, stream);
   if (rc) return rc;
-  hipLaunchKernelGGL(select_bits_kernel, dim3(nchunks, nsets), dim3(kSelThreads), 0, s, scores, score_stride, span,
-                     caps, state, cnt, nchunks, bits, words, steps, trigger, trig_of);
+  hipLaunchKernelGGL(drift_bits_kernel, dim3(nchunks, nsets), dim3(kSelThreads), 0, s, scores, score_stride, span,
+                     thr, bits, words, steps, trigger, trig_of, nchunks);
   return check_launch("hc_drift_select(bits)");
 }

@@ -82,6 +82,10 @@ class Workspace:
 WORKSPACE = Workspace()
 # hc_select_topk keeps self-clearing histograms in this buffer.
 SELECT_HIST = Workspace()
+# Bins of the first-digit key histogram hc_score builds for hc_drift_select,
+# and the query rows below which it can (the logit-store path).
+HIST_BINS = 4096
+HIST_MAX_ROWS = 31
 
 
 def _lens_i32(host_row_len):
@@ -395,12 +399,14 @@ def store_read(kstore, vstore, row_tile_off, rows_sel, count, stream=None):
 
 
 def score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, seq_len, group, window, span, pooling,
-          kernel, scale, flags=0, row_tile_off=None, k_row=None, out=None, stream=None):
+          kernel, scale, flags=0, row_tile_off=None, k_row=None, out=None, hist=None, stream=None):
     """Pooled window scores [jobs, W', span] (see hc_score in include/hc.h).
 
     q / k are the base tensors; q_off / k_off are int64 device tensors of
     per-job element offsets (k_off unused when reading a tiled store through
-    row_tile_off / k_row).
+    row_tile_off / k_row).  hist: optional uint32-sized int32 tensor of
+    [jobs * W', HIST_BINS] that receives each score row's first-digit key
+    histogram (for drift_select).
     """
     lib = _lib.load()
     _require_cuda(q, k, q_off, k_off, row_tile_off, k_row)
@@ -416,13 +422,17 @@ def score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, seq_len
         raise TypeError("offsets must be int64")
     if k_row is not None and k_row.dtype != torch.int32:
         raise TypeError("k_row must be int32")
+    if hist is not None:
+        _require_cuda(hist)
+        if hist.dtype != torch.int32 or not hist.is_contiguous() or hist.numel() < njobs * wout * HIST_BINS:
+            raise ValueError(f"hist must be a contiguous int32 tensor of [jobs * W', {HIST_BINS}]")
     nbytes = lib.hc_score_workspace_size(njobs, seq_len, group, window, flags)
     ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=q.device)
     pool = {"avgpool": 0, "maxpool": 1}[pooling] if isinstance(pooling, str) else int(pooling)
     _lib.check(lib.hc_score(dtype_code(q.dtype), _ptr(q), _ptr(q_off), int(q_head_stride), int(q_row_stride), _ptr(k),
                             _ptr(k_off), int(k_tok_stride), _ptr(row_tile_off), _ptr(k_row), njobs, int(seq_len),
                             int(group), int(window), int(flags), int(span), pool, int(kernel), float(scale),
-                            _ptr(out), _ptr(ws), ws.numel(), _stream(stream, q)))
+                            _ptr(out), _ptr(ws), ws.numel(), _ptr(hist), _stream(stream, q)))
     return out
 
 
@@ -477,19 +487,21 @@ def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None
     return idx, counts
 
 
-def drift_select(scores, caps, K, bits, nbits, trig_of, nlead, batch, steps, threshold, trigger, overlap=None,
+def drift_select(scores, caps, K, bits, nbits, trig_of, nlead, batch, steps, threshold, trigger, hist, overlap=None,
                  stream=None):
     """Drift decision of sets j = leader * batch + b from their step scores
-    (scores [sets * steps, >= nbits] float32, row j * steps + s): per step the
-    overlap of its top-K with bits[j] (out: overlap [sets * steps] int32),
+    (scores [sets * steps, >= nbits] float32, row j * steps + s, with the
+    first-digit key histograms `hist` that score() built for them, or None
+    to build them here): per step
+    the overlap of its top-K with bits[j] (out: overlap [sets * steps] int32),
     trigger[leader] = median over steps of the batch-mean overlap / K <
     threshold, and bits[j] := top-K of the last step where trigger[trig_of[j]]."""
     lib = _lib.load()
-    _require_cuda(scores, caps, bits, trig_of, trigger, overlap)
+    _require_cuda(scores, caps, bits, trig_of, trigger, overlap, hist)
     if scores.dtype != torch.float32 or scores.dim() != 2 or scores.stride(1) != 1:
         raise ValueError("scores must be float32 [jobs, n] with unit stride")
-    for name, t in (("caps", caps), ("bits", bits), ("trig_of", trig_of), ("trigger", trigger)):
-        if t.dtype != torch.int32:
+    for name, t in (("caps", caps), ("bits", bits), ("trig_of", trig_of), ("trigger", trigger), ("hist", hist)):
+        if t is not None and t.dtype != torch.int32:
             raise TypeError(f"{name} must be int32")
     njobs = scores.shape[0]
     if njobs % steps or caps.numel() < njobs:
@@ -497,15 +509,16 @@ def drift_select(scores, caps, K, bits, nbits, trig_of, nlead, batch, steps, thr
     nsets = njobs // steps
     if bits.dim() != 2 or bits.shape[0] < nsets or trig_of.numel() < nsets:
         raise ValueError("one bitmask set and one leader index per set")
+    if hist is not None and (not hist.is_contiguous() or hist.numel() < njobs * HIST_BINS):
+        raise ValueError(f"hist must be a contiguous int32 tensor of [jobs, {HIST_BINS}]")
     if overlap is None:
         overlap = torch.empty(njobs, dtype=torch.int32, device=scores.device)
-    hist = SELECT_HIST.get(scores.device, lib.hc_select_hist_size(njobs))
-    scratch = torch.empty(max(lib.hc_select_scratch_size(njobs, int(nbits)), 16), dtype=torch.uint8,
+    scratch = torch.empty(max(lib.hc_drift_scratch_size(njobs, int(nbits)), 16), dtype=torch.uint8,
                           device=scores.device)
     _lib.check(lib.hc_drift_select(_ptr(scores), scores.stride(0), nsets, int(steps), int(batch), int(nbits),
                                    _ptr(caps), int(K), _ptr(bits), bits.stride(0), _ptr(trig_of), int(nlead),
-                                   float(threshold), _ptr(overlap), _ptr(trigger), _ptr(hist), hist.numel(),
-                                   _ptr(scratch), scratch.numel(), _stream(stream, scores)))
+                                   float(threshold), _ptr(overlap), _ptr(trigger), _ptr(hist), _ptr(scratch),
+                                   scratch.numel(), _stream(stream, scores)))
     return overlap
 
 

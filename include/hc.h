@@ -242,15 +242,20 @@ int hc_head_pool(int dtype, const void* attn, int64_t batch_stride, int64_t head
  * when row_tile_off != NULL, slots [0, seq_len) of store row k_row[j] of the
  * tiled store k (read in place).  pooling: 0 = avg_pool1d (zero padding,
  * divisor kernel), 1 = max_pool1d (-inf padding); odd kernel, padding kernel/2.
- * scores: [njobs][W' ][span] float32.  Replaces the scoring op sequences of
- * HeteroCache.prefill_select (heterocache/cache_utils.py:807-829),
- * init_coefficient (:1158-1187), decode_select (:1030-1057) and
- * SnapKVCluster.update_kv (heterocache/kv_cluster.py:165-185).
+ * scores: [njobs][W' ][span] float32.  hist (optional, fewer than 32 query
+ * rows, no accumulation): per output row (job, w') 4096 uint32 bins counting
+ * the scores by the top 12 bits of their order-preserving keys -- the
+ * first digit hc_drift_select selects on; the call zeroes it first.
+ * Replaces the scoring op sequences of HeteroCache.prefill_select
+ * (heterocache/cache_utils.py:807-829), init_coefficient (:1158-1187),
+ * decode_select (:1030-1057) and SnapKVCluster.update_kv
+ * (heterocache/kv_cluster.py:165-185).
  */
 int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride, int64_t q_row_stride,
              const void* k, const int64_t* k_off, int64_t k_tok_stride, const int64_t* row_tile_off,
              const int32_t* k_row, int njobs, int seq_len, int group, int window, int flags, int span, int pooling,
-             int kernel, float scale, float* scores, void* workspace, size_t workspace_bytes, void* stream);
+             int kernel, float scale, float* scores, void* workspace, size_t workspace_bytes, uint32_t* hist,
+             void* stream);
 size_t hc_score_workspace_size(int njobs, int seq_len, int group, int window, int flags);
 
 /*
@@ -327,15 +332,21 @@ int hc_overlap_count(const int32_t* idx, int64_t idx_stride, int count, int nlis
  * threshold), and finally, for every set whose leader triggered
  * (trigger[trig_of[j]]), rewrites set j as top_K of its last step.  Replaces
  * the topk + sort + searchsorted + median + set update of
- * heterocache/cache_utils.py:1059-1082 (hc_select_topk + hc_overlap_count +
- * hc_drift_decide + hc_set_bits in one pass structure that never writes the
- * K-long index lists).  hist / scratch: as hc_select_topk for nsets*steps
- * jobs.
+ * heterocache/cache_utils.py:1059-1082 without writing the K-long index
+ * lists.  hist: the score histograms hc_score built for these rows (its
+ * `hist` output, [nsets*steps][4096]), or NULL to have them built here with
+ * one more pass over the scores; from them one pass over the scores counts
+ * the overlap above each row's threshold bin and collects the bin's
+ * positions, and a per-row radix over those candidates fixes the exact
+ * threshold and tie cut (ties of the threshold: lowest positions first).
+ * scratch: hc_drift_scratch_size(nsets*steps, span) bytes, no
+ * initialisation.
  */
 int hc_drift_select(const float* scores, int64_t score_stride, int nsets, int steps, int batch, int span,
                     const int32_t* caps, int K, uint32_t* bits, int64_t words, const int32_t* trig_of, int nlead,
-                    double threshold, int32_t* overlap, int32_t* trigger, void* hist, size_t hist_bytes,
-                    void* scratch, size_t scratch_bytes, void* stream);
+                    double threshold, int32_t* overlap, int32_t* trigger, const uint32_t* hist, void* scratch,
+                    size_t scratch_bytes, void* stream);
+size_t hc_drift_scratch_size(int njobs, int span);
 
 /*
  * counts: [npiv][batch][steps] overlap counts of top-K sets.  Per pivot:
