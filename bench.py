@@ -236,13 +236,17 @@ def full_step_phase(args, torch, dev):
         trig = cache._trigger_all
         triggered = torch.zeros_like(trig)
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+        main, checks_on = torch.cuda.current_stream(dev), cache.drift_stream(dev)
         t0 = time.perf_counter()
         for i in range(steps):
             ev[i][0].record()
             decode_step(S + i)
+            if i == steps - 1:
+                main.wait_stream(checks_on)  # the last check's work counts in the last step
             ev[i][1].record()
             if (S + i + 1) % S == 0:
-                triggered += trig      # device-side count of triggered leaders
+                with torch.cuda.stream(checks_on):
+                    triggered += trig  # device-side count of triggered leaders, ordered after the check
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3 / steps
         step_ms = [a.elapsed_time(b) for a, b in ev]

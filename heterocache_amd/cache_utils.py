@@ -61,6 +61,12 @@ class HeteroCacheConfig:
     step, so the outputs are unchanged).  drift_check_groups: number of
     contiguous layer groups checked separately (1 = all layers after the
     last one; more groups start the early groups' retrieval sooner).
+    overlap_drift_check: run each group's batched check and retrieval on a
+    side stream, overlapping the attention of the layers outside the group;
+    the group's layers wait for it before their next attention.  Off by
+    default: the check and decode attention are both HBM-bound, so on their
+    own they gain nothing from running together; it pays where the rest of
+    the model leaves HBM bandwidth idle.
     tier_placement: where the satellites' full-KV tier lives when
     real_offload is set -- "host" (pinned host memory, retrieval read over
     the host link), "device" (an HBM arena, retrieval a device gather) or
@@ -77,7 +83,7 @@ class HeteroCacheConfig:
                  num_layers: Optional[int] = 32, retrieval_topk: Optional[int] = None, window_size: int = 1,
                  round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None,
                  batched_drift_check: bool = True, drift_check_groups: int = 1, tier_placement: str = "auto",
-                 tier_device_budget: Optional[int] = None):
+                 tier_device_budget: Optional[int] = None, overlap_drift_check: bool = False):
         self.data = data
         self.stable_threshold = stable_threshold
         self.compression_ratio = compression_ratio
@@ -101,6 +107,7 @@ class HeteroCacheConfig:
             raise ValueError(f"tier_placement must be 'auto', 'host' or 'device', not {tier_placement!r}")
         self.tier_placement = tier_placement
         self.tier_device_budget = tier_device_budget
+        self.overlap_drift_check = overlap_drift_check
 
 
 def _f32_caps(base, ratios, seq_len):
@@ -158,6 +165,8 @@ class HeteroCache(DynamicCache):
         self.round_scores = bool(getattr(cfg, "round_scores", False))
         self.chunk_tiles = getattr(cfg, "chunk_tiles", None)
         self.batched_check = bool(getattr(cfg, "batched_drift_check", True))
+        self.overlap_check = bool(getattr(cfg, "overlap_drift_check", False))
+        self._side_shared = set()   # data pointers of device buffers already recorded on the side stream
         ngroups = max(1, min(int(getattr(cfg, "drift_check_groups", 1) or 1), self.num_layers))
         # Last layer of each check group (contiguous layer ranges).
         self._group_end = {((g + 1) * self.num_layers) // ngroups - 1 for g in range(ngroups)}
@@ -281,6 +290,23 @@ class HeteroCache(DynamicCache):
         if self._side is None:
             self._side = torch.cuda.Stream(device=device)
         return self._side
+
+    def drift_stream(self, device):
+        """The stream the batched drift checks and their retrieval run on: the
+        trigger flags, reference sets and retrieved rows are ordered on it
+        (the main stream when checks do not overlap)."""
+        if self.overlap_check or self.tier_mode == "host":
+            return self._side_stream(device)
+        return torch.cuda.current_stream(device)
+
+    def _share_with_side(self, side, tensors):
+        """Record device buffers allocated on the main stream as used by the
+        side stream, so that their memory is not handed out again while side
+        work on them is still queued."""
+        for t in tensors:
+            if torch.is_tensor(t) and t.is_cuda and t.data_ptr() not in self._side_shared:
+                t.record_stream(side)
+                self._side_shared.add(t.data_ptr())
 
     def _layer_row_caps(self, layer_idx):
         """Row capacities for the whole lifetime (heterocache/cache_utils.py:693-766)."""
@@ -664,8 +690,9 @@ class HeteroCache(DynamicCache):
         """Drift checks of a group of leader layers in one launch sequence: scores
         of every (layer, leader, batch) row read in place from the shared
         arena, one selection, overlap, decision and set update for all, one
-        retrieval selection; then the gated gathers layer by layer on the
-        side stream (each layer's event guards its next attention)."""
+        retrieval selection, then the gated gathers.  On the side stream
+        (overlap_drift_check or a host tier) the group's layers wait for it
+        at their next attention through _retrieval_done."""
         key = tuple(layers)
         bm = self._batch_meta.get(key)
         if bm is None:
@@ -678,43 +705,51 @@ class HeteroCache(DynamicCache):
         trig = self._trigger_all[gl0:gl0 + nlead]
         bits = self._ref_bits_all[gl0 * B:(gl0 + nlead) * B]
         flags = compress.ROUND_FLAGS[self._round_dtype(qa.dtype)]
-        scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,
-                           self.pooling, self.kernel_size, 1.0 / math.sqrt(self.head_dim), flags=flags,
-                           row_tile_off=self._tile_table, k_row=bm["k_row"], hist=bm["hist"]).view(J, S, L)
-        ops.drift_select(scores.view(J * S, L), bm["caps_K"], K, bits, L, bm["trig_of"], nlead, B, S,
-                         self.stable_threshold, trig, bm["hist"], overlap=bm["overlap"])
-        if bm["retrieve"]:
-            ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
-        if self.observer is not None:
-            self.observer("drift_check", row_ids=bm["row_ids"], scores=scores, overlap=bm["overlap"], trigger=trig,
-                          trig_of=bm["trig_of"], ret_idx=bm.get("ret_idx"), ret_counts=bm.get("ret_counts"))
-        if not bm["retrieve"]:
-            return
         dev = qa.device
         main = torch.cuda.current_stream(dev)
         host = self.tier_mode == "host"
-        side = self._side_stream(dev) if host else main
-        if host:
+        side = self._side_stream(dev) if (host or self.overlap_check) else main
+        if side is not main:
             side.wait_stream(main)
-        gp = bm["group_plan"]
+            self._share_with_side(side, [qa, self._arena[0], self._arena[1], self._tile_table, self._trigger_all,
+                                         self._ref_bits_all]
+                                  + ([] if self._tier is None else list(self._tier))
+                                  + [t for layer, _ in bm["plans"]
+                                     for t in (self.key_cache_cpu[layer], self.value_cache_cpu[layer])]
+                                  + [v for v in bm.values() if torch.is_tensor(v)]
+                                  + [v for v in (bm["group_plan"] or {}).values() if torch.is_tensor(v)])
         with torch.cuda.stream(side):
-            if gp is not None:
+            scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,
+                               self.pooling, self.kernel_size, 1.0 / math.sqrt(self.head_dim), flags=flags,
+                               row_tile_off=self._tile_table, k_row=bm["k_row"], hist=bm["hist"]).view(J, S, L)
+            ops.drift_select(scores.view(J * S, L), bm["caps_K"], K, bits, L, bm["trig_of"], nlead, B, S,
+                             self.stable_threshold, trig, bm["hist"], overlap=bm["overlap"])
+            if bm["retrieve"]:
+                ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
+            if self.observer is not None:
+                self.observer("drift_check", row_ids=bm["row_ids"], scores=scores, overlap=bm["overlap"],
+                              trigger=trig, trig_of=bm["trig_of"], ret_idx=bm.get("ret_idx"),
+                              ret_counts=bm.get("ret_counts"))
+            gp = bm["group_plan"]
+            if bm["retrieve"] and gp is not None:
                 # Every layer of the group in one launch from the tier arena.
                 tk, tv = self._tier
                 ops.gather_store(tk, tv, gp["src_off"], self.head_dim, L, bm["ret_idx"], gp["idx_off"], gp["counts"],
                                  gp["dst_row"], self._arena[0], self._arena[1], self._tile_table, gp["max_count"],
                                  src_is_host=host, trigger=trig, trig_of=gp["trig_of"], stream=side,
                                  max_workgroups=self.RETRIEVAL_WORKGROUPS if host else 0)
-                if host:
-                    ev = torch.cuda.Event()
-                    ev.record(side)
-                    for layer in gp["layers"]:
-                        self._retrieval_done[layer] = ev
-                return
-            for layer, plan in bm["plans"]:
-                kc, vc = self.key_cache_cpu[layer], self.value_cache_cpu[layer]
-                self.stores[layer].launch_rows(plan, kc, vc, idx=bm["ret_idx"], src_is_host=host, stream=side,
-                                               trigger=trig, set_len=False)
+            elif bm["retrieve"]:
+                for layer, plan in bm["plans"]:
+                    kc, vc = self.key_cache_cpu[layer], self.value_cache_cpu[layer]
+                    self.stores[layer].launch_rows(plan, kc, vc, idx=bm["ret_idx"], src_is_host=host, stream=side,
+                                                   trigger=trig, set_len=False)
+        if side is not main:
+            # The group's layers read the new sets and retrieved rows at their
+            # next attention; every other layer goes on meanwhile.
+            ev = torch.cuda.Event()
+            ev.record(side)
+            for layer in layers:
+                self._retrieval_done[layer] = ev
 
     def _batched_metadata(self, layers):
         """Device metadata of _check_batched; rows j follow the

@@ -42,9 +42,10 @@ def head_data(seed=0):
 
 
 def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True, groups=1,
-        chunks=None, tier="host"):
+        chunks=None, tier="host", overlap=False):
     """tier: "host" / "device" placement of the full-KV tier, or "prefill"
-    (real_offload=False: the prefill K/V kept as the tier)."""
+    (real_offload=False: the prefill K/V kept as the tier).  overlap: batched
+    checks on the side stream (overlap_drift_check)."""
     torch.manual_seed(0)
     B, Hq, Hkv, NL, D = 1, 32, 8, 2, 128
     data = head_data()
@@ -52,7 +53,7 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
                             max_gen_len=steps + 4, decode_step=5, pooling="avgpool", kernel_size=5,
                             num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=topk,
                             reference_quirks=quirks, batched_drift_check=batched, drift_check_groups=groups,
-                            tier_placement="host" if tier == "prefill" else tier)
+                            tier_placement="host" if tier == "prefill" else tier, overlap_drift_check=overlap)
     cache = HeteroCache(cfg)
     if chunks is not None:
         cache.begin_prefill(L)
@@ -97,7 +98,9 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
             err = np.abs(as_np(out).reshape(B, Hq, D) - ref).max()
             assert err <= tol, f"step {step} layer {layer}: max-abs {err}"
         if (step + 1) % 5 == 0:
-            # A deferred (batched) check has run once the last layer is done.
+            # A deferred (batched) check has run once the last layer is done
+            # (on the side stream when overlapped: wait for every stream).
+            torch.cuda.synchronize()
             for layer in range(NL):
                 st = cache._drift[layer]
                 for i, leader in enumerate(st.leaders):
@@ -127,6 +130,15 @@ def test_llama_order_two_check_groups(dev):
     """Each layer's check as its own batched group (the second group's
     leaders start past the first global leader)."""
     trig = run(dev, torch.float32, groups=2)
+    assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
+
+
+@pytest.mark.parametrize("groups,tier", [(1, "device"), (2, "device"), (1, "host")])
+def test_llama_order_overlapped_checks(dev, groups, tier):
+    """Batched checks and their retrieval on the side stream, overlapping the
+    other layers' attention (overlap_drift_check): every output, trigger and
+    store equals the oracle's, as on the main stream."""
+    trig = run(dev, torch.float32, groups=groups, tier=tier, overlap=True)
     assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
 
 
