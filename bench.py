@@ -43,12 +43,15 @@ def parse():
     p.add_argument("--drift-groups", type=int, default=None,
                    help="drift_check_groups of the HeteroCache phase (default: the config's default)")
     p.add_argument("--full-step-only", action="store_true", help="run only the HeteroCache full-step phase")
+    p.add_argument("--full-runs", default="natural,never,always,host_never,host_always",
+                   help="comma-separated runs of the full-step phase (natural, never, always, host_never, "
+                        "host_always)")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
     p.add_argument("--prefill-only", action="store_true",
                    help="run only the prefill-attention phase and print its figures (for counter profiling)")
     p.add_argument("--calibrate-copy", action="store_true",
-                   help="after the decode phase, run a 256 MiB fp32 streaming copy (negate) three times as the "
-                        "reference kernel for HBM counter calibration")
+                   help="after the decode (or full-step) phase, run a 256 MiB fp32 streaming copy (negate) three "
+                        "times as the reference kernel for HBM counter calibration")
     return p.parse_args()
 
 
@@ -179,6 +182,11 @@ def full_step_phase(args, torch, dev):
     # the 12.8 GB tier in HBM; the host-pinned tier is measured beside it.
     runs = (("natural", 0.5, args.full_steps, "auto"), ("never", -1.0, 100, "auto"), ("always", 2.0, 100, "auto"),
             ("host_never", -1.0, 100, "host"), ("host_always", 2.0, 100, "host"))
+    wanted = set(args.full_runs.split(","))
+    unknown = wanted - {r[0] for r in runs}
+    if unknown:
+        raise ValueError(f"unknown full-step runs: {sorted(unknown)}")
+    runs = tuple(r for r in runs if r[0] in wanted)
     nsteps = max(n for _, _, n, _ in runs) + S
     wl = workloads.NeedleWorkload(L, kv_heads=Hkv, group=G, steps=nsteps, decode_step=S, seed=args.seed, device=dev)
     npiv = sum(len(p) for p in data["need_to_select_counts"])
@@ -272,25 +280,31 @@ def full_step_phase(args, torch, dev):
         torch.cuda.empty_cache()
     tier_bytes = sats * L * D * 2 * 2  # satellites' full K and V
     per_check = sats * 1024 * D * 2 * 2
-    a = res["always"]
-    return {"workload": "reference Llama-3.1-8B head JSON (33 pivots, 196 satellites), 131072 ctx, ratio 0.5, "
-                        "needle queries with natural drift, top-1024 retrieval from the full-KV tier",
-            "decode_step": S, "retrieval_topk": 1024, "pivots": npiv, "satellites": sats,
-            "drift_check_groups": groups or HeteroCacheConfig(None).drift_check_groups,
-            "check_key_bytes": check_k_bytes, "tier_bytes": tier_bytes, "tier": a["tier"],
-            "retrieval_bytes_per_check": per_check, "runs": res,
-            "ms_per_step_no_retrieval": res["never"]["ms_per_step"],
-            "ms_per_step_retrieval_every_check": a["ms_per_step"],
-            "retrieval_exposed_ms_per_check": round((a["ms_per_step"] - res["never"]["ms_per_step"]) * S, 4),
-            "host_tier_retrieval_exposed_ms_per_check":
-                round((res["host_always"]["ms_per_step"] - res["host_never"]["ms_per_step"]) * S, 4),
-            "roofline": {"bound": "hbm", "achieved": round(a["tbs"] * 1000, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": a["frac_of_hbm_peak"], "run": f"retrieval every check, {a['tier']} tier",
-                         "bytes": "attended K/V + q/out, pivot keys per check / 5, retrieved rows written / 5"},
-            "prefill": {"compress_ms_per_layer": a["prefill_main_ms_per_layer"],
-                        "total_ms_device_tier": a["prefill_total_ms"],
-                        "total_ms_host_tier": res["host_always"]["prefill_total_ms"],
-                        "host_tier_link_gbs": round(tier_bytes / res["host_always"]["prefill_total_ms"] / 1e6, 1)}}
+    a = res.get("always") or res[runs[-1][0]]
+
+    def exposed(hi, lo):
+        return round((res[hi]["ms_per_step"] - res[lo]["ms_per_step"]) * S, 4) if hi in res and lo in res else None
+
+    out = {"workload": "reference Llama-3.1-8B head JSON (33 pivots, 196 satellites), 131072 ctx, ratio 0.5, "
+                       "needle queries with natural drift, top-1024 retrieval from the full-KV tier",
+           "decode_step": S, "retrieval_topk": 1024, "pivots": npiv, "satellites": sats,
+           "drift_check_groups": groups or HeteroCacheConfig(None).drift_check_groups,
+           "check_key_bytes": check_k_bytes, "tier_bytes": tier_bytes, "tier": a["tier"],
+           "retrieval_bytes_per_check": per_check, "runs": res,
+           "ms_per_step_no_retrieval": res["never"]["ms_per_step"] if "never" in res else None,
+           "ms_per_step_retrieval_every_check": res["always"]["ms_per_step"] if "always" in res else None,
+           "retrieval_exposed_ms_per_check": exposed("always", "never"),
+           "host_tier_retrieval_exposed_ms_per_check": exposed("host_always", "host_never"),
+           "roofline": {"bound": "hbm", "achieved": round(a["tbs"] * 1000, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": a["frac_of_hbm_peak"], "run": f"{'retrieval every check' if a is res.get('always') else 'run'}"
+                                                             f", {a['tier']} tier",
+                        "bytes": "attended K/V + q/out, pivot keys per check / 5, retrieved rows written / 5"},
+           "prefill": {"compress_ms_per_layer": a["prefill_main_ms_per_layer"],
+                       "total_ms_device_tier": a["prefill_total_ms"]}}
+    if "host_always" in res:
+        out["prefill"]["total_ms_host_tier"] = res["host_always"]["prefill_total_ms"]
+        out["prefill"]["host_tier_link_gbs"] = round(tier_bytes / res["host_always"]["prefill_total_ms"] / 1e6, 1)
+    return out
 
 
 def gather_phase(args, torch, dev):
@@ -626,7 +640,10 @@ def main():
         print(json.dumps({"prefill_attention": prefill_attention_phase(args, torch, dev)}))
         return
     if args.full_step_only:
-        print(json.dumps({"full_decode_step": full_step_phase(args, torch, dev)}))
+        rec = {"full_decode_step": full_step_phase(args, torch, dev)}
+        if args.calibrate_copy:
+            rec["copy_calibration"] = copy_calibration(torch, dev)
+        print(json.dumps(rec))
         return
     torch.manual_seed(args.seed)
     L, Hkv, G, D = args.ctx, 8, 4, 128
