@@ -47,6 +47,8 @@ def parse():
                    help="comma-separated runs of the full-step phase (natural, never, always, host_never, "
                         "host_always)")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
+    p.add_argument("--window-scoring-only", action="store_true",
+                   help="run only the SnapKV window-scoring phase and print its figures (for counter profiling)")
     p.add_argument("--prefill-only", action="store_true",
                    help="run only the prefill-attention phase and print its figures (for counter profiling)")
     p.add_argument("--calibrate-copy", action="store_true",
@@ -638,6 +640,12 @@ def main():
     dev = torch.device("cuda:0")
     if args.prefill_only:
         print(json.dumps({"prefill_attention": prefill_attention_phase(args, torch, dev)}))
+        return
+    if args.window_scoring_only:
+        rec = {"window_scoring": window_scoring_phase(args, torch, dev)}
+        if args.calibrate_copy:
+            rec["copy_calibration"] = copy_calibration(torch, dev)
+        print(json.dumps(rec))
         return
     if args.full_step_only:
         rec = {"full_decode_step": full_step_phase(args, torch, dev)}
