@@ -119,7 +119,7 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
     return triggers
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_llama_order(dev, dtype):
     trig = run(dev, dtype)
     # First check: overlap 1.0 everywhere; second: every leader retrieves.
@@ -233,10 +233,12 @@ def test_chunked_prefill_with_observation_window_equals_single_shot(dev):
             assert torch.equal(whole._drift[layer].ref_bits, chunked._drift[layer].ref_bits)
 
 
-def test_reference_cast_chain_bf16(dev):
+@pytest.mark.parametrize("dtype,io,step", [(torch.bfloat16, "bfloat16", 2.0 ** -7), (torch.float16, "float16", 2.0 ** -10)])
+def test_reference_cast_chain(dev, dtype, io, step):
     """round_scores=True (the reference's casts of logits, probabilities and
-    pooled scores to bfloat16) on a bfloat16 model: the device scores equal
-    the oracle's cast chain to within one bfloat16 step; the oracle's
+    pooled scores to the model dtype) on a bfloat16 model and on a float16
+    one (the reference's load dtype): the device scores equal the oracle's
+    cast chain to within one step of that dtype; the oracle's
     integer flow run on the device scores reproduces the
     triggers and the stores bit for bit, and the attention outputs match
     the float64 closed form.  The cast scores tie massively, so this also
@@ -251,14 +253,14 @@ def test_reference_cast_chain_bf16(dev):
     rec = Recorder(range(NL))
     cache.observer = rec
     hook = DeviceScores(rec, 0.5)
-    orc = O.CacheOracle(data, B, Hq, Hkv, NL, 0.5, 0.5, 5, "avgpool", 5, score_hook=hook, io_dtype="bfloat16")
+    orc = O.CacheOracle(data, B, Hq, Hkv, NL, 0.5, 0.5, 5, "avgpool", 5, score_hook=hook, io_dtype=io)
     hook.orc = orc
     g = torch.Generator().manual_seed(3)
     last_q = []
     for layer in range(NL):
-        q = torch.randn((B, Hq, 1, D), generator=g).to(torch.bfloat16).to(dev)
-        k = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(dev)
-        v = torch.randn((B, Hkv, L, D), generator=g).to(torch.bfloat16).to(dev)
+        q = torch.randn((B, Hq, 1, D), generator=g).to(dtype).to(dev)
+        k = torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev)
+        v = torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev)
         kc, vc = cache.update(k, v, layer)
         cache.init_coefficient(q, kc, layer)
         cache.prefill_select(q, kc, vc, layer)
@@ -267,9 +269,9 @@ def test_reference_cast_chain_bf16(dev):
     for step in range(steps):
         outs = []
         for layer in range(NL):
-            q = last_q[layer] if step < 5 else torch.randn((B, Hq, 1, D), generator=g).to(torch.bfloat16).to(dev)
-            kn = torch.randn((B, Hkv, 1, D), generator=g).to(torch.bfloat16).to(dev)
-            vn = torch.randn((B, Hkv, 1, D), generator=g).to(torch.bfloat16).to(dev)
+            q = last_q[layer] if step < 5 else torch.randn((B, Hq, 1, D), generator=g).to(dtype).to(dev)
+            kn = torch.randn((B, Hkv, 1, D), generator=g).to(dtype).to(dev)
+            vn = torch.randn((B, Hkv, 1, D), generator=g).to(dtype).to(dev)
             cache.update(kn, vn, layer)
             outs.append((cache.decode_attention(q, layer), q, kn, vn))
             cache.decode_select(q, layer)
@@ -280,7 +282,7 @@ def test_reference_cast_chain_bf16(dev):
     torch.cuda.synchronize()
     flags = [(l, h, c[(l, h)]) for c in rec.checks for l in range(NL) for h in cache._drift[l].leaders]
     assert flags == orc.triggers and [f for *_, f in flags] == [False] * 3 + [True] * 3
-    assert max(e for *_, e in hook.err) <= 2.0 ** -7 * 1.01
+    assert max(e for *_, e in hook.err) <= step * 1.01
     for layer in range(NL):
         store = cache.stores[layer]
         for r in range(B * Hkv):
