@@ -24,7 +24,9 @@
 //     over the window rows of each query head (xor-shuffle tree: fixed
 //     order), write A[job][w'][g][t]; score_pool_kernel: pooling over t and
 //     max over g -> S[job][w'][t].
-//  3b. (< 32 rows) score_finish_kernel: the same from the stored logits.
+//  3b. (< 32 rows) score_finish_kernel: the same from the stored logits
+//     (score_finish_reg_kernel for pool kernels 5 and 7: pooling in
+//     registers).
 // CAKE scoring (hc_cake_score) runs phases 1-2, the probability pass with
 // window moments, and its own pooling and reductions.
 #include <cfloat>
@@ -614,6 +616,7 @@ __device__ __forceinline__ float fin_prob(float x, float m, float iz) {
 
 constexpr int kFinHalo = 32;  // >= kPoolMaxHalf, keeps the strip 16-byte aligned
 constexpr int kFinHeads = 4;  // query heads whose loads are in flight together
+constexpr int kFinWaveSlots = 6;  // the left halo, the four waves of a tile, the right halo
 
 // With HIST, every output row also gets a kKeyDigitBins histogram of the
 // top kKeyDigitBits bits of its scores' order keys (hist[row][digit], zeroed
@@ -737,6 +740,188 @@ __global__ __launch_bounds__(256) void score_finish_kernel(const float* __restri
 // flushes (global atomics on the same few lines serialise).
 constexpr int kFinHistTiles = 4;
 
+// Pool kernels 5 and 7 (the half-width P a template parameter, so the taps
+// unroll without per-tap selects): each thread pools its own kFinRegPos
+// consecutive positions in registers (tiles of kFinRegTile positions, two
+// 16-byte loads per row and thread).  The P neighbours on either side come
+// from the adjacent lanes by shuffles; only each wave's edge values and the
+// tile's halo go through LDS, one barrier per group of kFinHeads query heads
+// (the edge buffer alternates between groups).  Sums and maxima run in
+// score_finish_kernel's order; with the reference's casts the scores are the
+// same bit for bit, without them the row sum is folded into the exponent
+// (within a few ulp of the reciprocal form).
+constexpr int kFinRegHalf = 4;  // widest half-width the window registers hold
+// Probability of one logit: without casts m holds m + log2 l (the row sum
+// folded into the exponent); with casts as fin_prob.
+template <int RMODE>
+__device__ __forceinline__ float fin_prob_reg(float x, float m, float iz) {
+  if constexpr (RMODE == 0) return fast_exp2(x - m);
+  return fin_prob<RMODE>(x, m, iz);
+}
+constexpr int kFinRegPos = 8;
+constexpr int kFinRegTile = 256 * kFinRegPos;
+constexpr int kFinRegHistTiles = 2;
+template <int RMODE, int POOL, bool HIST, int P>
+__global__ __launch_bounds__(256) void score_finish_reg_kernel(const float* __restrict__ logits,
+                                                               const float* __restrict__ stats, int R, int G, int W,
+                                                               int span, int sum_w, int kernel, int accumulate,
+                                                               float* __restrict__ S, uint32_t* __restrict__ hist) {
+  constexpr int NV = kFinRegPos / 4;  // 16-byte vectors per thread and row
+  // s_edge[buffer][head][slot][side]: slot 0 = the tile's left halo, 1 + w =
+  // wave w, 5 = the right halo; side 0 = first four positions, 1 = last four.
+  __shared__ f32x4 s_edge[2][kFinHeads][kFinWaveSlots][2];
+  __shared__ float s_m[kLogitRowsMax], s_iz[kLogitRowsMax];
+  __shared__ uint32_t s_hist[HIST ? kKeyDigitBins : 1];
+  const int wout = sum_w ? 1 : W;
+  const int job = blockIdx.y / wout, wo = blockIdx.y % wout;
+  static_assert(P >= 0 && P <= kFinRegHalf, "pool half-width");
+  const int ntiles = (span + kFinRegTile - 1) / kFinRegTile;
+  constexpr int p = P;  // kernel == 2P + 1
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
+  for (int r = threadIdx.x; r < R; r += 256) {
+    if constexpr (RMODE == 0) {
+      // Without casts p = exp2(x - (m + log2 l)): one subtract, and a masked
+      // logit (-inf) gives 0 by itself.
+      s_m[r] = stats[((int64_t)job * R + r) * 2] + __log2f(stats[((int64_t)job * R + r) * 2 + 1]);
+    } else {
+      s_m[r] = stats[((int64_t)job * R + r) * 2];
+      s_iz[r] = 1.f / stats[((int64_t)job * R + r) * 2 + 1];
+    }
+  }
+  if constexpr (HIST)
+    for (int b = threadIdx.x; b < kKeyDigitBins; b += 256) s_hist[b] = 0u;
+  const int w_lo = sum_w ? 0 : wo, w_hi = sum_w ? W : wo + 1;
+  const bool halo = threadIdx.x < 2 * p;
+  const float inv_k = 1.f / (float)kernel;
+  float* o = S + ((int64_t)job * wout + wo) * span;
+  int buf = 0;
+  __syncthreads();
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int t0 = tile * kFinRegTile;
+    const int tb = t0 + kFinRegPos * threadIdx.x;
+    const bool vec_ok = (span & 3) == 0 && tb + kFinRegPos <= span;
+    // Halo threads: [0, p) positions t0 - p + x, [p, 2p) t0 + kFinRegTile + (x - p).
+    const int th = threadIdx.x < p ? t0 - p + threadIdx.x : t0 + kFinRegTile + (threadIdx.x - p);
+    float best[kFinRegPos];
+#pragma unroll
+    for (int i = 0; i < kFinRegPos; ++i) best[i] = -INFINITY;
+    for (int g0 = 0; g0 < G; g0 += kFinHeads) {
+      float a[kFinHeads][kFinRegPos];
+      float ah[kFinHeads];
+#pragma unroll
+      for (int gg = 0; gg < kFinHeads; ++gg) {
+        const int g = g0 + gg;
+#pragma unroll
+        for (int i = 0; i < kFinRegPos; ++i) a[gg][i] = pad;
+        ah[gg] = pad;
+        if (g >= G) continue;
+        if (tb < span) {
+          float acc[kFinRegPos];
+#pragma unroll
+          for (int i = 0; i < kFinRegPos; ++i) acc[i] = 0.f;
+          for (int w = w_lo; w < w_hi; ++w) {
+            const int r = g * W + w;
+            const float* row = logits + ((int64_t)job * R + r) * span;
+            const float m = s_m[r], iz = s_iz[r];
+            if (vec_ok) {
+              f32x4 x[NV];
+#pragma unroll
+              for (int v = 0; v < NV; ++v) x[v] = *reinterpret_cast<const f32x4*>(row + tb + 4 * v);
+#pragma unroll
+              for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[4 * v + e] += fin_prob_reg<RMODE>(x[v][e], m, iz);
+            } else {
+#pragma unroll
+              for (int i = 0; i < kFinRegPos; ++i)
+                if (tb + i < span) acc[i] += fin_prob_reg<RMODE>(row[tb + i], m, iz);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < kFinRegPos; ++i) a[gg][i] = tb + i < span ? round_fixed<RMODE>(acc[i]) : pad;
+        }
+        if (halo && th >= 0 && th < span) {
+          float acc = 0.f;
+          for (int w = w_lo; w < w_hi; ++w) {
+            const int r = g * W + w;
+            acc += fin_prob_reg<RMODE>(logits[((int64_t)job * R + r) * span + th], s_m[r], s_iz[r]);
+          }
+          ah[gg] = round_fixed<RMODE>(acc);
+        }
+      }
+      // Edges and halo to LDS; the buffer alternates, so a group's writes
+      // never meet the previous group's reads.
+#pragma unroll
+      for (int gg = 0; gg < kFinHeads; ++gg) {
+        if (lane == 0) s_edge[buf][gg][1 + wave][0] = f32x4{a[gg][0], a[gg][1], a[gg][2], a[gg][3]};
+        if (lane == 63)
+          s_edge[buf][gg][1 + wave][1] = f32x4{a[gg][kFinRegPos - 4], a[gg][kFinRegPos - 3], a[gg][kFinRegPos - 2],
+                                               a[gg][kFinRegPos - 1]};
+        if (halo) {
+          if (threadIdx.x < p)
+            s_edge[buf][gg][0][1][kFinRegHalf - p + threadIdx.x] = ah[gg];
+          else
+            s_edge[buf][gg][kFinWaveSlots - 1][0][threadIdx.x - p] = ah[gg];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int gg = 0; gg < kFinHeads; ++gg) {
+        if (g0 + gg >= G) break;
+        // w[4 + d] = position tb + d, d in [-4, kFinRegPos + 4).
+        float w[kFinRegPos + 8];
+#pragma unroll
+        for (int i = 0; i < kFinRegPos; ++i) w[4 + i] = a[gg][i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          w[e] = __shfl_up(a[gg][kFinRegPos - 4 + e], 1, 64);
+          w[kFinRegPos + 4 + e] = __shfl_down(a[gg][e], 1, 64);
+        }
+        if (lane == 0) {
+          const f32x4 l = s_edge[buf][gg][wave][1];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = l[e];
+        }
+        if (lane == 63) {
+          const f32x4 r = s_edge[buf][gg][wave + 2][0];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[kFinRegPos + 4 + e] = r[e];
+        }
+#pragma unroll
+        for (int i = 0; i < kFinRegPos; ++i) {
+          float v = pad;
+#pragma unroll
+          for (int off = -P; off <= P; ++off) v = POOL == 0 ? v + w[4 + i + off] : fmaxf(v, w[4 + i + off]);
+          if constexpr (POOL == 0) v *= inv_k;
+          best[i] = fmaxf(best[i], round_fixed<RMODE>(v));
+        }
+      }
+      buf ^= 1;
+    }
+    if (vec_ok && !accumulate) {
+#pragma unroll
+      for (int v = 0; v < NV; ++v)
+        *reinterpret_cast<f32x4*>(o + tb + 4 * v) = f32x4{best[4 * v], best[4 * v + 1], best[4 * v + 2], best[4 * v + 3]};
+    } else {
+#pragma unroll
+      for (int i = 0; i < kFinRegPos; ++i)
+        if (tb + i < span) o[tb + i] = accumulate ? o[tb + i] + best[i] : best[i];
+    }
+    if constexpr (HIST) {
+#pragma unroll
+      for (int i = 0; i < kFinRegPos; ++i)
+        if (tb + i < span) atomicAdd(&s_hist[order_key(best[i]) >> kKeyDigitShift], 1u);
+    }
+  }
+  if constexpr (HIST) {
+    __syncthreads();
+    uint32_t* h = hist + ((int64_t)job * wout + wo) * kKeyDigitBins;
+    for (int b = threadIdx.x; b < kKeyDigitBins; b += 256)
+      if (s_hist[b]) atomicAdd(&h[b], s_hist[b]);
+  }
+}
+
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Query sets below this many rows take the logit-store path.
@@ -826,15 +1011,28 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   if ((rc = check_launch("hc_score(merge)"))) return rc;
   if (via_logits) {
     if (a.span > 0) {
-      const int ntiles = (a.span + kFinTile - 1) / kFinTile;
+      const bool reg_pool = kernel == 5 || kernel == 7;
+      const int ntiles = (a.span + (reg_pool ? kFinRegTile : kFinTile) - 1) / (reg_pool ? kFinRegTile : kFinTile);
       const int rows = njobs * wout;
-      const int per_row = hist ? (ntiles + kFinHistTiles - 1) / kFinHistTiles : ntiles;
+      const int ht = reg_pool ? kFinRegHistTiles : kFinHistTiles;
+      const int per_row = hist ? (ntiles + ht - 1) / ht : ntiles;
       const dim3 fgrid(per_row, rows);
       const int sum_w = (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : 0;
       const int rmode = rm;
-#define HC_FINISH2(RM, PL, HI)                                                                             \
-  hipLaunchKernelGGL((score_finish_kernel<RM, PL, HI>), fgrid, dim3(256), 0, s, A, stats, a.R, a.G, a.W,       \
-                     a.span, sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores, hist)
+#define HC_FINISH2(RM, PL, HI)                                                                              \
+  do {                                                                                                      \
+    if (kernel == 5)                                                                                        \
+      hipLaunchKernelGGL((score_finish_reg_kernel<RM, PL, HI, 2>), fgrid, dim3(256), 0, s, A, stats, a.R,     \
+                         a.G, a.W, a.span, sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores,    \
+                         hist);                                                                             \
+    else if (kernel == 7)                                                                                   \
+      hipLaunchKernelGGL((score_finish_reg_kernel<RM, PL, HI, 3>), fgrid, dim3(256), 0, s, A, stats, a.R,     \
+                         a.G, a.W, a.span, sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores,    \
+                         hist);                                                                             \
+    else                                                                                                    \
+      hipLaunchKernelGGL((score_finish_kernel<RM, PL, HI>), fgrid, dim3(256), 0, s, A, stats, a.R, a.G, a.W,  \
+                         a.span, sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores, hist);      \
+  } while (0)
 #define HC_FINISH(RM, PL)          \
   do {                             \
     if (hist)                      \
