@@ -152,13 +152,15 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // each swap hands every lane its own value and its partner's (l^16, then
 // l^32) as the two results, in a lane-dependent order; max and + are
 // commutative, so the result equals that of the xor-shuffle form bit for bit.
+// The maximum is IEEE maximum (NaN-propagating; one instruction, where
+// fmaxf first canonicalises operands it cannot prove canonical).
 __device__ __forceinline__ float rows4_max(float v) {
   const unsigned u = __float_as_uint(v);
   const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const float w = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float w = __builtin_elementwise_maximum(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const unsigned uw = __float_as_uint(w);
   const auto b = __builtin_amdgcn_permlane32_swap(uw, uw, false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return __builtin_elementwise_maximum(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 // Sum over the two lanes l and l^16 (row swap only).
 __device__ __forceinline__ float rows2_sum(float v) {

@@ -207,9 +207,14 @@ __device__ __forceinline__ void stats_chunk(const ScoreArgs& a, const KRegs<T>& 
     }
     // -FLT_MAX (not -inf) as the empty maximum: exp2(-inf - m) = 0 for a
     // row with no visible value, never NaN.
+    // IEEE maximum (v_maximum3 on gfx950): the raw accumulators need no
+    // canonicalising, three operands per instruction.
     float m = -FLT_MAX;
 #pragma unroll
-    for (int u = 0; u < kSubTiles; ++u) m = fmaxf(m, fmaxf(fmaxf(x[u][0], x[u][1]), fmaxf(x[u][2], x[u][3])));
+    for (int u = 0; u < kSubTiles; ++u)
+      m = __builtin_elementwise_maximum(
+          m, __builtin_elementwise_maximum(__builtin_elementwise_maximum(x[u][0], x[u][1]),
+                                           __builtin_elementwise_maximum(x[u][2], x[u][3])));
     m = rows4_max(m);
     float l = 0.f;
     if constexpr (RAW) {
