@@ -461,7 +461,6 @@ __global__ __launch_bounds__(kSelThreads) void drift_compact_kernel(
   const uint32_t* ref = bits + (int64_t)(job / steps) * words;
   const int t0 = chunk * kSelChunk;
   uint2* seg = cand + (int64_t)job * cand_stride + t0;
-  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   constexpr int kWords = kSelChunk / 32;
   __shared__ uint32_t s_ref[kWords];
   __shared__ int s_cnt;
@@ -480,30 +479,45 @@ __global__ __launch_bounds__(kSelThreads) void drift_compact_kernel(
   __syncthreads();
   // Per row: the wave's hits above b* and its candidate ballot; then one
   // LDS reservation per wave for all rows' candidates.
-  int hits = 0, ncand = 0;
-  uint64_t mc[kSelRows];
-  uint32_t keys[kSelRows];
+  // Ballots are wave-uniform (scalar registers); the keys are recomputed
+  // from the scores when the candidates are written, and the rows go in two
+  // halves, which keeps the kernel near 64 VGPRs without scalar spills.
+  constexpr int kHalf = kSelRows / 2;
+  int hits = 0;
 #pragma unroll
-  for (int r = 0; r < kSelRows; ++r) {
-    const int wb = r * kSelThreads + 64 * wave;  // chunk-local position of the wave's lane 0
-    const bool valid = t0 + wb + lane < span;
-    keys[r] = order_key(v[r]);
-    const uint32_t d = keys[r] >> kKeyDigitShift;
-    const uint64_t mh = __ballot(valid && (mode == kDriftAll || d > bstar));
-    const uint64_t rb = (uint64_t)s_ref[wb >> 5] | ((uint64_t)s_ref[(wb >> 5) + 1] << 32);
-    hits += __popcll(mh & rb);
-    mc[r] = __ballot(valid && mode == kDriftPartial && d == bstar);
-    ncand += __popcll(mc[r]);
-  }
-  if (ncand) {
-    int base = 0;
-    if (lane == 0) base = atomicAdd(&s_cnt, ncand);
-    base = __shfl(base, 0, 64);
+  for (int h = 0; h < 2; ++h) {
+    int ncand = 0;
+    uint64_t mc[kHalf];
 #pragma unroll
-    for (int r = 0; r < kSelRows; ++r) {
-      if ((mc[r] >> lane) & 1ull)
-        seg[base + __popcll(mc[r] & below)] = make_uint2(keys[r], (uint32_t)(t0 + r * kSelThreads + 64 * wave + lane));
-      base += __popcll(mc[r]);
+    for (int i = 0; i < kHalf; ++i) {
+      const int r = h * kHalf + i;
+      const int wb = r * kSelThreads + 64 * wave;  // chunk-local position of the wave's lane 0
+      const bool valid = t0 + wb + lane < span;
+      const uint32_t d = order_key(v[r]) >> kKeyDigitShift;
+      const uint64_t mh = __ballot(valid && (mode == kDriftAll || d > bstar));
+      const uint64_t rb = (uint64_t)s_ref[wb >> 5] | ((uint64_t)s_ref[(wb >> 5) + 1] << 32);
+      hits += __popcll(mh & rb);
+      mc[i] = __ballot(valid && mode == kDriftPartial && d == bstar);
+      ncand += __popcll(mc[i]);
+    }
+    if (ncand) {
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&s_cnt, ncand);
+      base = __shfl(base, 0, 64);
+#pragma unroll
+      for (int i = 0; i < kHalf; ++i) {
+        const int r = h * kHalf + i;
+        const int t = t0 + r * kSelThreads + 64 * wave + lane;
+        const uint32_t key = order_key(v[r]);
+        if (t < span && mode == kDriftPartial && (key >> kKeyDigitShift) == bstar) {
+          // Rank among the row's candidates of this wave: set bits of the
+          // (uniform) ballot below this lane.
+          const int rank = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mc[i] >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)mc[i], 0u));
+          seg[base + rank] = make_uint2(key, (uint32_t)t);
+        }
+        base += __popcll(mc[i]);
+      }
     }
   }
   if (lane == 0) s_sum[wave] = hits;
