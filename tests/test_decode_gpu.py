@@ -146,10 +146,11 @@ def test_fused_append_matches_oracle_over_steps(dev, dt):
         assert torch.equal(ka, kb) and torch.equal(va, vb)
 
 
-def test_merge_folds_parts_beyond_the_register_batch(dev):
+@pytest.mark.parametrize("G", [1, 4, 7, 16])
+def test_merge_folds_parts_beyond_the_register_batch(dev, G):
     """A row of 547 parts: the merge folds its first 128 parts from registers
-    and the rest in its online loop."""
-    err, _ = run_case(dev, "bf16", [70000, 300], 16, seed=31, chunk_tiles=4)
+    and the rest in its online loop, for several group sizes."""
+    err, _ = run_case(dev, "bf16", [70000, 300], G, seed=31 + G, chunk_tiles=4)
     assert err <= ATTN_TOL["bf16"], err
 
 
