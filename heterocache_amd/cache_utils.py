@@ -67,6 +67,13 @@ class HeteroCacheConfig:
     default: the check and decode attention are both HBM-bound, so on their
     own they gain nothing from running together; it pays where the rest of
     the model leaves HBM bandwidth idle.
+    one_pass_drift_check: let the decode attention of the leader rows report
+    each step query's softmax statistics over the prompt keys
+    (hc_decode_attn_stats), so that a batched check scores in one pass over
+    the pivot keys (hc_score_given_stats) instead of a statistics pass that
+    stores every logit and a pass over the logits.  Applies to the uncast
+    float32 scores with pooling widths up to 9; otherwise, and when off, the
+    two-pass scorer runs.
     tier_placement: where the satellites' full-KV tier lives when
     real_offload is set -- "host" (pinned host memory, retrieval read over
     the host link), "device" (an HBM arena, retrieval a device gather) or
@@ -83,7 +90,8 @@ class HeteroCacheConfig:
                  num_layers: Optional[int] = 32, retrieval_topk: Optional[int] = None, window_size: int = 1,
                  round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None,
                  batched_drift_check: bool = True, drift_check_groups: int = 1, tier_placement: str = "auto",
-                 tier_device_budget: Optional[int] = None, overlap_drift_check: bool = False):
+                 tier_device_budget: Optional[int] = None, overlap_drift_check: bool = False,
+                 one_pass_drift_check: bool = True):
         self.data = data
         self.stable_threshold = stable_threshold
         self.compression_ratio = compression_ratio
@@ -108,6 +116,7 @@ class HeteroCacheConfig:
         self.tier_placement = tier_placement
         self.tier_device_budget = tier_device_budget
         self.overlap_drift_check = overlap_drift_check
+        self.one_pass_drift_check = one_pass_drift_check
 
 
 def _f32_caps(base, ratios, seq_len):
@@ -129,6 +138,7 @@ class _LayerDrift:
         self.qlist = []        # the step queries [B, Hq, 1, 128] since the last check (references)
         self.count = 0
         self.meta = None       # device metadata and buffers, built on the first check
+        self.stat_mask = 0     # steps of this cycle whose softmax statistics the decode reported
 
 
 class HeteroCache(DynamicCache):
@@ -166,6 +176,7 @@ class HeteroCache(DynamicCache):
         self.chunk_tiles = getattr(cfg, "chunk_tiles", None)
         self.batched_check = bool(getattr(cfg, "batched_drift_check", True))
         self.overlap_check = bool(getattr(cfg, "overlap_drift_check", False))
+        self.one_pass = bool(getattr(cfg, "one_pass_drift_check", True))
         self._side_shared = set()   # data pointers of device buffers already recorded on the side stream
         ngroups = max(1, min(int(getattr(cfg, "drift_check_groups", 1) or 1), self.num_layers))
         # Last layer of each check group (contiguous layer ranges).
@@ -200,6 +211,11 @@ class HeteroCache(DynamicCache):
         self._arena = None
         self._tile_table = None      # int64 arena tile offsets of all rows, layer-major
         self._qbuf_all = None        # [NL, B, Hq, S, 128] buffered decode queries
+        # [NL, B*Hkv, G, S, 2] softmax statistics (max bound, sum) of every
+        # buffered decode query over its row's prefill keys, reported by the
+        # decode launches (hc_decode_attn_stats) for the one-pass check.
+        self._step_stats = None
+        self.one_pass_checks = 0     # batched checks scored in one pass over the pivot keys
         self._qbuf_index = {}        # layers of a batched query gather -> device index
         self._ref_bits_all = None    # [leaders * B, words] pivot reference sets
         self._trigger_all = None     # [leaders] int32 drift flags
@@ -582,8 +598,35 @@ class HeteroCache(DynamicCache):
         if p is not None:
             kn = p[0].reshape(-1, D)
             vn = p[1].reshape(-1, D)
-        o = store.attend(q, 1.0 / (D ** 0.5), out=out, k_new=kn, v_new=vn, chunk_tiles=self.chunk_tiles)
+        stat = self._step_stat_view(layer_idx, query_states)
+        o = store.attend(q, 1.0 / (D ** 0.5), out=out, k_new=kn, v_new=vn, chunk_tiles=self.chunk_tiles,
+                         stat_len=self.prefill_len if stat is not None else 0, stat_out=stat)
         return o.view(B, 1, Hq * D)
+
+    def _one_pass_check(self, dtype):
+        """Whether a batched drift check can score in one pass over the pivot
+        keys from the decode-reported statistics: the uncast float32 chain,
+        a pooling width hc_score_given_stats takes and fewer than 32 query
+        rows per pivot."""
+        return (self.one_pass and self.batched_check and self._round_dtype(dtype) is None and self.kernel_size % 2 == 1
+                and self.kernel_size <= 9 and self.num_key_value_groups * self.decode_step < 32)
+
+    def _step_stat_view(self, layer_idx, query_states):
+        """Output view [B*Hkv, G, 2] of this step's softmax statistics for a
+        layer with leaders (slot: the step's position in the check cycle), or
+        None.  In Llama order the attention runs before the step's query is
+        buffered, so the slot is the count of queries buffered so far."""
+        st = self._drift[layer_idx]
+        if st is None or not st.leaders or not self._one_pass_check(query_states.dtype):
+            return None
+        slot = st.count
+        if slot >= self.decode_step:
+            return None
+        if self._step_stats is None:
+            self._step_stats = torch.zeros((self.num_layers, self.bsz * self.num_kv_heads, self.num_key_value_groups,
+                                            self.decode_step, 2), dtype=torch.float32, device=query_states.device)
+        st.stat_mask |= 1 << slot
+        return self._step_stats[layer_idx, :, :, slot]
 
     def decode_select(self, query_states, layer_idx):
         """Buffered pivot drift check and satellite retrieval
@@ -714,16 +757,33 @@ class HeteroCache(DynamicCache):
             self._share_with_side(side, [qa, self._arena[0], self._arena[1], self._tile_table, self._trigger_all,
                                          self._ref_bits_all]
                                   + ([] if self._tier is None else list(self._tier))
+                                  + ([] if self._step_stats is None else [self._step_stats])
                                   + [t for layer, _ in bm["plans"]
                                      for t in (self.key_cache_cpu[layer], self.value_cache_cpu[layer])]
                                   + [v for v in bm.values() if torch.is_tensor(v)]
                                   + [v for v in (bm["group_plan"] or {}).values() if torch.is_tensor(v)])
+        # One pass over the pivot keys when every step of the cycle had its
+        # softmax statistics reported by its decode launch; otherwise the
+        # statistics pass with stored logits.
+        full = (1 << S) - 1
+        one_pass = self._step_stats is not None and all(self._drift[layer].stat_mask == full for layer in layers)
+        for layer in layers:
+            self._drift[layer].stat_mask = 0
+        self.one_pass_checks += int(one_pass)
         with torch.cuda.stream(side):
-            scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,
-                               self.pooling, self.kernel_size, 1.0 / math.sqrt(self.head_dim), flags=flags,
-                               row_tile_off=self._tile_table, k_row=bm["k_row"], hist=bm["hist"]).view(J, S, L)
+            if one_pass:
+                scores = ops.score_given_stats(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0],
+                                               self._tile_table, bm["k_row"], L, G, S, self.pooling,
+                                               self.kernel_size, 1.0 / math.sqrt(self.head_dim), self._step_stats,
+                                               bm["st_off"], out=bm["scores"]).view(J, S, L)
+                hist = None  # the selection builds the first-digit histograms itself
+            else:
+                scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,
+                                   self.pooling, self.kernel_size, 1.0 / math.sqrt(self.head_dim), flags=flags,
+                                   row_tile_off=self._tile_table, k_row=bm["k_row"], hist=bm["hist"]).view(J, S, L)
+                hist = bm["hist"]
             ops.drift_select(scores.view(J * S, L), bm["caps_K"], K, bits, L, bm["trig_of"], nlead, B, S,
-                             self.stable_threshold, trig, bm["hist"], overlap=bm["overlap"])
+                             self.stable_threshold, trig, hist, overlap=bm["overlap"])
             if bm["retrieve"]:
                 ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
             if self.observer is not None:
@@ -785,6 +845,9 @@ class HeteroCache(DynamicCache):
         m = {"K": K, "J": J, "lead0": gl0, "row_ids": row_ids}
         m["q_off"] = torch.as_tensor(np.asarray(q_off, dtype=np.int64)).to(dev)
         m["k_row"] = torch.as_tensor(np.asarray(k_row, dtype=np.int32)).to(dev)
+        # The step statistics of arena row k_row (same layer-major row order).
+        m["st_off"] = torch.as_tensor(np.asarray(k_row, dtype=np.int64) * (G * S * 2)).to(dev)
+        m["scores"] = torch.empty((J, S, L), dtype=torch.float32, device=dev)
         m["caps_K"] = torch.full((J * S,), K, dtype=torch.int32, device=dev)
         m["overlap"] = torch.empty(J * S, dtype=torch.int32, device=dev)
         m["hist"] = self._drift_hist(J * S, dev)

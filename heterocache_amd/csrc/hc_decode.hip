@@ -151,10 +151,13 @@ __device__ __forceinline__ void load_tile(typename Elem<T>::vec8 (&kr)[8], typen
 // tokens at or beyond len, online base-2 softmax, O^T += V^T.P^T.  Lane
 // state: m_run is the running maximum of query n = lane%16 (scaled, base 2),
 // l_run this lane's share of the running sum, o[mt][j] = O^T[16mt+4g+j][n].
-template <typename T>
+// STATS: (m_snap, l_snap) also follow the state over the tokens below
+// stat_len only (see decode_partial_kernel).
+template <typename T, bool STATS>
 __device__ __forceinline__ void attend_tile(typename Elem<T>::vec8 (&kr)[8], typename Elem<T>::vec8 (&vr)[8],
                                             const typename Elem<T>::vec8 (&qreg)[4], int t, int len, int lane,
-                                            float scale_log2, float& m_run, float& l_run, f32x4 (&o)[8]) {
+                                            float scale_log2, float& m_run, float& l_run, f32x4 (&o)[8],
+                                            int stat_len, float& m_snap, float& l_snap) {
   typedef typename Elem<T>::vec8 vec8;
   const int g = lane >> 4;
   const int tok0 = t * HC_TILE;
@@ -201,6 +204,23 @@ __device__ __forceinline__ void attend_tile(typename Elem<T>::vec8 (&kr)[8], typ
     p[e] = fast_exp2(fmaf(sv[e], scale_log2, -m_new));
     psum += p[e];
   }
+  if constexpr (STATS) {
+    // Tiles are visited in increasing order, so while every tile so far lies
+    // below stat_len the snapshot is the running state itself; the tile
+    // that crosses stat_len adds only its tokens below it (against the new
+    // maximum, which bounds them); later tiles leave it alone.
+    if (tok0 + HC_TILE <= stat_len) {
+      m_snap = m_new;
+      l_snap = fmaf(l_run, alpha, psum);
+    } else if (tok0 < stat_len) {
+      float ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (tok0 + 16 * (e >> 2) + 4 * g + (e & 3) < stat_len) ps += p[e];
+      m_snap = m_new;
+      l_snap = fmaf(l_run, alpha, ps);
+    }
+  }
   l_run = fmaf(l_run, alpha, psum);
   m_run = m_new;
   vec8 pb = pack8<T>(p);
@@ -240,14 +260,57 @@ __device__ __forceinline__ void attend_new_token(const typename Elem<T>::vec8 (&
     for (int j = 0; j < 4; ++j) o[mt][j] = fmaf(p, Elem<T>::to_f32(vn[16 * mt + 4 * g + j]), o[mt][j] * alpha);
 }
 
+// Stream tiles [t_begin, t_end) of a row through attend_tile (SNAP: with the
+// below-stat_len snapshot).  Two tile buffers: the next tile's 16 wave-loads
+// are in flight while the current one is consumed.  The buffers alternate by
+// name (no register copies) and the loads inside the paired loop are
+// unconditional, so every wait leaves the younger tile outstanding.
+// Scheduling barriers keep each request between the two consumers (hoisting
+// both requests would hold three tiles and spill).
+template <typename T, bool SNAP>
+__device__ __forceinline__ void stream_tiles(const T* __restrict__ kstore, const T* __restrict__ vstore,
+                                             int64_t row_base, int lane, int t_begin, int t_end,
+                                             const typename Elem<T>::vec8 (&qreg)[4], int len_st, float scale_log2,
+                                             float& m_run, float& l_run, f32x4 (&o)[8], int stat_len, float& m_snap,
+                                             float& l_snap) {
+  typedef typename Elem<T>::vec8 vec8;
+  const T* kb = kstore + row_base + lane * 8;
+  const T* vb = vstore + row_base + lane * 8;
+  vec8 kA[8], vA[8], kB[8], vB[8];
+  load_tile<T>(kA, vA, kb, vb, t_begin);
+  int t = t_begin;
+  for (; t + 2 < t_end; t += 2) {
+    load_tile<T>(kB, vB, kb, vb, t + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    attend_tile<T, SNAP>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+    __builtin_amdgcn_sched_barrier(0);
+    load_tile<T>(kA, vA, kb, vb, t + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    attend_tile<T, SNAP>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (t + 1 < t_end) {
+    load_tile<T>(kB, vB, kb, vb, t + 1);
+    attend_tile<T, SNAP>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+    attend_tile<T, SNAP>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+  } else {
+    attend_tile<T, SNAP>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+  }
+}
+
 constexpr int kOPitch = HC_HEAD_DIM + 4;
 
-template <typename T, int NWAVES>
+// STATS: besides its (m, l, O) partial, each workgroup writes part_st, the
+// (max, sum) of its queries' scaled base-2 scores over the attended tokens
+// below stat_len, which the merge folds into the row's softmax statistics
+// over its first stat_len tokens.
+template <typename T, int NWAVES, bool STATS>
 __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_partial_kernel(
     const T* __restrict__ q, T* __restrict__ kstore, T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off,
     const int* __restrict__ row_len, const int* __restrict__ row_cap, const int* __restrict__ row_order, int rows,
     int G, float scale_log2, int chunk_tiles, const T* __restrict__ k_new, const T* __restrict__ v_new,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ row_info, int* __restrict__ status) {
+    float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ row_info, int* __restrict__ status,
+    int stat_len, float* __restrict__ part_st) {
   typedef typename Elem<T>::vec8 vec8;
   constexpr int NT = NWAVES * 64;
   const bool fused_append = (k_new != nullptr);
@@ -261,6 +324,8 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
 
   __shared__ float s_m[NWAVES][16];
   __shared__ float s_l[NWAVES][16];
+  __shared__ float s_ms[STATS ? NWAVES : 1][16];
+  __shared__ float s_ls[STATS ? NWAVES : 1][16];
   // Per-wave O^T of the G queries, [wave][query][channel], pitch kOPitch;
   // sized by the launch for G queries.
   extern __shared__ float s_o[];
@@ -313,45 +378,36 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
     const int t_end_st = min(t_end, (len_st + HC_TILE - 1) / HC_TILE);
 
     float m_run = -INFINITY, l_run = 0.f;
+    float m_snap = -INFINITY, l_snap = 0.f;  // STATS: the state below stat_len
     f32x4 o[8];
 #pragma unroll
     for (int mt = 0; mt < 8; ++mt) o[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int64_t row_base = loc.tiles * (int64_t)HC_TILE_ELEMS;
     if (t_begin < t_end_st) {
-      const T* kb = kstore + row_base + lane * 8;
-      const T* vb = vstore + row_base + lane * 8;
-      // Two tile buffers: the next tile's 16 wave-loads are in flight while
-      // the current one is consumed.  The buffers alternate by name (no
-      // register copies) and the loads inside the paired loop are
-      // unconditional, so every wait leaves the younger tile outstanding.
-      // Scheduling barriers keep each request between the two consumers
-      // (hoisting both requests would hold three tiles and spill).
-      vec8 kA[8], vA[8], kB[8], vB[8];
-      load_tile<T>(kA, vA, kb, vb, t_begin);
-      int t = t_begin;
-      for (; t + 2 < t_end_st; t += 2) {
-        load_tile<T>(kB, vB, kb, vb, t + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        attend_tile<T>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o);
-        __builtin_amdgcn_sched_barrier(0);
-        load_tile<T>(kA, vA, kb, vb, t + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        attend_tile<T>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (t + 1 < t_end_st) {
-        load_tile<T>(kB, vB, kb, vb, t + 1);
-        attend_tile<T>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o);
-        attend_tile<T>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o);
-      } else {
-        attend_tile<T>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o);
+      // Only the wave whose tiles straddle stat_len follows the snapshot
+      // tile by tile; a wave wholly below it takes its final state, one
+      // wholly above leaves the snapshot empty.
+      const bool cross = STATS && t_begin * HC_TILE < stat_len && t_end_st * HC_TILE > stat_len;
+      if (cross)
+        stream_tiles<T, STATS>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2, m_run,
+                               l_run, o, stat_len, m_snap, l_snap);
+      else
+        stream_tiles<T, false>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2, m_run,
+                               l_run, o, stat_len, m_snap, l_snap);
+      if (STATS && t_end_st * HC_TILE <= stat_len) {
+        m_snap = m_run;
+        l_snap = l_run;
       }
     }
     // The wave whose tile range holds the new slot attends the new token and
     // stores it (no other workgroup of this launch reads that slot).
     if (fused_append && new_pos >= t_begin * HC_TILE && new_pos < t_end * HC_TILE) {
       attend_new_token<T>(qreg, kn, vn, lane, scale_log2, m_run, l_run, o);
+      if (STATS && new_pos < stat_len) {  // every earlier token lies below it too
+        m_snap = m_run;
+        l_snap = l_run;
+      }
       const int64_t tb = row_base + (int64_t)(new_pos / HC_TILE) * HC_TILE_ELEMS;
       const int tn = new_pos % HC_TILE;
       for (int d = lane; d < HC_HEAD_DIM; d += 64) {
@@ -360,12 +416,17 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
       }
     }
     l_run = rows4_sum(l_run);
+    if constexpr (STATS) l_snap = rows4_sum(l_snap);
 
     // Wave states -> LDS.  Lane holds O^T[d = 16mt + 4g + j][q = n].
     if (n < G) {
       if (g == 0) {
         s_m[wave][n] = m_run;
         s_l[wave][n] = l_run;
+        if constexpr (STATS) {
+          s_ms[wave][n] = m_snap;
+          s_ls[wave][n] = l_snap;
+        }
       }
 #pragma unroll
       for (int mt = 0; mt < 8; ++mt)
@@ -393,6 +454,20 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
         part_ml[(part * G + qq) * 2 + 1] = lsum;
       }
     }
+    if constexpr (STATS) {
+      for (int qq = threadIdx.x; qq < G; qq += NT) {
+        float M = -INFINITY, Ls = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWAVES; ++w) M = fmaxf(M, s_ms[w][qq]);
+        if (M != -INFINITY) {
+#pragma unroll
+          for (int w = 0; w < NWAVES; ++w)
+            if (s_ms[w][qq] != -INFINITY) Ls = fmaf(s_ls[w][qq], fast_exp2(s_ms[w][qq] - M), Ls);
+        }
+        part_st[(part * G + qq) * 2 + 0] = M;
+        part_st[(part * G + qq) * 2 + 1] = Ls;
+      }
+    }
     if (threadIdx.x == 0 && loc.chunk == 0) {
       row_info[2 * row] = (int)loc.p0;
       row_info[2 * row + 1] = loc.nparts;
@@ -417,10 +492,25 @@ constexpr int kMergeThreads = kMergeSlice * kMergeGroups;
 // (flagged np = -1 by an undersized grid or a full row) is written as NaN
 // and its length is not advanced: only rows whose new token was stored and
 // attended advance.
-template <typename T>
+// STATS: the grid has one more channel slice, whose workgroup of (row,
+// query) folds the parts' statistics below stat_len instead (its first wave:
+// lanes striding over the parts, then a xor tree) into
+// stat_out[row * st_row_stride + query * st_head_stride] = (max, sum), NaN
+// for a flagged row.  (Folded by one of the merge waves of slice 0 the
+// statistics cost 0.6 us per layer; by a fifth wave of every merge
+// workgroup, 0.3.)
+__device__ __forceinline__ void merge_ml_pair(float& m, float& l, float m2, float l2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  l = l * fast_exp2(m - mn) + l2 * fast_exp2(m2 - mn);
+  m = mn;
+}
+
+template <typename T, bool STATS>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_ml, const int* __restrict__ row_info, int G,
-    int64_t grid_parts, int* __restrict__ row_len, int advance, T* __restrict__ out) {
+    int64_t grid_parts, int* __restrict__ row_len, int advance, T* __restrict__ out, const float* __restrict__ part_st,
+    float* __restrict__ stat_out, int64_t st_row_stride, int64_t st_head_stride) {
   constexpr int kBatch = 8;  // parts per thread whose loads are in flight together
   const int row = blockIdx.x, qq = blockIdx.y, d0 = blockIdx.z * kMergeSlice;
   const int tid = threadIdx.x;
@@ -429,6 +519,32 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
   __shared__ float s_o[kMergeGroups][kMergeSlice];
   T* o = out + ((int64_t)row * G + qq) * HC_HEAD_DIM + d0;
   const bool valid = np >= 1 && p0 >= 0 && (int64_t)p0 + np <= grid_parts;
+  if constexpr (STATS) {
+    if (blockIdx.z == HC_HEAD_DIM / kMergeSlice) {  // the statistics slice
+      if (tid >= 64) return;
+      float* so = stat_out + row * st_row_stride + qq * st_head_stride;
+      if (!valid) {
+        if (tid == 0) so[0] = so[1] = NAN;
+        return;
+      }
+      const int ln = tid;
+      float sm = -INFINITY, sl = 0.f;
+      for (int p = ln; p < np; p += 64) {
+        const float2 x = *reinterpret_cast<const float2*>(part_st + ((int64_t)(p0 + p) * G + qq) * 2);
+        merge_ml_pair(sm, sl, x.x, x.y);
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float m2 = __shfl_xor(sm, off, 64), l2 = __shfl_xor(sl, off, 64);
+        merge_ml_pair(sm, sl, m2, l2);
+      }
+      if (ln == 0) {
+        so[0] = sm;
+        so[1] = sl;
+      }
+      return;
+    }
+  }
   if (advance && valid && qq == 0 && blockIdx.z == 0 && tid == 0) row_len[row] += 1;
   if (!valid) {
     if (tid < kMergeSlice) o[tid] = Elem<T>::from_f32(NAN);
@@ -516,21 +632,29 @@ int64_t decode_num_parts(const int* host_row_len, int rows, int chunk_tiles) {
 }
 
 // Workspace: [row_info: (first part, part count) per row, padded to 256 B]
-//            [part_ml: parts*G*2 f32][part_o: parts*G*128 f32]
+//            [part_ml: parts*G*2 f32][part_st: parts*G*2 f32]
+//            [part_o: parts*G*128 f32]
 // Every field is written before it is read within one call, so the buffer
 // needs no initialisation and may be reused freely by calls on one stream.
 static size_t workspace_head(int rows) { return ((size_t)rows * 2 * sizeof(int) + 255) / 256 * 256; }
 
 size_t decode_workspace_bytes_rows(int rows, int group, int64_t num_parts) {
   if (num_parts <= 0 || group <= 0) return workspace_head(rows);
-  return workspace_head(rows) + (size_t)num_parts * (size_t)group * (HC_HEAD_DIM + 2) * sizeof(float);
+  return workspace_head(rows) + (size_t)num_parts * (size_t)group * (HC_HEAD_DIM + 4) * sizeof(float);
 }
+
+// Softmax statistics requested of a decode launch (hc_decode_attn_stats).
+struct DecodeStats {
+  int len = 0;  // 0: none
+  float* out = nullptr;
+  int64_t row_stride = 0, head_stride = 0;
+};
 
 template <typename T>
 static int launch_decode(const void* q, void* kstore, void* vstore, const int64_t* row_tile_off, int* row_len,
                          const int* row_cap, const int* row_order, int rows, int G, float scale, const void* k_new,
                          const void* v_new, void* out, void* workspace, size_t workspace_bytes, int64_t grid_parts,
-                         int chunk_tiles, int* status, hipStream_t stream) {
+                         int chunk_tiles, int* status, const DecodeStats& st, hipStream_t stream) {
   if (grid_parts < rows)
     return set_error(HC_ERR_INVALID, "hc_decode_attn: num_parts=%lld below the row count %d", (long long)grid_parts,
                      rows);
@@ -540,18 +664,32 @@ static int launch_decode(const void* q, void* kstore, void* vstore, const int64_
     return set_error(HC_ERR_INVALID, "hc_decode_attn: workspace too small (%zu < %zu bytes)", workspace_bytes, need);
   int* row_info = reinterpret_cast<int*>(workspace);
   float* part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + workspace_head(rows));
-  float* part_o = part_ml + (size_t)grid_parts * G * 2;
+  float* part_st = part_ml + (size_t)grid_parts * G * 2;
+  float* part_o = part_st + (size_t)grid_parts * G * 2;
   const float scale_log2 = scale * 1.4426950408889634f;
   const size_t lds_o = (size_t)kDecodeWaves * G * kOPitch * sizeof(float);
-  hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves>), dim3((unsigned)grid_parts), dim3(kDecodeWaves * 64),
-                     lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off, row_len, row_cap, row_order,
-                     rows, G, scale_log2, chunk_tiles, (const T*)k_new, (const T*)v_new, part_o, part_ml, row_info,
-                     status);
+  const dim3 mgrid(rows, G, HC_HEAD_DIM / kMergeSlice), mblock(kMergeSlice * kMergeGroups);
+  if (st.len > 0) {
+    hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves, true>), dim3((unsigned)grid_parts),
+                       dim3(kDecodeWaves * 64), lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off,
+                       row_len, row_cap, row_order, rows, G, scale_log2, chunk_tiles, (const T*)k_new,
+                       (const T*)v_new, part_o, part_ml, row_info, status, st.len, part_st);
+    int rc = check_launch("hc_decode_attn(partial)");
+    if (rc) return rc;
+    hipLaunchKernelGGL((decode_merge_kernel<T, true>), dim3(rows, G, HC_HEAD_DIM / kMergeSlice + 1), mblock, 0,
+                       stream, part_o, part_ml, row_info, G,
+                       grid_parts, row_len, k_new ? 1 : 0, (T*)out, part_st, st.out, st.row_stride,
+                       st.head_stride);
+    return check_launch("hc_decode_attn(merge)");
+  }
+  hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves, false>), dim3((unsigned)grid_parts),
+                     dim3(kDecodeWaves * 64), lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off,
+                     row_len, row_cap, row_order, rows, G, scale_log2, chunk_tiles, (const T*)k_new, (const T*)v_new,
+                     part_o, part_ml, row_info, status, 0, nullptr);
   int rc = check_launch("hc_decode_attn(partial)");
   if (rc) return rc;
-  hipLaunchKernelGGL((decode_merge_kernel<T>), dim3(rows, G, HC_HEAD_DIM / kMergeSlice),
-                     dim3(kMergeSlice * kMergeGroups), 0, stream, part_o, part_ml, row_info, G, grid_parts, row_len,
-                     k_new ? 1 : 0, (T*)out);
+  hipLaunchKernelGGL((decode_merge_kernel<T, false>), mgrid, mblock, 0, stream, part_o, part_ml, row_info, G,
+                     grid_parts, row_len, k_new ? 1 : 0, (T*)out, nullptr, nullptr, (int64_t)0, (int64_t)0);
   return check_launch("hc_decode_attn(merge)");
 }
 
@@ -568,9 +706,9 @@ static int decode_slots(int dtype, int G) {
   const size_t lds = (size_t)kDecodeWaves * G * kOPitch * sizeof(float);
   const void* fn = nullptr;
   switch (dtype) {
-    case HC_DTYPE_BF16: fn = reinterpret_cast<const void*>(decode_partial_kernel<__bf16, kDecodeWaves>); break;
-    case HC_DTYPE_F16: fn = reinterpret_cast<const void*>(decode_partial_kernel<_Float16, kDecodeWaves>); break;
-    default: fn = reinterpret_cast<const void*>(decode_partial_kernel<float, kDecodeWaves>); break;
+    case HC_DTYPE_BF16: fn = reinterpret_cast<const void*>(decode_partial_kernel<__bf16, kDecodeWaves, false>); break;
+    case HC_DTYPE_F16: fn = reinterpret_cast<const void*>(decode_partial_kernel<_Float16, kDecodeWaves, false>); break;
+    default: fn = reinterpret_cast<const void*>(decode_partial_kernel<float, kDecodeWaves, false>); break;
   }
   int per_cu = 0, cus = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDecodeWaves * 64, lds) != hipSuccess) return -1;
@@ -629,7 +767,8 @@ extern "C" int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, in
 static int decode_entry(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
                         int32_t* row_len, const int32_t* row_cap, const int32_t* row_order, int rows, int group,
                         float scale, const void* k_new, const void* v_new, void* out, void* workspace,
-                        size_t workspace_bytes, int64_t num_parts, int chunk_tiles, int32_t* status, void* stream) {
+                        size_t workspace_bytes, int64_t num_parts, int chunk_tiles, int32_t* status, void* stream,
+                        const DecodeStats& st = DecodeStats()) {
   if (rows < 0 || group < 1 || group > 16)
     return set_error(HC_ERR_INVALID, "hc_decode_attn: rows=%d group=%d (group must be 1..16)", rows, group);
   if (chunk_tiles < 1 || chunk_tiles > (1 << 22))
@@ -644,13 +783,13 @@ static int decode_entry(int dtype, const void* q, void* kstore, void* vstore, co
   switch (dtype) {
     case HC_DTYPE_BF16:
       return launch_decode<__bf16>(q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale,
-                                   k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, s);
+                                   k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, st, s);
     case HC_DTYPE_F16:
       return launch_decode<_Float16>(q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale,
-                                     k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, s);
+                                     k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, st, s);
     case HC_DTYPE_F32:
       return launch_decode<float>(q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale,
-                                  k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, s);
+                                  k_new, v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, st, s);
     default:
       return set_error(HC_ERR_INVALID, "hc_decode_attn: unknown dtype %d", dtype);
   }
@@ -664,6 +803,25 @@ extern "C" int hc_decode_attn(int dtype, const void* q, void* kstore, void* vsto
   clear_error();
   return decode_entry(dtype, q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale, k_new,
                       v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, stream);
+}
+
+extern "C" int hc_decode_attn_stats(int dtype, const void* q, void* kstore, void* vstore, const int64_t* row_tile_off,
+                                    int32_t* row_len, const int32_t* row_cap, const int32_t* row_order, int rows,
+                                    int group, float scale, const void* k_new, const void* v_new, void* out,
+                                    void* workspace, size_t workspace_bytes, int64_t num_parts, int chunk_tiles,
+                                    int32_t* status, int stat_len, float* stat_out, int64_t stat_row_stride,
+                                    int64_t stat_head_stride, void* stream) {
+  clear_error();
+  if (stat_len < 1 || !stat_out || stat_row_stride < 0 || stat_head_stride < 0)
+    return set_error(HC_ERR_INVALID, "hc_decode_attn_stats: stat_len=%d, stat_out %s", stat_len,
+                     stat_out ? "given" : "null");
+  DecodeStats st;
+  st.len = stat_len;
+  st.out = stat_out;
+  st.row_stride = stat_row_stride;
+  st.head_stride = stat_head_stride;
+  return decode_entry(dtype, q, kstore, vstore, row_tile_off, row_len, row_cap, row_order, rows, group, scale, k_new,
+                      v_new, out, workspace, workspace_bytes, num_parts, chunk_tiles, status, stream, st);
 }
 
 // Address of this device's scratch array, resolved once per device on the

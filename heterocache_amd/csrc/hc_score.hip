@@ -927,6 +927,199 @@ __global__ __launch_bounds__(256) void score_finish_reg_kernel(const float* __re
   }
 }
 
+// ---------------------------------------------------------------------------
+// One-pass scoring with given softmax statistics (hc_score_given_stats).
+// When the normaliser of every query row over the keys is already known --
+// the drift check's buffered decode queries, whose decode attention launches
+// (hc_decode_attn_stats) reported (M, L) over the pivot's prefill keys --
+// the probabilities need no statistics pass and no stored logits:
+//   p = exp2(s - (M + log2 L)),  S[w'][t] = max_g pool(p[g*W + w'])[t].
+// Each workgroup takes a run of 256-token chunks of one job.  Per chunk its
+// four waves form the probabilities of all R rows (keys from the tiled
+// store as the MFMA A operand, queries staged in LDS once) into an LDS strip
+// of the chunk's 256 positions, and the pooling runs 16 positions behind:
+// positions [cb - 16, cb + 240) of chunk c, whose right neighbours are now
+// in the strip.  The left neighbours -- the previous chunk's last 32
+// positions -- sit in one of two margin buffers, which the pooling of chunk
+// c also fills for chunk c + 1, so each chunk costs two barriers (strip
+// written; strip read).  Only a run's ends cost an extra 16-token sub-tile:
+// the left margin of its first chunk and the right margin of its last 16
+// positions.  The next chunk's keys are requested before the pooling, so
+// their latency is spent pooling.  The first-digit key histograms that
+// hc_drift_select needs are left to its own pass over the scores (24 us at
+// 33 pivots x 5 steps x 128K): counted here, in LDS as 16-bit counters of
+// the 1024 digits a probability can have, they took the kernel from 0.25 to
+// 0.39 ms, and counted into global memory, 0.69 ms.
+// (Four independent waves per workgroup, each with its own 128-position ring
+// and no barriers, measured slower: 0.32 against 0.25 ms at 33 pivots x 5
+// steps x 128K, at three waves per SIMD instead of four.)
+// ---------------------------------------------------------------------------
+constexpr int kGsMargin = 32;                     // margin positions before a chunk
+constexpr int kGsRight = 16;                      // the run's right margin
+constexpr int kGsPitch = kScoreChunk + kGsRight + 4;   // strip row: chunk + right margin + bank skew
+constexpr int kGsMPitch = kGsMargin + 4;          // margin row
+constexpr int kGsPosPerTask = 4;                  // pooled positions per task
+
+// Strip view of one chunk: position cb + i (i in [-32, 272)) of row r is
+// margin[r][i + 32] for i < 0, strip[r][i] otherwise.
+struct GsView {
+  float* strip;        // [R][kGsPitch]
+  const float* mrg;    // [R][kGsMPitch] (previous chunk's last 32 positions)
+  __device__ __forceinline__ f32x4 read4(int r, int i) const {  // i a multiple of 4
+    return i < 0 ? *reinterpret_cast<const f32x4*>(mrg + r * kGsMPitch + kGsMargin + i)
+                 : *reinterpret_cast<const f32x4*>(strip + r * kGsPitch + i);
+  }
+};
+
+// Probabilities of the 16-token sub-tiles tw + 16u (u < NU) of every row,
+// written to dst + r * pitch + (token - base); positions outside [0, span)
+// get the pooling pad.  Per row tile the NU sub-tiles' MFMA chains are
+// issued before any exponential.
+template <typename T, int POOL, int NU>
+__device__ __forceinline__ void gs_subtiles(const ScoreArgs& a, const typename Elem<T>::vec8 (*kr)[4], const T* s_q,
+                                            const float* s_mz, float* dst, int pitch, int base, int tw, int lane) {
+  constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
+  const bool mask = tw + 16 * NU - 1 >= a.L;
+  for (int nt = 0; nt < a.NT; ++nt) {
+    const int r = 16 * nt + (lane & 15);
+    float x[NU][4];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      if (mask)
+        subtile_logits<T, 0, true, true>(a, kr[u], s_q, nt, tw + 16 * u, lane, a.L - 1, x[u]);
+      else
+        subtile_logits<T, 0, false, true>(a, kr[u], s_q, nt, tw + 16 * u, lane, a.L - 1, x[u]);
+    }
+    if (r < a.R) {
+      const float mz = s_mz[r];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int tb = tw + 16 * u + 4 * (lane >> 4);
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int t = tb + j;
+          v[j] = (t >= 0 && t < a.span) ? fast_exp2(fmaf(x[u][j], a.scale2, -mz)) : pad;
+        }
+        *reinterpret_cast<f32x4*>(dst + r * pitch + (tb - base)) = v;
+      }
+    }
+  }
+}
+
+// Pool chunk positions cb + [i0, i0 + n) (i0, n multiples of 4), take the
+// group max and write the scores: task = (output row w', four consecutive
+// positions), reading its 4 + 2P window values per query head as three
+// 16-byte LDS reads.
+template <int POOL, int P>
+__device__ __forceinline__ void gs_pool(const ScoreArgs& a, const GsView& v, int cb, int i0, int n, int job,
+                                        float* __restrict__ S) {
+  static_assert(P <= 4, "window registers hold 4 values on either side");
+  constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
+  const float inv_k = 1.f / (float)(2 * P + 1);
+  const int per_row = n / kGsPosPerTask;
+  for (int task = threadIdx.x; task < a.W * per_row; task += kScoreWaves * 64) {
+    const int w = task / per_row, i = i0 + (task % per_row) * kGsPosPerTask;
+    float best[kGsPosPerTask];
+#pragma unroll
+    for (int e = 0; e < kGsPosPerTask; ++e) best[e] = -INFINITY;
+    for (int g = 0; g < a.G; ++g) {
+      const int r = g * a.W + w;
+      // win[d] = position cb + i - 4 + d, d in [0, 12).
+      const f32x4 lo = v.read4(r, i - 4), mid = v.read4(r, i), hi = v.read4(r, i + 4);
+      const float win[12] = {lo[0], lo[1], lo[2], lo[3], mid[0], mid[1], mid[2], mid[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+      for (int e = 0; e < kGsPosPerTask; ++e) {
+        float x = pad;
+#pragma unroll
+        for (int d = -P; d <= P; ++d) x = POOL == 0 ? x + win[4 + e + d] : fmaxf(x, win[4 + e + d]);
+        if constexpr (POOL == 0) x *= inv_k;
+        best[e] = fmaxf(best[e], x);
+      }
+    }
+    const int t = cb + i;
+    float* o = S + ((int64_t)job * a.W + w) * a.span + t;
+    if (t + kGsPosPerTask <= a.span && (a.span & 3) == 0) {
+      *reinterpret_cast<f32x4*>(o) = f32x4{best[0], best[1], best[2], best[3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < kGsPosPerTask; ++e)
+        if (t + e < a.span) o[e] = best[e];
+    }
+  }
+}
+
+template <typename T, bool STORE, int POOL, int P>
+__global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(ScoreArgs a,
+                                                                            const float* __restrict__ stats,
+                                                                            const int64_t* __restrict__ st_off,
+                                                                            float* __restrict__ S) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* s_q = reinterpret_cast<T*>(smem);
+  float* strip = reinterpret_cast<float*>(smem + (size_t)a.NT * 16 * kQPitch * sizeof(T));  // [R][kGsPitch]
+  float* mrg[2] = {strip + a.R * kGsPitch, strip + a.R * kGsPitch + a.R * kGsMPitch};        // [R][kGsMPitch]
+  __shared__ float s_mz[kLogitRowsMax];
+  constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
+  typedef typename Elem<T>::vec8 vec8;
+  const int job = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
+  const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
+  const int woff = wave * 16 * kSubTiles;
+  KRegs<T> ka;
+  vec8 kh[1][4];  // wave 1: the run's left margin; wave 0: its right margin
+  load_k_chunk<T, STORE>(a, job, c0 * kScoreChunk + woff, lane, ka);
+  if (wave == 1 && c0 > 0) load_k_subtile<T, STORE>(a, job, c0 * kScoreChunk - 16, lane, kh[0]);
+  stage_queries<T>(a, job, s_q);
+  for (int r = threadIdx.x; r < a.R; r += kScoreWaves * 64) {
+    const float* st = stats + st_off[job] + 2 * r;
+    // p = exp2(s - (M + log2 L)); a row without keys (L = 0) gives p = 0.
+    s_mz[r] = st[1] > 0.f ? st[0] + __log2f(st[1]) : INFINITY;
+  }
+  __syncthreads();
+  // The run's left margin: positions c0*256 - 16 .. - 1 (margin entries
+  // [16, 32) of buffer 1, which the first chunk reads).
+  if (wave == 1) {
+    const int cb0 = c0 * kScoreChunk;
+    if (c0 > 0) {
+      gs_subtiles<T, POOL, 1>(a, kh, s_q, s_mz, mrg[1], kGsMPitch, cb0 - kGsMargin, cb0 - 16, lane);
+    } else {
+      for (int i = lane; i < a.R * 16; i += 64) mrg[1][(i / 16) * kGsMPitch + 16 + i % 16] = pad;
+    }
+  }
+  for (int c = c0; c < c1; ++c) {
+    const int cb = c * kScoreChunk;
+    gs_subtiles<T, POOL, kSubTiles>(a, ka.v, s_q, s_mz, strip, kGsPitch, cb, cb + woff, lane);
+    __syncthreads();  // strip written (and the margin of the previous chunk)
+    // Next chunk's keys in flight while this one pools.
+    if (c + 1 < c1) load_k_chunk<T, STORE>(a, job, cb + kScoreChunk + woff, lane, ka);
+    const int mb = (c - c0 + 1) & 1;  // margin buffer holding the previous chunk's tail
+    GsView v{strip, mrg[mb]};
+    // Positions [cb - 16, cb + 240) (the run's first chunk: from cb).
+    if (c == c0)
+      gs_pool<POOL, P>(a, v, cb, 0, kScoreChunk - 16, job, S);
+    else
+      gs_pool<POOL, P>(a, v, cb, -16, kScoreChunk, job, S);
+    // This chunk's last 32 positions are the next chunk's margin.
+    float* nm = mrg[mb ^ 1];
+    for (int i = threadIdx.x; i < a.R * kGsMargin; i += kScoreWaves * 64) {
+      const int r = i / kGsMargin, e = i % kGsMargin;
+      nm[r * kGsMPitch + e] = strip[r * kGsPitch + kScoreChunk - kGsMargin + e];
+    }
+    __syncthreads();  // strip read
+  }
+  // The run's last 16 positions, with its right margin c1*256 .. +15 at
+  // strip entries [256, 272).
+  if (wave == 0) {
+    const int tr = c1 * kScoreChunk;
+    load_k_subtile<T, STORE>(a, job, tr, lane, kh[0]);
+    gs_subtiles<T, POOL, 1>(a, kh, s_q, s_mz, strip, kGsPitch, tr - kScoreChunk, tr, lane);
+  }
+  __syncthreads();
+  const int mb = (c1 - c0) & 1;
+  gs_pool<POOL, P>(a, GsView{strip, mrg[mb]}, (c1 - 1) * kScoreChunk, kScoreChunk - 16, 16, job, S);
+}
+
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 // Query sets below this many rows take the logit-store path.
@@ -1327,6 +1520,81 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
       return set_error(HC_ERR_INVALID, "hc_score: unknown dtype %d", dtype);
   }
 #undef HC_SCORE_DISPATCH
+}
+
+template <typename T, int POOL, int P>
+static int launch_given_stats(ScoreArgs a, int njobs, const float* stats, const int64_t* st_off, float* scores,
+                              hipStream_t s) {
+  const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
+  const size_t lds =
+      (size_t)a.NT * 16 * kQPitch * sizeof(T) + (size_t)a.R * (kGsPitch + 2 * kGsMPitch) * sizeof(float);
+  auto fn = score_given_stats_kernel<T, true, POOL, P>;
+  const int gx = plan_chunks(reinterpret_cast<const void*>(fn), lds, njobs, nchunks, a);
+  hipLaunchKernelGGL(fn, dim3(gx, njobs), dim3(kScoreWaves * 64), lds, s, a, stats, st_off, scores);
+  return check_launch("hc_score_given_stats");
+}
+
+template <typename T>
+static int dispatch_given_stats(const ScoreArgs& a, int njobs, int pooling, int kernel, const float* stats,
+                                const int64_t* st_off, float* scores, hipStream_t s) {
+#define HC_GS(PL)                                                                              \
+  switch (kernel / 2) {                                                                        \
+    case 0: return launch_given_stats<T, PL, 0>(a, njobs, stats, st_off, scores, s);     \
+    case 1: return launch_given_stats<T, PL, 1>(a, njobs, stats, st_off, scores, s);     \
+    case 2: return launch_given_stats<T, PL, 2>(a, njobs, stats, st_off, scores, s);     \
+    case 3: return launch_given_stats<T, PL, 3>(a, njobs, stats, st_off, scores, s);     \
+    default: return launch_given_stats<T, PL, 4>(a, njobs, stats, st_off, scores, s);    \
+  }
+  if (pooling == 0) { HC_GS(0) } else { HC_GS(1) }
+#undef HC_GS
+}
+
+extern "C" int hc_score_given_stats(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride,
+                                    int64_t q_row_stride, const void* kstore, const int64_t* row_tile_off,
+                                    const int32_t* k_row, int njobs, int seq_len, int group, int window, int pooling,
+                                    int kernel, float scale, const float* stats, const int64_t* stat_off,
+                                    float* scores, void* stream) {
+  clear_error();
+  if (njobs < 0 || njobs > 65535 || seq_len < 0 || group < 1 || window < 1)
+    return set_error(HC_ERR_INVALID, "hc_score_given_stats: njobs=%d seq_len=%d group=%d window=%d", njobs, seq_len,
+                     group, window);
+  if (njobs == 0 || seq_len == 0) return HC_OK;
+  const int R = group * window;
+  if (R >= kLogitRowsMax)
+    return set_error(HC_ERR_INVALID, "hc_score_given_stats: group*window = %d, at most %d rows", R, kLogitRowsMax - 1);
+  if (pooling != 0 && pooling != 1)
+    return set_error(HC_ERR_INVALID, "hc_score_given_stats: pooling must be 0 (avg) or 1 (max)");
+  if (kernel < 1 || (kernel % 2) == 0 || kernel / 2 > 4)
+    return set_error(HC_ERR_INVALID, "hc_score_given_stats: pooling kernel must be 1, 3, 5, 7 or 9 (got %d)", kernel);
+  if (!q || !q_off || !kstore || !row_tile_off || !k_row || !stats || !stat_off || !scores)
+    return set_error(HC_ERR_INVALID, "hc_score_given_stats: null pointer argument");
+  ScoreArgs a;
+  a.q = q;
+  a.q_off = q_off;
+  a.q_head_stride = q_head_stride;
+  a.q_row_stride = q_row_stride;
+  a.k = kstore;
+  a.k_off = nullptr;
+  a.k_tok_stride = 0;
+  a.row_tile_off = row_tile_off;
+  a.k_row = k_row;
+  a.L = seq_len;
+  a.G = group;
+  a.W = window;
+  a.R = R;
+  a.NT = (R + 15) / 16;
+  a.flags = 0;
+  a.span = seq_len;
+  a.scale = scale;
+  a.scale2 = scale * 1.4426950408889634f;
+  a.cpw = 1;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case HC_DTYPE_BF16: return dispatch_given_stats<__bf16>(a, njobs, pooling, kernel, stats, stat_off, scores, s);
+    case HC_DTYPE_F16: return dispatch_given_stats<_Float16>(a, njobs, pooling, kernel, stats, stat_off, scores, s);
+    case HC_DTYPE_F32: return dispatch_given_stats<float>(a, njobs, pooling, kernel, stats, stat_off, scores, s);
+    default: return set_error(HC_ERR_INVALID, "hc_score_given_stats: unknown dtype %d", dtype);
+  }
 }
 
 extern "C" size_t hc_cake_workspace_size(int batch, int kv_heads, int seq_len, int group, int window) {

@@ -26,6 +26,8 @@
 //       scan across rows), so the output is ascending by construction.  It
 //       also clears the global histograms for the next call and writes the
 //       force-kept window tail.
+#include <algorithm>
+
 #include "hc_common.h"
 #include "hc_internal.h"
 
@@ -37,7 +39,6 @@ constexpr int kSelChunk = 4096;                      // positions per workgroup
 constexpr int kSelRows = kSelChunk / kSelThreads;    // 16 rows of 256 positions
 constexpr int kSelBins = 256;
 constexpr int kSelMaxChunks = 4096;
-constexpr int kSelMatch = 6;  // digits aggregated per wave before per-lane atomics
 constexpr int kSelSub = 1;    // LDS sub-histograms per wave (power of two)
 
 struct SelJob {
@@ -139,21 +140,11 @@ __global__ __launch_bounds__(kSelThreads) void select_hist_kernel(const float* _
     const uint32_t u = order_key(v[r]);
     const bool valid = t < span && (u & st.mask) == st.prefix;
     const uint32_t d = (u >> shift) & 0xFFu;
-    // Lanes sharing a digit are counted by one atomic of their first lane:
-    // up to kSelMatch distinct digits per wave this way (score digits
-    // cluster in few bins, where per-lane LDS atomics would serialise),
-    // the remaining lanes one atomic each.
-    uint64_t rem = __ballot(valid);
-#pragma unroll
-    for (int it = 0; it < kSelMatch; ++it) {
-      if (rem == 0) break;
-      const int leader = __ffsll((long long)rem) - 1;
-      const uint32_t dl = (uint32_t)__builtin_amdgcn_readlane((int)d, leader);
-      const uint64_t m = __ballot(valid && d == dl) & rem;
-      if ((int)(threadIdx.x & 63) == leader) atomicAdd(&wh[dl], (unsigned)__popcll(m));
-      rem &= ~m;
-    }
-    if ((rem >> (threadIdx.x & 63)) & 1ull) atomicAdd(&wh[d], 1u);
+    // One LDS atomic per position.  (Counting the lanes of a wave that share
+    // a digit by one atomic of their first lane, up to six digits a wave by
+    // readlane / ballot rounds, was slower on clustered pooled scores:
+    // 0.067 against 0.050 ms for 8 rows of 128K, top 49629.)
+    if (valid) atomicAdd(&wh[d], 1u);
   }
   __syncthreads();
   for (int b = threadIdx.x; b < kSelBins; b += kSelThreads) {
@@ -355,18 +346,55 @@ size_t drift_scratch_bytes(int njobs, int span) {
   return drift_head_bytes(njobs, span) + drift_cand_bytes(njobs, span) + drift_hist_bytes(njobs);
 }
 
-// First-digit key histogram of one score row per workgroup, for callers whose
-// scorer did not build it.
-__global__ __launch_bounds__(1024) void drift_hist_kernel(const float* __restrict__ scores, int64_t score_stride,
-                                                          int span, uint32_t* __restrict__ hist) {
+// First-digit key histograms of the score rows, for callers whose scorer did
+// not build them: workgroup (x, row) counts positions [x * kDriftHistSpan,
+// +kDriftHistSpan) of the row in LDS and adds its nonzero bins to the row's
+// histogram, which drift_zero_kernel cleared.  Each thread loads its 32
+// positions (eight 16-byte loads) before counting any, so the loads are in
+// flight together, then adds one LDS atomic per position.  Measured on the
+// drift check's 165 rows of 128K pooled probabilities: 24 us; one workgroup
+// per row, one position per thread and loop step, 66 us; counting lanes of a
+// wave that share a digit by one atomic of their first lane (the readlane /
+// ballot rounds of select_hist_kernel), 81 us; runs of equal digits among a
+// thread's four consecutive positions counted once, 24 us (no gain).
+constexpr int kDriftHistThreads = 256;
+constexpr int kDriftHistVec = 8;  // 16-byte loads per thread
+constexpr int kDriftHistSpan = kDriftHistThreads * 4 * kDriftHistVec;
+__global__ __launch_bounds__(256) void drift_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+
+__global__ __launch_bounds__(kDriftHistThreads) void drift_hist_kernel(const float* __restrict__ scores,
+                                                                       int64_t score_stride, int span,
+                                                                       uint32_t* __restrict__ hist) {
   __shared__ uint32_t h[kKeyDigitBins];
-  for (int b = threadIdx.x; b < kKeyDigitBins; b += 1024) h[b] = 0u;
+  for (int b = threadIdx.x; b < kKeyDigitBins; b += kDriftHistThreads) h[b] = 0u;
+  const float* s = scores + (int64_t)blockIdx.y * score_stride;
+  const int t0 = blockIdx.x * kDriftHistSpan;
+  const bool vec = (score_stride & 3) == 0;
+  f32x4 x[kDriftHistVec];
+#pragma unroll
+  for (int v = 0; v < kDriftHistVec; ++v) {
+    const int t = t0 + (v * kDriftHistThreads + threadIdx.x) * 4;
+    if (vec && t + 4 <= span) {
+      x[v] = *reinterpret_cast<const f32x4*>(s + t);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[v][e] = t + e < span ? s[t + e] : 0.f;
+    }
+  }
   __syncthreads();
-  const float* s = scores + (int64_t)blockIdx.x * score_stride;
-  for (int t = threadIdx.x; t < span; t += 1024) atomicAdd(&h[order_key(s[t]) >> kKeyDigitShift], 1u);
+#pragma unroll
+  for (int v = 0; v < kDriftHistVec; ++v)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = t0 + (v * kDriftHistThreads + threadIdx.x) * 4 + e;
+      if (t < span) atomicAdd(&h[order_key(x[v][e]) >> kKeyDigitShift], 1u);
+    }
   __syncthreads();
-  uint32_t* o = hist + (int64_t)blockIdx.x * kKeyDigitBins;
-  for (int b = threadIdx.x; b < kKeyDigitBins; b += 1024) o[b] = h[b];
+  uint32_t* o = hist + (int64_t)blockIdx.y * kKeyDigitBins;
+  for (int b = threadIdx.x; b < kKeyDigitBins; b += kDriftHistThreads)
+    if (h[b]) atomicAdd(&o[b], h[b]);
 }
 
 // Inclusive prefix sum of one value per thread across a workgroup of NT.
@@ -809,7 +837,12 @@ extern "C" int hc_drift_select(const float* scores, int64_t score_stride, int ns
   int rc;
   if (!hist) {
     uint32_t* own = reinterpret_cast<uint32_t*>(base + drift_head_bytes(njobs, span) + drift_cand_bytes(njobs, span));
-    hipLaunchKernelGGL(drift_hist_kernel, dim3(njobs), dim3(1024), 0, s, scores, score_stride, span, own);
+    const int64_t words = (int64_t)njobs * kKeyDigitBins;
+    hipLaunchKernelGGL(drift_zero_kernel, dim3((unsigned)std::min<int64_t>((words + 255) / 256, 1024)), dim3(256), 0,
+                       s, own, words);
+    if ((rc = check_launch("hc_drift_select(hist zero)"))) return rc;
+    hipLaunchKernelGGL(drift_hist_kernel, dim3((span + kDriftHistSpan - 1) / kDriftHistSpan, njobs),
+                       dim3(kDriftHistThreads), 0, s, scores, score_stride, span, own);
     if ((rc = check_launch("hc_drift_select(hist)"))) return rc;
     hist = own;
   }

@@ -116,7 +116,7 @@ def decode_chunk_tiles(host_row_len, group, dtype):
 
 def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, out=None, row_order=None,
                 k_new=None, v_new=None, chunk_tiles=None, stream=None, workspace=None, num_parts=None,
-                row_cap=None, status=None):
+                row_cap=None, status=None, stat_len=0, stat_out=None):
     """out[r, g] = softmax(scale * q[r, g] . K_r^T) V_r over row_len[r] tokens.
 
     q: [rows, G, 128]; host_row_len: host copy of the lengths (sizes the grid).
@@ -130,6 +130,10 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
     a larger grid (surplus workgroups exit at once) lets a captured HIP graph
     replay while the device lengths grow.  workspace: a uint8 device tensor
     of at least hc_decode_workspace_size bytes (default: a shared buffer).
+    stat_len > 0 with stat_out (float32 [rows, G, 2] view, any strides with
+    a unit last-dim stride): each row's softmax statistics (base-2 max bound,
+    sum of exp2 against it) over its first stat_len tokens
+    (hc_decode_attn_stats).
     """
     lib = _lib.load()
     _require_cuda(q, kstore, vstore, row_tile_off, row_len, row_order, k_new, v_new)
@@ -173,10 +177,22 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
         nparts = int(num_parts)
     nbytes = lib.hc_decode_workspace_size(rows, G, nparts)
     ws = workspace if workspace is not None else WORKSPACE.get(q.device, nbytes)
+    st_ptr = _ptr(status) if k_new is not None else None
+    if stat_len:
+        _require_cuda(stat_out)
+        if (stat_out is None or stat_out.dtype != torch.float32 or tuple(stat_out.shape) != (rows, G, 2)
+                or stat_out.stride(2) != 1 or stat_out.device != q.device):
+            raise ValueError(f"stat_out must be a float32 [{rows}, {G}, 2] device view with unit last stride")
+        _lib.check(lib.hc_decode_attn_stats(
+            dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off), _ptr(row_len),
+            _ptr(row_cap), _ptr(row_order), rows, G, float(scale), _ptr(k_new), _ptr(v_new), _ptr(out), _ptr(ws),
+            ws.numel(), nparts, int(chunk_tiles), st_ptr, int(stat_len), _ptr(stat_out), stat_out.stride(0),
+            stat_out.stride(1), _stream(stream, q)))
+        return out
     _lib.check(lib.hc_decode_attn(dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
                                   _ptr(row_len), _ptr(row_cap), _ptr(row_order), rows, G, float(scale), _ptr(k_new),
                                   _ptr(v_new), _ptr(out), _ptr(ws), ws.numel(), nparts, int(chunk_tiles),
-                                  _ptr(status) if k_new is not None else None, _stream(stream, q)))
+                                  st_ptr, _stream(stream, q)))
     return out
 
 
@@ -433,6 +449,32 @@ def score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, seq_len
                             _ptr(k_off), int(k_tok_stride), _ptr(row_tile_off), _ptr(k_row), njobs, int(seq_len),
                             int(group), int(window), int(flags), int(span), pool, int(kernel), float(scale),
                             _ptr(out), _ptr(ws), ws.numel(), _ptr(hist), _stream(stream, q)))
+    return out
+
+
+def score_given_stats(q, q_off, q_head_stride, q_row_stride, kstore, row_tile_off, k_row, seq_len, group, window,
+                      pooling, kernel, scale, stats, stat_off, out=None, stream=None):
+    """Pivot drift scores [jobs, window, seq_len] in one pass over the keys of
+    store rows k_row, given each query row's softmax statistics (M, L) at
+    stats[stat_off[j] + 2r] (hc_score_given_stats in include/hc.h)."""
+    lib = _lib.load()
+    _require_cuda(q, kstore, q_off, row_tile_off, k_row, stats, stat_off)
+    if q.dtype != kstore.dtype:
+        raise TypeError("q and the store must share a dtype")
+    if q_off.dtype != torch.int64 or stat_off.dtype != torch.int64 or k_row.dtype != torch.int32:
+        raise TypeError("q_off / stat_off must be int64 and k_row int32")
+    if stats.dtype != torch.float32:
+        raise TypeError("stats must be float32")
+    njobs = q_off.numel()
+    if out is None:
+        out = torch.empty((njobs, window, seq_len), dtype=torch.float32, device=q.device)
+    elif out.dtype != torch.float32 or out.numel() < njobs * window * seq_len or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float32 tensor of [jobs, window, seq_len]")
+    pool = {"avgpool": 0, "maxpool": 1}[pooling] if isinstance(pooling, str) else int(pooling)
+    _lib.check(lib.hc_score_given_stats(dtype_code(q.dtype), _ptr(q), _ptr(q_off), int(q_head_stride),
+                                        int(q_row_stride), _ptr(kstore), _ptr(row_tile_off), _ptr(k_row), njobs,
+                                        int(seq_len), int(group), int(window), pool, int(kernel), float(scale),
+                                        _ptr(stats), _ptr(stat_off), _ptr(out), _stream(stream, q)))
     return out
 
 

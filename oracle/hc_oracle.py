@@ -21,6 +21,8 @@ Pinning of each function (beyond its own formula) -- tests/test_oracle.py:
       snapkv_update_kv at G=1 (the two reference functions it generalises).
   decode_attention                float64 closed form vs torch SDPA; a
       one-token row returns V exactly; uniform keys give the mean of V.
+  softmax_lse2                    scipy.special.logsumexp / ln 2 on random
+      rows; n equal keys give s + log2(n); stat_len cuts the keys.
   drift_check                     overlap of identical sets is 1, of disjoint
       sets is 0; statistics.median.
   retrieval_indices               ascending-prefix rule on a hand example.
@@ -609,6 +611,31 @@ def decode_attention(q, ks, vs, scale=None):
         p = np.exp(z)
         p /= p.sum(axis=-1, keepdims=True)
         out[r] = p @ v
+    return out
+
+
+def softmax_lse2(q, ks, stat_len, scale=None):
+    """Base-2 log-normaliser of every (row, query head) softmax over the
+    row's first stat_len keys, float64.
+
+    The drift check's probabilities (heterocache/cache_utils.py:1037-1043,
+    softmax(q K^T / sqrt(d), dtype=float32) over a pivot's prefill keys) are
+    exp2(s_t - lse2) with s_t = scale * log2(e) * q.k_t and
+    lse2 = log2(sum_t exp2(s_t)); hc_decode_attn_stats reports lse2 as a
+    (bound M, sum of exp2(s_t - M)) pair.  q: [rows, G, d]; ks: list of
+    [len_r, d].  Returns [rows, G] (-inf for a row with no key below stat_len).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    rows, G, d = q.shape
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    out = np.full((rows, G), -np.inf)
+    for r in range(rows):
+        k = np.asarray(ks[r], dtype=np.float64)[:stat_len]
+        if k.shape[0] == 0:
+            continue
+        s2 = scale * math.log2(math.e) * (q[r] @ k.T)
+        m = s2.max(axis=-1, keepdims=True)
+        out[r] = m[:, 0] + np.log2(np.exp2(s2 - m).sum(axis=-1))
     return out
 
 

@@ -107,6 +107,10 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
                     triggers.append((layer, leader, bool(st.trigger[i].item())))
     torch.cuda.synchronize()
     assert cache.tier_mode == tier
+    # Batched checks in Llama order score in one pass from the statistics the
+    # decode launches reported (every cycle, the first included).
+    one_pass = batched and not select_first
+    assert cache.one_pass_checks == ((steps // 5) * groups if one_pass else 0)
     assert triggers == orc.triggers
     for layer in range(NL):
         store = cache.stores[layer]

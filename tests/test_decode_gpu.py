@@ -154,6 +154,49 @@ def test_merge_folds_parts_beyond_the_register_batch(dev, G):
     assert err <= ATTN_TOL["bf16"], err
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("chunk", [4, None])
+def test_softmax_stats_below_stat_len(dev, dt, chunk):
+    """hc_decode_attn_stats: for every row and query head, M + log2(L) is the
+    float64 base-2 log-normaliser over the row's first stat_len attended
+    tokens (tile-aligned and not, beyond every row, with and without a fused
+    append whose new token lies above or below stat_len); the attention
+    output is the plain call's, bit for bit."""
+    from heterocache_amd import ops
+    lens, G = [5000, 3000, 40, 0, 2055], 4
+    tdt = TORCH_DT[dt]
+    rng = np.random.default_rng(17)
+    ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(tdt) for L in lens]
+    vs = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(tdt) for L in lens]
+    for k in ks:
+        k[:, :4] *= 6  # outlier channels: wide score range
+    q = torch.as_tensor(rng.standard_normal((len(lens), G, 128)), dtype=torch.float32).to(tdt).to(dev)
+    kn = torch.as_tensor(rng.standard_normal((len(lens), 128)), dtype=torch.float32).to(tdt).to(dev)
+    vn = torch.as_tensor(rng.standard_normal((len(lens), 128)), dtype=torch.float32).to(tdt).to(dev)
+    scale = 1 / math.sqrt(128)
+    for stat_len in (1000, 2048, 2056, 4100, 100000):
+        for append in (False, True):
+            a = KVStore([L + 4 for L in lens], tdt, dev)
+            b = KVStore([L + 4 for L in lens], tdt, dev)
+            for st in (a, b):
+                fill_store(st, [k.to(dev) for k in ks], [v.to(dev) for v in vs], dev)
+            stats = torch.full((len(lens), G, 2), 7.0, dtype=torch.float32, device=dev)
+            extra = dict(k_new=kn, v_new=vn) if append else {}
+            oa = a.attend(q, scale, chunk_tiles=chunk, stat_len=stat_len, stat_out=stats, **extra).clone()
+            ob = b.attend(q, scale, chunk_tiles=chunk, **extra)
+            torch.cuda.synchronize()
+            assert torch.equal(oa, ob), (stat_len, append)
+            keys = [as_np(torch.cat([k.to(dev), kn[r:r + 1]]) if append else k) for r, k in enumerate(ks)]
+            ref = O.softmax_lse2(as_np(q), keys, stat_len, scale)
+            st = stats.cpu().numpy().astype(np.float64)
+            with np.errstate(divide="ignore"):
+                got = st[..., 0] + np.log2(st[..., 1])
+            empty = np.isinf(ref)
+            assert np.all(st[empty][:, 0] == -np.inf) and np.all(st[empty][:, 1] == 0), (stat_len, append)
+            err = np.abs(got[~empty] - ref[~empty]).max()
+            assert err <= 2e-5 * max(1.0, np.abs(ref[~empty]).max()), (stat_len, append, err)
+
+
 def test_row_order_does_not_change_results(dev):
     lens = [300, 5000, 64, 2049]
     rng = np.random.default_rng(4)

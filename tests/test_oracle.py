@@ -678,3 +678,21 @@ def test_torch_cpu_restatement_matches_the_oracle():
     assert np.abs(out.numpy() - ref_out).max() < 1e-4
     med = torch_cpu.time_stages(t, threads=1, runs=2, warmup=1)
     assert set(med) >= {"score_pool_topk", "gather", "decode", "decode_gbs"}
+
+
+def test_softmax_lse2_against_scipy_and_closed_forms():
+    from scipy.special import logsumexp
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((3, 4, 128))
+    ks = [rng.standard_normal((n, 128)) * 2 for n in (50, 7, 0)]
+    got = O.softmax_lse2(q, ks, 30)
+    scale = 1 / math.sqrt(128)
+    for r in range(2):
+        z = scale * (q[r] @ ks[r][:30].T)
+        np.testing.assert_allclose(got[r], logsumexp(z, axis=-1) / math.log(2), rtol=0, atol=1e-12)
+    assert np.all(got[2] == -np.inf)
+    # n equal keys: log2(n) above the one score.
+    k = np.tile(rng.standard_normal((1, 128)), (16, 1))
+    s = scale * math.log2(math.e) * (q[0] @ k[0])
+    np.testing.assert_allclose(O.softmax_lse2(q[:1], [k], 1000)[0], s + 4.0, atol=1e-12)
+    np.testing.assert_allclose(O.softmax_lse2(q[:1], [k], 4)[0], s + 2.0, atol=1e-12)

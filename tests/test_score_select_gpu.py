@@ -102,6 +102,56 @@ def test_pivot_step_scores_read_store_in_place(dev):
         assert rel_err(as_np(s[j]), ref) < 2e-4
 
 
+@pytest.mark.parametrize("L,pooling,kernel", [(4099, "avgpool", 7), (4099, "maxpool", 5), (300, "avgpool", 1),
+                                               (1000, "maxpool", 9), (131072, "avgpool", 7)])
+def test_score_given_stats(dev, L, pooling, kernel):
+    """hc_score_given_stats: drift scores of S buffered queries per pivot in
+    one key pass, (a) with the oracle's float64 normalisers as the statistics
+    and (b) with the statistics the decode launches of the S steps reported
+    (hc_decode_attn_stats over the prompt of L keys): both within 2e-4 of the
+    oracle's scores, and (b) within 1e-5 of the two-pass scorer's."""
+    from heterocache_amd import ops
+    B, Hq, Hkv, S, G = 2, 16, 4, 5, 4
+    rng = np.random.default_rng(L + kernel)
+    k = torch.as_tensor(rng.standard_normal((B, Hkv, L, 128)), dtype=torch.float32)
+    k[..., :4] *= 5
+    k = k.to(torch.bfloat16).to(dev)
+    steps = torch.as_tensor(rng.standard_normal((B, Hq, S, 128)), dtype=torch.float32).to(torch.bfloat16).to(dev)
+    store = KVStore([L + 64] * (B * Hkv), torch.bfloat16, dev)
+    store.write_rows(k, k, [(b, h) for b in range(B) for h in range(Hkv)], list(range(B * Hkv)), [L] * (B * Hkv))
+    pivots = [(0, 1), (0, 3), (1, 0), (1, 3)]
+    rows = [b * Hkv + h for b, h in pivots]
+    q_off, k_row = compress.pivot_step_metadata(steps, store, rows, [h for _, h in pivots], G)
+    scale = 1 / math.sqrt(128)
+    sn, kn = as_np(steps), as_np(k)
+    refs = [O.pivot_step_scores(sn[b, h * G:(h + 1) * G], kn[b, h], pooling, kernel) for b, h in pivots]
+    # (a) the oracle's normalisers: M = lse2, L = 1.
+    st = np.zeros((len(pivots), G * S, 2), dtype=np.float32)
+    for j, (b, h) in enumerate(pivots):
+        qr = sn[b, h * G:(h + 1) * G].reshape(1, G * S, 128)  # rows g*S + w
+        st[j, :, 0] = O.softmax_lse2(qr, [kn[b, h]], L, scale)[0]
+        st[j, :, 1] = 1.0
+    stats = torch.tensor(st).to(dev)
+    st_off = torch.arange(len(pivots), dtype=torch.int64, device=dev) * (G * S * 2)
+    got = ops.score_given_stats(steps, q_off, steps.stride(1), steps.stride(2), store.k, store.row_tile_off, k_row,
+                                L, G, S, pooling, kernel, scale, stats, st_off)
+    for j in range(len(pivots)):
+        assert rel_err(as_np(got[j]), refs[j]) < 2e-4, j
+    # (b) statistics from the S decode launches over the stored prompt.
+    dstats = torch.full((B * Hkv, G, S, 2), float("nan"), dtype=torch.float32, device=dev)
+    for w in range(S):
+        qw = steps[:, :, w].reshape(B * Hkv, G, 128).contiguous()
+        store.attend(qw, scale, stat_len=L, stat_out=dstats[:, :, w])
+    st_off = torch.tensor(rows, dtype=torch.int64, device=dev) * (G * S * 2)
+    got2 = ops.score_given_stats(steps, q_off, steps.stride(1), steps.stride(2), store.k, store.row_tile_off, k_row,
+                                 L, G, S, pooling, kernel, scale, dstats, st_off)
+    two_pass = compress.pivot_step_scores(steps, store, rows, [h for _, h in pivots], G, L, pooling, kernel)
+    torch.cuda.synchronize()
+    for j in range(len(pivots)):
+        assert rel_err(as_np(got2[j]), refs[j]) < 2e-4, j
+        assert rel_err(as_np(got2[j]), as_np(two_pass[j])) < 1e-5, j
+
+
 # -- selection --------------------------------------------------------------------
 def check_select(scores_np, caps, window, idx, counts):
     span = scores_np.shape[1]
