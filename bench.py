@@ -368,7 +368,7 @@ def window_scoring_phase(args, torch, dev):
     """SnapKV-style window scoring (W = 32, GQA 4, 8 KV heads) of one layer at
     the bench context.  The MFMA figure counts the algorithmic product once;
     the kernels form the logits twice (statistics pass, probability pass)."""
-    from heterocache_amd import compress
+    from heterocache_amd import compress, ops
     L, Hkv, G, W, D = args.ctx, 8, 4, 32, 128
     q = torch.randn((1, Hkv * G, W, D), device=dev, dtype=torch.bfloat16)
     k = torch.randn((1, Hkv, L, D), device=dev, dtype=torch.bfloat16)
@@ -384,10 +384,32 @@ def window_scoring_phase(args, torch, dev):
     ms = e0.elapsed_time(e1) / n
     flops = 2 * Hkv * G * W * L * D  # algorithmic: one logit product (the kernels compute it twice)
     kbytes = 2 * Hkv * L * D * 2     # K read once per pass, two passes
-    return {"ms_per_layer": round(ms, 4), "tflops_algorithmic": round(flops / ms / 1e9, 2),
-            "mfma_util_vs_bf16_dense_peak": round(flops / ms / 1e9 / 2500.0, 4),
-            "tflops_executed": round(2 * flops / ms / 1e9, 2),
-            "k_read_gbs": round(kbytes / ms / 1e6, 1), "window": W, "ctx": L}
+    rec = {"ms_per_layer": round(ms, 4), "tflops_algorithmic": round(flops / ms / 1e9, 2),
+           "mfma_util_vs_bf16_dense_peak": round(flops / ms / 1e9 / 2500.0, 4),
+           "tflops_executed": round(2 * flops / ms / 1e9, 2),
+           "k_read_gbs": round(kbytes / ms / 1e6, 1), "window": W, "ctx": L}
+    # The same scores given the window queries' softmax statistics, which the
+    # prefill attention reports for its last W queries: one pass over K.  The
+    # statistics come from the attention of the W window queries over the
+    # prompt (bottom-right causal alignment gives the rows of a whole-prompt
+    # call).
+    v = torch.randn((1, Hkv, L, D), device=dev, dtype=torch.bfloat16)
+    st = torch.empty((1, Hkv * G, W, 2), device=dev, dtype=torch.float32)
+    ops.prefill_attn(q, k, v, 1.0 / math.sqrt(D), stat_out=st)
+    del v
+    compress.window_scores(q, k, range(Hkv), G, W, "maxpool", 7, window_keep=True, stats=st)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(n):
+        compress.window_scores(q, k, range(Hkv), G, W, "maxpool", 7, window_keep=True, stats=st)
+    e1.record()
+    torch.cuda.synchronize()
+    ms1 = e0.elapsed_time(e1) / n
+    one_pass_bytes = Hkv * L * D * 2
+    rec["with_attention_stats"] = {
+        "ms_per_layer": round(ms1, 4), "k_read_gbs": round(one_pass_bytes / ms1 / 1e6, 1),
+        "frac_of_single_pass_hbm_bound": round(one_pass_bytes / 8e12 / (ms1 / 1e3), 4)}
+    return rec
 
 
 def time_decode_steps(torch, stores, q, kn, vn, outs, scale, steps, chunk=None, graph=False):

@@ -55,6 +55,9 @@ SIGNATURES = {
     "hc_prefill_attn": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t,
                                 c_void_p]),
+    "hc_prefill_attn_stats": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t,
+                                      c_int, c_void_p, c_void_p]),
     "hc_prefill_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
     "hc_gather_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p,
                                c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p]),
@@ -69,6 +72,9 @@ SIGNATURES = {
     "hc_score_given_stats": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
                                      c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p,
                                      c_void_p, c_void_p]),
+    "hc_score_with_stats": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
+                                    c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float,
+                                    c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_size_t, c_void_p]),
     "hc_cake_score": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int, c_int,
                               c_int, c_int, c_int, c_int, c_float, c_float, c_void_p, c_void_p, c_void_p, c_size_t,
                               c_void_p]),

@@ -74,6 +74,13 @@ class HeteroCacheConfig:
     stores every logit and a pass over the logits.  Applies to the uncast
     float32 scores with pooling widths up to 9; otherwise, and when off, the
     two-pass scorer runs.
+    attention_stats_scoring: let the prefill attention report the softmax
+    statistics of the last window_size queries (hc_prefill_attn_stats), so
+    that prefill_select and init_coefficient score in one pass over the keys
+    (hc_score_with_stats) instead of a statistics pass and a probability
+    pass.  The scores are those of the same uncast float32 softmax; with
+    round_scores, or when the prefill call holds fewer than window_size
+    queries (a short last chunk), the two-pass scorer runs.
     tier_placement: where the satellites' full-KV tier lives when
     real_offload is set -- "host" (pinned host memory, retrieval read over
     the host link), "device" (an HBM arena, retrieval a device gather) or
@@ -91,7 +98,7 @@ class HeteroCacheConfig:
                  round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None,
                  batched_drift_check: bool = True, drift_check_groups: int = 1, tier_placement: str = "auto",
                  tier_device_budget: Optional[int] = None, overlap_drift_check: bool = False,
-                 one_pass_drift_check: bool = True):
+                 one_pass_drift_check: bool = True, attention_stats_scoring: bool = True):
         self.data = data
         self.stable_threshold = stable_threshold
         self.compression_ratio = compression_ratio
@@ -117,6 +124,7 @@ class HeteroCacheConfig:
         self.tier_device_budget = tier_device_budget
         self.overlap_drift_check = overlap_drift_check
         self.one_pass_drift_check = one_pass_drift_check
+        self.attention_stats_scoring = attention_stats_scoring
 
 
 def _f32_caps(base, ratios, seq_len):
@@ -177,6 +185,8 @@ class HeteroCache(DynamicCache):
         self.batched_check = bool(getattr(cfg, "batched_drift_check", True))
         self.overlap_check = bool(getattr(cfg, "overlap_drift_check", False))
         self.one_pass = bool(getattr(cfg, "one_pass_drift_check", True))
+        self.attn_stats = bool(getattr(cfg, "attention_stats_scoring", True))
+        self.attn_stats_layers = 0   # prefill layers scored with the attention's statistics
         self._side_shared = set()   # data pointers of device buffers already recorded on the side stream
         ngroups = max(1, min(int(getattr(cfg, "drift_check_groups", 1) or 1), self.num_layers))
         # Last layer of each check group (contiguous layer ranges).
@@ -485,9 +495,21 @@ class HeteroCache(DynamicCache):
     def _round_dtype(self, dtype):
         return dtype if self.round_scores else None
 
-    def init_coefficient(self, query_states, key_states, layer_idx):
+    def prefill_stat_rows(self, query_states, layer_idx):
+        """Query rows whose softmax statistics the prefill attention of this
+        call should report for the selection scorers (0: none; see
+        attention_stats_scoring).  The scorers read the last window_size
+        query rows over the same keys as the attention."""
+        if not self.attn_stats or self.round_scores or self.prefill_pending(layer_idx):
+            return 0
+        W = self.window_size
+        return W if query_states.shape[2] >= W else 0
+
+    def init_coefficient(self, query_states, key_states, layer_idx, stats=None):
         """Pivot reference sets: top-base of the pooled last-query scores
-        (heterocache/cache_utils.py:1149-1190), kept as device bitmasks."""
+        (heterocache/cache_utils.py:1149-1190), kept as device bitmasks.
+        stats: the prefill attention's statistics of the last queries
+        (prefill_stat_rows), which let the scorer read the keys once."""
         if self.prefill_pending(layer_idx):
             return
         query_states = self._prefill_queries(query_states, layer_idx)
@@ -500,7 +522,7 @@ class HeteroCache(DynamicCache):
         L = key_states.shape[-2]
         G = self.num_key_value_groups
         scores = compress.last_query_scores(query_states, key_states, pivots, G, self.pooling, self.kernel_size,
-                                            round_dtype=self._round_dtype(query_states.dtype))
+                                            round_dtype=self._round_dtype(query_states.dtype), stats=stats)
         K = min(self.base_compress_len, L)
         idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
         if self.observer is not None:
@@ -546,9 +568,10 @@ class HeteroCache(DynamicCache):
     def _score_row(b, pivot_pos, npiv):
         return b * npiv + pivot_pos
 
-    def prefill_select(self, query_states, key_states, value_states, layer_idx):
+    def prefill_select(self, query_states, key_states, value_states, layer_idx, stats=None):
         """Compressed heads keep their top cap_h tokens in temporal order
-        (heterocache/cache_utils.py:782-882)."""
+        (heterocache/cache_utils.py:782-882).  stats: as for
+        init_coefficient."""
         if self.prefill_pending(layer_idx):
             return
         query_states = self._prefill_queries(query_states, layer_idx)
@@ -565,13 +588,16 @@ class HeteroCache(DynamicCache):
             return
         G = self.num_key_value_groups
         W = self.window_size
+        if stats is not None:
+            self.attn_stats_layers += 1
         if W > 1:
             scores = compress.window_scores(query_states, key_states, range(n_c), G, W, self.pooling,
                                             self.kernel_size, window_keep=True,
-                                            round_dtype=self._round_dtype(query_states.dtype))
+                                            round_dtype=self._round_dtype(query_states.dtype), stats=stats)
         else:
             scores = compress.last_query_scores(query_states, key_states, range(n_c), G, self.pooling,
-                                                self.kernel_size, round_dtype=self._round_dtype(query_states.dtype))
+                                                self.kernel_size, round_dtype=self._round_dtype(query_states.dtype),
+                                                stats=stats)
         idx, counts = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0)
         if self.observer is not None:
             self.observer("prefill_select", layer=layer_idx, rows=rows, scores=scores, idx=idx, counts=counts)

@@ -57,13 +57,17 @@ def _job_offsets(key, device, build):
 
 
 def window_scores(q, k, kv_heads, group, window, pooling="avgpool", kernel=5, window_keep=False, causal=True,
-                  round_dtype=None, scale=None, stream=None):
+                  round_dtype=None, scale=None, stream=None, stats=None):
     """Scores [B * len(kv_heads), span] of the last `window` query positions.
 
     q: [B, Hq, Lq, 128]; k: [B, Hkv, L, 128] (post-RoPE, any strides with unit
     channel stride).  Query heads h*group .. h*group+group-1 score kv head h.
     window_keep=True scores only [0, L - window) (SnapKV); otherwise [0, L).
     round_dtype reproduces the reference's casts to that dtype.
+    stats: the softmax statistics [B, Hq, Ws, 2] (Ws >= window) that
+    ops.prefill_attn reported for the last Ws queries of this q over this k;
+    given them, the scorer reads the keys once (uncast scores only, and the
+    window must see causally, as the attention did, unless it is one row).
     """
     _check_qk(q, k)
     B, Hq, Lq, _ = q.shape
@@ -84,6 +88,21 @@ def window_scores(q, k, kv_heads, group, window, pooling="avgpool", kernel=5, wi
     if causal:
         flags |= _lib.HC_SCORE_CAUSAL_WINDOW
     span = L - window if window_keep else L
+    if stats is not None:
+        if ROUND_FLAGS[round_dtype]:
+            raise ValueError("attention statistics are of uncast logits: no round_dtype with stats")
+        if not causal and window > 1:
+            raise ValueError("attention statistics describe a causal window")
+        Ws = stats.shape[2]
+        if stats.shape[:2] != (B, Hq) or Ws < window or stats.shape[3] != 2 or not stats.is_contiguous():
+            raise ValueError(f"stats must be a contiguous [{B}, {Hq}, >= {window}, 2] tensor")
+        stat_off = _job_offsets(("window_stats", B, kv_heads, group, window, Hq, Ws), q.device,
+                                lambda: ([((b * Hq + h * group) * Ws + Ws - window) * 2 for b in range(B)
+                                          for h in kv_heads], [0]))[0]
+        out = ops.score_with_stats(q, q_off, q.stride(1), q.stride(2), k, k_off, k.stride(2), L, group, window, span,
+                                   pooling, kernel, scale, stats, stat_off=stat_off, stat_head_stride=2 * Ws,
+                                   flags=flags, stream=stream)
+        return out.view(q_off.numel(), span)
     out = ops.score(q, q_off, q.stride(1), q.stride(2), k, k_off, k.stride(2), L, group, window, span, pooling, kernel,
                     scale, flags=flags, stream=stream)
     return out.view(q_off.numel(), span)
@@ -117,10 +136,12 @@ def cake_scores(q, k, window, gamma=200.0, round_dtype=None, scale=None, stream=
                           gamma, flags=ROUND_FLAGS[round_dtype], stream=stream)
 
 
-def last_query_scores(q, k, kv_heads, group, pooling="avgpool", kernel=5, round_dtype=None, scale=None, stream=None):
-    """Pooled last-query attention per KV head, max over its query group."""
+def last_query_scores(q, k, kv_heads, group, pooling="avgpool", kernel=5, round_dtype=None, scale=None, stream=None,
+                      stats=None):
+    """Pooled last-query attention per KV head, max over its query group
+    (stats: as for window_scores; the last row is used)."""
     return window_scores(q, k, kv_heads, group, 1, pooling, kernel, window_keep=False, causal=False,
-                         round_dtype=round_dtype, scale=scale, stream=stream)
+                         round_dtype=round_dtype, scale=scale, stream=stream, stats=stats)
 
 
 def pivot_step_metadata(q_steps, store, rows, heads, group):

@@ -65,6 +65,10 @@ struct PfArgs {
   int Hq, Hkv, Lq, Lk, nqb, rows;  // rows = batch * Hkv
   int vt_tiles;                    // tiles per row of vt
   float scale_log2;
+  // Optional softmax statistics of the last st_rows queries of every
+  // (batch, query head): st[((b * Hq + hq) * st_rows + w) * 2 + {0, 1}].
+  float* st;
+  int st_rows;
 };
 
 // LDS: two K buffers and one V buffer of kPfTiles tiles each.
@@ -374,6 +378,16 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
     const float inv = 1.f / lt;
     const int qi = qw0 + 16 * j + n16;
     if (qi >= a.Lq) continue;
+    // The softmax state of query qi over its visible keys, as a scorer's
+    // statistics pass would form it: m bounds the scaled base-2 scores (the
+    // lazy rescale keeps it within 2^kPfLazy of their maximum) and lt is the
+    // sum of exp2(score - m).
+    const int w = qi - (a.Lq - a.st_rows);
+    if (a.st && w >= 0 && g4 == 0) {
+      float* so = a.st + (((int64_t)b * a.Hq + hq) * a.st_rows + w) * 2;
+      so[0] = m[j];
+      so[1] = lt;
+    }
     T* orow = obase + (int64_t)qi * a.o_st + 4 * g4;
 #pragma unroll
     for (int db = 0; db < 8; ++db) {
@@ -424,11 +438,37 @@ extern "C" size_t hc_prefill_workspace_size(int dtype, int batch, int kv_heads, 
   return (size_t)batch * kv_heads * v_tiles_per_row(kv_len) * HC_TILE_ELEMS * esz;
 }
 
+static int prefill_entry(int dtype, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides, void* out, const int64_t* out_strides, int batch,
+                         int q_heads, int kv_heads, int q_len, int kv_len, float scale, void* workspace,
+                         size_t workspace_bytes, int stat_rows, float* stat_out, void* stream);
+
 extern "C" int hc_prefill_attn(int dtype, const void* q, const int64_t* q_strides, const void* k,
                                const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out,
                                const int64_t* out_strides, int batch, int q_heads, int kv_heads, int q_len,
                                int kv_len, float scale, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
+  return prefill_entry(dtype, q, q_strides, k, k_strides, v, v_strides, out, out_strides, batch, q_heads, kv_heads,
+                       q_len, kv_len, scale, workspace, workspace_bytes, 0, nullptr, stream);
+}
+
+extern "C" int hc_prefill_attn_stats(int dtype, const void* q, const int64_t* q_strides, const void* k,
+                                     const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out,
+                                     const int64_t* out_strides, int batch, int q_heads, int kv_heads, int q_len,
+                                     int kv_len, float scale, void* workspace, size_t workspace_bytes, int stat_rows,
+                                     float* stat_out, void* stream) {
+  clear_error();
+  if (stat_rows < 1 || stat_rows > q_len || !stat_out)
+    return set_error(HC_ERR_INVALID, "hc_prefill_attn_stats: stat_rows=%d (q_len %d), stat_out %s", stat_rows, q_len,
+                     stat_out ? "given" : "null");
+  return prefill_entry(dtype, q, q_strides, k, k_strides, v, v_strides, out, out_strides, batch, q_heads, kv_heads,
+                       q_len, kv_len, scale, workspace, workspace_bytes, stat_rows, stat_out, stream);
+}
+
+static int prefill_entry(int dtype, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                         const void* v, const int64_t* v_strides, void* out, const int64_t* out_strides, int batch,
+                         int q_heads, int kv_heads, int q_len, int kv_len, float scale, void* workspace,
+                         size_t workspace_bytes, int stat_rows, float* stat_out, void* stream) {
   const int esz = dtype == HC_DTYPE_F32 ? 4 : (dtype == HC_DTYPE_BF16 || dtype == HC_DTYPE_F16) ? 2 : 0;
   if (esz == 0) return set_error(HC_ERR_INVALID, "hc_prefill_attn: unknown dtype %d", dtype);
   if (batch < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads || q_len < 0 || kv_len < 0)
@@ -474,6 +514,8 @@ extern "C" int hc_prefill_attn(int dtype, const void* q, const int64_t* q_stride
   a.vt_tiles = (int)v_tiles_per_row(kv_len);
   a.rows = batch * kv_heads;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.st = stat_out;
+  a.st_rows = stat_rows;
   const int64_t grid = (int64_t)a.rows * (q_heads / kv_heads) * a.nqb;
   if (grid > 0x7fffffffLL) return set_error(HC_ERR_INVALID, "hc_prefill_attn: grid too large");
   hipStream_t s = (hipStream_t)stream;

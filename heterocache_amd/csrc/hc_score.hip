@@ -29,6 +29,11 @@
 //     registers).
 // CAKE scoring (hc_cake_score) runs phases 1-2, the probability pass with
 // window moments, and its own pooling and reductions.
+// With the rows' softmax statistics already known (prefill attention reports
+// them for its last queries, decode attention for each step query), phases
+// 1-2 drop out: hc_score_with_stats runs phase 3a alone (one key pass), and
+// hc_score_given_stats is the fused one-pass kernel of the drift check
+// (fewer than 32 rows, tiled store, pooling in LDS).
 #include <cfloat>
 #include <algorithm>
 #include <cmath>
@@ -346,8 +351,22 @@ enum WinMode { kWinNone = 0, kWin16 = 1, kWin8 = 2, kWin4 = 3, kWin2 = 4, kWin1 
 // MOM (CAKE scoring, kWin16): besides the window sum A, write the window sum
 // of squares A2 unrounded and one partial of sum p*log(p + 1e-10) over
 // t < span per (job, chunk) into ent.
+// Where the probability pass finds row r = g*W + w's statistics (M, L) of
+// job j: at p + base + 2r with base = off ? off[j] : 2*R*j, or, with a
+// nonzero head_stride, at p + base + g*head_stride + 2w (statistics laid out
+// per query head, such as the ones prefill attention reports).
+struct StatsView {
+  const float* p;
+  const int64_t* off;
+  int64_t head_stride;
+  __device__ __forceinline__ const float* row(const ScoreArgs& a, int job, int r) const {
+    const int64_t base = off ? off[job] : (int64_t)job * a.R * 2;
+    return p + base + (head_stride ? (r / a.W) * head_stride + 2 * (r % a.W) : 2 * (int64_t)r);
+  }
+};
+
 template <typename T, bool STORE, int RM, int WM, bool MOM>
-__global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs a, const float* __restrict__ stats,
+__global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs a, StatsView stats,
                                                                       float* __restrict__ A, float* __restrict__ A2,
                                                                       float* __restrict__ ent) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -366,13 +385,13 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   stage_queries<T>(a, job, s_q);
   for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
     // Padding rows get probability 0 even where logits are not masked.
+    const float* st = r < a.R ? stats.row(a, job, r) : nullptr;
     if constexpr (RM == 0) {
       // Without casts p = exp2(x - (m + log2 l)): one subtract, no divide.
-      s_m[r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] + __log2f(stats[((int64_t)job * a.R + r) * 2 + 1])
-                       : INFINITY;
+      s_m[r] = st ? st[0] + __log2f(st[1]) : INFINITY;
     } else {
-      s_m[r] = r < a.R ? stats[((int64_t)job * a.R + r) * 2] : 0.f;
-      s_iz[r] = r < a.R ? 1.f / stats[((int64_t)job * a.R + r) * 2 + 1] : 0.f;
+      s_m[r] = st ? st[0] : 0.f;
+      s_iz[r] = st ? 1.f / st[1] : 0.f;
     }
   }
   const int wout = WM == kWinNone ? a.W : 1;
@@ -1174,6 +1193,50 @@ static int plan_chunks(const void* fn, size_t lds, int njobs, int nchunks, Score
   return (nchunks + a.cpw - 1) / a.cpw;
 }
 
+// The probability pass (row statistics given) and the pooling pass:
+// scores over [0, a.span), A = the window-summed probabilities.
+template <typename T, bool STORE>
+static int launch_probs_pool(ScoreArgs a, int njobs, int pooling, int kernel, StatsView sv, float* A, float* scores,
+                             hipStream_t s) {
+  const int wout = (a.flags & HC_SCORE_SUM_WINDOW) ? 1 : a.W;
+  const size_t lds3 = (size_t)a.NT * 16 * kQPitch * sizeof(T) + (size_t)a.NT * 16 * 2 * sizeof(float);
+  const int rm = (a.flags & HC_SCORE_ROUND_BF16) ? 1 : (a.flags & HC_SCORE_ROUND_F16) ? 2 : 0;
+  int rc;
+  const int nchunks_span = (a.span + kScoreChunk - 1) / kScoreChunk;
+  if (nchunks_span > 0) {
+    const int wm = !(a.flags & HC_SCORE_SUM_WINDOW) ? kWinNone
+                   : a.W >= 16                       ? kWin16
+                   : a.W == 8                        ? kWin8
+                   : a.W == 4                        ? kWin4
+                   : a.W == 2                        ? kWin2
+                                                     : kWin1;
+#define HC_PROBS(RM, WM)                                                                                    \
+  do {                                                                                                      \
+    auto fn = score_probs_kernel<T, STORE, RM, WM, false>;                                                  \
+    ScoreArgs as = a;                                                                                       \
+    const int gx = plan_chunks(reinterpret_cast<const void*>(fn), lds3, njobs, nchunks_span, as);           \
+    hipLaunchKernelGGL(fn, dim3(gx, njobs), dim3(kScoreWaves * 64), lds3, s, as, sv, A, nullptr, nullptr);    \
+  } while (0)
+#define HC_PROBS_RM(RM)                                     \
+  switch (wm) {                                             \
+    case kWinNone: HC_PROBS(RM, kWinNone); break;           \
+    case kWin16: HC_PROBS(RM, kWin16); break;               \
+    case kWin8: HC_PROBS(RM, kWin8); break;                 \
+    case kWin4: HC_PROBS(RM, kWin4); break;                 \
+    case kWin2: HC_PROBS(RM, kWin2); break;                 \
+    default: HC_PROBS(RM, kWin1); break;                    \
+  }
+    if (rm == 0) { HC_PROBS_RM(0) } else if (rm == 1) { HC_PROBS_RM(1) } else { HC_PROBS_RM(2) }
+#undef HC_PROBS_RM
+#undef HC_PROBS
+    if ((rc = check_launch("hc_score(probs)"))) return rc;
+    hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + kPoolTile - 1) / kPoolTile, njobs * wout),
+                       dim3(kPoolThreads), 0, s, A, a.G, a.span, pooling, kernel, a.flags, scores);
+    if ((rc = check_launch("hc_score(pool)"))) return rc;
+  }
+  return HC_OK;
+}
+
 template <typename T, bool STORE>
 static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* scores, void* ws, uint32_t* hist,
                         hipStream_t s) {
@@ -1185,7 +1248,6 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   float* A = reinterpret_cast<float*>(reinterpret_cast<char*>(stats) + align256((size_t)njobs * a.R * 2 * sizeof(float)));
   const size_t qbytes = (size_t)a.NT * 16 * kQPitch * sizeof(T);
   const size_t lds1 = qbytes + (size_t)kScoreWaves * a.NT * 16 * 2 * sizeof(float);
-  const size_t lds3 = qbytes + (size_t)a.NT * 16 * 2 * sizeof(float);
   const bool via_logits = a.R < kLogitRows;
   const int rm = (a.flags & HC_SCORE_ROUND_BF16) ? 1 : (a.flags & HC_SCORE_ROUND_F16) ? 2 : 0;
   int nparts = 0;  // statistics partials per job: the stats grid's x extent
@@ -1247,39 +1309,7 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
     }
     return HC_OK;
   }
-  const int nchunks_span = (a.span + kScoreChunk - 1) / kScoreChunk;
-  if (nchunks_span > 0) {
-    const int wm = !(a.flags & HC_SCORE_SUM_WINDOW) ? kWinNone
-                   : a.W >= 16                       ? kWin16
-                   : a.W == 8                        ? kWin8
-                   : a.W == 4                        ? kWin4
-                   : a.W == 2                        ? kWin2
-                                                     : kWin1;
-#define HC_PROBS(RM, WM)                                                                                    \
-  do {                                                                                                      \
-    auto fn = score_probs_kernel<T, STORE, RM, WM, false>;                                                  \
-    ScoreArgs as = a;                                                                                       \
-    const int gx = plan_chunks(reinterpret_cast<const void*>(fn), lds3, njobs, nchunks_span, as);           \
-    hipLaunchKernelGGL(fn, dim3(gx, njobs), dim3(kScoreWaves * 64), lds3, s, as, stats, A, nullptr, nullptr); \
-  } while (0)
-#define HC_PROBS_RM(RM)                                     \
-  switch (wm) {                                             \
-    case kWinNone: HC_PROBS(RM, kWinNone); break;           \
-    case kWin16: HC_PROBS(RM, kWin16); break;               \
-    case kWin8: HC_PROBS(RM, kWin8); break;                 \
-    case kWin4: HC_PROBS(RM, kWin4); break;                 \
-    case kWin2: HC_PROBS(RM, kWin2); break;                 \
-    default: HC_PROBS(RM, kWin1); break;                    \
-  }
-    if (rm == 0) { HC_PROBS_RM(0) } else if (rm == 1) { HC_PROBS_RM(1) } else { HC_PROBS_RM(2) }
-#undef HC_PROBS_RM
-#undef HC_PROBS
-    if ((rc = check_launch("hc_score(probs)"))) return rc;
-    hipLaunchKernelGGL(score_pool_kernel, dim3((a.span + kPoolTile - 1) / kPoolTile, njobs * wout),
-                       dim3(kPoolThreads), 0, s, A, a.G, a.span, pooling, kernel, a.flags, scores);
-    if ((rc = check_launch("hc_score(pool)"))) return rc;
-  }
-  return HC_OK;
+  return launch_probs_pool<T, STORE>(a, njobs, pooling, kernel, StatsView{stats, nullptr, 0}, A, scores, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1428,7 +1458,8 @@ static int launch_cake(ScoreArgs a, int njobs, int batch, int heads, float gamma
   auto fprobs = score_probs_kernel<T, false, RM, kWin16, true>;
   ScoreArgs ap = a;
   const int nprob = plan_chunks(reinterpret_cast<const void*>(fprobs), lds3, njobs, nspan, ap);
-  hipLaunchKernelGGL(fprobs, dim3(nprob, njobs), dim3(kScoreWaves * 64), lds3, s, ap, stats, A1, A2, ent);
+  hipLaunchKernelGGL(fprobs, dim3(nprob, njobs), dim3(kScoreWaves * 64), lds3, s, ap, StatsView{stats, nullptr, 0}, A1,
+                     A2, ent);
   if ((rc = check_launch("hc_cake_score(probs)"))) return rc;
   hipLaunchKernelGGL((cake_pool_kernel<RM>), dim3((a.span + kCakeThreads - 1) / kCakeThreads, njobs),
                      dim3(kCakeThreads), 0, s, A1, A2, a.G, a.W, a.span, gamma, scores);
@@ -1595,6 +1626,89 @@ extern "C" int hc_score_given_stats(int dtype, const void* q, const int64_t* q_o
     case HC_DTYPE_F32: return dispatch_given_stats<float>(a, njobs, pooling, kernel, stats, stat_off, scores, s);
     default: return set_error(HC_ERR_INVALID, "hc_score_given_stats: unknown dtype %d", dtype);
   }
+}
+
+extern "C" int hc_score_with_stats(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride,
+                                   int64_t q_row_stride, const void* k, const int64_t* k_off, int64_t k_tok_stride,
+                                   const int64_t* row_tile_off, const int32_t* k_row, int njobs, int seq_len,
+                                   int group, int window, int flags, int span, int pooling, int kernel, float scale,
+                                   const float* stats, const int64_t* stat_off, int64_t stat_head_stride,
+                                   float* scores, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (njobs < 0 || njobs > 65535 || seq_len < 0 || group < 1 || window < 1)
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: njobs=%d seq_len=%d group=%d window=%d", njobs, seq_len,
+                     group, window);
+  if (njobs == 0 || seq_len == 0) return HC_OK;
+  if (flags & ~(HC_SCORE_CAUSAL_WINDOW | HC_SCORE_SUM_WINDOW | HC_SCORE_ACCUMULATE))
+    return set_error(HC_ERR_INVALID,
+                     "hc_score_with_stats: flags 0x%x (the given statistics are of unrounded logits: no rounding "
+                     "flag)",
+                     flags);
+  const bool sum_w = (flags & HC_SCORE_SUM_WINDOW) != 0;
+  if (sum_w && window >= 16 ? (window % 16) != 0 : (sum_w && (window & (window - 1)) != 0))
+    return set_error(HC_ERR_INVALID,
+                     "hc_score_with_stats: a summed window must be 1, 2, 4, 8 or a multiple of 16 (got %d)", window);
+  if (span < 0 || span > seq_len)
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: span %d outside [0, %d]", span, seq_len);
+  if (pooling != 0 && pooling != 1)
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: pooling must be 0 (avg) or 1 (max)");
+  if (kernel < 1 || (kernel % 2) == 0 || kernel > kPoolMaxKernel)
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: pooling kernel must be odd and <= %d (got %d)",
+                     kPoolMaxKernel, kernel);
+  const int R = group * window;
+  const int wout = sum_w ? 1 : window;
+  if ((int64_t)njobs * wout > 65535)
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: njobs x window rows %lld exceed 65535",
+                     (long long)njobs * wout);
+  const int NT = (R + 15) / 16;
+  if (NT > 16) return set_error(HC_ERR_INVALID, "hc_score_with_stats: group*window = %d exceeds 256 rows", R);
+  if (dtype == HC_DTYPE_F32 && NT > 8)
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: float32 supports group*window <= 128 (got %d)", R);
+  if (!q || !q_off || !k || !stats || !scores || (span > 0 && !workspace))
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: null pointer argument");
+  if (stat_head_stride < 0 || (stat_head_stride > 0 && stat_head_stride < 2 * (int64_t)window))
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: stat_head_stride %lld (0, or >= 2 * window)",
+                     (long long)stat_head_stride);
+  const bool store = row_tile_off != nullptr;
+  if (store ? !k_row : !k_off) return set_error(HC_ERR_INVALID, "hc_score_with_stats: missing key addressing");
+  if (!store && (k_tok_stride < HC_HEAD_DIM || (k_tok_stride % 8) != 0))
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: key token stride %lld", (long long)k_tok_stride);
+  if (workspace_bytes < (size_t)njobs * wout * group * span * sizeof(float))
+    return set_error(HC_ERR_INVALID, "hc_score_with_stats: workspace too small");
+  ScoreArgs a;
+  a.q = q;
+  a.q_off = q_off;
+  a.q_head_stride = q_head_stride;
+  a.q_row_stride = q_row_stride;
+  a.k = k;
+  a.k_off = k_off;
+  a.k_tok_stride = k_tok_stride;
+  a.row_tile_off = row_tile_off;
+  a.k_row = k_row;
+  a.L = seq_len;
+  a.G = group;
+  a.W = window;
+  a.R = R;
+  a.NT = NT;
+  a.flags = flags;
+  a.span = span;
+  a.scale = scale;
+  a.scale2 = scale * 1.4426950408889634f;
+  a.cpw = 1;
+  const StatsView sv{stats, stat_off, stat_head_stride};
+  float* A = reinterpret_cast<float*>(workspace);
+  hipStream_t s = (hipStream_t)stream;
+#define HC_WS_DISPATCH(T)                                                                            \
+  return store ? launch_probs_pool<T, true>(a, njobs, pooling, kernel, sv, A, scores, s)            \
+               : launch_probs_pool<T, false>(a, njobs, pooling, kernel, sv, A, scores, s);
+  switch (dtype) {
+    case HC_DTYPE_BF16: { HC_WS_DISPATCH(__bf16) }
+    case HC_DTYPE_F16: { HC_WS_DISPATCH(_Float16) }
+    case HC_DTYPE_F32: { HC_WS_DISPATCH(float) }
+    default:
+      return set_error(HC_ERR_INVALID, "hc_score_with_stats: unknown dtype %d", dtype);
+  }
+#undef HC_WS_DISPATCH
 }
 
 extern "C" size_t hc_cake_workspace_size(int batch, int kv_heads, int seq_len, int group, int window) {

@@ -1,10 +1,14 @@
 """Llama attention with HeteroCache on libhc kernels.
 
 Drop-in for heterocache/llama_model.py:279-405 (`LlamaAttention`): same
-constructor, same forward contract, same call order on the cache:
-  prefill: update -> init_coefficient -> prefill_select -> full causal
-           attention over the uncompressed K/V (hc_prefill_attn) -> o_proj;
-           in a chunked prefill every chunk runs this branch, and the two
+constructor, same forward contract, the same cache calls:
+  prefill: update -> full causal attention over the uncompressed K/V
+           (hc_prefill_attn, reporting the last queries' softmax
+           statistics) -> init_coefficient -> prefill_select -> o_proj;
+           the reference selects before it attends, but neither step reads
+           what the other writes, so moving the attention first changes no
+           result and lets the selection scorers reuse its normalisers.  In
+           a chunked prefill every chunk runs this branch, and the two
            selection calls act once the declared prompt is complete
   decode:  update -> decode attention (hc_decode_attn, replacing
            flash_attn_with_kvcache) -> decode_select -> o_proj
@@ -51,21 +55,36 @@ def _plain_causal(mask, Lq, Lk):
     return plain
 
 
-def prefill_attention(query_states, key_states, value_states, attention_mask, scaling):
+def _native_prefill(query_states, key_states, attention_mask):
+    """Whether prefill_attention runs hc_prefill_attn for these inputs (a
+    ROCm device, head_dim 128, no padding in the mask)."""
+    L, D, Lk = query_states.shape[2], query_states.shape[3], key_states.shape[2]
+    mask = attention_mask
+    if mask is not None and mask.dim() == 4 and _plain_causal(mask, L, Lk):
+        mask = None
+    return query_states.is_cuda and mask is None and D == ops.HEAD_DIM
+
+
+def prefill_attention(query_states, key_states, value_states, attention_mask, scaling, stat_out=None):
     """Causal attention of the L query positions over the Lk uncompressed
     keys; the queries are the last L positions (a whole prompt, or one chunk
     of a chunked prefill over the keys staged so far).  Returns [B, L, Hq*d].
 
     On a ROCm device without a padding mask this is hc_prefill_attn (the
     reference calls flash-attn here, heterocache/llama_model.py:353-361).  A
-    mask that carries padding goes through PyTorch's SDPA with that mask."""
+    mask that carries padding goes through PyTorch's SDPA with that mask.
+    stat_out ([B, Hq, W, 2] float32, native path only) receives the last W
+    queries' softmax statistics (ops.prefill_attn)."""
     B, Hq, L, D = query_states.shape
     Lk = key_states.shape[2]
     mask = attention_mask
     if mask is not None and mask.dim() == 4 and _plain_causal(mask, L, Lk):
         mask = None
     if query_states.is_cuda and mask is None and D == ops.HEAD_DIM:
-        return ops.prefill_attn(query_states, key_states, value_states, scaling).view(B, L, Hq * D)
+        return ops.prefill_attn(query_states, key_states, value_states, scaling,
+                                stat_out=stat_out).view(B, L, Hq * D)
+    if stat_out is not None:
+        raise ValueError("softmax statistics come from the native prefill attention only")
     q = query_states.contiguous()
     k = key_states.contiguous()
     v = value_states.contiguous()
@@ -147,9 +166,19 @@ class LlamaAttention(nn.Module):
         prefill = query_states.shape[-2] != 1 or cache.prefill_pending(self.layer_idx)
         key_states, value_states = cache.update(key_states, value_states, self.layer_idx, cache_kwargs)
         if prefill:
-            cache.init_coefficient(query_states, key_states, self.layer_idx)
-            cache.prefill_select(query_states, key_states, value_states, self.layer_idx)
-            out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling)
+            # The attention runs first so that it can hand the selection
+            # scorers the softmax normalisers of the last queries; neither
+            # reads what the other writes, so the results are those of the
+            # reference's order (select, then attend).
+            stats = None
+            W = cache.prefill_stat_rows(query_states, self.layer_idx)
+            if W and _native_prefill(query_states, key_states, attention_mask):
+                stats = torch.empty((bsz, query_states.shape[1], W, 2), dtype=torch.float32,
+                                    device=query_states.device)
+            out = prefill_attention(query_states, key_states, value_states, attention_mask, self.scaling,
+                                    stat_out=stats)
+            cache.init_coefficient(query_states, key_states, self.layer_idx, stats=stats)
+            cache.prefill_select(query_states, key_states, value_states, self.layer_idx, stats=stats)
         else:
             if self.select_before_attention:
                 cache.decode_select(query_states, self.layer_idx)

@@ -288,13 +288,16 @@ def copy_rows(src_k, src_v, src_bh, dst_k, dst_v, dst_bh, counts, dst_is_host=Fa
                                 _stream(stream, src_k)))
 
 
-def prefill_attn(q, k, v, scale, out=None, stream=None):
+def prefill_attn(q, k, v, scale, out=None, stream=None, stat_out=None):
     """Causal attention of the last Lq positions over Lk keys (hc_prefill_attn).
 
     q: [B, Hq, Lq, 128]; k, v: [B, Hkv, Lk, 128] (any batch/head/token
     strides, unit channel stride; Lq <= Lk, query i sits at position
     Lk - Lq + i).  Returns out [B, Lq, Hq, 128] (or writes the given `out`,
     which may be any view of that shape with unit channel stride).
+    stat_out: optional contiguous float32 [B, Hq, W, 2] (W <= Lq) that
+    receives the softmax statistics (M, L) of the last W queries of each
+    head (hc_prefill_attn_stats), the normalisers the window scorers reuse.
     """
     lib = _lib.load()
     _require_cuda(q, k, v, out)
@@ -327,9 +330,18 @@ def prefill_attn(q, k, v, scale, out=None, stream=None):
     nbytes = lib.hc_prefill_workspace_size(code, B, Hkv, Lk)
     # Per-call scratch from the caching allocator (stream-ordered reuse).
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
-    _lib.check(lib.hc_prefill_attn(code, _ptr(q), base, _ptr(k), base + 24, _ptr(v), base + 48, _ptr(out),
-                                   base + 72, B, Hq, Hkv, Lq, Lk, float(scale), _ptr(ws), ws.numel(),
-                                   _stream(stream, q)))
+    if stat_out is None:
+        _lib.check(lib.hc_prefill_attn(code, _ptr(q), base, _ptr(k), base + 24, _ptr(v), base + 48, _ptr(out),
+                                       base + 72, B, Hq, Hkv, Lq, Lk, float(scale), _ptr(ws), ws.numel(),
+                                       _stream(stream, q)))
+        return out
+    _require_cuda(stat_out)
+    if (stat_out.dim() != 4 or tuple(stat_out.shape[:2]) != (B, Hq) or stat_out.shape[3] != 2
+            or stat_out.dtype != torch.float32 or not stat_out.is_contiguous()):
+        raise ValueError(f"stat_out must be a contiguous float32 tensor of [{B}, {Hq}, W, 2]")
+    _lib.check(lib.hc_prefill_attn_stats(code, _ptr(q), base, _ptr(k), base + 24, _ptr(v), base + 48, _ptr(out),
+                                         base + 72, B, Hq, Hkv, Lq, Lk, float(scale), _ptr(ws), ws.numel(),
+                                         stat_out.shape[2], _ptr(stat_out), _stream(stream, q)))
     return out
 
 
@@ -449,6 +461,40 @@ def score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, seq_len
                             _ptr(k_off), int(k_tok_stride), _ptr(row_tile_off), _ptr(k_row), njobs, int(seq_len),
                             int(group), int(window), int(flags), int(span), pool, int(kernel), float(scale),
                             _ptr(out), _ptr(ws), ws.numel(), _ptr(hist), _stream(stream, q)))
+    return out
+
+
+def score_with_stats(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, seq_len, group, window, span,
+                     pooling, kernel, scale, stats, stat_off=None, stat_head_stride=0, flags=0, row_tile_off=None,
+                     k_row=None, out=None, stream=None):
+    """ops.score with each query row's softmax statistics given (one key pass,
+    no rounding flags): row r = g*window + w of job j reads (M, L) at
+    stats[base + 2r], or stats[base + g*stat_head_stride + 2w] with a
+    nonzero head stride, base = stat_off[j] (or 2*group*window*j without
+    stat_off).  See hc_score_with_stats in include/hc.h."""
+    lib = _lib.load()
+    _require_cuda(q, k, q_off, k_off, row_tile_off, k_row, stats, stat_off)
+    if q.dtype != k.dtype:
+        raise TypeError("q and k must share a dtype")
+    if q_off.dtype != torch.int64 or (k_off is not None and k_off.dtype != torch.int64):
+        raise TypeError("offsets must be int64")
+    if stat_off is not None and stat_off.dtype != torch.int64:
+        raise TypeError("stat_off must be int64")
+    if stats.dtype != torch.float32:
+        raise TypeError("stats must be float32")
+    njobs = q_off.numel()
+    wout = 1 if flags & _lib.HC_SCORE_SUM_WINDOW else window
+    if out is None:
+        out = torch.empty((njobs, wout, span), dtype=torch.float32, device=q.device)
+    elif out.dtype != torch.float32 or out.numel() < njobs * wout * span or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float32 tensor of [jobs, W', span]")
+    ws = torch.empty(max(njobs * wout * group * span * 4, 256), dtype=torch.uint8, device=q.device)
+    pool = {"avgpool": 0, "maxpool": 1}[pooling] if isinstance(pooling, str) else int(pooling)
+    _lib.check(lib.hc_score_with_stats(dtype_code(q.dtype), _ptr(q), _ptr(q_off), int(q_head_stride),
+                                       int(q_row_stride), _ptr(k), _ptr(k_off), int(k_tok_stride), _ptr(row_tile_off),
+                                       _ptr(k_row), njobs, int(seq_len), int(group), int(window), int(flags),
+                                       int(span), pool, int(kernel), float(scale), _ptr(stats), _ptr(stat_off),
+                                       int(stat_head_stride), _ptr(out), _ptr(ws), ws.numel(), _stream(stream, q)))
     return out
 
 

@@ -216,6 +216,28 @@ int hc_prefill_attn(int dtype, const void* q, const int64_t* q_strides, const vo
                     int q_heads, int kv_heads, int q_len, int kv_len, float scale, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/*
+ * hc_prefill_attn that also reports the softmax statistics of the last
+ * stat_rows queries of every (batch, query head), 1 <= stat_rows <= q_len:
+ *   stat_out[((b*q_heads + hq)*stat_rows + w)*2 + 0] = M,
+ *   stat_out[((b*q_heads + hq)*stat_rows + w)*2 + 1] = L,
+ * for query i = q_len - stat_rows + w over its visible keys, with
+ * max_t s_t - 8 <= M <= max_t s_t for the scaled base-2 scores
+ * s_t = scale * log2(e) * q_i . k_t and L = sum_t exp2(s_t - M), so
+ * softmax_t = exp2(s_t - (M + log2 L)).  These are the normalisers of the
+ * observation-window softmax the prefill scorers recompute over the same
+ * keys (HeteroCache.prefill_select and init_coefficient,
+ * heterocache/cache_utils.py:807-829 and :1158-1187; SnapKV,
+ * heterocache/kv_cluster.py:165-185), which then need one key pass
+ * (hc_score_with_stats).  The attention output is bit-identical to
+ * hc_prefill_attn's.
+ */
+int hc_prefill_attn_stats(int dtype, const void* q, const int64_t* q_strides, const void* k,
+                          const int64_t* k_strides, const void* v, const int64_t* v_strides, void* out,
+                          const int64_t* out_strides, int batch, int q_heads, int kv_heads, int q_len, int kv_len,
+                          float scale, void* workspace, size_t workspace_bytes, int stat_rows, float* stat_out,
+                          void* stream);
+
 /* Device workspace bytes hc_prefill_attn needs (V re-laid out in 32-token
  * tiles, written and read within the call: no initialisation). */
 size_t hc_prefill_workspace_size(int dtype, int batch, int kv_heads, int kv_len);
@@ -277,6 +299,29 @@ int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stri
              int kernel, float scale, float* scores, void* workspace, size_t workspace_bytes, uint32_t* hist,
              void* stream);
 size_t hc_score_workspace_size(int njobs, int seq_len, int group, int window, int flags);
+
+/*
+ * hc_score with every query row's softmax statistics given, in the uncast
+ * float32 form (no rounding flag): the probability and pooling passes alone,
+ * so the keys are read once.  Arguments as hc_score's, plus the statistics
+ * (M, L) of row r = g*window + w of job j (M bounds the scaled base-2 scores,
+ * L = sum_t exp2(s_t - M) over the row's visible keys, as
+ * hc_prefill_attn_stats and hc_decode_attn_stats report them) at
+ *   stats + base + 2r                              (stat_head_stride == 0)
+ *   stats + base + g*stat_head_stride + 2w         (otherwise, >= 2*window)
+ * with base = stat_off ? stat_off[j] : 2*group*window*j.  Workspace: at least
+ * njobs * W' * group * span floats (hc_score_workspace_size suffices).
+ * Replaces the same scoring op sequences as hc_score (prefill_select,
+ * heterocache/cache_utils.py:807-829; init_coefficient, :1158-1187; SnapKV,
+ * heterocache/kv_cluster.py:165-185) when the prefill attention has already
+ * formed the softmax normalisers.
+ */
+int hc_score_with_stats(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride, int64_t q_row_stride,
+                        const void* k, const int64_t* k_off, int64_t k_tok_stride, const int64_t* row_tile_off,
+                        const int32_t* k_row, int njobs, int seq_len, int group, int window, int flags, int span,
+                        int pooling, int kernel, float scale, const float* stats, const int64_t* stat_off,
+                        int64_t stat_head_stride, float* scores, void* workspace, size_t workspace_bytes,
+                        void* stream);
 
 /*
  * hc_score's pivot drift scoring in one pass over the keys, given every query

@@ -8,11 +8,13 @@ final store rows (copies: bit-exact) are compared too.  Llama order, Qwen
 order (select before attention), retrieval top-k and the reference-quirk
 mode are covered.
 """
+import math
+
 import numpy as np
 import pytest
 import torch
 
-from heterocache_amd import workloads
+from heterocache_amd import ops, workloads
 from heterocache_amd.cache_utils import HeteroCache, HeteroCacheConfig
 from heterocache_amd.utils import augment_head_data, head_permutation
 from oracle import hc_oracle as O
@@ -42,10 +44,12 @@ def head_data(seed=0):
 
 
 def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True, groups=1,
-        chunks=None, tier="host", overlap=False):
+        chunks=None, tier="host", overlap=False, attn_stats=True):
     """tier: "host" / "device" placement of the full-KV tier, or "prefill"
     (real_offload=False: the prefill K/V kept as the tier).  overlap: batched
-    checks on the side stream (overlap_drift_check)."""
+    checks on the side stream (overlap_drift_check).  attn_stats: the
+    prefill selection scores from the prefill attention's statistics, as the
+    model's attention hands them over (else the two-pass scorer)."""
     torch.manual_seed(0)
     B, Hq, Hkv, NL, D = 1, 32, 8, 2, 128
     data = head_data()
@@ -57,6 +61,15 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
     cache = HeteroCache(cfg)
     if chunks is not None:
         cache.begin_prefill(L)
+
+    def select(qc, kc, vc, layer):
+        st = None
+        W = cache.prefill_stat_rows(qc, layer)
+        if attn_stats and W:
+            st = torch.empty((B, Hq, W, 2), dtype=torch.float32, device=dev)
+            ops.prefill_attn(qc, kc, vc, 1 / math.sqrt(D), stat_out=st)
+        cache.init_coefficient(qc, kc, layer, stats=st)
+        cache.prefill_select(qc, kc, vc, layer, stats=st)
     orc = O.CacheOracle(data, B, Hq, Hkv, NL, 0.5, 0.5, 5, "avgpool", 5, retrieval_topk=topk, quirks=quirks,
                         select_before_attention=select_first)
     g = torch.Generator().manual_seed(1)
@@ -67,8 +80,7 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
         v = torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev)
         if chunks is None:
             kc, vc = cache.update(k, v, layer)
-            cache.init_coefficient(q, kc, layer)
-            cache.prefill_select(q, kc, vc, layer)
+            select(q, kc, vc, layer)
         else:  # chunked prefill: the oracle still sees the whole prompt
             bounds = np.cumsum([0] + list(chunks))
             assert bounds[-1] == L
@@ -76,8 +88,7 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
                 qc = q[:, :, s:e]
                 kc, vc = cache.update(k[:, :, s:e], v[:, :, s:e], layer, {"query_states": qc})
                 assert kc.shape[2] == e
-                cache.init_coefficient(qc, kc, layer)
-                cache.prefill_select(qc, kc, vc, layer)
+                select(qc, kc, vc, layer)
                 assert cache.prefill_pending(layer) == (e < L)
         orc.prefill(layer, as_np(q), as_np(k), as_np(v))
         last_q.append(q[:, :, -1:].clone())
@@ -111,6 +122,7 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
     # decode launches reported (every cycle, the first included).
     one_pass = batched and not select_first
     assert cache.one_pass_checks == ((steps // 5) * groups if one_pass else 0)
+    assert cache.attn_stats_layers == (NL if attn_stats else 0)
     assert triggers == orc.triggers
     for layer in range(NL):
         store = cache.stores[layer]
@@ -144,6 +156,12 @@ def test_llama_order_overlapped_checks(dev, groups, tier):
     store equals the oracle's, as on the main stream."""
     trig = run(dev, torch.float32, groups=groups, tier=tier, overlap=True)
     assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
+
+
+def test_llama_order_two_pass_prefill_scoring(dev):
+    """The prefill selection without the attention's statistics (the
+    two-pass scorer) gives the oracle's triggers and stores too."""
+    run(dev, torch.float32, attn_stats=False)
 
 
 def test_llama_order_layer_by_layer_checks(dev):

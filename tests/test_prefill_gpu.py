@@ -118,3 +118,50 @@ def test_prefill_rejects_bad_shapes(dev):
     k3 = torch.zeros(1, 3, 20, 128, dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError):
         ops.prefill_attn(q, k3, k3, 0.1)        # 4 query heads over 3 KV heads
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("case", [(1, 8, 2, 300, 300, 32), (2, 4, 4, 64, 200, 64), (1, 7, 1, 1, 129, 1),
+                                  (1, 28, 4, 256, 256, 32), (1, 4, 1, 130, 1000, 7)])
+def test_prefill_stats(dev, dt, case):
+    """hc_prefill_attn_stats: the output is bit-identical to hc_prefill_attn's,
+    and each of the last W queries' (M, L) gives the oracle's base-2
+    log-normaliser over its visible keys, M + log2 L, within 1e-3 (log2
+    units), with M inside [max s - 8, max s]."""
+    B, Hq, Hkv, Lq, Lk, W = case
+    seed = 3000 + sum(case)
+    print(f"prefill_attn_stats dt={dt} B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} W={W} seed={seed}", flush=True)
+    q, k, v = _inputs(dev, dt, B, Hq, Hkv, Lq, Lk, seed, pad=40)
+    scale = 1.0 / math.sqrt(128)
+    plain = ops.prefill_attn(q, k, v, scale)
+    st = torch.full((B, Hq, W, 2), float("nan"), dtype=torch.float32, device=dev)
+    out = ops.prefill_attn(q, k, v, scale, stat_out=st)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    G = Hq // Hkv
+    qn, kn = as_np(q), as_np(k)
+    rows, ks = [], []
+    for b in range(B):
+        for h in range(Hkv):
+            for w in range(W):
+                i = Lq - W + w
+                rows.append(qn[b, h * G:(h + 1) * G, i])
+                ks.append(kn[b, h, :Lk - Lq + i + 1])
+    ref = O.softmax_lse2(np.stack(rows), ks, Lk, scale).reshape(B, Hkv, W, G).transpose(0, 1, 3, 2)
+    ref = ref.reshape(B, Hq, W)
+    got = as_np(st)
+    M, Ls = got[..., 0], got[..., 1]
+    assert np.isfinite(M).all() and (Ls >= 1.0).all()
+    assert np.abs(M + np.log2(Ls) - ref).max() <= 1e-3
+    # The bound: the row maxima of the scaled base-2 scores.
+    smax = np.array([(scale * math.log2(math.e) * (r.astype(np.float64) @ kk.astype(np.float64).T)).max(axis=-1)
+                     for r, kk in zip(rows, ks)]).reshape(B, Hkv, W, G).transpose(0, 1, 3, 2).reshape(B, Hq, W)
+    assert (M <= smax + 1e-3).all() and (M >= smax - 8 - 1e-3).all()
+
+
+def test_prefill_stats_rejects_bad_rows(dev):
+    q, k, v = _inputs(dev, "bf16", 1, 4, 1, 16, 16, 5)
+    for shape in ((1, 4, 17, 2), (1, 4, 0, 2), (1, 2, 8, 2)):
+        st = torch.zeros(shape, dtype=torch.float32, device=dev)
+        with pytest.raises((RuntimeError, ValueError)):
+            ops.prefill_attn(q, k, v, 0.1, stat_out=st)

@@ -213,3 +213,48 @@ def test_end_to_end_indices_outside_tie_band(dev):
         band = [t for t in diff if abs(ref_s[h][t] - tau) > 1e-5 * abs(tau)]
         assert not band, f"head {h}: {len(band)} positions differ outside the tie band"
         assert len(diff) <= 0.01 * caps[h]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,Hkv,G,W,Ws,heads", [(1, 3, 4, 32, 32, (0, 1, 2)), (2, 4, 4, 32, 64, (1, 3)),
+                                                (1, 2, 7, 32, 32, (0, 1)), (1, 2, 1, 16, 16, (0, 1)),
+                                                (2, 2, 2, 8, 8, (1,))])
+def test_window_scores_with_attention_stats(dev, dtype, B, Hkv, G, W, Ws, heads):
+    """Window scores and last-query scores with the prefill attention's
+    statistics (one key pass) against the oracle (2e-4) and against the
+    two-pass scorer on the same inputs (2e-5)."""
+    from heterocache_amd import ops
+    L = 2500
+    if dtype == torch.float32 and G * W > 128:
+        pytest.skip("float32 scoring holds at most 128 query rows")
+    print(f"window scores with stats dtype={dtype} B={B} Hkv={Hkv} G={G} W={W} Ws={Ws} heads={heads}", flush=True)
+    q, k = qk(dev, B, Hkv * G, Hkv, L, L, dtype, 11 + G + W, sinks=True)
+    v = torch.randn(k.shape, generator=torch.Generator().manual_seed(12)).to(dtype).to(dev)
+    scale = 1 / math.sqrt(128)
+    st = torch.full((B, Hkv * G, Ws, 2), float("nan"), dtype=torch.float32, device=dev)
+    ops.prefill_attn(q, k, v, scale, stat_out=st)
+    s1 = compress.window_scores(q, k, heads, G, W, "maxpool", 7, window_keep=True, stats=st)
+    s0 = compress.window_scores(q, k, heads, G, W, "maxpool", 7, window_keep=True)
+    l1 = compress.last_query_scores(q, k, heads, G, "avgpool", 5, stats=st)
+    l0 = compress.last_query_scores(q, k, heads, G, "avgpool", 5)
+    torch.cuda.synchronize()
+    qn, kn = as_np(q), as_np(k)
+    for b in range(B):
+        for j, h in enumerate(heads):
+            r = b * len(heads) + j
+            ref = O.window_scores(qn[b, h * G:(h + 1) * G, -W:][None], kn[b, h][None], "maxpool", 7,
+                                  window_keep=True)[0]
+            assert rel_err(as_np(s1[r]), ref) < 2e-4, (b, h)
+            lref = O.last_query_scores(qn[b, h * G:(h + 1) * G, -1][None], kn[b, h][None], "avgpool", 5)[0]
+            assert rel_err(as_np(l1[r]), lref) < 2e-4, (b, h)
+    assert rel_err(as_np(s1), as_np(s0)) < 2e-5
+    assert rel_err(as_np(l1), as_np(l0)) < 2e-5
+
+
+def test_window_scores_with_stats_rejects_rounding(dev):
+    q, k = qk(dev, 1, 4, 1, 64, 64, torch.bfloat16, 3)
+    st = torch.zeros((1, 4, 32, 2), dtype=torch.float32, device=dev)
+    with pytest.raises(ValueError):
+        compress.window_scores(q, k, [0], 4, 32, "maxpool", 7, window_keep=True, round_dtype=torch.bfloat16, stats=st)
+    with pytest.raises(ValueError):
+        compress.window_scores(q, k, [0], 4, 32, "maxpool", 7, causal=False, stats=st)
