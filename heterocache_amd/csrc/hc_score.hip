@@ -520,6 +520,165 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   }
 }
 
+// ---------------------------------------------------------------------------
+// Probability pass with the pooling fused (summed windows of whole 16-row
+// tiles, W a multiple of 16, pooling kernels up to 2 * kPpMaxHalf + 1): the
+// window sums of the workgroup's chunk stay in LDS (one strip row per query
+// head) and the chunk is pooled and maxed over the group there, so neither
+// the window sums nor a pooling launch go through HBM.  A workgroup runs the
+// chunks [c0, c1) in order: the pooled output trails the chunk by the pool
+// half-width P (its last P positions wait for the next chunk's first ones),
+// and the 16 positions before the run and after it are recomputed as one
+// extra sub-tile each (by waves 0 and kScoreWaves - 1).  Same arithmetic, in
+// the same order, as score_probs_kernel followed by score_pool_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kPpMargin = 16;                       // positions of a margin sub-tile
+constexpr int kPpPitch = kScoreChunk + kPpMargin;   // strip row: the chunk, then the run's right margin
+constexpr int kPpMaxHalf = 4;
+
+// Window sums of query head g over tokens tw + 16u + (lane & 15), u < NU,
+// written (by the lanes of row group 0) to dst[g * pitch + 16u + (lane & 15)],
+// the pad value for tokens outside [0, span).
+template <typename T, int RM, bool MASK, int NU>
+__device__ __forceinline__ void window_sums(const ScoreArgs& a, const typename Elem<T>::vec8 (&k)[NU][4],
+                                            const T* s_q, const float* s_m, const float* s_iz, int tw, int lane,
+                                            float* dst, int pitch, float pad) {
+  const int rg = lane >> 4;
+  float gsum[NU];
+#pragma unroll
+  for (int u = 0; u < NU; ++u) gsum[u] = 0.f;
+  for (int nt = 0; nt < a.NT; ++nt) {
+    const int r0 = 16 * nt + 4 * rg;
+    float M[4], IZ[4];
+    int limit[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      M[j] = s_m[r0 + j];
+      IZ[j] = RM != 0 ? s_iz[r0 + j] : 0.f;
+      limit[j] = row_limit(a, r0 + j);
+    }
+    float x[NU][4];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) subtile_logits_rows<T, RM, MASK, RM == 0>(a, k[u], s_q, nt, tw + 16 * u, lane, limit, x[u]);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      float p[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (RM == 0)
+          p[j] = fast_exp2(fmaf(x[u][j], a.scale2, -M[j]));
+        else
+          p[j] = x[u][j] == -INFINITY ? 0.f : round_fixed<RM>(fast_exp2(x[u][j] - M[j]) * IZ[j]);
+      }
+      gsum[u] += (p[0] + p[1]) + (p[2] + p[3]);
+    }
+    if (((16 * (nt + 1)) % a.W) == 0) {  // the last tile of a query head
+      const int g = (16 * nt) / a.W;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        const int t = tw + 16 * u + (lane & 15);
+        const float v = rows4_sum(gsum[u]);
+        if (rg == 0) dst[g * pitch + 16 * u + (lane & 15)] = t >= 0 && t < a.span ? round_fixed<RM>(v) : pad;
+        gsum[u] = 0.f;
+      }
+    }
+  }
+}
+
+template <typename T, bool STORE, int RM, int POOL, int P>
+__global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 : 3) void score_probs_pool_kernel(ScoreArgs a, StatsView stats,
+                                                                           float* __restrict__ S) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr float kPad = POOL == 0 ? 0.f : -INFINITY;
+  T* s_q = reinterpret_cast<T*>(smem);
+  const int rows = a.NT * 16;
+  float* s_m = reinterpret_cast<float*>(smem + (size_t)rows * kQPitch * sizeof(T));  // [rows]
+  float* s_iz = s_m + rows;                                                           // [rows], casts only
+  float* strip = s_iz + (RM != 0 ? rows : 0);  // [G][kPpPitch]
+  float* mrg = strip + a.G * kPpPitch;         // [2][G][kPpMargin]: the 16 positions before the chunk
+  const int job = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nchunks = (a.span + kScoreChunk - 1) / kScoreChunk;
+  const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
+  if (c0 >= c1) return;  // uniform per workgroup
+  const int woff = wave * 16 * kSubTiles;
+  KRegs<T> ka;
+  load_k_chunk<T, STORE>(a, job, c0 * kScoreChunk + woff, lane, ka);
+  stage_queries<T>(a, job, s_q);
+  for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
+    const float* st = stats.row(a, job, r);  // rows = R here: W is a multiple of 16
+    if constexpr (RM == 0) {
+      s_m[r] = st[0] + __log2f(st[1]);
+    } else {
+      s_m[r] = st[0];
+      s_iz[r] = 1.f / st[1];
+    }
+  }
+  __syncthreads();
+  const int min_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W : a.L - 1;
+  const bool acc_out = (a.flags & HC_SCORE_ACCUMULATE) != 0;
+  float* const out = S + (int64_t)job * a.span;
+  for (int c = c0; c < c1; ++c) {
+    const int cb = c * kScoreChunk;
+    float* mcur = mrg + ((c - c0) & 1) * a.G * kPpMargin;
+    float* mnext = mrg + ((c - c0 + 1) & 1) * a.G * kPpMargin;
+    if (cb + kScoreChunk - 1 > min_limit)
+      window_sums<T, RM, true, kSubTiles>(a, ka.v, s_q, s_m, s_iz, cb + woff, lane, strip + woff, kPpPitch, kPad);
+    else
+      window_sums<T, RM, false, kSubTiles>(a, ka.v, s_q, s_m, s_iz, cb + woff, lane, strip + woff, kPpPitch, kPad);
+    if (c == c0 && wave == 0) {
+      // The run's left margin: positions cb - 16 .. cb - 1.
+      if (cb > 0) {
+        typename Elem<T>::vec8 km[1][4];
+        load_k_subtile<T, STORE>(a, job, cb - kPpMargin, lane, km[0]);
+        window_sums<T, RM, true, 1>(a, km, s_q, s_m, s_iz, cb - kPpMargin, lane, mcur, kPpMargin, kPad);
+      } else {
+        for (int i = lane; i < a.G * kPpMargin; i += 64) mcur[i] = kPad;
+      }
+    }
+    if (c == c1 - 1 && wave == kScoreWaves - 1) {
+      // The run's right margin: positions cb + 256 .. cb + 271.
+      const int te = cb + kScoreChunk;
+      if (te < a.span) {
+        typename Elem<T>::vec8 km[1][4];
+        load_k_subtile<T, STORE>(a, job, te, lane, km[0]);
+        window_sums<T, RM, true, 1>(a, km, s_q, s_m, s_iz, te, lane, strip + kScoreChunk, kPpPitch, kPad);
+      } else {
+        for (int i = lane; i < a.G * kPpMargin; i += 64) strip[(i / kPpMargin) * kPpPitch + kScoreChunk + i % kPpMargin] = kPad;
+      }
+    }
+    if (c + 1 < c1) load_k_chunk<T, STORE>(a, job, cb + kScoreChunk + woff, lane, ka);
+    __syncthreads();
+    // Pool positions [lo, hi): the previous chunk's last P, then this chunk's
+    // up to its last P (all of them in the run's last chunk).
+    const int lo = c == c0 ? cb : cb - P;
+    const int hi = min(c == c1 - 1 ? cb + kScoreChunk : cb + kScoreChunk - P, a.span);
+    for (int x = lo + (int)threadIdx.x; x < hi; x += kScoreWaves * 64) {
+      const int i = x - cb;
+      float best = -INFINITY;
+      for (int g = 0; g < a.G; ++g) {
+        const float* srow = strip + g * kPpPitch;
+        const float* mrow = mcur + g * kPpMargin + kPpMargin;
+        float acc = kPad;
+#pragma unroll
+        for (int d = -P; d <= P; ++d) {
+          const int li = i + d;
+          const float v = li < 0 ? mrow[li] : srow[li];
+          acc = POOL == 0 ? acc + v : fmaxf(acc, v);
+        }
+        if constexpr (POOL == 0) acc = acc / (float)(2 * P + 1);
+        best = fmaxf(best, round_fixed<RM>(acc));
+      }
+      out[x] = acc_out ? out[x] + best : best;
+    }
+    // The chunk's last 16 positions are the next chunk's left neighbours.
+    if (c + 1 < c1)
+      for (int i = threadIdx.x; i < a.G * kPpMargin; i += kScoreWaves * 64)
+        mnext[i] = strip[(i / kPpMargin) * kPpPitch + kScoreChunk - kPpMargin + i % kPpMargin];
+    __syncthreads();
+  }
+}
+
 // kPoolTile consecutive positions of one (job, w') per workgroup, four
 // consecutive ones per thread (one 16-byte load per query head); each head's
 // strip and its pooling halo are staged in LDS in turn.  Kernels up to
@@ -1193,6 +1352,41 @@ static int plan_chunks(const void* fn, size_t lds, int njobs, int nchunks, Score
   return (nchunks + a.cpw - 1) / a.cpw;
 }
 
+template <typename T, int RM, int POOL, int P>
+static void launch_fused(ScoreArgs a, int njobs, StatsView sv, float* scores, hipStream_t s) {
+  const int rows = a.NT * 16;
+  const size_t lds = (size_t)rows * kQPitch * sizeof(T) + (size_t)rows * (RM != 0 ? 2 : 1) * sizeof(float) +
+                     (size_t)a.G * (kPpPitch + 2 * kPpMargin) * sizeof(float);
+  auto fn = score_probs_pool_kernel<T, false, RM, POOL, P>;
+  const int nchunks = (a.span + kScoreChunk - 1) / kScoreChunk;
+  const int gx = plan_chunks(reinterpret_cast<const void*>(fn), lds, njobs, nchunks, a);
+  hipLaunchKernelGGL(fn, dim3(gx, njobs), dim3(kScoreWaves * 64), lds, s, a, sv, scores);
+}
+
+// The fused probability + pooling pass over natural-layout keys; the
+// rounding mode of an instance is the one its key type takes (or none).
+template <typename T>
+static int launch_probs_pool_fused(ScoreArgs a, int njobs, int pooling, int kernel, StatsView sv, float* scores,
+                                   hipStream_t s) {
+  constexpr int kRm = std::is_same<T, __bf16>::value ? 1 : std::is_same<T, _Float16>::value ? 2 : 0;
+  const bool cast = (a.flags & (HC_SCORE_ROUND_BF16 | HC_SCORE_ROUND_F16)) != 0;
+#define HC_FUSED_P(RM, PL)                                                           \
+  switch (kernel / 2) {                                                              \
+    case 0: launch_fused<T, RM, PL, 0>(a, njobs, sv, scores, s); break;              \
+    case 1: launch_fused<T, RM, PL, 1>(a, njobs, sv, scores, s); break;              \
+    case 2: launch_fused<T, RM, PL, 2>(a, njobs, sv, scores, s); break;              \
+    case 3: launch_fused<T, RM, PL, 3>(a, njobs, sv, scores, s); break;              \
+    default: launch_fused<T, RM, PL, 4>(a, njobs, sv, scores, s); break;             \
+  }
+  if (!cast) {
+    if (pooling == 0) { HC_FUSED_P(0, 0) } else { HC_FUSED_P(0, 1) }
+  } else if constexpr (kRm != 0) {
+    if (pooling == 0) { HC_FUSED_P(kRm, 0) } else { HC_FUSED_P(kRm, 1) }
+  }
+#undef HC_FUSED_P
+  return check_launch("hc_score(probs+pool)");
+}
+
 // The probability pass (row statistics given) and the pooling pass:
 // scores over [0, a.span), A = the window-summed probabilities.
 template <typename T, bool STORE>
@@ -1203,6 +1397,9 @@ static int launch_probs_pool(ScoreArgs a, int njobs, int pooling, int kernel, St
   const int rm = (a.flags & HC_SCORE_ROUND_BF16) ? 1 : (a.flags & HC_SCORE_ROUND_F16) ? 2 : 0;
   int rc;
   const int nchunks_span = (a.span + kScoreChunk - 1) / kScoreChunk;
+  if (nchunks_span > 0 && !STORE && (a.flags & HC_SCORE_SUM_WINDOW) && a.W % 16 == 0 && kernel / 2 <= kPpMaxHalf &&
+      (rm == 0 || rm == (std::is_same<T, __bf16>::value ? 1 : std::is_same<T, _Float16>::value ? 2 : -1)))
+    return launch_probs_pool_fused<T>(a, njobs, pooling, kernel, sv, scores, s);
   if (nchunks_span > 0) {
     const int wm = !(a.flags & HC_SCORE_SUM_WINDOW) ? kWinNone
                    : a.W >= 16                       ? kWin16
