@@ -797,7 +797,7 @@ __device__ __forceinline__ float fin_prob(float x, float m, float iz) {
   return x == -INFINITY ? 0.f : round_fixed<RMODE>(fast_exp2(x - m) * iz);
 }
 
-constexpr int kFinHalo = 32;  // >= kPoolMaxHalf, keeps the strip 16-byte aligned
+constexpr int kFinHalo = 32;  // >= kPoolMaxKernel / 2, keeps the strip 16-byte aligned
 constexpr int kFinHeads = 4;  // query heads whose loads are in flight together
 constexpr int kFinWaveSlots = 6;  // the left halo, the four waves of a tile, the right halo
 
