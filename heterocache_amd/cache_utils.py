@@ -76,11 +76,13 @@ class HeteroCacheConfig:
     two-pass scorer runs.
     attention_stats_scoring: let the prefill attention report the softmax
     statistics of the last window_size queries (hc_prefill_attn_stats), so
-    that prefill_select and init_coefficient score in one pass over the keys
+    that prefill_select's observation-window scorer reads the keys once
     (hc_score_with_stats) instead of a statistics pass and a probability
-    pass.  The scores are those of the same uncast float32 softmax; with
-    round_scores, or when the prefill call holds fewer than window_size
-    queries (a short last chunk), the two-pass scorer runs.
+    pass.  The scores are those of the same uncast float32 softmax.  It
+    applies to windows of at least 32 query rows (group * window_size); with
+    round_scores, for narrower windows (the default last-query scorer among
+    them) or when the prefill call holds fewer than window_size queries (a
+    short last chunk), the two-pass scorer runs.
     tier_placement: where the satellites' full-KV tier lives when
     real_offload is set -- "host" (pinned host memory, retrieval read over
     the host link), "device" (an HBM arena, retrieval a device gather) or
@@ -497,19 +499,24 @@ class HeteroCache(DynamicCache):
 
     def prefill_stat_rows(self, query_states, layer_idx):
         """Query rows whose softmax statistics the prefill attention of this
-        call should report for the selection scorers (0: none; see
-        attention_stats_scoring).  The scorers read the last window_size
-        query rows over the same keys as the attention."""
+        call should report for prefill_select's window scorer (0: none; see
+        attention_stats_scoring).  The scorer reads the last window_size
+        query rows over the same keys as the attention.  Windows of fewer
+        than 32 query rows (group * window_size; the last-query scorers of
+        prefill_select and init_coefficient among them) keep the two-pass
+        scorer, which stores their few logits and is the faster form there
+        (55.6 against 61.0 us for 8 heads x 128K at group 4, window 1)."""
         if not self.attn_stats or self.round_scores or self.prefill_pending(layer_idx):
             return 0
         W = self.window_size
-        return W if query_states.shape[2] >= W else 0
+        return W if W > 1 and self.num_key_value_groups * W >= 32 and query_states.shape[2] >= W else 0
 
     def init_coefficient(self, query_states, key_states, layer_idx, stats=None):
         """Pivot reference sets: top-base of the pooled last-query scores
         (heterocache/cache_utils.py:1149-1190), kept as device bitmasks.
-        stats: the prefill attention's statistics of the last queries
-        (prefill_stat_rows), which let the scorer read the keys once."""
+        stats (the prefill attention's statistics, prefill_stat_rows) is
+        accepted for the call's symmetry with prefill_select; the last-query
+        scorer's few rows take the two-pass form, which is faster there."""
         if self.prefill_pending(layer_idx):
             return
         query_states = self._prefill_queries(query_states, layer_idx)
@@ -522,7 +529,7 @@ class HeteroCache(DynamicCache):
         L = key_states.shape[-2]
         G = self.num_key_value_groups
         scores = compress.last_query_scores(query_states, key_states, pivots, G, self.pooling, self.kernel_size,
-                                            round_dtype=self._round_dtype(query_states.dtype), stats=stats)
+                                            round_dtype=self._round_dtype(query_states.dtype))
         K = min(self.base_compress_len, L)
         idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
         if self.observer is not None:
@@ -596,8 +603,7 @@ class HeteroCache(DynamicCache):
                                             round_dtype=self._round_dtype(query_states.dtype), stats=stats)
         else:
             scores = compress.last_query_scores(query_states, key_states, range(n_c), G, self.pooling,
-                                                self.kernel_size, round_dtype=self._round_dtype(query_states.dtype),
-                                                stats=stats)
+                                                self.kernel_size, round_dtype=self._round_dtype(query_states.dtype))
         idx, counts = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0)
         if self.observer is not None:
             self.observer("prefill_select", layer=layer_idx, rows=rows, scores=scores, idx=idx, counts=counts)

@@ -44,12 +44,12 @@ def head_data(seed=0):
 
 
 def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True, groups=1,
-        chunks=None, tier="host", overlap=False, attn_stats=True):
+        chunks=None, tier="host", overlap=False):
     """tier: "host" / "device" placement of the full-KV tier, or "prefill"
     (real_offload=False: the prefill K/V kept as the tier).  overlap: batched
-    checks on the side stream (overlap_drift_check).  attn_stats: the
-    prefill selection scores from the prefill attention's statistics, as the
-    model's attention hands them over (else the two-pass scorer)."""
+    checks on the side stream (overlap_drift_check).  The prefill runs as the
+    model's attention runs it (prefill_stat_rows asks for no statistics at
+    window_size 1)."""
     torch.manual_seed(0)
     B, Hq, Hkv, NL, D = 1, 32, 8, 2, 128
     data = head_data()
@@ -65,7 +65,7 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
     def select(qc, kc, vc, layer):
         st = None
         W = cache.prefill_stat_rows(qc, layer)
-        if attn_stats and W:
+        if W:
             st = torch.empty((B, Hq, W, 2), dtype=torch.float32, device=dev)
             ops.prefill_attn(qc, kc, vc, 1 / math.sqrt(D), stat_out=st)
         cache.init_coefficient(qc, kc, layer, stats=st)
@@ -122,7 +122,7 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
     # decode launches reported (every cycle, the first included).
     one_pass = batched and not select_first
     assert cache.one_pass_checks == ((steps // 5) * groups if one_pass else 0)
-    assert cache.attn_stats_layers == (NL if attn_stats else 0)
+    assert cache.attn_stats_layers == 0
     assert triggers == orc.triggers
     for layer in range(NL):
         store = cache.stores[layer]
@@ -156,12 +156,6 @@ def test_llama_order_overlapped_checks(dev, groups, tier):
     store equals the oracle's, as on the main stream."""
     trig = run(dev, torch.float32, groups=groups, tier=tier, overlap=True)
     assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
-
-
-def test_llama_order_two_pass_prefill_scoring(dev):
-    """The prefill selection without the attention's statistics (the
-    two-pass scorer) gives the oracle's triggers and stores too."""
-    run(dev, torch.float32, attn_stats=False)
 
 
 def test_llama_order_layer_by_layer_checks(dev):
@@ -312,3 +306,60 @@ def test_reference_cast_chain(dev, dtype, io, step):
             ks, vs = store.read_rows([r], n)
             ok, ov = orc.rows[layer][r]
             assert n == len(ok) and np.array_equal(as_np(ks[0]), ok) and np.array_equal(as_np(vs[0]), ov)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_observation_window_from_attention_statistics(dev, dtype):
+    """window_size = 32 (128 query rows per KV head): prefill_select scores
+    from the prefill attention's statistics (one key pass) as the patched
+    attention hands them over.  The scores are within 2e-5 of the two-pass
+    scorer's on the same inputs and within 2e-4 of the oracle's window
+    scores, and the two caches' stores are identical on this seed."""
+    B, Hq, Hkv, NL, D, L, W = 1, 32, 8, 2, 128, 3000, 32
+    data = head_data()
+    seen = {}
+
+    def make(tag):
+        cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
+                                max_gen_len=4, decode_step=5, pooling="maxpool", kernel_size=7,
+                                num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, window_size=W,
+                                attention_stats_scoring=tag == "stats")
+        cache = HeteroCache(cfg)
+        cache.observer = lambda event, **kw: seen.setdefault((tag, event, kw.get("layer")), kw.get("scores"))
+        return cache
+
+    g = torch.Generator().manual_seed(21)
+    qs = [torch.randn((B, Hq, L, D), generator=g).to(dtype).to(dev) for _ in range(NL)]
+    ks = [torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev) for _ in range(NL)]
+    vs = [torch.randn((B, Hkv, L, D), generator=g).to(dtype).to(dev) for _ in range(NL)]
+    caches = {"stats": make("stats"), "two_pass": make("two_pass")}
+    for tag, cache in caches.items():
+        for layer in range(NL):
+            kc, vc = cache.update(ks[layer], vs[layer], layer)
+            st = None
+            n = cache.prefill_stat_rows(qs[layer], layer)
+            assert n == (W if tag == "stats" else 0)
+            if n:
+                st = torch.empty((B, Hq, n, 2), dtype=torch.float32, device=dev)
+                ops.prefill_attn(qs[layer], kc, vc, 1 / math.sqrt(D), stat_out=st)
+            cache.init_coefficient(qs[layer], kc, layer, stats=st)
+            cache.prefill_select(qs[layer], kc, vc, layer, stats=st)
+    torch.cuda.synchronize()
+    assert caches["stats"].attn_stats_layers == NL and caches["two_pass"].attn_stats_layers == 0
+    G = Hq // Hkv
+    for layer in range(NL):
+        s1 = as_np(seen[("stats", "prefill_select", layer)])
+        s0 = as_np(seen[("two_pass", "prefill_select", layer)])
+        assert np.abs(s1 - s0).max() / np.abs(s0).max() < 2e-5
+        qn, kn = as_np(qs[layer]), as_np(ks[layer])
+        n_c = data["need_to_compress_counts"][layer]
+        ref = O.window_scores(np.stack([qn[0, h * G:(h + 1) * G, -W:] for h in range(n_c)]), kn[0, :n_c], "maxpool",
+                              7, window_keep=True)
+        assert np.abs(s1 - ref).max() / np.abs(ref).max() < 2e-4
+        a, b = caches["stats"].stores[layer], caches["two_pass"].stores[layer]
+        assert np.array_equal(a.host_len, b.host_len)
+        for r in range(B * Hkv):
+            m = int(a.host_len[r])
+            ka, va = a.read_rows([r], m)
+            kb, vb = b.read_rows([r], m)
+            assert torch.equal(ka, kb) and torch.equal(va, vb), (layer, r)
