@@ -258,3 +258,27 @@ def test_window_scores_with_stats_rejects_rounding(dev):
         compress.window_scores(q, k, [0], 4, 32, "maxpool", 7, window_keep=True, round_dtype=torch.bfloat16, stats=st)
     with pytest.raises(ValueError):
         compress.window_scores(q, k, [0], 4, 32, "maxpool", 7, causal=False, stats=st)
+
+
+def test_window_scores_with_attention_stats_128k(dev):
+    """At the full 128K context (8 KV heads, GQA 4, W = 32, bf16): scores
+    from the attention's statistics against the two-pass scorer (2e-5) for
+    every head, and against the oracle for one head (2e-4)."""
+    from heterocache_amd import ops
+    B, Hkv, G, W, L = 1, 8, 4, 32, 131072
+    print(f"window scores with stats at L={L}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn((B, Hkv * G, W, 128), generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn((B, Hkv, L, 128), generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn((B, Hkv, L, 128), generator=g).to(torch.bfloat16).to(dev)
+    st = torch.full((B, Hkv * G, W, 2), float("nan"), dtype=torch.float32, device=dev)
+    ops.prefill_attn(q, k, v, 1 / math.sqrt(128), stat_out=st)
+    s1 = compress.window_scores(q, k, range(Hkv), G, W, "maxpool", 7, window_keep=True, stats=st)
+    s0 = compress.window_scores(q, k, range(Hkv), G, W, "maxpool", 7, window_keep=True)
+    torch.cuda.synchronize()
+    assert s1.shape == (Hkv, L - W)
+    assert rel_err(as_np(s1), as_np(s0)) < 2e-5
+    h = 5
+    qn, kn = as_np(q[0, h * G:(h + 1) * G]), as_np(k[0, h])
+    ref = O.window_scores(qn[None], kn[None], "maxpool", 7, window_keep=True)[0]
+    assert rel_err(as_np(s1[h]), ref) < 2e-4
