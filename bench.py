@@ -653,6 +653,33 @@ def prefill_attention_phase(args, torch, dev):
     return out
 
 
+def north_star_summary(rec, args):
+    """The step target in its own terms: the attention and retrieval-gather
+    kernels of the 128K, ratio-0.5 decode step against the HBM roofline, and
+    the retrieval time the step does not hide.  Attention: the headline
+    (graph-replayed step, algorithmic K/V bytes).  Gather: the retrieval's
+    rows per check (the reference head JSON's satellites x top-1024, K and V
+    read once and written once) at the device-gather rate of the gather
+    phase, amortised over the check's 5 steps.  The full step, drift check
+    included, is reported beside it."""
+    fs = rec["full_decode_step"]
+    dev_gather = rec["gather"]["device_src"]
+    attn_bytes = rec["roofline"]["bytes_per_launch"] * args.layers
+    attn_ms = rec["ms_per_step"]
+    ret_bytes = fs["satellites"] * fs["retrieval_topk"] * 128 * 2 * 2 * 2  # K and V, read + written
+    gather_ms = ret_bytes / (dev_gather["gbs"] * 1e6)
+    S = fs["decode_step"]
+    both = (attn_bytes + ret_bytes / S) / ((attn_ms + gather_ms / S) * 1e-3) / 1e9
+    return {"attention_frac": rec["roofline"]["frac"],
+            "gather_frac": round(dev_gather["gbs"] / HBM_PEAK_GBS, 4),
+            "attention_plus_gather_frac": round(both / HBM_PEAK_GBS, 4),
+            "retrieval_gather_ms_per_check": round(gather_ms, 4),
+            "retrieval_exposed_ms_per_check": fs.get("retrieval_exposed_ms_per_check"),
+            "retrieval_tier": fs.get("tier"),
+            "host_tier_retrieval_exposed_ms_per_check": fs.get("host_tier_retrieval_exposed_ms_per_check"),
+            "full_step_frac_with_drift_check": fs["roofline"]["frac"]}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -784,6 +811,8 @@ def main():
         rec["decode_other_configs"] = decode_configs_phase(args, torch, dev)
         rec["baseline_compressors"] = baseline_compressors_phase(args, torch, dev)
         rec["head_analysis"] = head_analysis_phase(args, torch, dev)
+    if "full_decode_step" in rec and "gather" in rec:
+        rec["north_star"] = north_star_summary(rec, args)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(budgets[0], args.cpu_seconds)
     print(json.dumps(rec))
