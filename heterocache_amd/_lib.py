@@ -59,6 +59,7 @@ SIGNATURES = {
                                       c_void_p, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t,
                                       c_int, c_void_p, c_void_p]),
     "hc_prefill_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "hc_prefill_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int, c_int]),
     "hc_gather_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p,
                                c_void_p, c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p]),
     "hc_head_pool": (c_int, [c_int, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_int, c_int, c_void_p,

@@ -69,7 +69,16 @@ struct PfArgs {
   // (batch, query head): st[((b * Hq + hq) * st_rows + w) * 2 + {0, 1}].
   float* st;
   int st_rows;
+  // Split over the keys (short query blocks over long key ranges): grid
+  // slice `split` of nsplit takes iterations [split * its, (split + 1) * its)
+  // and writes its unnormalised partials to part (kPfPartStride floats per
+  // (query, split)); prefill_merge_kernel combines them.  nsplit = 1: no split.
+  int nsplit, its;
+  float* part;
 };
+
+// One partial: 128 unnormalised output channels, then (m, l); 16-byte rows.
+constexpr int kPfPartStride = HC_HEAD_DIM + 4;
 
 // LDS: two K buffers and one V buffer of kPfTiles tiles each.
 template <typename T>
@@ -137,7 +146,7 @@ __device__ __forceinline__ void wait_lds_dma_but() {
   __builtin_amdgcn_s_waitcnt(0x0f70 | N);
 }
 
-template <typename T>
+template <typename T, bool SPLIT>
 __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_attn_kernel(const PfArgs a) {
   typedef typename Elem<T>::vec8 vec8;
   extern __shared__ __attribute__((aligned(16))) unsigned char pf_lds[];
@@ -154,7 +163,9 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
   const int row = x % a.rows;
   const int rest = x / a.rows;
   const int gi = rest % G;
-  const int qb = a.nqb - 1 - rest / G;
+  const int rest2 = rest / G;
+  const int split = SPLIT ? rest2 % a.nsplit : 0;
+  const int qb = a.nqb - 1 - (SPLIT ? rest2 / a.nsplit : rest2);
   const int b = row / a.Hkv, kvh = row % a.Hkv, hq = kvh * G + gi;
 
   const T* qbase = reinterpret_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh;
@@ -163,7 +174,10 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
 
   const int shift = a.Lk - a.Lq;  // position of query i is shift + i
   const int q_last = min(qb * kPfBlockQ + kPfBlockQ - 1, a.Lq - 1);
-  const int nit = (shift + q_last + 1 + kPfKeys - 1) / kPfKeys;
+  const int nit_all = (shift + q_last + 1 + kPfKeys - 1) / kPfKeys;
+  // This workgroup's iterations (all of them without a split).
+  const int it0 = SPLIT ? min(split * a.its, nit_all) : 0;
+  const int nit = SPLIT ? min(it0 + a.its, nit_all) : nit_all;
   const int qw0 = qb * kPfBlockQ + wave * kPfWaveQ;
   const bool active = qw0 < a.Lq;
   const int pos_lo = shift + qw0;                           // first query position of this wave
@@ -253,13 +267,17 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
   // buffer, loaded between two barriers around the P.V step: V(it+1)
   // arrives while the next iteration forms its scores and probabilities.
   // 48 KB of LDS per workgroup leaves room for three workgroups per CU.
-  stage_k(0, 0);
-  stage_v(0);
+  // (An empty split range stages nothing: its first tile would lie past the
+  // keys; its partials come out empty.)
+  if (it0 < nit) {
+    stage_k(0, it0);
+    stage_v(it0);
+  }
   wait_lds_dma();
   __syncthreads();
 
-  for (int it = 0; it < nit; ++it) {
-    const int cur = it & 1;
+  for (int it = it0; it < nit; ++it) {
+    const int cur = (it - it0) & 1;
     const int t0 = it * kPfKeys;
     const bool more = it + 1 < nit;
     if (more) stage_k(cur ^ 1, it + 1);
@@ -375,9 +393,21 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const float lt = rows4_sum(l[j]);
-    const float inv = 1.f / lt;
     const int qi = qw0 + 16 * j + n16;
     if (qi >= a.Lq) continue;
+    if constexpr (SPLIT) {
+      // Split: the unnormalised partial and its (m, l); the merge forms the
+      // output (and the statistics).
+      float* pp = a.part + (((int64_t)(b * a.Hq + hq) * a.Lq + qi) * a.nsplit + split) * kPfPartStride;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) *reinterpret_cast<f32x4*>(pp + 16 * db + 4 * g4) = o[db][j];
+      if (g4 == 0) {
+        pp[HC_HEAD_DIM] = m[j];
+        pp[HC_HEAD_DIM + 1] = lt;
+      }
+      continue;
+    }
+    const float inv = 1.f / lt;
     // The softmax state of query qi over its visible keys, as a scorer's
     // statistics pass would form it: m bounds the scaled base-2 scores (the
     // lazy rescale keeps it within 2^kPfLazy of their maximum) and lt is the
@@ -401,6 +431,37 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
   }
 }
 
+// Split partials of one query -> its output row (and, for the last st_rows
+// queries, its statistics): one workgroup per (batch, query head, query),
+// thread d = channel d.  Splits with no visible key (m = -inf) add nothing.
+template <typename T>
+__global__ __launch_bounds__(HC_HEAD_DIM) void prefill_merge_kernel(const PfArgs a) {
+  const int64_t qx = blockIdx.x;  // (b * Hq + hq) * Lq + qi
+  const int qi = (int)(qx % a.Lq);
+  const int bh = (int)(qx / a.Lq);
+  const int hq = bh % a.Hq, b = bh / a.Hq;
+  const float* pp = a.part + qx * a.nsplit * kPfPartStride;
+  const int d = threadIdx.x;
+  float M = -INFINITY;
+  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, pp[s * kPfPartStride + HC_HEAD_DIM]);
+  float L = 0.f, acc = 0.f;
+  for (int s = 0; s < a.nsplit; ++s) {
+    const float ms = pp[s * kPfPartStride + HC_HEAD_DIM];
+    if (ms == -INFINITY) continue;
+    const float e = fast_exp2(ms - M);
+    L = fmaf(pp[s * kPfPartStride + HC_HEAD_DIM + 1], e, L);
+    acc = fmaf(pp[s * kPfPartStride + d], e, acc);
+  }
+  T* o = reinterpret_cast<T*>(a.out) + b * a.o_sb + hq * a.o_sh + (int64_t)qi * a.o_st;
+  o[d] = Elem<T>::from_f32(acc / L);
+  const int w = qi - (a.Lq - a.st_rows);
+  if (a.st && w >= 0 && d == 0) {
+    float* so = a.st + (((int64_t)b * a.Hq + hq) * a.st_rows + w) * 2;
+    so[0] = M;
+    so[1] = L;
+  }
+}
+
 template <typename T>
 int launch_prefill(const PfArgs& a, hipStream_t stream) {
   hipLaunchKernelGGL((v_tiles_kernel<T>), dim3((unsigned)a.vt_tiles, (unsigned)a.rows), dim3(256), 0, stream, a);
@@ -409,14 +470,67 @@ int launch_prefill(const PfArgs& a, hipStream_t stream) {
   static std::once_flag once;
   static hipError_t attr = hipSuccess;
   std::call_once(once, [] {
-    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_kernel<T>),
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_kernel<T, false>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<T>());
+    if (attr == hipSuccess)
+      attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_attn_kernel<T, true>),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<T>());
   });
   if (attr != hipSuccess) return set_error(HC_ERR_HIP, "hc_prefill_attn: %s", hipGetErrorString(attr));
-  const int64_t grid = (int64_t)a.rows * (a.Hq / a.Hkv) * a.nqb;
-  hipLaunchKernelGGL((prefill_attn_kernel<T>), dim3((unsigned)grid), dim3(kPfThreads), pf_lds_bytes<T>(), stream,
-                     a);
-  return check_launch("hc_prefill_attn");
+  const int64_t grid = (int64_t)a.rows * (a.Hq / a.Hkv) * a.nqb * a.nsplit;
+  if (a.nsplit > 1)
+    hipLaunchKernelGGL((prefill_attn_kernel<T, true>), dim3((unsigned)grid), dim3(kPfThreads), pf_lds_bytes<T>(),
+                       stream, a);
+  else
+    hipLaunchKernelGGL((prefill_attn_kernel<T, false>), dim3((unsigned)grid), dim3(kPfThreads), pf_lds_bytes<T>(),
+                       stream, a);
+  if ((rc = check_launch("hc_prefill_attn"))) return rc;
+  if (a.nsplit > 1) {
+    const int64_t nq = (int64_t)(a.rows / a.Hkv) * a.Hq * a.Lq;
+    hipLaunchKernelGGL((prefill_merge_kernel<T>), dim3((unsigned)nq), dim3(HC_HEAD_DIM), 0, stream, a);
+    rc = check_launch("hc_prefill_attn(merge)");
+  }
+  return rc;
+}
+
+// Workgroups of the attention kernel resident on the current device at once
+// (0 when the query fails), cached per device and element size.
+template <typename T>
+int prefill_slots() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  static std::mutex mu;
+  static int cache[64];
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] > 0) return cache[dev];
+  int per_cu = 0, cus = 0;
+  const void* fn = reinterpret_cast<const void*>(&prefill_attn_kernel<T, true>);
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)pf_lds_bytes<T>()) != hipSuccess)
+    return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kPfThreads, pf_lds_bytes<T>()) != hipSuccess)
+    return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  cache[dev] = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  return cache[dev];
+}
+
+// Key splits for a launch: a split only pays where one query block per
+// (row, query head) leaves most of the device idle over a long key range
+// (decode-like and short-chunk calls).  Each split keeps at least
+// kPfMinSplitIts iterations; the split grid aims at one resident round.
+constexpr int kPfMinSplitIts = 8;
+int prefill_nsplit(int dtype, int batch, int q_heads, int kv_heads, int q_len, int kv_len) {
+  if (q_len > kPfBlockQ || batch <= 0 || q_heads <= 0 || kv_heads <= 0) return 1;
+  const int slots = dtype == HC_DTYPE_F32 ? prefill_slots<float>()
+                    : dtype == HC_DTYPE_F16 ? prefill_slots<_Float16>()
+                                            : prefill_slots<__bf16>();
+  const int64_t natural = (int64_t)batch * q_heads;  // one query block per (row, query head)
+  if (slots <= 0 || 2 * natural > slots) return 1;
+  const int nit = (kv_len + kPfKeys - 1) / kPfKeys;
+  const int by_keys = nit / kPfMinSplitIts;
+  const int by_slots = (int)(slots / natural);
+  const int n = std::min(by_keys, by_slots);
+  return n >= 2 ? n : 1;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -436,6 +550,21 @@ extern "C" size_t hc_prefill_workspace_size(int dtype, int batch, int kv_heads, 
   const int esz = dtype == HC_DTYPE_F32 ? 4 : 2;
   if (batch <= 0 || kv_heads <= 0 || kv_len <= 0) return 0;
   return (size_t)batch * kv_heads * v_tiles_per_row(kv_len) * HC_TILE_ELEMS * esz;
+}
+
+static size_t pf_align256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Split partials after the V tiles: [batch * q_heads * q_len][nsplit][kPfPartStride] floats.
+static size_t pf_part_bytes(int batch, int q_heads, int q_len, int nsplit) {
+  return nsplit > 1 ? (size_t)batch * q_heads * q_len * nsplit * kPfPartStride * sizeof(float) : 0;
+}
+
+extern "C" size_t hc_prefill_workspace_bytes(int dtype, int batch, int q_heads, int kv_heads, int q_len,
+                                             int kv_len) {
+  const size_t vt = hc_prefill_workspace_size(dtype, batch, kv_heads, kv_len);
+  if (vt == 0 || q_heads <= 0 || q_len <= 0) return vt;
+  const int ns = prefill_nsplit(dtype, batch, q_heads, kv_heads, q_len, kv_len);
+  return ns > 1 ? pf_align256(vt) + pf_part_bytes(batch, q_heads, q_len, ns) : vt;
 }
 
 static int prefill_entry(int dtype, const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
@@ -516,7 +645,19 @@ static int prefill_entry(int dtype, const void* q, const int64_t* q_strides, con
   a.scale_log2 = scale * 1.4426950408889634f;
   a.st = stat_out;
   a.st_rows = stat_rows;
-  const int64_t grid = (int64_t)a.rows * (q_heads / kv_heads) * a.nqb;
+  // A key split when it pays and the caller's workspace holds its partials
+  // (hc_prefill_workspace_bytes); otherwise one pass over the keys.
+  a.nsplit = 1;
+  a.its = 1 << 30;
+  a.part = nullptr;
+  const int ns = prefill_nsplit(dtype, batch, q_heads, kv_heads, q_len, kv_len);
+  if (ns > 1 && workspace_bytes >= pf_align256(need) + pf_part_bytes(batch, q_heads, q_len, ns)) {
+    const int nit = (kv_len + kPfKeys - 1) / kPfKeys;
+    a.nsplit = ns;
+    a.its = (nit + ns - 1) / ns;
+    a.part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + pf_align256(need));
+  }
+  const int64_t grid = (int64_t)a.rows * (q_heads / kv_heads) * a.nqb * a.nsplit;
   if (grid > 0x7fffffffLL) return set_error(HC_ERR_INVALID, "hc_prefill_attn: grid too large");
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {

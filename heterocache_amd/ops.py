@@ -327,7 +327,9 @@ def prefill_attn(q, k, v, scale, out=None, stream=None, stat_out=None):
                         [out.stride(0), out.stride(2), out.stride(1)]], dtype=np.int64)
     base = strides.ctypes.data
     code = dtype_code(q.dtype)
-    nbytes = lib.hc_prefill_workspace_size(code, B, Hkv, Lk)
+    # Room for the key-split partials where a short call splits (decode-like
+    # steps, a short last chunk).
+    nbytes = lib.hc_prefill_workspace_bytes(code, B, Hq, Hkv, Lq, Lk)
     # Per-call scratch from the caching allocator (stream-ordered reuse).
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=q.device)
     if stat_out is None:

@@ -242,6 +242,19 @@ int hc_prefill_attn_stats(int dtype, const void* q, const int64_t* q_strides, co
  * tiles, written and read within the call: no initialisation). */
 size_t hc_prefill_workspace_size(int dtype, int batch, int kv_heads, int kv_len);
 
+/* Workspace bytes that also hold the split partials of a short call: where
+ * one block of at most 128 queries per (batch, query head) would leave most
+ * of the current device idle over a long key range (decode-like steps of
+ * the baseline caches, a short last chunk of a chunked prefill), a
+ * workspace of this size lets hc_prefill_attn / hc_prefill_attn_stats split
+ * the keys across workgroups and merge the partials (flash-decoding style).
+ * With hc_prefill_workspace_size bytes the call runs unsplit.  The split
+ * changes the fp32 summation order, not the result's tolerance.  No
+ * reference counterpart: flash-attn picks its own split inside
+ * (heterocache/llama_model.py:353-361 and transformers' attention call for
+ * the baseline caches). */
+size_t hc_prefill_workspace_bytes(int dtype, int batch, int q_heads, int kv_heads, int q_len, int kv_len);
+
 /*
  * Gather token rows by index between natural layouts:
  *   dst[dst_off[j] + t*dst_tok_stride + c] = src[src_off[j] + i*src_tok_stride + c],

@@ -165,3 +165,83 @@ def test_prefill_stats_rejects_bad_rows(dev):
         st = torch.zeros(shape, dtype=torch.float32, device=dev)
         with pytest.raises((RuntimeError, ValueError)):
             ops.prefill_attn(q, k, v, 0.1, stat_out=st)
+
+
+SPLIT_CASES = [
+    # B, Hq, Hkv, Lq, Lk: one query block per (row, query head) over many keys
+    (1, 32, 8, 1, 20000),     # a decode-like step (baseline caches)
+    (1, 28, 4, 7, 9000),      # GQA 7, a few queries
+    (2, 8, 2, 100, 30000),    # a short last chunk, batch 2
+    (1, 4, 1, 128, 5000),     # a full query block
+]
+
+
+def _nbytes(dt, B, Hq, Hkv, Lq, Lk):
+    from heterocache_amd import _lib
+    lib = _lib.load()
+    code = {"bf16": 2, "f16": 1, "f32": 0}[dt]
+    return lib.hc_prefill_workspace_size(code, B, Hkv, Lk), lib.hc_prefill_workspace_bytes(code, B, Hq, Hkv, Lq, Lk)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("case", SPLIT_CASES)
+def test_prefill_key_split_matches_oracle(dev, dt, case):
+    """Short calls over long key ranges split the keys across workgroups
+    (the workspace of hc_prefill_workspace_bytes holds the partials): the
+    output meets the oracle at the unsplit tolerance, and a call given only
+    the unsplit workspace (one pass) agrees with it to the same bar."""
+    from heterocache_amd import _lib
+    B, Hq, Hkv, Lq, Lk = case
+    seed = 4000 + sum(case)
+    print(f"prefill_attn split dt={dt} B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} seed={seed}", flush=True)
+    vt, full = _nbytes(dt, B, Hq, Hkv, Lq, Lk)
+    assert full > vt, "the shape should take the key split"
+    q, k, v = _inputs(dev, dt, B, Hq, Hkv, Lq, Lk, seed, pad=40)
+    scale = 1.0 / math.sqrt(128)
+    out = ops.prefill_attn(q, k, v, scale)
+    # The same call with only the V-tile workspace: one pass over the keys.
+    lib = _lib.load()
+    one = torch.empty((B, Lq, Hq, 128), dtype=q.dtype, device=dev)
+    ws = torch.empty(vt, dtype=torch.uint8, device=dev)
+    strides = np.array([[q.stride(0), q.stride(1), q.stride(2)], [k.stride(0), k.stride(1), k.stride(2)],
+                        [v.stride(0), v.stride(1), v.stride(2)], [one.stride(0), one.stride(2), one.stride(1)]],
+                       dtype=np.int64)
+    base = strides.ctypes.data
+    _lib.check(lib.hc_prefill_attn(ops.dtype_code(q.dtype), q.data_ptr(), base, k.data_ptr(), base + 24, v.data_ptr(),
+                                   base + 48, one.data_ptr(), base + 72, B, Hq, Hkv, Lq, Lk, scale, ws.data_ptr(),
+                                   ws.numel(), torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    ref = O.prefill_attention(as_np(q), as_np(k), as_np(v), scale)
+    got = as_np(out)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ATTN_TOL[dt]
+    assert np.abs(got - as_np(one)).max() <= ATTN_TOL[dt]
+
+
+def test_prefill_key_split_statistics(dev):
+    """Statistics from a split call: the merge folds the splits' (m, l) into
+    the oracle's log-normaliser (1e-3, log2 units), M inside [max s - 8, max s]."""
+    B, Hq, Hkv, Lq, Lk, W = 1, 8, 2, 32, 20000, 32
+    vt, full = _nbytes("bf16", B, Hq, Hkv, Lq, Lk)
+    assert full > vt
+    q, k, v = _inputs(dev, "bf16", B, Hq, Hkv, Lq, Lk, 77)
+    scale = 1.0 / math.sqrt(128)
+    st = torch.full((B, Hq, W, 2), float("nan"), dtype=torch.float32, device=dev)
+    out = ops.prefill_attn(q, k, v, scale, stat_out=st)
+    plain = ops.prefill_attn(q, k, v, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    G = Hq // Hkv
+    qn, kn = as_np(q), as_np(k)
+    rows, ks = [], []
+    for h in range(Hkv):
+        for w in range(W):
+            i = Lq - W + w
+            rows.append(qn[0, h * G:(h + 1) * G, i])
+            ks.append(kn[0, h, :Lk - Lq + i + 1])
+    ref = O.softmax_lse2(np.stack(rows), ks, Lk, scale).reshape(1, Hkv, W, G).transpose(0, 1, 3, 2).reshape(1, Hq, W)
+    got = as_np(st)
+    assert np.abs(got[..., 0] + np.log2(got[..., 1]) - ref).max() <= 1e-3
+    smax = np.array([(scale * math.log2(math.e) * (r.astype(np.float64) @ kk.astype(np.float64).T)).max(axis=-1)
+                     for r, kk in zip(rows, ks)]).reshape(1, Hkv, W, G).transpose(0, 1, 3, 2).reshape(1, Hq, W)
+    assert (got[..., 0] <= smax + 1e-3).all() and (got[..., 0] >= smax - 8 - 1e-3).all()
