@@ -47,6 +47,8 @@ def parse():
                    help="comma-separated runs of the full-step phase (natural, never, always, host_never, "
                         "host_always)")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
+    p.add_argument("--overlap-check", action="store_true",
+                   help="full step: run the drift checks and their retrieval on a side stream (overlap_drift_check)")
     p.add_argument("--two-pass-check", action="store_true",
                    help="HeteroCache phase: score drift checks with the two-pass scorer (statistics pass storing "
                         "the logits, then a pass over them) instead of the one-pass scorer on the statistics the "
@@ -205,7 +207,8 @@ def full_step_phase(args, torch, dev):
         cfg = HeteroCacheConfig(data, compression_ratio=args.ratio, stable_threshold=thr, real_offload=True,
                                 max_gen_len=max_gen, decode_step=S, pooling="avgpool", kernel_size=5,
                                 num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
-                                tier_placement=tier, one_pass_drift_check=not args.two_pass_check, **kw)
+                                tier_placement=tier, one_pass_drift_check=not args.two_pass_check,
+                                overlap_drift_check=args.overlap_check, **kw)
         return HeteroCache(cfg)
 
     def prefill(cache, keep_inputs):
