@@ -1130,7 +1130,10 @@ __global__ __launch_bounds__(256) void score_finish_reg_kernel(const float* __re
 // 0.39 ms, and counted into global memory, 0.69 ms.
 // (Four independent waves per workgroup, each with its own 128-position ring
 // and no barriers, measured slower: 0.32 against 0.25 ms at 33 pivots x 5
-// steps x 128K, at three waves per SIMD instead of four.)
+// steps x 128K, at three waves per SIMD instead of four.  So did requesting
+// the next chunk's keys earlier -- sub-tile by sub-tile as each one's
+// products are issued (270 against 260 us: two MFMA chains per step instead
+// of eight), or all four right after the last row tile's products (263).)
 // ---------------------------------------------------------------------------
 constexpr int kGsMargin = 32;                     // margin positions before a chunk
 constexpr int kGsRight = 16;                      // the run's right margin
