@@ -431,29 +431,309 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
   }
 }
 
-// Split partials of one query -> its output row (and, for the last st_rows
-// queries, its statistics): one workgroup per (batch, query head, query),
-// thread d = channel d.  Splits with no visible key (m = -inf) add nothing.
+// ---------------------------------------------------------------------------
+// Decode-shaped calls (query heads x queries of a KV row <= 16: a decode
+// step of the baseline caches, which attend through this entry point, or a
+// few-token chunk).  The G*Lq (query head, query) pairs of a KV row are the
+// 16 columns of one MFMA block, so each key is read once per row, not once
+// per query head; K and V are read in their natural layout (no V re-layout
+// pass): K rows are the A operand of S^T = K Q^T as they lie in memory, and
+// each wave transposes its V tile through its own LDS buffer into the A
+// operand of O^T += V^T P^T, whose k-slots follow the order in which the
+// S^T accumulators hold P (k-slot 8g + i <-> token 16*(i/4) + 4g + i%4).
+// A workgroup takes one split of the row's 32-token tiles; its four waves
+// take every fourth tile of it and each writes its own partial (the split
+// count seen by prefill_merge_kernel is 4 * splits).
+// ---------------------------------------------------------------------------
+constexpr int kDvPitch = HC_TILE + 8;            // fp32: transposed V row, 32 k-slots + skew
+constexpr int kDvNPitch = HC_HEAD_DIM + 16;      // 16-bit: natural V row, 128 channels + skew
+constexpr int kDvWaves = 4;
+
+// Per-wave V buffer (elements): fp32 keeps the tile transposed ([channel][k-slot]);
+// 16-bit types keep it in natural layout ([token][channel]) and read the A
+// operand with the LDS transpose read.
 template <typename T>
-__global__ __launch_bounds__(HC_HEAD_DIM) void prefill_merge_kernel(const PfArgs a) {
+constexpr int dv_wave_elems() {
+  return sizeof(T) == 4 ? HC_HEAD_DIM * kDvPitch : HC_TILE * kDvNPitch;
+}
+template <typename T>
+constexpr size_t dv_lds_bytes() {
+  // The buffers are reused by the end-of-kernel combine of the four waves.
+  const size_t v = (size_t)kDvWaves * dv_wave_elems<T>() * sizeof(T);
+  const size_t comb = (size_t)kDvWaves * 16 * (HC_HEAD_DIM + 2) * sizeof(float);
+  return v > comb ? v : comb;
+}
+
+typedef short __attribute__((ext_vector_type(4))) dv_s4;
+
+// gfx950 LDS transpose read (ds_read_b64_tr_b16), 16-bit elements: within
+// each 16-lane group, lane i receives {B[i/4 + 4k][i%4] : k < 4}, where
+// B[r][e] is element e of the 8 bytes at lane r's address.
+__device__ __forceinline__ dv_s4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) dv_s4*)(p));
+}
+
+struct DvArgs {
+  PfArgs a;
+  int tps;      // tiles per workgroup split
+  int ntiles;   // 32-token tiles of the key range
+  int ncols;    // G * Lq valid columns
+};
+
+template <typename T>
+__global__ __launch_bounds__(kDvWaves * 64, sizeof(T) == 4 ? 1 : 2) void prefill_decode_kernel(const DvArgs d) {
+  typedef typename Elem<T>::vec8 vec8;
+  const PfArgs& a = d.a;
+  extern __shared__ __attribute__((aligned(16))) unsigned char dv_lds[];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g4 = lane >> 4, n16 = lane & 15;
+  T* sv = reinterpret_cast<T*>(dv_lds) + wave * dv_wave_elems<T>();
+  const int G = a.Hq / a.Hkv;
+  const int row = blockIdx.x % a.rows, split = blockIdx.x / a.rows;
+  const int b = row / a.Hkv, kvh = row % a.Hkv;
+  const int shift = a.Lk - a.Lq;
+  // Column n16 of this lane: query head kvh*G + gi, query qi.
+  const bool col_ok = n16 < d.ncols;
+  const int gi = col_ok ? n16 / a.Lq : 0, qi = col_ok ? n16 % a.Lq : 0;
+  const int hq = kvh * G + gi;
+  const int lim = shift + qi;  // last visible key of this column
+  vec8 qop[4];
+  {
+    const T* qp = reinterpret_cast<const T*>(a.q) + b * a.q_sb + hq * a.q_sh + (int64_t)qi * a.q_st + 8 * g4;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qop[s] = col_ok ? load8(qp + 32 * s) : zero8<T>();
+  }
+  const T* kb = reinterpret_cast<const T*>(a.k) + b * a.k_sb + kvh * a.k_sh;
+  const T* vb = reinterpret_cast<const T*>(a.v) + b * a.v_sb + kvh * a.v_sh;
+  const int tile0 = split * d.tps + wave, tile_end = min(split * d.tps + d.tps, d.ntiles);
+
+  // K: A operand rows = tokens t0 + 16h + n16, k-slots = channels 32s + 8*g4 + [0, 8).
+  // V: chunk c = lane + 64i of the tile = token c / 16, channels 8*(c % 16) + [0, 8).
+  auto load_tile = [&](int tile, vec8 (&kr)[2][4], vec8 (&vr)[8]) {
+    const int t0 = tile * HC_TILE;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int t = t0 + 16 * h + n16;
+      const T* p = kb + (int64_t)min(t, a.Lk - 1) * a.k_st + 8 * g4;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kr[h][s] = t < a.Lk ? load8_stream<T>(p + 32 * s) : zero8<T>();
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = lane + 64 * i, t = t0 + (c >> 4);
+      vr[i] = t < a.Lk ? load8_stream<T>(vb + (int64_t)min(t, a.Lk - 1) * a.v_st + 8 * (c & 15)) : zero8<T>();
+    }
+  };
+
+  f32x4 o[8];
+#pragma unroll
+  for (int db = 0; db < 8; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.f;
+
+  auto step = [&](int tile, const vec8 (&kr)[2][4], const vec8 (&vr)[8]) {
+    const int t0 = tile * HC_TILE;
+    if constexpr (sizeof(T) == 4) {
+      // V tile -> transposed LDS rows: channel 8*(c%16) + e, k-slot of token c/16.
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = lane + 64 * i, tt = c >> 4, r = tt & 15;
+        const int ks = 8 * (r >> 2) + 4 * (tt >> 4) + (r & 3);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          sv[(8 * (c & 15) + e) * kDvPitch + ks] = e < 4 ? vr[i].lo[e] : vr[i].hi[e - 4];
+      }
+    } else {
+      // V tile -> LDS in natural layout, one 16-byte write per chunk.
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = lane + 64 * i;
+        *reinterpret_cast<vec8*>(sv + (c >> 4) * kDvNPitch + 8 * (c & 15)) = vr[i];
+      }
+    }
+    // S^T = K Q^T: rows = tokens t0 + 16h + 4*g4 + j, column n16.
+    f32x4 sacc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sacc[h] = mma_16x16x32(kr[h][s], qop[s], sacc[h]);
+    if (t0 + HC_TILE - 1 > shift) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (t0 + 16 * h + 4 * g4 + j > lim) sacc[h][j] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) mx = fmaxf(mx, sacc[h][j]);
+    mx = rows4_max(mx);
+    const float mt = mx * a.scale_log2;
+    if (__any(mt > m + kPfLazy)) {
+      const float mnew = fmaxf(m, mt);
+      const float alpha = m == -INFINITY ? 0.f : fast_exp2(m - mnew);
+      m = mnew;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) o[db] *= alpha;
+    }
+    // (m = -inf only while every key so far is masked: p = 0.)
+    const float nm = m == -INFINITY ? 0.f : -m;
+    float pv[8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pv[4 * h + j] = fast_exp2(fmaf(sacc[h][j], a.scale_log2, nm));
+        l += pv[4 * h + j];
+      }
+    const vec8 pb = pack8<T>(pv);
+    // The transposed tile is read only after this wave's writes are done.
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      vec8 va;
+      if constexpr (sizeof(T) == 4) {
+        const T* vp = sv + (16 * db + n16) * kDvPitch + 8 * g4;
+        va.lo = *reinterpret_cast<const f32x4*>(vp);
+        va.hi = *reinterpret_cast<const f32x4*>(vp + 4);
+      } else {
+        // Lane r of group g4 points at token 16h + 4*g4 + r/4, channels
+        // 16db + 4*(r%4) + [0, 4); the transpose hands lane r the channel
+        // 16db + r at tokens 16h + 4*g4 + [0, 4): k-slots 4h + [0, 4).
+        const T* vp = sv + (4 * g4 + (n16 >> 2)) * kDvNPitch + 16 * db + 4 * (n16 & 3);
+        const dv_s4 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 16 * kDvNPitch);
+        typedef short __attribute__((ext_vector_type(8))) dv_s8;
+        const dv_s8 both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        va = __builtin_bit_cast(vec8, both);
+      }
+      o[db] = mma_16x16x32(va, pb, o[db]);
+    }
+    // The next tile's writes follow this tile's reads (in-order LDS per wave).
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  vec8 ka[2][4], va_[8], kb2[2][4], vb2[8];
+  int tile = tile0;
+  if (tile < tile_end) load_tile(tile, ka, va_);
+  while (tile < tile_end) {
+    const int t1 = tile + kDvWaves;
+    if (t1 < tile_end) load_tile(t1, kb2, vb2);
+    step(tile, ka, va_);
+    if (t1 >= tile_end) break;
+    const int t2 = t1 + kDvWaves;
+    if (t2 < tile_end) load_tile(t2, ka, va_);
+    step(t1, kb2, vb2);
+    tile = t2;
+  }
+
+  // The four waves' states -> one partial of the workgroup's split, through
+  // the (now free) LDS: wave w's O^T block, maxima and sums.
+  const float lt = rows4_sum(l);
+  __syncthreads();  // every wave is done with its V buffer
+  float* so = reinterpret_cast<float*>(dv_lds);        // [wave][16 columns][128 channels]
+  float* sm = so + kDvWaves * 16 * HC_HEAD_DIM;         // [wave][16]
+  float* sl = sm + kDvWaves * 16;                       // [wave][16]
+#pragma unroll
+  for (int db = 0; db < 8; ++db)
+    *reinterpret_cast<f32x4*>(so + (wave * 16 + n16) * HC_HEAD_DIM + 16 * db + 4 * g4) = o[db];
+  if (g4 == 0) {
+    sm[wave * 16 + n16] = m;
+    sl[wave * 16 + n16] = lt;
+  }
+  __syncthreads();
+  // Thread x: column x / 16, channels 8 * (x % 16) + [0, 8).
+  const int col = threadIdx.x >> 4, c0 = 8 * (threadIdx.x & 15);
+  if (col >= d.ncols) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kDvWaves; ++w) M = fmaxf(M, sm[w * 16 + col]);
+  float wt[kDvWaves], L = 0.f;
+#pragma unroll
+  for (int w = 0; w < kDvWaves; ++w) {
+    const float mw = sm[w * 16 + col];
+    wt[w] = mw == -INFINITY ? 0.f : fast_exp2(mw - M);
+    L = fmaf(sl[w * 16 + col], wt[w], L);
+  }
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kDvWaves; ++w)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = fmaf(so[(w * 16 + col) * HC_HEAD_DIM + c0 + e], wt[w], acc[e]);
+  const int cgi = col / a.Lq, cqi = col % a.Lq, chq = kvh * G + cgi;
+  float* pp = a.part + (((int64_t)(b * a.Hq + chq) * a.Lq + cqi) * a.nsplit + split) * kPfPartStride;
+  *reinterpret_cast<f32x4*>(pp + c0) = f32x4{acc[0], acc[1], acc[2], acc[3]};
+  *reinterpret_cast<f32x4*>(pp + c0 + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+  if (c0 == 0) {
+    pp[HC_HEAD_DIM] = M;
+    pp[HC_HEAD_DIM + 1] = L;
+  }
+}
+
+// Split partials of one query -> its output row (and, for the last st_rows
+// queries, its statistics): one workgroup per (batch, query head, query) of
+// kMergeGroups x 128 threads, thread (group, d) summing channel d over the
+// splits s = group (mod kMergeGroups).  The splits' maximum and weights
+// 2^(m_s - M) are formed once, cooperatively, into LDS, so each thread's sum
+// is a run of independent loads; the groups' sums are added in LDS.  Splits
+// with no visible key (m = -inf) add nothing.
+constexpr int kPfMaxSplits = 1024;
+constexpr int kMergeGroups = 4;
+constexpr int kMergeThreads = kMergeGroups * HC_HEAD_DIM;
+template <typename T>
+__global__ __launch_bounds__(kMergeThreads) void prefill_merge_kernel(const PfArgs a) {
+  __shared__ float s_w[kPfMaxSplits];
+  __shared__ float s_red[kMergeThreads / 64];
+  __shared__ float s_acc[kMergeGroups][HC_HEAD_DIM];
   const int64_t qx = blockIdx.x;  // (b * Hq + hq) * Lq + qi
   const int qi = (int)(qx % a.Lq);
   const int bh = (int)(qx / a.Lq);
   const int hq = bh % a.Hq, b = bh / a.Hq;
   const float* pp = a.part + qx * a.nsplit * kPfPartStride;
-  const int d = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int d = tid % HC_HEAD_DIM, grp = tid / HC_HEAD_DIM;
+  constexpr int nw = kMergeThreads / 64;
+  float mloc = -INFINITY;
+  for (int s = tid; s < a.nsplit; s += kMergeThreads) mloc = fmaxf(mloc, pp[s * kPfPartStride + HC_HEAD_DIM]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mloc = fmaxf(mloc, __shfl_xor(mloc, off, 64));
+  if (lane == 0) s_red[wv] = mloc;
+  __syncthreads();
   float M = -INFINITY;
-  for (int s = 0; s < a.nsplit; ++s) M = fmaxf(M, pp[s * kPfPartStride + HC_HEAD_DIM]);
-  float L = 0.f, acc = 0.f;
-  for (int s = 0; s < a.nsplit; ++s) {
+#pragma unroll
+  for (int w = 0; w < nw; ++w) M = fmaxf(M, s_red[w]);
+  __syncthreads();  // s_red is reused below
+  float lloc = 0.f;
+  for (int s = tid; s < a.nsplit; s += kMergeThreads) {
     const float ms = pp[s * kPfPartStride + HC_HEAD_DIM];
-    if (ms == -INFINITY) continue;
-    const float e = fast_exp2(ms - M);
-    L = fmaf(pp[s * kPfPartStride + HC_HEAD_DIM + 1], e, L);
-    acc = fmaf(pp[s * kPfPartStride + d], e, acc);
+    const float e = ms == -INFINITY ? 0.f : fast_exp2(ms - M);
+    s_w[s] = e;
+    if (e > 0.f) lloc = fmaf(pp[s * kPfPartStride + HC_HEAD_DIM + 1], e, lloc);
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) lloc += __shfl_xor(lloc, off, 64);
+  if (lane == 0) s_red[wv] = lloc;
+  __syncthreads();
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < nw; ++w) L += s_red[w];
+  float acc = 0.f;
+#pragma unroll 8
+  for (int s = grp; s < a.nsplit; s += kMergeGroups) {
+    const float e = s_w[s];
+    const float x = pp[s * kPfPartStride + d];
+    acc = e > 0.f ? fmaf(x, e, acc) : acc;
+  }
+  s_acc[grp][d] = acc;
+  __syncthreads();
+  if (grp != 0) return;
+  float sum = 0.f;
+#pragma unroll
+  for (int g = 0; g < kMergeGroups; ++g) sum += s_acc[g][d];
   T* o = reinterpret_cast<T*>(a.out) + b * a.o_sb + hq * a.o_sh + (int64_t)qi * a.o_st;
-  o[d] = Elem<T>::from_f32(acc / L);
+  o[d] = Elem<T>::from_f32(sum / L);
   const int w = qi - (a.Lq - a.st_rows);
   if (a.st && w >= 0 && d == 0) {
     float* so = a.st + (((int64_t)b * a.Hq + hq) * a.st_rows + w) * 2;
@@ -487,10 +767,70 @@ int launch_prefill(const PfArgs& a, hipStream_t stream) {
   if ((rc = check_launch("hc_prefill_attn"))) return rc;
   if (a.nsplit > 1) {
     const int64_t nq = (int64_t)(a.rows / a.Hkv) * a.Hq * a.Lq;
-    hipLaunchKernelGGL((prefill_merge_kernel<T>), dim3((unsigned)nq), dim3(HC_HEAD_DIM), 0, stream, a);
+    hipLaunchKernelGGL((prefill_merge_kernel<T>), dim3((unsigned)nq), dim3(kMergeThreads), 0, stream, a);
     rc = check_launch("hc_prefill_attn(merge)");
   }
   return rc;
+}
+
+template <typename T>
+int launch_decode_shaped(const DvArgs& d, hipStream_t stream) {
+  static std::once_flag once;
+  static hipError_t attr = hipSuccess;
+  std::call_once(once, [] {
+    attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill_decode_kernel<T>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)dv_lds_bytes<T>());
+  });
+  if (attr != hipSuccess) return set_error(HC_ERR_HIP, "hc_prefill_attn: %s", hipGetErrorString(attr));
+  const int64_t grid = (int64_t)d.a.rows * d.a.nsplit;
+  hipLaunchKernelGGL((prefill_decode_kernel<T>), dim3((unsigned)grid), dim3(kDvWaves * 64), dv_lds_bytes<T>(), stream,
+                     d);
+  int rc = check_launch("hc_prefill_attn(decode-shaped)");
+  if (rc) return rc;
+  const int64_t nq = (int64_t)(d.a.rows / d.a.Hkv) * d.a.Hq * d.a.Lq;
+  hipLaunchKernelGGL((prefill_merge_kernel<T>), dim3((unsigned)nq), dim3(kMergeThreads), 0, stream, d.a);
+  return check_launch("hc_prefill_attn(merge)");
+}
+
+// Resident workgroups of the decode-shaped kernel on the current device.
+template <typename T>
+int decode_shaped_slots() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  static std::mutex mu;
+  static int cache[64];
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[dev] > 0) return cache[dev];
+  const void* fn = reinterpret_cast<const void*>(&prefill_decode_kernel<T>);
+  int per_cu = 0, cus = 0;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dv_lds_bytes<T>()) != hipSuccess)
+    return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDvWaves * 64, dv_lds_bytes<T>()) != hipSuccess)
+    return 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  cache[dev] = (per_cu > 0 ? per_cu : 1) * (cus > 0 ? cus : 1);
+  return cache[dev];
+}
+
+// Workgroup splits of a decode-shaped call (0: not decode-shaped).  At most
+// 16 (query head, query) columns per KV row and at least kDvMinTiles tiles
+// of keys; each wave keeps at least kDvMinWaveTiles tiles; the grid aims at
+// one resident round.
+constexpr int kDvMinTiles = 32;
+constexpr int kDvMinWaveTiles = 4;
+int decode_shaped_splits(int dtype, int batch, int q_heads, int kv_heads, int q_len, int kv_len) {
+  if (batch <= 0 || kv_heads <= 0 || q_heads <= 0 || q_heads % kv_heads) return 0;
+  if ((q_heads / kv_heads) * q_len > 16) return 0;
+  const int ntiles = (kv_len + HC_TILE - 1) / HC_TILE;
+  if (ntiles < kDvMinTiles) return 0;
+  const int slots = dtype == HC_DTYPE_F32 ? decode_shaped_slots<float>()
+                    : dtype == HC_DTYPE_F16 ? decode_shaped_slots<_Float16>()
+                                            : decode_shaped_slots<__bf16>();
+  if (slots <= 0) return 0;
+  const int rows = batch * kv_heads;
+  const int by_slots = std::max(1, slots / rows);
+  const int by_keys = std::max(1, ntiles / (kDvWaves * kDvMinWaveTiles));
+  return std::min(std::min(by_slots, by_keys), kPfMaxSplits);
 }
 
 // Workgroups of the attention kernel resident on the current device at once
@@ -529,7 +869,7 @@ int prefill_nsplit(int dtype, int batch, int q_heads, int kv_heads, int q_len, i
   const int nit = (kv_len + kPfKeys - 1) / kPfKeys;
   const int by_keys = nit / kPfMinSplitIts;
   const int by_slots = (int)(slots / natural);
-  const int n = std::min(by_keys, by_slots);
+  const int n = std::min(std::min(by_keys, by_slots), kPfMaxSplits);
   return n >= 2 ? n : 1;
 }
 
@@ -563,6 +903,8 @@ extern "C" size_t hc_prefill_workspace_bytes(int dtype, int batch, int q_heads, 
                                              int kv_len) {
   const size_t vt = hc_prefill_workspace_size(dtype, batch, kv_heads, kv_len);
   if (vt == 0 || q_heads <= 0 || q_len <= 0) return vt;
+  const int dv = decode_shaped_splits(dtype, batch, q_heads, kv_heads, q_len, kv_len);
+  if (dv > 0) return pf_align256(vt) + pf_part_bytes(batch, q_heads, q_len, dv);
   const int ns = prefill_nsplit(dtype, batch, q_heads, kv_heads, q_len, kv_len);
   return ns > 1 ? pf_align256(vt) + pf_part_bytes(batch, q_heads, q_len, ns) : vt;
 }
@@ -650,6 +992,23 @@ static int prefill_entry(int dtype, const void* q, const int64_t* q_strides, con
   a.nsplit = 1;
   a.its = 1 << 30;
   a.part = nullptr;
+  hipStream_t s = (hipStream_t)stream;
+  // Decode-shaped calls: the packed-column kernel over natural-layout K/V.
+  const int dv = decode_shaped_splits(dtype, batch, q_heads, kv_heads, q_len, kv_len);
+  if (dv > 0 && workspace_bytes >= pf_align256(need) + pf_part_bytes(batch, q_heads, q_len, dv)) {
+    DvArgs d;
+    a.nsplit = dv;
+    a.part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + pf_align256(need));
+    d.a = a;
+    d.ntiles = (kv_len + HC_TILE - 1) / HC_TILE;
+    d.tps = (d.ntiles + dv - 1) / dv;
+    d.ncols = (q_heads / kv_heads) * q_len;
+    switch (dtype) {
+      case HC_DTYPE_BF16: return launch_decode_shaped<__bf16>(d, s);
+      case HC_DTYPE_F16: return launch_decode_shaped<_Float16>(d, s);
+      default: return launch_decode_shaped<float>(d, s);
+    }
+  }
   const int ns = prefill_nsplit(dtype, batch, q_heads, kv_heads, q_len, kv_len);
   if (ns > 1 && workspace_bytes >= pf_align256(need) + pf_part_bytes(batch, q_heads, q_len, ns)) {
     const int nit = (kv_len + kPfKeys - 1) / kPfKeys;
@@ -659,7 +1018,6 @@ static int prefill_entry(int dtype, const void* q, const int64_t* q_strides, con
   }
   const int64_t grid = (int64_t)a.rows * (q_heads / kv_heads) * a.nqb * a.nsplit;
   if (grid > 0x7fffffffLL) return set_error(HC_ERR_INVALID, "hc_prefill_attn: grid too large");
-  hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case HC_DTYPE_BF16: return launch_prefill<__bf16>(a, s);
     case HC_DTYPE_F16: return launch_prefill<_Float16>(a, s);

@@ -247,7 +247,9 @@ size_t hc_prefill_workspace_size(int dtype, int batch, int kv_heads, int kv_len)
  * of the current device idle over a long key range (decode-like steps of
  * the baseline caches, a short last chunk of a chunked prefill), a
  * workspace of this size lets hc_prefill_attn / hc_prefill_attn_stats split
- * the keys across workgroups and merge the partials (flash-decoding style).
+ * the keys across workgroups and merge the partials (flash-decoding style;
+ * calls with at most 16 query heads x queries per KV row pack them into one
+ * MFMA column block and read K and V in their natural layout).
  * With hc_prefill_workspace_size bytes the call runs unsplit.  The split
  * changes the fp32 summation order, not the result's tolerance.  No
  * reference counterpart: flash-attn picks its own split inside

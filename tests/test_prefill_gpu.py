@@ -245,3 +245,61 @@ def test_prefill_key_split_statistics(dev):
     smax = np.array([(scale * math.log2(math.e) * (r.astype(np.float64) @ kk.astype(np.float64).T)).max(axis=-1)
                      for r, kk in zip(rows, ks)]).reshape(1, Hkv, W, G).transpose(0, 1, 3, 2).reshape(1, Hq, W)
     assert (got[..., 0] <= smax + 1e-3).all() and (got[..., 0] >= smax - 8 - 1e-3).all()
+
+
+DECODE_SHAPED_CASES = [
+    # B, Hq, Hkv, Lq, Lk: at most 16 (query head, query) columns per KV row
+    (1, 32, 8, 1, 131072),    # a Llama-3-8B decode step at 128K
+    (2, 28, 4, 2, 5000),      # GQA 7, two queries: 14 columns, batch 2
+    (1, 8, 8, 16, 3001),      # no GQA, 16 queries, a ragged last tile
+    (3, 4, 2, 8, 1100),       # GQA 2 x 8 queries, batch 3
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("case", DECODE_SHAPED_CASES)
+def test_prefill_decode_shaped_matches_oracle(dev, dt, case):
+    """Decode-shaped calls (a KV row's query heads x queries packed into one
+    MFMA column block, K and V read in their natural layout, V transposed
+    through LDS): the oracle at the unsplit tolerance, also with NaN-filled
+    slots past the keys."""
+    B, Hq, Hkv, Lq, Lk = case
+    seed = 5000 + sum(case)
+    print(f"prefill_attn decode-shaped dt={dt} B={B} Hq={Hq} Hkv={Hkv} Lq={Lq} Lk={Lk} seed={seed}", flush=True)
+    vt, full = _nbytes(dt, B, Hq, Hkv, Lq, Lk)
+    assert full > vt
+    q, k, v = _inputs(dev, dt, B, Hq, Hkv, Lq, Lk, seed, pad=40)
+    scale = 1.0 / math.sqrt(128)
+    out = ops.prefill_attn(q, k, v, scale)
+    torch.cuda.synchronize()
+    ref = O.prefill_attention(as_np(q), as_np(k), as_np(v), scale)
+    got = as_np(out)
+    assert np.isfinite(got).all()
+    assert np.abs(got - ref).max() <= ATTN_TOL[dt]
+
+
+def test_prefill_decode_shaped_statistics(dev):
+    """Statistics of a decode-shaped call: the oracle's log-normaliser within
+    1e-3 (log2 units), the bound within 8 of the row maximum."""
+    B, Hq, Hkv, Lq, Lk, W = 1, 8, 2, 4, 20000, 4
+    q, k, v = _inputs(dev, "bf16", B, Hq, Hkv, Lq, Lk, 78)
+    scale = 1.0 / math.sqrt(128)
+    st = torch.full((B, Hq, W, 2), float("nan"), dtype=torch.float32, device=dev)
+    out = ops.prefill_attn(q, k, v, scale, stat_out=st)
+    plain = ops.prefill_attn(q, k, v, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out, plain)
+    G = Hq // Hkv
+    qn, kn = as_np(q), as_np(k)
+    rows, ks = [], []
+    for h in range(Hkv):
+        for w in range(W):
+            i = Lq - W + w
+            rows.append(qn[0, h * G:(h + 1) * G, i])
+            ks.append(kn[0, h, :Lk - Lq + i + 1])
+    ref = O.softmax_lse2(np.stack(rows), ks, Lk, scale).reshape(1, Hkv, W, G).transpose(0, 1, 3, 2).reshape(1, Hq, W)
+    got = as_np(st)
+    assert np.abs(got[..., 0] + np.log2(got[..., 1]) - ref).max() <= 1e-3
+    smax = np.array([(scale * math.log2(math.e) * (r.astype(np.float64) @ kk.astype(np.float64).T)).max(axis=-1)
+                     for r, kk in zip(rows, ks)]).reshape(1, Hkv, W, G).transpose(0, 1, 3, 2).reshape(1, Hq, W)
+    assert (got[..., 0] <= smax + 1e-3).all() and (got[..., 0] >= smax - 8 - 1e-3).all()
