@@ -605,7 +605,9 @@ def head_analysis_phase(args, torch, dev):
 def prefill_attention_phase(args, torch, dev):
     """Causal prefill attention of one Llama-3-8B layer (32 query heads over 8
     KV heads, projection layout [B, T, H, 128]): a 32K prompt in one call, and
-    the last 8K chunk of a chunked prefill over the bench context.  MFMA
+    the last 8K chunk of a chunked prefill over the bench context, and a
+    one-query decode step over the bench context (the baseline caches'
+    decode).  MFMA
     figures count the causal product once (4*128 flops per visible
     query-key pair); PyTorch's SDPA on the same prompt is timed beside it."""
     import torch.nn.functional as F
@@ -651,6 +653,17 @@ def prefill_attention_phase(args, torch, dev):
     tf = flops(Lq, Lk) / ms / 1e9
     out["last_chunk"] = {"q_len": Lq, "kv_len": Lk, "ms": round(ms, 3), "tflops": round(tf, 1),
                          "mfma_frac_bf16_dense": round(tf / 2500.0, 4)}
+    del q, k, v, o
+    # A decode step of a full-KV (or baseline-compressed) layer through the
+    # same entry point: one query per head over the bench context, the
+    # decode-shaped path (HBM-bound: K and V read once per KV row).
+    q, k, v = inputs(1, args.ctx)
+    o = torch.empty((1, 1, Hq, D), device=dev, dtype=torch.bfloat16)
+    ms = timed(lambda: ops.prefill_attn(q, k, v, scale, out=o), reps=10)
+    kv_bytes = 2 * Hkv * args.ctx * D * 2
+    out["decode_step_full_kv"] = {"kv_len": args.ctx, "ms": round(ms, 4),
+                                  "gbs": round(kv_bytes / ms / 1e6, 1),
+                                  "frac_of_hbm_peak": round(kv_bytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
     del q, k, v, o
     torch.cuda.empty_cache()
     return out
