@@ -388,16 +388,47 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
       // Only the wave whose tiles straddle stat_len follows the snapshot
       // tile by tile; a wave wholly below it takes its final state, one
       // wholly above leaves the snapshot empty.
-      const bool cross = STATS && t_begin * HC_TILE < stat_len && t_end_st * HC_TILE > stat_len;
-      if (cross)
-        stream_tiles<T, STATS>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2, m_run,
-                               l_run, o, stat_len, m_snap, l_snap);
-      else
-        stream_tiles<T, false>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2, m_run,
-                               l_run, o, stat_len, m_snap, l_snap);
-      if (STATS && t_end_st * HC_TILE <= stat_len) {
-        m_snap = m_run;
-        l_snap = l_run;
+      if constexpr (STATS) {
+        const bool cross = t_begin * HC_TILE < stat_len && t_end_st * HC_TILE > stat_len;
+        if (cross)
+          stream_tiles<T, true>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2, m_run,
+                                l_run, o, stat_len, m_snap, l_snap);
+        else
+          stream_tiles<T, false>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2, m_run,
+                                 l_run, o, stat_len, m_snap, l_snap);
+        if (t_end_st * HC_TILE <= stat_len) {
+          m_snap = m_run;
+          l_snap = l_run;
+        }
+      } else {
+        // The same loop as stream_tiles, written out: the plain instance keeps
+        // the schedule it had before the statistics variant existed (through
+        // stream_tiles the compiler interleaves its MFMAs differently, 0.5 us
+        // per layer slower).
+        const T* kb = kstore + row_base + lane * 8;
+        const T* vb = vstore + row_base + lane * 8;
+        vec8 kA[8], vA[8], kB[8], vB[8];
+        load_tile<T>(kA, vA, kb, vb, t_begin);
+        int t = t_begin;
+        for (; t + 2 < t_end_st; t += 2) {
+          load_tile<T>(kB, vB, kb, vb, t + 1);
+          __builtin_amdgcn_sched_barrier(0);
+          attend_tile<T, false>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+          __builtin_amdgcn_sched_barrier(0);
+          load_tile<T>(kA, vA, kb, vb, t + 2);
+          __builtin_amdgcn_sched_barrier(0);
+          attend_tile<T, false>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap,
+                                l_snap);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (t + 1 < t_end_st) {
+          load_tile<T>(kB, vB, kb, vb, t + 1);
+          attend_tile<T, false>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+          attend_tile<T, false>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap,
+                                l_snap);
+        } else {
+          attend_tile<T, false>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+        }
       }
     }
     // The wave whose tile range holds the new slot attends the new token and
@@ -632,8 +663,8 @@ int64_t decode_num_parts(const int* host_row_len, int rows, int chunk_tiles) {
 }
 
 // Workspace: [row_info: (first part, part count) per row, padded to 256 B]
-//            [part_ml: parts*G*2 f32][part_st: parts*G*2 f32]
-//            [part_o: parts*G*128 f32]
+//            [part_o: parts*G*128 f32][part_ml: parts*G*2 f32][part_st: parts*G*2 f32]
+// (the 512-byte partial rows first, so each starts on a cache line)
 // Every field is written before it is read within one call, so the buffer
 // needs no initialisation and may be reused freely by calls on one stream.
 static size_t workspace_head(int rows) { return ((size_t)rows * 2 * sizeof(int) + 255) / 256 * 256; }
@@ -663,9 +694,9 @@ static int launch_decode(const void* q, void* kstore, void* vstore, const int64_
   if (!workspace || workspace_bytes < need)
     return set_error(HC_ERR_INVALID, "hc_decode_attn: workspace too small (%zu < %zu bytes)", workspace_bytes, need);
   int* row_info = reinterpret_cast<int*>(workspace);
-  float* part_ml = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + workspace_head(rows));
+  float* part_o = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + workspace_head(rows));
+  float* part_ml = part_o + (size_t)grid_parts * G * HC_HEAD_DIM;
   float* part_st = part_ml + (size_t)grid_parts * G * 2;
-  float* part_o = part_st + (size_t)grid_parts * G * 2;
   const float scale_log2 = scale * 1.4426950408889634f;
   const size_t lds_o = (size_t)kDecodeWaves * G * kOPitch * sizeof(float);
   const dim3 mgrid(rows, G, HC_HEAD_DIM / kMergeSlice), mblock(kMergeSlice * kMergeGroups);
