@@ -401,10 +401,10 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
           l_snap = l_run;
         }
       } else {
-        // The same loop as stream_tiles, written out: the plain instance keeps
-        // the schedule it had before the statistics variant existed (through
-        // stream_tiles the compiler interleaves its MFMAs differently, 0.5 us
-        // per layer slower).
+        // The same loop as stream_tiles, written out: through stream_tiles the
+        // compiler schedules the plain instance's MFMAs and waits differently;
+        // written out, its code is the one it had before the statistics
+        // variant existed.
         const T* kb = kstore + row_base + lane * 8;
         const T* vb = vstore + row_base + lane * 8;
         vec8 kA[8], vA[8], kB[8], vB[8];
