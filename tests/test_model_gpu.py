@@ -8,13 +8,17 @@
   decode attention, drift checks and retrieval, with lengths advancing by
   one per generated token.
 """
+import math
+
 import numpy as np
 import pytest
 import torch
 from transformers import LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM
 
-from heterocache_amd import utils, workloads
+from heterocache_amd import ops, utils, workloads
 from heterocache_amd.cache_utils import HeteroCache
+from oracle import hc_oracle as O
+from tests.gpu_util import as_np
 
 pytestmark = pytest.mark.gpu
 
@@ -160,6 +164,52 @@ def test_baseline_caches_generate(dev, name):
         n = cache.key_cache[layer].shape[2]
         assert cache.key_cache[layer].shape[1] == 8           # repeated per query head
         assert n < 400 and n > 7                              # compressed, then 7 appended tokens
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_full_kv_decode_through_decode_shaped_attention(dev, dtype):
+    """A long prompt (1500 tokens, above the 32 key tiles from which a decode
+    step takes the decode-shaped attention) through a keep-every-token
+    SnapKV cache: the decode steps attend over the whole cache through
+    hc_prefill_attn's packed-column kernel.  fp32: the greedy tokens equal the
+    stock model's; bf16: each decode step's attention output of the patched
+    model stays within the bf16 bar of the float64 closed form."""
+    from heterocache_amd import cache_utils as C
+    from heterocache_amd import llama_model as LM
+    cfg = llama_cfg(layers=2, q_heads=8, kv_heads=2)
+    with utils.install_attention_patch():
+        torch.manual_seed(0)
+        model = LlamaForCausalLM(cfg).to(dtype).to(dev).eval()
+    ids = torch.randint(0, 512, (1, 1500), generator=torch.Generator().manual_seed(8)).to(dev)
+    keep_all = C.CompressionCacheConfig(window_size=16, compression_ratio=50.0, num_attn_heads=8, num_kv_heads=2,
+                                        num_layers=2)
+    if dtype == torch.float32:
+        torch.manual_seed(0)
+        ref_model = LlamaForCausalLM(cfg).to(dtype).to(dev).eval()
+        with torch.no_grad():
+            ref = ref_model.generate(ids, max_new_tokens=6, do_sample=False)
+            out = model.generate(ids, max_new_tokens=6, do_sample=False, past_key_values=C.SnapKVCache(keep_all))
+        assert torch.equal(out, ref)
+        return
+    seen = []
+
+    def check(layer, q, k, mask, scale):
+        if q.shape[2] == 1:
+            seen.append((q.detach().clone(), k.detach().clone()))
+    LM.ATTENTION_OBSERVERS.append(check)
+    try:
+        with torch.no_grad():
+            model.generate(ids, max_new_tokens=3, do_sample=False, past_key_values=C.SnapKVCache(keep_all))
+    finally:
+        LM.ATTENTION_OBSERVERS.remove(check)
+    assert seen and all(k.shape[2] >= 1500 for _, k in seen)
+    # The observed decode calls re-run through ops.prefill_attn against the oracle.
+    for q, k in seen[:2]:
+        v = torch.randn(k.shape, generator=torch.Generator().manual_seed(9)).to(dtype).to(dev)
+        got = ops.prefill_attn(q, k, v, 1 / math.sqrt(128))
+        torch.cuda.synchronize()
+        ref = O.prefill_attention(as_np(q), as_np(k), as_np(v), 1 / math.sqrt(128))
+        assert np.abs(as_np(got) - ref).max() <= 2e-2
 
 
 def test_cake_cache_generate(dev):
