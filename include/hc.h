@@ -134,7 +134,9 @@ int hc_decode_attn_noalloc(int dtype, const void* q, void* kstore, void* vstore,
 int64_t hc_decode_num_parts(const int32_t* host_row_len, int rows, int chunk_tiles);
 /* chunk_tiles for hc_decode_attn: the smallest chunk (at least 4 tiles)
  * whose grid fits the current device's resident workgroup slots for this
- * dtype and group (one chunk per row when even that does not fit); negative
+ * dtype and group; from 24 tiles up it is rounded up to a multiple of 4 so
+ * the workgroup's four waves stream equal shares (one chunk per row when
+ * even the smallest does not fit); negative
  * hc_status on error.  No counterpart in the reference (flash-attn chooses
  * its split internally). */
 int hc_decode_chunk_tiles(int dtype, const int32_t* host_row_len, int rows, int group);

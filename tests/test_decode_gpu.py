@@ -213,15 +213,23 @@ def test_row_order_does_not_change_results(dev):
 
 
 def test_auto_chunk_fits_one_round(dev):
-    """hc_decode_chunk_tiles: at least one tile per wave, minimal (one tile
-    less would need more workgroups), one chunk per row when rows alone
-    exceed the device's slots, and an error for a bad dtype."""
+    """hc_decode_chunk_tiles: at least one tile per wave; below 24 tiles
+    minimal (one tile less would need more workgroups); from 24 tiles whole
+    tiles per wave (a multiple of 4) and minimal among those; one chunk per
+    row when rows alone exceed the device's slots; an error for a bad
+    dtype."""
     from heterocache_amd import _lib, ops
-    for lens in ([131072] * 4 + [65536] * 4, [5000, 17, 1024], [0, 3], [200_000] * 3 + [10] * 5):
+    seen = set()
+    for lens in ([131072] * 4 + [65536] * 4, [5000, 17, 1024], [0, 3], [200_000] * 3 + [10] * 5,
+                 [16384, 2048, 4096, 6144] * 4):
         c = ops.decode_chunk_tiles(lens, 4, torch.bfloat16)
         assert c >= 4
+        step = 4 if c >= 24 else 1
+        seen.add(step)
+        assert c % step == 0
         if c > 4:
-            assert ops.decode_num_parts(lens, c - 1) > ops.decode_num_parts(lens, c)
+            assert ops.decode_num_parts(lens, c - step) > ops.decode_num_parts(lens, c)
+    assert seen == {1, 4}, "both regimes covered"
     many = [4096] * 20000
     assert ops.decode_chunk_tiles(many, 4, torch.bfloat16) == 128
     lens = np.asarray([10], dtype=np.int32)
