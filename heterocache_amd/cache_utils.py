@@ -87,7 +87,9 @@ class HeteroCacheConfig:
     real_offload is set -- "host" (pinned host memory, retrieval read over
     the host link), "device" (an HBM arena, retrieval a device gather) or
     "auto" (device when the whole model's tier fits in tier_device_budget
-    bytes, default a quarter of the device's memory; host otherwise).
+    bytes, by default the device memory still free after the KV arena less
+    an eighth of the device; host otherwise, and host when the device
+    allocation fails).
     Without real_offload the tier is the prefill K/V itself, as in the
     reference's GPU mode.
     """
@@ -217,6 +219,10 @@ class HeteroCache(DynamicCache):
         self._staged = [0] * self.num_layers
         self._q_tail = [None] * self.num_layers
         self._seen_tokens = 0
+        # The reference's multi-turn scratch caches (cleared by
+        # clear_temp_kv_cache); this cache never fills them.
+        self.temp_key_cache = {}
+        self.temp_value_cache = {}
         self._side = None
         # Model-wide buffers: one K/V arena for every layer's rows, and the
         # drift state of every layer (per-layer objects hold views of them).
@@ -233,6 +239,10 @@ class HeteroCache(DynamicCache):
         self._trigger_all = None     # [leaders] int32 drift flags
         self._lead_base = None       # first global leader index of each layer
         self._due = []               # layers whose check waits for the batched launch
+        # Whether the model calls decode_select after the step's attention
+        # (Llama order: True) or before it (Qwen order: False); None until
+        # the first decode_select tells.
+        self._select_after_attention = None
         self._batch_meta = {}
         # Optional callable observer(event, **tensors), told about every score
         # array the cache ranks and the sets and flags it derives from them
@@ -250,6 +260,16 @@ class HeteroCache(DynamicCache):
 
     def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
         return self._seen_tokens if self._seen_tokens is not None else 0
+
+    def clear_temp_kv_cache(self):
+        """heterocache/cache_utils.py:1192-1196: drop the temporary caches and
+        the tokens they counted.  The reference reads temp_key_cache without
+        ever creating it on HeteroCache (AttributeError on a first call); here
+        both start empty, so the call is a no-op until something fills them."""
+        if self.temp_key_cache:
+            self._seen_tokens -= next(iter(self.temp_key_cache.values())).shape[-2]
+        self.temp_key_cache = {}
+        self.temp_value_cache = {}
 
     @property
     def heads_len(self):
@@ -385,20 +405,39 @@ class HeteroCache(DynamicCache):
         L = self.prefill_len
         nbytes = 2 * rows * L * self.head_dim * torch.empty((), dtype=dtype).element_size()
         mode = getattr(self.config, "tier_placement", "auto")
-        if mode == "auto":
-            budget = getattr(self.config, "tier_device_budget", None)
-            if budget is None:
-                budget = torch.cuda.get_device_properties(device).total_memory // 4
-            mode = "device" if nbytes <= budget else "host"
+        auto = mode == "auto"
+        if auto:
+            mode = "device" if nbytes <= self._tier_device_room(device) else "host"
         self.tier_mode = mode
         if rows == 0:
             return
         shape = (rows, L, self.head_dim)
         if mode == "device":
-            self._tier = (torch.empty(shape, dtype=dtype, device=device), torch.empty(shape, dtype=dtype, device=device))
-        else:
+            try:
+                self._tier = (torch.empty(shape, dtype=dtype, device=device),
+                              torch.empty(shape, dtype=dtype, device=device))
+            except torch.cuda.OutOfMemoryError:
+                if not auto:
+                    raise
+                self._tier = None
+                torch.cuda.empty_cache()
+                mode = self.tier_mode = "host"
+        if mode == "host":
             self._tier = (torch.empty(shape, dtype=dtype, pin_memory=True),
                           torch.empty(shape, dtype=dtype, pin_memory=True))
+
+    def _tier_device_room(self, device):
+        """Bytes "auto" lets the full-KV tier take in HBM: tier_device_budget
+        when set; otherwise the device memory still free once the KV arena
+        is allocated (the driver's free memory plus what torch's allocator
+        holds unused), less a reserve of an eighth of the device for the
+        model's weights growth, activations and workspaces."""
+        budget = getattr(self.config, "tier_device_budget", None)
+        if budget is not None:
+            return int(budget)
+        free, total = torch.cuda.mem_get_info(device)
+        cached = torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+        return max(free + cached - total // 8, 0)
 
     def update(self, key_states, value_states, layer_idx, cache_kwargs=None):
         """heterocache/cache_utils.py:884-1005."""
@@ -646,10 +685,14 @@ class HeteroCache(DynamicCache):
     def _step_stat_view(self, layer_idx, query_states):
         """Output view [B*Hkv, G, 2] of this step's softmax statistics for a
         layer with leaders (slot: the step's position in the check cycle), or
-        None.  In Llama order the attention runs before the step's query is
-        buffered, so the slot is the count of queries buffered so far."""
+        None.  Only the batched check of the Llama order consumes them: there
+        the attention runs before the step's query is buffered, so the slot
+        is the count of queries buffered so far.  In Qwen order (select
+        before attention, each layer checked at once with the two-pass
+        scorer) nothing is requested."""
         st = self._drift[layer_idx]
-        if st is None or not st.leaders or not self._one_pass_check(query_states.dtype):
+        if (st is None or not st.leaders or self._select_after_attention is False
+                or not self._one_pass_check(query_states.dtype)):
             return None
         slot = st.count
         if slot >= self.decode_step:
@@ -673,6 +716,9 @@ class HeteroCache(DynamicCache):
         st = self._drift[layer_idx]
         if st is None:
             st = self._drift[layer_idx] = _LayerDrift()
+        if self._select_after_attention is None:
+            # The attention consumed the step's pending token if it ran first.
+            self._select_after_attention = self._pending[layer_idx] is None
         S = self.decode_step
         if st.qbuf is None:
             if self._qbuf_all is None:
@@ -735,8 +781,10 @@ class HeteroCache(DynamicCache):
                 self._check_layer(layer)
 
     def _check_layer(self, layer_idx):
-        """One layer's drift check and gated retrieval."""
+        """One layer's drift check and gated retrieval (two-pass scorer: any
+        statistics the decode launches reported for this cycle go unused)."""
         st = self._drift[layer_idx]
+        st.stat_mask = 0
         if not st.leaders or not any(st.members):
             return
         S = self.decode_step
@@ -1128,6 +1176,27 @@ class BaseKVCache(DynamicCache):
         if len(self.key_cache) <= (layer_idx or 0):
             return 0
         return self._seen_tokens
+
+    def to_legacy_cache(self):
+        """((key, value), ...) per layer (heterocache/cache_utils.py:213-217)."""
+        return tuple((self.key_cache[i], self.value_cache[i]) for i in range(len(self.key_cache)))
+
+    @classmethod
+    def from_legacy_cache(cls, past_key_values, config=None):
+        """A cache holding the given per-layer (key, value) pairs
+        (heterocache/cache_utils.py:219-225).  The pairs are taken as they are
+        -- they are what to_legacy_cache returned, already compressed -- and
+        the token count is layer 0's length.  (The reference re-enters update
+        without the cache_kwargs its update requires, :142-146, so its
+        version raises TypeError; replaying the pairs through update would
+        compress them a second time.)  config: the subclass's constructor
+        argument, for the subclasses that take one."""
+        cache = cls() if config is None else cls(config)
+        for k, v in past_key_values:
+            cache.key_cache.append(k)
+            cache.value_cache.append(v)
+        cache._seen_tokens = int(past_key_values[0][0].shape[-2]) if len(past_key_values) else 0
+        return cache
 
     def clear_temp_kv_cache(self):
         if self.temp_key_cache:

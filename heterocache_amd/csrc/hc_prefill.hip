@@ -408,10 +408,13 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
       continue;
     }
     const float inv = 1.f / lt;
-    // The softmax state of query qi over its visible keys, as a scorer's
-    // statistics pass would form it: m bounds the scaled base-2 scores (the
-    // lazy rescale keeps it within 2^kPfLazy of their maximum) and lt is the
-    // sum of exp2(score - m).
+    // The softmax state of query qi over its visible keys: m is a reference
+    // point of the scaled base-2 scores, not a bound -- the lazy rescale
+    // lets the true maximum sit up to kPfLazy above it, so a single
+    // exp2(score - m) can reach 2^kPfLazy -- and lt is the sum of
+    // exp2(score - m).  Consumers use only m + log2(lt), the log-sum-exp,
+    // which is exact whatever m is; one that needs p <= 1 per term must
+    // renormalise first.
     const int w = qi - (a.Lq - a.st_rows);
     if (a.st && w >= 0 && g4 == 0) {
       float* so = a.st + (((int64_t)b * a.Hq + hq) * a.st_rows + w) * 2;
@@ -442,8 +445,9 @@ __global__ __launch_bounds__(kPfThreads, sizeof(T) == 4 ? 1 : 3) void prefill_at
 // operand of O^T += V^T P^T, whose k-slots follow the order in which the
 // S^T accumulators hold P (k-slot 8g + i <-> token 16*(i/4) + 4g + i%4).
 // A workgroup takes one split of the row's 32-token tiles; its four waves
-// take every fourth tile of it and each writes its own partial (the split
-// count seen by prefill_merge_kernel is 4 * splits).
+// take every fourth tile of it, are combined in LDS, and the split writes
+// one partial of kPfPartStride floats (the split count seen by
+// prefill_merge_kernel is the number of splits).
 // ---------------------------------------------------------------------------
 constexpr int kDvPitch = HC_TILE + 8;            // fp32: transposed V row, 32 k-slots + skew
 constexpr int kDvNPitch = HC_HEAD_DIM + 16;      // 16-bit: natural V row, 128 channels + skew

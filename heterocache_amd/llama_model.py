@@ -21,7 +21,6 @@ from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
 from . import ops
@@ -70,35 +69,28 @@ def prefill_attention(query_states, key_states, value_states, attention_mask, sc
     keys; the queries are the last L positions (a whole prompt, or one chunk
     of a chunked prefill over the keys staged so far).  Returns [B, L, Hq*d].
 
-    On a ROCm device without a padding mask this is hc_prefill_attn (the
-    reference calls flash-attn here, heterocache/llama_model.py:353-361).  A
-    mask that carries padding goes through PyTorch's SDPA with that mask.
-    stat_out ([B, Hq, W, 2] float32, native path only) receives the last W
-    queries' softmax statistics (ops.prefill_attn)."""
+    This is hc_prefill_attn (the reference calls flash-attn here,
+    heterocache/llama_model.py:353-361).  There is no second code path: a
+    mask that carries more than bottom-right causality (padding), inputs
+    off the ROCm device or a head_dim other than 128 raise
+    NotImplementedError.  The reference's HeteroCache scores and sizes its
+    pool for one unpadded sequence (heterocache/cache_utils.py:704-722,
+    :807-829), so its path never sees a padded prompt; ragged batches are
+    served as one cache per sequence.
+    stat_out ([B, Hq, W, 2] float32) receives the last W queries' softmax
+    statistics (ops.prefill_attn)."""
     B, Hq, L, D = query_states.shape
     Lk = key_states.shape[2]
     mask = attention_mask
     if mask is not None and mask.dim() == 4 and _plain_causal(mask, L, Lk):
         mask = None
-    if query_states.is_cuda and mask is None and D == ops.HEAD_DIM:
-        return ops.prefill_attn(query_states, key_states, value_states, scaling,
-                                stat_out=stat_out).view(B, L, Hq * D)
-    if stat_out is not None:
-        raise ValueError("softmax statistics come from the native prefill attention only")
-    q = query_states.contiguous()
-    k = key_states.contiguous()
-    v = value_states.contiguous()
-    gqa = Hq != k.shape[1]
-    if mask is not None and mask.dim() == 4:
-        mask = mask[..., :L, :Lk]
-        out = F.scaled_dot_product_attention(q, k, v, attn_mask=mask, scale=scaling, enable_gqa=gqa)
-    elif L == Lk:
-        out = F.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scaling, enable_gqa=gqa)
-    else:  # queries at positions Lk-L .. Lk-1
-        pos_q = torch.arange(Lk - L, Lk, device=q.device)[:, None]
-        allowed = torch.arange(Lk, device=q.device)[None, :] <= pos_q
-        out = F.scaled_dot_product_attention(q, k, v, attn_mask=allowed, scale=scaling, enable_gqa=gqa)
-    return out.transpose(1, 2).reshape(B, L, Hq * D)
+    if mask is not None:
+        raise NotImplementedError("hc_prefill_attn takes causal prompts without padding; this attention mask "
+                                  "carries padding (serve ragged prompts as one sequence per cache)")
+    if not query_states.is_cuda or D != ops.HEAD_DIM:
+        raise NotImplementedError(f"hc_prefill_attn needs ROCm device tensors of head_dim {ops.HEAD_DIM} "
+                                  f"(got {query_states.device}, head_dim {D})")
+    return ops.prefill_attn(query_states, key_states, value_states, scaling, stat_out=stat_out).view(B, L, Hq * D)
 
 
 class LlamaAttention(nn.Module):

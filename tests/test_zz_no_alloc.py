@@ -77,17 +77,47 @@ def test_noalloc_matches_workspace_entry_point_twice(dev):
     _check_case(dev, [700, 33, 2048, 5, 1200], 7, torch.float16, 32)
 
 
-def test_noalloc_refuses_workspace_beyond_the_scratch(dev):
+def _largest_fitting_parts(lib, rows, G, limit=16 << 20):
+    """Largest part count whose workspace (hc_decode_workspace_size) fits the scratch."""
+    lo, hi = 1, 1
+    while lib.hc_decode_workspace_size(rows, G, hi) <= limit:
+        lo, hi = hi, hi * 2
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        if lib.hc_decode_workspace_size(rows, G, mid) <= limit:
+            lo = mid
+        else:
+            hi = mid
+    return lo
+
+
+def test_noalloc_accepts_the_largest_fitting_workspace_and_refuses_one_part_more(dev):
+    """The scratch limit is exact: the largest grid whose workspace fits 16 MiB
+    runs and matches the workspace entry point bit for bit (surplus
+    workgroups find no chunk); one part more is refused before anything runs."""
     lib = _lib.load()
-    rows, G = 8, 16
-    parts = (16 << 20) // (G * 130 * 4) + 1   # one part past the 16 MiB scratch
-    assert lib.hc_decode_workspace_size(rows, G, parts) > (16 << 20)
-    st = KVStore([64] * rows, torch.bfloat16, dev)
-    q = torch.zeros((rows, G, 128), dtype=torch.bfloat16, device=dev)
-    kn = torch.zeros((rows, 128), dtype=torch.bfloat16, device=dev)
+    lens, G, dtype = [64, 1, 0, 300, 31, 64, 2, 129], 16, torch.bfloat16
+    rows = len(lens)
+    parts = _largest_fitting_parts(lib, rows, G)
+    assert lib.hc_decode_workspace_size(rows, G, parts) <= (16 << 20) < lib.hc_decode_workspace_size(rows, G, parts + 1)
+    a, b = _twin_stores(lens, dtype, dev, 41)
+    g = torch.Generator(device=dev).manual_seed(41)
+    q = torch.randn((rows, G, 128), device=dev, generator=g).to(dtype)
+    kn = torch.randn((rows, 128), device=dev, generator=g).to(dtype)
+    vn = torch.randn((rows, 128), device=dev, generator=g).to(dtype)
+    ws = torch.empty(lib.hc_decode_workspace_size(rows, G, parts), dtype=torch.uint8, device=dev)
+    out_ws = torch.empty_like(q)
+    out_na = torch.full_like(q, float("nan"))
+    assert _call(lib, a, q, kn, vn, out_ws, parts, 4, ws) == 0
+    rc = _call(lib, b, q, kn, vn, out_na, parts, 4)
+    assert rc == 0, lib.hc_last_error()
+    torch.cuda.synchronize()
+    assert torch.isfinite(out_ws.float()).all() and torch.equal(out_ws, out_na)
+    assert a.row_len.tolist() == b.row_len.tolist() == [n + 1 for n in lens]
+    # One part more: refused, nothing launched (lengths and output unchanged).
     out = torch.zeros_like(q)
-    rc = _call(lib, st, q, kn, kn, out, parts, 4)
+    rc = _call(lib, b, q, kn, vn, out, parts + 1, 4)
     assert rc == _lib.HC_ERR_INVALID
     assert b"16777216" in lib.hc_last_error()
     torch.cuda.synchronize()
-    assert st.row_len.tolist() == [0] * rows and torch.equal(out, torch.zeros_like(out))
+    assert b.row_len.tolist() == [n + 1 for n in lens] and torch.equal(out, torch.zeros_like(out))
