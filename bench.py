@@ -43,9 +43,9 @@ def parse():
     p.add_argument("--drift-groups", type=int, default=None,
                    help="drift_check_groups of the HeteroCache phase (default: the config's default)")
     p.add_argument("--full-step-only", action="store_true", help="run only the HeteroCache full-step phase")
-    p.add_argument("--full-runs", default="natural,never,always,host_never,host_always",
-                   help="comma-separated runs of the full-step phase (natural, never, always, host_never, "
-                        "host_always)")
+    p.add_argument("--full-runs", default="natural,never,always,always_f32,host_never,host_always",
+                   help="comma-separated runs of the full-step phase (natural, never, always, always_f32, "
+                        "host_never, host_always)")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
     p.add_argument("--overlap-check", action="store_true",
                    help="full step: run the drift checks and their retrieval on a side stream (overlap_drift_check)")
@@ -188,8 +188,11 @@ def full_step_phase(args, torch, dev):
     groups = args.drift_groups
     # (label, threshold, steps, tier placement): the default placement keeps
     # the 12.8 GB tier in HBM; the host-pinned tier is measured beside it.
+    # The runs use the default configuration (the reference's casts of the
+    # scores to the model dtype); "always_f32" ranks float32 scores instead
+    # (round_scores=False, the one-pass drift check).
     runs = (("natural", 0.5, args.full_steps, "auto"), ("never", -1.0, 100, "auto"), ("always", 2.0, 100, "auto"),
-            ("host_never", -1.0, 100, "host"), ("host_always", 2.0, 100, "host"))
+            ("always_f32", 2.0, 100, "auto"), ("host_never", -1.0, 100, "host"), ("host_always", 2.0, 100, "host"))
     wanted = set(args.full_runs.split(","))
     unknown = wanted - {r[0] for r in runs}
     if unknown:
@@ -202,13 +205,13 @@ def full_step_phase(args, torch, dev):
     check_k_bytes = npiv * L * D * 2
     res = {}
 
-    def make_cache(thr, tier, max_gen):
+    def make_cache(thr, tier, max_gen, round_scores):
         kw = {} if groups is None else {"drift_check_groups": groups}
         cfg = HeteroCacheConfig(data, compression_ratio=args.ratio, stable_threshold=thr, real_offload=True,
                                 max_gen_len=max_gen, decode_step=S, pooling="avgpool", kernel_size=5,
                                 num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
                                 tier_placement=tier, one_pass_drift_check=not args.two_pass_check,
-                                overlap_drift_check=args.overlap_check, **kw)
+                                overlap_drift_check=args.overlap_check, round_scores=round_scores, **kw)
         return HeteroCache(cfg)
 
     def prefill(cache, keep_inputs):
@@ -234,7 +237,7 @@ def full_step_phase(args, torch, dev):
         return ms / NL, total, inputs
 
     for label, thr, steps, tier in runs:
-        cache = make_cache(thr, tier, steps + S + 8)
+        cache = make_cache(thr, tier, steps + S + 8, not label.endswith("_f32"))
         pre_ms, pre_total, inputs = prefill(cache, True)
         tier_mode = cache.tier_mode
 
@@ -254,12 +257,14 @@ def full_step_phase(args, torch, dev):
         triggered = torch.zeros_like(trig)
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
         main, checks_on = torch.cuda.current_stream(dev), cache.drift_stream(dev)
+        gathers_on = cache.retrieval_stream(dev)
         t0 = time.perf_counter()
         for i in range(steps):
             ev[i][0].record()
             decode_step(S + i)
             if i == steps - 1:
                 main.wait_stream(checks_on)  # the last check's work counts in the last step
+                main.wait_stream(gathers_on)
             ev[i][1].record()
             if (S + i + 1) % S == 0:
                 with torch.cuda.stream(checks_on):
@@ -278,7 +283,8 @@ def full_step_phase(args, torch, dev):
         attn_bytes = sum((len0 + rows * (i + 1)) * D * 2 * 2 for i in range(steps)) + steps * NL * 2 * Hkv * G * D * 2
         nbytes = attn_bytes + checks * check_k_bytes + ret_bytes
         ms = float(np.mean(step_ms))
-        res[label] = {"tier": tier_mode, "steps": steps, "checks": checks, "ms_per_step": round(ms, 4),
+        res[label] = {"tier": tier_mode, "round_scores": cache.round_scores, "one_pass_checks": cache.one_pass_checks,
+                      "steps": steps, "checks": checks, "ms_per_step": round(ms, 4),
                       "wall_ms_per_step": round(wall, 4),
                       "leader_triggers": trig_total, "leaders": int(trig.numel()),
                       "bytes_per_step": int(nbytes / steps),
@@ -303,6 +309,8 @@ def full_step_phase(args, torch, dev):
            "ms_per_step_no_retrieval": res["never"]["ms_per_step"] if "never" in res else None,
            "ms_per_step_retrieval_every_check": res["always"]["ms_per_step"] if "always" in res else None,
            "retrieval_exposed_ms_per_check": exposed("always", "never"),
+           "reference_cast_chain_cost_ms_per_step": (round(res["always"]["ms_per_step"] - res["always_f32"]["ms_per_step"], 4)
+                                                     if "always_f32" in res and "always" in res else None),
            "host_tier_retrieval_exposed_ms_per_check": exposed("host_always", "host_never"),
            "roofline": {"bound": "hbm", "achieved": round(a["tbs"] * 1000, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": a["frac_of_hbm_peak"], "run": f"{'retrieval every check' if a is res.get('always') else 'run'}"

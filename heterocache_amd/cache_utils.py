@@ -51,8 +51,13 @@ class HeteroCacheConfig:
 
     retrieval_topk: cap on the tokens retrieved into a satellite (None =
     the reference's full budget).  window_size: observation window of the
-    prefill scorer (1 = the reference's last query).  round_scores: reproduce
-    the reference's casts of scores to the model dtype.  reference_quirks:
+    prefill scorer (1 = the reference's last query).  round_scores (default
+    True, as the baseline compressors): the reference's casts of the scores
+    to the model dtype -- logits, softmax probabilities and pooled scores
+    rounded as heterocache/cache_utils.py:814-829, 1037-1057 and 1167-1187
+    round them; False ranks the float32 scores (finer: fewer ties, and
+    the one-pass drift check and the attention-statistics window scorer
+    apply).  reference_quirks:
     float64 retrieval lengths and relation-order pivot sets, as the reference.
     chunk_tiles: decode-attention chunk (None = one resident round).
     batched_drift_check: when the model selects after attention (Llama
@@ -83,6 +88,12 @@ class HeteroCacheConfig:
     round_scores, for narrower windows (the default last-query scorer among
     them) or when the prefill call holds fewer than window_size queries (a
     short last chunk), the two-pass scorer runs.
+    retrieval_stream: where a batched check's retrieval gathers from the
+    tier arena run -- "side" (one gather per layer on a side stream, each
+    layer's next attention waiting for its own rows only), "main" (one
+    gather for the whole group on the check's stream) or "auto" ("side" for
+    the host-pinned tier, whose reads take milliseconds over the host link;
+    "main" for the HBM tier, whose gather takes tens of microseconds).
     tier_placement: where the satellites' full-KV tier lives when
     real_offload is set -- "host" (pinned host memory, retrieval read over
     the host link), "device" (an HBM arena, retrieval a device gather) or
@@ -99,10 +110,11 @@ class HeteroCacheConfig:
                  max_gen_len: Optional[int] = 128, decode_step: Optional[int] = 4, pooling: Optional[str] = "avgpool",
                  kernel_size: Optional[int] = 5, num_attn_heads: Optional[int] = 32, num_kv_heads: Optional[int] = 8,
                  num_layers: Optional[int] = 32, retrieval_topk: Optional[int] = None, window_size: int = 1,
-                 round_scores: bool = False, reference_quirks: bool = False, chunk_tiles: Optional[int] = None,
+                 round_scores: bool = True, reference_quirks: bool = False, chunk_tiles: Optional[int] = None,
                  batched_drift_check: bool = True, drift_check_groups: int = 1, tier_placement: str = "auto",
                  tier_device_budget: Optional[int] = None, overlap_drift_check: bool = False,
-                 one_pass_drift_check: bool = True, attention_stats_scoring: bool = True):
+                 one_pass_drift_check: bool = True, attention_stats_scoring: bool = True,
+                 retrieval_stream: str = "auto"):
         self.data = data
         self.stable_threshold = stable_threshold
         self.compression_ratio = compression_ratio
@@ -129,6 +141,9 @@ class HeteroCacheConfig:
         self.overlap_drift_check = overlap_drift_check
         self.one_pass_drift_check = one_pass_drift_check
         self.attention_stats_scoring = attention_stats_scoring
+        if retrieval_stream not in ("auto", "side", "main"):
+            raise ValueError(f"retrieval_stream must be 'auto', 'side' or 'main', not {retrieval_stream!r}")
+        self.retrieval_stream = retrieval_stream
 
 
 def _f32_caps(base, ratios, seq_len):
@@ -136,6 +151,61 @@ def _f32_caps(base, ratios, seq_len):
     r = np.asarray(ratios, dtype=np.float32)
     caps = np.trunc(np.float32(base) * r).astype(np.int64)
     return np.clip(caps, 0, seq_len)
+
+
+class _DevicePack:
+    """Small host arrays packed into one buffer and copied to the device in
+    one transfer; add() returns a placeholder that resolve() turns into the
+    device view of that array."""
+
+    class Slot:
+        __slots__ = ("off", "dtype", "n")
+
+        def __init__(self, off, dtype, n):
+            self.off, self.dtype, self.n = off, dtype, n
+
+    _TORCH = {np.dtype(np.int32): torch.int32, np.dtype(np.int64): torch.int64}
+
+    def __init__(self):
+        self.parts = []
+        self.words = 0   # int64 words used
+
+    def add(self, values, dtype):
+        a = np.ascontiguousarray(np.asarray(values), dtype=dtype).reshape(-1)
+        slot = _DevicePack.Slot(self.words, a.dtype, a.size)
+        self.parts.append((self.words, a))
+        self.words += max((a.nbytes + 7) // 8, 1)
+        return slot
+
+    def upload(self, device):
+        buf = np.zeros(max(self.words, 1), dtype=np.int64)
+        raw = buf.view(np.uint8)
+        for off, a in self.parts:
+            raw[off * 8:off * 8 + a.nbytes] = a.view(np.uint8)
+        return ops.to_device(buf, device, torch.int64)
+
+    @staticmethod
+    def view(dev, slot):
+        """Device view of one added array inside the uploaded buffer."""
+        words = max((slot.n * slot.dtype.itemsize + 7) // 8, 1)
+        t = dev[slot.off:slot.off + words]
+        if slot.dtype == np.int32:
+            t = t.view(torch.int32)
+        return t[:slot.n]
+
+    @staticmethod
+    def resolve(obj, dev):
+        """Replace every Slot inside nested dicts / tuples of obj by its view."""
+        def walk(x):
+            if isinstance(x, _DevicePack.Slot):
+                return _DevicePack.view(dev, x)
+            if isinstance(x, dict):
+                return {k: walk(v) for k, v in x.items()}
+            if isinstance(x, tuple):
+                return tuple(walk(v) for v in x)
+            return x
+        for k in list(obj):
+            obj[k] = walk(obj[k])
 
 
 class _LayerDrift:
@@ -158,9 +228,12 @@ class HeteroCache(DynamicCache):
 
     # Workgroups of the prefill copy into the host-pinned tier.
     TIER_COPY_WORKGROUPS = 32
-    # Workgroups of a retrieval gather from the host-pinned tier.  Reads over
-    # the host link slow concurrent HBM streaming in proportion to the reads
-    # in flight; 32 workgroups keep the link near its peak.
+    # Workgroups of a retrieval gather from the host-pinned tier, and of any
+    # gather beside the decode on the side stream.  Reads over the host link
+    # slow concurrent HBM streaming in proportion to the reads in flight; 32
+    # workgroups keep the link near its peak, and a side-stream gather of
+    # one layer's rows from HBM still finishes within a layer's attention,
+    # without taking the slots the decode kernel sizes its grid for.
     RETRIEVAL_WORKGROUPS = 32
 
     def __init__(self, cache_config):
@@ -184,7 +257,7 @@ class HeteroCache(DynamicCache):
         self.quirks = bool(getattr(cfg, "reference_quirks", False))
         self.retrieval_topk = getattr(cfg, "retrieval_topk", None)
         self.window_size = int(getattr(cfg, "window_size", 1) or 1)
-        self.round_scores = bool(getattr(cfg, "round_scores", False))
+        self.round_scores = bool(getattr(cfg, "round_scores", True))
         self.chunk_tiles = getattr(cfg, "chunk_tiles", None)
         self.batched_check = bool(getattr(cfg, "batched_drift_check", True))
         self.overlap_check = bool(getattr(cfg, "overlap_drift_check", False))
@@ -228,6 +301,9 @@ class HeteroCache(DynamicCache):
         # drift state of every layer (per-layer objects hold views of them).
         self._arena = None
         self._tile_table = None      # int64 arena tile offsets of all rows, layer-major
+        # Every layer's prefill metadata on the device, built once per cache
+        # for inputs of one shape and stride: (key, [per-layer dict or None]).
+        self._pplans = None
         self._qbuf_all = None        # [NL, B, Hq, S, 128] buffered decode queries
         # [NL, B*Hkv, G, S, 2] softmax statistics (max bound, sum) of every
         # buffered decode query over its row's prefill keys, reported by the
@@ -340,12 +416,26 @@ class HeteroCache(DynamicCache):
         return self._side
 
     def drift_stream(self, device):
-        """The stream the batched drift checks and their retrieval run on: the
-        trigger flags, reference sets and retrieved rows are ordered on it
-        (the main stream when checks do not overlap)."""
-        if self.overlap_check or self.tier_mode == "host":
+        """The stream the batched drift checks run on: the trigger flags and
+        reference sets are ordered on it (the main stream unless checks
+        overlap, overlap_drift_check)."""
+        if self.overlap_check:
             return self._side_stream(device)
         return torch.cuda.current_stream(device)
+
+    def _side_retrieval(self):
+        mode = getattr(self.config, "retrieval_stream", "auto")
+        if mode == "auto":
+            return self.tier_mode == "host"
+        return mode == "side"
+
+    def retrieval_stream(self, device):
+        """The stream the batched checks' retrieval gathers from the tier
+        arena run on (with "side", each layer's next attention waits for its
+        own rows)."""
+        if self._tier is not None and self._side_retrieval():
+            return self._side_stream(device)
+        return self.drift_stream(device)
 
     def _share_with_side(self, side, tensors):
         """Record device buffers allocated on the main stream as used by the
@@ -379,14 +469,37 @@ class HeteroCache(DynamicCache):
         row_caps = [self._layer_row_caps(layer) for layer in range(self.num_layers)]
         tiles = [KVStore.tiles_for(c) for c in row_caps]
         n = max(sum(tiles), 1) * ops.TILE * ops.HEAD_DIM
-        k = torch.zeros(n, dtype=dtype, device=device)
-        v = torch.zeros(n, dtype=dtype, device=device)
+        # Left uninitialised (clearing 17 GB at 128K took ~5 ms): every reader
+        # masks by position -- decode attention past each row's length (V
+        # operands zeroed), the scorers past their visible limit -- so stale
+        # slots, even NaN, never reach a result.
+        k = torch.empty(n, dtype=dtype, device=device)
+        v = torch.empty(n, dtype=dtype, device=device)
         self._arena = (k, v)
-        base = 0
+        # Every store's row metadata in one transfer: tile offsets of all
+        # rows (layer-major, which is also the model-wide tile table), then
+        # per layer capacities, zero lengths, identity order, status word.
+        pack = _DevicePack()
+        offs, slots, base = [], [], 0
         for layer in range(self.num_layers):
-            self.stores[layer] = KVStore(row_caps[layer], dtype, device, arena=(k, v, base), layer_idx=layer)
+            off, cap = KVStore.host_metadata(row_caps[layer], base)
+            offs.append(off)
             base += tiles[layer]
-        self._tile_table = torch.cat([st.row_tile_off for st in self.stores])
+            nr = len(cap)
+            slots.append({"row_cap": pack.add(cap, np.int32), "row_len": pack.add(np.zeros(nr), np.int32),
+                          "row_order": pack.add(np.arange(nr), np.int32), "status": pack.add([0], np.int32)})
+        table = pack.add(np.concatenate(offs), np.int64)
+        dev_meta = pack.upload(device)
+        self._tile_table = _DevicePack.view(dev_meta, table)
+        base, r0 = 0, 0
+        for layer in range(self.num_layers):
+            nr = len(row_caps[layer])
+            meta = {k_: _DevicePack.view(dev_meta, v_) for k_, v_ in slots[layer].items()}
+            meta["row_tile_off"] = self._tile_table[r0:r0 + nr]
+            self.stores[layer] = KVStore(row_caps[layer], dtype, device, arena=(k, v, base), layer_idx=layer,
+                                         meta=meta)
+            base += tiles[layer]
+            r0 += nr
         self._init_tier(device, dtype)
 
     def _init_tier(self, device, dtype):
@@ -439,6 +552,106 @@ class HeteroCache(DynamicCache):
         cached = torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
         return max(free + cached - total // 8, 0)
 
+    def _layer_plan(self, layer_idx, key_states, value_states=None):
+        """This layer's prefill metadata already on the device, or None when
+        the inputs differ in shape or stride from those the plans were
+        built for (the calls then build their metadata themselves).  The
+        plans of all layers are built at the first prefill call and copied
+        to the device in one transfer, so a layer's prefill launches its
+        kernels without host-to-device copies of small lists."""
+        if value_states is not None and (value_states.shape != key_states.shape
+                                         or value_states.stride() != key_states.stride()):
+            return None
+        key = (tuple(key_states.shape), tuple(key_states.stride()), key_states.dtype, str(key_states.device))
+        if self._pplans is None:
+            self._pplans = (key,) + self._build_prefill_plans(key_states)
+        if self._pplans[0] != key:
+            return None
+        _, plans, dev = self._pplans
+        p = plans[layer_idx]
+        if p is not None and not p.get("resolved"):
+            _DevicePack.resolve(p, dev)   # this layer's views, made at its first use
+            p["resolved"] = True
+        return p
+
+    def _build_prefill_plans(self, key_states):
+        """Per layer (batch rows b, kv-heads h, row r = b * Hkv + h):
+        keep-head store plan and lengths; tier copy offsets; pivot-set caps
+        and the (leader, batch) row order of the reference sets; budget
+        selection caps, gather plan and lengths of the compressed heads; the
+        row order after the prefill.  Layers whose head data the per-call
+        paths would reject get None (the per-call path raises as before)."""
+        B, Hkv, L, D = self.bsz, self.num_kv_heads, self.prefill_len, self.head_dim
+        s0, s1, s2 = key_states.stride()[:3]
+        shape, stride = tuple(key_states.shape), tuple(key_states.stride())
+        esz = key_states.element_size()
+        if key_states.dim() != 4 or key_states.stride(3) != 1 or any((x * esz) % 16 for x in (s0, s1, s2)):
+            return [None] * self.num_layers, None   # the per-call paths validate (and refuse) such inputs
+        pack = _DevicePack()
+        tier = None if self._tier is None else self._tier_arena4()[0]
+        plans = []
+        for layer in range(self.num_layers):
+            try:
+                plans.append(self._layer_prefill_plan(layer, pack, B, Hkv, L, D, s0, s1, s2, shape, stride, tier))
+            except (ValueError, KeyError, IndexError):
+                plans.append(None)
+        return plans, pack.upload(key_states.device)
+
+    def _layer_prefill_plan(self, layer, pack, B, Hkv, L, D, s0, s1, s2, shape, stride, tier):
+        data = self.data
+        p = {}
+        host_len = np.zeros(B * Hkv, dtype=np.int64)
+        keep = list(data["need_to_keep_counts"][layer])
+        if keep:
+            bh = [(b, h) for b in range(B) for h in keep]
+            rows = np.asarray([b * Hkv + h for b, h in bh], dtype=np.int64)
+            counts = np.full(len(rows), L, dtype=np.int64)
+            p["keep"] = {"src_off": pack.add([b * s0 + h * s1 for b, h in bh], np.int64), "tok_stride": s2,
+                         "src_len": L, "trig_of": None, "shape": shape, "stride": stride, "idx_off": None,
+                         "counts": pack.add(counts, np.int32), "host_counts": counts,
+                         "rows": pack.add(rows, np.int32), "host_rows": rows, "max_count": L}
+            p["keep_len"] = (rows, counts, pack.add(rows, np.int64), p["keep"]["counts"])
+            host_len[rows] = L
+        sats = list(data["need_to_update_counts"][layer])
+        if sats and tier is not None:
+            n, r0 = len(sats), self._tier_base[layer]
+            p["tier"] = {"src_off": pack.add([b * s0 + h * s1 for b in range(B) for h in sats], np.int64),
+                         "dst_off": pack.add([(r0 + b * n + i) * tier.stride(1) for b in range(B) for i in range(n)],
+                                             np.int64),
+                         "counts": pack.add(np.full(B * n, L), np.int32), "max_count": L}
+        pivots = list(data["need_to_select_counts"][layer])
+        rel = data["leader_member_relations"][layer]
+        if pivots:
+            K = min(self.base_compress_len, L)
+            leaders = [int(h) for h in rel]
+            src = ([min(i, len(pivots) - 1) for i in range(len(leaders))] if self.quirks
+                   else [pivots.index(h) for h in leaders])
+            p["piv_caps"] = pack.add(np.full(B * len(pivots), K), np.int32)
+            p["piv_order"] = pack.add([self._score_row(b, si, len(pivots)) for si in src for b in range(B)], np.int64)
+        n_c = data["need_to_compress_counts"][layer]
+        if n_c:
+            caps = _f32_caps(self.base_compress_len, data["allocation_matrix"][layer][:n_c], L)
+            rows = np.asarray([b * Hkv + h for b in range(B) for h in range(n_c)], dtype=np.int64)
+            caps_rows = np.asarray([int(caps[h]) for b in range(B) for h in range(n_c)], dtype=np.int64)
+            if caps_rows.max() > 0:
+                W = self.window_size
+                span = L - W if W > 1 else L
+                width = max(1, min(int(caps_rows.max()), span + (W if W > 1 else 0)))
+                cdev = pack.add(caps_rows, np.int32)
+                p["caps"] = cdev
+                p["max_cap"] = int(caps_rows.max())
+                p["compress"] = {"src_off": pack.add([b * s0 + h * s1 for b in range(B) for h in range(n_c)], np.int64),
+                                 "tok_stride": s2, "src_len": L, "trig_of": None, "shape": shape,
+                                 "stride": stride, "idx_off": pack.add(np.arange(len(rows)) * width, np.int64),
+                                 "counts": cdev, "host_counts": caps_rows, "rows": pack.add(rows, np.int32),
+                                 "host_rows": rows, "max_count": int(caps_rows.max())}
+                p["idx_width"] = width
+                p["compress_len"] = (rows, caps_rows, pack.add(rows, np.int64), cdev)
+                host_len[rows] = caps_rows
+        # Row order once the prefill has set every length (longest first).
+        p["order"] = pack.add(np.argsort(-host_len, kind="stable"), np.int32)
+        return p
+
     def update(self, key_states, value_states, layer_idx, cache_kwargs=None):
         """heterocache/cache_utils.py:884-1005."""
         if layer_idx == 0:
@@ -469,13 +682,19 @@ class HeteroCache(DynamicCache):
         seq_len = key_states.shape[-2]
         self.prefill_len = seq_len
         keep = self.data["need_to_keep_counts"][layer_idx]
-        if keep:
+        plan = self._layer_plan(layer_idx, key_states, value_states)
+        store = self.stores[layer_idx]
+        if keep and plan is not None:
+            store.launch_rows(plan["keep"], key_states, value_states, set_len=False)
+            rows, lens, drows, dlens = plan["keep_len"]
+            store.set_lengths_planned(rows, lens, drows, dlens, plan["order"])
+        elif keep:
             bh = [(b, h) for b in range(self.bsz) for h in keep]
-            self.stores[layer_idx].write_rows(key_states, value_states, bh,
-                                              [b * self.num_kv_heads + h for b, h in bh], [seq_len] * len(bh))
-        self._backup_full_tier(key_states, value_states, layer_idx)
+            store.write_rows(key_states, value_states, bh, [b * self.num_kv_heads + h for b, h in bh],
+                             [seq_len] * len(bh))
+        self._backup_full_tier(key_states, value_states, layer_idx, plan)
 
-    def _backup_full_tier(self, key_states, value_states, layer_idx):
+    def _backup_full_tier(self, key_states, value_states, layer_idx, plan=None):
         """Full-KV tier of the satellite heads (heterocache/cache_utils.py:939-967)."""
         sats = list(self.data["need_to_update_counts"][layer_idx])
         if not sats:
@@ -492,8 +711,12 @@ class HeteroCache(DynamicCache):
         tk, tv = self._tier_arena4()
         src = [(b, h) for b in range(self.bsz) for h in sats]
         dst = [(0, r0 + b * n + i) for b in range(self.bsz) for i in range(n)]
+        tp = plan.get("tier") if plan is not None else None
         if self.tier_mode == "device":
-            ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), max_workgroups=1024)
+            if tp is not None:
+                ops.copy_rows_planned(key_states, value_states, tp, tk, tv, max_workgroups=1024)
+            else:
+                ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), max_workgroups=1024)
         else:
             dev = key_states.device
             side = self._side_stream(dev)
@@ -501,8 +724,12 @@ class HeteroCache(DynamicCache):
             # A few workgroups write the satellites' rows straight from the
             # prefill tensors into the pinned tier at link speed, beside the
             # compression kernels on the main stream.
-            ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), dst_is_host=True,
-                          max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
+            if tp is not None:
+                ops.copy_rows_planned(key_states, value_states, tp, tk, tv, dst_is_host=True,
+                                      max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
+            else:
+                ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), dst_is_host=True,
+                              max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
             key_states.record_stream(side)
             value_states.record_stream(side)
         # The layer's rows of the arena, in the reference's [B, heads, L, 128] shape.
@@ -570,7 +797,11 @@ class HeteroCache(DynamicCache):
         scores = compress.last_query_scores(query_states, key_states, pivots, G, self.pooling, self.kernel_size,
                                             round_dtype=self._round_dtype(query_states.dtype))
         K = min(self.base_compress_len, L)
-        idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
+        plan = self._layer_plan(layer_idx, key_states)
+        if plan is not None:
+            idx, _ = compress.select_kept(scores, plan["piv_caps"], max_cap=max(K, 1))
+        else:
+            idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
         if self.observer is not None:
             self.observer("pivot_sets", layer=layer_idx, pivots=pivots, scores=scores, idx=idx, K=K)
         # Sets are stored in relation order, one row per (leader, batch).
@@ -583,8 +814,11 @@ class HeteroCache(DynamicCache):
         else:
             src = [pivots.index(h) for h in leaders]
         # Score rows are (b, pivot position); reorder them to (leader, b).
-        order = ops.to_device([self._score_row(b, s, len(pivots)) for s in src for b in range(self.bsz)], idx.device,
-                              torch.long)
+        if plan is not None:
+            order = plan["piv_order"]
+        else:
+            order = ops.to_device([self._score_row(b, s, len(pivots)) for s in src for b in range(self.bsz)],
+                                  idx.device, torch.long)
         if self._ref_bits_all is None:
             self._init_drift_buffers(idx.device, L)
         lb, B = self._lead_base[layer_idx], self.bsz
@@ -643,11 +877,24 @@ class HeteroCache(DynamicCache):
         else:
             scores = compress.last_query_scores(query_states, key_states, range(n_c), G, self.pooling,
                                                 self.kernel_size, round_dtype=self._round_dtype(query_states.dtype))
-        idx, counts = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0)
+        plan = self._layer_plan(layer_idx, key_states, value_states)
+        if plan is not None and "compress" in plan:
+            idx, counts = compress.select_kept(scores, plan["caps"], window=W if W > 1 else 0,
+                                               max_cap=plan["max_cap"])
+            if idx.shape[1] != plan["idx_width"]:
+                raise RuntimeError("prefill plan: index width differs from the selection's")
+        else:
+            plan = None
+            idx, counts = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0)
         if self.observer is not None:
             self.observer("prefill_select", layer=layer_idx, rows=rows, scores=scores, idx=idx, counts=counts)
-        store.write_rows(key_states, value_states, [(b, h) for b in range(self.bsz) for h in range(n_c)], rows,
-                         caps_rows, idx=idx)
+        if plan is not None:
+            store.launch_rows(plan["compress"], key_states, value_states, idx=idx, set_len=False)
+            hrows, lens, drows, dlens = plan["compress_len"]
+            store.set_lengths_planned(hrows, lens, drows, dlens, plan["order"])
+        else:
+            store.write_rows(key_states, value_states, [(b, h) for b in range(self.bsz) for h in range(n_c)], rows,
+                             caps_rows, idx=idx)
 
     def decode_attention(self, query_states, layer_idx, out=None):
         """Decode attention of q [B, Hq, 1, 128] over the layer's rows, with the
@@ -831,17 +1078,27 @@ class HeteroCache(DynamicCache):
         dev = qa.device
         main = torch.cuda.current_stream(dev)
         host = self.tier_mode == "host"
-        side = self._side_stream(dev) if (host or self.overlap_check) else main
-        if side is not main:
-            side.wait_stream(main)
-            self._share_with_side(side, [qa, self._arena[0], self._arena[1], self._tile_table, self._trigger_all,
-                                         self._ref_bits_all]
+        gp = bm["group_plan"]
+        # The check runs on the main stream (on the side stream with
+        # overlap_drift_check); the retrieval gathers of a tier arena run on
+        # the side stream, one per layer, each layer's next attention waiting
+        # for its own rows only.
+        side = self._side_stream(dev) if self.overlap_check else main
+        gather_side = self._side_stream(dev) if (gp is not None and bm["retrieve"] and self._side_retrieval()) else side
+        if side is not main or gather_side is not main:
+            s2 = side if side is not main else gather_side
+            s2.wait_stream(main)
+        if (side is not main or gather_side is not main) and not bm.get("shared"):
+            # Once per check group: its buffers are the same at every check.
+            bm["shared"] = True
+            self._share_with_side(s2, [qa, self._arena[0], self._arena[1], self._tile_table, self._trigger_all,
+                                       self._ref_bits_all]
                                   + ([] if self._tier is None else list(self._tier))
                                   + ([] if self._step_stats is None else [self._step_stats])
                                   + [t for layer, _ in bm["plans"]
                                      for t in (self.key_cache_cpu[layer], self.value_cache_cpu[layer])]
                                   + [v for v in bm.values() if torch.is_tensor(v)]
-                                  + [v for v in (bm["group_plan"] or {}).values() if torch.is_tensor(v)])
+                                  + [v for v in (gp or {}).values() if torch.is_tensor(v)])
         # One pass over the pivot keys when every step of the cycle had its
         # softmax statistics reported by its decode launch; otherwise the
         # statistics pass with stored logits.
@@ -870,26 +1127,40 @@ class HeteroCache(DynamicCache):
                 self.observer("drift_check", row_ids=bm["row_ids"], scores=scores, overlap=bm["overlap"],
                               trigger=trig, trig_of=bm["trig_of"], ret_idx=bm.get("ret_idx"),
                               ret_counts=bm.get("ret_counts"))
-            gp = bm["group_plan"]
-            if bm["retrieve"] and gp is not None:
-                # Every layer of the group in one launch from the tier arena.
-                tk, tv = self._tier
-                ops.gather_store(tk, tv, gp["src_off"], self.head_dim, L, bm["ret_idx"], gp["idx_off"], gp["counts"],
-                                 gp["dst_row"], self._arena[0], self._arena[1], self._tile_table, gp["max_count"],
-                                 src_is_host=host, trigger=trig, trig_of=gp["trig_of"], stream=side,
-                                 max_workgroups=self.RETRIEVAL_WORKGROUPS if host else 0)
-            elif bm["retrieve"]:
+            if bm["retrieve"] and gp is None:
                 for layer, plan in bm["plans"]:
                     kc, vc = self.key_cache_cpu[layer], self.value_cache_cpu[layer]
                     self.stores[layer].launch_rows(plan, kc, vc, idx=bm["ret_idx"], src_is_host=host, stream=side,
                                                    trigger=trig, set_len=False)
-        if side is not main:
-            # The group's layers read the new sets and retrieved rows at their
-            # next attention; every other layer goes on meanwhile.
-            ev = torch.cuda.Event()
-            ev.record(side)
-            for layer in layers:
+        if bm["retrieve"] and gp is not None and gather_side is side:
+            # From the tier arena, every layer of the group in one launch on
+            # the check's stream.
+            tk, tv = self._tier
+            ops.gather_store(tk, tv, gp["src_off"], self.head_dim, L, bm["ret_idx"], gp["idx_off"], gp["counts"],
+                             gp["dst_row"], self._arena[0], self._arena[1], self._tile_table, gp["max_count"],
+                             src_is_host=host, trigger=trig, trig_of=gp["trig_of"], stream=side,
+                             max_workgroups=self.RETRIEVAL_WORKGROUPS if host else 0)
+        elif bm["retrieve"] and gp is not None:
+            # From the tier arena: one gather per layer on the side stream
+            # (after the selection), each recording its layer's event.
+            gather_side.wait_stream(side)
+            tk, tv = self._tier
+            ops.gather_store_groups(tk, tv, gp["src_off"], gp["group_stride"], L, bm["ret_idx"], gp["idx_off"],
+                                    gp["counts"], gp["dst_row"], self._arena[0], self._arena[1], self._tile_table,
+                                    gp["group_begin"], gp["group_max"], gp["events"], src_is_host=host,
+                                    trigger=trig, trig_of=gp["trig_of"], stream=gather_side,
+                                    max_workgroups=self.RETRIEVAL_WORKGROUPS)
+            for layer, ev in zip(gp["layers"], gp["events"]):
                 self._retrieval_done[layer] = ev
+        if side is not main:
+            # overlap_drift_check: the group's other layers wait for the whole
+            # check before their next attention (its buffers are reused by
+            # the next check of the main stream).
+            ev = torch.cuda.Event()
+            ev.record(gather_side if gather_side is not main else side)
+            for layer in layers:
+                if self._retrieval_done[layer] is None:
+                    self._retrieval_done[layer] = ev
 
     def _batched_metadata(self, layers):
         """Device metadata of _check_batched; rows j follow the
@@ -975,7 +1246,23 @@ class HeteroCache(DynamicCache):
                 dst.append(layer * B * Hkv + b * Hkv + mm)
                 trig_of.append(t)
             layers.append(layer)
-        return {"src_off": ops.to_device(np.asarray(src_off, dtype=np.int64), dev),
+        # One gather group per layer (jobs are in layer order), each with the
+        # event its layer's next attention waits for.
+        begin = [0]
+        gmax = []
+        for layer in layers:
+            n = len(jobs[layer])
+            gmax.append(max(c for *_, c in jobs[layer]))
+            begin.append(begin[-1] + n)
+        side = self._side_stream(dev)
+        events = []
+        for _ in layers:
+            ev = torch.cuda.Event()
+            ev.record(side)   # creates the event's handle
+            events.append(ev)
+        return {"group_begin": np.asarray(begin, dtype=np.int32), "group_max": np.asarray(gmax, dtype=np.int32),
+                "group_stride": np.full(len(layers), D, dtype=np.int64), "events": events,
+                "src_off": ops.to_device(np.asarray(src_off, dtype=np.int64), dev),
                 "idx_off": ops.to_device(np.asarray(idx_off, dtype=np.int64), dev),
                 "counts": ops.to_device(np.asarray(counts, dtype=np.int32), dev),
                 "dst_row": ops.to_device(np.asarray(dst, dtype=np.int32), dev),

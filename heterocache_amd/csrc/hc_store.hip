@@ -42,13 +42,30 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
   __shared__ T sk[HC_TILE][HC_HEAD_DIM + 8];
   __shared__ T sv[HC_TILE][HC_HEAD_DIM + 8];
   const int64_t items = (int64_t)njobs * tiles_per_job;
-  for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+  const int lane = threadIdx.x & 63;
+  // The workgroup's items are blockIdx.x + i * gridDim.x.  They are taken 64
+  // at a time: lane i reads item i's trigger flag and count, and a ballot
+  // keeps the live items, so gated-off and empty items cost one round trip
+  // per 64 instead of one each (a small host-sourced grid walks many items).
+  // Every wave computes the same mask, so all threads run the same items.
+  for (int64_t base = blockIdx.x; base < items; base += (int64_t)gridDim.x * 64) {
+  bool live = false;
+  {
+    const int64_t it = base + (int64_t)lane * gridDim.x;
+    if (it < items) {
+      const int jb = (int)(it / tiles_per_job);
+      live = (!trigger || trigger[trig_of ? trig_of[jb] : 0] != 0) &&
+             (int)(it % tiles_per_job) * HC_TILE < count[jb];
+    }
+  }
+  uint64_t live_mask = __ballot(live);
+  while (live_mask) {
+  const int64_t item = base + (int64_t)__builtin_ctzll(live_mask) * gridDim.x;
+  live_mask &= live_mask - 1;
   const int job = (int)(item / tiles_per_job);
   const int tile = (int)(item % tiles_per_job);
-  if (trigger && trigger[trig_of ? trig_of[job] : 0] == 0) continue;
   const int n = count[job];
   const int tok0 = tile * HC_TILE;
-  if (tok0 >= n) continue;
   const int valid = min(HC_TILE, n - tok0);
 
   const T* bk = src_k + src_off[job];
@@ -112,6 +129,7 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
     }
   }
   __syncthreads();  // the next item refills the LDS tiles
+  }
   }
 }
 
@@ -281,6 +299,91 @@ extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, 
     default:
       return set_error(HC_ERR_INVALID, "hc_gather_store: unknown dtype %d", dtype);
   }
+}
+
+extern "C" int hc_gather_store_groups(int dtype, const void* src_k, const void* src_v, int src_is_host,
+                                      const int64_t* src_off, const int64_t* group_tok_stride, int src_len,
+                                      const int32_t* idx, const int64_t* idx_off, const int32_t* count,
+                                      const int32_t* dst_row, void* kstore, void* vstore,
+                                      const int64_t* row_tile_off, int ngroups, const int32_t* group_begin,
+                                      const int32_t* group_max_count, const int32_t* trigger,
+                                      const int32_t* trig_of, int max_workgroups, void* const* events,
+                                      void* stream) {
+  clear_error();
+  if (ngroups < 0 || ngroups > 65535 || max_workgroups < 0)
+    return set_error(HC_ERR_INVALID, "hc_gather_store_groups: ngroups=%d", ngroups);
+  if (ngroups == 0) return HC_OK;
+  if (!group_begin || !group_max_count || !group_tok_stride)
+    return set_error(HC_ERR_INVALID, "hc_gather_store_groups: null group array");
+  for (int g = 0; g < ngroups; ++g) {
+    if (group_begin[g + 1] < group_begin[g] || group_begin[g] < 0 || group_max_count[g] < 0)
+      return set_error(HC_ERR_INVALID, "hc_gather_store_groups: group %d spans jobs [%d, %d), max count %d", g,
+                       group_begin[g], group_begin[g + 1], group_max_count[g]);
+  }
+  if (group_begin[ngroups] > 65535)
+    return set_error(HC_ERR_INVALID, "hc_gather_store_groups: %d jobs", group_begin[ngroups]);
+  // Every group is validated before anything is launched, so an invalid
+  // group leaves no earlier group half done.
+  for (int g = 0; g < ngroups; ++g) {
+    const int nj = group_begin[g + 1] - group_begin[g];
+    if (nj == 0 || group_max_count[g] == 0) continue;
+    if (src_len <= 0) return set_error(HC_ERR_INVALID, "hc_gather_store_groups: src_len=%d", src_len);
+    if (!idx && group_max_count[g] > src_len)
+      return set_error(HC_ERR_INVALID, "hc_gather_store_groups: identity copy of %d tokens from a %d-token source",
+                       group_max_count[g], src_len);
+    if (group_tok_stride[g] < HC_HEAD_DIM || (group_tok_stride[g] % 8) != 0)
+      return set_error(HC_ERR_INVALID, "hc_gather_store_groups: group %d token stride %lld", g,
+                       (long long)group_tok_stride[g]);
+  }
+  if (!src_k || !src_v || !src_off || !count || !dst_row || !kstore || !vstore || !row_tile_off ||
+      (idx && !idx_off))
+    return set_error(HC_ERR_INVALID, "hc_gather_store_groups: null pointer argument");
+  const void* sk = src_k;
+  const void* sv = src_v;
+  if (src_is_host) {
+    int rc = map_host_ptr(src_k, &sk);
+    if (rc) return rc;
+    rc = map_host_ptr(src_v, &sv);
+    if (rc) return rc;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  for (int g = 0; g < ngroups; ++g) {
+    const int b0 = group_begin[g], nj = group_begin[g + 1] - b0;
+    if (nj > 0 && group_max_count[g] > 0) {
+      const int64_t* so = src_off + b0;
+      const int64_t* io = idx ? idx_off + b0 : nullptr;
+      const int32_t* cn = count + b0;
+      const int32_t* dr = dst_row + b0;
+      const int32_t* to = trig_of ? trig_of + b0 : nullptr;
+      int rc;
+      switch (dtype) {
+        case HC_DTYPE_BF16:
+          rc = launch_gather_store<__bf16>(sk, sv, so, group_tok_stride[g], src_len, idx, io, cn, dr, kstore, vstore,
+                                           row_tile_off, nj, group_max_count[g], trigger, to, src_is_host != 0,
+                                           max_workgroups, s);
+          break;
+        case HC_DTYPE_F16:
+          rc = launch_gather_store<_Float16>(sk, sv, so, group_tok_stride[g], src_len, idx, io, cn, dr, kstore,
+                                             vstore, row_tile_off, nj, group_max_count[g], trigger, to,
+                                             src_is_host != 0, max_workgroups, s);
+          break;
+        case HC_DTYPE_F32:
+          rc = launch_gather_store<float>(sk, sv, so, group_tok_stride[g], src_len, idx, io, cn, dr, kstore, vstore,
+                                          row_tile_off, nj, group_max_count[g], trigger, to, src_is_host != 0,
+                                          max_workgroups, s);
+          break;
+        default:
+          return set_error(HC_ERR_INVALID, "hc_gather_store_groups: unknown dtype %d", dtype);
+      }
+      if (rc) return rc;
+    }
+    if (events && events[g]) {
+      const hipError_t e = hipEventRecord((hipEvent_t)events[g], s);
+      if (e != hipSuccess)
+        return set_error(HC_ERR_HIP, "hc_gather_store_groups: event of group %d: %s", g, hipGetErrorString(e));
+    }
+  }
+  return HC_OK;
 }
 
 extern "C" int hc_append(int dtype, const void* k_new, const void* v_new, int64_t src_row_stride, void* kstore,

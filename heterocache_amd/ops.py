@@ -237,6 +237,41 @@ def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, c
                                    _stream(stream, kstore)))
 
 
+def gather_store_groups(src_k, src_v, src_off, group_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
+                        vstore, row_tile_off, group_begin, group_max_count, events, src_is_host=False, trigger=None,
+                        trig_of=None, stream=None, max_workgroups=0):
+    """gather_store over consecutive job groups, one launch per group, each
+    followed by a record of that group's event (hc_gather_store_groups).
+
+    group_begin (int32, ngroups + 1), group_max_count (int32, ngroups) and
+    group_tok_stride (int64, ngroups): host numpy arrays.  events: one
+    torch.cuda.Event (or None) per group; each is recorded on `stream` once
+    its group's rows are written."""
+    lib = _lib.load()
+    _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger, trig_of)
+    if src_is_host:
+        if src_k.is_cuda or not src_k.is_pinned() or not src_v.is_pinned():
+            raise ValueError("host sources must be pinned CPU tensors")
+    else:
+        _require_cuda(src_k, src_v)
+    if src_k.dtype != kstore.dtype or src_v.dtype != vstore.dtype:
+        raise TypeError("source and store dtypes differ")
+    gb = np.ascontiguousarray(group_begin, dtype=np.int32)
+    gm = np.ascontiguousarray(group_max_count, dtype=np.int32)
+    gs = np.ascontiguousarray(group_tok_stride, dtype=np.int64)
+    ng = len(gm)
+    if len(gb) != ng + 1 or len(gs) != ng or len(events) != ng:
+        raise ValueError("group arrays and events must describe the same groups")
+    if gb[-1] != count.numel():
+        raise ValueError(f"groups cover {gb[-1]} jobs, count holds {count.numel()}")
+    handles = (ctypes.c_void_p * max(ng, 1))(*[(e.cuda_event if e is not None else 0) for e in events])
+    _lib.check(lib.hc_gather_store_groups(dtype_code(kstore.dtype), _ptr(src_k), _ptr(src_v), int(bool(src_is_host)),
+                                          _ptr(src_off), gs.ctypes.data, int(src_len), _ptr(idx), _ptr(idx_off),
+                                          _ptr(count), _ptr(dst_row), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
+                                          ng, gb.ctypes.data, gm.ctypes.data, _ptr(trigger), _ptr(trig_of),
+                                          int(max_workgroups), handles, _stream(stream, kstore)))
+
+
 def copy_rows(src_k, src_v, src_bh, dst_k, dst_v, dst_bh, counts, dst_is_host=False, max_workgroups=32,
               stream=None):
     """dst[b', h', t] = src[b, h, t] for t < counts[j], (b, h) = src_bh[j], (b', h') = dst_bh[j].
@@ -273,18 +308,29 @@ def copy_rows(src_k, src_v, src_bh, dst_k, dst_v, dst_bh, counts, dst_is_host=Fa
     if (counts < 0).any() or (counts > src_k.shape[2]).any() or (counts > dst_k.shape[2]).any():
         raise ValueError("count exceeds a source or destination length")
     dev = src_k.device
-    src_off = torch.as_tensor(src_bh[:, 0] * src_k.stride(0) + src_bh[:, 1] * src_k.stride(1)).to(dev)
-    dst_off = torch.as_tensor(dst_bh[:, 0] * dst_k.stride(0) + dst_bh[:, 1] * dst_k.stride(1)).to(dev)
-    cnt = torch.as_tensor(counts.astype(np.int32)).to(dev)
+    plan = {"src_off": to_device(src_bh[:, 0] * src_k.stride(0) + src_bh[:, 1] * src_k.stride(1), dev, torch.int64),
+            "dst_off": to_device(dst_bh[:, 0] * dst_k.stride(0) + dst_bh[:, 1] * dst_k.stride(1), dev, torch.int64),
+            "counts": to_device(counts, dev, torch.int32), "max_count": int(counts.max())}
+    copy_rows_planned(src_k, src_v, plan, dst_k, dst_v, dst_is_host, max_workgroups, stream)
+
+
+def copy_rows_planned(src_k, src_v, plan, dst_k, dst_v, dst_is_host=False, max_workgroups=32, stream=None):
+    """copy_rows with its device metadata already built: plan holds int64
+    device tensors src_off / dst_off (element offsets of each job's head),
+    int32 counts and the host max_count (the caller validated them against
+    these tensors' shapes).  With `stream`, that stream first waits for the
+    current one."""
+    lib = _lib.load()
     if stream is not None:
-        # The launch stream waits for the offsets (and whatever produced the
+        # The launch stream waits for the metadata (and whatever produced the
         # sources) on the current stream.
-        stream.wait_stream(torch.cuda.current_stream(dev))
-        for t in (src_off, dst_off, cnt):
+        stream.wait_stream(torch.cuda.current_stream(src_k.device))
+        for t in (plan["src_off"], plan["dst_off"], plan["counts"]):
             t.record_stream(stream)
-    _lib.check(lib.hc_copy_rows(dtype_code(src_k.dtype), _ptr(src_k), _ptr(src_v), _ptr(src_off), src_k.stride(2),
-                                _ptr(dst_k), _ptr(dst_v), int(bool(dst_is_host)), _ptr(dst_off), dst_k.stride(2),
-                                _ptr(cnt), len(counts), int(counts.max()), int(max_workgroups),
+    _lib.check(lib.hc_copy_rows(dtype_code(src_k.dtype), _ptr(src_k), _ptr(src_v), _ptr(plan["src_off"]),
+                                src_k.stride(2), _ptr(dst_k), _ptr(dst_v), int(bool(dst_is_host)),
+                                _ptr(plan["dst_off"]), dst_k.stride(2), _ptr(plan["counts"]),
+                                plan["counts"].numel(), int(plan["max_count"]), int(max_workgroups),
                                 _stream(stream, src_k)))
 
 

@@ -31,7 +31,7 @@ class KVStore:
     rows of several stores through the shared base pointers.
     """
 
-    def __init__(self, row_caps, dtype, device, arena=None, layer_idx=None):
+    def __init__(self, row_caps, dtype, device, arena=None, layer_idx=None, meta=None):
         caps = np.asarray(row_caps, dtype=np.int64)
         if (caps < 0).any():
             raise ValueError("negative row capacity")
@@ -62,13 +62,32 @@ class KVStore:
             self.tile_base = int(tile_base)
             off = off + self.tile_base
         self.host_tile_off = off
+        self.host_len = np.zeros(self.rows, dtype=np.int32)
+        self._headroom = int(self.host_cap.min()) if self.rows else 0  # min over rows of cap - len
+        if meta is not None:
+            # Device metadata prepared by the owner of the arena (one transfer
+            # for every store): views holding these rows' tile offsets
+            # (int64), capacities (int32), zero lengths, the identity row
+            # order and a zero status word.
+            self.row_tile_off, self.row_cap = meta["row_tile_off"], meta["row_cap"]
+            self.row_len, self.row_order, self.status = meta["row_len"], meta["row_order"], meta["status"]
+            return
         self.row_tile_off = torch.as_tensor(off, dtype=torch.int64).to(self.device)
         self.row_cap = torch.as_tensor(self.host_cap, dtype=torch.int32).to(self.device)
         self.row_len = torch.zeros(self.rows, dtype=torch.int32, device=self.device)
-        self.host_len = np.zeros(self.rows, dtype=np.int32)
-        self._headroom = int(self.host_cap.min()) if self.rows else 0  # min over rows of cap - len
         self.status = torch.zeros(1, dtype=torch.int32, device=self.device)
         self.row_order = torch.arange(self.rows, dtype=torch.int32, device=self.device)
+
+    @staticmethod
+    def host_metadata(row_caps, tile_base=0):
+        """(tile offsets int64, capacities int32) of a store with these row
+        capacities whose rows start at arena tile tile_base."""
+        caps = np.asarray(row_caps, dtype=np.int64)
+        tiles = (caps + TILE - 1) // TILE
+        off = np.zeros(len(caps), dtype=np.int64)
+        if len(caps) > 1:
+            off[1:] = np.cumsum(tiles)[:-1]
+        return off + int(tile_base), (tiles * TILE).astype(np.int32)
 
     @staticmethod
     def tiles_for(row_caps):
@@ -96,6 +115,23 @@ class KVStore:
         order = np.argsort(-self.host_len.astype(np.int64), kind="stable").astype(np.int32)
         self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
         self.row_order = ops.to_device(order, self.device)
+
+    def set_lengths_planned(self, rows, lens, dev_rows, dev_lens, dev_order=None):
+        """set_lengths with the device copies already made: rows / lens on
+        the host (numpy), dev_rows (int64) / dev_lens (int32) the same
+        values on the device, dev_order (int32, optional) a row order to
+        schedule by (any permutation of the rows is correct; longest first
+        is the fast one).  Launches one index copy, and one copy for the
+        order, and no host-to-device transfer."""
+        rows = np.asarray(rows, dtype=np.int64)
+        lens = np.asarray(lens, dtype=np.int64)
+        if (lens > self.host_cap[rows]).any() or (lens < 0).any():
+            raise RuntimeError("row length outside its capacity")
+        self.host_len[rows] = lens
+        self.row_len.index_copy_(0, dev_rows, dev_lens)
+        if dev_order is not None:
+            self.row_order.copy_(dev_order)
+        self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
 
     def sync_host_lengths(self, lens):
         """Set the host mirror to lengths the device already holds (after HIP
@@ -168,7 +204,7 @@ class KVStore:
         if tuple(src_k.shape) != plan["shape"] or tuple(src_k.stride()) != plan["stride"] or \
                 src_v.shape != src_k.shape or src_v.stride() != src_k.stride():
             raise ValueError("sources do not match the plan")
-        if src_v.data_ptr() % 16:
+        if src_k.data_ptr() % 16 or src_v.data_ptr() % 16:
             raise ValueError("sources must be 16-byte aligned per token")
         if (idx is None) != (plan["idx_off"] is None):
             raise ValueError("index tensor does not match the plan")

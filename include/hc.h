@@ -165,6 +165,28 @@ int hc_gather_store(int dtype, const void* src_k, const void* src_v, int src_is_
                     int max_count, const int32_t* trigger, const int32_t* trig_of, int max_workgroups, void* stream);
 
 /*
+ * hc_gather_store over jobs split into ngroups consecutive groups (host
+ * arrays: group_begin[ngroups + 1] job boundaries, group_max_count[ngroups],
+ * group_tok_stride[ngroups] source token stride of each group): one gather
+ * launch per group on `stream`, each followed by hipEventRecord(events[g])
+ * when events (host array of hipEvent_t, entries may be NULL) is given --
+ * also for an empty group -- so a consumer of group g's rows waits for that
+ * group alone.  Device arrays are indexed by global job as in
+ * hc_gather_store; trig_of keeps global trigger indices.  All groups are
+ * validated before the first launch.  Serves the retrieval of one drift
+ * check, one group per layer: the reference copies each satellite's rows
+ * with its own H2D copy_ on the default stream before the next step
+ * (heterocache/cache_utils.py:1097-1123); here each layer's next attention
+ * waits only for its own satellites' rows.
+ */
+int hc_gather_store_groups(int dtype, const void* src_k, const void* src_v, int src_is_host, const int64_t* src_off,
+                           const int64_t* group_tok_stride, int src_len, const int32_t* idx, const int64_t* idx_off,
+                           const int32_t* count, const int32_t* dst_row, void* kstore, void* vstore,
+                           const int64_t* row_tile_off, int ngroups, const int32_t* group_begin,
+                           const int32_t* group_max_count, const int32_t* trigger, const int32_t* trig_of,
+                           int max_workgroups, void* const* events, void* stream);
+
+/*
  * Append one token per row at slot row_len[r], then row_len[r] += 1.
  * k_new/v_new row r starts at r * src_row_stride elements.  A full row is left
  * unchanged and sets bit 0 of *status (device, optional).

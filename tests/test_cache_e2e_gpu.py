@@ -57,7 +57,8 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
                             max_gen_len=steps + 4, decode_step=5, pooling="avgpool", kernel_size=5,
                             num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=topk,
                             reference_quirks=quirks, batched_drift_check=batched, drift_check_groups=groups,
-                            tier_placement="host" if tier == "prefill" else tier, overlap_drift_check=overlap)
+                            tier_placement="host" if tier == "prefill" else tier, overlap_drift_check=overlap,
+                            round_scores=False)
     cache = HeteroCache(cfg)
     if chunks is not None:
         cache.begin_prefill(L)
@@ -207,7 +208,8 @@ def test_chunked_prefill_with_observation_window_equals_single_shot(dev):
     def make():
         cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
                                 max_gen_len=4, decode_step=5, pooling="maxpool", kernel_size=7,
-                                num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, window_size=8)
+                                num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, window_size=8,
+                                round_scores=False)
         return HeteroCache(cfg)
 
     g = torch.Generator().manual_seed(9)
@@ -323,7 +325,7 @@ def test_observation_window_from_attention_statistics(dev, dtype):
         cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
                                 max_gen_len=4, decode_step=5, pooling="maxpool", kernel_size=7,
                                 num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, window_size=W,
-                                attention_stats_scoring=tag == "stats")
+                                attention_stats_scoring=tag == "stats", round_scores=False)
         cache = HeteroCache(cfg)
         cache.observer = lambda event, **kw: seen.setdefault((tag, event, kw.get("layer")), kw.get("scores"))
         return cache

@@ -141,7 +141,7 @@ def test_config2_needles_128k_llama_json(dev):
     cfg = HeteroCacheConfig(data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
                             max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
                             num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
-                            tier_placement="host")
+                            tier_placement="host", round_scores=False)
     cache = HeteroCache(cfg)
     cache.observer = rec
     wl = workloads.NeedleWorkload(L, kv_heads=Hkv, group=G, steps=steps, decode_step=S, seed=1002, device=dev)
@@ -206,6 +206,109 @@ def test_config2_needles_128k_llama_json(dev):
                     assert (rows_k == tier_k[m, p]).all(axis=1).any(), (layer, m, p)
 
 
+def f16_steps(got, ref):
+    """|got - ref| in units of the float16 spacing at ref (2^-24 below the
+    normal range, where the cast chain's small probabilities live)."""
+    got, ref = np.asarray(got, dtype=np.float64), np.asarray(ref, dtype=np.float64)
+    sp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    return np.abs(got - ref) / sp
+
+
+class CastChainScores(DeviceScores):
+    """DeviceScores for the reference's float16 cast chain: also records,
+    per scored head, how far the device scores sit from the oracle's cast
+    chain in float16 steps."""
+
+    def __init__(self, rec, threshold):
+        super().__init__(rec, threshold)
+        self.steps = []        # (kind, layer, head, max steps, positions off by more than one step, positions)
+
+    def __call__(self, kind, layer, head, s):
+        dev = super().__call__(kind, layer, head, s)
+        st = f16_steps(dev, s)
+        self.steps.append((kind, layer, head, float(st.max()), int((st > 1.0).sum()), int(st.size)))
+        return dev
+
+
+def test_config2_reference_cast_chain_fp16_128k(dev):
+    """Config 2 in the reference's own arithmetic: a float16 model (the
+    reference's load dtype) with round_scores=True, i.e. logits rounded to
+    float16, scaled and rounded again, float32 softmax rounded to float16,
+    pooled and rounded (heterocache/cache_utils.py:814-819, 1037-1043,
+    1167-1175).  131072 tokens, all 32 layers with the reference's head
+    JSON, needle queries, drift check every 5 steps at threshold 0.5,
+    top-1024 retrieval, 20 steps (4 checks: every leader triggers at checks
+    2 and 4).  Layers 0 and 23 are checked stage by stage:
+
+    * every score the device ranks (prefill selection, pivot sets, drift
+      steps) equals the oracle's float16 cast chain to within one float16
+      step at the score's magnitude (subnormal spacing below 2^-14);
+    * the oracle's integer flow on the device scores -- where the cast
+      chain ties massively, the lowest position first -- reproduces the
+      triggers, reference sets and stores bit for bit;
+    * attention is within 2e-2 of the float64 closed form."""
+    L, Hkv, G, D, NL, S, steps = 131072, 8, 4, 128, 32, 5, 20
+    checked = [0, 23]
+    data = llama_json()
+    rec = Recorder(checked)
+    cfg = HeteroCacheConfig(data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
+                            max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
+                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
+                            round_scores=True)
+    cache = HeteroCache(cfg)
+    cache.observer = rec
+    wl = workloads.NeedleWorkload(L, kv_heads=Hkv, group=G, steps=steps, decode_step=S, seed=1002, device=dev,
+                                  dtype=torch.float16)
+    hook = CastChainScores(rec, 0.5)
+    orc = O.CacheOracle(data, 1, Hkv * G, Hkv, NL, 0.5, 0.5, S, "avgpool", 5, retrieval_topk=1024,
+                        max_gen=steps + 4, score_hook=hook, io_dtype="float16")
+    hook.orc = orc
+    step_inputs = {}
+    for layer in range(NL):
+        x = wl.layer(layer)
+        k, v = cache.update(x["k"], x["v"], layer)
+        cache.init_coefficient(x["q_last"], k, layer)
+        cache.prefill_select(x["q_last"], k, v, layer)
+        if layer in checked:
+            orc.prefill(layer, as_np(x["q_last"]), as_np(x["k"]), as_np(x["v"]))
+        step_inputs[layer] = (x["q_steps"], x["k_new"], x["v_new"])
+        del x, k, v
+    assert orc.base == cache.base_compress_len == 49629
+    assert cache.one_pass_checks == 0
+    for t in range(steps):
+        outs = {}
+        for layer in range(NL):
+            q, kn, vn = (a[t] for a in step_inputs[layer])
+            cache.update(kn, vn, layer)
+            o = cache.decode_attention(q, layer)
+            cache.decode_select(q, layer)
+            if layer in checked:
+                outs[layer] = o
+        for layer in checked:
+            q, kn, vn = (as_np(a[t]) for a in step_inputs[layer])
+            ref = orc.decode(layer, q, kn, vn)
+            err = np.abs(as_np(outs[layer]).reshape(1, Hkv * G, D) - ref).max()
+            assert err <= ATTN_TOL, f"step {t} layer {layer}: max-abs {err}"
+    torch.cuda.synchronize()
+    assert len(rec.checks) == steps // S
+    for c, flags in enumerate(rec.checks):
+        assert len(flags) == 33
+        assert all(f == (c % 2 == 1) for f in flags.values()), (c, flags)
+    dev_trig = [(l, h, rec.checks[c][(l, h)]) for c in range(len(rec.checks)) for l in checked
+                for h in cache._drift[l].leaders]
+    assert sorted(dev_trig) == sorted(orc.triggers)
+    kinds = sorted({k for k, *_ in hook.steps})
+    assert kinds == ["drift", "pivot", "prefill"], kinds
+    worst = max(hook.steps, key=lambda x: x[3])
+    off = sum(x[4] for x in hook.steps)
+    total = sum(x[5] for x in hook.steps)
+    print(f"cast chain: {len(hook.steps)} score rows, {total} scores, worst {worst[3]:.2f} float16 steps "
+          f"({worst[:3]}), {off} beyond one step")
+    assert worst[3] <= 1.0, worst
+    check_stores(cache, orc, checked, 1, Hkv)
+    check_ref_sets(cache, orc, checked, L)
+
+
 def test_config4_chunked_224k_then_drift_block(dev):
     """Config 4: Llama-3-8B shape at 229376 tokens, all 32 layers with the
     reference's head JSON.  An 8K-chunked prefill (chunks fed layer by
@@ -226,7 +329,7 @@ def test_config4_chunked_224k_then_drift_block(dev):
         cfg = HeteroCacheConfig(data, compression_ratio=0.5, stable_threshold=0.5, real_offload=host_tier,
                                 max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
                                 num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
-                                tier_placement="host")
+                                tier_placement="host", round_scores=False)
         return HeteroCache(cfg)
 
     whole, chunked = make(False), make(True)
@@ -255,10 +358,14 @@ def test_config4_chunked_224k_then_drift_block(dev):
             assert chunked.prefill_pending(layer) == (e < L)
     torch.cuda.synchronize()
     assert whole.base_compress_len == chunked.base_compress_len == 86851
-    assert torch.equal(whole._arena[0], chunked._arena[0]) and torch.equal(whole._arena[1], chunked._arena[1])
     assert torch.equal(whole._ref_bits_all, chunked._ref_bits_all)
     for a, b in zip(whole.stores, chunked.stores):
         assert a.host_len.tolist() == b.host_len.tolist() and torch.equal(a.row_len, b.row_len)
+        for r in range(a.rows):  # written slots only (the arenas are not cleared)
+            n = int(a.host_len[r])
+            ka, va = a.read_rows([r], n)
+            kb, vb = b.read_rows([r], n)
+            assert torch.equal(ka, kb) and torch.equal(va, vb), (a.layer_idx, r)
     del whole
     hook = DeviceScores(rec, 0.5)
     orc = O.CacheOracle(data, 1, Hkv * G, Hkv, NL, 0.5, 0.5, S, "avgpool", 5, retrieval_topk=1024,
@@ -317,7 +424,8 @@ def test_config3_qwen_sequence_full_context(dev, ctx):
     rec = Recorder(checked)
     cfg = HeteroCacheConfig(data, compression_ratio=0.25, stable_threshold=0.5, real_offload=True,
                             max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
-                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=512)
+                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=512,
+                            round_scores=False)
     cache = HeteroCache(cfg)
     cache.observer = rec
     wl = workloads.NeedleWorkload(ctx, kv_heads=Hkv, group=G, steps=steps, decode_step=S, seed=1003 + ctx, device=dev)

@@ -159,3 +159,72 @@ def test_copy_rows_strided_source_small_grid(dev, to_host):
     ek = torch.zeros(shape, dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError, match="count exceeds"):
         ops.copy_rows(k, v, [(0, 0)], ek, ek.clone(), [(0, 0)], [L + 1])
+
+
+@pytest.mark.parametrize("host", [False, True])
+def test_gather_groups_match_one_gather_and_record_each_event(dev, host):
+    """hc_gather_store_groups: jobs in four groups (one of them empty, one
+    whose leader did not trigger, one with a 2x token stride over an
+    interleaved source) give the same store, bit for bit, as one
+    hc_gather_store per group, and every group's event is recorded on the
+    gather stream -- also the empty group's."""
+    from heterocache_amd import ops
+    L, D = 700, 128
+    dt = torch.bfloat16
+    base_k = rand((2 * L * D * 4,), dt, dev, 11)
+    base_v = rand((2 * L * D * 4,), dt, dev, 12)
+    if host:
+        src_k = torch.empty(base_k.shape, dtype=dt, pin_memory=True)
+        src_v = torch.empty(base_v.shape, dtype=dt, pin_memory=True)
+        src_k.copy_(base_k.cpu())
+        src_v.copy_(base_v.cpu())
+    else:
+        src_k, src_v = base_k, base_v
+    rng = np.random.default_rng(5)
+    # Groups: [0, 3) stride 128, [3, 3) empty, [3, 5) stride 256 (interleaved), [5, 7) gated off.
+    begin = np.array([0, 3, 3, 5, 7], dtype=np.int32)
+    strides = np.array([D, D, 2 * D, D], dtype=np.int64)
+    counts = np.array([300, 1, 33, 64, 200, 90, 17], dtype=np.int32)
+    src_off = np.array([0, L * D, 2 * L * D, 3 * L * D, 3 * L * D + D, 5 * L * D, 6 * L * D], dtype=np.int64)
+    trig_of = np.array([0, 0, 0, 1, 1, 2, 2], dtype=np.int32)
+    trigger = torch.tensor([1, 1, 0], dtype=torch.int32, device=dev)
+    M = int(counts.max())
+    idx = np.zeros((len(counts), M), dtype=np.int32)
+    for j, n in enumerate(counts):
+        idx[j, :n] = np.sort(rng.choice(L, n, replace=False))
+    idx_d = torch.as_tensor(idx).to(dev)
+    idx_off = torch.as_tensor(np.arange(len(counts)) * M, dtype=torch.int64).to(dev)
+    a = KVStore([512] * len(counts), dt, dev)
+    b = KVStore([512] * len(counts), dt, dev)
+    dst = torch.arange(len(counts), dtype=torch.int32, device=dev)
+    cnt = torch.as_tensor(counts).to(dev)
+    so = torch.as_tensor(src_off).to(dev)
+    to = torch.as_tensor(trig_of).to(dev)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    events = [torch.cuda.Event() for _ in range(4)]
+    for ev in events:
+        ev.record(side)
+    gmax = [int(counts[begin[g]:begin[g + 1]].max()) if begin[g + 1] > begin[g] else 0 for g in range(4)]
+    ops.gather_store_groups(src_k, src_v, so, strides, L, idx_d, idx_off, cnt, dst, a.k, a.v, a.row_tile_off,
+                            begin, gmax, events, src_is_host=host, trigger=trigger, trig_of=to, stream=side)
+    for g in range(4):
+        b0, b1 = begin[g], begin[g + 1]
+        if b1 > b0:
+            ops.gather_store(src_k, src_v, so[b0:b1], int(strides[g]), L, idx_d, idx_off[b0:b1], cnt[b0:b1],
+                             dst[b0:b1], b.k, b.v, b.row_tile_off, gmax[g], src_is_host=host, trigger=trigger,
+                             trig_of=to[b0:b1])
+    torch.cuda.current_stream().wait_event(events[-1])
+    torch.cuda.synchronize()
+    assert all(ev.query() for ev in events)
+    for j, n in enumerate(counts):
+        ka, va = a.read_rows([j], int(n))
+        kb, vb = b.read_rows([j], int(n))
+        assert torch.equal(ka, kb) and torch.equal(va, vb), j
+        if trig_of[j] == 2:   # gated off: the store keeps its (zero) slots
+            assert not ka.any()
+        else:
+            g = int(np.searchsorted(begin, j, side="right") - 1)
+            sel = torch.as_tensor(src_off[j] + idx[j, :n].astype(np.int64) * strides[g], device=dev)
+            rows = sel[:, None] + torch.arange(D, device=dev)[None, :]
+            assert torch.equal(ka[0], base_k[rows]) and torch.equal(va[0], base_v[rows]), j
