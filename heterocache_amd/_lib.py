@@ -52,7 +52,8 @@ SIGNATURES = {
                                 c_void_p]),
     "hc_gather_store_groups": (c_int, [c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
-                                       c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+                                       c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+                                       c_void_p]),
     "hc_copy_rows": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_int, c_void_p,
                              c_int64, c_void_p, c_int, c_int, c_int, c_void_p]),
     "hc_prefill_attn": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -304,6 +304,9 @@ class HeteroCache(DynamicCache):
         # Every layer's prefill metadata on the device, built once per cache
         # for inputs of one shape and stride: (key, [per-layer dict or None]).
         self._pplans = None
+        # Per layer: (tensor key, scores, idx, counts) of init_coefficient's
+        # joint selection, taken by prefill_select on the same tensors.
+        self._joint_sel = [None] * self.num_layers
         self._qbuf_all = None        # [NL, B, Hq, S, 128] buffered decode queries
         # [NL, B*Hkv, G, S, 2] softmax statistics (max bound, sum) of every
         # buffered decode query over its row's prefill keys, reported by the
@@ -431,9 +434,9 @@ class HeteroCache(DynamicCache):
 
     def retrieval_stream(self, device):
         """The stream the batched checks' retrieval gathers from the tier
-        arena run on (with "side", each layer's next attention waits for its
-        own rows)."""
-        if self._tier is not None and self._side_retrieval():
+        run on (with "side", each layer's next attention waits for its own
+        rows)."""
+        if self.tier_mode is not None and self._side_retrieval():
             return self._side_stream(device)
         return self.drift_stream(device)
 
@@ -503,9 +506,13 @@ class HeteroCache(DynamicCache):
         self._init_tier(device, dtype)
 
     def _init_tier(self, device, dtype):
-        """Place the satellites' full-KV tier: one arena of [rows, L, 128] K
-        and V for every layer, rows (layer, b, satellite) in that order, in
-        HBM or in pinned host memory (see HeteroCacheConfig.tier_placement)."""
+        """Place the satellites' full-KV tier (see
+        HeteroCacheConfig.tier_placement).  In HBM ("device", and "prefill"
+        without real_offload) the tier is each layer's prefill K/V itself,
+        kept by reference as the reference's GPU mode keeps it: no copy and
+        no second allocation.  In host memory it is one pinned arena of
+        [rows, L, 128] K and V for every layer, rows (layer, b, satellite)
+        in that order."""
         if not self.config.real_offload:
             self.tier_mode = "prefill"
             return
@@ -516,28 +523,18 @@ class HeteroCache(DynamicCache):
             rows += self.bsz * n
         self._tier_base = base
         L = self.prefill_len
-        nbytes = 2 * rows * L * self.head_dim * torch.empty((), dtype=dtype).element_size()
+        esz = torch.empty((), dtype=dtype).element_size()
         mode = getattr(self.config, "tier_placement", "auto")
-        auto = mode == "auto"
-        if auto:
-            mode = "device" if nbytes <= self._tier_device_room(device) else "host"
+        if mode == "auto":
+            # In HBM the tier keeps every layer with satellites' prefill K and V.
+            kept = sum(1 for n in nsat if n) * 2 * self.bsz * self.num_kv_heads * L * self.head_dim * esz
+            mode = "device" if kept <= self._tier_device_room(device) else "host"
         self.tier_mode = mode
-        if rows == 0:
+        if rows == 0 or mode == "device":
             return
         shape = (rows, L, self.head_dim)
-        if mode == "device":
-            try:
-                self._tier = (torch.empty(shape, dtype=dtype, device=device),
-                              torch.empty(shape, dtype=dtype, device=device))
-            except torch.cuda.OutOfMemoryError:
-                if not auto:
-                    raise
-                self._tier = None
-                torch.cuda.empty_cache()
-                mode = self.tier_mode = "host"
-        if mode == "host":
-            self._tier = (torch.empty(shape, dtype=dtype, pin_memory=True),
-                          torch.empty(shape, dtype=dtype, pin_memory=True))
+        self._tier = (torch.empty(shape, dtype=dtype, pin_memory=True),
+                      torch.empty(shape, dtype=dtype, pin_memory=True))
 
     def _tier_device_room(self, device):
         """Bytes "auto" lets the full-KV tier take in HBM: tier_device_budget
@@ -573,6 +570,12 @@ class HeteroCache(DynamicCache):
             _DevicePack.resolve(p, dev)   # this layer's views, made at its first use
             p["resolved"] = True
         return p
+
+    @staticmethod
+    def _tensor_key(*ts):
+        """Identity of tensors' contents: storage, shape, strides and
+        in-place version counter."""
+        return tuple((t.data_ptr(), tuple(t.shape), tuple(t.stride()), t._version) for t in ts)
 
     def _build_prefill_plans(self, key_states):
         """Per layer (batch rows b, kv-heads h, row r = b * Hkv + h):
@@ -621,14 +624,32 @@ class HeteroCache(DynamicCache):
                          "counts": pack.add(np.full(B * n, L), np.int32), "max_count": L}
         pivots = list(data["need_to_select_counts"][layer])
         rel = data["leader_member_relations"][layer]
+        K = min(self.base_compress_len, L)
+        src = []
         if pivots:
-            K = min(self.base_compress_len, L)
             leaders = [int(h) for h in rel]
             src = ([min(i, len(pivots) - 1) for i in range(len(leaders))] if self.quirks
                    else [pivots.index(h) for h in leaders])
             p["piv_caps"] = pack.add(np.full(B * len(pivots), K), np.int32)
             p["piv_order"] = pack.add([self._score_row(b, si, len(pivots)) for si in src for b in range(B)], np.int64)
         n_c = data["need_to_compress_counts"][layer]
+        if n_c and pivots and self.window_size == 1:
+            # Joint scoring and selection of the compressed heads and the
+            # pivots (one scorer, one selection: init_coefficient runs it,
+            # prefill_select takes the compressed heads' part).  Rows
+            # (b, head) over heads [0, n_c) + pivots, batch-major.
+            J = n_c + len(pivots)
+            caps = _f32_caps(self.base_compress_len, data["allocation_matrix"][layer][:n_c], L)
+            jcaps = np.asarray([int(caps[h]) for h in range(n_c)] + [K] * len(pivots), dtype=np.int64)
+            jcaps = np.tile(jcaps, B)
+            jmax = int(jcaps.max())
+            if jmax > 0 and caps.max() > 0:
+                width = max(1, min(jmax, L))
+                p["joint"] = {"heads": list(range(n_c)) + pivots, "caps": pack.add(jcaps, np.int32),
+                              "max_cap": jmax, "width": width,
+                              "piv_order": pack.add([b * J + n_c + si for si in src for b in range(B)], np.int64),
+                              "idx_off": pack.add([(b * J + h) * width for b in range(B) for h in range(n_c)],
+                                                  np.int64)}
         if n_c:
             caps = _f32_caps(self.base_compress_len, data["allocation_matrix"][layer][:n_c], L)
             rows = np.asarray([b * Hkv + h for b in range(B) for h in range(n_c)], dtype=np.int64)
@@ -647,6 +668,8 @@ class HeteroCache(DynamicCache):
                                  "host_rows": rows, "max_count": int(caps_rows.max())}
                 p["idx_width"] = width
                 p["compress_len"] = (rows, caps_rows, pack.add(rows, np.int64), cdev)
+                if "joint" in p:
+                    p["compress_joint"] = dict(p["compress"], idx_off=p["joint"]["idx_off"])
                 host_len[rows] = caps_rows
         # Row order once the prefill has set every length (longest first).
         p["order"] = pack.add(np.argsort(-host_len, kind="stable"), np.int32)
@@ -699,8 +722,9 @@ class HeteroCache(DynamicCache):
         sats = list(self.data["need_to_update_counts"][layer_idx])
         if not sats:
             return
-        if self.tier_mode == "prefill":
-            # GPU direct mode keeps the prefill K/V itself, as the reference.
+        if self.tier_mode in ("prefill", "device"):
+            # The tier in HBM is the prefill K/V itself, kept by reference
+            # (the reference's GPU mode keeps them the same way).
             self.key_cache_cpu[layer_idx] = key_states.detach()
             self.value_cache_cpu[layer_idx] = value_states.detach()
             self._tier_heads[layer_idx] = {h: h for h in sats}
@@ -712,26 +736,20 @@ class HeteroCache(DynamicCache):
         src = [(b, h) for b in range(self.bsz) for h in sats]
         dst = [(0, r0 + b * n + i) for b in range(self.bsz) for i in range(n)]
         tp = plan.get("tier") if plan is not None else None
-        if self.tier_mode == "device":
-            if tp is not None:
-                ops.copy_rows_planned(key_states, value_states, tp, tk, tv, max_workgroups=1024)
-            else:
-                ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), max_workgroups=1024)
+        # The host-pinned arena: a few workgroups write the satellites' rows
+        # straight from the prefill tensors into it at link speed, on the
+        # side stream beside the compression kernels on the main stream.
+        dev = key_states.device
+        side = self._side_stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        if tp is not None:
+            ops.copy_rows_planned(key_states, value_states, tp, tk, tv, dst_is_host=True,
+                                  max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
         else:
-            dev = key_states.device
-            side = self._side_stream(dev)
-            side.wait_stream(torch.cuda.current_stream(dev))
-            # A few workgroups write the satellites' rows straight from the
-            # prefill tensors into the pinned tier at link speed, beside the
-            # compression kernels on the main stream.
-            if tp is not None:
-                ops.copy_rows_planned(key_states, value_states, tp, tk, tv, dst_is_host=True,
-                                      max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
-            else:
-                ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), dst_is_host=True,
-                              max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
-            key_states.record_stream(side)
-            value_states.record_stream(side)
+            ops.copy_rows(key_states, value_states, src, tk, tv, dst, [L] * len(src), dst_is_host=True,
+                          max_workgroups=self.TIER_COPY_WORKGROUPS, stream=side)
+        key_states.record_stream(side)
+        value_states.record_stream(side)
         # The layer's rows of the arena, in the reference's [B, heads, L, 128] shape.
         self.key_cache_cpu[layer_idx] = self._tier[0][r0:r0 + self.bsz * n].view(self.bsz, n, L, self.head_dim)
         self.value_cache_cpu[layer_idx] = self._tier[1][r0:r0 + self.bsz * n].view(self.bsz, n, L, self.head_dim)
@@ -746,7 +764,7 @@ class HeteroCache(DynamicCache):
     def _tier_source(self, layer, b, m):
         """(K, V, (b', h')) addressing satellite m of batch row b of a layer
         in the tier: a row of the arena, or the prefill K/V in GPU mode."""
-        if self.tier_mode == "prefill":
+        if self.tier_mode in ("prefill", "device"):
             return self.key_cache_cpu[layer], self.value_cache_cpu[layer], (b, m)
         tk, tv = self._tier_arena4()
         n = len(self._tier_heads[layer])
@@ -794,16 +812,35 @@ class HeteroCache(DynamicCache):
             return
         L = key_states.shape[-2]
         G = self.num_key_value_groups
-        scores = compress.last_query_scores(query_states, key_states, pivots, G, self.pooling, self.kernel_size,
-                                            round_dtype=self._round_dtype(query_states.dtype))
         K = min(self.base_compress_len, L)
         plan = self._layer_plan(layer_idx, key_states)
-        if plan is not None:
-            idx, _ = compress.select_kept(scores, plan["piv_caps"], max_cap=max(K, 1))
+        jp = plan.get("joint") if plan is not None else None
+        rd = self._round_dtype(query_states.dtype)
+        if jp is not None:
+            # The compressed heads are scored and selected in the same
+            # launches; prefill_select takes their part if it is called with
+            # these same query and key tensors.
+            n_c = self.data["need_to_compress_counts"][layer_idx]
+            J = len(jp["heads"])
+            sc_all = compress.last_query_scores(query_states, key_states, jp["heads"], G, self.pooling,
+                                                self.kernel_size, round_dtype=rd)
+            idx, counts = compress.select_kept(sc_all, jp["caps"], max_cap=jp["max_cap"])
+            if idx.shape[1] != jp["width"]:
+                raise RuntimeError("prefill plan: index width differs from the joint selection's")
+            self._joint_sel[layer_idx] = (self._tensor_key(query_states, key_states), sc_all, idx, counts)
+            scores = None
+            if self.observer is not None:
+                scores = sc_all.view(self.bsz, J, L)[:, n_c:].reshape(-1, L)
         else:
-            idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
+            scores = compress.last_query_scores(query_states, key_states, pivots, G, self.pooling, self.kernel_size,
+                                                round_dtype=rd)
+            if plan is not None:
+                idx, _ = compress.select_kept(scores, plan["piv_caps"], max_cap=max(K, 1))
+            else:
+                idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
         if self.observer is not None:
-            self.observer("pivot_sets", layer=layer_idx, pivots=pivots, scores=scores, idx=idx, K=K)
+            pidx = idx if jp is None else idx.view(self.bsz, J, -1)[:, n_c:].reshape(self.bsz * len(pivots), -1)
+            self.observer("pivot_sets", layer=layer_idx, pivots=pivots, scores=scores, idx=pidx, K=K)
         # Sets are stored in relation order, one row per (leader, batch).
         leaders = [int(h) for h, m in rel.items()]
         members = [list(m) for h, m in rel.items()]
@@ -814,7 +851,9 @@ class HeteroCache(DynamicCache):
         else:
             src = [pivots.index(h) for h in leaders]
         # Score rows are (b, pivot position); reorder them to (leader, b).
-        if plan is not None:
+        if jp is not None:
+            order = jp["piv_order"]
+        elif plan is not None:
             order = plan["piv_order"]
         else:
             order = ops.to_device([self._score_row(b, s, len(pivots)) for s in src for b in range(self.bsz)],
@@ -870,6 +909,23 @@ class HeteroCache(DynamicCache):
         W = self.window_size
         if stats is not None:
             self.attn_stats_layers += 1
+        joint = self._joint_sel[layer_idx]
+        self._joint_sel[layer_idx] = None
+        plan = self._layer_plan(layer_idx, key_states, value_states)
+        if (joint is not None and plan is not None and "compress_joint" in plan
+                and joint[0] == self._tensor_key(query_states, key_states)):
+            # Selected by init_coefficient's joint launches on these tensors.
+            _, sc_all, idx, counts = joint
+            if self.observer is not None:
+                J = len(plan["joint"]["heads"])
+                self.observer("prefill_select", layer=layer_idx, rows=rows,
+                              scores=sc_all.view(self.bsz, J, L)[:, :n_c].reshape(-1, L),
+                              idx=idx.view(self.bsz, J, -1)[:, :n_c].reshape(self.bsz * n_c, -1),
+                              counts=counts.view(self.bsz, J)[:, :n_c].reshape(-1))
+            store.launch_rows(plan["compress_joint"], key_states, value_states, idx=idx, set_len=False)
+            hrows, lens, drows, dlens = plan["compress_len"]
+            store.set_lengths_planned(hrows, lens, drows, dlens, plan["order"])
+            return
         if W > 1:
             scores = compress.window_scores(query_states, key_states, range(n_c), G, W, self.pooling,
                                             self.kernel_size, window_keep=True,
@@ -877,7 +933,6 @@ class HeteroCache(DynamicCache):
         else:
             scores = compress.last_query_scores(query_states, key_states, range(n_c), G, self.pooling,
                                                 self.kernel_size, round_dtype=self._round_dtype(query_states.dtype))
-        plan = self._layer_plan(layer_idx, key_states, value_states)
         if plan is not None and "compress" in plan:
             idx, counts = compress.select_kept(scores, plan["caps"], window=W if W > 1 else 0,
                                                max_cap=plan["max_cap"])
@@ -1098,7 +1153,10 @@ class HeteroCache(DynamicCache):
                                   + [t for layer, _ in bm["plans"]
                                      for t in (self.key_cache_cpu[layer], self.value_cache_cpu[layer])]
                                   + [v for v in bm.values() if torch.is_tensor(v)]
-                                  + [v for v in (gp or {}).values() if torch.is_tensor(v)])
+                                  + [v for v in (gp or {}).values() if torch.is_tensor(v)]
+                                  + [t for layer in (gp or {}).get("layers", [])
+                                     for t in (self.key_cache_cpu[layer], self.value_cache_cpu[layer])
+                                     if t is not None])
         # One pass over the pivot keys when every step of the cycle had its
         # softmax statistics reported by its decode launch; otherwise the
         # statistics pass with stored logits.
@@ -1132,26 +1190,31 @@ class HeteroCache(DynamicCache):
                     kc, vc = self.key_cache_cpu[layer], self.value_cache_cpu[layer]
                     self.stores[layer].launch_rows(plan, kc, vc, idx=bm["ret_idx"], src_is_host=host, stream=side,
                                                    trigger=trig, set_len=False)
-        if bm["retrieve"] and gp is not None and gather_side is side:
-            # From the tier arena, every layer of the group in one launch on
-            # the check's stream.
-            tk, tv = self._tier
-            ops.gather_store(tk, tv, gp["src_off"], self.head_dim, L, bm["ret_idx"], gp["idx_off"], gp["counts"],
-                             gp["dst_row"], self._arena[0], self._arena[1], self._tile_table, gp["max_count"],
-                             src_is_host=host, trigger=trig, trig_of=gp["trig_of"], stream=side,
-                             max_workgroups=self.RETRIEVAL_WORKGROUPS if host else 0)
-        elif bm["retrieve"] and gp is not None:
-            # From the tier arena: one gather per layer on the side stream
-            # (after the selection), each recording its layer's event.
-            gather_side.wait_stream(side)
-            tk, tv = self._tier
-            ops.gather_store_groups(tk, tv, gp["src_off"], gp["group_stride"], L, bm["ret_idx"], gp["idx_off"],
-                                    gp["counts"], gp["dst_row"], self._arena[0], self._arena[1], self._tile_table,
-                                    gp["group_begin"], gp["group_max"], gp["events"], src_is_host=host,
-                                    trigger=trig, trig_of=gp["trig_of"], stream=gather_side,
-                                    max_workgroups=self.RETRIEVAL_WORKGROUPS)
-            for layer, ev in zip(gp["layers"], gp["events"]):
-                self._retrieval_done[layer] = ev
+        if bm["retrieve"] and gp is not None:
+            # Sources: the pinned tier arena, or (in HBM) each layer's prefill
+            # K/V through the plan's per-job address tables.
+            tk, tv = self._tier if self._tier is not None else self._arena
+            if gather_side is side:
+                # Every layer of the group in one launch on the check's stream.
+                ops.gather_store_groups(tk, tv, gp["src_off"], gp["group_stride"][:1], L, bm["ret_idx"],
+                                        gp["idx_off"], gp["counts"], gp["dst_row"], self._arena[0], self._arena[1],
+                                        self._tile_table, np.asarray([0, gp["counts"].numel()], dtype=np.int32),
+                                        [gp["max_count"]], [None], src_is_host=host, trigger=trig,
+                                        trig_of=gp["trig_of"], stream=side,
+                                        max_workgroups=self.RETRIEVAL_WORKGROUPS if host else 0,
+                                        src_k_addr=gp["k_addr"], src_v_addr=gp["v_addr"])
+            else:
+                # One gather per layer on the side stream (after the
+                # selection), each recording its layer's event.
+                gather_side.wait_stream(side)
+                ops.gather_store_groups(tk, tv, gp["src_off"], gp["group_stride"], L, bm["ret_idx"], gp["idx_off"],
+                                        gp["counts"], gp["dst_row"], self._arena[0], self._arena[1],
+                                        self._tile_table, gp["group_begin"], gp["group_max"], gp["events"],
+                                        src_is_host=host, trigger=trig, trig_of=gp["trig_of"], stream=gather_side,
+                                        max_workgroups=self.RETRIEVAL_WORKGROUPS, src_k_addr=gp["k_addr"],
+                                        src_v_addr=gp["v_addr"])
+                for layer, ev in zip(gp["layers"], gp["events"]):
+                    self._retrieval_done[layer] = ev
         if side is not main:
             # overlap_drift_check: the group's other layers wait for the whole
             # check before their next attention (its buffers are reused by
@@ -1209,9 +1272,8 @@ class HeteroCache(DynamicCache):
             m["ret_caps"] = torch.as_tensor(np.asarray(ret_caps, dtype=np.int32)).to(dev)
             m["ret_idx"] = torch.empty((J, max(mk, 1)), dtype=torch.int32, device=dev)
             m["ret_counts"] = torch.empty(J, dtype=torch.int32, device=dev)
-            if self.tier_mode in ("host", "device"):
-                m["group_plan"] = self._group_retrieval_plan(jobs, m["ret_idx"])
-            else:
+            m["group_plan"] = self._group_retrieval_plan(jobs, m["ret_idx"])
+            if m["group_plan"] is None:
                 for layer in layers:
                     lj = jobs.get(layer)
                     if not lj:
@@ -1234,18 +1296,32 @@ class HeteroCache(DynamicCache):
         B, Hkv, L, D = self.bsz, self.num_kv_heads, self.prefill_len, self.head_dim
         dev = ret_idx.device
         src_off, idx_off, counts, dst, trig_of, layers = [], [], [], [], [], []
+        in_hbm = self._tier is None   # each layer's prefill K/V, kept by reference
+        k_addr, v_addr, tok_stride = [], [], set()
         for layer, lj in sorted(jobs.items()):
             n_sat = len(self._tier_heads[layer])
             caps = self.stores[layer].host_cap
+            if in_hbm:
+                kc, vc = self.key_cache_cpu[layer], self.value_cache_cpu[layer]
+                if kc.stride() != vc.stride():
+                    return None
+                tok_stride.add(kc.stride(2))
             for jj, t, b, mm, n in lj:
                 if n > caps[b * Hkv + mm]:
                     raise RuntimeError(f"Layer {layer} OOM.")
-                src_off.append((self._tier_base[layer] + b * n_sat + self._tier_heads[layer][mm]) * L * D)
+                if in_hbm:
+                    src_off.append(b * kc.stride(0) + mm * kc.stride(1))
+                    k_addr.append(kc.data_ptr())
+                    v_addr.append(vc.data_ptr())
+                else:
+                    src_off.append((self._tier_base[layer] + b * n_sat + self._tier_heads[layer][mm]) * L * D)
                 idx_off.append(jj * ret_idx.stride(0))
                 counts.append(n)
                 dst.append(layer * B * Hkv + b * Hkv + mm)
                 trig_of.append(t)
             layers.append(layer)
+        if len(tok_stride) > 1:
+            return None   # layers of different token strides: gathered layer by layer
         # One gather group per layer (jobs are in layer order), each with the
         # event its layer's next attention waits for.
         begin = [0]
@@ -1260,8 +1336,11 @@ class HeteroCache(DynamicCache):
             ev = torch.cuda.Event()
             ev.record(side)   # creates the event's handle
             events.append(ev)
+        stride = tok_stride.pop() if in_hbm else D
         return {"group_begin": np.asarray(begin, dtype=np.int32), "group_max": np.asarray(gmax, dtype=np.int32),
-                "group_stride": np.full(len(layers), D, dtype=np.int64), "events": events,
+                "group_stride": np.full(len(layers), stride, dtype=np.int64), "events": events,
+                "k_addr": ops.to_device(np.asarray(k_addr, dtype=np.int64), dev) if in_hbm else None,
+                "v_addr": ops.to_device(np.asarray(v_addr, dtype=np.int64), dev) if in_hbm else None,
                 "src_off": ops.to_device(np.asarray(src_off, dtype=np.int64), dev),
                 "idx_off": ops.to_device(np.asarray(idx_off, dtype=np.int64), dev),
                 "counts": ops.to_device(np.asarray(counts, dtype=np.int32), dev),

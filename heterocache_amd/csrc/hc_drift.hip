@@ -34,22 +34,40 @@ __global__ __launch_bounds__(1024) void set_bits_kernel(const int32_t* __restric
   uint32_t* b = bits + (int64_t)j * words;
   const int n = counts ? counts[j] : fixed_count;
   const int32_t* ix = idx + (int64_t)j * idx_stride;
-  if (words <= kBitsLds) {
+  const bool lds = words <= kBitsLds;
+  if (lds) {
     for (int w = threadIdx.x; w < words; w += blockDim.x) s_bits[w] = 0u;
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      const int t = ix[i];
-      if (t >= 0 && t < nbits) atomicOr(&s_bits[t >> 5], 1u << (t & 31));
-    }
-    __syncthreads();
-    for (int w = threadIdx.x; w < words; w += blockDim.x) b[w] = s_bits[w];
   } else {
     for (int64_t w = threadIdx.x; w < words; w += blockDim.x) b[w] = 0u;
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-      const int t = ix[i];
-      if (t >= 0 && t < nbits) atomicOr(&b[t >> 5], 1u << (t & 31));
+  }
+  __syncthreads();
+  // Lists are ascending (selections), so neighbouring lanes mostly set bits
+  // of one word: a segmented OR over lanes with equal words (adjacent in an
+  // ascending list) leaves one atomic per word and wave instead of one per
+  // position, which serialised on that word.  Any order stays correct:
+  // words that are not adjacent simply take their own atomics.
+  const int lane = threadIdx.x & 63;
+  for (int i0 = 0; i0 < n; i0 += blockDim.x) {
+    const int i = i0 + threadIdx.x;
+    const int t = i < n ? ix[i] : -1;
+    const bool valid = t >= 0 && t < nbits;
+    const int w = valid ? (t >> 5) : -1 - lane;  // invalid lanes form segments of their own
+    uint32_t m = valid ? 1u << (t & 31) : 0u;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const uint32_t mo = __shfl_up(m, off, 64);
+      const int wo = __shfl_up(w, off, 64);
+      if (lane >= off && wo == w) m |= mo;
     }
+    const int wn = __shfl_down(w, 1, 64);
+    if (valid && (lane == 63 || wn != w)) {
+      if (lds) atomicOr(&s_bits[w], m);
+      else atomicOr(&b[w], m);
+    }
+  }
+  if (lds) {
+    __syncthreads();
+    for (int w = threadIdx.x; w < words; w += blockDim.x) b[w] = s_bits[w];
   }
 }
 

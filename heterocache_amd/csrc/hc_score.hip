@@ -302,6 +302,111 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
   }
 }
 
+// Statistics pass for few query rows (R <= 16) over natural-layout keys, on
+// the vector ALUs.  With at most 16 rows the contraction is 2*R*128 flops
+// per 256-byte key row, so the pass is bound by streaming the keys -- and
+// the MFMA operand layout of score_stats_kernel makes every wave load touch
+// 16 rows of 64 bytes each.  Here the 16 lanes of group s hold channels
+// 8c..8c+7 (c = lane % 16) of token 4*step + s, so a wave load reads four
+// whole 256-byte token rows; the groups' partial dot products are summed by
+// a butterfly, after which lane c < R of a group holds row c's logit of its
+// token.  Logits are stored as score_stats_kernel stores them (base-2
+// scaled and masked, [job][R][span]) and every workgroup writes one
+// (max, sum) partial per row, so the merge and finish passes are shared.
+// NR: rows held per lane (R rounded up to 4, 8 or 16).
+constexpr int kRowsSteps = 8;  // 4-token steps per wave and iteration
+template <typename T, int NR, int RM>
+__global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(ScoreArgs a, float* __restrict__ part,
+                                                                          float* __restrict__ logits) {
+  typedef typename Elem<T>::vec8 vec8;
+  __shared__ float s_st[kScoreWaves][16][2];
+  const int job = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane >> 4, c = lane & 15;
+  // This lane's 8 channels of every query row, as floats (zero past R).
+  float qr[NR][8];
+  {
+    const T* q = reinterpret_cast<const T*>(a.q) + a.q_off[job] + 8 * c;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      if (r < a.R) {
+        const vec8 v = load8<T>(q + (r / a.W) * a.q_head_stride + (r % a.W) * a.q_row_stride);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[r][e] = vec8_at<T>(v, e);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[r][e] = 0.f;
+      }
+    }
+  }
+  const bool owner = c < a.R;  // lane c post-processes row c of its group's token
+  const int limit = owner ? row_limit(a, c) : -1;
+  const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
+  const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
+  const int t_end = min(c1 * kScoreChunk, a.L);
+  const T* kb = reinterpret_cast<const T*>(a.k) + a.k_off[job] + 8 * c;
+  float* lrow = logits + ((int64_t)job * a.R + (owner ? c : 0)) * a.span;
+  float m = -FLT_MAX, l = 0.f;
+  constexpr int kIter = kScoreWaves * kRowsSteps * 4;  // tokens per workgroup iteration
+  for (int t0 = c0 * kScoreChunk + wave * kRowsSteps * 4; t0 < t_end; t0 += kIter) {
+    vec8 kr[kRowsSteps];
+#pragma unroll
+    for (int st = 0; st < kRowsSteps; ++st) {
+      const int t = t0 + 4 * st + sub;
+      kr[st] = t < a.L ? load8<T>(kb + (int64_t)t * a.k_tok_stride) : zero8<T>();
+    }
+    float x[kRowsSteps];
+#pragma unroll
+    for (int st = 0; st < kRowsSteps; ++st) {
+      float acc[NR];
+#pragma unroll
+      for (int r = 0; r < NR; ++r) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qr[r][e], vec8_at<T>(kr[st], e), d);
+        acc[r] = d;
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) acc[r] += __shfl_xor(acc[r], off, 16);
+      }
+      float mine = acc[0];
+#pragma unroll
+      for (int r = 1; r < NR; ++r) mine = c == r ? acc[r] : mine;
+      const int t = t0 + 4 * st + sub;
+      x[st] = t <= limit ? scaled_logit<RM>(a, mine) : -INFINITY;
+      if (owner && t < a.span) lrow[t] = x[st];
+    }
+    float mx = x[0];
+#pragma unroll
+    for (int st = 1; st < kRowsSteps; ++st) mx = __builtin_elementwise_maximum(mx, x[st]);
+    const float mn = __builtin_elementwise_maximum(m, mx);
+    float add = 0.f;
+#pragma unroll
+    for (int st = 0; st < kRowsSteps; ++st) add += fast_exp2(x[st] - mn);
+    l = fmaf(l, fast_exp2(m - mn), add);
+    m = mn;
+  }
+  // Rows are held by lanes c, c+16, c+32, c+48 of each wave; then the waves.
+  const float M = rows4_max(m);
+  const float Ls = rows4_sum(l * fast_exp2(m - M));
+  if (sub == 0) {
+    s_st[wave][c][0] = M;
+    s_st[wave][c][1] = Ls;
+  }
+  __syncthreads();
+  if (threadIdx.x < a.R) {
+    const int r = threadIdx.x;
+    float mm = -INFINITY, ll = 0.f;
+#pragma unroll
+    for (int w = 0; w < kScoreWaves; ++w) merge_ml(mm, ll, s_st[w][r][0], s_st[w][r][1]);
+    float* o = part + (((int64_t)job * gridDim.x + blockIdx.x) * a.R + r) * 2;
+    o[0] = mm;
+    o[1] = ll;
+  }
+}
+
 // One wave per (job, row): lanes stride over the chunks, then a xor tree.
 __global__ __launch_bounds__(256) void score_stats_merge_kernel(const float* __restrict__ part, int nchunks, int R,
                                                                 int njobs, float* __restrict__ stats,
@@ -1456,6 +1561,20 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   const bool via_logits = a.R < kLogitRows;
   const int rm = (a.flags & HC_SCORE_ROUND_BF16) ? 1 : (a.flags & HC_SCORE_ROUND_F16) ? 2 : 0;
   int nparts = 0;  // statistics partials per job: the stats grid's x extent
+  if (!STORE && via_logits && a.R <= 16) {
+#define HC_ROWS(NR, RM)                                                                                     \
+  do {                                                                                                      \
+    auto fn = score_rows_valu_kernel<T, NR, RM>;                                                            \
+    ScoreArgs as = a;                                                                                       \
+    nparts = plan_chunks(reinterpret_cast<const void*>(fn), 0, njobs, nchunks, as);                         \
+    hipLaunchKernelGGL(fn, dim3(nparts, njobs), dim3(kScoreWaves * 64), 0, s, as, part, A);                 \
+  } while (0)
+#define HC_ROWS_RM(NR) \
+  if (rm == 0) HC_ROWS(NR, 0); else if (rm == 1) HC_ROWS(NR, 1); else HC_ROWS(NR, 2);
+    if (a.R <= 4) { HC_ROWS_RM(4) } else if (a.R <= 8) { HC_ROWS_RM(8) } else { HC_ROWS_RM(16) }
+#undef HC_ROWS_RM
+#undef HC_ROWS
+  } else {
 #define HC_STATS(RM, LG)                                                                                    \
   do {                                                                                                      \
     auto fn = score_stats_kernel<T, STORE, RM, LG>;                                                         \
@@ -1469,6 +1588,7 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
     if (rm == 0) HC_STATS(0, false); else if (rm == 1) HC_STATS(1, false); else HC_STATS(2, false);
   }
 #undef HC_STATS
+  }
   int rc = check_launch("hc_score(stats)");
   if (rc) return rc;
   hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nparts, a.R,

@@ -38,7 +38,8 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
     int64_t src_tok_stride, int src_len, const int32_t* __restrict__ idx, const int64_t* __restrict__ idx_off,
     const int32_t* __restrict__ count, const int32_t* __restrict__ dst_row, T* __restrict__ kstore,
     T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off, const int32_t* __restrict__ trigger,
-    const int32_t* __restrict__ trig_of, int njobs, int tiles_per_job) {
+    const int32_t* __restrict__ trig_of, int njobs, int tiles_per_job, const int64_t* __restrict__ src_k_addr,
+    const int64_t* __restrict__ src_v_addr) {
   __shared__ T sk[HC_TILE][HC_HEAD_DIM + 8];
   __shared__ T sv[HC_TILE][HC_HEAD_DIM + 8];
   const int64_t items = (int64_t)njobs * tiles_per_job;
@@ -68,8 +69,10 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
   const int tok0 = tile * HC_TILE;
   const int valid = min(HC_TILE, n - tok0);
 
-  const T* bk = src_k + src_off[job];
-  const T* bv = src_v + src_off[job];
+  // Per-job source tensors (src_*_addr: device addresses, one per job) or
+  // one base for all jobs.
+  const T* bk = (src_k_addr ? reinterpret_cast<const T*>(src_k_addr[job]) : src_k) + src_off[job];
+  const T* bv = (src_v_addr ? reinterpret_cast<const T*>(src_v_addr[job]) : src_v) + src_off[job];
   const int32_t* ix = idx ? idx + idx_off[job] : nullptr;
   // 32 tokens x 16 chunks of 8 elements.
   for (int c = threadIdx.x; c < HC_TILE * 16; c += 256) {
@@ -181,14 +184,15 @@ static int launch_gather_store(const void* src_k, const void* src_v, const int64
                                int src_len, const int32_t* idx, const int64_t* idx_off, const int32_t* count,
                                const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off,
                                int njobs, int max_count, const int32_t* trigger, const int32_t* trig_of,
-                               bool host_src, int max_workgroups, hipStream_t s) {
+                               bool host_src, int max_workgroups, hipStream_t s,
+                               const int64_t* src_k_addr = nullptr, const int64_t* src_v_addr = nullptr) {
   const int tiles = (max_count + HC_TILE - 1) / HC_TILE;
   const int64_t items = (int64_t)tiles * njobs;
   const int64_t cap = max_workgroups > 0 ? max_workgroups : (host_src ? kHostGatherWorkgroups : items);
   const unsigned grid = (unsigned)std::min<int64_t>(items, cap);
   hipLaunchKernelGGL((gather_store_kernel<T>), dim3(grid), dim3(256), 0, s, (const T*)src_k, (const T*)src_v, src_off,
                      src_tok_stride, src_len, idx, idx_off, count, dst_row, (T*)kstore, (T*)vstore, row_tile_off, trigger,
-                     trig_of, njobs, tiles);
+                     trig_of, njobs, tiles, src_k_addr, src_v_addr);
   return check_launch("hc_gather_store");
 }
 
@@ -308,7 +312,7 @@ extern "C" int hc_gather_store_groups(int dtype, const void* src_k, const void* 
                                       const int64_t* row_tile_off, int ngroups, const int32_t* group_begin,
                                       const int32_t* group_max_count, const int32_t* trigger,
                                       const int32_t* trig_of, int max_workgroups, void* const* events,
-                                      void* stream) {
+                                      const int64_t* src_k_addr, const int64_t* src_v_addr, void* stream) {
   clear_error();
   if (ngroups < 0 || ngroups > 65535 || max_workgroups < 0)
     return set_error(HC_ERR_INVALID, "hc_gather_store_groups: ngroups=%d", ngroups);
@@ -335,8 +339,13 @@ extern "C" int hc_gather_store_groups(int dtype, const void* src_k, const void* 
       return set_error(HC_ERR_INVALID, "hc_gather_store_groups: group %d token stride %lld", g,
                        (long long)group_tok_stride[g]);
   }
-  if (!src_k || !src_v || !src_off || !count || !dst_row || !kstore || !vstore || !row_tile_off ||
-      (idx && !idx_off))
+  const bool by_addr = src_k_addr != nullptr;
+  if ((src_k_addr == nullptr) != (src_v_addr == nullptr))
+    return set_error(HC_ERR_INVALID, "hc_gather_store_groups: give both per-job address tables or neither");
+  if (by_addr && src_is_host)
+    return set_error(HC_ERR_INVALID, "hc_gather_store_groups: per-job addresses are device addresses");
+  if ((!by_addr && (!src_k || !src_v)) || !src_off || !count || !dst_row || !kstore || !vstore ||
+      !row_tile_off || (idx && !idx_off))
     return set_error(HC_ERR_INVALID, "hc_gather_store_groups: null pointer argument");
   const void* sk = src_k;
   const void* sv = src_v;
@@ -355,22 +364,24 @@ extern "C" int hc_gather_store_groups(int dtype, const void* src_k, const void* 
       const int32_t* cn = count + b0;
       const int32_t* dr = dst_row + b0;
       const int32_t* to = trig_of ? trig_of + b0 : nullptr;
+      const int64_t* ka = by_addr ? src_k_addr + b0 : nullptr;
+      const int64_t* va = by_addr ? src_v_addr + b0 : nullptr;
       int rc;
       switch (dtype) {
         case HC_DTYPE_BF16:
           rc = launch_gather_store<__bf16>(sk, sv, so, group_tok_stride[g], src_len, idx, io, cn, dr, kstore, vstore,
                                            row_tile_off, nj, group_max_count[g], trigger, to, src_is_host != 0,
-                                           max_workgroups, s);
+                                           max_workgroups, s, ka, va);
           break;
         case HC_DTYPE_F16:
           rc = launch_gather_store<_Float16>(sk, sv, so, group_tok_stride[g], src_len, idx, io, cn, dr, kstore,
                                              vstore, row_tile_off, nj, group_max_count[g], trigger, to,
-                                             src_is_host != 0, max_workgroups, s);
+                                             src_is_host != 0, max_workgroups, s, ka, va);
           break;
         case HC_DTYPE_F32:
           rc = launch_gather_store<float>(sk, sv, so, group_tok_stride[g], src_len, idx, io, cn, dr, kstore, vstore,
                                           row_tile_off, nj, group_max_count[g], trigger, to, src_is_host != 0,
-                                          max_workgroups, s);
+                                          max_workgroups, s, ka, va);
           break;
         default:
           return set_error(HC_ERR_INVALID, "hc_gather_store_groups: unknown dtype %d", dtype);

@@ -239,16 +239,25 @@ def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, c
 
 def gather_store_groups(src_k, src_v, src_off, group_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
                         vstore, row_tile_off, group_begin, group_max_count, events, src_is_host=False, trigger=None,
-                        trig_of=None, stream=None, max_workgroups=0):
+                        trig_of=None, stream=None, max_workgroups=0, src_k_addr=None, src_v_addr=None):
     """gather_store over consecutive job groups, one launch per group, each
     followed by a record of that group's event (hc_gather_store_groups).
 
     group_begin (int32, ngroups + 1), group_max_count (int32, ngroups) and
     group_tok_stride (int64, ngroups): host numpy arrays.  events: one
     torch.cuda.Event (or None) per group; each is recorded on `stream` once
-    its group's rows are written."""
+    its group's rows are written.  src_k_addr / src_v_addr: optional int64
+    device tensors of one source address per job (src_off is added to it);
+    src_k / src_v then only give the dtype."""
     lib = _lib.load()
-    _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger, trig_of)
+    _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger, trig_of, src_k_addr,
+                  src_v_addr)
+    if src_k_addr is not None:
+        if src_v_addr is None or src_k_addr.dtype != torch.int64 or src_k_addr.numel() != count.numel() or \
+                src_v_addr.dtype != torch.int64 or src_v_addr.numel() != count.numel():
+            raise ValueError("src_k_addr and src_v_addr must be int64 tensors of one address per job")
+        if src_is_host:
+            raise ValueError("per-job source addresses are device addresses")
     if src_is_host:
         if src_k.is_cuda or not src_k.is_pinned() or not src_v.is_pinned():
             raise ValueError("host sources must be pinned CPU tensors")
@@ -269,7 +278,8 @@ def gather_store_groups(src_k, src_v, src_off, group_tok_stride, src_len, idx, i
                                           _ptr(src_off), gs.ctypes.data, int(src_len), _ptr(idx), _ptr(idx_off),
                                           _ptr(count), _ptr(dst_row), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
                                           ng, gb.ctypes.data, gm.ctypes.data, _ptr(trigger), _ptr(trig_of),
-                                          int(max_workgroups), handles, _stream(stream, kstore)))
+                                          int(max_workgroups), handles, _ptr(src_k_addr), _ptr(src_v_addr),
+                                          _stream(stream, kstore)))
 
 
 def copy_rows(src_k, src_v, src_bh, dst_k, dst_v, dst_bh, counts, dst_is_host=False, max_workgroups=32,

@@ -173,7 +173,11 @@ int hc_gather_store(int dtype, const void* src_k, const void* src_v, int src_is_
  * also for an empty group -- so a consumer of group g's rows waits for that
  * group alone.  Device arrays are indexed by global job as in
  * hc_gather_store; trig_of keeps global trigger indices.  All groups are
- * validated before the first launch.  Serves the retrieval of one drift
+ * validated before the first launch.  src_k_addr / src_v_addr (device
+ * int64 arrays, one address per job, or both NULL): each job's source
+ * tensor base in device memory, to which src_off[j] is added -- so one
+ * launch gathers from several tensors (each layer's prefill K/V) -- in
+ * place of src_k / src_v.  Serves the retrieval of one drift
  * check, one group per layer: the reference copies each satellite's rows
  * with its own H2D copy_ on the default stream before the next step
  * (heterocache/cache_utils.py:1097-1123); here each layer's next attention
@@ -184,7 +188,8 @@ int hc_gather_store_groups(int dtype, const void* src_k, const void* src_v, int 
                            const int32_t* count, const int32_t* dst_row, void* kstore, void* vstore,
                            const int64_t* row_tile_off, int ngroups, const int32_t* group_begin,
                            const int32_t* group_max_count, const int32_t* trigger, const int32_t* trig_of,
-                           int max_workgroups, void* const* events, void* stream);
+                           int max_workgroups, void* const* events, const int64_t* src_k_addr,
+                           const int64_t* src_v_addr, void* stream);
 
 /*
  * Append one token per row at slot row_len[r], then row_len[r] += 1.

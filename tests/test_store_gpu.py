@@ -228,3 +228,43 @@ def test_gather_groups_match_one_gather_and_record_each_event(dev, host):
             sel = torch.as_tensor(src_off[j] + idx[j, :n].astype(np.int64) * strides[g], device=dev)
             rows = sel[:, None] + torch.arange(D, device=dev)[None, :]
             assert torch.equal(ka[0], base_k[rows]) and torch.equal(va[0], base_v[rows]), j
+
+
+def test_gather_groups_from_per_job_tensors(dev):
+    """hc_gather_store_groups with per-job source addresses: jobs read two
+    separate [1, H, L, 128] tensors (one a strided projection view) in one
+    launch (one token stride), each row bit for bit the rows indexed."""
+    from heterocache_amd import ops
+    L, D, H = 500, 128, 3
+    dt = torch.bfloat16
+    x = rand((1, L, H * D), dt, dev, 23)
+    kb = x.view(1, L, H, D).transpose(1, 2)          # token stride H * 128, as the projections give
+    y = rand((1, L, H * D), dt, dev, 24)
+    vb = y.view(1, L, H, D).transpose(1, 2)
+    # A second pair of tensors with the same (projection) token stride.
+    ka = rand((1, L, H * D), dt, dev, 25).view(1, L, H, D).transpose(1, 2)
+    va = rand((1, L, H * D), dt, dev, 26).view(1, L, H, D).transpose(1, 2)
+    rng = np.random.default_rng(9)
+    srcs = [(ka, va, 1), (kb, vb, 2), (kb, vb, 0)]
+    counts = np.array([77, 200, 5], dtype=np.int32)
+    M = int(counts.max())
+    idx = np.zeros((3, M), dtype=np.int32)
+    for j, n in enumerate(counts):
+        idx[j, :n] = np.sort(rng.choice(L, n, replace=False))
+    idx_d = torch.as_tensor(idx).to(dev)
+    idx_off = torch.as_tensor(np.arange(3) * M, dtype=torch.int64).to(dev)
+    src_off = torch.as_tensor([k.stride(1) * h for k, _, h in srcs], dtype=torch.int64).to(dev)
+    k_addr = torch.as_tensor([k.data_ptr() for k, _, _ in srcs], dtype=torch.int64).to(dev)
+    v_addr = torch.as_tensor([v.data_ptr() for _, v, _ in srcs], dtype=torch.int64).to(dev)
+    st = KVStore([256] * 3, dt, dev)
+    cnt = torch.as_tensor(counts).to(dev)
+    dst = torch.arange(3, dtype=torch.int32, device=dev)
+    ops.gather_store_groups(ka, va, src_off, np.array([H * D], dtype=np.int64), L, idx_d, idx_off, cnt, dst,
+                            st.k, st.v, st.row_tile_off, np.array([0, 3], dtype=np.int32), [M], [None],
+                            src_k_addr=k_addr, src_v_addr=v_addr)
+    torch.cuda.synchronize()
+    for j, (k, v, h) in enumerate(srcs):
+        n = int(counts[j])
+        rk, rv = st.read_rows([j], n)
+        sel = torch.as_tensor(idx[j, :n], dtype=torch.long, device=dev)
+        assert torch.equal(rk[0], k[0, h].index_select(0, sel)) and torch.equal(rv[0], v[0, h].index_select(0, sel)), j
