@@ -215,10 +215,10 @@ def full_step_phase(args, torch, dev):
         return HeteroCache(cfg)
 
     def prefill(cache, keep_inputs):
-        """All layers' prefill: main-stream ms per layer (events) and total
-        ms until every stream is idle (tier copies included)."""
+        """All layers' prefill: main-stream ms of each layer (events) and
+        total ms until every stream is idle (tier copies included)."""
         inputs = []
-        ms, total = 0.0, 0.0
+        ms, total = [], 0.0
         for layer in range(NL):
             x = wl.layer(layer)
             torch.cuda.synchronize()
@@ -231,10 +231,10 @@ def full_step_phase(args, torch, dev):
             e1.record()
             torch.cuda.synchronize()
             total += (time.perf_counter() - t0) * 1e3
-            ms += e0.elapsed_time(e1)
+            ms.append(e0.elapsed_time(e1))
             inputs.append((x["q_steps"], x["k_new"], x["v_new"]))
             del x, k, v
-        return ms / NL, total, inputs
+        return ms, total, inputs
 
     for label, thr, steps, tier in runs:
         cache = make_cache(thr, tier, steps + S + 8, not label.endswith("_f32"))
@@ -283,7 +283,9 @@ def full_step_phase(args, torch, dev):
         attn_bytes = sum((len0 + rows * (i + 1)) * D * 2 * 2 for i in range(steps)) + steps * NL * 2 * Hkv * G * D * 2
         nbytes = attn_bytes + checks * check_k_bytes + ret_bytes
         ms = float(np.mean(step_ms))
+        pre_ms, pre_steady = float(np.mean(pre_ms)), float(np.mean(pre_ms[1:]))
         res[label] = {"tier": tier_mode, "round_scores": cache.round_scores, "one_pass_checks": cache.one_pass_checks,
+                      "prefill_steady_ms_per_layer": round(pre_steady, 3),
                       "steps": steps, "checks": checks, "ms_per_step": round(ms, 4),
                       "wall_ms_per_step": round(wall, 4),
                       "leader_triggers": trig_total, "leaders": int(trig.numel()),
@@ -316,11 +318,60 @@ def full_step_phase(args, torch, dev):
                         "frac": a["frac_of_hbm_peak"], "run": f"{'retrieval every check' if a is res.get('always') else 'run'}"
                                                              f", {a['tier']} tier",
                         "bytes": "attended K/V + q/out, pivot keys per check / 5, retrieved rows written / 5"},
-           "prefill": {"compress_ms_per_layer": a["prefill_main_ms_per_layer"],
-                       "total_ms_device_tier": a["prefill_total_ms"]}}
+           "prefill": prefill_roofline(data, L, args.ratio, a, res)}
     if "host_always" in res:
         out["prefill"]["total_ms_host_tier"] = res["host_always"]["prefill_total_ms"]
         out["prefill"]["host_tier_link_gbs"] = round(tier_bytes / res["host_always"]["prefill_total_ms"] / 1e6, 1)
+    return out
+
+
+def prefill_bytes(data, L, ratio, tier, G=4, D=128, esz=2):
+    """Algorithmic HBM bytes of one prefill-compression call sequence per
+    layer (update, init_coefficient, prefill_select) on the reference head
+    JSON, batch 1: keep-head K/V read and stored; the satellites' K/V read
+    for a host-pinned tier (an HBM tier keeps the prefill tensors, no
+    copy); the scored heads' keys read once and their pooled scores written
+    once and read by the selection; the compressed heads' kept rows read
+    and stored."""
+    from heterocache_amd import workloads
+    from heterocache_amd.cache_utils import _f32_caps
+    NL = len(data["classification_matrix"])
+    base = workloads.get_compress_len(ratio, workloads.full_head_count(data), L, 8 * NL)
+    out = []
+    for layer in range(NL):
+        keep = len(data["need_to_keep_counts"][layer])
+        sats = len(data["need_to_update_counts"][layer])
+        piv = len(data["need_to_select_counts"][layer])
+        n_c = data["need_to_compress_counts"][layer]
+        caps = _f32_caps(base, data["allocation_matrix"][layer][:n_c], L) if n_c else np.zeros(0)
+        row = L * D * esz
+        parts = {"keep_copy": keep * row * 2 * 2,
+                 "tier_copy": sats * row * 2 if tier == "host" else 0,
+                 "score": (n_c + piv) * (row + L * 4),
+                 "select": (n_c + piv) * L * 4,
+                 "gather": int(caps.sum()) * D * esz * 2 * 2}
+        out.append(parts)
+    return out
+
+
+def prefill_roofline(data, L, ratio, run, res):
+    """Prefill compression of the run the full step is quoted on: ms per
+    layer over layers 1.. (layer 0 also allocates the cache's storage and
+    builds every layer's metadata: reported as setup), algorithmic bytes and
+    the fraction of the HBM roofline."""
+    per = prefill_bytes(data, L, ratio, run["tier"])
+    mean = {k: int(np.mean([p[k] for p in per])) for k in per[0]}
+    nbytes = float(np.mean([sum(p.values()) for p in per[1:]]))
+    steady = run["prefill_steady_ms_per_layer"]
+    out = {"compress_ms_per_layer": steady, "all_layers_mean_ms": run["prefill_main_ms_per_layer"],
+           "first_layer_setup_ms": round((run["prefill_main_ms_per_layer"] - steady) * len(per), 3),
+           "bytes_per_layer": int(nbytes), "bytes_parts_mean": mean,
+           "gbs": round(nbytes / (steady * 1e-3) / 1e9, 1),
+           "frac_of_hbm_peak": round(nbytes / (steady * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "tier": run["tier"], "total_ms": run["prefill_total_ms"]}
+    if "host_always" in res:
+        out["host_tier_compress_ms_per_layer"] = res["host_always"]["prefill_steady_ms_per_layer"]
+        out["total_ms_host_tier"] = res["host_always"]["prefill_total_ms"]
     return out
 
 

@@ -452,17 +452,13 @@ class HeteroCache(DynamicCache):
     def _layer_row_caps(self, layer_idx):
         """Row capacities for the whole lifetime (heterocache/cache_utils.py:693-766)."""
         L, gen = self.prefill_len, self.config.max_gen_len
-        keep = set(self.data["need_to_keep_counts"][layer_idx])
-        alloc = self.data["allocation_matrix"][layer_idx]
-        caps = []
-        for h in range(self.num_kv_heads):
-            if h in keep:
-                cap = L
-            else:
-                c64 = max(min(int(self.base_compress_len * alloc[h]), L), 0)
-                c32 = int(_f32_caps(self.base_compress_len, [alloc[h]], L)[0])
-                cap = max(c64, c32)
-            caps.append(cap)
+        keep = np.zeros(self.num_kv_heads, dtype=bool)
+        keep[list(self.data["need_to_keep_counts"][layer_idx])] = True
+        alloc = np.asarray(self.data["allocation_matrix"][layer_idx], dtype=np.float64)
+        # float64 capacity (int() truncation, clamped to [0, L]) and float32 cap: room for both.
+        c64 = np.clip(np.trunc(self.base_compress_len * alloc), 0, L).astype(np.int64)
+        c32 = _f32_caps(self.base_compress_len, alloc, L)
+        caps = np.where(keep, L, np.maximum(c64, c32)).astype(np.int64).tolist()
         self.layer_head_capacities[layer_idx] = caps
         return [caps[r % self.num_kv_heads] + gen for r in range(self.bsz * self.num_kv_heads)]
 

@@ -145,6 +145,22 @@ __device__ __forceinline__ float vec8_at<float>(const Elem<float>::vec8& v, int 
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Sum of a value over the 16 lanes of its row (lanes 16r .. 16r+15), in
+// every lane of the row: four DPP adds (rotate the row by 8 and by 4, then
+// swap within quads by 2 and by 1), full rate on the VALU, where a
+// __shfl_xor butterfly goes through the LDS crossbar once per step.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_mov<0x128>(v);  // row_ror:8
+  v += dpp_mov<0x124>(v);  // row_ror:4
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  return v;
+}
+
 // Combine a value over the four lanes l, l^16, l^32, l^48 of a wave (one
 // lane per 16-lane row), as the MFMA layouts need for a per-column max or
 // sum.  gfx950's row swaps (v_permlane16_swap / v_permlane32_swap) move the

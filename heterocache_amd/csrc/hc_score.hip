@@ -309,8 +309,8 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
 // 16 rows of 64 bytes each.  Here the 16 lanes of group s hold channels
 // 8c..8c+7 (c = lane % 16) of token 4*step + s, so a wave load reads four
 // whole 256-byte token rows; the groups' partial dot products are summed by
-// a butterfly, after which lane c < R of a group holds row c's logit of its
-// token.  Logits are stored as score_stats_kernel stores them (base-2
+// four DPP adds (row16_sum), after which lane c < R of a group holds row c's
+// logit of its token.  Logits are stored as score_stats_kernel stores them (base-2
 // scaled and masked, [job][R][span]) and every workgroup writes one
 // (max, sum) partial per row, so the merge and finish passes are shared.
 // NR: rows held per lane (R rounded up to 4, 8 or 16).
@@ -349,6 +349,8 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(Score
   float m = -FLT_MAX, l = 0.f;
   constexpr int kIter = kScoreWaves * kRowsSteps * 4;  // tokens per workgroup iteration
   for (int t0 = c0 * kScoreChunk + wave * kRowsSteps * 4; t0 < t_end; t0 += kIter) {
+    // (A second key buffer, loads of the next iteration in flight during
+    // this one, costs occupancy and was slower: 83 against 73 us.)
     vec8 kr[kRowsSteps];
 #pragma unroll
     for (int st = 0; st < kRowsSteps; ++st) {
@@ -367,10 +369,7 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(Score
         acc[r] = d;
       }
 #pragma unroll
-      for (int off = 1; off < 16; off <<= 1) {
-#pragma unroll
-        for (int r = 0; r < NR; ++r) acc[r] += __shfl_xor(acc[r], off, 16);
-      }
+      for (int r = 0; r < NR; ++r) acc[r] = row16_sum(acc[r]);
       float mine = acc[0];
 #pragma unroll
       for (int r = 1; r < NR; ++r) mine = c == r ? acc[r] : mine;
