@@ -47,6 +47,8 @@ def parse():
                    help="comma-separated runs of the full-step phase (natural, never, always, always_f32, "
                         "host_never, host_always)")
     p.add_argument("--no-full-step", action="store_true", help="skip the HeteroCache drift/retrieval phase")
+    p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end phases of configs 4 and 1")
+    p.add_argument("--e2e-only", action="store_true", help="run only the end-to-end phases of configs 4 and 1")
     p.add_argument("--overlap-check", action="store_true",
                    help="full step: run the drift checks and their retrieval on a side stream (overlap_drift_check)")
     p.add_argument("--two-pass-check", action="store_true",
@@ -728,6 +730,192 @@ def prefill_attention_phase(args, torch, dev):
     return out
 
 
+def config4_phase(args, torch, dev, L=229376, chunk=8192, steps=2000, period=200):
+    """Config 4 end to end: Llama-3-8B shape at 229376 tokens with the
+    reference's head JSON, batch 1, bf16.  An 8K-chunked prefill through
+    HeteroCache: each chunk is staged layer by layer and its causal
+    attention runs over the keys staged so far (hc_prefill_attn, chunk
+    queries synthetic: the attention's cost depends on shapes only; the
+    last query is the workload's); after the last chunk each layer's
+    compression (pivot sets, budget selection, gather, keep-head store) and
+    the copy of the satellites' K/V into the host-pinned tier.  Then 2000
+    decode steps (append + attention + drift check every 5 steps,
+    top-1024 retrieval from the pinned tier) with attention that drifts to
+    a new block of 8 keys every 200 steps.  Reported: prefill attention
+    TFLOP/s and MFMA fraction, compression ms, decode step time and the
+    attention's HBM GB/s, and the retrieval time the decode steps after a
+    triggered check do not hide (their time above the steps after checks
+    that triggered nothing)."""
+    from heterocache_amd import workloads
+    from heterocache_amd.cache_utils import HeteroCache, HeteroCacheConfig
+    from heterocache_amd.llama_model import prefill_attention
+    Hkv, G, D, NL, S = 8, 4, 128, 32, 5
+    Hq = Hkv * G
+    data = llama_head_json()
+    cfg = HeteroCacheConfig(data, compression_ratio=args.ratio, stable_threshold=0.5, real_offload=True,
+                            max_gen_len=steps + 8, decode_step=S, pooling="avgpool", kernel_size=5,
+                            num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
+                            tier_placement="host")
+    cache = HeteroCache(cfg)
+    cache.begin_prefill(L)
+    wl = workloads.BlockDriftWorkload(L, kv_heads=Hkv, group=G, steps=steps, period=period, seed=1004, device=dev)
+    g = torch.Generator(device=dev).manual_seed(4)
+    qchunk = torch.randn((1, Hq, chunk, D), generator=g, device=dev).to(torch.bfloat16)
+    kv, step_inputs = {}, {}
+    for layer in range(NL):
+        k, v = wl.prefill(layer)
+        x = wl.queries(layer, k)
+        kv[layer] = (k, v)
+        step_inputs[layer] = (x["q_last"], x["q_steps"], x["k_new"], x["v_new"])
+    torch.cuda.synchronize()
+    scale = 1.0 / math.sqrt(D)
+    attn_ms = comp_ms = 0.0
+    flops = 0.0
+    comp_last = []
+    ev = lambda: torch.cuda.Event(enable_timing=True)
+    t_wall = time.perf_counter()
+    for s0 in range(0, L, chunk):
+        e = min(s0 + chunk, L)
+        n = e - s0
+        for layer in range(NL):
+            k, v = kv[layer]
+            q = qchunk[:, :, :n]
+            if e == L:
+                q = torch.cat([qchunk[:, :, :n - 1], step_inputs[layer][0]], dim=2)
+            a0, a1, c0, c1 = ev(), ev(), ev(), ev()
+            c0.record()
+            kc, vc = cache.update(k[:, :, s0:e], v[:, :, s0:e], layer, {"query_states": q})
+            c1.record()
+            a0.record()
+            prefill_attention(q, kc, vc, None, scale)
+            a1.record()
+            b0, b1 = ev(), ev()
+            b0.record()
+            cache.init_coefficient(q, kc, layer)
+            cache.prefill_select(q, kc, vc, layer)
+            b1.record()
+            torch.cuda.synchronize()
+            attn_ms += a0.elapsed_time(a1)
+            comp_ms += c0.elapsed_time(c1) + b0.elapsed_time(b1)
+            if e == L:
+                comp_last.append(c0.elapsed_time(c1) + b0.elapsed_time(b1))
+            flops += 4 * D * Hq * (n * s0 + n * (n + 1) / 2)
+    torch.cuda.synchronize()
+    prefill_wall = time.perf_counter() - t_wall
+    del kv, qchunk
+    torch.cuda.empty_cache()
+    # Decode: per-step events; the check's trigger flags logged after every check.
+    ncheck = steps // S
+    trig_log = torch.zeros((ncheck, cache._trigger_all.numel()), dtype=torch.int32, device=dev)
+    evs = [(ev(), ev()) for _ in range(steps)]
+    attn_bytes = []
+    for t in range(steps):
+        attn_bytes.append(sum(st.kv_bytes() + st.rows * st.bytes_per_token() for st in cache.stores))
+        evs[t][0].record()
+        for layer in range(NL):
+            _, qs, kn, vn = step_inputs[layer]
+            cache.update(kn[t], vn[t], layer)
+            cache.decode_attention(qs[t], layer)
+            cache.decode_select(qs[t], layer)
+        if t == steps - 1:
+            torch.cuda.current_stream().wait_stream(cache.retrieval_stream(dev))
+        evs[t][1].record()
+        if (t + 1) % S == 0:
+            trig_log[(t + 1) // S - 1].copy_(cache._trigger_all)
+    torch.cuda.synchronize()
+    step_ms = np.array([a.elapsed_time(b) for a, b in evs])
+    trig = trig_log.sum(dim=1).cpu().numpy()
+    # Steps after check c (its retrieval runs before them) are 5c+5 .. 5c+9.
+    after = [step_ms[S * (c + 1):S * (c + 2)].sum() for c in range(ncheck - 1)]
+    quiet = [a for a, n_t in zip(after, trig[:-1]) if n_t == 0]
+    busy = [(a, n_t) for a, n_t in zip(after, trig[:-1]) if n_t > 0]
+    base = float(np.median(quiet)) if quiet else None
+    sats = sum(len(r) for r in data["need_to_update_counts"])
+    per_check = sats * 1024 * D * 2 * 2
+    exposed = round(float(np.mean([a - base for a, _ in busy])), 4) if busy and base is not None else None
+    bytes_step = float(np.mean(attn_bytes)) + NL * 2 * Hq * D * 2
+    out = {"workload": f"Llama-3-8B shape, {L} ctx, reference head JSON, ratio {args.ratio}, {chunk}-token prefill "
+                       f"chunks, {steps} decode steps, block drift every {period} steps, host-pinned tier, "
+                       "top-1024 retrieval",
+           "prefill": {"attention_ms": round(attn_ms, 1), "attention_tflops": round(flops / attn_ms / 1e9, 1),
+                       "mfma_frac_bf16_dense": round(flops / attn_ms / 1e9 / 2500.0, 4),
+                       "staging_and_compression_ms": round(comp_ms, 1),
+                       "compression_ms_per_layer_last_chunk": round(float(np.mean(comp_last)), 3),
+                       "wall_s": round(prefill_wall, 2)},
+           "decode": {"steps": steps, "ms_per_step_mean": round(float(step_ms.mean()), 4),
+                      "ms_per_step_median": round(float(np.median(step_ms)), 4),
+                      "attention_bytes_per_step": int(bytes_step),
+                      "attention_gbs_at_step_time": round(bytes_step / (float(np.median(step_ms)) * 1e-3) / 1e9, 1),
+                      "checks": ncheck, "checks_with_triggers": int((trig > 0).sum()),
+                      "leader_triggers": int(trig.sum())},
+           "retrieval": {"bytes_per_full_trigger": per_check,
+                         "five_step_ms_after_quiet_checks": round(base, 4) if base is not None else None,
+                         "exposed_ms_per_triggered_check": exposed,
+                         "triggered_checks_measured": len(busy)}}
+    del cache, step_inputs
+    torch.cuda.empty_cache()
+    return out
+
+
+def config1_phase(args, torch, dev, L=32768, new=256):
+    """Config 1 end to end: the 32-layer Llama-3-8B shape (hidden 4096, 32 q
+    / 8 kv heads, vocab 128256), random-init bf16 weights, the attention
+    patch installed and a synthetic head classification (clusters of 1-4
+    heads per layer, seeded), compression ratio 0.5; transformers'
+    generate() on a 32768-token prompt of seeded random ids, 256 greedy
+    tokens.  Reported: prefill seconds (time to the first token) and decode
+    tokens/s (the remaining 255 tokens), the whole model's decode step
+    included."""
+    from transformers import LlamaConfig, LlamaForCausalLM, StoppingCriteria, StoppingCriteriaList
+    from heterocache_amd import utils, workloads
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=L + new + 8,
+                      rope_theta=500000.0)
+    raw = workloads.synthetic_head_json(32, 8, 1001)
+    with utils.install_attention_patch():
+        torch.manual_seed(1001)
+        with torch.device(dev):
+            model = LlamaForCausalLM._from_config(cfg, torch_dtype=torch.bfloat16).eval()
+    perms = utils.reorder_model_weights_by_classification(model, raw)
+    data = utils.augment_head_data(raw, perms)
+    cc = utils.build_cache_config(model, data, compression_ratio=0.5, max_gen_len=new + 8, decode_step=5)
+    utils.attach_cache(model, cc)
+    ids = torch.randint(0, 128256, (1, L), generator=torch.Generator().manual_seed(1001)).to(dev)
+
+    class Clock(StoppingCriteria):
+        """Records an event after every generated token; never stops."""
+        def __init__(self):
+            self.events = []
+
+        def __call__(self, input_ids, scores, **kw):
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            self.events.append(e)
+            return torch.zeros(input_ids.shape[0], dtype=torch.bool, device=input_ids.device)
+
+    clock = Clock()
+    start = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start.record()
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=new, min_new_tokens=new, do_sample=False,
+                             stopping_criteria=StoppingCriteriaList([clock]), pad_token_id=0)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev = clock.events
+    prefill_s = start.elapsed_time(ev[0]) / 1e3
+    decode_s = ev[0].elapsed_time(ev[-1]) / 1e3
+    res = {"workload": f"Llama-3-8B shape (32 layers, random-init bf16), {L}-token prompt, {new} greedy tokens, "
+                       "ratio 0.5, synthetic head JSON (clusters of 1-4 heads), transformers generate()",
+           "tokens_generated": int(out.shape[1] - L), "prefill_s": round(prefill_s, 3),
+           "decode_tokens_per_s": round((len(ev) - 1) / decode_s, 2),
+           "decode_ms_per_token": round(decode_s * 1e3 / (len(ev) - 1), 3), "wall_s": round(wall, 2)}
+    del model, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def north_star_summary(rec, args):
     """The step target in its own terms: the attention and retrieval-gather
     kernels of the 128K, ratio-0.5 decode step against the HBM roofline, and
@@ -774,6 +962,10 @@ def main():
         if args.calibrate_copy:
             rec["copy_calibration"] = copy_calibration(torch, dev)
         print(json.dumps(rec))
+        return
+    if args.e2e_only:
+        print(json.dumps({"config4_end_to_end": config4_phase(args, torch, dev),
+                          "config1_generate": config1_phase(args, torch, dev)}))
         return
     if args.full_step_only:
         rec = {"full_decode_step": full_step_phase(args, torch, dev)}
@@ -886,6 +1078,9 @@ def main():
         rec["decode_other_configs"] = decode_configs_phase(args, torch, dev)
         rec["baseline_compressors"] = baseline_compressors_phase(args, torch, dev)
         rec["head_analysis"] = head_analysis_phase(args, torch, dev)
+        if not args.no_e2e:
+            rec["config4_end_to_end"] = config4_phase(args, torch, dev)
+            rec["config1_generate"] = config1_phase(args, torch, dev)
     if "full_decode_step" in rec and "gather" in rec:
         rec["north_star"] = north_star_summary(rec, args)
     if not args.no_cpu_baseline:

@@ -333,6 +333,18 @@ class HeteroCache(DynamicCache):
         # nothing.
         self.observer = None
 
+    def __del__(self):
+        # The host-pinned tier is read and written by kernels through its
+        # device mapping (raw pointers), which torch's pinned-memory cache
+        # does not track: before the arena can return to that cache (and be
+        # handed to another allocation), the side-stream work that uses it
+        # must be done.
+        try:
+            if self._tier is not None and self._side is not None and not self._tier[0].is_cuda:
+                self._side.synchronize()
+        except Exception:
+            pass
+
     # -- reference API ------------------------------------------------------
     def __bool__(self):
         return True
