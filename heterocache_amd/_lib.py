@@ -40,7 +40,7 @@ SIGNATURES = {
                                c_void_p, c_void_p]),
     "hc_decode_attn_stats": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                      c_int, c_int, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_int64,
-                                     c_int, c_void_p, c_int, c_void_p, c_int64, c_int64, c_void_p]),
+                                     c_int, c_void_p, c_int, c_void_p, c_int64, c_int64, c_int, c_void_p]),
     "hc_decode_attn_noalloc": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_int, c_int, c_float, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_void_p,
                                        c_void_p]),
@@ -75,7 +75,7 @@ SIGNATURES = {
                          c_void_p, c_size_t, c_void_p, c_void_p]),
     "hc_score_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "hc_score_given_stats": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
-                                     c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p,
+                                     c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_void_p, c_void_p,
                                      c_void_p, c_void_p]),
     "hc_score_with_stats": (c_int, [c_int, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64,
                                     c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_float,

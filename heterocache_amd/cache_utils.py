@@ -76,9 +76,10 @@ class HeteroCacheConfig:
     each step query's softmax statistics over the prompt keys
     (hc_decode_attn_stats), so that a batched check scores in one pass over
     the pivot keys (hc_score_given_stats) instead of a statistics pass that
-    stores every logit and a pass over the logits.  Applies to the uncast
-    float32 scores with pooling widths up to 9; otherwise, and when off, the
-    two-pass scorer runs.
+    stores every logit and a pass over the logits.  Applies to pooling widths
+    up to 9, with or without the reference's cast chain (round_scores: the
+    decode launch then reports the statistics of the rounded logits);
+    otherwise, and when off, the two-pass scorer runs.
     attention_stats_scoring: let the prefill attention report the softmax
     statistics of the last window_size queries (hc_prefill_attn_stats), so
     that prefill_select's observation-window scorer reads the keys once
@@ -981,15 +982,16 @@ class HeteroCache(DynamicCache):
             vn = p[1].reshape(-1, D)
         stat = self._step_stat_view(layer_idx, query_states)
         o = store.attend(q, 1.0 / (D ** 0.5), out=out, k_new=kn, v_new=vn, chunk_tiles=self.chunk_tiles,
-                         stat_len=self.prefill_len if stat is not None else 0, stat_out=stat)
+                         stat_len=self.prefill_len if stat is not None else 0, stat_out=stat,
+                         stat_flags=compress.ROUND_FLAGS[self._round_dtype(query_states.dtype)])
         return o.view(B, 1, Hq * D)
 
     def _one_pass_check(self, dtype):
         """Whether a batched drift check can score in one pass over the pivot
-        keys from the decode-reported statistics: the uncast float32 chain,
-        a pooling width hc_score_given_stats takes and fewer than 32 query
-        rows per pivot."""
-        return (self.one_pass and self.batched_check and self._round_dtype(dtype) is None and self.kernel_size % 2 == 1
+        keys from the decode-reported statistics (of the cast chain when the
+        scores round): a pooling width hc_score_given_stats takes and fewer
+        than 32 query rows per pivot."""
+        return (self.one_pass and self.batched_check and self.kernel_size % 2 == 1
                 and self.kernel_size <= 9 and self.num_key_value_groups * self.decode_step < 32)
 
     def _step_stat_view(self, layer_idx, query_states):
@@ -1178,7 +1180,7 @@ class HeteroCache(DynamicCache):
                 scores = ops.score_given_stats(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0],
                                                self._tile_table, bm["k_row"], L, G, S, self.pooling,
                                                self.kernel_size, 1.0 / math.sqrt(self.head_dim), self._step_stats,
-                                               bm["st_off"], out=bm["scores"]).view(J, S, L)
+                                               bm["st_off"], out=bm["scores"], flags=flags).view(J, S, L)
                 hist = None  # the selection builds the first-digit histograms itself
             else:
                 scores = ops.score(qa, bm["q_off"], qa.stride(2), qa.stride(3), self._arena[0], None, 0, L, G, S, L,

@@ -145,6 +145,15 @@ __device__ __forceinline__ float vec8_at<float>(const Elem<float>::vec8& v, int 
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Rounding of the reference's casts to the model dtype, fixed per kernel
+// instance: 0 none, 1 bfloat16, 2 float16.
+template <int RM>
+__device__ __forceinline__ float round_fixed(float x) {
+  if constexpr (RM == 1) return (float)(__bf16)x;
+  if constexpr (RM == 2) return (float)(_Float16)x;
+  return x;
+}
+
 // Sum of a value over the 16 lanes of its row (lanes 16r .. 16r+15), in
 // every lane of the row: four DPP adds (rotate the row by 8 and by 4, then
 // swap within quads by 2 and by 1), full rate on the VALU, where a

@@ -152,12 +152,15 @@ __device__ __forceinline__ void load_tile(typename Elem<T>::vec8 (&kr)[8], typen
 // state: m_run is the running maximum of query n = lane%16 (scaled, base 2),
 // l_run this lane's share of the running sum, o[mt][j] = O^T[16mt+4g+j][n].
 // STATS: (m_snap, l_snap) also follow the state over the tokens below
-// stat_len only (see decode_partial_kernel).
-template <typename T, bool STATS>
+// stat_len only (see decode_partial_kernel).  RM (a rounding mode of
+// round_fixed, with STATS): that state is the one of the reference's cast
+// chain instead, x = round(round(q.k) * scale) * log2(e), which the
+// attention itself does not use.
+template <typename T, bool STATS, int RM = 0>
 __device__ __forceinline__ void attend_tile(typename Elem<T>::vec8 (&kr)[8], typename Elem<T>::vec8 (&vr)[8],
                                             const typename Elem<T>::vec8 (&qreg)[4], int t, int len, int lane,
                                             float scale_log2, float& m_run, float& l_run, f32x4 (&o)[8],
-                                            int stat_len, float& m_snap, float& l_snap) {
+                                            int stat_len, float& m_snap, float& l_snap, float scale = 0.f) {
   typedef typename Elem<T>::vec8 vec8;
   const int g = lane >> 4;
   const int tok0 = t * HC_TILE;
@@ -204,7 +207,29 @@ __device__ __forceinline__ void attend_tile(typename Elem<T>::vec8 (&kr)[8], typ
     p[e] = fast_exp2(fmaf(sv[e], scale_log2, -m_new));
     psum += p[e];
   }
-  if constexpr (STATS) {
+  if constexpr (STATS && RM != 0) {
+    // The cast chain's own online state over the tile's tokens below
+    // stat_len (masked tokens are -inf already, and stay so).
+    if (tok0 < stat_len) {
+      float xs[8];
+      float mxs = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int tok = tok0 + 16 * (e >> 2) + 4 * g + (e & 3);
+        xs[e] = tok < stat_len ? round_fixed<RM>(round_fixed<RM>(sv[e]) * scale) * 1.4426950408889634f : -INFINITY;
+        mxs = fmaxf(mxs, xs[e]);
+      }
+      mxs = rows4_max(mxs);
+      const float mn = fmaxf(m_snap, mxs);
+      if (mn != -INFINITY) {
+        float ps = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ps += fast_exp2(xs[e] - mn);
+        l_snap = fmaf(l_snap, fast_exp2(m_snap - mn), ps);
+        m_snap = mn;
+      }
+    }
+  } else if constexpr (STATS) {
     // Tiles are visited in increasing order, so while every tile so far lies
     // below stat_len the snapshot is the running state itself; the tile
     // that crosses stat_len adds only its tokens below it (against the new
@@ -234,9 +259,9 @@ __device__ __forceinline__ void attend_tile(typename Elem<T>::vec8 (&kr)[8], typ
 // Fold the appended token (k_new, v_new of this row) into the lane state of
 // attend_tile.  The score is a VALU dot product of the operand registers
 // (exact bf16/f16 products, fp32 sums), reduced over the four k-groups; P is
-// rounded to T as on the matrix-core path.
+// rounded to T as on the matrix-core path.  Returns the score's dot product.
 template <typename T>
-__device__ __forceinline__ void attend_new_token(const typename Elem<T>::vec8 (&qreg)[4], const T* __restrict__ kn,
+__device__ __forceinline__ float attend_new_token(const typename Elem<T>::vec8 (&qreg)[4], const T* __restrict__ kn,
                                                  const T* __restrict__ vn, int lane, float scale_log2, float& m_run,
                                                  float& l_run, f32x4 (&o)[8]) {
   const int g = lane >> 4;
@@ -258,6 +283,7 @@ __device__ __forceinline__ void attend_new_token(const typename Elem<T>::vec8 (&
   for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
     for (int j = 0; j < 4; ++j) o[mt][j] = fmaf(p, Elem<T>::to_f32(vn[16 * mt + 4 * g + j]), o[mt][j] * alpha);
+  return dot;
 }
 
 // Stream tiles [t_begin, t_end) of a row through attend_tile (SNAP: with the
@@ -267,12 +293,12 @@ __device__ __forceinline__ void attend_new_token(const typename Elem<T>::vec8 (&
 // unconditional, so every wait leaves the younger tile outstanding.
 // Scheduling barriers keep each request between the two consumers (hoisting
 // both requests would hold three tiles and spill).
-template <typename T, bool SNAP>
+template <typename T, bool SNAP, int RM = 0>
 __device__ __forceinline__ void stream_tiles(const T* __restrict__ kstore, const T* __restrict__ vstore,
                                              int64_t row_base, int lane, int t_begin, int t_end,
                                              const typename Elem<T>::vec8 (&qreg)[4], int len_st, float scale_log2,
                                              float& m_run, float& l_run, f32x4 (&o)[8], int stat_len, float& m_snap,
-                                             float& l_snap) {
+                                             float& l_snap, float scale) {
   typedef typename Elem<T>::vec8 vec8;
   const T* kb = kstore + row_base + lane * 8;
   const T* vb = vstore + row_base + lane * 8;
@@ -282,19 +308,19 @@ __device__ __forceinline__ void stream_tiles(const T* __restrict__ kstore, const
   for (; t + 2 < t_end; t += 2) {
     load_tile<T>(kB, vB, kb, vb, t + 1);
     __builtin_amdgcn_sched_barrier(0);
-    attend_tile<T, SNAP>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+    attend_tile<T, SNAP, RM>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap, scale);
     __builtin_amdgcn_sched_barrier(0);
     load_tile<T>(kA, vA, kb, vb, t + 2);
     __builtin_amdgcn_sched_barrier(0);
-    attend_tile<T, SNAP>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+    attend_tile<T, SNAP, RM>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap, scale);
     __builtin_amdgcn_sched_barrier(0);
   }
   if (t + 1 < t_end) {
     load_tile<T>(kB, vB, kb, vb, t + 1);
-    attend_tile<T, SNAP>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
-    attend_tile<T, SNAP>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+    attend_tile<T, SNAP, RM>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap, scale);
+    attend_tile<T, SNAP, RM>(kB, vB, qreg, t + 1, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap, scale);
   } else {
-    attend_tile<T, SNAP>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap);
+    attend_tile<T, SNAP, RM>(kA, vA, qreg, t, len_st, lane, scale_log2, m_run, l_run, o, stat_len, m_snap, l_snap, scale);
   }
 }
 
@@ -303,14 +329,15 @@ constexpr int kOPitch = HC_HEAD_DIM + 4;
 // STATS: besides its (m, l, O) partial, each workgroup writes part_st, the
 // (max, sum) of its queries' scaled base-2 scores over the attended tokens
 // below stat_len, which the merge folds into the row's softmax statistics
-// over its first stat_len tokens.
-template <typename T, int NWAVES, bool STATS>
+// over its first stat_len tokens (RM != 0: of the cast chain's logits,
+// see attend_tile).
+template <typename T, int NWAVES, bool STATS, int RM = 0>
 __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_partial_kernel(
     const T* __restrict__ q, T* __restrict__ kstore, T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off,
     const int* __restrict__ row_len, const int* __restrict__ row_cap, const int* __restrict__ row_order, int rows,
     int G, float scale_log2, int chunk_tiles, const T* __restrict__ k_new, const T* __restrict__ v_new,
     float* __restrict__ part_o, float* __restrict__ part_ml, int* __restrict__ row_info, int* __restrict__ status,
-    int stat_len, float* __restrict__ part_st) {
+    int stat_len, float* __restrict__ part_st, float scale) {
   typedef typename Elem<T>::vec8 vec8;
   constexpr int NT = NWAVES * 64;
   const bool fused_append = (k_new != nullptr);
@@ -387,16 +414,18 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
     if (t_begin < t_end_st) {
       // Only the wave whose tiles straddle stat_len follows the snapshot
       // tile by tile; a wave wholly below it takes its final state, one
-      // wholly above leaves the snapshot empty.
+      // wholly above leaves the snapshot empty.  The cast chain's state is
+      // its own: every wave with tiles below stat_len follows it.
       if constexpr (STATS) {
-        const bool cross = t_begin * HC_TILE < stat_len && t_end_st * HC_TILE > stat_len;
+        const bool cross = RM != 0 ? t_begin * HC_TILE < stat_len
+                                   : t_begin * HC_TILE < stat_len && t_end_st * HC_TILE > stat_len;
         if (cross)
-          stream_tiles<T, true>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2, m_run,
-                                l_run, o, stat_len, m_snap, l_snap);
+          stream_tiles<T, true, RM>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2,
+                                    m_run, l_run, o, stat_len, m_snap, l_snap, scale);
         else
-          stream_tiles<T, false>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2, m_run,
-                                 l_run, o, stat_len, m_snap, l_snap);
-        if (t_end_st * HC_TILE <= stat_len) {
+          stream_tiles<T, false, RM>(kstore, vstore, row_base, lane, t_begin, t_end_st, qreg, len_st, scale_log2,
+                                     m_run, l_run, o, stat_len, m_snap, l_snap, scale);
+        if (RM == 0 && t_end_st * HC_TILE <= stat_len) {
           m_snap = m_run;
           l_snap = l_run;
         }
@@ -434,10 +463,17 @@ __global__ __launch_bounds__(NWAVES * 64, sizeof(T) == 4 ? 1 : 2) void decode_pa
     // The wave whose tile range holds the new slot attends the new token and
     // stores it (no other workgroup of this launch reads that slot).
     if (fused_append && new_pos >= t_begin * HC_TILE && new_pos < t_end * HC_TILE) {
-      attend_new_token<T>(qreg, kn, vn, lane, scale_log2, m_run, l_run, o);
+      const float dot = attend_new_token<T>(qreg, kn, vn, lane, scale_log2, m_run, l_run, o);
       if (STATS && new_pos < stat_len) {  // every earlier token lies below it too
-        m_snap = m_run;
-        l_snap = l_run;
+        if constexpr (RM == 0) {
+          m_snap = m_run;
+          l_snap = l_run;
+        } else {
+          const float x = round_fixed<RM>(round_fixed<RM>(dot) * scale) * 1.4426950408889634f;
+          const float mn = fmaxf(m_snap, x);
+          l_snap = fmaf(l_snap, fast_exp2(m_snap - mn), g == 0 ? fast_exp2(x - mn) : 0.f);
+          m_snap = mn;
+        }
       }
       const int64_t tb = row_base + (int64_t)(new_pos / HC_TILE) * HC_TILE_ELEMS;
       const int tn = new_pos % HC_TILE;
@@ -677,6 +713,7 @@ size_t decode_workspace_bytes_rows(int rows, int group, int64_t num_parts) {
 // Softmax statistics requested of a decode launch (hc_decode_attn_stats).
 struct DecodeStats {
   int len = 0;  // 0: none
+  int rm = 0;   // rounding mode of the cast chain the statistics follow (0: none)
   float* out = nullptr;
   int64_t row_stride = 0, head_stride = 0;
 };
@@ -701,10 +738,13 @@ static int launch_decode(const void* q, void* kstore, void* vstore, const int64_
   const size_t lds_o = (size_t)kDecodeWaves * G * kOPitch * sizeof(float);
   const dim3 mgrid(rows, G, HC_HEAD_DIM / kMergeSlice), mblock(kMergeSlice * kMergeGroups);
   if (st.len > 0) {
-    hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves, true>), dim3((unsigned)grid_parts),
-                       dim3(kDecodeWaves * 64), lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off,
-                       row_len, row_cap, row_order, rows, G, scale_log2, chunk_tiles, (const T*)k_new,
-                       (const T*)v_new, part_o, part_ml, row_info, status, st.len, part_st);
+    auto fn = st.rm == 1   ? decode_partial_kernel<T, kDecodeWaves, true, 1>
+              : st.rm == 2 ? decode_partial_kernel<T, kDecodeWaves, true, 2>
+                           : decode_partial_kernel<T, kDecodeWaves, true, 0>;
+    hipLaunchKernelGGL(fn, dim3((unsigned)grid_parts), dim3(kDecodeWaves * 64), lds_o, stream, (const T*)q,
+                       (T*)kstore, (T*)vstore, row_tile_off, row_len, row_cap, row_order, rows, G, scale_log2,
+                       chunk_tiles, (const T*)k_new, (const T*)v_new, part_o, part_ml, row_info, status, st.len,
+                       part_st, scale);
     int rc = check_launch("hc_decode_attn(partial)");
     if (rc) return rc;
     hipLaunchKernelGGL((decode_merge_kernel<T, true>), dim3(rows, G, HC_HEAD_DIM / kMergeSlice + 1), mblock, 0,
@@ -716,7 +756,7 @@ static int launch_decode(const void* q, void* kstore, void* vstore, const int64_
   hipLaunchKernelGGL((decode_partial_kernel<T, kDecodeWaves, false>), dim3((unsigned)grid_parts),
                      dim3(kDecodeWaves * 64), lds_o, stream, (const T*)q, (T*)kstore, (T*)vstore, row_tile_off,
                      row_len, row_cap, row_order, rows, G, scale_log2, chunk_tiles, (const T*)k_new, (const T*)v_new,
-                     part_o, part_ml, row_info, status, 0, nullptr);
+                     part_o, part_ml, row_info, status, 0, nullptr, scale);
   int rc = check_launch("hc_decode_attn(partial)");
   if (rc) return rc;
   hipLaunchKernelGGL((decode_merge_kernel<T, false>), mgrid, mblock, 0, stream, part_o, part_ml, row_info, G,
@@ -850,13 +890,17 @@ extern "C" int hc_decode_attn_stats(int dtype, const void* q, void* kstore, void
                                     int group, float scale, const void* k_new, const void* v_new, void* out,
                                     void* workspace, size_t workspace_bytes, int64_t num_parts, int chunk_tiles,
                                     int32_t* status, int stat_len, float* stat_out, int64_t stat_row_stride,
-                                    int64_t stat_head_stride, void* stream) {
+                                    int64_t stat_head_stride, int stat_flags, void* stream) {
   clear_error();
   if (stat_len < 1 || !stat_out || stat_row_stride < 0 || stat_head_stride < 0)
     return set_error(HC_ERR_INVALID, "hc_decode_attn_stats: stat_len=%d, stat_out %s", stat_len,
                      stat_out ? "given" : "null");
+  if (stat_flags != 0 && stat_flags != HC_SCORE_ROUND_BF16 && stat_flags != HC_SCORE_ROUND_F16)
+    return set_error(HC_ERR_INVALID, "hc_decode_attn_stats: stat_flags=%d (0, HC_SCORE_ROUND_BF16 or _F16)",
+                     stat_flags);
   DecodeStats st;
   st.len = stat_len;
+  st.rm = stat_flags == HC_SCORE_ROUND_BF16 ? 1 : stat_flags == HC_SCORE_ROUND_F16 ? 2 : 0;
   st.out = stat_out;
   st.row_stride = stat_row_stride;
   st.head_stride = stat_head_stride;

@@ -66,14 +66,6 @@ struct ScoreArgs {
   float scale2;  // scale * log2(e): base-2 logits without the reference's casts
 };
 
-// Rounding of the reference's casts, fixed per kernel instance: 0 none,
-// 1 bfloat16, 2 float16.
-template <int RM>
-__device__ __forceinline__ float round_fixed(float x) {
-  if constexpr (RM == 1) return (float)(__bf16)x;
-  if constexpr (RM == 2) return (float)(_Float16)x;
-  return x;
-}
 
 __device__ __forceinline__ float round_mode(float x, int flags) {
   if (flags & HC_SCORE_ROUND_BF16) return (float)(__bf16)x;
@@ -1264,10 +1256,14 @@ struct GsView {
 // Probabilities of the 16-token sub-tiles tw + 16u (u < NU) of every row,
 // written to dst + r * pitch + (token - base); positions outside [0, span)
 // get the pooling pad.  Per row tile the NU sub-tiles' MFMA chains are
-// issued before any exponential.
-template <typename T, int POOL, int NU>
+// issued before any exponential.  RM == 0: p = exp2(s - s_mz[r]) with s_mz
+// = M + log2 L; otherwise the cast chain of the probability pass,
+// p = round(exp2(x - M) * (1 / L)) of the rounded logit x, with s_mz = M
+// and s_iz = 1 / L.
+template <typename T, int POOL, int NU, int RM>
 __device__ __forceinline__ void gs_subtiles(const ScoreArgs& a, const typename Elem<T>::vec8 (*kr)[4], const T* s_q,
-                                            const float* s_mz, float* dst, int pitch, int base, int tw, int lane) {
+                                            const float* s_mz, const float* s_iz, float* dst, int pitch, int base,
+                                            int tw, int lane) {
   constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
   const bool mask = tw + 16 * NU - 1 >= a.L;
   for (int nt = 0; nt < a.NT; ++nt) {
@@ -1276,12 +1272,13 @@ __device__ __forceinline__ void gs_subtiles(const ScoreArgs& a, const typename E
 #pragma unroll
     for (int u = 0; u < NU; ++u) {
       if (mask)
-        subtile_logits<T, 0, true, true>(a, kr[u], s_q, nt, tw + 16 * u, lane, a.L - 1, x[u]);
+        subtile_logits<T, RM, true, RM == 0>(a, kr[u], s_q, nt, tw + 16 * u, lane, a.L - 1, x[u]);
       else
-        subtile_logits<T, 0, false, true>(a, kr[u], s_q, nt, tw + 16 * u, lane, a.L - 1, x[u]);
+        subtile_logits<T, RM, false, RM == 0>(a, kr[u], s_q, nt, tw + 16 * u, lane, a.L - 1, x[u]);
     }
     if (r < a.R) {
       const float mz = s_mz[r];
+      const float iz = RM == 0 ? 0.f : s_iz[r];
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
         const int tb = tw + 16 * u + 4 * (lane >> 4);
@@ -1289,7 +1286,12 @@ __device__ __forceinline__ void gs_subtiles(const ScoreArgs& a, const typename E
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int t = tb + j;
-          v[j] = (t >= 0 && t < a.span) ? fast_exp2(fmaf(x[u][j], a.scale2, -mz)) : pad;
+          float p;
+          if constexpr (RM == 0)
+            p = fast_exp2(fmaf(x[u][j], a.scale2, -mz));
+          else
+            p = x[u][j] == -INFINITY ? 0.f : round_fixed<RM>(fast_exp2(x[u][j] - mz) * iz);
+          v[j] = (t >= 0 && t < a.span) ? p : pad;
         }
         *reinterpret_cast<f32x4*>(dst + r * pitch + (tb - base)) = v;
       }
@@ -1300,8 +1302,9 @@ __device__ __forceinline__ void gs_subtiles(const ScoreArgs& a, const typename E
 // Pool chunk positions cb + [i0, i0 + n) (i0, n multiples of 4), take the
 // group max and write the scores: task = (output row w', four consecutive
 // positions), reading its 4 + 2P window values per query head as three
-// 16-byte LDS reads.
-template <int POOL, int P>
+// 16-byte LDS reads.  RM: the pooled value is rounded before the group max,
+// as in the cast chain.
+template <int POOL, int P, int RM>
 __device__ __forceinline__ void gs_pool(const ScoreArgs& a, const GsView& v, int cb, int i0, int n, int job,
                                         float* __restrict__ S) {
   static_assert(P <= 4, "window registers hold 4 values on either side");
@@ -1324,7 +1327,7 @@ __device__ __forceinline__ void gs_pool(const ScoreArgs& a, const GsView& v, int
 #pragma unroll
         for (int d = -P; d <= P; ++d) x = POOL == 0 ? x + win[4 + e + d] : fmaxf(x, win[4 + e + d]);
         if constexpr (POOL == 0) x *= inv_k;
-        best[e] = fmaxf(best[e], x);
+        best[e] = fmaxf(best[e], round_fixed<RM>(x));
       }
     }
     const int t = cb + i;
@@ -1339,7 +1342,7 @@ __device__ __forceinline__ void gs_pool(const ScoreArgs& a, const GsView& v, int
   }
 }
 
-template <typename T, bool STORE, int POOL, int P>
+template <typename T, bool STORE, int POOL, int P, int RM>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(ScoreArgs a,
                                                                             const float* __restrict__ stats,
                                                                             const int64_t* __restrict__ st_off,
@@ -1349,6 +1352,7 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   float* strip = reinterpret_cast<float*>(smem + (size_t)a.NT * 16 * kQPitch * sizeof(T));  // [R][kGsPitch]
   float* mrg[2] = {strip + a.R * kGsPitch, strip + a.R * kGsPitch + a.R * kGsMPitch};        // [R][kGsMPitch]
   __shared__ float s_mz[kLogitRowsMax];
+  __shared__ float s_iz[RM == 0 ? 1 : kLogitRowsMax];
   constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
   typedef typename Elem<T>::vec8 vec8;
   const int job = blockIdx.y;
@@ -1364,7 +1368,12 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   for (int r = threadIdx.x; r < a.R; r += kScoreWaves * 64) {
     const float* st = stats + st_off[job] + 2 * r;
     // p = exp2(s - (M + log2 L)); a row without keys (L = 0) gives p = 0.
-    s_mz[r] = st[1] > 0.f ? st[0] + __log2f(st[1]) : INFINITY;
+    if constexpr (RM == 0) {
+      s_mz[r] = st[1] > 0.f ? st[0] + __log2f(st[1]) : INFINITY;
+    } else {
+      s_mz[r] = st[1] > 0.f ? st[0] : INFINITY;
+      s_iz[r] = st[1] > 0.f ? 1.f / st[1] : 0.f;
+    }
   }
   __syncthreads();
   // The run's left margin: positions c0*256 - 16 .. - 1 (margin entries
@@ -1372,14 +1381,14 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   if (wave == 1) {
     const int cb0 = c0 * kScoreChunk;
     if (c0 > 0) {
-      gs_subtiles<T, POOL, 1>(a, kh, s_q, s_mz, mrg[1], kGsMPitch, cb0 - kGsMargin, cb0 - 16, lane);
+      gs_subtiles<T, POOL, 1, RM>(a, kh, s_q, s_mz, s_iz, mrg[1], kGsMPitch, cb0 - kGsMargin, cb0 - 16, lane);
     } else {
       for (int i = lane; i < a.R * 16; i += 64) mrg[1][(i / 16) * kGsMPitch + 16 + i % 16] = pad;
     }
   }
   for (int c = c0; c < c1; ++c) {
     const int cb = c * kScoreChunk;
-    gs_subtiles<T, POOL, kSubTiles>(a, ka.v, s_q, s_mz, strip, kGsPitch, cb, cb + woff, lane);
+    gs_subtiles<T, POOL, kSubTiles, RM>(a, ka.v, s_q, s_mz, s_iz, strip, kGsPitch, cb, cb + woff, lane);
     __syncthreads();  // strip written (and the margin of the previous chunk)
     // Next chunk's keys in flight while this one pools.
     if (c + 1 < c1) load_k_chunk<T, STORE>(a, job, cb + kScoreChunk + woff, lane, ka);
@@ -1387,9 +1396,9 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
     GsView v{strip, mrg[mb]};
     // Positions [cb - 16, cb + 240) (the run's first chunk: from cb).
     if (c == c0)
-      gs_pool<POOL, P>(a, v, cb, 0, kScoreChunk - 16, job, S);
+      gs_pool<POOL, P, RM>(a, v, cb, 0, kScoreChunk - 16, job, S);
     else
-      gs_pool<POOL, P>(a, v, cb, -16, kScoreChunk, job, S);
+      gs_pool<POOL, P, RM>(a, v, cb, -16, kScoreChunk, job, S);
     // This chunk's last 32 positions are the next chunk's margin.
     float* nm = mrg[mb ^ 1];
     for (int i = threadIdx.x; i < a.R * kGsMargin; i += kScoreWaves * 64) {
@@ -1403,11 +1412,11 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   if (wave == 0) {
     const int tr = c1 * kScoreChunk;
     load_k_subtile<T, STORE>(a, job, tr, lane, kh[0]);
-    gs_subtiles<T, POOL, 1>(a, kh, s_q, s_mz, strip, kGsPitch, tr - kScoreChunk, tr, lane);
+    gs_subtiles<T, POOL, 1, RM>(a, kh, s_q, s_mz, s_iz, strip, kGsPitch, tr - kScoreChunk, tr, lane);
   }
   __syncthreads();
   const int mb = (c1 - c0) & 1;
-  gs_pool<POOL, P>(a, GsView{strip, mrg[mb]}, (c1 - 1) * kScoreChunk, kScoreChunk - 16, 16, job, S);
+  gs_pool<POOL, P, RM>(a, GsView{strip, mrg[mb]}, (c1 - 1) * kScoreChunk, kScoreChunk - 16, 16, job, S);
 }
 
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }
@@ -1877,37 +1886,46 @@ extern "C" int hc_score(int dtype, const void* q, const int64_t* q_off, int64_t 
 #undef HC_SCORE_DISPATCH
 }
 
-template <typename T, int POOL, int P>
+template <typename T, int POOL, int P, int RM>
 static int launch_given_stats(ScoreArgs a, int njobs, const float* stats, const int64_t* st_off, float* scores,
                               hipStream_t s) {
   const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
   const size_t lds =
       (size_t)a.NT * 16 * kQPitch * sizeof(T) + (size_t)a.R * (kGsPitch + 2 * kGsMPitch) * sizeof(float);
-  auto fn = score_given_stats_kernel<T, true, POOL, P>;
+  auto fn = score_given_stats_kernel<T, true, POOL, P, RM>;
   const int gx = plan_chunks(reinterpret_cast<const void*>(fn), lds, njobs, nchunks, a);
   hipLaunchKernelGGL(fn, dim3(gx, njobs), dim3(kScoreWaves * 64), lds, s, a, stats, st_off, scores);
   return check_launch("hc_score_given_stats");
 }
 
-template <typename T>
+template <typename T, int RM>
 static int dispatch_given_stats(const ScoreArgs& a, int njobs, int pooling, int kernel, const float* stats,
                                 const int64_t* st_off, float* scores, hipStream_t s) {
 #define HC_GS(PL)                                                                              \
   switch (kernel / 2) {                                                                        \
-    case 0: return launch_given_stats<T, PL, 0>(a, njobs, stats, st_off, scores, s);     \
-    case 1: return launch_given_stats<T, PL, 1>(a, njobs, stats, st_off, scores, s);     \
-    case 2: return launch_given_stats<T, PL, 2>(a, njobs, stats, st_off, scores, s);     \
-    case 3: return launch_given_stats<T, PL, 3>(a, njobs, stats, st_off, scores, s);     \
-    default: return launch_given_stats<T, PL, 4>(a, njobs, stats, st_off, scores, s);    \
+    case 0: return launch_given_stats<T, PL, 0, RM>(a, njobs, stats, st_off, scores, s);  \
+    case 1: return launch_given_stats<T, PL, 1, RM>(a, njobs, stats, st_off, scores, s);  \
+    case 2: return launch_given_stats<T, PL, 2, RM>(a, njobs, stats, st_off, scores, s);  \
+    case 3: return launch_given_stats<T, PL, 3, RM>(a, njobs, stats, st_off, scores, s);  \
+    default: return launch_given_stats<T, PL, 4, RM>(a, njobs, stats, st_off, scores, s); \
   }
   if (pooling == 0) { HC_GS(0) } else { HC_GS(1) }
 #undef HC_GS
 }
 
+// Rounding mode of the flags' cast chain (0: the uncast chain).
+template <typename T>
+static int dispatch_given_stats_flags(const ScoreArgs& a, int njobs, int pooling, int kernel, int flags,
+                                      const float* stats, const int64_t* st_off, float* scores, hipStream_t s) {
+  if (flags == HC_SCORE_ROUND_BF16) return dispatch_given_stats<T, 1>(a, njobs, pooling, kernel, stats, st_off, scores, s);
+  if (flags == HC_SCORE_ROUND_F16) return dispatch_given_stats<T, 2>(a, njobs, pooling, kernel, stats, st_off, scores, s);
+  return dispatch_given_stats<T, 0>(a, njobs, pooling, kernel, stats, st_off, scores, s);
+}
+
 extern "C" int hc_score_given_stats(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride,
                                     int64_t q_row_stride, const void* kstore, const int64_t* row_tile_off,
-                                    const int32_t* k_row, int njobs, int seq_len, int group, int window, int pooling,
-                                    int kernel, float scale, const float* stats, const int64_t* stat_off,
+                                    const int32_t* k_row, int njobs, int seq_len, int group, int window, int flags,
+                                    int pooling, int kernel, float scale, const float* stats, const int64_t* stat_off,
                                     float* scores, void* stream) {
   clear_error();
   if (njobs < 0 || njobs > 65535 || seq_len < 0 || group < 1 || window < 1)
@@ -1919,6 +1937,8 @@ extern "C" int hc_score_given_stats(int dtype, const void* q, const int64_t* q_o
     return set_error(HC_ERR_INVALID, "hc_score_given_stats: group*window = %d, at most %d rows", R, kLogitRowsMax - 1);
   if (pooling != 0 && pooling != 1)
     return set_error(HC_ERR_INVALID, "hc_score_given_stats: pooling must be 0 (avg) or 1 (max)");
+  if (flags != 0 && flags != HC_SCORE_ROUND_BF16 && flags != HC_SCORE_ROUND_F16)
+    return set_error(HC_ERR_INVALID, "hc_score_given_stats: flags=%d (0, HC_SCORE_ROUND_BF16 or _F16)", flags);
   if (kernel < 1 || (kernel % 2) == 0 || kernel / 2 > 4)
     return set_error(HC_ERR_INVALID, "hc_score_given_stats: pooling kernel must be 1, 3, 5, 7 or 9 (got %d)", kernel);
   if (!q || !q_off || !kstore || !row_tile_off || !k_row || !stats || !stat_off || !scores)
@@ -1945,9 +1965,12 @@ extern "C" int hc_score_given_stats(int dtype, const void* q, const int64_t* q_o
   a.cpw = 1;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case HC_DTYPE_BF16: return dispatch_given_stats<__bf16>(a, njobs, pooling, kernel, stats, stat_off, scores, s);
-    case HC_DTYPE_F16: return dispatch_given_stats<_Float16>(a, njobs, pooling, kernel, stats, stat_off, scores, s);
-    case HC_DTYPE_F32: return dispatch_given_stats<float>(a, njobs, pooling, kernel, stats, stat_off, scores, s);
+    case HC_DTYPE_BF16:
+      return dispatch_given_stats_flags<__bf16>(a, njobs, pooling, kernel, flags, stats, stat_off, scores, s);
+    case HC_DTYPE_F16:
+      return dispatch_given_stats_flags<_Float16>(a, njobs, pooling, kernel, flags, stats, stat_off, scores, s);
+    case HC_DTYPE_F32:
+      return dispatch_given_stats_flags<float>(a, njobs, pooling, kernel, flags, stats, stat_off, scores, s);
     default: return set_error(HC_ERR_INVALID, "hc_score_given_stats: unknown dtype %d", dtype);
   }
 }

@@ -116,7 +116,7 @@ def decode_chunk_tiles(host_row_len, group, dtype):
 
 def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, out=None, row_order=None,
                 k_new=None, v_new=None, chunk_tiles=None, stream=None, workspace=None, num_parts=None,
-                row_cap=None, status=None, stat_len=0, stat_out=None):
+                row_cap=None, status=None, stat_len=0, stat_out=None, stat_flags=0):
     """out[r, g] = softmax(scale * q[r, g] . K_r^T) V_r over row_len[r] tokens.
 
     q: [rows, G, 128]; host_row_len: host copy of the lengths (sizes the grid).
@@ -133,7 +133,8 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
     stat_len > 0 with stat_out (float32 [rows, G, 2] view, any strides with
     a unit last-dim stride): each row's softmax statistics (base-2 max bound,
     sum of exp2 against it) over its first stat_len tokens
-    (hc_decode_attn_stats).
+    (hc_decode_attn_stats); stat_flags HC_SCORE_ROUND_BF16 / _F16: of the
+    reference's cast chain of the logits instead.
     """
     lib = _lib.load()
     _require_cuda(q, kstore, vstore, row_tile_off, row_len, row_order, k_new, v_new)
@@ -187,7 +188,7 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
             dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off), _ptr(row_len),
             _ptr(row_cap), _ptr(row_order), rows, G, float(scale), _ptr(k_new), _ptr(v_new), _ptr(out), _ptr(ws),
             ws.numel(), nparts, int(chunk_tiles), st_ptr, int(stat_len), _ptr(stat_out), stat_out.stride(0),
-            stat_out.stride(1), _stream(stream, q)))
+            stat_out.stride(1), int(stat_flags), _stream(stream, q)))
         return out
     _lib.check(lib.hc_decode_attn(dtype_code(q.dtype), _ptr(q), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off),
                                   _ptr(row_len), _ptr(row_cap), _ptr(row_order), rows, G, float(scale), _ptr(k_new),
@@ -557,10 +558,12 @@ def score_with_stats(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stri
 
 
 def score_given_stats(q, q_off, q_head_stride, q_row_stride, kstore, row_tile_off, k_row, seq_len, group, window,
-                      pooling, kernel, scale, stats, stat_off, out=None, stream=None):
+                      pooling, kernel, scale, stats, stat_off, out=None, stream=None, flags=0):
     """Pivot drift scores [jobs, window, seq_len] in one pass over the keys of
     store rows k_row, given each query row's softmax statistics (M, L) at
-    stats[stat_off[j] + 2r] (hc_score_given_stats in include/hc.h)."""
+    stats[stat_off[j] + 2r] (hc_score_given_stats in include/hc.h); flags
+    HC_SCORE_ROUND_BF16 / _F16 apply the reference's cast chain, with
+    statistics of that chain (decode_attn's stat_flags)."""
     lib = _lib.load()
     _require_cuda(q, kstore, q_off, row_tile_off, k_row, stats, stat_off)
     if q.dtype != kstore.dtype:
@@ -577,7 +580,8 @@ def score_given_stats(q, q_off, q_head_stride, q_row_stride, kstore, row_tile_of
     pool = {"avgpool": 0, "maxpool": 1}[pooling] if isinstance(pooling, str) else int(pooling)
     _lib.check(lib.hc_score_given_stats(dtype_code(q.dtype), _ptr(q), _ptr(q_off), int(q_head_stride),
                                         int(q_row_stride), _ptr(kstore), _ptr(row_tile_off), _ptr(k_row), njobs,
-                                        int(seq_len), int(group), int(window), pool, int(kernel), float(scale),
+                                        int(seq_len), int(group), int(window), int(flags), pool, int(kernel),
+                                        float(scale),
                                         _ptr(stats), _ptr(stat_off), _ptr(out), _stream(stream, q)))
     return out
 

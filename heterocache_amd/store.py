@@ -251,7 +251,7 @@ class KVStore:
         return ops.store_read(self.k, self.v, self.row_tile_off, rows, count)
 
     def attend(self, q, scale, out=None, k_new=None, v_new=None, chunk_tiles=None,
-               stream=None, num_parts=None, workspace=None, stat_len=0, stat_out=None):
+               stream=None, num_parts=None, workspace=None, stat_len=0, stat_out=None, stat_flags=0):
         """Decode attention of q [rows, G, 128] over every row's tokens.
 
         With k_new / v_new [rows, 128] the decode append happens in the same
@@ -260,15 +260,15 @@ class KVStore:
         (a fixed chunk_tiles, a num_parts covering the longest lengths to
         come and an explicit workspace make the call capturable in a HIP
         graph; a replay advances the device lengths, not this object's host
-        mirror).  stat_len / stat_out: softmax statistics of every row's first
-        stat_len tokens (ops.decode_attn).
+        mirror).  stat_len / stat_out / stat_flags: softmax statistics of
+        every row's first stat_len tokens (ops.decode_attn).
         """
         if k_new is not None:
             self._check_room()
         out = ops.decode_attn(q, self.k, self.v, self.row_tile_off, self.row_len, self.host_len, scale, out=out,
                               row_order=self.row_order, k_new=k_new, v_new=v_new, chunk_tiles=chunk_tiles,
                               stream=stream, workspace=workspace, num_parts=num_parts, row_cap=self.row_cap,
-                              status=self.status, stat_len=stat_len, stat_out=stat_out)
+                              status=self.status, stat_len=stat_len, stat_out=stat_out, stat_flags=stat_flags)
         if k_new is not None:
             self.host_len += 1
             self._headroom -= 1

@@ -94,7 +94,10 @@ int hc_decode_attn(int dtype, const void* q, void* kstore, void* vstore, const i
 /*
  * hc_decode_attn that also reports, for every row r and query head g, the
  * softmax statistics of the row's first stat_len attended tokens: with
- * s_t = scale * log2(e) * q[r, g, :] . k_t (base-2 scores),
+ * s_t = scale * log2(e) * q[r, g, :] . k_t (base-2 scores; with stat_flags
+ * HC_SCORE_ROUND_BF16 / HC_SCORE_ROUND_F16 the reference's cast chain
+ * s_t = round(round(q . k_t) * scale) * log2(e), rounding to that type, as
+ * hc_score's flags do -- the attention output itself never rounds),
  *   stat_out[r * stat_row_stride + g * stat_head_stride + 0] = M (a bound of
  *     max_t s_t over t < stat_len; -inf when no token lies below stat_len),
  *   stat_out[... + 1] = sum over t < stat_len of exp2(s_t - M),
@@ -110,7 +113,8 @@ int hc_decode_attn_stats(int dtype, const void* q, void* kstore, void* vstore, c
                          int32_t* row_len, const int32_t* row_cap, const int32_t* row_order, int rows, int group,
                          float scale, const void* k_new, const void* v_new, void* out, void* workspace,
                          size_t workspace_bytes, int64_t num_parts, int chunk_tiles, int32_t* status, int stat_len,
-                         float* stat_out, int64_t stat_row_stride, int64_t stat_head_stride, void* stream);
+                         float* stat_out, int64_t stat_row_stride, int64_t stat_head_stride, int stat_flags,
+                         void* stream);
 /*
  * hc_decode_attn without a caller workspace, for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that
@@ -369,24 +373,28 @@ int hc_score_with_stats(int dtype, const void* q, const int64_t* q_off, int64_t 
 
 /*
  * hc_score's pivot drift scoring in one pass over the keys, given every query
- * row's softmax statistics (heterocache/cache_utils.py:1030-1057, the
- * uncast float32 form): for job j, query row r = g*window + w (query
- * q + q_off[j] + g*q_head_stride + w*q_row_stride) and key t < seq_len of
- * store row k_row[j] (read in place through row_tile_off),
+ * row's softmax statistics (heterocache/cache_utils.py:1030-1057): for job j,
+ * query row r = g*window + w (query q + q_off[j] + g*q_head_stride +
+ * w*q_row_stride) and key t < seq_len of store row k_row[j] (read in place
+ * through row_tile_off),
  *   p[r][t] = exp2(s - (M + log2 L)),  s = scale * log2(e) * q . k_t,
  *   (M, L) = stats[stat_off[j] + 2r], stats[stat_off[j] + 2r + 1]
  * (as hc_decode_attn_stats reports them; L = 0 gives p = 0), and
  *   scores[j][w][t] = max_g pool(p[g*window + w])[t]
  * with avg (pooling 0, zero padding, divided by kernel) or max (pooling 1)
- * pooling of width kernel in {1, 3, 5, 7, 9}; group*window < 32.  No
- * statistics pass and no stored logits: the keys are read once.  No
- * workspace; scores is [njobs][window][seq_len] float32 (hc_drift_select
- * builds the score histograms itself when given none).
+ * pooling of width kernel in {1, 3, 5, 7, 9}; group*window < 32.  flags
+ * HC_SCORE_ROUND_BF16 / HC_SCORE_ROUND_F16 (or 0): hc_score's cast chain,
+ * s = round(round(q . k_t) * scale) * log2(e), p = round(exp2(s - M) / L),
+ * the pooled value rounded before the max, with (M, L) of that chain
+ * (hc_decode_attn_stats under the same flag).  No statistics pass and no
+ * stored logits: the keys are read once.  No workspace; scores is
+ * [njobs][window][seq_len] float32 (hc_drift_select builds the score
+ * histograms itself when given none).
  */
 int hc_score_given_stats(int dtype, const void* q, const int64_t* q_off, int64_t q_head_stride,
                          int64_t q_row_stride, const void* kstore, const int64_t* row_tile_off, const int32_t* k_row,
-                         int njobs, int seq_len, int group, int window, int pooling, int kernel, float scale,
-                         const float* stats, const int64_t* stat_off, float* scores, void* stream);
+                         int njobs, int seq_len, int group, int window, int flags, int pooling, int kernel,
+                         float scale, const float* stats, const int64_t* stat_off, float* scores, void* stream);
 
 /*
  * CAKE layer scoring, CAKECluster.update_kv (heterocache/kv_cluster.py:284-315).

@@ -614,7 +614,7 @@ def decode_attention(q, ks, vs, scale=None):
     return out
 
 
-def softmax_lse2(q, ks, stat_len, scale=None):
+def softmax_lse2(q, ks, stat_len, scale=None, io_dtype=None):
     """Base-2 log-normaliser of every (row, query head) softmax over the
     row's first stat_len keys, float64.
 
@@ -622,8 +622,11 @@ def softmax_lse2(q, ks, stat_len, scale=None):
     softmax(q K^T / sqrt(d), dtype=float32) over a pivot's prefill keys) are
     exp2(s_t - lse2) with s_t = scale * log2(e) * q.k_t and
     lse2 = log2(sum_t exp2(s_t)); hc_decode_attn_stats reports lse2 as a
-    (bound M, sum of exp2(s_t - M)) pair.  q: [rows, G, d]; ks: list of
-    [len_r, d].  Returns [rows, G] (-inf for a row with no key below stat_len).
+    (bound M, sum of exp2(s_t - M)) pair.  io_dtype ('bfloat16' /
+    'float16'): the logits of the reference's casts instead, as
+    _pooled_group_max forms them, s_t = log2(e) * round(round(q.k_t) * scale).
+    q: [rows, G, d]; ks: list of [len_r, d].  Returns [rows, G] (-inf for a
+    row with no key below stat_len).
     """
     q = np.asarray(q, dtype=np.float64)
     rows, G, d = q.shape
@@ -633,7 +636,11 @@ def softmax_lse2(q, ks, stat_len, scale=None):
         k = np.asarray(ks[r], dtype=np.float64)[:stat_len]
         if k.shape[0] == 0:
             continue
-        s2 = scale * math.log2(math.e) * (q[r] @ k.T)
+        if io_dtype not in (None, "float32"):
+            logits = round_to(round_to(q[r] @ k.T, io_dtype) * np.float32(scale), io_dtype)
+            s2 = math.log2(math.e) * logits.astype(np.float64)
+        else:
+            s2 = scale * math.log2(math.e) * (q[r] @ k.T)
         m = s2.max(axis=-1, keepdims=True)
         out[r] = m[:, 0] + np.log2(np.exp2(s2 - m).sum(axis=-1))
     return out

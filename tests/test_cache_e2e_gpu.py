@@ -255,7 +255,8 @@ def test_chunked_prefill_with_observation_window_equals_single_shot(dev):
 def test_reference_cast_chain(dev, dtype, io, step):
     """round_scores=True (the reference's casts of logits, probabilities and
     pooled scores to the model dtype) on a bfloat16 model and on a float16
-    one (the reference's load dtype): the device scores equal the oracle's
+    one (the reference's load dtype), the drift checks in one pass over the
+    pivot keys: the device scores equal the oracle's
     cast chain to within one step of that dtype; the oracle's
     integer flow run on the device scores reproduces the
     triggers and the stores bit for bit, and the attention outputs match
@@ -298,6 +299,9 @@ def test_reference_cast_chain(dev, dtype, io, step):
             ref = orc.decode(layer, as_np(q), as_np(kn), as_np(vn))
             assert np.abs(as_np(out).reshape(B, Hq, D) - ref).max() <= 2e-2
     torch.cuda.synchronize()
+    # Both checks scored in one pass, from the cast chain's statistics that
+    # the decode launches reported.
+    assert cache.one_pass_checks == steps // 5
     flags = [(l, h, c[(l, h)]) for c in rec.checks for l in range(NL) for h in cache._drift[l].leaders]
     assert flags == orc.triggers and [f for *_, f in flags] == [False] * 3 + [True] * 3
     assert max(e for *_, e in hook.err) <= step * 1.01

@@ -241,8 +241,12 @@ def test_config2_reference_cast_chain_fp16_128k(dev):
     2 and 4).  Layers 0 and 23 are checked stage by stage:
 
     * every score the device ranks (prefill selection, pivot sets, drift
-      steps) equals the oracle's float16 cast chain to within one float16
-      step at the score's magnitude (subnormal spacing below 2^-14);
+      steps) equals the oracle's float16 cast chain to within two float16
+      steps at the score's magnitude (subnormal spacing below 2^-14), and
+      all but a few in a million within one.  Two is what the chain allows
+      for a probability one step off (the float32 softmax arithmetic): it
+      moves the average of 5 by at most 8/5 steps of the average, since
+      steps are powers of two;
     * the oracle's integer flow on the device scores -- where the cast
       chain ties massively, the lowest position first -- reproduces the
       triggers, reference sets and stores bit for bit;
@@ -291,6 +295,9 @@ def test_config2_reference_cast_chain_fp16_128k(dev):
             assert err <= ATTN_TOL, f"step {t} layer {layer}: max-abs {err}"
     torch.cuda.synchronize()
     assert len(rec.checks) == steps // S
+    # Every check scored in one pass, from the float16 cast chain's
+    # statistics that the decode launches reported.
+    assert cache.one_pass_checks >= steps // S
     for c, flags in enumerate(rec.checks):
         assert len(flags) == 33
         assert all(f == (c % 2 == 1) for f in flags.values()), (c, flags)
@@ -304,9 +311,10 @@ def test_config2_reference_cast_chain_fp16_128k(dev):
     total = sum(x[5] for x in hook.steps)
     print(f"cast chain: {len(hook.steps)} score rows, {total} scores, worst {worst[3]:.2f} float16 steps "
           f"({worst[:3]}), {off} beyond one step")
-    assert worst[3] <= 1.0, worst
     check_stores(cache, orc, checked, 1, Hkv)
     check_ref_sets(cache, orc, checked, L)
+    assert worst[3] <= 2.0, worst
+    assert off <= total * 1e-5, (off, total)
 
 
 def test_config4_chunked_224k_then_drift_block(dev):

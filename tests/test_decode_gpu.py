@@ -154,16 +154,19 @@ def test_merge_folds_parts_beyond_the_register_batch(dev, G):
     assert err <= ATTN_TOL["bf16"], err
 
 
-@pytest.mark.parametrize("dt", ["bf16", "f32"])
+@pytest.mark.parametrize("dt,io_dtype", [("bf16", None), ("f32", None), ("bf16", "bfloat16"), ("f16", "float16")])
 @pytest.mark.parametrize("chunk", [4, None])
-def test_softmax_stats_below_stat_len(dev, dt, chunk):
+def test_softmax_stats_below_stat_len(dev, dt, io_dtype, chunk):
     """hc_decode_attn_stats: for every row and query head, M + log2(L) is the
     float64 base-2 log-normaliser over the row's first stat_len attended
     tokens (tile-aligned and not, beyond every row, with and without a fused
     append whose new token lies above or below stat_len); the attention
-    output is the plain call's, bit for bit."""
-    from heterocache_amd import ops
+    output is the plain call's, bit for bit.  With a rounding flag, the
+    normaliser of the reference's cast chain of the logits (the oracle's
+    io_dtype form)."""
+    from heterocache_amd import compress
     lens, G = [5000, 3000, 40, 0, 2055], 4
+    flags = compress.ROUND_FLAGS[TORCH_DT[dt]] if io_dtype else 0
     tdt = TORCH_DT[dt]
     rng = np.random.default_rng(17)
     ks = [torch.as_tensor(rng.standard_normal((L, 128)), dtype=torch.float32).to(tdt) for L in lens]
@@ -182,12 +185,13 @@ def test_softmax_stats_below_stat_len(dev, dt, chunk):
                 fill_store(st, [k.to(dev) for k in ks], [v.to(dev) for v in vs], dev)
             stats = torch.full((len(lens), G, 2), 7.0, dtype=torch.float32, device=dev)
             extra = dict(k_new=kn, v_new=vn) if append else {}
-            oa = a.attend(q, scale, chunk_tiles=chunk, stat_len=stat_len, stat_out=stats, **extra).clone()
+            oa = a.attend(q, scale, chunk_tiles=chunk, stat_len=stat_len, stat_out=stats, stat_flags=flags,
+                          **extra).clone()
             ob = b.attend(q, scale, chunk_tiles=chunk, **extra)
             torch.cuda.synchronize()
             assert torch.equal(oa, ob), (stat_len, append)
             keys = [as_np(torch.cat([k.to(dev), kn[r:r + 1]]) if append else k) for r, k in enumerate(ks)]
-            ref = O.softmax_lse2(as_np(q), keys, stat_len, scale)
+            ref = O.softmax_lse2(as_np(q), keys, stat_len, scale, io_dtype=io_dtype)
             st = stats.cpu().numpy().astype(np.float64)
             with np.errstate(divide="ignore"):
                 got = st[..., 0] + np.log2(st[..., 1])

@@ -696,3 +696,23 @@ def test_softmax_lse2_against_scipy_and_closed_forms():
     s = scale * math.log2(math.e) * (q[0] @ k[0])
     np.testing.assert_allclose(O.softmax_lse2(q[:1], [k], 1000)[0], s + 4.0, atol=1e-12)
     np.testing.assert_allclose(O.softmax_lse2(q[:1], [k], 4)[0], s + 2.0, atol=1e-12)
+
+
+@pytest.mark.parametrize("io_dtype,tdt", [("float16", torch.float16), ("bfloat16", torch.bfloat16)])
+def test_softmax_lse2_cast_chain_against_torch(io_dtype, tdt):
+    """The cast chain's log-normaliser: integer queries and keys make every
+    dot product exact, so torch's own half-precision ops (the product cast to
+    the model dtype, then the scaling, rounded again) give the logits, and
+    scipy's logsumexp the normaliser."""
+    from scipy.special import logsumexp
+    rng = np.random.default_rng(22)
+    q = rng.integers(-3, 4, size=(2, 4, 128)).astype(np.float64)
+    ks = [rng.integers(-3, 4, size=(n, 128)).astype(np.float64) for n in (90, 33)]
+    scale = 1 / math.sqrt(128)
+    got = O.softmax_lse2(q, ks, 60, io_dtype=io_dtype)
+    for r in range(2):
+        dots = torch.tensor(q[r]).to(tdt) @ torch.tensor(ks[r][:60]).to(tdt).T
+        logits = (dots * scale).to(tdt).double().numpy()
+        np.testing.assert_allclose(got[r], logsumexp(logits, axis=-1) / math.log(2), rtol=0, atol=1e-9)
+    # The chain differs from the uncast normaliser (the casts are not a no-op).
+    assert np.abs(got - O.softmax_lse2(q, ks, 60)).max() > 1e-4

@@ -14,10 +14,10 @@ import numpy as np
 import pytest
 import torch
 
-from heterocache_amd import compress
+from heterocache_amd import compress, ops
 from heterocache_amd.store import KVStore
 from oracle import hc_oracle as O
-from tests.gpu_util import as_np
+from tests.gpu_util import TORCH_DT, as_np
 
 pytestmark = pytest.mark.gpu
 
@@ -150,6 +150,58 @@ def test_score_given_stats(dev, L, pooling, kernel):
     for j in range(len(pivots)):
         assert rel_err(as_np(got2[j]), refs[j]) < 2e-4, j
         assert rel_err(as_np(got2[j]), as_np(two_pass[j])) < 1e-5, j
+
+
+@pytest.mark.parametrize("dt,L,pooling,kernel", [("bf16", 4099, "avgpool", 5), ("f16", 4099, "maxpool", 7),
+                                                  ("f16", 131072, "avgpool", 5), ("bf16", 300, "avgpool", 1)])
+def test_score_given_stats_cast_chain(dev, dt, L, pooling, kernel):
+    """hc_score_given_stats under the reference's cast chain (flags
+    HC_SCORE_ROUND_*), with the statistics the S decode launches reported
+    under the same flag: every score within two steps of the model dtype of
+    the oracle's cast-chain scores and of the two-pass cast-chain scorer's
+    (the statistics' summation order may move a probability, and then its
+    pooled value, across a rounding boundary), and over 99 % of them equal
+    to the two-pass scores."""
+    B, Hq, Hkv, S, G = 1, 16, 4, 5, 4
+    tdt = TORCH_DT[dt]
+    io = {"bf16": "bfloat16", "f16": "float16"}[dt]
+    flags = compress.ROUND_FLAGS[tdt]
+    rng = np.random.default_rng(L + kernel + 7)
+    k = torch.as_tensor(rng.standard_normal((B, Hkv, L, 128)), dtype=torch.float32)
+    k[..., :4] *= 5
+    k = k.to(tdt).to(dev)
+    steps = torch.as_tensor(rng.standard_normal((B, Hq, S, 128)), dtype=torch.float32).to(tdt).to(dev)
+    store = KVStore([L + 64] * (B * Hkv), tdt, dev)
+    store.write_rows(k, k, [(0, h) for h in range(Hkv)], list(range(Hkv)), [L] * Hkv)
+    pivots = [1, 3]
+    q_off, k_row = compress.pivot_step_metadata(steps, store, pivots, pivots, G)
+    scale = 1 / math.sqrt(128)
+    dstats = torch.full((B * Hkv, G, S, 2), float("nan"), dtype=torch.float32, device=dev)
+    for w in range(S):
+        qw = steps[:, :, w].reshape(B * Hkv, G, 128).contiguous()
+        store.attend(qw, scale, stat_len=L, stat_out=dstats[:, :, w], stat_flags=flags)
+    st_off = torch.tensor(pivots, dtype=torch.int64, device=dev) * (G * S * 2)
+    got = ops.score_given_stats(steps, q_off, steps.stride(1), steps.stride(2), store.k, store.row_tile_off, k_row,
+                                L, G, S, pooling, kernel, scale, dstats, st_off, flags=flags)
+    two_pass = compress.pivot_step_scores(steps, store, pivots, pivots, G, L, pooling, kernel, round_dtype=tdt)
+    torch.cuda.synchronize()
+    sn, kn = as_np(steps), as_np(k)
+    for j, h in enumerate(pivots):
+        g, t = as_np(got[j]), as_np(two_pass[j])
+        ref = O.pivot_step_scores(sn[0, h * G:(h + 1) * G], kn[0, h], pooling, kernel, io_dtype=io)
+        tol = 2 * dtype_spacing(ref, dt)
+        assert np.all(np.abs(g - ref) <= tol), (j, (np.abs(g - ref) / tol).max())
+        assert np.all(np.abs(g - t) <= tol), (j, (np.abs(g - t) / tol).max())
+        assert np.mean(g == t) > 0.99, (j, np.mean(g == t))
+
+
+def dtype_spacing(x, dt):
+    """Step of the model dtype at |x| (float16: its subnormal step near 0)."""
+    x = np.abs(np.asarray(x, dtype=np.float64))
+    if dt == "f16":
+        return np.spacing(x.astype(np.float16)).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(x, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
 
 
 # -- selection --------------------------------------------------------------------
