@@ -184,3 +184,52 @@ def test_score_hist_refused_for_large_query_sets(dev):
     with pytest.raises(Exception, match="histogram"):
         ops.score(q, zero, q.stride(1), q.stride(2), k, zero, k.stride(2), L, G, W, L, "avgpool", 5, 128 ** -0.5,
                   hist=hist)
+
+
+@pytest.mark.parametrize("kind", ["ascending_dense", "ascending_sparse", "shuffled", "duplicates_and_out_of_range"])
+def test_set_bits_matches_numpy(dev, kind):
+    """hc_set_bits: bitmaps of position lists (the pivot reference sets) are
+    the lists' sets exactly, for ascending lists dense and sparse in their
+    words, shuffled ones, and lists with repeats and positions outside
+    [0, nbits) (ignored); per-set counts and a fixed count; a set beyond the
+    LDS path's 262144 positions; whole rows (row stride) cleared first."""
+    rng = np.random.default_rng(len(kind))
+    for nbits, nsets in ((131072, 3), (4099, 2), (300000, 2)):
+        words = (nbits + 31) // 32
+        lists, counts = [], []
+        for j in range(nsets):
+            n = {0: nbits // 2, 1: 1000, 2: 37}[j % 3]
+            if kind == "ascending_sparse":
+                n = min(n, nbits // 64)
+            x = np.sort(rng.choice(nbits, size=min(n, nbits), replace=False))
+            if kind == "shuffled":
+                x = rng.permutation(x)
+            if kind == "duplicates_and_out_of_range":
+                x = np.concatenate([x, x[: len(x) // 3], [-5, nbits, nbits + 77, -1]])
+                x = rng.permutation(x)
+            lists.append(x.astype(np.int32))
+            counts.append(len(x))
+        width = max(counts) + 3
+        idx = np.full((nsets, width), 7, dtype=np.int32)  # past each count: must be ignored
+        for j, x in enumerate(lists):
+            idx[j, :len(x)] = x
+        bits = torch.full((nsets, words + 5), -1, dtype=torch.int32, device=dev)
+        ops.set_bits(torch.tensor(idx, device=dev), torch.tensor(counts, dtype=torch.int32, device=dev), bits, nbits)
+        got = bits.cpu().numpy()
+        for j, x in enumerate(lists):
+            ref = np.zeros(words * 32, dtype=bool)
+            v = x[(x >= 0) & (x < nbits)]
+            ref[v] = True
+            row = np.unpackbits(got[j, :words].view(np.uint8), bitorder="little").astype(bool)
+            assert np.array_equal(row, ref), (kind, nbits, j)
+            assert np.all(got[j, words:] == 0), "the row's padding words are cleared too"
+        # A fixed count: the first count positions of every row.
+        k = min(counts)
+        bits2 = torch.zeros((nsets, words), dtype=torch.int32, device=dev)
+        ops.set_bits(torch.tensor(idx, device=dev), None, bits2, nbits, fixed_count=k)
+        got2 = bits2.cpu().numpy()
+        for j, x in enumerate(lists):
+            ref = np.zeros(words * 32, dtype=bool)
+            v = x[:k]
+            ref[v[(v >= 0) & (v < nbits)]] = True
+            assert np.array_equal(np.unpackbits(got2[j].view(np.uint8), bitorder="little").astype(bool), ref)
