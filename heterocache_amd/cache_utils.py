@@ -186,24 +186,29 @@ class _DevicePack:
         return ops.to_device(buf, device, torch.int64)
 
     @staticmethod
-    def view(dev, slot):
-        """Device view of one added array inside the uploaded buffer."""
-        words = max((slot.n * slot.dtype.itemsize + 7) // 8, 1)
-        t = dev[slot.off:slot.off + words]
+    def view(dev, slot, dev32=None):
+        """Device view of one added array inside the uploaded buffer (dev32:
+        the same buffer viewed as int32, to slice int32 arrays in one step)."""
         if slot.dtype == np.int32:
-            t = t.view(torch.int32)
-        return t[:slot.n]
+            d32 = dev.view(torch.int32) if dev32 is None else dev32
+            return d32[2 * slot.off:2 * slot.off + slot.n]
+        return dev[slot.off:slot.off + slot.n]
 
     @staticmethod
     def resolve(obj, dev):
-        """Replace every Slot inside nested dicts / tuples of obj by its view."""
+        """Replace every Slot inside nested dicts / tuples of obj by its view
+        (one tensor slice per slot: a layer's plan holds a few dozen)."""
+        dev32 = dev.view(torch.int32)
+        slot_t, view = _DevicePack.Slot, _DevicePack.view
+
         def walk(x):
-            if isinstance(x, _DevicePack.Slot):
-                return _DevicePack.view(dev, x)
-            if isinstance(x, dict):
+            t = type(x)
+            if t is slot_t:
+                return view(dev, x, dev32)
+            if t is dict:
                 return {k: walk(v) for k, v in x.items()}
-            if isinstance(x, tuple):
-                return tuple(walk(v) for v in x)
+            if t is tuple:
+                return tuple([walk(v) for v in x])
             return x
         for k in list(obj):
             obj[k] = walk(obj[k])
