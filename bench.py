@@ -222,12 +222,14 @@ def full_step_phase(args, torch, dev):
         """Keep the stream busy for about `ms` (torch.cuda._sleep), so that
         the launches issued meanwhile queue up behind it."""
         if not sleep_cycles[0]:
+            torch.cuda._sleep(1 << 16)  # first launch loads the kernel
+            torch.cuda.synchronize()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            torch.cuda._sleep(1 << 20)
+            torch.cuda._sleep(1 << 23)
             b.record()
             torch.cuda.synchronize()
-            sleep_cycles[0] = max(1, int((1 << 20) / max(a.elapsed_time(b), 1e-3)))  # cycles per ms
+            sleep_cycles[0] = max(1, int((1 << 23) / max(a.elapsed_time(b), 1e-3)))  # cycles per ms
         torch.cuda._sleep(int(sleep_cycles[0] * ms))
 
     def prefill(cache, keep_inputs, queued=False):
@@ -244,7 +246,7 @@ def full_step_phase(args, torch, dev):
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             if queued:
-                hold_device(3.0)
+                hold_device(5.0)
             t0 = time.perf_counter()
             e0.record()
             k, v = cache.update(x["k"], x["v"], layer)
