@@ -95,6 +95,31 @@ def copy_calibration(torch, dev):
     return {"kernel": "torch.neg fp32 elementwise", "bytes_read": n * 4, "bytes_written": n * 4, "launches": 3}
 
 
+def read_ceiling(torch, dev, gib=2, reps=5):
+    """The device's streaming-read ceiling (hc_stream_read over a fresh
+    zero-filled buffer of `gib` GiB, several times the 256 MB last-level
+    cache, so every read goes to HBM): the best of `reps` event-timed
+    calls, GB/s."""
+    from heterocache_amd import ops
+    buf = torch.zeros(gib << 28, dtype=torch.float32, device=dev)
+    sink = torch.zeros(1, dtype=torch.float32, device=dev)
+    ops.stream_read(buf, sink=sink)
+    best = None
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        ops.stream_read(buf, sink=sink)
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b)
+        best = ms if best is None else min(best, ms)
+    nbytes = buf.numel() * 4
+    del buf
+    torch.cuda.empty_cache()
+    return {"gbs": round(nbytes / (best * 1e-3) / 1e9, 1), "bytes": nbytes, "workgroups_per_cu": 8,
+            "kernel": "hc_stream_read: nontemporal 16-byte loads, one in flight per thread"}
+
+
 def c_port_decode(budgets, seconds):
     """The C oracle's decode attention on one layer of the 128K bench
     workload (bf16 rows, GQA 4), all usable cores, for about `seconds`."""
@@ -1101,6 +1126,10 @@ def main():
     }
     del stores, q, kn, vn, outs
     torch.cuda.empty_cache()
+    # The part's measured streaming-read ceiling beside the data-sheet peak.
+    ceil = read_ceiling(torch, dev)
+    ceil["layer_frac_of_ceiling"] = round(gbs / ceil["gbs"], 4)
+    rec["roofline"]["read_ceiling"] = ceil
     if args.calibrate_copy:
         rec["copy_calibration"] = copy_calibration(torch, dev)
     if not args.no_full_step:

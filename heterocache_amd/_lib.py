@@ -35,6 +35,7 @@ SIGNATURES = {
     "hc_tile_tokens": (c_int, []),
     "hc_head_dim": (c_int, []),
     "hc_read_status": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "hc_stream_read": (c_int, [c_void_p, c_size_t, c_void_p, c_int, c_void_p]),
     "hc_decode_attn": (c_int, [c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                c_int, c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_int64, c_int,
                                c_void_p, c_void_p]),

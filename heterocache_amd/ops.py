@@ -197,6 +197,21 @@ def decode_attn(q, kstore, vstore, row_tile_off, row_len, host_row_len, scale, o
     return out
 
 
+def stream_read(buf, workgroups_per_cu=8, sink=None, stream=None):
+    """Read a device buffer once with nontemporal 16-byte loads and discard
+    it (hc_stream_read): timed over a buffer larger than the last-level
+    cache, the device's streaming-read ceiling."""
+    lib = _lib.load()
+    _require_cuda(buf)
+    if not buf.is_contiguous():
+        raise ValueError("buf must be contiguous")
+    if sink is None:
+        sink = torch.zeros(1, dtype=torch.float32, device=buf.device)
+    _lib.check(lib.hc_stream_read(_ptr(buf), buf.numel() * buf.element_size(), _ptr(sink), int(workgroups_per_cu),
+                                  _stream(stream, buf)))
+    return sink
+
+
 def read_status(status, clear=True, stream=None):
     """Wait for the stream and read the device status word of hc_append /
     hc_decode_attn (zeroing it when clear).  Returns the word; raises

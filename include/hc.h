@@ -49,6 +49,20 @@ const char* hc_last_error(void);
  * heterocache/cache_utils.py:988-990) as a typed error.
  */
 int hc_read_status(int32_t* status, int clear, int32_t* value, void* stream);
+
+/*
+ * No counterpart in the reference: a measurement aid for the roofline of
+ * the HBM-bound kernels.  Reads `bytes` (a multiple of 16, 16-byte aligned)
+ * from device memory with nontemporal 16-byte loads, one in flight per
+ * thread, over workgroups_per_cu * (compute units) workgroups of 256 threads
+ * (8 read fastest on MI355X), and discards them (sink, one float, is
+ * written only when the sum equals one arbitrary value, -1.2345e-37, so the
+ * loads are kept; a zero-filled buffer never writes it).  The time of a
+ * call over a buffer larger than the last-level cache is the part's
+ * streaming-read ceiling, against which a kernel's achieved bandwidth can be
+ * set beside the data-sheet peak.
+ */
+int hc_stream_read(const void* src, size_t bytes, float* sink, int workgroups_per_cu, void* stream);
 int hc_version(void);
 int hc_tile_tokens(void);
 int hc_head_dim(void);

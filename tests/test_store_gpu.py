@@ -268,3 +268,20 @@ def test_gather_groups_from_per_job_tensors(dev):
         rk, rv = st.read_rows([j], n)
         sel = torch.as_tensor(idx[j, :n], dtype=torch.long, device=dev)
         assert torch.equal(rk[0], k[0, h].index_select(0, sel)) and torch.equal(rv[0], v[0, h].index_select(0, sel)), j
+
+
+def test_stream_read_reads_and_leaves_the_sink(dev):
+    """hc_stream_read (the bench's read-ceiling measurement): over a
+    zero-filled buffer it leaves the sink alone, and it refuses a size that
+    is not a multiple of 16 bytes and an out-of-range workgroup count."""
+    from heterocache_amd import _lib, ops
+    buf = torch.zeros(1 << 20, dtype=torch.float32, device=dev)
+    sink = torch.full((1,), 7.0, dtype=torch.float32, device=dev)
+    ops.stream_read(buf, sink=sink)
+    ops.stream_read(buf, workgroups_per_cu=1, sink=sink)
+    torch.cuda.synchronize()
+    assert sink.item() == 7.0
+    with pytest.raises(_lib.HCError):
+        ops.stream_read(buf[:3], sink=sink)
+    with pytest.raises(_lib.HCError):
+        ops.stream_read(buf, workgroups_per_cu=0, sink=sink)
