@@ -73,3 +73,24 @@ def test_num_parts_matches_chunking():
     assert ops.decode_num_parts([0, 1, 512, 513], chunk_tiles=16) == 1 + 1 + 1 + 2
     assert ops.decode_num_parts([131072], chunk_tiles=32) == 131072 // 1024
     assert ops.decode_num_parts([100, 4097], chunk_tiles=5) == 1 + 26
+
+
+def test_rounding_flags_are_checked_before_any_launch():
+    """hc_decode_attn_stats and hc_score_given_stats take the cast chain's
+    rounding flag (HC_SCORE_ROUND_BF16 / _F16, or 0) and refuse any other
+    value before a HIP call; hc_stream_read refuses sizes that are not
+    16-byte multiples and out-of-range workgroup counts."""
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libhc.so not built")
+    lib = _lib.load()
+    fake = 16  # never dereferenced: validation fails first
+    for bad in (1, 3, _lib.HC_SCORE_ROUND_BF16 | _lib.HC_SCORE_ROUND_F16, _lib.HC_SCORE_SUM_WINDOW):
+        rc = lib.hc_decode_attn_stats(2, fake, fake, fake, fake, fake, None, None, 4, 4, 1.0, None, None, fake, fake,
+                                      1 << 20, 4, 4, None, 1000, fake, 8, 2, bad, None)
+        assert rc == _lib.HC_ERR_INVALID and b"stat_flags" in lib.hc_last_error(), bad
+        rc = lib.hc_score_given_stats(2, fake, fake, 640, 128, fake, fake, fake, 2, 1000, 4, 5, bad, 0, 5, 0.088,
+                                      fake, fake, fake, None)
+        assert rc == _lib.HC_ERR_INVALID and b"flags" in lib.hc_last_error(), bad
+    assert lib.hc_stream_read(fake, 24, fake, 8, None) == _lib.HC_ERR_INVALID
+    assert lib.hc_stream_read(fake, 4096, fake, 0, None) == _lib.HC_ERR_INVALID
+    assert lib.hc_stream_read(None, 4096, fake, 8, None) == _lib.HC_ERR_INVALID
