@@ -974,7 +974,7 @@ def config1_phase(args, torch, dev, L=32768, new=256):
     return res
 
 
-def north_star_summary(rec, args):
+def step_target_summary(rec, args):
     """The step target in its own terms: the attention and retrieval-gather
     kernels of the 128K, ratio-0.5 decode step against the HBM roofline, and
     the retrieval time the step does not hide.  Attention: the headline
@@ -1005,7 +1005,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the path is sharded by KV head "
-              "across GPUs by design but no multi-GPU run is part of this build.", file=sys.stderr)
+              "across GPUs by design but this benchmark runs one GPU.", file=sys.stderr)
         sys.exit(2)
     import torch
     from heterocache_amd import ops, workloads
@@ -1144,7 +1144,7 @@ def main():
             rec["config4_end_to_end"] = config4_phase(args, torch, dev)
             rec["config1_generate"] = config1_phase(args, torch, dev)
     if "full_decode_step" in rec and "gather" in rec:
-        rec["north_star"] = north_star_summary(rec, args)
+        rec["step_target"] = step_target_summary(rec, args)
     if not args.no_cpu_baseline:
         rec["cpu_baseline"] = cpu_baseline(budgets[0], args.cpu_seconds)
     print(json.dumps(rec))

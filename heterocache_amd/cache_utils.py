@@ -47,7 +47,7 @@ def get_compress_len(compression_ratio, full_heads, ori_len, num_kv_heads):
 
 
 class HeteroCacheConfig:
-    """heterocache/cache_utils.py:41-68, plus the options of this build.
+    """heterocache/cache_utils.py:41-68, plus this package's own options.
 
     retrieval_topk: cap on the tokens retrieved into a satellite (None =
     the reference's full budget).  window_size: observation window of the

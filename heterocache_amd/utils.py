@@ -123,7 +123,7 @@ def build_cache_config(model, data, compression_ratio=0.5, stable_threshold=0.5,
 
 
 class install_attention_patch:
-    """Swap this build's attention classes into transformers; do it before
+    """Swap this package's attention classes into transformers; do it before
     the model is constructed (the decoder layer instantiates the module
     global).  Usable as a plain call or as a context manager that restores
     the original classes on exit."""
@@ -198,7 +198,7 @@ def load_model_and_tokenizer(args):
     real_offload, max_gen_len, steps (the drift-check period).  Optional:
     attn_implementation (default "sdpa"), torch_dtype (default float16, as
     the reference), device_map (default "auto").  The attention classes are
-    patched before the model is built (every method runs this build's
+    patched before the model is built (every method runs this package's
     kernels); heterocache reorders the heads by the JSON, augments it and
     checks the ratio as the reference does.  4-bit quantization (the
     reference's bitsandbytes path) is not provided.
@@ -212,7 +212,7 @@ def load_model_and_tokenizer(args):
     if method not in classes:
         raise ValueError(f"unknown method {args.method!r}; expected one of {sorted(classes)}")
     if getattr(args, "quant", False):
-        raise NotImplementedError("4-bit quantization (bitsandbytes) is not provided by this build")
+        raise NotImplementedError("4-bit quantization (bitsandbytes) is not provided by heterocache_amd")
     data = None
     if method == "heterocache":
         path = head_analysis_path(args.load_dir, args.model_path, args.topk, args.stable_threshold,
