@@ -50,7 +50,7 @@ SIGNATURES = {
     "hc_decode_workspace_size": (c_size_t, [c_int, c_int, c_int64]),
     "hc_gather_store": (c_int, [c_int, c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p,
                                 c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p, c_int,
-                                c_void_p]),
+                                c_void_p, c_void_p]),
     "hc_gather_store_groups": (c_int, [c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p,
@@ -90,7 +90,7 @@ SIGNATURES = {
     "hc_select_hist_size": (c_size_t, [c_int]),
     "hc_select_scratch_size": (c_size_t, [c_int, c_int]),
     "hc_set_bits": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,
-                            c_void_p]),
+                            c_void_p, c_void_p]),
     "hc_overlap_count": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,
                                  c_void_p]),
     "hc_drift_select": (c_int, [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int64,

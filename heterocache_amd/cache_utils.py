@@ -722,9 +722,9 @@ class HeteroCache(DynamicCache):
         plan = self._layer_plan(layer_idx, key_states, value_states)
         store = self.stores[layer_idx]
         if keep and plan is not None:
-            store.launch_rows(plan["keep"], key_states, value_states, set_len=False)
+            store.launch_rows(plan["keep"], key_states, value_states, set_len=False, write_len=True)
             rows, lens, drows, dlens = plan["keep_len"]
-            store.set_lengths_planned(rows, lens, drows, dlens, plan["order"])
+            store.set_lengths_planned(rows, lens, drows, dlens, plan["order"], on_device=True)
         elif keep:
             bh = [(b, h) for b in range(self.bsz) for h in keep]
             store.write_rows(key_states, value_states, bh, [b * self.num_kv_heads + h for b, h in bh],
@@ -879,7 +879,8 @@ class HeteroCache(DynamicCache):
             raise ValueError(f"layer {layer_idx}: leader count differs from leader_member_relations")
         st.ref_bits = self._ref_bits_all[lb * B:(lb + len(leaders)) * B]
         if len(leaders):
-            ops.set_bits(idx.index_select(0, order).contiguous(), None, st.ref_bits, L, fixed_count=K)
+            # Set (leader, b) takes its list from selection row order[...].
+            ops.set_bits(idx, None, st.ref_bits, L, fixed_count=K, row_of=order)
             st.trigger = self._trigger_all[lb:lb + len(leaders)]
         else:
             st.trigger = torch.zeros(1, dtype=torch.int32, device=idx.device)
@@ -913,22 +914,16 @@ class HeteroCache(DynamicCache):
             return
         store = self.stores[layer_idx]
         L = key_states.shape[-2]
-        caps = _f32_caps(self.base_compress_len, self.data["allocation_matrix"][layer_idx][:n_c], L)
         rows = [b * self.num_kv_heads + h for b in range(self.bsz) for h in range(n_c)]
-        caps_rows = [int(caps[h]) for b in range(self.bsz) for h in range(n_c)]
-        if max(caps_rows) == 0:
-            store.set_lengths([0] * len(rows), rows)
-            return
-        G = self.num_key_value_groups
-        W = self.window_size
-        if stats is not None:
-            self.attn_stats_layers += 1
         joint = self._joint_sel[layer_idx]
         self._joint_sel[layer_idx] = None
         plan = self._layer_plan(layer_idx, key_states, value_states)
         if (joint is not None and plan is not None and "compress_joint" in plan
                 and joint[0] == self._tensor_key(query_states, key_states)):
-            # Selected by init_coefficient's joint launches on these tensors.
+            # Selected by init_coefficient's joint launches on these tensors
+            # (a plan has "compress_joint" only when some cap is above 0).
+            if stats is not None:
+                self.attn_stats_layers += 1
             _, sc_all, idx, counts = joint
             if self.observer is not None:
                 J = len(plan["joint"]["heads"])
@@ -936,10 +931,20 @@ class HeteroCache(DynamicCache):
                               scores=sc_all.view(self.bsz, J, L)[:, :n_c].reshape(-1, L),
                               idx=idx.view(self.bsz, J, -1)[:, :n_c].reshape(self.bsz * n_c, -1),
                               counts=counts.view(self.bsz, J)[:, :n_c].reshape(-1))
-            store.launch_rows(plan["compress_joint"], key_states, value_states, idx=idx, set_len=False)
+            store.launch_rows(plan["compress_joint"], key_states, value_states, idx=idx, set_len=False,
+                              write_len=True)
             hrows, lens, drows, dlens = plan["compress_len"]
-            store.set_lengths_planned(hrows, lens, drows, dlens, plan["order"])
+            store.set_lengths_planned(hrows, lens, drows, dlens, plan["order"], on_device=True)
             return
+        caps = _f32_caps(self.base_compress_len, self.data["allocation_matrix"][layer_idx][:n_c], L)
+        caps_rows = [int(caps[h]) for b in range(self.bsz) for h in range(n_c)]
+        if max(caps_rows) == 0:
+            store.set_lengths([0] * len(rows), rows)
+            return
+        if stats is not None:
+            self.attn_stats_layers += 1
+        G = self.num_key_value_groups
+        W = self.window_size
         if W > 1:
             scores = compress.window_scores(query_states, key_states, range(n_c), G, W, self.pooling,
                                             self.kernel_size, window_keep=True,
@@ -958,9 +963,9 @@ class HeteroCache(DynamicCache):
         if self.observer is not None:
             self.observer("prefill_select", layer=layer_idx, rows=rows, scores=scores, idx=idx, counts=counts)
         if plan is not None:
-            store.launch_rows(plan["compress"], key_states, value_states, idx=idx, set_len=False)
+            store.launch_rows(plan["compress"], key_states, value_states, idx=idx, set_len=False, write_len=True)
             hrows, lens, drows, dlens = plan["compress_len"]
-            store.set_lengths_planned(hrows, lens, drows, dlens, plan["order"])
+            store.set_lengths_planned(hrows, lens, drows, dlens, plan["order"], on_device=True)
         else:
             store.write_rows(key_states, value_states, [(b, h) for b in range(self.bsz) for h in range(n_c)], rows,
                              caps_rows, idx=idx)

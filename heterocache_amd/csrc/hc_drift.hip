@@ -41,7 +41,8 @@ __global__ __launch_bounds__(1024) void set_bits_kernel(const int32_t* __restric
                                                         const int32_t* __restrict__ counts, int fixed_count,
                                                         uint32_t* __restrict__ bits, int64_t words, int nbits,
                                                         const int32_t* __restrict__ trigger,
-                                                        const int32_t* __restrict__ trig_of, int slice_words) {
+                                                        const int32_t* __restrict__ trig_of, int slice_words,
+                                                        const int64_t* __restrict__ row_of) {
   const int j = blockIdx.y;
   if (trigger && trigger[trig_of ? trig_of[j] : j] == 0) return;
   const int64_t w0 = (int64_t)blockIdx.x * slice_words;
@@ -54,7 +55,7 @@ __global__ __launch_bounds__(1024) void set_bits_kernel(const int32_t* __restric
   const int lo = (int)min(w0 * 32, (int64_t)nbits);
   const int hi = (int)min((w0 + nw) * 32, (int64_t)nbits);
   const int n = counts ? counts[j] : fixed_count;
-  const int32_t* ix = idx + (int64_t)j * idx_stride;
+  const int32_t* ix = idx + (row_of ? row_of[j] : (int64_t)j) * idx_stride;
   const int wb = (int)w0;
   const int bd = blockDim.x;
   int i_tail = 0;
@@ -170,7 +171,7 @@ using namespace hc;
 
 extern "C" int hc_set_bits(const int32_t* idx, int64_t idx_stride, const int32_t* counts, int fixed_count, int nsets,
                            uint32_t* bits, int64_t words, int nbits, const int32_t* trigger, const int32_t* trig_of,
-                           void* stream) {
+                           const int64_t* row_of, void* stream) {
   clear_error();
   if (nsets < 0 || nsets > 65535 || words < (nbits + 31) / 32 || nbits < 0)
     return set_error(HC_ERR_INVALID, "hc_set_bits: nsets=%d words=%lld nbits=%d", nsets, (long long)words, nbits);
@@ -183,7 +184,7 @@ extern "C" int hc_set_bits(const int32_t* idx, int64_t idx_stride, const int32_t
   const int slice_words = (int)((words + slices - 1) / slices);
   const int grid_x = (int)((words + slice_words - 1) / slice_words);
   hipLaunchKernelGGL(set_bits_kernel, dim3(grid_x, nsets), dim3(1024), 0, (hipStream_t)stream, idx, idx_stride, counts,
-                     fixed_count, bits, words, nbits, trigger, trig_of, slice_words);
+                     fixed_count, bits, words, nbits, trigger, trig_of, slice_words, row_of);
   return check_launch("hc_set_bits");
 }
 

@@ -39,10 +39,15 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
     const int32_t* __restrict__ count, const int32_t* __restrict__ dst_row, T* __restrict__ kstore,
     T* __restrict__ vstore, const int64_t* __restrict__ row_tile_off, const int32_t* __restrict__ trigger,
     const int32_t* __restrict__ trig_of, int njobs, int tiles_per_job, const int64_t* __restrict__ src_k_addr,
-    const int64_t* __restrict__ src_v_addr) {
+    const int64_t* __restrict__ src_v_addr, int32_t* __restrict__ set_len) {
   __shared__ T sk[HC_TILE][HC_HEAD_DIM + 8];
   __shared__ T sv[HC_TILE][HC_HEAD_DIM + 8];
   const int64_t items = (int64_t)njobs * tiles_per_job;
+  // set_len: each copied row's length becomes its count (workgroup 0; the
+  // lengths are read only by later launches).
+  if (set_len && blockIdx.x == 0)
+    for (int j = threadIdx.x; j < njobs; j += blockDim.x)
+      if (!trigger || trigger[trig_of ? trig_of[j] : 0] != 0) set_len[dst_row[j]] = count[j];
   const int lane = threadIdx.x & 63;
   // The workgroup's items are blockIdx.x + i * gridDim.x.  They are taken 64
   // at a time: lane i reads item i's trigger flag and count, and a ballot
@@ -185,14 +190,17 @@ static int launch_gather_store(const void* src_k, const void* src_v, const int64
                                const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off,
                                int njobs, int max_count, const int32_t* trigger, const int32_t* trig_of,
                                bool host_src, int max_workgroups, hipStream_t s,
-                               const int64_t* src_k_addr = nullptr, const int64_t* src_v_addr = nullptr) {
+                               const int64_t* src_k_addr = nullptr, const int64_t* src_v_addr = nullptr,
+                               int32_t* set_len = nullptr) {
   const int tiles = (max_count + HC_TILE - 1) / HC_TILE;
   const int64_t items = (int64_t)tiles * njobs;
   const int64_t cap = max_workgroups > 0 ? max_workgroups : (host_src ? kHostGatherWorkgroups : items);
-  const unsigned grid = (unsigned)std::min<int64_t>(items, cap);
+  // At least one workgroup: with set_len a launch of no tiles still writes
+  // the lengths.
+  const unsigned grid = (unsigned)std::max<int64_t>(1, std::min<int64_t>(items, cap));
   hipLaunchKernelGGL((gather_store_kernel<T>), dim3(grid), dim3(256), 0, s, (const T*)src_k, (const T*)src_v, src_off,
                      src_tok_stride, src_len, idx, idx_off, count, dst_row, (T*)kstore, (T*)vstore, row_tile_off, trigger,
-                     trig_of, njobs, tiles, src_k_addr, src_v_addr);
+                     trig_of, njobs, tiles, src_k_addr, src_v_addr, set_len);
   return check_launch("hc_gather_store");
 }
 
@@ -266,11 +274,13 @@ extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, 
                                const int64_t* src_off, int64_t src_tok_stride, int src_len, const int32_t* idx,
                                const int64_t* idx_off, const int32_t* count, const int32_t* dst_row, void* kstore,
                                void* vstore, const int64_t* row_tile_off, int njobs, int max_count,
-                               const int32_t* trigger, const int32_t* trig_of, int max_workgroups, void* stream) {
+                               const int32_t* trigger, const int32_t* trig_of, int max_workgroups, int32_t* set_len,
+                               void* stream) {
   clear_error();
   if (njobs < 0 || max_count < 0 || njobs > 65535 || max_workgroups < 0)
     return set_error(HC_ERR_INVALID, "hc_gather_store: njobs=%d max_count=%d", njobs, max_count);
-  if (njobs == 0 || max_count == 0) return HC_OK;
+  if (njobs == 0) return HC_OK;
+  if (max_count == 0 && !set_len) return HC_OK;
   if (src_len <= 0) return set_error(HC_ERR_INVALID, "hc_gather_store: src_len=%d", src_len);
   if (!idx && max_count > src_len)
     return set_error(HC_ERR_INVALID, "hc_gather_store: identity copy of %d tokens from a %d-token source", max_count,
@@ -293,13 +303,16 @@ extern "C" int hc_gather_store(int dtype, const void* src_k, const void* src_v, 
   switch (dtype) {
     case HC_DTYPE_BF16:
       return launch_gather_store<__bf16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                         vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s);
+                                         vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s,
+                                         nullptr, nullptr, set_len);
     case HC_DTYPE_F16:
       return launch_gather_store<_Float16>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                           vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s);
+                                           vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s,
+                                         nullptr, nullptr, set_len);
     case HC_DTYPE_F32:
       return launch_gather_store<float>(sk, sv, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore,
-                                        vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s);
+                                        vstore, row_tile_off, njobs, max_count, trigger, trig_of, src_is_host != 0, max_workgroups, s,
+                                         nullptr, nullptr, set_len);
     default:
       return set_error(HC_ERR_INVALID, "hc_gather_store: unknown dtype %d", dtype);
   }

@@ -226,12 +226,13 @@ def read_status(status, clear=True, stream=None):
 
 
 def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, count, dst_row, kstore, vstore, row_tile_off,
-                 max_count, src_is_host=False, trigger=None, trig_of=None, stream=None, max_workgroups=0):
+                 max_count, src_is_host=False, trigger=None, trig_of=None, stream=None, max_workgroups=0, set_len=None):
     """store[dst_row[j]][i] = src[src_off[j] + idx[idx_off[j] + i] * stride], i < count[j].
 
-    max_workgroups: grid cap (0: the library default for the source kind)."""
+    max_workgroups: grid cap (0: the library default for the source kind).
+    set_len: the store's int32 row lengths; row dst_row[j]'s becomes count[j]."""
     lib = _lib.load()
-    _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger, trig_of)
+    _require_cuda(src_off, count, dst_row, kstore, vstore, row_tile_off, idx, idx_off, trigger, trig_of, set_len)
     if src_is_host:
         if src_k.is_cuda or not src_k.is_pinned() or not src_v.is_pinned():
             raise ValueError("host sources must be pinned CPU tensors")
@@ -242,14 +243,14 @@ def gather_store(src_k, src_v, src_off, src_tok_stride, src_len, idx, idx_off, c
     for name, t, dt in (("src_off", src_off, torch.int64), ("count", count, torch.int32),
                         ("dst_row", dst_row, torch.int32), ("idx", idx, torch.int32),
                         ("idx_off", idx_off, torch.int64), ("trigger", trigger, torch.int32),
-                        ("trig_of", trig_of, torch.int32)):
+                        ("trig_of", trig_of, torch.int32), ("set_len", set_len, torch.int32)):
         if t is not None and t.dtype != dt:
             raise TypeError(f"{name} must be {dt}")
     njobs = count.numel()
     _lib.check(lib.hc_gather_store(dtype_code(kstore.dtype), _ptr(src_k), _ptr(src_v), int(bool(src_is_host)),
                                    _ptr(src_off), int(src_tok_stride), int(src_len), _ptr(idx), _ptr(idx_off), _ptr(count),
                                    _ptr(dst_row), _ptr(kstore), _ptr(vstore), _ptr(row_tile_off), njobs,
-                                   int(max_count), _ptr(trigger), _ptr(trig_of), int(max_workgroups),
+                                   int(max_count), _ptr(trigger), _ptr(trig_of), int(max_workgroups), _ptr(set_len),
                                    _stream(stream, kstore)))
 
 
@@ -687,14 +688,22 @@ def drift_select(scores, caps, K, bits, nbits, trig_of, nlead, batch, steps, thr
     return overlap
 
 
-def set_bits(idx, counts, bits, nbits, fixed_count=0, trigger=None, trig_of=None, stream=None):
-    """bits[j] = set of the first counts[j] (or fixed_count) positions of idx[j] (cleared first)."""
+def set_bits(idx, counts, bits, nbits, fixed_count=0, trigger=None, trig_of=None, stream=None, row_of=None):
+    """bits[j] = set of the first counts[j] (or fixed_count) positions of idx[r]
+    (cleared first), r = row_of[j] (int64 device tensor, one valid row of idx
+    per set) or j."""
     lib = _lib.load()
-    _require_cuda(idx, counts, bits, trigger, trig_of)
+    _require_cuda(idx, counts, bits, trigger, trig_of, row_of)
     if idx.dtype != torch.int32 or bits.dtype != torch.int32 or idx.dim() != 2 or bits.dim() != 2:
         raise TypeError("idx and bits must be 2-D int32 tensors")
-    _lib.check(lib.hc_set_bits(_ptr(idx), idx.stride(0), _ptr(counts), int(fixed_count), idx.shape[0], _ptr(bits),
-                               bits.stride(0), int(nbits), _ptr(trigger), _ptr(trig_of), _stream(stream, bits)))
+    if row_of is not None and row_of.dtype != torch.int64:
+        raise TypeError("row_of must be int64")
+    nsets = idx.shape[0] if row_of is None else row_of.numel()
+    if bits.shape[0] < nsets:
+        raise ValueError("one bitmask row per set")
+    _lib.check(lib.hc_set_bits(_ptr(idx), idx.stride(0), _ptr(counts), int(fixed_count), nsets, _ptr(bits),
+                               bits.stride(0), int(nbits), _ptr(trigger), _ptr(trig_of), _ptr(row_of),
+                               _stream(stream, bits)))
 
 
 def overlap_count(idx, count, bits, nbits, ref_of=None, out=None, stream=None):

@@ -116,19 +116,22 @@ class KVStore:
         self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
         self.row_order = ops.to_device(order, self.device)
 
-    def set_lengths_planned(self, rows, lens, dev_rows, dev_lens, dev_order=None):
+    def set_lengths_planned(self, rows, lens, dev_rows, dev_lens, dev_order=None, on_device=False):
         """set_lengths with the device copies already made: rows / lens on
         the host (numpy), dev_rows (int64) / dev_lens (int32) the same
         values on the device, dev_order (int32, optional) a row order to
         schedule by (any permutation of the rows is correct; longest first
         is the fast one).  Launches one index copy, and one copy for the
-        order, and no host-to-device transfer."""
+        order, and no host-to-device transfer.  on_device: a launch already
+        wrote the device lengths (launch_rows(write_len=True)); only the
+        host mirror and the order are updated."""
         rows = np.asarray(rows, dtype=np.int64)
         lens = np.asarray(lens, dtype=np.int64)
         if (lens > self.host_cap[rows]).any() or (lens < 0).any():
             raise RuntimeError("row length outside its capacity")
         self.host_len[rows] = lens
-        self.row_len.index_copy_(0, dev_rows, dev_lens)
+        if not on_device:
+            self.row_len.index_copy_(0, dev_rows, dev_lens)
         if dev_order is not None:
             self.row_order.copy_(dev_order)
         self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
@@ -197,8 +200,11 @@ class KVStore:
                 "max_count": int(counts.max())}
 
     def launch_rows(self, plan, src_k, src_v, idx=None, src_is_host=False, stream=None, trigger=None,
-                    set_len=True, max_workgroups=0):
-        """Run a gather planned by plan_rows (no host-to-device copies)."""
+                    set_len=True, max_workgroups=0, write_len=False):
+        """Run a gather planned by plan_rows (no host-to-device copies).
+        write_len: the gather kernel itself sets the device lengths of the
+        plan's rows to their counts (the caller then updates the host mirror
+        with set_lengths_planned(..., on_device=True))."""
         if plan is None:
             return
         if tuple(src_k.shape) != plan["shape"] or tuple(src_k.stride()) != plan["stride"] or \
@@ -211,7 +217,7 @@ class KVStore:
         ops.gather_store(src_k, src_v, plan["src_off"], plan["tok_stride"], plan["src_len"], idx, plan["idx_off"],
                          plan["counts"], plan["rows"], self.k, self.v, self.row_tile_off, plan["max_count"],
                          src_is_host=src_is_host, trigger=trigger, trig_of=plan["trig_of"], stream=stream,
-                         max_workgroups=max_workgroups)
+                         max_workgroups=max_workgroups, set_len=self.row_len if write_len else None)
         if set_len:
             self.set_lengths(plan["host_counts"], plan["host_rows"])
 

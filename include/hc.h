@@ -172,7 +172,9 @@ size_t hc_decode_workspace_size(int rows, int group, int64_t num_parts);
  * 32-token tile) items (0: one workgroup per item from device memory, 64
  * from host memory -- a host-sourced gather waits on the link, and beside a
  * decode launch that fills the device its workgroups take slots the decode
- * kernel needs).
+ * kernel needs).  set_len (optional, int32 per store row): the length of
+ * every copied row dst_row[j] becomes count[j] (gated like the copy), so a
+ * prefill store needs no separate length update.
  * Replaces the keep-head index_copy_ (heterocache/cache_utils.py:914-937),
  * the compressed-head gather + index_copy_ (heterocache/cache_utils.py:854-877)
  * and the retrieval index_select + copy_ (heterocache/cache_utils.py:1097-1123).
@@ -180,7 +182,8 @@ size_t hc_decode_workspace_size(int rows, int group, int64_t num_parts);
 int hc_gather_store(int dtype, const void* src_k, const void* src_v, int src_is_host, const int64_t* src_off,
                     int64_t src_tok_stride, int src_len, const int32_t* idx, const int64_t* idx_off, const int32_t* count,
                     const int32_t* dst_row, void* kstore, void* vstore, const int64_t* row_tile_off, int njobs,
-                    int max_count, const int32_t* trigger, const int32_t* trig_of, int max_workgroups, void* stream);
+                    int max_count, const int32_t* trigger, const int32_t* trig_of, int max_workgroups,
+                    int32_t* set_len, void* stream);
 
 /*
  * hc_gather_store over jobs split into ngroups consecutive groups (host
@@ -457,13 +460,15 @@ size_t hc_select_scratch_size(int njobs, int span);
 /*
  * Position lists -> bitmasks: set j (words uint32 words at bits + j*words) is
  * cleared and then holds the first counts[j] (or fixed_count) positions of
- * idx + j*idx_stride.  With trigger != NULL set j is left untouched unless
+ * list row r = (row_of ? row_of[j] : j), idx + r*idx_stride (row_of lets the
+ * sets take their lists from a selection's rows in another order, without a
+ * reordering copy).  With trigger != NULL set j is left untouched unless
  * trigger[trig_of ? trig_of[j] : j] != 0.  Holds the pivot reference sets of
  * heterocache/cache_utils.py:1189-1190 (prefill) and :1082 (update on drift).
  */
 int hc_set_bits(const int32_t* idx, int64_t idx_stride, const int32_t* counts, int fixed_count, int nsets,
                 uint32_t* bits, int64_t words, int nbits, const int32_t* trigger, const int32_t* trig_of,
-                void* stream);
+                const int64_t* row_of, void* stream);
 
 /*
  * out[j] = |{ idx[j*idx_stride + i] : i < count } ∩ set(ref_of ? ref_of[j] : j)|.

@@ -58,7 +58,7 @@ def test_constants_and_error_reporting_without_gpu():
     assert b"row_cap" in lib.hc_last_error()
     assert lib.hc_read_status(None, 1, None, None) == _lib.HC_ERR_INVALID
     rc = lib.hc_gather_store(2, None, None, 0, None, 128, 16, None, None, None, None, None, None, None, 1, 4, None, None,
-                             0, None)
+                             0, None, None)
     assert rc == _lib.HC_ERR_INVALID
     assert b"null pointer" in lib.hc_last_error()
     assert lib.hc_decode_num_parts(None, 1, 4) == -1

@@ -233,3 +233,25 @@ def test_set_bits_matches_numpy(dev, kind):
             v = x[:k]
             ref[v[(v >= 0) & (v < nbits)]] = True
             assert np.array_equal(np.unpackbits(got2[j].view(np.uint8), bitorder="little").astype(bool), ref)
+
+
+def test_set_bits_row_order_matches_reordered_lists(dev):
+    """hc_set_bits(row_of): set j takes its list from row row_of[j] of a
+    larger selection, the same bitmaps as the reordered lists copied first."""
+    rng = np.random.default_rng(5)
+    nbits, rows, width = 131072, 10, 50000
+    idx = np.stack([np.sort(rng.choice(nbits, size=width, replace=False)) for _ in range(rows)]).astype(np.int32)
+    order = np.asarray([7, 2, 9, 2], dtype=np.int64)
+    words = nbits // 32
+    got = torch.zeros((len(order), words), dtype=torch.int32, device=dev)
+    ref = torch.zeros_like(got)
+    ti = torch.tensor(idx, device=dev)
+    ops.set_bits(ti, None, got, nbits, fixed_count=40000, row_of=torch.tensor(order, device=dev))
+    ops.set_bits(ti[torch.tensor(order, device=dev)].contiguous(), None, ref, nbits, fixed_count=40000)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    g = got.cpu().numpy()
+    for j, r in enumerate(order):
+        want = np.zeros(words * 32, dtype=bool)
+        want[idx[r, :40000]] = True
+        assert np.array_equal(np.unpackbits(g[j].view(np.uint8), bitorder="little").astype(bool), want)

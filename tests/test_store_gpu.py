@@ -285,3 +285,39 @@ def test_stream_read_reads_and_leaves_the_sink(dev):
         ops.stream_read(buf[:3], sink=sink)
     with pytest.raises(_lib.HCError):
         ops.stream_read(buf, workgroups_per_cu=0, sink=sink)
+
+
+def test_gather_sets_row_lengths_in_the_launch(dev):
+    """hc_gather_store(set_len=row_len): the copied rows' device lengths
+    become their counts in the same launch (gated rows keep theirs, rows
+    outside the plan keep theirs), and the stores equal a gather followed
+    by set_lengths."""
+    from heterocache_amd import ops
+    B, H, L = 1, 6, 300
+    k = rand((B, H, L, 128), torch.bfloat16, dev, 11)
+    v = rand((B, H, L, 128), torch.bfloat16, dev, 12)
+    a = KVStore([L + 8] * H, torch.bfloat16, dev)
+    b = KVStore([L + 8] * H, torch.bfloat16, dev)
+    a.set_lengths([5] * H)
+    b.set_lengths([5] * H)
+    rows, counts = [0, 2, 3, 5], [300, 17, 0, 64]
+    g = torch.Generator(device="cpu").manual_seed(13)
+    idx = torch.sort(torch.randint(0, L, (len(rows), 300), generator=g), dim=1).values.to(torch.int32).to(dev)
+    plan = a.plan_rows(k, [(0, r) for r in rows], rows, counts, idx=idx)
+    a.launch_rows(plan, k, v, idx=idx, set_len=False, write_len=True)
+    b.write_rows(k, v, [(0, r) for r in rows], rows, counts, idx=idx)
+    torch.cuda.synchronize()
+    assert a.row_len.tolist() == [300, 5, 17, 0, 5, 64]
+    assert a.row_len.tolist() == b.row_len.tolist()
+    for r, n in zip(rows, counts):
+        if n:
+            xa, ya = a.read_rows([r], n)
+            xb, yb = b.read_rows([r], n)
+            assert torch.equal(xa, xb) and torch.equal(ya, yb)
+    # Gated off: lengths stay.
+    trig = torch.zeros(1, dtype=torch.int32, device=dev)
+    ops.gather_store(k, v, plan["src_off"], plan["tok_stride"], plan["src_len"], idx, plan["idx_off"], plan["counts"],
+                     plan["rows"], a.k, a.v, a.row_tile_off, plan["max_count"], trigger=trig, trig_of=None,
+                     set_len=a.row_len)
+    torch.cuda.synchronize()
+    assert a.row_len.tolist() == [300, 5, 17, 0, 5, 64]
