@@ -86,7 +86,7 @@ SIGNATURES = {
                               c_void_p]),
     "hc_cake_workspace_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "hc_select_topk": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_int, c_void_p, c_int64, c_void_p,
-                               c_void_p, c_size_t, c_void_p, c_size_t, c_void_p]),
+                               c_void_p, c_size_t, c_void_p, c_size_t, c_int, c_void_p]),
     "hc_select_hist_size": (c_size_t, [c_int]),
     "hc_select_scratch_size": (c_size_t, [c_int, c_int]),
     "hc_set_bits": (c_int, [c_void_p, c_int64, c_void_p, c_int, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p,

@@ -838,7 +838,7 @@ class HeteroCache(DynamicCache):
             J = len(jp["heads"])
             sc_all = compress.last_query_scores(query_states, key_states, jp["heads"], G, self.pooling,
                                                 self.kernel_size, round_dtype=rd)
-            idx, counts = compress.select_kept(sc_all, jp["caps"], max_cap=jp["max_cap"])
+            idx, counts = compress.select_kept(sc_all, jp["caps"], max_cap=jp["max_cap"], round_dtype=rd)
             if idx.shape[1] != jp["width"]:
                 raise RuntimeError("prefill plan: index width differs from the joint selection's")
             self._joint_sel[layer_idx] = (self._tensor_key(query_states, key_states), sc_all, idx, counts)
@@ -849,9 +849,9 @@ class HeteroCache(DynamicCache):
             scores = compress.last_query_scores(query_states, key_states, pivots, G, self.pooling, self.kernel_size,
                                                 round_dtype=rd)
             if plan is not None:
-                idx, _ = compress.select_kept(scores, plan["piv_caps"], max_cap=max(K, 1))
+                idx, _ = compress.select_kept(scores, plan["piv_caps"], max_cap=max(K, 1), round_dtype=rd)
             else:
-                idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1))
+                idx, _ = compress.select_kept(scores, [K] * scores.shape[0], max_cap=max(K, 1), round_dtype=rd)
         if self.observer is not None:
             pidx = idx if jp is None else idx.view(self.bsz, J, -1)[:, n_c:].reshape(self.bsz * len(pivots), -1)
             self.observer("pivot_sets", layer=layer_idx, pivots=pivots, scores=scores, idx=pidx, K=K)
@@ -945,6 +945,7 @@ class HeteroCache(DynamicCache):
             self.attn_stats_layers += 1
         G = self.num_key_value_groups
         W = self.window_size
+        rd = self._round_dtype(query_states.dtype)
         if W > 1:
             scores = compress.window_scores(query_states, key_states, range(n_c), G, W, self.pooling,
                                             self.kernel_size, window_keep=True,
@@ -954,12 +955,12 @@ class HeteroCache(DynamicCache):
                                                 self.kernel_size, round_dtype=self._round_dtype(query_states.dtype))
         if plan is not None and "compress" in plan:
             idx, counts = compress.select_kept(scores, plan["caps"], window=W if W > 1 else 0,
-                                               max_cap=plan["max_cap"])
+                                               max_cap=plan["max_cap"], round_dtype=rd)
             if idx.shape[1] != plan["idx_width"]:
                 raise RuntimeError("prefill plan: index width differs from the selection's")
         else:
             plan = None
-            idx, counts = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0)
+            idx, counts = compress.select_kept(scores, caps_rows, window=W if W > 1 else 0, round_dtype=rd)
         if self.observer is not None:
             self.observer("prefill_select", layer=layer_idx, rows=rows, scores=scores, idx=idx, counts=counts)
         if plan is not None:
@@ -1200,7 +1201,8 @@ class HeteroCache(DynamicCache):
             ops.drift_select(scores.view(J * S, L), bm["caps_K"], K, bits, L, bm["trig_of"], nlead, B, S,
                              self.stable_threshold, trig, hist, overlap=bm["overlap"])
             if bm["retrieve"]:
-                ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"])
+                ops.select_topk(scores[:, S - 1], bm["ret_caps"], L, idx=bm["ret_idx"], counts=bm["ret_counts"],
+                                key_bits=compress.KEY_BITS[self._round_dtype(qa.dtype)])
             if self.observer is not None:
                 self.observer("drift_check", row_ids=bm["row_ids"], scores=scores, overlap=bm["overlap"],
                               trigger=trig, trig_of=bm["trig_of"], ret_idx=bm.get("ret_idx"),

@@ -23,6 +23,10 @@ from . import _lib, ops
 
 ROUND_FLAGS = {None: 0, torch.float32: 0, torch.bfloat16: _lib.HC_SCORE_ROUND_BF16,
                torch.float16: _lib.HC_SCORE_ROUND_F16}
+# Leading bits of the float32 pattern a score rounded to that dtype can set
+# (bfloat16: sign, exponent and 7 mantissa bits; float16: its 10 mantissa
+# bits below the float32 exponent): hc_select_topk's key_bits.
+KEY_BITS = {None: 0, torch.float32: 0, torch.bfloat16: 16, torch.float16: 19}
 
 
 def _check_qk(q, k):
@@ -173,11 +177,14 @@ def pivot_step_scores(q_steps, store, rows, heads, group, seq_len, pooling="avgp
     return out.view(q_off.numel(), S, seq_len)
 
 
-def select_kept(scores, caps, window=0, max_cap=None, stream=None):
+def select_kept(scores, caps, window=0, max_cap=None, stream=None, round_dtype=None):
     """Ascending kept positions [jobs, max_cap (+window)] and counts [jobs].
 
     scores: [jobs, span] float32 (span excludes a force-kept window).
     caps: per-job budgets (python ints or an int32 device tensor).
+    round_dtype: the dtype the scores were rounded to by the reference's
+    cast chain (non-negative scores; the selection then runs fewer radix
+    passes, with the same result).
     """
     jobs, span = scores.shape
     if not torch.is_tensor(caps):
@@ -187,5 +194,6 @@ def select_kept(scores, caps, window=0, max_cap=None, stream=None):
             max_cap = max(caps_list) if caps_list else 0
     width = max(1, min(max_cap if max_cap is not None else span + window, span + window))
     idx = torch.empty((jobs, width), dtype=torch.int32, device=scores.device)
-    idx, counts = ops.select_topk(scores, caps, span, window=window, idx=idx, stream=stream)
+    idx, counts = ops.select_topk(scores, caps, span, window=window, idx=idx, stream=stream,
+                                  key_bits=KEY_BITS.get(round_dtype, 0))
     return idx, counts

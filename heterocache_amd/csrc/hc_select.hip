@@ -163,7 +163,7 @@ __global__ __launch_bounds__(kSelThreads) void select_count_kernel(const float* 
                                                                    const unsigned* __restrict__ ghist,
                                                                    int* __restrict__ state, int* __restrict__ cnt,
                                                                    int32_t* __restrict__ counts, int nchunks,
-                                                                   int32_t* __restrict__ zero_out) {
+                                                                   int32_t* __restrict__ zero_out, int npass) {
   const int job = blockIdx.y, chunk = blockIdx.x;
   const SelJob jb = sel_job(caps, job, span, window, idx_stride);
   if (chunk == 0 && threadIdx.x == 0 && counts) counts[job] = jb.body + jb.tail;
@@ -171,7 +171,9 @@ __global__ __launch_bounds__(kSelThreads) void select_count_kernel(const float* 
   if (jb.body <= 0 || jb.body >= span) return;
   __shared__ int s_pick[3];
   __shared__ int s_red[2][kSelWaves];
-  const SelState st = sel_replay(ghist + (int64_t)job * 4 * kSelBins, jb.body, 4, s_pick);
+  // With npass < 4 the keys' remaining low digits are zero (the caller's
+  // contract), so the picked prefix is the key itself.
+  const SelState st = sel_replay(ghist + (int64_t)job * 4 * kSelBins, jb.body, npass, s_pick);
   const uint32_t tau = st.prefix;
   if (chunk == 0 && threadIdx.x == 0) {
     int* sp = state + job * 4;
@@ -766,10 +768,14 @@ extern "C" size_t hc_select_scratch_size(int njobs, int span) {
 
 extern "C" int hc_select_topk(const float* scores, int64_t score_stride, int njobs, int span, const int32_t* caps,
                               int window, int32_t* idx, int64_t idx_stride, int32_t* counts, void* hist,
-                              size_t hist_bytes, void* scratch, size_t scratch_bytes, void* stream) {
+                              size_t hist_bytes, void* scratch, size_t scratch_bytes, int key_bits, void* stream) {
   clear_error();
   if (njobs < 0 || njobs > 65535 || span < 0 || window < 0)
     return set_error(HC_ERR_INVALID, "hc_select_topk: njobs=%d span=%d window=%d", njobs, span, window);
+  if (key_bits < 0 || key_bits > 32)
+    return set_error(HC_ERR_INVALID, "hc_select_topk: key_bits=%d (0..32)", key_bits);
+  // Radix passes: the 8-bit digits that can differ between the scores' keys.
+  const int npass = key_bits == 0 ? 4 : std::max(1, (key_bits + 7) / 8);
   if (njobs == 0) return HC_OK;
   if (!scores || !caps || !idx || !hist || !scratch)
     return set_error(HC_ERR_INVALID, "hc_select_topk: null pointer argument");
@@ -786,7 +792,7 @@ extern "C" int hc_select_topk(const float* scores, int64_t score_stride, int njo
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(nchunks > 0 ? nchunks : 1, njobs);
   if (nchunks > 0) {
-    for (int pass = 0; pass < 4; ++pass) {
+    for (int pass = 0; pass < npass; ++pass) {
       hipLaunchKernelGGL(select_hist_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, window,
                          idx_stride, ghist, pass);
       int rc = check_launch("hc_select_topk(hist)");
@@ -794,7 +800,7 @@ extern "C" int hc_select_topk(const float* scores, int64_t score_stride, int njo
     }
   }
   hipLaunchKernelGGL(select_count_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, window,
-                     idx_stride, ghist, state, cnt, counts, nchunks, (int32_t*)nullptr);
+                     idx_stride, ghist, state, cnt, counts, nchunks, (int32_t*)nullptr, npass);
   int rc = check_launch("hc_select_topk(count)");
   if (rc) return rc;
   hipLaunchKernelGGL(select_write_kernel, grid, dim3(kSelThreads), 0, s, scores, score_stride, span, caps, window,

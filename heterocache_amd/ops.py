@@ -631,8 +631,9 @@ def cake_score(q, q_off, q_head_stride, q_row_stride, k, k_off, k_tok_stride, ba
     return out, stats
 
 
-def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None):
-    """Ascending kept positions per job: scores [jobs, >= span] float32, caps int32 [jobs]."""
+def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None, key_bits=0):
+    """Ascending kept positions per job: scores [jobs, >= span] float32, caps int32 [jobs].
+    key_bits: see hc_select_topk (KEY_BITS[round dtype] for cast-chain scores)."""
     lib = _lib.load()
     _require_cuda(scores, caps, idx, counts)
     if scores.dtype != torch.float32 or scores.dim() != 2 or scores.stride(1) != 1:
@@ -649,7 +650,7 @@ def select_topk(scores, caps, span, window=0, idx=None, counts=None, stream=None
                           device=scores.device)
     _lib.check(lib.hc_select_topk(_ptr(scores), scores.stride(0), njobs, int(span), _ptr(caps), int(window), _ptr(idx),
                                   idx.stride(0), _ptr(counts), _ptr(hist), hist.numel(), _ptr(scratch),
-                                  scratch.numel(), _stream(stream, scores)))
+                                  scratch.numel(), int(key_bits), _stream(stream, scores)))
     return idx, counts
 
 

@@ -447,10 +447,15 @@ size_t hc_cake_workspace_size(int batch, int kv_heads, int seq_len, int group, i
  * Replaces topk -> mask -> sort of heterocache/cache_utils.py:831-851, the
  * SnapKV topk + window concat of heterocache/kv_cluster.py:187-197 and the
  * drift / retrieval topk of heterocache/cache_utils.py:1060-1061, 1090-1093.
+ * key_bits (0 = 32): the scores are non-negative and their float32 bit
+ * patterns end in 32 - key_bits zero bits (scores rounded to bfloat16: 16;
+ * to float16: 19, the reference's cast chain), so a radix pass per 8 of the
+ * leading key_bits suffices; the result is the one of 32.  A wrong hint
+ * ranks scores that differ only in the ignored bits as ties.
  */
 int hc_select_topk(const float* scores, int64_t score_stride, int njobs, int span, const int32_t* caps, int window,
                    int32_t* idx, int64_t idx_stride, int32_t* counts, void* hist, size_t hist_bytes, void* scratch,
-                   size_t scratch_bytes, void* stream);
+                   size_t scratch_bytes, int key_bits, void* stream);
 /* hist: hc_select_hist_size(njobs) bytes, zero-filled before its first use;
  * every completed call leaves it zeroed again (calls on one stream may share
  * it).  scratch: hc_select_scratch_size(njobs, span) bytes, no initialisation. */

@@ -334,3 +334,31 @@ def test_window_scores_with_attention_stats_128k(dev):
     qn, kn = as_np(q[0, h * G:(h + 1) * G]), as_np(k[0, h])
     ref = O.window_scores(qn[None], kn[None], "maxpool", 7, window_keep=True)[0]
     assert rel_err(as_np(s1[h]), ref) < 2e-4
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_select_with_key_bits_equals_all_passes(dev, dt):
+    """hc_select_topk's key_bits for scores rounded by the cast chain (16 for
+    bfloat16, 19 for float16: two and three radix passes instead of four):
+    the kept sets and counts are the four-pass ones, also where most scores
+    tie (a handful of distinct values) and where the budget cuts inside a
+    tie run, and they match the oracle's ranking."""
+    rng = np.random.default_rng(7)
+    jobs, span = 6, 40000
+    base = rng.random((jobs, span)) ** 3
+    base[1] = rng.integers(0, 4, span) / 7.0          # four distinct values
+    base[2] = 0.25                                     # all equal
+    base[3, ::3] = 0.0                                 # zeros among the rest
+    s = torch.tensor(base, dtype=torch.float32).to(dt).to(torch.float32).to(dev)
+    caps = torch.tensor([1000, 12345, 777, 39999, 1, 20000], dtype=torch.int32, device=dev)
+    a_idx, a_cnt = ops.select_topk(s, caps, span, idx=torch.empty((jobs, span), dtype=torch.int32, device=dev))
+    b_idx, b_cnt = ops.select_topk(s, caps, span, idx=torch.empty((jobs, span), dtype=torch.int32, device=dev),
+                                   key_bits=compress.KEY_BITS[dt])
+    torch.cuda.synchronize()
+    assert torch.equal(a_cnt, b_cnt)
+    sn = s.cpu().numpy()
+    for j in range(jobs):
+        n = int(a_cnt[j])
+        assert torch.equal(a_idx[j, :n], b_idx[j, :n]), j
+        want = np.sort(O.topk_select(sn[j], int(caps[j])))
+        assert np.array_equal(b_idx[j, :n].cpu().numpy(), want), j
