@@ -818,7 +818,10 @@ class CacheOracle:
     oracle's own scores there and substitute a device's, so that the flow's
     integer logic (top-k and its tie rule, overlaps, medians, triggers,
     ascending prefixes, slot writes) is checked exactly on the device's
-    scores while the scores themselves are compared within a tolerance.
+    scores while the scores themselves are compared within a tolerance.  A
+    hook with a true `replaces_drift` attribute is called with scores None
+    for "drift" and returns the [B, S, L] scores outright, so the oracle
+    does not score the step queries itself.
     """
 
     def __init__(self, data, batch, q_heads, kv_heads, num_layers, ratio, threshold, decode_step, pooling, kernel,
@@ -938,10 +941,16 @@ class CacheOracle:
             leader = int(leader_s)
             if not members:
                 continue
-            sc = np.stack([pivot_step_scores(qs[b, leader * self.G:(leader + 1) * self.G],
-                                             self.rows[layer][b * self.Hkv + leader][0][:self.L], self.pooling,
-                                             self.kernel, io_dtype=self.io_dtype) for b in range(self.B)])
-            sc = self._scores("drift", layer, leader, sc)
+            if getattr(self.score_hook, "replaces_drift", False):
+                # The hook supplies the step scores itself (a device's), and
+                # the oracle's own float64 scoring of the step queries is
+                # skipped: a long run replays the integer flow at every check.
+                sc = np.asarray(self.score_hook("drift", layer, leader, None))
+            else:
+                sc = np.stack([pivot_step_scores(qs[b, leader * self.G:(leader + 1) * self.G],
+                                                 self.rows[layer][b * self.Hkv + leader][0][:self.L], self.pooling,
+                                                 self.kernel, io_dtype=self.io_dtype) for b in range(self.B)])
+                sc = self._scores("drift", layer, leader, sc)
             _, med, trig, cur_last = drift_check(sc, [sorted(s) for s in self.ref[layer][leader]], K, self.threshold)
             self.triggers.append((layer, leader, bool(trig)))
             self.medians.append((layer, leader, med))

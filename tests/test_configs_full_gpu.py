@@ -317,6 +317,92 @@ def test_config2_reference_cast_chain_fp16_128k(dev):
     assert off <= total * 1e-5, (off, total)
 
 
+class ReplayDriftScores(DeviceScores):
+    """DeviceScores whose drift scores replace the oracle's outright: the
+    oracle skips its own float64 scoring of the step queries, so a long run
+    can replay the integer flow on the device's scores at every check."""
+    replaces_drift = True
+
+    def __call__(self, kind, layer, head, s):
+        if kind == "drift":
+            return self.rec.drift[(layer, head)].pop(0)[None]
+        return super().__call__(kind, layer, head, s)
+
+
+def test_config2_needles_128k_all_1000_steps(dev):
+    """Config 2 for its whole run: 1000 decode steps at 131072 tokens, all
+    32 layers with the reference's head JSON, the full-KV tier in
+    host-pinned memory, the default configuration (bfloat16, the
+    reference's cast chain), drift check every 5 steps at threshold 0.5 and
+    top-1024 retrieval: 200 checks, every leader of every layer triggering
+    at every second one (100 retrievals per leader).
+
+    * Every check's trigger flags, for all 33 leaders, follow the needle
+      workload's schedule.
+    * Layer 23 (two leaders, relation order not ascending) is replayed by
+      the oracle's integer flow on the device's own scores at every check
+      (top-k with its tie rule, overlaps, medians, triggers, ascending
+      prefixes, slot writes): the triggers match check by check, and after
+      the 1000 steps its stores and reference sets are bit for bit the
+      oracle's.
+    * Its attention is within 2e-2 of the float64 closed form at sampled
+      steps: the first, the two after the first retrieval, and steps in the
+      middle and at the end of the run."""
+    L, Hkv, G, D, NL, S, steps = 131072, 8, 4, 128, 32, 5, 1000
+    lc = 23
+    data = llama_json()
+    rec = Recorder([lc])
+    cfg = HeteroCacheConfig(data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
+                            max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
+                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
+                            tier_placement="host")
+    cache = HeteroCache(cfg)
+    assert cache.round_scores
+    cache.observer = rec
+    wl = workloads.NeedleWorkload(L, kv_heads=Hkv, group=G, steps=steps, decode_step=S, seed=1002, device=dev)
+    hook = ReplayDriftScores(rec, 0.5)
+    orc = O.CacheOracle(data, 1, Hkv * G, Hkv, NL, 0.5, 0.5, S, "avgpool", 5, retrieval_topk=1024,
+                        max_gen=steps + 4, score_hook=hook)
+    hook.orc = orc
+    step_inputs = {}
+    for layer in range(NL):
+        x = wl.layer(layer)
+        k, v = cache.update(x["k"], x["v"], layer)
+        cache.init_coefficient(x["q_last"], k, layer)
+        cache.prefill_select(x["q_last"], k, v, layer)
+        if layer == lc:
+            orc.prefill(layer, as_np(x["q_last"]), as_np(x["k"]), as_np(x["v"]))
+        step_inputs[layer] = (x["q_steps"], x["k_new"], x["v_new"])
+        del x, k, v
+    assert cache.tier_mode == "host"
+    sampled = {0, 10, 11, 500, 999}
+    for t in range(steps):
+        out = None
+        for layer in range(NL):
+            q, kn, vn = (a[t] for a in step_inputs[layer])
+            cache.update(kn, vn, layer)
+            o = cache.decode_attention(q, layer)
+            cache.decode_select(q, layer)
+            if layer == lc:
+                out = o
+        q, kn, vn = (as_np(a[t]) for a in step_inputs[lc])
+        ref = orc.decode(lc, q, kn, vn, attend=t in sampled)
+        if ref is not None:
+            err = np.abs(as_np(out).reshape(1, Hkv * G, D) - ref).max()
+            assert err <= ATTN_TOL, f"step {t}: max-abs {err}"
+    torch.cuda.synchronize()
+    assert len(rec.checks) == steps // S
+    for c, flags in enumerate(rec.checks):
+        assert len(flags) == 33
+        assert all(f == (c % 2 == 1) for f in flags.values()), (c, flags)
+    assert not any(rec.drift.values())  # every recorded check was replayed
+    dev_trig = [(lc, h, rec.checks[c][(lc, h)]) for c in range(len(rec.checks)) for h in cache._drift[lc].leaders]
+    assert dev_trig == orc.triggers
+    assert sum(t for *_, t in orc.triggers) == len(cache._drift[lc].leaders) * steps // S // 2
+    check_stores(cache, orc, [lc], 1, Hkv)
+    check_ref_sets(cache, orc, [lc], L)
+
+
 def test_config4_chunked_224k_then_drift_block(dev):
     """Config 4: Llama-3-8B shape at 229376 tokens, all 32 layers with the
     reference's head JSON.  An 8K-chunked prefill (chunks fed layer by

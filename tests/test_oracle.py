@@ -563,7 +563,7 @@ def _hand_case_data():
             "allocation_matrix": [[0.5, 1.5, -1.0]]}
 
 
-def _hand_case_run(select_first):
+def _hand_case_run(select_first, score_hook=None):
     """L = 16, d = 128, G = 1, decode_step 2, kernel-1 average pooling (the
     scores are the softmax itself).  Every key holds its position t in
     channel 0, so a query +e0 ranks positions t descending and -e0
@@ -582,7 +582,7 @@ def _hand_case_run(select_first):
     q = np.zeros((1, H, L, d))
     q[0, :, -1, 0] = 1.0
     orc = O.CacheOracle(_hand_case_data(), 1, H, H, 1, 0.5, 0.5, 2, "avgpool", 1,
-                        select_before_attention=select_first)
+                        select_before_attention=select_first, score_hook=score_hook)
     orc.prefill(0, q, k, v)
     signs = [+1, +1, +1, -1, -1, -1]   # the pivot's query direction per decode step
     outs, refs = [], []
@@ -633,6 +633,41 @@ def test_cache_oracle_hand_worked_drift_and_retrieval(select_first):
     assert abs(got - expect) < 1e-9
     # Before any retrieval satellite 0 attends its prompt picks {14, 15}.
     assert abs(outs[0][0, 0, 0] - (14 + 15 + 1000) / 3) < 1e-9
+
+
+class _StepRanks:
+    """Drift-score hook that replaces the oracle's scoring: rankings of the
+    hand case's step queries (+e0 ranks positions descending, -e0
+    ascending), one [1, 2, 16] array per check."""
+    replaces_drift = True
+
+    def __init__(self):
+        self.calls = []
+
+    def __call__(self, kind, layer, head, s):
+        if kind != "drift":
+            return s
+        assert s is None
+        signs = [(+1, +1), (+1, -1), (-1, -1)][len(self.calls)]
+        self.calls.append((layer, head))
+        return np.stack([sg * np.arange(16.0) for sg in signs])[None]
+
+
+@pytest.mark.parametrize("select_first", [False, True])
+def test_cache_oracle_replaced_drift_scores_give_the_same_flow(select_first):
+    """A hook that supplies the step scores outright (the oracle skips its own
+    scoring) drives the same checks, triggers, sets and retrievals as the
+    oracle's own scores: only the rankings enter the integer flow."""
+    own, own_outs, own_refs = _hand_case_run(select_first)
+    hook = _StepRanks()
+    rep, rep_outs, rep_refs = _hand_case_run(select_first, score_hook=hook)
+    assert hook.calls == [(0, 2)] * 3
+    assert rep.triggers == own.triggers == [(0, 2, False), (0, 2, False), (0, 2, True)]
+    assert rep_refs == own_refs
+    for (ka, va), (kb, vb) in zip(rep.rows[0], own.rows[0]):
+        assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+    for a, b in zip(rep_outs, own_outs):
+        assert np.array_equal(a, b)
 
 
 def test_drift_check_even_median_is_not_below_threshold():
