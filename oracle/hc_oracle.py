@@ -17,6 +17,8 @@ Pinning of each function (beyond its own formula) -- tests/test_oracle.py:
       max_pool1d) on random inputs, and closed forms (uniform scores).
   topk_select                     brute force over all subsets on tiny
       inputs; torch.topk on distinct scores.
+  topk_set                        equals the sorted topk_indices list on
+      random, heavily tied and edge-case (k = 0, k >= n) inputs.
   window_scores                   reduces to last_query_scores at W=1 and to
       snapkv_update_kv at G=1 (the two reference functions it generalises).
   decode_attention                float64 closed form vs torch SDPA; a
@@ -564,6 +566,23 @@ def topk_indices(scores, k):
     return order[:k].astype(np.int64)
 
 
+def topk_set(scores, k):
+    """The positions topk_indices(scores, k) selects, ascending, in linear
+    time: every score above the k-th largest value, then the lowest
+    positions among the scores equal to it (the same tie rule).  The drift
+    check and the retrieval take their sets this way; `scores` holds no NaN."""
+    s = np.asarray(scores, dtype=np.float64)
+    n = s.size
+    if k <= 0:
+        return np.empty(0, dtype=np.int64)
+    if k >= n:
+        return np.arange(n, dtype=np.int64)
+    tau = np.partition(s, n - k)[n - k]
+    above = np.flatnonzero(s > tau)
+    tied = np.flatnonzero(s == tau)[:k - above.size]
+    return np.sort(np.concatenate([above, tied])).astype(np.int64)
+
+
 def topk_select(scores, cap):
     """Kept token set of one head, ascending positions.
 
@@ -701,16 +720,18 @@ def drift_check(step_scores, ref_set, base_len, threshold):
     heterocache/cache_utils.py:1059-1080.  step_scores: [B, S, L];
     ref_set: [B, K] indices.  overlap_s = mean_b |topK_s ∩ ref_b| / K;
     coefficient = statistics.median(overlap); trigger = coefficient < thr.
-    Returns (overlaps [S], median, trigger, cur_last [B, K] (topK of last step)).
+    Returns (overlaps [S], median, trigger, cur_last [B, K] (topK of the last
+    step, ascending)).
     """
     B, S, L = step_scores.shape
     overl = np.zeros((B, S), dtype=np.float64)
     cur_last = []
     for b in range(B):
-        ref = set(np.asarray(ref_set[b]).tolist())
+        ref = np.zeros(L, dtype=bool)
+        ref[np.asarray(ref_set[b], dtype=np.int64)] = True
         for s in range(S):
-            cur = topk_indices(step_scores[b, s], base_len)
-            overl[b, s] = np.float32(len(ref.intersection(cur.tolist()))) / np.float32(base_len)
+            cur = topk_set(step_scores[b, s], base_len)
+            overl[b, s] = np.float32(np.count_nonzero(ref[cur])) / np.float32(base_len)
             if s == S - 1:
                 cur_last.append(cur)
     overlaps = overl.astype(np.float32).mean(axis=0, dtype=np.float32)
@@ -741,7 +762,7 @@ def retrieval_indices(last_step_scores, lengths):
     squeeze() makes the B=1 case the defined one).
     """
     mk = max(lengths) if lengths else 0
-    idx = np.sort(topk_indices(last_step_scores, mk))
+    idx = topk_set(last_step_scores, mk)
     return [idx[:n] for n in lengths]
 
 
@@ -951,7 +972,8 @@ class CacheOracle:
                                                  self.rows[layer][b * self.Hkv + leader][0][:self.L], self.pooling,
                                                  self.kernel, io_dtype=self.io_dtype) for b in range(self.B)])
                 sc = self._scores("drift", layer, leader, sc)
-            _, med, trig, cur_last = drift_check(sc, [sorted(s) for s in self.ref[layer][leader]], K, self.threshold)
+            ref = [np.fromiter(s, dtype=np.int64, count=len(s)) for s in self.ref[layer][leader]]
+            _, med, trig, cur_last = drift_check(sc, ref, K, self.threshold)
             self.triggers.append((layer, leader, bool(trig)))
             self.medians.append((layer, leader, med))
             if not trig:

@@ -500,6 +500,74 @@ def test_config4_chunked_224k_then_drift_block(dev):
     check_ref_sets(chunked, orc, checked, L)
 
 
+def test_config4_224k_all_2000_steps(dev):
+    """Config 4's decode run in full: 229376 tokens, all 32 layers with the
+    reference's head JSON, the default configuration (bfloat16, the
+    reference's cast chain), full-KV tier in host-pinned memory, top-1024
+    retrieval, and 2000 decode steps whose attention moves to a new block of
+    8 keys every 200 steps: of the 400 checks exactly the 9 after a block
+    change trigger, each for all 33 leaders.  Layer 23 is replayed by the
+    oracle's integer flow on the device's scores at every check: triggers
+    check by check, stores and reference sets bit for bit after the run,
+    attention within 2e-2 of float64 at sampled steps.  (The chunked
+    prefill's equality with a single-shot one is the 205-step test's.)"""
+    L, Hkv, G, D, NL, S, steps, period = 229376, 8, 4, 128, 32, 5, 2000, 200
+    lc = 23
+    data = llama_json()
+    rec = Recorder([lc])
+    cfg = HeteroCacheConfig(data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
+                            max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
+                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=1024,
+                            tier_placement="host")
+    cache = HeteroCache(cfg)
+    assert cache.round_scores
+    cache.observer = rec
+    wl = workloads.BlockDriftWorkload(L, kv_heads=Hkv, group=G, steps=steps, period=period, seed=1004, device=dev)
+    hook = ReplayDriftScores(rec, 0.5)
+    orc = O.CacheOracle(data, 1, Hkv * G, Hkv, NL, 0.5, 0.5, S, "avgpool", 5, retrieval_topk=1024,
+                        max_gen=steps + 4, score_hook=hook)
+    hook.orc = orc
+    step_inputs = {}
+    for layer in range(NL):
+        k, v = wl.prefill(layer)
+        x = wl.queries(layer, k)
+        kc, vc = cache.update(k, v, layer)
+        cache.init_coefficient(x["q_last"], kc, layer)
+        cache.prefill_select(x["q_last"], kc, vc, layer)
+        if layer == lc:
+            orc.prefill(layer, as_np(x["q_last"]), as_np(k), as_np(v))
+        step_inputs[layer] = (x["q_steps"], x["k_new"], x["v_new"])
+        del k, v, kc, vc, x
+    assert cache.tier_mode == "host" and cache.base_compress_len == orc.base == 86851
+    sampled = {0, 200, 201, 1000, 1800, 1999}
+    for t in range(steps):
+        out = None
+        for layer in range(NL):
+            q, kn, vn = (a[t] for a in step_inputs[layer])
+            cache.update(kn, vn, layer)
+            o = cache.decode_attention(q, layer)
+            cache.decode_select(q, layer)
+            if layer == lc:
+                out = o
+        q, kn, vn = (as_np(a[t]) for a in step_inputs[lc])
+        ref = orc.decode(lc, q, kn, vn, attend=t in sampled)
+        if ref is not None:
+            err = np.abs(as_np(out).reshape(1, Hkv * G, D) - ref).max()
+            assert err <= ATTN_TOL, f"step {t}: max-abs {err}"
+    torch.cuda.synchronize()
+    assert len(rec.checks) == steps // S == 400
+    change = {c for c in range(400) if c > 0 and (c * S) % period == 0}
+    assert len(change) == 9
+    for c, flags in enumerate(rec.checks):
+        assert len(flags) == 33
+        assert all(f == (c in change) for f in flags.values()), (c, [k for k, f in flags.items() if f != (c in change)])
+    assert not any(rec.drift.values())  # every recorded check was replayed
+    dev_trig = [(lc, h, rec.checks[c][(lc, h)]) for c in range(len(rec.checks)) for h in cache._drift[lc].leaders]
+    assert dev_trig == orc.triggers
+    check_stores(cache, orc, [lc], 1, Hkv)
+    check_ref_sets(cache, orc, [lc], L)
+
+
 @pytest.mark.parametrize("ctx", [16384, 32768, 49152, 65536])
 def test_config3_qwen_sequence_full_context(dev, ctx):
     """Config 3, one sequence of the ragged batch per run (the reference's

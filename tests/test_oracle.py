@@ -188,6 +188,24 @@ def test_topk_select_brute_force_with_ties():
         assert winners == [tuple(sel.tolist())]
 
 
+def test_topk_set_equals_the_sorted_topk_list():
+    """The linear-time selection of the drift check and the retrieval keeps
+    exactly the positions of topk_indices (same tie rule), ascending: on
+    distinct, heavily tied (few distinct values, bfloat16-rounded) and
+    all-equal scores, signed zeros among them, and at k = 0, 1, n - 1, n
+    and beyond n."""
+    rng = np.random.default_rng(31)
+    n = 3000
+    cases = [rng.standard_normal(n), rng.integers(0, 7, n).astype(np.float64), np.zeros(n),
+             torch.tensor(rng.random(n)).to(torch.bfloat16).float().numpy(),
+             np.where(rng.random(n) < 0.5, -0.0, 0.0) + (rng.random(n) < 0.1)]
+    for s in cases:
+        for k in (0, 1, 2, 17, 700, n // 2, n - 1, n, n + 5):
+            got = O.topk_set(s, k)
+            ref = np.sort(O.topk_indices(s, k))
+            assert got.dtype == np.int64 and np.array_equal(got, ref), k
+
+
 def test_topk_matches_torch_on_distinct_scores():
     s = np.random.default_rng(10).permutation(5000).astype(np.float32)
     ref = torch.topk(torch.tensor(s), 700).indices.numpy()
