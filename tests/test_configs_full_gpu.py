@@ -639,6 +639,71 @@ def test_config3_qwen_sequence_full_context(dev, ctx):
     check_ref_sets(cache, orc, checked, ctx)
 
 
+def test_config3_qwen_64k_200_steps_default_configuration(dev):
+    """Config 3's longest sequence (65536 tokens) over 200 decode steps in the
+    default configuration (bfloat16, the reference's cast chain), Qwen order
+    (select before attention), top-512 retrieval every 5 steps: 40 checks,
+    every leader triggering at every second one.  The first layer with a
+    satellite is replayed by the oracle's integer flow on the device's
+    scores at every check; its stores and reference sets are bit for bit
+    the oracle's after the run, and its attention is within 2e-2 of float64
+    at sampled steps (a retrieval is attended in its own step here)."""
+    ctx, Hkv, G, D, NL, S, steps = 65536, 4, 7, 128, 28, 5, 200
+    raw = workloads.synthetic_head_json(NL, Hkv, 1003, max_full=14)
+    data = utils.augment_head_data(raw, [utils.head_permutation(r) for r in raw["classification_matrix"]])
+    lc = next(l for l in range(NL) if any(data["leader_member_relations"][l].values()))
+    rec = Recorder([lc])
+    cfg = HeteroCacheConfig(data, compression_ratio=0.25, stable_threshold=0.5, real_offload=True,
+                            max_gen_len=steps + 4, decode_step=S, pooling="avgpool", kernel_size=5,
+                            num_attn_heads=Hkv * G, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=512)
+    cache = HeteroCache(cfg)
+    assert cache.round_scores
+    cache.observer = rec
+    wl = workloads.NeedleWorkload(ctx, kv_heads=Hkv, group=G, steps=steps, decode_step=S, seed=1003 + ctx, device=dev)
+    hook = ReplayDriftScores(rec, 0.5)
+    orc = O.CacheOracle(data, 1, Hkv * G, Hkv, NL, 0.25, 0.5, S, "avgpool", 5, retrieval_topk=512,
+                        select_before_attention=True, max_gen=steps + 4, score_hook=hook)
+    hook.orc = orc
+    step_inputs = {}
+    for layer in range(NL):
+        x = wl.layer(layer)
+        k, v = cache.update(x["k"], x["v"], layer)
+        cache.init_coefficient(x["q_last"], k, layer)
+        cache.prefill_select(x["q_last"], k, v, layer)
+        if layer == lc:
+            orc.prefill(layer, as_np(x["q_last"]), as_np(x["k"]), as_np(x["v"]))
+        step_inputs[layer] = (x["q_steps"], x["k_new"], x["v_new"])
+        del x, k, v
+    sampled = {0, 9, 10, 100, 199}
+    for t in range(steps):
+        out = None
+        for layer in range(NL):
+            q, kn, vn = (a[t] for a in step_inputs[layer])
+            cache.update(kn, vn, layer)
+            cache.decode_select(q, layer)
+            o = cache.decode_attention(q, layer)
+            if layer == lc:
+                out = o
+        q, kn, vn = (as_np(a[t]) for a in step_inputs[lc])
+        ref = orc.decode(lc, q, kn, vn, attend=t in sampled)
+        if ref is not None:
+            err = np.abs(as_np(out).reshape(1, Hkv * G, D) - ref).max()
+            assert err <= ATTN_TOL, f"step {t}: max-abs {err}"
+    torch.cuda.synchronize()
+    nlead = sum(len(r) for r in data["leader_member_relations"])
+    flags = {}
+    for f in rec.checks:
+        for key, val in f.items():
+            flags.setdefault(key, []).append(val)
+    pattern = [c % 2 == 1 for c in range(steps // S)]
+    assert len(flags) == nlead and all(v == pattern for v in flags.values())
+    assert not any(rec.drift.values())
+    dev_trig = [(lc, h, flags[(lc, h)][c]) for c in range(steps // S) for h in cache._drift[lc].leaders]
+    assert dev_trig == orc.triggers
+    check_stores(cache, orc, [lc], 1, Hkv)
+    check_ref_sets(cache, orc, [lc], ctx)
+
+
 def _sdpa_repeated_kv(module, query, key, value, attention_mask, dropout=0.0, scaling=None, is_causal=None,
                       **kwargs):
     """transformers attention function for the float32 stock reference:
