@@ -549,7 +549,11 @@ def time_decode_steps(torch, stores, q, kn, vn, outs, scale, steps, chunk=None, 
         G = q.shape[2]
         cts, parts = [], []
         for st in stores:
-            ct = chunk or ops.decode_chunk_tiles(st.host_len + 1, G, q.dtype)
+            # The chunk whose grid fits one resident round at the lengths
+            # the last replay reaches (chosen for the first replay's
+            # lengths, rows that cross a chunk boundary during the replays
+            # would push a workgroup into a second round).
+            ct = chunk or ops.decode_chunk_tiles(st.host_len + 1 + steps, G, q.dtype)
             cts.append(ct)
             parts.append(ops.decode_num_parts(st.host_len + 1 + steps, ct))
         rows = stores[0].rows
