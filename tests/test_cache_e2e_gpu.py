@@ -44,12 +44,14 @@ def head_data(seed=0):
 
 
 def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=10, batched=True, groups=1,
-        chunks=None, tier="host", overlap=False):
-    """tier: "host" / "device" placement of the full-KV tier, or "prefill"
-    (real_offload=False: the prefill K/V kept as the tier).  overlap: batched
-    checks on the side stream (overlap_drift_check).  The prefill runs as the
-    model's attention runs it (prefill_stat_rows asks for no statistics at
-    window_size 1)."""
+        chunks=None, tier="host", overlap=False, stream="auto", one_pass=True, budget=None, expect_tier=None):
+    """tier: "host" / "device" / "auto" placement of the full-KV tier, or
+    "prefill" (real_offload=False: the prefill K/V kept as the tier); with
+    "auto", budget is tier_device_budget and expect_tier the placement it
+    must choose.  overlap: batched checks on the side stream
+    (overlap_drift_check).  stream: retrieval_stream.  one_pass:
+    one_pass_drift_check.  The prefill runs as the model's attention runs it
+    (prefill_stat_rows asks for no statistics at window_size 1)."""
     torch.manual_seed(0)
     B, Hq, Hkv, NL, D = 1, 32, 8, 2, 128
     data = head_data()
@@ -58,7 +60,8 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
                             num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, retrieval_topk=topk,
                             reference_quirks=quirks, batched_drift_check=batched, drift_check_groups=groups,
                             tier_placement="host" if tier == "prefill" else tier, overlap_drift_check=overlap,
-                            round_scores=False)
+                            round_scores=False, retrieval_stream=stream, one_pass_drift_check=one_pass,
+                            tier_device_budget=budget)
     cache = HeteroCache(cfg)
     if chunks is not None:
         cache.begin_prefill(L)
@@ -118,10 +121,10 @@ def run(dev, dtype, select_first=False, topk=None, quirks=False, L=2048, steps=1
                 for i, leader in enumerate(st.leaders):
                     triggers.append((layer, leader, bool(st.trigger[i].item())))
     torch.cuda.synchronize()
-    assert cache.tier_mode == tier
+    assert cache.tier_mode == (expect_tier or tier)
     # Batched checks in Llama order score in one pass from the statistics the
     # decode launches reported (every cycle, the first included).
-    one_pass = batched and not select_first
+    one_pass = one_pass and batched and not select_first
     assert cache.one_pass_checks == ((steps // 5) * groups if one_pass else 0)
     assert cache.attn_stats_layers == 0
     assert triggers == orc.triggers
@@ -179,6 +182,31 @@ def test_tier_placements(dev, tier, select_first):
     one gather from the arena)."""
     trig = run(dev, torch.float32, select_first=select_first, topk=64, tier=tier)
     assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
+
+
+@pytest.mark.parametrize("tier,stream", [("device", "side"), ("host", "main")])
+def test_retrieval_stream_choices(dev, tier, stream):
+    """The retrieval gathers on the stream the default does not pick for the
+    tier (per-layer gathers and events on the side stream for the HBM tier,
+    one gather on the check's stream for the host tier): same outputs,
+    triggers and stores."""
+    trig = run(dev, torch.float32, topk=64, tier=tier, stream=stream)
+    assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
+
+
+def test_two_pass_drift_check(dev):
+    """one_pass_drift_check=False: the batched checks take the statistics
+    pass with stored logits (no decode-reported statistics); same outputs,
+    triggers and stores."""
+    trig = run(dev, torch.float32, one_pass=False)
+    assert [t for _, _, t in trig] == [False] * 3 + [True] * 3
+
+
+@pytest.mark.parametrize("budget,expect", [(1, "host"), (1 << 40, "device")])
+def test_auto_tier_placement_follows_the_budget(dev, budget, expect):
+    """tier_placement="auto": the tier goes to HBM when the model's whole
+    tier fits tier_device_budget bytes, to pinned host memory otherwise."""
+    run(dev, torch.float32, topk=64, tier="auto", budget=budget, expect_tier=expect)
 
 
 def test_retrieval_topk(dev):
