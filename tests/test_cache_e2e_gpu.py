@@ -279,8 +279,9 @@ def test_chunked_prefill_with_observation_window_equals_single_shot(dev):
             assert torch.equal(whole._drift[layer].ref_bits, chunked._drift[layer].ref_bits)
 
 
+@pytest.mark.parametrize("one_pass", [True, False])
 @pytest.mark.parametrize("dtype,io,step", [(torch.bfloat16, "bfloat16", 2.0 ** -7), (torch.float16, "float16", 2.0 ** -10)])
-def test_reference_cast_chain(dev, dtype, io, step):
+def test_reference_cast_chain(dev, dtype, io, step, one_pass):
     """round_scores=True (the reference's casts of logits, probabilities and
     pooled scores to the model dtype) on a bfloat16 model and on a float16
     one (the reference's load dtype), the drift checks in one pass over the
@@ -289,13 +290,16 @@ def test_reference_cast_chain(dev, dtype, io, step):
     integer flow run on the device scores reproduces the
     triggers and the stores bit for bit, and the attention outputs match
     the float64 closed form.  The cast scores tie massively, so this also
-    exercises the lowest-position tie rule of every selection."""
+    exercises the lowest-position tie rule of every selection.  one_pass
+    False: the checks take the two-pass scorer (statistics pass with stored
+    logits) instead."""
     from tests.test_configs_full_gpu import DeviceScores, Recorder
     B, Hq, Hkv, NL, D, L, steps = 1, 32, 8, 2, 128, 2048, 10
     data = head_data()
     cfg = HeteroCacheConfig(data=data, compression_ratio=0.5, stable_threshold=0.5, real_offload=True,
                             max_gen_len=steps + 4, decode_step=5, pooling="avgpool", kernel_size=5,
-                            num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, round_scores=True)
+                            num_attn_heads=Hq, num_kv_heads=Hkv, num_layers=NL, round_scores=True,
+                            one_pass_drift_check=one_pass)
     cache = HeteroCache(cfg)
     rec = Recorder(range(NL))
     cache.observer = rec
@@ -327,9 +331,9 @@ def test_reference_cast_chain(dev, dtype, io, step):
             ref = orc.decode(layer, as_np(q), as_np(kn), as_np(vn))
             assert np.abs(as_np(out).reshape(B, Hq, D) - ref).max() <= 2e-2
     torch.cuda.synchronize()
-    # Both checks scored in one pass, from the cast chain's statistics that
-    # the decode launches reported.
-    assert cache.one_pass_checks == steps // 5
+    # With one_pass, both checks scored in one pass, from the cast chain's
+    # statistics that the decode launches reported.
+    assert cache.one_pass_checks == (steps // 5 if one_pass else 0)
     flags = [(l, h, c[(l, h)]) for c in rec.checks for l in range(NL) for h in cache._drift[l].leaders]
     assert flags == orc.triggers and [f for *_, f in flags] == [False] * 3 + [True] * 3
     assert max(e for *_, e in hook.err) <= step * 1.01
