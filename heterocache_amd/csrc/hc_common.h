@@ -162,12 +162,53 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float row16_sum(float v) {
-  v += dpp_mov<0x128>(v);  // row_ror:8
-  v += dpp_mov<0x124>(v);  // row_ror:4
-  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
-  return v;
+// Sums over the 16 lanes of each 16-lane row of a wave, for NR values per
+// lane at once (NR = 4, 8 or 16): lane l ends with its row's sum of value
+// l % NR.  A reduce-scatter: at each of the first log2(NR) stages a lane
+// keeps the half of its values whose index bit equals its own lane bit and
+// adds the copy of that half sent by a lane whose bit differs -- l ^ 1 and
+// l ^ 2 by quad permutes, then a row rotation by 4 and one by 8 (a rotated
+// lane holds the same values as l ^ 4 or l ^ 8, and the later stages
+// gather the remaining quads whichever way the rotation turns) -- so the
+// values held halve at every stage; rotations by 8 and 4 sum what is left.
+// 16 operations at NR = 4 where separate sums of each value take 32.
+template <int NR>
+__device__ __forceinline__ float row16_sum_scatter(float (&a)[NR], int lane) {
+  static_assert(NR == 4 || NR == 8 || NR == 16, "4, 8 or 16 values per lane");
+  {
+    const bool b = lane & 1;
+#pragma unroll
+    for (int j = 0; j < NR / 2; ++j) {
+      const float keep = b ? a[2 * j + 1] : a[2 * j], send = b ? a[2 * j] : a[2 * j + 1];
+      a[j] = keep + dpp_mov<0xB1>(send);  // quad_perm [1,0,3,2]
+    }
+  }
+  {
+    const bool b = lane & 2;
+#pragma unroll
+    for (int j = 0; j < NR / 4; ++j) {
+      const float keep = b ? a[2 * j + 1] : a[2 * j], send = b ? a[2 * j] : a[2 * j + 1];
+      a[j] = keep + dpp_mov<0x4E>(send);  // quad_perm [2,3,0,1]
+    }
+  }
+  if constexpr (NR >= 8) {
+    const bool b = lane & 4;
+#pragma unroll
+    for (int j = 0; j < NR / 8; ++j) {
+      const float keep = b ? a[2 * j + 1] : a[2 * j], send = b ? a[2 * j] : a[2 * j + 1];
+      a[j] = keep + dpp_mov<0x124>(send);  // row_ror:4
+    }
+  }
+  if constexpr (NR == 16) {
+    const bool b = lane & 8;
+    const float keep = b ? a[1] : a[0], send = b ? a[0] : a[1];
+    return keep + dpp_mov<0x128>(send);  // row_ror:8
+  } else if constexpr (NR == 8) {
+    return a[0] + dpp_mov<0x128>(a[0]);
+  } else {
+    const float v = a[0] + dpp_mov<0x128>(a[0]);
+    return v + dpp_mov<0x124>(v);
+  }
 }
 
 // Combine a value over the four lanes l, l^16, l^32, l^48 of a wave (one

@@ -300,9 +300,9 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
 // the MFMA operand layout of score_stats_kernel makes every wave load touch
 // 16 rows of 64 bytes each.  Here the 16 lanes of group s hold channels
 // 8c..8c+7 (c = lane % 16) of token 4*step + s, so a wave load reads four
-// whole 256-byte token rows; the groups' partial dot products are summed by
-// four DPP adds (row16_sum), after which lane c < R of a group holds row c's
-// logit of its token.  Logits are stored as score_stats_kernel stores them (base-2
+// whole 256-byte token rows; the groups' partial dot products of all NR
+// rows are summed by one DPP reduce-scatter (row16_sum_scatter), after which
+// lane c < R of a group holds row c's logit of its token.  Logits are stored as score_stats_kernel stores them (base-2
 // scaled and masked, [job][R][span]) and every workgroup writes one
 // (max, sum) partial per row, so the merge and finish passes are shared.
 // NR: rows held per lane (R rounded up to 4, 8 or 16).
@@ -360,11 +360,7 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(Score
         for (int e = 0; e < 8; ++e) d = fmaf(qr[r][e], vec8_at<T>(kr[st], e), d);
         acc[r] = d;
       }
-#pragma unroll
-      for (int r = 0; r < NR; ++r) acc[r] = row16_sum(acc[r]);
-      float mine = acc[0];
-#pragma unroll
-      for (int r = 1; r < NR; ++r) mine = c == r ? acc[r] : mine;
+      const float mine = row16_sum_scatter<NR>(acc, lane);  // row c % NR
       const int t = t0 + 4 * st + sub;
       x[st] = t <= limit ? scaled_logit<RM>(a, mine) : -INFINITY;
       if (owner && t < a.span) lrow[t] = x[st];
