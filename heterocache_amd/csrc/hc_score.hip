@@ -307,6 +307,36 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
 // (max, sum) partial per row, so the merge and finish passes are shared.
 // NR: rows held per lane (R rounded up to 4, 8 or 16).
 constexpr int kRowsSteps = 8;  // 4-token steps per wave and iteration
+
+// Two products per instruction for 16-bit inputs: v_dot2_f32_bf16 /
+// v_dot2_f32_f16 multiply packed pairs exactly and accumulate in float32,
+// so the queries stay in the input type (half the registers) and the keys
+// need no conversion.  Float32 inputs take FMAs.
+template <typename T>
+struct Dot2 {
+  typedef float pair;
+};
+template <>
+struct Dot2<__bf16> {
+  typedef __attribute__((ext_vector_type(2))) __bf16 pair;
+  static __device__ __forceinline__ float dot(pair a, pair b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, b, c, false);
+  }
+};
+template <>
+struct Dot2<_Float16> {
+  typedef __attribute__((ext_vector_type(2))) _Float16 pair;
+  static __device__ __forceinline__ float dot(pair a, pair b, float c) { return __builtin_amdgcn_fdot2(a, b, c, false); }
+};
+// Pair j (elements 2j, 2j + 1) of eight 16-bit values.
+template <typename T>
+__device__ __forceinline__ typename Dot2<T>::pair pair_at(const typename Elem<T>::vec8& v, int j) {
+  typename Dot2<T>::pair p;
+  p.x = v[2 * j];
+  p.y = v[2 * j + 1];
+  return p;
+}
+
 template <typename T, int NR, int RM>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(ScoreArgs a, float* __restrict__ part,
                                                                           float* __restrict__ logits) {
@@ -315,19 +345,24 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(Score
   const int job = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane >> 4, c = lane & 15;
-  // This lane's 8 channels of every query row, as floats (zero past R).
-  float qr[NR][8];
+  // This lane's 8 channels of every query row (zero past R): four packed
+  // pairs of the input type for 16-bit inputs, eight floats for float32.
+  constexpr bool kPairs = sizeof(T) == 2;
+  typedef typename Dot2<T>::pair QP;
+  constexpr int QW = kPairs ? 4 : 8;
+  typedef std::conditional_t<kPairs, QP, float> QE;
+  QE qr[NR][QW];
   {
     const T* q = reinterpret_cast<const T*>(a.q) + a.q_off[job] + 8 * c;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      if (r < a.R) {
-        const vec8 v = load8<T>(q + (r / a.W) * a.q_head_stride + (r % a.W) * a.q_row_stride);
+      const vec8 v = r < a.R ? load8<T>(q + (r / a.W) * a.q_head_stride + (r % a.W) * a.q_row_stride) : zero8<T>();
+      if constexpr (kPairs) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qr[r][e] = vec8_at<T>(v, e);
+        for (int j = 0; j < 4; ++j) qr[r][j] = pair_at<T>(v, j);
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) qr[r][e] = 0.f;
+        for (int e = 0; e < 8; ++e) qr[r][e] = vec8_at<T>(v, e);
       }
     }
   }
@@ -340,15 +375,20 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(Score
   float* lrow = logits + ((int64_t)job * a.R + (owner ? c : 0)) * a.span;
   float m = -FLT_MAX, l = 0.f;
   constexpr int kIter = kScoreWaves * kRowsSteps * 4;  // tokens per workgroup iteration
-  for (int t0 = c0 * kScoreChunk + wave * kRowsSteps * 4; t0 < t_end; t0 += kIter) {
-    // (A second key buffer, loads of the next iteration in flight during
-    // this one, costs occupancy and was slower: 83 against 73 us.)
-    vec8 kr[kRowsSteps];
+  // Keys of one iteration, streamed past L2 (this pass reads them once):
+  // with ordinary loads the pass took 69-71 us per 128K Llama-3-8B layer
+  // (eight heads), nontemporal 50 us, while the gather that follows loses
+  // ~4 us of cache hits.  Token addresses are clamped into [0, L) (a token
+  // past the keys is read from the last one and its logit masked below), so
+  // the loads take no branches.  A second key buffer, the next iteration's
+  // loads in flight during this one, measured the same (50.4 against 50.7
+  // us) at 132 instead of 76 registers.
+  auto load_keys = [&](vec8 (&kr)[kRowsSteps], int t0) {
 #pragma unroll
-    for (int st = 0; st < kRowsSteps; ++st) {
-      const int t = t0 + 4 * st + sub;
-      kr[st] = t < a.L ? load8<T>(kb + (int64_t)t * a.k_tok_stride) : zero8<T>();
-    }
+    for (int st = 0; st < kRowsSteps; ++st)
+      kr[st] = load8_stream<T>(kb + (int64_t)min(t0 + 4 * st + sub, a.L - 1) * a.k_tok_stride);
+  };
+  auto consume = [&](const vec8 (&kr)[kRowsSteps], int t0) {
     float x[kRowsSteps];
 #pragma unroll
     for (int st = 0; st < kRowsSteps; ++st) {
@@ -356,8 +396,13 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(Score
 #pragma unroll
       for (int r = 0; r < NR; ++r) {
         float d = 0.f;
+        if constexpr (kPairs) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qr[r][e], vec8_at<T>(kr[st], e), d);
+          for (int j = 0; j < 4; ++j) d = Dot2<T>::dot(qr[r][j], pair_at<T>(kr[st], j), d);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d = fmaf(qr[r][e], vec8_at<T>(kr[st], e), d);
+        }
         acc[r] = d;
       }
       const float mine = row16_sum_scatter<NR>(acc, lane);  // row c % NR
@@ -374,6 +419,11 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(Score
     for (int st = 0; st < kRowsSteps; ++st) add += fast_exp2(x[st] - mn);
     l = fmaf(l, fast_exp2(m - mn), add);
     m = mn;
+  };
+  for (int t0 = c0 * kScoreChunk + wave * kRowsSteps * 4; t0 < t_end; t0 += kIter) {
+    vec8 kr[kRowsSteps];
+    load_keys(kr, t0);
+    consume(kr, t0);
   }
   // Rows are held by lanes c, c+16, c+32, c+48 of each wave; then the waves.
   const float M = rows4_max(m);
