@@ -87,8 +87,11 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
       // clamp(max=L-1) before its gather (heterocache/cache_utils.py:852).
       const int64_t stok = ix ? (int64_t)min(max(ix[tok0 + t], 0), src_len - 1) : (int64_t)(tok0 + t);
       const int64_t off = stok * src_tok_stride + ch * 8;
-      typename Elem<T>::vec8 a = load8<T>(bk + off);
-      typename Elem<T>::vec8 b = load8<T>(bv + off);
+      // Each source row is read once: streamed past L2 (the prefill
+      // compression of a 128K Llama-3-8B layer, two gathers and the
+      // scorer, 0.204 -> 0.200 ms).
+      typename Elem<T>::vec8 a = load8_stream<T>(bk + off);
+      typename Elem<T>::vec8 b = load8_stream<T>(bv + off);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if constexpr (sizeof(T) == 4) {
