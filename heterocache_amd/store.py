@@ -121,10 +121,12 @@ class KVStore:
         the host (numpy), dev_rows (int64) / dev_lens (int32) the same
         values on the device, dev_order (int32, optional) a row order to
         schedule by (any permutation of the rows is correct; longest first
-        is the fast one).  Launches one index copy, and one copy for the
-        order, and no host-to-device transfer.  on_device: a launch already
-        wrote the device lengths (launch_rows(write_len=True)); only the
-        host mirror and the order are updated."""
+        is the fast one), a device tensor that stays unchanged while the
+        store uses it: the store schedules by it from now on, without a
+        copy.  Launches one index copy and no host-to-device transfer.
+        on_device: a launch already wrote the device lengths
+        (launch_rows(write_len=True)); only the host mirror and the order
+        are updated, and nothing is launched."""
         rows = np.asarray(rows, dtype=np.int64)
         lens = np.asarray(lens, dtype=np.int64)
         if (lens > self.host_cap[rows]).any() or (lens < 0).any():
@@ -133,7 +135,9 @@ class KVStore:
         if not on_device:
             self.row_len.index_copy_(0, dev_rows, dev_lens)
         if dev_order is not None:
-            self.row_order.copy_(dev_order)
+            if dev_order.dtype != torch.int32 or dev_order.numel() != self.rows or not dev_order.is_cuda:
+                raise ValueError("dev_order must be an int32 device tensor of one entry per row")
+            self.row_order = dev_order
         self._headroom = int((self.host_cap - self.host_len).min()) if self.rows else 0
 
     def sync_host_lengths(self, lens):
