@@ -518,14 +518,17 @@ __global__ __launch_bounds__(kDvWaves * 64, sizeof(T) == 4 ? 1 : 2) void prefill
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int t = t0 + 16 * h + n16;
+      // Keys past Lk are read from the last one (clamped, branch-free
+      // loads); their logits are masked.
       const T* p = kb + (int64_t)min(t, a.Lk - 1) * a.k_st + 8 * g4;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kr[h][s] = t < a.Lk ? load8_stream<T>(p + 32 * s) : zero8<T>();
+      for (int s = 0; s < 4; ++s) kr[h][s] = load8_stream<T>(p + 32 * s);
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int c = lane + 64 * i, t = t0 + (c >> 4);
-      vr[i] = t < a.Lk ? load8_stream<T>(vb + (int64_t)min(t, a.Lk - 1) * a.v_st + 8 * (c & 15)) : zero8<T>();
+      const vec8 x = load8_stream<T>(vb + (int64_t)min(t, a.Lk - 1) * a.v_st + 8 * (c & 15));
+      vr[i] = t < a.Lk ? x : zero8<T>();
     }
   };
 
