@@ -732,9 +732,42 @@ __device__ __forceinline__ void window_sums(const ScoreArgs& a, const typename E
   }
 }
 
+// Keys of NU sub-tiles from tw on, natural layout, each lane's row clamped
+// to the job's last key (L >= 1): no branch around the loads, so the waits
+// on one half of a double buffer leave the other half's loads in flight.
+// Clamped rows only feed masked logits: a chunk holding a token at or past
+// L - 1 takes the masked path, where every such token is past its row's
+// limit.
+// `base` is the lane's column in the job's key rows, read once per kernel:
+// the offset table sits in global memory, and read inside the chunk loop
+// (after the pooled stores, which could alias it) it was read again each
+// chunk, its wait draining every key load in flight.
+template <typename T, int NU>
+__device__ __forceinline__ void load_k_clamped(const ScoreArgs& a, const T* base, int tw, int lane,
+                                               typename Elem<T>::vec8 (&k)[NU][4]) {
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int t = min(tw + 16 * u + (lane & 15), a.L - 1);
+    const T* p = base + (int64_t)t * a.k_tok_stride;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) k[u][s] = load8<T>(p + 32 * s);
+  }
+}
+
+// Natural-layout keys only (STORE is false in every instance).  Each wave's
+// 64 tokens of a chunk are two halves of two sub-tiles in two register
+// sets: a half's keys for the next chunk are requested as soon as the half
+// has been consumed, so every load has the other half's work to land in.
+// In the run's last chunk the "next" keys are the same keys again, so the
+// loads stay unconditional.  Alternated on one box with one buffer reloaded
+// after the whole chunk (8 heads x 128K, W = 32, max pool 7, host work
+// included): 0.0742-0.0757 against 0.0749-0.0772 ms per layer, so the key
+// loads were not what bounds the pass; VALU issue and latency are.
 template <typename T, bool STORE, int RM, int POOL, int P>
 __global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 : 3) void score_probs_pool_kernel(ScoreArgs a, StatsView stats,
                                                                            float* __restrict__ S) {
+  static_assert(!STORE, "the fused pass reads natural-layout keys");
+  constexpr int kHalf = kSubTiles / 2;
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr float kPad = POOL == 0 ? 0.f : -INFINITY;
   T* s_q = reinterpret_cast<T*>(smem);
@@ -747,10 +780,12 @@ __global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nchunks = (a.span + kScoreChunk - 1) / kScoreChunk;
   const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
-  if (c0 >= c1) return;  // uniform per workgroup
+  if (c0 >= c1 || a.L <= 0) return;  // uniform per workgroup
   const int woff = wave * 16 * kSubTiles;
-  KRegs<T> ka;
-  load_k_chunk<T, STORE>(a, job, c0 * kScoreChunk + woff, lane, ka);
+  const T* const kbase = reinterpret_cast<const T*>(a.k) + a.k_off[job] + 8 * (lane >> 4);
+  typename Elem<T>::vec8 kh0[kHalf][4], kh1[kHalf][4];
+  load_k_clamped<T, kHalf>(a, kbase, c0 * kScoreChunk + woff, lane, kh0);
+  load_k_clamped<T, kHalf>(a, kbase, c0 * kScoreChunk + woff + 16 * kHalf, lane, kh1);
   stage_queries<T>(a, job, s_q);
   for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
     const float* st = stats.row(a, job, r);  // rows = R here: W is a multiple of 16
@@ -762,27 +797,43 @@ __global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 
     }
   }
   __syncthreads();
+  if (wave == 0) {
+    // The run's left margin: positions c0 * kScoreChunk - 16 .. - 1.
+    const int cb = c0 * kScoreChunk;
+    if (cb > 0) {
+      typename Elem<T>::vec8 km[1][4];
+      load_k_subtile<T, STORE>(a, job, cb - kPpMargin, lane, km[0]);
+      window_sums<T, RM, true, 1>(a, km, s_q, s_m, s_iz, cb - kPpMargin, lane, mrg, kPpMargin, kPad);
+    } else {
+      for (int i = lane; i < a.G * kPpMargin; i += 64) mrg[i] = kPad;
+    }
+  }
+  // Drain every load of the set-up (the first chunk's keys included).  The
+  // staging loops and the margin leave a count of loads in flight that the
+  // compiler cannot bound; with that state at the loop head it made each
+  // chunk's first key wait a wait for every load, the prefetch included.
+  __builtin_amdgcn_s_waitcnt(0);
   const int min_limit = (a.flags & HC_SCORE_CAUSAL_WINDOW) ? a.L - a.W : a.L - 1;
   const bool acc_out = (a.flags & HC_SCORE_ACCUMULATE) != 0;
   float* const out = S + (int64_t)job * a.span;
   for (int c = c0; c < c1; ++c) {
     const int cb = c * kScoreChunk;
+    const int nb = (c + 1 < c1 ? cb + kScoreChunk : cb) + woff;  // next chunk's keys (or these again)
     float* mcur = mrg + ((c - c0) & 1) * a.G * kPpMargin;
     float* mnext = mrg + ((c - c0 + 1) & 1) * a.G * kPpMargin;
-    if (cb + kScoreChunk - 1 > min_limit)
-      window_sums<T, RM, true, kSubTiles>(a, ka.v, s_q, s_m, s_iz, cb + woff, lane, strip + woff, kPpPitch, kPad);
+    const bool masked = cb + kScoreChunk - 1 > min_limit;
+    if (masked)
+      window_sums<T, RM, true, kHalf>(a, kh0, s_q, s_m, s_iz, cb + woff, lane, strip + woff, kPpPitch, kPad);
     else
-      window_sums<T, RM, false, kSubTiles>(a, ka.v, s_q, s_m, s_iz, cb + woff, lane, strip + woff, kPpPitch, kPad);
-    if (c == c0 && wave == 0) {
-      // The run's left margin: positions cb - 16 .. cb - 1.
-      if (cb > 0) {
-        typename Elem<T>::vec8 km[1][4];
-        load_k_subtile<T, STORE>(a, job, cb - kPpMargin, lane, km[0]);
-        window_sums<T, RM, true, 1>(a, km, s_q, s_m, s_iz, cb - kPpMargin, lane, mcur, kPpMargin, kPad);
-      } else {
-        for (int i = lane; i < a.G * kPpMargin; i += 64) mcur[i] = kPad;
-      }
-    }
+      window_sums<T, RM, false, kHalf>(a, kh0, s_q, s_m, s_iz, cb + woff, lane, strip + woff, kPpPitch, kPad);
+    load_k_clamped<T, kHalf>(a, kbase, nb, lane, kh0);
+    if (masked)
+      window_sums<T, RM, true, kHalf>(a, kh1, s_q, s_m, s_iz, cb + woff + 16 * kHalf, lane,
+                                      strip + woff + 16 * kHalf, kPpPitch, kPad);
+    else
+      window_sums<T, RM, false, kHalf>(a, kh1, s_q, s_m, s_iz, cb + woff + 16 * kHalf, lane,
+                                       strip + woff + 16 * kHalf, kPpPitch, kPad);
+    load_k_clamped<T, kHalf>(a, kbase, nb + 16 * kHalf, lane, kh1);
     if (c == c1 - 1 && wave == kScoreWaves - 1) {
       // The run's right margin: positions cb + 256 .. cb + 271.
       const int te = cb + kScoreChunk;
@@ -793,14 +844,22 @@ __global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 
       } else {
         for (int i = lane; i < a.G * kPpMargin; i += 64) strip[(i / kPpMargin) * kPpPitch + kScoreChunk + i % kPpMargin] = kPad;
       }
+      __builtin_amdgcn_s_waitcnt(0);  // the run's last chunk: only the unused reloads are in flight
     }
-    if (c + 1 < c1) load_k_chunk<T, STORE>(a, job, cb + kScoreChunk + woff, lane, ka);
     __syncthreads();
     // Pool positions [lo, hi): the previous chunk's last P, then this chunk's
-    // up to its last P (all of them in the run's last chunk).
+    // up to its last P (all of them in the run's last chunk), at most two
+    // per thread.  Straight-line code, not a loop: stores count against the
+    // same wait counter as the key loads in flight, and after a loop of
+    // stores the compiler can no longer tell how many are pending, so the
+    // next chunk's first key wait became a wait for every load.
+    static_assert(kScoreChunk + kPpMaxHalf <= 2 * kScoreWaves * 64, "two pooled positions per thread");
     const int lo = c == c0 ? cb : cb - P;
     const int hi = min(c == c1 - 1 ? cb + kScoreChunk : cb + kScoreChunk - P, a.span);
-    for (int x = lo + (int)threadIdx.x; x < hi; x += kScoreWaves * 64) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int x = lo + (int)threadIdx.x + q * kScoreWaves * 64;
+      if (x >= hi) continue;
       const int i = x - cb;
       float best = -INFINITY;
       for (int g = 0; g < a.G; ++g) {
