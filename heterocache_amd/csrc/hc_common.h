@@ -91,6 +91,25 @@ __device__ __forceinline__ Elem<float>::vec8 load8_stream<float>(const float* p)
   return r;
 }
 
+// load8_stream for a pointer the compiler cannot place in global memory by
+// itself (one made from a device address passed as an integer): a generic
+// pointer makes a flat load, which counts against both the vector-memory and
+// the LDS wait counters, so each wait on it also waits for every LDS access.
+// The cast tells the compiler the address is global.
+template <typename T>
+__device__ __forceinline__ typename Elem<T>::vec8 load8_stream_global(const T* p) {
+  typedef __attribute__((address_space(1))) const typename Elem<T>::vec8 GV;
+  return __builtin_nontemporal_load((GV*)p);
+}
+template <>
+__device__ __forceinline__ Elem<float>::vec8 load8_stream_global<float>(const float* p) {
+  typedef __attribute__((address_space(1))) const f32x4 GV;
+  Elem<float>::vec8 r;
+  r.lo = __builtin_nontemporal_load((GV*)p);
+  r.hi = __builtin_nontemporal_load((GV*)(p + 4));
+  return r;
+}
+
 // acc += A(16x32) * B(32x16) where each lane supplies 8 k-values of its row
 // (A) / column (B): lane l owns row/col l%16 and k-slots 8*(l/16)+[0..8).
 // For fp32 the same 32-wide contraction is issued as 8 x (16x16x4) MFMAs in

@@ -91,8 +91,18 @@ __device__ __forceinline__ void stage_queries(const ScoreArgs& a, int job, T* s_
 
 // K operand of one 16-token sub-tile: lane holds token t0 + (lane & 15),
 // channels 32s + 8*(lane >> 4) + [0, 8).
+// The job's keys: its first tile in the store, or its first row in natural
+// layout.  Read once per kernel: the offset tables sit in global memory, and
+// read again in a chunk loop after the loop's own stores (which could alias
+// them) each read was a chain of waits that drained every load in flight.
 template <typename T, bool STORE>
-__device__ __forceinline__ void load_k_subtile(const ScoreArgs& a, int job, int t0, int lane,
+__device__ __forceinline__ const T* job_keys(const ScoreArgs& a, int job) {
+  if constexpr (STORE) return reinterpret_cast<const T*>(a.k) + a.row_tile_off[a.k_row[job]] * (int64_t)HC_TILE_ELEMS;
+  return reinterpret_cast<const T*>(a.k) + a.k_off[job];
+}
+
+template <typename T, bool STORE>
+__device__ __forceinline__ void load_k_subtile(const ScoreArgs& a, const T* kj, int t0, int lane,
                                                typename Elem<T>::vec8 (&kr)[4]) {
   if constexpr (STORE) {
     if (t0 >= a.L) {  // the sub-tile may lie past the row's capacity
@@ -100,7 +110,7 @@ __device__ __forceinline__ void load_k_subtile(const ScoreArgs& a, int job, int 
       for (int s = 0; s < 4; ++s) kr[s] = zero8<T>();
       return;
     }
-    const T* base = reinterpret_cast<const T*>(a.k) + (a.row_tile_off[a.k_row[job]] + t0 / HC_TILE) * (int64_t)HC_TILE_ELEMS;
+    const T* base = kj + (t0 / HC_TILE) * (int64_t)HC_TILE_ELEMS;
     const int h = (t0 / 16) & 1;
 #pragma unroll
     // Keys read in place from the store are read once per launch: streamed
@@ -112,7 +122,7 @@ __device__ __forceinline__ void load_k_subtile(const ScoreArgs& a, int job, int 
   } else {
     const int t = t0 + (lane & 15);
     if (t < a.L) {
-      const T* p = reinterpret_cast<const T*>(a.k) + a.k_off[job] + (int64_t)t * a.k_tok_stride + 8 * (lane >> 4);
+      const T* p = kj + (int64_t)t * a.k_tok_stride + 8 * (lane >> 4);
 #pragma unroll
       for (int s = 0; s < 4; ++s) kr[s] = load8<T>(p + 32 * s);
     } else {
@@ -167,9 +177,9 @@ struct KRegs {
 };
 
 template <typename T, bool STORE>
-__device__ __forceinline__ void load_k_chunk(const ScoreArgs& a, int job, int tw, int lane, KRegs<T>& k) {
+__device__ __forceinline__ void load_k_chunk(const ScoreArgs& a, const T* kj, int tw, int lane, KRegs<T>& k) {
 #pragma unroll
-  for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, job, tw + 16 * u, lane, k.v[u]);
+  for (int u = 0; u < kSubTiles; ++u) load_k_subtile<T, STORE>(a, kj, tw + 16 * u, lane, k.v[u]);
 }
 
 // Statistics of one 256-token chunk: the (max, sum) of every row over this
@@ -258,8 +268,9 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
   const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
   // Each wave owns kSubTiles consecutive 16-token sub-tiles of a chunk.
   const int woff = wave * 16 * kSubTiles;
+  const T* const kj = job_keys<T, STORE>(a, job);
   KRegs<T> ka;
-  load_k_chunk<T, STORE>(a, job, c0 * kScoreChunk + woff, lane, ka);
+  load_k_chunk<T, STORE>(a, kj, c0 * kScoreChunk + woff, lane, ka);
   stage_queries<T>(a, job, s_q);
   float* my = s_st + (size_t)wave * rows * 2;
   for (int r = lane; r < rows; r += 64) {
@@ -279,7 +290,7 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_stats_kernel(ScoreArgs
       stats_chunk<T, RM, LOGITS, false>(a, k, s_q, my, job, tw, lane, logits);
   };
   for (int c = c0; c < c1; ++c) {
-    if (c > c0) load_k_chunk<T, STORE>(a, job, c * kScoreChunk + woff, lane, ka);
+    if (c > c0) load_k_chunk<T, STORE>(a, kj, c * kScoreChunk + woff, lane, ka);
     chunk_stats(ka, c);
   }
   __syncthreads();
@@ -527,8 +538,9 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
   const int nchunks = (a.span + kScoreChunk - 1) / kScoreChunk;
   const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
   const int woff = wave * 16 * kSubTiles;
+  const T* const kj = job_keys<T, STORE>(a, job);
   KRegs<T> ka;
-  load_k_chunk<T, STORE>(a, job, c0 * kScoreChunk + woff, lane, ka);
+  load_k_chunk<T, STORE>(a, kj, c0 * kScoreChunk + woff, lane, ka);
   stage_queries<T>(a, job, s_q);
   for (int r = threadIdx.x; r < rows; r += kScoreWaves * 64) {
     // Padding rows get probability 0 even where logits are not masked.
@@ -654,7 +666,7 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_probs_kernel(ScoreArgs
       body(std::false_type{}, k, tw);
   };
   for (int c = c0; c < c1; ++c) {
-    if (c > c0) load_k_chunk<T, STORE>(a, job, c * kScoreChunk + woff, lane, ka);
+    if (c > c0) load_k_chunk<T, STORE>(a, kj, c * kScoreChunk + woff, lane, ka);
     chunk_probs(ka, c);
   }
   if constexpr (MOM) {
@@ -738,10 +750,7 @@ __device__ __forceinline__ void window_sums(const ScoreArgs& a, const typename E
 // Clamped rows only feed masked logits: a chunk holding a token at or past
 // L - 1 takes the masked path, where every such token is past its row's
 // limit.
-// `base` is the lane's column in the job's key rows, read once per kernel:
-// the offset table sits in global memory, and read inside the chunk loop
-// (after the pooled stores, which could alias it) it was read again each
-// chunk, its wait draining every key load in flight.
+// `base` is the lane's column in the job's key rows (job_keys).
 template <typename T, int NU>
 __device__ __forceinline__ void load_k_clamped(const ScoreArgs& a, const T* base, int tw, int lane,
                                                typename Elem<T>::vec8 (&k)[NU][4]) {
@@ -782,7 +791,8 @@ __global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 
   const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
   if (c0 >= c1 || a.L <= 0) return;  // uniform per workgroup
   const int woff = wave * 16 * kSubTiles;
-  const T* const kbase = reinterpret_cast<const T*>(a.k) + a.k_off[job] + 8 * (lane >> 4);
+  const T* const kj = job_keys<T, STORE>(a, job);
+  const T* const kbase = kj + 8 * (lane >> 4);
   typename Elem<T>::vec8 kh0[kHalf][4], kh1[kHalf][4];
   load_k_clamped<T, kHalf>(a, kbase, c0 * kScoreChunk + woff, lane, kh0);
   load_k_clamped<T, kHalf>(a, kbase, c0 * kScoreChunk + woff + 16 * kHalf, lane, kh1);
@@ -802,7 +812,7 @@ __global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 
     const int cb = c0 * kScoreChunk;
     if (cb > 0) {
       typename Elem<T>::vec8 km[1][4];
-      load_k_subtile<T, STORE>(a, job, cb - kPpMargin, lane, km[0]);
+      load_k_subtile<T, STORE>(a, kj, cb - kPpMargin, lane, km[0]);
       window_sums<T, RM, true, 1>(a, km, s_q, s_m, s_iz, cb - kPpMargin, lane, mrg, kPpMargin, kPad);
     } else {
       for (int i = lane; i < a.G * kPpMargin; i += 64) mrg[i] = kPad;
@@ -839,7 +849,7 @@ __global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 
       const int te = cb + kScoreChunk;
       if (te < a.span) {
         typename Elem<T>::vec8 km[1][4];
-        load_k_subtile<T, STORE>(a, job, te, lane, km[0]);
+        load_k_subtile<T, STORE>(a, kj, te, lane, km[0]);
         window_sums<T, RM, true, 1>(a, km, s_q, s_m, s_iz, te, lane, strip + kScoreChunk, kPpPitch, kPad);
       } else {
         for (int i = lane; i < a.G * kPpMargin; i += 64) strip[(i / kPpMargin) * kPpPitch + kScoreChunk + i % kPpMargin] = kPad;
@@ -1447,15 +1457,39 @@ __device__ __forceinline__ void gs_pool(const ScoreArgs& a, const GsView& v, int
   }
 }
 
+// Keys of NU 16-token sub-tiles from tw on, read in place from the tiled
+// store past L2.  A sub-tile past the job's last key is read at the last
+// sub-tile holding a key instead (inside the row's tiles; its tokens are
+// masked), so no lane branches around the loads.
+template <typename T, int NU>
+__device__ __forceinline__ void load_k_run(const ScoreArgs& a, const T* kj, int tw, int lane,
+                                           typename Elem<T>::vec8 (&k)[NU][4]) {
+  const int last = ((a.L - 1) / 16) * 16;
+#pragma unroll
+  for (int u = 0; u < NU; ++u) {
+    const int t0 = min(tw + 16 * u, last);
+    const T* base = kj + (t0 / HC_TILE) * (int64_t)HC_TILE_ELEMS + ((t0 / 16) & 1) * 4 * 512 + lane * 8;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) k[u][s] = load8_stream<T>(base + s * 512);
+  }
+}
+
 template <typename T, bool STORE, int POOL, int P, int RM>
 __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(ScoreArgs a,
                                                                             const float* __restrict__ stats,
                                                                             const int64_t* __restrict__ st_off,
                                                                             float* __restrict__ S) {
+  static_assert(STORE, "keys are read in place from the tiled store");
   extern __shared__ __align__(16) unsigned char smem[];
   T* s_q = reinterpret_cast<T*>(smem);
   float* strip = reinterpret_cast<float*>(smem + (size_t)a.NT * 16 * kQPitch * sizeof(T));  // [R][kGsPitch]
-  float* mrg[2] = {strip + a.R * kGsPitch, strip + a.R * kGsPitch + a.R * kGsMPitch};        // [R][kGsMPitch]
+  // Two margin buffers [R][kGsMPitch] after the strip.  Addressed by
+  // arithmetic on the strip pointer: picked from an array of pointers, the
+  // buffer's address lost its LDS address space, so the margin reads and
+  // writes were flat instructions, which count against both wait counters
+  // and made every wait in the chunk loop a wait for all loads and stores.
+  float* const mrg0 = strip + a.R * kGsPitch;
+  const int mstride = a.R * kGsMPitch;
   __shared__ float s_mz[kLogitRowsMax];
   __shared__ float s_iz[RM == 0 ? 1 : kLogitRowsMax];
   constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
@@ -1465,10 +1499,16 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
   const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
   const int woff = wave * 16 * kSubTiles;
-  KRegs<T> ka;
+  const T* const kj = job_keys<T, STORE>(a, job);
+  // A wave's 64 tokens of a chunk in two halves, double-buffered: a half's
+  // keys for the next chunk are requested as soon as its products are
+  // formed, so they land while the other half is scored and the chunk pools.
+  constexpr int kHalf = kSubTiles / 2;
+  vec8 ka0[kHalf][4], ka1[kHalf][4];
   vec8 kh[1][4];  // wave 1: the run's left margin; wave 0: its right margin
-  load_k_chunk<T, STORE>(a, job, c0 * kScoreChunk + woff, lane, ka);
-  if (wave == 1 && c0 > 0) load_k_subtile<T, STORE>(a, job, c0 * kScoreChunk - 16, lane, kh[0]);
+  load_k_run<T, kHalf>(a, kj, c0 * kScoreChunk + woff, lane, ka0);
+  load_k_run<T, kHalf>(a, kj, c0 * kScoreChunk + woff + 16 * kHalf, lane, ka1);
+  if (wave == 1 && c0 > 0) load_k_subtile<T, STORE>(a, kj, c0 * kScoreChunk - 16, lane, kh[0]);
   stage_queries<T>(a, job, s_q);
   for (int r = threadIdx.x; r < a.R; r += kScoreWaves * 64) {
     const float* st = stats + st_off[job] + 2 * r;
@@ -1486,26 +1526,32 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   if (wave == 1) {
     const int cb0 = c0 * kScoreChunk;
     if (c0 > 0) {
-      gs_subtiles<T, POOL, 1, RM>(a, kh, s_q, s_mz, s_iz, mrg[1], kGsMPitch, cb0 - kGsMargin, cb0 - 16, lane);
+      gs_subtiles<T, POOL, 1, RM>(a, kh, s_q, s_mz, s_iz, mrg0 + mstride, kGsMPitch, cb0 - kGsMargin, cb0 - 16, lane);
     } else {
-      for (int i = lane; i < a.R * 16; i += 64) mrg[1][(i / 16) * kGsMPitch + 16 + i % 16] = pad;
+      for (int i = lane; i < a.R * 16; i += 64) mrg0[mstride + (i / 16) * kGsMPitch + 16 + i % 16] = pad;
     }
   }
+  // Drain the set-up's loads: the staging loops leave a count in flight that
+  // the compiler cannot bound, and with that state at the loop head its
+  // waits for a half's keys would wait for the other half's as well.
+  __builtin_amdgcn_s_waitcnt(0);
   for (int c = c0; c < c1; ++c) {
     const int cb = c * kScoreChunk;
-    gs_subtiles<T, POOL, kSubTiles, RM>(a, ka.v, s_q, s_mz, s_iz, strip, kGsPitch, cb, cb + woff, lane);
+    const bool more = c + 1 < c1;
+    gs_subtiles<T, POOL, kHalf, RM>(a, ka0, s_q, s_mz, s_iz, strip, kGsPitch, cb, cb + woff, lane);
+    if (more) load_k_run<T, kHalf>(a, kj, cb + kScoreChunk + woff, lane, ka0);
+    gs_subtiles<T, POOL, kHalf, RM>(a, ka1, s_q, s_mz, s_iz, strip, kGsPitch, cb, cb + woff + 16 * kHalf, lane);
+    if (more) load_k_run<T, kHalf>(a, kj, cb + kScoreChunk + woff + 16 * kHalf, lane, ka1);
     __syncthreads();  // strip written (and the margin of the previous chunk)
-    // Next chunk's keys in flight while this one pools.
-    if (c + 1 < c1) load_k_chunk<T, STORE>(a, job, cb + kScoreChunk + woff, lane, ka);
     const int mb = (c - c0 + 1) & 1;  // margin buffer holding the previous chunk's tail
-    GsView v{strip, mrg[mb]};
+    GsView v{strip, mrg0 + mb * mstride};
     // Positions [cb - 16, cb + 240) (the run's first chunk: from cb).
     if (c == c0)
       gs_pool<POOL, P, RM>(a, v, cb, 0, kScoreChunk - 16, job, S);
     else
       gs_pool<POOL, P, RM>(a, v, cb, -16, kScoreChunk, job, S);
     // This chunk's last 32 positions are the next chunk's margin.
-    float* nm = mrg[mb ^ 1];
+    float* nm = mrg0 + (mb ^ 1) * mstride;
     for (int i = threadIdx.x; i < a.R * kGsMargin; i += kScoreWaves * 64) {
       const int r = i / kGsMargin, e = i % kGsMargin;
       nm[r * kGsMPitch + e] = strip[r * kGsPitch + kScoreChunk - kGsMargin + e];
@@ -1516,12 +1562,12 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   // strip entries [256, 272).
   if (wave == 0) {
     const int tr = c1 * kScoreChunk;
-    load_k_subtile<T, STORE>(a, job, tr, lane, kh[0]);
+    load_k_subtile<T, STORE>(a, kj, tr, lane, kh[0]);
     gs_subtiles<T, POOL, 1, RM>(a, kh, s_q, s_mz, s_iz, strip, kGsPitch, tr - kScoreChunk, tr, lane);
   }
   __syncthreads();
   const int mb = (c1 - c0) & 1;
-  gs_pool<POOL, P, RM>(a, GsView{strip, mrg[mb]}, (c1 - 1) * kScoreChunk, kScoreChunk - 16, 16, job, S);
+  gs_pool<POOL, P, RM>(a, GsView{strip, mrg0 + mb * mstride}, (c1 - 1) * kScoreChunk, kScoreChunk - 16, 16, job, S);
 }
 
 static size_t align256(size_t x) { return (x + 255) / 256 * 256; }

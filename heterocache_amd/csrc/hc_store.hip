@@ -79,19 +79,37 @@ __global__ __launch_bounds__(256) void gather_store_kernel(
   const T* bk = (src_k_addr ? reinterpret_cast<const T*>(src_k_addr[job]) : src_k) + src_off[job];
   const T* bv = (src_v_addr ? reinterpret_cast<const T*>(src_v_addr[job]) : src_v) + src_off[job];
   const int32_t* ix = idx ? idx + idx_off[job] : nullptr;
-  // 32 tokens x 16 chunks of 8 elements.
-  for (int c = threadIdx.x; c < HC_TILE * 16; c += 256) {
+  // 32 tokens x 16 chunks of 8 elements, two chunks per thread.  All four
+  // loads are issued before the first wait: a chunk past the item's last
+  // token reads the last token's row again (in the source, not stored).
+  static_assert(HC_TILE * 16 == 2 * 256, "two 8-element chunks per thread");
+  typename Elem<T>::vec8 ra[2], rb[2];
+  int pos[2];  // both positions first: an index read after the first row
+               // loads would wait for them (the wait counter is in order)
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int t = min((threadIdx.x + 256 * q) >> 4, valid - 1);
+    pos[q] = ix ? ix[tok0 + t] : tok0 + t;
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int ch = (threadIdx.x + 256 * q) & 15;
+    // Positions are clamped into the source like the reference's
+    // clamp(max=L-1) before its gather (heterocache/cache_utils.py:852).
+    const int64_t stok = ix ? (int64_t)min(max(pos[q], 0), src_len - 1) : (int64_t)pos[q];
+    const int64_t off = stok * src_tok_stride + ch * 8;
+    // Each source row is read once: streamed past L2 (the prefill
+    // compression of a 128K Llama-3-8B layer, two gathers and the scorer,
+    // 0.204 -> 0.200 ms).
+    ra[q] = load8_stream_global<T>(bk + off);
+    rb[q] = load8_stream_global<T>(bv + off);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int c = threadIdx.x + 256 * q;
     const int t = c >> 4, ch = c & 15;
     if (t < valid) {
-      // Positions are clamped into the source like the reference's
-      // clamp(max=L-1) before its gather (heterocache/cache_utils.py:852).
-      const int64_t stok = ix ? (int64_t)min(max(ix[tok0 + t], 0), src_len - 1) : (int64_t)(tok0 + t);
-      const int64_t off = stok * src_tok_stride + ch * 8;
-      // Each source row is read once: streamed past L2 (the prefill
-      // compression of a 128K Llama-3-8B layer, two gathers and the
-      // scorer, 0.204 -> 0.200 ms).
-      typename Elem<T>::vec8 a = load8_stream<T>(bk + off);
-      typename Elem<T>::vec8 b = load8_stream<T>(bv + off);
+      const typename Elem<T>::vec8 a = ra[q], b = rb[q];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         if constexpr (sizeof(T) == 4) {
