@@ -1381,7 +1381,13 @@ __device__ __forceinline__ void gs_subtiles(const ScoreArgs& a, const typename E
                                             int tw, int lane) {
   constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
   const bool mask = tw + 16 * NU - 1 >= a.L;
-  for (int nt = 0; nt < a.NT; ++nt) {
+  // At most two row tiles (R < 32): unrolled, so the code holds no loop and
+  // the compiler's waits for the keys are exact (inside a rolled loop they
+  // also waited for the other key buffer in flight).
+  static_assert(kLogitRowsMax <= 32, "two row tiles at most");
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    if (nt >= a.NT) break;
     const int r = 16 * nt + (lane & 15);
     float x[NU][4];
 #pragma unroll
@@ -1498,6 +1504,7 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nchunks = (a.L + kScoreChunk - 1) / kScoreChunk;
   const int c0 = blockIdx.x * a.cpw, c1 = min(c0 + a.cpw, nchunks);
+  if (c0 >= c1) return;  // uniform per workgroup (the grid holds none such)
   const int woff = wave * 16 * kSubTiles;
   const T* const kj = job_keys<T, STORE>(a, job);
   // A wave's 64 tokens of a chunk in two halves, double-buffered: a half's
@@ -1535,13 +1542,17 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
   // the compiler cannot bound, and with that state at the loop head its
   // waits for a half's keys would wait for the other half's as well.
   __builtin_amdgcn_s_waitcnt(0);
-  for (int c = c0; c < c1; ++c) {
+  // The chunk loop with the run's last chunk peeled: a chunk requests the
+  // next chunk's keys unconditionally, so the compiler's waits count every
+  // load in flight (behind a branch around the requests its waits for one
+  // half also waited for the other).
+  auto run_chunk = [&](int c, auto load_next) {
     const int cb = c * kScoreChunk;
-    const bool more = c + 1 < c1;
     gs_subtiles<T, POOL, kHalf, RM>(a, ka0, s_q, s_mz, s_iz, strip, kGsPitch, cb, cb + woff, lane);
-    if (more) load_k_run<T, kHalf>(a, kj, cb + kScoreChunk + woff, lane, ka0);
+    if constexpr (decltype(load_next)::value) load_k_run<T, kHalf>(a, kj, cb + kScoreChunk + woff, lane, ka0);
     gs_subtiles<T, POOL, kHalf, RM>(a, ka1, s_q, s_mz, s_iz, strip, kGsPitch, cb, cb + woff + 16 * kHalf, lane);
-    if (more) load_k_run<T, kHalf>(a, kj, cb + kScoreChunk + woff + 16 * kHalf, lane, ka1);
+    if constexpr (decltype(load_next)::value)
+      load_k_run<T, kHalf>(a, kj, cb + kScoreChunk + woff + 16 * kHalf, lane, ka1);
     __syncthreads();  // strip written (and the margin of the previous chunk)
     const int mb = (c - c0 + 1) & 1;  // margin buffer holding the previous chunk's tail
     GsView v{strip, mrg0 + mb * mstride};
@@ -1557,7 +1568,9 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_given_stats_kernel(Sco
       nm[r * kGsMPitch + e] = strip[r * kGsPitch + kScoreChunk - kGsMargin + e];
     }
     __syncthreads();  // strip read
-  }
+  };
+  for (int c = c0; c < c1 - 1; ++c) run_chunk(c, std::true_type{});
+  run_chunk(c1 - 1, std::false_type{});
   // The run's last 16 positions, with its right margin c1*256 .. +15 at
   // strip entries [256, 272).
   if (wave == 0) {
