@@ -768,10 +768,10 @@ __device__ __forceinline__ void load_k_clamped(const ScoreArgs& a, const T* base
 // sets: a half's keys for the next chunk are requested as soon as the half
 // has been consumed, so every load has the other half's work to land in.
 // In the run's last chunk the "next" keys are the same keys again, so the
-// loads stay unconditional.  Alternated on one box with one buffer reloaded
-// after the whole chunk (8 heads x 128K, W = 32, max pool 7, host work
-// included): 0.0742-0.0757 against 0.0749-0.0772 ms per layer, so the key
-// loads were not what bounds the pass; VALU issue and latency are.
+// loads stay unconditional.  Against one buffer reloaded after the whole
+// chunk (8 heads x 128K, W = 32, max pool 7): 70.0 against 70.1 us per
+// launch, so the key loads were not what bounds the pass; VALU issue and
+// latency are.
 template <typename T, bool STORE, int RM, int POOL, int P>
 __global__ __launch_bounds__(kScoreWaves * 64, sizeof(T) == 4 ? 1 : RM == 0 ? 4 : 3) void score_probs_pool_kernel(ScoreArgs a, StatsView stats,
                                                                            float* __restrict__ S) {
