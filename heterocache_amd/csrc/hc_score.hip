@@ -1023,9 +1023,48 @@ constexpr int kFinWaveSlots = 6;  // the left halo, the four waves of a tile, th
 // built while the scores are in registers.  Workgroups then take several
 // tiles of their row (gridDim.x < tiles) so that each flushes its LDS
 // histogram to the row's once.
+// Row statistics of the finish passes.  From the merged (max, sum) pairs,
+// or, with `part` given, folded here from the statistics pass's
+// per-workgroup partials (one wave per row, in the order of
+// score_stats_merge_kernel, so the same values), which spares the merge
+// launch.  LOG2: s_m = max + log2(sum) (p = exp2(x - s_m)); otherwise
+// s_m = max and s_iz = 1 / sum.
+template <bool LOG2>
+__device__ __forceinline__ void finish_row_stats(const float* __restrict__ stats, const float* __restrict__ part,
+                                                 int nparts, int job, int R, float* s_m, float* s_iz) {
+  auto set = [&](int r, float m, float l) {
+    if constexpr (LOG2) {
+      s_m[r] = m + __log2f(l);
+    } else {
+      s_m[r] = m;
+      s_iz[r] = 1.f / l;
+    }
+  };
+  if (part) {
+    const int lane = threadIdx.x & 63;
+    for (int r = threadIdx.x >> 6; r < R; r += blockDim.x >> 6) {
+      float m = -INFINITY, l = 0.f;
+      for (int c = lane; c < nparts; c += 64) {
+        const float* q = part + (((int64_t)job * nparts + c) * R + r) * 2;
+        merge_ml(m, l, q[0], q[1]);
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, 64), l2 = __shfl_xor(l, off, 64);
+        merge_ml(m, l, m2, l2);
+      }
+      if (lane == 0) set(r, m, l);
+    }
+  } else {
+    for (int r = threadIdx.x; r < R; r += blockDim.x)
+      set(r, stats[((int64_t)job * R + r) * 2], stats[((int64_t)job * R + r) * 2 + 1]);
+  }
+}
+
 template <int RMODE, int POOL, bool HIST>
 __global__ __launch_bounds__(256) void score_finish_kernel(const float* __restrict__ logits,
-                                                           const float* __restrict__ stats, int R, int G, int W,
+                                                           const float* __restrict__ stats,
+                                                           const float* __restrict__ part, int nparts, int R, int G, int W,
                                                            int span, int sum_w, int kernel, int accumulate,
                                                            float* __restrict__ S, uint32_t* __restrict__ hist) {
   // s_a[kFinHalo + i] holds position t0 + i of the current head's strip,
@@ -1040,10 +1079,7 @@ __global__ __launch_bounds__(256) void score_finish_kernel(const float* __restri
   const int ntiles = (span + kFinTile - 1) / kFinTile;
   const int p = kernel / 2;
   constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
-  for (int r = threadIdx.x; r < R; r += 256) {
-    s_m[r] = stats[((int64_t)job * R + r) * 2];
-    s_iz[r] = 1.f / stats[((int64_t)job * R + r) * 2 + 1];
-  }
+  finish_row_stats<false>(stats, part, nparts, job, R, s_m, s_iz);
   if constexpr (HIST)
     for (int b = threadIdx.x; b < kKeyDigitBins; b += 256) s_hist[b] = 0u;
   const int w_lo = sum_w ? 0 : wo, w_hi = sum_w ? W : wo + 1;
@@ -1162,7 +1198,9 @@ constexpr int kFinRegTile = 256 * kFinRegPos;
 constexpr int kFinRegHistTiles = 2;
 template <int RMODE, int POOL, bool HIST, int P>
 __global__ __launch_bounds__(256) void score_finish_reg_kernel(const float* __restrict__ logits,
-                                                               const float* __restrict__ stats, int R, int G, int W,
+                                                               const float* __restrict__ stats,
+                                                               const float* __restrict__ part, int nparts, int R,
+                                                               int G, int W,
                                                                int span, int sum_w, int kernel, int accumulate,
                                                                float* __restrict__ S, uint32_t* __restrict__ hist) {
   constexpr int NV = kFinRegPos / 4;  // 16-byte vectors per thread and row
@@ -1178,16 +1216,7 @@ __global__ __launch_bounds__(256) void score_finish_reg_kernel(const float* __re
   constexpr int p = P;  // kernel == 2P + 1
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   constexpr float pad = POOL == 0 ? 0.f : -INFINITY;
-  for (int r = threadIdx.x; r < R; r += 256) {
-    if constexpr (RMODE == 0) {
-      // Without casts p = exp2(x - (m + log2 l)): one subtract, and a masked
-      // logit (-inf) gives 0 by itself.
-      s_m[r] = stats[((int64_t)job * R + r) * 2] + __log2f(stats[((int64_t)job * R + r) * 2 + 1]);
-    } else {
-      s_m[r] = stats[((int64_t)job * R + r) * 2];
-      s_iz[r] = 1.f / stats[((int64_t)job * R + r) * 2 + 1];
-    }
-  }
+  finish_row_stats<RMODE == 0>(stats, part, nparts, job, R, s_m, s_iz);
   if constexpr (HIST)
     for (int b = threadIdx.x; b < kKeyDigitBins; b += 256) s_hist[b] = 0u;
   const int w_lo = sum_w ? 0 : wo, w_hi = sum_w ? W : wo + 1;
@@ -1763,9 +1792,15 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
   }
   int rc = check_launch("hc_score(stats)");
   if (rc) return rc;
-  hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nparts, a.R,
-                     njobs, stats, hist, hist ? (int64_t)njobs * wout * kKeyDigitBins : (int64_t)0);
-  if ((rc = check_launch("hc_score(merge)"))) return rc;
+  // The logit path's finish folds the partials itself, unless the merge
+  // launch also has the histograms to clear.
+  const bool fold_in_finish = via_logits && !hist;
+  if (!fold_in_finish) {
+    hipLaunchKernelGGL(score_stats_merge_kernel, dim3((njobs * a.R + 3) / 4), dim3(256), 0, s, part, nparts, a.R,
+                       njobs, stats, hist, hist ? (int64_t)njobs * wout * kKeyDigitBins : (int64_t)0);
+    if ((rc = check_launch("hc_score(merge)"))) return rc;
+  }
+  const float* fpart = fold_in_finish ? part : nullptr;
   if (via_logits) {
     if (a.span > 0) {
       const bool reg_pool = kernel == 5 || kernel == 7;
@@ -1779,15 +1814,18 @@ static int launch_score(ScoreArgs a, int njobs, int pooling, int kernel, float* 
 #define HC_FINISH2(RM, PL, HI)                                                                              \
   do {                                                                                                      \
     if (kernel == 5)                                                                                        \
-      hipLaunchKernelGGL((score_finish_reg_kernel<RM, PL, HI, 2>), fgrid, dim3(256), 0, s, A, stats, a.R,     \
+      hipLaunchKernelGGL((score_finish_reg_kernel<RM, PL, HI, 2>), fgrid, dim3(256), 0, s, A, stats, fpart,   \
+                         nparts, a.R,                                                                 \
                          a.G, a.W, a.span, sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores,    \
                          hist);                                                                             \
     else if (kernel == 7)                                                                                   \
-      hipLaunchKernelGGL((score_finish_reg_kernel<RM, PL, HI, 3>), fgrid, dim3(256), 0, s, A, stats, a.R,     \
+      hipLaunchKernelGGL((score_finish_reg_kernel<RM, PL, HI, 3>), fgrid, dim3(256), 0, s, A, stats, fpart,   \
+                         nparts, a.R,                                                                 \
                          a.G, a.W, a.span, sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores,    \
                          hist);                                                                             \
     else                                                                                                    \
-      hipLaunchKernelGGL((score_finish_kernel<RM, PL, HI>), fgrid, dim3(256), 0, s, A, stats, a.R, a.G, a.W,  \
+      hipLaunchKernelGGL((score_finish_kernel<RM, PL, HI>), fgrid, dim3(256), 0, s, A, stats, fpart, nparts,  \
+                         a.R, a.G, a.W,                                                               \
                          a.span, sum_w, kernel, (a.flags & HC_SCORE_ACCUMULATE) ? 1 : 0, scores, hist);      \
   } while (0)
 #define HC_FINISH(RM, PL)          \
