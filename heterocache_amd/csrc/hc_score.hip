@@ -19,7 +19,9 @@
 //     the A operand, loaded straight from HBM; queries are B operands staged
 //     in LDS once per workgroup), reduced to a (max, sum exp) per row; with
 //     fewer than 32 rows the logits are stored too.
-//  2. score_stats_merge_kernel: fold the workgroups' (max, sum) per row.
+//  2. score_stats_merge_kernel: fold the workgroups' (max, sum) per row
+//     (on the stored-logit path, phase 3b folds them itself unless the
+//     drift histograms need clearing).
 //  3a. (>= 32 rows) score_probs_kernel: recompute the logits, normalise, sum
 //     over the window rows of each query head (xor-shuffle tree: fixed
 //     order), write A[job][w'][g][t]; score_pool_kernel: pooling over t and
