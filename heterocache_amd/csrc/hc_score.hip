@@ -1369,18 +1369,21 @@ __global__ __launch_bounds__(256) void score_finish_reg_kernel(const float* __re
 // c also fills for chunk c + 1, so each chunk costs two barriers (strip
 // written; strip read).  Only a run's ends cost an extra 16-token sub-tile:
 // the left margin of its first chunk and the right margin of its last 16
-// positions.  The next chunk's keys are requested before the pooling, so
-// their latency is spent pooling.  The first-digit key histograms that
-// hc_drift_select needs are left to its own pass over the scores (24 us at
+// positions.  Each wave's keys are two double-buffered halves: a half's next
+// keys are requested as soon as its products are formed, so they land while
+// the other half is scored and the chunk pools.  The first-digit key
+// histograms that hc_drift_select needs are left to its own pass over the
+// scores (24 us at
 // 33 pivots x 5 steps x 128K): counted here, in LDS as 16-bit counters of
 // the 1024 digits a probability can have, they took the kernel from 0.25 to
 // 0.39 ms, and counted into global memory, 0.69 ms.
 // (Four independent waves per workgroup, each with its own 128-position ring
 // and no barriers, measured slower: 0.32 against 0.25 ms at 33 pivots x 5
-// steps x 128K, at three waves per SIMD instead of four.  So did requesting
-// the next chunk's keys earlier -- sub-tile by sub-tile as each one's
-// products are issued (270 against 260 us: two MFMA chains per step instead
-// of eight), or all four right after the last row tile's products (263).)
+// steps x 128K, at three waves per SIMD instead of four.  With one key
+// buffer, so did requesting the next chunk's keys earlier -- sub-tile by
+// sub-tile as each one's products are issued (270 against 260 us: two MFMA
+// chains per step instead of eight), or all four right after the last row
+// tile's products (263).)
 // ---------------------------------------------------------------------------
 constexpr int kGsMargin = 32;                     // margin positions before a chunk
 constexpr int kGsRight = 16;                      // the run's right margin
