@@ -421,6 +421,14 @@ __global__ __launch_bounds__(kScoreWaves * 64) void score_rows_valu_kernel(Score
       const float mine = row16_sum_scatter<NR>(acc, lane);  // row c % NR
       const int t = t0 + 4 * st + sub;
       x[st] = t <= limit ? scaled_logit<RM>(a, mine) : -INFINITY;
+    }
+    // The logits are stored after all the iteration's keys are consumed:
+    // stores between the key waits count against the same in-order counter,
+    // so each wait also waited for the next key (prefill compression 0.192-
+    // 0.193 -> 0.191 ms per 128K layer).
+#pragma unroll
+    for (int st = 0; st < kRowsSteps; ++st) {
+      const int t = t0 + 4 * st + sub;
       if (owner && t < a.span) lrow[t] = x[st];
     }
     float mx = x[0];
