@@ -242,16 +242,27 @@ __global__ __launch_bounds__(kSelThreads) void select_write_kernel(const float* 
   const uint32_t tau = (uint32_t)state[job * 4];
   const int need_eq = state[job * 4 + 1];
   const bool all_ties = state[job * 4 + 2] != 0;
-  if (tid == 0) {
-    // Kept elements and ties in the chunks before this one.
-    int sel = 0, eq = 0;
-    for (int c = 0; c < chunk; ++c) {
-      const int g = cnt[((int64_t)job * nchunks + c) * 2], e = cnt[((int64_t)job * nchunks + c) * 2 + 1];
-      sel += g + (all_ties ? e : max(0, min(e, need_eq - eq)));
-      eq += e;
+  if (wave == 0) {
+    // Kept elements and ties in the chunks before this one: G keys above tau
+    // and EQ ties in all, of which the ties taken in position order number
+    // min(max(need_eq, 0), EQ) (the chunk-by-chunk sum of
+    // max(0, min(e_c, need_eq - ties before c)) telescopes to it).  Summed
+    // by the 64 lanes: one thread walking the chunks took a round trip per
+    // few chunks, ~8 us for the last chunk of a 128K row.
+    int g = 0, e = 0;
+    for (int c = lane; c < chunk; c += 64) {
+      g += cnt[((int64_t)job * nchunks + c) * 2];
+      e += cnt[((int64_t)job * nchunks + c) * 2 + 1];
     }
-    s_base[0] = sel;
-    s_base[1] = eq;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      g += __shfl_xor(g, off, 64);
+      e += __shfl_xor(e, off, 64);
+    }
+    if (lane == 0) {
+      s_base[0] = g + (all_ties ? e : min(max(need_eq, 0), e));
+      s_base[1] = e;
+    }
   }
   const float* s = scores + (int64_t)job * score_stride;
   uint32_t keys[kSelRows];
